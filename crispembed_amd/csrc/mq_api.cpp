@@ -1,0 +1,266 @@
+// mq_api.cpp -- the extern "C" entry points of libmq.so (declared in include/mq.h).
+//
+// Argument checking happens here, on the host, before any launch: every kernel
+// assumes the shapes validated below (k a multiple of the block size, m <= 8 for
+// the GEMV, 16-byte aligned planes), so no kernel is ever launched on a shape it
+// would index out of bounds.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "mq_internal.h"
+
+namespace mq {
+namespace host {
+size_t quantize_chunk(int type, const float *src, void *dst, int64_t nrows, int64_t k);
+}
+}  // namespace mq
+
+using namespace mq;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(MQ_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// env knobs: unset, "" or "0" mean off (the reference's core_env::on semantics,
+// src/core/env_gate.h:25-42); numeric knobs parse the value
+int env_int(const char *name, int dflt) {
+    const char *v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    char *end = nullptr;
+    const long x = std::strtol(v, &end, 10);
+    return (end && *end == 0) ? (int)x : dflt;
+}
+
+int g_gemv_max_m = -1;
+int g_q8_0_variant = -1;
+
+struct Workspace {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+Workspace g_ws[64];  // per HIP device ordinal
+
+bool type_ok(int t) {
+    return t == MQ_TYPE_Q8_0 || t == MQ_TYPE_Q4_K || t == MQ_TYPE_Q6_K || t == MQ_TYPE_F16;
+}
+
+int check_weight_shape(int type, int64_t n, int64_t k) {
+    if (!type_ok(type)) return fail(MQ_EUNSUPPORTED, "weight type %d is not Q8_0/Q4_K/Q6_K/F16", type);
+    if (n <= 0 || k <= 0) return fail(MQ_EINVAL, "bad shape n=%lld k=%lld", (long long)n, (long long)k);
+    if (!mq_supports(type, k))
+        return fail(MQ_EUNSUPPORTED, "k=%lld is not a multiple of the %s block", (long long)k,
+                    type == MQ_TYPE_F16 ? "32-value F16" : "quant");
+    if (n > INT32_MAX || k > INT32_MAX || n * k > ((int64_t)1 << 40))
+        return fail(MQ_EINVAL, "tensor too large n=%lld k=%lld", (long long)n, (long long)k);
+    return MQ_OK;
+}
+
+bool is_aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char *mq_last_error(void) { return g_err.c_str(); }
+
+int mq_init(void) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(MQ_ENODEV, "device %d is %s, this library is built for gfx950", dev, prop.gcnArchName);
+    return MQ_OK;
+}
+
+int mq_gemv_max_m(void) {
+    if (g_gemv_max_m < 0) {
+        int v = env_int("MQ_FORCE_GEMV_MAX_M", 8);
+        g_gemv_max_m = v < 0 ? 0 : (v > 8 ? 8 : v);
+    }
+    return g_gemv_max_m;
+}
+
+int mq_q8_0_variant(void) {
+    if (g_q8_0_variant < 0) {
+        const int v = env_int("MQ_Q8_0_VARIANT", MQ_Q8_0_X86);
+        g_q8_0_variant = (v == MQ_Q8_0_NEON || v == MQ_Q8_0_REF) ? v : MQ_Q8_0_X86;
+    }
+    return g_q8_0_variant;
+}
+
+int mq_set_q8_0_variant(int variant) {
+    if (variant != MQ_Q8_0_X86 && variant != MQ_Q8_0_NEON && variant != MQ_Q8_0_REF)
+        return fail(MQ_EINVAL, "unknown Q8_0 variant %d", variant);
+    g_q8_0_variant = variant;
+    return MQ_OK;
+}
+
+int64_t mq_blck_size(int type) { return blck_size(type); }
+size_t mq_type_size(int type) { return type_size(type); }
+size_t mq_row_size(int type, int64_t k) { return row_size(type, k); }
+
+int mq_vec_dot_type(int type) {
+    switch (type) {
+        case MQ_TYPE_Q8_0: return MQ_TYPE_Q8_0;
+        case MQ_TYPE_Q4_K:
+        case MQ_TYPE_Q6_K: return MQ_TYPE_Q8_K;
+        case MQ_TYPE_F16: return MQ_TYPE_F16;
+        default: return -1;
+    }
+}
+
+int mq_supports(int type, int64_t k) {
+    if (k <= 0) return 0;
+    switch (type) {
+        case MQ_TYPE_Q8_0: return k % QK8_0 == 0;
+        case MQ_TYPE_Q4_K:
+        case MQ_TYPE_Q6_K: return k % QK_K == 0;
+        case MQ_TYPE_F16: return k % 32 == 0;
+        default: return 0;
+    }
+}
+
+size_t mq_quantize_chunk(int type, const float *src_host, void *dst_host, int64_t nrows, int64_t k) {
+    const size_t r = host::quantize_chunk(type, src_host, dst_host, nrows, k);
+    if (r == 0 && nrows > 0) fail(MQ_EINVAL, "mq_quantize_chunk: bad type %d or k=%lld", type, (long long)k);
+    return r;
+}
+
+int mq_quantize_q8_0(const float *x, int64_t ldx, void *y, int64_t nrows, int64_t k, int variant, void *stream) {
+    if (!x || !y || nrows < 0 || k <= 0 || k % QK8_0 || ldx < k)
+        return fail(MQ_EINVAL, "mq_quantize_q8_0: bad arguments");
+    if (variant != MQ_Q8_0_X86 && variant != MQ_Q8_0_NEON && variant != MQ_Q8_0_REF)
+        return fail(MQ_EINVAL, "mq_quantize_q8_0: unknown variant %d", variant);
+    if (!is_aligned(y, 2)) return fail(MQ_EINVAL, "mq_quantize_q8_0: y must be 2-byte aligned");
+    const hipError_t e = launch_quantize_q8_0_gguf(x, ldx, y, nrows, k, variant, (hipStream_t)stream);
+    return e == hipSuccess ? MQ_OK : hip_fail(e, "mq_quantize_q8_0");
+}
+
+int mq_quantize_q8_K(const float *x, int64_t ldx, void *y, int64_t nrows, int64_t k, void *stream) {
+    if (!x || !y || nrows < 0 || k <= 0 || k % QK_K || ldx < k)
+        return fail(MQ_EINVAL, "mq_quantize_q8_K: bad arguments");
+    if (!is_aligned(y, 4)) return fail(MQ_EINVAL, "mq_quantize_q8_K: y must be 4-byte aligned");
+    const hipError_t e = launch_quantize_q8_K_gguf(x, ldx, y, nrows, k, (hipStream_t)stream);
+    return e == hipSuccess ? MQ_OK : hip_fail(e, "mq_quantize_q8_K");
+}
+
+int mq_quantize_f16(const float *x, int64_t ldx, void *y, int64_t nrows, int64_t k, void *stream) {
+    if (!x || !y || nrows < 0 || k <= 0 || k % 4 || ldx < k) return fail(MQ_EINVAL, "mq_quantize_f16: bad arguments");
+    if (!is_aligned(y, 2)) return fail(MQ_EINVAL, "mq_quantize_f16: y must be 2-byte aligned");
+    const hipError_t e = launch_quantize_f16(x, ldx, y, nrows, k, (hipStream_t)stream);
+    return e == hipSuccess ? MQ_OK : hip_fail(e, "mq_quantize_f16");
+}
+
+int mq_dequantize(int type, const void *w, float *y, int64_t nrows, int64_t k, int fused, void *stream) {
+    if (!w || !y || nrows < 0 || k <= 0) return fail(MQ_EINVAL, "mq_dequantize: bad arguments");
+    if (type != MQ_TYPE_F16 && type != MQ_TYPE_Q8_0 && type != MQ_TYPE_Q4_K && type != MQ_TYPE_Q6_K &&
+        type != MQ_TYPE_Q8_K)
+        return fail(MQ_EUNSUPPORTED, "mq_dequantize: type %d", type);
+    if (k % blck_size(type)) return fail(MQ_EINVAL, "mq_dequantize: k=%lld not a multiple of the block", (long long)k);
+    if (!is_aligned(w, 4)) return fail(MQ_EINVAL, "mq_dequantize: w must be 4-byte aligned");
+    const hipError_t e = launch_dequantize(type, w, y, nrows, k, fused, (hipStream_t)stream);
+    return e == hipSuccess ? MQ_OK : hip_fail(e, "mq_dequantize");
+}
+
+size_t mq_gguf_bytes(int type, int64_t n, int64_t k) { return weight_planes(type, n, k).gguf; }
+size_t mq_gguf_bytes_aligned(int type, int64_t n, int64_t k) { return align256(weight_planes(type, n, k).gguf); }
+size_t mq_weight_image_bytes(int type, int64_t n, int64_t k) {
+    if (!type_ok(type) || n <= 0 || k <= 0 || !mq_supports(type, k)) return 0;
+    return weight_planes(type, n, k).total;
+}
+
+int mq_weight_prepare(int type, void *image, int64_t n, int64_t k, int64_t row0, int64_t row1, void *stream) {
+    int rc = check_weight_shape(type, n, k);
+    if (rc) return rc;
+    if (!image || !is_aligned(image, 256)) return fail(MQ_EINVAL, "mq_weight_prepare: image must be 256-byte aligned");
+    if (row0 < 0) row0 = 0;
+    if (row1 > n) row1 = n;
+    const hipError_t e = launch_weight_prepare(type, image, n, k, row0, row1, (hipStream_t)stream);
+    return e == hipSuccess ? MQ_OK : hip_fail(e, "mq_weight_prepare");
+}
+
+size_t mq_workspace_bytes(int type, int64_t m, int64_t k) {
+    if (!type_ok(type) || m < 0 || k <= 0) return 0;
+    return act_planes(type, m, k).total;
+}
+
+int mq_mul_mat_ex(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m,
+                  float *y, int64_t ldy, void *workspace, size_t workspace_bytes, int path, void *stream) {
+    int rc = check_weight_shape(type, n, k);
+    if (rc) return rc;
+    if (!w_image || !x || !y) return fail(MQ_EINVAL, "mq_mul_mat: NULL pointer");
+    if (m < 0 || m > INT32_MAX || ldx < k || ldy < n) return fail(MQ_EINVAL, "mq_mul_mat: bad m/ldx/ldy");
+    if (m == 0) return MQ_OK;
+    if (!is_aligned(w_image, 256)) return fail(MQ_EINVAL, "mq_mul_mat: weight image must be 256-byte aligned");
+    if (path == MQ_PATH_AUTO) path = (m <= mq_gemv_max_m()) ? MQ_PATH_GEMV : MQ_PATH_GEMM;
+    if (path == MQ_PATH_GEMV && m > 8) return fail(MQ_EINVAL, "mq_mul_mat: GEMV path takes m <= 8 (m=%lld)", (long long)m);
+    if (path != MQ_PATH_GEMV && path != MQ_PATH_GEMM) return fail(MQ_EINVAL, "mq_mul_mat: unknown path %d", path);
+    const hipStream_t s = (hipStream_t)stream;
+    const size_t need = act_planes(type, m, k).total;
+    void *ws = workspace;
+    if (ws) {
+        if (workspace_bytes < need)
+            return fail(MQ_EINVAL, "mq_mul_mat: workspace %zu bytes < %zu needed", workspace_bytes, need);
+        if (!is_aligned(ws, 256)) return fail(MQ_EINVAL, "mq_mul_mat: workspace must be 256-byte aligned");
+    } else {
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+        if (dev < 0 || dev >= 64) return fail(MQ_EINVAL, "device ordinal %d", dev);
+        std::lock_guard<std::mutex> lk(g_ws_mu);
+        Workspace &w = g_ws[dev];
+        if (w.bytes < need) {
+            // the old buffer may still be read by work queued earlier on any stream
+            e = hipDeviceSynchronize();
+            if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+            if (w.ptr) (void)hipFree(w.ptr);
+            w.ptr = nullptr;
+            w.bytes = 0;
+            e = hipMalloc(&w.ptr, need);
+            if (e != hipSuccess) {
+                w.ptr = nullptr;
+                return fail(MQ_ENOMEM, "hipMalloc(%zu) for the activation workspace failed", need);
+            }
+            w.bytes = need;
+        }
+        ws = w.ptr;
+    }
+    hipError_t e = launch_quantize_act_planar(type, x, ldx, ws, m, k, mq_q8_0_variant(), s);
+    if (e != hipSuccess) return hip_fail(e, "activation quantization");
+    e = (path == MQ_PATH_GEMV) ? launch_gemv(type, w_image, n, k, ws, m, y, ldy, s)
+                               : launch_gemm(type, w_image, n, k, ws, m, y, ldy, s);
+    if (e != hipSuccess) return hip_fail(e, path == MQ_PATH_GEMV ? "gemv" : "gemm");
+    return MQ_OK;
+}
+
+int mq_mul_mat(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m, float *y,
+               int64_t ldy, void *workspace, size_t workspace_bytes, void *stream) {
+    return mq_mul_mat_ex(type, w_image, n, k, x, ldx, m, y, ldy, workspace, workspace_bytes, MQ_PATH_AUTO, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,76 @@
+"""ctypes binding of libmq.so (include/mq.h).  Device pointers are plain ints."""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmq.so")
+
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K = 0, 1, 8, 12, 14, 15
+Q8_0_X86, Q8_0_NEON, Q8_0_REF = 0, 1, 2
+PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
+
+TYPE_NAMES = {TYPE_F32: "f32", TYPE_F16: "f16", TYPE_Q8_0: "q8_0", TYPE_Q4_K: "q4_K",
+              TYPE_Q6_K: "q6_K", TYPE_Q8_K: "q8_K"}
+
+
+class MQError(RuntimeError):
+    pass
+
+
+_lib = None
+
+_c_i64 = ctypes.c_int64
+_c_sz = ctypes.c_size_t
+_c_vp = ctypes.c_void_p
+_c_int = ctypes.c_int
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "mq_init": (_c_int, []),
+    "mq_last_error": (ctypes.c_char_p, []),
+    "mq_gemv_max_m": (_c_int, []),
+    "mq_q8_0_variant": (_c_int, []),
+    "mq_set_q8_0_variant": (_c_int, [_c_int]),
+    "mq_blck_size": (_c_i64, [_c_int]),
+    "mq_type_size": (_c_sz, [_c_int]),
+    "mq_row_size": (_c_sz, [_c_int, _c_i64]),
+    "mq_vec_dot_type": (_c_int, [_c_int]),
+    "mq_supports": (_c_int, [_c_int, _c_i64]),
+    "mq_quantize_chunk": (_c_sz, [_c_int, _c_vp, _c_vp, _c_i64, _c_i64]),
+    "mq_quantize_q8_0": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_int, _c_vp]),
+    "mq_quantize_q8_K": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp]),
+    "mq_quantize_f16": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp]),
+    "mq_dequantize": (_c_int, [_c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_vp]),
+    "mq_gguf_bytes": (_c_sz, [_c_int, _c_i64, _c_i64]),
+    "mq_gguf_bytes_aligned": (_c_sz, [_c_int, _c_i64, _c_i64]),
+    "mq_weight_image_bytes": (_c_sz, [_c_int, _c_i64, _c_i64]),
+    "mq_weight_prepare": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
+    "mq_workspace_bytes": (_c_sz, [_c_int, _c_i64, _c_i64]),
+    "mq_mul_mat": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
+                            _c_sz, _c_vp]),
+    "mq_mul_mat_ex": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
+                               _c_sz, _c_int, _c_vp]),
+}
+
+
+def lib():
+    """Load libmq.so (raises if it was not built: there is no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MQError(f"{LIB_PATH} is missing; run `python -c 'import __graft_entry__ as g; g.build()'`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    """Raise MQError with the library's message when rc != 0."""
+    if rc != 0:
+        msg = lib().mq_last_error()
+        raise MQError(f"libmq error {rc}: {msg.decode() if msg else ''}")
+    return rc

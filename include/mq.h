@@ -1,0 +1,130 @@
+/*
+ * mq.h -- C ABI of the MI355X (gfx950) quantized mat-mul library (libmq.so).
+ *
+ * This is the drop-in boundary for CrispEmbed's GGML_OP_MUL_MAT hot path on
+ * GGUF block-quantized weights.  In CrispEmbed every linear layer is
+ * ggml_mul_mat(W, X) (src/crispembed.cpp:1168-1170,1300,1410,1416;
+ * src/decoder_embed.cpp:724-802; src/qwen2vl_ocr.cpp:2368-2452) and is executed
+ * by a ggml backend's graph_compute, reached from ggml_backend_sched_graph_compute
+ * (src/crispembed.cpp:1471-1483).  The ggml backend in ggml-mi355.h is built on
+ * top of these entry points; callers that do not use ggml can call them directly.
+ *
+ * Conventions
+ *   - All tensor pointers are DEVICE pointers unless the name says host.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ *     Entry points enqueue work and return; they do not synchronize.
+ *   - Return value: 0 on success, a negative MQ_E* code on failure;
+ *     mq_last_error() returns a message for the calling thread.
+ *   - Layout follows ggml: a weight W has ne[0] = k (in-features, the axis the
+ *     quant blocks run along) and ne[1] = n rows; activations X are m rows of
+ *     k floats with row stride ldx (floats); Y[i*ldy + j] = sum_k W[j,k]*X[i,k].
+ *   - Type ids are ggml/GGUF ids: F32 0, F16 1, Q8_0 8, Q4_K 12, Q6_K 14, Q8_K 15.
+ */
+#ifndef MQ_H
+#define MQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MQ_TYPE_F32 0
+#define MQ_TYPE_F16 1
+#define MQ_TYPE_Q8_0 8
+#define MQ_TYPE_Q4_K 12
+#define MQ_TYPE_Q6_K 14
+#define MQ_TYPE_Q8_K 15
+
+#define MQ_OK 0
+#define MQ_EINVAL (-1)      /* bad argument: shape, type, alignment, NULL pointer */
+#define MQ_EUNSUPPORTED (-2) /* valid ggml input this library does not handle */
+#define MQ_EHIP (-3)        /* a HIP runtime call failed */
+#define MQ_ENOMEM (-4)      /* device allocation failed */
+#define MQ_ENODEV (-5)      /* no gfx950 device */
+
+/* Q8_0 activation rounding variants (the host ISA decides which one ggml-cpu runs):
+ * X86 : id = 127/amax, q = round-half-even(x*id)   (AVX/AVX2/AVX-512 quantize_row_q8_0)
+ * NEON: id = 1/(amax/127), q = round-half-even(x*id)
+ * REF : id = 1/(amax/127), q = roundf(x*id)          (quantize_row_q8_0_ref) */
+#define MQ_Q8_0_X86 0
+#define MQ_Q8_0_NEON 1
+#define MQ_Q8_0_REF 2
+
+/* mq_mul_mat_ex path selection */
+#define MQ_PATH_AUTO 0 /* GEMV when m <= mq_gemv_max_m(), else GEMM */
+#define MQ_PATH_GEMV 1 /* weight-streaming GEMV, m <= 8 */
+#define MQ_PATH_GEMM 2 /* MFMA GEMM */
+
+/* ---- library / device ---- */
+
+/* Checks that the current HIP device is gfx950.  Replaces nothing in the reference
+ * (ggml backends check their device inside ggml_backend_dev_init). */
+int mq_init(void);
+const char *mq_last_error(void);
+/* Largest m routed to the GEMV path by MQ_PATH_AUTO (default 8; env MQ_FORCE_GEMV_MAX_M). */
+int mq_gemv_max_m(void);
+/* Q8_0 activation rounding variant used by mq_mul_mat (default MQ_Q8_0_X86; env MQ_Q8_0_VARIANT). */
+int mq_q8_0_variant(void);
+int mq_set_q8_0_variant(int variant);
+
+/* ---- type traits (ggml_blck_size / ggml_type_size / ggml_row_size) ---- */
+int64_t mq_blck_size(int type);
+size_t mq_type_size(int type);
+size_t mq_row_size(int type, int64_t k);
+/* ggml's vec_dot_type: the type CPU mul_mat converts X to (Q8_0->Q8_0, Q4_K/Q6_K->Q8_K, F16->F16). */
+int mq_vec_dot_type(int type);
+/* 1 if mq_mul_mat accepts weights of this type with this k (k % block == 0, F16 k % 32 == 0). */
+int mq_supports(int type, int64_t k);
+
+/* ---- host weight quantization (producer side) ----
+ * Replaces ggml_quantize_chunk(type, src, dst, 0, nrows, k, NULL) as called by
+ * tools/quantize.cpp:804-805 (no importance matrix: ggml's _ref quantizers).
+ * HOST pointers.  Returns bytes written, 0 on bad type/shape. */
+size_t mq_quantize_chunk(int type, const float *src_host, void *dst_host, int64_t nrows, int64_t k);
+
+/* ---- activation quantization, GGUF block layout (device) ----
+ * quantize_row_q8_0 (ggml-cpu from_float for Q8_0 weights), one row of k per x row. */
+int mq_quantize_q8_0(const float *x, int64_t ldx, void *y, int64_t nrows, int64_t k, int variant, void *stream);
+/* quantize_row_q8_K (from_float for Q4_K / Q6_K weights): block_q8_K {float d; int8 qs[256]; int16 bsums[16]}. */
+int mq_quantize_q8_K(const float *x, int64_t ldx, void *y, int64_t nrows, int64_t k, void *stream);
+/* fp32 -> fp16 round-to-nearest-even (from_float for F16 weights). */
+int mq_quantize_f16(const float *x, int64_t ldx, void *y, int64_t nrows, int64_t k, void *stream);
+
+/* ---- dequantization (ggml type_traits to_float; src/core/cpu_ops.h:63-65) ----
+ * GGUF rows -> fp32.  fused=1 evaluates Q4_K's d1*q - m1 as one fma (what a
+ * contracting compiler emits); fused=0 rounds the product and the difference
+ * separately.  Other types are unaffected by the flag. */
+int mq_dequantize(int type, const void *w, float *y, int64_t nrows, int64_t k, int fused, void *stream);
+
+/* ---- weight images ----
+ * A weight image is the GGUF bytes of an n x k tensor (row-major blocks, exactly
+ * what core_gguf::load_weights uploads with ggml_backend_tensor_set,
+ * src/core/gguf_loader.cpp:480), followed at mq_gguf_bytes_aligned() by derived
+ * planes in the layout the GEMM / GEMV kernels read.  mq_weight_prepare() builds
+ * the planes from the GGUF part; the GGUF part is never modified, so reading it
+ * back returns the original bytes. */
+size_t mq_gguf_bytes(int type, int64_t n, int64_t k);
+size_t mq_gguf_bytes_aligned(int type, int64_t n, int64_t k);
+size_t mq_weight_image_bytes(int type, int64_t n, int64_t k);
+/* Rebuild planes for rows [row0, row1) after a (partial) write of the GGUF part. */
+int mq_weight_prepare(int type, void *image, int64_t n, int64_t k, int64_t row0, int64_t row1, void *stream);
+
+/* ---- mul_mat ----
+ * Y = X * W^T with ggml CPU semantics: X is requantized to mq_vec_dot_type(type)
+ * exactly as ggml's from_float does, the integer block dots are exact, and the
+ * per-block fp16/fp32 scales are applied in fp32.
+ * `w_image` is a prepared weight image.  `workspace` receives the quantized
+ * activations; size it with mq_workspace_bytes().  workspace == NULL makes the
+ * library use (and grow with hipMalloc) an internal per-device buffer. */
+size_t mq_workspace_bytes(int type, int64_t m, int64_t k);
+int mq_mul_mat(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m, float *y,
+               int64_t ldy, void *workspace, size_t workspace_bytes, void *stream);
+int mq_mul_mat_ex(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m,
+                  float *y, int64_t ldy, void *workspace, size_t workspace_bytes, int path, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,63 @@
+"""Device plumbing for the GPU tests: torch owns the memory, libmq does the work."""
+import ctypes
+
+import numpy as np
+
+from crispembed_amd import mq
+
+
+def torch():
+    import torch as _t
+    return _t
+
+
+def stream():
+    return ctypes.c_void_p(torch().cuda.current_stream().cuda_stream)
+
+
+def dev(a):
+    return torch().from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch().cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def empty_u8(nbytes):
+    t = torch().empty(max(1, nbytes) + 256, dtype=torch().uint8, device="cuda")
+    off = (-t.data_ptr()) % 256
+    return t, off  # keep t alive; use t.data_ptr() + off
+
+
+def weight_image(wtype, w_gguf, n, k):
+    """Upload GGUF rows into a 256-aligned weight image and build its planes."""
+    L = mq.lib()
+    size = L.mq_weight_image_bytes(wtype, n, k)
+    assert size > 0
+    buf, off = empty_u8(size)
+    g = np.ascontiguousarray(w_gguf, dtype=np.uint8).ravel()
+    assert g.size == L.mq_gguf_bytes(wtype, n, k)
+    buf[off:off + g.size] = dev(g)
+    ptr = buf.data_ptr() + off
+    mq.check(L.mq_weight_prepare(wtype, ctypes.c_void_p(ptr), n, k, 0, n, stream()))
+    return buf, ptr
+
+
+def mul_mat(wtype, wptr, n, k, x_dev, path=mq.PATH_AUTO, y_dev=None, ldy=None, workspace=True):
+    """x_dev: torch float32 [m, ldx>=k] (row stride from the tensor)."""
+    L = mq.lib()
+    m = x_dev.shape[0]
+    ldx = x_dev.stride(0)
+    if y_dev is None:
+        y_dev = torch().empty((m, n), dtype=torch().float32, device="cuda")
+    ldy = y_dev.stride(0) if ldy is None else ldy
+    ws_ptr, ws_bytes, keep = None, 0, None
+    if workspace:
+        ws_bytes = L.mq_workspace_bytes(wtype, m, k)
+        keep, off = empty_u8(ws_bytes)
+        ws_ptr = ctypes.c_void_p(keep.data_ptr() + off)
+    mq.check(L.mq_mul_mat_ex(wtype, ctypes.c_void_p(wptr), n, k, ctypes.c_void_p(x_dev.data_ptr()), ldx, m,
+                             ctypes.c_void_p(y_dev.data_ptr()), ldy, ws_ptr, ws_bytes, path, stream()))
+    torch().cuda.synchronize()
+    return y_dev

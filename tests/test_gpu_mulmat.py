@@ -1,0 +1,110 @@
+"""GPU mul_mat (GEMM and GEMV paths) against the oracle.
+
+Bar: max|dY| / max|Y_ref| <= 1e-4, where Y_ref is (a) the fp64 integer-exact
+product of the quantized operands and (b) the oracle's ggml-order fp32 result.
+"""
+import numpy as np
+import pytest
+
+import oracle_ffi as O
+from ggml_numpy import rel_err
+from gpu_util import dev, host, mul_mat, weight_image
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+TYPES = [O.Q8_0, O.Q4_K, O.Q6_K, O.F16]
+
+
+def _mk(oracle, wtype, m, n, k, seed, act_fn=None):
+    rng = np.random.default_rng(seed)
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    if act_fn is not None:
+        x = act_fn(x)
+    w = oracle.quantize_chunk(wtype, wf)
+    return w, x
+
+
+def _check(oracle, wtype, w, x, y, k):
+    xq = oracle.quantize_act(wtype, x)
+    ex = oracle.mul_mat_exact(wtype, w, xq, k)
+    ref = oracle.mul_mat_q(wtype, w, xq, k)
+    e1, e2 = rel_err(y, ex), rel_err(y, ref)
+    assert e1 <= TOL and e2 <= TOL, (e1, e2)
+    return e1
+
+
+@pytest.mark.parametrize("wtype", TYPES)
+@pytest.mark.parametrize("m,n,k", [(37, 70, 512), (128, 128, 256), (300, 260, 768), (129, 257, 1024), (9, 33, 256)])
+def test_gemm(oracle, wtype, m, n, k):
+    from crispembed_amd import mq
+    w, x = _mk(oracle, wtype, m, n, k, m * 7 + n + k)
+    _, wp = weight_image(wtype, w, n, k)
+    y = host(mul_mat(wtype, wp, n, k, dev(x), path=mq.PATH_GEMM))
+    _check(oracle, wtype, w, x, y, k)
+
+
+@pytest.mark.parametrize("wtype", TYPES)
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("n,k", [(67, 256), (130, 2048), (20, 6144)])
+def test_gemv(oracle, wtype, m, n, k):
+    from crispembed_amd import mq
+    w, x = _mk(oracle, wtype, m, n, k, 1000 + m * 13 + n + k)
+    _, wp = weight_image(wtype, w, n, k)
+    y = host(mul_mat(wtype, wp, n, k, dev(x), path=mq.PATH_GEMV))
+    _check(oracle, wtype, w, x, y, k)
+
+
+def test_q8_0_k_tail_and_strides(oracle):
+    """k not a multiple of the 128-byte stage; row strides ldx > k and ldy > n."""
+    from crispembed_amd import mq
+    import torch
+    m, n, k = 70, 90, 96
+    w, x = _mk(oracle, O.Q8_0, m, n, k, 77)
+    _, wp = weight_image(O.Q8_0, w, n, k)
+    xpad = np.zeros((m, k + 40), np.float32)
+    xpad[:, :k] = x
+    ybuf = torch.full((m, n + 5), 7.0, device="cuda")
+    for path in (mq.PATH_GEMM,):
+        mul_mat(O.Q8_0, wp, n, k, dev(xpad)[:, :k], path=path, y_dev=ybuf, ldy=n + 5)
+        yy = host(ybuf)
+        _check(oracle, O.Q8_0, w, x, yy[:, :n], k)
+        assert np.all(yy[:, n:] == 7.0)  # columns past n untouched
+
+
+def test_library_workspace_and_auto_path(oracle):
+    from crispembed_amd import mq
+    m, n, k = 8, 64, 512
+    w, x = _mk(oracle, O.Q4_K, m, n, k, 78)
+    _, wp = weight_image(O.Q4_K, w, n, k)
+    y1 = host(mul_mat(O.Q4_K, wp, n, k, dev(x), path=mq.PATH_AUTO, workspace=False))
+    y2 = host(mul_mat(O.Q4_K, wp, n, k, dev(x), path=mq.PATH_GEMM, workspace=False))
+    _check(oracle, O.Q4_K, w, x, y1, k)
+    _check(oracle, O.Q4_K, w, x, y2, k)
+
+
+@pytest.mark.parametrize("wtype,n,k,m,act", [
+    (O.Q8_0, 1536, 384, 4096, None),          # MiniLM-L6 FFN-up
+    (O.Q4_K, 4096, 1024, 8192, None),         # XLM-R-large FFN-up
+    (O.Q4_K, 1024, 4096, 8192, "gelu"),       # XLM-R-large FFN-down on GELU(N(0,1))
+])
+def test_full_size_sampled_rows(oracle, wtype, n, k, m, act):
+    """Full-size GEMM; oracle on 40 sampled rows; GEMV on 8 of them must agree too."""
+    from crispembed_amd import mq, synth
+    rng = np.random.default_rng(n + k)
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    from crispembed_amd.mq import lib
+    import ctypes
+    w = np.empty((n, O.row_size(wtype, k)), np.uint8)
+    lib().mq_quantize_chunk(wtype, wf.ctypes.data_as(ctypes.c_void_p), w.ctypes.data_as(ctypes.c_void_p), n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    if act == "gelu":
+        x = synth.gelu_erf(x)
+    _, wp = weight_image(wtype, w, n, k)
+    xd = dev(x)
+    y = host(mul_mat(wtype, wp, n, k, xd, path=mq.PATH_GEMM))
+    rows = np.unique(np.concatenate([[0, m - 1], rng.integers(0, m, 38)]))
+    _check(oracle, wtype, w, x[rows], y[rows], k)
+    yv = host(mul_mat(wtype, wp, n, k, dev(x[rows[:8]]), path=mq.PATH_GEMV))
+    assert rel_err(yv, y[rows[:8]]) <= TOL
