@@ -57,6 +57,13 @@ def lib():
     """Load libmq.so (raises if it was not built: there is no fallback)."""
     global _lib
     if _lib is None:
+        # libmq.so and torch's bundled HIP runtime share the soname
+        # libamdhip64.so.7: importing torch first makes libmq bind to that same
+        # runtime, so torch's device pointers and streams are valid in libmq.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise MQError(f"{LIB_PATH} is missing; run `python -c 'import __graft_entry__ as g; g.build()'`")
         L = ctypes.CDLL(LIB_PATH)
