@@ -1,0 +1,220 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized MUL_MAT hot path on one MI355X.
+
+Default workload (the headline): Q4_K mul_mat at the XLM-R-large / BGE-M3 FFN
+shape -- up W[4096 x 1024] on X[8192 x 1024] (16 seq x 512 tokens) and down
+W[1024 x 4096] on GELU(X)[8192 x 4096].  One step = both mul_mats, each with its
+Q8_K activation quantization, inputs already resident in HBM.
+
+value = whole-step int8 TOPS (2*M*N*K per mul_mat / step time).
+roofline = the dominant kernel (the Q4_K GEMM): algorithmic ops per launch /
+its average launch time from HIP events on the launch stream, against the int8
+dense MFMA peak (5.0 POP/s).
+cpu_baseline = the CPU oracle (restated ggml-cpu mul_mat, C) on a bounded
+sample of token rows of the same workload, on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q8_0/Q4_K mul_mat TOPS & % roofline; MiniLM-shape embeddings/sec, 1 GPU"
+PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Dev:
+    """Device-side state for one weight matrix and its activations."""
+
+    def __init__(self, torch, L, mq, wtype, w_gguf, n, k, x, name):
+        self.wtype, self.n, self.k, self.m = wtype, n, k, x.shape[0]
+        size = L.mq_weight_image_bytes(wtype, n, k)
+        self.img = torch.zeros(size + 256, dtype=torch.uint8, device="cuda")
+        self.wp = self.img.data_ptr() + ((-self.img.data_ptr()) % 256)
+        off = self.wp - self.img.data_ptr()
+        self.img[off:off + w_gguf.size] = torch.from_numpy(w_gguf.ravel()).cuda()
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        mq.check(L.mq_weight_prepare(wtype, ctypes.c_void_p(self.wp), n, k, 0, n, s))
+        self.x = torch.from_numpy(x).cuda()
+        self.y = torch.empty((self.m, n), dtype=torch.float32, device="cuda")
+        self.wsb = L.mq_workspace_bytes(wtype, self.m, k)
+        self.ws = torch.empty(self.wsb + 256, dtype=torch.uint8, device="cuda")
+        self.wsp = self.ws.data_ptr() + ((-self.ws.data_ptr()) % 256)
+        self.name = name
+
+
+def quantize_weights(L, wtype, wf):
+    import numpy as np
+    n, k = wf.shape
+    out = np.empty(L.mq_row_size(wtype, k) * n, dtype=np.uint8)
+    got = L.mq_quantize_chunk(wtype, wf.ctypes.data_as(ctypes.c_void_p), out.ctypes.data_as(ctypes.c_void_p), n, k)
+    assert got == out.size
+    return out
+
+
+def bench_q4k_ffn(args, torch, L, mq, synth):
+    import numpy as np
+    M, H, F = 8192, 1024, 4096
+    t0 = time.time()
+    w_up = synth.normal("xlmr_ffn/W_up", (F, H), std=0.02)
+    w_dn = synth.normal("xlmr_ffn/W_down", (H, F), std=0.02)
+    x_up = synth.normal("xlmr_ffn/X_up", (M, H))
+    x_dn = synth.gelu_erf(synth.normal("xlmr_ffn/X_down_pre", (M, F)))
+    q_up = quantize_weights(L, mq.TYPE_Q4_K, w_up)
+    q_dn = quantize_weights(L, mq.TYPE_Q4_K, w_dn)
+    up = Dev(torch, L, mq, mq.TYPE_Q4_K, q_up, F, H, x_up, "up")
+    dn = Dev(torch, L, mq, mq.TYPE_Q4_K, q_dn, H, F, x_dn, "down")
+    torch.cuda.synchronize()
+    log(f"[bench] inputs ready in {time.time() - t0:.1f}s")
+    stream = torch.cuda.current_stream()
+    s = ctypes.c_void_p(stream.cuda_stream)
+    ops_up = 2.0 * M * F * H
+    ops_dn = 2.0 * M * H * F
+
+    def step(evs=None):
+        for i, d in enumerate((up, dn)):
+            mq.check(L.mq_quantize_act(d.wtype, ctypes.c_void_p(d.x.data_ptr()), d.k, d.m, d.k,
+                                       ctypes.c_void_p(d.wsp), d.wsb, mq.PATH_GEMM, s))
+            if evs is not None:
+                evs[2 * i].record(stream)
+            mq.check(L.mq_mul_mat_q(d.wtype, ctypes.c_void_p(d.wp), d.n, d.k, ctypes.c_void_p(d.wsp), d.m,
+                                    ctypes.c_void_p(d.y.data_ptr()), d.n, mq.PATH_GEMM, s))
+            if evs is not None:
+                evs[2 * i + 1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # whole-step timing: no events between launches
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / args.steps
+    # per-GEMM timing on the same stream (events bracket only the GEMM launches)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    t_up = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    t_dn = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
+    gemm_avg_ms = (t_up + t_dn) / 2
+    gemm_ops = (ops_up + ops_dn) / 2
+    achieved = gemm_ops / (gemm_avg_ms * 1e-3) / 1e12
+    res = {
+        "ms_per_step": ms_step,
+        "value": (ops_up + ops_dn) / (ms_step * 1e-3) / 1e12,
+        "gemm_up_us": t_up * 1e3,
+        "gemm_down_us": t_dn * 1e3,
+        "roofline": {
+            "kernel": "k_gemm<Q4_K> (MFMA int8, 2 limbs)",
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": PEAK_INT8_TOPS,
+            "unit": "TFLOP/s",
+            "peak_source": "MI355X dense int8 MFMA 5.0 POP/s (integer ops counted as 2*M*N*K)",
+            "frac": achieved / PEAK_INT8_TOPS,
+            "traffic": None,
+            "algorithmic_ops_per_launch": gemm_ops,
+        },
+        "x": (x_up, x_dn, q_up, q_dn),
+    }
+    return res
+
+
+def cpu_baseline_q4k(args, x_up, x_dn, q_up, q_dn):
+    """Oracle (restated ggml-cpu mul_mat in C) on a bounded row sample."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_ffi as O
+    orc = O.Oracle()
+    nthreads = int(os.environ.get("BENCH_CPU_THREADS", min(16, os.cpu_count() or 1)))
+    H, F = 1024, 4096
+    # calibrate on 32 rows, then size the sample for about args.cpu_seconds
+    t = time.perf_counter()
+    orc.mul_mat(O.Q4_K, q_up, x_up[:32], nthreads=nthreads)
+    orc.mul_mat(O.Q4_K, q_dn, x_dn[:32], nthreads=nthreads)
+    per_row = (time.perf_counter() - t) / 32
+    rows = int(max(32, min(x_up.shape[0], args.cpu_seconds / max(per_row, 1e-9))))
+    t = time.perf_counter()
+    orc.mul_mat(O.Q4_K, q_up, x_up[:rows], nthreads=nthreads)
+    orc.mul_mat(O.Q4_K, q_dn, x_dn[:rows], nthreads=nthreads)
+    dt = time.perf_counter() - t
+    ops = 2.0 * rows * (F * H + H * F)
+    return {
+        "value": ops / dt / 1e12,
+        "unit": "TOPS",
+        "cores": nthreads,
+        "kind": "port",
+        "sample": f"Q4_K up+down mul_mat incl. Q8_K activation quantization on the first {rows} of 8192 "
+                  f"token rows ({dt:.1f} s), scalar C oracle, {nthreads} threads",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--gemm-cfg", default=None, help="MQ_GEMM_CFG tile configuration (1, 2, 3)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    if args.gemm_cfg:
+        os.environ["MQ_GEMM_CFG"] = args.gemm_cfg
+    import torch
+    from crispembed_amd import mq, synth
+    L = mq.lib()
+    mq.check(L.mq_init())
+
+    r = bench_q4k_ffn(args, torch, L, mq, synth)
+    x_up, x_dn, q_up, q_dn = r.pop("x")
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline_q4k(args, x_up, x_dn, q_up, q_dn)
+    out = {
+        "metric": METRIC,
+        "value": r["value"],
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": "Q4_K mul_mat, XLM-R-large/BGE-M3 FFN shape: up W[4096x1024] x X[8192x1024] + down "
+                        "W[1024x4096] x GELU(X)[8192x4096], each with Q8_K activation quantization",
+            "tokens": 8192,
+            "weights": "fp32 N(0,0.02) -> Q4_K (ggml _ref quantizer)",
+            "gemm_up_us": round(r["gemm_up_us"], 2),
+            "gemm_down_us": round(r["gemm_down_us"], 2),
+        },
+        "roofline": r["roofline"],
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

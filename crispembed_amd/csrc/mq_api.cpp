@@ -206,7 +206,47 @@ int mq_weight_prepare(int type, void *image, int64_t n, int64_t k, int64_t row0,
 
 size_t mq_workspace_bytes(int type, int64_t m, int64_t k) {
     if (!type_ok(type) || m < 0 || k <= 0) return 0;
-    return act_planes(type, m, k).total;
+    return act_workspace_bytes(type, m, k);
+}
+
+static int resolve_path(int path, int64_t m) {
+    if (path == MQ_PATH_AUTO) path = (m <= mq_gemv_max_m()) ? MQ_PATH_GEMV : MQ_PATH_GEMM;
+    if (path == MQ_PATH_GEMV && m > 8) return fail(MQ_EINVAL, "GEMV path takes m <= 8 (m=%lld)", (long long)m);
+    if (path != MQ_PATH_GEMV && path != MQ_PATH_GEMM) return fail(MQ_EINVAL, "unknown path %d", path);
+    return path;
+}
+
+int mq_quantize_act(int type, const float *x, int64_t ldx, int64_t m, int64_t k, void *workspace,
+                    size_t workspace_bytes, int path, void *stream) {
+    if (!type_ok(type)) return fail(MQ_EUNSUPPORTED, "weight type %d is not Q8_0/Q4_K/Q6_K/F16", type);
+    if (!mq_supports(type, k)) return fail(MQ_EUNSUPPORTED, "k=%lld not supported for type %d", (long long)k, type);
+    if (!x || !workspace || m < 0 || m > INT32_MAX || ldx < k) return fail(MQ_EINVAL, "mq_quantize_act: bad arguments");
+    if (!is_aligned(workspace, 256)) return fail(MQ_EINVAL, "mq_quantize_act: workspace must be 256-byte aligned");
+    if (m == 0) return MQ_OK;
+    path = resolve_path(path, m);
+    if (path < 0) return path;
+    const bool tiled = (path == MQ_PATH_GEMM);
+    const size_t need = act_planes(type, m, k, tiled).total;
+    if (workspace_bytes < need)
+        return fail(MQ_EINVAL, "mq_quantize_act: workspace %zu bytes < %zu needed", workspace_bytes, need);
+    const hipError_t e =
+        launch_quantize_act_planar(type, x, ldx, workspace, m, k, mq_q8_0_variant(), tiled, (hipStream_t)stream);
+    return e == hipSuccess ? MQ_OK : hip_fail(e, "activation quantization");
+}
+
+int mq_mul_mat_q(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m, float *y,
+                 int64_t ldy, int path, void *stream) {
+    int rc = check_weight_shape(type, n, k);
+    if (rc) return rc;
+    if (!w_image || !workspace || !y || m < 0 || m > INT32_MAX || ldy < n) return fail(MQ_EINVAL, "mq_mul_mat_q: bad arguments");
+    if (!is_aligned(w_image, 256) || !is_aligned(workspace, 256))
+        return fail(MQ_EINVAL, "mq_mul_mat_q: weight image and workspace must be 256-byte aligned");
+    if (m == 0) return MQ_OK;
+    path = resolve_path(path, m);
+    if (path < 0) return path;
+    const hipError_t e = (path == MQ_PATH_GEMV) ? launch_gemv(type, w_image, n, k, workspace, m, y, ldy, (hipStream_t)stream)
+                                                : launch_gemm(type, w_image, n, k, workspace, m, y, ldy, (hipStream_t)stream);
+    return e == hipSuccess ? MQ_OK : hip_fail(e, path == MQ_PATH_GEMV ? "gemv" : "gemm");
 }
 
 int mq_mul_mat_ex(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m,
@@ -217,16 +257,13 @@ int mq_mul_mat_ex(int type, const void *w_image, int64_t n, int64_t k, const flo
     if (m < 0 || m > INT32_MAX || ldx < k || ldy < n) return fail(MQ_EINVAL, "mq_mul_mat: bad m/ldx/ldy");
     if (m == 0) return MQ_OK;
     if (!is_aligned(w_image, 256)) return fail(MQ_EINVAL, "mq_mul_mat: weight image must be 256-byte aligned");
-    if (path == MQ_PATH_AUTO) path = (m <= mq_gemv_max_m()) ? MQ_PATH_GEMV : MQ_PATH_GEMM;
-    if (path == MQ_PATH_GEMV && m > 8) return fail(MQ_EINVAL, "mq_mul_mat: GEMV path takes m <= 8 (m=%lld)", (long long)m);
-    if (path != MQ_PATH_GEMV && path != MQ_PATH_GEMM) return fail(MQ_EINVAL, "mq_mul_mat: unknown path %d", path);
-    const hipStream_t s = (hipStream_t)stream;
-    const size_t need = act_planes(type, m, k).total;
+    path = resolve_path(path, m);
+    if (path < 0) return path;
+    const size_t need = act_workspace_bytes(type, m, k);
     void *ws = workspace;
     if (ws) {
         if (workspace_bytes < need)
             return fail(MQ_EINVAL, "mq_mul_mat: workspace %zu bytes < %zu needed", workspace_bytes, need);
-        if (!is_aligned(ws, 256)) return fail(MQ_EINVAL, "mq_mul_mat: workspace must be 256-byte aligned");
     } else {
         int dev = 0;
         hipError_t e = hipGetDevice(&dev);
@@ -249,13 +286,11 @@ int mq_mul_mat_ex(int type, const void *w_image, int64_t n, int64_t k, const flo
             w.bytes = need;
         }
         ws = w.ptr;
+        workspace_bytes = w.bytes;
     }
-    hipError_t e = launch_quantize_act_planar(type, x, ldx, ws, m, k, mq_q8_0_variant(), s);
-    if (e != hipSuccess) return hip_fail(e, "activation quantization");
-    e = (path == MQ_PATH_GEMV) ? launch_gemv(type, w_image, n, k, ws, m, y, ldy, s)
-                               : launch_gemm(type, w_image, n, k, ws, m, y, ldy, s);
-    if (e != hipSuccess) return hip_fail(e, path == MQ_PATH_GEMV ? "gemv" : "gemm");
-    return MQ_OK;
+    rc = mq_quantize_act(type, x, ldx, m, k, ws, workspace_bytes, path, stream);
+    if (rc) return rc;
+    return mq_mul_mat_q(type, w_image, n, k, ws, m, y, ldy, path, stream);
 }
 
 int mq_mul_mat(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m, float *y,

@@ -265,7 +265,7 @@ hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const 
     if (m <= 0 || n <= 0) return hipSuccess;
     if (m > 8) return hipErrorInvalidValue;
     const WeightPlanes p = weight_planes(type, n, k);
-    const ActPlanes ap = act_planes(type, m, k);
+    const ActPlanes ap = act_planes(type, m, k, false);
     const uint8_t *wb = (const uint8_t *)image;
     const uint8_t *xb = (const uint8_t *)ws;
     switch (m) {

@@ -49,24 +49,45 @@ static_assert(sizeof(block_q8_K) == 292, "block_q8_K");
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // ---------------------------------------------------------------------------
+// Tiled ("fragment-major") int8 planes, read by the MFMA GEMM.
+// Rows are padded to TILE_ROWS, the K bytes of a row to KSTAGE.  The plane is a
+// sequence of 1 KB fragments, one per (32-row tile rt, 32-byte K chunk kc), at
+// ((rt * kb_pad/32) + kc) * 1024; inside a fragment lane l's 16 bytes hold row
+// rt*32 + l%32, bytes kc*32 + 16*(l/32) .. +16 -- exactly the operand a lane
+// feeds to a 32x32x32 int8 (or 32x32x16 fp16) MFMA.  A wave moves one fragment
+// with one 16-byte-per-lane load, global -> LDS -> registers, all contiguous.
+// ---------------------------------------------------------------------------
+constexpr int TILE_ROWS = 256;
+constexpr int KSTAGE = 128;
+
+__host__ __device__ inline int64_t pad_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+__host__ __device__ inline int64_t tiled_off(int64_t r, int64_t kb, int64_t kb_pad) {
+    const int64_t rt = r >> 5, lr = r & 31, kc = kb >> 5, w = kb & 31;
+    return ((((rt * (kb_pad >> 5) + kc) << 6) + ((w >> 4) << 5) + lr) << 4) + (w & 15);
+}
+
+// ---------------------------------------------------------------------------
 // Weight image: GGUF bytes, then planes (each 256-byte aligned).
+//  GEMV planes (row-major, byte-identical to the GGUF fields):
 //   Q8_0: qs  i8 [n][k]            d16  u16 [n][k/32]
-//   Q4_K: lo  i8 [n][k]  hi i8 [n][k]   (sc_j*q4 = lo + 128*hi, lo in [0,127])
-//         dw  f32 [n][k/256]  dmin f32 [n][k/256]  mins f16 [n][k/256][8]
-//   Q6_K: lo  i8 [n][k]  hi i8 [n][k]   (sc*(q6-32) = lo + 128*hi)
-//         dw  f32 [n][k/256]
-//         ql  u8 [n][k/2]  qh u8 [n][k/4]  sc i8 [n][k/16]  d16 u16 [n][k/256]
-//   F16 : no planes (the GGUF rows are already k-contiguous fp16)
+//   Q6_K: ql  u8 [n][k/2]  qh u8 [n][k/4]  sc i8 [n][k/16]  d16 u16 [n][k/256]
+//   (Q4_K and F16 GEMVs read the GGUF rows directly)
+//  GEMM planes (tiled, n padded to n_pad = pad(n, 256)):
+//   Q8_0: tq  i8 tiled [n_pad][kb_pad]     tdw f32 [kb_pad/32][n_pad]
+//   Q4_K: tq (lo limb), thi (hi limb) i8 tiled [n_pad][k]: sc_j*q4 = lo + 128*hi,
+//         lo in [0,127], hi in [0,7]
+//         tdw, tdmin f32 [k/256][n_pad]
+//         tmin f16 fragments [n_pad/32][k/256][64 lanes][8]: lane l holds m_0..m_7
+//         of column l%32 (both lane halves), the B operand of the min-term MFMA
+//   Q6_K: tq, thi limbs of sc*(q6-32) (lo in [0,127], hi in [-32,32]); tdw
+//   F16 : tq  f16 tiled [n_pad][kb_pad bytes]
 // ---------------------------------------------------------------------------
 struct WeightPlanes {
-    size_t gguf = 0;   // bytes of the GGUF part
-    size_t qs = 0;     // Q8_0 int8 plane / Q4_K,Q6_K lo limb
-    size_t hi = 0;     // hi limb
-    size_t dw = 0;     // f32 per-superblock d (K-quants)
-    size_t dmin = 0;   // f32 per-superblock dmin (Q4_K)
-    size_t mins = 0;   // f16 mins (Q4_K)
-    size_t d16 = 0;    // fp16 scale plane (Q8_0 per block, Q6_K per superblock)
-    size_t ql = 0, qh = 0, sc = 0;  // Q6_K streaming planes
+    size_t gguf = 0;
+    size_t qs = 0, d16 = 0, ql = 0, qh = 0, sc = 0;        // GEMV planes
+    size_t tq = 0, thi = 0, tdw = 0, tdmin = 0, tmin = 0;  // GEMM planes
+    int64_t n_pad = 0, kb_pad = 0;
     size_t total = 0;
 };
 
@@ -99,11 +120,20 @@ inline size_t row_size(int type, int64_t k) {
     return b ? (size_t)(k / b) * type_size(type) : 0;
 }
 
+// bytes of K per row in the GEMM operand planes (int8 formats: k; F16: 2k), padded
+inline int64_t gemm_kb_pad(int type, int64_t k) {
+    return pad_up(type == MQ_TYPE_F16 ? 2 * k : k, KSTAGE);
+}
+
 inline WeightPlanes weight_planes(int type, int64_t n, int64_t k) {
     WeightPlanes p;
     p.gguf = row_size(type, k) * (size_t)n;
+    p.n_pad = pad_up(n, TILE_ROWS);
+    p.kb_pad = gemm_kb_pad(type, k);
     size_t off = align256(p.gguf);
     const size_t nk = (size_t)n * (size_t)k;
+    const size_t tiled = (size_t)p.n_pad * (size_t)p.kb_pad;
+    const size_t nsb = (size_t)(k / QK_K);
     auto take = [&](size_t bytes) {
         const size_t o = off;
         off = align256(off + bytes);
@@ -113,70 +143,113 @@ inline WeightPlanes weight_planes(int type, int64_t n, int64_t k) {
         case MQ_TYPE_Q8_0:
             p.qs = take(nk);
             p.d16 = take(nk / QK8_0 * 2);
+            p.tq = take(tiled);
+            p.tdw = take((size_t)(p.kb_pad / QK8_0) * p.n_pad * 4);
             break;
         case MQ_TYPE_Q4_K:
-            p.qs = take(nk);
-            p.hi = take(nk);
-            p.dw = take(nk / QK_K * 4);
-            p.dmin = take(nk / QK_K * 4);
-            p.mins = take(nk / QK_K * 8 * 2);
+            p.tq = take(tiled);
+            p.thi = take(tiled);
+            p.tdw = take(nsb * p.n_pad * 4);
+            p.tdmin = take(nsb * p.n_pad * 4);
+            p.tmin = take((size_t)(p.n_pad / 32) * nsb * 1024);
             break;
         case MQ_TYPE_Q6_K:
-            p.qs = take(nk);
-            p.hi = take(nk);
-            p.dw = take(nk / QK_K * 4);
             p.ql = take(nk / 2);
             p.qh = take(nk / 4);
             p.sc = take(nk / 16);
             p.d16 = take(nk / QK_K * 2);
+            p.tq = take(tiled);
+            p.thi = take(tiled);
+            p.tdw = take(nsb * p.n_pad * 4);
             break;
+        case MQ_TYPE_F16: p.tq = take(tiled); break;
         default: break;
     }
-    p.total = (type == MQ_TYPE_F16) ? p.gguf : off;
+    p.total = off;
     return p;
 }
 
 // ---------------------------------------------------------------------------
-// Activation workspace (planar quantized X, m rows):
+// Activation workspace.
+//  Row-major layout (GEMV path, m <= 8):
 //   Q8_0: xq i8 [m][k]   xd f32 [m][k/32]      (xd holds the fp16 d widened exactly)
 //   Q8_K: xq i8 [m][k]   xd f32 [m][k/256]   xbs i16 [m][k/16]  (ggml's bsums)
-//   F16 : xh f16 [m][k]
+//   F16 : xq f16 [m][k]
+//  Tiled layout (GEMM path, m padded to m_pad = pad(m, 256), pad rows zero):
+//   Q8_0: xq i8 tiled [m_pad][kb_pad]   xd f32 [kb_pad/32][m_pad]
+//   Q8_K: xq i8 tiled [m_pad][k]        xd f32 [k/256][m_pad]
+//         xmin f16 fragments [m_pad/32][k/256][64 lanes][8]: lane l, row l%32, holds
+//         B_j & 63 (lanes 0-31) or 64*(B_j >> 6) (lanes 32-63) for j = 0..7, where
+//         B_j = the sum of the 32 quants of sub-block j: the A operand of the
+//         min-term MFMA
+//   F16 : xq f16 tiled [m_pad][kb_pad bytes]
 // ---------------------------------------------------------------------------
 struct ActPlanes {
-    size_t xq = 0, xd = 0, xbs = 0, total = 0;
+    size_t xq = 0, xd = 0, xbs = 0, xmin = 0, total = 0;
+    int64_t m_pad = 0, kb_pad = 0;
+    bool tiled = false;
 };
 
-inline ActPlanes act_planes(int wtype, int64_t m, int64_t k) {
+inline ActPlanes act_planes(int wtype, int64_t m, int64_t k, bool tiled) {
     ActPlanes a;
-    const size_t mk = (size_t)m * (size_t)k;
+    a.tiled = tiled;
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;
         off = align256(off + bytes);
         return o;
     };
-    switch (wtype) {
-        case MQ_TYPE_Q8_0:
-            a.xq = take(mk);
-            a.xd = take(mk / QK8_0 * 4);
-            break;
-        case MQ_TYPE_Q4_K:
-        case MQ_TYPE_Q6_K:
-            a.xq = take(mk);
-            a.xd = take(mk / QK_K * 4);
-            a.xbs = take(mk / 16 * 2);
-            break;
-        case MQ_TYPE_F16: a.xq = take(mk * 2); break;
-        default: break;
+    if (!tiled) {
+        const size_t mk = (size_t)m * (size_t)k;
+        a.m_pad = m;
+        a.kb_pad = (wtype == MQ_TYPE_F16) ? 2 * k : k;
+        switch (wtype) {
+            case MQ_TYPE_Q8_0:
+                a.xq = take(mk);
+                a.xd = take(mk / QK8_0 * 4);
+                break;
+            case MQ_TYPE_Q4_K:
+            case MQ_TYPE_Q6_K:
+                a.xq = take(mk);
+                a.xd = take(mk / QK_K * 4);
+                a.xbs = take(mk / 16 * 2);
+                break;
+            case MQ_TYPE_F16: a.xq = take(mk * 2); break;
+            default: break;
+        }
+    } else {
+        a.m_pad = pad_up(m, TILE_ROWS);
+        a.kb_pad = gemm_kb_pad(wtype, k);
+        const size_t t = (size_t)a.m_pad * (size_t)a.kb_pad;
+        const size_t nsb = (size_t)(k / QK_K);
+        switch (wtype) {
+            case MQ_TYPE_Q8_0:
+                a.xq = take(t);
+                a.xd = take((size_t)(a.kb_pad / QK8_0) * a.m_pad * 4);
+                break;
+            case MQ_TYPE_Q4_K:
+            case MQ_TYPE_Q6_K:
+                a.xq = take(t);
+                a.xd = take(nsb * a.m_pad * 4);
+                a.xmin = take((size_t)(a.m_pad / 32) * nsb * 1024);
+                break;
+            case MQ_TYPE_F16: a.xq = take(t); break;
+            default: break;
+        }
     }
     a.total = off;
     return a;
 }
 
+inline size_t act_workspace_bytes(int wtype, int64_t m, int64_t k) {
+    const size_t r = act_planes(wtype, m, k, false).total, t = act_planes(wtype, m, k, true).total;
+    return r > t ? r : t;
+}
+
 // ---- launchers (defined in the .hip files; return hipError_t) ----
 // Quantize m rows of x (stride ldx floats) into the planar workspace layout.
 hipError_t launch_quantize_act_planar(int wtype, const float *x, int64_t ldx, void *ws, int64_t m, int64_t k,
-                                      int q8_0_variant, hipStream_t s);
+                                      int q8_0_variant, bool tiled, hipStream_t s);
 hipError_t launch_quantize_q8_0_gguf(const float *x, int64_t ldx, void *y, int64_t m, int64_t k, int variant,
                                      hipStream_t s);
 hipError_t launch_quantize_q8_K_gguf(const float *x, int64_t ldx, void *y, int64_t m, int64_t k, hipStream_t s);

@@ -32,22 +32,31 @@ __device__ __forceinline__ float4 load4(const float *p) {
     return make_float4(p[0], p[1], p[2], p[3]);
 }
 
+// Output layouts of the activation quantizers.
+enum { OUT_GGUF = 0, OUT_ROWS = 1, OUT_TILED = 2 };
+
 // ---------------------------------------------------------------------------
 // Q8_0 activations: quantize_row_q8_0 (variant selects the rounding).
 // Lanes 8g..8g+7 of a wave own one 32-value block.
-// PLANAR: xq int8 [m][k] + xd float [m][k/32]; else GGUF block_q8_0 rows.
+// OUT_ROWS : xq int8 [m][k] + xd float [m][k/32]
+// OUT_TILED: xq tiled [m_pad][kb_pad] + xd float [kb_pad/32][m_pad]; blocks past
+//            m or k are written as zeros (d = 0)
+// OUT_GGUF : block_q8_0 rows
 // ---------------------------------------------------------------------------
-template <int VARIANT, bool PLANAR, bool VEC4>
+template <int VARIANT, int OUT, bool VEC4>
 __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__ x, int64_t ldx,
                                                        int8_t *__restrict__ out, float *__restrict__ xd,
-                                                       int64_t m, int64_t k) {
+                                                       int64_t m, int64_t k, int64_t m_pad, int64_t kb_pad) {
     const int64_t nbr = k / QK8_0;
+    const int64_t nbx = (OUT == OUT_TILED) ? kb_pad / QK8_0 : nbr;
+    const int64_t rows = (OUT == OUT_TILED) ? m_pad : m;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t blk = gid >> 3;
     const int sub = (int)(gid & 7);
-    if (blk >= m * nbr) return;  // 8-lane groups leave together
-    const int64_t row = blk / nbr, b = blk - row * nbr;
-    const float4 v = load4<VEC4>(x + row * ldx + b * QK8_0 + sub * 4);
+    if (blk >= rows * nbx) return;  // 8-lane groups leave together
+    const int64_t row = blk / nbx, b = blk - row * nbx;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (row < m && b < nbr) v = load4<VEC4>(x + row * ldx + b * QK8_0 + sub * 4);
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
     amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
@@ -64,9 +73,12 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__
     };
     const uint32_t packed = q(v.x) | (q(v.y) << 8) | (q(v.z) << 16) | (q(v.w) << 24);
     const uint16_t dh = f32_to_f16_bits(d);
-    if (PLANAR) {
+    if (OUT == OUT_ROWS) {
         *(uint32_t *)(out + row * k + b * QK8_0 + sub * 4) = packed;
         if (sub == 0) xd[row * nbr + b] = f16_bits_to_f32(dh);
+    } else if (OUT == OUT_TILED) {
+        *(uint32_t *)(out + tiled_off(row, b * QK8_0 + sub * 4, kb_pad)) = packed;
+        if (sub == 0) xd[b * m_pad + row] = f16_bits_to_f32(dh);
     } else {
         uint8_t *blkp = (uint8_t *)out + (row * nbr + b) * sizeof(block_q8_0);
         uint16_t *qs16 = (uint16_t *)(blkp + 2 + sub * 4);  // 2-byte aligned in the 34-byte block
@@ -80,18 +92,24 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__
 // Q8_K activations: quantize_row_q8_K.  One wave per 256-value block; lane l
 // owns values 4l..4l+3.  max is the FIRST value of largest magnitude: the
 // reduction orders (|x| descending, index ascending).
-// PLANAR: xq int8 [m][k], xd float [m][k/256], xbs int16 [m][k/16].
+// OUT_ROWS : xq int8 [m][k], xd float [m][k/256], xbs int16 [m][k/16]
+// OUT_TILED: xq tiled [m_pad][k], xd float [k/256][m_pad], xmin fragments
+//            (rows past m are written as zeros)
+// OUT_GGUF : block_q8_K rows
 // ---------------------------------------------------------------------------
-template <bool PLANAR, bool VEC4>
+template <int OUT, bool VEC4>
 __global__ __launch_bounds__(256) void k_quantize_q8_K(const float *__restrict__ x, int64_t ldx,
                                                        int8_t *__restrict__ out, float *__restrict__ xd,
-                                                       int16_t *__restrict__ xbs, int64_t m, int64_t k) {
+                                                       int16_t *__restrict__ xbs, _Float16 *__restrict__ xmin,
+                                                       int64_t m, int64_t k, int64_t m_pad) {
     const int64_t nbr = k / QK_K;
+    const int64_t rows = (OUT == OUT_TILED) ? m_pad : m;
     const int lane = threadIdx.x & 63;
     const int64_t blk = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    if (blk >= m * nbr) return;  // whole waves leave together
+    if (blk >= rows * nbr) return;  // whole waves leave together
     const int64_t row = blk / nbr, b = blk - row * nbr;
-    const float4 v = load4<VEC4>(x + row * ldx + b * QK_K + lane * 4);
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (row < m) v = load4<VEC4>(x + row * ldx + b * QK_K + lane * 4);
     const float vals[4] = {v.x, v.y, v.z, v.w};
     float amax = 0.0f, mx = 0.0f;
     int idx = 0x7fffffff;
@@ -131,10 +149,21 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const float *__restrict__
     }
     s16 += __shfl_xor(s16, 1);
     s16 += __shfl_xor(s16, 2);
-    if (PLANAR) {
+    if (OUT == OUT_ROWS) {
         *(uint32_t *)(out + row * k + b * QK_K + lane * 4) = packed;
         if ((lane & 3) == 0) xbs[row * (k / 16) + b * 16 + (lane >> 2)] = (int16_t)s16;
         if (lane == 0) xd[row * nbr + b] = dval;
+    } else if (OUT == OUT_TILED) {
+        *(uint32_t *)(out + tiled_off(row, b * QK_K + lane * 4, k)) = packed;
+        if (lane == 0) xd[b * m_pad + row] = dval;
+        // B_j (sum of the 32 quants of sub-block j) lands in lane 8j
+        const int B = s16 + __shfl_xor(s16, 4);
+        if ((lane & 7) == 0) {
+            const int j = lane >> 3;
+            _Float16 *frag = xmin + (((row >> 5) * nbr + b) << 9);  // 1 KB = 512 halves
+            frag[((row & 31) << 3) + j] = (_Float16)(B & 63);
+            frag[((32 + (row & 31)) << 3) + j] = (_Float16)((B >> 6) * 64);
+        }
     } else {
         uint8_t *blkp = (uint8_t *)out + (row * nbr + b) * sizeof(block_q8_K);
         *(uint32_t *)(blkp + 4 + lane * 4) = packed;
@@ -157,6 +186,24 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
     o[1] = f32_to_f16_bits(v.y);
     o[2] = f32_to_f16_bits(v.z);
     o[3] = f32_to_f16_bits(v.w);
+}
+
+// fp32 -> fp16 into the tiled plane [m_pad][kb_pad bytes]; 4 values (8 bytes) per lane.
+template <bool VEC4>
+__global__ __launch_bounds__(256) void k_quantize_f16_tiled(const float *__restrict__ x, int64_t ldx,
+                                                            uint8_t *__restrict__ y, int64_t m, int64_t k,
+                                                            int64_t m_pad, int64_t kb_pad) {
+    const int64_t q8 = kb_pad / 8;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= m_pad * q8) return;
+    const int64_t row = gid / q8, c = gid - row * q8;
+    uint2 o = make_uint2(0u, 0u);
+    if (row < m && c * 4 < k) {
+        const float4 v = load4<VEC4>(x + row * ldx + c * 4);
+        o.x = (uint32_t)f32_to_f16_bits(v.x) | ((uint32_t)f32_to_f16_bits(v.y) << 16);
+        o.y = (uint32_t)f32_to_f16_bits(v.z) | ((uint32_t)f32_to_f16_bits(v.w) << 16);
+    }
+    *(uint2 *)(y + tiled_off(row, c * 8, kb_pad)) = o;
 }
 
 // ---------------------------------------------------------------------------
@@ -224,11 +271,14 @@ __global__ __launch_bounds__(256) void k_dequantize(const uint8_t *__restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// Weight-plane preparation: one thread per (row, GGUF block).
+// Weight-plane preparation.  GEMV planes: one thread per (row, GGUF block) for
+// rows [row0, row1).  GEMM planes: one thread per (row, block) for rows
+// [row0, row_end) where row_end extends to n_pad when the range reaches n, so the
+// padding rows (and the K padding) are written as zeros.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_prepare_q8_0(const uint8_t *__restrict__ gguf, int8_t *__restrict__ qs,
-                                                      uint16_t *__restrict__ d16, int64_t row0, int64_t row1,
-                                                      int64_t k) {
+__global__ __launch_bounds__(256) void k_prepare_q8_0_rows(const uint8_t *__restrict__ gguf, int8_t *__restrict__ qs,
+                                                           uint16_t *__restrict__ d16, int64_t row0, int64_t row1,
+                                                           int64_t k) {
     const int64_t nbr = k / QK8_0;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= (row1 - row0) * nbr) return;
@@ -241,69 +291,150 @@ __global__ __launch_bounds__(256) void k_prepare_q8_0(const uint8_t *__restrict_
     for (int i = 0; i < 8; i++) dst[i] = (uint32_t)s16[2 * i] | ((uint32_t)s16[2 * i + 1] << 16);
 }
 
-__global__ __launch_bounds__(256) void k_prepare_q4_K(const uint8_t *__restrict__ gguf, int8_t *__restrict__ lo,
-                                                      int8_t *__restrict__ hi, float *__restrict__ dw,
-                                                      float *__restrict__ dmin, _Float16 *__restrict__ mins,
-                                                      int64_t row0, int64_t row1, int64_t k) {
+__global__ __launch_bounds__(256) void k_prepare_q8_0_tiled(const uint8_t *__restrict__ gguf, int8_t *__restrict__ tq,
+                                                            float *__restrict__ tdw, int64_t n, int64_t row0,
+                                                            int64_t row_end, int64_t k, int64_t n_pad,
+                                                            int64_t kb_pad) {
+    const int64_t nbr = k / QK8_0, nbx = kb_pad / QK8_0;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (row_end - row0) * nbx) return;
+    const int64_t row = row0 + gid / nbx, b = gid % nbx;
+    uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float d = 0.f;
+    if (row < n && b < nbr) {
+        const uint8_t *src = gguf + (row * nbr + b) * sizeof(block_q8_0);
+        d = f16_bits_to_f32(*(const uint16_t *)src);
+        const uint16_t *s16 = (const uint16_t *)(src + 2);
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i] = (uint32_t)s16[2 * i] | ((uint32_t)s16[2 * i + 1] << 16);
+    }
+    *(uint4 *)(tq + tiled_off(row, b * QK8_0, kb_pad)) = make_uint4(w[0], w[1], w[2], w[3]);
+    *(uint4 *)(tq + tiled_off(row, b * QK8_0 + 16, kb_pad)) = make_uint4(w[4], w[5], w[6], w[7]);
+    tdw[b * n_pad + row] = d;
+}
+
+__device__ __forceinline__ uint4 pack16(const int *v) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        w[i] = (uint32_t)(v[4 * i] & 0xff) | ((uint32_t)(v[4 * i + 1] & 0xff) << 8) |
+               ((uint32_t)(v[4 * i + 2] & 0xff) << 16) | ((uint32_t)(v[4 * i + 3] & 0xff) << 24);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Q4_K: limbs of sc_j * q4 (lo = v & 127, hi = v >> 7), per-superblock scales, min fragment.
+__global__ __launch_bounds__(256) void k_prepare_q4_K_tiled(const uint8_t *__restrict__ gguf, int8_t *__restrict__ tlo,
+                                                            int8_t *__restrict__ thi, float *__restrict__ tdw,
+                                                            float *__restrict__ tdmin, _Float16 *__restrict__ tmin,
+                                                            int64_t n, int64_t row0, int64_t row_end, int64_t k,
+                                                            int64_t n_pad) {
     const int64_t nbr = k / QK_K;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (row1 - row0) * nbr) return;
+    if (gid >= (row_end - row0) * nbr) return;
     const int64_t row = row0 + gid / nbr, b = gid % nbr;
+    const bool valid = row < n;
     const uint8_t *src = gguf + (row * nbr + b) * sizeof(block_q4_K);
-    const int64_t sbi = row * nbr + b;
-    dw[sbi] = f16_bits_to_f32(*(const uint16_t *)src);
-    dmin[sbi] = f16_bits_to_f32(*(const uint16_t *)(src + 2));
     int sc[8], mn[8];
+    float d = 0.f, dmin = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) sc[j] = mn[j] = 0;
+    if (valid) {
+        d = f16_bits_to_f32(*(const uint16_t *)src);
+        dmin = f16_bits_to_f32(*(const uint16_t *)(src + 2));
+#pragma unroll
+        for (int j = 0; j < 8; j++) scale_min_k4(j, src + 4, sc[j], mn[j]);
+    }
+    tdw[b * n_pad + row] = d;
+    tdmin[b * n_pad + row] = dmin;
+    _Float16 *frag = tmin + (((row >> 5) * nbr + b) << 9);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        scale_min_k4(j, src + 4, sc[j], mn[j]);
-        mins[sbi * 8 + j] = (_Float16)mn[j];
+        frag[((row & 31) << 3) + j] = (_Float16)mn[j];
+        frag[((32 + (row & 31)) << 3) + j] = (_Float16)mn[j];
     }
-    int8_t *plo = lo + row * k + b * QK_K;
-    int8_t *phi = hi + row * k + b * QK_K;
-    for (int c = 0; c < 4; c++) {
-        for (int l = 0; l < 32; l++) {
-            const uint8_t byte = src[16 + 32 * c + l];
-            const int v0 = sc[2 * c] * (byte & 0xF);       // value 64c + l
-            const int v1 = sc[2 * c + 1] * (byte >> 4);    // value 64c + 32 + l
-            plo[64 * c + l] = (int8_t)(v0 & 127);
-            phi[64 * c + l] = (int8_t)(v0 >> 7);
-            plo[64 * c + 32 + l] = (int8_t)(v1 & 127);
-            phi[64 * c + 32 + l] = (int8_t)(v1 >> 7);
+    for (int t = 0; t < 16; t++) {  // 16 chunks of 16 values
+        const int c = t >> 2, part = t & 3;
+        const int j = 2 * c + (part >> 1);
+        int lo[16], hi[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            int q = 0;
+            if (valid) {
+                const uint8_t byte = src[16 + 32 * c + 16 * (part & 1) + i];
+                q = (part < 2) ? (byte & 0xF) : (byte >> 4);
+            }
+            const int v = sc[j] * q;
+            lo[i] = v & 127;
+            hi[i] = v >> 7;
         }
+        const int64_t off = tiled_off(row, b * QK_K + 16 * t, k);
+        *(uint4 *)(tlo + off) = pack16(lo);
+        *(uint4 *)(thi + off) = pack16(hi);
     }
 }
 
-__global__ __launch_bounds__(256) void k_prepare_q6_K(const uint8_t *__restrict__ gguf, int8_t *__restrict__ lo,
-                                                      int8_t *__restrict__ hi, float *__restrict__ dw,
-                                                      uint8_t *__restrict__ ql, uint8_t *__restrict__ qh,
-                                                      int8_t *__restrict__ scp, uint16_t *__restrict__ d16,
-                                                      int64_t row0, int64_t row1, int64_t k) {
+__global__ __launch_bounds__(256) void k_prepare_q6_K_rows(const uint8_t *__restrict__ gguf, uint8_t *__restrict__ ql,
+                                                           uint8_t *__restrict__ qh, int8_t *__restrict__ scp,
+                                                           uint16_t *__restrict__ d16, int64_t row0, int64_t row1,
+                                                           int64_t k) {
     const int64_t nbr = k / QK_K;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= (row1 - row0) * nbr) return;
     const int64_t row = row0 + gid / nbr, b = gid % nbr;
     const uint8_t *src = gguf + (row * nbr + b) * sizeof(block_q6_K);
     const int64_t sbi = row * nbr + b;
-    const uint16_t dbits = *(const uint16_t *)(src + 208);
-    d16[sbi] = dbits;
-    dw[sbi] = f16_bits_to_f32(dbits);
+    d16[sbi] = *(const uint16_t *)(src + 208);
     for (int i = 0; i < 128; i++) ql[sbi * 128 + i] = src[i];
     for (int i = 0; i < 64; i++) qh[sbi * 64 + i] = src[128 + i];
     for (int i = 0; i < 16; i++) scp[sbi * 16 + i] = (int8_t)src[192 + i];
-    int8_t *plo = lo + row * k + b * QK_K;
-    int8_t *phi = hi + row * k + b * QK_K;
-    for (int e = 0; e < QK_K; e++) {
-        const int h = e >> 7, rr = e & 127, g = rr >> 5, l = rr & 31;
-        const uint8_t qlb = src[64 * h + l + (g & 1) * 32];
-        const int nib = (g < 2) ? (qlb & 0xF) : (qlb >> 4);
-        const int hb = (src[128 + 32 * h + l] >> (2 * g)) & 3;
-        const int qv = (nib | (hb << 4)) - 32;
-        const int sc = (int8_t)src[192 + 8 * h + (l >> 4) + 2 * g];
-        const int v = sc * qv;  // in [-4064, 4096]
-        plo[e] = (int8_t)(v & 127);
-        phi[e] = (int8_t)(v >> 7);  // arithmetic shift: v = lo + 128*hi
+}
+
+// Q6_K: limbs of sc * (q6 - 32) (lo = v & 127, hi = v >> 7 arithmetic), per-superblock d.
+__global__ __launch_bounds__(256) void k_prepare_q6_K_tiled(const uint8_t *__restrict__ gguf, int8_t *__restrict__ tlo,
+                                                            int8_t *__restrict__ thi, float *__restrict__ tdw,
+                                                            int64_t n, int64_t row0, int64_t row_end, int64_t k,
+                                                            int64_t n_pad) {
+    const int64_t nbr = k / QK_K;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (row_end - row0) * nbr) return;
+    const int64_t row = row0 + gid / nbr, b = gid % nbr;
+    const bool valid = row < n;
+    const uint8_t *src = gguf + (row * nbr + b) * sizeof(block_q6_K);
+    tdw[b * n_pad + row] = valid ? f16_bits_to_f32(*(const uint16_t *)(src + 208)) : 0.f;
+    for (int t = 0; t < 16; t++) {  // 16 chunks of 16 values
+        const int h = t >> 3, g = (t & 7) >> 1, l0 = (t & 1) * 16;
+        const int sc = valid ? (int)(int8_t)src[192 + 8 * h + (l0 >> 4) + 2 * g] : 0;
+        int lo[16], hi[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            int v = 0;
+            if (valid) {
+                const int l = l0 + i;
+                const uint8_t qlb = src[64 * h + l + (g & 1) * 32];
+                const int nib = (g < 2) ? (qlb & 0xF) : (qlb >> 4);
+                const int hb = (src[128 + 32 * h + l] >> (2 * g)) & 3;
+                v = sc * ((nib | (hb << 4)) - 32);  // in [-4064, 4096]
+            }
+            lo[i] = v & 127;
+            hi[i] = v >> 7;
+        }
+        const int64_t off = tiled_off(row, b * QK_K + 16 * t, k);
+        *(uint4 *)(tlo + off) = pack16(lo);
+        *(uint4 *)(thi + off) = pack16(hi);
     }
+}
+
+// F16: copy the GGUF rows into the tiled plane, 16 bytes per thread.
+__global__ __launch_bounds__(256) void k_prepare_f16_tiled(const uint8_t *__restrict__ gguf, uint8_t *__restrict__ tq,
+                                                           int64_t n, int64_t row0, int64_t row_end, int64_t k,
+                                                           int64_t kb_pad) {
+    const int64_t np = kb_pad / 16;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (row_end - row0) * np) return;
+    const int64_t row = row0 + gid / np, c = gid % np;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row < n && 16 * c < 2 * k) v = *(const uint4 *)(gguf + row * 2 * k + 16 * c);
+    *(uint4 *)(tq + tiled_off(row, 16 * c, kb_pad)) = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -315,16 +446,18 @@ static inline bool aligned16(const void *p, int64_t ld_floats) {
 
 static inline unsigned grid_for(int64_t threads) { return (unsigned)((threads + 255) / 256); }
 
-template <bool PLANAR>
+template <int OUT>
 static hipError_t q8_0_dispatch(const float *x, int64_t ldx, int8_t *out, float *xd, int64_t m, int64_t k, int variant,
-                                hipStream_t s) {
-    const int64_t threads = m * (k / QK8_0) * 8;
+                                int64_t m_pad, int64_t kb_pad, hipStream_t s) {
+    const int64_t rows = (OUT == OUT_TILED) ? m_pad : m;
+    const int64_t nbx = (OUT == OUT_TILED) ? kb_pad / QK8_0 : k / QK8_0;
+    const int64_t threads = rows * nbx * 8;
     if (threads == 0) return hipSuccess;
     const bool v4 = aligned16(x, ldx);
     const dim3 g(grid_for(threads)), b(256);
-#define MQ_Q80(VAR)                                                                                      \
-    if (v4) hipLaunchKernelGGL((k_quantize_q8_0<VAR, PLANAR, true>), g, b, 0, s, x, ldx, out, xd, m, k); \
-    else hipLaunchKernelGGL((k_quantize_q8_0<VAR, PLANAR, false>), g, b, 0, s, x, ldx, out, xd, m, k);
+#define MQ_Q80(VAR)                                                                                             \
+    if (v4) hipLaunchKernelGGL((k_quantize_q8_0<VAR, OUT, true>), g, b, 0, s, x, ldx, out, xd, m, k, m_pad, kb_pad); \
+    else hipLaunchKernelGGL((k_quantize_q8_0<VAR, OUT, false>), g, b, 0, s, x, ldx, out, xd, m, k, m_pad, kb_pad);
     switch (variant) {
         case MQ_Q8_0_X86: MQ_Q80(MQ_Q8_0_X86); break;
         case MQ_Q8_0_NEON: MQ_Q80(MQ_Q8_0_NEON); break;
@@ -335,16 +468,17 @@ static hipError_t q8_0_dispatch(const float *x, int64_t ldx, int8_t *out, float 
     return hipGetLastError();
 }
 
-template <bool PLANAR>
-static hipError_t q8_K_dispatch(const float *x, int64_t ldx, int8_t *out, float *xd, int16_t *xbs, int64_t m,
-                                int64_t k, hipStream_t s) {
-    const int64_t threads = m * (k / QK_K) * 64;
+template <int OUT>
+static hipError_t q8_K_dispatch(const float *x, int64_t ldx, int8_t *out, float *xd, int16_t *xbs, _Float16 *xmin,
+                                int64_t m, int64_t k, int64_t m_pad, hipStream_t s) {
+    const int64_t rows = (OUT == OUT_TILED) ? m_pad : m;
+    const int64_t threads = rows * (k / QK_K) * 64;
     if (threads == 0) return hipSuccess;
     const dim3 g(grid_for(threads)), b(256);
     if (aligned16(x, ldx))
-        hipLaunchKernelGGL((k_quantize_q8_K<PLANAR, true>), g, b, 0, s, x, ldx, out, xd, xbs, m, k);
+        hipLaunchKernelGGL((k_quantize_q8_K<OUT, true>), g, b, 0, s, x, ldx, out, xd, xbs, xmin, m, k, m_pad);
     else
-        hipLaunchKernelGGL((k_quantize_q8_K<PLANAR, false>), g, b, 0, s, x, ldx, out, xd, xbs, m, k);
+        hipLaunchKernelGGL((k_quantize_q8_K<OUT, false>), g, b, 0, s, x, ldx, out, xd, xbs, xmin, m, k, m_pad);
     return hipGetLastError();
 }
 
@@ -360,28 +494,41 @@ hipError_t launch_quantize_f16(const float *x, int64_t ldx, void *y, int64_t m, 
 }
 
 hipError_t launch_quantize_act_planar(int wtype, const float *x, int64_t ldx, void *ws, int64_t m, int64_t k,
-                                      int q8_0_variant, hipStream_t s) {
-    const ActPlanes a = act_planes(wtype, m, k);
+                                      int q8_0_variant, bool tiled, hipStream_t s) {
+    const ActPlanes a = act_planes(wtype, m, k, tiled);
     uint8_t *base = (uint8_t *)ws;
+    int8_t *xq = (int8_t *)(base + a.xq);
+    float *xd = (float *)(base + a.xd);
     switch (wtype) {
         case MQ_TYPE_Q8_0:
-            return q8_0_dispatch<true>(x, ldx, (int8_t *)(base + a.xq), (float *)(base + a.xd), m, k, q8_0_variant, s);
+            if (tiled) return q8_0_dispatch<OUT_TILED>(x, ldx, xq, xd, m, k, q8_0_variant, a.m_pad, a.kb_pad, s);
+            return q8_0_dispatch<OUT_ROWS>(x, ldx, xq, xd, m, k, q8_0_variant, m, k, s);
         case MQ_TYPE_Q4_K:
         case MQ_TYPE_Q6_K:
-            return q8_K_dispatch<true>(x, ldx, (int8_t *)(base + a.xq), (float *)(base + a.xd),
-                                       (int16_t *)(base + a.xbs), m, k, s);
-        case MQ_TYPE_F16: return launch_quantize_f16(x, ldx, base + a.xq, m, k, s);
+            if (tiled)
+                return q8_K_dispatch<OUT_TILED>(x, ldx, xq, xd, nullptr, (_Float16 *)(base + a.xmin), m, k, a.m_pad, s);
+            return q8_K_dispatch<OUT_ROWS>(x, ldx, xq, xd, (int16_t *)(base + a.xbs), nullptr, m, k, m, s);
+        case MQ_TYPE_F16: {
+            if (!tiled) return launch_quantize_f16(x, ldx, base + a.xq, m, k, s);
+            const int64_t threads = a.m_pad * (a.kb_pad / 8);
+            const dim3 g(grid_for(threads)), b(256);
+            if (aligned16(x, ldx))
+                hipLaunchKernelGGL((k_quantize_f16_tiled<true>), g, b, 0, s, x, ldx, base + a.xq, m, k, a.m_pad, a.kb_pad);
+            else
+                hipLaunchKernelGGL((k_quantize_f16_tiled<false>), g, b, 0, s, x, ldx, base + a.xq, m, k, a.m_pad, a.kb_pad);
+            return hipGetLastError();
+        }
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_quantize_q8_0_gguf(const float *x, int64_t ldx, void *y, int64_t m, int64_t k, int variant,
                                      hipStream_t s) {
-    return q8_0_dispatch<false>(x, ldx, (int8_t *)y, nullptr, m, k, variant, s);
+    return q8_0_dispatch<OUT_GGUF>(x, ldx, (int8_t *)y, nullptr, m, k, variant, m, k, s);
 }
 
 hipError_t launch_quantize_q8_K_gguf(const float *x, int64_t ldx, void *y, int64_t m, int64_t k, hipStream_t s) {
-    return q8_K_dispatch<false>(x, ldx, (int8_t *)y, nullptr, nullptr, m, k, s);
+    return q8_K_dispatch<OUT_GGUF>(x, ldx, (int8_t *)y, nullptr, nullptr, nullptr, m, k, m, s);
 }
 
 hipError_t launch_dequantize(int type, const void *w, float *y, int64_t nrows, int64_t k, int fused, hipStream_t s) {
@@ -408,29 +555,34 @@ hipError_t launch_weight_prepare(int type, void *image, int64_t n, int64_t k, in
     const WeightPlanes p = weight_planes(type, n, k);
     uint8_t *base = (uint8_t *)image;
     if (row1 <= row0) return hipSuccess;
+    const int64_t row_end = (row1 >= n) ? p.n_pad : row1;  // tiled planes: zero the padding rows too
+    const int64_t nbr = k / (type == MQ_TYPE_Q8_0 ? QK8_0 : QK_K);
+    const dim3 b(256);
     switch (type) {
-        case MQ_TYPE_F16: return hipSuccess;
-        case MQ_TYPE_Q8_0: {
-            const int64_t threads = (row1 - row0) * (k / QK8_0);
-            hipLaunchKernelGGL(k_prepare_q8_0, dim3(grid_for(threads)), dim3(256), 0, s, base,
+        case MQ_TYPE_F16:
+            hipLaunchKernelGGL(k_prepare_f16_tiled, dim3(grid_for((row_end - row0) * (p.kb_pad / 16))), b, 0, s, base,
+                               base + p.tq, n, row0, row_end, k, p.kb_pad);
+            break;
+        case MQ_TYPE_Q8_0:
+            hipLaunchKernelGGL(k_prepare_q8_0_rows, dim3(grid_for((row1 - row0) * nbr)), b, 0, s, base,
                                (int8_t *)(base + p.qs), (uint16_t *)(base + p.d16), row0, row1, k);
+            hipLaunchKernelGGL(k_prepare_q8_0_tiled, dim3(grid_for((row_end - row0) * (p.kb_pad / QK8_0))), b, 0, s,
+                               base, (int8_t *)(base + p.tq), (float *)(base + p.tdw), n, row0, row_end, k, p.n_pad,
+                               p.kb_pad);
             break;
-        }
-        case MQ_TYPE_Q4_K: {
-            const int64_t threads = (row1 - row0) * (k / QK_K);
-            hipLaunchKernelGGL(k_prepare_q4_K, dim3(grid_for(threads)), dim3(256), 0, s, base,
-                               (int8_t *)(base + p.qs), (int8_t *)(base + p.hi), (float *)(base + p.dw),
-                               (float *)(base + p.dmin), (_Float16 *)(base + p.mins), row0, row1, k);
+        case MQ_TYPE_Q4_K:
+            hipLaunchKernelGGL(k_prepare_q4_K_tiled, dim3(grid_for((row_end - row0) * nbr)), b, 0, s, base,
+                               (int8_t *)(base + p.tq), (int8_t *)(base + p.thi), (float *)(base + p.tdw),
+                               (float *)(base + p.tdmin), (_Float16 *)(base + p.tmin), n, row0, row_end, k, p.n_pad);
             break;
-        }
-        case MQ_TYPE_Q6_K: {
-            const int64_t threads = (row1 - row0) * (k / QK_K);
-            hipLaunchKernelGGL(k_prepare_q6_K, dim3(grid_for(threads)), dim3(256), 0, s, base,
-                               (int8_t *)(base + p.qs), (int8_t *)(base + p.hi), (float *)(base + p.dw),
-                               (uint8_t *)(base + p.ql), (uint8_t *)(base + p.qh), (int8_t *)(base + p.sc),
-                               (uint16_t *)(base + p.d16), row0, row1, k);
+        case MQ_TYPE_Q6_K:
+            hipLaunchKernelGGL(k_prepare_q6_K_rows, dim3(grid_for((row1 - row0) * nbr)), b, 0, s, base,
+                               base + p.ql, base + p.qh, (int8_t *)(base + p.sc), (uint16_t *)(base + p.d16), row0,
+                               row1, k);
+            hipLaunchKernelGGL(k_prepare_q6_K_tiled, dim3(grid_for((row_end - row0) * nbr)), b, 0, s, base,
+                               (int8_t *)(base + p.tq), (int8_t *)(base + p.thi), (float *)(base + p.tdw), n, row0,
+                               row_end, k, p.n_pad);
             break;
-        }
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

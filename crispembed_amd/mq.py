@@ -48,6 +48,8 @@ _SIGS = {
     "mq_workspace_bytes": (_c_sz, [_c_int, _c_i64, _c_i64]),
     "mq_mul_mat": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                             _c_sz, _c_vp]),
+    "mq_quantize_act": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_sz, _c_int, _c_vp]),
+    "mq_mul_mat_q": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_vp]),
     "mq_mul_mat_ex": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                                _c_sz, _c_int, _c_vp]),
 }

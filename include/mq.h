@@ -124,6 +124,17 @@ int mq_mul_mat(int type, const void *w_image, int64_t n, int64_t k, const float 
 int mq_mul_mat_ex(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m,
                   float *y, int64_t ldy, void *workspace, size_t workspace_bytes, int path, void *stream);
 
+/* The two halves of mq_mul_mat_ex, for callers that reuse one quantized X for
+ * several weights (q, k and v share their input in every encoder layer,
+ * src/crispembed.cpp:1168-1170) or time the stages separately.
+ * mq_quantize_act writes X in mq_vec_dot_type(type) to `workspace`, in the layout of
+ * the path that will read it (the GEMV reads row-major quants, the GEMM tiled
+ * ones); mq_mul_mat_q then runs that path.  Pass the same `path` to both. */
+int mq_quantize_act(int type, const float *x, int64_t ldx, int64_t m, int64_t k, void *workspace,
+                    size_t workspace_bytes, int path, void *stream);
+int mq_mul_mat_q(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m, float *y,
+                 int64_t ldy, int path, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,10 +35,14 @@ def _check(oracle, wtype, w, x, y, k):
     return e1
 
 
+@pytest.mark.parametrize("cfg", ["1", "2", "3"])
 @pytest.mark.parametrize("wtype", TYPES)
-@pytest.mark.parametrize("m,n,k", [(37, 70, 512), (128, 128, 256), (300, 260, 768), (129, 257, 1024), (9, 33, 256)])
-def test_gemm(oracle, wtype, m, n, k):
+@pytest.mark.parametrize("m,n,k", [(37, 70, 512), (128, 128, 256), (300, 260, 768), (129, 257, 1024), (9, 33, 256),
+                                   (520, 390, 1536)])
+def test_gemm(oracle, wtype, m, n, k, cfg, monkeypatch):
+    """Every tile configuration (MQ_GEMM_CFG) on ragged and multi-tile shapes."""
     from crispembed_amd import mq
+    monkeypatch.setenv("MQ_GEMM_CFG", cfg)
     w, x = _mk(oracle, wtype, m, n, k, m * 7 + n + k)
     _, wp = weight_image(wtype, w, n, k)
     y = host(mul_mat(wtype, wp, n, k, dev(x), path=mq.PATH_GEMM))
