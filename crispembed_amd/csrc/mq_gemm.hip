@@ -66,112 +66,164 @@ struct GemmArgs {
     int tiles_m, tiles_n, group_m;
 };
 
+constexpr int KC = 2;     // 32-byte K chunks per stage (64 bytes of K)
+constexpr int NBUF = 4;   // stage ring in LDS
+constexpr int DIST = 3;   // stages in flight ahead of the newest one being computed
+constexpr int SPB = 4;    // stages per 256-value superblock
+// The upper half of the waves can lag the lower half by LAG stages (waves w and
+// w + NW/2 share a SIMD, so a lag keeps their superblock epilogues apart).
+// Measured on MI355X: LAG 1 (with DIST 2) was 7% slower than LAG 0 (DIST 3)
+// for the Q4_K FFN shape, so the lag is off.  Ring: LAG + DIST + 1 <= NBUF.
+constexpr int LAG = 0;
+static_assert(LAG + DIST + 1 <= NBUF, "stage ring too small for the lag");
+
 // WM x WN waves per workgroup, each wave TM x TN MFMA tiles of 32x32.
 template <int FMT, int WM, int WN, int TM, int TN>
 struct Cfg {
     static constexpr int NW = WM * WN, NT = 64 * NW, BM = 32 * TM * WM, BN = 32 * TN * WN;
     static constexpr bool limbs = (FMT == FMT_Q4_K || FMT == FMT_Q6_K);
     static constexpr int NPL = limbs ? 2 : 1;
-    static constexpr int XF = (BM / 32) * 4, WF = (BN / 32) * 4;  // fragments per stage
+    static constexpr int XF = (BM / 32) * KC, WF = (BN / 32) * KC;  // data fragments per stage
     static constexpr int X_BYTES = XF * 1024, W_BYTES = WF * 1024;
-    static constexpr int SCX = (FMT == FMT_Q8_0) ? 4 * BM * 4 : 0;
-    static constexpr int SCW = (FMT == FMT_Q8_0) ? 4 * BN * 4 : 0;
+    static constexpr int NSC = (FMT == FMT_Q8_0) ? 2 * KC : 0;     // Q8_0 scale rows per stage
+    // scale rows move as full 64-lane DMAs into 1 KB slots (a row of BM or BN
+    // floats fills the first BM*4 / BN*4 bytes), so no DMA is lane-masked
+    static constexpr int SCX = (FMT == FMT_Q8_0) ? KC * 1024 : 0;
+    static constexpr int SCW = (FMT == FMT_Q8_0) ? KC * 1024 : 0;
     static constexpr int STAGE = X_BYTES + NPL * W_BYTES + SCX + SCW;
-    static constexpr int EP_DX = limbs ? BM * 4 : 0;
-    static constexpr int EP_DW = limbs ? BN * 4 : 0;
-    static constexpr int EP_DMIN = (FMT == FMT_Q4_K) ? BN * 4 : 0;
+    static constexpr int NITEM = XF + NPL * WF + NSC;               // DMA instructions per stage
+    static constexpr int IPW = (NITEM + NW - 1) / NW;               // per wave (upper bound)
+    static constexpr int EP_DX = limbs ? 1024 : 0;
+    static constexpr int EP_DW = limbs ? 1024 : 0;
+    static constexpr int EP_DMIN = (FMT == FMT_Q4_K) ? 1024 : 0;
     static constexpr int EP_AMIN = (FMT == FMT_Q4_K) ? (BM / 32) * 1024 : 0;
     static constexpr int EP_BMIN = (FMT == FMT_Q4_K) ? (BN / 32) * 1024 : 0;
     static constexpr int EP = EP_DX + EP_DW + EP_DMIN + EP_AMIN + EP_BMIN;
-    static constexpr int LDS = 2 * STAGE + 2 * EP;
+    static constexpr int NEPI = (FMT == FMT_Q4_K) ? 3 + BM / 32 + BN / 32 : (limbs ? 2 : 0);
+    static constexpr int EPW = (NEPI + NW - 1) / NW;
+    static constexpr int LDS = NBUF * STAGE + 2 * EP;
     static_assert(LDS <= 160 * 1024, "LDS budget");
     static_assert(BM <= 256 && BN <= 256, "one 64-lane DMA covers a scale row");
+    static_assert((BM & (BM - 1)) == 0 && (BN & (BN - 1)) == 0, "scale rows of 2^k floats (lane masks)");
 };
 
 __device__ __forceinline__ void dma16(const void *g, void *lds) {
     __builtin_amdgcn_global_load_lds(g, (lds_void *)lds, 16, 0, 0);
 }
 
-// Issue the DMA of stage s into buffer p.  Wave-uniform branches only.
-template <class C, int FMT>
-__device__ __forceinline__ void issue_stage(const GemmArgs &a, int8_t *smem, int s, int p, int m0, int n0, int wave,
-                                            int lane) {
-    int8_t *st = smem + p * C::STAGE;
-    constexpr int TOT = C::XF + C::NPL * C::WF;
-#pragma unroll
-    for (int f = wave; f < TOT; f += C::NW) {
-        const int8_t *g;
-        int8_t *l;
-        if (f < C::XF) {
-            const int rt = f >> 2, kc = f & 3;
-            g = a.xq + ((int64_t)((m0 >> 5) + rt) * a.kch + s * 4 + kc) * 1024;
-            l = st + f * 1024;
-        } else {
-            const int f2 = f - C::XF;
-            const int pl = f2 / C::WF, f3 = f2 % C::WF;
-            const int ct = f3 >> 2, kc = f3 & 3;
-            g = (pl ? a.whi : a.wq) + ((int64_t)((n0 >> 5) + ct) * a.kch + s * 4 + kc) * 1024;
-            l = st + C::X_BYTES + pl * C::W_BYTES + f3 * 1024;
-        }
-        dma16(g + lane * 16, l);
-    }
-    if constexpr (FMT == FMT_Q8_0) {
-        // per-block scales of this stage: 4 blocks x BM (X side) and 4 x BN (W side)
-        for (int f = wave; f < 8; f += C::NW) {
-            const float *src;
-            int8_t *dst;
-            int pieces;
-            if (f < 4) {
-                src = a.xd + (int64_t)(s * 4 + f) * a.m_pad + m0;
-                dst = st + C::X_BYTES + C::W_BYTES + f * C::BM * 4;
-                pieces = C::BM / 4;
-            } else {
-                src = a.wd + (int64_t)(s * 4 + f - 4) * a.n_pad + n0;
-                dst = st + C::X_BYTES + C::W_BYTES + C::SCX + (f - 4) * C::BN * 4;
-                pieces = C::BN / 4;
-            }
-            if (lane < pieces) dma16(src + lane * 4, dst);
-        }
-    }
-    if constexpr (C::limbs) {
-        if ((s & 1) == 0) {
-            const int sb = s >> 1;
-            int8_t *ep = smem + 2 * C::STAGE + (sb & 1) * C::EP;
-            constexpr int NI = (FMT == FMT_Q4_K) ? 3 + C::BM / 32 + C::BN / 32 : 2;
-            for (int f = wave; f < NI; f += C::NW) {
-                if (f == 0) {
-                    if (lane < C::BM / 4) dma16(a.xd + (int64_t)sb * a.m_pad + m0 + lane * 4, ep);
-                } else if (f == 1) {
-                    if (lane < C::BN / 4) dma16(a.wd + (int64_t)sb * a.n_pad + n0 + lane * 4, ep + C::EP_DX);
-                } else if (f == 2) {
-                    if (lane < C::BN / 4)
-                        dma16(a.wdmin + (int64_t)sb * a.n_pad + n0 + lane * 4, ep + C::EP_DX + C::EP_DW);
-                } else if (f < 3 + C::BM / 32) {
-                    const int rt = f - 3;
-                    dma16((const int8_t *)a.xmin + ((int64_t)((m0 >> 5) + rt) * a.nsb + sb) * 1024 + lane * 16,
-                          ep + C::EP_DX + C::EP_DW + C::EP_DMIN + rt * 1024);
-                } else {
-                    const int ct = f - 3 - C::BM / 32;
-                    dma16((const int8_t *)a.wmin + ((int64_t)((n0 >> 5) + ct) * a.nsb + sb) * 1024 + lane * 16,
-                          ep + C::EP_DX + C::EP_DW + C::EP_DMIN + C::EP_AMIN + ct * 1024);
-                }
-            }
-        }
+// s_waitcnt needs an immediate: dispatch on the (wave-uniform) count.
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+#define W_(k) \
+    case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
+        W_(1) W_(2) W_(3) W_(4) W_(5) W_(6) W_(7) W_(8) W_(9) W_(10) W_(11) W_(12) W_(13) W_(14) W_(15)
+        W_(16) W_(17) W_(18) W_(19) W_(20)
+#undef W_
+        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
     }
 }
 
-__device__ __forceinline__ void wait_dma_and_barrier() {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+// LDS reads of DMA-filled epilogue data.  Written as asm so the compiler does not
+// guard them with a wait for every outstanding DMA (its LDS-DMA alias tracking
+// cannot tell the epilogue region from the stages still in flight); the data was
+// ordered by the explicit vmcnt wait + barrier at the top of the iteration.
+typedef __attribute__((address_space(3))) const char lds_cchar;
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(lds_cchar *)p; }
+__device__ __forceinline__ v4i ds_read128(uint32_t a) {
+    v4i r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+__device__ __forceinline__ float ds_read32(uint32_t a) {
+    float r;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+
+// Workgroup barrier without a memory fence: the DMA waits are explicit (a fenced
+// __syncthreads would wait for every outstanding DMA, i.e. empty the pipeline).
+__device__ __forceinline__ void barrier_nofence() { asm volatile("s_barrier" ::: "memory"); }
+
+// One DMA item: a stage-relative source (advancing `step` bytes per stage) and a
+// stage-relative LDS offset.  Every item moves 64 lanes x 16 bytes; for rows
+// shorter than 1 KB (`pieces` < 64) the upper lanes re-read the row's first bytes
+// into the unused tail of the 1 KB slot, so all DMAs run with a full exec mask.
+struct DmaItem {
+    const int8_t *g0;
+    int64_t step;
+    int lds;
+    int pieces;
+};
+
+template <class C, int FMT>
+__device__ __forceinline__ DmaItem stage_item(const GemmArgs &a, int f, int m0, int n0) {
+    DmaItem it;
+    it.pieces = 64;
+    if (f < C::XF) {
+        const int rt = f / KC, kc = f % KC;
+        it.g0 = a.xq + ((int64_t)((m0 >> 5) + rt) * a.kch + kc) * 1024;
+        it.step = KC * 1024;
+        it.lds = f * 1024;
+    } else if (f < C::XF + C::NPL * C::WF) {
+        const int f2 = f - C::XF;
+        const int pl = f2 / C::WF, f3 = f2 % C::WF;
+        const int ct = f3 / KC, kc = f3 % KC;
+        it.g0 = (pl ? a.whi : a.wq) + ((int64_t)((n0 >> 5) + ct) * a.kch + kc) * 1024;
+        it.step = KC * 1024;
+        it.lds = C::X_BYTES + pl * C::W_BYTES + f3 * 1024;
+    } else {
+        const int f4 = f - C::XF - C::NPL * C::WF;  // Q8_0 scale rows
+        if (f4 < KC) {
+            it.g0 = (const int8_t *)(a.xd + (int64_t)f4 * a.m_pad + m0);
+            it.step = (int64_t)KC * a.m_pad * 4;
+            it.lds = C::X_BYTES + C::W_BYTES + f4 * 1024;
+            it.pieces = C::BM / 4;
+        } else {
+            it.g0 = (const int8_t *)(a.wd + (int64_t)(f4 - KC) * a.n_pad + n0);
+            it.step = (int64_t)KC * a.n_pad * 4;
+            it.lds = C::X_BYTES + C::W_BYTES + C::SCX + (f4 - KC) * 1024;
+            it.pieces = C::BN / 4;
+        }
+    }
+    return it;
+}
+
+// Superblock epilogue item e for superblock sb (K-quants).
+template <class C, int FMT>
+__device__ __forceinline__ DmaItem epi_item(const GemmArgs &a, int e, int sb, int m0, int n0) {
+    DmaItem it;
+    it.step = 0;
+    it.pieces = 64;
+    if (e == 0) {
+        it.g0 = (const int8_t *)(a.xd + (int64_t)sb * a.m_pad + m0);
+        it.lds = 0;
+        it.pieces = C::BM / 4;
+    } else if (e == 1) {
+        it.g0 = (const int8_t *)(a.wd + (int64_t)sb * a.n_pad + n0);
+        it.lds = C::EP_DX;
+        it.pieces = C::BN / 4;
+    } else if (e == 2) {
+        it.g0 = (const int8_t *)(a.wdmin + (int64_t)sb * a.n_pad + n0);
+        it.lds = C::EP_DX + C::EP_DW;
+        it.pieces = C::BN / 4;
+    } else if (e < 3 + C::BM / 32) {
+        const int rt = e - 3;
+        it.g0 = (const int8_t *)a.xmin + ((int64_t)((m0 >> 5) + rt) * a.nsb + sb) * 1024;
+        it.lds = C::EP_DX + C::EP_DW + C::EP_DMIN + rt * 1024;
+    } else {
+        const int ct = e - 3 - C::BM / 32;
+        it.g0 = (const int8_t *)a.wmin + ((int64_t)((n0 >> 5) + ct) * a.nsb + sb) * 1024;
+        it.lds = C::EP_DX + C::EP_DW + C::EP_DMIN + C::EP_AMIN + ct * 1024;
+    }
+    return it;
 }
 
 template <int FMT, int WM, int WN, int TM, int TN, int MINB>
 __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
     using C = Cfg<FMT, WM, WN, TM, TN>;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // uniform: SALU addressing
     const int wm = wave / WN, wn = wave % WN;
     const int lrow = lane & 31;
     const int lhalf = lane >> 5;
@@ -185,6 +237,49 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
     const int gm = min(a.group_m, a.tiles_m - grp * a.group_m);
     const int tm = grp * a.group_m + r % gm, tn = r / gm;
     const int m0 = tm * C::BM, n0 = tn * C::BN;
+    const int nst = a.nstages;
+
+    // this wave's DMA items (wave-uniform)
+    DmaItem items[C::IPW];
+    int n_items = 0;
+#pragma unroll
+    for (int i = 0; i < C::IPW; i++) {
+        const int f = wave + C::NW * i;
+        if (f < C::NITEM) {
+            items[i] = stage_item<C, FMT>(a, f, m0, n0);
+            n_items++;
+        }
+    }
+    int n_epi = 0;
+#pragma unroll
+    for (int i = 0; i < C::EPW; i++)
+        if (wave + C::NW * i < C::NEPI) n_epi++;
+
+    auto issue = [&](int s) {
+        int8_t *st = smem + (s % NBUF) * C::STAGE;
+        if constexpr (C::limbs) {
+            if (s % SPB == 0) {
+                const int sb = s / SPB;
+                int8_t *ep = smem + NBUF * C::STAGE + (sb & 1) * C::EP;
+#pragma unroll
+                for (int i = 0; i < C::EPW; i++) {
+                    const int e = wave + C::NW * i;
+                    if (e < C::NEPI) {
+                        const DmaItem it = epi_item<C, FMT>(a, e, sb, m0, n0);
+                        dma16(it.g0 + (lane & (it.pieces - 1)) * 16, ep + it.lds);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::IPW; i++) {
+            if (wave + C::NW * i < C::NITEM) {
+                dma16(items[i].g0 + (int64_t)s * items[i].step + (lane & (items[i].pieces - 1)) * 16, st + items[i].lds);
+            }
+        }
+    };
+    // DMA instructions this wave issues for stage x
+    auto dmas_of = [&](int x) { return n_items + ((C::limbs && x % SPB == 0) ? n_epi : 0); };
 
     v16f acc[TM][TN];
     v16i alo[TM][TN], ahi[C::limbs ? TM : 1][C::limbs ? TN : 1];
@@ -196,24 +291,36 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
             alo[i][j] = (v16i){};
             if constexpr (C::limbs) ahi[i][j] = (v16i){};
         }
-    const int xfrag0 = wm * TM * 4 * 1024 + lane * 16;  // LDS byte offset of this wave's first X fragment
-    const int wfrag0 = C::X_BYTES + wn * TN * 4 * 1024 + lane * 16;
+    const int xfrag0 = wm * TM * KC * 1024 + lane * 16;  // LDS offset of this wave's first X fragment
+    const int wfrag0 = C::X_BYTES + wn * TN * KC * 1024 + lane * 16;
 
-    issue_stage<C, FMT>(a, smem, 0, 0, m0, n0, wave, lane);
-    wait_dma_and_barrier();
-
-    for (int s = 0; s < a.nstages; s++) {
-        if (s + 1 < a.nstages) issue_stage<C, FMT>(a, smem, s + 1, (s + 1) & 1, m0, n0, wave, lane);
-        const int8_t *st = smem + (s & 1) * C::STAGE;
 #pragma unroll
-        for (int kc = 0; kc < 4; kc++) {
+    for (int x = 0; x < DIST; x++)
+        if (x < nst) issue(x);
+
+    const int lag = (C::NW >= 2 && wave >= C::NW / 2) ? LAG : 0;
+    for (int it = 0; it < nst + LAG; it++) {
+        // stage `it` has landed once only the DMAs of later stages are outstanding
+        int after = 0;
+#pragma unroll
+        for (int x = 1; x < DIST; x++)
+            if (it + x < nst) after += dmas_of(it + x);
+        if (it < nst) wait_vmcnt(after);
+        barrier_nofence();  // stage `it` landed for every wave; stage it-LAG-1 fully consumed
+        if (it + DIST < nst) issue(it + DIST);
+        const int s = it - lag;
+        if (s < 0 || s >= nst) continue;
+
+        const int8_t *st = smem + (s % NBUF) * C::STAGE;
+#pragma unroll
+        for (int kc = 0; kc < KC; kc++) {
             v4i xa[TM];
 #pragma unroll
-            for (int i = 0; i < TM; i++) xa[i] = *(const v4i *)(st + xfrag0 + (i * 4 + kc) * 1024);
+            for (int i = 0; i < TM; i++) xa[i] = *(const v4i *)(st + xfrag0 + (i * KC + kc) * 1024);
             if constexpr (FMT == FMT_F16) {
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
-                    const v4i wb = *(const v4i *)(st + wfrag0 + (j * 4 + kc) * 1024);
+                    const v4i wb = *(const v4i *)(st + wfrag0 + (j * KC + kc) * 1024);
 #pragma unroll
                     for (int i = 0; i < TM; i++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, xa[i]),
@@ -221,33 +328,45 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
                                                                           0, 0);
                 }
             } else if constexpr (FMT == FMT_Q8_0) {
-                const float *scx = (const float *)(st + C::X_BYTES + C::W_BYTES) + kc * C::BM;
-                const float *scw = (const float *)(st + C::X_BYTES + C::W_BYTES + C::SCX) + kc * C::BN;
+                // per-block scales (asm reads: see ds_read128)
+                const uint32_t scx = lds_addr(st + C::X_BYTES + C::W_BYTES + kc * 1024);
+                const uint32_t scw = lds_addr(st + C::X_BYTES + C::W_BYTES + C::SCX + kc * 1024);
+                float dw[TN];
+                v4i dx4[TM][4];
+#pragma unroll
+                for (int j = 0; j < TN; j++) dw[j] = ds_read32(scw + ((wn * TN + j) * 32 + lrow) * 4);
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++) dx4[i][g] = ds_read128(scx + ((wm * TM + i) * 32 + 8 * g + 4 * lhalf) * 4);
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(dw[0]), "+v"(dw[TN - 1]), "+v"(dx4[0][0]), "+v"(dx4[0][1]),
+                             "+v"(dx4[0][2]), "+v"(dx4[0][3]), "+v"(dx4[TM - 1][0]), "+v"(dx4[TM - 1][1]),
+                             "+v"(dx4[TM - 1][2]), "+v"(dx4[TM - 1][3]));
+                static_assert(TM <= 2 && TN <= 2, "the wait above names every scale register");
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
-                    const v4i wb = *(const v4i *)(st + wfrag0 + (j * 4 + kc) * 1024);
-                    const float dw = scw[(wn * TN + j) * 32 + lrow];
+                    const v4i wb = *(const v4i *)(st + wfrag0 + (j * KC + kc) * 1024);
 #pragma unroll
                     for (int i = 0; i < TM; i++) {
                         const v16i tq = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[i], wb, (v16i){}, 0, 0, 0);
 #pragma unroll
                         for (int g = 0; g < 4; g++) {
-                            const float4 dx4 = *(const float4 *)(scx + (wm * TM + i) * 32 + 8 * g + 4 * lhalf);
-                            acc[i][j][4 * g + 0] += (float)tq[4 * g + 0] * (dx4.x * dw);
-                            acc[i][j][4 * g + 1] += (float)tq[4 * g + 1] * (dx4.y * dw);
-                            acc[i][j][4 * g + 2] += (float)tq[4 * g + 2] * (dx4.z * dw);
-                            acc[i][j][4 * g + 3] += (float)tq[4 * g + 3] * (dx4.w * dw);
+                            const float4 d4 = __builtin_bit_cast(float4, dx4[i][g]);
+                            acc[i][j][4 * g + 0] += (float)tq[4 * g + 0] * (d4.x * dw[j]);
+                            acc[i][j][4 * g + 1] += (float)tq[4 * g + 1] * (d4.y * dw[j]);
+                            acc[i][j][4 * g + 2] += (float)tq[4 * g + 2] * (d4.z * dw[j]);
+                            acc[i][j][4 * g + 3] += (float)tq[4 * g + 3] * (d4.w * dw[j]);
                         }
                     }
                 }
             } else {
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
-                    const v4i wl = *(const v4i *)(st + wfrag0 + (j * 4 + kc) * 1024);
+                    const v4i wl = *(const v4i *)(st + wfrag0 + (j * KC + kc) * 1024);
 #pragma unroll
                     for (int i = 0; i < TM; i++)
                         alo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[i], wl, alo[i][j], 0, 0, 0);
-                    const v4i wh = *(const v4i *)(st + C::W_BYTES + wfrag0 + (j * 4 + kc) * 1024);
+                    const v4i wh = *(const v4i *)(st + C::W_BYTES + wfrag0 + (j * KC + kc) * 1024);
 #pragma unroll
                     for (int i = 0; i < TM; i++)
                         ahi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[i], wh, ahi[i][j], 0, 0, 0);
@@ -255,41 +374,64 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
             }
         }
         if constexpr (C::limbs) {
-            if (s & 1) {
-                // superblock s/2 complete: scale and fold into the fp32 accumulators
-                const int8_t *ep = smem + 2 * C::STAGE + ((s >> 1) & 1) * C::EP;
-                const float *edx = (const float *)ep;
-                const float *edw = (const float *)(ep + C::EP_DX);
-                const float *edm = (const float *)(ep + C::EP_DX + C::EP_DW);
-                const int8_t *eam = ep + C::EP_DX + C::EP_DW + C::EP_DMIN;
-                const int8_t *ebm = eam + C::EP_AMIN;
+            if (s % SPB == SPB - 1) {
+                // superblock s/SPB complete: scale and fold into the fp32 accumulators
+                const uint32_t ep = lds_addr(smem + NBUF * C::STAGE + ((s / SPB) & 1) * C::EP);
+                const uint32_t edx = ep, edw = ep + C::EP_DX, edm = ep + C::EP_DX + C::EP_DW;
+                const uint32_t eam = ep + C::EP_DX + C::EP_DW + C::EP_DMIN, ebm = eam + C::EP_AMIN;
+                float dw[TN], dmn[TN];
+                v4i bmin[TN];
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
                     const int wc = (wn * TN + j) * 32 + lrow;
-                    const float dw = edw[wc];
-                    float dmn = 0.f;
-                    v8h bmin = {};
+                    dw[j] = ds_read32(edw + wc * 4);
                     if constexpr (FMT == FMT_Q4_K) {
-                        dmn = edm[wc];
-                        bmin = *(const v8h *)(ebm + (wn * TN + j) * 1024 + lane * 16);
+                        dmn[j] = ds_read32(edm + wc * 4);
+                        bmin[j] = ds_read128(ebm + (wn * TN + j) * 1024 + lane * 16);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    v4i amin = {};
+                    if constexpr (FMT == FMT_Q4_K) amin = ds_read128(eam + (wm * TM + i) * 1024 + lane * 16);
+                    v4i dx4[4];
+#pragma unroll
+                    for (int g = 0; g < 4; g++) dx4[g] = ds_read128(edx + ((wm * TM + i) * 32 + 8 * g + 4 * lhalf) * 4);
+                    // the asm reads above complete here; the operands tie every result to the wait
+                    if constexpr (FMT == FMT_Q4_K) {
+                        if (i == 0)
+                            asm volatile("s_waitcnt lgkmcnt(0)"
+                                         : "+v"(dx4[0]), "+v"(dx4[1]), "+v"(dx4[2]), "+v"(dx4[3]), "+v"(amin),
+                                           "+v"(bmin[0]), "+v"(bmin[TN - 1]), "+v"(dw[0]), "+v"(dw[TN - 1]),
+                                           "+v"(dmn[0]), "+v"(dmn[TN - 1]));
+                        else
+                            asm volatile("s_waitcnt lgkmcnt(0)"
+                                         : "+v"(dx4[0]), "+v"(dx4[1]), "+v"(dx4[2]), "+v"(dx4[3]), "+v"(amin));
+                    } else {
+                        if (i == 0)
+                            asm volatile("s_waitcnt lgkmcnt(0)"
+                                         : "+v"(dx4[0]), "+v"(dx4[1]), "+v"(dx4[2]), "+v"(dx4[3]), "+v"(dw[0]),
+                                           "+v"(dw[TN - 1]));
+                        else
+                            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(dx4[0]), "+v"(dx4[1]), "+v"(dx4[2]), "+v"(dx4[3]));
                     }
 #pragma unroll
-                    for (int i = 0; i < TM; i++) {
+                    for (int j = 0; j < TN; j++) {
                         v16f fmin = {};
-                        if constexpr (FMT == FMT_Q4_K) {
-                            const v8h amin = *(const v8h *)(eam + (wm * TM + i) * 1024 + lane * 16);
-                            fmin = __builtin_amdgcn_mfma_f32_32x32x16_f16(amin, bmin, (v16f){}, 0, 0, 0);
-                        }
+                        if constexpr (FMT == FMT_Q4_K)
+                            fmin = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, amin),
+                                                                         __builtin_bit_cast(v8h, bmin[j]), (v16f){}, 0,
+                                                                         0, 0);
 #pragma unroll
                         for (int g = 0; g < 4; g++) {
-                            const float4 dx4 = *(const float4 *)(edx + (wm * TM + i) * 32 + 8 * g + 4 * lhalf);
-                            const float dxs[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+                            const float4 d4 = __builtin_bit_cast(float4, dx4[g]);
+                            const float dxs[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                             for (int q = 0; q < 4; q++) {
                                 const int rr = 4 * g + q;
                                 const int isum = alo[i][j][rr] + (ahi[i][j][rr] << 7);
-                                float tv = dw * (float)isum;
-                                if constexpr (FMT == FMT_Q4_K) tv -= dmn * fmin[rr];
+                                float tv = dw[j] * (float)isum;
+                                if constexpr (FMT == FMT_Q4_K) tv -= dmn[j] * fmin[rr];
                                 acc[i][j][rr] += dxs[q] * tv;
                             }
                         }
@@ -299,7 +441,6 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
                 }
             }
         }
-        wait_dma_and_barrier();
     }
 
     // store: lanes 0..31 of a register write 32 consecutive floats of one row
@@ -337,7 +478,6 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
 
 // Tile configuration, selectable with MQ_GEMM_CFG for measurements:
 //   1: 8 waves x (64x64)  WG 256x128, 2 waves/SIMD
-//   2: 4 waves x (128x64) WG 256x128, 1 wave/SIMD, 512 registers
 //   3: 4 waves x (64x64)  WG 128x128, 2 WGs/CU
 static int gemm_cfg_env() {
     const char *e = getenv("MQ_GEMM_CFG");  // read per launch so a process can compare configurations
@@ -347,13 +487,12 @@ static int gemm_cfg_env() {
 template <int FMT>
 static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
     int cfg = gemm_cfg_env();
-    if (cfg < 1 || cfg > 3) {
+    if (cfg != 1 && cfg != 3) {
         // 256x128 tiles when that still gives every CU a tile, else 128x128
         const int64_t big = (int64_t)((a.M + 255) / 256) * ((a.N + 127) / 128);
-        cfg = (big >= 256) ? (FMT == FMT_Q4_K || FMT == FMT_Q6_K ? 2 : 1) : 3;
+        cfg = (big >= 256) ? 1 : 3;
     }
     if (cfg == 1) return launch_cfg<FMT, 4, 2, 2, 2, 1>(a, s);
-    if (cfg == 2) return launch_cfg<FMT, 2, 2, 4, 2, 1>(a, s);
     return launch_cfg<FMT, 2, 2, 2, 2, 2>(a, s);
 }
 
@@ -380,7 +519,7 @@ hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const 
     a.m_pad = (int)ap.m_pad;
     a.n_pad = (int)p.n_pad;
     a.kch = (int)(p.kb_pad / 32);
-    a.nstages = (int)(p.kb_pad / KSTAGE);
+    a.nstages = (int)(p.kb_pad / (KC * 32));
     a.nsb = (int)(k / QK_K);
     switch (type) {
         case MQ_TYPE_Q8_0: return launch_fmt<FMT_Q8_0>(a, s);
