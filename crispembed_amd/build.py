@@ -35,13 +35,23 @@ MQ_SOURCES = [
     ("mq_api.cpp", ["-x", "hip"]),
     ("mq_host_quant.cpp", ["-x", "hip", "-ffp-contract=off"]),
 ]
+# The backend compiles against ggml's backend headers.  Standalone builds use the
+# compat transcription in csrc/ggml_compat (and libggml-compat.so for the ggml
+# symbols); an integration sets MQ_GGML_INCLUDE to ggml's include+src dirs and
+# links the backend against ggml instead.
+GGML_INC = os.environ.get("MQ_GGML_INCLUDE", os.path.join(CSRC, "ggml_compat"))
 GGML_SOURCES = [
-    ("ggml_backend_mi355.cpp", ["-x", "hip"]),
-    ("ggml_compat/ggml_compat.cpp", ["-x", "hip"]),
+    ("ggml_backend_mi355.cpp", ["-x", "hip", "-I", GGML_INC]),
+]
+COMPAT_SOURCES = [
+    ("ggml_compat/ggml_compat.cpp", ["-x", "c++", "-I", os.path.join(CSRC, "ggml_compat")]),
 ]
 
 LIBMQ = os.path.join(HERE, "libmq.so")
 LIBGGML = os.path.join(HERE, "libggml-mi355.so")
+LIBCOMPAT = os.path.join(HERE, "libggml-compat.so")
+BIN = os.path.join(HERE, "bin")
+TESTS = os.path.join(ROOT, "tests")
 
 
 def _compile(src, extra):
@@ -62,23 +72,40 @@ def _link(objs, out, extra=()):
     os.replace(tmp, out)
 
 
+def build_test_driver():
+    """tests/native/test_backend_mi355.cpp -> crispembed_amd/bin/test-backend-mi355 (test code:
+    it links the CPU oracle as the checker)."""
+    os.makedirs(BIN, exist_ok=True)
+    out = os.path.join(BIN, "test-backend-mi355")
+    oracle = os.path.join(ROOT, "oracle")
+    cmd = ["g++", "-O2", "-std=c++17", "-I", os.path.join(CSRC, "ggml_compat"), "-I", os.path.join(ROOT, "include"),
+           "-I", oracle, os.path.join(TESTS, "native", "test_backend_mi355.cpp"), "-o", out + ".tmp",
+           "-L", HERE, "-lggml-mi355", "-lggml-compat", "-lmq", "-L", oracle, "-loracle",
+           "-Wl,-rpath," + HERE, "-Wl,-rpath," + oracle, "-Wl,-rpath,$ORIGIN/..", "-Wl,-rpath,$ORIGIN/../../oracle"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"driver build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build(verbose=True):
     os.makedirs(BUILD, exist_ok=True)
-    srcs = list(MQ_SOURCES)
-    have_ggml = os.path.exists(os.path.join(CSRC, "ggml_backend_mi355.cpp"))
-    if have_ggml:
-        srcs += GGML_SOURCES
+    srcs = list(MQ_SOURCES) + list(GGML_SOURCES)
     with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
         objs = list(ex.map(lambda a: _compile(*a), srcs))
+        compat_objs = list(ex.map(lambda a: _compile(*a), COMPAT_SOURCES))
     mq_objs = objs[: len(MQ_SOURCES)]
     _link(mq_objs, LIBMQ)
-    if have_ggml:
-        _link(objs[len(MQ_SOURCES):], LIBGGML, ["-L", HERE, "-lmq", "-Wl,-rpath,$ORIGIN"])
+    _link(compat_objs, LIBCOMPAT)
+    _link(objs[len(MQ_SOURCES):], LIBGGML, ["-L", HERE, "-lmq", "-lggml-compat", "-Wl,-rpath,$ORIGIN"])
     if verbose:
-        print(f"built {LIBMQ}" + (f" and {LIBGGML}" if have_ggml else ""))
+        print(f"built {LIBMQ}, {LIBGGML}, {LIBCOMPAT}")
     return LIBMQ
 
 
 if __name__ == "__main__":
     build()
+    if os.path.exists(os.path.join(ROOT, "oracle", "liboracle.so")):
+        build_test_driver()
     sys.exit(0)

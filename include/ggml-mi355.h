@@ -1,0 +1,45 @@
+/*
+ * ggml-mi355.h -- ggml backend for AMD MI355X (gfx950) quantized MUL_MAT.
+ *
+ * A ggml backend (ggml_backend_reg / ggml_backend_device / buffer type / buffer /
+ * ggml_backend_i) whose supports_op claims GGML_OP_MUL_MAT on Q8_0, Q4_K, Q6_K
+ * and F16 weights with F32 activations; every other op stays on the CPU backend
+ * through ggml_backend_sched, the reference's own fallback contract.  It plugs in
+ * where CrispEmbed picks a GPU backend: crispasr_init_gpu_backend() prefix-matches
+ * the --gpu-backend string against registered device names
+ * (src/core/gpu_backend_pref.h:117-152), so "mi355" selects device "MI355X0".
+ * CrispEmbed never loads backends dynamically, so the host registers this one
+ * once before the first crispembed_init (one line next to
+ * crispembed_set_gpu_backend, src/crispembed.cpp:2802-2804):
+ *     ggml_backend_register(ggml_backend_mi355_reg());
+ *
+ * Weights: ggml_backend_tensor_set uploads GGUF bytes unchanged (as
+ * core_gguf::load_weights does, src/core/gguf_loader.cpp:480); the backend then
+ * builds the kernel planes after them (see mq.h, "weight images"), so
+ * get_tensor returns the original bytes and partial writes rebuild only the rows
+ * they touch.  The buffer type's get_alloc_size reports the enlarged size,
+ * which the reference's split loader already honours (gguf_loader.cpp:535-540).
+ */
+#ifndef GGML_MI355_H
+#define GGML_MI355_H
+
+#include "ggml-backend.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Replaces a backend library's registry entry point (ggml_backend_cuda_reg and
+ * the like); registry name "MI355X". */
+GGML_BACKEND_API ggml_backend_reg_t ggml_backend_mi355_reg(void);
+/* Direct constructor for HIP device `device` (like ggml_backend_cuda_init). */
+GGML_BACKEND_API ggml_backend_t ggml_backend_mi355_init(int device);
+GGML_BACKEND_API bool ggml_backend_is_mi355(ggml_backend_t backend);
+GGML_BACKEND_API ggml_backend_buffer_type_t ggml_backend_mi355_buffer_type(int device);
+/* Number of gfx950 devices the backend exposes. */
+GGML_BACKEND_API int ggml_backend_mi355_get_device_count(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

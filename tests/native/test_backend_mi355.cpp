@@ -1,0 +1,197 @@
+// test-backend-mi355 -- runs GGML_OP_MUL_MAT graphs through the MI355X ggml
+// backend exactly as a ggml host would (registry lookup by name, one backend
+// buffer from ggml_backend_alloc_ctx_tensors, tensor_set of GGUF bytes,
+// ggml_backend_graph_compute, tensor_get) and checks every result against the
+// CPU oracle.  It follows the reference's backend smoke test
+// (tests/test_backend_smoke.cpp: backend chosen by name, graph computed, JSON
+// summary) with MUL_MAT graphs in place of the 16-element ADD.
+//
+// usage: test-backend-mi355 [backend-name-prefix] [--json]
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "ggml-backend.h"
+#include "ggml-mi355.h"
+#include "ggml.h"
+#include "ggml_oracle.h"
+
+static bool starts_with_ci(const char *s, const char *prefix) {
+    for (; *prefix; ++s, ++prefix)
+        if (!*s || std::tolower((unsigned char)*s) != std::tolower((unsigned char)*prefix)) return false;
+    return true;
+}
+
+// first GPU device whose name starts with `pref` (the selection rule of
+// crispasr_init_gpu_backend, src/core/gpu_backend_pref.h:117-132)
+static ggml_backend_t init_by_name(const char *pref) {
+    for (size_t i = 0; i < ggml_backend_dev_count(); ++i) {
+        ggml_backend_dev_t dev = ggml_backend_dev_get(i);
+        if (ggml_backend_dev_type(dev) != GGML_BACKEND_DEVICE_TYPE_GPU) continue;
+        if (starts_with_ci(ggml_backend_dev_name(dev), pref)) return ggml_backend_dev_init(dev, nullptr);
+    }
+    return nullptr;
+}
+
+static uint64_t g_state = 0x1234567u;
+static double uniform01() {
+    uint64_t z = (g_state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return ((z >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+}
+static std::vector<float> normal(size_t n, double sd) {
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; i += 2) {
+        const double r = std::sqrt(-2.0 * std::log(uniform01())), t = 2.0 * M_PI * uniform01();
+        v[i] = (float)(sd * r * std::cos(t));
+        if (i + 1 < n) v[i + 1] = (float)(sd * r * std::sin(t));
+    }
+    return v;
+}
+
+static double rel_err(const std::vector<float> &got, const std::vector<float> &ref) {
+    double num = 0, den = 0;
+    for (size_t i = 0; i < got.size(); i++) {
+        num = std::fmax(num, std::fabs((double)got[i] - ref[i]));
+        den = std::fmax(den, std::fabs((double)ref[i]));
+    }
+    return den > 0 ? num / den : num;
+}
+
+struct Result {
+    int cases = 0;
+    double max_err = 0;
+    bool roundtrip = true, partial = true, batched = true, supports = true, computed = true;
+};
+
+// One weight of `type` [K in, N out], activations [K, M] (ne2 batches), through the graph.
+static void run_case(ggml_backend_t be, ggml_type type, int64_t K, int64_t N, int64_t M, int64_t B, Result &res) {
+    ggml_init_params ip = {ggml_tensor_overhead() * 8 + ggml_graph_overhead(), nullptr, true};
+    ggml_context *ctx = ggml_init(ip);
+    ggml_tensor *W = ggml_new_tensor_2d(ctx, type, K, N);
+    ggml_tensor *X = B > 1 ? ggml_new_tensor_3d(ctx, GGML_TYPE_F32, K, M, B) : ggml_new_tensor_2d(ctx, GGML_TYPE_F32, K, M);
+    ggml_set_name(W, "w");
+    ggml_set_name(X, "x");
+    ggml_tensor *Y = ggml_mul_mat(ctx, W, X);
+    ggml_set_output(Y);
+    if (!ggml_backend_supports_op(be, Y)) {
+        std::fprintf(stderr, "case %s K=%lld: supports_op refused\n", ggml_type_name(type), (long long)K);
+        res.supports = false;
+        ggml_free(ctx);
+        return;
+    }
+    ggml_backend_buffer_t buf = ggml_backend_alloc_ctx_tensors(ctx, be);
+    if (!buf) {
+        res.computed = false;
+        ggml_free(ctx);
+        return;
+    }
+    const size_t rs = or_row_size((int)type, K);
+    std::vector<float> wf = normal((size_t)(N * K), 0.02);
+    std::vector<uint8_t> wq(rs * N);
+    or_quantize_chunk((int)type, wf.data(), wq.data(), N, K);
+    ggml_backend_tensor_set(W, wq.data(), 0, wq.size());
+    std::vector<float> x = normal((size_t)(K * M * B), 1.0);
+    ggml_backend_tensor_set(X, x.data(), 0, x.size() * 4);
+    ggml_cgraph *gf = ggml_new_graph(ctx);
+    ggml_build_forward_expand(gf, Y);
+
+    auto check = [&](const std::vector<uint8_t> &wbytes, bool &flag) {
+        if (ggml_backend_graph_compute(be, gf) != GGML_STATUS_SUCCESS) {
+            res.computed = false;
+            return;
+        }
+        std::vector<float> y((size_t)(N * M * B)), yref((size_t)(N * M * B));
+        ggml_backend_tensor_get(Y, y.data(), 0, y.size() * 4);
+        or_mul_mat((int)type, wbytes.data(), N, K, x.data(), K, M * B, yref.data(), N, 4, OR_Q8_0_X86);
+        const double e = rel_err(y, yref);
+        res.max_err = std::fmax(res.max_err, e);
+        res.cases++;
+        if (!(e <= 1e-4)) {
+            flag = false;
+            std::fprintf(stderr, "case %s K=%lld N=%lld M=%lld B=%lld: rel err %.3g\n", ggml_type_name(type),
+                         (long long)K, (long long)N, (long long)M, (long long)B, e);
+        }
+    };
+    bool ok = true;
+    check(wq, ok);
+    if (B > 1) res.batched = res.batched && ok;
+    // get_tensor returns the uploaded GGUF bytes
+    std::vector<uint8_t> back(wq.size());
+    ggml_backend_tensor_get(W, back.data(), 0, back.size());
+    if (back != wq) res.roundtrip = false;
+    // partial write of rows [5, 13): the backend rebuilds the planes of those rows only
+    if (N >= 13) {
+        std::vector<float> wf2 = normal((size_t)(8 * K), 0.03);
+        std::vector<uint8_t> rows(rs * 8);
+        or_quantize_chunk((int)type, wf2.data(), rows.data(), 8, K);
+        ggml_backend_tensor_set(W, rows.data(), 5 * rs, rows.size());
+        std::memcpy(wq.data() + 5 * rs, rows.data(), rows.size());
+        bool pok = true;
+        check(wq, pok);
+        res.partial = res.partial && pok;
+    }
+    ggml_backend_buffer_free(buf);
+    ggml_free(ctx);
+}
+
+int main(int argc, char **argv) {
+    const char *requested = "MI355X";
+    bool json = false;
+    for (int i = 1; i < argc; ++i) {
+        if (std::strcmp(argv[i], "--json") == 0) json = true;
+        else requested = argv[i];
+    }
+    ggml_backend_register(ggml_backend_mi355_reg());  // the one-line host hook
+    ggml_backend_t be = init_by_name(requested);
+    if (!be) {
+        std::fprintf(stderr, "test-backend-mi355: no GPU device matching '%s' (%zu devices registered)\n", requested,
+                     ggml_backend_dev_count());
+        if (json) std::printf("{\"requested\":\"%s\",\"device_available\":false,\"correct\":false}\n", requested);
+        return 1;
+    }
+    ggml_backend_dev_t dev = ggml_backend_get_device(be);
+    Result res;
+    const ggml_type types[] = {GGML_TYPE_Q8_0, GGML_TYPE_Q4_K, GGML_TYPE_Q6_K, GGML_TYPE_F16};
+    for (ggml_type t : types) {
+        const int64_t K = (t == GGML_TYPE_Q8_0) ? 384 : 512;
+        for (int64_t M : {1, 4, 8, 77, 300}) run_case(be, t, K, 96, M, 1, res);
+        run_case(be, t, K, 40, 7, 3, res);  // batched activations [K, 7, 3]
+    }
+    // supports_op must refuse what the kernels do not handle (CPU fallback)
+    {
+        ggml_init_params ip = {ggml_tensor_overhead() * 8 + ggml_graph_overhead(), nullptr, true};
+        ggml_context *ctx = ggml_init(ip);
+        ggml_tensor *wf32 = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 64, 8);
+        ggml_tensor *wf16 = ggml_new_tensor_2d(ctx, GGML_TYPE_F16, 48, 8);  // k % 32 != 0
+        ggml_tensor *wq = ggml_new_tensor_2d(ctx, GGML_TYPE_Q4_K, 256, 8);
+        ggml_tensor *x64 = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 64, 3);
+        ggml_tensor *x48 = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 48, 3);
+        ggml_tensor *xh = ggml_new_tensor_2d(ctx, GGML_TYPE_F16, 256, 3);
+        if (ggml_backend_supports_op(be, ggml_mul_mat(ctx, wf32, x64))) res.supports = false;
+        if (ggml_backend_supports_op(be, ggml_mul_mat(ctx, wf16, x48))) res.supports = false;
+        if (ggml_backend_supports_op(be, ggml_mul_mat(ctx, wq, xh))) res.supports = false;
+        if (ggml_backend_supports_op(be, ggml_add(ctx, x64, x64))) res.supports = false;
+        ggml_free(ctx);
+    }
+    const bool correct = res.computed && res.roundtrip && res.partial && res.batched && res.supports &&
+                         res.cases > 0 && res.max_err <= 1e-4;
+    if (json)
+        std::printf("{\"requested\":\"%s\",\"name\":\"%s\",\"description\":\"%s\",\"type\":%d,\"cases\":%d,"
+                    "\"max_rel_err\":%.3g,\"roundtrip_ok\":%s,\"partial_write_ok\":%s,\"batched_ok\":%s,"
+                    "\"supports_op_ok\":%s,\"computed\":%s,\"correct\":%s}\n",
+                    requested, ggml_backend_dev_name(dev), ggml_backend_dev_description(dev),
+                    (int)ggml_backend_dev_type(dev), res.cases, res.max_err, res.roundtrip ? "true" : "false",
+                    res.partial ? "true" : "false", res.batched ? "true" : "false", res.supports ? "true" : "false",
+                    res.computed ? "true" : "false", correct ? "true" : "false");
+    else
+        std::printf("backend-mi355 name=%s cases=%d max_rel_err=%.3g correct=%d\n", ggml_backend_dev_name(dev),
+                    res.cases, res.max_err, correct ? 1 : 0);
+    ggml_backend_free(be);
+    return correct ? 0 : 2;
+}

@@ -11,7 +11,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 def _declared(header):
     text = open(os.path.join(ROOT, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b((?:mq|ggml_backend_mi355)\w*)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(mq_\w+|\w*mi355\w*)\s*\(", text)))
 
 
 def test_libmq_exports_all_declared_symbols():
@@ -38,3 +38,32 @@ def test_host_only_entry_points_without_gpu():
     # argument errors come back as codes with a message, before any HIP call
     rc = L.mq_mul_mat(mq.TYPE_Q4_K, None, 8, 300, None, 300, 1, None, 8, None, 0, None)
     assert rc == -2 and b"multiple" in L.mq_last_error()
+
+
+def test_ggml_backend_library_exports():
+    import ctypes
+    from crispembed_amd import mq
+    mq.lib()
+    here = os.path.join(ROOT, "crispembed_amd")
+    ctypes.CDLL(os.path.join(here, "libggml-compat.so"), mode=ctypes.RTLD_GLOBAL)
+    L = ctypes.CDLL(os.path.join(here, "libggml-mi355.so"))
+    names = _declared("ggml-mi355.h")
+    assert set(names) >= {"ggml_backend_mi355_reg", "ggml_backend_mi355_init", "ggml_backend_is_mi355",
+                          "ggml_backend_mi355_buffer_type", "ggml_backend_mi355_get_device_count"}
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_backend_driver_without_gpu_reports_no_device():
+    """On a machine without a gfx950 device the registry is empty and the driver
+    exits cleanly with device_available false (no crash, no fallback)."""
+    import json
+    import subprocess
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present; the GPU test covers the driver")
+    exe = os.path.join(ROOT, "crispembed_amd", "bin", "test-backend-mi355")
+    r = subprocess.run([exe, "--json"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 1
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["device_available"] is False

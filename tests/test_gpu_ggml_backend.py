@@ -1,0 +1,25 @@
+"""The ggml backend end to end on the GPU: registry lookup by name, buffer
+allocation, GGUF upload, graph_compute of MUL_MAT nodes (GEMV and GEMM sizes,
+batched activations), tensor_get round trip, partial weight writes and the
+supports_op contract, all checked against the CPU oracle by the native driver."""
+import json
+import os
+import subprocess
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_backend_driver_json():
+    exe = os.path.join(ROOT, "crispembed_amd", "bin", "test-backend-mi355")
+    r = subprocess.run([exe, "mi355", "--json"], capture_output=True, text=True, timeout=300)
+    print(r.stderr[-2000:])
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["name"].startswith("MI355X")
+    assert out["cases"] >= 24
+    assert out["max_rel_err"] <= 1e-4
+    for k in ("roundtrip_ok", "partial_write_ok", "batched_ok", "supports_op_ok", "computed", "correct"):
+        assert out[k] is True, k
+    assert r.returncode == 0
