@@ -54,6 +54,18 @@ class Dev:
         self.name = name
 
 
+def _measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 byte-counter
+    runs (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE per dispatch, each
+    scaled by what the counter reads for a plain copy of known size)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        t = json.load(open(path))
+    except (OSError, ValueError):
+        return None
+    return t.get("bytes_per_launch") if t.get("kernel") == kernel else None
+
+
 def quantize_weights(L, wtype, wf):
     import numpy as np
     n, k = wf.shape
@@ -127,7 +139,8 @@ def bench_q4k_ffn(args, torch, L, mq, synth):
             "unit": "TFLOP/s",
             "peak_source": "MI355X dense int8 MFMA 5.0 POP/s (integer ops counted as 2*M*N*K)",
             "frac": achieved / PEAK_INT8_TOPS,
-            "traffic": None,
+            "traffic": _measured_traffic("k_gemm<Q4_K>"),
+            "traffic_unit": "bytes per launch (HBM, rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
             "algorithmic_ops_per_launch": gemm_ops,
         },
         "x": (x_up, x_dn, q_up, q_dn),
@@ -170,7 +183,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--gemm-cfg", default=None, help="MQ_GEMM_CFG tile configuration (1, 2, 3)")
+    ap.add_argument("--gemm-cfg", default=None, help="MQ_GEMM_CFG tile configuration (1 or 3)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 10 device copies of 256 MiB (reference kernel for rocprof byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
@@ -180,6 +195,14 @@ def main():
     if args.gemm_cfg:
         os.environ["MQ_GEMM_CFG"] = args.gemm_cfg
     import torch
+    if args.calibrate_copy:
+        src = torch.empty(64 << 20, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
+        return
     from crispembed_amd import mq, synth
     L = mq.lib()
     mq.check(L.mq_init())

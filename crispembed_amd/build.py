@@ -39,9 +39,9 @@ MQ_SOURCES = [
 # compat transcription in csrc/ggml_compat (and libggml-compat.so for the ggml
 # symbols); an integration sets MQ_GGML_INCLUDE to ggml's include+src dirs and
 # links the backend against ggml instead.
-GGML_INC = os.environ.get("MQ_GGML_INCLUDE", os.path.join(CSRC, "ggml_compat"))
+GGML_INC = os.environ.get("MQ_GGML_INCLUDE", os.path.join(CSRC, "ggml_compat")).split(os.pathsep)
 GGML_SOURCES = [
-    ("ggml_backend_mi355.cpp", ["-x", "hip", "-I", GGML_INC]),
+    ("ggml_backend_mi355.cpp", ["-x", "hip", *[f"-I{d}" for d in GGML_INC if d]]),
 ]
 COMPAT_SOURCES = [
     ("ggml_compat/ggml_compat.cpp", ["-x", "c++", "-I", os.path.join(CSRC, "ggml_compat")]),
