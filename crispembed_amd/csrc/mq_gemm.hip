@@ -38,6 +38,8 @@
 // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 #include "mq_internal.h"
 
+#include <type_traits>
+
 namespace mq {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -70,12 +72,7 @@ constexpr int KC = 2;     // 32-byte K chunks per stage (64 bytes of K)
 constexpr int NBUF = 4;   // stage ring in LDS
 constexpr int DIST = 3;   // stages in flight ahead of the newest one being computed
 constexpr int SPB = 4;    // stages per 256-value superblock
-// The upper half of the waves can lag the lower half by LAG stages (waves w and
-// w + NW/2 share a SIMD, so a lag keeps their superblock epilogues apart).
-// Measured on MI355X: LAG 1 (with DIST 2) was 7% slower than LAG 0 (DIST 3)
-// for the Q4_K FFN shape, so the lag is off.  Ring: LAG + DIST + 1 <= NBUF.
-constexpr int LAG = 0;
-static_assert(LAG + DIST + 1 <= NBUF, "stage ring too small for the lag");
+static_assert(DIST + 1 <= NBUF, "stage ring: DIST stages in flight plus the one being computed");
 
 // WM x WN waves per workgroup, each wave TM x TN MFMA tiles of 32x32.
 template <int FMT, int WM, int WN, int TM, int TN>
@@ -102,6 +99,15 @@ struct Cfg {
     static constexpr int NEPI = (FMT == FMT_Q4_K) ? 3 + BM / 32 + BN / 32 : (limbs ? 2 : 0);
     static constexpr int EPW = (NEPI + NW - 1) / NW;
     static constexpr int LDS = NBUF * STAGE + 2 * EP;
+    // DMAs issued per stage by every wave, and the count still in flight when stage
+    // position q (of a superblock) may be computed: those of the DIST-1 later stages.
+    static constexpr int dmas(int stage_pos) { return IPW + ((limbs && stage_pos % SPB == 0) ? EPW : 0); }
+    template <int D>
+    static constexpr int waits(int q) {
+        int w = 0;
+        for (int x = 1; x < D; x++) w += dmas(q + x);
+        return w;
+    }
     static_assert(LDS <= 160 * 1024, "LDS budget");
     static_assert(BM <= 256 && BN <= 256, "one 64-lane DMA covers a scale row");
     static_assert((BM & (BM - 1)) == 0 && (BN & (BN - 1)) == 0, "scale rows of 2^k floats (lane masks)");
@@ -111,16 +117,20 @@ __device__ __forceinline__ void dma16(const void *g, void *lds) {
     __builtin_amdgcn_global_load_lds(g, (lds_void *)lds, 16, 0, 0);
 }
 
-// s_waitcnt needs an immediate: dispatch on the (wave-uniform) count.
-__device__ __forceinline__ void wait_vmcnt(int n) {
-    switch (n) {
-#define W_(k) \
-    case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
-        W_(1) W_(2) W_(3) W_(4) W_(5) W_(6) W_(7) W_(8) W_(9) W_(10) W_(11) W_(12) W_(13) W_(14) W_(15)
-        W_(16) W_(17) W_(18) W_(19) W_(20)
-#undef W_
-        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+// compile-time loop: f(integral_constant<int, Q>) for Q in [B, E)
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
     }
+}
+
+// s_waitcnt with a compile-time count
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_c() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 // LDS reads of DMA-filled epilogue data.  Written as asm so the compiler does not
@@ -140,9 +150,12 @@ __device__ __forceinline__ float ds_read32(uint32_t a) {
     return r;
 }
 
-// Workgroup barrier without a memory fence: the DMA waits are explicit (a fenced
-// __syncthreads would wait for every outstanding DMA, i.e. empty the pipeline).
-__device__ __forceinline__ void barrier_nofence() { asm volatile("s_barrier" ::: "memory"); }
+// Workgroup barrier that does not wait for outstanding DMAs (a fenced
+// __syncthreads would wait for every one of them, i.e. empty the pipeline).  It
+// does wait for this wave's own LDS reads: after the barrier other waves refill
+// the ring slot this wave read last, and the compiler may leave those reads in
+// flight up to here.
+__device__ __forceinline__ void barrier_nofence() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // One DMA item: a stage-relative source (advancing `step` bytes per stage) and a
 // stage-relative LDS offset.  Every item moves 64 lanes x 16 bytes; for rows
@@ -239,47 +252,37 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
     const int m0 = tm * C::BM, n0 = tn * C::BN;
     const int nst = a.nstages;
 
-    // this wave's DMA items (wave-uniform)
+    // This wave's DMA items.  Every wave issues exactly IPW stage DMAs per stage
+    // (plus EPW epilogue DMAs with the first stage of each superblock): a wave
+    // past the item count repeats an item (same source, same LDS bytes, same
+    // data).  The number of DMAs in flight is then the same on every wave at
+    // every point, so each wait below is a compile-time constant.
     DmaItem items[C::IPW];
-    int n_items = 0;
 #pragma unroll
-    for (int i = 0; i < C::IPW; i++) {
-        const int f = wave + C::NW * i;
-        if (f < C::NITEM) {
-            items[i] = stage_item<C, FMT>(a, f, m0, n0);
-            n_items++;
-        }
-    }
-    int n_epi = 0;
-#pragma unroll
-    for (int i = 0; i < C::EPW; i++)
-        if (wave + C::NW * i < C::NEPI) n_epi++;
+    for (int i = 0; i < C::IPW; i++) items[i] = stage_item<C, FMT>(a, (wave + C::NW * i) % C::NITEM, m0, n0);
 
+    // Stages past the end are issued too, re-reading the last stage into the
+    // slot of a stage that is never computed, so the DMA count per stage stays
+    // uniform through the tail.
     auto issue = [&](int s) {
         int8_t *st = smem + (s % NBUF) * C::STAGE;
+        const int64_t sc = s < nst ? s : nst - 1;
         if constexpr (C::limbs) {
             if (s % SPB == 0) {
                 const int sb = s / SPB;
                 int8_t *ep = smem + NBUF * C::STAGE + (sb & 1) * C::EP;
+                const int sbc = sb < a.nsb ? sb : a.nsb - 1;
 #pragma unroll
                 for (int i = 0; i < C::EPW; i++) {
-                    const int e = wave + C::NW * i;
-                    if (e < C::NEPI) {
-                        const DmaItem it = epi_item<C, FMT>(a, e, sb, m0, n0);
-                        dma16(it.g0 + (lane & (it.pieces - 1)) * 16, ep + it.lds);
-                    }
+                    const DmaItem it = epi_item<C, FMT>(a, (wave + C::NW * i) % C::NEPI, sbc, m0, n0);
+                    dma16(it.g0 + (lane & (it.pieces - 1)) * 16, ep + it.lds);
                 }
             }
         }
 #pragma unroll
-        for (int i = 0; i < C::IPW; i++) {
-            if (wave + C::NW * i < C::NITEM) {
-                dma16(items[i].g0 + (int64_t)s * items[i].step + (lane & (items[i].pieces - 1)) * 16, st + items[i].lds);
-            }
-        }
+        for (int i = 0; i < C::IPW; i++)
+            dma16(items[i].g0 + sc * items[i].step + (lane & (items[i].pieces - 1)) * 16, st + items[i].lds);
     };
-    // DMA instructions this wave issues for stage x
-    auto dmas_of = [&](int x) { return n_items + ((C::limbs && x % SPB == 0) ? n_epi : 0); };
 
     v16f acc[TM][TN];
     v16i alo[TM][TN], ahi[C::limbs ? TM : 1][C::limbs ? TN : 1];
@@ -294,24 +297,8 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
     const int xfrag0 = wm * TM * KC * 1024 + lane * 16;  // LDS offset of this wave's first X fragment
     const int wfrag0 = C::X_BYTES + wn * TN * KC * 1024 + lane * 16;
 
-#pragma unroll
-    for (int x = 0; x < DIST; x++)
-        if (x < nst) issue(x);
-
-    const int lag = (C::NW >= 2 && wave >= C::NW / 2) ? LAG : 0;
-    for (int it = 0; it < nst + LAG; it++) {
-        // stage `it` has landed once only the DMAs of later stages are outstanding
-        int after = 0;
-#pragma unroll
-        for (int x = 1; x < DIST; x++)
-            if (it + x < nst) after += dmas_of(it + x);
-        if (it < nst) wait_vmcnt(after);
-        barrier_nofence();  // stage `it` landed for every wave; stage it-LAG-1 fully consumed
-        if (it + DIST < nst) issue(it + DIST);
-        const int s = it - lag;
-        if (s < 0 || s >= nst) continue;
-
-        const int8_t *st = smem + (s % NBUF) * C::STAGE;
+    // MFMAs of one stage
+    auto compute = [&](const int8_t *st) {
 #pragma unroll
         for (int kc = 0; kc < KC; kc++) {
             v4i xa[TM];
@@ -360,88 +347,102 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
                     }
                 }
             } else {
+                v4i wl[TN], wh[TN];
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
-                    const v4i wl = *(const v4i *)(st + wfrag0 + (j * KC + kc) * 1024);
-#pragma unroll
-                    for (int i = 0; i < TM; i++)
-                        alo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[i], wl, alo[i][j], 0, 0, 0);
-                    const v4i wh = *(const v4i *)(st + C::W_BYTES + wfrag0 + (j * KC + kc) * 1024);
-#pragma unroll
-                    for (int i = 0; i < TM; i++)
-                        ahi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[i], wh, ahi[i][j], 0, 0, 0);
+                    wl[j] = *(const v4i *)(st + wfrag0 + (j * KC + kc) * 1024);
+                    wh[j] = *(const v4i *)(st + C::W_BYTES + wfrag0 + (j * KC + kc) * 1024);
                 }
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        alo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[i], wl[j], alo[i][j], 0, 0, 0);
+                        ahi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[i], wh[j], ahi[i][j], 0, 0, 0);
+                    }
             }
         }
-        if constexpr (C::limbs) {
-            if (s % SPB == SPB - 1) {
-                // superblock s/SPB complete: scale and fold into the fp32 accumulators
-                const uint32_t ep = lds_addr(smem + NBUF * C::STAGE + ((s / SPB) & 1) * C::EP);
-                const uint32_t edx = ep, edw = ep + C::EP_DX, edm = ep + C::EP_DX + C::EP_DW;
-                const uint32_t eam = ep + C::EP_DX + C::EP_DW + C::EP_DMIN, ebm = eam + C::EP_AMIN;
-                float dw[TN], dmn[TN];
-                v4i bmin[TN];
+    };
+
+    // Superblock epilogue (K-quants): scale the exact integer sums and fold them
+    // into the fp32 accumulators.  Per row tile, the limbs are combined first and
+    // the min-term MFMAs issued, so their latency overlaps the scale reads.
+    auto epilogue = [&](int sb) {
+        const uint32_t ep = lds_addr(smem + NBUF * C::STAGE + (sb & 1) * C::EP);
+        const uint32_t edx = ep, edw = ep + C::EP_DX, edm = ep + C::EP_DX + C::EP_DW;
+        const uint32_t eam = ep + C::EP_DX + C::EP_DW + C::EP_DMIN, ebm = eam + C::EP_AMIN;
 #pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    const int wc = (wn * TN + j) * 32 + lrow;
-                    dw[j] = ds_read32(edw + wc * 4);
-                    if constexpr (FMT == FMT_Q4_K) {
-                        dmn[j] = ds_read32(edm + wc * 4);
-                        bmin[j] = ds_read128(ebm + (wn * TN + j) * 1024 + lane * 16);
+        for (int i = 0; i < TM; i++) {
+            v4i amin = {};
+            if constexpr (FMT == FMT_Q4_K) amin = ds_read128(eam + (wm * TM + i) * 1024 + lane * 16);
+            v4i dx4[4];
+#pragma unroll
+            for (int g = 0; g < 4; g++) dx4[g] = ds_read128(edx + ((wm * TM + i) * 32 + 8 * g + 4 * lhalf) * 4);
+            // exact integer sum in place of the lo limb (the hi limb is dead after this)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int rr = 0; rr < 16; rr++) alo[i][j][rr] += ahi[i][j][rr] << 7;
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int wc = (wn * TN + j) * 32 + lrow;
+                float dw = ds_read32(edw + wc * 4), dmn = 0.0f;
+                v4i bmin = {};
+                if constexpr (FMT == FMT_Q4_K) {
+                    dmn = ds_read32(edm + wc * 4);
+                    bmin = ds_read128(ebm + (wn * TN + j) * 1024 + lane * 16);
+                }
+                // the asm reads above complete here; the operands tie every result to the wait
+                if (j == 0)
+                    asm volatile("s_waitcnt lgkmcnt(0)"
+                                 : "+v"(dx4[0]), "+v"(dx4[1]), "+v"(dx4[2]), "+v"(dx4[3]), "+v"(amin), "+v"(bmin),
+                                   "+v"(dw), "+v"(dmn));
+                else
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(bmin), "+v"(dw), "+v"(dmn));
+                v16f fmin = {};
+                if constexpr (FMT == FMT_Q4_K)
+                    fmin = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, amin),
+                                                                 __builtin_bit_cast(v8h, bmin), (v16f){}, 0, 0, 0);
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const float4 d4 = __builtin_bit_cast(float4, dx4[g]);
+                    const float dxs[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int rr = 4 * g + q;
+                        float tv = dw * (float)alo[i][j][rr];
+                        if constexpr (FMT == FMT_Q4_K) tv -= dmn * fmin[rr];
+                        acc[i][j][rr] += dxs[q] * tv;
                     }
                 }
-#pragma unroll
-                for (int i = 0; i < TM; i++) {
-                    v4i amin = {};
-                    if constexpr (FMT == FMT_Q4_K) amin = ds_read128(eam + (wm * TM + i) * 1024 + lane * 16);
-                    v4i dx4[4];
-#pragma unroll
-                    for (int g = 0; g < 4; g++) dx4[g] = ds_read128(edx + ((wm * TM + i) * 32 + 8 * g + 4 * lhalf) * 4);
-                    // the asm reads above complete here; the operands tie every result to the wait
-                    if constexpr (FMT == FMT_Q4_K) {
-                        if (i == 0)
-                            asm volatile("s_waitcnt lgkmcnt(0)"
-                                         : "+v"(dx4[0]), "+v"(dx4[1]), "+v"(dx4[2]), "+v"(dx4[3]), "+v"(amin),
-                                           "+v"(bmin[0]), "+v"(bmin[TN - 1]), "+v"(dw[0]), "+v"(dw[TN - 1]),
-                                           "+v"(dmn[0]), "+v"(dmn[TN - 1]));
-                        else
-                            asm volatile("s_waitcnt lgkmcnt(0)"
-                                         : "+v"(dx4[0]), "+v"(dx4[1]), "+v"(dx4[2]), "+v"(dx4[3]), "+v"(amin));
-                    } else {
-                        if (i == 0)
-                            asm volatile("s_waitcnt lgkmcnt(0)"
-                                         : "+v"(dx4[0]), "+v"(dx4[1]), "+v"(dx4[2]), "+v"(dx4[3]), "+v"(dw[0]),
-                                           "+v"(dw[TN - 1]));
-                        else
-                            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(dx4[0]), "+v"(dx4[1]), "+v"(dx4[2]), "+v"(dx4[3]));
-                    }
-#pragma unroll
-                    for (int j = 0; j < TN; j++) {
-                        v16f fmin = {};
-                        if constexpr (FMT == FMT_Q4_K)
-                            fmin = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, amin),
-                                                                         __builtin_bit_cast(v8h, bmin[j]), (v16f){}, 0,
-                                                                         0, 0);
-#pragma unroll
-                        for (int g = 0; g < 4; g++) {
-                            const float4 d4 = __builtin_bit_cast(float4, dx4[g]);
-                            const float dxs[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                            for (int q = 0; q < 4; q++) {
-                                const int rr = 4 * g + q;
-                                const int isum = alo[i][j][rr] + (ahi[i][j][rr] << 7);
-                                float tv = dw[j] * (float)isum;
-                                if constexpr (FMT == FMT_Q4_K) tv -= dmn[j] * fmin[rr];
-                                acc[i][j][rr] += dxs[q] * tv;
-                            }
-                        }
-                        alo[i][j] = (v16i){};
-                        ahi[i][j] = (v16i){};
-                    }
-                }
+                alo[i][j] = (v16i){};
+                ahi[i][j] = (v16i){};
             }
         }
+    };
+
+#pragma unroll
+    for (int x = 0; x < DIST; x++) issue(x);
+    // UNR stages per iteration (a whole superblock for the K-quants), so the
+    // stage slot and the DMA count still in flight are constants per position.
+    constexpr int UNR = C::limbs ? SPB : NBUF;
+    static_assert(UNR == NBUF, "slot of each unrolled stage is its position");
+    for (int s0 = 0; s0 < nst; s0 += UNR) {
+        static_for<0, UNR>([&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            const int s = s0 + q;
+            if (C::limbs || s < nst) {  // nst is a multiple of 2 (Q8_0 / F16), of SPB (K-quants)
+                // stage s has landed once only the DMAs of stages s+1 .. s+DIST-1 are outstanding
+                wait_vmcnt_c<C::template waits<DIST>(q)>();
+                barrier_nofence();  // stage s landed for every wave; stage s-1 fully consumed
+                issue(s + DIST);
+                compute(smem + q * C::STAGE);  // s0 is a multiple of NBUF: stage s sits in slot q
+            }
+        });
+        if constexpr (C::limbs) epilogue(s0 / SPB);
     }
+    // no DMA may still be writing this workgroup's LDS when it exits
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // store: lanes 0..31 of a register write 32 consecutive floats of one row
 #pragma unroll

@@ -33,23 +33,22 @@ __device__ __forceinline__ float4 load4(const float *p) {
 }
 
 // Output layouts of the activation quantizers.
-enum { OUT_GGUF = 0, OUT_ROWS = 1, OUT_TILED = 2 };
+enum { OUT_GGUF = 0, OUT_ROWS = 1 };
 
 // ---------------------------------------------------------------------------
 // Q8_0 activations: quantize_row_q8_0 (variant selects the rounding).
 // Lanes 8g..8g+7 of a wave own one 32-value block.
 // OUT_ROWS : xq int8 [m][k] + xd float [m][k/32]
-// OUT_TILED: xq tiled [m_pad][kb_pad] + xd float [kb_pad/32][m_pad]; blocks past
-//            m or k are written as zeros (d = 0)
 // OUT_GGUF : block_q8_0 rows
+// (the tiled GEMM layout is written by k_quantize_tiled below)
 // ---------------------------------------------------------------------------
 template <int VARIANT, int OUT, bool VEC4>
 __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__ x, int64_t ldx,
                                                        int8_t *__restrict__ out, float *__restrict__ xd,
                                                        int64_t m, int64_t k, int64_t m_pad, int64_t kb_pad) {
     const int64_t nbr = k / QK8_0;
-    const int64_t nbx = (OUT == OUT_TILED) ? kb_pad / QK8_0 : nbr;
-    const int64_t rows = (OUT == OUT_TILED) ? m_pad : m;
+    const int64_t nbx = nbr;
+    const int64_t rows = m;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t blk = gid >> 3;
     const int sub = (int)(gid & 7);
@@ -76,9 +75,6 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__
     if (OUT == OUT_ROWS) {
         *(uint32_t *)(out + row * k + b * QK8_0 + sub * 4) = packed;
         if (sub == 0) xd[row * nbr + b] = f16_bits_to_f32(dh);
-    } else if (OUT == OUT_TILED) {
-        *(uint32_t *)(out + tiled_off(row, b * QK8_0 + sub * 4, kb_pad)) = packed;
-        if (sub == 0) xd[b * m_pad + row] = f16_bits_to_f32(dh);
     } else {
         uint8_t *blkp = (uint8_t *)out + (row * nbr + b) * sizeof(block_q8_0);
         uint16_t *qs16 = (uint16_t *)(blkp + 2 + sub * 4);  // 2-byte aligned in the 34-byte block
@@ -93,8 +89,6 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__
 // owns values 4l..4l+3.  max is the FIRST value of largest magnitude: the
 // reduction orders (|x| descending, index ascending).
 // OUT_ROWS : xq int8 [m][k], xd float [m][k/256], xbs int16 [m][k/16]
-// OUT_TILED: xq tiled [m_pad][k], xd float [k/256][m_pad], xmin fragments
-//            (rows past m are written as zeros)
 // OUT_GGUF : block_q8_K rows
 // ---------------------------------------------------------------------------
 template <int OUT, bool VEC4>
@@ -103,7 +97,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const float *__restrict__
                                                        int16_t *__restrict__ xbs, _Float16 *__restrict__ xmin,
                                                        int64_t m, int64_t k, int64_t m_pad) {
     const int64_t nbr = k / QK_K;
-    const int64_t rows = (OUT == OUT_TILED) ? m_pad : m;
+    const int64_t rows = m;
     const int lane = threadIdx.x & 63;
     const int64_t blk = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     if (blk >= rows * nbr) return;  // whole waves leave together
@@ -153,17 +147,6 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const float *__restrict__
         *(uint32_t *)(out + row * k + b * QK_K + lane * 4) = packed;
         if ((lane & 3) == 0) xbs[row * (k / 16) + b * 16 + (lane >> 2)] = (int16_t)s16;
         if (lane == 0) xd[row * nbr + b] = dval;
-    } else if (OUT == OUT_TILED) {
-        *(uint32_t *)(out + tiled_off(row, b * QK_K + lane * 4, k)) = packed;
-        if (lane == 0) xd[b * m_pad + row] = dval;
-        // B_j (sum of the 32 quants of sub-block j) lands in lane 8j
-        const int B = s16 + __shfl_xor(s16, 4);
-        if ((lane & 7) == 0) {
-            const int j = lane >> 3;
-            _Float16 *frag = xmin + (((row >> 5) * nbr + b) << 9);  // 1 KB = 512 halves
-            frag[((row & 31) << 3) + j] = (_Float16)(B & 63);
-            frag[((32 + (row & 31)) << 3) + j] = (_Float16)((B >> 6) * 64);
-        }
     } else {
         uint8_t *blkp = (uint8_t *)out + (row * nbr + b) * sizeof(block_q8_K);
         *(uint32_t *)(blkp + 4 + lane * 4) = packed;
@@ -188,22 +171,166 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
     o[3] = f32_to_f16_bits(v.w);
 }
 
-// fp32 -> fp16 into the tiled plane [m_pad][kb_pad bytes]; 4 values (8 bytes) per lane.
-template <bool VEC4>
-__global__ __launch_bounds__(256) void k_quantize_f16_tiled(const float *__restrict__ x, int64_t ldx,
-                                                            uint8_t *__restrict__ y, int64_t m, int64_t k,
-                                                            int64_t m_pad, int64_t kb_pad) {
-    const int64_t q8 = kb_pad / 8;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= m_pad * q8) return;
-    const int64_t row = gid / q8, c = gid - row * q8;
-    uint2 o = make_uint2(0u, 0u);
-    if (row < m && c * 4 < k) {
-        const float4 v = load4<VEC4>(x + row * ldx + c * 4);
-        o.x = (uint32_t)f32_to_f16_bits(v.x) | ((uint32_t)f32_to_f16_bits(v.y) << 16);
-        o.y = (uint32_t)f32_to_f16_bits(v.z) | ((uint32_t)f32_to_f16_bits(v.w) << 16);
+
+// Cross-lane steps on the DPP path (no LDS round trip).  Each step combines a
+// lane with a partner inside its 16-lane row: quad_perm [1,0,3,2] (xor 1),
+// quad_perm [2,3,0,1] (xor 2), row_half_mirror (i <-> 7-i within 8 lanes),
+// row_mirror (i <-> 15-i).  After xor1, xor2, half_mirror every lane holds the
+// combination over its 8-lane group; after row_mirror, over its 16-lane row.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    return fmaxf(v, dpp_f<0x141>(v));
+}
+__device__ __forceinline__ int sum8(int v) {
+    v += dpp_i<0xB1>(v);
+    v += dpp_i<0x4E>(v);
+    return v + dpp_i<0x141>(v);
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+// max over the whole wave, wave-uniform result
+__device__ __forceinline__ float wave_max(float v) {
+    v = max8(v);
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
+// ---------------------------------------------------------------------------
+// Activations into the tiled GEMM layout (1 KB fragments: lane L of a fragment
+// holds row L%32, bytes 16*(L/32)..+16 of a 32-byte K chunk).  One workgroup
+// per (32-row tile, CB bytes of K): it quantizes the 32 rows with the same
+// per-block arithmetic as the row kernels above, assembles the CB/32 fragments
+// in LDS and writes them as whole 1 KB fragments (16 bytes per lane, fully
+// coalesced), then the scales (32 consecutive floats per block) and, for
+// Q8_K, the min-term fragment.  Rows past m and K bytes past the row are
+// written as zeros (d = 0).
+//   Q8_0 (TQ_Q8_0): CB = 128 (4 blocks per row), xd float [kb_pad/32][m_pad]
+//   Q8_K (TQ_Q8_K): CB = 256 (one superblock), xd float [k/256][m_pad], and
+//        the min-term fragment of (tile, superblock): halves (r, j) = B_j & 63
+//        and (32 + r, j) = 64*(B_j >> 6), B_j = sum of the 32 quants of
+//        sub-block j (exact in fp16)
+//   F16  (TQ_F16) : CB = 128 (64 values per row)
+// ---------------------------------------------------------------------------
+enum { TQ_Q8_0 = 0, TQ_Q8_K = 1, TQ_F16 = 2 };
+
+template <int FMT, int VARIANT, bool VEC4>
+__global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict__ x, int64_t ldx,
+                                                        int8_t *__restrict__ xq, float *__restrict__ xd,
+                                                        _Float16 *__restrict__ xmin, int64_t m, int64_t k,
+                                                        int64_t m_pad, int64_t kb_pad) {
+    constexpr int CB = (FMT == TQ_Q8_K) ? 256 : 128;   // K bytes per workgroup
+    constexpr int BPV = (FMT == TQ_F16) ? 2 : 1;       // bytes per value
+    constexpr int NCH = CB / 32;                        // fragments per workgroup
+    constexpr int LPR = CB / (4 * BPV);                 // lanes per row (4 values each)
+    constexpr int RPI = 64 / LPR;                       // rows per wave pass
+    constexpr int FST = 1024 + 16;                      // padded fragment stride (LDS banks)
+    constexpr int NSC = (FMT == TQ_Q8_0) ? NCH : (FMT == TQ_Q8_K ? 1 : 0);  // scale rows
+    __shared__ __attribute__((aligned(16))) int8_t frag[NCH * FST];
+    __shared__ float dsh[NSC > 0 ? NSC : 1][32];
+    __shared__ __attribute__((aligned(16))) _Float16 msh[FMT == TQ_Q8_K ? 512 : 8];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t ncb = kb_pad / CB;
+    const int64_t rt = blockIdx.x / ncb, cb = blockIdx.x - rt * ncb;
+    const int sub = lane % LPR, rsub = lane / LPR;
+    const int kbyte = sub * 4 * BPV;                    // byte of this lane's 4 values within CB
+    const int c = kbyte >> 5, cbyte = kbyte & 31;       // fragment, byte within the 32-byte chunk
+    constexpr int NIT = 8 / RPI;                        // rows per lane
+    const int64_t kv = (cb * CB + kbyte) / BPV;         // first value index of this lane
+    float4 vin[NIT];                                    // every load in flight before any math
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int64_t row = rt * 32 + wave * 8 + it * RPI + rsub;
+        vin[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (row < m && kv < k) vin[it] = load4<VEC4>(x + row * ldx + kv);
     }
-    *(uint2 *)(y + tiled_off(row, c * 8, kb_pad)) = o;
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int r = wave * 8 + it * RPI + rsub;       // row within the tile
+        const float4 v = vin[it];
+        int8_t *dst = frag + c * FST + ((r + 32 * (cbyte >> 4)) << 4) + (cbyte & 15);
+        if constexpr (FMT == TQ_F16) {
+            uint2 o;
+            o.x = (uint32_t)f32_to_f16_bits(v.x) | ((uint32_t)f32_to_f16_bits(v.y) << 16);
+            o.y = (uint32_t)f32_to_f16_bits(v.z) | ((uint32_t)f32_to_f16_bits(v.w) << 16);
+            *(uint2 *)dst = o;
+        } else if constexpr (FMT == TQ_Q8_0) {
+            const float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            const float d = amax / 127.f;
+            float id;
+            if (VARIANT == MQ_Q8_0_X86) id = (amax != 0.0f) ? 127.f / amax : 0.0f;
+            else id = (d != 0.0f) ? 1.0f / d : 0.0f;
+            auto q = [&](float xv) -> uint32_t {
+                const float t = xv * id;
+                float rr = (VARIANT == MQ_Q8_0_REF) ? roundf(t) : rintf(t);
+                rr = fminf(fmaxf(rr, -128.f), 127.f);
+                return (uint32_t)((int)rr & 0xff);
+            };
+            *(uint32_t *)dst = q(v.x) | (q(v.y) << 8) | (q(v.z) << 16) | (q(v.w) << 24);
+            if ((sub & 7) == 0) dsh[c][r] = f16_bits_to_f32(f32_to_f16_bits(d));
+        } else {
+            // ggml's max: the FIRST value of largest magnitude.  Per lane, the first
+            // of its 4 values with the lane's largest |x|; then the lowest lane that
+            // holds the wave's largest |x|.
+            const float vals[4] = {v.x, v.y, v.z, v.w};
+            float la = 0.0f, lm = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (fabsf(vals[i]) > la) {
+                    la = fabsf(vals[i]);
+                    lm = vals[i];
+                }
+            const float amax = wave_max(la);
+            uint32_t packed = 0;
+            int s16 = 0;
+            float dval = 0.0f;
+            if (amax != 0.0f) {
+                const unsigned long long hit = __ballot(la == amax);
+                const float mx = readlane_f(lm, __ffsll((long long)hit) - 1);
+                const float iscale = -127.f / mx;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    int qv = nearest_int(iscale * vals[i]);
+                    qv = qv < 127 ? qv : 127;
+                    packed |= (uint32_t)(qv & 0xff) << (8 * i);
+                    s16 += qv;
+                }
+                dval = 1.0f / iscale;
+            }
+            *(uint32_t *)dst = packed;
+            if (lane == 0) dsh[0][r] = dval;
+            // B_j (sum of the 32 quants of sub-block j) lands in lane 8j
+            const int B = sum8(s16);
+            if ((lane & 7) == 0) {
+                const int j = lane >> 3;
+                msh[(r << 3) + j] = (_Float16)(B & 63);
+                msh[((32 + r) << 3) + j] = (_Float16)((B >> 6) * 64);
+            }
+        }
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int p = t; p < NCH * 64; p += 256) {
+        const int f = p >> 6, L = p & 63;
+        const int4 val = *(const int4 *)(frag + f * FST + L * 16);
+        *(int4 *)(xq + ((rt * (kb_pad >> 5) + cb * NCH + f) << 10) + L * 16) = val;
+    }
+    if constexpr (NSC > 0) {
+        if (t < NSC * 32) xd[(cb * NSC + (t >> 5)) * m_pad + rt * 32 + (t & 31)] = dsh[t >> 5][t & 31];
+    }
+    if constexpr (FMT == TQ_Q8_K) {
+        if (t < 64) ((int4 *)(xmin + ((rt * ncb + cb) << 9)))[t] = ((const int4 *)msh)[t];
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -449,8 +576,8 @@ static inline unsigned grid_for(int64_t threads) { return (unsigned)((threads + 
 template <int OUT>
 static hipError_t q8_0_dispatch(const float *x, int64_t ldx, int8_t *out, float *xd, int64_t m, int64_t k, int variant,
                                 int64_t m_pad, int64_t kb_pad, hipStream_t s) {
-    const int64_t rows = (OUT == OUT_TILED) ? m_pad : m;
-    const int64_t nbx = (OUT == OUT_TILED) ? kb_pad / QK8_0 : k / QK8_0;
+    const int64_t rows = m;
+    const int64_t nbx = k / QK8_0;
     const int64_t threads = rows * nbx * 8;
     if (threads == 0) return hipSuccess;
     const bool v4 = aligned16(x, ldx);
@@ -471,7 +598,7 @@ static hipError_t q8_0_dispatch(const float *x, int64_t ldx, int8_t *out, float 
 template <int OUT>
 static hipError_t q8_K_dispatch(const float *x, int64_t ldx, int8_t *out, float *xd, int16_t *xbs, _Float16 *xmin,
                                 int64_t m, int64_t k, int64_t m_pad, hipStream_t s) {
-    const int64_t rows = (OUT == OUT_TILED) ? m_pad : m;
+    const int64_t rows = m;
     const int64_t threads = rows * (k / QK_K) * 64;
     if (threads == 0) return hipSuccess;
     const dim3 g(grid_for(threads)), b(256);
@@ -479,6 +606,32 @@ static hipError_t q8_K_dispatch(const float *x, int64_t ldx, int8_t *out, float 
         hipLaunchKernelGGL((k_quantize_q8_K<OUT, true>), g, b, 0, s, x, ldx, out, xd, xbs, xmin, m, k, m_pad);
     else
         hipLaunchKernelGGL((k_quantize_q8_K<OUT, false>), g, b, 0, s, x, ldx, out, xd, xbs, xmin, m, k, m_pad);
+    return hipGetLastError();
+}
+
+template <int FMT>
+static hipError_t tiled_dispatch(const float *x, int64_t ldx, int8_t *xq, float *xd, _Float16 *xmin, int64_t m,
+                                 int64_t k, int variant, int64_t m_pad, int64_t kb_pad, hipStream_t s) {
+    constexpr int CB = (FMT == TQ_Q8_K) ? 256 : 128;
+    if (m_pad % 32 != 0 || kb_pad % CB != 0) return hipErrorInvalidValue;
+    const int64_t wgs = (m_pad / 32) * (kb_pad / CB);
+    if (wgs == 0) return hipSuccess;
+    const dim3 g((unsigned)wgs), b(256);
+    const bool v4 = aligned16(x, ldx);
+#define MQ_TQ(VAR)                                                                                                      \
+    if (v4) hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, true>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad); \
+    else hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, false>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad);
+    if (FMT != TQ_Q8_0) {
+        MQ_TQ(MQ_Q8_0_X86);
+    } else {
+        switch (variant) {
+            case MQ_Q8_0_X86: MQ_TQ(MQ_Q8_0_X86); break;
+            case MQ_Q8_0_NEON: MQ_TQ(MQ_Q8_0_NEON); break;
+            case MQ_Q8_0_REF: MQ_TQ(MQ_Q8_0_REF); break;
+            default: return hipErrorInvalidValue;
+        }
+    }
+#undef MQ_TQ
     return hipGetLastError();
 }
 
@@ -501,23 +654,16 @@ hipError_t launch_quantize_act_planar(int wtype, const float *x, int64_t ldx, vo
     float *xd = (float *)(base + a.xd);
     switch (wtype) {
         case MQ_TYPE_Q8_0:
-            if (tiled) return q8_0_dispatch<OUT_TILED>(x, ldx, xq, xd, m, k, q8_0_variant, a.m_pad, a.kb_pad, s);
+            if (tiled) return tiled_dispatch<TQ_Q8_0>(x, ldx, xq, xd, nullptr, m, k, q8_0_variant, a.m_pad, a.kb_pad, s);
             return q8_0_dispatch<OUT_ROWS>(x, ldx, xq, xd, m, k, q8_0_variant, m, k, s);
         case MQ_TYPE_Q4_K:
         case MQ_TYPE_Q6_K:
             if (tiled)
-                return q8_K_dispatch<OUT_TILED>(x, ldx, xq, xd, nullptr, (_Float16 *)(base + a.xmin), m, k, a.m_pad, s);
+                return tiled_dispatch<TQ_Q8_K>(x, ldx, xq, xd, (_Float16 *)(base + a.xmin), m, k, 0, a.m_pad, a.kb_pad, s);
             return q8_K_dispatch<OUT_ROWS>(x, ldx, xq, xd, (int16_t *)(base + a.xbs), nullptr, m, k, m, s);
-        case MQ_TYPE_F16: {
-            if (!tiled) return launch_quantize_f16(x, ldx, base + a.xq, m, k, s);
-            const int64_t threads = a.m_pad * (a.kb_pad / 8);
-            const dim3 g(grid_for(threads)), b(256);
-            if (aligned16(x, ldx))
-                hipLaunchKernelGGL((k_quantize_f16_tiled<true>), g, b, 0, s, x, ldx, base + a.xq, m, k, a.m_pad, a.kb_pad);
-            else
-                hipLaunchKernelGGL((k_quantize_f16_tiled<false>), g, b, 0, s, x, ldx, base + a.xq, m, k, a.m_pad, a.kb_pad);
-            return hipGetLastError();
-        }
+        case MQ_TYPE_F16:
+            if (tiled) return tiled_dispatch<TQ_F16>(x, ldx, xq, nullptr, nullptr, m, k, 0, a.m_pad, a.kb_pad, s);
+            return launch_quantize_f16(x, ldx, base + a.xq, m, k, s);
         default: return hipErrorInvalidValue;
     }
 }
