@@ -444,7 +444,9 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
     // no DMA may still be writing this workgroup's LDS when it exits
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // store: lanes 0..31 of a register write 32 consecutive floats of one row
+    // store: lanes 0..31 of a register write 32 consecutive floats of one row.
+    // (Staging the tile through LDS for 16-byte row stores was measured slower on
+    // MI355X: the extra barrier and LDS pass cost more than the store instructions.)
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
