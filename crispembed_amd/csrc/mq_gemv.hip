@@ -7,11 +7,15 @@
 // byte is read exactly once; activations (m x k int8, a few KB) stay in L1/L2.
 // Integer block dots use v_dot4_i32_i8; per-block scales are applied in fp32,
 // as ggml's vec_dot does.
-//   Q4_K reads the GGUF blocks directly (144-byte blocks stay 16-byte aligned).
-//   Q6_K and Q8_0 read the byte-identical split planes of the weight image
-//   (their 210- and 34-byte GGUF blocks are only 2-byte aligned).
+//   Q4_K runs on the matrix cores (k_gemv_kq_mfma below): at m <= 8 the dot4
+//   form is VALU-bound long before HBM is.
+//   Q6_K runs on the matrix cores too (same kernel).
+//   Q8_0 reads the byte-identical split planes of the weight image (its 34-byte
+//   GGUF blocks are only 2-byte aligned).
 //   F16 uses v_dot2_f32_f16 on fp16 activations.
 #include "mq_internal.h"
+
+#include <type_traits>
 
 namespace mq {
 
@@ -104,71 +108,6 @@ __global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t *__restrict__ w
     wave_sum_store<MM>(part, y, ldy, row, lane);
 }
 
-// ---- Q6_K x Q8_K on the split planes: lane = 4*sb_slot + (2*h + t), 64 values per lane ----
-template <int MM>
-__global__ __launch_bounds__(256) void k_gemv_q6_K(const uint8_t *__restrict__ ql, const uint8_t *__restrict__ qh,
-                                                   const int8_t *__restrict__ scp, const uint16_t *__restrict__ d16,
-                                                   const int8_t *__restrict__ xq, const float *__restrict__ xd,
-                                                   const int16_t *__restrict__ xbs, float *__restrict__ y, int N,
-                                                   int K, int64_t ldy) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= N) return;
-    const int nsb = K / QK_K;
-    const int t4 = lane & 3, h = t4 >> 1, t = t4 & 1;
-    float part[MM];
-#pragma unroll
-    for (int m = 0; m < MM; m++) part[m] = 0.f;
-    for (int sb = lane >> 2; sb < nsb; sb += 16) {
-        const int64_t sbi = (int64_t)row * nsb + sb;
-        const uint4 L = *(const uint4 *)(ql + sbi * 128 + 64 * h + 16 * t);
-        const uint4 Lh = *(const uint4 *)(ql + sbi * 128 + 64 * h + 32 + 16 * t);
-        const uint4 H = *(const uint4 *)(qh + sbi * 64 + 32 * h + 16 * t);
-        const uint2 scw = *(const uint2 *)(scp + sbi * 16 + 8 * h);
-        const float d = (float)__builtin_bit_cast(_Float16, d16[sbi]);
-        int8_t sc8[8];
-        *(uint2 *)sc8 = scw;
-        const int sc0 = sc8[t], sc1 = sc8[t + 2], sc2 = sc8[t + 4], sc3 = sc8[t + 6];
-        const uint32_t Lw[4] = {L.x, L.y, L.z, L.w}, Lhw[4] = {Lh.x, Lh.y, Lh.z, Lh.w}, Hw[4] = {H.x, H.y, H.z, H.w};
-        uint32_t g0[4], g1[4], g2[4], g3[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            g0[i] = (Lw[i] & 0x0F0F0F0F) | ((Hw[i] << 4) & 0x30303030);
-            g1[i] = (Lhw[i] & 0x0F0F0F0F) | ((Hw[i] << 2) & 0x30303030);
-            g2[i] = ((Lw[i] >> 4) & 0x0F0F0F0F) | (Hw[i] & 0x30303030);
-            g3[i] = ((Lhw[i] >> 4) & 0x0F0F0F0F) | ((Hw[i] >> 2) & 0x30303030);
-        }
-#pragma unroll
-        for (int m = 0; m < MM; m++) {
-            const int8_t *xr = xq + (int64_t)m * K + sb * QK_K + 128 * h + 16 * t;
-            const uint4 x0 = *(const uint4 *)(xr + 0);
-            const uint4 x1 = *(const uint4 *)(xr + 32);
-            const uint4 x2 = *(const uint4 *)(xr + 64);
-            const uint4 x3 = *(const uint4 *)(xr + 96);
-            int s0 = dot4(g0[0], x0.x, 0), s1 = dot4(g1[0], x1.x, 0), s2 = dot4(g2[0], x2.x, 0),
-                s3 = dot4(g3[0], x3.x, 0);
-            s0 = dot4(g0[1], x0.y, s0);
-            s1 = dot4(g1[1], x1.y, s1);
-            s2 = dot4(g2[1], x2.y, s2);
-            s3 = dot4(g3[1], x3.y, s3);
-            s0 = dot4(g0[2], x0.z, s0);
-            s1 = dot4(g1[2], x1.z, s1);
-            s2 = dot4(g2[2], x2.z, s2);
-            s3 = dot4(g3[2], x3.z, s3);
-            s0 = dot4(g0[3], x0.w, s0);
-            s1 = dot4(g1[3], x1.w, s1);
-            s2 = dot4(g2[3], x2.w, s2);
-            s3 = dot4(g3[3], x3.w, s3);
-            // (q6 - 32) * q8 summed = q6.q8 - 32 * bsum16 of the same 16 values
-            const int16_t *bs = xbs + (int64_t)m * (K / 16) + sb * 16 + 8 * h + t;
-            const int isum = sc0 * (s0 - 32 * bs[0]) + sc1 * (s1 - 32 * bs[2]) + sc2 * (s2 - 32 * bs[4]) +
-                             sc3 * (s3 - 32 * bs[6]);
-            part[m] += (d * xd[(int64_t)m * nsb + sb]) * (float)isum;
-        }
-    }
-    wave_sum_store<MM>(part, y, ldy, row, lane);
-}
-
 // ---- Q8_0 x Q8_0 on the split planes: one 32-value block per lane ----
 template <int MM>
 __global__ __launch_bounds__(256) void k_gemv_q8_0(const int8_t *__restrict__ qs, const uint16_t *__restrict__ d16,
@@ -233,21 +172,248 @@ __global__ __launch_bounds__(256) void k_gemv_f16(const uint16_t *__restrict__ w
     wave_sum_store<MM>(part, y, ldy, row, lane);
 }
 
+// ---- K-quants on MFMA (m <= 8) ----
+// Q4_K: per 64-value chunk c of a superblock, v_mfma_i32_16x16x64_i8 multiplies the 16
+// rows' 4-bit quants (A: row l%16, k 16*(l/16)..+16 of the chunk) by an activation operand
+// whose 16 columns are (token m = col%8, sub-block g = col/8): column (m, g) holds the
+// token's quants on the k range of sub-block 2c+g and zeros elsewhere.  So output column
+// (m, g) is the exact sub-block sum isum_{2c+g}[row][m], and the 6-bit scale is one
+// integer multiply-add per output.  The min term sum_j m_j * B_j is one
+// v_mfma_f32_16x16x16_f16 (m_j and the two limbs of B_j exact in fp16, products and sums
+// below 2^24: exact).  Per superblock, as ggml's vec_dot_q4_K_q8_K:
+//   y += d_x * (d * sum_j sc_j isum_j - dmin * sum_j m_j B_j).
+// Q6_K: per 32-value K-step, v_mfma_i32_16x16x32_i8 multiplies the unsigned 6-bit quants q
+// (rebuilt from the nibble and 2-bit planes) by an activation operand whose columns are
+// (token m, 16-group g) the same way, so each output is one 16-value group sum and its
+// int8 scale is one integer multiply-add.  The -32 offset of every quant is
+// sum_g sc_g * 32 * bsum16_g, one v_mfma_f32_16x16x16_f16 per superblock (sc and
+// 32*bsum16 exact in fp16).  Per superblock, as ggml's vec_dot_q6_K_q8_K:
+//   y += d_x * d * sum_g sc_g (sum_{i in g} q_i x_i - 32 bsum_g).
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+struct GvLane {
+    int lane, wave, col, q, m, g;
+    bool xlive;  // this lane carries activation data: its k range lies in the column's sub-block / group
+    bool mlive;  // min-term / offset operand column is a real token (cols >= 8 stay zero: M <= 8)
+};
+
+__device__ __forceinline__ GvLane gv_lane(int M) {
+    GvLane L;
+    L.lane = threadIdx.x & 63;
+    L.wave = threadIdx.x >> 6;
+    L.col = L.lane & 15;
+    L.q = L.lane >> 4;
+    L.m = L.col & 7;
+    L.g = L.col >> 3;
+    L.xlive = (L.m < M) && ((L.q >> 1) == L.g);
+    L.mlive = L.col < M;
+    return L;
+}
+
+struct Q4Act {
+    v4i_t xa[4];
+    v4h bmin;
+    float dx;
+};
+__device__ __forceinline__ Q4Act q4_act(const GvLane &L, const int8_t *xq, const float *xd, const _Float16 *xgm, int K,
+                                        int M, int sb) {
+    Q4Act A;
+    const int8_t *xr = xq + (int64_t)L.m * K + sb * QK_K + 16 * L.q;
+#pragma unroll
+    for (int c = 0; c < 4; c++) A.xa[c] = L.xlive ? *(const v4i_t *)(xr + 64 * c) : (v4i_t){0, 0, 0, 0};
+    A.bmin = (v4h){};
+    if (L.mlive) A.bmin = *(const v4h *)(xgm + ((sb * 8 + L.col) << 4) + 4 * L.q);
+    A.dx = (L.m < M) ? xd[(int64_t)L.m * (K / QK_K) + sb] : 0.0f;
+    return A;
+}
+struct Q4W {  // one (tile, superblock) of the Q4_K GEMV plane, this lane's share
+    v4i_t wq[4], scv;
+    uint32_t mnv;
+    float4 dd0, dd1;
+};
+__device__ __forceinline__ Q4W q4_load(const GvLane &L, const uint8_t *T) {
+    Q4W W;
+#pragma unroll
+    for (int c = 0; c < 4; c++) W.wq[c] = *(const v4i_t *)(T + GV4_QS + ((c * 2 + (L.q & 1)) * GV_ROWS + L.col) * 16);
+    W.scv = *(const v4i_t *)(T + GV4_SC + (L.g * 4 + L.q) * 16);  // sc of rows 4q+i, chunk c: byte 4c+i
+    W.mnv = *(const uint32_t *)(T + GV4_MN + ((L.q & 1) * GV_ROWS + L.col) * 4);
+    W.dd0 = *(const float4 *)(T + GV4_DD + L.q * 32);
+    W.dd1 = *(const float4 *)(T + GV4_DD + L.q * 32 + 16);
+    return W;
+}
+__device__ __forceinline__ void q4_compute(const GvLane &L, const Q4W &W, const Q4Act &A, float (&part)[4]) {
+    const int sh = 4 * (L.q >> 1);  // low nibbles for k < 32 of the chunk, high for k >= 32
+    int acc[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const v4i_t w = {(W.wq[c].x >> sh) & 0x0F0F0F0F, (W.wq[c].y >> sh) & 0x0F0F0F0F,
+                         (W.wq[c].z >> sh) & 0x0F0F0F0F, (W.wq[c].w >> sh) & 0x0F0F0F0F};
+        const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, A.xa[c], (v4i_t){0, 0, 0, 0}, 0, 0, 0);
+        const int scw = W.scv[c];
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] += __mul24((scw >> (8 * i)) & 0xff, d[i]);  // |d| < 2^23: v_mad_i32_i24
+    }
+    const v4h amin = {(_Float16)(float)(W.mnv & 0xff), (_Float16)(float)((W.mnv >> 8) & 0xff),
+                      (_Float16)(float)((W.mnv >> 16) & 0xff), (_Float16)(float)(W.mnv >> 24)};
+    const v4f fm = __builtin_amdgcn_mfma_f32_16x16x16f16(amin, A.bmin, (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    const float dr[4] = {W.dd0.x, W.dd0.z, W.dd1.x, W.dd1.z}, mr[4] = {W.dd0.y, W.dd0.w, W.dd1.y, W.dd1.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        // column m + 8 (sub-blocks 2c+1) joins column m: row_ror:8 inside each 16-lane row
+        const int isum = acc[i] + __builtin_amdgcn_update_dpp(0, acc[i], 0x128, 0xF, 0xF, false);
+        part[i] += A.dx * (dr[i] * (float)isum - mr[i] * fm[i]);
+    }
+}
+
+struct Q6Act {
+    int64_t xa[8];
+    v4h bofs;
+    float dx;
+};
+__device__ __forceinline__ Q6Act q6_act(const GvLane &L, const int8_t *xq, const float *xd, const int16_t *xbs, int K,
+                                        int M, int sb) {
+    Q6Act A;
+    const int8_t *xr = xq + (int64_t)L.m * K + sb * QK_K + 8 * L.q;
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++) A.xa[kk] = L.xlive ? *(const int64_t *)(xr + 32 * kk) : 0;
+    int64_t bsv = 0;
+    if (L.mlive) bsv = *(const int64_t *)(xbs + (int64_t)L.col * (K / 16) + sb * 16 + 4 * L.q);
+    A.bofs = (v4h){(_Float16)(32.0f * (float)(int16_t)(bsv & 0xffff)),
+                   (_Float16)(32.0f * (float)(int16_t)((bsv >> 16) & 0xffff)),
+                   (_Float16)(32.0f * (float)(int16_t)((bsv >> 32) & 0xffff)),
+                   (_Float16)(32.0f * (float)(int16_t)((bsv >> 48) & 0xffff))};
+    A.dx = (L.m < M) ? xd[(int64_t)L.m * (K / QK_K) + sb] : 0.0f;
+    return A;
+}
+struct Q6W {  // one (tile, superblock) of the Q6_K GEMV plane, this lane's share
+    v4i_t lo0, lo1, hiv, sc0, sc1;
+    uint32_t sc2;
+    float4 dv;
+};
+__device__ __forceinline__ Q6W q6_load(const GvLane &L, const uint8_t *T) {
+    Q6W W;
+    W.lo0 = *(const v4i_t *)(T + GV6_LO + (L.q * GV_ROWS + L.col) * 32);
+    W.lo1 = *(const v4i_t *)(T + GV6_LO + (L.q * GV_ROWS + L.col) * 32 + 16);
+    W.hiv = *(const v4i_t *)(T + GV6_HI + (L.q * GV_ROWS + L.col) * 16);
+    W.sc0 = *(const v4i_t *)(T + GV6_SC + (L.g * 4 + L.q) * 32);
+    W.sc1 = *(const v4i_t *)(T + GV6_SC + (L.g * 4 + L.q) * 32 + 16);
+    W.sc2 = *(const uint32_t *)(T + GV6_SC2 + (L.q * GV_ROWS + L.col) * 4);
+    W.dv = *(const float4 *)(T + GV6_D + L.q * 16);
+    return W;
+}
+__device__ __forceinline__ void q6_compute(const GvLane &L, const Q6W &W, const Q6Act &A, float (&part)[4]) {
+    const int los[8] = {W.lo0.x, W.lo0.y, W.lo0.z, W.lo0.w, W.lo1.x, W.lo1.y, W.lo1.z, W.lo1.w};
+    const int his[4] = {W.hiv.x, W.hiv.y, W.hiv.z, W.hiv.w};
+    const int scs[8] = {W.sc0.x, W.sc0.y, W.sc0.z, W.sc0.w, W.sc1.x, W.sc1.y, W.sc1.z, W.sc1.w};
+    int acc[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++) {
+        const uint32_t h = (uint32_t)his[kk >> 1];
+        const uint32_t h0 = (kk & 1) ? h : (h << 4), h1 = (kk & 1) ? (h >> 2) : (h << 2);
+        const uint32_t w0 = ((uint32_t)los[kk] & 0x0F0F0F0Fu) | (h0 & 0x30303030u);
+        const uint32_t w1 = (((uint32_t)los[kk] >> 4) & 0x0F0F0F0Fu) | (h1 & 0x30303030u);
+        const int64_t w = (int64_t)w0 | ((int64_t)w1 << 32);
+        const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(w, A.xa[kk], (v4i_t){0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] += __mul24((int)(int8_t)(scs[kk] >> (8 * i)), d[i]);  // |d| < 2^23
+    }
+    const v4h asc = {(_Float16)(float)(int8_t)(W.sc2 & 0xff), (_Float16)(float)(int8_t)((W.sc2 >> 8) & 0xff),
+                     (_Float16)(float)(int8_t)((W.sc2 >> 16) & 0xff), (_Float16)(float)(int8_t)(W.sc2 >> 24)};
+    const v4f corr = __builtin_amdgcn_mfma_f32_16x16x16f16(asc, A.bofs, (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    const float dr[4] = {W.dv.x, W.dv.y, W.dv.z, W.dv.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        // column m + 8 (odd 16-groups) joins column m: row_ror:8 inside each 16-lane row
+        const int isum = acc[i] + __builtin_amdgcn_update_dpp(0, acc[i], 0x128, 0xF, 0xF, false);
+        part[i] += A.dx * (dr[i] * ((float)isum - corr[i]));
+    }
+}
+
+// One workgroup per RT row tiles: wave w takes superblocks w, w+8, ... of K, builds their
+// activation operands once, and issues the weight loads of all RT tiles before computing
+// (many small workgroups in flight hide the HBM latency; RT > 1 spreads the activation
+// operand loads over more weight bytes).  The 8 waves' partial 16-row tiles are summed in LDS.
+template <int TYPE, int RT>
+__global__ __launch_bounds__(512) void k_gemv_kq_mfma(const uint8_t *__restrict__ gv, const int8_t *__restrict__ xq,
+                                                      const float *__restrict__ xd, const void *__restrict__ xaux,
+                                                      float *__restrict__ y, int N, int K, int M, int64_t ldy) {
+    constexpr bool Q4 = TYPE == MQ_TYPE_Q4_K;
+    constexpr int BYTES = Q4 ? GV4_BYTES : GV6_BYTES;
+    using W = typename std::conditional<Q4, Q4W, Q6W>::type;
+    __shared__ float red[RT][8][GV_ROWS][8];
+    const GvLane L = gv_lane(M);
+    const int nsb = K / QK_K;
+    const int ntiles = (N + GV_ROWS - 1) / GV_ROWS;
+    const int tile0 = blockIdx.x * RT;
+    float part[RT][4];
+#pragma unroll
+    for (int r = 0; r < RT; r++) part[r][0] = part[r][1] = part[r][2] = part[r][3] = 0.f;
+    for (int sb = L.wave; sb < nsb; sb += 8) {
+        W w[RT];
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            if (tile0 + r < ntiles) {
+                const uint8_t *T = gv + ((int64_t)(tile0 + r) * nsb + sb) * BYTES;
+                if constexpr (Q4) w[r] = q4_load(L, T);
+                else w[r] = q6_load(L, T);
+            }
+        }
+        if constexpr (Q4) {
+            const Q4Act A = q4_act(L, xq, xd, (const _Float16 *)xaux, K, M, sb);
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+                if (tile0 + r < ntiles) q4_compute(L, w[r], A, part[r]);
+        } else {
+            const Q6Act A = q6_act(L, xq, xd, (const int16_t *)xaux, K, M, sb);
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+                if (tile0 + r < ntiles) q6_compute(L, w[r], A, part[r]);
+        }
+    }
+    if (L.col < 8) {
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) red[r][L.wave][4 * L.q + i][L.col] = part[r][i];
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < RT * GV_ROWS * 8; t += blockDim.x) {
+        const int r = t / (GV_ROWS * 8), rr = (t / 8) % GV_ROWS, mm = t & 7;
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < 8; w++) sum += red[r][w][rr][mm];
+        const int64_t row = (int64_t)(tile0 + r) * GV_ROWS + rr;
+        if (row < N && mm < M) y[(int64_t)mm * ldy + row] = sum;
+    }
+}
+
+template <int TYPE>
+static hipError_t launch_kq_mfma(const uint8_t *gv, const int8_t *xq, const float *xd, const void *xaux, float *y,
+                                 int64_t n, int64_t k, int m, int64_t ldy, hipStream_t s) {
+    const int64_t ntiles = (n + GV_ROWS - 1) / GV_ROWS;
+    const dim3 block(512);
+    // two row tiles per workgroup once that still leaves several workgroups per CU
+    if (ntiles >= 4096)
+        hipLaunchKernelGGL((k_gemv_kq_mfma<TYPE, 2>), dim3((unsigned)((ntiles + 1) / 2)), block, 0, s, gv, xq, xd, xaux,
+                           y, (int)n, (int)k, m, ldy);
+    else
+        hipLaunchKernelGGL((k_gemv_kq_mfma<TYPE, 1>), dim3((unsigned)ntiles), block, 0, s, gv, xq, xd, xaux, y, (int)n,
+                           (int)k, m, ldy);
+    return hipSuccess;
+}
+
 template <int MM>
-static void gemv_launch(int type, const uint8_t *wb, const WeightPlanes &p, int64_t n, int64_t k, const uint8_t *xb,
+static hipError_t gemv_launch(int type, const uint8_t *wb, const WeightPlanes &p, int64_t n, int64_t k, const uint8_t *xb,
                         const ActPlanes &ap, float *y, int64_t ldy, hipStream_t s) {
     const dim3 grid((unsigned)((n + 3) / 4)), block(256);
     const int8_t *xq = (const int8_t *)(xb + ap.xq);
     const float *xd = (const float *)(xb + ap.xd);
     const int16_t *xbs = (const int16_t *)(xb + ap.xbs);
     switch (type) {
-        case MQ_TYPE_Q4_K:
-            hipLaunchKernelGGL(k_gemv_q4_K<MM>, grid, block, 0, s, wb, xq, xd, xbs, y, (int)n, (int)k, ldy);
-            break;
-        case MQ_TYPE_Q6_K:
-            hipLaunchKernelGGL(k_gemv_q6_K<MM>, grid, block, 0, s, wb + p.ql, wb + p.qh, (const int8_t *)(wb + p.sc),
-                               (const uint16_t *)(wb + p.d16), xq, xd, xbs, y, (int)n, (int)k, ldy);
-            break;
+        case MQ_TYPE_Q4_K: return launch_kq_mfma<MQ_TYPE_Q4_K>(wb + p.gv, xq, xd, xb + ap.xgm, y, n, k, MM, ldy, s);
+        case MQ_TYPE_Q6_K: return launch_kq_mfma<MQ_TYPE_Q6_K>(wb + p.gv, xq, xd, xbs, y, n, k, MM, ldy, s);
         case MQ_TYPE_Q8_0:
             hipLaunchKernelGGL(k_gemv_q8_0<MM>, grid, block, 0, s, (const int8_t *)(wb + p.qs),
                                (const uint16_t *)(wb + p.d16), xq, xd, y, (int)n, (int)k, ldy);
@@ -256,8 +422,9 @@ static void gemv_launch(int type, const uint8_t *wb, const WeightPlanes &p, int6
             hipLaunchKernelGGL(k_gemv_f16<MM>, grid, block, 0, s, (const uint16_t *)wb, (const uint16_t *)xq, y, (int)n,
                                (int)k, ldy);
             break;
-        default: break;
+        default: return hipErrorInvalidValue;
     }
+    return hipSuccess;
 }
 
 hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
@@ -268,17 +435,19 @@ hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const 
     const ActPlanes ap = act_planes(type, m, k, false);
     const uint8_t *wb = (const uint8_t *)image;
     const uint8_t *xb = (const uint8_t *)ws;
+    hipError_t e = hipErrorInvalidValue;
     switch (m) {
-        case 1: gemv_launch<1>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 2: gemv_launch<2>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 3: gemv_launch<3>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 4: gemv_launch<4>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 5: gemv_launch<5>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 6: gemv_launch<6>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 7: gemv_launch<7>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 8: gemv_launch<8>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        default: return hipErrorInvalidValue;
+        case 1: e = gemv_launch<1>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
+        case 2: e = gemv_launch<2>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
+        case 3: e = gemv_launch<3>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
+        case 4: e = gemv_launch<4>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
+        case 5: e = gemv_launch<5>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
+        case 6: e = gemv_launch<6>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
+        case 7: e = gemv_launch<7>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
+        case 8: e = gemv_launch<8>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
+        default: break;
     }
+    if (e != hipSuccess) return e;
     return hipGetLastError();
 }
 

@@ -58,6 +58,10 @@ __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size
 // with one 16-byte-per-lane load, global -> LDS -> registers, all contiguous.
 // ---------------------------------------------------------------------------
 constexpr int TILE_ROWS = 256;
+// Q4_K GEMV plane: one tile = 16 weight rows x one 256-value superblock
+constexpr int GV_ROWS = 16;
+constexpr int GV4_QS = 0, GV4_SC = 2048, GV4_MN = 2176, GV4_DD = 2304, GV4_BYTES = 2432;
+constexpr int GV6_LO = 0, GV6_HI = 2048, GV6_SC = 3072, GV6_SC2 = 3328, GV6_D = 3584, GV6_BYTES = 3648;
 constexpr int KSTAGE = 128;
 
 __host__ __device__ inline int64_t pad_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
@@ -71,8 +75,19 @@ __host__ __device__ inline int64_t tiled_off(int64_t r, int64_t kb, int64_t kb_p
 // Weight image: GGUF bytes, then planes (each 256-byte aligned).
 //  GEMV planes (row-major, byte-identical to the GGUF fields):
 //   Q8_0: qs  i8 [n][k]            d16  u16 [n][k/32]
-//   Q6_K: ql  u8 [n][k/2]  qh u8 [n][k/4]  sc i8 [n][k/16]  d16 u16 [n][k/256]
-//   (Q4_K and F16 GEMVs read the GGUF rows directly)
+//   Q6_K: gv  [ceil(n/16)][k/256] tiles of GV6_BYTES, the operands of the MFMA GEMV, with
+//         q = the unsigned 6-bit quant (q6 - 32 is the value) of value 32kk+8p+b (b < 8) of
+//         row r (K-step kk, lane group p):
+//           lo [p][r][kk] u32: byte j = (q_j & 15) | (q_{j+4} & 15) << 4
+//           hi [p][r][kk/2] u32: byte j holds (q >> 4) of q_j, q_{j+4} of step 2*(kk/2)
+//              (bits 0-1, 2-3) and of step 2*(kk/2)+1 (bits 4-5, 6-7)
+//           sc [g][r/4][kk][r%4] i8 = scale of 16-group 2kk+g;  sc2 [p][r][t] i8 = scale of
+//           16-group 4p+t;  d [r] f32; rows past n are zero
+//   Q4_K: gv  [ceil(n/16)][k/256] tiles of GV4_BYTES (16 rows x one superblock), the
+//         operands of the MFMA GEMV: qs [chunk c][half h][row r][16 B] (GGUF qs bytes
+//         32c+16h..+16 of row r), sc [g][r/4][c][r%4] (u8 sc_{2c+g}), mn [half][r][4]
+//         (u8 m_{4*half+t}), dd [r][2] f32 (d, dmin); rows past n are zero
+//   (F16 GEMVs read the GGUF rows directly)
 //  GEMM planes (tiled, n padded to n_pad = pad(n, 256)):
 //   Q8_0: tq  i8 tiled [n_pad][kb_pad]     tdw f32 [kb_pad/32][n_pad]
 //   Q4_K: tq (lo limb), thi (hi limb) i8 tiled [n_pad][k]: sc_j*q4 = lo + 128*hi,
@@ -85,7 +100,7 @@ __host__ __device__ inline int64_t tiled_off(int64_t r, int64_t kb, int64_t kb_p
 // ---------------------------------------------------------------------------
 struct WeightPlanes {
     size_t gguf = 0;
-    size_t qs = 0, d16 = 0, ql = 0, qh = 0, sc = 0;        // GEMV planes
+    size_t qs = 0, d16 = 0, gv = 0;                        // GEMV planes
     size_t tq = 0, thi = 0, tdw = 0, tdmin = 0, tmin = 0;  // GEMM planes
     int64_t n_pad = 0, kb_pad = 0;
     size_t total = 0;
@@ -147,6 +162,7 @@ inline WeightPlanes weight_planes(int type, int64_t n, int64_t k) {
             p.tdw = take((size_t)(p.kb_pad / QK8_0) * p.n_pad * 4);
             break;
         case MQ_TYPE_Q4_K:
+            p.gv = take((size_t)((n + GV_ROWS - 1) / GV_ROWS) * nsb * GV4_BYTES);
             p.tq = take(tiled);
             p.thi = take(tiled);
             p.tdw = take(nsb * p.n_pad * 4);
@@ -154,10 +170,7 @@ inline WeightPlanes weight_planes(int type, int64_t n, int64_t k) {
             p.tmin = take((size_t)(p.n_pad / 32) * nsb * 1024);
             break;
         case MQ_TYPE_Q6_K:
-            p.ql = take(nk / 2);
-            p.qh = take(nk / 4);
-            p.sc = take(nk / 16);
-            p.d16 = take(nk / QK_K * 2);
+            p.gv = take((size_t)((n + GV_ROWS - 1) / GV_ROWS) * nsb * GV6_BYTES);
             p.tq = take(tiled);
             p.thi = take(tiled);
             p.tdw = take(nsb * p.n_pad * 4);
@@ -174,6 +187,9 @@ inline WeightPlanes weight_planes(int type, int64_t n, int64_t k) {
 //  Row-major layout (GEMV path, m <= 8):
 //   Q8_0: xq i8 [m][k]   xd f32 [m][k/32]      (xd holds the fp16 d widened exactly)
 //   Q8_K: xq i8 [m][k]   xd f32 [m][k/256]   xbs i16 [m][k/16]  (ggml's bsums)
+//         xgm f16 [k/256][8][16]: for row m < 8, entry e: B_{e%8} & 63 (e < 8) or
+//         64*(B_{e%8} >> 6) (e >= 8), B_j = sum of the 32 quants of sub-block j:
+//         the B operand of the Q4_K GEMV min-term MFMA
 //   F16 : xq f16 [m][k]
 //  Tiled layout (GEMM path, m padded to m_pad = pad(m, 256), pad rows zero):
 //   Q8_0: xq i8 tiled [m_pad][kb_pad]   xd f32 [kb_pad/32][m_pad]
@@ -185,7 +201,7 @@ inline WeightPlanes weight_planes(int type, int64_t n, int64_t k) {
 //   F16 : xq f16 tiled [m_pad][kb_pad bytes]
 // ---------------------------------------------------------------------------
 struct ActPlanes {
-    size_t xq = 0, xd = 0, xbs = 0, xmin = 0, total = 0;
+    size_t xq = 0, xd = 0, xbs = 0, xmin = 0, xgm = 0, total = 0;
     int64_t m_pad = 0, kb_pad = 0;
     bool tiled = false;
 };
@@ -213,6 +229,7 @@ inline ActPlanes act_planes(int wtype, int64_t m, int64_t k, bool tiled) {
                 a.xq = take(mk);
                 a.xd = take(mk / QK_K * 4);
                 a.xbs = take(mk / 16 * 2);
+                a.xgm = take((size_t)(k / QK_K) * 8 * 16 * 2);
                 break;
             case MQ_TYPE_F16: a.xq = take(mk * 2); break;
             default: break;

@@ -147,6 +147,14 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const float *__restrict__
         *(uint32_t *)(out + row * k + b * QK_K + lane * 4) = packed;
         if ((lane & 3) == 0) xbs[row * (k / 16) + b * 16 + (lane >> 2)] = (int16_t)s16;
         if (lane == 0) xd[row * nbr + b] = dval;
+        // GEMV min-term operand (rows < 8): B_j = sum of the 32 quants of sub-block j, in lane 8j
+        const int B = s16 + __shfl_xor(s16, 4);
+        if (xmin != nullptr && row < 8 && (lane & 7) == 0) {
+            const int j = lane >> 3;
+            _Float16 *g = xmin + ((b * 8 + row) << 4);
+            g[j] = (_Float16)(B & 63);
+            g[j + 8] = (_Float16)((B >> 6) * 64);
+        }
     } else {
         uint8_t *blkp = (uint8_t *)out + (row * nbr + b) * sizeof(block_q8_K);
         *(uint32_t *)(blkp + 4 + lane * 4) = packed;
@@ -500,20 +508,50 @@ __global__ __launch_bounds__(256) void k_prepare_q4_K_tiled(const uint8_t *__res
     }
 }
 
-__global__ __launch_bounds__(256) void k_prepare_q6_K_rows(const uint8_t *__restrict__ gguf, uint8_t *__restrict__ ql,
-                                                           uint8_t *__restrict__ qh, int8_t *__restrict__ scp,
-                                                           uint16_t *__restrict__ d16, int64_t row0, int64_t row1,
-                                                           int64_t k) {
-    const int64_t nbr = k / QK_K;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (row1 - row0) * nbr) return;
-    const int64_t row = row0 + gid / nbr, b = gid % nbr;
-    const uint8_t *src = gguf + (row * nbr + b) * sizeof(block_q6_K);
-    const int64_t sbi = row * nbr + b;
-    d16[sbi] = *(const uint16_t *)(src + 208);
-    for (int i = 0; i < 128; i++) ql[sbi * 128 + i] = src[i];
-    for (int i = 0; i < 64; i++) qh[sbi * 64 + i] = src[128 + i];
-    for (int i = 0; i < 16; i++) scp[sbi * 16 + i] = (int8_t)src[192 + i];
+// Q6_K GEMV plane (layout in mq_internal.h): one thread per (row, superblock).
+__device__ __forceinline__ int q6_value(const uint8_t *blk, int e) {  // unsigned 6-bit quant of value e
+    const int h = e >> 7, lp = e & 127, s = lp >> 5, l = lp & 31;
+    const int qlb = blk[64 * h + (s & 1) * 32 + l];
+    const int lo = (s >> 1) ? (qlb >> 4) : (qlb & 15);
+    return lo | (((blk[128 + 32 * h + l] >> (2 * s)) & 3) << 4);
+}
+
+__global__ __launch_bounds__(256) void k_prepare_q6_K_gv(const uint8_t *__restrict__ gguf, uint8_t *__restrict__ gv,
+                                                         int64_t n, int64_t row0, int64_t row1, int64_t k) {
+    const int64_t nsb = k / QK_K;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t row = row0 + t / nsb, sb = t % nsb;
+    if (row >= row1) return;
+    const int r = (int)(row % GV_ROWS);
+    uint8_t *T = gv + ((row / GV_ROWS) * nsb + sb) * GV6_BYTES;
+    const bool live = row < n;
+    const uint8_t *blk = gguf + (row * nsb + sb) * sizeof(block_q6_K);  // 2-byte aligned: byte reads
+    for (int p = 0; p < 4; p++) {
+        uint32_t his[4] = {0, 0, 0, 0};
+        for (int kk = 0; kk < 8; kk++) {
+            uint32_t lo = 0;
+            for (int j = 0; j < 4; j++) {
+                const int e = 32 * kk + 8 * p + j;
+                const uint32_t qa = live ? (uint32_t)q6_value(blk, e) : 0u;
+                const uint32_t qb = live ? (uint32_t)q6_value(blk, e + 4) : 0u;
+                lo |= ((qa & 15) | ((qb & 15) << 4)) << (8 * j);
+                const int sh = 8 * j + 4 * (kk & 1);
+                his[kk >> 1] |= ((qa >> 4) << sh) | ((qb >> 4) << (sh + 2));
+            }
+            ((uint32_t *)(T + GV6_LO))[(p * GV_ROWS + r) * 8 + kk] = lo;
+        }
+        for (int hp = 0; hp < 4; hp++) ((uint32_t *)(T + GV6_HI))[(p * GV_ROWS + r) * 4 + hp] = his[hp];
+    }
+    const int8_t *scl = (const int8_t *)(blk + 192);
+    for (int grp = 0; grp < 16; grp++) {
+        const int8_t sc = live ? scl[grp] : (int8_t)0;
+        const int kk = grp >> 1, g = grp & 1;
+        ((int8_t *)(T + GV6_SC))[((g * 4 + r / 4) * 8 + kk) * 4 + (r & 3)] = sc;
+        ((int8_t *)(T + GV6_SC2))[((grp >> 2) * GV_ROWS + r) * 4 + (grp & 3)] = sc;
+    }
+    float d = 0.f;
+    if (live) d = (float)__builtin_bit_cast(_Float16, (uint16_t)(blk[208] | (blk[209] << 8)));
+    ((float *)(T + GV6_D))[r] = d;
 }
 
 // Q6_K: limbs of sc * (q6 - 32) (lo = v & 127, hi = v >> 7 arithmetic), per-superblock d.
@@ -660,7 +698,8 @@ hipError_t launch_quantize_act_planar(int wtype, const float *x, int64_t ldx, vo
         case MQ_TYPE_Q6_K:
             if (tiled)
                 return tiled_dispatch<TQ_Q8_K>(x, ldx, xq, xd, (_Float16 *)(base + a.xmin), m, k, 0, a.m_pad, a.kb_pad, s);
-            return q8_K_dispatch<OUT_ROWS>(x, ldx, xq, xd, (int16_t *)(base + a.xbs), nullptr, m, k, m, s);
+            return q8_K_dispatch<OUT_ROWS>(x, ldx, xq, xd, (int16_t *)(base + a.xbs), (_Float16 *)(base + a.xgm), m, k,
+                                           m, s);
         case MQ_TYPE_F16:
             if (tiled) return tiled_dispatch<TQ_F16>(x, ldx, xq, nullptr, nullptr, m, k, 0, a.m_pad, a.kb_pad, s);
             return launch_quantize_f16(x, ldx, base + a.xq, m, k, s);
@@ -696,6 +735,44 @@ hipError_t launch_dequantize(int type, const void *w, float *y, int64_t nrows, i
     return hipGetLastError();
 }
 
+// Q4_K GEMV plane (layout in mq_internal.h): one thread per (row, superblock).
+__global__ __launch_bounds__(256) void k_prepare_q4_K_gv(const uint8_t *__restrict__ gguf, uint8_t *__restrict__ gv,
+                                                         int64_t n, int64_t row0, int64_t row1, int64_t k) {
+    const int64_t nsb = k / QK_K;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t row = row0 + t / nsb, sb = t % nsb;
+    if (row >= row1) return;
+    const int r = (int)(row % GV_ROWS);
+    uint8_t *T = gv + ((row / GV_ROWS) * nsb + sb) * GV4_BYTES;
+    const bool live = row < n;
+    const uint8_t *blk = gguf + (row * nsb + sb) * sizeof(block_q4_K);
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            int4 v = make_int4(0, 0, 0, 0);
+            if (live) {
+                const uint8_t *src = blk + 16 + 32 * c + 16 * h;  // qs bytes 32c+16h..+16 (16-byte aligned)
+                v = *(const int4 *)src;
+            }
+            *(int4 *)(T + GV4_QS + ((c * 2 + h) * GV_ROWS + r) * 16) = v;
+        }
+    float d = 0.f, dmin = 0.f;
+    if (live) {
+        d = (float)__builtin_bit_cast(_Float16, *(const uint16_t *)blk);
+        dmin = (float)__builtin_bit_cast(_Float16, *(const uint16_t *)(blk + 2));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        int sc = 0, mn = 0;
+        if (live) scale_min_k4(j, blk + 4, sc, mn);
+        T[GV4_SC + (((j & 1) * 4 + r / 4) * 4 + (j >> 1)) * 4 + (r & 3)] = (uint8_t)sc;
+        T[GV4_MN + ((j >> 2) * GV_ROWS + r) * 4 + (j & 3)] = (uint8_t)mn;
+    }
+    ((float *)(T + GV4_DD))[2 * r] = d;
+    ((float *)(T + GV4_DD))[2 * r + 1] = dmin;
+}
+
 hipError_t launch_weight_prepare(int type, void *image, int64_t n, int64_t k, int64_t row0, int64_t row1,
                                  hipStream_t s) {
     const WeightPlanes p = weight_planes(type, n, k);
@@ -716,15 +793,21 @@ hipError_t launch_weight_prepare(int type, void *image, int64_t n, int64_t k, in
                                base, (int8_t *)(base + p.tq), (float *)(base + p.tdw), n, row0, row_end, k, p.n_pad,
                                p.kb_pad);
             break;
-        case MQ_TYPE_Q4_K:
+        case MQ_TYPE_Q4_K: {
+            const int64_t gv_end = (row1 >= n) ? pad_up(n, GV_ROWS) : row1;  // zero the last tile's padding rows
+            hipLaunchKernelGGL(k_prepare_q4_K_gv, dim3(grid_for((gv_end - row0) * nbr)), b, 0, s, base, base + p.gv, n,
+                               row0, gv_end, k);
+        }
             hipLaunchKernelGGL(k_prepare_q4_K_tiled, dim3(grid_for((row_end - row0) * nbr)), b, 0, s, base,
                                (int8_t *)(base + p.tq), (int8_t *)(base + p.thi), (float *)(base + p.tdw),
                                (float *)(base + p.tdmin), (_Float16 *)(base + p.tmin), n, row0, row_end, k, p.n_pad);
             break;
         case MQ_TYPE_Q6_K:
-            hipLaunchKernelGGL(k_prepare_q6_K_rows, dim3(grid_for((row1 - row0) * nbr)), b, 0, s, base,
-                               base + p.ql, base + p.qh, (int8_t *)(base + p.sc), (uint16_t *)(base + p.d16), row0,
-                               row1, k);
+        {
+            const int64_t gv_end = (row1 >= n) ? pad_up(n, GV_ROWS) : row1;  // zero the last tile's padding rows
+            hipLaunchKernelGGL(k_prepare_q6_K_gv, dim3(grid_for((gv_end - row0) * nbr)), b, 0, s, base, base + p.gv, n,
+                               row0, gv_end, k);
+        }
             hipLaunchKernelGGL(k_prepare_q6_K_tiled, dim3(grid_for((row_end - row0) * nbr)), b, 0, s, base,
                                (int8_t *)(base + p.tq), (int8_t *)(base + p.thi), (float *)(base + p.tdw), n, row0,
                                row_end, k, p.n_pad);
