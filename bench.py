@@ -148,6 +148,134 @@ def bench_q4k_ffn(args, torch, L, mq, synth):
     return res
 
 
+def _upload_image(torch, L, mq, wtype, gguf, n, k):
+    """Weight image in device memory (256-byte aligned) with its planes built."""
+    size = L.mq_weight_image_bytes(wtype, n, k)
+    buf = torch.zeros(size + 256, dtype=torch.uint8, device="cuda")
+    wp = buf.data_ptr() + ((-buf.data_ptr()) % 256)
+    off = wp - buf.data_ptr()
+    buf[off:off + gguf.size] = torch.from_numpy(gguf.ravel()).cuda()
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    mq.check(L.mq_weight_prepare(wtype, ctypes.c_void_p(wp), n, k, 0, n, s))
+    return buf, wp
+
+
+def _timed(torch, fn, reps):
+    stream = torch.cuda.current_stream()
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e3  # us
+
+
+def bench_q8_0_minilm(torch, L, mq, synth):
+    """Q8_0 mul_mat at the MiniLM-L6 FFN-up shape: W[1536 x 384] x X[4096 x 384] (32 seq x 128)."""
+    N, K, M = 1536, 384, 4096
+    q = quantize_weights(L, mq.TYPE_Q8_0, synth.normal("minilm_ffn/W_up", (N, K), std=0.02))
+    d = Dev(torch, L, mq, mq.TYPE_Q8_0, q, N, K, synth.normal("minilm_ffn/X", (M, K)), "minilm")
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def quant():
+        mq.check(L.mq_quantize_act(d.wtype, ctypes.c_void_p(d.x.data_ptr()), K, M, K, ctypes.c_void_p(d.wsp), d.wsb,
+                                   mq.PATH_GEMM, s))
+
+    def gemm():
+        mq.check(L.mq_mul_mat_q(d.wtype, ctypes.c_void_p(d.wp), N, K, ctypes.c_void_p(d.wsp), M,
+                                ctypes.c_void_p(d.y.data_ptr()), N, mq.PATH_GEMM, s))
+
+    quant()
+    t_gemm = _timed(torch, gemm, 200)
+    t_all = _timed(torch, lambda: (quant(), gemm()), 200)
+    ops = 2.0 * M * N * K
+    gemm_bytes = q.size + M * K + M * (K // 32) * 4 + M * N * 4  # W + X quants + X scales + Y
+    return {
+        "workload": "Q8_0 mul_mat, MiniLM-L6 FFN-up shape W[1536x384] x X[4096x384]",
+        "mul_mat_us": round(t_all, 2), "gemm_us": round(t_gemm, 2),
+        "tops": round(ops / (t_all * 1e-6) / 1e12, 1),
+        "gemm_tops": round(ops / (t_gemm * 1e-6) / 1e12, 1),
+        "gemm_hbm_gbs": round(gemm_bytes / (t_gemm * 1e-6) / 1e9, 1),
+        "gemm_hbm_frac": round(gemm_bytes / (t_gemm * 1e-6) / 1e9 / PEAK_HBM_GBS, 3),
+        "gemm_bytes": gemm_bytes,
+    }
+
+
+def bench_decode(torch, L, mq, synth):
+    """M <= 8 GEMV at Qwen3-VL-2B text-decoder shapes: the Q6_K lm_head [151936 x 2048]
+    and a sweep over 28 layers x 7 Q4_K matrices (792.7 MB of weights, beyond the 256 MB
+    last-level cache), activation quantization included (shared by q/k/v and gate/up)."""
+    import numpy as np
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = {}
+    # ---- lm_head: 4096 quantized rows tiled to 151936 (bandwidth does not depend on values) ----
+    NV, H = 151936, 2048
+    blk = quantize_weights(L, mq.TYPE_Q6_K, synth.normal("qwen3vl/lm_head_rows", (4096, H), std=0.02))
+    rs = L.mq_row_size(mq.TYPE_Q6_K, H)
+    g = np.tile(blk.reshape(4096, rs), (NV // 4096 + 1, 1))[:NV].copy()
+    heads = [_upload_image(torch, L, mq, mq.TYPE_Q6_K, g, NV, H) for _ in range(2)]  # alternate: > cache
+    del g
+    for m in (1, 8):
+        x = torch.from_numpy(synth.normal(f"qwen3vl/x_head_m{m}", (m, H))).cuda()
+        y = torch.empty((m, NV), dtype=torch.float32, device="cuda")
+        wsb = L.mq_workspace_bytes(mq.TYPE_Q6_K, m, H)
+        ws = torch.empty(wsb + 256, dtype=torch.uint8, device="cuda")
+        wsp = ws.data_ptr() + ((-ws.data_ptr()) % 256)
+        mq.check(L.mq_quantize_act(mq.TYPE_Q6_K, ctypes.c_void_p(x.data_ptr()), H, m, H, ctypes.c_void_p(wsp), wsb,
+                                   mq.PATH_GEMV, s))
+        it = [0]
+
+        def head():
+            wp = heads[it[0] & 1][1]
+            it[0] += 1
+            mq.check(L.mq_mul_mat_q(mq.TYPE_Q6_K, ctypes.c_void_p(wp), NV, H, ctypes.c_void_p(wsp), m,
+                                    ctypes.c_void_p(y.data_ptr()), NV, mq.PATH_GEMV, s))
+        us = _timed(torch, head, 40)
+        nbytes = blk.size // 4096 * NV + m * H + m * NV * 4
+        out[f"lm_head_q6_K_m{m}"] = {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                     "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 3)}
+    del heads
+    # ---- layer sweep ----
+    H, F, KV = 2048, 6144, 1024
+    mats = [("q", H, H), ("k", KV, H), ("v", KV, H), ("o", H, H), ("gate", F, H), ("up", F, H), ("down", H, F)]
+    gguf = {nm: quantize_weights(L, mq.TYPE_Q4_K, synth.normal(f"qwen3vl/layer/{nm}", (n, k), std=0.02))
+            for nm, n, k in mats}
+    layers = [{nm: _upload_image(torch, L, mq, mq.TYPE_Q4_K, gguf[nm], n, k) for nm, n, k in mats} for _ in range(28)]
+    wbytes = sum(gguf[nm].size for nm, _, _ in mats) * 28
+    for m in (1, 8):
+        xs = {kd: torch.from_numpy(synth.normal(f"qwen3vl/x_{kd}_m{m}", (m, kd))).cuda() for kd in (H, F)}
+        ys = {nm: torch.empty((m, n), dtype=torch.float32, device="cuda") for nm, n, _ in mats}
+        wss = {}
+        for kd in (H, F):
+            wsb = L.mq_workspace_bytes(mq.TYPE_Q4_K, m, kd)
+            t = torch.empty(wsb + 256, dtype=torch.uint8, device="cuda")
+            wss[kd] = (t, t.data_ptr() + ((-t.data_ptr()) % 256), wsb)
+
+        def quant(kd):
+            _, p, b = wss[kd]
+            mq.check(L.mq_quantize_act(mq.TYPE_Q4_K, ctypes.c_void_p(xs[kd].data_ptr()), kd, m, kd, ctypes.c_void_p(p),
+                                       b, mq.PATH_GEMV, s))
+
+        def sweep():
+            for lay in layers:
+                for nm, n, k in mats:
+                    if nm in ("q", "o", "gate", "down"):
+                        quant(k)  # q/k/v and gate/up share their input
+                    mq.check(L.mq_mul_mat_q(mq.TYPE_Q4_K, ctypes.c_void_p(lay[nm][1]), n, k,
+                                            ctypes.c_void_p(wss[k][1]), m, ctypes.c_void_p(ys[nm].data_ptr()), n,
+                                            mq.PATH_GEMV, s))
+        us = _timed(torch, sweep, 5)
+        out[f"layer_sweep_q4_K_m{m}"] = {"sweep_us": round(us, 1), "layer_us": round(us / 28, 2),
+                                         "weight_gbs": round(wbytes / (us * 1e-6) / 1e9, 1),
+                                         "kernels_per_layer": 11}
+    out["workload"] = ("GEMV m in {1,8}: Qwen3-VL-2B lm_head Q6_K [151936x2048]; 28-layer sweep of Q4_K "
+                       "q,k,v,o [2048|1024 x 2048], gate,up [6144x2048], down [2048x6144] (792.7 MB)")
+    return out
+
+
 def cpu_baseline_q4k(args, x_up, x_dn, q_up, q_dn):
     """Oracle (restated ggml-cpu mul_mat in C) on a bounded row sample."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -182,6 +310,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extras", action="store_true", help="skip the Q8_0 and GEMV side measurements")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--gemm-cfg", default=None, help="MQ_GEMM_CFG tile configuration (1 or 3)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -209,6 +338,10 @@ def main():
 
     r = bench_q4k_ffn(args, torch, L, mq, synth)
     x_up, x_dn, q_up, q_dn = r.pop("x")
+    extras = None
+    if not args.no_extras:
+        extras = {"q8_0_minilm_ffn_up": bench_q8_0_minilm(torch, L, mq, synth),
+                  "decode_gemv": bench_decode(torch, L, mq, synth)}
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_q4k(args, x_up, x_dn, q_up, q_dn)
@@ -235,6 +368,7 @@ def main():
         },
         "roofline": r["roofline"],
         "cpu_baseline": cpu,
+        "extras": extras,
     }
     print(json.dumps(out), flush=True)
 

@@ -264,7 +264,8 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
     // Stages past the end are issued too, re-reading the last stage into the
     // slot of a stage that is never computed, so the DMA count per stage stays
     // uniform through the tail.
-    auto issue = [&](int s) {
+    // always_inline: a call would move the accumulators to scratch memory
+    auto issue = [&](int s) __attribute__((always_inline)) {
         int8_t *st = smem + (s % NBUF) * C::STAGE;
         const int64_t sc = s < nst ? s : nst - 1;
         if constexpr (C::limbs) {
@@ -298,7 +299,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
     const int wfrag0 = C::X_BYTES + wn * TN * KC * 1024 + lane * 16;
 
     // MFMAs of one stage
-    auto compute = [&](const int8_t *st) {
+    auto compute = [&](const int8_t *st) __attribute__((always_inline)) {
 #pragma unroll
         for (int kc = 0; kc < KC; kc++) {
             v4i xa[TM];
@@ -367,7 +368,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
     // Superblock epilogue (K-quants): scale the exact integer sums and fold them
     // into the fp32 accumulators.  Per row tile, the limbs are combined first and
     // the min-term MFMAs issued, so their latency overlaps the scale reads.
-    auto epilogue = [&](int sb) {
+    auto epilogue = [&](int sb) __attribute__((always_inline)) {
         const uint32_t ep = lds_addr(smem + NBUF * C::STAGE + (sb & 1) * C::EP);
         const uint32_t edx = ep, edw = ep + C::EP_DX, edm = ep + C::EP_DX + C::EP_DW;
         const uint32_t eam = ep + C::EP_DX + C::EP_DW + C::EP_DMIN, ebm = eam + C::EP_AMIN;
@@ -428,7 +429,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
     constexpr int UNR = C::limbs ? SPB : NBUF;
     static_assert(UNR == NBUF, "slot of each unrolled stage is its position");
     for (int s0 = 0; s0 < nst; s0 += UNR) {
-        static_for<0, UNR>([&](auto qc) {
+        static_for<0, UNR>([&](auto qc) __attribute__((always_inline)) {
             constexpr int q = decltype(qc)::value;
             const int s = s0 + q;
             if (C::limbs || s < nst) {  // nst is a multiple of 2 (Q8_0 / F16), of SPB (K-quants)
