@@ -276,6 +276,29 @@ def bench_decode(torch, L, mq, synth):
     return out
 
 
+def bench_minilm_e2e(torch, L, mq):
+    """End-to-end MiniLM-L6-shaped encoder (6 layers, H 384, 12 heads, FFN 1536, vocab 30522,
+    Q8_0 linears, random init), 32 sequences x 128 tokens, full attention mask, mean pool + L2:
+    embeddings per second with every mul_mat on the quantized GPU path."""
+    from crispembed_amd import bert, synth
+    hp = dict(bert.MINILM_L6)
+    B, T = 32, 128
+    W = bert.synthetic_weights(hp, mq.TYPE_Q8_0, name="minilm")
+    enc = bert.BertEncoder(hp, mq.TYPE_Q8_0, W)
+    ids = torch.from_numpy(synth.integers(f"minilm/ids_{B}x{T}", (B * T,), 1000, 30521)).cuda()
+    out = torch.empty((B, hp["n_embd"]), dtype=torch.float32, device="cuda")
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    run = lambda: enc.encode(ids.data_ptr(), B, T, out.data_ptr(), s)  # noqa: E731
+    for _ in range(3):
+        run()
+    us = _timed(torch, run, 20)
+    H, F, nl, M = hp["n_embd"], hp["n_ff"], hp["n_layer"], B * T
+    lin_ops = 2.0 * M * nl * (4 * H * H + 2 * H * F)
+    return {"workload": "MiniLM-L6 shape, Q8_0 linears, 32 seq x 128 tokens, mean pool + L2",
+            "batch_ms": round(us / 1e3, 3), "embeddings_per_s": round(B / (us * 1e-6), 1),
+            "linear_tops": round(lin_ops / (us * 1e-6) / 1e12, 1)}
+
+
 def cpu_baseline_q4k(args, x_up, x_dn, q_up, q_dn):
     """Oracle (restated ggml-cpu mul_mat in C) on a bounded row sample."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -341,6 +364,7 @@ def main():
     extras = None
     if not args.no_extras:
         extras = {"q8_0_minilm_ffn_up": bench_q8_0_minilm(torch, L, mq, synth),
+                  "minilm_l6_e2e": bench_minilm_e2e(torch, L, mq),
                   "decode_gemv": bench_decode(torch, L, mq, synth)}
     cpu = None
     if not args.no_cpu:

@@ -34,6 +34,8 @@ MQ_SOURCES = [
     ("mq_gemv.hip", []),
     ("mq_api.cpp", ["-x", "hip"]),
     ("mq_host_quant.cpp", ["-x", "hip", "-ffp-contract=off"]),
+    ("mq_encoder.hip", []),
+    ("mq_bert.cpp", ["-x", "hip"]),
 ]
 # The backend compiles against ggml's backend headers.  Standalone builds use the
 # compat transcription in csrc/ggml_compat (and libggml-compat.so for the ggml

@@ -19,6 +19,7 @@ namespace mq {
 namespace host {
 size_t quantize_chunk(int type, const float *src, void *dst, int64_t nrows, int64_t k);
 }
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 }  // namespace mq
 
 using namespace mq;
@@ -37,6 +38,21 @@ int fail(int code, const char *fmt, ...) {
     g_err = buf;
     return code;
 }
+
+}  // namespace
+
+// error reporting shared with the other host files of the library (mq_bert.cpp)
+int mq::set_error(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+namespace {
 
 int hip_fail(hipError_t e, const char *what) {
     return fail(MQ_EHIP, "%s: %s", what, hipGetErrorString(e));

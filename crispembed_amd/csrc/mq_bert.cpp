@@ -1,0 +1,212 @@
+// mq_bert.cpp -- native BERT-encoder runner on the quantized MUL_MAT path (mq_bert.h).
+//
+// Per layer (post-LN BERT, src/crispembed.cpp:1159-1436):
+//   qkv  = X . [Wq; Wk; Wv]^T        one mul_mat: the three weights' GGUF rows are
+//                                    concatenated into one [3H x H] image (rows are
+//                                    independent dot products, so this is exact)
+//   A    = attention(qkv + b_qkv)    fp32, scale 1/sqrt(head_dim), full mask
+//   X    = LN1(X + A . Wo^T + bo)
+//   Hh   = gelu_erf(X . W1^T + b1)
+//   X    = LN2(X + Hh . W2^T + b2)
+// then mean pooling and L2 normalisation.  Device memory comes from hipMalloc; the
+// activation buffers grow to the largest B*T seen.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "../../include/mq.h"
+#include "../../include/mq_bert.h"
+#include "mq_internal.h"
+
+namespace mq {
+hipError_t launch_embed_ln(const int32_t *ids, const int32_t *types, const float *word, const float *pos,
+                           const float *type, const float *lw, const float *lb, float eps, float *out, int64_t rows,
+                           int T, int H, hipStream_t s);
+hipError_t launch_bias_res_ln(const float *y, const float *bias, const float *res, const float *lw, const float *lb,
+                              float eps, float *out, int64_t rows, int H, hipStream_t s);
+hipError_t launch_bias_gelu(float *x, const float *bias, int64_t rows, int F, hipStream_t s);
+hipError_t launch_attention(const float *qkv, const float *bqkv, float *out, int B, int T, int H, int nh,
+                            hipStream_t s);
+hipError_t launch_mean_pool_l2(const float *x, float *out, int B, int T, int H, hipStream_t s);
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));  // mq_api.cpp
+}  // namespace mq
+
+using namespace mq;
+
+namespace {
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    bool ensure(size_t n) {
+        if (n <= bytes) return true;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+        if (hipMalloc(&p, n) != hipSuccess) return false;
+        bytes = n;
+        return true;
+    }
+    float *f() const { return (float *)p; }
+};
+
+struct Linear {
+    DevBuf img;
+    int64_t n = 0, k = 0;
+};
+
+struct Layer {
+    Linear qkv, o, fc1, fc2;
+    DevBuf bqkv, bo, b1, b2, ln1w, ln1b, ln2w, ln2b;
+};
+
+}  // namespace
+
+struct mq_bert {
+    mq_bert_hparams hp{};
+    DevBuf tok, pos, type, lnw, lnb;
+    std::vector<Layer> layers;
+    DevBuf x, qkv, att, y, ff, ws;
+    int64_t rows_cap = 0;
+};
+
+static int upload(DevBuf &d, const void *src, size_t bytes) {
+    if (!d.ensure(bytes)) return set_error(MQ_ENOMEM, "hipMalloc(%zu) failed", bytes);
+    if (hipMemcpy(d.p, src, bytes, hipMemcpyHostToDevice) != hipSuccess)
+        return set_error(MQ_EHIP, "hipMemcpy of %zu bytes failed", bytes);
+    return MQ_OK;
+}
+
+// GGUF rows of one or more weights with the same k, concatenated, as a prepared image.
+static int upload_linear(Linear &L, int type, const std::vector<const void *> &parts, int64_t rows_each, int64_t k) {
+    const size_t rs = mq_row_size(type, k);
+    const int64_t n = rows_each * (int64_t)parts.size();
+    if (rs == 0) return set_error(MQ_EINVAL, "bad weight type %d / k %lld", type, (long long)k);
+    const size_t img = mq_weight_image_bytes(type, n, k);
+    if (!L.img.ensure(img)) return set_error(MQ_ENOMEM, "hipMalloc(%zu) failed", img);
+    for (size_t i = 0; i < parts.size(); i++) {
+        if (!parts[i]) return set_error(MQ_EINVAL, "NULL weight");
+        if (hipMemcpy((char *)L.img.p + i * rows_each * rs, parts[i], rows_each * rs, hipMemcpyHostToDevice) !=
+            hipSuccess)
+            return set_error(MQ_EHIP, "hipMemcpy of weights failed");
+    }
+    L.n = n;
+    L.k = k;
+    const int rc = mq_weight_prepare(type, L.img.p, n, k, 0, n, nullptr);
+    if (rc) return rc;
+    return hipDeviceSynchronize() == hipSuccess ? MQ_OK : set_error(MQ_EHIP, "weight preparation failed");
+}
+
+extern "C" mq_bert *mq_bert_create(const mq_bert_hparams *hp) {
+    if (!hp || hp->n_layer <= 0 || hp->n_embd <= 0 || hp->n_head <= 0 || hp->n_embd % hp->n_head != 0 ||
+        hp->n_ff <= 0 || hp->n_vocab <= 0 || hp->n_max_pos <= 0 || hp->n_type < 0) {
+        set_error(MQ_EINVAL, "bad BERT hyper-parameters");
+        return nullptr;
+    }
+    if (!mq_supports(hp->wtype, hp->n_embd) || !mq_supports(hp->wtype, hp->n_ff)) {
+        set_error(MQ_EUNSUPPORTED, "weight type %d does not tile k = %d / %d", hp->wtype, hp->n_embd, hp->n_ff);
+        return nullptr;
+    }
+    mq_bert *m = new mq_bert();
+    m->hp = *hp;
+    m->layers.resize(hp->n_layer);
+    return m;
+}
+
+extern "C" void mq_bert_free(mq_bert *m) { delete m; }
+
+extern "C" int mq_bert_set_embeddings(mq_bert *m, const float *tok, const float *pos, const float *type,
+                                      const float *ln_w, const float *ln_b) {
+    if (!m || !tok || !pos || !ln_w || !ln_b || (m->hp.n_type > 0 && !type))
+        return set_error(MQ_EINVAL, "NULL embedding table");
+    const size_t H = (size_t)m->hp.n_embd * sizeof(float);
+    int rc;
+    if ((rc = upload(m->tok, tok, H * m->hp.n_vocab))) return rc;
+    if ((rc = upload(m->pos, pos, H * m->hp.n_max_pos))) return rc;
+    if (m->hp.n_type > 0 && (rc = upload(m->type, type, H * m->hp.n_type))) return rc;
+    if ((rc = upload(m->lnw, ln_w, H))) return rc;
+    return upload(m->lnb, ln_b, H);
+}
+
+extern "C" int mq_bert_set_layer(mq_bert *m, int il, const void *wq, const void *wk, const void *wv, const void *wo,
+                                 const void *w1, const void *w2, const float *bq, const float *bk, const float *bv,
+                                 const float *bo, const float *b1, const float *b2, const float *ln1_w,
+                                 const float *ln1_b, const float *ln2_w, const float *ln2_b) {
+    if (!m || il < 0 || il >= m->hp.n_layer) return set_error(MQ_EINVAL, "bad layer index %d", il);
+    if (!bq || !bk || !bv || !bo || !b1 || !b2 || !ln1_w || !ln1_b || !ln2_w || !ln2_b)
+        return set_error(MQ_EINVAL, "NULL bias / LayerNorm parameter");
+    Layer &L = m->layers[il];
+    const int t = m->hp.wtype;
+    const int64_t H = m->hp.n_embd, F = m->hp.n_ff;
+    int rc;
+    if ((rc = upload_linear(L.qkv, t, {wq, wk, wv}, H, H))) return rc;
+    if ((rc = upload_linear(L.o, t, {wo}, H, H))) return rc;
+    if ((rc = upload_linear(L.fc1, t, {w1}, F, H))) return rc;
+    if ((rc = upload_linear(L.fc2, t, {w2}, H, F))) return rc;
+    std::vector<float> bqkv(3 * H);
+    std::memcpy(bqkv.data(), bq, H * sizeof(float));
+    std::memcpy(bqkv.data() + H, bk, H * sizeof(float));
+    std::memcpy(bqkv.data() + 2 * H, bv, H * sizeof(float));
+    if ((rc = upload(L.bqkv, bqkv.data(), 3 * H * sizeof(float)))) return rc;
+    if ((rc = upload(L.bo, bo, H * sizeof(float)))) return rc;
+    if ((rc = upload(L.b1, b1, F * sizeof(float)))) return rc;
+    if ((rc = upload(L.b2, b2, H * sizeof(float)))) return rc;
+    if ((rc = upload(L.ln1w, ln1_w, H * sizeof(float)))) return rc;
+    if ((rc = upload(L.ln1b, ln1_b, H * sizeof(float)))) return rc;
+    if ((rc = upload(L.ln2w, ln2_w, H * sizeof(float)))) return rc;
+    return upload(L.ln2b, ln2_b, H * sizeof(float));
+}
+
+static int hip_rc(hipError_t e, const char *what) {
+    return e == hipSuccess ? MQ_OK : set_error(MQ_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *types, int B, int T, float *out,
+                              float *hidden, void *stream) {
+    if (!m || !ids || !out || B <= 0 || T <= 0) return set_error(MQ_EINVAL, "bad encode arguments");
+    const mq_bert_hparams &hp = m->hp;
+    if (T > hp.n_max_pos) return set_error(MQ_EINVAL, "T = %d exceeds n_max_pos = %d", T, hp.n_max_pos);
+    for (const Layer &L : m->layers)
+        if (!L.qkv.img.p) return set_error(MQ_EINVAL, "layer weights not set");
+    if (!m->tok.p) return set_error(MQ_EINVAL, "embeddings not set");
+    const int64_t rows = (int64_t)B * T, H = hp.n_embd, F = hp.n_ff;
+    const int t = hp.wtype;
+    const size_t f4 = sizeof(float);
+    const size_t wsb = std::max({mq_workspace_bytes(t, rows, H), mq_workspace_bytes(t, rows, F)});
+    if (!m->x.ensure(rows * H * f4) || !m->qkv.ensure(rows * 3 * H * f4) || !m->att.ensure(rows * H * f4) ||
+        !m->y.ensure(rows * H * f4) || !m->ff.ensure(rows * F * f4) || !m->ws.ensure(wsb))
+        return set_error(MQ_ENOMEM, "activation buffers for %lld rows", (long long)rows);
+    hipStream_t s = (hipStream_t)stream;
+    const float eps = hp.layer_norm_eps;
+    float *X = hidden ? hidden : m->x.f();
+    int rc;
+    if ((rc = hip_rc(launch_embed_ln(ids, hp.n_type > 0 ? types : nullptr, m->tok.f(), m->pos.f(),
+                                     hp.n_type > 0 ? m->type.f() : nullptr, m->lnw.f(), m->lnb.f(), eps, X, rows, T,
+                                     (int)H, s),
+                     "embeddings")))
+        return rc;
+    auto mm = [&](const Linear &L, const float *in, float *y) {
+        return mq_mul_mat(t, L.img.p, L.n, L.k, in, L.k, rows, y, L.n, m->ws.p, m->ws.bytes, s);
+    };
+    for (const Layer &L : m->layers) {
+        if ((rc = mm(L.qkv, X, m->qkv.f()))) return rc;
+        if ((rc = hip_rc(launch_attention(m->qkv.f(), L.bqkv.f(), m->att.f(), B, T, (int)H, hp.n_head, s), "attention")))
+            return rc;
+        if ((rc = mm(L.o, m->att.f(), m->y.f()))) return rc;
+        if ((rc = hip_rc(launch_bias_res_ln(m->y.f(), L.bo.f(), X, L.ln1w.f(), L.ln1b.f(), eps, X, rows, (int)H, s),
+                         "attention residual")))
+            return rc;
+        if ((rc = mm(L.fc1, X, m->ff.f()))) return rc;
+        if ((rc = hip_rc(launch_bias_gelu(m->ff.f(), L.b1.f(), rows, (int)F, s), "gelu"))) return rc;
+        if ((rc = mm(L.fc2, m->ff.f(), m->y.f()))) return rc;
+        if ((rc = hip_rc(launch_bias_res_ln(m->y.f(), L.b2.f(), X, L.ln2w.f(), L.ln2b.f(), eps, X, rows, (int)H, s),
+                         "ffn residual")))
+            return rc;
+    }
+    return hip_rc(launch_mean_pool_l2(X, out, B, T, (int)H, s), "pooling");
+}

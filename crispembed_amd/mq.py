@@ -52,7 +52,20 @@ _SIGS = {
     "mq_mul_mat_q": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_vp]),
     "mq_mul_mat_ex": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                                _c_sz, _c_int, _c_vp]),
+    # include/mq_bert.h
+    "mq_bert_create": (_c_vp, [_c_vp]),
+    "mq_bert_free": (None, [_c_vp]),
+    "mq_bert_set_embeddings": (_c_int, [_c_vp] * 6),
+    "mq_bert_set_layer": (_c_int, [_c_vp, _c_int] + [_c_vp] * 16),
+    "mq_bert_encode": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp]),
 }
+
+
+class BertHparams(ctypes.Structure):
+    """mq_bert_hparams (include/mq_bert.h)."""
+    _fields_ = [("n_layer", _c_int), ("n_embd", _c_int), ("n_head", _c_int), ("n_ff", _c_int),
+                ("n_vocab", _c_int), ("n_max_pos", _c_int), ("n_type", _c_int),
+                ("layer_norm_eps", ctypes.c_float), ("wtype", _c_int)]
 
 
 def lib():
