@@ -234,9 +234,15 @@ static int resolve_path(int path, int64_t m) {
 
 int mq_quantize_act(int type, const float *x, int64_t ldx, int64_t m, int64_t k, void *workspace,
                     size_t workspace_bytes, int path, void *stream) {
+    return mq_quantize_act_ex(type, x, ldx, m, k, nullptr, MQ_PRE_NONE, workspace, workspace_bytes, path, stream);
+}
+
+int mq_quantize_act_ex(int type, const float *x, int64_t ldx, int64_t m, int64_t k, const float *bias, int op,
+                       void *workspace, size_t workspace_bytes, int path, void *stream) {
     if (!type_ok(type)) return fail(MQ_EUNSUPPORTED, "weight type %d is not Q8_0/Q4_K/Q6_K/F16", type);
     if (!mq_supports(type, k)) return fail(MQ_EUNSUPPORTED, "k=%lld not supported for type %d", (long long)k, type);
     if (!x || !workspace || m < 0 || m > INT32_MAX || ldx < k) return fail(MQ_EINVAL, "mq_quantize_act: bad arguments");
+    if (op != MQ_PRE_NONE && op != MQ_PRE_GELU_ERF) return fail(MQ_EINVAL, "mq_quantize_act: unknown prologue op %d", op);
     if (!is_aligned(workspace, 256)) return fail(MQ_EINVAL, "mq_quantize_act: workspace must be 256-byte aligned");
     if (m == 0) return MQ_OK;
     path = resolve_path(path, m);
@@ -246,7 +252,7 @@ int mq_quantize_act(int type, const float *x, int64_t ldx, int64_t m, int64_t k,
     if (workspace_bytes < need)
         return fail(MQ_EINVAL, "mq_quantize_act: workspace %zu bytes < %zu needed", workspace_bytes, need);
     const hipError_t e =
-        launch_quantize_act_planar(type, x, ldx, workspace, m, k, mq_q8_0_variant(), tiled, (hipStream_t)stream);
+        launch_quantize_act_planar(type, x, ldx, workspace, m, k, mq_q8_0_variant(), tiled, (hipStream_t)stream, op, bias);
     return e == hipSuccess ? MQ_OK : hip_fail(e, "activation quantization");
 }
 

@@ -26,7 +26,6 @@ hipError_t launch_embed_ln(const int32_t *ids, const int32_t *types, const float
                            int T, int H, hipStream_t s);
 hipError_t launch_bias_res_ln(const float *y, const float *bias, const float *res, const float *lw, const float *lb,
                               float eps, float *out, int64_t rows, int H, hipStream_t s);
-hipError_t launch_bias_gelu(float *x, const float *bias, int64_t rows, int F, hipStream_t s);
 hipError_t launch_attention(const float *qkv, const float *bqkv, float *out, int B, int T, int H, int nh,
                             hipStream_t s);
 hipError_t launch_mean_pool_l2(const float *x, float *out, int B, int T, int H, hipStream_t s);
@@ -202,8 +201,12 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
                          "attention residual")))
             return rc;
         if ((rc = mm(L.fc1, X, m->ff.f()))) return rc;
-        if ((rc = hip_rc(launch_bias_gelu(m->ff.f(), L.b1.f(), rows, (int)F, s), "gelu"))) return rc;
-        if ((rc = mm(L.fc2, m->ff.f(), m->y.f()))) return rc;
+        // FFN-up bias and GELU-erf are applied by the FFN-down activation quantizer
+        if ((rc = mq_quantize_act_ex(t, m->ff.f(), F, rows, F, L.b1.f(), MQ_PRE_GELU_ERF, m->ws.p, m->ws.bytes,
+                                     MQ_PATH_AUTO, s)))
+            return rc;
+        if ((rc = mq_mul_mat_q(t, L.fc2.img.p, L.fc2.n, L.fc2.k, m->ws.p, rows, m->y.f(), L.fc2.n, MQ_PATH_AUTO, s)))
+            return rc;
         if ((rc = hip_rc(launch_bias_res_ln(m->y.f(), L.b2.f(), X, L.ln2w.f(), L.ln2b.f(), eps, X, rows, (int)H, s),
                          "ffn residual")))
             return rc;

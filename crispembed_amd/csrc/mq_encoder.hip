@@ -104,15 +104,6 @@ __global__ __launch_bounds__(256) void k_bias_res_ln(const float *__restrict__ y
     ln_row(v, H, lane, lw, lb, eps, out + row * H);
 }
 
-// x = gelu_erf(x + bias), 0.5 x (1 + erf(x / sqrt 2))  (ggml_gelu_erf)
-__global__ __launch_bounds__(256) void k_bias_gelu(float *__restrict__ x, const float *__restrict__ bias, int64_t n,
-                                                   int F) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const float v = x[i] + (bias ? bias[i % F] : 0.f);
-    x[i] = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
-}
-
 // Attention of one (sequence, head): qkv rows [T][3H] (q | k | v, bias not yet added),
 // out rows [T][H] at this head's columns.  K and V of the head sit in LDS.  Thread t takes
 // query row t % T and the t / T-th of KS equal key ranges, walks its keys in blocks of
@@ -327,13 +318,6 @@ hipError_t launch_bias_res_ln(const float *y, const float *bias, const float *re
     return hipGetLastError();
 }
 #undef MQ_LN_DISPATCH
-
-hipError_t launch_bias_gelu(float *x, const float *bias, int64_t rows, int F, hipStream_t s) {
-    const int64_t n = rows * F;
-    if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_bias_gelu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, bias, n, F);
-    return hipGetLastError();
-}
 
 template <int HD, int KS>
 static hipError_t attention_cfg(const float *qkv, const float *bqkv, float *out, int B, int T, int H, int nh,

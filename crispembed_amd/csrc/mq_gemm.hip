@@ -483,21 +483,30 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
 // Tile configuration, selectable with MQ_GEMM_CFG for measurements:
 //   1: 8 waves x (64x64)  WG 256x128, 2 waves/SIMD
 //   3: 4 waves x (64x64)  WG 128x128, 2 WGs/CU
+//   4: 2 waves x (64x64)  WG 128x64
+//   5: 1 wave  x (64x64)  WG 64x64
 static int gemm_cfg_env() {
     const char *e = getenv("MQ_GEMM_CFG");  // read per launch so a process can compare configurations
     return (e && *e) ? atoi(e) : 0;
 }
 
+static inline int64_t tiles(int64_t M, int64_t N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
+
 template <int FMT>
 static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
     int cfg = gemm_cfg_env();
-    if (cfg != 1 && cfg != 3) {
-        // 256x128 tiles when that still gives every CU a tile, else 128x128
-        const int64_t big = (int64_t)((a.M + 255) / 256) * ((a.N + 127) / 128);
-        cfg = (big >= 256) ? 1 : 3;
+    if (cfg < 1 || cfg > 5 || cfg == 2) {
+        // the largest tile that still gives every CU (256) a workgroup
+        if (tiles(a.M, a.N, 256, 128) >= 256) cfg = 1;
+        else if (tiles(a.M, a.N, 128, 128) >= 256) cfg = 3;
+        else cfg = 4;
     }
-    if (cfg == 1) return launch_cfg<FMT, 4, 2, 2, 2, 1>(a, s);
-    return launch_cfg<FMT, 2, 2, 2, 2, 2>(a, s);
+    switch (cfg) {
+        case 1: return launch_cfg<FMT, 4, 2, 2, 2, 1>(a, s);
+        case 3: return launch_cfg<FMT, 2, 2, 2, 2, 2>(a, s);
+        case 4: return launch_cfg<FMT, 2, 1, 2, 2, 2>(a, s);
+        default: return launch_cfg<FMT, 1, 1, 2, 2, 2>(a, s);
+    }
 }
 
 hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,

@@ -32,6 +32,21 @@ __device__ __forceinline__ float4 load4(const float *p) {
     return make_float4(p[0], p[1], p[2], p[3]);
 }
 
+// Prologue applied to an activation before it is quantized (a fused ADD and GELU_ERF of the
+// graph): v = x + bias[col] (bias may be NULL), then for MQ_PRE_GELU_ERF
+// v = 0.5 v (1 + erf(v / sqrt 2)) (ggml_gelu_erf), all in fp32.  `pre` and `bias` are
+// wave-uniform: the branch costs nothing when there is no prologue.
+__device__ __forceinline__ float4 pre_apply(float4 v, int pre, const float *bias, int64_t col) {
+    if (pre == MQ_PRE_NONE && bias == nullptr) return v;
+    float r[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (bias) r[i] = r[i] + bias[col + i];
+        if (pre == MQ_PRE_GELU_ERF) r[i] = 0.5f * r[i] * (1.0f + erff(r[i] * 0.70710678118654752f));
+    }
+    return make_float4(r[0], r[1], r[2], r[3]);
+}
+
 // Output layouts of the activation quantizers.
 enum { OUT_GGUF = 0, OUT_ROWS = 1 };
 
@@ -45,7 +60,8 @@ enum { OUT_GGUF = 0, OUT_ROWS = 1 };
 template <int VARIANT, int OUT, bool VEC4>
 __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__ x, int64_t ldx,
                                                        int8_t *__restrict__ out, float *__restrict__ xd,
-                                                       int64_t m, int64_t k, int64_t m_pad, int64_t kb_pad) {
+                                                       int64_t m, int64_t k, int64_t m_pad, int64_t kb_pad, int pre,
+                                                       const float *__restrict__ bias) {
     const int64_t nbr = k / QK8_0;
     const int64_t nbx = nbr;
     const int64_t rows = m;
@@ -55,7 +71,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__
     if (blk >= rows * nbx) return;  // 8-lane groups leave together
     const int64_t row = blk / nbx, b = blk - row * nbx;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (row < m && b < nbr) v = load4<VEC4>(x + row * ldx + b * QK8_0 + sub * 4);
+    if (row < m && b < nbr) v = pre_apply(load4<VEC4>(x + row * ldx + b * QK8_0 + sub * 4), pre, bias, b * QK8_0 + sub * 4);
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
     amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
@@ -95,7 +111,8 @@ template <int OUT, bool VEC4>
 __global__ __launch_bounds__(256) void k_quantize_q8_K(const float *__restrict__ x, int64_t ldx,
                                                        int8_t *__restrict__ out, float *__restrict__ xd,
                                                        int16_t *__restrict__ xbs, _Float16 *__restrict__ xmin,
-                                                       int64_t m, int64_t k, int64_t m_pad) {
+                                                       int64_t m, int64_t k, int64_t m_pad, int pre,
+                                                       const float *__restrict__ bias) {
     const int64_t nbr = k / QK_K;
     const int64_t rows = m;
     const int lane = threadIdx.x & 63;
@@ -103,7 +120,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const float *__restrict__
     if (blk >= rows * nbr) return;  // whole waves leave together
     const int64_t row = blk / nbr, b = blk - row * nbr;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (row < m) v = load4<VEC4>(x + row * ldx + b * QK_K + lane * 4);
+    if (row < m) v = pre_apply(load4<VEC4>(x + row * ldx + b * QK_K + lane * 4), pre, bias, b * QK_K + lane * 4);
     const float vals[4] = {v.x, v.y, v.z, v.w};
     float amax = 0.0f, mx = 0.0f;
     int idx = 0x7fffffff;
@@ -166,12 +183,13 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const float *__restrict__
 // fp32 -> fp16 (round to nearest even), 4 values per lane.
 template <bool VEC4>
 __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ x, int64_t ldx,
-                                                      uint16_t *__restrict__ y, int64_t m, int64_t k) {
+                                                      uint16_t *__restrict__ y, int64_t m, int64_t k, int pre,
+                                                      const float *__restrict__ bias) {
     const int64_t q4 = k / 4;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= m * q4) return;
     const int64_t row = gid / q4, c = gid - row * q4;
-    const float4 v = load4<VEC4>(x + row * ldx + c * 4);
+    const float4 v = pre_apply(load4<VEC4>(x + row * ldx + c * 4), pre, bias, c * 4);
     uint16_t *o = y + row * k + c * 4;
     o[0] = f32_to_f16_bits(v.x);
     o[1] = f32_to_f16_bits(v.y);
@@ -235,7 +253,8 @@ template <int FMT, int VARIANT, bool VEC4>
 __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict__ x, int64_t ldx,
                                                         int8_t *__restrict__ xq, float *__restrict__ xd,
                                                         _Float16 *__restrict__ xmin, int64_t m, int64_t k,
-                                                        int64_t m_pad, int64_t kb_pad) {
+                                                        int64_t m_pad, int64_t kb_pad, int pre,
+                                                        const float *__restrict__ bias) {
     constexpr int CB = (FMT == TQ_Q8_K) ? 256 : 128;   // K bytes per workgroup
     constexpr int BPV = (FMT == TQ_F16) ? 2 : 1;       // bytes per value
     constexpr int NCH = CB / 32;                        // fragments per workgroup
@@ -259,7 +278,7 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
     for (int it = 0; it < NIT; it++) {
         const int64_t row = rt * 32 + wave * 8 + it * RPI + rsub;
         vin[it] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (row < m && kv < k) vin[it] = load4<VEC4>(x + row * ldx + kv);
+        if (row < m && kv < k) vin[it] = pre_apply(load4<VEC4>(x + row * ldx + kv), pre, bias, kv);
     }
 #pragma unroll
     for (int it = 0; it < NIT; it++) {
@@ -613,7 +632,8 @@ static inline unsigned grid_for(int64_t threads) { return (unsigned)((threads + 
 
 template <int OUT>
 static hipError_t q8_0_dispatch(const float *x, int64_t ldx, int8_t *out, float *xd, int64_t m, int64_t k, int variant,
-                                int64_t m_pad, int64_t kb_pad, hipStream_t s) {
+                                int64_t m_pad, int64_t kb_pad, hipStream_t s, int pre = MQ_PRE_NONE,
+                                const float *bias = nullptr) {
     const int64_t rows = m;
     const int64_t nbx = k / QK8_0;
     const int64_t threads = rows * nbx * 8;
@@ -621,8 +641,8 @@ static hipError_t q8_0_dispatch(const float *x, int64_t ldx, int8_t *out, float 
     const bool v4 = aligned16(x, ldx);
     const dim3 g(grid_for(threads)), b(256);
 #define MQ_Q80(VAR)                                                                                             \
-    if (v4) hipLaunchKernelGGL((k_quantize_q8_0<VAR, OUT, true>), g, b, 0, s, x, ldx, out, xd, m, k, m_pad, kb_pad); \
-    else hipLaunchKernelGGL((k_quantize_q8_0<VAR, OUT, false>), g, b, 0, s, x, ldx, out, xd, m, k, m_pad, kb_pad);
+    if (v4) hipLaunchKernelGGL((k_quantize_q8_0<VAR, OUT, true>), g, b, 0, s, x, ldx, out, xd, m, k, m_pad, kb_pad, pre, bias); \
+    else hipLaunchKernelGGL((k_quantize_q8_0<VAR, OUT, false>), g, b, 0, s, x, ldx, out, xd, m, k, m_pad, kb_pad, pre, bias);
     switch (variant) {
         case MQ_Q8_0_X86: MQ_Q80(MQ_Q8_0_X86); break;
         case MQ_Q8_0_NEON: MQ_Q80(MQ_Q8_0_NEON); break;
@@ -635,21 +655,23 @@ static hipError_t q8_0_dispatch(const float *x, int64_t ldx, int8_t *out, float 
 
 template <int OUT>
 static hipError_t q8_K_dispatch(const float *x, int64_t ldx, int8_t *out, float *xd, int16_t *xbs, _Float16 *xmin,
-                                int64_t m, int64_t k, int64_t m_pad, hipStream_t s) {
+                                int64_t m, int64_t k, int64_t m_pad, hipStream_t s, int pre = MQ_PRE_NONE,
+                                const float *bias = nullptr) {
     const int64_t rows = m;
     const int64_t threads = rows * (k / QK_K) * 64;
     if (threads == 0) return hipSuccess;
     const dim3 g(grid_for(threads)), b(256);
     if (aligned16(x, ldx))
-        hipLaunchKernelGGL((k_quantize_q8_K<OUT, true>), g, b, 0, s, x, ldx, out, xd, xbs, xmin, m, k, m_pad);
+        hipLaunchKernelGGL((k_quantize_q8_K<OUT, true>), g, b, 0, s, x, ldx, out, xd, xbs, xmin, m, k, m_pad, pre, bias);
     else
-        hipLaunchKernelGGL((k_quantize_q8_K<OUT, false>), g, b, 0, s, x, ldx, out, xd, xbs, xmin, m, k, m_pad);
+        hipLaunchKernelGGL((k_quantize_q8_K<OUT, false>), g, b, 0, s, x, ldx, out, xd, xbs, xmin, m, k, m_pad, pre, bias);
     return hipGetLastError();
 }
 
 template <int FMT>
 static hipError_t tiled_dispatch(const float *x, int64_t ldx, int8_t *xq, float *xd, _Float16 *xmin, int64_t m,
-                                 int64_t k, int variant, int64_t m_pad, int64_t kb_pad, hipStream_t s) {
+                                 int64_t k, int variant, int64_t m_pad, int64_t kb_pad, hipStream_t s, int pre,
+                                 const float *bias) {
     constexpr int CB = (FMT == TQ_Q8_K) ? 256 : 128;
     if (m_pad % 32 != 0 || kb_pad % CB != 0) return hipErrorInvalidValue;
     const int64_t wgs = (m_pad / 32) * (kb_pad / CB);
@@ -657,8 +679,8 @@ static hipError_t tiled_dispatch(const float *x, int64_t ldx, int8_t *xq, float 
     const dim3 g((unsigned)wgs), b(256);
     const bool v4 = aligned16(x, ldx);
 #define MQ_TQ(VAR)                                                                                                      \
-    if (v4) hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, true>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad); \
-    else hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, false>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad);
+    if (v4) hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, true>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad, pre, bias); \
+    else hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, false>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad, pre, bias);
     if (FMT != TQ_Q8_0) {
         MQ_TQ(MQ_Q8_0_X86);
     } else {
@@ -673,36 +695,41 @@ static hipError_t tiled_dispatch(const float *x, int64_t ldx, int8_t *xq, float 
     return hipGetLastError();
 }
 
-hipError_t launch_quantize_f16(const float *x, int64_t ldx, void *y, int64_t m, int64_t k, hipStream_t s) {
+hipError_t launch_quantize_f16(const float *x, int64_t ldx, void *y, int64_t m, int64_t k, hipStream_t s, int pre,
+                               const float *bias) {
     const int64_t threads = m * (k / 4);
     if (threads == 0) return hipSuccess;
     const dim3 g(grid_for(threads)), b(256);
     if (aligned16(x, ldx))
-        hipLaunchKernelGGL((k_quantize_f16<true>), g, b, 0, s, x, ldx, (uint16_t *)y, m, k);
+        hipLaunchKernelGGL((k_quantize_f16<true>), g, b, 0, s, x, ldx, (uint16_t *)y, m, k, pre, bias);
     else
-        hipLaunchKernelGGL((k_quantize_f16<false>), g, b, 0, s, x, ldx, (uint16_t *)y, m, k);
+        hipLaunchKernelGGL((k_quantize_f16<false>), g, b, 0, s, x, ldx, (uint16_t *)y, m, k, pre, bias);
     return hipGetLastError();
 }
 
 hipError_t launch_quantize_act_planar(int wtype, const float *x, int64_t ldx, void *ws, int64_t m, int64_t k,
-                                      int q8_0_variant, bool tiled, hipStream_t s) {
+                                      int q8_0_variant, bool tiled, hipStream_t s, int pre, const float *bias) {
     const ActPlanes a = act_planes(wtype, m, k, tiled);
     uint8_t *base = (uint8_t *)ws;
     int8_t *xq = (int8_t *)(base + a.xq);
     float *xd = (float *)(base + a.xd);
     switch (wtype) {
         case MQ_TYPE_Q8_0:
-            if (tiled) return tiled_dispatch<TQ_Q8_0>(x, ldx, xq, xd, nullptr, m, k, q8_0_variant, a.m_pad, a.kb_pad, s);
-            return q8_0_dispatch<OUT_ROWS>(x, ldx, xq, xd, m, k, q8_0_variant, m, k, s);
+            if (tiled)
+                return tiled_dispatch<TQ_Q8_0>(x, ldx, xq, xd, nullptr, m, k, q8_0_variant, a.m_pad, a.kb_pad, s, pre,
+                                               bias);
+            return q8_0_dispatch<OUT_ROWS>(x, ldx, xq, xd, m, k, q8_0_variant, m, k, s, pre, bias);
         case MQ_TYPE_Q4_K:
         case MQ_TYPE_Q6_K:
             if (tiled)
-                return tiled_dispatch<TQ_Q8_K>(x, ldx, xq, xd, (_Float16 *)(base + a.xmin), m, k, 0, a.m_pad, a.kb_pad, s);
+                return tiled_dispatch<TQ_Q8_K>(x, ldx, xq, xd, (_Float16 *)(base + a.xmin), m, k, 0, a.m_pad, a.kb_pad, s,
+                                               pre, bias);
             return q8_K_dispatch<OUT_ROWS>(x, ldx, xq, xd, (int16_t *)(base + a.xbs), (_Float16 *)(base + a.xgm), m, k,
-                                           m, s);
+                                           m, s, pre, bias);
         case MQ_TYPE_F16:
-            if (tiled) return tiled_dispatch<TQ_F16>(x, ldx, xq, nullptr, nullptr, m, k, 0, a.m_pad, a.kb_pad, s);
-            return launch_quantize_f16(x, ldx, base + a.xq, m, k, s);
+            if (tiled)
+                return tiled_dispatch<TQ_F16>(x, ldx, xq, nullptr, nullptr, m, k, 0, a.m_pad, a.kb_pad, s, pre, bias);
+            return launch_quantize_f16(x, ldx, base + a.xq, m, k, s, pre, bias);
         default: return hipErrorInvalidValue;
     }
 }

@@ -8,6 +8,7 @@ LIB_PATH = os.path.join(HERE, "libmq.so")
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K = 0, 1, 8, 12, 14, 15
 Q8_0_X86, Q8_0_NEON, Q8_0_REF = 0, 1, 2
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
+PRE_NONE, PRE_GELU_ERF = 0, 1
 
 TYPE_NAMES = {TYPE_F32: "f32", TYPE_F16: "f16", TYPE_Q8_0: "q8_0", TYPE_Q4_K: "q4_K",
               TYPE_Q6_K: "q6_K", TYPE_Q8_K: "q8_K"}
@@ -49,6 +50,7 @@ _SIGS = {
     "mq_mul_mat": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                             _c_sz, _c_vp]),
     "mq_quantize_act": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_sz, _c_int, _c_vp]),
+    "mq_quantize_act_ex": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_int, _c_vp, _c_sz, _c_int, _c_vp]),
     "mq_mul_mat_q": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_vp]),
     "mq_mul_mat_ex": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                                _c_sz, _c_int, _c_vp]),

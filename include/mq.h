@@ -57,6 +57,10 @@ extern "C" {
 #define MQ_PATH_GEMV 1 /* weight-streaming GEMV, m <= 8 */
 #define MQ_PATH_GEMM 2 /* MFMA GEMM */
 
+/* Elementwise prologue of mq_quantize_act_ex, applied to X before it is quantized. */
+#define MQ_PRE_NONE 0     /* x (+ bias) */
+#define MQ_PRE_GELU_ERF 1 /* gelu_erf(x + bias) */
+
 /* ---- library / device ---- */
 
 /* Checks that the current HIP device is gfx950.  Replaces nothing in the reference
@@ -134,6 +138,15 @@ int mq_quantize_act(int type, const float *x, int64_t ldx, int64_t m, int64_t k,
                     size_t workspace_bytes, int path, void *stream);
 int mq_mul_mat_q(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m, float *y,
                  int64_t ldy, int path, void *stream);
+
+/* mq_quantize_act with the graph's elementwise producer folded in: it quantizes
+ * op(X + bias) where bias is an fp32 [k] row added to every row of X (NULL: none) and
+ * op is MQ_PRE_NONE or MQ_PRE_GELU_ERF.  The value quantized is the fp32 tensor the
+ * ggml graph materialises between those nodes and the MUL_MAT: the ADD of the FFN-up
+ * bias and ggml_gelu_erf feeding the FFN-down projection (src/crispembed.cpp:1410-1416,
+ * 0.5 v (1 + erf(v / sqrt 2)) in fp32). */
+int mq_quantize_act_ex(int type, const float *x, int64_t ldx, int64_t m, int64_t k, const float *bias, int op,
+                       void *workspace, size_t workspace_bytes, int path, void *stream);
 
 #ifdef __cplusplus
 }

@@ -17,8 +17,8 @@ def _declared(header):
 def test_libmq_exports_all_declared_symbols():
     from crispembed_amd import mq
     L = mq.lib()
-    names = _declared("mq.h")
-    assert len(names) >= 20
+    names = _declared("mq.h") + _declared("mq_bert.h")
+    assert len(names) >= 25
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing, missing
 
@@ -38,6 +38,8 @@ def test_host_only_entry_points_without_gpu():
     # argument errors come back as codes with a message, before any HIP call
     rc = L.mq_mul_mat(mq.TYPE_Q4_K, None, 8, 300, None, 300, 1, None, 8, None, 0, None)
     assert rc == -2 and b"multiple" in L.mq_last_error()
+    rc = L.mq_quantize_act_ex(mq.TYPE_Q8_0, 256, 256, 2, 256, None, 7, 4096, 1 << 20, mq.PATH_AUTO, None)
+    assert rc == -1 and b"prologue" in L.mq_last_error()
 
 
 def test_ggml_backend_library_exports():

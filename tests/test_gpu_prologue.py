@@ -1,0 +1,87 @@
+"""Fused activation prologue (mq_quantize_act_ex): the bias ADD and GELU_ERF nodes that feed
+the FFN-down MUL_MAT (src/crispembed.cpp:1410-1416) applied inside the activation quantizer.
+
+Bias only: the quantized workspace is byte-identical to quantizing x + bias (one fp32 add
+per element, the rounding numpy does), so bit-exactness carries over from the plain
+quantizer.  GELU-erf: the device erff may differ from a correctly rounded erf by an ulp,
+which can move a quant by one step near a rounding boundary, so the check is the mul_mat
+bar (max|dY| / max|Y_ref| <= 1e-4) against the oracle fed gelu(x + bias) computed in fp64
+and rounded to fp32, plus >= 99% identical workspace bytes.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+from scipy.special import erf
+
+import oracle_ffi as O
+from ggml_numpy import rel_err
+from gpu_util import dev, empty_u8, host, stream, weight_image
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+TYPES = [O.Q8_0, O.Q4_K, O.Q6_K, O.F16]
+
+
+def _quant(wtype, x_dev, m, k, path, bias_dev=None, op=0):
+    from crispembed_amd import mq
+    L = mq.lib()
+    nb = L.mq_workspace_bytes(wtype, m, k)
+    buf, off = empty_u8(nb)
+    buf.zero_()
+    ptr = buf.data_ptr() + off
+    bias = ctypes.c_void_p(bias_dev.data_ptr()) if bias_dev is not None else None
+    mq.check(L.mq_quantize_act_ex(wtype, ctypes.c_void_p(x_dev.data_ptr()), x_dev.stride(0), m, k, bias, op,
+                                  ctypes.c_void_p(ptr), nb, path, stream()))
+    return buf, ptr, host(buf)[off:off + nb]
+
+
+def _gelu_ref(t32):
+    t = t32.astype(np.float64)
+    return (0.5 * t * (1.0 + erf(t / np.sqrt(2.0)))).astype(np.float32)
+
+
+def _inputs(m, k, ld, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((m, k)) * 2.0).astype(np.float32)
+    b = rng.standard_normal(k).astype(np.float32)
+    full = np.zeros((m, ld), np.float32)
+    full[:, :k] = x
+    return x, b, dev(full)[:, :k]
+
+
+@pytest.mark.parametrize("wtype", TYPES)
+@pytest.mark.parametrize("m,k,ld,path", [(5, 1536, 1536, 1), (8, 512, 520, 1), (37, 1536, 1536, 2),
+                                         (300, 512, 516, 2)])
+def test_bias_prologue_bit_exact(wtype, m, k, ld, path):
+    x, b, xd = _inputs(m, k, ld, 11 * m + k)
+    _, _, got = _quant(wtype, xd, m, k, path, dev(b), 0)
+    _, _, want = _quant(wtype, dev((x + b).astype(np.float32)), m, k, path)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("wtype", TYPES)
+@pytest.mark.parametrize("m,n,k,ld,path", [(3, 70, 1536, 1536, 1), (8, 33, 512, 520, 1), (64, 96, 1536, 1536, 2),
+                                           (129, 70, 512, 516, 2)])
+def test_gelu_prologue_mul_mat(oracle, wtype, m, n, k, ld, path):
+    from crispembed_amd import mq
+    import torch
+    x, b, xd = _inputs(m, k, ld, 7 * m + n + k)
+    xg = _gelu_ref((x + b).astype(np.float32))
+    keep, ws, got = _quant(wtype, xd, m, k, path, dev(b), 1)  # keep: the workspace read by mq_mul_mat_q
+    _, _, want = _quant(wtype, dev(xg), m, k, path)
+    same = np.mean(got == want)
+    assert same >= 0.99, same
+    wf = (np.random.default_rng(n).standard_normal((n, k)) * 0.02).astype(np.float32)
+    w = oracle.quantize_chunk(wtype, wf)
+    _, wp = weight_image(wtype, w, n, k)
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    mq.check(mq.lib().mq_mul_mat_q(wtype, ctypes.c_void_p(wp), n, k, ctypes.c_void_p(ws), m,
+                                   ctypes.c_void_p(y.data_ptr()), n, path, stream()))
+    y = host(y)
+    xq = oracle.quantize_act(wtype, xg)
+    e1 = rel_err(y, oracle.mul_mat_exact(wtype, w, xq, k))
+    e2 = rel_err(y, oracle.mul_mat_q(wtype, w, xq, k))
+    assert e1 <= TOL and e2 <= TOL, (e1, e2, same)
+
