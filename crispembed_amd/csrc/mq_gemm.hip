@@ -4,7 +4,11 @@
 //
 // Arithmetic (exact integer block dots, fp32 scales, as ggml_vec_dot_*):
 //   Q8_0  v_mfma_i32_32x32x32_i8, one Q8_0 block (K = 32) per MFMA; the int32
-//         block dot is scaled by d_x * d_w in fp32 right after the block.
+//         block dot is scaled by d_x * d_w in fp32 right after the block.  The
+//         32x32 tile of scale products d_x[r] * d_w[c] comes from a rank-1
+//         v_mfma_f32_32x32x2_f32 (exact: both scales are fp16 values), which leaves
+//         two VALU ops per output and block (convert, fma) instead of three: the
+//         per-block scaling, not the int8 MFMA, bounds this format.
 //   Q4_K  the weight operand is sc_j*q4 (10 bits) split at load time into two
 //         int8 limbs, lo in [0,127] and hi in [0,7] (value = lo + 128*hi).  Two
 //         int32 accumulators run over a whole 256-value superblock, so the 6-bit
@@ -298,8 +302,66 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
     const int xfrag0 = wm * TM * KC * 1024 + lane * 16;  // LDS offset of this wave's first X fragment
     const int wfrag0 = C::X_BYTES + wn * TN * KC * 1024 + lane * 16;
 
+    // Q8_0 stage: per block and 32x32 tile, an int8 MFMA (block dot), a rank-1 f32
+    // MFMA (scale products) and the convert + fma of the 16 outputs per lane.  The
+    // steps are software-pipelined: the MFMAs of step u+1 are issued before the
+    // VALU work of step u, so the matrix and vector pipes overlap within a wave.
+    auto compute_q8_0 = [&](const int8_t *st) __attribute__((always_inline)) {
+        constexpr int NTL = TM * TN, NSTEP = KC * NTL;
+        v4i xa[KC][TM], wb[KC][TN];
+        float dx[KC][TM], dw[KC][TN];
+#pragma unroll
+        for (int kc = 0; kc < KC; kc++) {
+            // scale reads (asm: see ds_read128); lane l < 32 holds the k = 0 operands of
+            // the rank-1 MFMA, d_x of row l and d_w of column l; A's k = 1 half is zero
+            const uint32_t scx = lds_addr(st + C::X_BYTES + C::W_BYTES + kc * 1024);
+            const uint32_t scw = lds_addr(st + C::X_BYTES + C::W_BYTES + C::SCX + kc * 1024);
+#pragma unroll
+            for (int j = 0; j < TN; j++) dw[kc][j] = ds_read32(scw + ((wn * TN + j) * 32 + lrow) * 4);
+#pragma unroll
+            for (int i = 0; i < TM; i++) dx[kc][i] = ds_read32(scx + ((wm * TM + i) * 32 + lrow) * 4);
+#pragma unroll
+            for (int i = 0; i < TM; i++) xa[kc][i] = *(const v4i *)(st + xfrag0 + (i * KC + kc) * 1024);
+#pragma unroll
+            for (int j = 0; j < TN; j++) wb[kc][j] = *(const v4i *)(st + wfrag0 + (j * KC + kc) * 1024);
+        }
+        static_assert(KC == 2 && TM <= 2 && TN <= 2, "the wait below names every scale register");
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(dw[0][0]), "+v"(dw[0][TN - 1]), "+v"(dx[0][0]), "+v"(dx[0][TM - 1]), "+v"(dw[1][0]),
+                       "+v"(dw[1][TN - 1]), "+v"(dx[1][0]), "+v"(dx[1][TM - 1]));
+#pragma unroll
+        for (int kc = 0; kc < KC; kc++)
+#pragma unroll
+            for (int i = 0; i < TM; i++) dx[kc][i] = lhalf ? 0.0f : dx[kc][i];
+        v16i tq[2];
+        v16f sc[2];
+        auto mfma = [&](auto uc) __attribute__((always_inline)) {
+            constexpr int u = decltype(uc)::value, kc = u / NTL, i = u % TM, j = (u % NTL) / TM;
+            tq[u & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[kc][i], wb[kc][j], (v16i){}, 0, 0, 0);
+            sc[u & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(dx[kc][i], dw[kc][j], (v16f){}, 0, 0, 0);
+        };
+        auto scale = [&](auto uc) __attribute__((always_inline)) {
+            constexpr int u = decltype(uc)::value, i = u % TM, j = (u % NTL) / TM;
+#pragma unroll
+            for (int rr = 0; rr < 16; rr++) acc[i][j][rr] += (float)tq[u & 1][rr] * sc[u & 1][rr];
+        };
+        mfma(std::integral_constant<int, 0>{});
+        static_for<1, NSTEP>([&](auto uc) __attribute__((always_inline)) {
+            constexpr int u = decltype(uc)::value;
+            mfma(std::integral_constant<int, u>{});
+            __builtin_amdgcn_sched_barrier(0);
+            scale(std::integral_constant<int, u - 1>{});
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        scale(std::integral_constant<int, NSTEP - 1>{});
+    };
+
     // MFMAs of one stage
     auto compute = [&](const int8_t *st) __attribute__((always_inline)) {
+        if constexpr (FMT == FMT_Q8_0) {
+            compute_q8_0(st);
+            return;
+        }
 #pragma unroll
         for (int kc = 0; kc < KC; kc++) {
             v4i xa[TM];
@@ -314,38 +376,6 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, xa[i]),
                                                                           __builtin_bit_cast(v8h, wb), acc[i][j], 0,
                                                                           0, 0);
-                }
-            } else if constexpr (FMT == FMT_Q8_0) {
-                // per-block scales (asm reads: see ds_read128)
-                const uint32_t scx = lds_addr(st + C::X_BYTES + C::W_BYTES + kc * 1024);
-                const uint32_t scw = lds_addr(st + C::X_BYTES + C::W_BYTES + C::SCX + kc * 1024);
-                float dw[TN];
-                v4i dx4[TM][4];
-#pragma unroll
-                for (int j = 0; j < TN; j++) dw[j] = ds_read32(scw + ((wn * TN + j) * 32 + lrow) * 4);
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int g = 0; g < 4; g++) dx4[i][g] = ds_read128(scx + ((wm * TM + i) * 32 + 8 * g + 4 * lhalf) * 4);
-                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(dw[0]), "+v"(dw[TN - 1]), "+v"(dx4[0][0]), "+v"(dx4[0][1]),
-                             "+v"(dx4[0][2]), "+v"(dx4[0][3]), "+v"(dx4[TM - 1][0]), "+v"(dx4[TM - 1][1]),
-                             "+v"(dx4[TM - 1][2]), "+v"(dx4[TM - 1][3]));
-                static_assert(TM <= 2 && TN <= 2, "the wait above names every scale register");
-#pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    const v4i wb = *(const v4i *)(st + wfrag0 + (j * KC + kc) * 1024);
-#pragma unroll
-                    for (int i = 0; i < TM; i++) {
-                        const v16i tq = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[i], wb, (v16i){}, 0, 0, 0);
-#pragma unroll
-                        for (int g = 0; g < 4; g++) {
-                            const float4 d4 = __builtin_bit_cast(float4, dx4[i][g]);
-                            acc[i][j][4 * g + 0] += (float)tq[4 * g + 0] * (d4.x * dw[j]);
-                            acc[i][j][4 * g + 1] += (float)tq[4 * g + 1] * (d4.y * dw[j]);
-                            acc[i][j][4 * g + 2] += (float)tq[4 * g + 2] * (d4.z * dw[j]);
-                            acc[i][j][4 * g + 3] += (float)tq[4 * g + 3] * (d4.w * dw[j]);
-                        }
-                    }
                 }
             } else {
                 v4i wl[TN], wh[TN];
@@ -496,10 +526,10 @@ template <int FMT>
 static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
     int cfg = gemm_cfg_env();
     if (cfg < 1 || cfg > 5 || cfg == 2) {
-        // the largest tile that still gives every CU (256) a workgroup
-        if (tiles(a.M, a.N, 256, 128) >= 256) cfg = 1;
-        else if (tiles(a.M, a.N, 128, 128) >= 256) cfg = 3;
-        else cfg = 4;
+        // 256x128 tiles when that still gives every CU (256) a workgroup, else 128x128
+        // (the smaller tiles measured slower even where 128x128 leaves CUs idle:
+        // 4096x384x384 Q8_0 12.7 us at 128x128, 13.2 us at 128x64, 14.1 us at 64x64)
+        cfg = (tiles(a.M, a.N, 256, 128) >= 256) ? 1 : 3;
     }
     switch (cfg) {
         case 1: return launch_cfg<FMT, 4, 2, 2, 2, 1>(a, s);

@@ -108,6 +108,11 @@ void or_mul_mat_q(int wtype, const void *w, int64_t n, int64_t k, const void *xq
 /* fp64 product of the quantized operands: integer block sums, fp64 scaling. */
 void or_mul_mat_exact(int wtype, const void *w, int64_t n, int64_t k, const void *xq, int64_t m, double *y);
 
+/* ---- CPU baseline (cpu_fast.c): the same mul_mat with AVX2 integer dots and threads ---- */
+int or_fast_supported(int wtype);
+int or_fast_mul_mat(int wtype, const void *w, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m, float *y,
+                    int64_t ldy, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

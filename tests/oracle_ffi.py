@@ -49,6 +49,8 @@ class Oracle:
             "or_mul_mat": (None, [ci, vp, i64, i64, vp, i64, i64, vp, i64, ci, ci]),
             "or_mul_mat_q": (None, [ci, vp, i64, i64, vp, i64, vp, i64, ci]),
             "or_mul_mat_exact": (None, [ci, vp, i64, i64, vp, i64, vp]),
+            "or_fast_supported": (ci, [ci]),
+            "or_fast_mul_mat": (ci, [ci, vp, i64, i64, vp, i64, i64, vp, i64, ci]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -109,6 +111,21 @@ class Oracle:
         m = xq.size // row_size(VEC_DOT[wtype], k)
         y = np.empty((m, n), dtype=np.float32)
         self.L.or_mul_mat_q(wtype, _ptr(w), n, k, _ptr(xq), m, _ptr(y), n, nthreads)
+        return y
+
+    def fast_supported(self, wtype):
+        return bool(self.L.or_fast_supported(wtype))
+
+    def fast_mul_mat(self, wtype, w, x, nthreads=8):
+        """The CPU baseline (AVX2 integer dots, threads); same semantics as mul_mat."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        m, k = x.shape
+        n = w.size // row_size(wtype, k)
+        y = np.empty((m, n), dtype=np.float32)
+        rc = self.L.or_fast_mul_mat(wtype, _ptr(w), n, k, _ptr(x), k, m, _ptr(y), n, nthreads)
+        if rc != 0:
+            raise RuntimeError(f"or_fast_mul_mat: type {wtype} unsupported on this host")
         return y
 
     def mul_mat_exact(self, wtype, w, xq, k):

@@ -53,3 +53,17 @@ def test_q4_K_min_term_matters(oracle):
     a = oracle.mul_mat_q(O.Q4_K, w, xq, k)
     b = oracle.mul_mat_q(O.Q4_K, w_nomin.ravel(), xq, k)
     assert rel_err(b, a) > 1e-2
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("m,n,k", [(1, 3, 256), (17, 33, 512), (40, 20, 1536)])
+def test_cpu_baseline_matches_exact_product(oracle, wtype, m, n, k):
+    """The SIMD + threads CPU baseline computes the same mul_mat (block dots in another order)."""
+    if not oracle.fast_supported(wtype):
+        pytest.skip("host without AVX2/FMA/F16C")
+    wf, x = _case(wtype, m, n, k, 300 + m + n + k + wtype)
+    w = oracle.quantize_chunk(wtype, wf)
+    xq = oracle.quantize_act(wtype, x)
+    y = oracle.fast_mul_mat(wtype, w, x, nthreads=3)
+    assert rel_err(y, mul_mat_exact(wtype, w, xq, k)) < 1e-5
+    assert rel_err(y, oracle.mul_mat(wtype, w, x)) < 1e-5
