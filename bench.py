@@ -13,7 +13,7 @@ dense MFMA peak (5.0 POP/s).
 cpu_baseline = the restated ggml-cpu mul_mat (AVX2 integer dots, threads) on a
 bounded sample of token rows of the same workload, on the host cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras] [--only q8_0|e2e|decode]
 """
 import argparse
 import ctypes
@@ -346,6 +346,8 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="skip the Q8_0 and GEMV side measurements")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--gemm-cfg", default=None, help="MQ_GEMM_CFG tile configuration (1 or 3)")
+    ap.add_argument("--only", choices=["q8_0", "e2e", "decode"], default=None,
+                    help="run one side measurement alone (for per-workload profiles) and print its JSON")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 10 device copies of 256 MiB (reference kernel for rocprof byte counters)")
     args = ap.parse_args()
@@ -368,6 +370,12 @@ def main():
     from crispembed_amd import mq, synth
     L = mq.lib()
     mq.check(L.mq_init())
+    if args.only:
+        fn = {"q8_0": lambda: bench_q8_0_minilm(torch, L, mq, synth),
+              "e2e": lambda: bench_minilm_e2e(torch, L, mq),
+              "decode": lambda: bench_decode(torch, L, mq, synth)}[args.only]
+        print(json.dumps({"only": args.only, "result": fn()}), flush=True)
+        return
 
     r = bench_q4k_ffn(args, torch, L, mq, synth)
     x_up, x_dn, q_up, q_dn = r.pop("x")

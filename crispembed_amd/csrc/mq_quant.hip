@@ -476,6 +476,20 @@ __device__ __forceinline__ uint4 pack16(const int *v) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// The weight-prepare kernels run one thread per (row, superblock); the workgroup's 256
+// consecutive GGUF blocks are first copied to LDS with coalesced 2-byte loads (blocks are
+// 2-byte aligned), so each thread's many small reads of its block hit LDS, not memory.
+// Blocks [b0, b1) exist in the GGUF part (rows < n); the copy is done by every thread.
+template <int BB>
+__device__ __forceinline__ void stage_blocks(const uint8_t *gguf, int64_t b0, int64_t b1, uint8_t *lds) {
+    static_assert(BB % 2 == 0, "2-byte units");
+    const int64_t nunits = b1 > b0 ? (b1 - b0) * (BB / 2) : 0;
+    const uint16_t *src = (const uint16_t *)(gguf + b0 * BB);
+    uint16_t *dst = (uint16_t *)lds;
+    for (int64_t i = threadIdx.x; i < nunits; i += blockDim.x) dst[i] = src[i];
+    __syncthreads();
+}
+
 // Q4_K: limbs of sc_j * q4 (lo = v & 127, hi = v >> 7), per-superblock scales, min fragment.
 __global__ __launch_bounds__(256) void k_prepare_q4_K_tiled(const uint8_t *__restrict__ gguf, int8_t *__restrict__ tlo,
                                                             int8_t *__restrict__ thi, float *__restrict__ tdw,
@@ -484,10 +498,13 @@ __global__ __launch_bounds__(256) void k_prepare_q4_K_tiled(const uint8_t *__res
                                                             int64_t n_pad) {
     const int64_t nbr = k / QK_K;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    __shared__ __attribute__((aligned(16))) uint8_t sblk[256 * sizeof(block_q4_K)];
+    const int64_t gb0 = row0 * nbr + (int64_t)blockIdx.x * blockDim.x;
+    stage_blocks<sizeof(block_q4_K)>(gguf, gb0, min(gb0 + (int64_t)blockDim.x, min(row_end, n) * nbr), sblk);
     if (gid >= (row_end - row0) * nbr) return;
     const int64_t row = row0 + gid / nbr, b = gid % nbr;
     const bool valid = row < n;
-    const uint8_t *src = gguf + (row * nbr + b) * sizeof(block_q4_K);
+    const uint8_t *src = sblk + threadIdx.x * sizeof(block_q4_K);
     int sc[8], mn[8];
     float d = 0.f, dmin = 0.f;
 #pragma unroll
@@ -539,12 +556,15 @@ __global__ __launch_bounds__(256) void k_prepare_q6_K_gv(const uint8_t *__restri
                                                          int64_t n, int64_t row0, int64_t row1, int64_t k) {
     const int64_t nsb = k / QK_K;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    __shared__ __attribute__((aligned(16))) uint8_t sblk[256 * sizeof(block_q6_K)];
+    const int64_t gb0 = row0 * nsb + (int64_t)blockIdx.x * blockDim.x;
+    stage_blocks<sizeof(block_q6_K)>(gguf, gb0, min(gb0 + (int64_t)blockDim.x, min(row1, n) * nsb), sblk);
     const int64_t row = row0 + t / nsb, sb = t % nsb;
     if (row >= row1) return;
     const int r = (int)(row % GV_ROWS);
     uint8_t *T = gv + ((row / GV_ROWS) * nsb + sb) * GV6_BYTES;
     const bool live = row < n;
-    const uint8_t *blk = gguf + (row * nsb + sb) * sizeof(block_q6_K);  // 2-byte aligned: byte reads
+    const uint8_t *blk = sblk + threadIdx.x * sizeof(block_q6_K);
     for (int p = 0; p < 4; p++) {
         uint32_t his[4] = {0, 0, 0, 0};
         for (int kk = 0; kk < 8; kk++) {
@@ -580,10 +600,13 @@ __global__ __launch_bounds__(256) void k_prepare_q6_K_tiled(const uint8_t *__res
                                                             int64_t n_pad) {
     const int64_t nbr = k / QK_K;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    __shared__ __attribute__((aligned(16))) uint8_t sblk[256 * sizeof(block_q6_K)];
+    const int64_t gb0 = row0 * nbr + (int64_t)blockIdx.x * blockDim.x;
+    stage_blocks<sizeof(block_q6_K)>(gguf, gb0, min(gb0 + (int64_t)blockDim.x, min(row_end, n) * nbr), sblk);
     if (gid >= (row_end - row0) * nbr) return;
     const int64_t row = row0 + gid / nbr, b = gid % nbr;
     const bool valid = row < n;
-    const uint8_t *src = gguf + (row * nbr + b) * sizeof(block_q6_K);
+    const uint8_t *src = sblk + threadIdx.x * sizeof(block_q6_K);
     tdw[b * n_pad + row] = valid ? f16_bits_to_f32(*(const uint16_t *)(src + 208)) : 0.f;
     for (int t = 0; t < 16; t++) {  // 16 chunks of 16 values
         const int h = t >> 3, g = (t & 7) >> 1, l0 = (t & 1) * 16;
