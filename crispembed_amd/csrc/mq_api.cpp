@@ -242,7 +242,11 @@ int mq_quantize_act_ex(int type, const float *x, int64_t ldx, int64_t m, int64_t
     if (!type_ok(type)) return fail(MQ_EUNSUPPORTED, "weight type %d is not Q8_0/Q4_K/Q6_K/F16", type);
     if (!mq_supports(type, k)) return fail(MQ_EUNSUPPORTED, "k=%lld not supported for type %d", (long long)k, type);
     if (!x || !workspace || m < 0 || m > INT32_MAX || ldx < k) return fail(MQ_EINVAL, "mq_quantize_act: bad arguments");
-    if (op != MQ_PRE_NONE && op != MQ_PRE_GELU_ERF) return fail(MQ_EINVAL, "mq_quantize_act: unknown prologue op %d", op);
+    if (op != MQ_PRE_NONE && op != MQ_PRE_GELU_ERF && op != MQ_PRE_SILU_MUL)
+        return fail(MQ_EINVAL, "mq_quantize_act: unknown prologue op %d", op);
+    if (op == MQ_PRE_SILU_MUL && ldx < 2 * k)
+        return fail(MQ_EINVAL, "mq_quantize_act: MQ_PRE_SILU_MUL reads 2k = %lld values per row, ldx = %lld",
+                    (long long)(2 * k), (long long)ldx);
     if (!is_aligned(workspace, 256)) return fail(MQ_EINVAL, "mq_quantize_act: workspace must be 256-byte aligned");
     if (m == 0) return MQ_OK;
     path = resolve_path(path, m);

@@ -19,45 +19,22 @@
 #include "../../include/mq.h"
 #include "../../include/mq_bert.h"
 #include "mq_internal.h"
+#include "mq_runner.h"
 
 namespace mq {
 hipError_t launch_embed_ln(const int32_t *ids, const int32_t *types, const float *word, const float *pos,
                            const float *type, const float *lw, const float *lb, float eps, float *out, int64_t rows,
-                           int T, int H, hipStream_t s);
+                           int T, int H, int n_vocab, int n_type, hipStream_t s);
 hipError_t launch_bias_res_ln(const float *y, const float *bias, const float *res, const float *lw, const float *lb,
                               float eps, float *out, int64_t rows, int H, hipStream_t s);
 hipError_t launch_attention(const float *qkv, const float *bqkv, float *out, int B, int T, int H, int nh,
                             hipStream_t s);
 hipError_t launch_mean_pool_l2(const float *x, float *out, int B, int T, int H, hipStream_t s);
-int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));  // mq_api.cpp
 }  // namespace mq
 
 using namespace mq;
 
 namespace {
-
-struct DevBuf {
-    void *p = nullptr;
-    size_t bytes = 0;
-    ~DevBuf() {
-        if (p) (void)hipFree(p);
-    }
-    bool ensure(size_t n) {
-        if (n <= bytes) return true;
-        if (p) (void)hipFree(p);
-        p = nullptr;
-        bytes = 0;
-        if (hipMalloc(&p, n) != hipSuccess) return false;
-        bytes = n;
-        return true;
-    }
-    float *f() const { return (float *)p; }
-};
-
-struct Linear {
-    DevBuf img;
-    int64_t n = 0, k = 0;
-};
 
 struct Layer {
     Linear qkv, o, fc1, fc2;
@@ -73,33 +50,6 @@ struct mq_bert {
     DevBuf x, qkv, att, y, ff, ws;
     int64_t rows_cap = 0;
 };
-
-static int upload(DevBuf &d, const void *src, size_t bytes) {
-    if (!d.ensure(bytes)) return set_error(MQ_ENOMEM, "hipMalloc(%zu) failed", bytes);
-    if (hipMemcpy(d.p, src, bytes, hipMemcpyHostToDevice) != hipSuccess)
-        return set_error(MQ_EHIP, "hipMemcpy of %zu bytes failed", bytes);
-    return MQ_OK;
-}
-
-// GGUF rows of one or more weights with the same k, concatenated, as a prepared image.
-static int upload_linear(Linear &L, int type, const std::vector<const void *> &parts, int64_t rows_each, int64_t k) {
-    const size_t rs = mq_row_size(type, k);
-    const int64_t n = rows_each * (int64_t)parts.size();
-    if (rs == 0) return set_error(MQ_EINVAL, "bad weight type %d / k %lld", type, (long long)k);
-    const size_t img = mq_weight_image_bytes(type, n, k);
-    if (!L.img.ensure(img)) return set_error(MQ_ENOMEM, "hipMalloc(%zu) failed", img);
-    for (size_t i = 0; i < parts.size(); i++) {
-        if (!parts[i]) return set_error(MQ_EINVAL, "NULL weight");
-        if (hipMemcpy((char *)L.img.p + i * rows_each * rs, parts[i], rows_each * rs, hipMemcpyHostToDevice) !=
-            hipSuccess)
-            return set_error(MQ_EHIP, "hipMemcpy of weights failed");
-    }
-    L.n = n;
-    L.k = k;
-    const int rc = mq_weight_prepare(type, L.img.p, n, k, 0, n, nullptr);
-    if (rc) return rc;
-    return hipDeviceSynchronize() == hipSuccess ? MQ_OK : set_error(MQ_EHIP, "weight preparation failed");
-}
 
 extern "C" mq_bert *mq_bert_create(const mq_bert_hparams *hp) {
     if (!hp || hp->n_layer <= 0 || hp->n_embd <= 0 || hp->n_head <= 0 || hp->n_embd % hp->n_head != 0 ||
@@ -143,10 +93,10 @@ extern "C" int mq_bert_set_layer(mq_bert *m, int il, const void *wq, const void 
     const int t = m->hp.wtype;
     const int64_t H = m->hp.n_embd, F = m->hp.n_ff;
     int rc;
-    if ((rc = upload_linear(L.qkv, t, {wq, wk, wv}, H, H))) return rc;
-    if ((rc = upload_linear(L.o, t, {wo}, H, H))) return rc;
-    if ((rc = upload_linear(L.fc1, t, {w1}, F, H))) return rc;
-    if ((rc = upload_linear(L.fc2, t, {w2}, H, F))) return rc;
+    if ((rc = upload_linear(L.qkv, t, {wq, wk, wv}, {H, H, H}, H))) return rc;
+    if ((rc = upload_linear(L.o, t, {wo}, {H}, H))) return rc;
+    if ((rc = upload_linear(L.fc1, t, {w1}, {F}, H))) return rc;
+    if ((rc = upload_linear(L.fc2, t, {w2}, {H}, F))) return rc;
     std::vector<float> bqkv(3 * H);
     std::memcpy(bqkv.data(), bq, H * sizeof(float));
     std::memcpy(bqkv.data() + H, bk, H * sizeof(float));
@@ -159,10 +109,6 @@ extern "C" int mq_bert_set_layer(mq_bert *m, int il, const void *wq, const void 
     if ((rc = upload(L.ln1b, ln1_b, H * sizeof(float)))) return rc;
     if ((rc = upload(L.ln2w, ln2_w, H * sizeof(float)))) return rc;
     return upload(L.ln2b, ln2_b, H * sizeof(float));
-}
-
-static int hip_rc(hipError_t e, const char *what) {
-    return e == hipSuccess ? MQ_OK : set_error(MQ_EHIP, "%s: %s", what, hipGetErrorString(e));
 }
 
 extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *types, int B, int T, float *out,
@@ -186,7 +132,7 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
     int rc;
     if ((rc = hip_rc(launch_embed_ln(ids, hp.n_type > 0 ? types : nullptr, m->tok.f(), m->pos.f(),
                                      hp.n_type > 0 ? m->type.f() : nullptr, m->lnw.f(), m->lnb.f(), eps, X, rows, T,
-                                     (int)H, s),
+                                     (int)H, hp.n_vocab, hp.n_type, s),
                      "embeddings")))
         return rc;
     auto mm = [&](const Linear &L, const float *in, float *y) {

@@ -1,0 +1,305 @@
+// mq_decoder.hip -- the non-MUL_MAT ops of a decoder-style embedder (Qwen3 family) on gfx950.
+//
+// CrispEmbed's decoder graph (src/decoder_embed.cpp:565-830) around the mul_mats:
+//   embedding   GET_ROWS(token_embd)
+//   norms       RMS_NORM(eps) * w before attention and before the FFN; the residual ADD
+//               that produces the norm's input is fused in front of it
+//   q / k       per-head RMS_NORM * q_norm / k_norm, then ROPE_EXT in NEOX mode (pair
+//               (i, i + d/2) rotated by pos * base^(-2i/d), positions 0..T-1 per sequence)
+//   attention   FLASH_ATTN_EXT, scale 1/sqrt(head_dim), causal mask (0 / -inf), grouped
+//               query heads (head h reads key/value head h / (n_head / n_kv_head))
+//   FFN         silu(gate) * up -- applied by the FFN-down activation quantizer
+//   pooling     output RMS_NORM of the last token (or of every token, then the mean), L2
+//               normalised with sqrtf(max(sum x^2, 1e-12)) (src/decoder_embed.cpp:1044-1100)
+// Arithmetic is fp32 throughout; the attention runs its products on fp32 MFMAs.
+#include "mq_internal.h"
+#include "mq_wave.h"
+
+namespace mq {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// One wave per row (V values per lane, rows up to 64*V wide):
+//   x = ids ? tok[ids[row]] : y + res      (GET_ROWS, or the residual ADD; res may be NULL)
+//   xout = x (if non-NULL; may alias res), hout = x / sqrt(mean(x^2) + eps) * w
+template <int V>
+__global__ __launch_bounds__(256) void k_add_rmsnorm(const float *y, const float *res, const int32_t *__restrict__ ids,
+                                                     const float *__restrict__ tok, const float *__restrict__ w,
+                                                     float eps, float *xout, float *__restrict__ hout, int64_t rows,
+                                                     int H, int n_vocab) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    // ids outside the table are clamped: a bad id reads a valid row, never out of bounds
+    const float *src = ids ? tok + (int64_t)min(max(ids[row], 0), n_vocab - 1) * H : y + row * H;
+    float v[V];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int c = lane + 64 * i;
+        v[i] = 0.f;
+        if (c < H) {
+            v[i] = src[c];
+            if (!ids && res) v[i] += res[row * H + c];
+        }
+        ss += v[i] * v[i];
+    }
+    if (xout) {
+#pragma unroll
+        for (int i = 0; i < V; i++)
+            if (lane + 64 * i < H) xout[row * H + lane + 64 * i] = v[i];
+    }
+    const float scale = 1.0f / sqrtf(wave_sum_f(ss) / (float)H + eps);
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int c = lane + 64 * i;
+        if (c < H) hout[row * H + c] = v[i] * scale * w[c];
+    }
+}
+
+// One wave per (row, head) of Q and K inside the fused projection output qkv[rows][ld]
+// (Q heads at columns h*HD for h < nq, K heads right after them).  Lane l < HD/2 holds the
+// NEOX pair (l, l + HD/2): per-head RMS norm (when the weight is given), then the rotation
+// by theta = pos * theta_scale^l, the angle built by the same repeated multiplication as
+// ggml's rope cache.
+template <int HD>
+__global__ __launch_bounds__(256) void k_qk_norm_rope(float *qkv, int64_t ld, const float *__restrict__ qw,
+                                                      const float *__restrict__ kw, float eps, int nq, int nkv, int T,
+                                                      float theta_scale, int64_t rows) {
+    constexpr int HALF = HD / 2;
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int nh = nq + nkv;
+    if (item >= rows * nh) return;
+    const int64_t row = item / nh;
+    const int h = (int)(item - row * nh);
+    float *x = qkv + row * ld + (int64_t)h * HD;
+    const float *w = h < nq ? qw : kw;
+    const bool on = lane < HALF;
+    float a = on ? x[lane] : 0.f, b = on ? x[lane + HALF] : 0.f;
+    if (w) {
+        const float scale = 1.0f / sqrtf(wave_sum_f(a * a + b * b) / (float)HD + eps);
+        if (on) {
+            a = a * scale * w[lane];
+            b = b * scale * w[lane + HALF];
+        }
+    }
+    float theta = (float)(row % T);
+    for (int i = 0; i < lane && i < HALF; i++) theta *= theta_scale;
+    if (on) {
+        const float c = cosf(theta), s = sinf(theta);
+        x[lane] = a * c - b * s;
+        x[lane + HALF] = a * s + b * c;
+    }
+}
+
+// Attention on fp32 MFMAs.  Workgroup: 4 waves x 32 queries of one (sequence, head); the
+// K and V rows of 32 keys at a time are staged in LDS (row stride HD + 4 floats keeps a
+// wave's 32 row reads on distinct banks).  Per key block, each wave computes
+//   S^T[key][query] = sum_d K[key][d] Q[query][d]   (v_mfma_f32_32x32x2_f32, 2 dims a step,
+//                                                    A = K from LDS, B = Q^T from registers)
+// so every lane owns one query column: 16 scores of its half of the keys.  The online
+// softmax needs one cross-half exchange; the probabilities in those 16 registers are
+// exactly the A operands of
+//   O[query][d] += sum_key P[query][key] V[key][d]   (step i: keys 8(i/4) + i%4 and +4)
+// with B = V from LDS.  O's rows are queries 8(r/4) + 4 half + r%4 of register r, so the
+// per-query rescale factors are passed through a 32-float LDS slot per wave.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_mfma(const float *__restrict__ qkv, int64_t ld, float *__restrict__ out,
+                                                   int64_t ldo, int T, int nq, int nkv, float scale, int causal) {
+    constexpr int HALF = HD / 2, AKS = HD + 4, NT = HD / 32;
+    __shared__ __attribute__((aligned(16))) float Ks[32 * AKS];
+    __shared__ __attribute__((aligned(16))) float Vs[32 * AKS];
+    __shared__ __attribute__((aligned(16))) float rs[4][32];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
+    const int h = blockIdx.y, hk = h / (nq / nkv);
+    const int64_t rbase = (int64_t)blockIdx.z * T;  // first row of the sequence
+    const int q0 = blockIdx.x * 128 + wave * 32;    // this wave's first query
+    const int qi = q0 + l32;
+    const int64_t qcol = (int64_t)h * HD, kcol = (int64_t)nq * HD + (int64_t)hk * HD,
+                  vcol = (int64_t)(nq + nkv) * HD + (int64_t)hk * HD;
+
+    // Q^T operand: lane holds Q[qi][d] for d = s + HALF*half, s < HALF, times the scale
+    float qv[HALF];
+    {
+        const float *qp = qkv + (rbase + min(qi, T - 1)) * ld + qcol + HALF * half;
+#pragma unroll
+        for (int s = 0; s < HALF; s += 4) {
+            const float4 t = *(const float4 *)(qp + s);
+            qv[s] = t.x * scale, qv[s + 1] = t.y * scale, qv[s + 2] = t.z * scale, qv[s + 3] = t.w * scale;
+        }
+    }
+    v16f oacc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; j++) oacc[j] = (v16f){};
+    float m_run = -INFINITY, l_run = 0.f;
+    const int kend = causal ? min(T, (int)blockIdx.x * 128 + 128) : T;  // keys the workgroup needs
+    const int kend_w = q0 >= T ? 0 : causal ? min(T, q0 + 32) : T;      // keys this wave needs
+
+    for (int kb = 0; kb < kend; kb += 32) {
+        __syncthreads();  // the previous block's K/V are no longer read
+        for (int e = threadIdx.x; e < 32 * HD / 4; e += 256) {
+            const int r = e / (HD / 4), c4 = (e % (HD / 4)) * 4;
+            float4 kk = make_float4(0.f, 0.f, 0.f, 0.f), vv = kk;
+            if (kb + r < T) {
+                kk = *(const float4 *)(qkv + (rbase + kb + r) * ld + kcol + c4);
+                vv = *(const float4 *)(qkv + (rbase + kb + r) * ld + vcol + c4);
+            }
+            *(float4 *)&Ks[r * AKS + c4] = kk;
+            *(float4 *)&Vs[r * AKS + c4] = vv;
+        }
+        __syncthreads();
+        if (kb >= kend_w) continue;  // past this wave's causal range (wave-uniform)
+
+        v16f st = (v16f){};
+        const float *krow = &Ks[l32 * AKS + HALF * half];
+#pragma unroll
+        for (int s = 0; s < HALF; s += 4) {
+            const float4 k4 = *(const float4 *)(krow + s);
+            st = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.x, qv[s], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.y, qv[s + 1], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.z, qv[s + 2], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.w, qv[s + 3], st, 0, 0, 0);
+        }
+        float p[16], mblk = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int key = kb + 8 * (i / 4) + 4 * half + (i % 4);
+            p[i] = (key >= T || (causal && key > qi)) ? -INFINITY : st[i];
+            mblk = fmaxf(mblk, p[i]);
+        }
+        mblk = fmaxf(mblk, __shfl_xor(mblk, 32));
+        const float m_new = fmaxf(m_run, mblk);
+        const float alpha = expf(m_run - m_new);  // 0 on the first block
+        float lblk = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            p[i] = expf(p[i] - m_new);
+            lblk += p[i];
+        }
+        lblk += __shfl_xor(lblk, 32);
+        l_run = l_run * alpha + lblk;
+        m_run = m_new;
+
+        // rescale O's rows (queries 8(r/4) + 4 half + r%4) by their query's alpha
+        rs[wave][l32] = alpha;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // one wave writes and reads its slot
+        float al[16];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const float4 t = *(const float4 *)&rs[wave][8 * g + 4 * half];
+            al[4 * g] = t.x, al[4 * g + 1] = t.y, al[4 * g + 2] = t.z, al[4 * g + 3] = t.w;
+        }
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) oacc[j][r] *= al[r];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float *vrow = &Vs[(8 * (i / 4) + 4 * half + (i % 4)) * AKS + l32];
+#pragma unroll
+            for (int j = 0; j < NT; j++) oacc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(p[i], vrow[32 * j], oacc[j], 0, 0, 0);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot is rewritten next block
+    }
+
+    rs[wave][l32] = 1.0f / l_run;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    float inv[16];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const float4 t = *(const float4 *)&rs[wave][8 * g + 4 * half];
+        inv[4 * g] = t.x, inv[4 * g + 1] = t.y, inv[4 * g + 2] = t.z, inv[4 * g + 3] = t.w;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int q = q0 + 8 * (r / 4) + 4 * half + (r % 4);
+        if (q >= T) continue;
+        float *o = out + (rbase + q) * ldo + qcol + l32;
+#pragma unroll
+        for (int j = 0; j < NT; j++) o[32 * j] = oacc[j][r] * inv[r];
+    }
+}
+
+// One wave per sequence: the last token's row, RMS-normed with w, then L2-normalised.
+template <int V>
+__global__ __launch_bounds__(64) void k_last_rmsnorm_l2(const float *__restrict__ x, const float *__restrict__ w,
+                                                        float eps, float *__restrict__ out, int T, int H) {
+    const int b = blockIdx.x, lane = threadIdx.x;
+    const float *row = x + ((int64_t)b * T + T - 1) * H;
+    float v[V], ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int c = lane + 64 * i;
+        v[i] = c < H ? row[c] : 0.f;
+        ss += v[i] * v[i];
+    }
+    const float scale = 1.0f / sqrtf(wave_sum_f(ss) / (float)H + eps);
+    float s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int c = lane + 64 * i;
+        v[i] = c < H ? v[i] * scale * w[c] : 0.f;
+        s2 += v[i] * v[i];
+    }
+    const float inv = 1.0f / sqrtf(fmaxf(wave_sum_f(s2), 1e-12f));
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int c = lane + 64 * i;
+        if (c < H) out[(int64_t)b * H + c] = v[i] * inv;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+#define MQ_RMS_DISPATCH(KERNEL, GRID, BLOCK, ...)                                           \
+    do {                                                                                    \
+        const int need = (H + 63) / 64;                                                     \
+        if (need <= 4) hipLaunchKernelGGL((KERNEL<4>), GRID, BLOCK, 0, s, __VA_ARGS__);     \
+        else if (need <= 8) hipLaunchKernelGGL((KERNEL<8>), GRID, BLOCK, 0, s, __VA_ARGS__); \
+        else if (need <= 16) hipLaunchKernelGGL((KERNEL<16>), GRID, BLOCK, 0, s, __VA_ARGS__); \
+        else if (need <= 32) hipLaunchKernelGGL((KERNEL<32>), GRID, BLOCK, 0, s, __VA_ARGS__); \
+        else if (need <= 64) hipLaunchKernelGGL((KERNEL<64>), GRID, BLOCK, 0, s, __VA_ARGS__); \
+        else return hipErrorInvalidValue;                                                   \
+    } while (0)
+
+hipError_t launch_add_rmsnorm(const float *y, const float *res, const int32_t *ids, const float *tok, int n_vocab,
+                              const float *w, float eps, float *xout, float *hout, int64_t rows, int H, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    MQ_RMS_DISPATCH(k_add_rmsnorm, dim3((unsigned)((rows + 3) / 4)), dim3(256), y, res, ids, tok, w, eps, xout, hout,
+                    rows, H, n_vocab);
+    return hipGetLastError();
+}
+
+hipError_t launch_qk_norm_rope(float *qkv, int64_t ld, const float *qw, const float *kw, float eps, int nq, int nkv,
+                               int hd, int T, float theta_base, int64_t rows, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    const float theta_scale = powf(theta_base, -2.0f / (float)hd);
+    const dim3 g((unsigned)((rows * (nq + nkv) + 3) / 4)), b(256);
+    if (hd == 128) hipLaunchKernelGGL((k_qk_norm_rope<128>), g, b, 0, s, qkv, ld, qw, kw, eps, nq, nkv, T, theta_scale, rows);
+    else if (hd == 64) hipLaunchKernelGGL((k_qk_norm_rope<64>), g, b, 0, s, qkv, ld, qw, kw, eps, nq, nkv, T, theta_scale, rows);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_mfma(const float *qkv, int64_t ld, float *out, int64_t ldo, int B, int T, int nq, int nkv, int hd,
+                            float scale, int causal, hipStream_t s) {
+    if (B <= 0 || T <= 0) return hipSuccess;
+    if (nkv <= 0 || nq % nkv != 0 || ld % 4 != 0 || ((uintptr_t)qkv & 15) != 0) return hipErrorInvalidValue;
+    const dim3 g((unsigned)((T + 127) / 128), (unsigned)nq, (unsigned)B), b(256);
+    if (hd == 128) hipLaunchKernelGGL((k_attn_mfma<128>), g, b, 0, s, qkv, ld, out, ldo, T, nq, nkv, scale, causal);
+    else if (hd == 64) hipLaunchKernelGGL((k_attn_mfma<64>), g, b, 0, s, qkv, ld, out, ldo, T, nq, nkv, scale, causal);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_last_rmsnorm_l2(const float *x, const float *w, float eps, float *out, int B, int T, int H,
+                                  hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    MQ_RMS_DISPATCH(k_last_rmsnorm_l2, dim3((unsigned)B), dim3(64), x, w, eps, out, T, H);
+    return hipGetLastError();
+}
+#undef MQ_RMS_DISPATCH
+
+}  // namespace mq

@@ -1,0 +1,202 @@
+// mq_decoder_run.cpp -- native decoder-embedder runner on the quantized MUL_MAT path (mq_decoder.h).
+//
+// Per layer (pre-norm Qwen3 block, src/decoder_embed.cpp:718-814):
+//   Hn   = rms_norm(X) * attn_norm                  (fused with the previous residual ADD)
+//   qkv  = Hn . [Wq; Wk; Wv]^T                      one mul_mat over the concatenated rows
+//   q, k = rope(rms_norm_head(q|k) * q_norm|k_norm) in place
+//   A    = causal GQA attention(q, k, v)            fp32 MFMA
+//   X    = X + A . Wo^T;  Hn = rms_norm(X) * ffn_norm
+//   gu   = Hn . [Wgate; Wup]^T                      one mul_mat, gate and up side by side
+//   X    = X + (silu(gate) * up) . Wdown^T          the product formed by the quantizer
+// then the output RMS norm of the pooled rows and L2 normalisation.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "../../include/mq.h"
+#include "../../include/mq_decoder.h"
+#include "mq_internal.h"
+#include "mq_runner.h"
+
+namespace mq {
+hipError_t launch_add_rmsnorm(const float *y, const float *res, const int32_t *ids, const float *tok, int n_vocab,
+                              const float *w, float eps, float *xout, float *hout, int64_t rows, int H, hipStream_t s);
+hipError_t launch_qk_norm_rope(float *qkv, int64_t ld, const float *qw, const float *kw, float eps, int nq, int nkv,
+                               int hd, int T, float theta_base, int64_t rows, hipStream_t s);
+hipError_t launch_attn_mfma(const float *qkv, int64_t ld, float *out, int64_t ldo, int B, int T, int nq, int nkv, int hd,
+                            float scale, int causal, hipStream_t s);
+hipError_t launch_last_rmsnorm_l2(const float *x, const float *w, float eps, float *out, int B, int T, int H,
+                                  hipStream_t s);
+hipError_t launch_mean_pool_l2(const float *x, float *out, int B, int T, int H, hipStream_t s);  // mq_encoder.hip
+}  // namespace mq
+
+using namespace mq;
+
+namespace {
+struct DecLayer {
+    Linear qkv, o, gu, down;
+    DevBuf attn_norm, ffn_norm, q_norm, k_norm;
+    bool has_qn = false, has_kn = false;
+};
+}  // namespace
+
+struct mq_decoder {
+    mq_decoder_hparams hp{};
+    DevBuf tok, out_norm;
+    std::vector<DecLayer> layers;
+    DevBuf x, h, qkv, att, y, gu, ws;
+};
+
+extern "C" mq_decoder *mq_decoder_create(const mq_decoder_hparams *hp) {
+    if (!hp || hp->n_layer <= 0 || hp->n_embd <= 0 || hp->n_head <= 0 || hp->n_kv_head <= 0 ||
+        hp->n_head % hp->n_kv_head != 0 || hp->n_ff <= 0 || hp->n_vocab <= 0 || !(hp->rms_norm_eps > 0.f) ||
+        !(hp->rope_theta > 0.f) || (hp->pooling != 1 && hp->pooling != 2)) {
+        set_error(MQ_EINVAL, "bad decoder hyper-parameters");
+        return nullptr;
+    }
+    if (hp->head_dim != 64 && hp->head_dim != 128) {
+        set_error(MQ_EUNSUPPORTED, "head_dim %d (this runner takes 64 or 128)", hp->head_dim);
+        return nullptr;
+    }
+    if (hp->n_embd > 4096) {
+        set_error(MQ_EUNSUPPORTED, "n_embd %d > 4096", hp->n_embd);
+        return nullptr;
+    }
+    const int q_dim = hp->n_head * hp->head_dim;
+    if (!mq_supports(hp->wtype, hp->n_embd) || !mq_supports(hp->wtype, hp->n_ff) || !mq_supports(hp->wtype, q_dim)) {
+        set_error(MQ_EUNSUPPORTED, "weight type %d does not tile k = %d / %d / %d", hp->wtype, hp->n_embd, hp->n_ff,
+                  q_dim);
+        return nullptr;
+    }
+    mq_decoder *m = new mq_decoder();
+    m->hp = *hp;
+    m->layers.resize(hp->n_layer);
+    return m;
+}
+
+extern "C" void mq_decoder_free(mq_decoder *m) { delete m; }
+
+extern "C" int mq_decoder_set_embeddings(mq_decoder *m, const float *tok, const float *out_norm) {
+    if (!m || !tok || !out_norm) return set_error(MQ_EINVAL, "NULL embedding table / output norm");
+    const size_t H = (size_t)m->hp.n_embd * sizeof(float);
+    int rc;
+    if ((rc = upload(m->tok, tok, H * m->hp.n_vocab))) return rc;
+    return upload(m->out_norm, out_norm, H);
+}
+
+extern "C" int mq_decoder_set_layer(mq_decoder *m, int il, const void *wq, const void *wk, const void *wv,
+                                    const void *wo, const void *wgate, const void *wup, const void *wdown,
+                                    const float *attn_norm, const float *ffn_norm, const float *q_norm,
+                                    const float *k_norm) {
+    if (!m || il < 0 || il >= m->hp.n_layer) return set_error(MQ_EINVAL, "bad layer index %d", il);
+    if (!attn_norm || !ffn_norm) return set_error(MQ_EINVAL, "NULL norm weight");
+    DecLayer &L = m->layers[il];
+    const mq_decoder_hparams &hp = m->hp;
+    const int t = hp.wtype;
+    const int64_t H = hp.n_embd, F = hp.n_ff, qd = (int64_t)hp.n_head * hp.head_dim,
+                  kvd = (int64_t)hp.n_kv_head * hp.head_dim;
+    const size_t f4 = sizeof(float);
+    int rc;
+    if ((rc = upload_linear(L.qkv, t, {wq, wk, wv}, {qd, kvd, kvd}, H))) return rc;
+    if ((rc = upload_linear(L.o, t, {wo}, {H}, qd))) return rc;
+    if ((rc = upload_linear(L.gu, t, {wgate, wup}, {F, F}, H))) return rc;
+    if ((rc = upload_linear(L.down, t, {wdown}, {H}, F))) return rc;
+    if ((rc = upload(L.attn_norm, attn_norm, H * f4))) return rc;
+    if ((rc = upload(L.ffn_norm, ffn_norm, H * f4))) return rc;
+    L.has_qn = q_norm != nullptr;
+    L.has_kn = k_norm != nullptr;
+    if (q_norm && (rc = upload(L.q_norm, q_norm, hp.head_dim * f4))) return rc;
+    if (k_norm && (rc = upload(L.k_norm, k_norm, hp.head_dim * f4))) return rc;
+    return MQ_OK;
+}
+
+extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T, float *out, float *hidden,
+                                 void *stream) {
+    if (!m || !ids || !out || B <= 0 || T <= 0) return set_error(MQ_EINVAL, "bad encode arguments");
+    const mq_decoder_hparams &hp = m->hp;
+    for (const DecLayer &L : m->layers)
+        if (!L.qkv.img.p) return set_error(MQ_EINVAL, "layer weights not set");
+    if (!m->tok.p) return set_error(MQ_EINVAL, "embeddings not set");
+    const int64_t rows = (int64_t)B * T, H = hp.n_embd, F = hp.n_ff;
+    const int hd = hp.head_dim, nq = hp.n_head, nkv = hp.n_kv_head;
+    const int64_t qd = (int64_t)nq * hd, ldqkv = qd + 2 * (int64_t)nkv * hd;
+    const int t = hp.wtype;
+    const size_t f4 = sizeof(float);
+    const size_t wsb = std::max({mq_workspace_bytes(t, rows, H), mq_workspace_bytes(t, rows, qd),
+                                 mq_workspace_bytes(t, rows, F)});
+    if (!m->x.ensure(rows * H * f4) || !m->h.ensure(rows * H * f4) || !m->qkv.ensure(rows * ldqkv * f4) ||
+        !m->att.ensure(rows * qd * f4) || !m->y.ensure(rows * H * f4) || !m->gu.ensure(rows * 2 * F * f4) ||
+        !m->ws.ensure(wsb))
+        return set_error(MQ_ENOMEM, "activation buffers for %lld rows", (long long)rows);
+    hipStream_t s = (hipStream_t)stream;
+    const float eps = hp.rms_norm_eps;
+    float *X = hidden ? hidden : m->x.f();
+    float *Hn = m->h.f();
+    int rc;
+    auto mm = [&](const Linear &L, const float *in, int64_t ldin, float *y) {
+        return mq_mul_mat(t, L.img.p, L.n, L.k, in, ldin, rows, y, L.n, m->ws.p, m->ws.bytes, s);
+    };
+    // X = token_embd[ids]; Hn = rms_norm(X) * attn_norm[0]
+    if ((rc = hip_rc(launch_add_rmsnorm(nullptr, nullptr, ids, m->tok.f(), hp.n_vocab, m->layers[0].attn_norm.f(), eps, X, Hn, rows,
+                                        (int)H, s),
+                     "embedding")))
+        return rc;
+    for (size_t il = 0; il < m->layers.size(); il++) {
+        const DecLayer &L = m->layers[il];
+        if ((rc = mm(L.qkv, Hn, H, m->qkv.f()))) return rc;
+        if ((rc = hip_rc(launch_qk_norm_rope(m->qkv.f(), ldqkv, L.has_qn ? L.q_norm.f() : nullptr,
+                                             L.has_kn ? L.k_norm.f() : nullptr, eps, nq, nkv, hd, T, hp.rope_theta,
+                                             rows, s),
+                         "q/k norm + rope")))
+            return rc;
+        if ((rc = hip_rc(launch_attn_mfma(m->qkv.f(), ldqkv, m->att.f(), qd, B, T, nq, nkv, hd, 1.0f / sqrtf((float)hd),
+                                          hp.causal, s),
+                         "attention")))
+            return rc;
+        if ((rc = mm(L.o, m->att.f(), qd, m->y.f()))) return rc;
+        // X += A Wo^T; Hn = rms_norm(X) * ffn_norm
+        if ((rc = hip_rc(launch_add_rmsnorm(m->y.f(), X, nullptr, nullptr, 0, L.ffn_norm.f(), eps, X, Hn, rows, (int)H, s),
+                         "attention residual")))
+            return rc;
+        if ((rc = mm(L.gu, Hn, H, m->gu.f()))) return rc;
+        // down projection of silu(gate) * up, the product formed inside the quantizer
+        if ((rc = mq_quantize_act_ex(t, m->gu.f(), 2 * F, rows, F, nullptr, MQ_PRE_SILU_MUL, m->ws.p, m->ws.bytes,
+                                     MQ_PATH_AUTO, s)))
+            return rc;
+        if ((rc = mq_mul_mat_q(t, L.down.img.p, L.down.n, L.down.k, m->ws.p, rows, m->y.f(), H, MQ_PATH_AUTO, s)))
+            return rc;
+        // X += FFN; Hn = rms_norm(X) * (next layer's attn_norm, or the output norm)
+        const float *wn = (il + 1 < m->layers.size()) ? m->layers[il + 1].attn_norm.f() : m->out_norm.f();
+        if ((rc = hip_rc(launch_add_rmsnorm(m->y.f(), X, nullptr, nullptr, 0, wn, eps, X, Hn, rows, (int)H, s),
+                         "ffn residual")))
+            return rc;
+    }
+    // mean pooling averages the output-normed rows (Hn); last-token pooling norms the last row
+    if (hp.pooling == 1) return hip_rc(launch_mean_pool_l2(Hn, out, B, T, (int)H, s), "pooling");
+    return hip_rc(launch_last_rmsnorm_l2(X, m->out_norm.f(), eps, out, B, T, (int)H, s), "pooling");
+}
+
+extern "C" int mq_qk_norm_rope(float *qkv, int64_t ld, const float *q_norm, const float *k_norm, float eps, int n_head,
+                               int n_kv_head, int head_dim, int T, float theta, int64_t rows, void *stream) {
+    if (!qkv || n_head <= 0 || n_kv_head <= 0 || T <= 0 || rows < 0 || !(theta > 0.f) ||
+        ld < (int64_t)(n_head + 2 * n_kv_head) * head_dim)
+        return set_error(MQ_EINVAL, "mq_qk_norm_rope: bad arguments");
+    if (head_dim != 64 && head_dim != 128) return set_error(MQ_EUNSUPPORTED, "head_dim %d (64 or 128)", head_dim);
+    return hip_rc(launch_qk_norm_rope(qkv, ld, q_norm, k_norm, eps, n_head, n_kv_head, head_dim, T, theta, rows,
+                                      (hipStream_t)stream),
+                  "q/k norm + rope");
+}
+
+extern "C" int mq_attention(const float *qkv, int64_t ld, float *out, int64_t ldo, int B, int T, int n_head,
+                            int n_kv_head, int head_dim, float scale, int causal, void *stream) {
+    if (!qkv || !out || B <= 0 || T <= 0 || n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head != 0 ||
+        ld % 4 != 0 || ((uintptr_t)qkv & 15) != 0 || ld < (int64_t)(n_head + 2 * n_kv_head) * head_dim ||
+        ldo < (int64_t)n_head * head_dim)
+        return set_error(MQ_EINVAL, "mq_attention: bad arguments");
+    if (head_dim != 64 && head_dim != 128) return set_error(MQ_EUNSUPPORTED, "head_dim %d (64 or 128)", head_dim);
+    return hip_rc(launch_attn_mfma(qkv, ld, out, ldo, B, T, n_head, n_kv_head, head_dim, scale, causal,
+                                   (hipStream_t)stream),
+                  "attention");
+}

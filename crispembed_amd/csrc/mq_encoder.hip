@@ -11,25 +11,9 @@
 // Each group is one kernel here (fused): the data stays in registers/LDS between ops.
 // All arithmetic is fp32; NORM follows ggml's two-pass mean / variance form.
 #include "mq_internal.h"
+#include "mq_wave.h"
 
 namespace mq {
-
-// Wave reductions on the DPP path: xor 1, xor 2 (quad_perm), i <-> 7-i, i <-> 15-i inside
-// each 16-lane row, then the four row results via readlane (wave-uniform result).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float lane_f(float v, int l) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
-}
-__device__ __forceinline__ float wave_sum_f(float v) {
-    v += dpp_f<0xB1>(v);
-    v += dpp_f<0x4E>(v);
-    v += dpp_f<0x141>(v);
-    v += dpp_f<0x140>(v);
-    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
-}
 
 constexpr int LN_MAXV = 16;  // values per lane: rows up to 1024 wide
 
@@ -63,13 +47,14 @@ __global__ __launch_bounds__(256) void k_embed_ln(const int32_t *__restrict__ id
                                                   const float *__restrict__ word, const float *__restrict__ pos,
                                                   const float *__restrict__ type, const float *__restrict__ lw,
                                                   const float *__restrict__ lb, float eps, float *__restrict__ out,
-                                                  int64_t rows, int T, int H) {
+                                                  int64_t rows, int T, int H, int n_vocab, int n_type) {
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
-    const int64_t id = ids[row];
+    // ids outside the tables are clamped: a bad id reads a valid row, never out of bounds
+    const int64_t id = min(max(ids[row], 0), n_vocab - 1);
     const int p = (int)(row % T);
-    const int64_t ty = types ? types[row] : 0;
+    const int64_t ty = types ? min(max(types[row], 0), max(n_type, 1) - 1) : 0;
     float v[V];
 #pragma unroll
     for (int i = 0; i < V; i++) {
@@ -303,10 +288,10 @@ size_t attention_lds_bytes(int T, int hd, int ks) {
 
 hipError_t launch_embed_ln(const int32_t *ids, const int32_t *types, const float *word, const float *pos,
                            const float *type, const float *lw, const float *lb, float eps, float *out, int64_t rows,
-                           int T, int H, hipStream_t s) {
-    if (H > 64 * LN_MAXV || T <= 0) return hipErrorInvalidValue;
+                           int T, int H, int n_vocab, int n_type, hipStream_t s) {
+    if (H > 64 * LN_MAXV || T <= 0 || n_vocab <= 0) return hipErrorInvalidValue;
     if (rows == 0) return hipSuccess;
-    MQ_LN_DISPATCH(k_embed_ln, ids, types, word, pos, type, lw, lb, eps, out, rows, T, H);
+    MQ_LN_DISPATCH(k_embed_ln, ids, types, word, pos, type, lw, lb, eps, out, rows, T, H, n_vocab, n_type);
     return hipGetLastError();
 }
 

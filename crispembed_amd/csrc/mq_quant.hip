@@ -32,17 +32,26 @@ __device__ __forceinline__ float4 load4(const float *p) {
     return make_float4(p[0], p[1], p[2], p[3]);
 }
 
-// Prologue applied to an activation before it is quantized (a fused ADD and GELU_ERF of the
-// graph): v = x + bias[col] (bias may be NULL), then for MQ_PRE_GELU_ERF
-// v = 0.5 v (1 + erf(v / sqrt 2)) (ggml_gelu_erf), all in fp32.  `pre` and `bias` are
-// wave-uniform: the branch costs nothing when there is no prologue.
-__device__ __forceinline__ float4 pre_apply(float4 v, int pre, const float *bias, int64_t col) {
+// Prologue applied to an activation before it is quantized (the graph's elementwise
+// producers of the MUL_MAT input, fused): v = x + bias[col] (bias may be NULL), then
+//   MQ_PRE_GELU_ERF : v = 0.5 v (1 + erf(v / sqrt 2))            (ggml_gelu_erf)
+//   MQ_PRE_SILU_MUL : v = silu(v) * u, u the value k columns later (ggml_silu, ggml_mul:
+//                     the row holds the gate projection, then the up projection)
+// all in fp32.  `pre` and `bias` are uniform: the branches cost nothing without a prologue.
+template <bool VEC4>
+__device__ __forceinline__ float4 pre_load(const float *p, int pre, const float *bias, int64_t col, int64_t k) {
+    const float4 v = load4<VEC4>(p);
     if (pre == MQ_PRE_NONE && bias == nullptr) return v;
-    float r[4] = {v.x, v.y, v.z, v.w};
+    float r[4] = {v.x, v.y, v.z, v.w}, u[4] = {1.f, 1.f, 1.f, 1.f};
+    if (pre == MQ_PRE_SILU_MUL) {
+        const float4 w = load4<VEC4>(p + k);
+        u[0] = w.x, u[1] = w.y, u[2] = w.z, u[3] = w.w;
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         if (bias) r[i] = r[i] + bias[col + i];
         if (pre == MQ_PRE_GELU_ERF) r[i] = 0.5f * r[i] * (1.0f + erff(r[i] * 0.70710678118654752f));
+        else if (pre == MQ_PRE_SILU_MUL) r[i] = (r[i] / (1.0f + expf(-r[i]))) * u[i];
     }
     return make_float4(r[0], r[1], r[2], r[3]);
 }
@@ -71,7 +80,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__
     if (blk >= rows * nbx) return;  // 8-lane groups leave together
     const int64_t row = blk / nbx, b = blk - row * nbx;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (row < m && b < nbr) v = pre_apply(load4<VEC4>(x + row * ldx + b * QK8_0 + sub * 4), pre, bias, b * QK8_0 + sub * 4);
+    if (row < m && b < nbr) v = pre_load<VEC4>(x + row * ldx + b * QK8_0 + sub * 4, pre, bias, b * QK8_0 + sub * 4, k);
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
     amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
@@ -120,7 +129,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const float *__restrict__
     if (blk >= rows * nbr) return;  // whole waves leave together
     const int64_t row = blk / nbr, b = blk - row * nbr;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (row < m) v = pre_apply(load4<VEC4>(x + row * ldx + b * QK_K + lane * 4), pre, bias, b * QK_K + lane * 4);
+    if (row < m) v = pre_load<VEC4>(x + row * ldx + b * QK_K + lane * 4, pre, bias, b * QK_K + lane * 4, k);
     const float vals[4] = {v.x, v.y, v.z, v.w};
     float amax = 0.0f, mx = 0.0f;
     int idx = 0x7fffffff;
@@ -189,7 +198,7 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= m * q4) return;
     const int64_t row = gid / q4, c = gid - row * q4;
-    const float4 v = pre_apply(load4<VEC4>(x + row * ldx + c * 4), pre, bias, c * 4);
+    const float4 v = pre_load<VEC4>(x + row * ldx + c * 4, pre, bias, c * 4, k);
     uint16_t *o = y + row * k + c * 4;
     o[0] = f32_to_f16_bits(v.x);
     o[1] = f32_to_f16_bits(v.y);
@@ -278,7 +287,7 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
     for (int it = 0; it < NIT; it++) {
         const int64_t row = rt * 32 + wave * 8 + it * RPI + rsub;
         vin[it] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (row < m && kv < k) vin[it] = pre_apply(load4<VEC4>(x + row * ldx + kv), pre, bias, kv);
+        if (row < m && kv < k) vin[it] = pre_load<VEC4>(x + row * ldx + kv, pre, bias, kv, k);
     }
 #pragma unroll
     for (int it = 0; it < NIT; it++) {

@@ -1,0 +1,24 @@
+// mq_wave.h -- wave64 reductions shared by the fp32 runner kernels (gfx950).
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace mq {
+
+// DPP path: xor 1, xor 2 (quad_perm), i <-> 7-i, i <-> 15-i inside each 16-lane row, then
+// the four row results via readlane (the result is wave-uniform).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+
+}  // namespace mq

@@ -8,7 +8,7 @@ LIB_PATH = os.path.join(HERE, "libmq.so")
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K = 0, 1, 8, 12, 14, 15
 Q8_0_X86, Q8_0_NEON, Q8_0_REF = 0, 1, 2
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
-PRE_NONE, PRE_GELU_ERF = 0, 1
+PRE_NONE, PRE_GELU_ERF, PRE_SILU_MUL = 0, 1, 2
 
 TYPE_NAMES = {TYPE_F32: "f32", TYPE_F16: "f16", TYPE_Q8_0: "q8_0", TYPE_Q4_K: "q4_K",
               TYPE_Q6_K: "q6_K", TYPE_Q8_K: "q8_K"}
@@ -60,7 +60,24 @@ _SIGS = {
     "mq_bert_set_embeddings": (_c_int, [_c_vp] * 6),
     "mq_bert_set_layer": (_c_int, [_c_vp, _c_int] + [_c_vp] * 16),
     "mq_bert_encode": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp]),
+    # include/mq_decoder.h
+    "mq_decoder_create": (_c_vp, [_c_vp]),
+    "mq_decoder_free": (None, [_c_vp]),
+    "mq_decoder_set_embeddings": (_c_int, [_c_vp] * 3),
+    "mq_decoder_set_layer": (_c_int, [_c_vp, _c_int] + [_c_vp] * 11),
+    "mq_decoder_encode": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp]),
+    "mq_qk_norm_rope": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, ctypes.c_float, _c_int, _c_int, _c_int, _c_int,
+                                 ctypes.c_float, _c_i64, _c_vp]),
+    "mq_attention": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.c_float,
+                              _c_int, _c_vp]),
 }
+
+
+class DecoderHparams(ctypes.Structure):
+    """mq_decoder_hparams (include/mq_decoder.h)."""
+    _fields_ = [("n_layer", _c_int), ("n_embd", _c_int), ("n_head", _c_int), ("n_kv_head", _c_int),
+                ("head_dim", _c_int), ("n_ff", _c_int), ("n_vocab", _c_int), ("rms_norm_eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_float), ("causal", _c_int), ("pooling", _c_int), ("wtype", _c_int)]
 
 
 class BertHparams(ctypes.Structure):

@@ -60,6 +60,7 @@ extern "C" {
 /* Elementwise prologue of mq_quantize_act_ex, applied to X before it is quantized. */
 #define MQ_PRE_NONE 0     /* x (+ bias) */
 #define MQ_PRE_GELU_ERF 1 /* gelu_erf(x + bias) */
+#define MQ_PRE_SILU_MUL 2 /* silu(g) * u: row = [g (k values) | u (k values)], ldx >= 2k */
 
 /* ---- library / device ---- */
 
@@ -141,10 +142,13 @@ int mq_mul_mat_q(int type, const void *w_image, int64_t n, int64_t k, const void
 
 /* mq_quantize_act with the graph's elementwise producer folded in: it quantizes
  * op(X + bias) where bias is an fp32 [k] row added to every row of X (NULL: none) and
- * op is MQ_PRE_NONE or MQ_PRE_GELU_ERF.  The value quantized is the fp32 tensor the
- * ggml graph materialises between those nodes and the MUL_MAT: the ADD of the FFN-up
- * bias and ggml_gelu_erf feeding the FFN-down projection (src/crispembed.cpp:1410-1416,
- * 0.5 v (1 + erf(v / sqrt 2)) in fp32). */
+ * op is one of MQ_PRE_*.  The value quantized is the fp32 tensor the ggml graph
+ * materialises between those nodes and the MUL_MAT:
+ *   MQ_PRE_GELU_ERF: the ADD of the FFN-up bias and ggml_gelu_erf feeding the encoder's
+ *     FFN-down projection (src/crispembed.cpp:1410-1416), 0.5 v (1 + erf(v / sqrt 2));
+ *   MQ_PRE_SILU_MUL: ggml_silu(gate) * up feeding the decoder's FFN-down projection
+ *     (src/decoder_embed.cpp:793-802), v / (1 + exp(-v)) * u, with each row of x holding
+ *     the gate projection (k values) followed by the up projection (k values). */
 int mq_quantize_act_ex(int type, const float *x, int64_t ldx, int64_t m, int64_t k, const float *bias, int op,
                        void *workspace, size_t workspace_bytes, int path, void *stream);
 
