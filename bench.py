@@ -13,7 +13,7 @@ dense MFMA peak (5.0 POP/s).
 cpu_baseline = the restated ggml-cpu mul_mat (AVX2 integer dots, threads) on a
 bounded sample of token rows of the same workload, on the host cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras] [--only q8_0|e2e|decode]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras] [--only q8_0|e2e|qwen3|decode]
 """
 import argparse
 import ctypes
@@ -299,6 +299,35 @@ def bench_minilm_e2e(torch, L, mq):
             "linear_tops": round(lin_ops / (us * 1e-6) / 1e12, 1)}
 
 
+def bench_qwen3_e2e(torch, L, mq):
+    """End-to-end Qwen3-Embedding-0.6B-shaped decoder embedder (28 layers, H 1024, 16 query /
+    8 key-value heads of 128, SwiGLU FFN 3072, RMSNorm eps 1e-6, NEOX RoPE theta 1e6, causal,
+    vocab 151643, Q4_K linears, random init), 16 sequences x 512 tokens, last-token pooling + L2.
+    One random layer's Q4_K weights are uploaded into all 28 layers (separate device copies)."""
+    import numpy as np
+    from crispembed_amd import decoder, synth
+    hp = dict(decoder.QWEN3_EMBED_0_6B)
+    B, T = 16, 512
+    one = decoder.synthetic_weights(dict(hp, n_layer=1, n_vocab=1), mq.TYPE_Q4_K, name="qwen3")
+    tok = np.random.default_rng(20260101).standard_normal((hp["n_vocab"], hp["n_embd"]), dtype=np.float32)
+    tok *= 0.02
+    W = {"tok": tok, "out_norm": one["out_norm"], "layers": one["layers"] * hp["n_layer"]}
+    dec = decoder.DecoderEmbedder(hp, mq.TYPE_Q4_K, W)
+    del tok, W
+    ids = torch.from_numpy(synth.integers(f"qwen3/ids_{B}x{T}", (B * T,), 0, hp["n_vocab"] - 1)).cuda()
+    out = torch.empty((B, hp["n_embd"]), dtype=torch.float32, device="cuda")
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    run = lambda: dec.encode(ids.data_ptr(), B, T, out.data_ptr(), s)  # noqa: E731
+    run()
+    us = _timed(torch, run, 5)
+    H, F, nl, M = hp["n_embd"], hp["n_ff"], hp["n_layer"], B * T
+    qd, kvd = hp["n_head"] * hp["head_dim"], hp["n_kv_head"] * hp["head_dim"]
+    lin_ops = 2.0 * M * nl * (H * (qd + 2 * kvd) + qd * H + 3 * H * F)
+    return {"workload": "Qwen3-Embedding-0.6B shape, Q4_K linears, 16 seq x 512 tokens, causal, last-token pool + L2",
+            "batch_ms": round(us / 1e3, 3), "embeddings_per_s": round(B / (us * 1e-6), 1),
+            "linear_tops": round(lin_ops / (us * 1e-6) / 1e12, 1)}
+
+
 def cpu_baseline_q4k(args, x_up, x_dn, q_up, q_dn):
     """CPU baseline: the restated ggml-cpu mul_mat (Q8_K activation quantization, AVX2 integer
     block dots, fp32 scale accumulation, output tiles over threads) on a bounded sample of the
@@ -346,7 +375,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="skip the Q8_0 and GEMV side measurements")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--gemm-cfg", default=None, help="MQ_GEMM_CFG tile configuration (1 or 3)")
-    ap.add_argument("--only", choices=["q8_0", "e2e", "decode"], default=None,
+    ap.add_argument("--only", choices=["q8_0", "e2e", "qwen3", "decode"], default=None,
                     help="run one side measurement alone (for per-workload profiles) and print its JSON")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 10 device copies of 256 MiB (reference kernel for rocprof byte counters)")
@@ -373,6 +402,7 @@ def main():
     if args.only:
         fn = {"q8_0": lambda: bench_q8_0_minilm(torch, L, mq, synth),
               "e2e": lambda: bench_minilm_e2e(torch, L, mq),
+              "qwen3": lambda: bench_qwen3_e2e(torch, L, mq),
               "decode": lambda: bench_decode(torch, L, mq, synth)}[args.only]
         print(json.dumps({"only": args.only, "result": fn()}), flush=True)
         return
@@ -383,6 +413,7 @@ def main():
     if not args.no_extras:
         extras = {"q8_0_minilm_ffn_up": bench_q8_0_minilm(torch, L, mq, synth),
                   "minilm_l6_e2e": bench_minilm_e2e(torch, L, mq),
+                  "qwen3_0_6b_e2e": bench_qwen3_e2e(torch, L, mq),
                   "decode_gemv": bench_decode(torch, L, mq, synth)}
     cpu = None
     if not args.no_cpu:

@@ -57,15 +57,25 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(const float *y, const float
     }
 }
 
+// RoPE angle table for positions 0..T-1: cs[p][i] = (cos, sin) of p * theta_scale^i, the
+// angle built by the same repeated fp32 multiplication as ggml's rope cache.
+__global__ __launch_bounds__(256) void k_rope_table(float2 *__restrict__ cs, int T, int half, float theta_scale) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T * half) return;
+    const int p = t / half, i = t - p * half;
+    float theta = (float)p;
+    for (int j = 0; j < i; j++) theta *= theta_scale;
+    cs[t] = make_float2(cosf(theta), sinf(theta));
+}
+
 // One wave per (row, head) of Q and K inside the fused projection output qkv[rows][ld]
 // (Q heads at columns h*HD for h < nq, K heads right after them).  Lane l < HD/2 holds the
 // NEOX pair (l, l + HD/2): per-head RMS norm (when the weight is given), then the rotation
-// by theta = pos * theta_scale^l, the angle built by the same repeated multiplication as
-// ggml's rope cache.
+// by the table angle of position row % T.
 template <int HD>
 __global__ __launch_bounds__(256) void k_qk_norm_rope(float *qkv, int64_t ld, const float *__restrict__ qw,
                                                       const float *__restrict__ kw, float eps, int nq, int nkv, int T,
-                                                      float theta_scale, int64_t rows) {
+                                                      const float2 *__restrict__ cs, int64_t rows) {
     constexpr int HALF = HD / 2;
     const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -84,12 +94,10 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(float *qkv, int64_t ld, co
             b = b * scale * w[lane + HALF];
         }
     }
-    float theta = (float)(row % T);
-    for (int i = 0; i < lane && i < HALF; i++) theta *= theta_scale;
     if (on) {
-        const float c = cosf(theta), s = sinf(theta);
-        x[lane] = a * c - b * s;
-        x[lane + HALF] = a * s + b * c;
+        const float2 r = cs[(row % T) * HALF + lane];
+        x[lane] = a * r.x - b * r.y;
+        x[lane + HALF] = a * r.y + b * r.x;
     }
 }
 
@@ -272,14 +280,17 @@ hipError_t launch_add_rmsnorm(const float *y, const float *res, const int32_t *i
     return hipGetLastError();
 }
 
+// cs: device scratch of T * hd/2 float2 for the angle table
 hipError_t launch_qk_norm_rope(float *qkv, int64_t ld, const float *qw, const float *kw, float eps, int nq, int nkv,
-                               int hd, int T, float theta_base, int64_t rows, hipStream_t s) {
+                               int hd, int T, float theta_base, int64_t rows, float2 *cs, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
+    if (hd != 64 && hd != 128) return hipErrorInvalidValue;
     const float theta_scale = powf(theta_base, -2.0f / (float)hd);
+    hipLaunchKernelGGL(k_rope_table, dim3((unsigned)((T * (hd / 2) + 255) / 256)), dim3(256), 0, s, cs, T, hd / 2,
+                       theta_scale);
     const dim3 g((unsigned)((rows * (nq + nkv) + 3) / 4)), b(256);
-    if (hd == 128) hipLaunchKernelGGL((k_qk_norm_rope<128>), g, b, 0, s, qkv, ld, qw, kw, eps, nq, nkv, T, theta_scale, rows);
-    else if (hd == 64) hipLaunchKernelGGL((k_qk_norm_rope<64>), g, b, 0, s, qkv, ld, qw, kw, eps, nq, nkv, T, theta_scale, rows);
-    else return hipErrorInvalidValue;
+    if (hd == 128) hipLaunchKernelGGL((k_qk_norm_rope<128>), g, b, 0, s, qkv, ld, qw, kw, eps, nq, nkv, T, cs, rows);
+    else hipLaunchKernelGGL((k_qk_norm_rope<64>), g, b, 0, s, qkv, ld, qw, kw, eps, nq, nkv, T, cs, rows);
     return hipGetLastError();
 }
 

@@ -13,6 +13,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "../../include/mq.h"
@@ -24,7 +25,7 @@ namespace mq {
 hipError_t launch_add_rmsnorm(const float *y, const float *res, const int32_t *ids, const float *tok, int n_vocab,
                               const float *w, float eps, float *xout, float *hout, int64_t rows, int H, hipStream_t s);
 hipError_t launch_qk_norm_rope(float *qkv, int64_t ld, const float *qw, const float *kw, float eps, int nq, int nkv,
-                               int hd, int T, float theta_base, int64_t rows, hipStream_t s);
+                               int hd, int T, float theta_base, int64_t rows, float2 *cs, hipStream_t s);
 hipError_t launch_attn_mfma(const float *qkv, int64_t ld, float *out, int64_t ldo, int B, int T, int nq, int nkv, int hd,
                             float scale, int causal, hipStream_t s);
 hipError_t launch_last_rmsnorm_l2(const float *x, const float *w, float eps, float *out, int B, int T, int H,
@@ -46,7 +47,7 @@ struct mq_decoder {
     mq_decoder_hparams hp{};
     DevBuf tok, out_norm;
     std::vector<DecLayer> layers;
-    DevBuf x, h, qkv, att, y, gu, ws;
+    DevBuf x, h, qkv, att, y, gu, ws, rope;
 };
 
 extern "C" mq_decoder *mq_decoder_create(const mq_decoder_hparams *hp) {
@@ -128,7 +129,7 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
                                  mq_workspace_bytes(t, rows, F)});
     if (!m->x.ensure(rows * H * f4) || !m->h.ensure(rows * H * f4) || !m->qkv.ensure(rows * ldqkv * f4) ||
         !m->att.ensure(rows * qd * f4) || !m->y.ensure(rows * H * f4) || !m->gu.ensure(rows * 2 * F * f4) ||
-        !m->ws.ensure(wsb))
+        !m->ws.ensure(wsb) || !m->rope.ensure((size_t)T * (hd / 2) * sizeof(float2)))
         return set_error(MQ_ENOMEM, "activation buffers for %lld rows", (long long)rows);
     hipStream_t s = (hipStream_t)stream;
     const float eps = hp.rms_norm_eps;
@@ -148,7 +149,7 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
         if ((rc = mm(L.qkv, Hn, H, m->qkv.f()))) return rc;
         if ((rc = hip_rc(launch_qk_norm_rope(m->qkv.f(), ldqkv, L.has_qn ? L.q_norm.f() : nullptr,
                                              L.has_kn ? L.k_norm.f() : nullptr, eps, nq, nkv, hd, T, hp.rope_theta,
-                                             rows, s),
+                                             rows, (float2 *)m->rope.p, s),
                          "q/k norm + rope")))
             return rc;
         if ((rc = hip_rc(launch_attn_mfma(m->qkv.f(), ldqkv, m->att.f(), qd, B, T, nq, nkv, hd, 1.0f / sqrtf((float)hd),
@@ -184,8 +185,20 @@ extern "C" int mq_qk_norm_rope(float *qkv, int64_t ld, const float *q_norm, cons
         ld < (int64_t)(n_head + 2 * n_kv_head) * head_dim)
         return set_error(MQ_EINVAL, "mq_qk_norm_rope: bad arguments");
     if (head_dim != 64 && head_dim != 128) return set_error(MQ_EUNSUPPORTED, "head_dim %d (64 or 128)", head_dim);
+    // the angle table lives in a per-process buffer that only grows; the caller's stream is
+    // synchronised before it is replaced, and calls that overlap on two streams must not
+    // use different T or head_dim
+    // (never freed: it may outlive the HIP runtime at process exit)
+    static std::mutex mu;
+    static DevBuf *table = new DevBuf();
+    std::lock_guard<std::mutex> lk(mu);
+    const size_t need = (size_t)T * (head_dim / 2) * sizeof(float2);
+    if (need > table->bytes) {
+        if (hipDeviceSynchronize() != hipSuccess) return set_error(MQ_EHIP, "hipDeviceSynchronize failed");
+        if (!table->ensure(need)) return set_error(MQ_ENOMEM, "hipMalloc(%zu) failed", need);
+    }
     return hip_rc(launch_qk_norm_rope(qkv, ld, q_norm, k_norm, eps, n_head, n_kv_head, head_dim, T, theta, rows,
-                                      (hipStream_t)stream),
+                                      (float2 *)table->p, (hipStream_t)stream),
                   "q/k norm + rope");
 }
 
