@@ -11,7 +11,8 @@
 //   FFN         silu(gate) * up -- applied by the FFN-down activation quantizer
 //   pooling     output RMS_NORM of the last token (or of every token, then the mean), L2
 //               normalised with sqrtf(max(sum x^2, 1e-12)) (src/decoder_embed.cpp:1044-1100)
-// Arithmetic is fp32 throughout; the attention runs its products on fp32 MFMAs.
+// Arithmetic is fp32 throughout; the attention's products run on fp16 MFMAs over split
+// (hi + lo) operands, which keeps fp32 accuracy.
 #include "mq_internal.h"
 #include "mq_wave.h"
 
@@ -101,23 +102,57 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(float *qkv, int64_t ld, co
     }
 }
 
-// Attention on fp32 MFMAs.  Workgroup: 4 waves x 32 queries of one (sequence, head); the
-// K and V rows of 32 keys at a time are staged in LDS (row stride HD + 4 floats keeps a
-// wave's 32 row reads on distinct banks).  Per key block, each wave computes
-//   S^T[key][query] = sum_d K[key][d] Q[query][d]   (v_mfma_f32_32x32x2_f32, 2 dims a step,
-//                                                    A = K from LDS, B = Q^T from registers)
-// so every lane owns one query column: 16 scores of its half of the keys.  The online
-// softmax needs one cross-half exchange; the probabilities in those 16 registers are
-// exactly the A operands of
-//   O[query][d] += sum_key P[query][key] V[key][d]   (step i: keys 8(i/4) + i%4 and +4)
-// with B = V from LDS.  O's rows are queries 8(r/4) + 4 half + r%4 of register r, so the
-// per-query rescale factors are passed through a 32-float LDS slot per wave.
+// Attention with fp32-accurate products on fp16 MFMAs.  Every fp32 operand x is split into
+// fp16 x_hi = fp16(x) and x_lo = fp16(x - x_hi) (together ~21 significant bits), and a product
+// is accumulated as hi*hi + hi*lo + lo*hi in fp32 (the dropped lo*lo term is 2^-22 relative):
+// three v_mfma_f32_32x32x16_f16 per 16-deep step instead of eight fp32 32x32x2 steps.
+//
+// Workgroup: 4 waves x 32 queries of one (sequence, head); the K and V rows of 32 keys at a
+// time are split and staged in LDS (K row-major [key][d], V transposed [d][key]; the row
+// strides keep a wave's reads on distinct banks).  Per key block each wave computes
+//   S^T[key][query] = sum_d K[key][d] Q[query][d]   A = K (LDS), B = Q^T (registers)
+// so each lane owns one query column: 16 scores of its half of the keys, registers i holding
+// keys 8(i/4) + 4 half + i%4.  After the online softmax those 16 probabilities are the A
+// operands of
+//   O[query][d] += sum_key P[query][key] V[key][d]  two 16-deep steps; in step t lane slot j
+//                                                   is key 16t + 8(j/4) + 4 half + j%4, i.e.
+//                                                   register 8t + j, and B reads those keys'
+//                                                   V columns from the transposed tile.
+// O's rows are queries 8(r/4) + 4 half + r%4 of register r, so the per-query rescale
+// factors pass through a 32-float LDS slot per wave.  Operands below ~2^-4 in magnitude have
+// their low part in the fp16 subnormal range (absolute precision 2^-24), so their relative
+// precision degrades gracefully; P is scaled by 2^15 before the split to keep it exact.
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+// hi + lo split of two floats with one explicit rounding (round toward zero) for both
+// halves: the remainder is formed from the very hi value the MFMA will read.  (A plain
+// (_Float16) cast may be emitted as different conversion instructions for the operand and
+// for the remainder; where their roundings disagree the split loses a 2^-11 term.)
+__device__ __forceinline__ void split2(float a, float b, v2h &hi, v2h &lo) {
+    hi = __builtin_bit_cast(v2h, __builtin_amdgcn_cvt_pkrtz(a, b));
+    lo = __builtin_bit_cast(v2h, __builtin_amdgcn_cvt_pkrtz(a - (float)hi[0], b - (float)hi[1]));
+}
+
+__device__ __forceinline__ void split8(const float (&x)[8], v8h &hi, v8h &lo) {
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+        v2h h, l;
+        split2(x[j], x[j + 1], h, l);
+        hi[j] = h[0], hi[j + 1] = h[1], lo[j] = l[0], lo[j + 1] = l[1];
+    }
+}
+
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_mfma(const float *__restrict__ qkv, int64_t ld, float *__restrict__ out,
-                                                   int64_t ldo, int T, int nq, int nkv, float scale, int causal) {
-    constexpr int HALF = HD / 2, AKS = HD + 4, NT = HD / 32;
-    __shared__ __attribute__((aligned(16))) float Ks[32 * AKS];
-    __shared__ __attribute__((aligned(16))) float Vs[32 * AKS];
+__global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qkv, int64_t ld, float *__restrict__ out,
+                                                    int64_t ldo, int T, int nq, int nkv, float scale, int causal) {
+    constexpr int NS = HD / 16, NT = HD / 32;
+    constexpr int KST = HD + 8;  // K tile row stride (halves): 4 banks apart per row
+    constexpr int VST = 36;      // V^T tile row stride (halves): 18 dwords, odd multiple of 2
+    __shared__ __attribute__((aligned(16))) _Float16 Kh[32 * KST], Kl[32 * KST];
+    __shared__ __attribute__((aligned(16))) _Float16 Vh[HD * VST], Vl[HD * VST];
     __shared__ __attribute__((aligned(16))) float rs[4][32];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
     const int h = blockIdx.y, hk = h / (nq / nkv);
@@ -127,14 +162,16 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const float *__restrict__ qkv
     const int64_t qcol = (int64_t)h * HD, kcol = (int64_t)nq * HD + (int64_t)hk * HD,
                   vcol = (int64_t)(nq + nkv) * HD + (int64_t)hk * HD;
 
-    // Q^T operand: lane holds Q[qi][d] for d = s + HALF*half, s < HALF, times the scale
-    float qv[HALF];
+    // Q^T operand, split: step s holds Q[qi][16s + 8 half + j] * scale, j < 8
+    v8h qh[NS], ql[NS];
     {
-        const float *qp = qkv + (rbase + min(qi, T - 1)) * ld + qcol + HALF * half;
+        const float *qp = qkv + (rbase + min(qi, T - 1)) * ld + qcol + 8 * half;
 #pragma unroll
-        for (int s = 0; s < HALF; s += 4) {
-            const float4 t = *(const float4 *)(qp + s);
-            qv[s] = t.x * scale, qv[s + 1] = t.y * scale, qv[s + 2] = t.z * scale, qv[s + 3] = t.w * scale;
+        for (int st = 0; st < NS; st++) {
+            const float4 a = *(const float4 *)(qp + 16 * st), b = *(const float4 *)(qp + 16 * st + 4);
+            const float x[8] = {a.x * scale, a.y * scale, a.z * scale, a.w * scale,
+                                b.x * scale, b.y * scale, b.z * scale, b.w * scale};
+            split8(x, qh[st], ql[st]);
         }
     }
     v16f oacc[NT];
@@ -153,27 +190,38 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const float *__restrict__ qkv
                 kk = *(const float4 *)(qkv + (rbase + kb + r) * ld + kcol + c4);
                 vv = *(const float4 *)(qkv + (rbase + kb + r) * ld + vcol + c4);
             }
-            *(float4 *)&Ks[r * AKS + c4] = kk;
-            *(float4 *)&Vs[r * AKS + c4] = vv;
+            v2h k01h, k01l, k23h, k23l, v01h, v01l, v23h, v23l;
+            split2(kk.x, kk.y, k01h, k01l);
+            split2(kk.z, kk.w, k23h, k23l);
+            split2(vv.x, vv.y, v01h, v01l);
+            split2(vv.z, vv.w, v23h, v23l);
+            *(v4h *)&Kh[r * KST + c4] = (v4h){k01h[0], k01h[1], k23h[0], k23h[1]};
+            *(v4h *)&Kl[r * KST + c4] = (v4h){k01l[0], k01l[1], k23l[0], k23l[1]};
+            Vh[(c4 + 0) * VST + r] = v01h[0], Vl[(c4 + 0) * VST + r] = v01l[0];
+            Vh[(c4 + 1) * VST + r] = v01h[1], Vl[(c4 + 1) * VST + r] = v01l[1];
+            Vh[(c4 + 2) * VST + r] = v23h[0], Vl[(c4 + 2) * VST + r] = v23l[0];
+            Vh[(c4 + 3) * VST + r] = v23h[1], Vl[(c4 + 3) * VST + r] = v23l[1];
         }
         __syncthreads();
         if (kb >= kend_w) continue;  // past this wave's causal range (wave-uniform)
 
-        v16f st = (v16f){};
-        const float *krow = &Ks[l32 * AKS + HALF * half];
+        // three accumulators, so consecutive MFMAs never chain on one accumulator while a
+        // later load reuses their operand registers (the chained form gave wrong scores)
+        v16f s_hh = (v16f){}, s_hl = (v16f){}, s_lh = (v16f){};
+        const _Float16 *kh = &Kh[l32 * KST + 8 * half], *kl = &Kl[l32 * KST + 8 * half];
 #pragma unroll
-        for (int s = 0; s < HALF; s += 4) {
-            const float4 k4 = *(const float4 *)(krow + s);
-            st = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.x, qv[s], st, 0, 0, 0);
-            st = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.y, qv[s + 1], st, 0, 0, 0);
-            st = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.z, qv[s + 2], st, 0, 0, 0);
-            st = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.w, qv[s + 3], st, 0, 0, 0);
+        for (int st = 0; st < NS; st++) {
+            const v8h ah = *(const v8h *)(kh + 16 * st), al = *(const v8h *)(kl + 16 * st);
+            s_hh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[st], s_hh, 0, 0, 0);
+            s_hl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ql[st], s_hl, 0, 0, 0);
+            s_lh = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[st], s_lh, 0, 0, 0);
         }
+        const v16f sc = s_hh + (s_hl + s_lh);
         float p[16], mblk = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int key = kb + 8 * (i / 4) + 4 * half + (i % 4);
-            p[i] = (key >= T || (causal && key > qi)) ? -INFINITY : st[i];
+            p[i] = (key >= T || (causal && key > qi)) ? -INFINITY : sc[i];
             mblk = fmaxf(mblk, p[i]);
         }
         mblk = fmaxf(mblk, __shfl_xor(mblk, 32));
@@ -203,15 +251,36 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const float *__restrict__ qkv
 #pragma unroll
             for (int r = 0; r < 16; r++) oacc[j][r] *= al[r];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float *vrow = &Vs[(8 * (i / 4) + 4 * half + (i % 4)) * AKS + l32];
+        for (int t = 0; t < 2; t++) {
+            // P is split as 2^15 p (exact scaling; p <= 1 keeps it below the fp16 maximum) so
+            // that the low part of small probabilities stays out of the fp16 subnormal range
+            float px[8];
 #pragma unroll
-            for (int j = 0; j < NT; j++) oacc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(p[i], vrow[32 * j], oacc[j], 0, 0, 0);
+            for (int j = 0; j < 8; j++) px[j] = p[8 * t + j] * 32768.0f;
+            v8h ph, pl;
+            split8(px, ph, pl);
+            const int k0 = 16 * t + 4 * half;  // slot j < 4: keys k0 + j; j >= 4: keys k0 + 8 + j - 4
+            v8h bh[NT], bl[NT];
+#pragma unroll
+            for (int j = 0; j < NT; j++) {
+                const int d = 32 * j + l32;
+                const v4h h0 = *(const v4h *)&Vh[d * VST + k0], h1 = *(const v4h *)&Vh[d * VST + k0 + 8];
+                const v4h l0 = *(const v4h *)&Vl[d * VST + k0], l1 = *(const v4h *)&Vl[d * VST + k0 + 8];
+                bh[j] = (v8h){h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+                bl[j] = (v8h){l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+            }
+            // term-major order: consecutive MFMAs write different accumulators
+#pragma unroll
+            for (int j = 0; j < NT; j++) oacc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, bh[j], oacc[j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < NT; j++) oacc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, bl[j], oacc[j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < NT; j++) oacc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl, bh[j], oacc[j], 0, 0, 0);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot is rewritten next block
     }
 
-    rs[wave][l32] = 1.0f / l_run;
+    rs[wave][l32] = 1.0f / (l_run * 32768.0f);  // O accumulated 2^15 P V
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     float inv[16];
 #pragma unroll
@@ -299,8 +368,8 @@ hipError_t launch_attn_mfma(const float *qkv, int64_t ld, float *out, int64_t ld
     if (B <= 0 || T <= 0) return hipSuccess;
     if (nkv <= 0 || nq % nkv != 0 || ld % 4 != 0 || ((uintptr_t)qkv & 15) != 0) return hipErrorInvalidValue;
     const dim3 g((unsigned)((T + 127) / 128), (unsigned)nq, (unsigned)B), b(256);
-    if (hd == 128) hipLaunchKernelGGL((k_attn_mfma<128>), g, b, 0, s, qkv, ld, out, ldo, T, nq, nkv, scale, causal);
-    else if (hd == 64) hipLaunchKernelGGL((k_attn_mfma<64>), g, b, 0, s, qkv, ld, out, ldo, T, nq, nkv, scale, causal);
+    if (hd == 128) hipLaunchKernelGGL((k_attn_split<128>), g, b, 0, s, qkv, ld, out, ldo, T, nq, nkv, scale, causal);
+    else if (hd == 64) hipLaunchKernelGGL((k_attn_split<64>), g, b, 0, s, qkv, ld, out, ldo, T, nq, nkv, scale, causal);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
