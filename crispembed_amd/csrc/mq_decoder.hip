@@ -106,25 +106,32 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(float *qkv, int64_t ld, co
 // fp16 x_hi = fp16(x) and x_lo = fp16(x - x_hi) (together ~21 significant bits), and a product
 // is accumulated as hi*hi + hi*lo + lo*hi in fp32 (the dropped lo*lo term is 2^-22 relative):
 // three v_mfma_f32_32x32x16_f16 per 16-deep step instead of eight fp32 32x32x2 steps.
+// Operands below ~2^-4 in magnitude have their low part in the fp16 subnormal range (absolute
+// precision 2^-24), so their relative precision degrades gracefully; P is scaled by 2^15
+// before its split to keep it exact.
 //
-// Workgroup: 4 waves x 32 queries of one (sequence, head); the K and V rows of 32 keys at a
-// time are split and staged in LDS (K row-major [key][d], V transposed [d][key]; the row
-// strides keep a wave's reads on distinct banks).  Per key block each wave computes
-//   S^T[key][query] = sum_d K[key][d] Q[query][d]   A = K (LDS), B = Q^T (registers)
-// so each lane owns one query column: 16 scores of its half of the keys, registers i holding
-// keys 8(i/4) + 4 half + i%4.  After the online softmax those 16 probabilities are the A
-// operands of
-//   O[query][d] += sum_key P[query][key] V[key][d]  two 16-deep steps; in step t lane slot j
-//                                                   is key 16t + 8(j/4) + 4 half + j%4, i.e.
-//                                                   register 8t + j, and B reads those keys'
-//                                                   V columns from the transposed tile.
-// O's rows are queries 8(r/4) + 4 half + r%4 of register r, so the per-query rescale
-// factors pass through a 32-float LDS slot per wave.  Operands below ~2^-4 in magnitude have
-// their low part in the fp16 subnormal range (absolute precision 2^-24), so their relative
-// precision degrades gracefully; P is scaled by 2^15 before the split to keep it exact.
+// Two kernels:
+//  k_kv_frag   per (sequence, key/value head, block of 32 keys): K rows (optionally RMS-normed
+//              and rotated, as for Q) and V rows, split and written as MFMA operand fragments
+//              of 1 KB each (64 lanes x 8 halves, in lane order), so the attention kernel reads
+//              every operand with one coalesced 16-byte load per lane and no LDS staging:
+//                K fragment (st, p):    lane l holds K[32 kb + l%32][16 st + 8 (l/32) + j]
+//                V fragment (t, n, p):  lane l holds V[32 kb + 16 t + 8 (j/4) + 4 (l/32) + j%4][32 n + l%32]
+//              (p = hi / lo; j < 8 the lane's slot).  Each K and V element is split once,
+//              instead of once per query block that reads it.
+//  k_attn_frag each wave: 32 queries of one head.  Per key block
+//                S^T[key][query] = sum_d K[key][d] Q[query][d]   A = K fragments, B = Q^T (registers)
+//              so each lane owns one query column: 16 scores of its half of the keys, register
+//              i holding key 8(i/4) + 4 half + i%4.  After the online softmax (base 2: Q carries
+//              scale * log2 e) those 16 probabilities are the A operands of
+//                O[query][d] += sum_key P[query][key] V[key][d]
+//              in two 16-deep steps; in step t lane slot j is register 8t + j, the key the V
+//              fragment (t, n) holds in that slot.  O's rows are queries 8(r/4) + 4 half + r%4 of
+//              register r, so the per-query rescale factors pass through a 32-float LDS slot per
+//              wave.  A workgroup is 8 waves, 2 heads x 128 queries (the two heads of a grouped-
+//              query pair read the same fragments), two waves per SIMD so that one wave's
+//              softmax overlaps the other's matrix work; the longest causal ranges go first.
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 // hi + lo split of two floats with one explicit rounding (round toward zero) for both
@@ -145,139 +152,213 @@ __device__ __forceinline__ void split8(const float (&x)[8], v8h &hi, v8h &lo) {
     }
 }
 
+// fragments per 32-key block: K (NS steps) and V (2 steps x NT column tiles), hi and lo each
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qkv, int64_t ld, float *__restrict__ out,
-                                                    int64_t ldo, int T, int nq, int nkv, float scale, int causal) {
-    constexpr int NS = HD / 16, NT = HD / 32;
-    constexpr int KST = HD + 8;  // K tile row stride (halves): 4 banks apart per row
-    constexpr int VST = 36;      // V^T tile row stride (halves): 18 dwords, odd multiple of 2
-    __shared__ __attribute__((aligned(16))) _Float16 Kh[32 * KST], Kl[32 * KST];
-    __shared__ __attribute__((aligned(16))) _Float16 Vh[HD * VST], Vl[HD * VST];
-    __shared__ __attribute__((aligned(16))) float rs[4][32];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
-    const int h = blockIdx.y, hk = h / (nq / nkv);
-    const int64_t rbase = (int64_t)blockIdx.z * T;  // first row of the sequence
-    const int q0 = blockIdx.x * 128 + wave * 32;    // this wave's first query
-    const int qi = q0 + l32;
-    const int64_t qcol = (int64_t)h * HD, kcol = (int64_t)nq * HD + (int64_t)hk * HD,
-                  vcol = (int64_t)(nq + nkv) * HD + (int64_t)hk * HD;
+constexpr int kv_frags() { return 2 * (HD / 16) + 4 * (HD / 32); }
 
-    // Q^T operand, split: step s holds Q[qi][16s + 8 half + j] * scale, j < 8
+template <int HD>
+__global__ __launch_bounds__(256) void k_kv_frag(const float *__restrict__ qkv, int64_t ld, int nq, int nkv, int T,
+                                                 int nblk, const float *__restrict__ kw, float eps,
+                                                 const float2 *__restrict__ cs, _Float16 *__restrict__ frag) {
+    constexpr int NS = HD / 16, NT = HD / 32, HALF = HD / 2, KS = HD + 4, NFR = kv_frags<HD>();
+    __shared__ __attribute__((aligned(16))) float Ks[32 * KS];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
+    const int kb = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+    const int64_t rbase = (int64_t)b * T;
+    const float *kp = qkv + (int64_t)nq * HD + (int64_t)hk * HD;
+    const float *vp = qkv + (int64_t)(nq + nkv) * HD + (int64_t)hk * HD;
+    const bool on = lane < HALF;
+    // K rows of the block, normed and rotated (NEOX pair (i, i + HD/2) in one lane), to LDS;
+    // rows past T are zero
+    for (int r = wave; r < 32; r += 4) {
+        const int key = kb * 32 + r;
+        float a = 0.f, c = 0.f;
+        if (key < T) {
+            const float *x = kp + (rbase + key) * ld;
+            a = on ? x[lane] : 0.f;
+            c = on ? x[lane + HALF] : 0.f;
+            if (kw) {
+                const float scale = 1.0f / sqrtf(wave_sum_f(a * a + c * c) / (float)HD + eps);
+                if (on) {
+                    a = a * scale * kw[lane];
+                    c = c * scale * kw[lane + HALF];
+                }
+            }
+            if (cs && on) {
+                const float2 rot = cs[(int64_t)key * HALF + lane];
+                const float na = a * rot.x - c * rot.y, nc = a * rot.y + c * rot.x;
+                a = na, c = nc;
+            }
+        }
+        if (on) Ks[r * KS + lane] = a, Ks[r * KS + lane + HALF] = c;
+    }
+    __syncthreads();
+    _Float16 *F = frag + ((int64_t)(b * nkv + hk) * nblk + kb) * NFR * 512 + lane * 8;
+    for (int st = wave; st < NS; st += 4) {
+        const float4 u = *(const float4 *)&Ks[l32 * KS + 16 * st + 8 * half];
+        const float4 w = *(const float4 *)&Ks[l32 * KS + 16 * st + 8 * half + 4];
+        const float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+        v8h h, l;
+        split8(x, h, l);
+        *(v8h *)(F + (2 * st) * 512) = h;
+        *(v8h *)(F + (2 * st + 1) * 512) = l;
+    }
+    for (int f = wave; f < 2 * NT; f += 4) {
+        const int t = f / NT, n = f % NT;
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int key = kb * 32 + 16 * t + 8 * (j / 4) + 4 * half + j % 4;
+            x[j] = key < T ? vp[(rbase + key) * ld + 32 * n + l32] : 0.f;
+        }
+        v8h h, l;
+        split8(x, h, l);
+        *(v8h *)(F + (2 * NS + 2 * f) * 512) = h;
+        *(v8h *)(F + (2 * NS + 2 * f + 1) * 512) = l;
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(512) void k_attn_frag(const float *__restrict__ qkv, int64_t ld,
+                                                   const _Float16 *__restrict__ frag, int nblk, float *__restrict__ out,
+                                                   int64_t ldo, int T, int nq, int nkv, float qscale, int causal,
+                                                   const float *__restrict__ qw, float eps,
+                                                   const float2 *__restrict__ cs) {
+    constexpr int NS = HD / 16, NT = HD / 32, HALF = HD / 2, NFR = kv_frags<HD>();
+    __shared__ __attribute__((aligned(16))) float rs[8][32];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
+    const int h = blockIdx.x * 2 + (wave >> 2);
+    const int b = blockIdx.y;
+    // query tile of the wave: waves w and w + 4 share a SIMD, so they get tiles t and 3 - t
+    // (one long and one short causal range each); the longest ranges are dispatched first
+    const int qt = wave < 4 ? wave : 7 - wave;
+    const int q0 = ((int)gridDim.z - 1 - (int)blockIdx.z) * 128 + qt * 32;
+    if (h >= nq || q0 >= T) return;  // no workgroup barrier below
+    const int hk = h / (nq / nkv), qi = q0 + l32;
+    const int64_t rbase = (int64_t)b * T;
+
+    // Q^T operand: step st holds Q[qi][16 st + 8 half + j], normed, rotated, times qscale
     v8h qh[NS], ql[NS];
     {
-        const float *qp = qkv + (rbase + min(qi, T - 1)) * ld + qcol + 8 * half;
+        const int qrow = min(qi, T - 1);
+        const float *qp = qkv + (rbase + qrow) * ld + (int64_t)h * HD + 8 * half;
+        float x[NS][8];
 #pragma unroll
         for (int st = 0; st < NS; st++) {
-            const float4 a = *(const float4 *)(qp + 16 * st), b = *(const float4 *)(qp + 16 * st + 4);
-            const float x[8] = {a.x * scale, a.y * scale, a.z * scale, a.w * scale,
-                                b.x * scale, b.y * scale, b.z * scale, b.w * scale};
-            split8(x, qh[st], ql[st]);
+            const float4 u = *(const float4 *)(qp + 16 * st), w = *(const float4 *)(qp + 16 * st + 4);
+            x[st][0] = u.x, x[st][1] = u.y, x[st][2] = u.z, x[st][3] = u.w;
+            x[st][4] = w.x, x[st][5] = w.y, x[st][6] = w.z, x[st][7] = w.w;
+        }
+        if (qw) {
+            float ss = 0.f;
+#pragma unroll
+            for (int st = 0; st < NS; st++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) ss += x[st][j] * x[st][j];
+            ss += __shfl_xor(ss, 32);
+            const float scale = 1.0f / sqrtf(ss / (float)HD + eps);
+#pragma unroll
+            for (int st = 0; st < NS; st++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) x[st][j] = x[st][j] * scale * qw[16 * st + 8 * half + j];
+        }
+        if (cs) {
+            // pair (d, d + HD/2) sits in steps st and st + NS/2 of the same lane and slot
+#pragma unroll
+            for (int st = 0; st < NS / 2; st++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float2 rot = cs[(int64_t)qrow * HALF + 16 * st + 8 * half + j];
+                    const float a = x[st][j], c = x[st + NS / 2][j];
+                    x[st][j] = a * rot.x - c * rot.y;
+                    x[st + NS / 2][j] = a * rot.y + c * rot.x;
+                }
+        }
+#pragma unroll
+        for (int st = 0; st < NS; st++) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) x[st][j] *= qscale;
+            split8(x[st], qh[st], ql[st]);
         }
     }
     v16f oacc[NT];
 #pragma unroll
-    for (int j = 0; j < NT; j++) oacc[j] = (v16f){};
+    for (int n = 0; n < NT; n++) oacc[n] = (v16f){};
     float m_run = -INFINITY, l_run = 0.f;
-    const int kend = causal ? min(T, (int)blockIdx.x * 128 + 128) : T;  // keys the workgroup needs
-    const int kend_w = q0 >= T ? 0 : causal ? min(T, q0 + 32) : T;      // keys this wave needs
+    const int kend = causal ? min(T, q0 + 32) : T;
+    const v8h *F = (const v8h *)(frag + (int64_t)(b * nkv + hk) * nblk * NFR * 512) + lane;
 
-    for (int kb = 0; kb < kend; kb += 32) {
-        __syncthreads();  // the previous block's K/V are no longer read
-        for (int e = threadIdx.x; e < 32 * HD / 4; e += 256) {
-            const int r = e / (HD / 4), c4 = (e % (HD / 4)) * 4;
-            float4 kk = make_float4(0.f, 0.f, 0.f, 0.f), vv = kk;
-            if (kb + r < T) {
-                kk = *(const float4 *)(qkv + (rbase + kb + r) * ld + kcol + c4);
-                vv = *(const float4 *)(qkv + (rbase + kb + r) * ld + vcol + c4);
-            }
-            v2h k01h, k01l, k23h, k23l, v01h, v01l, v23h, v23l;
-            split2(kk.x, kk.y, k01h, k01l);
-            split2(kk.z, kk.w, k23h, k23l);
-            split2(vv.x, vv.y, v01h, v01l);
-            split2(vv.z, vv.w, v23h, v23l);
-            *(v4h *)&Kh[r * KST + c4] = (v4h){k01h[0], k01h[1], k23h[0], k23h[1]};
-            *(v4h *)&Kl[r * KST + c4] = (v4h){k01l[0], k01l[1], k23l[0], k23l[1]};
-            Vh[(c4 + 0) * VST + r] = v01h[0], Vl[(c4 + 0) * VST + r] = v01l[0];
-            Vh[(c4 + 1) * VST + r] = v01h[1], Vl[(c4 + 1) * VST + r] = v01l[1];
-            Vh[(c4 + 2) * VST + r] = v23h[0], Vl[(c4 + 2) * VST + r] = v23l[0];
-            Vh[(c4 + 3) * VST + r] = v23h[1], Vl[(c4 + 3) * VST + r] = v23l[1];
-        }
-        __syncthreads();
-        if (kb >= kend_w) continue;  // past this wave's causal range (wave-uniform)
-
-        // three accumulators, so consecutive MFMAs never chain on one accumulator while a
-        // later load reuses their operand registers (the chained form gave wrong scores)
+    for (int kb = 0; kb * 32 < kend; kb++) {
+        const v8h *Fb = F + (int64_t)kb * NFR * 64;
+        // three accumulators, so consecutive MFMAs never chain on one accumulator
         v16f s_hh = (v16f){}, s_hl = (v16f){}, s_lh = (v16f){};
-        const _Float16 *kh = &Kh[l32 * KST + 8 * half], *kl = &Kl[l32 * KST + 8 * half];
 #pragma unroll
         for (int st = 0; st < NS; st++) {
-            const v8h ah = *(const v8h *)(kh + 16 * st), al = *(const v8h *)(kl + 16 * st);
+            const v8h ah = Fb[(2 * st) * 64], al = Fb[(2 * st + 1) * 64];
             s_hh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[st], s_hh, 0, 0, 0);
             s_hl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ql[st], s_hl, 0, 0, 0);
             s_lh = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[st], s_lh, 0, 0, 0);
         }
+        v8h bh[2][NT], bl[2][NT];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int n = 0; n < NT; n++) {
+                bh[t][n] = Fb[(2 * NS + 2 * (t * NT + n)) * 64];
+                bl[t][n] = Fb[(2 * NS + 2 * (t * NT + n) + 1) * 64];
+            }
         const v16f sc = s_hh + (s_hl + s_lh);
         float p[16], mblk = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int key = kb + 8 * (i / 4) + 4 * half + (i % 4);
+            const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
             p[i] = (key >= T || (causal && key > qi)) ? -INFINITY : sc[i];
             mblk = fmaxf(mblk, p[i]);
         }
         mblk = fmaxf(mblk, __shfl_xor(mblk, 32));
-        const float m_new = fmaxf(m_run, mblk);
-        const float alpha = expf(m_run - m_new);  // 0 on the first block
+        const float m_new = fmaxf(m_run, mblk);  // finite: key 32 kb <= every query of the wave
+        const float alpha = exp2f(m_run - m_new);  // 0 on the first block
         float lblk = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            p[i] = expf(p[i] - m_new);
+            p[i] = exp2f(p[i] - m_new);
             lblk += p[i];
         }
         lblk += __shfl_xor(lblk, 32);
         l_run = l_run * alpha + lblk;
         m_run = m_new;
 
-        // rescale O's rows (queries 8(r/4) + 4 half + r%4) by their query's alpha
-        rs[wave][l32] = alpha;
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // one wave writes and reads its slot
-        float al[16];
+        if (__ballot(alpha != 1.0f)) {
+            // rescale O's rows (queries 8(r/4) + 4 half + r%4) by their query's alpha
+            rs[wave][l32] = alpha;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // one wave writes and reads its slot
+            float al[16];
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const float4 t = *(const float4 *)&rs[wave][8 * g + 4 * half];
-            al[4 * g] = t.x, al[4 * g + 1] = t.y, al[4 * g + 2] = t.z, al[4 * g + 3] = t.w;
+            for (int g = 0; g < 4; g++) {
+                const float4 t = *(const float4 *)&rs[wave][8 * g + 4 * half];
+                al[4 * g] = t.x, al[4 * g + 1] = t.y, al[4 * g + 2] = t.z, al[4 * g + 3] = t.w;
+            }
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) oacc[n][r] *= al[r];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot is rewritten later
         }
 #pragma unroll
-        for (int j = 0; j < NT; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) oacc[j][r] *= al[r];
-#pragma unroll
         for (int t = 0; t < 2; t++) {
-            // P is split as 2^15 p (exact scaling; p <= 1 keeps it below the fp16 maximum) so
-            // that the low part of small probabilities stays out of the fp16 subnormal range
             float px[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) px[j] = p[8 * t + j] * 32768.0f;
             v8h ph, pl;
             split8(px, ph, pl);
-            const int k0 = 16 * t + 4 * half;  // slot j < 4: keys k0 + j; j >= 4: keys k0 + 8 + j - 4
-            v8h bh[NT], bl[NT];
-#pragma unroll
-            for (int j = 0; j < NT; j++) {
-                const int d = 32 * j + l32;
-                const v4h h0 = *(const v4h *)&Vh[d * VST + k0], h1 = *(const v4h *)&Vh[d * VST + k0 + 8];
-                const v4h l0 = *(const v4h *)&Vl[d * VST + k0], l1 = *(const v4h *)&Vl[d * VST + k0 + 8];
-                bh[j] = (v8h){h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
-                bl[j] = (v8h){l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
-            }
             // term-major order: consecutive MFMAs write different accumulators
 #pragma unroll
-            for (int j = 0; j < NT; j++) oacc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, bh[j], oacc[j], 0, 0, 0);
+            for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, bh[t][n], oacc[n], 0, 0, 0);
 #pragma unroll
-            for (int j = 0; j < NT; j++) oacc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, bl[j], oacc[j], 0, 0, 0);
+            for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, bl[t][n], oacc[n], 0, 0, 0);
 #pragma unroll
-            for (int j = 0; j < NT; j++) oacc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl, bh[j], oacc[j], 0, 0, 0);
+            for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl, bh[t][n], oacc[n], 0, 0, 0);
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot is rewritten next block
     }
 
     rs[wave][l32] = 1.0f / (l_run * 32768.0f);  // O accumulated 2^15 P V
@@ -292,9 +373,9 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qk
     for (int r = 0; r < 16; r++) {
         const int q = q0 + 8 * (r / 4) + 4 * half + (r % 4);
         if (q >= T) continue;
-        float *o = out + (rbase + q) * ldo + qcol + l32;
+        float *o = out + (rbase + q) * ldo + (int64_t)h * HD + l32;
 #pragma unroll
-        for (int j = 0; j < NT; j++) o[32 * j] = oacc[j][r] * inv[r];
+        for (int n = 0; n < NT; n++) o[32 * n] = oacc[n][r] * inv[r];
     }
 }
 
@@ -363,14 +444,42 @@ hipError_t launch_qk_norm_rope(float *qkv, int64_t ld, const float *qw, const fl
     return hipGetLastError();
 }
 
-hipError_t launch_attn_mfma(const float *qkv, int64_t ld, float *out, int64_t ldo, int B, int T, int nq, int nkv, int hd,
-                            float scale, int causal, hipStream_t s) {
+size_t attn_workspace_bytes(int B, int T, int nkv, int hd) {
+    const int nfr = hd == 128 ? kv_frags<128>() : kv_frags<64>();
+    return (size_t)B * nkv * ((T + 31) / 32) * nfr * 1024;
+}
+
+hipError_t launch_rope_table(float2 *cs, int T, int hd, float theta_base, hipStream_t s) {
+    const float theta_scale = powf(theta_base, -2.0f / (float)hd);
+    hipLaunchKernelGGL(k_rope_table, dim3((unsigned)((T * (hd / 2) + 255) / 256)), dim3(256), 0, s, cs, T, hd / 2,
+                       theta_scale);
+    return hipGetLastError();
+}
+
+// qw / kw: per-head RMS norm weights (NULL: no norm); cs: RoPE table of T positions (NULL: no
+// rotation); ws: attn_workspace_bytes() of device memory for the K/V fragments
+hipError_t launch_attn_frag(const float *qkv, int64_t ld, float *out, int64_t ldo, int B, int T, int nq, int nkv,
+                            int hd, float scale, int causal, const float *qw, const float *kw, float eps,
+                            const float2 *cs, void *ws, hipStream_t s) {
     if (B <= 0 || T <= 0) return hipSuccess;
-    if (nkv <= 0 || nq % nkv != 0 || ld % 4 != 0 || ((uintptr_t)qkv & 15) != 0) return hipErrorInvalidValue;
-    const dim3 g((unsigned)((T + 127) / 128), (unsigned)nq, (unsigned)B), b(256);
-    if (hd == 128) hipLaunchKernelGGL((k_attn_split<128>), g, b, 0, s, qkv, ld, out, ldo, T, nq, nkv, scale, causal);
-    else if (hd == 64) hipLaunchKernelGGL((k_attn_split<64>), g, b, 0, s, qkv, ld, out, ldo, T, nq, nkv, scale, causal);
-    else return hipErrorInvalidValue;
+    if (nkv <= 0 || nq % nkv != 0 || ld % 4 != 0 || ((uintptr_t)qkv & 15) != 0 || ((uintptr_t)ws & 15) != 0)
+        return hipErrorInvalidValue;
+    const int nblk = (T + 31) / 32;
+    const float qscale = scale * 1.4426950408889634f;  // softmax in base 2
+    const dim3 gk((unsigned)nblk, (unsigned)nkv, (unsigned)B), ga((unsigned)((nq + 1) / 2), (unsigned)B,
+                                                                 (unsigned)((T + 127) / 128));
+    _Float16 *fr = (_Float16 *)ws;
+    if (hd == 128) {
+        hipLaunchKernelGGL((k_kv_frag<128>), gk, dim3(256), 0, s, qkv, ld, nq, nkv, T, nblk, kw, eps, cs, fr);
+        hipLaunchKernelGGL((k_attn_frag<128>), ga, dim3(512), 0, s, qkv, ld, fr, nblk, out, ldo, T, nq, nkv, qscale,
+                           causal, qw, eps, cs);
+    } else if (hd == 64) {
+        hipLaunchKernelGGL((k_kv_frag<64>), gk, dim3(256), 0, s, qkv, ld, nq, nkv, T, nblk, kw, eps, cs, fr);
+        hipLaunchKernelGGL((k_attn_frag<64>), ga, dim3(512), 0, s, qkv, ld, fr, nblk, out, ldo, T, nq, nkv, qscale,
+                           causal, qw, eps, cs);
+    } else {
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

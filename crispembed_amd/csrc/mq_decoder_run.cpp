@@ -3,8 +3,9 @@
 // Per layer (pre-norm Qwen3 block, src/decoder_embed.cpp:718-814):
 //   Hn   = rms_norm(X) * attn_norm                  (fused with the previous residual ADD)
 //   qkv  = Hn . [Wq; Wk; Wv]^T                      one mul_mat over the concatenated rows
-//   q, k = rope(rms_norm_head(q|k) * q_norm|k_norm) in place
-//   A    = causal GQA attention(q, k, v)            fp32 MFMA
+//   A    = causal GQA attention(rope(rms_norm_head(q) * q_norm),
+//                               rope(rms_norm_head(k) * k_norm), v)
+//          the per-head norms and rotations applied as the attention kernels load q and k
 //   X    = X + A . Wo^T;  Hn = rms_norm(X) * ffn_norm
 //   gu   = Hn . [Wgate; Wup]^T                      one mul_mat, gate and up side by side
 //   X    = X + (silu(gate) * up) . Wdown^T          the product formed by the quantizer
@@ -26,8 +27,11 @@ hipError_t launch_add_rmsnorm(const float *y, const float *res, const int32_t *i
                               const float *w, float eps, float *xout, float *hout, int64_t rows, int H, hipStream_t s);
 hipError_t launch_qk_norm_rope(float *qkv, int64_t ld, const float *qw, const float *kw, float eps, int nq, int nkv,
                                int hd, int T, float theta_base, int64_t rows, float2 *cs, hipStream_t s);
-hipError_t launch_attn_mfma(const float *qkv, int64_t ld, float *out, int64_t ldo, int B, int T, int nq, int nkv, int hd,
-                            float scale, int causal, hipStream_t s);
+size_t attn_workspace_bytes(int B, int T, int nkv, int hd);
+hipError_t launch_rope_table(float2 *cs, int T, int hd, float theta_base, hipStream_t s);
+hipError_t launch_attn_frag(const float *qkv, int64_t ld, float *out, int64_t ldo, int B, int T, int nq, int nkv,
+                            int hd, float scale, int causal, const float *qw, const float *kw, float eps,
+                            const float2 *cs, void *ws, hipStream_t s);
 hipError_t launch_last_rmsnorm_l2(const float *x, const float *w, float eps, float *out, int B, int T, int H,
                                   hipStream_t s);
 hipError_t launch_mean_pool_l2(const float *x, float *out, int B, int T, int H, hipStream_t s);  // mq_encoder.hip
@@ -47,7 +51,7 @@ struct mq_decoder {
     mq_decoder_hparams hp{};
     DevBuf tok, out_norm;
     std::vector<DecLayer> layers;
-    DevBuf x, h, qkv, att, y, gu, ws, rope;
+    DevBuf x, h, qkv, att, y, gu, ws, rope, kvf;
 };
 
 extern "C" mq_decoder *mq_decoder_create(const mq_decoder_hparams *hp) {
@@ -129,7 +133,8 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
                                  mq_workspace_bytes(t, rows, F)});
     if (!m->x.ensure(rows * H * f4) || !m->h.ensure(rows * H * f4) || !m->qkv.ensure(rows * ldqkv * f4) ||
         !m->att.ensure(rows * qd * f4) || !m->y.ensure(rows * H * f4) || !m->gu.ensure(rows * 2 * F * f4) ||
-        !m->ws.ensure(wsb) || !m->rope.ensure((size_t)T * (hd / 2) * sizeof(float2)))
+        !m->ws.ensure(wsb) || !m->rope.ensure((size_t)T * (hd / 2) * sizeof(float2)) ||
+        !m->kvf.ensure(attn_workspace_bytes(B, T, nkv, hd)))
         return set_error(MQ_ENOMEM, "activation buffers for %lld rows", (long long)rows);
     hipStream_t s = (hipStream_t)stream;
     const float eps = hp.rms_norm_eps;
@@ -144,16 +149,14 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
                                         (int)H, s),
                      "embedding")))
         return rc;
+    if ((rc = hip_rc(launch_rope_table((float2 *)m->rope.p, T, hd, hp.rope_theta, s), "rope table"))) return rc;
     for (size_t il = 0; il < m->layers.size(); il++) {
         const DecLayer &L = m->layers[il];
         if ((rc = mm(L.qkv, Hn, H, m->qkv.f()))) return rc;
-        if ((rc = hip_rc(launch_qk_norm_rope(m->qkv.f(), ldqkv, L.has_qn ? L.q_norm.f() : nullptr,
-                                             L.has_kn ? L.k_norm.f() : nullptr, eps, nq, nkv, hd, T, hp.rope_theta,
-                                             rows, (float2 *)m->rope.p, s),
-                         "q/k norm + rope")))
-            return rc;
-        if ((rc = hip_rc(launch_attn_mfma(m->qkv.f(), ldqkv, m->att.f(), qd, B, T, nq, nkv, hd, 1.0f / sqrtf((float)hd),
-                                          hp.causal, s),
+        if ((rc = hip_rc(launch_attn_frag(m->qkv.f(), ldqkv, m->att.f(), qd, B, T, nq, nkv, hd,
+                                          1.0f / sqrtf((float)hd), hp.causal, L.has_qn ? L.q_norm.f() : nullptr,
+                                          L.has_kn ? L.k_norm.f() : nullptr, eps, (const float2 *)m->rope.p,
+                                          m->kvf.p, s),
                          "attention")))
             return rc;
         if ((rc = mm(L.o, m->att.f(), qd, m->y.f()))) return rc;
@@ -202,14 +205,24 @@ extern "C" int mq_qk_norm_rope(float *qkv, int64_t ld, const float *q_norm, cons
                   "q/k norm + rope");
 }
 
+extern "C" size_t mq_attention_workspace_bytes(int B, int T, int n_kv_head, int head_dim) {
+    if (B <= 0 || T <= 0 || n_kv_head <= 0 || (head_dim != 64 && head_dim != 128)) return 0;
+    return attn_workspace_bytes(B, T, n_kv_head, head_dim);
+}
+
 extern "C" int mq_attention(const float *qkv, int64_t ld, float *out, int64_t ldo, int B, int T, int n_head,
-                            int n_kv_head, int head_dim, float scale, int causal, void *stream) {
+                            int n_kv_head, int head_dim, float scale, int causal, void *workspace,
+                            size_t workspace_bytes, void *stream) {
     if (!qkv || !out || B <= 0 || T <= 0 || n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head != 0 ||
         ld % 4 != 0 || ((uintptr_t)qkv & 15) != 0 || ld < (int64_t)(n_head + 2 * n_kv_head) * head_dim ||
         ldo < (int64_t)n_head * head_dim)
         return set_error(MQ_EINVAL, "mq_attention: bad arguments");
     if (head_dim != 64 && head_dim != 128) return set_error(MQ_EUNSUPPORTED, "head_dim %d (64 or 128)", head_dim);
-    return hip_rc(launch_attn_mfma(qkv, ld, out, ldo, B, T, n_head, n_kv_head, head_dim, scale, causal,
-                                   (hipStream_t)stream),
+    const size_t need = attn_workspace_bytes(B, T, n_kv_head, head_dim);
+    if (!workspace || ((uintptr_t)workspace & 15) != 0 || workspace_bytes < need)
+        return set_error(MQ_EINVAL, "mq_attention: workspace of %zu bytes (16-byte aligned) needed, %zu given", need,
+                         workspace_bytes);
+    return hip_rc(launch_attn_frag(qkv, ld, out, ldo, B, T, n_head, n_kv_head, head_dim, scale, causal, nullptr,
+                                   nullptr, 0.f, nullptr, workspace, (hipStream_t)stream),
                   "attention");
 }

@@ -68,8 +68,9 @@ _SIGS = {
     "mq_decoder_encode": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp]),
     "mq_qk_norm_rope": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, ctypes.c_float, _c_int, _c_int, _c_int, _c_int,
                                  ctypes.c_float, _c_i64, _c_vp]),
+    "mq_attention_workspace_bytes": (ctypes.c_size_t, [_c_int, _c_int, _c_int, _c_int]),
     "mq_attention": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.c_float,
-                              _c_int, _c_vp]),
+                              _c_int, _c_vp, ctypes.c_size_t, _c_vp]),
 }
 
 

@@ -66,11 +66,14 @@ int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T, float *ou
  *
  * mq_attention: out[row][h*head_dim + d] = softmax(scale * q k^T + mask) v per sequence and
  * query head h, key/value head h / (n_head / n_kv_head), mask causal or none
- * (ggml_flash_attn_ext, src/decoder_embed.cpp:769-777). */
+ * (ggml_flash_attn_ext, src/decoder_embed.cpp:769-777).  workspace: device memory of at least
+ * mq_attention_workspace_bytes(B, T, n_kv_head, head_dim) bytes, 16-byte aligned (the keys and
+ * values re-laid as matrix-core operands; B * n_kv_head * ceil(T/32) * 32 KB at head_dim 128). */
 int mq_qk_norm_rope(float *qkv, int64_t ld, const float *q_norm, const float *k_norm, float eps, int n_head,
                     int n_kv_head, int head_dim, int T, float theta, int64_t rows, void *stream);
+size_t mq_attention_workspace_bytes(int B, int T, int n_kv_head, int head_dim);
 int mq_attention(const float *qkv, int64_t ld, float *out, int64_t ldo, int B, int T, int n_head, int n_kv_head,
-                 int head_dim, float scale, int causal, void *stream);
+                 int head_dim, float scale, int causal, void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }
