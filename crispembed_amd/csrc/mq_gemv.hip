@@ -15,6 +15,8 @@
 //   F16 uses v_dot2_f32_f16 on fp16 activations.
 #include "mq_internal.h"
 
+#include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 namespace mq {
@@ -182,13 +184,12 @@ __global__ __launch_bounds__(256) void k_gemv_f16(const uint16_t *__restrict__ w
 // v_mfma_f32_16x16x16_f16 (m_j and the two limbs of B_j exact in fp16, products and sums
 // below 2^24: exact).  Per superblock, as ggml's vec_dot_q4_K_q8_K:
 //   y += d_x * (d * sum_j sc_j isum_j - dmin * sum_j m_j B_j).
-// Q6_K: per 32-value K-step, v_mfma_i32_16x16x32_i8 multiplies the unsigned 6-bit quants q
-// (rebuilt from the nibble and 2-bit planes) by an activation operand whose columns are
-// (token m, 16-group g) the same way, so each output is one 16-value group sum and its
-// int8 scale is one integer multiply-add.  The -32 offset of every quant is
-// sum_g sc_g * 32 * bsum16_g, one v_mfma_f32_16x16x16_f16 per superblock (sc and
-// 32*bsum16 exact in fp16).  Per superblock, as ggml's vec_dot_q6_K_q8_K:
-//   y += d_x * d * sum_g sc_g (sum_{i in g} q_i x_i - 32 bsum_g).
+// Q6_K: per 32-value K-step, v_mfma_i32_16x16x32_i8 multiplies 4 (q - 32) -- the 6-bit
+// two's complement v = q ^ 32 of the plane shifted into the top of each byte, exact in int8
+// -- by an activation operand whose columns are (token m, 16-group g) the same way, so each
+// output is 4 times one 16-value group sum and its int8 scale is one integer multiply-add.
+// Per superblock, as ggml's vec_dot_q6_K_q8_K:
+//   y += d_x * d * sum_g sc_g sum_{i in g} (q_i - 32) x_i      (the 4 leaves through d_x / 4)
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef int v4i_t __attribute__((ext_vector_type(4)));
@@ -196,7 +197,7 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
 struct GvLane {
     int lane, wave, col, q, m, g;
     bool xlive;  // this lane carries activation data: its k range lies in the column's sub-block / group
-    bool mlive;  // min-term / offset operand column is a real token (cols >= 8 stay zero: M <= 8)
+    bool mlive;  // min-term operand column is a real token (cols >= 8 stay zero: M <= 8)
 };
 
 __device__ __forceinline__ GvLane gv_lane(int M) {
@@ -210,6 +211,11 @@ __device__ __forceinline__ GvLane gv_lane(int M) {
     L.xlive = (L.m < M) && ((L.q >> 1) == L.g);
     L.mlive = L.col < M;
     return L;
+}
+
+__device__ __forceinline__ float2 half2_bits(uint32_t u) {
+    return make_float2((float)__builtin_bit_cast(_Float16, (uint16_t)(u & 0xffff)),
+                       (float)__builtin_bit_cast(_Float16, (uint16_t)(u >> 16)));
 }
 
 struct Q4Act {
@@ -229,9 +235,8 @@ __device__ __forceinline__ Q4Act q4_act(const GvLane &L, const int8_t *xq, const
     return A;
 }
 struct Q4W {  // one (tile, superblock) of the Q4_K GEMV plane, this lane's share
-    v4i_t wq[4], scv;
+    v4i_t wq[4], scv, dd;
     uint32_t mnv;
-    float4 dd0, dd1;
 };
 __device__ __forceinline__ Q4W q4_load(const GvLane &L, const uint8_t *T) {
     Q4W W;
@@ -239,8 +244,7 @@ __device__ __forceinline__ Q4W q4_load(const GvLane &L, const uint8_t *T) {
     for (int c = 0; c < 4; c++) W.wq[c] = *(const v4i_t *)(T + GV4_QS + ((c * 2 + (L.q & 1)) * GV_ROWS + L.col) * 16);
     W.scv = *(const v4i_t *)(T + GV4_SC + (L.g * 4 + L.q) * 16);  // sc of rows 4q+i, chunk c: byte 4c+i
     W.mnv = *(const uint32_t *)(T + GV4_MN + ((L.q & 1) * GV_ROWS + L.col) * 4);
-    W.dd0 = *(const float4 *)(T + GV4_DD + L.q * 32);
-    W.dd1 = *(const float4 *)(T + GV4_DD + L.q * 32 + 16);
+    W.dd = *(const v4i_t *)(T + GV4_DD + L.q * 16);  // (d, dmin) halves of rows 4q..4q+3
     return W;
 }
 __device__ __forceinline__ void q4_compute(const GvLane &L, const Q4W &W, const Q4Act &A, float (&part)[4]) {
@@ -258,49 +262,40 @@ __device__ __forceinline__ void q4_compute(const GvLane &L, const Q4W &W, const 
     const v4h amin = {(_Float16)(float)(W.mnv & 0xff), (_Float16)(float)((W.mnv >> 8) & 0xff),
                       (_Float16)(float)((W.mnv >> 16) & 0xff), (_Float16)(float)(W.mnv >> 24)};
     const v4f fm = __builtin_amdgcn_mfma_f32_16x16x16f16(amin, A.bmin, (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    const float dr[4] = {W.dd0.x, W.dd0.z, W.dd1.x, W.dd1.z}, mr[4] = {W.dd0.y, W.dd0.w, W.dd1.y, W.dd1.w};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
+        const float2 dm = half2_bits((uint32_t)W.dd[i]);
         // column m + 8 (sub-blocks 2c+1) joins column m: row_ror:8 inside each 16-lane row
         const int isum = acc[i] + __builtin_amdgcn_update_dpp(0, acc[i], 0x128, 0xF, 0xF, false);
-        part[i] += A.dx * (dr[i] * (float)isum - mr[i] * fm[i]);
+        part[i] += A.dx * (dm.x * (float)isum - dm.y * fm[i]);
     }
 }
 
 struct Q6Act {
     int64_t xa[8];
-    v4h bofs;
-    float dx;
+    float dx;  // d_x / 4
 };
-__device__ __forceinline__ Q6Act q6_act(const GvLane &L, const int8_t *xq, const float *xd, const int16_t *xbs, int K,
+__device__ __forceinline__ Q6Act q6_act(const GvLane &L, const int8_t *xq, const float *xd, const void *, int K,
                                         int M, int sb) {
     Q6Act A;
     const int8_t *xr = xq + (int64_t)L.m * K + sb * QK_K + 8 * L.q;
 #pragma unroll
     for (int kk = 0; kk < 8; kk++) A.xa[kk] = L.xlive ? *(const int64_t *)(xr + 32 * kk) : 0;
-    int64_t bsv = 0;
-    if (L.mlive) bsv = *(const int64_t *)(xbs + (int64_t)L.col * (K / 16) + sb * 16 + 4 * L.q);
-    A.bofs = (v4h){(_Float16)(32.0f * (float)(int16_t)(bsv & 0xffff)),
-                   (_Float16)(32.0f * (float)(int16_t)((bsv >> 16) & 0xffff)),
-                   (_Float16)(32.0f * (float)(int16_t)((bsv >> 32) & 0xffff)),
-                   (_Float16)(32.0f * (float)(int16_t)((bsv >> 48) & 0xffff))};
-    A.dx = (L.m < M) ? xd[(int64_t)L.m * (K / QK_K) + sb] : 0.0f;
+    A.dx = (L.m < M) ? 0.25f * xd[(int64_t)L.m * (K / QK_K) + sb] : 0.0f;
     return A;
 }
 struct Q6W {  // one (tile, superblock) of the Q6_K GEMV plane, this lane's share
     v4i_t lo0, lo1, hiv, sc0, sc1;
-    uint32_t sc2;
-    float4 dv;
+    uint2 dv;
 };
 __device__ __forceinline__ Q6W q6_load(const GvLane &L, const uint8_t *T) {
     Q6W W;
-    W.lo0 = *(const v4i_t *)(T + GV6_LO + (L.q * GV_ROWS + L.col) * 32);
-    W.lo1 = *(const v4i_t *)(T + GV6_LO + (L.q * GV_ROWS + L.col) * 32 + 16);
+    W.lo0 = *(const v4i_t *)(T + GV6_LO + (L.q * GV_ROWS + L.col) * 16);
+    W.lo1 = *(const v4i_t *)(T + GV6_LO + 1024 + (L.q * GV_ROWS + L.col) * 16);
     W.hiv = *(const v4i_t *)(T + GV6_HI + (L.q * GV_ROWS + L.col) * 16);
     W.sc0 = *(const v4i_t *)(T + GV6_SC + (L.g * 4 + L.q) * 32);
     W.sc1 = *(const v4i_t *)(T + GV6_SC + (L.g * 4 + L.q) * 32 + 16);
-    W.sc2 = *(const uint32_t *)(T + GV6_SC2 + (L.q * GV_ROWS + L.col) * 4);
-    W.dv = *(const float4 *)(T + GV6_D + L.q * 16);
+    W.dv = *(const uint2 *)(T + GV6_D + L.q * 8);  // d halves of rows 4q..4q+3
     return W;
 }
 __device__ __forceinline__ void q6_compute(const GvLane &L, const Q6W &W, const Q6Act &A, float (&part)[4]) {
@@ -310,97 +305,171 @@ __device__ __forceinline__ void q6_compute(const GvLane &L, const Q6W &W, const 
     int acc[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int kk = 0; kk < 8; kk++) {
-        const uint32_t h = (uint32_t)his[kk >> 1];
-        const uint32_t h0 = (kk & 1) ? h : (h << 4), h1 = (kk & 1) ? (h >> 2) : (h << 2);
-        const uint32_t w0 = ((uint32_t)los[kk] & 0x0F0F0F0Fu) | (h0 & 0x30303030u);
-        const uint32_t w1 = (((uint32_t)los[kk] >> 4) & 0x0F0F0F0Fu) | (h1 & 0x30303030u);
+        // bytes 4 v: low nibble of v into bits 2-5, its two high bits into bits 6-7
+        const uint32_t h = (uint32_t)his[kk >> 1], lo = (uint32_t)los[kk];
+        const uint32_t h0 = (kk & 1) ? (h << 2) : (h << 6), h1 = (kk & 1) ? h : (h << 4);
+        const uint32_t w0 = ((lo << 2) & 0x3C3C3C3Cu) | (h0 & 0xC0C0C0C0u);
+        const uint32_t w1 = ((lo >> 2) & 0x3C3C3C3Cu) | (h1 & 0xC0C0C0C0u);
         const int64_t w = (int64_t)w0 | ((int64_t)w1 << 32);
         const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(w, A.xa[kk], (v4i_t){0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[i] += __mul24((int)(int8_t)(scs[kk] >> (8 * i)), d[i]);  // |d| < 2^23
     }
-    const v4h asc = {(_Float16)(float)(int8_t)(W.sc2 & 0xff), (_Float16)(float)(int8_t)((W.sc2 >> 8) & 0xff),
-                     (_Float16)(float)(int8_t)((W.sc2 >> 16) & 0xff), (_Float16)(float)(int8_t)(W.sc2 >> 24)};
-    const v4f corr = __builtin_amdgcn_mfma_f32_16x16x16f16(asc, A.bofs, (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    const float dr[4] = {W.dv.x, W.dv.y, W.dv.z, W.dv.w};
+    const float2 d01 = half2_bits(W.dv.x), d23 = half2_bits(W.dv.y);
+    const float dr[4] = {d01.x, d01.y, d23.x, d23.y};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         // column m + 8 (odd 16-groups) joins column m: row_ror:8 inside each 16-lane row
         const int isum = acc[i] + __builtin_amdgcn_update_dpp(0, acc[i], 0x128, 0xF, 0xF, false);
-        part[i] += A.dx * (dr[i] * ((float)isum - corr[i]));
+        part[i] += A.dx * (dr[i] * (float)isum);
     }
 }
 
-// One workgroup per RT row tiles: wave w takes superblocks w, w+8, ... of K, builds their
-// activation operands once, and issues the weight loads of all RT tiles before computing
-// (many small workgroups in flight hide the HBM latency; RT > 1 spreads the activation
-// operand loads over more weight bytes).  The 8 waves' partial 16-row tiles are summed in LDS.
-template <int TYPE, int RT>
-__global__ __launch_bounds__(512) void k_gemv_kq_mfma(const uint8_t *__restrict__ gv, const int8_t *__restrict__ xq,
-                                                      const float *__restrict__ xd, const void *__restrict__ xaux,
-                                                      float *__restrict__ y, int N, int K, int M, int64_t ldy) {
+// Persistent form: a workgroup of 8 waves walks row tiles t = blockIdx.x, + gridDim.x, ...;
+// wave w owns superblocks w, w + 8, ... (SBW <= 3 of them, K <= 2048 SBW) and builds their
+// activation operands once.  Per tile it issues the weight loads of the NEXT tile before
+// computing this one, writes its 16-row partial sums to LDS and, after one barrier, the
+// workgroup reduces them (double-buffered, so one barrier per tile) and stores the rows.
+template <int TYPE, int SBW, int PF>
+__global__ __launch_bounds__(512) void k_gemv_kq_stream(const uint8_t *__restrict__ gv, const int8_t *__restrict__ xq,
+                                                        const float *__restrict__ xd, const void *__restrict__ xaux,
+                                                        float *__restrict__ y, int N, int K, int M, int64_t ldy) {
     constexpr bool Q4 = TYPE == MQ_TYPE_Q4_K;
     constexpr int BYTES = Q4 ? GV4_BYTES : GV6_BYTES;
     using W = typename std::conditional<Q4, Q4W, Q6W>::type;
-    __shared__ float red[RT][8][GV_ROWS][8];
+    using A = typename std::conditional<Q4, Q4Act, Q6Act>::type;
+    __shared__ float red[2][8][GV_ROWS][8];
     const GvLane L = gv_lane(M);
     const int nsb = K / QK_K;
     const int ntiles = (N + GV_ROWS - 1) / GV_ROWS;
-    const int tile0 = blockIdx.x * RT;
-    float part[RT][4];
+    bool live[SBW];
+    A act[SBW];
 #pragma unroll
-    for (int r = 0; r < RT; r++) part[r][0] = part[r][1] = part[r][2] = part[r][3] = 0.f;
-    for (int sb = L.wave; sb < nsb; sb += 8) {
-        W w[RT];
+    for (int i = 0; i < SBW; i++) {
+        const int sb = L.wave + 8 * i;
+        live[i] = sb < nsb;
+        if (live[i]) {
+            if constexpr (Q4) act[i] = q4_act(L, xq, xd, (const _Float16 *)xaux, K, M, sb);
+            else act[i] = q6_act(L, xq, xd, xaux, K, M, sb);
+        }
+    }
+    auto load = [&](W (&w)[SBW], int t) {
 #pragma unroll
-        for (int r = 0; r < RT; r++) {
-            if (tile0 + r < ntiles) {
-                const uint8_t *T = gv + ((int64_t)(tile0 + r) * nsb + sb) * BYTES;
-                if constexpr (Q4) w[r] = q4_load(L, T);
-                else w[r] = q6_load(L, T);
+        for (int i = 0; i < SBW; i++)
+            if (live[i] && t < ntiles) {
+                const uint8_t *T = gv + ((int64_t)t * nsb + L.wave + 8 * i) * BYTES;
+                if constexpr (Q4) w[i] = q4_load(L, T);
+                else w[i] = q6_load(L, T);
             }
-        }
-        if constexpr (Q4) {
-            const Q4Act A = q4_act(L, xq, xd, (const _Float16 *)xaux, K, M, sb);
+    };
+    // ring of PF + 1 register sets: the loads of the PF tiles after this one are in flight
+    W ring[PF + 1][SBW];
+    int t = blockIdx.x;
 #pragma unroll
-            for (int r = 0; r < RT; r++)
-                if (tile0 + r < ntiles) q4_compute(L, w[r], A, part[r]);
-        } else {
-            const Q6Act A = q6_act(L, xq, xd, (const int16_t *)xaux, K, M, sb);
+    for (int f = 0; f < PF; f++) load(ring[f], t + f * (int)gridDim.x);
+    for (int it = 0; t < ntiles; it++, t += gridDim.x) {
+        load(ring[PF], t + PF * (int)gridDim.x);
+        W (&cur)[SBW] = ring[0];
+        float part[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int r = 0; r < RT; r++)
-                if (tile0 + r < ntiles) q6_compute(L, w[r], A, part[r]);
+        for (int i = 0; i < SBW; i++)
+            if (live[i]) {
+                if constexpr (Q4) q4_compute(L, cur[i], act[i], part);
+                else q6_compute(L, cur[i], act[i], part);
+            }
+        const int buf = it & 1;
+        if (L.col < 8) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) red[buf][L.wave][4 * L.q + i][L.col] = part[i];
         }
+        __syncthreads();
+        if (threadIdx.x < GV_ROWS * 8) {
+            const int rr = threadIdx.x >> 3, mm = threadIdx.x & 7;
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < 8; w++) sum += red[buf][w][rr][mm];
+            const int64_t row = (int64_t)t * GV_ROWS + rr;
+            if (row < N && mm < M) y[(int64_t)mm * ldy + row] = sum;
+        }
+#pragma unroll
+        for (int f = 0; f < PF; f++)
+#pragma unroll
+            for (int i = 0; i < SBW; i++) ring[f][i] = ring[f + 1][i];
+    }
+}
+
+// Any K: per tile, wave w walks superblocks w, w + 8, ... building their activation
+// operands as it goes (no operand cache, no prefetch beyond what the waves overlap).
+template <int TYPE>
+__global__ __launch_bounds__(512) void k_gemv_kq_any(const uint8_t *__restrict__ gv, const int8_t *__restrict__ xq,
+                                                     const float *__restrict__ xd, const void *__restrict__ xaux,
+                                                     float *__restrict__ y, int N, int K, int M, int64_t ldy) {
+    constexpr bool Q4 = TYPE == MQ_TYPE_Q4_K;
+    constexpr int BYTES = Q4 ? GV4_BYTES : GV6_BYTES;
+    __shared__ float red[8][GV_ROWS][8];
+    const GvLane L = gv_lane(M);
+    const int nsb = K / QK_K;
+    const int t = blockIdx.x;
+    float part[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int sb = L.wave; sb < nsb; sb += 8) {
+        const uint8_t *T = gv + ((int64_t)t * nsb + sb) * BYTES;
+        if constexpr (Q4) q4_compute(L, q4_load(L, T), q4_act(L, xq, xd, (const _Float16 *)xaux, K, M, sb), part);
+        else q6_compute(L, q6_load(L, T), q6_act(L, xq, xd, xaux, K, M, sb), part);
     }
     if (L.col < 8) {
 #pragma unroll
-        for (int r = 0; r < RT; r++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) red[r][L.wave][4 * L.q + i][L.col] = part[r][i];
+        for (int i = 0; i < 4; i++) red[L.wave][4 * L.q + i][L.col] = part[i];
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < RT * GV_ROWS * 8; t += blockDim.x) {
-        const int r = t / (GV_ROWS * 8), rr = (t / 8) % GV_ROWS, mm = t & 7;
+    if (threadIdx.x < GV_ROWS * 8) {
+        const int rr = threadIdx.x >> 3, mm = threadIdx.x & 7;
         float sum = 0.f;
 #pragma unroll
-        for (int w = 0; w < 8; w++) sum += red[r][w][rr][mm];
-        const int64_t row = (int64_t)(tile0 + r) * GV_ROWS + rr;
+        for (int w = 0; w < 8; w++) sum += red[w][rr][mm];
+        const int64_t row = (int64_t)t * GV_ROWS + rr;
         if (row < N && mm < M) y[(int64_t)mm * ldy + row] = sum;
     }
 }
 
 template <int TYPE>
-static hipError_t launch_kq_mfma(const uint8_t *gv, const int8_t *xq, const float *xd, const void *xaux, float *y,
-                                 int64_t n, int64_t k, int m, int64_t ldy, hipStream_t s) {
+static hipError_t launch_kq_stream(const uint8_t *gv, const int8_t *xq, const float *xd, const void *xaux, float *y,
+                                   int64_t n, int64_t k, int m, int64_t ldy, hipStream_t s) {
     const int64_t ntiles = (n + GV_ROWS - 1) / GV_ROWS;
+    const int nsb = (int)(k / QK_K);
+    const int sbw = (nsb + 7) / 8;
+    static int ncu = 0;
+    if (!ncu) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+            v = 256;
+        ncu = v;
+    }
+    // workgroups per CU (at most what fits: two at one cached superblock per wave, one
+    // beyond, register-bound); MQ_GEMV_WGS overrides for measurements
+    int per_cu = sbw == 1 ? 2 : 1;
+    if (const char *e = getenv("MQ_GEMV_WGS"))
+        if (atoi(e) >= 1 && atoi(e) <= 4) per_cu = atoi(e);
+    const unsigned grid = (unsigned)std::min<int64_t>(ntiles, (int64_t)ncu * per_cu);
     const dim3 block(512);
-    // two row tiles per workgroup once that still leaves several workgroups per CU
-    if (ntiles >= 4096)
-        hipLaunchKernelGGL((k_gemv_kq_mfma<TYPE, 2>), dim3((unsigned)((ntiles + 1) / 2)), block, 0, s, gv, xq, xd, xaux,
-                           y, (int)n, (int)k, m, ldy);
-    else
-        hipLaunchKernelGGL((k_gemv_kq_mfma<TYPE, 1>), dim3((unsigned)ntiles), block, 0, s, gv, xq, xd, xaux, y, (int)n,
-                           (int)k, m, ldy);
+    const char *pe = getenv("MQ_GEMV_PF");
+    const int pf = pe ? atoi(pe) : 2;
+    if (pf == 3 && sbw == 1) {
+        hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 3>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy);
+        return hipSuccess;
+    }
+    if (pf == 2 && sbw == 1) {
+        hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 2>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy);
+        return hipSuccess;
+    }
+    switch (sbw) {
+        case 1: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 1>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy); break;
+        case 2: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 2, 1>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy); break;
+        case 3: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 3, 1>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy); break;
+        default:
+            hipLaunchKernelGGL((k_gemv_kq_any<TYPE>), dim3((unsigned)ntiles), block, 0, s, gv, xq, xd, xaux, y, (int)n,
+                               (int)k, m, ldy);
+            break;
+    }
     return hipSuccess;
 }
 
@@ -412,8 +481,8 @@ static hipError_t gemv_launch(int type, const uint8_t *wb, const WeightPlanes &p
     const float *xd = (const float *)(xb + ap.xd);
     const int16_t *xbs = (const int16_t *)(xb + ap.xbs);
     switch (type) {
-        case MQ_TYPE_Q4_K: return launch_kq_mfma<MQ_TYPE_Q4_K>(wb + p.gv, xq, xd, xb + ap.xgm, y, n, k, MM, ldy, s);
-        case MQ_TYPE_Q6_K: return launch_kq_mfma<MQ_TYPE_Q6_K>(wb + p.gv, xq, xd, xbs, y, n, k, MM, ldy, s);
+        case MQ_TYPE_Q4_K: return launch_kq_stream<MQ_TYPE_Q4_K>(wb + p.gv, xq, xd, xb + ap.xgm, y, n, k, MM, ldy, s);
+        case MQ_TYPE_Q6_K: return launch_kq_stream<MQ_TYPE_Q6_K>(wb + p.gv, xq, xd, xbs, y, n, k, MM, ldy, s);
         case MQ_TYPE_Q8_0:
             hipLaunchKernelGGL(k_gemv_q8_0<MM>, grid, block, 0, s, (const int8_t *)(wb + p.qs),
                                (const uint16_t *)(wb + p.d16), xq, xd, y, (int)n, (int)k, ldy);

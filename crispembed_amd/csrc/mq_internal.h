@@ -60,8 +60,8 @@ __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size
 constexpr int TILE_ROWS = 256;
 // Q4_K GEMV plane: one tile = 16 weight rows x one 256-value superblock
 constexpr int GV_ROWS = 16;
-constexpr int GV4_QS = 0, GV4_SC = 2048, GV4_MN = 2176, GV4_DD = 2304, GV4_BYTES = 2432;
-constexpr int GV6_LO = 0, GV6_HI = 2048, GV6_SC = 3072, GV6_SC2 = 3328, GV6_D = 3584, GV6_BYTES = 3648;
+constexpr int GV4_QS = 0, GV4_SC = 2048, GV4_MN = 2176, GV4_DD = 2304, GV4_BYTES = 2368;
+constexpr int GV6_LO = 0, GV6_HI = 2048, GV6_SC = 3072, GV6_D = 3328, GV6_BYTES = 3360;  // = 16 GGUF blocks
 constexpr int KSTAGE = 128;
 
 __host__ __device__ inline int64_t pad_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
@@ -75,18 +75,19 @@ __host__ __device__ inline int64_t tiled_off(int64_t r, int64_t kb, int64_t kb_p
 // Weight image: GGUF bytes, then planes (each 256-byte aligned).
 //  GEMV planes (row-major, byte-identical to the GGUF fields):
 //   Q8_0: qs  i8 [n][k]            d16  u16 [n][k/32]
-//   Q6_K: gv  [ceil(n/16)][k/256] tiles of GV6_BYTES, the operands of the MFMA GEMV, with
-//         q = the unsigned 6-bit quant (q6 - 32 is the value) of value 32kk+8p+b (b < 8) of
-//         row r (K-step kk, lane group p):
-//           lo [p][r][kk] u32: byte j = (q_j & 15) | (q_{j+4} & 15) << 4
-//           hi [p][r][kk/2] u32: byte j holds (q >> 4) of q_j, q_{j+4} of step 2*(kk/2)
+//   Q6_K: gv  [ceil(n/16)][k/256] tiles of GV6_BYTES (the GGUF size of 16 rows), the
+//         operands of the MFMA GEMV, with v = q ^ 32 = the 6-bit two's complement of q - 32
+//         (q the unsigned 6-bit quant) of value 32kk+8p+b (b < 8) of row r (K-step kk,
+//         lane group p):
+//           lo [kk/4][p][r][kk%4] u32: byte j = (v_j & 15) | (v_{j+4} & 15) << 4
+//           hi [p][r][kk/2] u32: byte j holds (v >> 4) of v_j, v_{j+4} of step 2*(kk/2)
 //              (bits 0-1, 2-3) and of step 2*(kk/2)+1 (bits 4-5, 6-7)
-//           sc [g][r/4][kk][r%4] i8 = scale of 16-group 2kk+g;  sc2 [p][r][t] i8 = scale of
-//           16-group 4p+t;  d [r] f32; rows past n are zero
+//           sc [g][r/4][kk][r%4] i8 = scale of 16-group 2kk+g;  d [r] f16 (the GGUF half);
+//           rows past n are zero
 //   Q4_K: gv  [ceil(n/16)][k/256] tiles of GV4_BYTES (16 rows x one superblock), the
 //         operands of the MFMA GEMV: qs [chunk c][half h][row r][16 B] (GGUF qs bytes
 //         32c+16h..+16 of row r), sc [g][r/4][c][r%4] (u8 sc_{2c+g}), mn [half][r][4]
-//         (u8 m_{4*half+t}), dd [r][2] f32 (d, dmin); rows past n are zero
+//         (u8 m_{4*half+t}), dd [r][2] f16 (d, dmin, the GGUF halves); rows past n are zero
 //   (F16 GEMVs read the GGUF rows directly)
 //  GEMM planes (tiled, n padded to n_pad = pad(n, 256)):
 //   Q8_0: tq  i8 tiled [n_pad][kb_pad]     tdw f32 [kb_pad/32][n_pad]

@@ -580,13 +580,13 @@ __global__ __launch_bounds__(256) void k_prepare_q6_K_gv(const uint8_t *__restri
             uint32_t lo = 0;
             for (int j = 0; j < 4; j++) {
                 const int e = 32 * kk + 8 * p + j;
-                const uint32_t qa = live ? (uint32_t)q6_value(blk, e) : 0u;
-                const uint32_t qb = live ? (uint32_t)q6_value(blk, e + 4) : 0u;
+                const uint32_t qa = live ? (uint32_t)q6_value(blk, e) ^ 32u : 0u;  // 6-bit two's complement of q - 32
+                const uint32_t qb = live ? (uint32_t)q6_value(blk, e + 4) ^ 32u : 0u;
                 lo |= ((qa & 15) | ((qb & 15) << 4)) << (8 * j);
                 const int sh = 8 * j + 4 * (kk & 1);
                 his[kk >> 1] |= ((qa >> 4) << sh) | ((qb >> 4) << (sh + 2));
             }
-            ((uint32_t *)(T + GV6_LO))[(p * GV_ROWS + r) * 8 + kk] = lo;
+            ((uint32_t *)(T + GV6_LO))[(((kk >> 2) * 4 + p) * GV_ROWS + r) * 4 + (kk & 3)] = lo;
         }
         for (int hp = 0; hp < 4; hp++) ((uint32_t *)(T + GV6_HI))[(p * GV_ROWS + r) * 4 + hp] = his[hp];
     }
@@ -595,11 +595,8 @@ __global__ __launch_bounds__(256) void k_prepare_q6_K_gv(const uint8_t *__restri
         const int8_t sc = live ? scl[grp] : (int8_t)0;
         const int kk = grp >> 1, g = grp & 1;
         ((int8_t *)(T + GV6_SC))[((g * 4 + r / 4) * 8 + kk) * 4 + (r & 3)] = sc;
-        ((int8_t *)(T + GV6_SC2))[((grp >> 2) * GV_ROWS + r) * 4 + (grp & 3)] = sc;
     }
-    float d = 0.f;
-    if (live) d = (float)__builtin_bit_cast(_Float16, (uint16_t)(blk[208] | (blk[209] << 8)));
-    ((float *)(T + GV6_D))[r] = d;
+    ((uint16_t *)(T + GV6_D))[r] = live ? (uint16_t)(blk[208] | (blk[209] << 8)) : (uint16_t)0;
 }
 
 // Q6_K: limbs of sc * (q6 - 32) (lo = v & 127, hi = v >> 7 arithmetic), per-superblock d.
@@ -816,11 +813,6 @@ __global__ __launch_bounds__(256) void k_prepare_q4_K_gv(const uint8_t *__restri
             }
             *(int4 *)(T + GV4_QS + ((c * 2 + h) * GV_ROWS + r) * 16) = v;
         }
-    float d = 0.f, dmin = 0.f;
-    if (live) {
-        d = (float)__builtin_bit_cast(_Float16, *(const uint16_t *)blk);
-        dmin = (float)__builtin_bit_cast(_Float16, *(const uint16_t *)(blk + 2));
-    }
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         int sc = 0, mn = 0;
@@ -828,8 +820,7 @@ __global__ __launch_bounds__(256) void k_prepare_q4_K_gv(const uint8_t *__restri
         T[GV4_SC + (((j & 1) * 4 + r / 4) * 4 + (j >> 1)) * 4 + (r & 3)] = (uint8_t)sc;
         T[GV4_MN + ((j >> 2) * GV_ROWS + r) * 4 + (j & 3)] = (uint8_t)mn;
     }
-    ((float *)(T + GV4_DD))[2 * r] = d;
-    ((float *)(T + GV4_DD))[2 * r + 1] = dmin;
+    ((uint32_t *)(T + GV4_DD))[r] = live ? *(const uint32_t *)blk : 0u;  // d, dmin halves
 }
 
 hipError_t launch_weight_prepare(int type, void *image, int64_t n, int64_t k, int64_t row0, int64_t row1,
