@@ -70,6 +70,19 @@ class BertEncoder:
                 p(lay["bq"]), p(lay["bk"]), p(lay["bv"]), p(lay["bo"]), p(lay["bfc1"]), p(lay["bfc2"]),
                 p(lay["ln1_w"]), p(lay["ln1_b"]), p(lay["ln2_w"]), p(lay["ln2_b"])))
 
+    @classmethod
+    def from_gguf(cls, path):
+        """A model loaded from a CrispEmbed BERT GGUF by the native loader (mq_bert_load)."""
+        self = cls.__new__(cls)
+        self.L = mq.lib()
+        self.h = self.L.mq_bert_load(str(path).encode())
+        if not self.h:
+            raise mq.MQError(self.L.mq_last_error().decode())
+        c = mq.BertHparams()
+        mq.check(self.L.mq_bert_get_hparams(self.h, ctypes.byref(c)))
+        self.hp = {f: getattr(c, f) for f, _ in c._fields_}
+        return self
+
     def encode(self, ids_dev, B, T, out_dev, stream, types_dev=None, hidden_dev=None):
         mq.check(self.L.mq_bert_encode(self.h, ctypes.c_void_p(ids_dev), ctypes.c_void_p(types_dev or 0), B, T,
                                        ctypes.c_void_p(out_dev), ctypes.c_void_p(hidden_dev or 0), stream))

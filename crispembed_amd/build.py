@@ -38,6 +38,8 @@ MQ_SOURCES = [
     ("mq_bert.cpp", ["-x", "hip"]),
     ("mq_decoder.hip", []),
     ("mq_decoder_run.cpp", ["-x", "hip"]),
+    ("mq_gguf.cpp", ["-x", "hip"]),
+    ("mq_gguf_load.cpp", ["-x", "hip"]),
 ]
 # The backend compiles against ggml's backend headers.  Standalone builds use the
 # compat transcription in csrc/ggml_compat (and libggml-compat.so for the ggml

@@ -159,3 +159,9 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
     }
     return hip_rc(launch_mean_pool_l2(X, out, B, T, (int)H, s), "pooling");
 }
+
+extern "C" int mq_bert_get_hparams(const mq_bert *m, mq_bert_hparams *hp) {
+    if (!m || !hp) return set_error(MQ_EINVAL, "NULL runner or output");
+    *hp = m->hp;
+    return MQ_OK;
+}

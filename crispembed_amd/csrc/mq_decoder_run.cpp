@@ -226,3 +226,9 @@ extern "C" int mq_attention(const float *qkv, int64_t ld, float *out, int64_t ld
                                    nullptr, 0.f, nullptr, workspace, (hipStream_t)stream),
                   "attention");
 }
+
+extern "C" int mq_decoder_get_hparams(const mq_decoder *m, mq_decoder_hparams *hp) {
+    if (!m || !hp) return set_error(MQ_EINVAL, "NULL runner or output");
+    *hp = m->hp;
+    return MQ_OK;
+}

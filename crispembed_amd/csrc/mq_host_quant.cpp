@@ -344,5 +344,75 @@ size_t quantize_chunk(int type, const float *src, void *dst, int64_t nrows, int6
     return rs * (size_t)nrows;
 }
 
+// Host dequantization of GGUF rows to fp32, as ggml's dequantize_row_* (the get_rows of an
+// embedding table): Q8_0 d*q; Q4_K d*sc_j*q - dmin*m_j; Q6_K d*sc*(q6 - 32); F16 exact.
+// Returns false for a type it does not decode.
+bool dequantize_rows(int type, const void *src, float *dst, int64_t nrows, int64_t k) {
+    const int64_t bs = blck_size(type);
+    if (!src || !dst || nrows < 0 || k <= 0 || bs == 0 || k % bs != 0) return false;
+    const size_t rs = row_size(type, k);
+    for (int64_t r = 0; r < nrows; r++) {
+        const uint8_t *x = (const uint8_t *)src + r * rs;
+        float *y = dst + r * k;
+        switch (type) {
+            case MQ_TYPE_F32: std::memcpy(y, x, (size_t)k * 4); break;
+            case MQ_TYPE_F16: {
+                const uint16_t *h = (const uint16_t *)x;
+                for (int64_t i = 0; i < k; i++) y[i] = fp16_to_fp32(h[i]);
+                break;
+            }
+            case MQ_TYPE_Q8_0:
+                for (int64_t b = 0; b < k / QK8_0; b++) {
+                    const block_q8_0 &q = ((const block_q8_0 *)x)[b];
+                    const float d = fp16_to_fp32(q.d);
+                    for (int i = 0; i < QK8_0; i++) y[b * QK8_0 + i] = d * (float)q.qs[i];
+                }
+                break;
+            case MQ_TYPE_Q4_K:
+                for (int64_t b = 0; b < k / QK_K; b++) {
+                    const block_q4_K &q = ((const block_q4_K *)x)[b];
+                    const float d = fp16_to_fp32(q.d), dmin = fp16_to_fp32(q.dmin);
+                    float *yb = y + b * QK_K;
+                    for (int c = 0; c < 4; c++) {
+                        int sc0, m0, sc1, m1;
+                        unpack_scale_min(2 * c, q.scales, sc0, m0);
+                        unpack_scale_min(2 * c + 1, q.scales, sc1, m1);
+                        const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
+                        const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
+                        for (int l = 0; l < 32; l++) {
+                            yb[64 * c + l] = d1 * (float)(q.qs[32 * c + l] & 0xF) - mm1;
+                            yb[64 * c + 32 + l] = d2 * (float)(q.qs[32 * c + l] >> 4) - mm2;
+                        }
+                    }
+                }
+                break;
+            case MQ_TYPE_Q6_K:
+                for (int64_t b = 0; b < k / QK_K; b++) {
+                    const block_q6_K &q = ((const block_q6_K *)x)[b];
+                    const float d = fp16_to_fp32(q.d);
+                    float *yb = y + b * QK_K;
+                    for (int h = 0; h < 2; h++) {
+                        const uint8_t *ql = q.ql + 64 * h, *qh = q.qh + 32 * h;
+                        const int8_t *sc = q.scales + 8 * h;
+                        for (int l = 0; l < 32; l++) {
+                            const int is = l / 16;
+                            const int q1 = (int)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                            const int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                            const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                            const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                            yb[128 * h + l] = d * (float)sc[is] * (float)q1;
+                            yb[128 * h + l + 32] = d * (float)sc[is + 2] * (float)q2;
+                            yb[128 * h + l + 64] = d * (float)sc[is + 4] * (float)q3;
+                            yb[128 * h + l + 96] = d * (float)sc[is + 6] * (float)q4;
+                        }
+                    }
+                }
+                break;
+            default: return false;
+        }
+    }
+    return true;
+}
+
 }  // namespace host
 }  // namespace mq

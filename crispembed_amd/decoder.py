@@ -57,6 +57,19 @@ class DecoderEmbedder:
                 self.h, il, p(lay["wq"]), p(lay["wk"]), p(lay["wv"]), p(lay["wo"]), p(lay["wgate"]), p(lay["wup"]),
                 p(lay["wdown"]), p(lay["attn_norm"]), p(lay["ffn_norm"]), p(lay.get("q_norm")), p(lay.get("k_norm"))))
 
+    @classmethod
+    def from_gguf(cls, path):
+        """A model loaded from a CrispEmbed decoder GGUF by the native loader (mq_decoder_load)."""
+        self = cls.__new__(cls)
+        self.L = mq.lib()
+        self.h = self.L.mq_decoder_load(str(path).encode())
+        if not self.h:
+            raise mq.MQError(self.L.mq_last_error().decode())
+        c = mq.DecoderHparams()
+        mq.check(self.L.mq_decoder_get_hparams(self.h, ctypes.byref(c)))
+        self.hp = {f: getattr(c, f) for f, _ in c._fields_}
+        return self
+
     def encode(self, ids_dev, B, T, out_dev, stream, hidden_dev=None):
         mq.check(self.L.mq_decoder_encode(self.h, ctypes.c_void_p(ids_dev), B, T, ctypes.c_void_p(out_dev),
                                           ctypes.c_void_p(hidden_dev or 0), stream))

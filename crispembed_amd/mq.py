@@ -60,6 +60,35 @@ _SIGS = {
     "mq_bert_set_embeddings": (_c_int, [_c_vp] * 6),
     "mq_bert_set_layer": (_c_int, [_c_vp, _c_int] + [_c_vp] * 16),
     "mq_bert_encode": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp]),
+    # include/mq_gguf.h
+    "mq_gguf_open": (_c_vp, [ctypes.c_char_p]),
+    "mq_gguf_close": (None, [_c_vp]),
+    "mq_gguf_version": (ctypes.c_uint32, [_c_vp]),
+    "mq_gguf_alignment": (_c_sz, [_c_vp]),
+    "mq_gguf_data_offset": (_c_sz, [_c_vp]),
+    "mq_gguf_n_kv": (_c_i64, [_c_vp]),
+    "mq_gguf_find_key": (_c_i64, [_c_vp, ctypes.c_char_p]),
+    "mq_gguf_kv_key": (ctypes.c_char_p, [_c_vp, _c_i64]),
+    "mq_gguf_kv_type": (_c_int, [_c_vp, _c_i64]),
+    "mq_gguf_arr_type": (_c_int, [_c_vp, _c_i64]),
+    "mq_gguf_arr_n": (_c_i64, [_c_vp, _c_i64]),
+    "mq_gguf_arr_data": (_c_vp, [_c_vp, _c_i64]),
+    "mq_gguf_arr_str": (ctypes.c_char_p, [_c_vp, _c_i64, _c_i64]),
+    "mq_gguf_kv_data": (_c_vp, [_c_vp, _c_i64]),
+    "mq_gguf_get_u32": (ctypes.c_uint32, [_c_vp, ctypes.c_char_p, ctypes.c_uint32]),
+    "mq_gguf_get_i32": (ctypes.c_int32, [_c_vp, ctypes.c_char_p, ctypes.c_int32]),
+    "mq_gguf_get_f32": (ctypes.c_float, [_c_vp, ctypes.c_char_p, ctypes.c_float]),
+    "mq_gguf_get_bool": (_c_int, [_c_vp, ctypes.c_char_p, _c_int]),
+    "mq_gguf_get_str": (ctypes.c_char_p, [_c_vp, ctypes.c_char_p, ctypes.c_char_p]),
+    "mq_gguf_n_tensors": (_c_i64, [_c_vp]),
+    "mq_gguf_find_tensor": (_c_i64, [_c_vp, ctypes.c_char_p]),
+    "mq_gguf_tensor_name": (ctypes.c_char_p, [_c_vp, _c_i64]),
+    "mq_gguf_tensor_info": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
+    "mq_gguf_tensor_data": (_c_vp, [_c_vp, _c_i64]),
+    "mq_bert_load": (_c_vp, [ctypes.c_char_p]),
+    "mq_decoder_load": (_c_vp, [ctypes.c_char_p]),
+    "mq_bert_get_hparams": (_c_int, [_c_vp, _c_vp]),
+    "mq_decoder_get_hparams": (_c_int, [_c_vp, _c_vp]),
     # include/mq_decoder.h
     "mq_decoder_create": (_c_vp, [_c_vp]),
     "mq_decoder_free": (None, [_c_vp]),

@@ -17,7 +17,7 @@ def _declared(header):
 def test_libmq_exports_all_declared_symbols():
     from crispembed_amd import mq
     L = mq.lib()
-    names = _declared("mq.h") + _declared("mq_bert.h") + _declared("mq_decoder.h")
+    names = _declared("mq.h") + _declared("mq_bert.h") + _declared("mq_decoder.h") + _declared("mq_gguf.h")
     assert len(names) >= 30
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing, missing
