@@ -72,15 +72,16 @@ struct GemmArgs {
     int tiles_m, tiles_n, group_m;
 };
 
-constexpr int KC = 2;     // 32-byte K chunks per stage (64 bytes of K)
 constexpr int NBUF = 4;   // stage ring in LDS
 constexpr int DIST = 3;   // stages in flight ahead of the newest one being computed
-constexpr int SPB = 4;    // stages per 256-value superblock
 static_assert(DIST + 1 <= NBUF, "stage ring: DIST stages in flight plus the one being computed");
 
-// WM x WN waves per workgroup, each wave TM x TN MFMA tiles of 32x32.
-template <int FMT, int WM, int WN, int TM, int TN>
+// WM x WN waves per workgroup, each wave TM x TN MFMA tiles of 32x32; stages of KC 32-byte
+// K chunks (64 bytes by default; 32 halves the ring so two workgroups share a CU).
+template <int FMT, int WM, int WN, int TM, int TN, int KCT = 2>
 struct Cfg {
+    static constexpr int KC = KCT;              // 32-byte K chunks per stage
+    static constexpr int SPB = 256 / (32 * KC);  // stages per 256-value superblock
     static constexpr int NW = WM * WN, NT = 64 * NW, BM = 32 * TM * WM, BN = 32 * TN * WN;
     static constexpr bool limbs = (FMT == FMT_Q4_K || FMT == FMT_Q6_K);
     static constexpr int NPL = limbs ? 2 : 1;
@@ -177,28 +178,28 @@ __device__ __forceinline__ DmaItem stage_item(const GemmArgs &a, int f, int m0, 
     DmaItem it;
     it.pieces = 64;
     if (f < C::XF) {
-        const int rt = f / KC, kc = f % KC;
+        const int rt = f / C::KC, kc = f % C::KC;
         it.g0 = a.xq + ((int64_t)((m0 >> 5) + rt) * a.kch + kc) * 1024;
-        it.step = KC * 1024;
+        it.step = C::KC * 1024;
         it.lds = f * 1024;
     } else if (f < C::XF + C::NPL * C::WF) {
         const int f2 = f - C::XF;
         const int pl = f2 / C::WF, f3 = f2 % C::WF;
-        const int ct = f3 / KC, kc = f3 % KC;
+        const int ct = f3 / C::KC, kc = f3 % C::KC;
         it.g0 = (pl ? a.whi : a.wq) + ((int64_t)((n0 >> 5) + ct) * a.kch + kc) * 1024;
-        it.step = KC * 1024;
+        it.step = C::KC * 1024;
         it.lds = C::X_BYTES + pl * C::W_BYTES + f3 * 1024;
     } else {
         const int f4 = f - C::XF - C::NPL * C::WF;  // Q8_0 scale rows
-        if (f4 < KC) {
+        if (f4 < C::KC) {
             it.g0 = (const int8_t *)(a.xd + (int64_t)f4 * a.m_pad + m0);
-            it.step = (int64_t)KC * a.m_pad * 4;
+            it.step = (int64_t)C::KC * a.m_pad * 4;
             it.lds = C::X_BYTES + C::W_BYTES + f4 * 1024;
             it.pieces = C::BM / 4;
         } else {
-            it.g0 = (const int8_t *)(a.wd + (int64_t)(f4 - KC) * a.n_pad + n0);
-            it.step = (int64_t)KC * a.n_pad * 4;
-            it.lds = C::X_BYTES + C::W_BYTES + C::SCX + (f4 - KC) * 1024;
+            it.g0 = (const int8_t *)(a.wd + (int64_t)(f4 - C::KC) * a.n_pad + n0);
+            it.step = (int64_t)C::KC * a.n_pad * 4;
+            it.lds = C::X_BYTES + C::W_BYTES + C::SCX + (f4 - C::KC) * 1024;
             it.pieces = C::BN / 4;
         }
     }
@@ -235,9 +236,10 @@ __device__ __forceinline__ DmaItem epi_item(const GemmArgs &a, int e, int sb, in
     return it;
 }
 
-template <int FMT, int WM, int WN, int TM, int TN, int MINB>
+template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2>
 __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
-    using C = Cfg<FMT, WM, WN, TM, TN>;
+    using C = Cfg<FMT, WM, WN, TM, TN, KCT>;
+    constexpr int KC = C::KC, SPB = C::SPB;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // uniform: SALU addressing
@@ -325,7 +327,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
 #pragma unroll
             for (int j = 0; j < TN; j++) wb[kc][j] = *(const v4i *)(st + wfrag0 + (j * KC + kc) * 1024);
         }
-        static_assert(KC == 2 && TM <= 2 && TN <= 2, "the wait below names every scale register");
+        static_assert(FMT != FMT_Q8_0 || (KC == 2 && TM <= 2 && TN <= 2), "the wait below names every scale register");
         asm volatile("s_waitcnt lgkmcnt(0)"
                      : "+v"(dw[0][0]), "+v"(dw[0][TN - 1]), "+v"(dx[0][0]), "+v"(dx[0][TM - 1]), "+v"(dw[1][0]),
                        "+v"(dw[1][TN - 1]), "+v"(dx[1][0]), "+v"(dx[1][TM - 1]));
@@ -457,17 +459,17 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
     // UNR stages per iteration (a whole superblock for the K-quants), so the
     // stage slot and the DMA count still in flight are constants per position.
     constexpr int UNR = C::limbs ? SPB : NBUF;
-    static_assert(UNR == NBUF, "slot of each unrolled stage is its position");
+    static_assert(UNR % NBUF == 0, "slot of each unrolled stage is its position modulo NBUF");
     for (int s0 = 0; s0 < nst; s0 += UNR) {
         static_for<0, UNR>([&](auto qc) __attribute__((always_inline)) {
             constexpr int q = decltype(qc)::value;
             const int s = s0 + q;
-            if (C::limbs || s < nst) {  // nst is a multiple of 2 (Q8_0 / F16), of SPB (K-quants)
+            if (C::limbs || s < nst) {  // nst is a multiple of NBUF/2 (Q8_0 / F16), of SPB (K-quants)
                 // stage s has landed once only the DMAs of stages s+1 .. s+DIST-1 are outstanding
                 wait_vmcnt_c<C::template waits<DIST>(q)>();
                 barrier_nofence();  // stage s landed for every wave; stage s-1 fully consumed
                 issue(s + DIST);
-                compute(smem + q * C::STAGE);  // s0 is a multiple of NBUF: stage s sits in slot q
+                compute(smem + (q % NBUF) * C::STAGE);  // s0 is a multiple of NBUF: stage s sits in slot q % NBUF
             }
         });
         if constexpr (C::limbs) epilogue(s0 / SPB);
@@ -492,12 +494,12 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
         }
 }
 
-template <int FMT, int WM, int WN, int TM, int TN, int MINB>
+template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2>
 static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
-    using C = Cfg<FMT, WM, WN, TM, TN>;
+    using C = Cfg<FMT, WM, WN, TM, TN, KCT>;
     static bool attr_set = false;
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm<FMT, WM, WN, TM, TN, MINB>,
+        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm<FMT, WM, WN, TM, TN, MINB, KCT>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
         if (e != hipSuccess) return e;
         attr_set = true;
@@ -505,8 +507,9 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
     a.tiles_m = (a.M + C::BM - 1) / C::BM;
     a.tiles_n = (a.N + C::BN - 1) / C::BN;
     a.group_m = 8;
+    a.nstages = a.kch / KCT;  // kb_pad is a multiple of 128 bytes
     const unsigned grid = (unsigned)(a.tiles_m * a.tiles_n);
-    hipLaunchKernelGGL((k_gemm<FMT, WM, WN, TM, TN, MINB>), dim3(grid), dim3(C::NT), C::LDS, s, a);
+    hipLaunchKernelGGL((k_gemm<FMT, WM, WN, TM, TN, MINB, KCT>), dim3(grid), dim3(C::NT), C::LDS, s, a);
     return hipGetLastError();
 }
 
@@ -515,6 +518,8 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
 //   3: 4 waves x (64x64)  WG 128x128, 2 WGs/CU
 //   4: 2 waves x (64x64)  WG 128x64
 //   5: 1 wave  x (64x64)  WG 64x64
+//   6: 4 waves x (64x64)  WG 128x128, 32-byte K stages: 70 KB of LDS, two workgroups per CU
+//      (K-quants)
 static int gemm_cfg_env() {
     const char *e = getenv("MQ_GEMM_CFG");  // read per launch so a process can compare configurations
     return (e && *e) ? atoi(e) : 0;
@@ -525,7 +530,7 @@ static inline int64_t tiles(int64_t M, int64_t N, int bm, int bn) { return ((M +
 template <int FMT>
 static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
     int cfg = gemm_cfg_env();
-    if (cfg < 1 || cfg > 5 || cfg == 2) {
+    if (cfg < 1 || cfg > 6 || cfg == 2 || (cfg == 6 && FMT != FMT_Q4_K && FMT != FMT_Q6_K)) {
         // 256x128 tiles when that still gives every CU (256) a workgroup, else 128x128
         // (the smaller tiles measured slower even where 128x128 leaves CUs idle:
         // 4096x384x384 Q8_0 12.7 us at 128x128, 13.2 us at 128x64, 14.1 us at 64x64)
@@ -535,6 +540,10 @@ static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
         case 1: return launch_cfg<FMT, 4, 2, 2, 2, 1>(a, s);
         case 3: return launch_cfg<FMT, 2, 2, 2, 2, 2>(a, s);
         case 4: return launch_cfg<FMT, 2, 1, 2, 2, 2>(a, s);
+        case 6:
+            if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q6_K) return launch_cfg<FMT, 2, 2, 2, 2, 2, 1>(a, s);
+            return hipErrorInvalidValue;
+
         default: return launch_cfg<FMT, 1, 1, 2, 2, 2>(a, s);
     }
 }
@@ -562,7 +571,7 @@ hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const 
     a.m_pad = (int)ap.m_pad;
     a.n_pad = (int)p.n_pad;
     a.kch = (int)(p.kb_pad / 32);
-    a.nstages = (int)(p.kb_pad / (KC * 32));
+    a.nstages = (int)(p.kb_pad / 64);  // set again per configuration
     a.nsb = (int)(k / QK_K);
     switch (type) {
         case MQ_TYPE_Q8_0: return launch_fmt<FMT_Q8_0>(a, s);
