@@ -40,6 +40,7 @@ MQ_SOURCES = [
     ("mq_decoder_run.cpp", ["-x", "hip"]),
     ("mq_gguf.cpp", ["-x", "hip"]),
     ("mq_gguf_load.cpp", ["-x", "hip"]),
+    ("mq_ops.hip", ["-ffp-contract=off"]),
 ]
 # The backend compiles against ggml's backend headers.  Standalone builds use the
 # compat transcription in csrc/ggml_compat (and libggml-compat.so for the ggml
@@ -79,20 +80,25 @@ def _link(objs, out, extra=()):
 
 
 def build_test_driver():
-    """tests/native/test_backend_mi355.cpp -> crispembed_amd/bin/test-backend-mi355 (test code:
-    it links the CPU oracle as the checker)."""
+    """tests/native/*.cpp -> crispembed_amd/bin/ (test code: test-backend-mi355 links the CPU
+    oracle as the checker; test-bert-graph-mi355 writes its result for the Python test to check)."""
     os.makedirs(BIN, exist_ok=True)
-    out = os.path.join(BIN, "test-backend-mi355")
     oracle = os.path.join(ROOT, "oracle")
-    cmd = ["g++", "-O2", "-std=c++17", "-I", os.path.join(CSRC, "ggml_compat"), "-I", os.path.join(ROOT, "include"),
-           "-I", oracle, os.path.join(TESTS, "native", "test_backend_mi355.cpp"), "-o", out + ".tmp",
-           "-L", HERE, "-lggml-mi355", "-lggml-compat", "-lmq", "-L", oracle, "-loracle",
-           "-Wl,-rpath," + HERE, "-Wl,-rpath," + oracle, "-Wl,-rpath,$ORIGIN/..", "-Wl,-rpath,$ORIGIN/../../oracle"]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"driver build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
-    os.replace(out + ".tmp", out)
-    return out
+    common = ["-O2", "-std=c++17", "-I", os.path.join(CSRC, "ggml_compat"), "-I", os.path.join(ROOT, "include"),
+              "-I", oracle]
+    libs = ["-L", HERE, "-lggml-mi355", "-lggml-compat", "-lmq", "-Wl,-rpath," + HERE, "-Wl,-rpath,$ORIGIN/.."]
+    outs = []
+    for src, name, extra in (("test_backend_mi355.cpp", "test-backend-mi355",
+                              ["-L", oracle, "-loracle", "-Wl,-rpath," + oracle, "-Wl,-rpath,$ORIGIN/../../oracle"]),
+                             ("test_bert_graph_mi355.cpp", "test-bert-graph-mi355", [])):
+        out = os.path.join(BIN, name)
+        cmd = ["g++", *common, os.path.join(TESTS, "native", src), "-o", out + ".tmp", *libs, *extra]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"driver build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+        os.replace(out + ".tmp", out)
+        outs.append(out)
+    return outs
 
 
 def build(verbose=True):

@@ -1,9 +1,24 @@
-// ggml_backend_mi355.cpp -- ggml backend that runs GGML_OP_MUL_MAT on MI355X.
+// ggml_backend_mi355.cpp -- ggml backend that runs CrispEmbed's graphs on MI355X.
 //
-// Interface tables follow ggml-backend-impl.h.  The backend executes only
-// MUL_MAT (plus the metadata-only view ops); ggml_backend_sched keeps every
-// other op on the CPU backend, which is how CrispEmbed already falls back for
-// ops a GPU backend rejects (src/crispembed.cpp:700-723).
+// Interface tables follow ggml-backend-impl.h.  The backend executes MUL_MAT on
+// quantized weights (mq.h) and the other ops of the encoder graph
+// (src/crispembed.cpp:1043-1468) through mq_ops.h: GET_ROWS, ADD / SUB / MUL / DIV,
+// NORM / RMS_NORM, UNARY (GELU_ERF, GELU, SILU, RELU), CPY / CONT / DUP and
+// FLASH_ATTN_EXT, plus the metadata-only view ops.  Anything else is refused by
+// supports_op, and ggml_backend_sched keeps it on the CPU backend, which is how
+// CrispEmbed already falls back for ops a GPU backend rejects (src/crispembed.cpp:700-723).
+//
+// graph_compute fuses chains whose intermediate results have no other reader
+// (ggml_node_get_use_count == 1) and are not graph outputs:
+//   MUL_MAT -> ADD(bias)                           the bias added by the GEMM / GEMV store
+//   [ADD(residual) ->] NORM|RMS_NORM -> MUL(w) [-> ADD(b)]
+//                                                  one row pass (mq_op_norm)
+//   ADD(bias) -> UNARY(GELU_ERF) -> MUL_MAT [-> ADD(bias)]
+//                                                  bias and GELU applied while the activation
+//                                                  is quantized for the mat-mul
+// and MUL_MATs that read the same activation with the same weight type and shape
+// one after another (q, k and v of a layer) quantize it once.  MQ_GGML_NO_FUSION=1
+// runs every node on its own.
 //
 // Threading: like every ggml backend, one backend instance must be driven by one
 // thread at a time (src/core/gpu_backend_pref.h:180-185); each instance owns one
@@ -18,9 +33,11 @@
 #include <vector>
 
 #include "ggml-backend-impl.h"
+#include "ggml-impl.h"
 #include "ggml-mi355.h"
 #include "ggml.h"
 #include "mq.h"
+#include "mq_ops.h"
 
 namespace {
 
@@ -50,6 +67,11 @@ struct BackendCtx {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     std::string name;
+    // what the workspace holds: the quantized activation of tensor ws_x for weight type
+    // ws_type at ws_m x ws_k (ws_x NULL: nothing reusable)
+    const ggml_tensor *ws_x = nullptr;
+    int ws_type = -1;
+    int64_t ws_m = 0, ws_k = 0;
 };
 
 std::vector<DeviceCtx *> &devices();
@@ -61,6 +83,52 @@ int mq_type_of(enum ggml_type t) {
         case GGML_TYPE_Q4_K: return MQ_TYPE_Q4_K;
         case GGML_TYPE_Q6_K: return MQ_TYPE_Q6_K;
         case GGML_TYPE_F16: return MQ_TYPE_F16;
+        default: return -1;
+    }
+}
+
+// any tensor type the graph ops read or write
+int mq_type_any(enum ggml_type t) {
+    switch (t) {
+        case GGML_TYPE_F32: return MQ_TYPE_F32;
+        case GGML_TYPE_I32: return MQ_TYPE_I32;
+        default: return mq_type_of(t);
+    }
+}
+
+// ggml metadata of a tensor as an mq_view.  Before allocation (supports_op) the view
+// offset stands in for the address, so alignment checks see what allocation keeps
+// (buffers and tensor offsets are 256-byte aligned).
+mq_view view_of(const ggml_tensor *t) {
+    mq_view v;
+    v.data = t->data ? t->data : (void *)(uintptr_t)t->view_offs;
+    v.type = mq_type_any(t->type);
+    for (int i = 0; i < 4; i++) v.ne[i] = t->ne[i], v.nb[i] = t->nb[i];
+    return v;
+}
+
+float op_param_f32(const ggml_tensor *t, int i) {
+    float f;
+    std::memcpy(&f, &t->op_params[i], sizeof(float));
+    return f;
+}
+
+int unary_of(const ggml_tensor *t) {
+    switch (ggml_get_unary_op(t)) {
+        case GGML_UNARY_OP_GELU_ERF: return MQ_UNARY_GELU_ERF;
+        case GGML_UNARY_OP_GELU: return MQ_UNARY_GELU;
+        case GGML_UNARY_OP_SILU: return MQ_UNARY_SILU;
+        case GGML_UNARY_OP_RELU: return MQ_UNARY_RELU;
+        default: return -1;
+    }
+}
+
+int binary_of(enum ggml_op op) {
+    switch (op) {
+        case GGML_OP_ADD: return MQ_BIN_ADD;
+        case GGML_OP_SUB: return MQ_BIN_SUB;
+        case GGML_OP_MUL: return MQ_BIN_MUL;
+        case GGML_OP_DIV: return MQ_BIN_DIV;
         default: return -1;
     }
 }
@@ -221,29 +289,61 @@ bool rows_flat(const ggml_tensor *t) {
     return t->nb[2] == t->nb[1] * (size_t)t->ne[1] && t->nb[3] == t->nb[2] * (size_t)t->ne[2];
 }
 
+bool ensure_ws(BackendCtx *c, size_t need) {
+    if (need <= c->ws_bytes) return true;
+    c->ws_x = nullptr;
+    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (c->ws) (void)hipFree(c->ws);
+    c->ws = nullptr;
+    c->ws_bytes = 0;
+    if (hipMalloc(&c->ws, need) != hipSuccess) {
+        c->ws = nullptr;
+        std::fprintf(stderr, "ggml-mi355: workspace allocation of %zu bytes failed\n", need);
+        return false;
+    }
+    c->ws_bytes = need;
+    return true;
+}
+
+// Quantizes activation x (M rows of K floats, row stride in x->nb[1]) for weight type mt into
+// the workspace, unless it is already there.  Returns an mq status.
+int quantize_x(BackendCtx *c, const ggml_tensor *x, int mt, int64_t M, int64_t K) {
+    if (c->ws_x == x && c->ws_type == mt && c->ws_m == M && c->ws_k == K) return 0;
+    c->ws_x = nullptr;
+    if (!ensure_ws(c, mq_workspace_bytes(mt, M, K))) return MQ_ENOMEM;
+    const int rc = mq_quantize_act_ex(mt, (const float *)x->data, (int64_t)(x->nb[1] / 4), M, K, nullptr, MQ_PRE_NONE,
+                                      c->ws, c->ws_bytes, MQ_PATH_AUTO, c->stream);
+    if (rc == 0) c->ws_x = x, c->ws_type = mt, c->ws_m = M, c->ws_k = K;
+    return rc;
+}
+
+// y = x w^T (+ bias) into dst, for dst rows that continue one another (any row stride)
+enum ggml_status mul_mat_flat(BackendCtx *c, const ggml_tensor *w, const ggml_tensor *x, ggml_tensor *dst,
+                              const float *bias, const ggml_tensor *named) {
+    const int mt = mq_type_of(w->type);
+    const int64_t K = w->ne[0], N = w->ne[1], M = x->ne[1] * x->ne[2] * x->ne[3];
+    int rc = quantize_x(c, x, mt, M, K);
+    if (rc == 0)
+        rc = mq_mul_mat_q_ex(mt, w->data, N, K, c->ws, M, (float *)dst->data, (int64_t)(dst->nb[1] / 4), bias,
+                             MQ_PATH_AUTO, c->stream);
+    if (rc != 0) {
+        std::fprintf(stderr, "ggml-mi355: MUL_MAT '%s' failed: %s\n", named->name, mq_last_error());
+        return rc == MQ_ENOMEM ? GGML_STATUS_ALLOC_FAILED : GGML_STATUS_FAILED;
+    }
+    return GGML_STATUS_SUCCESS;
+}
+
 enum ggml_status mul_mat(BackendCtx *c, ggml_tensor *dst) {
     const ggml_tensor *w = dst->src[0];
     const ggml_tensor *x = dst->src[1];
+    if (rows_flat(x) && rows_flat(dst)) return mul_mat_flat(c, w, x, dst, nullptr, dst);
+    // batches whose strides do not continue the rows: one mat-mul per (i2, i3)
     const int mt = mq_type_of(w->type);
-    const int64_t K = w->ne[0], N = w->ne[1];
-    const bool flat = rows_flat(x) && rows_flat(dst);
-    const int64_t M = flat ? x->ne[1] * x->ne[2] * x->ne[3] : x->ne[1];
-    const size_t need = mq_workspace_bytes(mt, M, K);
-    if (need > c->ws_bytes) {
-        hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-        if (c->ws) (void)hipFree(c->ws);
-        c->ws = nullptr;
-        c->ws_bytes = 0;
-        if (hipMalloc(&c->ws, need) != hipSuccess) {
-            c->ws = nullptr;
-            std::fprintf(stderr, "ggml-mi355: workspace allocation of %zu bytes failed\n", need);
-            return GGML_STATUS_ALLOC_FAILED;
-        }
-        c->ws_bytes = need;
-    }
-    const int64_t nbat2 = flat ? 1 : x->ne[2], nbat3 = flat ? 1 : x->ne[3];
-    for (int64_t i3 = 0; i3 < nbat3; i3++) {
-        for (int64_t i2 = 0; i2 < nbat2; i2++) {
+    const int64_t K = w->ne[0], N = w->ne[1], M = x->ne[1];
+    c->ws_x = nullptr;
+    if (!ensure_ws(c, mq_workspace_bytes(mt, M, K))) return GGML_STATUS_ALLOC_FAILED;
+    for (int64_t i3 = 0; i3 < x->ne[3]; i3++) {
+        for (int64_t i2 = 0; i2 < x->ne[2]; i2++) {
             const float *xp = (const float *)((const char *)x->data + i2 * x->nb[2] + i3 * x->nb[3]);
             float *yp = (float *)((char *)dst->data + i2 * dst->nb[2] + i3 * dst->nb[3]);
             const int rc = mq_mul_mat(mt, w->data, N, K, xp, (int64_t)(x->nb[1] / 4), M, yp,
@@ -257,21 +357,221 @@ enum ggml_status mul_mat(BackendCtx *c, ggml_tensor *dst) {
     return GGML_STATUS_SUCCESS;
 }
 
+enum ggml_status op_status(int rc, const ggml_tensor *node) {
+    if (rc == 0) return GGML_STATUS_SUCCESS;
+    std::fprintf(stderr, "ggml-mi355: %s '%s' failed: %s\n", ggml_op_name(node->op), node->name, mq_last_error());
+    return GGML_STATUS_FAILED;
+}
+
+// a contiguous F32 vector of n floats, broadcast over rows (a norm weight or a bias)
+bool is_row_vector(const ggml_tensor *t, int64_t n) {
+    return t && t->type == GGML_TYPE_F32 && t->ne[0] == n && t->ne[1] == 1 && t->ne[2] == 1 && t->ne[3] == 1 &&
+           t->nb[0] == sizeof(float);
+}
+
+// node i's result is read only by node i + 1 and is not a graph output
+bool feeds_only_next(ggml_cgraph *cg, int i) {
+    const ggml_tensor *t = ggml_graph_node(cg, i);
+    return !(t->flags & GGML_TENSOR_FLAG_OUTPUT) && ggml_node_get_use_count(cg, i) == 1;
+}
+
+bool same_shape(const ggml_tensor *a, const ggml_tensor *b) {
+    for (int i = 0; i < GGML_MAX_DIMS; i++)
+        if (a->ne[i] != b->ne[i]) return false;
+    return true;
+}
+
+// [ADD(x, r) ->] NORM|RMS_NORM -> MUL(w) [-> ADD(b)] starting at node i: returns the number of
+// nodes consumed (0: no match)
+int try_fuse_norm(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status &st) {
+    ggml_tensor *first = ggml_graph_node(cg, i);
+    const ggml_tensor *res = nullptr;
+    int j = i;
+    if (first->op == GGML_OP_ADD) {  // the residual sum feeding the norm
+        if (i + 1 >= n || !feeds_only_next(cg, i)) return 0;
+        const ggml_tensor *nx = ggml_graph_node(cg, i + 1);
+        if ((nx->op != GGML_OP_NORM && nx->op != GGML_OP_RMS_NORM) || nx->src[0] != first) return 0;
+        if (first->type != GGML_TYPE_F32 || !same_shape(first->src[0], first) || !same_shape(first->src[1], first))
+            return 0;
+        res = first->src[1];
+        j = i + 1;
+    }
+    ggml_tensor *nrm = ggml_graph_node(cg, j);
+    if (j + 1 >= n || !feeds_only_next(cg, j)) return 0;
+    ggml_tensor *mul = ggml_graph_node(cg, j + 1);
+    if (mul->op != GGML_OP_MUL || mul->src[0] != nrm || !is_row_vector(mul->src[1], nrm->ne[0])) return 0;
+    ggml_tensor *last = mul;
+    const float *b = nullptr;
+    if (j + 2 < n && feeds_only_next(cg, j + 1)) {
+        ggml_tensor *add = ggml_graph_node(cg, j + 2);
+        if (add->op == GGML_OP_ADD && add->src[0] == mul && is_row_vector(add->src[1], nrm->ne[0])) {
+            last = add;
+            b = (const float *)add->src[1]->data;
+        }
+    }
+    const int kind = nrm->op == GGML_OP_NORM ? MQ_NORM_LAYER : MQ_NORM_RMS;
+    const mq_view x = view_of(res ? first->src[0] : nrm->src[0]), d = view_of(last);
+    mq_view r{};
+    if (res) r = view_of(res);
+    if (!mq_op_supported(MQ_OP_NORM, kind, &x, res ? &r : nullptr, nullptr, nullptr, &d)) return 0;
+    st = op_status(mq_op_norm(kind, &x, res ? &r : nullptr, &d, op_param_f32(nrm, 0), (const float *)mul->src[1]->data,
+                              b, c->stream),
+                   nrm);
+    return (j - i) + (last == mul ? 2 : 3);
+}
+
+// a MUL_MAT whose activation and result rows can be walked as one matrix
+bool flat_mul_mat(const ggml_tensor *mm) {
+    const ggml_tensor *x = mm->src[1];
+    return x->type == GGML_TYPE_F32 && x->nb[0] == sizeof(float) && x->nb[1] % sizeof(float) == 0 && rows_flat(x) &&
+           rows_flat(mm) && mm->nb[0] == sizeof(float) && mm->nb[1] % sizeof(float) == 0;
+}
+
+// ADD(x, bias) -> UNARY(GELU_ERF) -> MUL_MAT(w, .) [-> ADD(., bias2)]: quantize
+// gelu_erf(x + bias) straight into the mat-mul's activation workspace
+int try_fuse_bias_gelu_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status &st) {
+    ggml_tensor *add = ggml_graph_node(cg, i);
+    if (i + 2 >= n || !feeds_only_next(cg, i) || !feeds_only_next(cg, i + 1)) return 0;
+    ggml_tensor *gelu = ggml_graph_node(cg, i + 1), *mm = ggml_graph_node(cg, i + 2);
+    if (gelu->op != GGML_OP_UNARY || ggml_get_unary_op(gelu) != GGML_UNARY_OP_GELU_ERF || gelu->src[0] != add) return 0;
+    if (mm->op != GGML_OP_MUL_MAT || mm->src[1] != gelu) return 0;
+    const ggml_tensor *x = add->src[0], *w = mm->src[0];
+    const int64_t K = w->ne[0], N = w->ne[1];
+    if (add->type != GGML_TYPE_F32 || x->type != GGML_TYPE_F32 || !is_row_vector(add->src[1], K) || x->ne[0] != K ||
+        !same_shape(x, add))
+        return 0;
+    if (x->nb[0] != sizeof(float) || x->nb[1] % sizeof(float) || !rows_flat(x) || !flat_mul_mat(mm)) return 0;
+    ggml_tensor *dst = mm;
+    const float *bias2 = nullptr;
+    if (i + 3 < n && feeds_only_next(cg, i + 2)) {
+        ggml_tensor *a2 = ggml_graph_node(cg, i + 3);
+        if (a2->op == GGML_OP_ADD && a2->src[0] == mm && is_row_vector(a2->src[1], N) && flat_mul_mat(mm) &&
+            rows_flat(a2) && a2->nb[0] == sizeof(float) && a2->nb[1] % sizeof(float) == 0) {
+            dst = a2;
+            bias2 = (const float *)a2->src[1]->data;
+        }
+    }
+    const int mt = mq_type_of(w->type);
+    const int64_t M = x->ne[1] * x->ne[2] * x->ne[3];
+    c->ws_x = nullptr;
+    if (!ensure_ws(c, mq_workspace_bytes(mt, M, K))) {
+        st = GGML_STATUS_ALLOC_FAILED;
+        return 3;
+    }
+    int rc = mq_quantize_act_ex(mt, (const float *)x->data, (int64_t)(x->nb[1] / 4), M, K,
+                                (const float *)add->src[1]->data, MQ_PRE_GELU_ERF, c->ws, c->ws_bytes, MQ_PATH_AUTO,
+                                c->stream);
+    if (rc == 0) {
+        c->ws_x = gelu, c->ws_type = mt, c->ws_m = M, c->ws_k = K;
+        rc = mq_mul_mat_q_ex(mt, w->data, N, K, c->ws, M, (float *)dst->data, (int64_t)(dst->nb[1] / 4), bias2,
+                             MQ_PATH_AUTO, c->stream);
+    }
+    st = op_status(rc, mm);
+    return dst == mm ? 3 : 4;
+}
+
+// MUL_MAT -> ADD(., bias): the bias added in the mat-mul's store.  Left alone when the ADD
+// starts a bias -> GELU_ERF -> MUL_MAT chain (that fusion saves more).
+int try_fuse_mul_mat_bias(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status &st) {
+    ggml_tensor *mm = ggml_graph_node(cg, i);
+    if (i + 1 >= n || !feeds_only_next(cg, i) || !flat_mul_mat(mm)) return 0;
+    ggml_tensor *add = ggml_graph_node(cg, i + 1);
+    const int64_t N = mm->src[0]->ne[1];
+    if (add->op != GGML_OP_ADD || add->src[0] != mm || !is_row_vector(add->src[1], N)) return 0;
+    if (!rows_flat(add) || add->nb[0] != sizeof(float) || add->nb[1] % sizeof(float)) return 0;
+    if (i + 3 < n && feeds_only_next(cg, i + 1)) {
+        const ggml_tensor *u = ggml_graph_node(cg, i + 2), *m2 = ggml_graph_node(cg, i + 3);
+        if (u->op == GGML_OP_UNARY && ggml_get_unary_op(u) == GGML_UNARY_OP_GELU_ERF && u->src[0] == add &&
+            m2->op == GGML_OP_MUL_MAT && m2->src[1] == u)
+            return 0;
+    }
+    st = mul_mat_flat(c, mm->src[0], mm->src[1], add, (const float *)add->src[1]->data, mm);
+    return 2;
+}
+
+enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node) {
+    switch (node->op) {
+        case GGML_OP_MUL_MAT: return mul_mat(c, node);
+        case GGML_OP_GET_ROWS: {
+            const mq_view a = view_of(node->src[0]), b = view_of(node->src[1]), d = view_of(node);
+            return op_status(mq_op_get_rows(&a, &b, &d, c->stream), node);
+        }
+        case GGML_OP_ADD:
+        case GGML_OP_SUB:
+        case GGML_OP_MUL:
+        case GGML_OP_DIV: {
+            const mq_view a = view_of(node->src[0]), b = view_of(node->src[1]), d = view_of(node);
+            return op_status(mq_op_binary(binary_of(node->op), &a, &b, &d, c->stream), node);
+        }
+        case GGML_OP_NORM:
+        case GGML_OP_RMS_NORM: {
+            const mq_view x = view_of(node->src[0]), d = view_of(node);
+            return op_status(mq_op_norm(node->op == GGML_OP_NORM ? MQ_NORM_LAYER : MQ_NORM_RMS, &x, nullptr, &d,
+                                        op_param_f32(node, 0), nullptr, nullptr, c->stream),
+                             node);
+        }
+        case GGML_OP_UNARY: {
+            const mq_view x = view_of(node->src[0]), d = view_of(node);
+            return op_status(mq_op_unary(unary_of(node), &x, &d, c->stream), node);
+        }
+        case GGML_OP_CPY:
+        case GGML_OP_CONT:
+        case GGML_OP_DUP: {
+            // CPY writes into its second source (the result is a view of it)
+            const mq_view s = view_of(node->src[0]), d = view_of(node->op == GGML_OP_CPY ? node->src[1] : node);
+            return op_status(mq_op_cpy(&s, &d, c->stream), node);
+        }
+        case GGML_OP_FLASH_ATTN_EXT: {
+            const mq_view q = view_of(node->src[0]), k = view_of(node->src[1]), v = view_of(node->src[2]),
+                          d = view_of(node);
+            mq_view m{};
+            if (node->src[3]) m = view_of(node->src[3]);
+            c->ws_x = nullptr;
+            if (!ensure_ws(c, mq_op_flash_attn_workspace_bytes(&k))) return GGML_STATUS_ALLOC_FAILED;
+            return op_status(mq_op_flash_attn(&q, &k, &v, node->src[3] ? &m : nullptr, &d, op_param_f32(node, 0), c->ws,
+                                              c->ws_bytes, c->stream),
+                             node);
+        }
+        default:
+            std::fprintf(stderr, "ggml-mi355: op %s reached graph_compute but is not supported\n",
+                         ggml_op_name(node->op));
+            return GGML_STATUS_FAILED;
+    }
+}
+
 enum ggml_status be_graph_compute(ggml_backend_t be, ggml_cgraph *cg) {
     BackendCtx *c = (BackendCtx *)be->context;
     DeviceGuard g(c->ordinal);
     const int n = ggml_graph_n_nodes(cg);
+    const bool fuse = std::getenv("MQ_GGML_NO_FUSION") == nullptr;
+    c->ws_x = nullptr;  // the inputs may have been rewritten since the last graph
     for (int i = 0; i < n; i++) {
         ggml_tensor *node = ggml_graph_node(cg, i);
         if (ggml_is_empty(node) || is_view_op(node->op)) continue;
-        if (node->op != GGML_OP_MUL_MAT) {
-            std::fprintf(stderr, "ggml-mi355: op %s reached graph_compute but is not supported\n",
-                         ggml_op_name(node->op));
-            return GGML_STATUS_FAILED;
+        enum ggml_status st = GGML_STATUS_SUCCESS;
+        int used = 0;
+        // a quantized activation stays reusable only from one mat-mul to the next
+        if (node->op != GGML_OP_MUL_MAT || !fuse) c->ws_x = nullptr;
+        if (fuse) {
+            switch (node->op) {
+                case GGML_OP_MUL_MAT: used = try_fuse_mul_mat_bias(c, cg, i, n, st); break;
+                case GGML_OP_NORM:
+                case GGML_OP_RMS_NORM: used = try_fuse_norm(c, cg, i, n, st); break;
+                case GGML_OP_ADD:
+                    used = try_fuse_norm(c, cg, i, n, st);
+                    if (!used) used = try_fuse_bias_gelu_mul_mat(c, cg, i, n, st);
+                    break;
+                default: break;
+            }
         }
-        const enum ggml_status st = mul_mat(c, node);
+        if (used == 0) {
+            st = compute_node(c, node);
+            used = 1;
+        }
         if (st != GGML_STATUS_SUCCESS) return st;
+        i += used - 1;
     }
+    c->ws_x = nullptr;
     return GGML_STATUS_SUCCESS;  // enqueued; ggml_backend_graph_compute synchronizes
 }
 
@@ -331,9 +631,12 @@ bool dev_supports_buft(ggml_backend_dev_t d, ggml_backend_buffer_type_t buft) {
     return buft == &((DeviceCtx *)d->context)->buft;
 }
 
-bool dev_supports_op(ggml_backend_dev_t d, const ggml_tensor *op) {
-    if (is_view_op(op->op)) return true;
-    if (op->op != GGML_OP_MUL_MAT) return false;
+bool in_this_device(ggml_backend_dev_t d, const ggml_tensor *t) {
+    const ggml_backend_buffer_t b = t->view_src ? t->view_src->buffer : t->buffer;
+    return !b || b->buft == &((DeviceCtx *)d->context)->buft;
+}
+
+bool supports_mul_mat(ggml_backend_dev_t d, const ggml_tensor *op) {
     const ggml_tensor *w = op->src[0], *x = op->src[1];
     if (!w || !x) return false;
     const int mt = mq_type_of(w->type);
@@ -345,6 +648,41 @@ bool dev_supports_op(ggml_backend_dev_t d, const ggml_tensor *op) {
     // the weight must live in this device's buffers (that is where its planes are)
     if (w->buffer && w->buffer->buft != &((DeviceCtx *)d->context)->buft) return false;
     return true;
+}
+
+bool dev_supports_op(ggml_backend_dev_t d, const ggml_tensor *op) {
+    if (is_view_op(op->op)) return true;
+    mq_view v[5], dst = view_of(op);
+    const mq_view *p[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+    for (int i = 0; i < 5; i++)
+        if (op->src[i]) {
+            v[i] = view_of(op->src[i]);
+            if (v[i].type < 0) return false;
+            p[i] = &v[i];
+        }
+    if (dst.type < 0) return false;
+    switch (op->op) {
+        case GGML_OP_MUL_MAT: return supports_mul_mat(d, op);
+        case GGML_OP_GET_ROWS:
+            // a weight table must be in this device's memory (the GGUF bytes at its start)
+            return in_this_device(d, op->src[0]) && mq_op_supported(MQ_OP_GET_ROWS, 0, p[0], p[1], nullptr, nullptr, &dst);
+        case GGML_OP_ADD:
+        case GGML_OP_SUB:
+        case GGML_OP_MUL:
+        case GGML_OP_DIV: return mq_op_supported(MQ_OP_BINARY, binary_of(op->op), p[0], p[1], nullptr, nullptr, &dst);
+        case GGML_OP_NORM: return mq_op_supported(MQ_OP_NORM, MQ_NORM_LAYER, p[0], nullptr, nullptr, nullptr, &dst);
+        case GGML_OP_RMS_NORM: return mq_op_supported(MQ_OP_NORM, MQ_NORM_RMS, p[0], nullptr, nullptr, nullptr, &dst);
+        case GGML_OP_UNARY:
+            return unary_of(op) >= 0 && mq_op_supported(MQ_OP_UNARY, unary_of(op), p[0], nullptr, nullptr, nullptr, &dst);
+        case GGML_OP_CPY: return mq_op_supported(MQ_OP_CPY, 0, p[0], nullptr, nullptr, nullptr, p[1]);
+        case GGML_OP_CONT:
+        case GGML_OP_DUP: return mq_op_supported(MQ_OP_CPY, 0, p[0], nullptr, nullptr, nullptr, &dst);
+        case GGML_OP_FLASH_ATTN_EXT:
+            // no ALiBi slopes, no logit soft-capping, no attention sinks
+            if (op_param_f32(op, 1) != 0.0f || op_param_f32(op, 2) != 0.0f || op->src[4]) return false;
+            return mq_op_supported(MQ_OP_FLASH_ATTN, 0, p[0], p[1], p[2], p[3], &dst);
+        default: return false;
+    }
 }
 
 bool dev_offload_op(ggml_backend_dev_t, const ggml_tensor *) { return false; }

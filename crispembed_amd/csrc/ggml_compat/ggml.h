@@ -5,8 +5,10 @@
 // MI355X backend and its test driver use, so they build without ggml.  A real
 // integration compiles ggml_backend_mi355.cpp against ggml's own headers instead
 // (include path switch only; the backend source does not change).
-// The struct layouts and enum values follow upstream ggml as published in 2025
-// and are NOT verified against CrispEmbed's fork pin 890278a8.
+// The struct layouts and the ggml_type / ggml_status / ggml_unary_op values follow
+// upstream ggml as published in 2025 (NOT verified against CrispEmbed's fork pin
+// 890278a8).  The ggml_op enum is a local subset with its own numbering: code names
+// ops, never their values, so the backend compiles unchanged against ggml's header.
 #pragma once
 #include <stdbool.h>
 #include <stddef.h>
@@ -44,16 +46,21 @@ enum ggml_type {
     GGML_TYPE_Q5_K = 13,
     GGML_TYPE_Q6_K = 14,
     GGML_TYPE_Q8_K = 15,
+    GGML_TYPE_I8 = 24,
+    GGML_TYPE_I16 = 25,
+    GGML_TYPE_I32 = 26,
     GGML_TYPE_COUNT = 40,
 };
 
-// Only the ops the backend names are listed; the numeric values are the compat
-// build's own (code refers to them by name).
+// Only the ops the backend and its tests name are listed; the numeric values are
+// the compat build's own (code refers to them by name).
 enum ggml_op {
     GGML_OP_NONE = 0,
     GGML_OP_DUP,
     GGML_OP_ADD,
+    GGML_OP_SUB,
     GGML_OP_MUL,
+    GGML_OP_DIV,
     GGML_OP_NORM,
     GGML_OP_RMS_NORM,
     GGML_OP_MUL_MAT,
@@ -66,7 +73,37 @@ enum ggml_op {
     GGML_OP_PERMUTE,
     GGML_OP_TRANSPOSE,
     GGML_OP_GET_ROWS,
+    GGML_OP_SOFT_MAX,
+    GGML_OP_ROPE,
+    GGML_OP_FLASH_ATTN_EXT,
+    GGML_OP_UNARY,
     GGML_OP_COUNT,
+};
+
+enum ggml_unary_op {
+    GGML_UNARY_OP_ABS,
+    GGML_UNARY_OP_SGN,
+    GGML_UNARY_OP_NEG,
+    GGML_UNARY_OP_STEP,
+    GGML_UNARY_OP_TANH,
+    GGML_UNARY_OP_ELU,
+    GGML_UNARY_OP_RELU,
+    GGML_UNARY_OP_SIGMOID,
+    GGML_UNARY_OP_GELU,
+    GGML_UNARY_OP_GELU_QUICK,
+    GGML_UNARY_OP_SILU,
+    GGML_UNARY_OP_HARDSWISH,
+    GGML_UNARY_OP_HARDSIGMOID,
+    GGML_UNARY_OP_EXP,
+    GGML_UNARY_OP_GELU_ERF,
+    GGML_UNARY_OP_COUNT,
+};
+
+enum ggml_tensor_flag {
+    GGML_TENSOR_FLAG_INPUT = 1,
+    GGML_TENSOR_FLAG_OUTPUT = 2,
+    GGML_TENSOR_FLAG_PARAM = 4,
+    GGML_TENSOR_FLAG_LOSS = 8,
 };
 
 struct ggml_backend_buffer;
@@ -121,12 +158,43 @@ GGML_API struct ggml_tensor *ggml_new_tensor_2d(struct ggml_context *ctx, enum g
                                                int64_t ne1);
 GGML_API struct ggml_tensor *ggml_new_tensor_3d(struct ggml_context *ctx, enum ggml_type type, int64_t ne0,
                                                int64_t ne1, int64_t ne2);
+GGML_API struct ggml_tensor *ggml_new_tensor_4d(struct ggml_context *ctx, enum ggml_type type, int64_t ne0,
+                                               int64_t ne1, int64_t ne2, int64_t ne3);
 GGML_API struct ggml_tensor *ggml_get_first_tensor(const struct ggml_context *ctx);
 GGML_API struct ggml_tensor *ggml_get_next_tensor(const struct ggml_context *ctx, struct ggml_tensor *tensor);
 GGML_API struct ggml_tensor *ggml_mul_mat(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b);
 GGML_API struct ggml_tensor *ggml_add(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b);
 GGML_API struct ggml_tensor *ggml_reshape_2d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0,
                                             int64_t ne1);
+GGML_API struct ggml_tensor *ggml_reshape_3d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0,
+                                            int64_t ne1, int64_t ne2);
+GGML_API struct ggml_tensor *ggml_reshape_4d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0,
+                                            int64_t ne1, int64_t ne2, int64_t ne3);
+GGML_API struct ggml_tensor *ggml_view_1d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0, size_t offset);
+GGML_API struct ggml_tensor *ggml_view_2d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0, int64_t ne1,
+                                         size_t nb1, size_t offset);
+GGML_API struct ggml_tensor *ggml_permute(struct ggml_context *ctx, struct ggml_tensor *a, int axis0, int axis1,
+                                         int axis2, int axis3);
+GGML_API struct ggml_tensor *ggml_cont(struct ggml_context *ctx, struct ggml_tensor *a);
+GGML_API struct ggml_tensor *ggml_cpy(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b);
+GGML_API struct ggml_tensor *ggml_sub(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b);
+GGML_API struct ggml_tensor *ggml_mul(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b);
+GGML_API struct ggml_tensor *ggml_div(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b);
+GGML_API struct ggml_tensor *ggml_get_rows(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b);
+GGML_API struct ggml_tensor *ggml_norm(struct ggml_context *ctx, struct ggml_tensor *a, float eps);
+GGML_API struct ggml_tensor *ggml_rms_norm(struct ggml_context *ctx, struct ggml_tensor *a, float eps);
+GGML_API struct ggml_tensor *ggml_unary(struct ggml_context *ctx, struct ggml_tensor *a, enum ggml_unary_op op);
+GGML_API struct ggml_tensor *ggml_gelu_erf(struct ggml_context *ctx, struct ggml_tensor *a);
+GGML_API struct ggml_tensor *ggml_gelu(struct ggml_context *ctx, struct ggml_tensor *a);
+GGML_API struct ggml_tensor *ggml_silu(struct ggml_context *ctx, struct ggml_tensor *a);
+GGML_API struct ggml_tensor *ggml_relu(struct ggml_context *ctx, struct ggml_tensor *a);
+GGML_API enum ggml_unary_op ggml_get_unary_op(const struct ggml_tensor *tensor);
+// q [hd, Tq, nh, B], k / v [hd, Tk, nkv, B], mask F16 or NULL -> [hd, nh, Tq, B] F32;
+// op_params: scale, max_bias, logit_softcap
+GGML_API struct ggml_tensor *ggml_flash_attn_ext(struct ggml_context *ctx, struct ggml_tensor *q, struct ggml_tensor *k,
+                                                struct ggml_tensor *v, struct ggml_tensor *mask, float scale,
+                                                float max_bias, float logit_softcap);
+GGML_API struct ggml_tensor *ggml_graph_get_tensor(const struct ggml_cgraph *cgraph, const char *name);
 GGML_API struct ggml_cgraph *ggml_new_graph(struct ggml_context *ctx);
 GGML_API void ggml_build_forward_expand(struct ggml_cgraph *cgraph, struct ggml_tensor *tensor);
 GGML_API int ggml_graph_n_nodes(struct ggml_cgraph *cgraph);

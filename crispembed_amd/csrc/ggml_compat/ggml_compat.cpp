@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "ggml-backend-impl.h"
+#include "ggml-impl.h"
 #include "ggml.h"
 
 // ---------------------------------------------------------------------------
@@ -20,7 +21,8 @@
 extern "C" int64_t ggml_blck_size(enum ggml_type type) {
     switch (type) {
         case GGML_TYPE_F32:
-        case GGML_TYPE_F16: return 1;
+        case GGML_TYPE_F16:
+        case GGML_TYPE_I32: return 1;
         case GGML_TYPE_Q8_0: return 32;
         case GGML_TYPE_Q4_K:
         case GGML_TYPE_Q6_K:
@@ -31,7 +33,8 @@ extern "C" int64_t ggml_blck_size(enum ggml_type type) {
 
 extern "C" size_t ggml_type_size(enum ggml_type type) {
     switch (type) {
-        case GGML_TYPE_F32: return 4;
+        case GGML_TYPE_F32:
+        case GGML_TYPE_I32: return 4;
         case GGML_TYPE_F16: return 2;
         case GGML_TYPE_Q8_0: return 34;
         case GGML_TYPE_Q4_K: return 144;
@@ -49,6 +52,7 @@ extern "C" const char *ggml_type_name(enum ggml_type type) {
         case GGML_TYPE_Q4_K: return "q4_K";
         case GGML_TYPE_Q6_K: return "q6_K";
         case GGML_TYPE_Q8_K: return "q8_K";
+        case GGML_TYPE_I32: return "i32";
         default: return "?";
     }
 }
@@ -56,12 +60,27 @@ extern "C" const char *ggml_type_name(enum ggml_type type) {
 extern "C" const char *ggml_op_name(enum ggml_op op) {
     switch (op) {
         case GGML_OP_NONE: return "NONE";
+        case GGML_OP_DUP: return "DUP";
         case GGML_OP_ADD: return "ADD";
+        case GGML_OP_SUB: return "SUB";
+        case GGML_OP_MUL: return "MUL";
+        case GGML_OP_DIV: return "DIV";
+        case GGML_OP_NORM: return "NORM";
+        case GGML_OP_RMS_NORM: return "RMS_NORM";
         case GGML_OP_MUL_MAT: return "MUL_MAT";
+        case GGML_OP_MUL_MAT_ID: return "MUL_MAT_ID";
+        case GGML_OP_SCALE: return "SCALE";
+        case GGML_OP_CPY: return "CPY";
+        case GGML_OP_CONT: return "CONT";
         case GGML_OP_RESHAPE: return "RESHAPE";
         case GGML_OP_VIEW: return "VIEW";
         case GGML_OP_PERMUTE: return "PERMUTE";
         case GGML_OP_TRANSPOSE: return "TRANSPOSE";
+        case GGML_OP_GET_ROWS: return "GET_ROWS";
+        case GGML_OP_SOFT_MAX: return "SOFT_MAX";
+        case GGML_OP_ROPE: return "ROPE";
+        case GGML_OP_FLASH_ATTN_EXT: return "FLASH_ATTN_EXT";
+        case GGML_OP_UNARY: return "UNARY";
         default: return "OP";
     }
 }
@@ -178,6 +197,12 @@ extern "C" struct ggml_tensor *ggml_new_tensor_3d(struct ggml_context *ctx, enum
     return new_tensor(ctx, type, 3, ne);
 }
 
+extern "C" struct ggml_tensor *ggml_new_tensor_4d(struct ggml_context *ctx, enum ggml_type type, int64_t ne0,
+                                                  int64_t ne1, int64_t ne2, int64_t ne3) {
+    const int64_t ne[4] = {ne0, ne1, ne2, ne3};
+    return new_tensor(ctx, type, 4, ne);
+}
+
 extern "C" struct ggml_tensor *ggml_get_first_tensor(const struct ggml_context *ctx) {
     return ctx->tensors.empty() ? nullptr : ctx->tensors.front();
 }
@@ -197,26 +222,180 @@ extern "C" struct ggml_tensor *ggml_mul_mat(struct ggml_context *ctx, struct ggm
     return r;
 }
 
-extern "C" struct ggml_tensor *ggml_add(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b) {
+static ggml_tensor *binary(ggml_context *ctx, ggml_tensor *a, ggml_tensor *b, ggml_op op) {
     ggml_tensor *r = new_tensor(ctx, a->type, 4, a->ne);
-    r->op = GGML_OP_ADD;
+    r->op = op;
     r->src[0] = a;
     r->src[1] = b;
     return r;
 }
 
-extern "C" struct ggml_tensor *ggml_reshape_2d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0,
-                                               int64_t ne1) {
+extern "C" struct ggml_tensor *ggml_add(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b) {
+    return binary(ctx, a, b, GGML_OP_ADD);
+}
+extern "C" struct ggml_tensor *ggml_sub(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b) {
+    return binary(ctx, a, b, GGML_OP_SUB);
+}
+extern "C" struct ggml_tensor *ggml_mul(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b) {
+    return binary(ctx, a, b, GGML_OP_MUL);
+}
+extern "C" struct ggml_tensor *ggml_div(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b) {
+    return binary(ctx, a, b, GGML_OP_DIV);
+}
+
+// A tensor sharing `a`'s memory: shape ne, strides nb, `offset` bytes into a's data.
+static ggml_tensor *view_of(ggml_context *ctx, ggml_tensor *a, const int64_t *ne, const size_t *nb, size_t offset,
+                            ggml_op op) {
     const bool na = ctx->no_alloc;
     ctx->no_alloc = true;
-    const int64_t ne[2] = {ne0, ne1};
-    ggml_tensor *r = new_tensor(ctx, a->type, 2, ne);
+    ggml_tensor *r = new_tensor(ctx, a->type, 4, ne);
     ctx->no_alloc = na;
-    r->op = GGML_OP_RESHAPE;
+    for (int i = 0; i < GGML_MAX_DIMS; i++) r->nb[i] = nb[i];
+    r->op = op;
     r->src[0] = a;
     r->view_src = a->view_src ? a->view_src : a;
-    r->view_offs = a->view_offs;
-    r->data = a->data;
+    r->view_offs = a->view_offs + offset;
+    r->data = a->data ? (char *)a->data + offset : nullptr;
+    r->buffer = a->buffer;
+    return r;
+}
+
+static ggml_tensor *reshape(ggml_context *ctx, ggml_tensor *a, int n, const int64_t *ne_in) {
+    if (!ggml_is_contiguous(a)) {
+        std::fprintf(stderr, "ggml_reshape: tensor '%s' is not contiguous\n", a->name);
+        std::abort();
+    }
+    int64_t ne[4] = {1, 1, 1, 1};
+    for (int i = 0; i < n; i++) ne[i] = ne_in[i];
+    if (ne[0] * ne[1] * ne[2] * ne[3] != ggml_nelements(a)) {
+        std::fprintf(stderr, "ggml_reshape: element count of '%s' changes\n", a->name);
+        std::abort();
+    }
+    size_t nb[4];
+    nb[0] = ggml_type_size(a->type);
+    nb[1] = nb[0] * (size_t)(ne[0] / ggml_blck_size(a->type));
+    for (int i = 2; i < 4; i++) nb[i] = nb[i - 1] * (size_t)ne[i - 1];
+    return view_of(ctx, a, ne, nb, 0, GGML_OP_RESHAPE);
+}
+
+extern "C" struct ggml_tensor *ggml_reshape_2d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0,
+                                               int64_t ne1) {
+    const int64_t ne[2] = {ne0, ne1};
+    return reshape(ctx, a, 2, ne);
+}
+extern "C" struct ggml_tensor *ggml_reshape_3d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0,
+                                               int64_t ne1, int64_t ne2) {
+    const int64_t ne[3] = {ne0, ne1, ne2};
+    return reshape(ctx, a, 3, ne);
+}
+extern "C" struct ggml_tensor *ggml_reshape_4d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0,
+                                               int64_t ne1, int64_t ne2, int64_t ne3) {
+    const int64_t ne[4] = {ne0, ne1, ne2, ne3};
+    return reshape(ctx, a, 4, ne);
+}
+
+extern "C" struct ggml_tensor *ggml_view_1d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0,
+                                            size_t offset) {
+    const int64_t ne[4] = {ne0, 1, 1, 1};
+    const size_t es = ggml_type_size(a->type);
+    const size_t nb[4] = {es, es * (size_t)ne0, es * (size_t)ne0, es * (size_t)ne0};
+    return view_of(ctx, a, ne, nb, offset, GGML_OP_VIEW);
+}
+
+extern "C" struct ggml_tensor *ggml_view_2d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0,
+                                            int64_t ne1, size_t nb1, size_t offset) {
+    const int64_t ne[4] = {ne0, ne1, 1, 1};
+    const size_t nb[4] = {ggml_type_size(a->type), nb1, nb1 * (size_t)ne1, nb1 * (size_t)ne1};
+    return view_of(ctx, a, ne, nb, offset, GGML_OP_VIEW);
+}
+
+// result dim axis_i is a's dim i
+extern "C" struct ggml_tensor *ggml_permute(struct ggml_context *ctx, struct ggml_tensor *a, int axis0, int axis1,
+                                            int axis2, int axis3) {
+    const int ax[4] = {axis0, axis1, axis2, axis3};
+    int64_t ne[4];
+    size_t nb[4];
+    for (int i = 0; i < 4; i++) {
+        ne[ax[i]] = a->ne[i];
+        nb[ax[i]] = a->nb[i];
+    }
+    return view_of(ctx, a, ne, nb, 0, GGML_OP_PERMUTE);
+}
+
+extern "C" struct ggml_tensor *ggml_cont(struct ggml_context *ctx, struct ggml_tensor *a) {
+    ggml_tensor *r = new_tensor(ctx, a->type, 4, a->ne);
+    r->op = GGML_OP_CONT;
+    r->src[0] = a;
+    return r;
+}
+
+// copies a into b; the result is a view of b
+extern "C" struct ggml_tensor *ggml_cpy(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b) {
+    ggml_tensor *r = view_of(ctx, b, b->ne, b->nb, 0, GGML_OP_CPY);
+    r->src[0] = a;
+    r->src[1] = b;
+    return r;
+}
+
+extern "C" struct ggml_tensor *ggml_get_rows(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b) {
+    const int64_t ne[4] = {a->ne[0], b->ne[0], b->ne[1], b->ne[2]};
+    ggml_tensor *r = new_tensor(ctx, GGML_TYPE_F32, 4, ne);
+    r->op = GGML_OP_GET_ROWS;
+    r->src[0] = a;
+    r->src[1] = b;
+    return r;
+}
+
+static ggml_tensor *norm_op(ggml_context *ctx, ggml_tensor *a, float eps, ggml_op op) {
+    ggml_tensor *r = new_tensor(ctx, a->type, 4, a->ne);
+    r->op = op;
+    std::memcpy(r->op_params, &eps, sizeof(float));
+    r->src[0] = a;
+    return r;
+}
+extern "C" struct ggml_tensor *ggml_norm(struct ggml_context *ctx, struct ggml_tensor *a, float eps) {
+    return norm_op(ctx, a, eps, GGML_OP_NORM);
+}
+extern "C" struct ggml_tensor *ggml_rms_norm(struct ggml_context *ctx, struct ggml_tensor *a, float eps) {
+    return norm_op(ctx, a, eps, GGML_OP_RMS_NORM);
+}
+
+extern "C" struct ggml_tensor *ggml_unary(struct ggml_context *ctx, struct ggml_tensor *a, enum ggml_unary_op op) {
+    ggml_tensor *r = new_tensor(ctx, a->type, 4, a->ne);
+    r->op = GGML_OP_UNARY;
+    r->op_params[0] = (int32_t)op;
+    r->src[0] = a;
+    return r;
+}
+extern "C" struct ggml_tensor *ggml_gelu_erf(struct ggml_context *ctx, struct ggml_tensor *a) {
+    return ggml_unary(ctx, a, GGML_UNARY_OP_GELU_ERF);
+}
+extern "C" struct ggml_tensor *ggml_gelu(struct ggml_context *ctx, struct ggml_tensor *a) {
+    return ggml_unary(ctx, a, GGML_UNARY_OP_GELU);
+}
+extern "C" struct ggml_tensor *ggml_silu(struct ggml_context *ctx, struct ggml_tensor *a) {
+    return ggml_unary(ctx, a, GGML_UNARY_OP_SILU);
+}
+extern "C" struct ggml_tensor *ggml_relu(struct ggml_context *ctx, struct ggml_tensor *a) {
+    return ggml_unary(ctx, a, GGML_UNARY_OP_RELU);
+}
+extern "C" enum ggml_unary_op ggml_get_unary_op(const struct ggml_tensor *t) {
+    return (enum ggml_unary_op)t->op_params[0];
+}
+
+extern "C" struct ggml_tensor *ggml_flash_attn_ext(struct ggml_context *ctx, struct ggml_tensor *q,
+                                                   struct ggml_tensor *k, struct ggml_tensor *v,
+                                                   struct ggml_tensor *mask, float scale, float max_bias,
+                                                   float logit_softcap) {
+    const int64_t ne[4] = {v->ne[0], q->ne[2], q->ne[1], q->ne[3]};
+    ggml_tensor *r = new_tensor(ctx, GGML_TYPE_F32, 4, ne);
+    r->op = GGML_OP_FLASH_ATTN_EXT;
+    const float p[3] = {scale, max_bias, logit_softcap};
+    std::memcpy(r->op_params, p, sizeof(p));
+    r->src[0] = q;
+    r->src[1] = k;
+    r->src[2] = v;
+    r->src[3] = mask;
     return r;
 }
 
@@ -236,6 +415,23 @@ static void visit(ggml_cgraph *g, ggml_tensor *t) {
 }
 
 extern "C" void ggml_build_forward_expand(struct ggml_cgraph *g, struct ggml_tensor *t) { visit(g, t); }
+
+extern "C" struct ggml_tensor *ggml_graph_get_tensor(const struct ggml_cgraph *g, const char *name) {
+    for (ggml_tensor *t : g->nodes)
+        if (std::strcmp(t->name, name) == 0) return t;
+    for (ggml_tensor *t : g->leafs)
+        if (std::strcmp(t->name, name) == 0) return t;
+    return nullptr;
+}
+
+extern "C" int ggml_node_get_use_count(const struct ggml_cgraph *g, int node_idx) {
+    const ggml_tensor *t = g->nodes[node_idx];
+    int n = 0;
+    for (const ggml_tensor *u : g->nodes)
+        for (int i = 0; i < GGML_MAX_SRC; i++)
+            if (u->src[i] == t) n++;
+    return n;
+}
 extern "C" int ggml_graph_n_nodes(struct ggml_cgraph *g) { return (int)g->nodes.size(); }
 extern "C" struct ggml_tensor *ggml_graph_node(struct ggml_cgraph *g, int i) {
     if (i < 0) i += (int)g->nodes.size();

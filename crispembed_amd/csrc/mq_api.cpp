@@ -260,8 +260,8 @@ int mq_quantize_act_ex(int type, const float *x, int64_t ldx, int64_t m, int64_t
     return e == hipSuccess ? MQ_OK : hip_fail(e, "activation quantization");
 }
 
-int mq_mul_mat_q(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m, float *y,
-                 int64_t ldy, int path, void *stream) {
+int mq_mul_mat_q_ex(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m, float *y,
+                    int64_t ldy, const float *bias, int path, void *stream) {
     int rc = check_weight_shape(type, n, k);
     if (rc) return rc;
     if (!w_image || !workspace || !y || m < 0 || m > INT32_MAX || ldy < n) return fail(MQ_EINVAL, "mq_mul_mat_q: bad arguments");
@@ -270,9 +270,15 @@ int mq_mul_mat_q(int type, const void *w_image, int64_t n, int64_t k, const void
     if (m == 0) return MQ_OK;
     path = resolve_path(path, m);
     if (path < 0) return path;
-    const hipError_t e = (path == MQ_PATH_GEMV) ? launch_gemv(type, w_image, n, k, workspace, m, y, ldy, (hipStream_t)stream)
-                                                : launch_gemm(type, w_image, n, k, workspace, m, y, ldy, (hipStream_t)stream);
+    const hipError_t e = (path == MQ_PATH_GEMV)
+                             ? launch_gemv(type, w_image, n, k, workspace, m, y, ldy, (hipStream_t)stream, bias)
+                             : launch_gemm(type, w_image, n, k, workspace, m, y, ldy, (hipStream_t)stream, bias);
     return e == hipSuccess ? MQ_OK : hip_fail(e, path == MQ_PATH_GEMV ? "gemv" : "gemm");
+}
+
+int mq_mul_mat_q(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m, float *y,
+                 int64_t ldy, int path, void *stream) {
+    return mq_mul_mat_q_ex(type, w_image, n, k, workspace, m, y, ldy, nullptr, path, stream);
 }
 
 int mq_mul_mat_ex(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m,

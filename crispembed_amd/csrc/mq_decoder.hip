@@ -157,43 +157,42 @@ template <int HD>
 constexpr int kv_frags() { return 2 * (HD / 16) + 4 * (HD / 32); }
 
 template <int HD>
-__global__ __launch_bounds__(256) void k_kv_frag(const float *__restrict__ qkv, int64_t ld, int nq, int nkv, int T,
-                                                 int nblk, const float *__restrict__ kw, float eps,
-                                                 const float2 *__restrict__ cs, _Float16 *__restrict__ frag) {
+__global__ __launch_bounds__(256) void k_kv_frag(const AttnArgs a, int nblk) {
     constexpr int NS = HD / 16, NT = HD / 32, HALF = HD / 2, KS = HD + 4, NFR = kv_frags<HD>();
     __shared__ __attribute__((aligned(16))) float Ks[32 * KS];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
     const int kb = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
-    const int64_t rbase = (int64_t)b * T;
-    const float *kp = qkv + (int64_t)nq * HD + (int64_t)hk * HD;
-    const float *vp = qkv + (int64_t)(nq + nkv) * HD + (int64_t)hk * HD;
+    const float *kp = a.k + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+    const float *vp = a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+    const float *kw = a.kw;
+    const float2 *cs = a.cs;
     const bool on = lane < HALF;
     // K rows of the block, normed and rotated (NEOX pair (i, i + HD/2) in one lane), to LDS;
-    // rows past T are zero
+    // rows past Tk are zero
     for (int r = wave; r < 32; r += 4) {
         const int key = kb * 32 + r;
-        float a = 0.f, c = 0.f;
-        if (key < T) {
-            const float *x = kp + (rbase + key) * ld;
-            a = on ? x[lane] : 0.f;
-            c = on ? x[lane + HALF] : 0.f;
+        float x0 = 0.f, x1 = 0.f;
+        if (key < a.Tk) {
+            const float *x = kp + (int64_t)key * a.k_st;
+            x0 = on ? x[lane] : 0.f;
+            x1 = on ? x[lane + HALF] : 0.f;
             if (kw) {
-                const float scale = 1.0f / sqrtf(wave_sum_f(a * a + c * c) / (float)HD + eps);
+                const float scale = 1.0f / sqrtf(wave_sum_f(x0 * x0 + x1 * x1) / (float)HD + a.eps);
                 if (on) {
-                    a = a * scale * kw[lane];
-                    c = c * scale * kw[lane + HALF];
+                    x0 = x0 * scale * kw[lane];
+                    x1 = x1 * scale * kw[lane + HALF];
                 }
             }
             if (cs && on) {
                 const float2 rot = cs[(int64_t)key * HALF + lane];
-                const float na = a * rot.x - c * rot.y, nc = a * rot.y + c * rot.x;
-                a = na, c = nc;
+                const float n0 = x0 * rot.x - x1 * rot.y, n1 = x0 * rot.y + x1 * rot.x;
+                x0 = n0, x1 = n1;
             }
         }
-        if (on) Ks[r * KS + lane] = a, Ks[r * KS + lane + HALF] = c;
+        if (on) Ks[r * KS + lane] = x0, Ks[r * KS + lane + HALF] = x1;
     }
     __syncthreads();
-    _Float16 *F = frag + ((int64_t)(b * nkv + hk) * nblk + kb) * NFR * 512 + lane * 8;
+    _Float16 *F = (_Float16 *)a.ws + ((int64_t)(b * a.nkv + hk) * nblk + kb) * NFR * 512 + lane * 8;
     for (int st = wave; st < NS; st += 4) {
         const float4 u = *(const float4 *)&Ks[l32 * KS + 16 * st + 8 * half];
         const float4 w = *(const float4 *)&Ks[l32 * KS + 16 * st + 8 * half + 4];
@@ -209,7 +208,7 @@ __global__ __launch_bounds__(256) void k_kv_frag(const float *__restrict__ qkv, 
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int key = kb * 32 + 16 * t + 8 * (j / 4) + 4 * half + j % 4;
-            x[j] = key < T ? vp[(rbase + key) * ld + 32 * n + l32] : 0.f;
+            x[j] = key < a.Tk ? vp[(int64_t)key * a.v_st + 32 * n + l32] : 0.f;
         }
         v8h h, l;
         split8(x, h, l);
@@ -218,30 +217,28 @@ __global__ __launch_bounds__(256) void k_kv_frag(const float *__restrict__ qkv, 
     }
 }
 
-template <int HD>
-__global__ __launch_bounds__(512) void k_attn_frag(const float *__restrict__ qkv, int64_t ld,
-                                                   const _Float16 *__restrict__ frag, int nblk, float *__restrict__ out,
-                                                   int64_t ldo, int T, int nq, int nkv, float qscale, int causal,
-                                                   const float *__restrict__ qw, float eps,
-                                                   const float2 *__restrict__ cs) {
+template <int HD, bool MASK>
+__global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, float qscale) {
     constexpr int NS = HD / 16, NT = HD / 32, HALF = HD / 2, NFR = kv_frags<HD>();
+    constexpr float LOG2E = 1.4426950408889634f;
     __shared__ __attribute__((aligned(16))) float rs[8][32];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
     const int h = blockIdx.x * 2 + (wave >> 2);
     const int b = blockIdx.y;
+    const int Tq = a.Tq, Tk = a.Tk, causal = a.causal;
     // query tile of the wave: waves w and w + 4 share a SIMD, so they get tiles t and 3 - t
     // (one long and one short causal range each); the longest ranges are dispatched first
     const int qt = wave < 4 ? wave : 7 - wave;
     const int q0 = ((int)gridDim.z - 1 - (int)blockIdx.z) * 128 + qt * 32;
-    if (h >= nq || q0 >= T) return;  // no workgroup barrier below
-    const int hk = h / (nq / nkv), qi = q0 + l32;
-    const int64_t rbase = (int64_t)b * T;
+    if (h >= a.nq || q0 >= Tq) return;  // no workgroup barrier below
+    const int hk = h / (a.nq / a.nkv), qi = q0 + l32;
+    const int qrow = min(qi, Tq - 1);
+    const float2 *cs = a.cs;
 
     // Q^T operand: step st holds Q[qi][16 st + 8 half + j], normed, rotated, times qscale
     v8h qh[NS], ql[NS];
     {
-        const int qrow = min(qi, T - 1);
-        const float *qp = qkv + (rbase + qrow) * ld + (int64_t)h * HD + 8 * half;
+        const float *qp = a.q + (int64_t)b * a.q_sb + (int64_t)qrow * a.q_st + (int64_t)h * a.q_sh + 8 * half;
         float x[NS][8];
 #pragma unroll
         for (int st = 0; st < NS; st++) {
@@ -249,18 +246,18 @@ __global__ __launch_bounds__(512) void k_attn_frag(const float *__restrict__ qkv
             x[st][0] = u.x, x[st][1] = u.y, x[st][2] = u.z, x[st][3] = u.w;
             x[st][4] = w.x, x[st][5] = w.y, x[st][6] = w.z, x[st][7] = w.w;
         }
-        if (qw) {
+        if (a.qw) {
             float ss = 0.f;
 #pragma unroll
             for (int st = 0; st < NS; st++)
 #pragma unroll
                 for (int j = 0; j < 8; j++) ss += x[st][j] * x[st][j];
             ss += __shfl_xor(ss, 32);
-            const float scale = 1.0f / sqrtf(ss / (float)HD + eps);
+            const float scale = 1.0f / sqrtf(ss / (float)HD + a.eps);
 #pragma unroll
             for (int st = 0; st < NS; st++)
 #pragma unroll
-                for (int j = 0; j < 8; j++) x[st][j] = x[st][j] * scale * qw[16 * st + 8 * half + j];
+                for (int j = 0; j < 8; j++) x[st][j] = x[st][j] * scale * a.qw[16 * st + 8 * half + j];
         }
         if (cs) {
             // pair (d, d + HD/2) sits in steps st and st + NS/2 of the same lane and slot
@@ -269,9 +266,9 @@ __global__ __launch_bounds__(512) void k_attn_frag(const float *__restrict__ qkv
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const float2 rot = cs[(int64_t)qrow * HALF + 16 * st + 8 * half + j];
-                    const float a = x[st][j], c = x[st + NS / 2][j];
-                    x[st][j] = a * rot.x - c * rot.y;
-                    x[st + NS / 2][j] = a * rot.y + c * rot.x;
+                    const float x0 = x[st][j], x1 = x[st + NS / 2][j];
+                    x[st][j] = x0 * rot.x - x1 * rot.y;
+                    x[st + NS / 2][j] = x0 * rot.y + x1 * rot.x;
                 }
         }
 #pragma unroll
@@ -281,12 +278,16 @@ __global__ __launch_bounds__(512) void k_attn_frag(const float *__restrict__ qkv
             split8(x[st], qh[st], ql[st]);
         }
     }
+    // the lane's mask row (its query column of S^T)
+    const _Float16 *mrow = nullptr;
+    if constexpr (MASK)
+        mrow = (const _Float16 *)a.mask + (int64_t)b * a.m_sb + (int64_t)h * a.m_sh + (int64_t)qrow * a.m_sq;
     v16f oacc[NT];
 #pragma unroll
     for (int n = 0; n < NT; n++) oacc[n] = (v16f){};
     float m_run = -INFINITY, l_run = 0.f;
-    const int kend = causal ? min(T, q0 + 32) : T;
-    const v8h *F = (const v8h *)(frag + (int64_t)(b * nkv + hk) * nblk * NFR * 512) + lane;
+    const int kend = causal ? min(Tk, q0 + 32) : Tk;
+    const v8h *F = (const v8h *)((const _Float16 *)a.ws + (int64_t)(b * a.nkv + hk) * nblk * NFR * 512) + lane;
 
     for (int kb = 0; kb * 32 < kend; kb++) {
         const v8h *Fb = F + (int64_t)kb * NFR * 64;
@@ -312,16 +313,24 @@ __global__ __launch_bounds__(512) void k_attn_frag(const float *__restrict__ qkv
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
-            p[i] = (key >= T || (causal && key > qi)) ? -INFINITY : sc[i];
+            if (key >= Tk || (causal && key > qi)) {
+                p[i] = -INFINITY;
+            } else {
+                p[i] = sc[i];
+                if constexpr (MASK) p[i] += LOG2E * (float)mrow[key];
+            }
             mblk = fmaxf(mblk, p[i]);
         }
         mblk = fmaxf(mblk, __shfl_xor(mblk, 32));
-        const float m_new = fmaxf(m_run, mblk);  // finite: key 32 kb <= every query of the wave
-        const float alpha = exp2f(m_run - m_new);  // 0 on the first block
+        const float m_new = fmaxf(m_run, mblk);
+        // -inf while every key so far is masked: then alpha and p are 0 (without a mask key
+        // 32 kb <= every query of the wave keeps m_new finite)
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = exp2f(m_run - m_use);  // 0 on the first block
         float lblk = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            p[i] = exp2f(p[i] - m_new);
+            p[i] = exp2f(p[i] - m_use);
             lblk += p[i];
         }
         lblk += __shfl_xor(lblk, 32);
@@ -361,7 +370,7 @@ __global__ __launch_bounds__(512) void k_attn_frag(const float *__restrict__ qkv
         }
     }
 
-    rs[wave][l32] = 1.0f / (l_run * 32768.0f);  // O accumulated 2^15 P V
+    rs[wave][l32] = l_run > 0.f ? 1.0f / (l_run * 32768.0f) : 0.f;  // O accumulated 2^15 P V
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     float inv[16];
 #pragma unroll
@@ -369,11 +378,12 @@ __global__ __launch_bounds__(512) void k_attn_frag(const float *__restrict__ qkv
         const float4 t = *(const float4 *)&rs[wave][8 * g + 4 * half];
         inv[4 * g] = t.x, inv[4 * g + 1] = t.y, inv[4 * g + 2] = t.z, inv[4 * g + 3] = t.w;
     }
+    float *ob = a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + l32;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const int q = q0 + 8 * (r / 4) + 4 * half + (r % 4);
-        if (q >= T) continue;
-        float *o = out + (rbase + q) * ldo + (int64_t)h * HD + l32;
+        if (q >= Tq) continue;
+        float *o = ob + (int64_t)q * a.o_st;
 #pragma unroll
         for (int n = 0; n < NT; n++) o[32 * n] = oacc[n][r] * inv[r];
     }
@@ -444,9 +454,9 @@ hipError_t launch_qk_norm_rope(float *qkv, int64_t ld, const float *qw, const fl
     return hipGetLastError();
 }
 
-size_t attn_workspace_bytes(int B, int T, int nkv, int hd) {
-    const int nfr = hd == 128 ? kv_frags<128>() : kv_frags<64>();
-    return (size_t)B * nkv * ((T + 31) / 32) * nfr * 1024;
+size_t attn_workspace_bytes(int B, int Tk, int nkv, int hd) {
+    const int nfr = hd == 128 ? kv_frags<128>() : hd == 64 ? kv_frags<64>() : kv_frags<32>();
+    return (size_t)B * nkv * ((Tk + 31) / 32) * nfr * 1024;
 }
 
 hipError_t launch_rope_table(float2 *cs, int T, int hd, float theta_base, hipStream_t s) {
@@ -456,31 +466,49 @@ hipError_t launch_rope_table(float2 *cs, int T, int hd, float theta_base, hipStr
     return hipGetLastError();
 }
 
-// qw / kw: per-head RMS norm weights (NULL: no norm); cs: RoPE table of T positions (NULL: no
-// rotation); ws: attn_workspace_bytes() of device memory for the K/V fragments
+template <int HD>
+static void launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_t s) {
+    const dim3 gk((unsigned)nblk, (unsigned)a.nkv, (unsigned)a.B);
+    const dim3 ga((unsigned)((a.nq + 1) / 2), (unsigned)a.B, (unsigned)((a.Tq + 127) / 128));
+    hipLaunchKernelGGL((k_kv_frag<HD>), gk, dim3(256), 0, s, a, nblk);
+    if (a.mask) hipLaunchKernelGGL((k_attn_frag<HD, true>), ga, dim3(512), 0, s, a, nblk, qscale);
+    else hipLaunchKernelGGL((k_attn_frag<HD, false>), ga, dim3(512), 0, s, a, nblk, qscale);
+}
+
+hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
+    if (a.B <= 0 || a.Tq <= 0 || a.Tk <= 0) return hipSuccess;
+    const bool q_ok = ((uintptr_t)a.q & 15) == 0 && a.q_sb % 4 == 0 && a.q_st % 4 == 0 && a.q_sh % 4 == 0;
+    if (a.nkv <= 0 || a.nq % a.nkv != 0 || !q_ok || ((uintptr_t)a.ws & 15) != 0 || a.B > 65535 ||
+        (a.causal && a.Tq != a.Tk))
+        return hipErrorInvalidValue;
+    const int nblk = (a.Tk + 31) / 32;
+    const float qscale = a.scale * 1.4426950408889634f;  // softmax in base 2
+    switch (a.hd) {
+        case 128: launch_attn_hd<128>(a, nblk, qscale, s); break;
+        case 64: launch_attn_hd<64>(a, nblk, qscale, s); break;
+        case 32: launch_attn_hd<32>(a, nblk, qscale, s); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// The fused q|k|v rows of the decoder (row stride ld floats: nq query heads, then nkv key
+// heads, then nkv value heads, hd floats each) as strided operands.
 hipError_t launch_attn_frag(const float *qkv, int64_t ld, float *out, int64_t ldo, int B, int T, int nq, int nkv,
                             int hd, float scale, int causal, const float *qw, const float *kw, float eps,
                             const float2 *cs, void *ws, hipStream_t s) {
-    if (B <= 0 || T <= 0) return hipSuccess;
-    if (nkv <= 0 || nq % nkv != 0 || ld % 4 != 0 || ((uintptr_t)qkv & 15) != 0 || ((uintptr_t)ws & 15) != 0)
-        return hipErrorInvalidValue;
-    const int nblk = (T + 31) / 32;
-    const float qscale = scale * 1.4426950408889634f;  // softmax in base 2
-    const dim3 gk((unsigned)nblk, (unsigned)nkv, (unsigned)B), ga((unsigned)((nq + 1) / 2), (unsigned)B,
-                                                                 (unsigned)((T + 127) / 128));
-    _Float16 *fr = (_Float16 *)ws;
-    if (hd == 128) {
-        hipLaunchKernelGGL((k_kv_frag<128>), gk, dim3(256), 0, s, qkv, ld, nq, nkv, T, nblk, kw, eps, cs, fr);
-        hipLaunchKernelGGL((k_attn_frag<128>), ga, dim3(512), 0, s, qkv, ld, fr, nblk, out, ldo, T, nq, nkv, qscale,
-                           causal, qw, eps, cs);
-    } else if (hd == 64) {
-        hipLaunchKernelGGL((k_kv_frag<64>), gk, dim3(256), 0, s, qkv, ld, nq, nkv, T, nblk, kw, eps, cs, fr);
-        hipLaunchKernelGGL((k_attn_frag<64>), ga, dim3(512), 0, s, qkv, ld, fr, nblk, out, ldo, T, nq, nkv, qscale,
-                           causal, qw, eps, cs);
-    } else {
-        return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    AttnArgs a;
+    a.q = qkv;
+    a.k = qkv + (int64_t)nq * hd;
+    a.v = qkv + (int64_t)(nq + nkv) * hd;
+    a.q_sb = a.k_sb = a.v_sb = (int64_t)T * ld;
+    a.q_st = a.k_st = a.v_st = ld;
+    a.q_sh = a.k_sh = a.v_sh = hd;
+    a.out = out;
+    a.o_sb = (int64_t)T * ldo, a.o_st = ldo, a.o_sh = hd;
+    a.B = B, a.Tq = a.Tk = T, a.nq = nq, a.nkv = nkv, a.hd = hd;
+    a.scale = scale, a.causal = causal, a.qw = qw, a.kw = kw, a.eps = eps, a.cs = cs, a.ws = ws;
+    return launch_attn(a, s);
 }
 
 hipError_t launch_last_rmsnorm_l2(const float *x, const float *w, float eps, float *out, int B, int T, int H,

@@ -64,6 +64,7 @@ struct GemmArgs {
     const float *wdmin;     // Q4_K
     const _Float16 *wmin;   // Q4_K: weight min-term fragments
     float *y;
+    const float *bias;  // NULL, or N floats added to every row in the store
     int M, N, ldy;
     int m_pad, n_pad;
     int kch;      // 32-byte K chunks per row (kb_pad / 32)
@@ -474,8 +475,27 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
         });
         if constexpr (C::limbs) epilogue(s0 / SPB);
     }
+    // the bias of the lane's output columns, loaded before the wait below so that its latency
+    // overlaps the last DMAs instead of stalling the stores
+    float bv[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int col = n0 + (wn * TN + j) * 32 + lrow;
+        bv[j] = (a.bias && col < a.N) ? a.bias[col] : 0.f;
+    }
     // no DMA may still be writing this workgroup's LDS when it exits
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // the bias goes into the accumulators in one uniform block: used inside the exec-masked
+    // store blocks below, each of them would get its own wait for the load, and a wait for
+    // the load is a wait for every store issued before it (vmcnt counts both)
+    if (a.bias) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int rr = 0; rr < 16; rr++) acc[i][j][rr] += bv[j];
+    }
 
     // store: lanes 0..31 of a register write 32 consecutive floats of one row.
     // (Staging the tile through LDS for 16-byte row stores was measured slower on
@@ -549,7 +569,7 @@ static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
 }
 
 hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
-                       int64_t ldy, hipStream_t s) {
+                       int64_t ldy, hipStream_t s, const float *bias) {
     if (m <= 0 || n <= 0) return hipSuccess;
     const WeightPlanes p = weight_planes(type, n, k);
     const ActPlanes ap = act_planes(type, m, k, true);
@@ -565,6 +585,7 @@ hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const 
     a.wdmin = (const float *)(wb + p.tdmin);
     a.wmin = (const _Float16 *)(wb + p.tmin);
     a.y = y;
+    a.bias = bias;
     a.M = (int)m;
     a.N = (int)n;
     a.ldy = (int)ldy;

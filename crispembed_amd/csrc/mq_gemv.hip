@@ -28,7 +28,8 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
 }
 
 template <int MM>
-__device__ __forceinline__ void wave_sum_store(float (&part)[MM], float *y, int64_t ldy, int row, int lane) {
+__device__ __forceinline__ void wave_sum_store(float (&part)[MM], float *y, int64_t ldy, int row, int lane,
+                                               const float *bias) {
 #pragma unroll
     for (int m = 0; m < MM; m++) {
         float v = part[m];
@@ -41,80 +42,16 @@ __device__ __forceinline__ void wave_sum_store(float (&part)[MM], float *y, int6
 #pragma unroll
         for (int m = 1; m < MM; m++)
             if (lane == m) v = part[m];
-        y[(int64_t)lane * ldy + row] = v;
+        y[(int64_t)lane * ldy + row] = bias ? v + bias[row] : v;
     }
-}
-
-// ---- Q4_K x Q8_K: lane = 8*sb_slot + (2*c + h); lane covers 16 low + 16 high nibbles ----
-template <int MM>
-__global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t *__restrict__ w, const int8_t *__restrict__ xq,
-                                                   const float *__restrict__ xd, const int16_t *__restrict__ xbs,
-                                                   float *__restrict__ y, int N, int K, int64_t ldy) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= N) return;
-    const int nsb = K / QK_K;
-    const uint8_t *wr = w + (int64_t)row * nsb * sizeof(block_q4_K);
-    const int t = lane & 7, c = t >> 1, h = t & 1;
-    float part[MM];
-#pragma unroll
-    for (int m = 0; m < MM; m++) part[m] = 0.f;
-    for (int sb = lane >> 3; sb < nsb; sb += 8) {
-        const uint8_t *blk = wr + sb * sizeof(block_q4_K);
-        const uint4 hdr = *(const uint4 *)blk;
-        const uint4 qv = *(const uint4 *)(blk + 16 + 32 * c + 16 * h);
-        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xffff));
-        const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
-        uint8_t s[12];
-        *(uint32_t *)&s[0] = hdr.y;
-        *(uint32_t *)&s[4] = hdr.z;
-        *(uint32_t *)&s[8] = hdr.w;
-        int sca, ma, scb, mb;
-        {
-            const int ja = 2 * c, jb = 2 * c + 1;
-            if (ja < 4) {
-                sca = s[ja] & 63;
-                ma = s[ja + 4] & 63;
-                scb = s[jb] & 63;
-                mb = s[jb + 4] & 63;
-            } else {
-                sca = (s[ja + 4] & 0xF) | ((s[ja - 4] >> 6) << 4);
-                ma = (s[ja + 4] >> 4) | ((s[ja] >> 6) << 4);
-                scb = (s[jb + 4] & 0xF) | ((s[jb - 4] >> 6) << 4);
-                mb = (s[jb + 4] >> 4) | ((s[jb] >> 6) << 4);
-            }
-        }
-        const uint32_t l0 = qv.x & 0x0F0F0F0F, l1 = qv.y & 0x0F0F0F0F, l2 = qv.z & 0x0F0F0F0F,
-                       l3 = qv.w & 0x0F0F0F0F;
-        const uint32_t h0 = (qv.x >> 4) & 0x0F0F0F0F, h1 = (qv.y >> 4) & 0x0F0F0F0F,
-                       h2 = (qv.z >> 4) & 0x0F0F0F0F, h3 = (qv.w >> 4) & 0x0F0F0F0F;
-#pragma unroll
-        for (int m = 0; m < MM; m++) {
-            const int8_t *xr = xq + (int64_t)m * K + sb * QK_K + 64 * c + 16 * h;
-            const uint4 xa = *(const uint4 *)xr;
-            const uint4 xb = *(const uint4 *)(xr + 32);
-            int sa = dot4(l0, xa.x, 0);
-            sa = dot4(l1, xa.y, sa);
-            sa = dot4(l2, xa.z, sa);
-            sa = dot4(l3, xa.w, sa);
-            int sbv = dot4(h0, xb.x, 0);
-            sbv = dot4(h1, xb.y, sbv);
-            sbv = dot4(h2, xb.z, sbv);
-            sbv = dot4(h3, xb.w, sbv);
-            const int16_t *bs = xbs + (int64_t)m * (K / 16) + sb * 16 + 4 * c + h;
-            const int imain = sca * sa + scb * sbv;
-            const int imin = ma * bs[0] + mb * bs[2];
-            part[m] += xd[(int64_t)m * nsb + sb] * (d * (float)imain - dmin * (float)imin);
-        }
-    }
-    wave_sum_store<MM>(part, y, ldy, row, lane);
 }
 
 // ---- Q8_0 x Q8_0 on the split planes: one 32-value block per lane ----
 template <int MM>
 __global__ __launch_bounds__(256) void k_gemv_q8_0(const int8_t *__restrict__ qs, const uint16_t *__restrict__ d16,
                                                    const int8_t *__restrict__ xq, const float *__restrict__ xd,
-                                                   float *__restrict__ y, int N, int K, int64_t ldy) {
+                                                   float *__restrict__ y, int N, int K, int64_t ldy,
+                                                   const float *__restrict__ bias) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= N) return;
@@ -143,13 +80,14 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0(const int8_t *__restrict__ qs
             part[m] += (float)s * (dw * xd[(int64_t)m * nb + b]);
         }
     }
-    wave_sum_store<MM>(part, y, ldy, row, lane);
+    wave_sum_store<MM>(part, y, ldy, row, lane, bias);
 }
 
 // ---- F16 x F16: 8 halves per lane per step ----
 template <int MM>
 __global__ __launch_bounds__(256) void k_gemv_f16(const uint16_t *__restrict__ w, const uint16_t *__restrict__ xh,
-                                                  float *__restrict__ y, int N, int K, int64_t ldy) {
+                                                  float *__restrict__ y, int N, int K, int64_t ldy,
+                                                  const float *__restrict__ bias) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= N) return;
@@ -171,7 +109,7 @@ __global__ __launch_bounds__(256) void k_gemv_f16(const uint16_t *__restrict__ w
             part[m] = s;
         }
     }
-    wave_sum_store<MM>(part, y, ldy, row, lane);
+    wave_sum_store<MM>(part, y, ldy, row, lane, bias);
 }
 
 // ---- K-quants on MFMA (m <= 8) ----
@@ -333,7 +271,8 @@ __device__ __forceinline__ void q6_compute(const GvLane &L, const Q6W &W, const 
 template <int TYPE, int SBW, int PF>
 __global__ __launch_bounds__(512) void k_gemv_kq_stream(const uint8_t *__restrict__ gv, const int8_t *__restrict__ xq,
                                                         const float *__restrict__ xd, const void *__restrict__ xaux,
-                                                        float *__restrict__ y, int N, int K, int M, int64_t ldy) {
+                                                        float *__restrict__ y, int N, int K, int M, int64_t ldy,
+                                                        const float *__restrict__ bias) {
     constexpr bool Q4 = TYPE == MQ_TYPE_Q4_K;
     constexpr int BYTES = Q4 ? GV4_BYTES : GV6_BYTES;
     using W = typename std::conditional<Q4, Q4W, Q6W>::type;
@@ -368,6 +307,11 @@ __global__ __launch_bounds__(512) void k_gemv_kq_stream(const uint8_t *__restric
 #pragma unroll
     for (int f = 0; f < PF; f++) load(ring[f], t + f * (int)gridDim.x);
     for (int it = 0; t < ntiles; it++, t += gridDim.x) {
+        // the storing lanes' bias, loaded ahead of the prefetch so that waiting for it at the
+        // store does not wait for the next tiles' weights
+        float bz = 0.f;
+        if (bias && threadIdx.x < GV_ROWS * 8 && (int64_t)t * GV_ROWS + (threadIdx.x >> 3) < N)
+            bz = bias[(int64_t)t * GV_ROWS + (threadIdx.x >> 3)];
         load(ring[PF], t + PF * (int)gridDim.x);
         W (&cur)[SBW] = ring[0];
         float part[4] = {0.f, 0.f, 0.f, 0.f};
@@ -389,7 +333,7 @@ __global__ __launch_bounds__(512) void k_gemv_kq_stream(const uint8_t *__restric
 #pragma unroll
             for (int w = 0; w < 8; w++) sum += red[buf][w][rr][mm];
             const int64_t row = (int64_t)t * GV_ROWS + rr;
-            if (row < N && mm < M) y[(int64_t)mm * ldy + row] = sum;
+            if (row < N && mm < M) y[(int64_t)mm * ldy + row] = bias ? sum + bz : sum;
         }
 #pragma unroll
         for (int f = 0; f < PF; f++)
@@ -403,7 +347,8 @@ __global__ __launch_bounds__(512) void k_gemv_kq_stream(const uint8_t *__restric
 template <int TYPE>
 __global__ __launch_bounds__(512) void k_gemv_kq_any(const uint8_t *__restrict__ gv, const int8_t *__restrict__ xq,
                                                      const float *__restrict__ xd, const void *__restrict__ xaux,
-                                                     float *__restrict__ y, int N, int K, int M, int64_t ldy) {
+                                                     float *__restrict__ y, int N, int K, int M, int64_t ldy,
+                                                     const float *__restrict__ bias) {
     constexpr bool Q4 = TYPE == MQ_TYPE_Q4_K;
     constexpr int BYTES = Q4 ? GV4_BYTES : GV6_BYTES;
     __shared__ float red[8][GV_ROWS][8];
@@ -427,13 +372,13 @@ __global__ __launch_bounds__(512) void k_gemv_kq_any(const uint8_t *__restrict__
 #pragma unroll
         for (int w = 0; w < 8; w++) sum += red[w][rr][mm];
         const int64_t row = (int64_t)t * GV_ROWS + rr;
-        if (row < N && mm < M) y[(int64_t)mm * ldy + row] = sum;
+        if (row < N && mm < M) y[(int64_t)mm * ldy + row] = bias ? sum + bias[row] : sum;
     }
 }
 
 template <int TYPE>
 static hipError_t launch_kq_stream(const uint8_t *gv, const int8_t *xq, const float *xd, const void *xaux, float *y,
-                                   int64_t n, int64_t k, int m, int64_t ldy, hipStream_t s) {
+                                   int64_t n, int64_t k, int m, int64_t ldy, const float *bias, hipStream_t s) {
     const int64_t ntiles = (n + GV_ROWS - 1) / GV_ROWS;
     const int nsb = (int)(k / QK_K);
     const int sbw = (nsb + 7) / 8;
@@ -454,20 +399,20 @@ static hipError_t launch_kq_stream(const uint8_t *gv, const int8_t *xq, const fl
     const char *pe = getenv("MQ_GEMV_PF");
     const int pf = pe ? atoi(pe) : 2;
     if (pf == 3 && sbw == 1) {
-        hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 3>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy);
+        hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 3>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy, bias);
         return hipSuccess;
     }
     if (pf == 2 && sbw == 1) {
-        hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 2>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy);
+        hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 2>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy, bias);
         return hipSuccess;
     }
     switch (sbw) {
-        case 1: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 1>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy); break;
-        case 2: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 2, 1>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy); break;
-        case 3: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 3, 1>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy); break;
+        case 1: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 1>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy, bias); break;
+        case 2: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 2, 1>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy, bias); break;
+        case 3: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 3, 1>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy, bias); break;
         default:
             hipLaunchKernelGGL((k_gemv_kq_any<TYPE>), dim3((unsigned)ntiles), block, 0, s, gv, xq, xd, xaux, y, (int)n,
-                               (int)k, m, ldy);
+                               (int)k, m, ldy, bias);
             break;
     }
     return hipSuccess;
@@ -475,21 +420,21 @@ static hipError_t launch_kq_stream(const uint8_t *gv, const int8_t *xq, const fl
 
 template <int MM>
 static hipError_t gemv_launch(int type, const uint8_t *wb, const WeightPlanes &p, int64_t n, int64_t k, const uint8_t *xb,
-                        const ActPlanes &ap, float *y, int64_t ldy, hipStream_t s) {
+                        const ActPlanes &ap, float *y, int64_t ldy, const float *bias, hipStream_t s) {
     const dim3 grid((unsigned)((n + 3) / 4)), block(256);
     const int8_t *xq = (const int8_t *)(xb + ap.xq);
     const float *xd = (const float *)(xb + ap.xd);
     const int16_t *xbs = (const int16_t *)(xb + ap.xbs);
     switch (type) {
-        case MQ_TYPE_Q4_K: return launch_kq_stream<MQ_TYPE_Q4_K>(wb + p.gv, xq, xd, xb + ap.xgm, y, n, k, MM, ldy, s);
-        case MQ_TYPE_Q6_K: return launch_kq_stream<MQ_TYPE_Q6_K>(wb + p.gv, xq, xd, xbs, y, n, k, MM, ldy, s);
+        case MQ_TYPE_Q4_K: return launch_kq_stream<MQ_TYPE_Q4_K>(wb + p.gv, xq, xd, xb + ap.xgm, y, n, k, MM, ldy, bias, s);
+        case MQ_TYPE_Q6_K: return launch_kq_stream<MQ_TYPE_Q6_K>(wb + p.gv, xq, xd, xbs, y, n, k, MM, ldy, bias, s);
         case MQ_TYPE_Q8_0:
             hipLaunchKernelGGL(k_gemv_q8_0<MM>, grid, block, 0, s, (const int8_t *)(wb + p.qs),
-                               (const uint16_t *)(wb + p.d16), xq, xd, y, (int)n, (int)k, ldy);
+                               (const uint16_t *)(wb + p.d16), xq, xd, y, (int)n, (int)k, ldy, bias);
             break;
         case MQ_TYPE_F16:
             hipLaunchKernelGGL(k_gemv_f16<MM>, grid, block, 0, s, (const uint16_t *)wb, (const uint16_t *)xq, y, (int)n,
-                               (int)k, ldy);
+                               (int)k, ldy, bias);
             break;
         default: return hipErrorInvalidValue;
     }
@@ -497,7 +442,7 @@ static hipError_t gemv_launch(int type, const uint8_t *wb, const WeightPlanes &p
 }
 
 hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
-                       int64_t ldy, hipStream_t s) {
+                       int64_t ldy, hipStream_t s, const float *bias) {
     if (m <= 0 || n <= 0) return hipSuccess;
     if (m > 8) return hipErrorInvalidValue;
     const WeightPlanes p = weight_planes(type, n, k);
@@ -506,14 +451,14 @@ hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const 
     const uint8_t *xb = (const uint8_t *)ws;
     hipError_t e = hipErrorInvalidValue;
     switch (m) {
-        case 1: e = gemv_launch<1>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 2: e = gemv_launch<2>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 3: e = gemv_launch<3>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 4: e = gemv_launch<4>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 5: e = gemv_launch<5>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 6: e = gemv_launch<6>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 7: e = gemv_launch<7>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
-        case 8: e = gemv_launch<8>(type, wb, p, n, k, xb, ap, y, ldy, s); break;
+        case 1: e = gemv_launch<1>(type, wb, p, n, k, xb, ap, y, ldy, bias, s); break;
+        case 2: e = gemv_launch<2>(type, wb, p, n, k, xb, ap, y, ldy, bias, s); break;
+        case 3: e = gemv_launch<3>(type, wb, p, n, k, xb, ap, y, ldy, bias, s); break;
+        case 4: e = gemv_launch<4>(type, wb, p, n, k, xb, ap, y, ldy, bias, s); break;
+        case 5: e = gemv_launch<5>(type, wb, p, n, k, xb, ap, y, ldy, bias, s); break;
+        case 6: e = gemv_launch<6>(type, wb, p, n, k, xb, ap, y, ldy, bias, s); break;
+        case 7: e = gemv_launch<7>(type, wb, p, n, k, xb, ap, y, ldy, bias, s); break;
+        case 8: e = gemv_launch<8>(type, wb, p, n, k, xb, ap, y, ldy, bias, s); break;
         default: break;
     }
     if (e != hipSuccess) return e;

@@ -278,9 +278,35 @@ hipError_t launch_quantize_f16(const float *x, int64_t ldx, void *y, int64_t m, 
 hipError_t launch_dequantize(int type, const void *w, float *y, int64_t nrows, int64_t k, int fused, hipStream_t s);
 hipError_t launch_weight_prepare(int type, void *image, int64_t n, int64_t k, int64_t row0, int64_t row1,
                                  hipStream_t s);
+// bias: NULL, or n floats added to every output row as it is stored
 hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
-                       int64_t ldy, hipStream_t s);
+                       int64_t ldy, hipStream_t s, const float *bias = nullptr);
 hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
-                       int64_t ldy, hipStream_t s);
+                       int64_t ldy, hipStream_t s, const float *bias = nullptr);
+
+// Operands of the fragment attention (mq_decoder.hip).  Element (b, t, h, d) of q is at
+// q + b*q_sb + t*q_st + h*q_sh + d (floats; q_sb, q_st, q_sh multiples of 4 and q 16-byte
+// aligned), likewise k, v (any float strides) and out; mask element (b, h, query, key) is at
+// mask + b*m_sb + h*m_sh + query*m_sq + key (fp16 bits; NULL: no mask).  Query head h reads
+// key/value head h / (nq / nkv).  qw / kw: per-head RMS norm weights applied at load (NULL:
+// none); cs: RoPE table of max(Tq, Tk) positions (NULL: no rotation); ws: attn_workspace_bytes
+// of 16-byte aligned device memory.
+struct AttnArgs {
+    const float *q = nullptr, *k = nullptr, *v = nullptr;
+    float *out = nullptr;
+    int64_t q_sb = 0, q_st = 0, q_sh = 0, k_sb = 0, k_st = 0, k_sh = 0, v_sb = 0, v_st = 0, v_sh = 0;
+    int64_t o_sb = 0, o_st = 0, o_sh = 0;
+    const uint16_t *mask = nullptr;
+    int64_t m_sb = 0, m_sh = 0, m_sq = 0;
+    int B = 0, Tq = 0, Tk = 0, nq = 0, nkv = 0, hd = 0;
+    float scale = 1.0f;
+    int causal = 0;
+    const float *qw = nullptr, *kw = nullptr;
+    float eps = 0.f;
+    const float2 *cs = nullptr;
+    void *ws = nullptr;
+};
+size_t attn_workspace_bytes(int B, int Tk, int nkv, int hd);
+hipError_t launch_attn(const AttnArgs &a, hipStream_t s);
 
 }  // namespace mq

@@ -1,0 +1,542 @@
+// mq_ops.hip -- the non-matmul ops of CrispEmbed's graphs (mq_ops.h) on strided ggml-style views.
+//
+// All of them are HBM-bound elementwise or row passes: one read of every input element and one
+// write of every output element is the whole cost, so the kernels are built around coalesced
+// 16-byte accesses (a float4 per lane when the views allow it), grid-stride loops sized to fill
+// the 256 CUs, and one wave per row where a row reduction is needed (norm) or a row is gathered
+// (get_rows).  Attention (mq_op_flash_attn) is the fragment-attention kernel pair of
+// mq_decoder.hip driven through strided operands.
+//
+// ggml semantics followed (ggml-cpu ops.cpp of the ggml submodule; the reference calls them from
+// src/crispembed.cpp:1043-1468): get_rows dst[:, i10, i11, i12] = src[:, ids[i10, i11, i12], i11,
+// i12]; binary ops broadcast src1 by index modulo its extent; norm is two-pass mean / variance with
+// scale 1/sqrtf(var + eps); rms_norm scale 1/sqrtf(mean(x^2) + eps); cpy walks both views in
+// row-major logical order.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <initializer_list>
+
+#include "../../include/mq_ops.h"
+#include "mq_deq.h"
+#include "mq_internal.h"
+#include "mq_runner.h"
+#include "mq_wave.h"
+
+namespace mq {
+namespace {
+
+// device-side copy of a view (byte strides)
+struct DV {
+    char *p;
+    int64_t ne[4];
+    int64_t nb[4];
+};
+
+DV dv(const mq_view *v) {
+    DV d;
+    d.p = (char *)v->data;
+    for (int i = 0; i < 4; i++) d.ne[i] = v->ne[i], d.nb[i] = (int64_t)v->nb[i];
+    return d;
+}
+
+__device__ __forceinline__ int64_t off3(const DV &v, int64_t i1, int64_t i2, int64_t i3) {
+    return i1 * v.nb[1] + i2 * v.nb[2] + i3 * v.nb[3];
+}
+
+// unit u of a view walked W elements at a time along ne0 -> (i0, i1, i2, i3)
+template <int W>
+__device__ __forceinline__ void unflat(int64_t u, const int64_t *ne, int64_t &i0, int64_t &i1, int64_t &i2,
+                                       int64_t &i3) {
+    const int64_t ne0u = ne[0] / W;
+    int64_t r = u / ne0u;
+    i0 = (u - r * ne0u) * W;
+    i1 = r % ne[1];
+    r /= ne[1];
+    i2 = r % ne[2];
+    i3 = r / ne[2];
+}
+
+template <int OP>
+__device__ __forceinline__ float bin(float x, float y) {
+    if constexpr (OP == MQ_BIN_ADD) return x + y;
+    else if constexpr (OP == MQ_BIN_SUB) return x - y;
+    else if constexpr (OP == MQ_BIN_MUL) return x * y;
+    else return x / y;
+}
+
+template <int OP>
+__device__ __forceinline__ float una(float x) {
+    if constexpr (OP == MQ_UNARY_GELU_ERF) {
+        return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+    } else if constexpr (OP == MQ_UNARY_GELU) {
+        const float c = 0.79788456080286535588f;  // sqrt(2 / pi)
+        return 0.5f * x * (1.0f + tanhf(c * x * (1.0f + 0.044715f * x * x)));
+    } else if constexpr (OP == MQ_UNARY_SILU) {
+        return x / (1.0f + expf(-x));
+    } else {
+        return x > 0.0f ? x : 0.0f;
+    }
+}
+
+// dst = a (op) b; W = 4: every view is walked in float4s (b not broadcast along ne0)
+template <int OP, int W>
+__global__ __launch_bounds__(256) void k_binary(const DV a, const DV b, const DV d, int64_t units) {
+    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (int64_t)gridDim.x * 256) {
+        int64_t i0, i1, i2, i3;
+        unflat<W>(u, a.ne, i0, i1, i2, i3);
+        const char *pa = a.p + i0 * 4 + off3(a, i1, i2, i3);
+        const char *pb = b.p + off3(b, i1 % b.ne[1], i2 % b.ne[2], i3 % b.ne[3]);
+        char *pd = d.p + i0 * 4 + off3(d, i1, i2, i3);
+        if constexpr (W == 4) {
+            const float4 x = *(const float4 *)pa, y = *(const float4 *)(pb + i0 * 4);
+            *(float4 *)pd = make_float4(bin<OP>(x.x, y.x), bin<OP>(x.y, y.y), bin<OP>(x.z, y.z), bin<OP>(x.w, y.w));
+        } else {
+            const float x = *(const float *)(a.p + i0 * a.nb[0] + off3(a, i1, i2, i3));
+            const float y = *(const float *)(pb + (i0 % b.ne[0]) * b.nb[0]);
+            *(float *)(d.p + i0 * d.nb[0] + off3(d, i1, i2, i3)) = bin<OP>(x, y);
+        }
+    }
+}
+
+template <int OP, int W>
+__global__ __launch_bounds__(256) void k_unary(const DV x, const DV d, int64_t units) {
+    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (int64_t)gridDim.x * 256) {
+        int64_t i0, i1, i2, i3;
+        unflat<W>(u, x.ne, i0, i1, i2, i3);
+        if constexpr (W == 4) {
+            const float4 v = *(const float4 *)(x.p + i0 * 4 + off3(x, i1, i2, i3));
+            *(float4 *)(d.p + i0 * 4 + off3(d, i1, i2, i3)) =
+                make_float4(una<OP>(v.x), una<OP>(v.y), una<OP>(v.z), una<OP>(v.w));
+        } else {
+            const float v = *(const float *)(x.p + i0 * x.nb[0] + off3(x, i1, i2, i3));
+            *(float *)(d.p + i0 * d.nb[0] + off3(d, i1, i2, i3)) = una<OP>(v);
+        }
+    }
+}
+
+// One wave per row; V values per lane held in registers (row length <= 64 V), or V = 0: the
+// row is read again from memory (L2) for each pass.
+template <int KIND, int V>
+__global__ __launch_bounds__(256) void k_norm(const DV x, const DV r, const DV d, float eps, const float *__restrict__ w,
+                                              const float *__restrict__ bias, int64_t nrows) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+    if (row >= nrows) return;
+    const int n = (int)x.ne[0];
+    const int64_t i1 = row % x.ne[1], i2 = (row / x.ne[1]) % x.ne[2], i3 = row / (x.ne[1] * x.ne[2]);
+    const float *xr = (const float *)(x.p + off3(x, i1, i2, i3));
+    const float *rr = r.p ? (const float *)(r.p + off3(r, i1, i2, i3)) : nullptr;
+    float *dr = (float *)(d.p + off3(d, i1, i2, i3));
+    const float inv_n = 1.0f / (float)n;
+    float mean = 0.f, scale;
+    if constexpr (V > 0) {
+        float v[V], s = 0.f;
+#pragma unroll
+        for (int i = 0; i < V; i++) {
+            const int c = lane + 64 * i;
+            v[i] = c < n ? (rr ? xr[c] + rr[c] : xr[c]) : 0.f;
+            s += KIND == MQ_NORM_LAYER ? v[i] : v[i] * v[i];
+        }
+        if constexpr (KIND == MQ_NORM_LAYER) {
+            mean = wave_sum_f(s) * inv_n;
+            float s2 = 0.f;
+#pragma unroll
+            for (int i = 0; i < V; i++) {
+                const float t = lane + 64 * i < n ? v[i] - mean : 0.f;
+                s2 += t * t;
+            }
+            scale = 1.0f / sqrtf(wave_sum_f(s2) * inv_n + eps);
+        } else {
+            scale = 1.0f / sqrtf(wave_sum_f(s) * inv_n + eps);
+        }
+#pragma unroll
+        for (int i = 0; i < V; i++) {
+            const int c = lane + 64 * i;
+            if (c < n) {
+                float y = (v[i] - mean) * scale;
+                if (w) y = y * w[c];
+                if (bias) y = y + bias[c];
+                dr[c] = y;
+            }
+        }
+    } else {
+        if (rr) {  // long rows: the sum is formed once, in dst, and normalised in place
+            for (int c = lane; c < n; c += 64) dr[c] = xr[c] + rr[c];
+            xr = dr;
+        }
+        float s = 0.f;
+        for (int c = lane; c < n; c += 64) s += KIND == MQ_NORM_LAYER ? xr[c] : xr[c] * xr[c];
+        if constexpr (KIND == MQ_NORM_LAYER) {
+            mean = wave_sum_f(s) * inv_n;
+            float s2 = 0.f;
+            for (int c = lane; c < n; c += 64) s2 += (xr[c] - mean) * (xr[c] - mean);
+            scale = 1.0f / sqrtf(wave_sum_f(s2) * inv_n + eps);
+        } else {
+            scale = 1.0f / sqrtf(wave_sum_f(s) * inv_n + eps);
+        }
+        for (int c = lane; c < n; c += 64) {
+            float y = (xr[c] - mean) * scale;
+            if (w) y = y * w[c];
+            if (bias) y = y + bias[c];
+            dr[c] = y;
+        }
+    }
+}
+
+template <typename S>
+__device__ __forceinline__ float ld_as_f32(const char *p) {
+    if constexpr (sizeof(S) == 4) return *(const float *)p;
+    else return (float)*(const _Float16 *)p;
+}
+template <typename D>
+__device__ __forceinline__ void st_from_f32(char *p, float v) {
+    if constexpr (sizeof(D) == 4) *(float *)p = v;
+    else *(_Float16 *)p = (_Float16)v;  // round to nearest even
+}
+
+// same shape both sides; W = 4: float4 rows (F32 -> F32 only)
+template <typename S, typename D, int W>
+__global__ __launch_bounds__(256) void k_cpy_same(const DV s, const DV d, int64_t units) {
+    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (int64_t)gridDim.x * 256) {
+        int64_t i0, i1, i2, i3;
+        unflat<W>(u, s.ne, i0, i1, i2, i3);
+        if constexpr (W == 4) {
+            *(float4 *)(d.p + i0 * 4 + off3(d, i1, i2, i3)) = *(const float4 *)(s.p + i0 * 4 + off3(s, i1, i2, i3));
+        } else {
+            st_from_f32<D>(d.p + i0 * d.nb[0] + off3(d, i1, i2, i3),
+                           ld_as_f32<S>(s.p + i0 * s.nb[0] + off3(s, i1, i2, i3)));
+        }
+    }
+}
+
+// element u of src in its row-major order goes to element u of dst in its own
+template <typename S, typename D>
+__global__ __launch_bounds__(256) void k_cpy_any(const DV s, const DV d, int64_t n) {
+    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < n; u += (int64_t)gridDim.x * 256) {
+        int64_t a0, a1, a2, a3, b0, b1, b2, b3;
+        unflat<1>(u, s.ne, a0, a1, a2, a3);
+        unflat<1>(u, d.ne, b0, b1, b2, b3);
+        st_from_f32<D>(d.p + b0 * d.nb[0] + off3(d, b1, b2, b3), ld_as_f32<S>(s.p + a0 * s.nb[0] + off3(s, a1, a2, a3)));
+    }
+}
+
+// One wave per gathered row.  A row id outside the table yields a zero row.
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_get_rows(const DV src, const DV ids, const DV d, int64_t nrows) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+    if (row >= nrows) return;
+    const int64_t i10 = row % ids.ne[0], i11 = (row / ids.ne[0]) % ids.ne[1], i12 = row / (ids.ne[0] * ids.ne[1]);
+    const int32_t id = *(const int32_t *)(ids.p + i10 * ids.nb[0] + i11 * ids.nb[1] + i12 * ids.nb[2]);
+    const bool ok = id >= 0 && id < src.ne[1];
+    const uint8_t *sr = (const uint8_t *)src.p + (ok ? (int64_t)id * src.nb[1] : 0) + i11 * src.nb[2] + i12 * src.nb[3];
+    float *dr = (float *)(d.p + off3(d, i10, i11, i12));
+    const int64_t n = src.ne[0];
+    if constexpr (TYPE == MQ_TYPE_F32) {
+        if (ok && n % 4 == 0 && ((uintptr_t)sr & 15) == 0 && ((uintptr_t)dr & 15) == 0) {
+            for (int64_t c = 4 * lane; c < n; c += 256) *(float4 *)(dr + c) = *(const float4 *)(sr + 4 * c);
+            return;
+        }
+    }
+    for (int64_t c = lane; c < n; c += 64) dr[c] = ok ? deq_elem<TYPE>(sr, c) : 0.f;
+}
+
+// ------------------------------------------------------------------ checks ----
+int64_t nel(const mq_view *v) { return v->ne[0] * v->ne[1] * v->ne[2] * v->ne[3]; }
+
+// Checks read only shapes, types and strides (and the data address's alignment, where data is
+// set: mq_op_supported is asked about tensors that are not allocated yet).
+bool shape_ok(const mq_view *v) {
+    for (int i = 0; i < 4; i++)
+        if (v->ne[i] < 1 || v->ne[i] > ((int64_t)1 << 31)) return false;
+    return true;
+}
+
+bool have_data(std::initializer_list<const mq_view *> vs) {
+    for (const mq_view *v : vs)
+        if (v && !v->data) return false;
+    return true;
+}
+
+bool same_shape(const mq_view *a, const mq_view *b) {
+    for (int i = 0; i < 4; i++)
+        if (a->ne[i] != b->ne[i]) return false;
+    return true;
+}
+
+// rows of the view are contiguous elements of `esize` bytes
+bool rows_dense(const mq_view *v, size_t esize) { return v->nb[0] == esize; }
+
+// every float4 access stays 16-byte aligned
+bool vec4_ok(const mq_view *v) {
+    if (v->nb[0] != 4 || v->ne[0] % 4 != 0 || ((uintptr_t)v->data & 15) != 0) return false;
+    for (int i = 1; i < 4; i++)
+        if (v->ne[i] > 1 && v->nb[i] % 16 != 0) return false;
+    return true;
+}
+
+size_t elem_size(int type) { return type == MQ_TYPE_F16 ? 2 : 4; }
+
+const char *check_get_rows(const mq_view *src, const mq_view *ids, const mq_view *dst) {
+    if (!src || !ids || !dst || !shape_ok(src) || !shape_ok(ids) || !shape_ok(dst)) return "missing or empty operand";
+    const int t = src->type;
+    if (t != MQ_TYPE_F32 && t != MQ_TYPE_F16 && t != MQ_TYPE_Q8_0 && t != MQ_TYPE_Q4_K && t != MQ_TYPE_Q6_K)
+        return "get_rows: table type not F32/F16/Q8_0/Q4_K/Q6_K";
+    if (ids->type != MQ_TYPE_I32 || dst->type != MQ_TYPE_F32) return "get_rows: ids must be I32 and dst F32";
+    if (ids->ne[3] != 1) return "get_rows: ids has 4 dimensions";
+    const int64_t bs = blck_size(t);
+    if (src->ne[0] % bs != 0) return "get_rows: row length not a multiple of the block";
+    if (t == MQ_TYPE_F32 || t == MQ_TYPE_F16) {
+        if (src->nb[0] != elem_size(t)) return "get_rows: table rows not contiguous";
+    } else if (src->nb[0] != type_size(t)) {
+        return "get_rows: table rows not contiguous";
+    }
+    if (dst->ne[0] != src->ne[0] || dst->ne[1] != ids->ne[0] || dst->ne[2] != ids->ne[1] || dst->ne[3] != ids->ne[2])
+        return "get_rows: dst shape";
+    if (ids->ne[1] != src->ne[2] || ids->ne[2] != src->ne[3]) return "get_rows: ids / table planes differ";
+    if (dst->nb[0] != 4) return "get_rows: dst rows not contiguous";
+    return nullptr;
+}
+
+const char *check_binary(int op, const mq_view *a, const mq_view *b, const mq_view *d) {
+    if (op < MQ_BIN_ADD || op > MQ_BIN_DIV) return "binary: unknown op";
+    if (!a || !b || !d || !shape_ok(a) || !shape_ok(b) || !shape_ok(d)) return "missing or empty operand";
+    if (a->type != MQ_TYPE_F32 || b->type != MQ_TYPE_F32 || d->type != MQ_TYPE_F32) return "binary: F32 only";
+    if (!same_shape(a, d)) return "binary: dst shape differs from src0";
+    for (int i = 0; i < 4; i++)
+        if (a->ne[i] % b->ne[i] != 0) return "binary: src1 does not broadcast over src0";
+    if (a->nb[0] % 4 || b->nb[0] % 4 || d->nb[0] % 4) return "binary: misaligned strides";
+    return nullptr;
+}
+
+const char *check_unary(int op, const mq_view *x, const mq_view *d) {
+    if (op < MQ_UNARY_GELU_ERF || op > MQ_UNARY_RELU) return "unary: unknown op";
+    if (!x || !d || !shape_ok(x) || !shape_ok(d)) return "missing or empty operand";
+    if (x->type != MQ_TYPE_F32 || d->type != MQ_TYPE_F32) return "unary: F32 only";
+    if (!same_shape(x, d)) return "unary: shapes differ";
+    return nullptr;
+}
+
+const char *check_norm(int kind, const mq_view *x, const mq_view *r, const mq_view *d) {
+    if (kind != MQ_NORM_LAYER && kind != MQ_NORM_RMS) return "norm: unknown kind";
+    if (!x || !d || !shape_ok(x) || !shape_ok(d)) return "missing or empty operand";
+    if (x->type != MQ_TYPE_F32 || d->type != MQ_TYPE_F32) return "norm: F32 only";
+    if (!same_shape(x, d)) return "norm: shapes differ";
+    if (!rows_dense(x, 4) || !rows_dense(d, 4)) return "norm: rows not contiguous";
+    if (r && (!shape_ok(r) || r->type != MQ_TYPE_F32 || !same_shape(x, r) || !rows_dense(r, 4)))
+        return "norm: the added tensor must be F32 with x's shape and contiguous rows";
+    return nullptr;
+}
+
+const char *check_cpy(const mq_view *s, const mq_view *d) {
+    if (!s || !d || !shape_ok(s) || !shape_ok(d)) return "missing or empty operand";
+    if ((s->type != MQ_TYPE_F32 && s->type != MQ_TYPE_F16) || (d->type != MQ_TYPE_F32 && d->type != MQ_TYPE_F16))
+        return "cpy: F32 / F16 only";
+    if (nel(s) != nel(d)) return "cpy: element counts differ";
+    if (s->nb[0] % elem_size(s->type) || d->nb[0] % elem_size(d->type)) return "cpy: misaligned strides";
+    return nullptr;
+}
+
+const char *check_flash(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *m, const mq_view *d) {
+    if (!q || !k || !v || !d || !shape_ok(q) || !shape_ok(k) || !shape_ok(v) || !shape_ok(d))
+        return "missing or empty operand";
+    if (q->type != MQ_TYPE_F32 || k->type != MQ_TYPE_F32 || v->type != MQ_TYPE_F32 || d->type != MQ_TYPE_F32)
+        return "flash_attn: q, k, v and dst must be F32";
+    const int64_t hd = q->ne[0];
+    if (hd != 32 && hd != 64 && hd != 128) return "flash_attn: head_dim not 32, 64 or 128";
+    if (k->ne[0] != hd || v->ne[0] != hd) return "flash_attn: k / v head_dim differs from q";
+    if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2] || k->ne[3] != v->ne[3]) return "flash_attn: k and v shapes differ";
+    if (q->ne[2] % k->ne[2] != 0) return "flash_attn: query heads not a multiple of kv heads";
+    if (k->ne[3] != q->ne[3] || q->ne[3] > 65535) return "flash_attn: batch";
+    if (d->ne[0] != hd || d->ne[1] != q->ne[2] || d->ne[2] != q->ne[1] || d->ne[3] != q->ne[3])
+        return "flash_attn: dst must be [hd, n_head, Tq, B]";
+    if (q->nb[0] != 4 || k->nb[0] != 4 || v->nb[0] != 4 || d->nb[0] != 4) return "flash_attn: head rows not contiguous";
+    if (((uintptr_t)q->data & 15) || q->nb[1] % 16 || q->nb[2] % 16 || q->nb[3] % 16)
+        return "flash_attn: q not 16-byte aligned";
+    for (const mq_view *t : {k, v, d})
+        if (t->nb[1] % 4 || t->nb[2] % 4 || t->nb[3] % 4) return "flash_attn: misaligned strides";
+    if (m) {
+        if (!shape_ok(m) || m->type != MQ_TYPE_F16 || m->nb[0] != 2) return "flash_attn: mask must be F16 rows";
+        if (m->ne[0] < k->ne[1] || m->ne[1] < q->ne[1]) return "flash_attn: mask smaller than [Tk, Tq]";
+        if ((m->ne[2] != 1 && m->ne[2] != q->ne[2]) || (m->ne[3] != 1 && m->ne[3] != q->ne[3]))
+            return "flash_attn: mask heads / batches do not broadcast";
+        if (m->nb[1] % 2 || m->nb[2] % 2 || m->nb[3] % 2) return "flash_attn: misaligned mask strides";
+    }
+    return nullptr;
+}
+
+unsigned grid_units(int64_t units) {
+    const int64_t g = (units + 255) / 256;
+    return (unsigned)(g < 8192 ? (g > 0 ? g : 1) : 8192);
+}
+
+int fail(const char *msg) { return set_error(strstr(msg, "missing") ? MQ_EINVAL : MQ_EUNSUPPORTED, "%s", msg); }
+
+template <int OP>
+void launch_binary_op(const mq_view *a, const mq_view *b, const mq_view *d, hipStream_t s) {
+    const bool v4 = vec4_ok(a) && vec4_ok(d) && b->ne[0] == a->ne[0] && vec4_ok(b);
+    const int64_t units = nel(a) / (v4 ? 4 : 1);
+    if (v4) hipLaunchKernelGGL((k_binary<OP, 4>), dim3(grid_units(units)), dim3(256), 0, s, dv(a), dv(b), dv(d), units);
+    else hipLaunchKernelGGL((k_binary<OP, 1>), dim3(grid_units(units)), dim3(256), 0, s, dv(a), dv(b), dv(d), units);
+}
+
+template <int OP>
+void launch_unary_op(const mq_view *x, const mq_view *d, hipStream_t s) {
+    const bool v4 = vec4_ok(x) && vec4_ok(d);
+    const int64_t units = nel(x) / (v4 ? 4 : 1);
+    if (v4) hipLaunchKernelGGL((k_unary<OP, 4>), dim3(grid_units(units)), dim3(256), 0, s, dv(x), dv(d), units);
+    else hipLaunchKernelGGL((k_unary<OP, 1>), dim3(grid_units(units)), dim3(256), 0, s, dv(x), dv(d), units);
+}
+
+template <int KIND>
+void launch_norm_kind(const mq_view *x, const mq_view *r, const mq_view *d, float eps, const float *w, const float *b,
+                      hipStream_t s) {
+    const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3];
+    const dim3 g((unsigned)((rows + 3) / 4)), blk(256);
+    const int64_t need = (x->ne[0] + 63) / 64;
+    DV rv{};
+    if (r) rv = dv(r);
+    if (need <= 4) hipLaunchKernelGGL((k_norm<KIND, 4>), g, blk, 0, s, dv(x), rv, dv(d), eps, w, b, rows);
+    else if (need <= 8) hipLaunchKernelGGL((k_norm<KIND, 8>), g, blk, 0, s, dv(x), rv, dv(d), eps, w, b, rows);
+    else if (need <= 16) hipLaunchKernelGGL((k_norm<KIND, 16>), g, blk, 0, s, dv(x), rv, dv(d), eps, w, b, rows);
+    else hipLaunchKernelGGL((k_norm<KIND, 0>), g, blk, 0, s, dv(x), rv, dv(d), eps, w, b, rows);
+}
+
+}  // namespace
+}  // namespace mq
+
+using namespace mq;
+
+extern "C" int mq_op_get_rows(const mq_view *src, const mq_view *ids, const mq_view *dst, void *stream) {
+    if (const char *e = check_get_rows(src, ids, dst)) return fail(e);
+    if (!have_data({src, ids, dst})) return fail("missing data pointer");
+    const int64_t rows = ids->ne[0] * ids->ne[1] * ids->ne[2];
+    const dim3 g((unsigned)((rows + 3) / 4)), b(256);
+    hipStream_t s = (hipStream_t)stream;
+    switch (src->type) {
+        case MQ_TYPE_F32: hipLaunchKernelGGL((k_get_rows<MQ_TYPE_F32>), g, b, 0, s, dv(src), dv(ids), dv(dst), rows); break;
+        case MQ_TYPE_F16: hipLaunchKernelGGL((k_get_rows<MQ_TYPE_F16>), g, b, 0, s, dv(src), dv(ids), dv(dst), rows); break;
+        case MQ_TYPE_Q8_0: hipLaunchKernelGGL((k_get_rows<MQ_TYPE_Q8_0>), g, b, 0, s, dv(src), dv(ids), dv(dst), rows); break;
+        case MQ_TYPE_Q4_K: hipLaunchKernelGGL((k_get_rows<MQ_TYPE_Q4_K>), g, b, 0, s, dv(src), dv(ids), dv(dst), rows); break;
+        default: hipLaunchKernelGGL((k_get_rows<MQ_TYPE_Q6_K>), g, b, 0, s, dv(src), dv(ids), dv(dst), rows); break;
+    }
+    return hip_rc(hipGetLastError(), "get_rows");
+}
+
+extern "C" int mq_op_binary(int op, const mq_view *a, const mq_view *b, const mq_view *dst, void *stream) {
+    if (const char *e = check_binary(op, a, b, dst)) return fail(e);
+    if (!have_data({a, b, dst})) return fail("missing data pointer");
+    hipStream_t s = (hipStream_t)stream;
+    switch (op) {
+        case MQ_BIN_ADD: launch_binary_op<MQ_BIN_ADD>(a, b, dst, s); break;
+        case MQ_BIN_SUB: launch_binary_op<MQ_BIN_SUB>(a, b, dst, s); break;
+        case MQ_BIN_MUL: launch_binary_op<MQ_BIN_MUL>(a, b, dst, s); break;
+        default: launch_binary_op<MQ_BIN_DIV>(a, b, dst, s); break;
+    }
+    return hip_rc(hipGetLastError(), "binary op");
+}
+
+extern "C" int mq_op_unary(int op, const mq_view *x, const mq_view *dst, void *stream) {
+    if (const char *e = check_unary(op, x, dst)) return fail(e);
+    if (!have_data({x, dst})) return fail("missing data pointer");
+    hipStream_t s = (hipStream_t)stream;
+    switch (op) {
+        case MQ_UNARY_GELU_ERF: launch_unary_op<MQ_UNARY_GELU_ERF>(x, dst, s); break;
+        case MQ_UNARY_GELU: launch_unary_op<MQ_UNARY_GELU>(x, dst, s); break;
+        case MQ_UNARY_SILU: launch_unary_op<MQ_UNARY_SILU>(x, dst, s); break;
+        default: launch_unary_op<MQ_UNARY_RELU>(x, dst, s); break;
+    }
+    return hip_rc(hipGetLastError(), "unary op");
+}
+
+extern "C" int mq_op_norm(int kind, const mq_view *x, const mq_view *add, const mq_view *dst, float eps,
+                          const float *w, const float *b, void *stream) {
+    if (const char *e = check_norm(kind, x, add, dst)) return fail(e);
+    if (!have_data({x, add, dst})) return fail("missing data pointer");
+    hipStream_t s = (hipStream_t)stream;
+    if (kind == MQ_NORM_LAYER) launch_norm_kind<MQ_NORM_LAYER>(x, add, dst, eps, w, b, s);
+    else launch_norm_kind<MQ_NORM_RMS>(x, add, dst, eps, w, b, s);
+    return hip_rc(hipGetLastError(), "norm");
+}
+
+extern "C" int mq_op_cpy(const mq_view *src, const mq_view *dst, void *stream) {
+    if (const char *e = check_cpy(src, dst)) return fail(e);
+    if (!have_data({src, dst})) return fail("missing data pointer");
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t n = nel(src);
+    const bool f32s = src->type == MQ_TYPE_F32, f32d = dst->type == MQ_TYPE_F32;
+    if (same_shape(src, dst)) {
+        if (f32s && f32d && vec4_ok(src) && vec4_ok(dst)) {
+            hipLaunchKernelGGL((k_cpy_same<float, float, 4>), dim3(grid_units(n / 4)), dim3(256), 0, s, dv(src), dv(dst),
+                               n / 4);
+        } else if (f32s && f32d) {
+            hipLaunchKernelGGL((k_cpy_same<float, float, 1>), dim3(grid_units(n)), dim3(256), 0, s, dv(src), dv(dst), n);
+        } else if (f32s) {
+            hipLaunchKernelGGL((k_cpy_same<float, _Float16, 1>), dim3(grid_units(n)), dim3(256), 0, s, dv(src), dv(dst), n);
+        } else if (f32d) {
+            hipLaunchKernelGGL((k_cpy_same<_Float16, float, 1>), dim3(grid_units(n)), dim3(256), 0, s, dv(src), dv(dst), n);
+        } else {
+            hipLaunchKernelGGL((k_cpy_same<_Float16, _Float16, 1>), dim3(grid_units(n)), dim3(256), 0, s, dv(src),
+                               dv(dst), n);
+        }
+    } else {
+        if (f32s && f32d) hipLaunchKernelGGL((k_cpy_any<float, float>), dim3(grid_units(n)), dim3(256), 0, s, dv(src), dv(dst), n);
+        else if (f32s) hipLaunchKernelGGL((k_cpy_any<float, _Float16>), dim3(grid_units(n)), dim3(256), 0, s, dv(src), dv(dst), n);
+        else if (f32d) hipLaunchKernelGGL((k_cpy_any<_Float16, float>), dim3(grid_units(n)), dim3(256), 0, s, dv(src), dv(dst), n);
+        else hipLaunchKernelGGL((k_cpy_any<_Float16, _Float16>), dim3(grid_units(n)), dim3(256), 0, s, dv(src), dv(dst), n);
+    }
+    return hip_rc(hipGetLastError(), "cpy");
+}
+
+extern "C" size_t mq_op_flash_attn_workspace_bytes(const mq_view *k) {
+    if (!k || (k->ne[0] != 32 && k->ne[0] != 64 && k->ne[0] != 128) || k->ne[1] < 1 || k->ne[2] < 1 || k->ne[3] < 1)
+        return 0;
+    return attn_workspace_bytes((int)k->ne[3], (int)k->ne[1], (int)k->ne[2], (int)k->ne[0]);
+}
+
+extern "C" int mq_op_flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
+                                const mq_view *dst, float scale, void *workspace, size_t workspace_bytes,
+                                void *stream) {
+    if (const char *e = check_flash(q, k, v, mask, dst)) return fail(e);
+    if (!have_data({q, k, v, mask, dst})) return fail("missing data pointer");
+    const size_t need = mq_op_flash_attn_workspace_bytes(k);
+    if (!workspace || ((uintptr_t)workspace & 15) != 0 || workspace_bytes < need)
+        return set_error(MQ_EINVAL, "mq_op_flash_attn: workspace of %zu bytes (16-byte aligned) needed, %zu given",
+                         need, workspace_bytes);
+    AttnArgs a;
+    a.q = (const float *)q->data, a.k = (const float *)k->data, a.v = (const float *)v->data;
+    a.out = (float *)dst->data;
+    a.q_st = q->nb[1] / 4, a.q_sh = q->nb[2] / 4, a.q_sb = q->nb[3] / 4;
+    a.k_st = k->nb[1] / 4, a.k_sh = k->nb[2] / 4, a.k_sb = k->nb[3] / 4;
+    a.v_st = v->nb[1] / 4, a.v_sh = v->nb[2] / 4, a.v_sb = v->nb[3] / 4;
+    a.o_sh = dst->nb[1] / 4, a.o_st = dst->nb[2] / 4, a.o_sb = dst->nb[3] / 4;
+    if (mask) {
+        a.mask = (const uint16_t *)mask->data;
+        a.m_sq = mask->nb[1] / 2;
+        a.m_sh = mask->ne[2] == 1 ? 0 : mask->nb[2] / 2;
+        a.m_sb = mask->ne[3] == 1 ? 0 : mask->nb[3] / 2;
+    }
+    a.B = (int)q->ne[3], a.Tq = (int)q->ne[1], a.Tk = (int)k->ne[1];
+    a.nq = (int)q->ne[2], a.nkv = (int)k->ne[2], a.hd = (int)q->ne[0];
+    a.scale = scale;
+    a.ws = workspace;
+    return hip_rc(launch_attn(a, (hipStream_t)stream), "flash_attn");
+}
+
+extern "C" int mq_op_supported(int op, int sub, const mq_view *s0, const mq_view *s1, const mq_view *s2,
+                               const mq_view *s3, const mq_view *dst) {
+    const char *e = "unknown op";
+    switch (op) {
+        case MQ_OP_GET_ROWS: e = check_get_rows(s0, s1, dst); break;
+        case MQ_OP_BINARY: e = check_binary(sub, s0, s1, dst); break;
+        case MQ_OP_UNARY: e = check_unary(sub, s0, dst); break;
+        case MQ_OP_NORM: e = check_norm(sub, s0, s1, dst); break;
+        case MQ_OP_CPY: e = check_cpy(s0, dst); break;
+        case MQ_OP_FLASH_ATTN: e = check_flash(s0, s1, s2, s3, dst); break;
+        default: break;
+    }
+    return e == nullptr;
+}

@@ -11,6 +11,7 @@
 // a 3-step xor-shuffle max), one wave per 256-value Q8_K block (a 6-step
 // shuffle reduction of the (|x|, index) pair).
 #include "mq_internal.h"
+#include "mq_deq.h"
 
 namespace mq {
 
@@ -372,65 +373,13 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
 // ---------------------------------------------------------------------------
 // Dequantization (ggml to_float), one thread per output value.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void scale_min_k4(int j, const uint8_t *q, int &sc, int &mn) {
-    if (j < 4) {
-        sc = q[j] & 63;
-        mn = q[j + 4] & 63;
-    } else {
-        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
-        mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
-    }
-}
-
 template <int TYPE, bool FUSED>
 __global__ __launch_bounds__(256) void k_dequantize(const uint8_t *__restrict__ w, float *__restrict__ y,
                                                     int64_t nrows, int64_t k) {
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= nrows * k) return;
     const int64_t row = gid / k, col = gid - row * k;
-    const size_t rs = (TYPE == MQ_TYPE_F16) ? (size_t)k * 2
-                                             : (size_t)(k / (TYPE == MQ_TYPE_Q8_0 ? QK8_0 : QK_K)) *
-                                                   (TYPE == MQ_TYPE_Q8_0   ? sizeof(block_q8_0)
-                                                    : TYPE == MQ_TYPE_Q4_K ? sizeof(block_q4_K)
-                                                    : TYPE == MQ_TYPE_Q6_K ? sizeof(block_q6_K)
-                                                                           : sizeof(block_q8_K));
-    const uint8_t *r = w + row * rs;
-    float out = 0.0f;
-    if (TYPE == MQ_TYPE_F16) {
-        out = f16_bits_to_f32(((const uint16_t *)r)[col]);
-    } else if (TYPE == MQ_TYPE_Q8_0) {
-        const uint8_t *b = r + (col / QK8_0) * sizeof(block_q8_0);
-        const float d = f16_bits_to_f32(*(const uint16_t *)b);
-        out = (float)(int8_t)b[2 + col % QK8_0] * d;
-    } else if (TYPE == MQ_TYPE_Q4_K) {
-        const uint8_t *b = r + (col / QK_K) * sizeof(block_q4_K);
-        const int e = (int)(col % QK_K);
-        const int c64 = e >> 6, w64 = e & 63;
-        const uint8_t byte = b[16 + 32 * c64 + (w64 & 31)];
-        const int qv = (w64 < 32) ? (byte & 0xF) : (byte >> 4);
-        int sc, mn;
-        scale_min_k4(e >> 5, b + 4, sc, mn);
-        const float d = f16_bits_to_f32(*(const uint16_t *)b);
-        const float dmin = f16_bits_to_f32(*(const uint16_t *)(b + 2));
-        const float d1 = d * (float)sc;
-        const float m1 = dmin * (float)mn;
-        out = FUSED ? __builtin_fmaf(d1, (float)qv, -m1) : d1 * (float)qv - m1;
-    } else if (TYPE == MQ_TYPE_Q6_K) {
-        const uint8_t *b = r + (col / QK_K) * sizeof(block_q6_K);
-        const int e = (int)(col % QK_K);
-        const int h = e >> 7, rr = e & 127, g = rr >> 5, l = rr & 31;
-        const uint8_t qlb = b[64 * h + l + (g & 1) * 32];
-        const int nib = (g < 2) ? (qlb & 0xF) : (qlb >> 4);
-        const int hb = (b[128 + 32 * h + l] >> (2 * g)) & 3;
-        const int qv = (nib | (hb << 4)) - 32;
-        const int8_t sc = (int8_t)b[192 + 8 * h + (l >> 4) + 2 * g];
-        const float d = f16_bits_to_f32(*(const uint16_t *)(b + 208));
-        out = d * (float)sc * (float)qv;
-    } else if (TYPE == MQ_TYPE_Q8_K) {
-        const uint8_t *b = r + (col / QK_K) * sizeof(block_q8_K);
-        out = *(const float *)b * (float)(int8_t)b[4 + col % QK_K];
-    }
-    y[gid] = out;
+    y[gid] = deq_elem<TYPE, FUSED>(w + row * deq_row_bytes<TYPE>(k), col);
 }
 
 // ---------------------------------------------------------------------------

@@ -9,6 +9,11 @@ TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K = 0, 1, 8, 12, 14
 Q8_0_X86, Q8_0_NEON, Q8_0_REF = 0, 1, 2
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
 PRE_NONE, PRE_GELU_ERF, PRE_SILU_MUL = 0, 1, 2
+TYPE_I32 = 26
+BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV = 0, 1, 2, 3
+UNARY_GELU_ERF, UNARY_GELU, UNARY_SILU, UNARY_RELU = 0, 1, 2, 3
+NORM_LAYER, NORM_RMS = 0, 1
+OP_GET_ROWS, OP_BINARY, OP_UNARY, OP_NORM, OP_CPY, OP_FLASH_ATTN = 0, 1, 2, 3, 4, 5
 
 TYPE_NAMES = {TYPE_F32: "f32", TYPE_F16: "f16", TYPE_Q8_0: "q8_0", TYPE_Q4_K: "q4_K",
               TYPE_Q6_K: "q6_K", TYPE_Q8_K: "q8_K"}
@@ -52,6 +57,7 @@ _SIGS = {
     "mq_quantize_act": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_sz, _c_int, _c_vp]),
     "mq_quantize_act_ex": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_int, _c_vp, _c_sz, _c_int, _c_vp]),
     "mq_mul_mat_q": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_vp]),
+    "mq_mul_mat_q_ex": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_int, _c_vp]),
     "mq_mul_mat_ex": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                                _c_sz, _c_int, _c_vp]),
     # include/mq_bert.h
@@ -100,7 +106,48 @@ _SIGS = {
     "mq_attention_workspace_bytes": (ctypes.c_size_t, [_c_int, _c_int, _c_int, _c_int]),
     "mq_attention": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.c_float,
                               _c_int, _c_vp, ctypes.c_size_t, _c_vp]),
+    # mq_ops.h entries are added after View is defined
 }
+
+
+class View(ctypes.Structure):
+    """mq_view (include/mq_ops.h): ggml metadata of a strided tensor (ne[0] fastest, nb in bytes)."""
+    _fields_ = [("data", _c_vp), ("type", _c_int), ("ne", _c_i64 * 4), ("nb", _c_sz * 4)]
+
+
+_TORCH_TYPES = {"torch.float32": TYPE_F32, "torch.float16": TYPE_F16, "torch.int32": TYPE_I32,
+                "torch.uint8": None}
+
+
+def view(t, type=None, ne=None, nb=None):
+    """mq_view of a torch tensor: ggml order (ne[0] = the last torch dim).  For byte tensors
+    holding quantized rows pass type and the ggml ne / nb explicitly."""
+    v = View()
+    v.data = t.data_ptr() if t is not None else None
+    if ne is None:
+        shape = list(t.shape)[::-1] + [1] * (4 - t.dim())
+        strides = [s_ * t.element_size() for s_ in list(t.stride())[::-1]]
+        strides += [strides[-1] * shape[len(strides) - 1] if strides else t.element_size()] * (4 - len(strides))
+        ne, nb = shape, strides
+        type = _TORCH_TYPES[str(t.dtype)] if type is None else type
+    v.type = type
+    for i in range(4):
+        v.ne[i] = ne[i]
+        v.nb[i] = nb[i]
+    return v
+
+
+_PV = ctypes.POINTER(View)
+_SIGS.update({
+    "mq_op_get_rows": (_c_int, [_PV, _PV, _PV, _c_vp]),
+    "mq_op_binary": (_c_int, [_c_int, _PV, _PV, _PV, _c_vp]),
+    "mq_op_unary": (_c_int, [_c_int, _PV, _PV, _c_vp]),
+    "mq_op_norm": (_c_int, [_c_int, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_vp, _c_vp]),
+    "mq_op_cpy": (_c_int, [_PV, _PV, _c_vp]),
+    "mq_op_flash_attn_workspace_bytes": (_c_sz, [_PV]),
+    "mq_op_flash_attn": (_c_int, [_PV, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_sz, _c_vp]),
+    "mq_op_supported": (_c_int, [_c_int, _c_int, _PV, _PV, _PV, _PV, _PV]),
+})
 
 
 class DecoderHparams(ctypes.Structure):

@@ -140,6 +140,13 @@ int mq_quantize_act(int type, const float *x, int64_t ldx, int64_t m, int64_t k,
 int mq_mul_mat_q(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m, float *y,
                  int64_t ldy, int path, void *stream);
 
+/* mq_mul_mat_q with the linear layer's bias: Y = X W^T + bias, bias an fp32 [n] row (NULL:
+ * none) added to every output row as the GEMM / GEMV stores it -- the MUL_MAT and the ADD of
+ * its bias in the graph (src/crispembed.cpp:1168-1170,1300-1301,1410-1416) in one pass, with
+ * the same fp32 rounding as the ADD node. */
+int mq_mul_mat_q_ex(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m, float *y,
+                    int64_t ldy, const float *bias, int path, void *stream);
+
 /* mq_quantize_act with the graph's elementwise producer folded in: it quantizes
  * op(X + bias) where bias is an fp32 [k] row added to every row of X (NULL: none) and
  * op is one of MQ_PRE_*.  The value quantized is the fp32 tensor the ggml graph

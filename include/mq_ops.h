@@ -1,0 +1,115 @@
+/*
+ * mq_ops.h -- the non-matmul graph ops of CrispEmbed's encoder and decoder graphs on MI355X
+ * (libmq.so), on strided tensor views with ggml's metadata (type, ne[4], nb[4] in bytes).
+ *
+ * These are the ops the MI355X ggml backend executes besides GGML_OP_MUL_MAT, so that the
+ * graph built by build_encoder_graph (src/crispembed.cpp:1043-1468) runs on the GPU without
+ * the scheduler splitting it at every non-matmul node:
+ *   ggml_get_rows        (src/crispembed.cpp:1068-1078)       mq_op_get_rows
+ *   ggml_add / ggml_mul  (src/crispembed.cpp:1071,1137,1301)  mq_op_binary
+ *   ggml_norm            (src/crispembed.cpp:1135,1321,1446)  mq_op_norm (also ggml_rms_norm,
+ *                                                             src/decoder_embed.cpp:717)
+ *   ggml_gelu_erf        (src/crispembed.cpp:1415)            mq_op_unary (also silu, relu, gelu)
+ *   ggml_cont / ggml_cpy (src/crispembed.cpp:1164-1166)       mq_op_cpy
+ *   ggml_flash_attn_ext  (src/crispembed.cpp:1293)            mq_op_flash_attn
+ * The semantics (shapes, broadcasting, op_params) are ggml's, as its CPU backend computes them
+ * (ggml-cpu ops.cpp, the ggml submodule pinned in .gitmodules): the ggml backend passes each
+ * node's tensors straight through.
+ *
+ * Conventions are mq.h's: device pointers, `stream` is a hipStream_t, 0 or a negative MQ_E*
+ * code with mq_last_error().  A view element (i0, i1, i2, i3) is at
+ * data + i0*nb[0] + i1*nb[1] + i2*nb[2] + i3*nb[3]; unused trailing dims have ne = 1.
+ * Shapes a kernel does not handle fail with MQ_EUNSUPPORTED before any launch, and
+ * mq_op_supported answers the same question without launching (the backend's supports_op).
+ */
+#ifndef MQ_OPS_H
+#define MQ_OPS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mq.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MQ_TYPE_I32 26 /* ggml GGML_TYPE_I32: row ids of get_rows */
+
+typedef struct mq_view {
+    void *data;
+    int type; /* MQ_TYPE_* */
+    int64_t ne[4];
+    size_t nb[4]; /* bytes */
+} mq_view;
+
+/* op ids of mq_op_binary / mq_op_unary / mq_op_norm */
+#define MQ_BIN_ADD 0
+#define MQ_BIN_SUB 1
+#define MQ_BIN_MUL 2
+#define MQ_BIN_DIV 3
+
+#define MQ_UNARY_GELU_ERF 0 /* 0.5 x (1 + erf(x / sqrt 2))              ggml_gelu_erf */
+#define MQ_UNARY_GELU 1     /* 0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3)))  ggml_gelu */
+#define MQ_UNARY_SILU 2     /* x / (1 + exp(-x))                         ggml_silu */
+#define MQ_UNARY_RELU 3     /* max(x, 0)                                 ggml_relu */
+
+#define MQ_NORM_LAYER 0 /* (x - mean) / sqrt(var + eps)   ggml_norm */
+#define MQ_NORM_RMS 1   /* x / sqrt(mean(x^2) + eps)      ggml_rms_norm */
+
+/* dst[:, i10, i11, i12] = dequantized row ids[i10, i11, i12] of src plane (i11, i12).
+ * src F32, F16, Q8_0, Q4_K or Q6_K (rows contiguous); ids I32; dst F32 [src.ne0, ids.ne0,
+ * ids.ne1, ids.ne2].  Quantized rows are dequantized with ggml's dequantize_row arithmetic
+ * (bit-identical).  A row id outside [0, src.ne1) is an error the kernel cannot report: the
+ * row is written as zeros instead of reading out of bounds. */
+int mq_op_get_rows(const mq_view *src, const mq_view *ids, const mq_view *dst, void *stream);
+
+/* dst = a (op) b, F32, with b broadcast over a (b.ne[i] divides a.ne[i]); dst has a's shape. */
+int mq_op_binary(int op, const mq_view *a, const mq_view *b, const mq_view *dst, void *stream);
+
+/* dst = f(x) elementwise, F32, same shape. */
+int mq_op_unary(int op, const mq_view *x, const mq_view *dst, void *stream);
+
+/* Row normalisation over ne0, F32, of x (plus `add`, a second F32 tensor of x's shape, when
+ * given: the residual ADD that feeds a post-LN block's norm); then, if given, times w and plus b
+ * (F32 vectors of ne0 floats, broadcast over rows).  The ADD -> NORM -> MUL -> ADD chain of a
+ * post-LN layer norm (src/crispembed.cpp:1320-1323) in one pass; with add, w and b NULL it is
+ * ggml_norm / ggml_rms_norm. */
+int mq_op_norm(int kind, const mq_view *x, const mq_view *add, const mq_view *dst, float eps, const float *w,
+               const float *b, void *stream);
+
+/* Copies src into dst element by element in logical (row-major over ne0..ne3) order; the two
+ * views hold the same number of elements and may differ in shape and strides (ggml_cpy,
+ * ggml_cont, ggml_dup).  F32 / F16 either side (F32 -> F16 rounds to nearest even). */
+int mq_op_cpy(const mq_view *src, const mq_view *dst, void *stream);
+
+/* Multi-head attention, ggml_flash_attn_ext semantics without ALiBi or soft-capping:
+ *   q [hd, Tq, nh, B], k and v [hd, Tk, nkv, B] (F32, any strides that are multiples of 16
+ *   bytes with nb[0] = 4; nh a multiple of nkv: query head h reads kv head h / (nh / nkv)),
+ *   mask NULL or F16 [>= Tk, >= Tq, 1 or nh, 1 or B] added to the scaled scores (-inf masks),
+ *   dst F32 [hd, nh, Tq, B] (strides as q's rules).  hd 32, 64 or 128.
+ * Softmax(scale * q k^T + mask) v in fp32-accurate arithmetic (split-fp16 MFMA products); a
+ * query whose keys are all masked gets a zero row.  workspace: mq_op_flash_attn_workspace_bytes
+ * of device memory (16-byte aligned) for the K/V operand fragments. */
+size_t mq_op_flash_attn_workspace_bytes(const mq_view *k);
+int mq_op_flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask, const mq_view *dst,
+                     float scale, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ids for mq_op_supported */
+#define MQ_OP_GET_ROWS 0
+#define MQ_OP_BINARY 1
+#define MQ_OP_UNARY 2
+#define MQ_OP_NORM 3
+#define MQ_OP_CPY 4
+#define MQ_OP_FLASH_ATTN 5
+
+/* 1 when mq_op_<op> accepts these operands (srcs in the op's argument order, NULL where an
+ * optional operand is absent -- for MQ_OP_NORM src1 is `add`; `sub` is the binary / unary /
+ * norm op id), else 0.  Host only. */
+int mq_op_supported(int op, int sub, const mq_view *src0, const mq_view *src1, const mq_view *src2,
+                    const mq_view *src3, const mq_view *dst);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

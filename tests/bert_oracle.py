@@ -53,14 +53,14 @@ def gelu_erf(x):
     return (0.5 * x * (1.0 + erf(x / np.sqrt(2.0)))).astype(np.float32)
 
 
-def encode(orc, hp, wtype, W, ids):
-    """ids int32 [B, T] -> (pooled fp32 [B, H], last hidden fp32 [B*T, H])."""
+def encode(orc, hp, wtype, W, ids, types=None):
+    """ids (and token types, default 0) int32 [B, T] -> (pooled fp32 [B, H], last hidden fp32 [B*T, H])."""
     B, T = ids.shape
     H, nh = hp["n_embd"], hp["n_head"]
     hd = H // nh
     eps = hp["layer_norm_eps"]
     x = (W["tok"][ids.ravel()] + np.tile(W["pos"][:T], (B, 1))).astype(np.float32)
-    x = (x + W["type"][0]).astype(np.float32)
+    x = (x + (W["type"][0] if types is None else W["type"][np.asarray(types).ravel()])).astype(np.float32)
     x = layernorm(x, W["ln_w"], W["ln_b"], eps)
     for lay in W["layers"]:
         q = linear(orc, wtype, x, lay["wq"], lay["bq"]).astype(np.float64).reshape(B, T, nh, hd)

@@ -165,7 +165,7 @@ int main(int argc, char **argv) {
     }
     // supports_op must refuse what the kernels do not handle (CPU fallback)
     {
-        ggml_init_params ip = {ggml_tensor_overhead() * 8 + ggml_graph_overhead(), nullptr, true};
+        ggml_init_params ip = {ggml_tensor_overhead() * 16 + ggml_graph_overhead(), nullptr, true};
         ggml_context *ctx = ggml_init(ip);
         ggml_tensor *wf32 = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 64, 8);
         ggml_tensor *wf16 = ggml_new_tensor_2d(ctx, GGML_TYPE_F16, 48, 8);  // k % 32 != 0
@@ -176,7 +176,13 @@ int main(int argc, char **argv) {
         if (ggml_backend_supports_op(be, ggml_mul_mat(ctx, wf32, x64))) res.supports = false;
         if (ggml_backend_supports_op(be, ggml_mul_mat(ctx, wf16, x48))) res.supports = false;
         if (ggml_backend_supports_op(be, ggml_mul_mat(ctx, wq, xh))) res.supports = false;
-        if (ggml_backend_supports_op(be, ggml_add(ctx, x64, x64))) res.supports = false;
+        // the encoder's elementwise ops are claimed for F32, refused for F16 operands or
+        // shapes that do not broadcast
+        if (!ggml_backend_supports_op(be, ggml_add(ctx, x64, x64))) res.supports = false;
+        if (!ggml_backend_supports_op(be, ggml_gelu_erf(ctx, x64))) res.supports = false;
+        if (ggml_backend_supports_op(be, ggml_add(ctx, xh, xh))) res.supports = false;
+        if (ggml_backend_supports_op(be, ggml_add(ctx, x64, x48))) res.supports = false;
+        if (ggml_backend_supports_op(be, ggml_unary(ctx, x64, GGML_UNARY_OP_TANH))) res.supports = false;
         ggml_free(ctx);
     }
     const bool correct = res.computed && res.roundtrip && res.partial && res.batched && res.supports &&

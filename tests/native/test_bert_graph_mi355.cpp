@@ -1,0 +1,231 @@
+// test-bert-graph-mi355 -- CrispEmbed's BERT encoder graph, built with ggml's graph API as
+// build_encoder_graph builds it (src/crispembed.cpp:1043-1468, the post-LN path: GET_ROWS
+// embeddings + NORM/MUL/ADD, per layer q/k/v MUL_MAT + ADD (or one fused qkv MUL_MAT and three
+// CONT(VIEW)s), RESHAPE_4D + PERMUTE, FLASH_ATTN_EXT with no mask or the per-item padding mask
+// of encode_tokens_group_4d (src/crispembed.cpp:2052-2127), the output projection, residual
+// ADD + layer norm, and the GELU_ERF FFN), computed entirely by the MI355X backend.
+//
+// usage: test-bert-graph-mi355 model.gguf B T ids.i32 types.i32 lens.i32 out.f32 [--fused-qkv] [--iters N]
+//   ids / types: B*T int32 (item-major, t fastest); lens: B int32 real lengths (all T: no mask);
+//   out: the encoder_out tensor [H, B*T] as float32.  Prints one JSON line.
+#include <chrono>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "ggml-backend.h"
+#include "ggml-mi355.h"
+#include "ggml.h"
+#include "mq_gguf.h"
+
+static std::vector<char> read_file(const char *path) {
+    std::vector<char> v;
+    FILE *f = std::fopen(path, "rb");
+    if (!f) return v;
+    std::fseek(f, 0, SEEK_END);
+    v.resize((size_t)std::ftell(f));
+    std::fseek(f, 0, SEEK_SET);
+    if (std::fread(v.data(), 1, v.size(), f) != v.size()) v.clear();
+    std::fclose(f);
+    return v;
+}
+
+static int fail(const char *msg) {
+    std::printf("{\"ok\": false, \"error\": \"%s\"}\n", msg);
+    return 1;
+}
+
+static uint16_t f16_bits(float x) {  // 0 and -inf only (the mask values)
+    return std::isinf(x) ? 0xFC00 : 0x0000;
+}
+
+int main(int argc, char **argv) {
+    if (argc < 8) return fail("usage: model.gguf B T ids types lens out [--fused-qkv] [--iters N]");
+    const char *path = argv[1];
+    const int B = std::atoi(argv[2]), T = std::atoi(argv[3]);
+    bool fused_qkv = false;
+    int iters = 0;
+    for (int i = 8; i < argc; i++) {
+        if (!std::strcmp(argv[i], "--fused-qkv")) fused_qkv = true;
+        if (!std::strcmp(argv[i], "--iters") && i + 1 < argc) iters = std::atoi(argv[++i]);
+    }
+    const int TB = B * T;
+    std::vector<char> ids_raw = read_file(argv[4]), types_raw = read_file(argv[5]), lens_raw = read_file(argv[6]);
+    if (ids_raw.size() != (size_t)TB * 4 || types_raw.size() != (size_t)TB * 4 || lens_raw.size() != (size_t)B * 4)
+        return fail("bad ids / types / lens file sizes");
+    const int32_t *lens = (const int32_t *)lens_raw.data();
+    bool padded = false;
+    for (int b = 0; b < B; b++) padded |= lens[b] != T;
+
+    ggml_backend_register(ggml_backend_mi355_reg());
+    ggml_backend_t be = ggml_backend_mi355_init(0);
+    if (!be) return fail("no MI355X device");
+
+    mq_gguf *g = mq_gguf_open(path);
+    if (!g) return fail("cannot open the GGUF");
+    const int n_layer = (int)mq_gguf_get_u32(g, "bert.num_hidden_layers", 0);
+    const int H = (int)mq_gguf_get_u32(g, "bert.hidden_size", 0);
+    const int n_head = (int)mq_gguf_get_u32(g, "bert.num_attention_heads", 0);
+    const float eps = mq_gguf_get_f32(g, "bert.layer_norm_eps", 1e-12f);
+    const int hd = H / n_head;
+
+    // weights: one context, one backend buffer, GGUF bytes uploaded with tensor_set
+    const int64_t nt = mq_gguf_n_tensors(g);
+    ggml_init_params wp = {ggml_tensor_overhead() * (size_t)(nt + 8), nullptr, true};
+    ggml_context *wctx = ggml_init(wp);
+    std::map<std::string, ggml_tensor *> W;
+    for (int64_t i = 0; i < nt; i++) {
+        int type, nd;
+        int64_t ne[4];
+        size_t off, nbytes;
+        mq_gguf_tensor_info(g, i, &type, &nd, ne, &off, &nbytes);
+        ggml_tensor *t = ggml_new_tensor_4d(wctx, (ggml_type)type, ne[0], ne[1], ne[2], ne[3]);
+        ggml_set_name(t, mq_gguf_tensor_name(g, i));
+        W[mq_gguf_tensor_name(g, i)] = t;
+    }
+    // the fused q|k|v variant concatenates the three projections into one weight and bias
+    ggml_tensor *qkv_w[64] = {}, *qkv_b[64] = {};
+    if (fused_qkv) {
+        for (int il = 0; il < n_layer; il++) {
+            const std::string p = "enc." + std::to_string(il) + ".attn.";
+            const ggml_tensor *q = W[p + "q.weight"];
+            qkv_w[il] = ggml_new_tensor_2d(wctx, q->type, q->ne[0], 3 * q->ne[1]);
+            qkv_b[il] = ggml_new_tensor_1d(wctx, GGML_TYPE_F32, 3 * q->ne[1]);
+        }
+    }
+    ggml_backend_buffer_t wbuf = ggml_backend_alloc_ctx_tensors(wctx, be);
+    if (!wbuf) return fail("weight buffer allocation failed");
+    for (int64_t i = 0; i < nt; i++) {
+        ggml_tensor *t = W[mq_gguf_tensor_name(g, i)];
+        ggml_backend_tensor_set(t, mq_gguf_tensor_data(g, i), 0, ggml_nbytes(t));
+    }
+    if (fused_qkv) {
+        for (int il = 0; il < n_layer; il++) {
+            const std::string p = "enc." + std::to_string(il) + ".attn.";
+            size_t ow = 0, ob = 0;
+            for (const char *x : {"q", "k", "v"}) {
+                const int64_t iw = mq_gguf_find_tensor(g, (p + x + ".weight").c_str());
+                const int64_t ib = mq_gguf_find_tensor(g, (p + x + ".bias").c_str());
+                const size_t nw = ggml_nbytes(W[p + x + ".weight"]), nbb = ggml_nbytes(W[p + x + ".bias"]);
+                ggml_backend_tensor_set(qkv_w[il], mq_gguf_tensor_data(g, iw), ow, nw);
+                ggml_backend_tensor_set(qkv_b[il], mq_gguf_tensor_data(g, ib), ob, nbb);
+                ow += nw, ob += nbb;
+            }
+        }
+    }
+
+    // the graph (build_encoder_graph's standard post-LN path)
+    ggml_init_params gp = {ggml_tensor_overhead() * (size_t)(n_layer * 64 + 64) + ggml_graph_overhead(), nullptr, true};
+    ggml_context *gctx = ggml_init(gp);
+    ggml_tensor *tok_ids = ggml_new_tensor_1d(gctx, GGML_TYPE_I32, TB);
+    ggml_set_name(tok_ids, "tok_ids");
+    ggml_set_input(tok_ids);
+    ggml_tensor *pos_ids = ggml_new_tensor_1d(gctx, GGML_TYPE_I32, TB);
+    ggml_set_name(pos_ids, "pos_ids");
+    ggml_set_input(pos_ids);
+    ggml_tensor *type_ids = ggml_new_tensor_1d(gctx, GGML_TYPE_I32, TB);
+    ggml_set_name(type_ids, "type_ids");
+    ggml_set_input(type_ids);
+    ggml_tensor *pad_mask = nullptr;
+    if (padded && B > 1) {
+        pad_mask = ggml_new_tensor_4d(gctx, GGML_TYPE_F16, T, T, 1, B);
+        ggml_set_name(pad_mask, "pad_mask");
+        ggml_set_input(pad_mask);
+    }
+    ggml_tensor *cur = ggml_get_rows(gctx, W["token_embd.weight"], tok_ids);
+    cur = ggml_add(gctx, cur, ggml_get_rows(gctx, W["position_embd.weight"], pos_ids));
+    cur = ggml_add(gctx, cur, ggml_get_rows(gctx, W["token_type_embd.weight"], type_ids));
+    cur = ggml_norm(gctx, cur, eps);
+    cur = ggml_mul(gctx, cur, W["embd_ln.weight"]);
+    cur = ggml_add(gctx, cur, W["embd_ln.bias"]);
+    for (int il = 0; il < n_layer; il++) {
+        const std::string p = "enc." + std::to_string(il) + ".";
+        auto w = [&](const char *n) { return W[p + n]; };
+        ggml_tensor *inp = cur, *Q, *K, *V;
+        if (fused_qkv) {
+            ggml_tensor *qkv = ggml_add(gctx, ggml_mul_mat(gctx, qkv_w[il], cur), qkv_b[il]);
+            Q = ggml_cont(gctx, ggml_view_2d(gctx, qkv, H, TB, 3 * H * sizeof(float), 0));
+            K = ggml_cont(gctx, ggml_view_2d(gctx, qkv, H, TB, 3 * H * sizeof(float), H * sizeof(float)));
+            V = ggml_cont(gctx, ggml_view_2d(gctx, qkv, H, TB, 3 * H * sizeof(float), 2 * H * sizeof(float)));
+        } else {
+            Q = ggml_add(gctx, ggml_mul_mat(gctx, w("attn.q.weight"), cur), w("attn.q.bias"));
+            K = ggml_add(gctx, ggml_mul_mat(gctx, w("attn.k.weight"), cur), w("attn.k.bias"));
+            V = ggml_add(gctx, ggml_mul_mat(gctx, w("attn.v.weight"), cur), w("attn.v.bias"));
+        }
+        Q = ggml_permute(gctx, ggml_reshape_4d(gctx, Q, hd, n_head, T, B), 0, 2, 1, 3);
+        K = ggml_permute(gctx, ggml_reshape_4d(gctx, K, hd, n_head, T, B), 0, 2, 1, 3);
+        V = ggml_permute(gctx, ggml_reshape_4d(gctx, V, hd, n_head, T, B), 0, 2, 1, 3);
+        ggml_tensor *attn = ggml_flash_attn_ext(gctx, Q, K, V, pad_mask, 1.0f / std::sqrt((float)hd), 0.0f, 0.0f);
+        attn = ggml_reshape_2d(gctx, attn, H, TB);
+        attn = ggml_add(gctx, ggml_mul_mat(gctx, w("attn.o.weight"), attn), w("attn.o.bias"));
+        cur = ggml_add(gctx, inp, attn);
+        cur = ggml_norm(gctx, cur, eps);
+        cur = ggml_mul(gctx, cur, w("ln1.weight"));
+        cur = ggml_add(gctx, cur, w("ln1.bias"));
+        ggml_tensor *ffn = ggml_add(gctx, ggml_mul_mat(gctx, w("ffn.fc1.weight"), cur), w("ffn.fc1.bias"));
+        ffn = ggml_gelu_erf(gctx, ffn);
+        ffn = ggml_add(gctx, ggml_mul_mat(gctx, w("ffn.fc2.weight"), ffn), w("ffn.fc2.bias"));
+        cur = ggml_add(gctx, cur, ffn);
+        cur = ggml_norm(gctx, cur, eps);
+        cur = ggml_mul(gctx, cur, w("ln2.weight"));
+        cur = ggml_add(gctx, cur, w("ln2.bias"));
+    }
+    ggml_set_name(cur, "encoder_out");
+    ggml_set_output(cur);
+    ggml_cgraph *gf = ggml_new_graph(gctx);
+    ggml_build_forward_expand(gf, cur);
+
+    // every node must be claimed by the backend (nothing would fall back to the CPU)
+    int unsupported = 0;
+    for (int i = 0; i < ggml_graph_n_nodes(gf); i++)
+        if (!ggml_backend_supports_op(be, ggml_graph_node(gf, i))) {
+            std::fprintf(stderr, "unsupported node %d: %s %s\n", i, ggml_op_name(ggml_graph_node(gf, i)->op),
+                         ggml_graph_node(gf, i)->name);
+            unsupported++;
+        }
+    ggml_backend_buffer_t gbuf = ggml_backend_alloc_ctx_tensors(gctx, be);
+    if (!gbuf) return fail("graph buffer allocation failed");
+
+    std::vector<int32_t> pos(TB);
+    for (int b = 0; b < B; b++)
+        for (int t = 0; t < T; t++) pos[(size_t)b * T + t] = t;
+    ggml_backend_tensor_set(tok_ids, ids_raw.data(), 0, (size_t)TB * 4);
+    ggml_backend_tensor_set(type_ids, types_raw.data(), 0, (size_t)TB * 4);
+    ggml_backend_tensor_set(pos_ids, pos.data(), 0, (size_t)TB * 4);
+    if (pad_mask) {
+        std::vector<uint16_t> m((size_t)B * T * T);
+        for (int b = 0; b < B; b++)
+            for (int q = 0; q < T; q++)
+                for (int k = 0; k < T; k++) m[((size_t)b * T + q) * T + k] = f16_bits(k < lens[b] ? 0.f : -INFINITY);
+        ggml_backend_tensor_set(pad_mask, m.data(), 0, m.size() * 2);
+    }
+
+    if (ggml_backend_graph_compute(be, gf) != GGML_STATUS_SUCCESS) return fail("graph_compute failed");
+    std::vector<float> out((size_t)H * TB);
+    ggml_backend_tensor_get(cur, out.data(), 0, out.size() * sizeof(float));
+    FILE *f = std::fopen(argv[7], "wb");
+    if (!f || std::fwrite(out.data(), sizeof(float), out.size(), f) != out.size()) return fail("cannot write output");
+    std::fclose(f);
+
+    double ms = 0.0;
+    if (iters > 0) {
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < iters; i++)
+            if (ggml_backend_graph_compute(be, gf) != GGML_STATUS_SUCCESS) return fail("graph_compute failed");
+        ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() / iters;
+    }
+    std::printf("{\"ok\": true, \"nodes\": %d, \"unsupported\": %d, \"ms_per_graph\": %.4f, \"iters\": %d}\n",
+                ggml_graph_n_nodes(gf), unsupported, ms, iters);
+    ggml_backend_buffer_free(gbuf);
+    ggml_backend_buffer_free(wbuf);
+    ggml_free(gctx);
+    ggml_free(wctx);
+    ggml_backend_free(be);
+    mq_gguf_close(g);
+    return 0;
+}

@@ -17,7 +17,8 @@ def _declared(header):
 def test_libmq_exports_all_declared_symbols():
     from crispembed_amd import mq
     L = mq.lib()
-    names = _declared("mq.h") + _declared("mq_bert.h") + _declared("mq_decoder.h") + _declared("mq_gguf.h")
+    names = (_declared("mq.h") + _declared("mq_bert.h") + _declared("mq_decoder.h") + _declared("mq_gguf.h") +
+             _declared("mq_ops.h"))
     assert len(names) >= 30
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing, missing
@@ -40,6 +41,45 @@ def test_host_only_entry_points_without_gpu():
     assert rc == -2 and b"multiple" in L.mq_last_error()
     rc = L.mq_quantize_act_ex(mq.TYPE_Q8_0, 256, 256, 2, 256, None, 7, 4096, 1 << 20, mq.PATH_AUTO, None)
     assert rc == -1 and b"prologue" in L.mq_last_error()
+
+
+def test_op_support_checks_without_gpu():
+    """mq_op_supported and the argument checks of the graph ops are host code."""
+    from crispembed_amd import mq
+    L = mq.lib()
+    V = mq.View
+
+    def view(ne, type=mq.TYPE_F32, esize=4, data=None):
+        nb = [esize]
+        for i in range(3):
+            nb.append(nb[-1] * ne[i])
+        return mq.view(None, type=type, ne=ne, nb=nb)
+
+    q = view([64, 40, 12, 2])
+    out = view([64, 12, 40, 2])
+    assert L.mq_op_supported(mq.OP_FLASH_ATTN, 0, q, q, q, None, out) == 1
+    assert L.mq_op_supported(mq.OP_FLASH_ATTN, 0, view([48, 40, 12, 2]), view([48, 40, 12, 2]),
+                             view([48, 40, 12, 2]), None, view([48, 12, 40, 2])) == 0  # head_dim 48
+    kv = view([64, 40, 5, 2])
+    assert L.mq_op_supported(mq.OP_FLASH_ATTN, 0, q, kv, kv, None, out) == 0  # 12 heads over 5 kv heads
+    mask = view([40, 40, 1, 2], mq.TYPE_F16, 2)
+    assert L.mq_op_supported(mq.OP_FLASH_ATTN, 0, q, q, q, mask, out) == 1
+    assert L.mq_op_supported(mq.OP_FLASH_ATTN, 0, q, q, q, view([30, 40, 1, 2], mq.TYPE_F16, 2), out) == 0
+    x = view([384, 128, 1, 1])
+    assert L.mq_op_supported(mq.OP_BINARY, mq.BIN_ADD, x, view([384, 1, 1, 1]), None, None, x) == 1
+    assert L.mq_op_supported(mq.OP_BINARY, mq.BIN_ADD, x, view([100, 1, 1, 1]), None, None, x) == 0
+    assert L.mq_op_supported(mq.OP_NORM, mq.NORM_LAYER, x, None, None, None, x) == 1
+    assert L.mq_op_supported(mq.OP_UNARY, 9, x, None, None, None, x) == 0
+    ids = view([128, 1, 1, 1], mq.TYPE_I32)
+    tbl = mq.view(None, type=mq.TYPE_Q8_0, ne=[384, 1000, 1, 1], nb=[34, 408, 408000, 408000])
+    assert L.mq_op_supported(mq.OP_GET_ROWS, 0, tbl, ids, None, None, x) == 1
+    assert L.mq_op_supported(mq.OP_GET_ROWS, 0, tbl, ids, None, None, view([384, 127, 1, 1])) == 0
+    # the entry points reject before launching anything
+    assert L.mq_op_binary(mq.BIN_ADD, x, view([100, 1, 1, 1]), x, None) == -2
+    assert b"broadcast" in L.mq_last_error()
+    assert L.mq_op_norm(mq.NORM_LAYER, x, None, x, 1e-5, None, None, None) == -1  # no data
+    assert L.mq_op_supported(mq.OP_NORM, mq.NORM_LAYER, x, view([384, 64, 1, 1]), None, None, x) == 0
+    assert V is not None
 
 
 def test_ggml_backend_library_exports():

@@ -1,0 +1,108 @@
+"""CrispEmbed's BERT encoder graph (build_encoder_graph, src/crispembed.cpp:1043-1468) built with
+ggml's graph API and computed entirely by the MI355X ggml backend (every node claimed by
+supports_op), checked against the CPU reference encoder on the same GGUF bytes.
+
+Cases: separate and fused q|k|v projections, equal-length batches (no mask) and the rectangular
+padded batch of encode_tokens_group_4d (src/crispembed.cpp:2052-2127: F16 padding mask, each
+item compared with the reference encoding that item alone at its own length), and the graph
+with the backend's fusion switched off (MQ_GGML_NO_FUSION) giving the same result to fp32
+rounding.  Gate: cosine >= 0.99999 per token row and for the pooled embedding."""
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import bert_oracle
+import oracle_ffi as O
+from crispembed_amd import bert, gguf
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+EXE = os.path.join(ROOT, "crispembed_amd", "bin", "test-bert-graph-mi355")
+COSINE_MIN = 0.99999
+HP = dict(n_layer=2, n_embd=128, n_head=4, n_ff=512, n_vocab=500, n_max_pos=64, n_type=2, layer_norm_eps=1e-12)
+
+
+def _run(tmp_path, model, B, T, ids, types, lens, extra=(), env=None):
+    for name, a in (("ids", ids), ("types", types), ("lens", lens)):
+        np.ascontiguousarray(a, dtype=np.int32).tofile(tmp_path / f"{name}.i32")
+    out = tmp_path / "out.f32"
+    r = subprocess.run([EXE, str(model), str(B), str(T), str(tmp_path / "ids.i32"), str(tmp_path / "types.i32"),
+                        str(tmp_path / "lens.i32"), str(out), *extra], capture_output=True, text=True, timeout=300,
+                       env=dict(os.environ, **(env or {})))
+    print(r.stderr[-2000:])
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert r.returncode == 0 and res["ok"], res
+    assert res["unsupported"] == 0
+    return np.fromfile(out, dtype=np.float32).reshape(B * T, -1), res
+
+
+def _cos_rows(a, b):
+    a, b = a.astype(np.float64), b.astype(np.float64)
+    return (a * b).sum(-1) / (np.linalg.norm(a, axis=-1) * np.linalg.norm(b, axis=-1))
+
+
+def _pool(h):
+    p = h.astype(np.float64).mean(0)
+    return p / np.linalg.norm(p)
+
+
+@pytest.mark.parametrize("wtype,hd", [(O.Q8_0, 32), (O.Q8_0, 64), (O.Q4_K, 64), (O.Q6_K, 32), (O.F16, 32)])
+def test_bert_graph_matches_reference(oracle, tmp_path, wtype, hd):
+    hp = dict(HP, n_head=HP["n_embd"] // hd)
+    if wtype in (O.Q4_K, O.Q6_K):
+        hp.update(n_embd=256, n_head=256 // hd)
+    W = bert.synthetic_weights(hp, wtype, name=f"graph{wtype}_{hd}")
+    model = tmp_path / "m.gguf"
+    gguf.write_bert_gguf(model, hp, wtype, W)
+    B, T = 3, 40
+    rng = np.random.default_rng(wtype + hd)
+    ids = rng.integers(0, hp["n_vocab"], (B, T)).astype(np.int32)
+    types = rng.integers(0, 2, (B, T)).astype(np.int32)
+    _, ref = bert_oracle.encode(oracle, hp, wtype, W, ids, types)
+    for extra in ((), ("--fused-qkv",)):
+        got, _ = _run(tmp_path, model, B, T, ids, types, np.full(B, T), extra)
+        cos = _cos_rows(got, ref)
+        print(wtype, hd, extra, "min row cosine", cos.min())
+        assert np.isfinite(got).all() and cos.min() >= COSINE_MIN
+        for b in range(B):
+            assert _pool(got[b * T:(b + 1) * T]) @ _pool(ref[b * T:(b + 1) * T]) >= COSINE_MIN
+
+
+def test_bert_graph_padded_batch(oracle, tmp_path):
+    """encode_tokens_group_4d: items padded to T_max with a -inf key mask; every item's real rows
+    equal the reference encoding of that item alone."""
+    hp = dict(HP)
+    W = bert.synthetic_weights(hp, O.Q8_0, name="graphpad")
+    model = tmp_path / "m.gguf"
+    gguf.write_bert_gguf(model, hp, O.Q8_0, W)
+    lens = np.array([37, 5, 20, 1], dtype=np.int32)
+    B, T = len(lens), int(lens.max())
+    rng = np.random.default_rng(7)
+    ids = np.zeros((B, T), np.int32)
+    types = np.zeros((B, T), np.int32)
+    for b, n in enumerate(lens):
+        ids[b, :n] = rng.integers(0, hp["n_vocab"], n)
+        types[b, :n] = rng.integers(0, 2, n)
+    got, _ = _run(tmp_path, model, B, T, ids, types, lens)
+    for b, n in enumerate(lens):
+        _, ref = bert_oracle.encode(oracle, hp, O.Q8_0, W, ids[b:b + 1, :n], types[b:b + 1, :n])
+        rows = got[b * T:b * T + n]
+        cos = _cos_rows(rows, ref)
+        assert np.isfinite(rows).all() and cos.min() >= COSINE_MIN, (b, cos.min())
+        assert _pool(rows) @ _pool(ref) >= COSINE_MIN
+
+
+def test_bert_graph_fusion_off_agrees(tmp_path):
+    """The fused chains (NORM-MUL-ADD, ADD-GELU_ERF-MUL_MAT) against the node-by-node graph."""
+    W = bert.synthetic_weights(HP, O.Q8_0, name="graphfuse")
+    model = tmp_path / "m.gguf"
+    gguf.write_bert_gguf(model, HP, O.Q8_0, W)
+    B, T = 2, 33
+    ids = np.random.default_rng(8).integers(0, HP["n_vocab"], (B, T)).astype(np.int32)
+    types = np.zeros((B, T), np.int32)
+    a, _ = _run(tmp_path, model, B, T, ids, types, np.full(B, T))
+    b, _ = _run(tmp_path, model, B, T, ids, types, np.full(B, T), env={"MQ_GGML_NO_FUSION": "1"})
+    assert _cos_rows(a, b).min() >= COSINE_MIN

@@ -1,0 +1,314 @@
+"""The graph ops of mq_ops.h on the GPU against numpy restatements of ggml's CPU semantics, on
+strided views as ggml hands them over (permuted, sliced, broadcast).
+
+Bars: get_rows is bit-exact against the oracle's dequantize_row (ggml's arithmetic); binary ops
+and copies are single IEEE operations per element, so bit-exact against numpy float32; norms,
+GELU/SiLU and attention are compared with float64 evaluations of their formulas at the stated
+tolerances (fp32 rounding of a row reduction, libm-vs-device transcendental ulps, and the
+split-fp16 products of the attention kernel)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle_ffi as O
+from crispembed_amd import mq
+from gpu_util import host, stream
+
+pytestmark = pytest.mark.gpu
+
+
+def _t():
+    import torch
+    return torch
+
+
+def _cuda(a):
+    return _t().from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _call(fn, *args):
+    mq.check(fn(*args))
+    _t().cuda.synchronize()
+
+
+# ------------------------------------------------------------------ get_rows ----
+@pytest.mark.parametrize("ttype", [O.F32, O.F16, O.Q8_0, O.Q4_K, O.Q6_K])
+def test_get_rows_bit_exact(oracle, ttype):
+    L = mq.lib()
+    H, V, n = 512, 97, 40
+    tbl = _rng(1).standard_normal((V, H)).astype(np.float32)
+    if ttype == O.F32:
+        raw, ref_tbl = tbl.view(np.uint8).reshape(V, -1), tbl
+    elif ttype == O.F16:
+        raw = tbl.astype(np.float16).view(np.uint8).reshape(V, -1)
+        ref_tbl = tbl.astype(np.float16).astype(np.float32)
+    else:
+        raw = np.ascontiguousarray(oracle.quantize_chunk(ttype, tbl)).reshape(V, -1)
+        ref_tbl = oracle.dequantize(ttype, raw, H)
+    ids = _rng(2).integers(0, V, n).astype(np.int32)
+    ids[3] = V + 5  # out of range: zero row
+    ids[7] = -1
+    d_raw, d_ids = _cuda(raw), _cuda(ids)
+    out = _t().full((n, H), np.nan, dtype=_t().float32, device="cuda")
+    rs = raw.shape[1]
+    nb0 = {O.F32: 4, O.F16: 2, O.Q8_0: 34, O.Q4_K: 144, O.Q6_K: 210}[ttype]
+    src = mq.view(d_raw, type=ttype, ne=[H, V, 1, 1], nb=[nb0, rs, rs * V, rs * V])
+    _call(L.mq_op_get_rows, src, mq.view(d_ids), mq.view(out), stream())
+    ref = ref_tbl[np.clip(ids, 0, V - 1)].copy()
+    ref[[3, 7]] = 0
+    assert np.array_equal(host(out), ref)
+
+
+def test_get_rows_planes_and_strided_dst():
+    """ids [n, 3] pick rows of table plane i11; dst written through a strided view."""
+    L = mq.lib()
+    H, V, P, n = 64, 11, 3, 5
+    tbl = _rng(3).standard_normal((P, V, H)).astype(np.float32)
+    ids = _rng(4).integers(0, V, (P, n)).astype(np.int32)
+    big = _t().zeros((P, n, 2 * H), dtype=_t().float32, device="cuda")
+    dst = big[:, :, H:]
+    _call(L.mq_op_get_rows, mq.view(_cuda(tbl)), mq.view(_cuda(ids)), mq.view(dst), stream())
+    ref = np.stack([tbl[p][ids[p]] for p in range(P)])
+    got = host(big)
+    assert np.array_equal(got[:, :, H:], ref) and not got[:, :, :H].any()
+
+
+# -------------------------------------------------------------------- binary ----
+@pytest.mark.parametrize("op,f", [(mq.BIN_ADD, np.add), (mq.BIN_SUB, np.subtract), (mq.BIN_MUL, np.multiply),
+                                  (mq.BIN_DIV, np.divide)])
+@pytest.mark.parametrize("bshape", ["row", "full", "col", "plane"])
+def test_binary_broadcast_bit_exact(op, f, bshape):
+    L = mq.lib()
+    B, T, H = 3, 17, 384
+    a = _rng(5).standard_normal((B, T, H)).astype(np.float32)
+    b = {"row": (1, 1, H), "full": (B, T, H), "col": (B, T, 1), "plane": (1, T, H)}[bshape]
+    bv = (_rng(6).standard_normal(b) + (3.0 if op == mq.BIN_DIV else 0.0)).astype(np.float32)
+    da, db = _cuda(a), _cuda(bv)
+    out = _t().empty_like(da)
+    _call(L.mq_op_binary, op, mq.view(da), mq.view(db), mq.view(out), stream())
+    assert np.array_equal(host(out), f(a, bv))
+
+
+def test_binary_on_permuted_views():
+    """src0 a permuted (non-contiguous) view, dst a column slice: the scalar path."""
+    L = mq.lib()
+    a = _rng(7).standard_normal((4, 6, 32)).astype(np.float32)
+    da = _cuda(a).permute(1, 0, 2)  # torch (6, 4, 32)
+    b = _rng(8).standard_normal((1, 1, 32)).astype(np.float32)
+    big = _t().zeros((6, 4, 40), dtype=_t().float32, device="cuda")
+    dst = big[:, :, 3:35]
+    _call(L.mq_op_binary, mq.BIN_ADD, mq.view(da), mq.view(_cuda(b)), mq.view(dst), stream())
+    assert np.array_equal(host(big)[:, :, 3:35], a.transpose(1, 0, 2) + b)
+
+
+# --------------------------------------------------------------------- unary ----
+def _gelu_erf64(x):
+    from scipy.special import erf
+    return 0.5 * x * (1.0 + erf(x / np.sqrt(2.0)))
+
+
+UNARY = [
+    (mq.UNARY_GELU_ERF, _gelu_erf64, 1e-6),
+    (mq.UNARY_GELU, lambda x: 0.5 * x * (1 + np.tanh(np.sqrt(2 / np.pi) * (x + 0.044715 * x ** 3))), 1e-6),
+    (mq.UNARY_SILU, lambda x: x / (1 + np.exp(-x)), 1e-6),
+    (mq.UNARY_RELU, lambda x: np.maximum(x, 0), 0.0),
+]
+
+
+@pytest.mark.parametrize("op,f,tol", UNARY)
+def test_unary(op, f, tol):
+    L = mq.lib()
+    x = (_rng(9).standard_normal((33, 1536)) * 3).astype(np.float32)
+    x[0, :8] = [0.0, -0.0, 1e-30, -1e-30, 20.0, -20.0, 8.0, -8.0]
+    dx = _cuda(x)
+    out = _t().empty_like(dx)
+    _call(L.mq_op_unary, op, mq.view(dx), mq.view(out), stream())
+    ref = f(x.astype(np.float64))
+    got = host(out).astype(np.float64)
+    # relative to max(|f(x)|, 1): the 1 + erf / 1 + tanh forms cancel for negative x in fp32
+    # (as in ggml's CPU kernels), which leaves an absolute error of a few 1e-8 |x| there
+    err = np.abs(got - ref) / np.maximum(np.abs(ref), 1.0)
+    assert err.max() <= tol, err.max()
+    # strided view (every other row)
+    sub = dx[::2]
+    out2 = _t().empty_like(sub)
+    _call(L.mq_op_unary, op, mq.view(sub), mq.view(out2), stream())
+    assert np.array_equal(host(out2), host(out)[::2])
+
+
+# ---------------------------------------------------------------------- norm ----
+@pytest.mark.parametrize("n", [100, 384, 768, 1024, 2560])
+@pytest.mark.parametrize("kind", [mq.NORM_LAYER, mq.NORM_RMS])
+def test_norm(kind, n):
+    L = mq.lib()
+    rows = 37
+    x = (_rng(10).standard_normal((rows, n)) * 2 + 0.5).astype(np.float32)
+    w = _rng(11).standard_normal(n).astype(np.float32)
+    b = _rng(12).standard_normal(n).astype(np.float32)
+    eps = 1e-12 if kind == mq.NORM_LAYER else 1e-6
+    x64 = x.astype(np.float64)
+    if kind == mq.NORM_LAYER:
+        y = (x64 - x64.mean(-1, keepdims=True)) / np.sqrt(x64.var(-1, keepdims=True) + eps)
+    else:
+        y = x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + eps)
+    dx = _cuda(x)
+    out = _t().empty_like(dx)
+    _call(L.mq_op_norm, kind, mq.view(dx), None, mq.view(out), eps, None, None, stream())
+    assert np.abs(host(out) - y).max() <= 5e-6 * np.abs(y).max()
+    dw, db = _cuda(w), _cuda(b)
+    _call(L.mq_op_norm, kind, mq.view(dx), None, mq.view(out), eps, ctypes.c_void_p(dw.data_ptr()),
+          ctypes.c_void_p(db.data_ptr()), stream())
+    ref = y * w + b
+    assert np.abs(host(out) - ref).max() <= 5e-6 * np.abs(ref).max()
+    # with the residual: norm(x + r) * w + b, the sum rounded to fp32 first as the ADD node does;
+    # also written in place over x
+    r = _rng(13).standard_normal((rows, n)).astype(np.float32)
+    s64 = (x + r).astype(np.float64)
+    if kind == mq.NORM_LAYER:
+        y2 = (s64 - s64.mean(-1, keepdims=True)) / np.sqrt(s64.var(-1, keepdims=True) + eps)
+    else:
+        y2 = s64 / np.sqrt((s64 ** 2).mean(-1, keepdims=True) + eps)
+    ref2 = y2 * w + b
+    _call(L.mq_op_norm, kind, mq.view(dx), mq.view(_cuda(r)), mq.view(dx), eps, ctypes.c_void_p(dw.data_ptr()),
+          ctypes.c_void_p(db.data_ptr()), stream())
+    assert np.abs(host(dx) - ref2).max() <= 5e-6 * np.abs(ref2).max()
+
+
+# ----------------------------------------------------------------------- cpy ----
+def test_cpy_cont_of_permute_and_qkv_slices():
+    L = mq.lib()
+    # ggml_cont(ggml_permute(x, 0, 2, 1, 3)) of x [hd, nh, T, B]
+    x = _rng(13).standard_normal((2, 9, 6, 32)).astype(np.float32)  # torch (B, T, nh, hd)
+    src = _cuda(x).permute(0, 2, 1, 3)  # (B, nh, T, hd)
+    out = _t().empty(src.shape, dtype=_t().float32, device="cuda")
+    _call(L.mq_op_cpy, mq.view(src), mq.view(out), stream())
+    assert np.array_equal(host(out), x.transpose(0, 2, 1, 3))
+    # ggml_cont(ggml_view_2d(qkv, H, TB, 3H*4, H*4)): the K third of fused q|k|v rows
+    qkv = _rng(14).standard_normal((50, 3 * 384)).astype(np.float32)
+    dq = _cuda(qkv)
+    k = dq[:, 384:768]
+    out = _t().empty((50, 384), dtype=_t().float32, device="cuda")
+    _call(L.mq_op_cpy, mq.view(k), mq.view(out), stream())
+    assert np.array_equal(host(out), qkv[:, 384:768])
+
+
+def test_cpy_types_and_reshape_order():
+    L = mq.lib()
+    x = (_rng(15).standard_normal((8, 6, 10)) * 100).astype(np.float32)
+    dx = _cuda(x)
+    h = _t().empty((8, 6, 10), dtype=_t().float16, device="cuda")
+    _call(L.mq_op_cpy, mq.view(dx), mq.view(h), stream())
+    assert np.array_equal(host(h).view(np.uint16), x.astype(np.float16).view(np.uint16))
+    back = _t().empty((8, 6, 10), dtype=_t().float32, device="cuda")
+    _call(L.mq_op_cpy, mq.view(h), mq.view(back), stream())
+    assert np.array_equal(host(back), x.astype(np.float16).astype(np.float32))
+    # different shapes: element order is row-major over both views (a transposed source)
+    src = dx.permute(2, 1, 0)  # (10, 6, 8) non-contiguous
+    dst = _t().empty((4, 120), dtype=_t().float32, device="cuda")
+    _call(L.mq_op_cpy, mq.view(src), mq.view(dst), stream())
+    assert np.array_equal(host(dst).ravel(), x.transpose(2, 1, 0).ravel())
+
+
+# ----------------------------------------------------------------- attention ----
+def _attn64(q, k, v, mask, scale):
+    """q [B, nh, Tq, hd], k/v [B, nkv, Tk, hd], mask [B|1, nh|1, Tq, Tk] or None -> [B, Tq, nh, hd]"""
+    B, nh, Tq, hd = q.shape
+    g = nh // k.shape[1]
+    kk = np.repeat(k, g, axis=1).astype(np.float64)
+    vv = np.repeat(v, g, axis=1).astype(np.float64)
+    s = np.einsum("bhqd,bhkd->bhqk", q.astype(np.float64), kk) * scale
+    if mask is not None:
+        s = s + mask.astype(np.float64)
+    mx = s.max(-1, keepdims=True)
+    mx = np.where(np.isfinite(mx), mx, 0.0)
+    p = np.exp(s - mx)
+    den = p.sum(-1, keepdims=True)
+    o = np.einsum("bhqk,bhkd->bhqd", p, vv) / np.where(den > 0, den, np.inf)
+    return o.transpose(0, 2, 1, 3)
+
+
+def _flash(q_t, k_t, v_t, mask_t, scale, out_t):
+    L = mq.lib()
+    kv = mq.view(k_t)
+    ws_bytes = L.mq_op_flash_attn_workspace_bytes(kv)
+    ws = _t().empty(ws_bytes + 256, dtype=_t().uint8, device="cuda")
+    wp = ws.data_ptr() + (-ws.data_ptr()) % 256
+    mv = mq.view(mask_t) if mask_t is not None else None
+    _call(L.mq_op_flash_attn, mq.view(q_t), kv, mq.view(v_t), mv, mq.view(out_t), scale, ctypes.c_void_p(wp),
+          ws_bytes, stream())
+
+
+@pytest.mark.parametrize("hd,nh,nkv,B,T", [(32, 12, 12, 3, 77), (64, 12, 12, 2, 128), (128, 8, 2, 2, 45),
+                                           (32, 4, 4, 1, 300)])
+def test_flash_attn_permuted_views(hd, nh, nkv, B, T):
+    """q/k/v as ggml_permute(reshape(x, hd, nh, T, B), 0, 2, 1, 3) of contiguous projections."""
+    rng = _rng(hd + T)
+    qx = rng.standard_normal((B, T, nh, hd)).astype(np.float32)
+    kx = rng.standard_normal((B, T, nkv, hd)).astype(np.float32)
+    vx = rng.standard_normal((B, T, nkv, hd)).astype(np.float32)
+    q = _cuda(qx).permute(0, 2, 1, 3)  # torch (B, nh, T, hd) = ggml [hd, T, nh, B]
+    k = _cuda(kx).permute(0, 2, 1, 3)
+    v = _cuda(vx).permute(0, 2, 1, 3)
+    out = _t().full((B, T, nh, hd), np.nan, dtype=_t().float32, device="cuda")  # ggml [hd, nh, T, B]
+    scale = 1.0 / np.sqrt(hd)
+    _flash(q, k, v, None, scale, out)
+    ref = _attn64(qx.transpose(0, 2, 1, 3), kx.transpose(0, 2, 1, 3), vx.transpose(0, 2, 1, 3), None, scale)
+    err = np.abs(host(out) - ref).max() / np.abs(ref).max()
+    assert err <= 2e-5, err
+
+
+def test_flash_attn_pad_mask():
+    """The rectangular batch of encode_tokens_group_4d: F16 mask [T, T, 1, B], 0 for real keys,
+    -inf for padding; padded query rows still attend to the real keys."""
+    hd, nh, B, T = 32, 6, 4, 50
+    lens = [50, 31, 1, 17]
+    rng = _rng(21)
+    qx, kx, vx = (rng.standard_normal((B, T, nh, hd)).astype(np.float32) for _ in range(3))
+    mask = np.zeros((B, 1, T, T), dtype=np.float16)
+    for b, n in enumerate(lens):
+        mask[b, 0, :, n:] = -np.inf
+    q, k, v = (_cuda(x).permute(0, 2, 1, 3) for x in (qx, kx, vx))
+    out = _t().empty((B, T, nh, hd), dtype=_t().float32, device="cuda")
+    _flash(q, k, v, _cuda(mask), 1.0 / np.sqrt(hd), out)
+    ref = _attn64(qx.transpose(0, 2, 1, 3), kx.transpose(0, 2, 1, 3), vx.transpose(0, 2, 1, 3), mask,
+                  1.0 / np.sqrt(hd))
+    assert np.abs(host(out) - ref).max() / np.abs(ref).max() <= 2e-5
+
+
+def test_flash_attn_general_mask_and_empty_rows():
+    """A finite additive mask per head (relative-position bias style), Tq != Tk, and query rows
+    whose keys are all masked (zero output)."""
+    hd, nh, B, Tq, Tk = 64, 4, 2, 20, 70
+    rng = _rng(22)
+    qx = rng.standard_normal((B, Tq, nh, hd)).astype(np.float32)
+    kx, vx = (rng.standard_normal((B, Tk, nh, hd)).astype(np.float32) for _ in range(2))
+    mask = (rng.standard_normal((B, nh, Tq, Tk)) * 2).astype(np.float16)
+    mask[:, :, 5, :] = -np.inf
+    mask[1, 2, 7, :] = -np.inf
+    mask[0, 1, 9, 40:] = -np.inf
+    q, k, v = (_cuda(x).permute(0, 2, 1, 3) for x in (qx, kx, vx))
+    out = _t().empty((B, Tq, nh, hd), dtype=_t().float32, device="cuda")
+    _flash(q, k, v, _cuda(mask), 0.125, out)
+    ref = _attn64(qx.transpose(0, 2, 1, 3), kx.transpose(0, 2, 1, 3), vx.transpose(0, 2, 1, 3), mask, 0.125)
+    got = host(out)
+    assert np.isfinite(got).all()
+    assert not got[:, 5].any() and not got[1, 7, 2].any()
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= 2e-5
+
+
+def test_op_rejections_name_the_problem():
+    L = mq.lib()
+    x = _t().zeros((4, 48), dtype=_t().float32, device="cuda")
+    v = mq.view(x.view(1, 4, 1, 48))
+    assert L.mq_op_flash_attn(v, v, v, None, v, 1.0, None, 0, stream()) == -2
+    assert b"head_dim" in L.mq_last_error()
+    assert L.mq_op_supported(mq.OP_FLASH_ATTN, 0, v, v, v, None, v) == 0
+    a, b = mq.view(x), mq.view(_t().zeros((3, 48), dtype=_t().float32, device="cuda"))
+    assert L.mq_op_binary(mq.BIN_ADD, a, b, a, stream()) == -2
+    assert b"broadcast" in L.mq_last_error()
+    assert L.mq_op_supported(mq.OP_BINARY, mq.BIN_ADD, a, a, None, None, a) == 1

@@ -85,3 +85,40 @@ def test_gelu_prologue_mul_mat(oracle, wtype, m, n, k, ld, path):
     e2 = rel_err(y, oracle.mul_mat_q(wtype, w, xq, k))
     assert e1 <= TOL and e2 <= TOL, (e1, e2, same)
 
+
+
+@pytest.mark.parametrize("wtype", TYPES)
+@pytest.mark.parametrize("m,n,k,path", [(1, 300, 512, 1), (6, 70, 1536, 1), (77, 96, 512, 2), (300, 200, 1536, 2)])
+def test_mul_mat_q_ex_bias_in_store(wtype, m, n, k, path):
+    """mq_mul_mat_q_ex adds the bias as the GEMM / GEMV stores each row: bit-identical to the
+    plain mat-mul followed by one fp32 add per element (the graph's ADD node)."""
+    import torch
+    from crispembed_amd import mq
+    L = mq.lib()
+    rng = np.random.default_rng(m * 7 + n + k + wtype)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    wq = np.ascontiguousarray(mq_quantized(wtype, w))
+    _, wptr = img = weight_image(wtype, wq, n, k)
+    x = dev(rng.standard_normal((m, k)).astype(np.float32))
+    bias = rng.standard_normal(n).astype(np.float32)
+    _, ptr, _ = ws = _quant(wtype, x, m, k, path)
+    y0 = torch.full((m, n + 3), np.nan, dtype=torch.float32, device="cuda")
+    y1 = torch.full((m, n + 3), np.nan, dtype=torch.float32, device="cuda")
+    mq.check(L.mq_mul_mat_q(wtype, ctypes.c_void_p(wptr), n, k, ctypes.c_void_p(ptr), m, ctypes.c_void_p(y0.data_ptr()),
+                            n + 3, path, stream()))
+    bd = dev(bias)
+    mq.check(L.mq_mul_mat_q_ex(wtype, ctypes.c_void_p(wptr), n, k, ctypes.c_void_p(ptr), m,
+                               ctypes.c_void_p(y1.data_ptr()), n + 3, ctypes.c_void_p(bd.data_ptr()), path, stream()))
+    a, b = host(y0), host(y1)
+    assert np.array_equal(b[:, :n], a[:, :n] + bias)
+    assert np.isnan(b[:, n:]).all()
+    del img, ws
+
+
+def mq_quantized(wtype, w):
+    from crispembed_amd import mq
+    L = mq.lib()
+    n, k = w.shape
+    out = np.zeros(L.mq_gguf_bytes(wtype, n, k), dtype=np.uint8)
+    L.mq_quantize_chunk(wtype, w.ctypes.data, out.ctypes.data, n, k)
+    return out
