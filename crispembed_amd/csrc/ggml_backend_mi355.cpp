@@ -10,15 +10,15 @@
 //
 // graph_compute fuses chains whose intermediate results have no other reader
 // (ggml_node_get_use_count == 1) and are not graph outputs:
-//   MUL_MAT -> ADD(bias)                           the bias added by the GEMM / GEMV store
+//   MUL_MAT [-> ADD(bias)], with the MUL_MATs after it on the same activation
+//                                                  one grouped GEMM, biases added by its store
 //   [ADD(residual) ->] NORM|RMS_NORM -> MUL(w) [-> ADD(b)]
 //                                                  one row pass (mq_op_norm)
 //   ADD(bias) -> UNARY(GELU_ERF) -> MUL_MAT [-> ADD(bias)]
 //                                                  bias and GELU applied while the activation
 //                                                  is quantized for the mat-mul
 // and MUL_MATs that read the same activation with the same weight type and shape
-// one after another (q, k and v of a layer) quantize it once.  MQ_GGML_NO_FUSION=1
-// runs every node on its own.
+// one after another quantize it once.  MQ_GGML_NO_FUSION=1 runs every node on its own.
 //
 // Threading: like every ggml backend, one backend instance must be driven by one
 // thread at a time (src/core/gpu_backend_pref.h:180-185); each instance owns one
@@ -470,23 +470,80 @@ int try_fuse_bias_gelu_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, enu
     return dst == mm ? 3 : 4;
 }
 
-// MUL_MAT -> ADD(., bias): the bias added in the mat-mul's store.  Left alone when the ADD
-// starts a bias -> GELU_ERF -> MUL_MAT chain (that fusion saves more).
-int try_fuse_mul_mat_bias(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status &st) {
-    ggml_tensor *mm = ggml_graph_node(cg, i);
-    if (i + 1 >= n || !feeds_only_next(cg, i) || !flat_mul_mat(mm)) return 0;
-    ggml_tensor *add = ggml_graph_node(cg, i + 1);
-    const int64_t N = mm->src[0]->ne[1];
-    if (add->op != GGML_OP_ADD || add->src[0] != mm || !is_row_vector(add->src[1], N)) return 0;
-    if (!rows_flat(add) || add->nb[0] != sizeof(float) || add->nb[1] % sizeof(float)) return 0;
-    if (i + 3 < n && feeds_only_next(cg, i + 1)) {
-        const ggml_tensor *u = ggml_graph_node(cg, i + 2), *m2 = ggml_graph_node(cg, i + 3);
+// A MUL_MAT of a group and the bias ADD fused into its store (add_idx < 0: none).
+struct MulMatMember {
+    ggml_tensor *mm, *dst;
+    const float *bias;
+    int idx, add_idx;
+};
+
+// MUL_MAT j with the ADD(., bias) that follows it, when the ADD can go into the store.  Left
+// alone when the ADD starts a bias -> GELU_ERF -> MUL_MAT chain (that fusion saves more).
+MulMatMember mul_mat_member(ggml_cgraph *cg, int j, int n) {
+    ggml_tensor *mm = ggml_graph_node(cg, j);
+    MulMatMember m{mm, mm, nullptr, j, -1};
+    if (j + 1 >= n || !feeds_only_next(cg, j)) return m;
+    ggml_tensor *add = ggml_graph_node(cg, j + 1);
+    if (add->op != GGML_OP_ADD || add->src[0] != mm || !is_row_vector(add->src[1], mm->src[0]->ne[1])) return m;
+    if (!rows_flat(add) || add->nb[0] != sizeof(float) || add->nb[1] % sizeof(float)) return m;
+    if (j + 3 < n && feeds_only_next(cg, j + 1)) {
+        const ggml_tensor *u = ggml_graph_node(cg, j + 2), *m2 = ggml_graph_node(cg, j + 3);
         if (u->op == GGML_OP_UNARY && ggml_get_unary_op(u) == GGML_UNARY_OP_GELU_ERF && u->src[0] == add &&
             m2->op == GGML_OP_MUL_MAT && m2->src[1] == u)
-            return 0;
+            return m;
     }
-    st = mul_mat_flat(c, mm->src[0], mm->src[1], add, (const float *)add->src[1]->data, mm);
-    return 2;
+    m.dst = add;
+    m.bias = (const float *)add->src[1]->data;
+    m.add_idx = j + 1;
+    return m;
+}
+
+// MUL_MAT [-> ADD(bias)] at node i and the MUL_MATs after it that read the same activation with
+// the same weight type and k (q, k and v of a layer), separated only by view nodes and their
+// own bias ADDs: one activation quantization and one grouped launch.  Returns the nodes
+// consumed from i on; the later members (and their ADDs) are marked in `done`.
+int try_group_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, std::vector<char> &done, enum ggml_status &st) {
+    ggml_tensor *mm = ggml_graph_node(cg, i);
+    if (!flat_mul_mat(mm)) return 0;
+    const ggml_tensor *x = mm->src[1], *w0 = mm->src[0];
+    MulMatMember mem[4];
+    int nm = 0;
+    mem[nm++] = mul_mat_member(cg, i, n);
+    for (int j = (mem[0].add_idx >= 0 ? mem[0].add_idx : i) + 1; j < n && nm < 4; j++) {
+        ggml_tensor *t = ggml_graph_node(cg, j);
+        if (is_view_op(t->op) || ggml_is_empty(t)) continue;
+        if (t->op != GGML_OP_MUL_MAT || done[j] || t->src[1] != x || t->src[0]->type != w0->type ||
+            t->src[0]->ne[0] != w0->ne[0] || !flat_mul_mat(t))
+            break;
+        mem[nm] = mul_mat_member(cg, j, n);
+        if (mem[nm].add_idx >= 0) j = mem[nm].add_idx;
+        nm++;
+    }
+    if (nm == 1 && mem[0].add_idx < 0) return 0;  // a lone MUL_MAT: the plain path
+    const int mt = mq_type_of(w0->type);
+    const int64_t K = w0->ne[0], M = x->ne[1] * x->ne[2] * x->ne[3];
+    const void *w[4];
+    int64_t nn[4], ldy[4];
+    float *y[4];
+    const float *b[4];
+    for (int g = 0; g < nm; g++) {
+        w[g] = mem[g].mm->src[0]->data;
+        nn[g] = mem[g].mm->src[0]->ne[1];
+        y[g] = (float *)mem[g].dst->data;
+        ldy[g] = (int64_t)(mem[g].dst->nb[1] / sizeof(float));
+        b[g] = mem[g].bias;
+    }
+    int rc = quantize_x(c, x, mt, M, K);
+    if (rc == 0) rc = mq_mul_mat_q_group(mt, nm, w, nn, K, c->ws, M, y, ldy, b, MQ_PATH_AUTO, c->stream);
+    if (rc != 0) {
+        std::fprintf(stderr, "ggml-mi355: MUL_MAT '%s' (%d grouped) failed: %s\n", mm->name, nm, mq_last_error());
+        st = rc == MQ_ENOMEM ? GGML_STATUS_ALLOC_FAILED : GGML_STATUS_FAILED;
+    }
+    for (int g = 1; g < nm; g++) {
+        done[mem[g].idx] = 1;
+        if (mem[g].add_idx >= 0) done[mem[g].add_idx] = 1;
+    }
+    return mem[0].add_idx >= 0 ? 2 : 1;
 }
 
 enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node) {
@@ -545,16 +602,17 @@ enum ggml_status be_graph_compute(ggml_backend_t be, ggml_cgraph *cg) {
     const int n = ggml_graph_n_nodes(cg);
     const bool fuse = std::getenv("MQ_GGML_NO_FUSION") == nullptr;
     c->ws_x = nullptr;  // the inputs may have been rewritten since the last graph
+    std::vector<char> done(n, 0);  // nodes already computed as part of an earlier group
     for (int i = 0; i < n; i++) {
         ggml_tensor *node = ggml_graph_node(cg, i);
-        if (ggml_is_empty(node) || is_view_op(node->op)) continue;
+        if (done[i] || ggml_is_empty(node) || is_view_op(node->op)) continue;
         enum ggml_status st = GGML_STATUS_SUCCESS;
         int used = 0;
         // a quantized activation stays reusable only from one mat-mul to the next
         if (node->op != GGML_OP_MUL_MAT || !fuse) c->ws_x = nullptr;
         if (fuse) {
             switch (node->op) {
-                case GGML_OP_MUL_MAT: used = try_fuse_mul_mat_bias(c, cg, i, n, st); break;
+                case GGML_OP_MUL_MAT: used = try_group_mul_mat(c, cg, i, n, done, st); break;
                 case GGML_OP_NORM:
                 case GGML_OP_RMS_NORM: used = try_fuse_norm(c, cg, i, n, st); break;
                 case GGML_OP_ADD:

@@ -276,6 +276,34 @@ int mq_mul_mat_q_ex(int type, const void *w_image, int64_t n, int64_t k, const v
     return e == hipSuccess ? MQ_OK : hip_fail(e, path == MQ_PATH_GEMV ? "gemv" : "gemm");
 }
 
+int mq_mul_mat_q_group(int type, int n_groups, const void *const *w_images, const int64_t *n, int64_t k,
+                       const void *workspace, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,
+                       int path, void *stream) {
+    if (n_groups < 1 || n_groups > 4 || !w_images || !n || !y || !ldy)
+        return fail(MQ_EINVAL, "mq_mul_mat_q_group: 1 to 4 groups with weights, n, y and ldy");
+    for (int g = 0; g < n_groups; g++) {
+        const int rc = check_weight_shape(type, n[g], k);
+        if (rc) return rc;
+        if (!w_images[g] || !y[g] || ldy[g] < n[g] || !is_aligned(w_images[g], 256))
+            return fail(MQ_EINVAL, "mq_mul_mat_q_group: group %d: bad weight image, output or ldy", g);
+    }
+    if (!workspace || m < 0 || m > INT32_MAX || !is_aligned(workspace, 256))
+        return fail(MQ_EINVAL, "mq_mul_mat_q_group: bad workspace or m");
+    if (m == 0) return MQ_OK;
+    path = resolve_path(path, m);
+    if (path < 0) return path;
+    if (path == MQ_PATH_GEMV) {  // weight-streaming: one launch per weight costs nothing extra
+        for (int g = 0; g < n_groups; g++) {
+            const hipError_t e = launch_gemv(type, w_images[g], n[g], k, workspace, m, y[g], ldy[g], (hipStream_t)stream,
+                                             bias ? bias[g] : nullptr);
+            if (e != hipSuccess) return hip_fail(e, "gemv");
+        }
+        return MQ_OK;
+    }
+    const hipError_t e = launch_gemm_group(type, n_groups, w_images, n, k, workspace, m, y, ldy, bias, (hipStream_t)stream);
+    return e == hipSuccess ? MQ_OK : hip_fail(e, "gemm");
+}
+
 int mq_mul_mat_q(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m, float *y,
                  int64_t ldy, int path, void *stream) {
     return mq_mul_mat_q_ex(type, w_image, n, k, workspace, m, y, ldy, nullptr, path, stream);

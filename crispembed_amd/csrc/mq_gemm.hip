@@ -42,6 +42,7 @@
 // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 #include "mq_internal.h"
 
+#include <climits>
 #include <type_traits>
 
 namespace mq {
@@ -53,6 +54,8 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 enum { FMT_Q8_0 = 0, FMT_Q4_K = 1, FMT_Q6_K = 2, FMT_F16 = 3 };
+
+constexpr int GEMM_GROUPS = 4;
 
 struct GemmArgs {
     const int8_t *xq;       // tiled activations
@@ -71,6 +74,19 @@ struct GemmArgs {
     int nstages;  // kb_pad / 128
     int nsb;      // K / 256
     int tiles_m, tiles_n, group_m;
+    // grouped launch (GEMM_GROUPS weights on the same activation and k): group g > 0 has its
+    // own weight planes, output, bias and N in grp[g - 1] and owns the feature tiles
+    // [tn_start[g], tn_start[g + 1]); tn_start[g] = INT_MAX past the last group
+    int ngroups;
+    int tn_start[GEMM_GROUPS];
+    struct Group {
+        const int8_t *wq, *whi;
+        const float *wd, *wdmin;
+        const _Float16 *wmin;
+        float *y;
+        const float *bias;
+        int N, n_pad, ldy;
+    } grp[GEMM_GROUPS - 1];
 };
 
 constexpr int NBUF = 4;   // stage ring in LDS
@@ -238,7 +254,7 @@ __device__ __forceinline__ DmaItem epi_item(const GemmArgs &a, int e, int sb, in
 }
 
 template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2>
-__global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
+__global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) {
     using C = Cfg<FMT, WM, WN, TM, TN, KCT>;
     constexpr int KC = C::KC, SPB = C::SPB;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
@@ -252,10 +268,24 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a) {
     int t = blockIdx.x;
     const int nt = gridDim.x;
     if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);
-    const int per_group = a.group_m * a.tiles_n;
+    const int per_group = a0.group_m * a0.tiles_n;
     const int grp = t / per_group, r = t - grp * per_group;
-    const int gm = min(a.group_m, a.tiles_m - grp * a.group_m);
-    const int tm = grp * a.group_m + r % gm, tn = r / gm;
+    const int gm = min(a0.group_m, a0.tiles_m - grp * a0.group_m);
+    const int tm = grp * a0.group_m + r % gm;
+    int tn = r / gm;
+    // the weight group owning feature tile tn (uniform: scalar selects)
+    GemmArgs a = a0;
+    if (a0.ngroups > 1) {
+        int g = 0;
+#pragma unroll
+        for (int i = 1; i < GEMM_GROUPS; i++) g += tn >= a0.tn_start[i];
+        if (g > 0) {
+            const GemmArgs::Group &G = a0.grp[g - 1];
+            a.wq = G.wq, a.whi = G.whi, a.wd = G.wd, a.wdmin = G.wdmin, a.wmin = G.wmin;
+            a.y = G.y, a.bias = G.bias, a.N = G.N, a.n_pad = G.n_pad, a.ldy = G.ldy;
+            tn -= a0.tn_start[g];
+        }
+    }
     const int m0 = tm * C::BM, n0 = tn * C::BN;
     const int nst = a.nstages;
 
@@ -526,6 +556,10 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
     }
     a.tiles_m = (a.M + C::BM - 1) / C::BM;
     a.tiles_n = (a.N + C::BN - 1) / C::BN;
+    for (int g = 1; g < GEMM_GROUPS; g++) {
+        a.tn_start[g] = g < a.ngroups ? a.tiles_n : INT_MAX;
+        if (g < a.ngroups) a.tiles_n += (a.grp[g - 1].N + C::BN - 1) / C::BN;
+    }
     a.group_m = 8;
     a.nstages = a.kch / KCT;  // kb_pad is a multiple of 128 bytes
     const unsigned grid = (unsigned)(a.tiles_m * a.tiles_n);
@@ -554,7 +588,9 @@ static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
         // 256x128 tiles when that still gives every CU (256) a workgroup, else 128x128
         // (the smaller tiles measured slower even where 128x128 leaves CUs idle:
         // 4096x384x384 Q8_0 12.7 us at 128x128, 13.2 us at 128x64, 14.1 us at 64x64)
-        cfg = (tiles(a.M, a.N, 256, 128) >= 256) ? 1 : 3;
+        int64_t n_all = a.N;
+        for (int g = 1; g < a.ngroups; g++) n_all += a.grp[g - 1].N;
+        cfg = (tiles(a.M, n_all, 256, 128) >= 256) ? 1 : 3;
     }
     switch (cfg) {
         case 1: return launch_cfg<FMT, 4, 2, 2, 2, 1>(a, s);
@@ -568,32 +604,49 @@ static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
     }
 }
 
-hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
-                       int64_t ldy, hipStream_t s, const float *bias) {
-    if (m <= 0 || n <= 0) return hipSuccess;
-    const WeightPlanes p = weight_planes(type, n, k);
+hipError_t launch_gemm_group(int type, int ngroups, const void *const *images, const int64_t *n, int64_t k,
+                             const void *ws, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,
+                             hipStream_t s) {
+    if (ngroups < 1 || ngroups > GEMM_GROUPS) return hipErrorInvalidValue;
+    if (m <= 0) return hipSuccess;
     const ActPlanes ap = act_planes(type, m, k, true);
-    const uint8_t *wb = (const uint8_t *)image;
     const uint8_t *xb = (const uint8_t *)ws;
     GemmArgs a{};
     a.xq = (const int8_t *)(xb + ap.xq);
     a.xd = (const float *)(xb + ap.xd);
     a.xmin = (const _Float16 *)(xb + ap.xmin);
-    a.wq = (const int8_t *)(wb + p.tq);
-    a.whi = (const int8_t *)(wb + p.thi);
-    a.wd = (const float *)(wb + p.tdw);
-    a.wdmin = (const float *)(wb + p.tdmin);
-    a.wmin = (const _Float16 *)(wb + p.tmin);
-    a.y = y;
-    a.bias = bias;
     a.M = (int)m;
-    a.N = (int)n;
-    a.ldy = (int)ldy;
     a.m_pad = (int)ap.m_pad;
-    a.n_pad = (int)p.n_pad;
-    a.kch = (int)(p.kb_pad / 32);
-    a.nstages = (int)(p.kb_pad / 64);  // set again per configuration
     a.nsb = (int)(k / QK_K);
+    // groups with n = 0 are dropped
+    int ng = 0;
+    for (int g = 0; g < ngroups; g++) {
+        if (n[g] <= 0) continue;
+        const WeightPlanes p = weight_planes(type, n[g], k);
+        const uint8_t *wb = (const uint8_t *)images[g];
+        GemmArgs::Group G;
+        G.wq = (const int8_t *)(wb + p.tq);
+        G.whi = (const int8_t *)(wb + p.thi);
+        G.wd = (const float *)(wb + p.tdw);
+        G.wdmin = (const float *)(wb + p.tdmin);
+        G.wmin = (const _Float16 *)(wb + p.tmin);
+        G.y = y[g];
+        G.bias = bias ? bias[g] : nullptr;
+        G.N = (int)n[g];
+        G.n_pad = (int)p.n_pad;
+        G.ldy = (int)ldy[g];
+        if (ng == 0) {
+            a.wq = G.wq, a.whi = G.whi, a.wd = G.wd, a.wdmin = G.wdmin, a.wmin = G.wmin;
+            a.y = G.y, a.bias = G.bias, a.N = G.N, a.n_pad = G.n_pad, a.ldy = G.ldy;
+            a.kch = (int)(p.kb_pad / 32);
+            a.nstages = (int)(p.kb_pad / 64);  // set again per configuration
+        } else {
+            a.grp[ng - 1] = G;
+        }
+        ng++;
+    }
+    if (ng == 0) return hipSuccess;
+    a.ngroups = ng;
     switch (type) {
         case MQ_TYPE_Q8_0: return launch_fmt<FMT_Q8_0>(a, s);
         case MQ_TYPE_Q4_K: return launch_fmt<FMT_Q4_K>(a, s);
@@ -601,6 +654,11 @@ hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const 
         case MQ_TYPE_F16: return launch_fmt<FMT_F16>(a, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
+                       int64_t ldy, hipStream_t s, const float *bias) {
+    return launch_gemm_group(type, 1, &image, &n, k, ws, m, &y, &ldy, &bias, s);
 }
 
 }  // namespace mq

@@ -283,6 +283,10 @@ hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const 
                        int64_t ldy, hipStream_t s, const float *bias = nullptr);
 hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
                        int64_t ldy, hipStream_t s, const float *bias = nullptr);
+// up to 4 weights of the same type and k on one activation, one launch (bias may be NULL)
+hipError_t launch_gemm_group(int type, int ngroups, const void *const *images, const int64_t *n, int64_t k,
+                             const void *ws, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,
+                             hipStream_t s);
 
 // Operands of the fragment attention (mq_decoder.hip).  Element (b, t, h, d) of q is at
 // q + b*q_sb + t*q_st + h*q_sh + d (floats; q_sb, q_st, q_sh multiples of 4 and q 16-byte

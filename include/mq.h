@@ -147,6 +147,17 @@ int mq_mul_mat_q(int type, const void *w_image, int64_t n, int64_t k, const void
 int mq_mul_mat_q_ex(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m, float *y,
                     int64_t ldy, const float *bias, int path, void *stream);
 
+/* Up to 4 mat-muls on the same quantized activation in one launch (the q, k and v projections
+ * of an encoder layer read one input, src/crispembed.cpp:1168-1170): for g < n_groups,
+ * Y_g = X W_g^T + bias_g (bias NULL, or bias[g] NULL: none), every W_g of `type` with k
+ * in-features, n[g] out-features, output row stride ldy[g].  The GEMM walks the feature tiles
+ * of all groups as one grid, so three narrow projections fill the GPU like one wide one; the
+ * GEMV path runs the groups one after another.  Results equal separate mq_mul_mat_q_ex calls
+ * bit for bit. */
+int mq_mul_mat_q_group(int type, int n_groups, const void *const *w_images, const int64_t *n, int64_t k,
+                       const void *workspace, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,
+                       int path, void *stream);
+
 /* mq_quantize_act with the graph's elementwise producer folded in: it quantizes
  * op(X + bias) where bias is an fp32 [k] row added to every row of X (NULL: none) and
  * op is one of MQ_PRE_*.  The value quantized is the fp32 tensor the ggml graph

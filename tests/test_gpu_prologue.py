@@ -122,3 +122,41 @@ def mq_quantized(wtype, w):
     out = np.zeros(L.mq_gguf_bytes(wtype, n, k), dtype=np.uint8)
     L.mq_quantize_chunk(wtype, w.ctypes.data, out.ctypes.data, n, k)
     return out
+
+
+@pytest.mark.parametrize("wtype", TYPES)
+@pytest.mark.parametrize("m,k,path", [(5, 512, 1), (300, 512, 2), (4096, 256, 2)])
+def test_mul_mat_q_group_equals_separate(wtype, m, k, path):
+    """mq_mul_mat_q_group (one launch over the feature tiles of every weight) against one
+    mq_mul_mat_q_ex per weight: bit-identical, with ragged n, per-group biases (one absent)
+    and output strides."""
+    import torch
+    from crispembed_amd import mq
+    L = mq.lib()
+    rng = np.random.default_rng(m + k + wtype)
+    ns = [384, 100, 37]
+    imgs, wps = [], []
+    for n in ns:
+        w = rng.standard_normal((n, k)).astype(np.float32)
+        img = weight_image(wtype, np.ascontiguousarray(mq_quantized(wtype, w)), n, k)
+        imgs.append(img)
+        wps.append(img[1])
+    x = dev(rng.standard_normal((m, k)).astype(np.float32))
+    _, ptr, _ = ws = _quant(wtype, x, m, k, path)
+    biases = [dev(rng.standard_normal(n).astype(np.float32)) for n in ns]
+    bptr = [biases[0].data_ptr(), None, biases[2].data_ptr()]
+    lds = [n + 5 for n in ns]
+    ref = [torch.full((m, ld), np.nan, dtype=torch.float32, device="cuda") for ld in lds]
+    got = [torch.full((m, ld), np.nan, dtype=torch.float32, device="cuda") for ld in lds]
+    for g, n in enumerate(ns):
+        mq.check(L.mq_mul_mat_q_ex(wtype, ctypes.c_void_p(wps[g]), n, k, ctypes.c_void_p(ptr), m,
+                                   ctypes.c_void_p(ref[g].data_ptr()), lds[g], bptr[g], path, stream()))
+    VP = ctypes.c_void_p * 3
+    I64 = ctypes.c_int64 * 3
+    mq.check(L.mq_mul_mat_q_group(wtype, 3, VP(*wps), I64(*ns), k, ctypes.c_void_p(ptr), m,
+                                  VP(*[t.data_ptr() for t in got]), I64(*lds), VP(*bptr), path, stream()))
+    for g, n in enumerate(ns):
+        a, b = host(ref[g]), host(got[g])
+        assert np.array_equal(a[:, :n], b[:, :n]), g
+        assert np.isnan(b[:, n:]).all()
+    del imgs, ws
