@@ -13,7 +13,7 @@ dense MFMA peak (5.0 POP/s).
 cpu_baseline = the restated ggml-cpu mul_mat (AVX2 integer dots, threads) on a
 bounded sample of token rows of the same workload, on the host cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras] [--only q8_0|e2e|qwen3|decode]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras] [--only q8_0|e2e|graph|qwen3|decode]
 """
 import argparse
 import ctypes
@@ -299,6 +299,45 @@ def bench_minilm_e2e(torch, L, mq):
             "linear_tops": round(lin_ops / (us * 1e-6) / 1e12, 1)}
 
 
+def bench_minilm_ggml_graph(torch, L, mq):
+    """The same MiniLM-L6 workload through the ggml backend: CrispEmbed's encoder graph
+    (build_encoder_graph's post-LN path, 182 nodes) built with ggml's graph API from a GGUF file
+    and computed by ggml_backend_graph_compute on MI355X, as a CrispEmbed build using the
+    backend runs it (tests/native/test_bert_graph_mi355.cpp, built by build_test_driver).
+    Time per graph from the host's clock around ggml_backend_graph_compute (which
+    synchronizes), inputs already uploaded."""
+    import subprocess
+    import tempfile
+
+    import numpy as np
+    from crispembed_amd import bert, gguf, synth
+    exe = os.path.join(ROOT, "crispembed_amd", "bin", "test-bert-graph-mi355")
+    if not os.path.exists(exe):
+        return {"error": f"{exe} not built"}
+    hp = dict(bert.MINILM_L6)
+    B, T = 32, 128
+    with tempfile.TemporaryDirectory() as d:
+        W = bert.synthetic_weights(hp, mq.TYPE_Q8_0, name="minilm")
+        gguf.write_bert_gguf(os.path.join(d, "m.gguf"), hp, mq.TYPE_Q8_0, W)
+        synth.integers(f"minilm/ids_{B}x{T}", (B * T,), 1000, 30521).astype(np.int32).tofile(os.path.join(d, "ids"))
+        np.zeros(B * T, np.int32).tofile(os.path.join(d, "types"))
+        np.full(B, T, np.int32).tofile(os.path.join(d, "lens"))
+        r = subprocess.run([exe, os.path.join(d, "m.gguf"), str(B), str(T), os.path.join(d, "ids"),
+                            os.path.join(d, "types"), os.path.join(d, "lens"), os.path.join(d, "out"), "--iters", "30"],
+                           capture_output=True, text=True, timeout=300)
+    try:
+        res = json.loads(r.stdout.strip().splitlines()[-1])
+    except (ValueError, IndexError):
+        return {"error": (r.stderr or r.stdout)[-300:]}
+    if not res.get("ok"):
+        return {"error": res.get("error")}
+    ms = res["ms_per_graph"]
+    return {"workload": "MiniLM-L6 shape, Q8_0, 32 seq x 128 tokens, CrispEmbed's ggml encoder graph on the "
+                        "MI355X ggml backend (every node on the GPU)",
+            "graph_nodes": res["nodes"], "nodes_not_on_gpu": res["unsupported"], "batch_ms": round(ms, 3),
+            "embeddings_per_s": round(B / (ms * 1e-3), 1)}
+
+
 def bench_qwen3_e2e(torch, L, mq):
     """End-to-end Qwen3-Embedding-0.6B-shaped decoder embedder (28 layers, H 1024, 16 query /
     8 key-value heads of 128, SwiGLU FFN 3072, RMSNorm eps 1e-6, NEOX RoPE theta 1e6, causal,
@@ -375,7 +414,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="skip the Q8_0 and GEMV side measurements")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--gemm-cfg", default=None, help="MQ_GEMM_CFG tile configuration (1 or 3)")
-    ap.add_argument("--only", choices=["q8_0", "e2e", "qwen3", "decode"], default=None,
+    ap.add_argument("--only", choices=["q8_0", "e2e", "graph", "qwen3", "decode"], default=None,
                     help="run one side measurement alone (for per-workload profiles) and print its JSON")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 10 device copies of 256 MiB (reference kernel for rocprof byte counters)")
@@ -402,6 +441,7 @@ def main():
     if args.only:
         fn = {"q8_0": lambda: bench_q8_0_minilm(torch, L, mq, synth),
               "e2e": lambda: bench_minilm_e2e(torch, L, mq),
+              "graph": lambda: bench_minilm_ggml_graph(torch, L, mq),
               "qwen3": lambda: bench_qwen3_e2e(torch, L, mq),
               "decode": lambda: bench_decode(torch, L, mq, synth)}[args.only]
         print(json.dumps({"only": args.only, "result": fn()}), flush=True)
@@ -413,6 +453,7 @@ def main():
     if not args.no_extras:
         extras = {"q8_0_minilm_ffn_up": bench_q8_0_minilm(torch, L, mq, synth),
                   "minilm_l6_e2e": bench_minilm_e2e(torch, L, mq),
+                  "minilm_l6_ggml_graph": bench_minilm_ggml_graph(torch, L, mq),
                   "qwen3_0_6b_e2e": bench_qwen3_e2e(torch, L, mq),
                   "decode_gemv": bench_decode(torch, L, mq, synth)}
     cpu = None
