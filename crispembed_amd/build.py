@@ -90,7 +90,8 @@ def build_test_driver():
     outs = []
     for src, name, extra in (("test_backend_mi355.cpp", "test-backend-mi355",
                               ["-L", oracle, "-loracle", "-Wl,-rpath," + oracle, "-Wl,-rpath,$ORIGIN/../../oracle"]),
-                             ("test_bert_graph_mi355.cpp", "test-bert-graph-mi355", [])):
+                             ("test_bert_graph_mi355.cpp", "test-bert-graph-mi355", []),
+                             ("test_decoder_graph_mi355.cpp", "test-decoder-graph-mi355", [])):
         out = os.path.join(BIN, name)
         cmd = ["g++", *common, os.path.join(TESTS, "native", src), "-o", out + ".tmp", *libs, *extra]
         r = subprocess.run(cmd, capture_output=True, text=True)

@@ -3,8 +3,8 @@
 // Interface tables follow ggml-backend-impl.h.  The backend executes MUL_MAT on
 // quantized weights (mq.h) and the other ops of the encoder graph
 // (src/crispembed.cpp:1043-1468) through mq_ops.h: GET_ROWS, ADD / SUB / MUL / DIV,
-// NORM / RMS_NORM, UNARY (GELU_ERF, GELU, SILU, RELU), CPY / CONT / DUP and
-// FLASH_ATTN_EXT, plus the metadata-only view ops.  Anything else is refused by
+// NORM / RMS_NORM, UNARY (GELU_ERF, GELU, SILU, RELU), CPY / CONT / DUP, ROPE
+// (ggml_rope_ext, normal and NEOX) and FLASH_ATTN_EXT, plus the metadata-only view ops.  Anything else is refused by
 // supports_op, and ggml_backend_sched keeps it on the CPU backend, which is how
 // CrispEmbed already falls back for ops a GPU backend rejects (src/crispembed.cpp:700-723).
 //
@@ -578,6 +578,16 @@ enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node) {
             const mq_view s = view_of(node->src[0]), d = view_of(node->op == GGML_OP_CPY ? node->src[1] : node);
             return op_status(mq_op_cpy(&s, &d, c->stream), node);
         }
+        case GGML_OP_ROPE: {
+            const mq_view x = view_of(node->src[0]), p = view_of(node->src[1]), d = view_of(node);
+            mq_view f{};
+            if (node->src[2]) f = view_of(node->src[2]);
+            const int32_t *ip = node->op_params;
+            return op_status(mq_op_rope(&x, &p, node->src[2] ? &f : nullptr, &d, ip[1], ip[2], ip[4],
+                                        op_param_f32(node, 5), op_param_f32(node, 6), op_param_f32(node, 7),
+                                        op_param_f32(node, 8), op_param_f32(node, 9), op_param_f32(node, 10), c->stream),
+                             node);
+        }
         case GGML_OP_FLASH_ATTN_EXT: {
             const mq_view q = view_of(node->src[0]), k = view_of(node->src[1]), v = view_of(node->src[2]),
                           d = view_of(node);
@@ -735,6 +745,11 @@ bool dev_supports_op(ggml_backend_dev_t d, const ggml_tensor *op) {
         case GGML_OP_CPY: return mq_op_supported(MQ_OP_CPY, 0, p[0], nullptr, nullptr, nullptr, p[1]);
         case GGML_OP_CONT:
         case GGML_OP_DUP: return mq_op_supported(MQ_OP_CPY, 0, p[0], nullptr, nullptr, nullptr, &dst);
+        case GGML_OP_ROPE: {
+            const int n_dims = op->op_params[1], mode = op->op_params[2];
+            if (n_dims <= 0 || n_dims % 2 || n_dims > op->src[0]->ne[0]) return false;
+            return mq_op_supported(MQ_OP_ROPE, mode, p[0], p[1], p[2], nullptr, &dst);
+        }
         case GGML_OP_FLASH_ATTN_EXT:
             // no ALiBi slopes, no logit soft-capping, no attention sinks
             if (op_param_f32(op, 1) != 0.0f || op_param_f32(op, 2) != 0.0f || op->src[4]) return false;

@@ -195,6 +195,14 @@ GGML_API struct ggml_tensor *ggml_flash_attn_ext(struct ggml_context *ctx, struc
                                                 struct ggml_tensor *v, struct ggml_tensor *mask, float scale,
                                                 float max_bias, float logit_softcap);
 GGML_API struct ggml_tensor *ggml_graph_get_tensor(const struct ggml_cgraph *cgraph, const char *name);
+#define GGML_ROPE_TYPE_NEOX 2
+// a [n_dims.., n_head, T, B], b I32 positions [T], c freq factors or NULL; op_params:
+// 0, n_dims, mode, 0, n_ctx_orig, then floats freq_base, freq_scale, ext_factor, attn_factor,
+// beta_fast, beta_slow
+GGML_API struct ggml_tensor *ggml_rope_ext(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b,
+                                          struct ggml_tensor *c, int n_dims, int mode, int n_ctx_orig, float freq_base,
+                                          float freq_scale, float ext_factor, float attn_factor, float beta_fast,
+                                          float beta_slow);
 GGML_API struct ggml_cgraph *ggml_new_graph(struct ggml_context *ctx);
 GGML_API void ggml_build_forward_expand(struct ggml_cgraph *cgraph, struct ggml_tensor *tensor);
 GGML_API int ggml_graph_n_nodes(struct ggml_cgraph *cgraph);

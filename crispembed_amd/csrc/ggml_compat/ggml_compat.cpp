@@ -383,6 +383,22 @@ extern "C" enum ggml_unary_op ggml_get_unary_op(const struct ggml_tensor *t) {
     return (enum ggml_unary_op)t->op_params[0];
 }
 
+extern "C" struct ggml_tensor *ggml_rope_ext(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b,
+                                             struct ggml_tensor *c, int n_dims, int mode, int n_ctx_orig,
+                                             float freq_base, float freq_scale, float ext_factor, float attn_factor,
+                                             float beta_fast, float beta_slow) {
+    ggml_tensor *r = new_tensor(ctx, a->type, 4, a->ne);
+    r->op = GGML_OP_ROPE;
+    const int32_t ip[5] = {0, n_dims, mode, 0, n_ctx_orig};
+    std::memcpy(r->op_params, ip, sizeof(ip));
+    const float fp[6] = {freq_base, freq_scale, ext_factor, attn_factor, beta_fast, beta_slow};
+    std::memcpy(r->op_params + 5, fp, sizeof(fp));
+    r->src[0] = a;
+    r->src[1] = b;
+    r->src[2] = c;
+    return r;
+}
+
 extern "C" struct ggml_tensor *ggml_flash_attn_ext(struct ggml_context *ctx, struct ggml_tensor *q,
                                                    struct ggml_tensor *k, struct ggml_tensor *v,
                                                    struct ggml_tensor *mask, float scale, float max_bias,

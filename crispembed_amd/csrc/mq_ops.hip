@@ -244,6 +244,50 @@ __global__ __launch_bounds__(256) void k_get_rows(const DV src, const DV ids, co
     for (int64_t c = lane; c < n; c += 64) dr[c] = ok ? deq_elem<TYPE>(sr, c) : 0.f;
 }
 
+// Rotary embedding: one thread per (row, pair slot j < ne0/2).  Slots j < n_dims/2 rotate
+// their pair; the others copy elements 2j, 2j + 1 (all at or past n_dims).
+struct RopeParams {
+    int n_dims, mode;
+    float theta_scale, freq_scale, ext_factor, attn_factor, corr_lo, corr_hi;
+};
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_rope(const DV x, const DV pos, const float *__restrict__ ff, const DV d,
+                                              const RopeParams rp, int64_t units) {
+    const int64_t half0 = x.ne[0] / 2;
+    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (int64_t)gridDim.x * 256) {
+        int64_t r = u / half0;
+        const int j = (int)(u - r * half0);
+        const int64_t i1 = r % x.ne[1];
+        r /= x.ne[1];
+        const int64_t i2 = r % x.ne[2], i3 = r / x.ne[2];
+        const float *xr = (const float *)(x.p + off3(x, i1, i2, i3));
+        float *dr = (float *)(d.p + off3(d, i1, i2, i3));
+        const int hn = rp.n_dims / 2;
+        if (j >= hn) {
+            const float a = xr[2 * j], b = xr[2 * j + 1];
+            dr[2 * j] = a, dr[2 * j + 1] = b;
+            continue;
+        }
+        // the rope cache's angle chain: theta = p, then one fp32 product per earlier pair
+        float theta = (float)*(const int32_t *)(pos.p + i2 * pos.nb[0]);
+        for (int k = 0; k < j; k++) theta *= rp.theta_scale;
+        const float extrap = ff ? theta / ff[j] : theta;
+        float th = rp.freq_scale * extrap, mscale = rp.attn_factor;
+        if (rp.ext_factor != 0.0f) {
+            const float y = ((float)j - rp.corr_lo) / fmaxf(0.001f, rp.corr_hi - rp.corr_lo);
+            const float mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * rp.ext_factor;
+            th = th * (1.0f - mix) + extrap * mix;
+            mscale *= 1.0f + 0.1f * logf(1.0f / rp.freq_scale);
+        }
+        const float c = cosf(th) * mscale, sn = sinf(th) * mscale;
+        const int e0 = MODE == MQ_ROPE_NEOX ? j : 2 * j, e1 = MODE == MQ_ROPE_NEOX ? j + hn : 2 * j + 1;
+        const float a = xr[e0], b = xr[e1];
+        dr[e0] = a * c - b * sn;
+        dr[e1] = a * sn + b * c;
+    }
+}
+
 // ------------------------------------------------------------------ checks ----
 int64_t nel(const mq_view *v) { return v->ne[0] * v->ne[1] * v->ne[2] * v->ne[3]; }
 
@@ -365,6 +409,18 @@ const char *check_flash(const mq_view *q, const mq_view *k, const mq_view *v, co
             return "flash_attn: mask heads / batches do not broadcast";
         if (m->nb[1] % 2 || m->nb[2] % 2 || m->nb[3] % 2) return "flash_attn: misaligned mask strides";
     }
+    return nullptr;
+}
+
+const char *check_rope(int mode, const mq_view *x, const mq_view *pos, const mq_view *ff, const mq_view *d, int n_dims) {
+    if (mode != MQ_ROPE_NORMAL && mode != MQ_ROPE_NEOX) return "rope: mode not 0 (normal) or 2 (NEOX)";
+    if (!x || !pos || !d || !shape_ok(x) || !shape_ok(pos) || !shape_ok(d)) return "missing or empty operand";
+    if (x->type != MQ_TYPE_F32 || d->type != MQ_TYPE_F32 || pos->type != MQ_TYPE_I32) return "rope: F32 x, I32 pos";
+    if (!same_shape(x, d) || !rows_dense(x, 4) || !rows_dense(d, 4)) return "rope: x / dst shapes or rows";
+    if (n_dims <= 0 || n_dims % 2 || n_dims > x->ne[0] || x->ne[0] % 2) return "rope: n_dims";
+    if (pos->ne[0] != x->ne[2] || pos->ne[1] != 1 || pos->ne[2] != 1 || pos->ne[3] != 1) return "rope: pos must be [T]";
+    if (ff && (!shape_ok(ff) || ff->type != MQ_TYPE_F32 || ff->nb[0] != 4 || ff->ne[0] < n_dims / 2))
+        return "rope: freq_factors must be F32 [n_dims/2]";
     return nullptr;
 }
 
@@ -491,6 +547,36 @@ extern "C" int mq_op_cpy(const mq_view *src, const mq_view *dst, void *stream) {
     return hip_rc(hipGetLastError(), "cpy");
 }
 
+// YaRN correction dimension of rotation count n_rot (ggml_rope_yarn_corr_dim's formula)
+static float yarn_corr_dim(int n_dims, int n_ctx_orig, float n_rot, float base) {
+    return n_dims * logf((float)n_ctx_orig / (n_rot * 2.0f * 3.14159265358979323846f)) / (2.0f * logf(base));
+}
+
+extern "C" int mq_op_rope(const mq_view *x, const mq_view *pos, const mq_view *freq_factors, const mq_view *dst,
+                          int n_dims, int mode, int n_ctx_orig, float freq_base, float freq_scale, float ext_factor,
+                          float attn_factor, float beta_fast, float beta_slow, void *stream) {
+    if (const char *e = check_rope(mode, x, pos, freq_factors, dst, n_dims)) return fail(e);
+    if (!have_data({x, pos, freq_factors, dst})) return fail("missing data pointer");
+    RopeParams rp;
+    rp.n_dims = n_dims, rp.mode = mode;
+    rp.theta_scale = powf(freq_base, -2.0f / (float)n_dims);
+    rp.freq_scale = freq_scale, rp.ext_factor = ext_factor, rp.attn_factor = attn_factor;
+    const float lo = floorf(yarn_corr_dim(n_dims, n_ctx_orig, beta_fast, freq_base));
+    const float hi = ceilf(yarn_corr_dim(n_dims, n_ctx_orig, beta_slow, freq_base));
+    rp.corr_lo = fmaxf(0.0f, lo);
+    rp.corr_hi = fminf((float)(n_dims - 1), hi);
+    const int64_t units = nel(x) / 2;
+    const float *ff = freq_factors ? (const float *)freq_factors->data : nullptr;
+    hipStream_t s = (hipStream_t)stream;
+    if (mode == MQ_ROPE_NEOX)
+        hipLaunchKernelGGL((k_rope<MQ_ROPE_NEOX>), dim3(grid_units(units)), dim3(256), 0, s, dv(x), dv(pos), ff, dv(dst), rp,
+                           units);
+    else
+        hipLaunchKernelGGL((k_rope<MQ_ROPE_NORMAL>), dim3(grid_units(units)), dim3(256), 0, s, dv(x), dv(pos), ff, dv(dst),
+                           rp, units);
+    return hip_rc(hipGetLastError(), "rope");
+}
+
 extern "C" size_t mq_op_flash_attn_workspace_bytes(const mq_view *k) {
     if (!k || (k->ne[0] != 32 && k->ne[0] != 64 && k->ne[0] != 128) || k->ne[1] < 1 || k->ne[2] < 1 || k->ne[3] < 1)
         return 0;
@@ -536,6 +622,7 @@ extern "C" int mq_op_supported(int op, int sub, const mq_view *s0, const mq_view
         case MQ_OP_NORM: e = check_norm(sub, s0, s1, dst); break;
         case MQ_OP_CPY: e = check_cpy(s0, dst); break;
         case MQ_OP_FLASH_ATTN: e = check_flash(s0, s1, s2, s3, dst); break;
+        case MQ_OP_ROPE: e = s0 ? check_rope(sub, s0, s1, s2, dst, (int)s0->ne[0]) : "missing or empty operand"; break;
         default: break;
     }
     return e == nullptr;

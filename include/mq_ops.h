@@ -12,6 +12,7 @@
  *   ggml_gelu_erf        (src/crispembed.cpp:1415)            mq_op_unary (also silu, relu, gelu)
  *   ggml_cont / ggml_cpy (src/crispembed.cpp:1164-1166)       mq_op_cpy
  *   ggml_flash_attn_ext  (src/crispembed.cpp:1293)            mq_op_flash_attn
+ *   ggml_rope_ext        (src/decoder_embed.cpp:756-759)      mq_op_rope
  * The semantics (shapes, broadcasting, op_params) are ggml's, as its CPU backend computes them
  * (ggml-cpu ops.cpp, the ggml submodule pinned in .gitmodules): the ggml backend passes each
  * node's tensors straight through.
@@ -95,6 +96,21 @@ size_t mq_op_flash_attn_workspace_bytes(const mq_view *k);
 int mq_op_flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask, const mq_view *dst,
                      float scale, void *workspace, size_t workspace_bytes, void *stream);
 
+/* ggml_rope_ext: rotates dimension pairs of x [ne0 >= n_dims, n_head, T, B] by the angles of
+ * positions pos[i2] (I32 [T]): pair i < n_dims/2 is (2i, 2i+1) for mode 0 and (i, i + n_dims/2)
+ * for MQ_ROPE_NEOX; dimensions from n_dims on are copied.  The angle of pair i at position p is
+ * theta_i = p * s * s ... (i products, s = freq_base^(-2/n_dims), fp32), divided by
+ * freq_factors[i] when given (F32 [n_dims/2], else NULL), then YaRN-mixed as ggml's rope_yarn:
+ * theta = freq_scale * theta_i, and when ext_factor != 0 the interpolation ramp between the
+ * correction dimensions of (n_ctx_orig, beta_fast, beta_slow) mixes in theta_i and the
+ * magnitude is scaled by 1 + 0.1 ln(1 / freq_scale); cos and sin are scaled by attn_factor.
+ * x and dst F32 with contiguous rows (may be the same tensor). */
+#define MQ_ROPE_NORMAL 0
+#define MQ_ROPE_NEOX 2
+int mq_op_rope(const mq_view *x, const mq_view *pos, const mq_view *freq_factors, const mq_view *dst, int n_dims,
+               int mode, int n_ctx_orig, float freq_base, float freq_scale, float ext_factor, float attn_factor,
+               float beta_fast, float beta_slow, void *stream);
+
 /* ids for mq_op_supported */
 #define MQ_OP_GET_ROWS 0
 #define MQ_OP_BINARY 1
@@ -102,6 +118,7 @@ int mq_op_flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const
 #define MQ_OP_NORM 3
 #define MQ_OP_CPY 4
 #define MQ_OP_FLASH_ATTN 5
+#define MQ_OP_ROPE 6 /* sub = mode; src0 x, src1 pos, src2 freq_factors; n_dims = x.ne0 assumed */
 
 /* 1 when mq_op_<op> accepts these operands (srcs in the op's argument order, NULL where an
  * optional operand is absent -- for MQ_OP_NORM src1 is `add`; `sub` is the binary / unary /

@@ -106,3 +106,53 @@ def test_bert_graph_fusion_off_agrees(tmp_path):
     a, _ = _run(tmp_path, model, B, T, ids, types, np.full(B, T))
     b, _ = _run(tmp_path, model, B, T, ids, types, np.full(B, T), env={"MQ_GGML_NO_FUSION": "1"})
     assert _cos_rows(a, b).min() >= COSINE_MIN
+
+
+# ------------------------------------------------------------------- decoder ----
+DEC_EXE = os.path.join(ROOT, "crispembed_amd", "bin", "test-decoder-graph-mi355")
+DEC_HP = dict(n_layer=2, n_embd=256, n_head=4, n_kv_head=2, head_dim=128, n_ff=512, n_vocab=300, rms_norm_eps=1e-6,
+              rope_theta=1e6, causal=1, pooling=2)
+
+
+def _run_dec(tmp_path, model, ids):
+    T = ids.size
+    np.ascontiguousarray(ids, dtype=np.int32).tofile(tmp_path / "ids.i32")
+    out = tmp_path / "dout.f32"
+    r = subprocess.run([DEC_EXE, str(model), str(T), str(tmp_path / "ids.i32"), str(out)], capture_output=True,
+                       text=True, timeout=300)
+    print(r.stderr[-2000:])
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert r.returncode == 0 and res["ok"], res
+    assert res["unsupported"] == 0
+    return np.fromfile(out, dtype=np.float32).reshape(T, -1)
+
+
+@pytest.mark.parametrize("wtype,hd,causal", [(O.Q8_0, 128, 1), (O.Q4_K, 128, 1), (O.Q6_K, 64, 1), (O.Q8_0, 64, 0)])
+def test_decoder_graph_matches_reference(oracle, tmp_path, wtype, hd, causal):
+    """CrispEmbed's Qwen3 decoder graph (ROPE_EXT NEOX, per-head RMS norms, causal
+    FLASH_ATTN_EXT mask, SiLU gate) computed by the backend against the CPU decoder: the normed
+    last hidden state's last-token row (last-token pooling) and mean at cosine >= 0.9999 (the
+    decoder bar: every mul_mat requantizes its input, and one flipped quant is not averaged
+    away by last-token pooling)."""
+    import decoder_oracle
+    from crispembed_amd import decoder
+    hp = dict(DEC_HP, head_dim=hd, causal=causal, pooling=2 if causal else 1)
+    if hd == 64:
+        hp.update(n_head=4, n_kv_head=4, n_embd=256)
+    W = decoder.synthetic_weights(hp, wtype, name=f"dgraph{wtype}_{hd}_{causal}")
+    model = tmp_path / "d.gguf"
+    gguf.write_decoder_gguf(model, hp, wtype, W)
+    T = 45
+    ids = np.random.default_rng(wtype + hd).integers(0, hp["n_vocab"], (1, T)).astype(np.int32)
+    got = _run_dec(tmp_path, model, ids)
+    _, x = decoder_oracle.encode(oracle, hp, wtype, W, ids)
+    ref = decoder_oracle.rms_norm(x, W["out_norm"], hp["rms_norm_eps"])
+    cos = _cos_rows(got, ref)
+    print(wtype, hd, causal, "row cosine min / median", cos.min(), np.median(cos))
+    assert np.isfinite(got).all()
+    # the median row: the CPU decoder rotates by exact angles, the graph by ggml's rope cache
+    # (an fp32 product chain, up to ~1.7e-4 rad off at position 44), which with full attention
+    # reaches every row
+    assert np.median(cos) >= 0.99995
+    assert cos[-1] >= 0.9999
+    assert _pool(got) @ _pool(ref) >= 0.9999

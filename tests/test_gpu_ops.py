@@ -312,3 +312,74 @@ def test_op_rejections_name_the_problem():
     assert L.mq_op_binary(mq.BIN_ADD, a, b, a, stream()) == -2
     assert b"broadcast" in L.mq_last_error()
     assert L.mq_op_supported(mq.OP_BINARY, mq.BIN_ADD, a, a, None, None, a) == 1
+
+
+# ---------------------------------------------------------------------- rope ----
+def _rope_ref(x, pos, n_dims, mode, base, freq_scale=1.0, ext_factor=0.0, attn_factor=1.0, n_ctx_orig=0,
+              beta_fast=32.0, beta_slow=1.0, ff=None):
+    """x torch-order [B, T, nh, ne0] float32.  Angles by the rope cache's fp32 product chain
+    theta_i = p * s * ... * s (i products), YaRN as ggml's rope_yarn; rotation in fp64."""
+    half = n_dims // 2
+    s = np.float32(np.float32(base) ** np.float32(-2.0 / n_dims))
+    th = np.zeros((len(pos), half), np.float32)
+    for t, p in enumerate(pos):
+        v = np.float32(p)
+        for i in range(half):
+            th[t, i] = v
+            v = np.float32(v * s)
+    extrap = th.astype(np.float64) / (1.0 if ff is None else ff[None, :half].astype(np.float64))
+    theta = freq_scale * extrap
+    msc = attn_factor
+    if ext_factor != 0.0:
+        def corr(nr):
+            return n_dims * np.log(n_ctx_orig / (nr * 2 * np.pi)) / (2 * np.log(base))
+        lo, hi = max(0.0, np.floor(corr(beta_fast))), min(n_dims - 1.0, np.ceil(corr(beta_slow)))
+        y = (np.arange(half) - lo) / max(0.001, hi - lo)
+        mix = (1 - np.clip(y, 0, 1)) * ext_factor
+        theta = theta * (1 - mix) + extrap * mix
+        msc = attn_factor * (1 + 0.1 * np.log(1.0 / freq_scale))
+    c, sn = np.cos(theta) * msc, np.sin(theta) * msc  # [T, half]
+    c, sn = c[None, :, None, :], sn[None, :, None, :]
+    out = x.astype(np.float64).copy()
+    if mode == mq.ROPE_NEOX:
+        a, b = x[..., :half].astype(np.float64), x[..., half:n_dims].astype(np.float64)
+        out[..., :half], out[..., half:n_dims] = a * c - b * sn, a * sn + b * c
+    else:
+        a, b = x[..., 0:n_dims:2].astype(np.float64), x[..., 1:n_dims:2].astype(np.float64)
+        out[..., 0:n_dims:2], out[..., 1:n_dims:2] = a * c - b * sn, a * sn + b * c
+    return out
+
+
+@pytest.mark.parametrize("mode", [mq.ROPE_NEOX, mq.ROPE_NORMAL])
+@pytest.mark.parametrize("case", ["plain", "partial", "yarn", "freq_factors", "offset_pos"])
+def test_rope(mode, case):
+    L = mq.lib()
+    B, T, nh, ne0 = 2, 37, 5, 128
+    rng = _rng(30 + mode)
+    x = rng.standard_normal((B, T, nh, ne0)).astype(np.float32)
+    pos = np.arange(T, dtype=np.int32) + (1000 if case == "offset_pos" else 0)
+    n_dims = 64 if case == "partial" else ne0
+    kw = dict(base=1e6)
+    ff = None
+    if case == "yarn":
+        kw.update(freq_scale=0.25, ext_factor=1.0, attn_factor=1.0 / (1 + 0.1 * np.log(4.0)), n_ctx_orig=4096,
+                  beta_fast=32.0, beta_slow=1.0)
+    if case == "freq_factors":
+        ff = (1.0 + rng.random(n_dims // 2) * 3).astype(np.float32)
+    ref = _rope_ref(x, pos, n_dims, mode, ff=ff, **kw)
+    dx, dp = _cuda(x), _cuda(pos)
+    out = _t().empty_like(dx)
+    fv = mq.view(_cuda(ff)) if ff is not None else None
+    _call(L.mq_op_rope, mq.view(dx), mq.view(dp), fv, mq.view(out), n_dims, mode, kw.get("n_ctx_orig", 0),
+          kw["base"], kw.get("freq_scale", 1.0), kw.get("ext_factor", 0.0), kw.get("attn_factor", 1.0),
+          kw.get("beta_fast", 0.0), kw.get("beta_slow", 0.0), stream())
+    got = host(out)
+    # device cosf / sinf against fp64 of the same fp32 angles: a few 1e-7
+    assert np.abs(got - ref).max() <= 2e-6 * max(1.0, np.abs(ref).max()), np.abs(got - ref).max()
+    assert np.array_equal(got[..., n_dims:], x[..., n_dims:])  # dimensions past n_dims copied
+    if case == "plain":
+        assert np.array_equal(got[:, 0], x[:, 0])  # position 0: cos 1, sin 0
+        # in place over x
+        _call(L.mq_op_rope, mq.view(dx), mq.view(dp), None, mq.view(dx), n_dims, mode, 0, 1e6, 1.0, 0.0, 1.0, 0.0,
+              0.0, stream())
+        assert np.array_equal(host(dx), got)
