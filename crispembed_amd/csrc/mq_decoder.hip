@@ -13,6 +13,8 @@
 //               normalised with sqrtf(max(sum x^2, 1e-12)) (src/decoder_embed.cpp:1044-1100)
 // Arithmetic is fp32 throughout; the attention's products run on fp16 MFMAs over split
 // (hi + lo) operands, which keeps fp32 accuracy.
+#include <cstdlib>
+
 #include "mq_internal.h"
 #include "mq_wave.h"
 
@@ -290,6 +292,19 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
     const v8h *F = (const v8h *)((const _Float16 *)a.ws + (int64_t)(b * a.nkv + hk) * nblk * NFR * 512) + lane;
 
     for (int kb = 0; kb * 32 < kend; kb++) {
+        // with a mask: a block that no query of the wave can see (a causal mask's upper
+        // triangle, padding) is skipped whole.  The values are read again after the MFMAs
+        // (cache hits) rather than kept live across them: at 2 waves per SIMD the 16 extra
+        // registers spill.
+        if constexpr (MASK) {
+            bool live = false;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
+                live |= key < Tk && (float)mrow[key] != -INFINITY;
+            }
+            if (__ballot(live) == 0) continue;
+        }
         const v8h *Fb = F + (int64_t)kb * NFR * 64;
         // three accumulators, so consecutive MFMAs never chain on one accumulator
         v16f s_hh = (v16f){}, s_hl = (v16f){}, s_lh = (v16f){};
@@ -389,6 +404,193 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
     }
 }
 
+// Split-key form for grids too small to fill the GPU (one sequence, few heads): a workgroup of
+// 4 waves owns one (head, 32-query tile); wave w runs the same online softmax over key blocks
+// w, w + 4, ... and the four partial (max, sum, O) are merged through LDS:
+//   m = max_w m_w,  O = sum_w 2^(m_w - m) O_w,  l = sum_w 2^(m_w - m) l_w,  out = O / l.
+template <int HD, bool MASK>
+__global__ __launch_bounds__(256) void k_attn_split(const AttnArgs a, int nblk, float qscale) {
+    constexpr int NS = HD / 16, NT = HD / 32, HALF = HD / 2, NFR = kv_frags<HD>();
+    constexpr float LOG2E = 1.4426950408889634f;
+    __shared__ __attribute__((aligned(16))) float rs[4][32];
+    __shared__ float mls[4][2][32];
+    __shared__ __attribute__((aligned(16))) float ored[4][NT][16][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int Tq = a.Tq, Tk = a.Tk, causal = a.causal;
+    const int q0 = ((int)gridDim.z - 1 - (int)blockIdx.z) * 32;  // longest causal ranges first
+    const int hk = h / (a.nq / a.nkv), qi = q0 + l32;
+    const int qrow = min(qi, Tq - 1);
+    const float2 *cs = a.cs;
+
+    v8h qh[NS], ql[NS];
+    {
+        const float *qp = a.q + (int64_t)b * a.q_sb + (int64_t)qrow * a.q_st + (int64_t)h * a.q_sh + 8 * half;
+        float x[NS][8];
+#pragma unroll
+        for (int st = 0; st < NS; st++) {
+            const float4 u = *(const float4 *)(qp + 16 * st), w = *(const float4 *)(qp + 16 * st + 4);
+            x[st][0] = u.x, x[st][1] = u.y, x[st][2] = u.z, x[st][3] = u.w;
+            x[st][4] = w.x, x[st][5] = w.y, x[st][6] = w.z, x[st][7] = w.w;
+        }
+        if (a.qw) {
+            float ss = 0.f;
+#pragma unroll
+            for (int st = 0; st < NS; st++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) ss += x[st][j] * x[st][j];
+            ss += __shfl_xor(ss, 32);
+            const float scale = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+            for (int st = 0; st < NS; st++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) x[st][j] = x[st][j] * scale * a.qw[16 * st + 8 * half + j];
+        }
+        if (cs) {
+#pragma unroll
+            for (int st = 0; st < NS / 2; st++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float2 rot = cs[(int64_t)qrow * HALF + 16 * st + 8 * half + j];
+                    const float x0 = x[st][j], x1 = x[st + NS / 2][j];
+                    x[st][j] = x0 * rot.x - x1 * rot.y;
+                    x[st + NS / 2][j] = x0 * rot.y + x1 * rot.x;
+                }
+        }
+#pragma unroll
+        for (int st = 0; st < NS; st++) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) x[st][j] *= qscale;
+            split8(x[st], qh[st], ql[st]);
+        }
+    }
+    const _Float16 *mrow = nullptr;
+    if constexpr (MASK)
+        mrow = (const _Float16 *)a.mask + (int64_t)b * a.m_sb + (int64_t)h * a.m_sh + (int64_t)qrow * a.m_sq;
+    v16f oacc[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++) oacc[n] = (v16f){};
+    float m_run = -INFINITY, l_run = 0.f;
+    const int kend = causal ? min(Tk, q0 + 32) : Tk;
+    const v8h *F = (const v8h *)((const _Float16 *)a.ws + (int64_t)(b * a.nkv + hk) * nblk * NFR * 512) + lane;
+
+    for (int kb = wave; kb * 32 < kend; kb += 4) {
+        float mv[16];
+        if constexpr (MASK) {
+            bool live = false;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
+                mv[i] = key < Tk ? (float)mrow[key] : -INFINITY;
+                live |= mv[i] != -INFINITY;
+            }
+            if (__ballot(live) == 0) continue;
+        }
+        const v8h *Fb = F + (int64_t)kb * NFR * 64;
+        v16f s_hh = (v16f){}, s_hl = (v16f){}, s_lh = (v16f){};
+#pragma unroll
+        for (int st = 0; st < NS; st++) {
+            const v8h ah = Fb[(2 * st) * 64], al = Fb[(2 * st + 1) * 64];
+            s_hh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[st], s_hh, 0, 0, 0);
+            s_hl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ql[st], s_hl, 0, 0, 0);
+            s_lh = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[st], s_lh, 0, 0, 0);
+        }
+        v8h bh[2][NT], bl[2][NT];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int n = 0; n < NT; n++) {
+                bh[t][n] = Fb[(2 * NS + 2 * (t * NT + n)) * 64];
+                bl[t][n] = Fb[(2 * NS + 2 * (t * NT + n) + 1) * 64];
+            }
+        const v16f sc = s_hh + (s_hl + s_lh);
+        float p[16], mblk = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
+            if (key >= Tk || (causal && key > qi)) {
+                p[i] = -INFINITY;
+            } else {
+                p[i] = sc[i];
+                if constexpr (MASK) p[i] += LOG2E * mv[i];
+            }
+            mblk = fmaxf(mblk, p[i]);
+        }
+        mblk = fmaxf(mblk, __shfl_xor(mblk, 32));
+        const float m_new = fmaxf(m_run, mblk);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = exp2f(m_run - m_use);
+        float lblk = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            p[i] = exp2f(p[i] - m_use);
+            lblk += p[i];
+        }
+        lblk += __shfl_xor(lblk, 32);
+        l_run = l_run * alpha + lblk;
+        m_run = m_new;
+        if (__ballot(alpha != 1.0f)) {
+            rs[wave][l32] = alpha;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            float al[16];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 t = *(const float4 *)&rs[wave][8 * g + 4 * half];
+                al[4 * g] = t.x, al[4 * g + 1] = t.y, al[4 * g + 2] = t.z, al[4 * g + 3] = t.w;
+            }
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) oacc[n][r] *= al[r];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            float px[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) px[j] = p[8 * t + j] * 32768.0f;
+            v8h ph, pl;
+            split8(px, ph, pl);
+#pragma unroll
+            for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, bh[t][n], oacc[n], 0, 0, 0);
+#pragma unroll
+            for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, bl[t][n], oacc[n], 0, 0, 0);
+#pragma unroll
+            for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl, bh[t][n], oacc[n], 0, 0, 0);
+        }
+    }
+
+    // merge the four waves' partial results
+    if (half == 0) mls[wave][0][l32] = m_run, mls[wave][1][l32] = l_run;
+#pragma unroll
+    for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) ored[wave][n][r][lane] = oacc[n][r];
+    __syncthreads();
+    for (int n = wave; n < NT; n += 4) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int qq = 8 * (r / 4) + 4 * half + (r % 4), q = q0 + qq;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < 4; w++) mx = fmaxf(mx, mls[w][0][qq]);
+            float o = 0.f, l = 0.f;
+            if (mx != -INFINITY) {
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const float f = exp2f(mls[w][0][qq] - mx);  // 0 for a wave that saw no key
+                    o += f * ored[w][n][r][lane];
+                    l += f * mls[w][1][qq];
+                }
+            }
+            if (q < Tq) {
+                float *ob = a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)q * a.o_st + l32 + 32 * n;
+                *ob = l > 0.f ? o / (l * 32768.0f) : 0.f;
+            }
+        }
+    }
+}
+
 // One wave per sequence: the last token's row, RMS-normed with w, then L2-normalised.
 template <int V>
 __global__ __launch_bounds__(64) void k_last_rmsnorm_l2(const float *__restrict__ x, const float *__restrict__ w,
@@ -469,8 +671,22 @@ hipError_t launch_rope_table(float2 *cs, int T, int hd, float theta_base, hipStr
 template <int HD>
 static void launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_t s) {
     const dim3 gk((unsigned)nblk, (unsigned)a.nkv, (unsigned)a.B);
-    const dim3 ga((unsigned)((a.nq + 1) / 2), (unsigned)a.B, (unsigned)((a.Tq + 127) / 128));
     hipLaunchKernelGGL((k_kv_frag<HD>), gk, dim3(256), 0, s, a, nblk);
+    // the split-key form when the regular grid (2 heads x 128 queries per workgroup) would
+    // leave most CUs idle and there are several key blocks to share out, and for masked
+    // head_dim 128 (the 8-wave kernel's mask addressing does not fit its 256 registers and
+    // spills); MQ_ATTN_SPLIT=0/1 forces either form (measurements)
+    const int64_t wgs = (int64_t)((a.nq + 1) / 2) * a.B * ((a.Tq + 127) / 128);
+    bool split = (wgs < 128 && nblk >= 4) || (HD == 128 && a.mask);
+    if (const char *e = getenv("MQ_ATTN_SPLIT"))
+        if (*e) split = atoi(e) != 0;
+    if (split) {
+        const dim3 g((unsigned)a.nq, (unsigned)a.B, (unsigned)((a.Tq + 31) / 32));
+        if (a.mask) hipLaunchKernelGGL((k_attn_split<HD, true>), g, dim3(256), 0, s, a, nblk, qscale);
+        else hipLaunchKernelGGL((k_attn_split<HD, false>), g, dim3(256), 0, s, a, nblk, qscale);
+        return;
+    }
+    const dim3 ga((unsigned)((a.nq + 1) / 2), (unsigned)a.B, (unsigned)((a.Tq + 127) / 128));
     if (a.mask) hipLaunchKernelGGL((k_attn_frag<HD, true>), ga, dim3(512), 0, s, a, nblk, qscale);
     else hipLaunchKernelGGL((k_attn_frag<HD, false>), ga, dim3(512), 0, s, a, nblk, qscale);
 }

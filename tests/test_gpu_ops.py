@@ -243,9 +243,18 @@ def _flash(q_t, k_t, v_t, mask_t, scale, out_t):
           ws_bytes, stream())
 
 
+@pytest.fixture(params=["auto", "split", "nosplit"])
+def attn_form(request, monkeypatch):
+    """Both attention forms: the 8-wave kernel and the split-key kernel (chosen by grid size,
+    or forced through MQ_ATTN_SPLIT, read at each launch)."""
+    if request.param != "auto":
+        monkeypatch.setenv("MQ_ATTN_SPLIT", "1" if request.param == "split" else "0")
+    return request.param
+
+
 @pytest.mark.parametrize("hd,nh,nkv,B,T", [(32, 12, 12, 3, 77), (64, 12, 12, 2, 128), (128, 8, 2, 2, 45),
-                                           (32, 4, 4, 1, 300)])
-def test_flash_attn_permuted_views(hd, nh, nkv, B, T):
+                                           (32, 4, 4, 1, 300), (128, 16, 8, 1, 200)])
+def test_flash_attn_permuted_views(attn_form, hd, nh, nkv, B, T):
     """q/k/v as ggml_permute(reshape(x, hd, nh, T, B), 0, 2, 1, 3) of contiguous projections."""
     rng = _rng(hd + T)
     qx = rng.standard_normal((B, T, nh, hd)).astype(np.float32)
@@ -262,7 +271,7 @@ def test_flash_attn_permuted_views(hd, nh, nkv, B, T):
     assert err <= 2e-5, err
 
 
-def test_flash_attn_pad_mask():
+def test_flash_attn_pad_mask(attn_form):
     """The rectangular batch of encode_tokens_group_4d: F16 mask [T, T, 1, B], 0 for real keys,
     -inf for padding; padded query rows still attend to the real keys."""
     hd, nh, B, T = 32, 6, 4, 50
@@ -280,10 +289,10 @@ def test_flash_attn_pad_mask():
     assert np.abs(host(out) - ref).max() / np.abs(ref).max() <= 2e-5
 
 
-def test_flash_attn_general_mask_and_empty_rows():
+def test_flash_attn_general_mask_and_empty_rows(attn_form):
     """A finite additive mask per head (relative-position bias style), Tq != Tk, and query rows
     whose keys are all masked (zero output)."""
-    hd, nh, B, Tq, Tk = 64, 4, 2, 20, 70
+    hd, nh, B, Tq, Tk = 64, 4, 2, 20, 170
     rng = _rng(22)
     qx = rng.standard_normal((B, Tq, nh, hd)).astype(np.float32)
     kx, vx = (rng.standard_normal((B, Tk, nh, hd)).astype(np.float32) for _ in range(2))
@@ -383,3 +392,23 @@ def test_rope(mode, case):
         _call(L.mq_op_rope, mq.view(dx), mq.view(dp), None, mq.view(dx), n_dims, mode, 0, 1e6, 1.0, 0.0, 1.0, 0.0,
               0.0, stream())
         assert np.array_equal(host(dx), got)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_flash_attn_causal_mask_one_sequence(attn_form, hd):
+    """The decoder graph's attention: one sequence, grouped-query heads, the causal F16 mask
+    [T, T] (0 on and below the diagonal, -inf above), whose upper blocks are skipped."""
+    nh, nkv, T = 16, 8, 333
+    rng = _rng(hd + 5)
+    qx = rng.standard_normal((1, T, nh, hd)).astype(np.float32)
+    kx, vx = (rng.standard_normal((1, T, nkv, hd)).astype(np.float32) for _ in range(2))
+    mask = np.where(np.tril(np.ones((T, T), bool)), 0.0, -np.inf).astype(np.float16)[None, None]
+    q, k, v = (_cuda(x).permute(0, 2, 1, 3) for x in (qx, kx, vx))
+    out = _t().empty((1, T, nh, hd), dtype=_t().float32, device="cuda")
+    scale = 1.0 / np.sqrt(hd)
+    _flash(q, k, v, _cuda(mask), scale, out)
+    ref = _attn64(qx.transpose(0, 2, 1, 3), kx.transpose(0, 2, 1, 3), vx.transpose(0, 2, 1, 3), mask, scale)
+    got = host(out)
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= 2e-5
+    # closed form: the first query sees only its own key, so it returns that value row
+    assert np.allclose(got[0, 0], np.repeat(vx[0, 0], nh // nkv, axis=0), atol=1e-6)
