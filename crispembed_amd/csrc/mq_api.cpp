@@ -225,9 +225,22 @@ size_t mq_workspace_bytes(int type, int64_t m, int64_t k) {
     return act_workspace_bytes(type, m, k);
 }
 
+// The path MQ_PATH_AUTO takes when n is known: the GEMV up to mq_gemv_max_m rows, and up to 32
+// rows (in 8-row launches, each streaming the weight) while the GEMM's 128x128 tile grid would
+// have fewer than 64 workgroups -- narrow layers of short inputs, where the GEMM's few
+// workgroups each walk the whole of K.
+int mq_mul_mat_path(int type, int64_t n, int64_t k, int64_t m) {
+    (void)type;
+    (void)k;
+    if (m <= mq_gemv_max_m()) return MQ_PATH_GEMV;
+    if (mq_gemv_max_m() >= 8 && m <= GEMV_MAX_M && ((m + 127) / 128) * ((n + 127) / 128) < 64) return MQ_PATH_GEMV;
+    return MQ_PATH_GEMM;
+}
+
 static int resolve_path(int path, int64_t m) {
     if (path == MQ_PATH_AUTO) path = (m <= mq_gemv_max_m()) ? MQ_PATH_GEMV : MQ_PATH_GEMM;
-    if (path == MQ_PATH_GEMV && m > 8) return fail(MQ_EINVAL, "GEMV path takes m <= 8 (m=%lld)", (long long)m);
+    if (path == MQ_PATH_GEMV && m > GEMV_MAX_M)
+        return fail(MQ_EINVAL, "GEMV path takes m <= %d (m=%lld)", GEMV_MAX_M, (long long)m);
     if (path != MQ_PATH_GEMV && path != MQ_PATH_GEMM) return fail(MQ_EINVAL, "unknown path %d", path);
     return path;
 }
@@ -252,7 +265,7 @@ int mq_quantize_act_ex(int type, const float *x, int64_t ldx, int64_t m, int64_t
     path = resolve_path(path, m);
     if (path < 0) return path;
     const bool tiled = (path == MQ_PATH_GEMM);
-    const size_t need = act_planes(type, m, k, tiled).total;
+    const size_t need = tiled ? act_planes(type, m, k, true).total : gemv_ws_bytes(type, m, k);
     if (workspace_bytes < need)
         return fail(MQ_EINVAL, "mq_quantize_act: workspace %zu bytes < %zu needed", workspace_bytes, need);
     const hipError_t e =
@@ -317,6 +330,7 @@ int mq_mul_mat_ex(int type, const void *w_image, int64_t n, int64_t k, const flo
     if (m < 0 || m > INT32_MAX || ldx < k || ldy < n) return fail(MQ_EINVAL, "mq_mul_mat: bad m/ldx/ldy");
     if (m == 0) return MQ_OK;
     if (!is_aligned(w_image, 256)) return fail(MQ_EINVAL, "mq_mul_mat: weight image must be 256-byte aligned");
+    if (path == MQ_PATH_AUTO) path = mq_mul_mat_path(type, n, k, m);
     path = resolve_path(path, m);
     if (path < 0) return path;
     const size_t need = act_workspace_bytes(type, m, k);

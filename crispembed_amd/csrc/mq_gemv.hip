@@ -444,7 +444,16 @@ static hipError_t gemv_launch(int type, const uint8_t *wb, const WeightPlanes &p
 hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
                        int64_t ldy, hipStream_t s, const float *bias) {
     if (m <= 0 || n <= 0) return hipSuccess;
-    if (m > 8) return hipErrorInvalidValue;
+    if (m > GEMV_MAX_M) return hipErrorInvalidValue;
+    if (m > GEMV_CHUNK) {  // 8 rows per launch, each on its own chunk of the activation layout
+        const size_t cb = gemv_chunk_bytes(type, k);
+        for (int64_t r0 = 0, c = 0; r0 < m; r0 += GEMV_CHUNK, c++) {
+            const hipError_t e = launch_gemv(type, image, n, k, (const uint8_t *)ws + c * cb,
+                                             std::min<int64_t>(GEMV_CHUNK, m - r0), y + r0 * ldy, ldy, s, bias);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     const WeightPlanes p = weight_planes(type, n, k);
     const ActPlanes ap = act_planes(type, m, k, false);
     const uint8_t *wb = (const uint8_t *)image;

@@ -259,8 +259,19 @@ inline ActPlanes act_planes(int wtype, int64_t m, int64_t k, bool tiled) {
     return a;
 }
 
+// The GEMV takes up to GEMV_MAX_M rows in launches of GEMV_CHUNK: its activation layout for m
+// rows is ceil(m / 8) independent row layouts (act_planes(type, rows, k, false)) of up to 8
+// rows each, chunk c at c * gemv_chunk_bytes.
+constexpr int GEMV_CHUNK = 8;
+constexpr int GEMV_MAX_M = 32;
+inline size_t gemv_chunk_bytes(int wtype, int64_t k) { return act_planes(wtype, GEMV_CHUNK, k, false).total; }
+inline size_t gemv_ws_bytes(int wtype, int64_t m, int64_t k) {
+    const int64_t full = m / GEMV_CHUNK, rem = m % GEMV_CHUNK;
+    return (size_t)full * gemv_chunk_bytes(wtype, k) + (rem ? act_planes(wtype, rem, k, false).total : 0);
+}
+
 inline size_t act_workspace_bytes(int wtype, int64_t m, int64_t k) {
-    const size_t r = act_planes(wtype, m, k, false).total, t = act_planes(wtype, m, k, true).total;
+    const size_t r = m <= GEMV_MAX_M ? gemv_ws_bytes(wtype, m, k) : 0, t = act_planes(wtype, m, k, true).total;
     return r > t ? r : t;
 }
 

@@ -10,6 +10,8 @@
 // plain coalesced streams -- 8 lanes per 32-value Q8_0 block (one float4 each,
 // a 3-step xor-shuffle max), one wave per 256-value Q8_K block (a 6-step
 // shuffle reduction of the (|x|, index) pair).
+#include <algorithm>
+
 #include "mq_internal.h"
 #include "mq_deq.h"
 
@@ -687,6 +689,16 @@ hipError_t launch_quantize_f16(const float *x, int64_t ldx, void *y, int64_t m, 
 
 hipError_t launch_quantize_act_planar(int wtype, const float *x, int64_t ldx, void *ws, int64_t m, int64_t k,
                                       int q8_0_variant, bool tiled, hipStream_t s, int pre, const float *bias) {
+    if (!tiled && m > GEMV_CHUNK) {  // the GEMV's chunked layout
+        const size_t cb = gemv_chunk_bytes(wtype, k);
+        for (int64_t r0 = 0, c = 0; r0 < m; r0 += GEMV_CHUNK, c++) {
+            const hipError_t e = launch_quantize_act_planar(wtype, x + r0 * ldx, ldx, (uint8_t *)ws + c * cb,
+                                                            std::min<int64_t>(GEMV_CHUNK, m - r0), k, q8_0_variant,
+                                                            false, s, pre, bias);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     const ActPlanes a = act_planes(wtype, m, k, tiled);
     uint8_t *base = (uint8_t *)ws;
     int8_t *xq = (int8_t *)(base + a.xq);

@@ -54,7 +54,7 @@ extern "C" {
 
 /* mq_mul_mat_ex path selection */
 #define MQ_PATH_AUTO 0 /* GEMV when m <= mq_gemv_max_m(), else GEMM */
-#define MQ_PATH_GEMV 1 /* weight-streaming GEMV, m <= 8 */
+#define MQ_PATH_GEMV 1 /* weight-streaming GEMV, m <= 32 (one launch per 8 rows) */
 #define MQ_PATH_GEMM 2 /* MFMA GEMM */
 
 /* Elementwise prologue of mq_quantize_act_ex, applied to X before it is quantized. */
@@ -123,6 +123,11 @@ int mq_weight_prepare(int type, void *image, int64_t n, int64_t k, int64_t row0,
  * `w_image` is a prepared weight image.  `workspace` receives the quantized
  * activations; size it with mq_workspace_bytes().  workspace == NULL makes the
  * library use (and grow with hipMalloc) an internal per-device buffer. */
+/* The path MQ_PATH_AUTO of mq_mul_mat / mq_mul_mat_ex takes for an n x k weight and m rows:
+ * MQ_PATH_GEMV up to mq_gemv_max_m() rows, and up to 32 rows while a 128 x 128 GEMM tile grid
+ * would have fewer than 64 workgroups (short inputs on narrow layers); else MQ_PATH_GEMM.
+ * Callers of the two-step API (mq_quantize_act_ex + mq_mul_mat_q*) pass it to both calls. */
+int mq_mul_mat_path(int type, int64_t n, int64_t k, int64_t m);
 size_t mq_workspace_bytes(int type, int64_t m, int64_t k);
 int mq_mul_mat(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m, float *y,
                int64_t ldy, void *workspace, size_t workspace_bytes, void *stream);

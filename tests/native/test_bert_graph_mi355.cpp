@@ -6,8 +6,14 @@
 // ADD + layer norm, and the GELU_ERF FFN), computed entirely by the MI355X backend.
 //
 // usage: test-bert-graph-mi355 model.gguf B T ids.i32 types.i32 lens.i32 out.f32 [--fused-qkv] [--iters N]
+//                              [--check-replay]
 //   ids / types: B*T int32 (item-major, t fastest); lens: B int32 real lengths (all T: no mask);
 //   out: the encoder_out tensor [H, B*T] as float32.  Prints one JSON line.
+//   --check-replay: after the first (eager) compute, computes the graph for a second id set
+//   (each id + 1; the backend captures it), then for the first set and the second again (the
+//   captured graph replayed, with uploads and readbacks in between), and reports whether the
+//   replays equal the first two results bit for bit; the second set's result goes to
+//   <out>.second.
 #include <chrono>
 #include <cmath>
 #include <cstdint>
@@ -48,10 +54,11 @@ int main(int argc, char **argv) {
     if (argc < 8) return fail("usage: model.gguf B T ids types lens out [--fused-qkv] [--iters N]");
     const char *path = argv[1];
     const int B = std::atoi(argv[2]), T = std::atoi(argv[3]);
-    bool fused_qkv = false;
+    bool fused_qkv = false, check_replay = false;
     int iters = 0;
     for (int i = 8; i < argc; i++) {
         if (!std::strcmp(argv[i], "--fused-qkv")) fused_qkv = true;
+        if (!std::strcmp(argv[i], "--check-replay")) check_replay = true;
         if (!std::strcmp(argv[i], "--iters") && i + 1 < argc) iters = std::atoi(argv[++i]);
     }
     const int TB = B * T;
@@ -212,6 +219,27 @@ int main(int argc, char **argv) {
     if (!f || std::fwrite(out.data(), sizeof(float), out.size(), f) != out.size()) return fail("cannot write output");
     std::fclose(f);
 
+    int replay_identical = -1;
+    if (check_replay) {
+        std::vector<int32_t> ids2(TB);
+        const int32_t *ids1 = (const int32_t *)ids_raw.data();
+        for (int i = 0; i < TB; i++) ids2[i] = ids1[i] + 1;
+        std::vector<float> o2(out.size()), o3(out.size()), o4(out.size());
+        auto run = [&](const void *ids, std::vector<float> &dst) {
+            ggml_backend_tensor_set(tok_ids, ids, 0, (size_t)TB * 4);
+            if (ggml_backend_graph_compute(be, gf) != GGML_STATUS_SUCCESS) return false;
+            ggml_backend_tensor_get(cur, dst.data(), 0, dst.size() * sizeof(float));
+            return true;
+        };
+        if (!run(ids2.data(), o2) || !run(ids1, o3) || !run(ids2.data(), o4)) return fail("graph_compute failed");
+        replay_identical = std::memcmp(o3.data(), out.data(), out.size() * 4) == 0 &&
+                           std::memcmp(o4.data(), o2.data(), out.size() * 4) == 0;
+        const std::string p2 = std::string(argv[7]) + ".second";
+        FILE *f2 = std::fopen(p2.c_str(), "wb");
+        if (!f2 || std::fwrite(o2.data(), sizeof(float), o2.size(), f2) != o2.size()) return fail("cannot write output");
+        std::fclose(f2);
+        ggml_backend_tensor_set(tok_ids, ids1, 0, (size_t)TB * 4);
+    }
     double ms = 0.0;
     if (iters > 0) {
         const auto t0 = std::chrono::steady_clock::now();
@@ -219,8 +247,9 @@ int main(int argc, char **argv) {
             if (ggml_backend_graph_compute(be, gf) != GGML_STATUS_SUCCESS) return fail("graph_compute failed");
         ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() / iters;
     }
-    std::printf("{\"ok\": true, \"nodes\": %d, \"unsupported\": %d, \"ms_per_graph\": %.4f, \"iters\": %d}\n",
-                ggml_graph_n_nodes(gf), unsupported, ms, iters);
+    std::printf("{\"ok\": true, \"nodes\": %d, \"unsupported\": %d, \"ms_per_graph\": %.4f, \"iters\": %d, "
+                "\"replay_identical\": %d}\n",
+                ggml_graph_n_nodes(gf), unsupported, ms, iters, replay_identical);
     ggml_backend_buffer_free(gbuf);
     ggml_backend_buffer_free(wbuf);
     ggml_free(gctx);

@@ -36,6 +36,11 @@ def test_host_only_entry_points_without_gpu():
     assert L.mq_gguf_bytes(mq.TYPE_Q4_K, 4096, 1024) == 4096 * 4 * 144
     assert L.mq_weight_image_bytes(mq.TYPE_Q4_K, 4096, 1024) > L.mq_gguf_bytes_aligned(mq.TYPE_Q4_K, 4096, 1024)
     assert L.mq_weight_image_bytes(mq.TYPE_F16, 8, 64) >= L.mq_gguf_bytes_aligned(mq.TYPE_F16, 8, 64) + 256 * 128
+    # the auto path: GEMV for m <= 8, and up to 32 rows on narrow layers (few GEMM tiles)
+    assert L.mq_mul_mat_path(mq.TYPE_Q8_0, 384, 384, 4) == mq.PATH_GEMV
+    assert L.mq_mul_mat_path(mq.TYPE_Q8_0, 384, 384, 16) == mq.PATH_GEMV
+    assert L.mq_mul_mat_path(mq.TYPE_Q8_0, 384, 384, 33) == mq.PATH_GEMM
+    assert L.mq_mul_mat_path(mq.TYPE_Q6_K, 151936, 2048, 16) == mq.PATH_GEMM
     # argument errors come back as codes with a message, before any HIP call
     rc = L.mq_mul_mat(mq.TYPE_Q4_K, None, 8, 300, None, 300, 1, None, 8, None, 0, None)
     assert rc == -2 and b"multiple" in L.mq_last_error()

@@ -156,3 +156,23 @@ def test_decoder_graph_matches_reference(oracle, tmp_path, wtype, hd, causal):
     assert np.median(cos) >= 0.99995
     assert cos[-1] >= 0.9999
     assert _pool(got) @ _pool(ref) >= 0.9999
+
+
+def test_bert_graph_hip_graph_replay(tmp_path):
+    """With MQ_GGML_GRAPH=1 the backend captures a graph computed twice in a row and replays
+    it: replays with different inputs uploaded in between (eager copies and readbacks between
+    the replays) equal the first results bit for bit, and the captured second input equals its
+    eager computation."""
+    W = bert.synthetic_weights(HP, O.Q8_0, name="graphreplay")
+    model = tmp_path / "m.gguf"
+    gguf.write_bert_gguf(model, HP, O.Q8_0, W)
+    B, T = 2, 29
+    ids = np.random.default_rng(11).integers(0, HP["n_vocab"] - 1, (B, T)).astype(np.int32)
+    types = np.zeros((B, T), np.int32)
+    a, res = _run(tmp_path, model, B, T, ids, types, np.full(B, T), ("--check-replay", "--iters", "5"),
+                  env={"MQ_GGML_GRAPH": "1"})
+    assert res["replay_identical"] == 1
+    second = np.fromfile(tmp_path / "out.f32.second", dtype=np.float32)
+    a_eager, _ = _run(tmp_path, model, B, T, ids, types, np.full(B, T), ("--check-replay",))
+    second_eager = np.fromfile(tmp_path / "out.f32.second", dtype=np.float32)
+    assert np.array_equal(a, a_eager) and np.array_equal(second, second_eager)

@@ -50,9 +50,10 @@ def test_gemm(oracle, wtype, m, n, k, cfg, monkeypatch):
 
 
 @pytest.mark.parametrize("wtype", TYPES)
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 16, 27, 32])
 @pytest.mark.parametrize("n,k", [(67, 256), (130, 2048), (20, 6144)])
 def test_gemv(oracle, wtype, m, n, k):
+    """m <= 8 in one launch; 9..32 in 8-row launches over the chunked activation layout."""
     from crispembed_amd import mq
     w, x = _mk(oracle, wtype, m, n, k, 1000 + m * 13 + n + k)
     _, wp = weight_image(wtype, w, n, k)

@@ -88,7 +88,8 @@ def test_gelu_prologue_mul_mat(oracle, wtype, m, n, k, ld, path):
 
 
 @pytest.mark.parametrize("wtype", TYPES)
-@pytest.mark.parametrize("m,n,k,path", [(1, 300, 512, 1), (6, 70, 1536, 1), (77, 96, 512, 2), (300, 200, 1536, 2)])
+@pytest.mark.parametrize("m,n,k,path", [(1, 300, 512, 1), (6, 70, 1536, 1), (19, 70, 1536, 1), (77, 96, 512, 2),
+                                        (300, 200, 1536, 2)])
 def test_mul_mat_q_ex_bias_in_store(wtype, m, n, k, path):
     """mq_mul_mat_q_ex adds the bias as the GEMM / GEMV stores each row: bit-identical to the
     plain mat-mul followed by one fp32 add per element (the graph's ADD node)."""
@@ -125,7 +126,7 @@ def mq_quantized(wtype, w):
 
 
 @pytest.mark.parametrize("wtype", TYPES)
-@pytest.mark.parametrize("m,k,path", [(5, 512, 1), (300, 512, 2), (4096, 256, 2)])
+@pytest.mark.parametrize("m,k,path", [(5, 512, 1), (21, 512, 1), (300, 512, 2), (4096, 256, 2)])
 def test_mul_mat_q_group_equals_separate(wtype, m, k, path):
     """mq_mul_mat_q_group (one launch over the feature tiles of every weight) against one
     mq_mul_mat_q_ex per weight: bit-identical, with ragged n, per-group biases (one absent)
