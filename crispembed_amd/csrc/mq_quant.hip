@@ -286,11 +286,22 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
     constexpr int NIT = 8 / RPI;                        // rows per lane
     const int64_t kv = (cb * CB + kbyte) / BPV;         // first value index of this lane
     float4 vin[NIT];                                    // every load in flight before any math
+    if (pre == MQ_PRE_NONE && bias == nullptr) {
+        // the plain loads on their own (uniform branch): with the prologue's code in the same
+        // loop the compiler no longer issues all NIT loads before the first use
 #pragma unroll
-    for (int it = 0; it < NIT; it++) {
-        const int64_t row = rt * 32 + wave * 8 + it * RPI + rsub;
-        vin[it] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (row < m && kv < k) vin[it] = pre_load<VEC4>(x + row * ldx + kv, pre, bias, kv, k);
+        for (int it = 0; it < NIT; it++) {
+            const int64_t row = rt * 32 + wave * 8 + it * RPI + rsub;
+            vin[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (row < m && kv < k) vin[it] = load4<VEC4>(x + row * ldx + kv);
+        }
+    } else {
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            const int64_t row = rt * 32 + wave * 8 + it * RPI + rsub;
+            vin[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (row < m && kv < k) vin[it] = pre_load<VEC4>(x + row * ldx + kv, pre, bias, kv, k);
+        }
     }
 #pragma unroll
     for (int it = 0; it < NIT; it++) {
