@@ -4,7 +4,8 @@
 // quantized weights (mq.h) and the other ops of the encoder graph
 // (src/crispembed.cpp:1043-1468) through mq_ops.h: GET_ROWS, ADD / SUB / MUL / DIV,
 // NORM / RMS_NORM, UNARY (GELU_ERF, GELU, SILU, RELU), CPY / CONT / DUP, ROPE
-// (ggml_rope_ext, normal and NEOX) and FLASH_ATTN_EXT, plus the metadata-only view ops.  Anything else is refused by
+// (ggml_rope_ext, normal and NEOX), FLASH_ATTN_EXT and MUL_MAT_ID (mixture-of-experts on
+// 3-D expert weights), plus the metadata-only view ops.  Anything else is refused by
 // supports_op, and ggml_backend_sched keeps it on the CPU backend, which is how
 // CrispEmbed already falls back for ops a GPU backend rejects (src/crispembed.cpp:700-723).
 //
@@ -27,6 +28,7 @@
 
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -143,9 +145,15 @@ int binary_of(enum ggml_op op) {
 // rows plus the tiled copy the MFMA GEMM reads.)
 bool is_image(const ggml_tensor *t) {
     const int mt = mq_type_of(t->type);
-    return mt >= 0 && t->view_src == nullptr && t->ne[2] == 1 && t->ne[3] == 1 && ggml_is_contiguous(t) &&
-           mq_supports(mt, t->ne[0]) && t->ne[1] > 0;
+    return mt >= 0 && t->view_src == nullptr && t->ne[3] == 1 && ggml_is_contiguous(t) && mq_supports(mt, t->ne[0]) &&
+           t->ne[1] > 0 && t->ne[2] > 0;
 }
+
+// A 3-D weight [k, n, n_exp] (the experts of MUL_MAT_ID) is allocated as n_exp weight images
+// of image_bytes each, expert e at data + e * image_bytes; a 2-D weight is one image.  The
+// GGUF byte offsets of set_tensor / get_tensor are mapped to the expert images, so readback
+// still returns the GGUF bytes.
+size_t image_bytes(const ggml_tensor *t) { return mq_weight_image_bytes(mq_type_of(t->type), t->ne[1], t->ne[0]); }
 
 class DeviceGuard {
    public:
@@ -174,38 +182,64 @@ void *buf_base(ggml_backend_buffer_t b) { return ((BufferCtx *)b->context)->base
 
 enum ggml_status buf_init_tensor(ggml_backend_buffer_t, ggml_tensor *) { return GGML_STATUS_SUCCESS; }
 
-void rebuild_planes(BufferCtx *c, ggml_tensor *t, size_t offset, size_t size) {
-    if (!is_image(t)) return;
+// planes of the rows of expert e touched by GGUF bytes [offset, offset + size) of that expert
+void rebuild_planes(ggml_tensor *t, int64_t e, size_t offset, size_t size) {
     const int mt = mq_type_of(t->type);
     const size_t rs = ggml_row_size(t->type, t->ne[0]);
     const int64_t r0 = (int64_t)(offset / rs), r1 = (int64_t)((offset + size + rs - 1) / rs);
-    if (mq_weight_prepare(mt, t->data, t->ne[1], t->ne[0], r0, r1, nullptr) != 0) {
+    char *img = (char *)t->data + (size_t)e * image_bytes(t);
+    if (mq_weight_prepare(mt, img, t->ne[1], t->ne[0], r0, r1, nullptr) != 0) {
         std::fprintf(stderr, "ggml-mi355: weight preparation of '%s' failed: %s\n", t->name, mq_last_error());
         std::abort();
     }
     hip_check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
-    (void)c;
+}
+
+// Calls f(device address, tensor byte offset, bytes, expert) for the pieces of the tensor's
+// byte range [offset, offset + size): one piece for plain tensors, one per expert image
+// touched for weight images.
+template <typename F>
+void for_each_piece(ggml_tensor *t, size_t offset, size_t size, F f) {
+    if (!is_image(t)) {
+        f((char *)t->data + offset, (size_t)0, size, (int64_t)0, offset);
+        return;
+    }
+    const size_t raw = ggml_row_size(t->type, t->ne[0]) * (size_t)t->ne[1], ib = image_bytes(t);
+    size_t done = 0;
+    while (done < size) {
+        const size_t at = offset + done;
+        const int64_t e = (int64_t)(at / raw);
+        const size_t local = at - (size_t)e * raw, n = std::min(size - done, raw - local);
+        f((char *)t->data + (size_t)e * ib + local, done, n, e, local);
+        done += n;
+    }
 }
 
 void buf_set_tensor(ggml_backend_buffer_t b, ggml_tensor *t, const void *data, size_t offset, size_t size) {
     BufferCtx *c = (BufferCtx *)b->context;
     DeviceGuard g(c->ordinal);
-    hip_check(hipMemcpy((char *)t->data + offset, data, size, hipMemcpyHostToDevice), "hipMemcpy H2D");
-    rebuild_planes(c, t, offset, size);
+    for_each_piece(t, offset, size, [&](char *dev, size_t src_off, size_t n, int64_t e, size_t local) {
+        hip_check(hipMemcpy(dev, (const char *)data + src_off, n, hipMemcpyHostToDevice), "hipMemcpy H2D");
+        if (is_image(t)) rebuild_planes(t, e, local, n);
+    });
 }
 
 void buf_get_tensor(ggml_backend_buffer_t b, const ggml_tensor *t, void *data, size_t offset, size_t size) {
     BufferCtx *c = (BufferCtx *)b->context;
     DeviceGuard g(c->ordinal);
     // hipMemcpy on the null stream waits for work queued on the (blocking) backend streams
-    hip_check(hipMemcpy(data, (const char *)t->data + offset, size, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    for_each_piece((ggml_tensor *)t, offset, size, [&](char *dev, size_t dst_off, size_t n, int64_t, size_t) {
+        hip_check(hipMemcpy((char *)data + dst_off, dev, n, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    });
 }
 
 void buf_memset_tensor(ggml_backend_buffer_t b, ggml_tensor *t, uint8_t value, size_t offset, size_t size) {
     BufferCtx *c = (BufferCtx *)b->context;
     DeviceGuard g(c->ordinal);
-    hip_check(hipMemset((char *)t->data + offset, value, size), "hipMemset");
-    rebuild_planes(c, t, offset, size);
+    for_each_piece(t, offset, size, [&](char *dev, size_t, size_t n, int64_t e, size_t local) {
+        hip_check(hipMemset(dev, value, n), "hipMemset");
+        if (is_image(t)) rebuild_planes(t, e, local, n);
+    });
 }
 
 bool buf_cpy_tensor(ggml_backend_buffer_t b, const ggml_tensor *src, ggml_tensor *dst) {
@@ -213,9 +247,15 @@ bool buf_cpy_tensor(ggml_backend_buffer_t b, const ggml_tensor *src, ggml_tensor
     if (!sb || sb->iface.free_buffer != buf_free) return false;  // only device-to-device within this backend
     BufferCtx *c = (BufferCtx *)b->context;
     DeviceGuard g(c->ordinal);
-    const size_t n = ggml_nbytes(src);
-    hip_check(hipMemcpy(dst->data, src->data, n, hipMemcpyDeviceToDevice), "hipMemcpy D2D");
-    rebuild_planes(c, dst, 0, n);
+    if (is_image(src) != is_image(dst)) return false;  // layouts differ: the caller copies through the host
+    if (is_image(dst)) {  // same type and shape: the whole images, planes included
+        if (src->type != dst->type || src->ne[0] != dst->ne[0] || src->ne[1] != dst->ne[1] || src->ne[2] != dst->ne[2])
+            return false;
+        hip_check(hipMemcpy(dst->data, src->data, image_bytes(dst) * (size_t)dst->ne[2], hipMemcpyDeviceToDevice),
+                  "hipMemcpy D2D");
+        return true;
+    }
+    hip_check(hipMemcpy(dst->data, src->data, ggml_nbytes(src), hipMemcpyDeviceToDevice), "hipMemcpy D2D");
     return true;
 }
 
@@ -253,7 +293,7 @@ size_t buft_alignment(ggml_backend_buffer_type_t) { return 256; }  // weight ima
 size_t buft_max_size(ggml_backend_buffer_type_t) { return SIZE_MAX; }
 
 size_t buft_alloc_size(ggml_backend_buffer_type_t, const ggml_tensor *t) {
-    if (is_image(t)) return mq_weight_image_bytes(mq_type_of(t->type), t->ne[1], t->ne[0]);
+    if (is_image(t)) return image_bytes(t) * (size_t)t->ne[2];
     return ggml_nbytes(t);
 }
 
@@ -594,6 +634,17 @@ enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node) {
             const mq_view s = view_of(node->src[0]), d = view_of(node->op == GGML_OP_CPY ? node->src[1] : node);
             return op_status(mq_op_cpy(&s, &d, c->stream), node);
         }
+        case GGML_OP_MUL_MAT_ID: {
+            const ggml_tensor *as = node->src[0];
+            const mq_view b = view_of(node->src[1]), ids = view_of(node->src[2]), d = view_of(node);
+            const int mt = mq_type_of(as->type);
+            c->ws_x = nullptr;
+            if (!ensure_ws(c, mq_op_mul_mat_id_workspace_bytes(mt, as->ne[1], as->ne[0], ids.ne[0] * ids.ne[1])))
+                return GGML_STATUS_ALLOC_FAILED;
+            return op_status(mq_op_mul_mat_id(mt, as->data, image_bytes(as), (int)as->ne[2], as->ne[1], as->ne[0], &b,
+                                              &ids, &d, c->ws, c->ws_bytes, c->stream),
+                             node);
+        }
         case GGML_OP_ROPE: {
             const mq_view x = view_of(node->src[0]), p = view_of(node->src[1]), d = view_of(node);
             mq_view f{};
@@ -841,6 +892,19 @@ bool dev_supports_op(ggml_backend_dev_t d, const ggml_tensor *op) {
         case GGML_OP_CPY: return mq_op_supported(MQ_OP_CPY, 0, p[0], nullptr, nullptr, nullptr, p[1]);
         case GGML_OP_CONT:
         case GGML_OP_DUP: return mq_op_supported(MQ_OP_CPY, 0, p[0], nullptr, nullptr, nullptr, &dst);
+        case GGML_OP_MUL_MAT_ID: {
+            // expert weights: a 3-D weight image set in this device's buffers; b [k, 1|n_used, T],
+            // ids [n_used, T], dst [n, n_used, T], F32 rows contiguous
+            const ggml_tensor *as = op->src[0], *b = op->src[1], *ids = op->src[2];
+            if (!as || !b || !ids || !is_image(as) || !in_this_device(d, as)) return false;
+            if (b->type != GGML_TYPE_F32 || ids->type != GGML_TYPE_I32 || op->type != GGML_TYPE_F32) return false;
+            const int64_t n_used = ids->ne[0], T = ids->ne[1];
+            if (b->ne[0] != as->ne[0] || (b->ne[1] != 1 && b->ne[1] != n_used) || b->ne[2] != T || b->ne[3] != 1 ||
+                ids->ne[2] != 1 || op->ne[0] != as->ne[1] || op->ne[1] != n_used || op->ne[2] != T)
+                return false;
+            return b->nb[0] == sizeof(float) && b->nb[1] % 16 == 0 && b->nb[2] % 16 == 0 && b->view_offs % 16 == 0 &&
+                   ids->nb[0] == sizeof(int32_t) && op->nb[0] == sizeof(float);
+        }
         case GGML_OP_ROPE: {
             const int n_dims = op->op_params[1], mode = op->op_params[2];
             if (n_dims <= 0 || n_dims % 2 || n_dims > op->src[0]->ne[0]) return false;

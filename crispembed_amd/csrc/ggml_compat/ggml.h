@@ -163,6 +163,9 @@ GGML_API struct ggml_tensor *ggml_new_tensor_4d(struct ggml_context *ctx, enum g
 GGML_API struct ggml_tensor *ggml_get_first_tensor(const struct ggml_context *ctx);
 GGML_API struct ggml_tensor *ggml_get_next_tensor(const struct ggml_context *ctx, struct ggml_tensor *tensor);
 GGML_API struct ggml_tensor *ggml_mul_mat(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b);
+// as [k, n, n_exp], b [k, 1|n_used, T], ids I32 [n_used, T] -> [n, n_used, T]
+GGML_API struct ggml_tensor *ggml_mul_mat_id(struct ggml_context *ctx, struct ggml_tensor *as, struct ggml_tensor *b,
+                                            struct ggml_tensor *ids);
 GGML_API struct ggml_tensor *ggml_add(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b);
 GGML_API struct ggml_tensor *ggml_reshape_2d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0,
                                             int64_t ne1);

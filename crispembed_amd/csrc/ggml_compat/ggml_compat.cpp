@@ -222,6 +222,17 @@ extern "C" struct ggml_tensor *ggml_mul_mat(struct ggml_context *ctx, struct ggm
     return r;
 }
 
+extern "C" struct ggml_tensor *ggml_mul_mat_id(struct ggml_context *ctx, struct ggml_tensor *as,
+                                               struct ggml_tensor *b, struct ggml_tensor *ids) {
+    const int64_t ne[4] = {as->ne[1], ids->ne[0], b->ne[2], 1};
+    ggml_tensor *r = new_tensor(ctx, GGML_TYPE_F32, 4, ne);
+    r->op = GGML_OP_MUL_MAT_ID;
+    r->src[0] = as;
+    r->src[1] = b;
+    r->src[2] = ids;
+    return r;
+}
+
 static ggml_tensor *binary(ggml_context *ctx, ggml_tensor *a, ggml_tensor *b, ggml_op op) {
     ggml_tensor *r = new_tensor(ctx, a->type, 4, a->ne);
     r->op = op;

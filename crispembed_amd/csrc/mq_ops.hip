@@ -18,6 +18,7 @@
 #include <cstdio>
 #include <cstring>
 #include <initializer_list>
+#include <vector>
 
 #include "../../include/mq_ops.h"
 #include "mq_deq.h"
@@ -286,6 +287,24 @@ __global__ __launch_bounds__(256) void k_rope(const DV x, const DV pos, const fl
         dr[e0] = a * c - b * sn;
         dr[e1] = a * sn + b * c;
     }
+}
+
+// Row moves of the mixture-of-experts mat-mul: one workgroup per row r, float4 copies
+// (rows of k floats, k a multiple of 32 for every weight type), byte offsets per row.
+__global__ __launch_bounds__(256) void k_gather_rows(const char *__restrict__ src, const int64_t *__restrict__ off,
+                                                     float *__restrict__ dst, int64_t k) {
+    const int64_t r = blockIdx.x;
+    const float4 *s = (const float4 *)(src + off[r]);
+    float4 *d = (float4 *)(dst + r * k);
+    for (int64_t c = threadIdx.x; c < k / 4; c += 256) d[c] = s[c];
+}
+
+__global__ __launch_bounds__(256) void k_scatter_rows(const float *__restrict__ src, const int64_t *__restrict__ off,
+                                                      char *__restrict__ dst, int64_t n) {
+    const int64_t r = blockIdx.x;
+    const float *s = src + r * n;
+    float *d = (float *)(dst + off[r]);
+    for (int64_t c = threadIdx.x; c < n; c += 256) d[c] = s[c];
 }
 
 // ------------------------------------------------------------------ checks ----
@@ -575,6 +594,103 @@ extern "C" int mq_op_rope(const mq_view *x, const mq_view *pos, const mq_view *f
         hipLaunchKernelGGL((k_rope<MQ_ROPE_NORMAL>), dim3(grid_units(units)), dim3(256), 0, s, dv(x), dv(pos), ff, dv(dst),
                            rp, units);
     return hip_rc(hipGetLastError(), "rope");
+}
+
+// workspace of the mixture-of-experts mat-mul: gathered rows, their results, the two offset
+// lists and the activation quantization of up to `rows` rows
+struct MoeWs {
+    size_t x, y, src_off, dst_off, q, total;
+};
+static MoeWs moe_ws(int type, int64_t n, int64_t k, int64_t rows) {
+    MoeWs w;
+    size_t o = 0;
+    auto take = [&](size_t b) {
+        const size_t at = o;
+        o = align256(o + b);
+        return at;
+    };
+    w.x = take((size_t)rows * k * 4);
+    w.y = take((size_t)rows * n * 4);
+    w.src_off = take((size_t)rows * 8);
+    w.dst_off = take((size_t)rows * 8);
+    w.q = take(mq_workspace_bytes(type, rows, k));
+    w.total = o;
+    return w;
+}
+
+extern "C" size_t mq_op_mul_mat_id_workspace_bytes(int type, int64_t n, int64_t k, int64_t rows) {
+    if (n <= 0 || k <= 0 || rows <= 0 || mq_row_size(type, k) == 0) return 0;
+    return moe_ws(type, n, k, rows).total;
+}
+
+extern "C" int mq_op_mul_mat_id(int type, const void *expert_images, size_t expert_stride, int n_exp, int64_t n,
+                                int64_t k, const mq_view *b, const mq_view *ids, const mq_view *dst, void *workspace,
+                                size_t workspace_bytes, void *stream) {
+    if (!expert_images || n_exp <= 0 || !b || !ids || !dst || !b->data || !ids->data || !dst->data || !workspace)
+        return set_error(MQ_EINVAL, "mq_op_mul_mat_id: missing operand");
+    if (!mq_supports(type, k) || n <= 0 || (expert_stride % 256) != 0 || ((uintptr_t)expert_images & 255) != 0)
+        return set_error(MQ_EUNSUPPORTED, "mq_op_mul_mat_id: weight type %d with k %lld", type, (long long)k);
+    if (!shape_ok(b) || !shape_ok(ids) || !shape_ok(dst) || b->type != MQ_TYPE_F32 || ids->type != MQ_TYPE_I32 ||
+        dst->type != MQ_TYPE_F32)
+        return set_error(MQ_EINVAL, "mq_op_mul_mat_id: types (F32 b and dst, I32 ids)");
+    const int64_t n_used = ids->ne[0], T = ids->ne[1];
+    if (b->ne[0] != k || (b->ne[1] != 1 && b->ne[1] != n_used) || b->ne[2] != T || b->ne[3] != 1 || ids->ne[2] != 1 ||
+        ids->ne[3] != 1 || dst->ne[0] != n || dst->ne[1] != n_used || dst->ne[2] != T || dst->ne[3] != 1)
+        return set_error(MQ_EINVAL, "mq_op_mul_mat_id: shapes (b [k, 1|n_used, T], ids [n_used, T], dst [n, n_used, T])");
+    if (b->nb[0] != 4 || dst->nb[0] != 4 || ids->nb[0] != 4 || b->nb[1] % 16 || b->nb[2] % 16 || dst->nb[1] % 4 ||
+        dst->nb[2] % 4 || ((uintptr_t)b->data & 15))
+        return set_error(MQ_EINVAL, "mq_op_mul_mat_id: rows must be contiguous (b rows 16-byte aligned)");
+    const int64_t R = n_used * T;
+    const MoeWs w = moe_ws(type, n, k, R);
+    if (((uintptr_t)workspace & 255) || workspace_bytes < w.total)
+        return set_error(MQ_EINVAL, "mq_op_mul_mat_id: workspace of %zu bytes (256-byte aligned) needed, %zu given",
+                         w.total, workspace_bytes);
+    hipStream_t s = (hipStream_t)stream;
+    // the routing, read back once
+    const size_t span = (size_t)(T - 1) * ids->nb[1] + (size_t)n_used * 4;
+    std::vector<char> ih(span);
+    if (hipMemcpyAsync(ih.data(), ids->data, span, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return set_error(MQ_EHIP, "mq_op_mul_mat_id: reading the expert ids failed");
+    std::vector<int64_t> cnt(n_exp + 1, 0);
+    for (int64_t t = 0; t < T; t++)
+        for (int64_t i = 0; i < n_used; i++) {
+            const int32_t e = *(const int32_t *)(ih.data() + t * ids->nb[1] + i * 4);
+            if (e < 0 || e >= n_exp)
+                return set_error(MQ_EINVAL, "mq_op_mul_mat_id: expert id %d of slot %lld, token %lld outside [0, %d)", e,
+                                 (long long)i, (long long)t, n_exp);
+            cnt[e + 1]++;
+        }
+    for (int e = 0; e < n_exp; e++) cnt[e + 1] += cnt[e];  // row ranges of the experts
+    std::vector<int64_t> offs(2 * R), fill(cnt.begin(), cnt.end() - 1);
+    for (int64_t t = 0; t < T; t++)
+        for (int64_t i = 0; i < n_used; i++) {
+            const int32_t e = *(const int32_t *)(ih.data() + t * ids->nb[1] + i * 4);
+            const int64_t r = fill[e]++;
+            offs[r] = (int64_t)((i % b->ne[1]) * b->nb[1] + t * b->nb[2]);
+            offs[R + r] = (int64_t)(i * dst->nb[1] + t * dst->nb[2]);
+        }
+    char *ws = (char *)workspace;
+    if (hipMemcpyAsync(ws + w.src_off, offs.data(), (size_t)R * 8, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipMemcpyAsync(ws + w.dst_off, offs.data() + R, (size_t)R * 8, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)  // the host lists go out of scope on return
+        return set_error(MQ_EHIP, "mq_op_mul_mat_id: uploading the row lists failed");
+    float *X = (float *)(ws + w.x), *Y = (float *)(ws + w.y);
+    hipLaunchKernelGGL(k_gather_rows, dim3((unsigned)R), dim3(256), 0, s, (const char *)b->data,
+                       (const int64_t *)(ws + w.src_off), X, k);
+    for (int e = 0; e < n_exp; e++) {
+        const int64_t r0 = cnt[e], m = cnt[e + 1] - cnt[e];
+        if (m == 0) continue;
+        const void *img = (const char *)expert_images + (size_t)e * expert_stride;
+        const int path = mq_mul_mat_path(type, n, k, m);
+        int rc = mq_quantize_act_ex(type, X + r0 * k, k, m, k, nullptr, MQ_PRE_NONE, ws + w.q, workspace_bytes - w.q,
+                                    path, stream);
+        if (rc == 0) rc = mq_mul_mat_q_ex(type, img, n, k, ws + w.q, m, Y + r0 * n, n, nullptr, path, stream);
+        if (rc != 0) return rc;
+    }
+    hipLaunchKernelGGL(k_scatter_rows, dim3((unsigned)R), dim3(256), 0, s, Y, (const int64_t *)(ws + w.dst_off),
+                       (char *)dst->data, n);
+    return hip_rc(hipGetLastError(), "mul_mat_id");
 }
 
 extern "C" size_t mq_op_flash_attn_workspace_bytes(const mq_view *k) {

@@ -13,6 +13,7 @@
  *   ggml_cont / ggml_cpy (src/crispembed.cpp:1164-1166)       mq_op_cpy
  *   ggml_flash_attn_ext  (src/crispembed.cpp:1293)            mq_op_flash_attn
  *   ggml_rope_ext        (src/decoder_embed.cpp:756-759)      mq_op_rope
+ *   ggml_mul_mat_id      (src/crispembed.cpp:1365,1371)       mq_op_mul_mat_id
  * The semantics (shapes, broadcasting, op_params) are ggml's, as its CPU backend computes them
  * (ggml-cpu ops.cpp, the ggml submodule pinned in .gitmodules): the ggml backend passes each
  * node's tensors straight through.
@@ -110,6 +111,23 @@ int mq_op_flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const
 int mq_op_rope(const mq_view *x, const mq_view *pos, const mq_view *freq_factors, const mq_view *dst, int n_dims,
                int mode, int n_ctx_orig, float freq_base, float freq_scale, float ext_factor, float attn_factor,
                float beta_fast, float beta_slow, void *stream);
+
+/* ggml_mul_mat_id, the mixture-of-experts mat-mul (src/crispembed.cpp:1365,1371):
+ *   experts: n_exp prepared weight images of `type` (n x k each, as mq_weight_prepare builds
+ *            them), expert e at expert_images + e * expert_stride bytes;
+ *   b   F32 [k, nb1, T] (rows contiguous): slot i of token t reads row i % nb1 of token t
+ *       (nb1 = 1: every slot reads the token's one row);
+ *   ids I32 [n_used, T] (any row stride): the expert of slot i of token t;
+ *   dst F32 [n, n_used, T] (rows contiguous): dst[:, i, t] = W_{ids[i, t]} b[:, i % nb1, t].
+ * The routing is read back to the host (the stream is synchronized once, as ggml's GPU
+ * backends do for ids), the rows are gathered by expert in one pass, every used expert runs one
+ * activation quantization and one GEMM or GEMV (mq_mul_mat_path) over its rows, and one pass
+ * scatters the results.  An id outside [0, n_exp) fails with MQ_EINVAL (after the sync).
+ * workspace: mq_op_mul_mat_id_workspace_bytes(type, n, k, n_used * T) bytes, 256-aligned. */
+size_t mq_op_mul_mat_id_workspace_bytes(int type, int64_t n, int64_t k, int64_t rows);
+int mq_op_mul_mat_id(int type, const void *expert_images, size_t expert_stride, int n_exp, int64_t n, int64_t k,
+                     const mq_view *b, const mq_view *ids, const mq_view *dst, void *workspace, size_t workspace_bytes,
+                     void *stream);
 
 /* ids for mq_op_supported */
 #define MQ_OP_GET_ROWS 0

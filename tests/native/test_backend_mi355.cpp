@@ -7,6 +7,7 @@
 // summary) with MUL_MAT graphs in place of the 16-element ADD.
 //
 // usage: test-backend-mi355 [backend-name-prefix] [--json]
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -66,7 +67,7 @@ static double rel_err(const std::vector<float> &got, const std::vector<float> &r
 struct Result {
     int cases = 0;
     double max_err = 0;
-    bool roundtrip = true, partial = true, batched = true, supports = true, computed = true;
+    bool roundtrip = true, partial = true, batched = true, supports = true, computed = true, moe = true;
 };
 
 // One weight of `type` [K in, N out], activations [K, M] (ne2 batches), through the graph.
@@ -140,6 +141,91 @@ static void run_case(ggml_backend_t be, ggml_type type, int64_t K, int64_t N, in
     ggml_free(ctx);
 }
 
+// GGML_OP_MUL_MAT_ID (src/crispembed.cpp:1365,1371): E experts [K, N] of `type` in one 3-D
+// weight, activations X [K, nb1, T] (nb1 = 1: every slot reads its token's row), routing ids
+// [n_used, T] as a view of a [E, T] tensor (the shape ggml_top_k leaves: the first n_used of
+// each token's sorted expert list).  Checked against the oracle row by row; also the 3-D
+// weight's GGUF-byte readback and a write spanning two experts.
+static void run_case_id(ggml_backend_t be, ggml_type type, int64_t K, int64_t N, int64_t E, int64_t n_used,
+                        int64_t T, bool bcast, Result &res) {
+    ggml_init_params ip = {ggml_tensor_overhead() * 8 + ggml_graph_overhead(), nullptr, true};
+    ggml_context *ctx = ggml_init(ip);
+    const int64_t nb1 = bcast ? 1 : n_used;
+    ggml_tensor *W = ggml_new_tensor_3d(ctx, type, K, N, E);
+    ggml_tensor *X = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, K, nb1, T);
+    ggml_tensor *I = ggml_new_tensor_2d(ctx, GGML_TYPE_I32, E, T);
+    ggml_tensor *ids = ggml_view_2d(ctx, I, n_used, T, I->nb[1], 0);
+    ggml_tensor *Y = ggml_mul_mat_id(ctx, W, X, ids);
+    if (!ggml_backend_supports_op(be, Y)) {
+        std::fprintf(stderr, "mul_mat_id %s: supports_op refused\n", ggml_type_name(type));
+        res.supports = false;
+        ggml_free(ctx);
+        return;
+    }
+    ggml_backend_buffer_t buf = ggml_backend_alloc_ctx_tensors(ctx, be);
+    if (!buf) {
+        res.computed = false;
+        ggml_free(ctx);
+        return;
+    }
+    const size_t rs = or_row_size((int)type, K);
+    std::vector<float> wf = normal((size_t)(E * N * K), 0.02);
+    std::vector<uint8_t> wq(rs * N * E);
+    or_quantize_chunk((int)type, wf.data(), wq.data(), N * E, K);
+    ggml_backend_tensor_set(W, wq.data(), 0, wq.size());
+    std::vector<float> x = normal((size_t)(K * nb1 * T), 1.0);
+    ggml_backend_tensor_set(X, x.data(), 0, x.size() * 4);
+    std::vector<int32_t> route((size_t)(E * T));
+    for (int64_t t = 0; t < T; t++) {  // a permutation of the experts per token
+        for (int64_t e = 0; e < E; e++) route[t * E + e] = (int32_t)e;
+        for (int64_t e = E - 1; e > 0; e--) std::swap(route[t * E + e], route[t * E + (int64_t)(uniform01() * (e + 1)) % (e + 1)]);
+    }
+    ggml_backend_tensor_set(I, route.data(), 0, route.size() * 4);
+    ggml_cgraph *gf = ggml_new_graph(ctx);
+    ggml_build_forward_expand(gf, Y);
+    auto check = [&](bool &flag) {
+        if (ggml_backend_graph_compute(be, gf) != GGML_STATUS_SUCCESS) {
+            res.computed = false;
+            return;
+        }
+        std::vector<float> y((size_t)(N * n_used * T)), yref(y.size());
+        ggml_backend_tensor_get(Y, y.data(), 0, y.size() * 4);
+        for (int64_t t = 0; t < T; t++)
+            for (int64_t i = 0; i < n_used; i++) {
+                const int32_t e = route[t * E + i];
+                or_mul_mat((int)type, wq.data() + (size_t)e * N * rs, N, K, x.data() + (t * nb1 + i % nb1) * K, K, 1,
+                           yref.data() + (t * n_used + i) * N, N, 1, OR_Q8_0_X86);
+            }
+        const double err = rel_err(y, yref);
+        res.max_err = std::fmax(res.max_err, err);
+        res.cases++;
+        if (!(err <= 1e-4)) {
+            flag = false;
+            std::fprintf(stderr, "mul_mat_id %s K=%lld N=%lld E=%lld used=%lld T=%lld: rel err %.3g\n",
+                         ggml_type_name(type), (long long)K, (long long)N, (long long)E, (long long)n_used, (long long)T,
+                         err);
+        }
+    };
+    bool ok = true;
+    check(ok);
+    std::vector<uint8_t> back(wq.size());
+    ggml_backend_tensor_get(W, back.data(), 0, back.size());
+    if (back != wq) {
+        res.roundtrip = false;
+        ok = false;
+    }
+    // rows N-3 .. N+2: the last rows of expert 0 and the first of expert 1
+    std::vector<float> wf2 = normal((size_t)(6 * K), 0.03);
+    std::vector<uint8_t> rows(rs * 6);
+    or_quantize_chunk((int)type, wf2.data(), rows.data(), 6, K);
+    ggml_backend_tensor_set(W, rows.data(), (N - 3) * rs, rows.size());
+    std::memcpy(wq.data() + (N - 3) * rs, rows.data(), rows.size());
+    check(ok);
+    res.moe = res.moe && ok;
+    ggml_backend_buffer_free(buf);
+    ggml_free(ctx);
+}
+
 int main(int argc, char **argv) {
     const char *requested = "MI355X";
     bool json = false;
@@ -163,6 +249,11 @@ int main(int argc, char **argv) {
         for (int64_t M : {1, 4, 8, 77, 300}) run_case(be, t, K, 96, M, 1, res);
         run_case(be, t, K, 40, 7, 3, res);  // batched activations [K, 7, 3]
     }
+    // mixture of experts: 8 experts, top-2, both activation layouts, GEMV- and GEMM-sized groups
+    run_case_id(be, GGML_TYPE_Q8_0, 256, 96, 8, 2, 40, true, res);
+    run_case_id(be, GGML_TYPE_Q4_K, 512, 64, 8, 2, 300, false, res);
+    run_case_id(be, GGML_TYPE_Q6_K, 256, 40, 4, 3, 7, true, res);
+    run_case_id(be, GGML_TYPE_F16, 128, 72, 6, 2, 90, false, res);
     // supports_op must refuse what the kernels do not handle (CPU fallback)
     {
         ggml_init_params ip = {ggml_tensor_overhead() * 16 + ggml_graph_overhead(), nullptr, true};
@@ -185,16 +276,16 @@ int main(int argc, char **argv) {
         if (ggml_backend_supports_op(be, ggml_unary(ctx, x64, GGML_UNARY_OP_TANH))) res.supports = false;
         ggml_free(ctx);
     }
-    const bool correct = res.computed && res.roundtrip && res.partial && res.batched && res.supports &&
+    const bool correct = res.computed && res.roundtrip && res.partial && res.batched && res.supports && res.moe &&
                          res.cases > 0 && res.max_err <= 1e-4;
     if (json)
         std::printf("{\"requested\":\"%s\",\"name\":\"%s\",\"description\":\"%s\",\"type\":%d,\"cases\":%d,"
                     "\"max_rel_err\":%.3g,\"roundtrip_ok\":%s,\"partial_write_ok\":%s,\"batched_ok\":%s,"
-                    "\"supports_op_ok\":%s,\"computed\":%s,\"correct\":%s}\n",
+                    "\"supports_op_ok\":%s,\"moe_ok\":%s,\"computed\":%s,\"correct\":%s}\n",
                     requested, ggml_backend_dev_name(dev), ggml_backend_dev_description(dev),
                     (int)ggml_backend_dev_type(dev), res.cases, res.max_err, res.roundtrip ? "true" : "false",
                     res.partial ? "true" : "false", res.batched ? "true" : "false", res.supports ? "true" : "false",
-                    res.computed ? "true" : "false", correct ? "true" : "false");
+                    res.moe ? "true" : "false", res.computed ? "true" : "false", correct ? "true" : "false");
     else
         std::printf("backend-mi355 name=%s cases=%d max_rel_err=%.3g correct=%d\n", ggml_backend_dev_name(dev),
                     res.cases, res.max_err, correct ? 1 : 0);

@@ -1,6 +1,7 @@
 """The ggml backend end to end on the GPU: registry lookup by name, buffer
 allocation, GGUF upload, graph_compute of MUL_MAT nodes (GEMV and GEMM sizes,
-batched activations), tensor_get round trip, partial weight writes and the
+batched activations), MUL_MAT_ID on 3-D expert weights (routing views, broadcast and per-slot
+activations), tensor_get round trips, partial weight writes (one spanning two experts) and the
 supports_op contract, all checked against the CPU oracle by the native driver."""
 import json
 import os
@@ -20,6 +21,6 @@ def test_backend_driver_json():
     assert out["name"].startswith("MI355X")
     assert out["cases"] >= 24
     assert out["max_rel_err"] <= 1e-4
-    for k in ("roundtrip_ok", "partial_write_ok", "batched_ok", "supports_op_ok", "computed", "correct"):
+    for k in ("roundtrip_ok", "partial_write_ok", "batched_ok", "supports_op_ok", "moe_ok", "computed", "correct"):
         assert out[k] is True, k
     assert r.returncode == 0
