@@ -4,8 +4,9 @@
 // quantized weights (mq.h) and the other ops of the encoder graph
 // (src/crispembed.cpp:1043-1468) through mq_ops.h: GET_ROWS, ADD / SUB / MUL / DIV,
 // NORM / RMS_NORM, UNARY (GELU_ERF, GELU, SILU, RELU), CPY / CONT / DUP, ROPE
-// (ggml_rope_ext, normal and NEOX), FLASH_ATTN_EXT and MUL_MAT_ID (mixture-of-experts on
-// 3-D expert weights), plus the metadata-only view ops.  Anything else is refused by
+// (ggml_rope_ext, normal and NEOX), FLASH_ATTN_EXT, MUL_MAT_ID (mixture-of-experts on 3-D
+// expert weights), SOFT_MAX, ARGSORT, REPEAT and MUL_MAT with an F32 first operand (the MoE
+// block's router and expert mix), plus the metadata-only view ops.  Anything else is refused by
 // supports_op, and ggml_backend_sched keeps it on the CPU backend, which is how
 // CrispEmbed already falls back for ops a GPU backend rejects (src/crispembed.cpp:700-723).
 //
@@ -476,6 +477,7 @@ int try_fuse_norm(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status
 // a MUL_MAT whose activation and result rows can be walked as one matrix
 bool flat_mul_mat(const ggml_tensor *mm) {
     const ggml_tensor *x = mm->src[1];
+    if (mq_type_of(mm->src[0]->type) < 0) return false;  // F32 weights: the small-product op
     return x->type == GGML_TYPE_F32 && x->nb[0] == sizeof(float) && x->nb[1] % sizeof(float) == 0 && rows_flat(x) &&
            rows_flat(mm) && mm->nb[0] == sizeof(float) && mm->nb[1] % sizeof(float) == 0;
 }
@@ -604,7 +606,12 @@ int try_group_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, std::vector<
 
 enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node) {
     switch (node->op) {
-        case GGML_OP_MUL_MAT: return mul_mat(c, node);
+        case GGML_OP_MUL_MAT:
+            if (node->src[0]->type == GGML_TYPE_F32) {  // the small F32 products (router, expert mix)
+                const mq_view a = view_of(node->src[0]), b = view_of(node->src[1]), d = view_of(node);
+                return op_status(mq_op_mul_mat_f32(&a, &b, &d, c->stream), node);
+            }
+            return mul_mat(c, node);
         case GGML_OP_GET_ROWS: {
             const mq_view a = view_of(node->src[0]), b = view_of(node->src[1]), d = view_of(node);
             return op_status(mq_op_get_rows(&a, &b, &d, c->stream), node);
@@ -633,6 +640,22 @@ enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node) {
             // CPY writes into its second source (the result is a view of it)
             const mq_view s = view_of(node->src[0]), d = view_of(node->op == GGML_OP_CPY ? node->src[1] : node);
             return op_status(mq_op_cpy(&s, &d, c->stream), node);
+        }
+        case GGML_OP_SOFT_MAX: {
+            const mq_view x = view_of(node->src[0]), d = view_of(node);
+            mq_view m{};
+            if (node->src[1]) m = view_of(node->src[1]);
+            return op_status(mq_op_soft_max(&x, node->src[1] ? &m : nullptr, &d, op_param_f32(node, 0), c->stream), node);
+        }
+        case GGML_OP_ARGSORT: {
+            const mq_view x = view_of(node->src[0]), d = view_of(node);
+            return op_status(mq_op_argsort(&x, &d, node->op_params[0] == GGML_SORT_ORDER_DESC ? MQ_SORT_DESC : MQ_SORT_ASC,
+                                           c->stream),
+                             node);
+        }
+        case GGML_OP_REPEAT: {
+            const mq_view x = view_of(node->src[0]), d = view_of(node);
+            return op_status(mq_op_repeat(&x, &d, c->stream), node);
         }
         case GGML_OP_MUL_MAT_ID: {
             const ggml_tensor *as = node->src[0];
@@ -877,7 +900,18 @@ bool dev_supports_op(ggml_backend_dev_t d, const ggml_tensor *op) {
         }
     if (dst.type < 0) return false;
     switch (op->op) {
-        case GGML_OP_MUL_MAT: return supports_mul_mat(d, op);
+        case GGML_OP_MUL_MAT:
+            if (op->src[0] && op->src[0]->type == GGML_TYPE_F32)
+                return mq_op_supported(MQ_OP_MUL_MAT_F32, 0, p[0], p[1], nullptr, nullptr, &dst);
+            return supports_mul_mat(d, op);
+        case GGML_OP_SOFT_MAX:
+            // no ALiBi slopes, no attention sinks
+            if (op_param_f32(op, 1) != 0.0f || op->src[2]) return false;
+            return mq_op_supported(MQ_OP_SOFT_MAX, 0, p[0], p[1], nullptr, nullptr, &dst);
+        case GGML_OP_ARGSORT:
+            return mq_op_supported(MQ_OP_ARGSORT, op->op_params[0] == GGML_SORT_ORDER_DESC ? MQ_SORT_DESC : MQ_SORT_ASC,
+                                   p[0], nullptr, nullptr, nullptr, &dst);
+        case GGML_OP_REPEAT: return mq_op_supported(MQ_OP_REPEAT, 0, p[0], nullptr, nullptr, nullptr, &dst);
         case GGML_OP_GET_ROWS:
             // a weight table must be in this device's memory (the GGUF bytes at its start)
             return in_this_device(d, op->src[0]) && mq_op_supported(MQ_OP_GET_ROWS, 0, p[0], p[1], nullptr, nullptr, &dst);

@@ -77,7 +77,14 @@ enum ggml_op {
     GGML_OP_ROPE,
     GGML_OP_FLASH_ATTN_EXT,
     GGML_OP_UNARY,
+    GGML_OP_ARGSORT,
+    GGML_OP_REPEAT,
     GGML_OP_COUNT,
+};
+
+enum ggml_sort_order {
+    GGML_SORT_ORDER_ASC,
+    GGML_SORT_ORDER_DESC,
 };
 
 enum ggml_unary_op {
@@ -198,6 +205,15 @@ GGML_API struct ggml_tensor *ggml_flash_attn_ext(struct ggml_context *ctx, struc
                                                 struct ggml_tensor *v, struct ggml_tensor *mask, float scale,
                                                 float max_bias, float logit_softcap);
 GGML_API struct ggml_tensor *ggml_graph_get_tensor(const struct ggml_cgraph *cgraph, const char *name);
+// softmax over ne0 of a * scale + mask (mask NULL or F16/F32); op_params: scale, max_bias
+GGML_API struct ggml_tensor *ggml_soft_max(struct ggml_context *ctx, struct ggml_tensor *a);
+GGML_API struct ggml_tensor *ggml_soft_max_ext(struct ggml_context *ctx, struct ggml_tensor *a,
+                                              struct ggml_tensor *mask, float scale, float max_bias);
+// I32 indices sorting each row; op_params[0] = order.  top_k: the first k columns, descending
+GGML_API struct ggml_tensor *ggml_argsort(struct ggml_context *ctx, struct ggml_tensor *a, enum ggml_sort_order order);
+GGML_API struct ggml_tensor *ggml_top_k(struct ggml_context *ctx, struct ggml_tensor *a, int k);
+// a tiled to b's shape
+GGML_API struct ggml_tensor *ggml_repeat(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b);
 #define GGML_ROPE_TYPE_NEOX 2
 // a [n_dims.., n_head, T, B], b I32 positions [T], c freq factors or NULL; op_params:
 // 0, n_dims, mode, 0, n_ctx_orig, then floats freq_base, freq_scale, ext_factor, attn_factor,

@@ -81,6 +81,8 @@ extern "C" const char *ggml_op_name(enum ggml_op op) {
         case GGML_OP_ROPE: return "ROPE";
         case GGML_OP_FLASH_ATTN_EXT: return "FLASH_ATTN_EXT";
         case GGML_OP_UNARY: return "UNARY";
+        case GGML_OP_ARGSORT: return "ARGSORT";
+        case GGML_OP_REPEAT: return "REPEAT";
         default: return "OP";
     }
 }
@@ -392,6 +394,42 @@ extern "C" struct ggml_tensor *ggml_relu(struct ggml_context *ctx, struct ggml_t
 }
 extern "C" enum ggml_unary_op ggml_get_unary_op(const struct ggml_tensor *t) {
     return (enum ggml_unary_op)t->op_params[0];
+}
+
+extern "C" struct ggml_tensor *ggml_soft_max_ext(struct ggml_context *ctx, struct ggml_tensor *a,
+                                                 struct ggml_tensor *mask, float scale, float max_bias) {
+    ggml_tensor *r = new_tensor(ctx, a->type, 4, a->ne);
+    r->op = GGML_OP_SOFT_MAX;
+    const float p[2] = {scale, max_bias};
+    std::memcpy(r->op_params, p, sizeof(p));
+    r->src[0] = a;
+    r->src[1] = mask;
+    return r;
+}
+extern "C" struct ggml_tensor *ggml_soft_max(struct ggml_context *ctx, struct ggml_tensor *a) {
+    return ggml_soft_max_ext(ctx, a, nullptr, 1.0f, 0.0f);
+}
+
+extern "C" struct ggml_tensor *ggml_argsort(struct ggml_context *ctx, struct ggml_tensor *a,
+                                            enum ggml_sort_order order) {
+    ggml_tensor *r = new_tensor(ctx, GGML_TYPE_I32, 4, a->ne);
+    r->op = GGML_OP_ARGSORT;
+    r->op_params[0] = (int32_t)order;
+    r->src[0] = a;
+    return r;
+}
+
+extern "C" struct ggml_tensor *ggml_top_k(struct ggml_context *ctx, struct ggml_tensor *a, int k) {
+    ggml_tensor *s = ggml_argsort(ctx, a, GGML_SORT_ORDER_DESC);
+    const int64_t ne[4] = {k, s->ne[1], s->ne[2], s->ne[3]};
+    return view_of(ctx, s, ne, s->nb, 0, GGML_OP_VIEW);
+}
+
+extern "C" struct ggml_tensor *ggml_repeat(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b) {
+    ggml_tensor *r = new_tensor(ctx, a->type, 4, b->ne);
+    r->op = GGML_OP_REPEAT;
+    r->src[0] = a;
+    return r;
 }
 
 extern "C" struct ggml_tensor *ggml_rope_ext(struct ggml_context *ctx, struct ggml_tensor *a, struct ggml_tensor *b,

@@ -307,6 +307,86 @@ __global__ __launch_bounds__(256) void k_scatter_rows(const float *__restrict__ 
     for (int64_t c = threadIdx.x; c < n; c += 256) d[c] = s[c];
 }
 
+// Softmax over ne0, one wave per row (values re-read from memory; rows are short here).
+template <int MT>  // mask element type: 0 none, 1 F16, 2 F32
+__global__ __launch_bounds__(256) void k_soft_max(const DV x, const DV m, const DV d, float scale, int64_t nrows) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+    if (row >= nrows) return;
+    const int64_t n = x.ne[0];
+    const int64_t i1 = row % x.ne[1], i2 = (row / x.ne[1]) % x.ne[2], i3 = row / (x.ne[1] * x.ne[2]);
+    const float *xr = (const float *)(x.p + off3(x, i1, i2, i3));
+    float *dr = (float *)(d.p + off3(d, i1, i2, i3));
+    const char *mr = MT ? m.p + off3(m, i1, i2 % m.ne[2], i3 % m.ne[3]) : nullptr;
+    auto val = [&](int64_t c) {
+        float v = xr[c] * scale;
+        if constexpr (MT == 1) v += (float)((const _Float16 *)mr)[c];
+        if constexpr (MT == 2) v += ((const float *)mr)[c];
+        return v;
+    };
+    float mx = -INFINITY;
+    for (int64_t c = lane; c < n; c += 64) mx = fmaxf(mx, val(c));
+    mx = wave_max_f(mx);
+    if (mx == -INFINITY) {  // every entry masked
+        for (int64_t c = lane; c < n; c += 64) dr[c] = 0.f;
+        return;
+    }
+    float sum = 0.f;
+    for (int64_t c = lane; c < n; c += 64) {
+        const float e = expf(val(c) - mx);
+        dr[c] = e;
+        sum += e;
+    }
+    const float inv = 1.0f / wave_sum_f(sum);
+    for (int64_t c = lane; c < n; c += 64) dr[c] *= inv;
+}
+
+// Stable argsort of one row per workgroup: element i's rank is the number of elements that
+// come before it (larger, or equal at a lower index, for descending order).
+template <bool DESC>
+__global__ __launch_bounds__(256) void k_argsort(const DV x, const DV d, int64_t nrows) {
+    __shared__ float v[1024];
+    const int64_t row = blockIdx.x;
+    const int n = (int)x.ne[0];
+    const int64_t i1 = row % x.ne[1], i2 = (row / x.ne[1]) % x.ne[2], i3 = row / (x.ne[1] * x.ne[2]);
+    const float *xr = (const float *)(x.p + off3(x, i1, i2, i3));
+    int32_t *dr = (int32_t *)(d.p + off3(d, i1, i2, i3));
+    for (int c = threadIdx.x; c < n; c += 256) v[c] = xr[c];
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float vi = v[i];
+        int rank = 0;
+        for (int j = 0; j < n; j++) {
+            const float vj = v[j];
+            rank += DESC ? (vj > vi || (vj == vi && j < i)) : (vj < vi || (vj == vi && j < i));
+        }
+        dr[rank] = i;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_repeat(const DV s, const DV d, int64_t n) {
+    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < n; u += (int64_t)gridDim.x * 256) {
+        int64_t i0, i1, i2, i3;
+        unflat<1>(u, d.ne, i0, i1, i2, i3);
+        *(float *)(d.p + i0 * d.nb[0] + off3(d, i1, i2, i3)) =
+            *(const float *)(s.p + (i0 % s.ne[0]) * s.nb[0] + off3(s, i1 % s.ne[1], i2 % s.ne[2], i3 % s.ne[3]));
+    }
+}
+
+// One thread per output element, fp32 multiply-adds in k order.
+__global__ __launch_bounds__(256) void k_mul_mat_f32(const DV a, const DV b, const DV d, int64_t n) {
+    const int64_t r2 = b.ne[2] / a.ne[2], r3 = b.ne[3] / a.ne[3];
+    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < n; u += (int64_t)gridDim.x * 256) {
+        int64_t i, j, b2, b3;
+        unflat<1>(u, d.ne, i, j, b2, b3);
+        const char *ar = a.p + i * a.nb[1] + (b2 / r2) * a.nb[2] + (b3 / r3) * a.nb[3];
+        const char *br = b.p + j * b.nb[1] + b2 * b.nb[2] + b3 * b.nb[3];
+        float acc = 0.f;
+        for (int64_t k = 0; k < a.ne[0]; k++) acc += *(const float *)(ar + k * a.nb[0]) * *(const float *)(br + k * b.nb[0]);
+        *(float *)(d.p + i * d.nb[0] + off3(d, j, b2, b3)) = acc;
+    }
+}
+
 // ------------------------------------------------------------------ checks ----
 int64_t nel(const mq_view *v) { return v->ne[0] * v->ne[1] * v->ne[2] * v->ne[3]; }
 
@@ -440,6 +520,47 @@ const char *check_rope(int mode, const mq_view *x, const mq_view *pos, const mq_
     if (pos->ne[0] != x->ne[2] || pos->ne[1] != 1 || pos->ne[2] != 1 || pos->ne[3] != 1) return "rope: pos must be [T]";
     if (ff && (!shape_ok(ff) || ff->type != MQ_TYPE_F32 || ff->nb[0] != 4 || ff->ne[0] < n_dims / 2))
         return "rope: freq_factors must be F32 [n_dims/2]";
+    return nullptr;
+}
+
+const char *check_soft_max(const mq_view *x, const mq_view *m, const mq_view *d) {
+    if (!x || !d || !shape_ok(x) || !shape_ok(d)) return "missing or empty operand";
+    if (x->type != MQ_TYPE_F32 || d->type != MQ_TYPE_F32 || !same_shape(x, d)) return "soft_max: F32 x / dst";
+    if (!rows_dense(x, 4) || !rows_dense(d, 4)) return "soft_max: rows not contiguous";
+    if (m) {
+        if (!shape_ok(m) || (m->type != MQ_TYPE_F16 && m->type != MQ_TYPE_F32) || !rows_dense(m, elem_size(m->type)))
+            return "soft_max: mask must be F16 or F32 rows";
+        if (m->ne[0] != x->ne[0] || m->ne[1] < x->ne[1]) return "soft_max: mask shape";
+        if (x->ne[2] % m->ne[2] || x->ne[3] % m->ne[3]) return "soft_max: mask planes do not broadcast";
+    }
+    return nullptr;
+}
+
+const char *check_argsort(int order, const mq_view *x, const mq_view *d) {
+    if (order != MQ_SORT_ASC && order != MQ_SORT_DESC) return "argsort: order";
+    if (!x || !d || !shape_ok(x) || !shape_ok(d)) return "missing or empty operand";
+    if (x->type != MQ_TYPE_F32 || d->type != MQ_TYPE_I32 || !same_shape(x, d)) return "argsort: F32 x, I32 dst";
+    if (x->ne[0] > 1024) return "argsort: rows of at most 1024";
+    if (!rows_dense(x, 4) || !rows_dense(d, 4)) return "argsort: rows not contiguous";
+    return nullptr;
+}
+
+const char *check_repeat(const mq_view *s, const mq_view *d) {
+    if (!s || !d || !shape_ok(s) || !shape_ok(d)) return "missing or empty operand";
+    if (s->type != MQ_TYPE_F32 || d->type != MQ_TYPE_F32) return "repeat: F32 only";
+    for (int i = 0; i < 4; i++)
+        if (d->ne[i] % s->ne[i]) return "repeat: src does not tile dst";
+    return nullptr;
+}
+
+const char *check_mul_mat_f32(const mq_view *a, const mq_view *b, const mq_view *d) {
+    if (!a || !b || !d || !shape_ok(a) || !shape_ok(b) || !shape_ok(d)) return "missing or empty operand";
+    if (a->type != MQ_TYPE_F32 || b->type != MQ_TYPE_F32 || d->type != MQ_TYPE_F32) return "mul_mat_f32: F32 only";
+    if (a->ne[0] != b->ne[0] || b->ne[2] % a->ne[2] || b->ne[3] % a->ne[3]) return "mul_mat_f32: shapes";
+    if (d->ne[0] != a->ne[1] || d->ne[1] != b->ne[1] || d->ne[2] != b->ne[2] || d->ne[3] != b->ne[3])
+        return "mul_mat_f32: dst shape";
+    if (a->nb[0] % 4 || b->nb[0] % 4 || d->nb[0] % 4) return "mul_mat_f32: misaligned strides";
+    if ((double)nel(d) * (double)a->ne[0] > (double)(1ll << 26)) return "mul_mat_f32: more than 2^26 multiply-adds";
     return nullptr;
 }
 
@@ -693,6 +814,46 @@ extern "C" int mq_op_mul_mat_id(int type, const void *expert_images, size_t expe
     return hip_rc(hipGetLastError(), "mul_mat_id");
 }
 
+extern "C" int mq_op_soft_max(const mq_view *x, const mq_view *mask, const mq_view *dst, float scale, void *stream) {
+    if (const char *e = check_soft_max(x, mask, dst)) return fail(e);
+    if (!have_data({x, mask, dst})) return fail("missing data pointer");
+    const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3];
+    const dim3 g((unsigned)((rows + 3) / 4)), b(256);
+    hipStream_t s = (hipStream_t)stream;
+    DV mv{};
+    if (mask) mv = dv(mask);
+    if (!mask) hipLaunchKernelGGL(k_soft_max<0>, g, b, 0, s, dv(x), mv, dv(dst), scale, rows);
+    else if (mask->type == MQ_TYPE_F16) hipLaunchKernelGGL(k_soft_max<1>, g, b, 0, s, dv(x), mv, dv(dst), scale, rows);
+    else hipLaunchKernelGGL(k_soft_max<2>, g, b, 0, s, dv(x), mv, dv(dst), scale, rows);
+    return hip_rc(hipGetLastError(), "soft_max");
+}
+
+extern "C" int mq_op_argsort(const mq_view *x, const mq_view *dst, int order, void *stream) {
+    if (const char *e = check_argsort(order, x, dst)) return fail(e);
+    if (!have_data({x, dst})) return fail("missing data pointer");
+    const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3];
+    hipStream_t s = (hipStream_t)stream;
+    if (order == MQ_SORT_DESC) hipLaunchKernelGGL(k_argsort<true>, dim3((unsigned)rows), dim3(256), 0, s, dv(x), dv(dst), rows);
+    else hipLaunchKernelGGL(k_argsort<false>, dim3((unsigned)rows), dim3(256), 0, s, dv(x), dv(dst), rows);
+    return hip_rc(hipGetLastError(), "argsort");
+}
+
+extern "C" int mq_op_repeat(const mq_view *src, const mq_view *dst, void *stream) {
+    if (const char *e = check_repeat(src, dst)) return fail(e);
+    if (!have_data({src, dst})) return fail("missing data pointer");
+    const int64_t n = nel(dst);
+    hipLaunchKernelGGL(k_repeat, dim3(grid_units(n)), dim3(256), 0, (hipStream_t)stream, dv(src), dv(dst), n);
+    return hip_rc(hipGetLastError(), "repeat");
+}
+
+extern "C" int mq_op_mul_mat_f32(const mq_view *a, const mq_view *b, const mq_view *dst, void *stream) {
+    if (const char *e = check_mul_mat_f32(a, b, dst)) return fail(e);
+    if (!have_data({a, b, dst})) return fail("missing data pointer");
+    const int64_t n = nel(dst);
+    hipLaunchKernelGGL(k_mul_mat_f32, dim3(grid_units(n)), dim3(256), 0, (hipStream_t)stream, dv(a), dv(b), dv(dst), n);
+    return hip_rc(hipGetLastError(), "mul_mat_f32");
+}
+
 extern "C" size_t mq_op_flash_attn_workspace_bytes(const mq_view *k) {
     if (!k || (k->ne[0] != 32 && k->ne[0] != 64 && k->ne[0] != 128) || k->ne[1] < 1 || k->ne[2] < 1 || k->ne[3] < 1)
         return 0;
@@ -739,6 +900,10 @@ extern "C" int mq_op_supported(int op, int sub, const mq_view *s0, const mq_view
         case MQ_OP_CPY: e = check_cpy(s0, dst); break;
         case MQ_OP_FLASH_ATTN: e = check_flash(s0, s1, s2, s3, dst); break;
         case MQ_OP_ROPE: e = s0 ? check_rope(sub, s0, s1, s2, dst, (int)s0->ne[0]) : "missing or empty operand"; break;
+        case MQ_OP_SOFT_MAX: e = check_soft_max(s0, s1, dst); break;
+        case MQ_OP_ARGSORT: e = check_argsort(sub, s0, dst); break;
+        case MQ_OP_REPEAT: e = check_repeat(s0, dst); break;
+        case MQ_OP_MUL_MAT_F32: e = check_mul_mat_f32(s0, s1, dst); break;
         default: break;
     }
     return e == nullptr;

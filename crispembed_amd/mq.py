@@ -15,6 +15,7 @@ UNARY_GELU_ERF, UNARY_GELU, UNARY_SILU, UNARY_RELU = 0, 1, 2, 3
 NORM_LAYER, NORM_RMS = 0, 1
 OP_GET_ROWS, OP_BINARY, OP_UNARY, OP_NORM, OP_CPY, OP_FLASH_ATTN, OP_ROPE = 0, 1, 2, 3, 4, 5, 6
 ROPE_NORMAL, ROPE_NEOX = 0, 2
+SORT_ASC, SORT_DESC = 0, 1
 
 TYPE_NAMES = {TYPE_F32: "f32", TYPE_F16: "f16", TYPE_Q8_0: "q8_0", TYPE_Q4_K: "q4_K",
               TYPE_Q6_K: "q6_K", TYPE_Q8_K: "q8_K"}
@@ -152,6 +153,10 @@ _SIGS.update({
     "mq_op_flash_attn_workspace_bytes": (_c_sz, [_PV]),
     "mq_op_flash_attn": (_c_int, [_PV, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_sz, _c_vp]),
     "mq_op_supported": (_c_int, [_c_int, _c_int, _PV, _PV, _PV, _PV, _PV]),
+    "mq_op_soft_max": (_c_int, [_PV, _PV, _PV, ctypes.c_float, _c_vp]),
+    "mq_op_argsort": (_c_int, [_PV, _PV, _c_int, _c_vp]),
+    "mq_op_repeat": (_c_int, [_PV, _PV, _c_vp]),
+    "mq_op_mul_mat_f32": (_c_int, [_PV, _PV, _PV, _c_vp]),
     "mq_op_rope": (_c_int, [_PV, _PV, _PV, _PV, _c_int, _c_int, _c_int] + [ctypes.c_float] * 6 + [_c_vp]),
 })
 

@@ -14,6 +14,9 @@
  *   ggml_flash_attn_ext  (src/crispembed.cpp:1293)            mq_op_flash_attn
  *   ggml_rope_ext        (src/decoder_embed.cpp:756-759)      mq_op_rope
  *   ggml_mul_mat_id      (src/crispembed.cpp:1365,1371)       mq_op_mul_mat_id
+ *   ggml_soft_max, ggml_top_k (argsort), ggml_repeat, F32 ggml_mul_mat: the rest of the MoE
+ *   FFN block (src/crispembed.cpp:1327-1382)                  mq_op_soft_max, _argsort, _repeat,
+ *                                                             _mul_mat_f32
  * The semantics (shapes, broadcasting, op_params) are ggml's, as its CPU backend computes them
  * (ggml-cpu ops.cpp, the ggml submodule pinned in .gitmodules): the ggml backend passes each
  * node's tensors straight through.
@@ -129,6 +132,30 @@ int mq_op_mul_mat_id(int type, const void *expert_images, size_t expert_stride, 
                      const mq_view *b, const mq_view *ids, const mq_view *dst, void *workspace, size_t workspace_bytes,
                      void *stream);
 
+/* ggml_soft_max_ext without ALiBi (src/crispembed.cpp:1267,1336): dst = softmax over ne0 of
+ * x * scale + mask, mask NULL or F16/F32 [ne0, >= ne1, ...] (row i1 of x uses mask row i1; mask
+ * planes broadcast over x's by index modulo), -inf entries masked; a row with every entry
+ * masked gives zeros.  F32 x and dst, rows contiguous. */
+int mq_op_soft_max(const mq_view *x, const mq_view *mask, const mq_view *dst, float scale, void *stream);
+
+/* ggml_argsort (ggml_top_k takes its first k columns, src/crispembed.cpp:1339): dst I32 row =
+ * the indices of x's F32 row in descending (MQ_SORT_DESC) or ascending order, equal values in
+ * index order (a stable sort).  ne0 <= 1024. */
+#define MQ_SORT_ASC 0
+#define MQ_SORT_DESC 1
+int mq_op_argsort(const mq_view *x, const mq_view *dst, int order, void *stream);
+
+/* ggml_repeat (src/crispembed.cpp:1361): dst[i0, i1, i2, i3] = src[i0 % ne0, i1 % ne1, ...];
+ * every extent of src divides dst's.  F32. */
+int mq_op_repeat(const mq_view *src, const mq_view *dst, void *stream);
+
+/* GGML_OP_MUL_MAT with an F32 first operand, for the small products of the graphs (the MoE
+ * router and its weighted sum over experts, src/crispembed.cpp:1333,1378):
+ * dst[i, j, b2, b3] = sum_k a[k, i, b2 / (ne12/ne02), b3 / (ne13/ne03)] * b[k, j, b2, b3] in
+ * fp32 (a's batches broadcast as ggml does).  One thread per output: meant for outputs with at
+ * most 2^26 multiply-adds. */
+int mq_op_mul_mat_f32(const mq_view *a, const mq_view *b, const mq_view *dst, void *stream);
+
 /* ids for mq_op_supported */
 #define MQ_OP_GET_ROWS 0
 #define MQ_OP_BINARY 1
@@ -137,6 +164,10 @@ int mq_op_mul_mat_id(int type, const void *expert_images, size_t expert_stride, 
 #define MQ_OP_CPY 4
 #define MQ_OP_FLASH_ATTN 5
 #define MQ_OP_ROPE 6 /* sub = mode; src0 x, src1 pos, src2 freq_factors; n_dims = x.ne0 assumed */
+#define MQ_OP_SOFT_MAX 7  /* src0 x, src1 mask */
+#define MQ_OP_ARGSORT 8   /* sub = order */
+#define MQ_OP_REPEAT 9
+#define MQ_OP_MUL_MAT_F32 10 /* src0 a, src1 b */
 
 /* 1 when mq_op_<op> accepts these operands (srcs in the op's argument order, NULL where an
  * optional operand is absent -- for MQ_OP_NORM src1 is `add`; `sub` is the binary / unary /

@@ -226,6 +226,105 @@ static void run_case_id(ggml_backend_t be, ggml_type type, int64_t K, int64_t N,
     ggml_free(ctx);
 }
 
+// The MoE FFN block exactly as build_encoder_graph builds it for Nomic-v2-style encoders
+// (src/crispembed.cpp:1327-1382): F32 router MUL_MAT, SOFT_MAX, top-k (ARGSORT + view),
+// GET_ROWS of the selected probabilities, REPEAT of the input over the k slots, MUL_MAT_ID
+// (fc1), GELU_ERF, MUL_MAT_ID (fc2), CONT(PERMUTE), the F32 weighted-sum MUL_MAT and the bias
+// ADD, every node on the backend.  Reference: the same steps on the host with the oracle's
+// mat-muls (activations requantized as ggml does) and fp64 softmax / GELU.
+static void run_moe_block(ggml_backend_t be, ggml_type type, Result &res) {
+    const int64_t H = 256, F = 512, E = 8, KT = 2, TB = 48;
+    ggml_init_params ip = {ggml_tensor_overhead() * 40 + ggml_graph_overhead(), nullptr, true};
+    ggml_context *ctx = ggml_init(ip);
+    ggml_tensor *cur = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, H, TB);
+    ggml_tensor *router = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, H, E);
+    ggml_tensor *fc1 = ggml_new_tensor_3d(ctx, type, H, F, E);
+    ggml_tensor *fc2 = ggml_new_tensor_3d(ctx, type, F, H, E);
+    ggml_tensor *bias = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, H);
+    ggml_tensor *logits = ggml_mul_mat(ctx, router, cur);
+    ggml_tensor *probs = ggml_soft_max(ctx, logits);
+    ggml_tensor *ids = ggml_top_k(ctx, probs, (int)KT);
+    ggml_tensor *top_w = ggml_get_rows(ctx, ggml_reshape_3d(ctx, probs, 1, E, TB), ids);
+    top_w = ggml_reshape_2d(ctx, top_w, KT, TB);
+    ggml_tensor *slots = ggml_repeat(ctx, ggml_reshape_3d(ctx, cur, H, 1, TB), ggml_new_tensor_3d(ctx, GGML_TYPE_F32, H, KT, TB));
+    ggml_tensor *up = ggml_gelu_erf(ctx, ggml_mul_mat_id(ctx, fc1, slots, ids));
+    ggml_tensor *down = ggml_mul_mat_id(ctx, fc2, up, ids);
+    ggml_tensor *down_p = ggml_cont(ctx, ggml_permute(ctx, down, 1, 0, 2, 3));
+    ggml_tensor *ffn = ggml_mul_mat(ctx, ggml_reshape_3d(ctx, top_w, KT, 1, TB), down_p);
+    ffn = ggml_add(ctx, ggml_reshape_2d(ctx, ffn, H, TB), bias);
+    ggml_set_output(ffn);
+    ggml_cgraph *gf = ggml_new_graph(ctx);
+    ggml_build_forward_expand(gf, ffn);
+    for (int i = 0; i < ggml_graph_n_nodes(gf); i++)
+        if (!ggml_backend_supports_op(be, ggml_graph_node(gf, i))) {
+            std::fprintf(stderr, "moe block: %s refused\n", ggml_op_name(ggml_graph_node(gf, i)->op));
+            res.supports = res.moe = false;
+        }
+    ggml_backend_buffer_t buf = ggml_backend_alloc_ctx_tensors(ctx, be);
+    if (!buf) {
+        res.computed = false;
+        ggml_free(ctx);
+        return;
+    }
+    std::vector<float> x = normal((size_t)(H * TB), 1.0), rw = normal((size_t)(H * E), 0.2), bv = normal((size_t)H, 0.1);
+    const size_t rs1 = or_row_size((int)type, H), rs2 = or_row_size((int)type, F);
+    std::vector<float> w1f = normal((size_t)(E * F * H), 0.05), w2f = normal((size_t)(E * H * F), 0.05);
+    std::vector<uint8_t> w1(rs1 * F * E), w2(rs2 * H * E);
+    or_quantize_chunk((int)type, w1f.data(), w1.data(), F * E, H);
+    or_quantize_chunk((int)type, w2f.data(), w2.data(), H * E, F);
+    ggml_backend_tensor_set(cur, x.data(), 0, x.size() * 4);
+    ggml_backend_tensor_set(router, rw.data(), 0, rw.size() * 4);
+    ggml_backend_tensor_set(fc1, w1.data(), 0, w1.size());
+    ggml_backend_tensor_set(fc2, w2.data(), 0, w2.size());
+    ggml_backend_tensor_set(bias, bv.data(), 0, bv.size() * 4);
+    if (ggml_backend_graph_compute(be, gf) != GGML_STATUS_SUCCESS) {
+        res.computed = res.moe = false;
+        ggml_backend_buffer_free(buf);
+        ggml_free(ctx);
+        return;
+    }
+    std::vector<float> y((size_t)(H * TB));
+    ggml_backend_tensor_get(ffn, y.data(), 0, y.size() * 4);
+    std::vector<float> yref(y.size());
+    for (int64_t t = 0; t < TB; t++) {
+        const float *xt = x.data() + t * H;
+        std::vector<double> p(E);
+        double mx = -1e300, sum = 0;
+        for (int64_t e = 0; e < E; e++) {
+            float acc = 0.f;  // the F32 router product in fp32, k order
+            for (int64_t h = 0; h < H; h++) acc += rw[e * H + h] * xt[h];
+            p[e] = acc;
+            mx = std::fmax(mx, p[e]);
+        }
+        for (auto &v : p) sum += (v = std::exp(v - mx));
+        std::vector<int> ord(E);
+        for (int e = 0; e < E; e++) ord[e] = e;
+        std::stable_sort(ord.begin(), ord.end(), [&](int a, int b) { return p[a] > p[b]; });
+        for (int64_t h = 0; h < H; h++) yref[t * H + h] = bv[h];
+        std::vector<double> acc(H, 0.0);
+        for (int64_t i = 0; i < KT; i++) {
+            const int e = ord[i];
+            std::vector<float> u(F), dn(H);
+            or_mul_mat((int)type, w1.data() + (size_t)e * F * rs1, F, H, xt, H, 1, u.data(), F, 1, OR_Q8_0_X86);
+            for (auto &v : u) v = (float)(0.5 * v * (1.0 + std::erf(v / std::sqrt(2.0))));
+            or_mul_mat((int)type, w2.data() + (size_t)e * H * rs2, H, F, u.data(), F, 1, dn.data(), H, 1, OR_Q8_0_X86);
+            for (int64_t h = 0; h < H; h++) acc[h] += (p[e] / sum) * dn[h];
+        }
+        for (int64_t h = 0; h < H; h++) yref[t * H + h] = (float)(acc[h] + bv[h]);
+    }
+    const double err = rel_err(y, yref);
+    res.cases++;
+    // the bar of the GELU prologue: device erff vs the host's erf may move a requantized fc2
+    // input by one step near a rounding boundary
+    if (!(err <= 1e-3)) {
+        res.moe = false;
+        std::fprintf(stderr, "moe block %s: rel err %.3g\n", ggml_type_name(type), err);
+    }
+    std::fprintf(stderr, "moe block %s: rel err %.3g\n", ggml_type_name(type), err);
+    ggml_backend_buffer_free(buf);
+    ggml_free(ctx);
+}
+
 int main(int argc, char **argv) {
     const char *requested = "MI355X";
     bool json = false;
@@ -254,6 +353,8 @@ int main(int argc, char **argv) {
     run_case_id(be, GGML_TYPE_Q4_K, 512, 64, 8, 2, 300, false, res);
     run_case_id(be, GGML_TYPE_Q6_K, 256, 40, 4, 3, 7, true, res);
     run_case_id(be, GGML_TYPE_F16, 128, 72, 6, 2, 90, false, res);
+    run_moe_block(be, GGML_TYPE_Q8_0, res);
+    run_moe_block(be, GGML_TYPE_Q4_K, res);
     // supports_op must refuse what the kernels do not handle (CPU fallback)
     {
         ggml_init_params ip = {ggml_tensor_overhead() * 16 + ggml_graph_overhead(), nullptr, true};
@@ -264,7 +365,11 @@ int main(int argc, char **argv) {
         ggml_tensor *x64 = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 64, 3);
         ggml_tensor *x48 = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 48, 3);
         ggml_tensor *xh = ggml_new_tensor_2d(ctx, GGML_TYPE_F16, 256, 3);
-        if (ggml_backend_supports_op(be, ggml_mul_mat(ctx, wf32, x64))) res.supports = false;
+        // F32 weights: the small products are claimed, large ones stay on the CPU
+        if (!ggml_backend_supports_op(be, ggml_mul_mat(ctx, wf32, x64))) res.supports = false;
+        ggml_tensor *wbig = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 4096, 4096);
+        ggml_tensor *xbig = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 4096, 8);
+        if (ggml_backend_supports_op(be, ggml_mul_mat(ctx, wbig, xbig))) res.supports = false;
         if (ggml_backend_supports_op(be, ggml_mul_mat(ctx, wf16, x48))) res.supports = false;
         if (ggml_backend_supports_op(be, ggml_mul_mat(ctx, wq, xh))) res.supports = false;
         // the encoder's elementwise ops are claimed for F32, refused for F16 operands or

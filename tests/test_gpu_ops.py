@@ -23,8 +23,19 @@ def _t():
     return torch
 
 
+_KEEP = []  # an mq_view holds only the address: the tensors behind views live until the test ends
+
+
+@pytest.fixture(autouse=True)
+def _release_tensors():
+    yield
+    _KEEP.clear()
+
+
 def _cuda(a):
-    return _t().from_numpy(np.ascontiguousarray(a)).cuda()
+    t = _t().from_numpy(np.ascontiguousarray(a)).cuda()
+    _KEEP.append(t)
+    return t
 
 
 def _rng(seed):
@@ -412,3 +423,69 @@ def test_flash_attn_causal_mask_one_sequence(attn_form, hd):
     assert np.abs(got - ref).max() / np.abs(ref).max() <= 2e-5
     # closed form: the first query sees only its own key, so it returns that value row
     assert np.allclose(got[0, 0], np.repeat(vx[0, 0], nh // nkv, axis=0), atol=1e-6)
+
+
+# ------------------------------------------------------- the MoE block's ops ----
+@pytest.mark.parametrize("mask", [None, "f16", "f32"])
+def test_soft_max(mask):
+    L = mq.lib()
+    rng = _rng(40)
+    x = (rng.standard_normal((3, 17, 70)) * 3).astype(np.float32)
+    m = None
+    ref_in = x.astype(np.float64) * 0.5
+    if mask:
+        mv = (rng.standard_normal((1, 20, 70)) * 2).astype(np.float32)
+        mv[0, 4, :] = -np.inf  # a fully masked row -> zeros
+        mv[0, 6, 10:] = -np.inf
+        m = mv.astype(np.float16 if mask == "f16" else np.float32)
+        ref_in = ref_in + m[:, :17].astype(np.float64)
+    mx = ref_in.max(-1, keepdims=True)
+    e = np.exp(ref_in - np.where(np.isfinite(mx), mx, 0))
+    den = e.sum(-1, keepdims=True)
+    ref = np.where(den > 0, e / np.where(den > 0, den, 1), 0)
+    dx = _cuda(x)
+    out = _t().empty_like(dx)
+    _call(L.mq_op_soft_max, mq.view(dx), mq.view(_cuda(m)) if m is not None else None, mq.view(out), 0.5, stream())
+    got = host(out)
+    assert np.isfinite(got).all() and np.abs(got - ref).max() <= 1e-6
+    if mask:
+        assert not got[:, 4].any()
+
+
+@pytest.mark.parametrize("order", [mq.SORT_DESC, mq.SORT_ASC])
+def test_argsort_stable(order):
+    L = mq.lib()
+    rng = _rng(41)
+    x = rng.standard_normal((40, 37)).astype(np.float32)
+    x[3, 5:9] = 0.25  # ties keep index order
+    x[7] = 1.0
+    dx = _cuda(x)
+    out = _t().empty((40, 37), dtype=_t().int32, device="cuda")
+    _call(L.mq_op_argsort, mq.view(dx), mq.view(out), order, stream())
+    key = -x if order == mq.SORT_DESC else x
+    ref = np.argsort(key, axis=-1, kind="stable").astype(np.int32)
+    assert np.array_equal(host(out), ref)
+
+
+def test_repeat_and_mul_mat_f32():
+    L = mq.lib()
+    rng = _rng(42)
+    a = rng.standard_normal((5, 1, 64)).astype(np.float32)  # ggml [64, 1, 5]
+    out = _t().empty((5, 3, 64), dtype=_t().float32, device="cuda")
+    _call(L.mq_op_repeat, mq.view(_cuda(a)), mq.view(out), stream())
+    assert np.array_equal(host(out), np.repeat(a, 3, axis=1))
+    # the expert mix: [K, 1, T] weights times [K, H, T] expert outputs -> [1, H, T]
+    K, H, T = 2, 96, 11
+    w = rng.standard_normal((T, 1, K)).astype(np.float32)
+    d = rng.standard_normal((T, H, K)).astype(np.float32)
+    y = _t().empty((T, H, 1), dtype=_t().float32, device="cuda")
+    _call(L.mq_op_mul_mat_f32, mq.view(_cuda(w)), mq.view(_cuda(d)), mq.view(y), stream())
+    ref = np.einsum("tik,tjk->tji", w.astype(np.float64), d.astype(np.float64))
+    assert np.abs(host(y) - ref).max() <= 1e-5
+    # a's batches broadcast over b's (router [H, E] on [H, T] is the 2-D case)
+    a2 = rng.standard_normal((2, 8, 33)).astype(np.float32)
+    b2 = rng.standard_normal((6, 10, 33)).astype(np.float32)
+    y2 = _t().empty((6, 10, 8), dtype=_t().float32, device="cuda")
+    _call(L.mq_op_mul_mat_f32, mq.view(_cuda(a2)), mq.view(_cuda(b2)), mq.view(y2), stream())
+    ref2 = np.einsum("bik,bjk->bji", np.repeat(a2, 3, axis=0).astype(np.float64), b2.astype(np.float64))
+    assert np.abs(host(y2) - ref2).max() <= 1e-5
