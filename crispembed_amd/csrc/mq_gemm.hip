@@ -359,9 +359,22 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
             for (int j = 0; j < TN; j++) wb[kc][j] = *(const v4i *)(st + wfrag0 + (j * KC + kc) * 1024);
         }
         static_assert(FMT != FMT_Q8_0 || (KC == 2 && TM <= 2 && TN <= 2), "the wait below names every scale register");
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(dw[0][0]), "+v"(dw[0][TN - 1]), "+v"(dx[0][0]), "+v"(dx[0][TM - 1]), "+v"(dw[1][0]),
-                       "+v"(dw[1][TN - 1]), "+v"(dx[1][0]), "+v"(dx[1][TM - 1]));
+        // each register named once: an operand listed twice is copied (v_mov) before the wait,
+        // i.e. read before its ds_read has landed, and that stale copy is what gets used
+        if constexpr (TM == 2 && TN == 2)
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(dw[0][0]), "+v"(dw[0][TN - 1]), "+v"(dx[0][0]), "+v"(dx[0][TM - 1]), "+v"(dw[1][0]),
+                           "+v"(dw[1][TN - 1]), "+v"(dx[1][0]), "+v"(dx[1][TM - 1]));
+        else if constexpr (TM == 2)
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(dw[0][0]), "+v"(dx[0][0]), "+v"(dx[0][TM - 1]), "+v"(dw[1][0]), "+v"(dx[1][0]),
+                           "+v"(dx[1][TM - 1]));
+        else if constexpr (TN == 2)
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(dw[0][0]), "+v"(dw[0][TN - 1]), "+v"(dx[0][0]), "+v"(dw[1][0]), "+v"(dw[1][TN - 1]),
+                           "+v"(dx[1][0]));
+        else
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(dw[0][0]), "+v"(dx[0][0]), "+v"(dw[1][0]), "+v"(dx[1][0]));
 #pragma unroll
         for (int kc = 0; kc < KC; kc++)
 #pragma unroll
@@ -574,6 +587,7 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
 //   5: 1 wave  x (64x64)  WG 64x64
 //   6: 4 waves x (64x64)  WG 128x128, 32-byte K stages: 70 KB of LDS, two workgroups per CU
 //      (K-quants)
+//   7: 4 waves x (32x32)  WG 64x64
 static int gemm_cfg_env() {
     const char *e = getenv("MQ_GEMM_CFG");  // read per launch so a process can compare configurations
     return (e && *e) ? atoi(e) : 0;
@@ -584,13 +598,17 @@ static inline int64_t tiles(int64_t M, int64_t N, int bm, int bn) { return ((M +
 template <int FMT>
 static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
     int cfg = gemm_cfg_env();
-    if (cfg < 1 || cfg > 6 || cfg == 2 || (cfg == 6 && FMT != FMT_Q4_K && FMT != FMT_Q6_K)) {
-        // 256x128 tiles when that still gives every CU (256) a workgroup, else 128x128
-        // (the smaller tiles measured slower even where 128x128 leaves CUs idle:
-        // 4096x384x384 Q8_0 12.7 us at 128x128, 13.2 us at 128x64, 14.1 us at 64x64)
+    if (cfg < 1 || cfg > 7 || cfg == 2 || (cfg == 6 && FMT != FMT_Q4_K && FMT != FMT_Q6_K)) {
+        // Small grids (under 512 tiles of 128x128): 64x64 workgroups of four 32x32 waves.
+        // Every 32-deep K chunk costs a wave VALU work per output of its tile (the block
+        // scales), so smaller wave tiles shorten the serial chain each wave walks; with few
+        // output tiles that chain, not operand reuse, sets the time (MI355X, Q8_0 4096x384x1536
+        // 32 -> 17 us, Q4_K 512x1024x3072 37 -> 16 us).  Larger grids: 256x128 tiles when that
+        // still gives every CU (256) a workgroup, else 128x128.
         int64_t n_all = a.N;
         for (int g = 1; g < a.ngroups; g++) n_all += a.grp[g - 1].N;
-        cfg = (tiles(a.M, n_all, 256, 128) >= 256) ? 1 : 3;
+        if (tiles(a.M, n_all, 128, 128) < 512) cfg = 7;
+        else cfg = (tiles(a.M, n_all, 256, 128) >= 256) ? 1 : 3;
     }
     switch (cfg) {
         case 1: return launch_cfg<FMT, 4, 2, 2, 2, 1>(a, s);
@@ -600,6 +618,7 @@ static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
             if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q6_K) return launch_cfg<FMT, 2, 2, 2, 2, 2, 1>(a, s);
             return hipErrorInvalidValue;
 
+        case 7: return launch_cfg<FMT, 2, 2, 1, 1, 2>(a, s);
         default: return launch_cfg<FMT, 1, 1, 2, 2, 2>(a, s);
     }
 }
