@@ -16,6 +16,9 @@
 //                                                  one grouped GEMM, biases added by its store
 //   [ADD(residual) ->] NORM|RMS_NORM -> MUL(w) [-> ADD(b)]
 //                                                  one row pass (mq_op_norm)
+//   MUL_MAT -> ADD(bias) -> UNARY(GELU_ERF) -> MUL_MAT(Q8_0) [-> ADD(bias)]
+//                                                  the first GEMM quantizes gelu(y + bias) for
+//                                                  the second; the FFN intermediate is never written
 //   ADD(bias) -> UNARY(GELU_ERF) -> MUL_MAT [-> ADD(bias)]
 //                                                  bias and GELU applied while the activation
 //                                                  is quantized for the mat-mul
@@ -525,6 +528,52 @@ int try_fuse_bias_gelu_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, enu
     return dst == mm ? 3 : 4;
 }
 
+// MUL_MAT(w1, x) -> ADD(., bias) -> UNARY(GELU_ERF) -> MUL_MAT(w2, .) [-> ADD(., bias2)] with a
+// Q8_0 w2 and both products on the GEMM path (the encoder FFN): the first GEMM adds the bias,
+// applies GELU-erf and quantizes its own output for the second (mq_mul_mat_q_requant, the same
+// bytes the activation quantizer would write), so the FFN's intermediate is never written.
+// The quantized intermediate sits in the workspace after x's quantized activation.
+int try_fuse_ffn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status &st) {
+    if (i + 3 >= n || !feeds_only_next(cg, i) || !feeds_only_next(cg, i + 1) || !feeds_only_next(cg, i + 2)) return 0;
+    ggml_tensor *mm1 = ggml_graph_node(cg, i), *add = ggml_graph_node(cg, i + 1);
+    ggml_tensor *gelu = ggml_graph_node(cg, i + 2), *mm2 = ggml_graph_node(cg, i + 3);
+    if (add->op != GGML_OP_ADD || add->src[0] != mm1 || add->type != GGML_TYPE_F32 || !same_shape(add, mm1)) return 0;
+    if (gelu->op != GGML_OP_UNARY || ggml_get_unary_op(gelu) != GGML_UNARY_OP_GELU_ERF || gelu->src[0] != add) return 0;
+    if (mm2->op != GGML_OP_MUL_MAT || mm2->src[1] != gelu || !flat_mul_mat(mm1) || !flat_mul_mat(mm2)) return 0;
+    const ggml_tensor *w1 = mm1->src[0], *x = mm1->src[1], *w2 = mm2->src[0];
+    const int64_t K1 = w1->ne[0], N1 = w1->ne[1], N2 = w2->ne[1];
+    if (w2->type != GGML_TYPE_Q8_0 || w2->ne[0] != N1 || N1 % 128 != 0 || !is_row_vector(add->src[1], N1)) return 0;
+    const int mt1 = mq_type_of(w1->type);
+    const int64_t M = x->ne[1] * x->ne[2] * x->ne[3];
+    if (mq_mul_mat_path(mt1, N1, K1, M) != MQ_PATH_GEMM || mq_mul_mat_path(MQ_TYPE_Q8_0, N2, N1, M) != MQ_PATH_GEMM)
+        return 0;
+    ggml_tensor *dst = mm2;
+    const float *bias2 = nullptr;
+    if (i + 4 < n && feeds_only_next(cg, i + 3)) {
+        ggml_tensor *a2 = ggml_graph_node(cg, i + 4);
+        if (a2->op == GGML_OP_ADD && a2->src[0] == mm2 && is_row_vector(a2->src[1], N2) && rows_flat(a2) &&
+            a2->nb[0] == sizeof(float) && a2->nb[1] % sizeof(float) == 0) {
+            dst = a2;
+            bias2 = (const float *)a2->src[1]->data;
+        }
+    }
+    const size_t off = (mq_workspace_bytes(mt1, M, K1) + 255) & ~(size_t)255;
+    if (!ensure_ws(c, off + mq_workspace_bytes(MQ_TYPE_Q8_0, M, N1))) {
+        st = GGML_STATUS_ALLOC_FAILED;
+        return dst == mm2 ? 4 : 5;
+    }
+    void *ws2 = (char *)c->ws + off;
+    int rc = quantize_x(c, x, mt1, M, K1, MQ_PATH_GEMM);
+    if (rc == 0)
+        rc = mq_mul_mat_q_requant(mt1, w1->data, N1, K1, c->ws, M, (const float *)add->src[1]->data, MQ_PRE_GELU_ERF,
+                                  MQ_TYPE_Q8_0, ws2, c->ws_bytes - off, c->stream);
+    if (rc == 0)
+        rc = mq_mul_mat_q_ex(MQ_TYPE_Q8_0, w2->data, N2, N1, ws2, M, (float *)dst->data, (int64_t)(dst->nb[1] / 4), bias2,
+                             MQ_PATH_GEMM, c->stream);
+    st = op_status(rc, mm1);
+    return dst == mm2 ? 4 : 5;
+}
+
 // A MUL_MAT of a group and the bias ADD fused into its store (add_idx < 0: none).
 struct MulMatMember {
     ggml_tensor *mm, *dst;
@@ -710,7 +759,10 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
         if (node->op != GGML_OP_MUL_MAT || !fuse) c->ws_x = nullptr;
         if (fuse) {
             switch (node->op) {
-                case GGML_OP_MUL_MAT: used = try_group_mul_mat(c, cg, i, n, done, st); break;
+                case GGML_OP_MUL_MAT:
+                    used = try_fuse_ffn(c, cg, i, n, st);
+                    if (!used) used = try_group_mul_mat(c, cg, i, n, done, st);
+                    break;
                 case GGML_OP_NORM:
                 case GGML_OP_RMS_NORM: used = try_fuse_norm(c, cg, i, n, st); break;
                 case GGML_OP_ADD:

@@ -289,6 +289,29 @@ int mq_mul_mat_q_ex(int type, const void *w_image, int64_t n, int64_t k, const v
     return e == hipSuccess ? MQ_OK : hip_fail(e, path == MQ_PATH_GEMV ? "gemv" : "gemm");
 }
 
+int mq_mul_mat_q_requant(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m,
+                         const float *bias, int op, int out_type, void *out_workspace, size_t out_workspace_bytes,
+                         void *stream) {
+    int rc = check_weight_shape(type, n, k);
+    if (rc) return rc;
+    if (out_type != MQ_TYPE_Q8_0) return fail(MQ_EUNSUPPORTED, "mq_mul_mat_q_requant: the output type must be Q8_0");
+    if (op != MQ_PRE_NONE && op != MQ_PRE_GELU_ERF)
+        return fail(MQ_EINVAL, "mq_mul_mat_q_requant: op must be MQ_PRE_NONE or MQ_PRE_GELU_ERF");
+    if (n % KSTAGE != 0) return fail(MQ_EINVAL, "mq_mul_mat_q_requant: n must be a multiple of %d", KSTAGE);
+    if (!w_image || !workspace || !out_workspace || m < 0 || m > INT32_MAX)
+        return fail(MQ_EINVAL, "mq_mul_mat_q_requant: bad arguments");
+    if (!is_aligned(w_image, 256) || !is_aligned(workspace, 256) || !is_aligned(out_workspace, 256))
+        return fail(MQ_EINVAL, "mq_mul_mat_q_requant: weight image and workspaces must be 256-byte aligned");
+    if (m == 0) return MQ_OK;
+    const size_t need = act_planes(MQ_TYPE_Q8_0, m, n, true).total;
+    if (out_workspace_bytes < need)
+        return fail(MQ_EINVAL, "mq_mul_mat_q_requant: output workspace of %zu bytes, %zu needed", out_workspace_bytes,
+                    need);
+    const hipError_t e = launch_gemm_requant(type, w_image, n, k, workspace, m, bias, op, mq_q8_0_variant(),
+                                             out_workspace, (hipStream_t)stream);
+    return e == hipSuccess ? MQ_OK : hip_fail(e, "gemm");
+}
+
 int mq_mul_mat_q_group(int type, int n_groups, const void *const *w_images, const int64_t *n, int64_t k,
                        const void *workspace, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,
                        int path, void *stream) {

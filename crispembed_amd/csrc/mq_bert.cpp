@@ -47,7 +47,7 @@ struct mq_bert {
     mq_bert_hparams hp{};
     DevBuf tok, pos, type, lnw, lnb;
     std::vector<Layer> layers;
-    DevBuf x, qkv, att, y, ff, ws;
+    DevBuf x, qkv, att, y, ff, ws, ws2;
     int64_t rows_cap = 0;
 };
 
@@ -123,8 +123,14 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
     const int t = hp.wtype;
     const size_t f4 = sizeof(float);
     const size_t wsb = std::max({mq_workspace_bytes(t, rows, H), mq_workspace_bytes(t, rows, F)});
+    // Q8_0 FFN on the GEMM path: the FFN-up GEMM adds its bias, applies GELU-erf and quantizes its
+    // own output for the FFN-down GEMM (mq_mul_mat_q_requant), into the second workspace
+    const bool ffn_fused = t == MQ_TYPE_Q8_0 && F % 128 == 0 && mq_mul_mat_path(t, F, H, rows) == MQ_PATH_GEMM &&
+                           mq_mul_mat_path(t, H, F, rows) == MQ_PATH_GEMM;
+    const size_t wsb2 = ffn_fused ? mq_workspace_bytes(MQ_TYPE_Q8_0, rows, F) : 0;
     if (!m->x.ensure(rows * H * f4) || !m->qkv.ensure(rows * 3 * H * f4) || !m->att.ensure(rows * H * f4) ||
-        !m->y.ensure(rows * H * f4) || !m->ff.ensure(rows * F * f4) || !m->ws.ensure(wsb))
+        !m->y.ensure(rows * H * f4) || !m->ff.ensure(rows * F * f4) || !m->ws.ensure(wsb) ||
+        (ffn_fused && !m->ws2.ensure(wsb2)))
         return set_error(MQ_ENOMEM, "activation buffers for %lld rows", (long long)rows);
     hipStream_t s = (hipStream_t)stream;
     const float eps = hp.layer_norm_eps;
@@ -146,13 +152,23 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
         if ((rc = hip_rc(launch_bias_res_ln(m->y.f(), L.bo.f(), X, L.ln1w.f(), L.ln1b.f(), eps, X, rows, (int)H, s),
                          "attention residual")))
             return rc;
-        if ((rc = mm(L.fc1, X, m->ff.f()))) return rc;
-        // FFN-up bias and GELU-erf are applied by the FFN-down activation quantizer
-        if ((rc = mq_quantize_act_ex(t, m->ff.f(), F, rows, F, L.b1.f(), MQ_PRE_GELU_ERF, m->ws.p, m->ws.bytes,
-                                     MQ_PATH_AUTO, s)))
-            return rc;
-        if ((rc = mq_mul_mat_q(t, L.fc2.img.p, L.fc2.n, L.fc2.k, m->ws.p, rows, m->y.f(), L.fc2.n, MQ_PATH_AUTO, s)))
-            return rc;
+        if (ffn_fused) {
+            if ((rc = mq_quantize_act_ex(t, X, H, rows, H, nullptr, MQ_PRE_NONE, m->ws.p, m->ws.bytes, MQ_PATH_GEMM,
+                                         s)) ||
+                (rc = mq_mul_mat_q_requant(t, L.fc1.img.p, L.fc1.n, L.fc1.k, m->ws.p, rows, L.b1.f(), MQ_PRE_GELU_ERF,
+                                           MQ_TYPE_Q8_0, m->ws2.p, m->ws2.bytes, s)) ||
+                (rc = mq_mul_mat_q(t, L.fc2.img.p, L.fc2.n, L.fc2.k, m->ws2.p, rows, m->y.f(), L.fc2.n, MQ_PATH_GEMM,
+                                   s)))
+                return rc;
+        } else {
+            if ((rc = mm(L.fc1, X, m->ff.f()))) return rc;
+            // FFN-up bias and GELU-erf are applied by the FFN-down activation quantizer
+            if ((rc = mq_quantize_act_ex(t, m->ff.f(), F, rows, F, L.b1.f(), MQ_PRE_GELU_ERF, m->ws.p, m->ws.bytes,
+                                         MQ_PATH_AUTO, s)))
+                return rc;
+            if ((rc = mq_mul_mat_q(t, L.fc2.img.p, L.fc2.n, L.fc2.k, m->ws.p, rows, m->y.f(), L.fc2.n, MQ_PATH_AUTO, s)))
+                return rc;
+        }
         if ((rc = hip_rc(launch_bias_res_ln(m->y.f(), L.b2.f(), X, L.ln2w.f(), L.ln2b.f(), eps, X, rows, (int)H, s),
                          "ffn residual")))
             return rc;

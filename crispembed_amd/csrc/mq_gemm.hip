@@ -41,6 +41,7 @@
 // Output mapping of a 32x32 MFMA: register r of lane l holds
 // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 #include "mq_internal.h"
+#include "mq_act.h"
 
 #include <climits>
 #include <type_traits>
@@ -68,6 +69,13 @@ struct GemmArgs {
     const _Float16 *wmin;   // Q4_K: weight min-term fragments
     float *y;
     const float *bias;  // NULL, or N floats added to every row in the store
+    // quantized output (qo not NULL, one weight group): v = op(acc + bias) is stored as the Q8_0
+    // activation of a following mat-mul in its GEMM layout -- quants tiled [q_m_pad][32 q_kch],
+    // scales [q_kch][q_m_pad] -- instead of as floats in y; q_pre is MQ_PRE_NONE or
+    // MQ_PRE_GELU_ERF, q_var the Q8_0 rounding variant
+    int8_t *qo;
+    float *qd;
+    int q_m_pad, q_kch, q_pre, q_var;
     int M, N, ldy;
     int m_pad, n_pad;
     int kch;      // 32-byte K chunks per row (kb_pad / 32)
@@ -251,6 +259,45 @@ __device__ __forceinline__ DmaItem epi_item(const GemmArgs &a, int e, int sb, in
         it.lds = C::EP_DX + C::EP_DW + C::EP_DMIN + C::EP_AMIN + ct * 1024;
     }
     return it;
+}
+
+// Half of one Q8_0 block of the quantized output: this lane's 16 values, the other 16 in lane
+// l ^ 32.  The values are op(acc + bias) (rows past M: zero, as the quantizer's pad rows), and
+// the block is quantized as k_quantize_tiled<TQ_Q8_0> quantizes a row (ggml's
+// quantize_row_q8_0 variants): the same max, scale, reciprocal and rounding, so the bytes
+// equal those of the fp32 output quantized by the activation quantizer.  Returns the scale
+// rounded through fp16; q receives the 16 quants.
+__device__ __forceinline__ float requant_q8_0(float (&v)[16], bool live, int pre, int variant, uint4 &q) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+        float x = v[e];
+        if (pre == MQ_PRE_GELU_ERF) x = gelu_erf_f32(x);
+        v[e] = live ? x : 0.f;
+    }
+    float amax = fabsf(v[0]);
+#pragma unroll
+    for (int e = 1; e < 16; e++) amax = fmaxf(amax, fabsf(v[e]));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const float d = amax / 127.f;
+    float id;
+    if (variant == MQ_Q8_0_X86) id = (amax != 0.0f) ? 127.f / amax : 0.0f;
+    else id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    uint32_t w[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        uint32_t pk = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float t = v[4 * u + b] * id;
+            float r = (variant == MQ_Q8_0_REF) ? roundf(t) : rintf(t);
+            r = fminf(fmaxf(r, -128.f), 127.f);
+            pk |= ((uint32_t)((int)r & 0xff)) << (8 * b);
+        }
+        w[u] = pk;
+    }
+    q = make_uint4(w[0], w[1], w[2], w[3]);
+    return f16_bits_to_f32(f32_to_f16_bits(d));
 }
 
 template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2>
@@ -540,6 +587,49 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
                 for (int rr = 0; rr < 16; rr++) acc[i][j][rr] += bv[j];
     }
 
+    if (a.qo) {
+        // Quantized output.  Each wave stages a 32x32 tile in LDS (the stage ring is free once
+        // every wave is past its last stage), then lane l takes row l % 32, values
+        // 16 (l / 32) .. +15 of it: exactly the 16 bytes lane l owns in the tile's 1 KB
+        // fragment, so the fragment leaves as one coalesced store per wave.
+        constexpr int QST = 36;  // staging row stride in floats (16-byte aligned rows, spread banks)
+        static_assert(C::LDS >= C::NW * 32 * QST * 4, "staging tiles fit in the stage ring");
+        __syncthreads();
+        float *tile = (float *)smem + wave * (32 * QST);
+        const int qr = lane & 31, qh = lane >> 5;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int rt = (m0 >> 5) + wm * TM + i;  // 32-row tile of the output
+                const int kb = (n0 >> 5) + wn * TN + j;  // its Q8_0 block along the next product's K
+                if (rt * 32 >= a.q_m_pad || kb >= a.q_kch) continue;  // uniform
+#pragma unroll
+                for (int rr = 0; rr < 16; rr++)
+                    tile[(8 * (rr >> 2) + 4 * lhalf + (rr & 3)) * QST + lrow] = acc[i][j][rr];
+                // other lanes' values are read back: keep the compiler from moving the reads
+                // above the writes (the LDS itself serves one wave's accesses in order)
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float4 t4 = *(const float4 *)(tile + qr * QST + 16 * qh + 4 * u);
+                    v[4 * u] = t4.x, v[4 * u + 1] = t4.y, v[4 * u + 2] = t4.z, v[4 * u + 3] = t4.w;
+                }
+                const int row = rt * 32 + qr;
+                uint4 q;
+                const float d = requant_q8_0(v, row < a.M, a.q_pre, a.q_var, q);
+                *(uint4 *)(a.qo + (((int64_t)rt * a.q_kch + kb) << 10) + lane * 16) = q;
+                if (qh == 0) a.qd[(int64_t)kb * a.q_m_pad + row] = d;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+        return;
+    }
+
     // store: lanes 0..31 of a register write 32 consecutive floats of one row.
     // (Staging the tile through LDS for 16-byte row stores was measured slower on
     // MI355X: the extra barrier and LDS pass cost more than the store instructions.)
@@ -678,6 +768,50 @@ hipError_t launch_gemm_group(int type, int ngroups, const void *const *images, c
 hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
                        int64_t ldy, hipStream_t s, const float *bias) {
     return launch_gemm_group(type, 1, &image, &n, k, ws, m, &y, &ldy, &bias, s);
+}
+
+hipError_t launch_gemm_requant(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m,
+                               const float *bias, int pre, int q8_0_variant, void *out_ws, hipStream_t s) {
+    if (m <= 0 || n <= 0) return hipSuccess;
+    if (n % KSTAGE != 0) return hipErrorInvalidValue;  // the output fills the next product's padded K
+    const ActPlanes ap = act_planes(type, m, k, true), op = act_planes(MQ_TYPE_Q8_0, m, n, true);
+    if (op.kb_pad != n || op.m_pad != ap.m_pad) return hipErrorInvalidValue;
+    const WeightPlanes p = weight_planes(type, n, k);
+    const uint8_t *xb = (const uint8_t *)ws, *wb = (const uint8_t *)image;
+    uint8_t *ob = (uint8_t *)out_ws;
+    GemmArgs a{};
+    a.xq = (const int8_t *)(xb + ap.xq);
+    a.xd = (const float *)(xb + ap.xd);
+    a.xmin = (const _Float16 *)(xb + ap.xmin);
+    a.wq = (const int8_t *)(wb + p.tq);
+    a.whi = (const int8_t *)(wb + p.thi);
+    a.wd = (const float *)(wb + p.tdw);
+    a.wdmin = (const float *)(wb + p.tdmin);
+    a.wmin = (const _Float16 *)(wb + p.tmin);
+    a.y = nullptr;
+    a.bias = bias;
+    a.qo = (int8_t *)(ob + op.xq);
+    a.qd = (float *)(ob + op.xd);
+    a.q_m_pad = (int)op.m_pad;
+    a.q_kch = (int)(n / 32);
+    a.q_pre = pre;
+    a.q_var = q8_0_variant;
+    a.M = (int)m;
+    a.N = (int)n;
+    a.ldy = (int)n;
+    a.m_pad = (int)ap.m_pad;
+    a.n_pad = (int)p.n_pad;
+    a.kch = (int)(p.kb_pad / 32);
+    a.nstages = (int)(p.kb_pad / 64);
+    a.nsb = (int)(k / QK_K);
+    a.ngroups = 1;
+    switch (type) {
+        case MQ_TYPE_Q8_0: return launch_fmt<FMT_Q8_0>(a, s);
+        case MQ_TYPE_Q4_K: return launch_fmt<FMT_Q4_K>(a, s);
+        case MQ_TYPE_Q6_K: return launch_fmt<FMT_Q6_K>(a, s);
+        case MQ_TYPE_F16: return launch_fmt<FMT_F16>(a, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace mq

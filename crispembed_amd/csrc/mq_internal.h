@@ -294,6 +294,11 @@ hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const 
                        int64_t ldy, hipStream_t s, const float *bias = nullptr);
 hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
                        int64_t ldy, hipStream_t s, const float *bias = nullptr);
+// the GEMM with its output v = pre(x w^T + bias) quantized to Q8_0 into out_ws, the GEMM-layout
+// activation workspace of a following mat-mul with k = n (n a multiple of KSTAGE); pre is
+// MQ_PRE_NONE or MQ_PRE_GELU_ERF.  ws must hold x in the tiled (GEMM) layout.
+hipError_t launch_gemm_requant(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m,
+                               const float *bias, int pre, int q8_0_variant, void *out_ws, hipStream_t s);
 // up to 4 weights of the same type and k on one activation, one launch (bias may be NULL)
 hipError_t launch_gemm_group(int type, int ngroups, const void *const *images, const int64_t *n, int64_t k,
                              const void *ws, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,

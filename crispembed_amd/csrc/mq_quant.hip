@@ -13,15 +13,10 @@
 #include <algorithm>
 
 #include "mq_internal.h"
+#include "mq_act.h"
 #include "mq_deq.h"
 
 namespace mq {
-
-__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
-    const _Float16 h = (_Float16)f;  // v_cvt_f16_f32: round to nearest even, fp16 subnormals kept
-    return __builtin_bit_cast(uint16_t, h);
-}
-__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 
 // ggml's nearest_int: (f + 1.5*2^23) keeps round-half-even(f) in the low mantissa bits.
 __device__ __forceinline__ int nearest_int(float f) {
@@ -53,7 +48,7 @@ __device__ __forceinline__ float4 pre_load(const float *p, int pre, const float 
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         if (bias) r[i] = r[i] + bias[col + i];
-        if (pre == MQ_PRE_GELU_ERF) r[i] = 0.5f * r[i] * (1.0f + erff(r[i] * 0.70710678118654752f));
+        if (pre == MQ_PRE_GELU_ERF) r[i] = gelu_erf_f32(r[i]);
         else if (pre == MQ_PRE_SILU_MUL) r[i] = (r[i] / (1.0f + expf(-r[i]))) * u[i];
     }
     return make_float4(r[0], r[1], r[2], r[3]);

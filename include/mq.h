@@ -163,6 +163,20 @@ int mq_mul_mat_q_group(int type, int n_groups, const void *const *w_images, cons
                        const void *workspace, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,
                        int path, void *stream);
 
+/* Two mat-muls in a row without the fp32 tensor between them: computes
+ * V = op(X W^T + bias) on the GEMM path (workspace: X quantized with path MQ_PATH_GEMM) and
+ * writes V quantized to Q8_0 straight into out_workspace, in the layout that
+ * mq_quantize_act_ex(MQ_TYPE_Q8_0, V, ..., MQ_PATH_GEMM) writes -- the same bytes, bit for
+ * bit -- ready for mq_mul_mat_q_ex(MQ_TYPE_Q8_0, W2, n2, n, out_workspace, m, ..., MQ_PATH_GEMM).
+ * V itself is never written.  This is the encoder FFN of src/crispembed.cpp:1410-1416 (FFN-up
+ * MUL_MAT, bias ADD, ggml_gelu_erf, then the FFN-down MUL_MAT, whose CPU backend quantizes its
+ * src1 through the Q8_0 from_float before the block dots).  out_type must be MQ_TYPE_Q8_0, op
+ * MQ_PRE_NONE or MQ_PRE_GELU_ERF, n a multiple of 128; out_workspace_bytes >=
+ * mq_workspace_bytes(MQ_TYPE_Q8_0, m, n). */
+int mq_mul_mat_q_requant(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m,
+                         const float *bias, int op, int out_type, void *out_workspace, size_t out_workspace_bytes,
+                         void *stream);
+
 /* mq_quantize_act with the graph's elementwise producer folded in: it quantizes
  * op(X + bias) where bias is an fp32 [k] row added to every row of X (NULL: none) and
  * op is one of MQ_PRE_*.  The value quantized is the fp32 tensor the ggml graph

@@ -46,6 +46,14 @@ def test_host_only_entry_points_without_gpu():
     assert rc == -2 and b"multiple" in L.mq_last_error()
     rc = L.mq_quantize_act_ex(mq.TYPE_Q8_0, 256, 256, 2, 256, None, 7, 4096, 1 << 20, mq.PATH_AUTO, None)
     assert rc == -1 and b"prologue" in L.mq_last_error()
+    # the quantized-output GEMM: Q8_0 output only, n a multiple of 128, GELU-erf or no op
+    rq = L.mq_mul_mat_q_requant
+    assert rq(mq.TYPE_Q8_0, 256, 1536, 384, 256, 4096, None, 1, mq.TYPE_Q4_K, 256, 1 << 30, None) == -2
+    assert rq(mq.TYPE_Q8_0, 256, 1500, 384, 256, 4096, None, 1, mq.TYPE_Q8_0, 256, 1 << 30, None) == -1
+    assert b"multiple of 128" in L.mq_last_error()
+    assert rq(mq.TYPE_Q8_0, 256, 1536, 384, 256, 4096, None, 2, mq.TYPE_Q8_0, 256, 1 << 30, None) == -1
+    assert rq(mq.TYPE_Q8_0, 256, 1536, 384, 256, 4096, None, 1, mq.TYPE_Q8_0, 256, 1024, None) == -1
+    assert b"output workspace" in L.mq_last_error()
 
 
 def test_op_support_checks_without_gpu():

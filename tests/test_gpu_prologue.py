@@ -161,3 +161,100 @@ def test_mul_mat_q_group_equals_separate(wtype, m, k, path):
         assert np.array_equal(a[:, :n], b[:, :n]), g
         assert np.isnan(b[:, n:]).all()
     del imgs, ws
+
+
+def _live_planes(raw, m, n):
+    """The Q8_0 GEMM-layout planes (tiled quants, block-major scales) of rows < m, as arrays."""
+    m_pad = -(-m // 256) * 256
+    kch = n // 32
+    q = raw[:m_pad * n].reshape(m_pad // 32, kch, 2, 32, 16)   # [row tile][chunk][half][row][byte]
+    q = q.transpose(0, 3, 1, 2, 4).reshape(m_pad, n)[:m]        # row-major quants
+    off = -(-(m_pad * n) // 256) * 256
+    d = raw[off:off + kch * m_pad * 4].view(np.float32).reshape(kch, m_pad)[:, :m]
+    return q, d
+
+
+@pytest.mark.parametrize("wtype", TYPES)
+@pytest.mark.parametrize("m,k,n,op,with_bias", [(37, 512, 384, 1, True), (300, 384, 1536, 1, True),
+                                                (1000, 512, 512, 0, False), (4096, 384, 1536, 1, True),
+                                                (520, 256, 256, 0, True)])
+def test_mul_mat_q_requant_equals_separate(wtype, m, k, n, op, with_bias):
+    """mq_mul_mat_q_requant (the GEMM quantizing its own output for the next mat-mul) against the
+    GEMM's fp32 output quantized by mq_quantize_act_ex with the same bias and op: the quants and
+    scales of every row are bit-identical, and so is the next Q8_0 mat-mul read from either."""
+    import torch
+    from crispembed_amd import mq
+    L = mq.lib()
+    if wtype in (O.Q4_K, O.Q6_K) and k % 256:
+        k = 512  # K-quant rows are whole 256-value superblocks
+    rng = np.random.default_rng(7 * m + n + wtype)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    img = weight_image(wtype, np.ascontiguousarray(mq_quantized(wtype, w)), n, k)
+    n2 = 200
+    w2 = rng.standard_normal((n2, n)).astype(np.float32)
+    img2 = weight_image(O.Q8_0, np.ascontiguousarray(mq_quantized(O.Q8_0, w2)), n2, n)
+    x = dev(rng.standard_normal((m, k)).astype(np.float32))
+    _, ptr, _ = ws = _quant(wtype, x, m, k, 2)
+    bias = dev(rng.standard_normal(n).astype(np.float32)) if with_bias else None
+    bptr = ctypes.c_void_p(bias.data_ptr()) if with_bias else None
+    # separate: fp32 GEMM output, then the quantizer with the bias and op
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    mq.check(L.mq_mul_mat_q_ex(wtype, ctypes.c_void_p(img[1]), n, k, ctypes.c_void_p(ptr), m,
+                               ctypes.c_void_p(y.data_ptr()), n, None, 2, stream()))
+    ref_buf, ref_ptr, ref_raw = _quant(O.Q8_0, y, m, n, 2, bias, op)
+    # fused, into a workspace filled with garbage
+    nb = L.mq_workspace_bytes(O.Q8_0, m, n)
+    out, off = empty_u8(nb)
+    out.fill_(0xAB)
+    optr = out.data_ptr() + off
+    mq.check(L.mq_mul_mat_q_requant(wtype, ctypes.c_void_p(img[1]), n, k, ctypes.c_void_p(ptr), m, bptr, op,
+                                    O.Q8_0, ctypes.c_void_p(optr), nb, stream()))
+    got_raw = host(out)[off:off + nb]
+    qa, da = _live_planes(ref_raw, m, n)
+    qb, db = _live_planes(got_raw, m, n)
+    assert np.array_equal(qa, qb)
+    assert np.array_equal(da.view(np.uint32), db.view(np.uint32))
+    # the next mat-mul reads either workspace to the same result
+    z = [torch.full((m, n2), np.nan, dtype=torch.float32, device="cuda") for _ in range(2)]
+    for t, p in zip(z, (ref_ptr, optr)):
+        mq.check(L.mq_mul_mat_q_ex(O.Q8_0, ctypes.c_void_p(img2[1]), n2, n, ctypes.c_void_p(p), m,
+                                   ctypes.c_void_p(t.data_ptr()), n2, None, 2, stream()))
+    assert np.array_equal(host(z[0]), host(z[1]))
+    del img, img2, ws, ref_buf
+
+
+@pytest.mark.parametrize("variant", [1, 2])
+def test_mul_mat_q_requant_variants(variant):
+    """The NEON and reference rounding variants of the Q8_0 quantizer carry over to the GEMM's
+    quantized output (bit-identical planes)."""
+    import torch
+    from crispembed_amd import mq
+    L = mq.lib()
+    old = L.mq_q8_0_variant()
+    L.mq_set_q8_0_variant(variant)
+    try:
+        m, k, n, wtype = 700, 512, 768, O.Q8_0
+        rng = np.random.default_rng(variant)
+        w = rng.standard_normal((n, k)).astype(np.float32)
+        img = weight_image(wtype, np.ascontiguousarray(mq_quantized(wtype, w)), n, k)
+        x = dev(rng.standard_normal((m, k)).astype(np.float32))
+        _, ptr, _ = ws = _quant(wtype, x, m, k, 2)
+        bias = dev(rng.standard_normal(n).astype(np.float32))
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        mq.check(L.mq_mul_mat_q_ex(wtype, ctypes.c_void_p(img[1]), n, k, ctypes.c_void_p(ptr), m,
+                                   ctypes.c_void_p(y.data_ptr()), n, None, 2, stream()))
+        _, _, ref_raw = _quant(O.Q8_0, y, m, n, 2, bias, 1)
+        nb = L.mq_workspace_bytes(O.Q8_0, m, n)
+        out, off = empty_u8(nb)
+        out.fill_(0xAB)
+        mq.check(L.mq_mul_mat_q_requant(wtype, ctypes.c_void_p(img[1]), n, k, ctypes.c_void_p(ptr), m,
+                                        ctypes.c_void_p(bias.data_ptr()), 1, O.Q8_0,
+                                        ctypes.c_void_p(out.data_ptr() + off), nb, stream()))
+        got_raw = host(out)[off:off + nb]
+        qa, da = _live_planes(ref_raw, m, n)
+        qb, db = _live_planes(got_raw, m, n)
+        assert np.array_equal(qa, qb)
+        assert np.array_equal(da.view(np.uint32), db.view(np.uint32))
+        del img, ws
+    finally:
+        L.mq_set_q8_0_variant(old)
