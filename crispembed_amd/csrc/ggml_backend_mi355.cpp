@@ -15,7 +15,9 @@
 //   MUL_MAT [-> ADD(bias)], with the MUL_MATs after it on the same activation
 //                                                  one grouped GEMM, biases added by its store
 //   [ADD(residual) ->] NORM|RMS_NORM -> MUL(w) [-> ADD(b)]
-//                                                  one row pass (mq_op_norm)
+//                                                  one row pass (mq_op_norm); before a Q8_0
+//                                                  MUL_MAT it also quantizes the result for it
+//                                                  (mq_op_norm_q8_0)
 //   MUL_MAT -> ADD(bias) -> UNARY(GELU_ERF) -> MUL_MAT(Q8_0) [-> ADD(bias)]
 //                                                  the first GEMM quantizes gelu(y + bias) for
 //                                                  the second; the FFN intermediate is never written
@@ -438,6 +440,8 @@ bool same_shape(const ggml_tensor *a, const ggml_tensor *b) {
     return true;
 }
 
+bool flat_mul_mat(const ggml_tensor *mm);
+
 // [ADD(x, r) ->] NORM|RMS_NORM -> MUL(w) [-> ADD(b)] starting at node i: returns the number of
 // nodes consumed (0: no match)
 int try_fuse_norm(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status &st) {
@@ -471,10 +475,31 @@ int try_fuse_norm(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status
     mq_view r{};
     if (res) r = view_of(res);
     if (!mq_op_supported(MQ_OP_NORM, kind, &x, res ? &r : nullptr, nullptr, nullptr, &d)) return 0;
-    st = op_status(mq_op_norm(kind, &x, res ? &r : nullptr, &d, op_param_f32(nrm, 0), (const float *)mul->src[1]->data,
-                              b, c->stream),
-                   nrm);
-    return (j - i) + (last == mul ? 2 : 3);
+    const int used = (j - i) + (last == mul ? 2 : 3);
+    const float eps = op_param_f32(nrm, 0), *w = (const float *)mul->src[1]->data;
+    // The next node that is not a view: when it is a Q8_0 MUL_MAT on the GEMM path reading this
+    // result, the norm also leaves the result quantized in the workspace for it (mq_op_norm_q8_0),
+    // and the activation cache lets that MUL_MAT (and its siblings) skip the quantizer.
+    int nx = i + used;
+    while (nx < n && (ggml_is_empty(ggml_graph_node(cg, nx)) || is_view_op(ggml_graph_node(cg, nx)->op))) nx++;
+    const ggml_tensor *mm = nx < n ? ggml_graph_node(cg, nx) : nullptr;
+    const int64_t K = last->ne[0], M = last->ne[1] * last->ne[2] * last->ne[3];
+    auto dense = [K](const ggml_tensor *t) {
+        return !t || (t->nb[0] == sizeof(float) && t->nb[1] == (size_t)K * sizeof(float) && rows_flat(t) &&
+                      ((uintptr_t)t->data & 15) == 0);
+    };
+    if (mm && mm->op == GGML_OP_MUL_MAT && mm->src[1] == last && mm->src[0]->type == GGML_TYPE_Q8_0 &&
+        flat_mul_mat(mm) && K % 128 == 0 && K <= 1024 && dense(last) && dense(res) &&
+        dense(res ? first->src[0] : nrm->src[0]) && ((uintptr_t)w & 15) == 0 && ((uintptr_t)b & 15) == 0 &&
+        mq_mul_mat_path(MQ_TYPE_Q8_0, mm->src[0]->ne[1], K, M) == MQ_PATH_GEMM &&
+        ensure_ws(c, mq_workspace_bytes(MQ_TYPE_Q8_0, M, K))) {
+        const int rc = mq_op_norm_q8_0(kind, &x, res ? &r : nullptr, &d, eps, w, b, c->ws, c->ws_bytes, c->stream);
+        if (rc == 0) c->ws_x = last, c->ws_type = MQ_TYPE_Q8_0, c->ws_m = M, c->ws_k = K, c->ws_path = MQ_PATH_GEMM;
+        st = op_status(rc, nrm);
+        return used;
+    }
+    st = op_status(mq_op_norm(kind, &x, res ? &r : nullptr, &d, eps, w, b, c->stream), nrm);
+    return used;
 }
 
 // a MUL_MAT whose activation and result rows can be walked as one matrix

@@ -18,6 +18,7 @@
 
 #include "../../include/mq.h"
 #include "../../include/mq_bert.h"
+#include "../../include/mq_ops.h"
 #include "mq_internal.h"
 #include "mq_runner.h"
 
@@ -144,6 +145,42 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
     auto mm = [&](const Linear &L, const float *in, float *y) {
         return mq_mul_mat(t, L.img.p, L.n, L.k, in, L.k, rows, y, L.n, m->ws.p, m->ws.bytes, s);
     };
+    // Q8_0 with every product on the GEMM path: each post-LN norm also leaves its result
+    // quantized for the GEMM that reads it (mq_op_norm_q8_0), the o and FFN-down biases go into
+    // the GEMM stores, and the FFN intermediate never leaves the FFN-up GEMM (above).
+    const bool norm_fused = ffn_fused && H % 128 == 0 && H <= 1024 &&
+                            mq_mul_mat_path(t, 3 * H, H, rows) == MQ_PATH_GEMM &&
+                            mq_mul_mat_path(t, H, H, rows) == MQ_PATH_GEMM;
+    if (norm_fused) {
+        mq_view xv{};
+        xv.data = X;
+        xv.type = MQ_TYPE_F32;
+        xv.ne[0] = H, xv.ne[1] = rows, xv.ne[2] = 1, xv.ne[3] = 1;
+        xv.nb[0] = 4, xv.nb[1] = 4 * H, xv.nb[2] = xv.nb[3] = 4 * H * rows;
+        mq_view yv = xv;
+        yv.data = m->y.f();
+        const int G = MQ_PATH_GEMM;
+        if ((rc = mq_quantize_act_ex(t, X, H, rows, H, nullptr, MQ_PRE_NONE, m->ws.p, m->ws.bytes, G, s))) return rc;
+        for (const Layer &L : m->layers) {  // m->ws holds X quantized at the top of each layer
+            if ((rc = mq_mul_mat_q(t, L.qkv.img.p, L.qkv.n, L.qkv.k, m->ws.p, rows, m->qkv.f(), L.qkv.n, G, s)))
+                return rc;
+            if ((rc = hip_rc(launch_attention(m->qkv.f(), L.bqkv.f(), m->att.f(), B, T, (int)H, hp.n_head, s),
+                             "attention")))
+                return rc;
+            if ((rc = mq_quantize_act_ex(t, m->att.f(), H, rows, H, nullptr, MQ_PRE_NONE, m->ws.p, m->ws.bytes, G, s)) ||
+                (rc = mq_mul_mat_q_ex(t, L.o.img.p, L.o.n, L.o.k, m->ws.p, rows, m->y.f(), L.o.n, L.bo.f(), G, s)) ||
+                (rc = mq_op_norm_q8_0(MQ_NORM_LAYER, &xv, &yv, &xv, eps, L.ln1w.f(), L.ln1b.f(), m->ws.p, m->ws.bytes,
+                                      s)) ||
+                (rc = mq_mul_mat_q_requant(t, L.fc1.img.p, L.fc1.n, L.fc1.k, m->ws.p, rows, L.b1.f(), MQ_PRE_GELU_ERF,
+                                           MQ_TYPE_Q8_0, m->ws2.p, m->ws2.bytes, s)) ||
+                (rc = mq_mul_mat_q_ex(t, L.fc2.img.p, L.fc2.n, L.fc2.k, m->ws2.p, rows, m->y.f(), L.fc2.n, L.b2.f(), G,
+                                      s)) ||
+                (rc = mq_op_norm_q8_0(MQ_NORM_LAYER, &xv, &yv, &xv, eps, L.ln2w.f(), L.ln2b.f(), m->ws.p, m->ws.bytes,
+                                      s)))
+                return rc;
+        }
+        return hip_rc(launch_mean_pool_l2(X, out, B, T, (int)H, s), "pooling");
+    }
     for (const Layer &L : m->layers) {
         if ((rc = mm(L.qkv, X, m->qkv.f()))) return rc;
         if ((rc = hip_rc(launch_attention(m->qkv.f(), L.bqkv.f(), m->att.f(), B, T, (int)H, hp.n_head, s), "attention")))

@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "../../include/mq_ops.h"
+#include "mq_act.h"
 #include "mq_deq.h"
 #include "mq_internal.h"
 #include "mq_runner.h"
@@ -185,6 +186,127 @@ __global__ __launch_bounds__(256) void k_norm(const DV x, const DV r, const DV d
             dr[c] = y;
         }
     }
+}
+
+// k_norm on dense rows of K = 128 NV floats whose result also leaves as the Q8_0 activation
+// of the mat-mul that reads it, in the GEMM layout the tiled activation quantizer writes
+// (1 KB fragments per 32-row tile and 32-value chunk: lane l's 16 bytes are row l % 32,
+// bytes 16 (l / 32) ..; scales [K / 32][m_pad], pad rows of the tile quantized as zeros).
+// Workgroup: one 32-row tile, NW waves; half a wave takes a row, lane s holding values
+// 4 s + 128 p (p < NV) as float4, so a Q8_0 block is 8 lanes (a 3-step xor max) and the row
+// sums are 5-step half-wave xor sums.  Quants go through LDS to leave as whole fragments.
+// Same arithmetic as k_norm (sum, mean, centred sum of squares, 1 / sqrt(var + eps), then
+// * w, + b), with the sums taken in this lane order; quantization as quantize_row_q8_0.
+template <int KIND, int NV, int NW>
+__global__ __launch_bounds__(64 * NW) void k_norm_q8_0(const float *x, const float *r, float *d, float eps,  // d may be x
+                                                       const float *__restrict__ w,
+                                                       const float *__restrict__ bias, int64_t nrows,
+                                                       int8_t *__restrict__ xq, float *__restrict__ xd, int64_t m_pad,
+                                                       int variant) {
+    constexpr int K = 128 * NV, NCH = K / 32, FST = 1024 + 16;
+    constexpr int RPW = 32 / NW, NIT = RPW / 2;  // rows per wave, passes of two rows
+    static_assert(NIT >= 1, "at most 16 waves");
+    __shared__ __attribute__((aligned(16))) int8_t frag[NCH * FST];
+    __shared__ float dsh[NCH][32];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane & 31, half = lane >> 5;
+    const int64_t rt = blockIdx.x;
+    const float inv_n = 1.0f / (float)K;
+    float4 v[NIT][NV];
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int64_t row = rt * 32 + wave * RPW + it * 2 + half;
+#pragma unroll
+        for (int p = 0; p < NV; p++) {
+            v[it][p] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (row < nrows) {
+                const int64_t o = row * K + 128 * p + 4 * sub;
+                float4 a = *(const float4 *)(x + o);
+                if (r) {
+                    const float4 c = *(const float4 *)(r + o);
+                    a.x = a.x + c.x, a.y = a.y + c.y, a.z = a.z + c.z, a.w = a.w + c.w;
+                }
+                v[it][p] = a;
+            }
+        }
+    }
+    float4 wv[NV], bv[NV];
+#pragma unroll
+    for (int p = 0; p < NV; p++) {
+        wv[p] = w ? *(const float4 *)(w + 128 * p + 4 * sub) : make_float4(1.f, 1.f, 1.f, 1.f);
+        bv[p] = bias ? *(const float4 *)(bias + 128 * p + 4 * sub) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    auto hsum = [](float t) {
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) t += __shfl_xor(t, o);
+        return t;
+    };
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int rr = wave * RPW + it * 2 + half;  // row within the tile
+        const int64_t row = rt * 32 + rr;
+        float mean = 0.f, s = 0.f;
+#pragma unroll
+        for (int p = 0; p < NV; p++) {
+            const float4 a = v[it][p];
+            if (KIND == MQ_NORM_LAYER) s += a.x + a.y + a.z + a.w;
+            else s += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+        }
+        float scale;
+        if (KIND == MQ_NORM_LAYER) {
+            mean = hsum(s) * inv_n;
+            float s2 = 0.f;
+#pragma unroll
+            for (int p = 0; p < NV; p++) {
+                const float4 a = v[it][p];
+                const float t0 = a.x - mean, t1 = a.y - mean, t2 = a.z - mean, t3 = a.w - mean;
+                s2 += t0 * t0 + t1 * t1 + t2 * t2 + t3 * t3;
+            }
+            scale = 1.0f / sqrtf(hsum(s2) * inv_n + eps);
+        } else {
+            scale = 1.0f / sqrtf(hsum(s) * inv_n + eps);
+        }
+#pragma unroll
+        for (int p = 0; p < NV; p++) {
+            const float4 a = v[it][p];
+            float y[4] = {a.x, a.y, a.z, a.w};
+            const float ww[4] = {wv[p].x, wv[p].y, wv[p].z, wv[p].w}, bb[4] = {bv[p].x, bv[p].y, bv[p].z, bv[p].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float t = (y[e] - mean) * scale;
+                if (w) t = t * ww[e];
+                if (bias) t = t + bb[e];
+                y[e] = row < nrows ? t : 0.f;  // pad rows of the tile quantize to zero
+            }
+            if (row < nrows) *(float4 *)(d + row * K + 128 * p + 4 * sub) = make_float4(y[0], y[1], y[2], y[3]);
+            float amax = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
+            amax = fmaxf(amax, __shfl_xor(amax, 1));
+            amax = fmaxf(amax, __shfl_xor(amax, 2));
+            amax = fmaxf(amax, __shfl_xor(amax, 4));
+            const float dq = amax / 127.f;
+            float id;
+            if (variant == MQ_Q8_0_X86) id = (amax != 0.0f) ? 127.f / amax : 0.0f;
+            else id = (dq != 0.0f) ? 1.0f / dq : 0.0f;
+            uint32_t pk = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float t = y[e] * id;
+                float q = (variant == MQ_Q8_0_REF) ? roundf(t) : rintf(t);
+                q = fminf(fmaxf(q, -128.f), 127.f);
+                pk |= ((uint32_t)((int)q & 0xff)) << (8 * e);
+            }
+            const int c = 4 * p + (sub >> 3), cbyte = 4 * (sub & 7);  // chunk, byte within it
+            *(uint32_t *)(frag + c * FST + ((rr + 32 * (cbyte >> 4)) << 4) + (cbyte & 15)) = pk;
+            if ((sub & 7) == 0) dsh[c][rr] = f16_bits_to_f32(f32_to_f16_bits(dq));
+        }
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+    for (int q = t; q < NCH * 64; q += 64 * NW) {
+        const int f = q >> 6, L = q & 63;
+        *(int4 *)(xq + ((rt * NCH + f) << 10) + L * 16) = *(const int4 *)(frag + f * FST + L * 16);
+    }
+    for (int q = t; q < NCH * 32; q += 64 * NW) xd[(int64_t)(q >> 5) * m_pad + rt * 32 + (q & 31)] = dsh[q >> 5][q & 31];
 }
 
 template <typename S>
@@ -656,6 +778,53 @@ extern "C" int mq_op_norm(int kind, const mq_view *x, const mq_view *add, const 
     if (kind == MQ_NORM_LAYER) launch_norm_kind<MQ_NORM_LAYER>(x, add, dst, eps, w, b, s);
     else launch_norm_kind<MQ_NORM_RMS>(x, add, dst, eps, w, b, s);
     return hip_rc(hipGetLastError(), "norm");
+}
+
+template <int KIND>
+static void launch_norm_q8_0_kind(int nv, const float *x, const float *r, float *d, float eps, const float *w,
+                                  const float *b, int64_t rows, int8_t *xq, float *xd, int64_t m_pad, int variant,
+                                  hipStream_t s) {
+    constexpr int NW = 8;
+    const dim3 grid((unsigned)((rows + 31) / 32)), block(64 * NW);
+    switch (nv) {
+#define MQ_NQ(NV)                                                                                                      \
+    case NV:                                                                                                           \
+        hipLaunchKernelGGL((k_norm_q8_0<KIND, NV, NW>), grid, block, 0, s, x, r, d, eps, w, b, rows, xq, xd, m_pad,   \
+                           variant);                                                                                   \
+        break;
+        MQ_NQ(1) MQ_NQ(2) MQ_NQ(3) MQ_NQ(4) MQ_NQ(5) MQ_NQ(6) MQ_NQ(7) MQ_NQ(8)
+#undef MQ_NQ
+        default: break;
+    }
+}
+
+extern "C" int mq_op_norm_q8_0(int kind, const mq_view *x, const mq_view *add, const mq_view *dst, float eps,
+                               const float *w, const float *b, void *workspace, size_t workspace_bytes, void *stream) {
+    if (const char *e = check_norm(kind, x, add, dst)) return fail(e);
+    if (!have_data({x, add, dst}) || !workspace) return fail("missing data pointer");
+    const int64_t K = x->ne[0], rows = x->ne[1] * x->ne[2] * x->ne[3];
+    if (K % 128 != 0 || K > 1024) return fail("norm_q8_0: ne0 must be a multiple of 128, at most 1024");
+    for (const mq_view *t : {x, add, dst})
+        if (t && (t->nb[1] != (size_t)K * 4 || t->nb[2] != t->nb[1] * (size_t)t->ne[1] ||
+                  t->nb[3] != t->nb[2] * (size_t)t->ne[2] || ((uintptr_t)t->data & 15)))
+            return fail("norm_q8_0: x, add and dst must be dense, 16-byte aligned rows");
+    if (((uintptr_t)w & 15) || ((uintptr_t)b & 15) || ((uintptr_t)workspace & 255))
+        return fail("norm_q8_0: w and b 16-byte, the workspace 256-byte aligned");
+    if (rows > INT32_MAX) return fail("norm_q8_0: too many rows");
+    const ActPlanes ap = act_planes(MQ_TYPE_Q8_0, rows, K, true);
+    if (ap.kb_pad != K) return fail("norm_q8_0: K padding");
+    if (workspace_bytes < ap.total) return fail("norm_q8_0: workspace too small");
+    uint8_t *ws = (uint8_t *)workspace;
+    hipStream_t s = (hipStream_t)stream;
+    const float *r = add ? (const float *)add->data : nullptr;
+    const int var = mq_q8_0_variant();
+    if (kind == MQ_NORM_LAYER)
+        launch_norm_q8_0_kind<MQ_NORM_LAYER>((int)(K / 128), (const float *)x->data, r, (float *)dst->data, eps, w, b,
+                                             rows, (int8_t *)(ws + ap.xq), (float *)(ws + ap.xd), ap.m_pad, var, s);
+    else
+        launch_norm_q8_0_kind<MQ_NORM_RMS>((int)(K / 128), (const float *)x->data, r, (float *)dst->data, eps, w, b,
+                                           rows, (int8_t *)(ws + ap.xq), (float *)(ws + ap.xd), ap.m_pad, var, s);
+    return hip_rc(hipGetLastError(), "norm_q8_0");
 }
 
 extern "C" int mq_op_cpy(const mq_view *src, const mq_view *dst, void *stream) {

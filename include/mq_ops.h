@@ -83,6 +83,17 @@ int mq_op_unary(int op, const mq_view *x, const mq_view *dst, void *stream);
 int mq_op_norm(int kind, const mq_view *x, const mq_view *add, const mq_view *dst, float eps, const float *w,
                const float *b, void *stream);
 
+/* mq_op_norm whose result also leaves quantized for the mat-mul that reads it: dst as
+ * mq_op_norm writes it (the sums taken in another lane order, so the last bit may differ), and
+ * dst's rows quantized to Q8_0 in the GEMM-path activation layout -- the bytes
+ * mq_quantize_act_ex(MQ_TYPE_Q8_0, dst, ..., MQ_PATH_GEMM) would write -- into workspace
+ * (>= mq_workspace_bytes(MQ_TYPE_Q8_0, rows, ne0)).  The post-LN norm of
+ * src/crispembed.cpp:1320-1323 and the from_float quantization of the q/k/v or FFN-up
+ * MUL_MAT that reads it (src/crispembed.cpp:1168-1170,1410), in one pass.  x, add and dst
+ * have dense, 16-byte aligned rows of ne0 floats, ne0 a multiple of 128 and at most 1024. */
+int mq_op_norm_q8_0(int kind, const mq_view *x, const mq_view *add, const mq_view *dst, float eps, const float *w,
+                    const float *b, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Copies src into dst element by element in logical (row-major over ne0..ne3) order; the two
  * views hold the same number of elements and may differ in shape and strides (ggml_cpy,
  * ggml_cont, ggml_dup).  F32 / F16 either side (F32 -> F16 rounds to nearest even). */

@@ -61,3 +61,16 @@ def mul_mat(wtype, wptr, n, k, x_dev, path=mq.PATH_AUTO, y_dev=None, ldy=None, w
                              ctypes.c_void_p(y_dev.data_ptr()), ldy, ws_ptr, ws_bytes, path, stream()))
     torch().cuda.synchronize()
     return y_dev
+
+
+def live_q8_0_planes(raw, m, k):
+    """The Q8_0 GEMM-layout activation planes (quants in 1 KB fragments per 32-row tile and
+    32-value chunk, scales [k / 32][m_pad]) of rows < m, as a row-major int8 [m][k] and a
+    float32 [k / 32][m]; k a multiple of 128, m_pad = m rounded up to 256."""
+    m_pad = -(-m // 256) * 256
+    kch = k // 32
+    q = raw[:m_pad * k].reshape(m_pad // 32, kch, 2, 32, 16)   # [row tile][chunk][half][row][byte]
+    q = q.transpose(0, 3, 1, 2, 4).reshape(m_pad, k)[:m]
+    off = -(-(m_pad * k) // 256) * 256
+    d = raw[off:off + kch * m_pad * 4].view(np.float32).reshape(kch, m_pad)[:, :m]
+    return q, d

@@ -190,6 +190,62 @@ def test_norm(kind, n):
     assert np.abs(host(dx) - ref2).max() <= 5e-6 * np.abs(ref2).max()
 
 
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("n,rows", [(128, 37), (384, 4096), (768, 300), (1024, 70)])
+def test_norm_q8_0(kind, n, rows):
+    """mq_op_norm_q8_0: the residual + norm + scale + shift of mq_op_norm, its fp32 result within
+    the norm bar of the fp64 reference, and the quantized activation it leaves bit-identical to
+    the activation quantizer run on that result (GEMM layout, every live row)."""
+    from gpu_util import empty_u8, live_q8_0_planes
+    L = mq.lib()
+    kind = mq.NORM_LAYER if kind == 0 else mq.NORM_RMS
+    x = (_rng(20 + n).standard_normal((rows, n)) * 2 + 0.5).astype(np.float32)
+    r = _rng(21 + n).standard_normal((rows, n)).astype(np.float32)
+    w = _rng(22).standard_normal(n).astype(np.float32)
+    b = _rng(23).standard_normal(n).astype(np.float32)
+    eps = 1e-12 if kind == mq.NORM_LAYER else 1e-6
+    s64 = (x + r).astype(np.float64)
+    if kind == mq.NORM_LAYER:
+        y = (s64 - s64.mean(-1, keepdims=True)) / np.sqrt(s64.var(-1, keepdims=True) + eps)
+    else:
+        y = s64 / np.sqrt((s64 ** 2).mean(-1, keepdims=True) + eps)
+    ref = y * w + b
+    dx, dr, dw, db = _cuda(x), _cuda(r), _cuda(w), _cuda(b)
+    out = _t().empty_like(dx)
+    nb = L.mq_workspace_bytes(mq.TYPE_Q8_0, rows, n)
+    ws, off = empty_u8(nb)
+    ws.fill_(0xAB)
+    _call(L.mq_op_norm_q8_0, kind, mq.view(dx), mq.view(dr), mq.view(out), eps, ctypes.c_void_p(dw.data_ptr()),
+          ctypes.c_void_p(db.data_ptr()), ctypes.c_void_p(ws.data_ptr() + off), nb, stream())
+    got = host(out)
+    assert np.abs(got - ref).max() <= 5e-6 * np.abs(ref).max()
+    ws2, off2 = empty_u8(nb)
+    mq.check(L.mq_quantize_act_ex(mq.TYPE_Q8_0, ctypes.c_void_p(out.data_ptr()), n, rows, n, None, 0,
+                                  ctypes.c_void_p(ws2.data_ptr() + off2), nb, mq.PATH_GEMM, stream()))
+    qa, da = live_q8_0_planes(host(ws2)[off2:off2 + nb], rows, n)
+    qb, db_ = live_q8_0_planes(host(ws)[off:off + nb], rows, n)
+    assert np.array_equal(qa, qb)
+    assert np.array_equal(da.view(np.uint32), db_.view(np.uint32))
+    # in place over x, no w / b: the same as mq_op_norm's result within the bar
+    _call(L.mq_op_norm_q8_0, kind, mq.view(dx), None, mq.view(dx), eps, None, None,
+          ctypes.c_void_p(ws.data_ptr() + off), nb, stream())
+    x64 = x.astype(np.float64)
+    if kind == mq.NORM_LAYER:
+        y0 = (x64 - x64.mean(-1, keepdims=True)) / np.sqrt(x64.var(-1, keepdims=True) + eps)
+    else:
+        y0 = x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + eps)
+    assert np.abs(host(dx) - y0).max() <= 5e-6 * np.abs(y0).max()
+
+
+def test_norm_q8_0_refusals():
+    L = mq.lib()
+    x = _cuda(np.zeros((4, 200), np.float32))
+    ws = _t().empty(1 << 20, dtype=_t().uint8, device="cuda")
+    rc = L.mq_op_norm_q8_0(mq.NORM_LAYER, mq.view(x), None, mq.view(x), 1e-5, None, None,
+                           ctypes.c_void_p(ws.data_ptr()), 1 << 20, stream())
+    assert rc == -2 and b"multiple of 128" in L.mq_last_error()
+
+
 # ----------------------------------------------------------------------- cpy ----
 def test_cpy_cont_of_permute_and_qkv_slices():
     L = mq.lib()

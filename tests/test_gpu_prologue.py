@@ -16,7 +16,7 @@ from scipy.special import erf
 
 import oracle_ffi as O
 from ggml_numpy import rel_err
-from gpu_util import dev, empty_u8, host, stream, weight_image
+from gpu_util import dev, empty_u8, host, live_q8_0_planes, stream, weight_image
 
 pytestmark = pytest.mark.gpu
 
@@ -163,17 +163,6 @@ def test_mul_mat_q_group_equals_separate(wtype, m, k, path):
     del imgs, ws
 
 
-def _live_planes(raw, m, n):
-    """The Q8_0 GEMM-layout planes (tiled quants, block-major scales) of rows < m, as arrays."""
-    m_pad = -(-m // 256) * 256
-    kch = n // 32
-    q = raw[:m_pad * n].reshape(m_pad // 32, kch, 2, 32, 16)   # [row tile][chunk][half][row][byte]
-    q = q.transpose(0, 3, 1, 2, 4).reshape(m_pad, n)[:m]        # row-major quants
-    off = -(-(m_pad * n) // 256) * 256
-    d = raw[off:off + kch * m_pad * 4].view(np.float32).reshape(kch, m_pad)[:, :m]
-    return q, d
-
-
 @pytest.mark.parametrize("wtype", TYPES)
 @pytest.mark.parametrize("m,k,n,op,with_bias", [(37, 512, 384, 1, True), (300, 384, 1536, 1, True),
                                                 (1000, 512, 512, 0, False), (4096, 384, 1536, 1, True),
@@ -210,8 +199,8 @@ def test_mul_mat_q_requant_equals_separate(wtype, m, k, n, op, with_bias):
     mq.check(L.mq_mul_mat_q_requant(wtype, ctypes.c_void_p(img[1]), n, k, ctypes.c_void_p(ptr), m, bptr, op,
                                     O.Q8_0, ctypes.c_void_p(optr), nb, stream()))
     got_raw = host(out)[off:off + nb]
-    qa, da = _live_planes(ref_raw, m, n)
-    qb, db = _live_planes(got_raw, m, n)
+    qa, da = live_q8_0_planes(ref_raw, m, n)
+    qb, db = live_q8_0_planes(got_raw, m, n)
     assert np.array_equal(qa, qb)
     assert np.array_equal(da.view(np.uint32), db.view(np.uint32))
     # the next mat-mul reads either workspace to the same result
@@ -251,8 +240,8 @@ def test_mul_mat_q_requant_variants(variant):
                                         ctypes.c_void_p(bias.data_ptr()), 1, O.Q8_0,
                                         ctypes.c_void_p(out.data_ptr() + off), nb, stream()))
         got_raw = host(out)[off:off + nb]
-        qa, da = _live_planes(ref_raw, m, n)
-        qb, db = _live_planes(got_raw, m, n)
+        qa, da = live_q8_0_planes(ref_raw, m, n)
+        qb, db = live_q8_0_planes(got_raw, m, n)
         assert np.array_equal(qa, qb)
         assert np.array_equal(da.view(np.uint32), db.view(np.uint32))
         del img, ws
