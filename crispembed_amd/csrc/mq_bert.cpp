@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <vector>
 
@@ -48,7 +49,7 @@ struct mq_bert {
     mq_bert_hparams hp{};
     DevBuf tok, pos, type, lnw, lnb;
     std::vector<Layer> layers;
-    DevBuf x, qkv, att, y, ff, ws, ws2;
+    DevBuf x, qkv, att, y, ff, ws, ws2, aws;
     int64_t rows_cap = 0;
 };
 
@@ -148,10 +149,31 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
     // Q8_0 with every product on the GEMM path: each post-LN norm also leaves its result
     // quantized for the GEMM that reads it (mq_op_norm_q8_0), the o and FFN-down biases go into
     // the GEMM stores, and the FFN intermediate never leaves the FFN-up GEMM (above).
-    const bool norm_fused = ffn_fused && H % 128 == 0 && H <= 1024 &&
+    // Attention there is the fragment attention of FLASH_ATTN_EXT on strided views of the qkv
+    // rows (the q/k/v biases added by the qkv GEMM's store).
+    const int hd = (int)(H / hp.n_head);
+    const bool norm_fused = ffn_fused && H % 128 == 0 && H <= 1024 && (hd == 32 || hd == 64 || hd == 128) &&
                             mq_mul_mat_path(t, 3 * H, H, rows) == MQ_PATH_GEMM &&
                             mq_mul_mat_path(t, H, H, rows) == MQ_PATH_GEMM;
     if (norm_fused) {
+        auto strided = [&](float *p, int64_t ld) {  // [hd, T, n_head, B] over rows of ld floats
+            mq_view v{};
+            v.data = p;
+            v.type = MQ_TYPE_F32;
+            v.ne[0] = hd, v.ne[1] = T, v.ne[2] = hp.n_head, v.ne[3] = B;
+            v.nb[0] = 4, v.nb[1] = 4 * ld, v.nb[2] = 4 * (size_t)hd, v.nb[3] = 4 * ld * T;
+            return v;
+        };
+        const mq_view qv = strided(m->qkv.f(), 3 * H), kv = strided(m->qkv.f() + H, 3 * H),
+                      vv = strided(m->qkv.f() + 2 * H, 3 * H);
+        mq_view ov{};  // [hd, n_head, T, B]: rows of H floats
+        ov.data = m->att.f();
+        ov.type = MQ_TYPE_F32;
+        ov.ne[0] = hd, ov.ne[1] = hp.n_head, ov.ne[2] = T, ov.ne[3] = B;
+        ov.nb[0] = 4, ov.nb[1] = 4 * (size_t)hd, ov.nb[2] = 4 * H, ov.nb[3] = 4 * H * T;
+        if (!m->aws.ensure(mq_op_flash_attn_workspace_bytes(&kv)))
+            return set_error(MQ_ENOMEM, "attention workspace for %lld rows", (long long)rows);
+        const float ascale = 1.0f / std::sqrt((float)hd);
         mq_view xv{};
         xv.data = X;
         xv.type = MQ_TYPE_F32;
@@ -162,10 +184,9 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
         const int G = MQ_PATH_GEMM;
         if ((rc = mq_quantize_act_ex(t, X, H, rows, H, nullptr, MQ_PRE_NONE, m->ws.p, m->ws.bytes, G, s))) return rc;
         for (const Layer &L : m->layers) {  // m->ws holds X quantized at the top of each layer
-            if ((rc = mq_mul_mat_q(t, L.qkv.img.p, L.qkv.n, L.qkv.k, m->ws.p, rows, m->qkv.f(), L.qkv.n, G, s)))
-                return rc;
-            if ((rc = hip_rc(launch_attention(m->qkv.f(), L.bqkv.f(), m->att.f(), B, T, (int)H, hp.n_head, s),
-                             "attention")))
+            if ((rc = mq_mul_mat_q_ex(t, L.qkv.img.p, L.qkv.n, L.qkv.k, m->ws.p, rows, m->qkv.f(), L.qkv.n,
+                                      L.bqkv.f(), G, s)) ||
+                (rc = mq_op_flash_attn(&qv, &kv, &vv, nullptr, &ov, ascale, m->aws.p, m->aws.bytes, s)))
                 return rc;
             if ((rc = mq_quantize_act_ex(t, m->att.f(), H, rows, H, nullptr, MQ_PRE_NONE, m->ws.p, m->ws.bytes, G, s)) ||
                 (rc = mq_mul_mat_q_ex(t, L.o.img.p, L.o.n, L.o.k, m->ws.p, rows, m->y.f(), L.o.n, L.bo.f(), G, s)) ||

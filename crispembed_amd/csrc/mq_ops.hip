@@ -192,30 +192,33 @@ __global__ __launch_bounds__(256) void k_norm(const DV x, const DV r, const DV d
 // of the mat-mul that reads it, in the GEMM layout the tiled activation quantizer writes
 // (1 KB fragments per 32-row tile and 32-value chunk: lane l's 16 bytes are row l % 32,
 // bytes 16 (l / 32) ..; scales [K / 32][m_pad], pad rows of the tile quantized as zeros).
-// Workgroup: one 32-row tile, NW waves; half a wave takes a row, lane s holding values
-// 4 s + 128 p (p < NV) as float4, so a Q8_0 block is 8 lanes (a 3-step xor max) and the row
-// sums are 5-step half-wave xor sums.  Quants go through LDS to leave as whole fragments.
+// Workgroup: RT rows (16: half of a 32-row tile, so a 4096-row input gives every CU a
+// workgroup), NW waves; half a wave takes a row, lane s holding values 4 s + 128 p (p < NV) as
+// float4, so a Q8_0 block is 8 lanes (a 3-step xor max) and the row sums are 5-step half-wave
+// xor sums.  Quants go through LDS and leave as the 16-byte lane units of this workgroup's
+// rows in each fragment (lanes r and r + 32 for its rows r): 256-byte contiguous runs.
 // Same arithmetic as k_norm (sum, mean, centred sum of squares, 1 / sqrt(var + eps), then
 // * w, + b), with the sums taken in this lane order; quantization as quantize_row_q8_0.
-template <int KIND, int NV, int NW>
+template <int KIND, int NV, int NW, int RT>
 __global__ __launch_bounds__(64 * NW) void k_norm_q8_0(const float *x, const float *r, float *d, float eps,  // d may be x
                                                        const float *__restrict__ w,
                                                        const float *__restrict__ bias, int64_t nrows,
                                                        int8_t *__restrict__ xq, float *__restrict__ xd, int64_t m_pad,
                                                        int variant) {
     constexpr int K = 128 * NV, NCH = K / 32, FST = 1024 + 16;
-    constexpr int RPW = 32 / NW, NIT = RPW / 2;  // rows per wave, passes of two rows
-    static_assert(NIT >= 1, "at most 16 waves");
+    constexpr int RPW = RT / NW, NIT = RPW / 2;  // rows per wave, passes of two rows
+    static_assert((RT == 16 || RT == 32) && NIT >= 1 && RPW % 2 == 0, "16 or 32 rows, whole passes");
     __shared__ __attribute__((aligned(16))) int8_t frag[NCH * FST];
     __shared__ float dsh[NCH][32];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane & 31, half = lane >> 5;
-    const int64_t rt = blockIdx.x;
+    const int64_t rt = blockIdx.x / (32 / RT);             // 32-row tile
+    const int r0 = (int)(blockIdx.x % (32 / RT)) * RT;     // first row of this workgroup in it
     const float inv_n = 1.0f / (float)K;
     float4 v[NIT][NV];
 #pragma unroll
     for (int it = 0; it < NIT; it++) {
-        const int64_t row = rt * 32 + wave * RPW + it * 2 + half;
+        const int64_t row = rt * 32 + r0 + wave * RPW + it * 2 + half;
 #pragma unroll
         for (int p = 0; p < NV; p++) {
             v[it][p] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -243,7 +246,7 @@ __global__ __launch_bounds__(64 * NW) void k_norm_q8_0(const float *x, const flo
     };
 #pragma unroll
     for (int it = 0; it < NIT; it++) {
-        const int rr = wave * RPW + it * 2 + half;  // row within the tile
+        const int rr = r0 + wave * RPW + it * 2 + half;  // row within the tile
         const int64_t row = rt * 32 + rr;
         float mean = 0.f, s = 0.f;
 #pragma unroll
@@ -302,11 +305,14 @@ __global__ __launch_bounds__(64 * NW) void k_norm_q8_0(const float *x, const flo
     }
     __syncthreads();
     const int t = threadIdx.x;
-    for (int q = t; q < NCH * 64; q += 64 * NW) {
-        const int f = q >> 6, L = q & 63;
+    constexpr int UPF = 2 * RT;  // 16-byte lane units of this workgroup's rows per fragment
+    for (int q = t; q < NCH * UPF; q += 64 * NW) {
+        const int f = q / UPF, u = q % UPF;
+        const int L = r0 + (u % RT) + 32 * (u / RT);  // lane of row r0 + u % RT, half u / RT
         *(int4 *)(xq + ((rt * NCH + f) << 10) + L * 16) = *(const int4 *)(frag + f * FST + L * 16);
     }
-    for (int q = t; q < NCH * 32; q += 64 * NW) xd[(int64_t)(q >> 5) * m_pad + rt * 32 + (q & 31)] = dsh[q >> 5][q & 31];
+    for (int q = t; q < NCH * RT; q += 64 * NW)
+        xd[(int64_t)(q / RT) * m_pad + rt * 32 + r0 + (q % RT)] = dsh[q / RT][r0 + (q % RT)];
 }
 
 template <typename S>
@@ -784,13 +790,13 @@ template <int KIND>
 static void launch_norm_q8_0_kind(int nv, const float *x, const float *r, float *d, float eps, const float *w,
                                   const float *b, int64_t rows, int8_t *xq, float *xd, int64_t m_pad, int variant,
                                   hipStream_t s) {
-    constexpr int NW = 8;
-    const dim3 grid((unsigned)((rows + 31) / 32)), block(64 * NW);
+    constexpr int NW = 8, RT = 16;
+    const dim3 grid((unsigned)((rows + 31) / 32 * (32 / RT))), block(64 * NW);
     switch (nv) {
 #define MQ_NQ(NV)                                                                                                      \
     case NV:                                                                                                           \
-        hipLaunchKernelGGL((k_norm_q8_0<KIND, NV, NW>), grid, block, 0, s, x, r, d, eps, w, b, rows, xq, xd, m_pad,   \
-                           variant);                                                                                   \
+        hipLaunchKernelGGL((k_norm_q8_0<KIND, NV, NW, RT>), grid, block, 0, s, x, r, d, eps, w, b, rows, xq, xd,       \
+                           m_pad, variant);                                                                            \
         break;
         MQ_NQ(1) MQ_NQ(2) MQ_NQ(3) MQ_NQ(4) MQ_NQ(5) MQ_NQ(6) MQ_NQ(7) MQ_NQ(8)
 #undef MQ_NQ
