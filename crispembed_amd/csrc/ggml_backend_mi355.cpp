@@ -14,6 +14,8 @@
 // (ggml_node_get_use_count == 1) and are not graph outputs:
 //   MUL_MAT [-> ADD(bias)], with the MUL_MATs after it on the same activation
 //                                                  one grouped GEMM, biases added by its store
+//   FLASH_ATTN_EXT -> (views) -> MUL_MAT(Q8_0)     the attention also quantizes its result
+//                                                  for the projection (mq_op_flash_attn_q8_0)
 //   [ADD(residual) ->] NORM|RMS_NORM -> MUL(w) [-> ADD(b)]
 //                                                  one row pass (mq_op_norm); before a Q8_0
 //                                                  MUL_MAT it also quantizes the result for it
@@ -599,6 +601,41 @@ int try_fuse_ffn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status 
     return dst == mm2 ? 4 : 5;
 }
 
+// FLASH_ATTN_EXT whose result (after view nodes, as rows of n_head * head_dim) is read by a
+// Q8_0 MUL_MAT on the GEMM path (the output projection): the attention also leaves it quantized
+// for that MUL_MAT (mq_op_flash_attn_q8_0) and the activation cache lets the MUL_MAT skip the
+// quantizer.  The quantized rows sit at the workspace start, the K/V fragments after them.
+int try_fuse_attn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status &st) {
+    ggml_tensor *node = ggml_graph_node(cg, i);
+    int nx = i + 1;
+    while (nx < n && (ggml_is_empty(ggml_graph_node(cg, nx)) || is_view_op(ggml_graph_node(cg, nx)->op))) nx++;
+    if (nx >= n) return 0;
+    const ggml_tensor *mm = ggml_graph_node(cg, nx);
+    if (mm->op != GGML_OP_MUL_MAT || mm->src[0]->type != GGML_TYPE_Q8_0 || !flat_mul_mat(mm)) return 0;
+    const ggml_tensor *x = mm->src[1];
+    if (x != node && (x->view_src != node || x->view_offs != 0)) return 0;
+    const int64_t K = x->ne[0], M = x->ne[1] * x->ne[2] * x->ne[3];
+    if (K != node->ne[0] * node->ne[1] || M != node->ne[2] * node->ne[3] || K % 128 != 0 ||
+        x->nb[1] != (size_t)K * sizeof(float) || node->nb[1] != (size_t)node->ne[0] * sizeof(float) ||
+        node->nb[2] != (size_t)K * sizeof(float) || node->nb[3] != node->nb[2] * (size_t)node->ne[2])
+        return 0;
+    if (mq_mul_mat_path(MQ_TYPE_Q8_0, mm->src[0]->ne[1], K, M) != MQ_PATH_GEMM) return 0;
+    const mq_view q = view_of(node->src[0]), k = view_of(node->src[1]), v = view_of(node->src[2]), d = view_of(node);
+    mq_view m{};
+    if (node->src[3]) m = view_of(node->src[3]);
+    const size_t act = (mq_workspace_bytes(MQ_TYPE_Q8_0, M, K) + 255) & ~(size_t)255;
+    c->ws_x = nullptr;
+    if (!ensure_ws(c, act + mq_op_flash_attn_workspace_bytes(&k))) {
+        st = GGML_STATUS_ALLOC_FAILED;
+        return 1;
+    }
+    const int rc = mq_op_flash_attn_q8_0(&q, &k, &v, node->src[3] ? &m : nullptr, &d, op_param_f32(node, 0),
+                                         (char *)c->ws + act, c->ws_bytes - act, c->ws, act, c->stream);
+    if (rc == 0) c->ws_x = x, c->ws_type = MQ_TYPE_Q8_0, c->ws_m = M, c->ws_k = K, c->ws_path = MQ_PATH_GEMM;
+    st = op_status(rc, node);
+    return 1;
+}
+
 // A MUL_MAT of a group and the bias ADD fused into its store (add_idx < 0: none).
 struct MulMatMember {
     ggml_tensor *mm, *dst;
@@ -790,6 +827,7 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
                     break;
                 case GGML_OP_NORM:
                 case GGML_OP_RMS_NORM: used = try_fuse_norm(c, cg, i, n, st); break;
+                case GGML_OP_FLASH_ATTN_EXT: used = try_fuse_attn(c, cg, i, n, st); break;
                 case GGML_OP_ADD:
                     used = try_fuse_norm(c, cg, i, n, st);
                     if (!used) used = try_fuse_bias_gelu_mul_mat(c, cg, i, n, st);

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/mq.h"
+
 namespace mq {
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
@@ -18,6 +20,45 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return (float)__b
 __device__ __forceinline__ float gelu_erf_f32(float v) {
 #pragma clang fp contract(off)
     return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+}
+
+// Half of one Q8_0 block of a kernel's quantized output: this lane's 16 values, the other 16
+// in lane l ^ 32.  The values are op(v) (pre: MQ_PRE_NONE or MQ_PRE_GELU_ERF; rows that are
+// not live: zero, as the activation quantizer's pad rows), and the block is quantized as
+// k_quantize_tiled<TQ_Q8_0> quantizes a row (ggml's quantize_row_q8_0 variants): the same max,
+// scale, reciprocal and rounding, so the bytes equal those of the fp32 values quantized by the
+// activation quantizer.  Returns the scale rounded through fp16; q receives the 16 quants.
+__device__ __forceinline__ float requant_q8_0(float (&v)[16], bool live, int pre, int variant, uint4 &q) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+        float x = v[e];
+        if (pre == MQ_PRE_GELU_ERF) x = gelu_erf_f32(x);
+        v[e] = live ? x : 0.f;
+    }
+    float amax = fabsf(v[0]);
+#pragma unroll
+    for (int e = 1; e < 16; e++) amax = fmaxf(amax, fabsf(v[e]));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const float d = amax / 127.f;
+    float id;
+    if (variant == MQ_Q8_0_X86) id = (amax != 0.0f) ? 127.f / amax : 0.0f;
+    else id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    uint32_t w[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        uint32_t pk = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float t = v[4 * u + b] * id;
+            float r = (variant == MQ_Q8_0_REF) ? roundf(t) : rintf(t);
+            r = fminf(fmaxf(r, -128.f), 127.f);
+            pk |= ((uint32_t)((int)r & 0xff)) << (8 * b);
+        }
+        w[u] = pk;
+    }
+    q = make_uint4(w[0], w[1], w[2], w[3]);
+    return f16_bits_to_f32(f32_to_f16_bits(d));
 }
 
 }  // namespace mq

@@ -186,10 +186,10 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
         for (const Layer &L : m->layers) {  // m->ws holds X quantized at the top of each layer
             if ((rc = mq_mul_mat_q_ex(t, L.qkv.img.p, L.qkv.n, L.qkv.k, m->ws.p, rows, m->qkv.f(), L.qkv.n,
                                       L.bqkv.f(), G, s)) ||
-                (rc = mq_op_flash_attn(&qv, &kv, &vv, nullptr, &ov, ascale, m->aws.p, m->aws.bytes, s)))
+                (rc = mq_op_flash_attn_q8_0(&qv, &kv, &vv, nullptr, &ov, ascale, m->aws.p, m->aws.bytes, m->ws.p,
+                                            m->ws.bytes, s)))
                 return rc;
-            if ((rc = mq_quantize_act_ex(t, m->att.f(), H, rows, H, nullptr, MQ_PRE_NONE, m->ws.p, m->ws.bytes, G, s)) ||
-                (rc = mq_mul_mat_q_ex(t, L.o.img.p, L.o.n, L.o.k, m->ws.p, rows, m->y.f(), L.o.n, L.bo.f(), G, s)) ||
+            if ((rc = mq_mul_mat_q_ex(t, L.o.img.p, L.o.n, L.o.k, m->ws.p, rows, m->y.f(), L.o.n, L.bo.f(), G, s)) ||
                 (rc = mq_op_norm_q8_0(MQ_NORM_LAYER, &xv, &yv, &xv, eps, L.ln1w.f(), L.ln1b.f(), m->ws.p, m->ws.bytes,
                                       s)) ||
                 (rc = mq_mul_mat_q_requant(t, L.fc1.img.p, L.fc1.n, L.fc1.k, m->ws.p, rows, L.b1.f(), MQ_PRE_GELU_ERF,

@@ -16,6 +16,7 @@
 #include <cstdlib>
 
 #include "mq_internal.h"
+#include "mq_act.h"
 #include "mq_wave.h"
 
 namespace mq {
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(256) void k_kv_frag(const AttnArgs a, int nblk) {
     }
 }
 
-template <int HD, bool MASK>
+template <int HD, bool MASK, bool QO = false>
 __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, float qscale) {
     constexpr int NS = HD / 16, NT = HD / 32, HALF = HD / 2, NFR = kv_frags<HD>();
     constexpr float LOG2E = 1.4426950408889634f;
@@ -401,6 +402,41 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
         float *o = ob + (int64_t)q * a.o_st;
 #pragma unroll
         for (int n = 0; n < NT; n++) o[32 * n] = oacc[n][r] * inv[r];
+    }
+    if constexpr (QO) {
+        // The same values quantized for the projection that reads them: 32 head dims of one
+        // query are one Q8_0 block of output row b * Tq + q, chunk h * NT + n.  The wave's
+        // 32 x 32 tile goes through LDS so that lane l holds query l % 32, dims 16 (l / 32) ..,
+        // its 16 bytes of the activation fragment.
+        constexpr int QST = 36;
+        __shared__ __attribute__((aligned(16))) float stg[8][32 * QST];
+        float *tile = stg[wave];
+        const int q = q0 + l32;
+        const int64_t row = (int64_t)b * Tq + q;
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) tile[(8 * (r / 4) + 4 * half + (r % 4)) * QST + l32] = oacc[n][r] * inv[r];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float4 t4 = *(const float4 *)(tile + l32 * QST + 16 * half + 4 * u);
+                v[4 * u] = t4.x, v[4 * u + 1] = t4.y, v[4 * u + 2] = t4.z, v[4 * u + 3] = t4.w;
+            }
+            uint4 pk;
+            const float d = requant_q8_0(v, true, MQ_PRE_NONE, a.q_var, pk);
+            if (q < Tq) {
+                const int64_t chunk = (int64_t)h * NT + n;
+                *(uint4 *)(a.qo + (((row >> 5) * a.q_kch + chunk) << 10) + (((row & 31) + 32 * half) << 4)) = pk;
+                if (half == 0) a.qd[chunk * a.q_m_pad + row] = d;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
     }
 }
 
@@ -687,8 +723,26 @@ static void launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_
         return;
     }
     const dim3 ga((unsigned)((a.nq + 1) / 2), (unsigned)a.B, (unsigned)((a.Tq + 127) / 128));
+    if constexpr (HD <= 64) {
+        if (a.qo) {  // quantized output: the unmasked / masked forms with the Q8_0 store
+            if (a.mask) hipLaunchKernelGGL((k_attn_frag<HD, true, true>), ga, dim3(512), 0, s, a, nblk, qscale);
+            else hipLaunchKernelGGL((k_attn_frag<HD, false, true>), ga, dim3(512), 0, s, a, nblk, qscale);
+            return;
+        }
+    }
     if (a.mask) hipLaunchKernelGGL((k_attn_frag<HD, true>), ga, dim3(512), 0, s, a, nblk, qscale);
     else hipLaunchKernelGGL((k_attn_frag<HD, false>), ga, dim3(512), 0, s, a, nblk, qscale);
+}
+
+// true when launch_attn_hd takes the 8-wave fragment kernel, which can also store the output
+// quantized (AttnArgs::qo); otherwise the caller quantizes the fp32 output itself
+static bool attn_frag_form(const AttnArgs &a) {
+    const int nblk = (a.Tk + 31) / 32;
+    const int64_t wgs = (int64_t)((a.nq + 1) / 2) * a.B * ((a.Tq + 127) / 128);
+    bool split = (wgs < 128 && nblk >= 4) || (a.hd == 128 && a.mask);
+    if (const char *e = getenv("MQ_ATTN_SPLIT"))
+        if (*e) split = atoi(e) != 0;
+    return !split && a.hd <= 64;
 }
 
 hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
@@ -699,11 +753,34 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
         return hipErrorInvalidValue;
     const int nblk = (a.Tk + 31) / 32;
     const float qscale = a.scale * 1.4426950408889634f;  // softmax in base 2
-    switch (a.hd) {
-        case 128: launch_attn_hd<128>(a, nblk, qscale, s); break;
-        case 64: launch_attn_hd<64>(a, nblk, qscale, s); break;
-        case 32: launch_attn_hd<32>(a, nblk, qscale, s); break;
+    AttnArgs b = a;
+    bool quant_after = false;
+    b.qo = nullptr;
+    if (a.q_ws) {
+        const int64_t rows = (int64_t)a.B * a.Tq, K = (int64_t)a.nq * a.hd;
+        const ActPlanes ap = act_planes(MQ_TYPE_Q8_0, rows, K, true);
+        if (ap.kb_pad != K || a.o_st != K || a.o_sh != a.hd || a.o_sb != a.Tq * K || ((uintptr_t)a.q_ws & 255))
+            return hipErrorInvalidValue;
+        if (attn_frag_form(a)) {
+            b.qo = (int8_t *)((uint8_t *)a.q_ws + ap.xq);
+            b.qd = (float *)((uint8_t *)a.q_ws + ap.xd);
+            b.q_m_pad = ap.m_pad;
+            b.q_kch = (int)(K / 32);
+        } else {
+            quant_after = true;  // the split-key form stores floats only
+        }
+    }
+    switch (b.hd) {
+        case 128: launch_attn_hd<128>(b, nblk, qscale, s); break;
+        case 64: launch_attn_hd<64>(b, nblk, qscale, s); break;
+        case 32: launch_attn_hd<32>(b, nblk, qscale, s); break;
         default: return hipErrorInvalidValue;
+    }
+    if (quant_after) {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const int64_t rows = (int64_t)a.B * a.Tq, K = (int64_t)a.nq * a.hd;
+        return launch_quantize_act_planar(MQ_TYPE_Q8_0, a.out, K, a.q_ws, rows, K, a.q_var, true, s);
     }
     return hipGetLastError();
 }

@@ -325,6 +325,16 @@ struct AttnArgs {
     float eps = 0.f;
     const float2 *cs = nullptr;
     void *ws = nullptr;
+    // q_ws not NULL: the output rows (B * Tq rows of K = nq * hd values; out must hold them as
+    // dense rows) also quantized to Q8_0 into the GEMM activation workspace q_ws, for the
+    // projection that reads them (rounding variant q_var; K a multiple of 128).  launch_attn
+    // fills qo, qd, q_m_pad and q_kch from it.
+    void *q_ws = nullptr;
+    int q_var = 0;
+    int8_t *qo = nullptr;
+    float *qd = nullptr;
+    int64_t q_m_pad = 0;
+    int q_kch = 0;
 };
 size_t attn_workspace_bytes(int B, int Tk, int nkv, int hd);
 hipError_t launch_attn(const AttnArgs &a, hipStream_t s);

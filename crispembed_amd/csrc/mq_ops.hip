@@ -1035,9 +1035,9 @@ extern "C" size_t mq_op_flash_attn_workspace_bytes(const mq_view *k) {
     return attn_workspace_bytes((int)k->ne[3], (int)k->ne[1], (int)k->ne[2], (int)k->ne[0]);
 }
 
-extern "C" int mq_op_flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
-                                const mq_view *dst, float scale, void *workspace, size_t workspace_bytes,
-                                void *stream) {
+static int flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask, const mq_view *dst,
+                      float scale, void *workspace, size_t workspace_bytes, void *act_ws, size_t act_ws_bytes,
+                      void *stream) {
     if (const char *e = check_flash(q, k, v, mask, dst)) return fail(e);
     if (!have_data({q, k, v, mask, dst})) return fail("missing data pointer");
     const size_t need = mq_op_flash_attn_workspace_bytes(k);
@@ -1061,7 +1061,31 @@ extern "C" int mq_op_flash_attn(const mq_view *q, const mq_view *k, const mq_vie
     a.nq = (int)q->ne[2], a.nkv = (int)k->ne[2], a.hd = (int)q->ne[0];
     a.scale = scale;
     a.ws = workspace;
+    if (act_ws) {
+        const int64_t K = dst->ne[0] * dst->ne[1], rows = dst->ne[2] * dst->ne[3];
+        if (K % 128 != 0 || dst->nb[1] != (size_t)dst->ne[0] * 4 || dst->nb[2] != (size_t)K * 4 ||
+            dst->nb[3] != dst->nb[2] * (size_t)dst->ne[2])
+            return fail("flash_attn_q8_0: dst must be dense rows of n_head * head_dim floats, a multiple of 128");
+        if (((uintptr_t)act_ws & 255) || act_ws_bytes < act_planes(MQ_TYPE_Q8_0, rows, K, true).total)
+            return set_error(MQ_EINVAL, "mq_op_flash_attn_q8_0: activation workspace (256-byte aligned) too small");
+        a.q_ws = act_ws;
+        a.q_var = mq_q8_0_variant();
+    }
     return hip_rc(launch_attn(a, (hipStream_t)stream), "flash_attn");
+}
+
+extern "C" int mq_op_flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
+                                const mq_view *dst, float scale, void *workspace, size_t workspace_bytes,
+                                void *stream) {
+    return flash_attn(q, k, v, mask, dst, scale, workspace, workspace_bytes, nullptr, 0, stream);
+}
+
+extern "C" int mq_op_flash_attn_q8_0(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
+                                     const mq_view *dst, float scale, void *workspace, size_t workspace_bytes,
+                                     void *act_workspace, size_t act_workspace_bytes, void *stream) {
+    if (!act_workspace) return set_error(MQ_EINVAL, "mq_op_flash_attn_q8_0: no activation workspace");
+    return flash_attn(q, k, v, mask, dst, scale, workspace, workspace_bytes, act_workspace, act_workspace_bytes,
+                      stream);
 }
 
 extern "C" int mq_op_supported(int op, int sub, const mq_view *s0, const mq_view *s1, const mq_view *s2,

@@ -111,6 +111,20 @@ size_t mq_op_flash_attn_workspace_bytes(const mq_view *k);
 int mq_op_flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask, const mq_view *dst,
                      float scale, void *workspace, size_t workspace_bytes, void *stream);
 
+/* mq_op_flash_attn that also leaves its result quantized for the output projection that reads
+ * it: dst as mq_op_flash_attn writes it, and dst's B * Tq rows of n_head * head_dim values
+ * quantized to Q8_0 in the GEMM-path activation layout -- the bytes
+ * mq_quantize_act_ex(MQ_TYPE_Q8_0, dst rows, ..., MQ_PATH_GEMM) would write -- into
+ * act_workspace (256-byte aligned, >= mq_workspace_bytes(MQ_TYPE_Q8_0, B * Tq, n_head *
+ * head_dim)).  The attention of src/crispembed.cpp:1293 and the from_float quantization of the
+ * output-projection MUL_MAT after it (src/crispembed.cpp:1300) in one kernel when the 8-wave
+ * form runs (head_dim 32 or 64); otherwise the quantizer runs after the attention.  dst must
+ * hold dense rows (nb[1] = 4 head_dim, nb[2] = 4 n_head head_dim, nb[3] = nb[2] Tq), n_head *
+ * head_dim a multiple of 128. */
+int mq_op_flash_attn_q8_0(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
+                          const mq_view *dst, float scale, void *workspace, size_t workspace_bytes,
+                          void *act_workspace, size_t act_workspace_bytes, void *stream);
+
 /* ggml_rope_ext: rotates dimension pairs of x [ne0 >= n_dims, n_head, T, B] by the angles of
  * positions pos[i2] (I32 [T]): pair i < n_dims/2 is (2i, 2i+1) for mode 0 and (i, i + n_dims/2)
  * for MQ_ROPE_NEOX; dimensions from n_dims on are copied.  The angle of pair i at position p is

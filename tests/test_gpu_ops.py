@@ -338,6 +338,49 @@ def test_flash_attn_permuted_views(attn_form, hd, nh, nkv, B, T):
     assert err <= 2e-5, err
 
 
+@pytest.mark.parametrize("hd,nh,B,T,masked", [(32, 12, 3, 77, False), (32, 12, 32, 128, False), (64, 12, 2, 128, True),
+                                              (64, 2, 5, 40, False), (128, 8, 2, 45, False)])
+def test_flash_attn_q8_0(attn_form, hd, nh, B, T, masked):
+    """mq_op_flash_attn_q8_0: dst as mq_op_flash_attn writes it (bit for bit), and the rows left
+    quantized for the output projection bit-identical to the activation quantizer run on dst --
+    from the attention kernel's own store (head_dim 32 / 64, 8-wave form) or the quantizer after
+    it (split-key form, head_dim 128)."""
+    from gpu_util import empty_u8, live_q8_0_planes
+    L = mq.lib()
+    rng = _rng(hd + T + B)
+    qx, kx, vx = (rng.standard_normal((B, T, nh, hd)).astype(np.float32) for _ in range(3))
+    q, k, v = (_cuda(x).permute(0, 2, 1, 3) for x in (qx, kx, vx))
+    mask_t = None
+    if masked:
+        mask = np.zeros((B, 1, T, T), dtype=np.float16)
+        for b in range(B):
+            mask[b, 0, :, T - 7 * b:] = -np.inf if b else 0
+        mask_t = _cuda(mask)
+    scale = 1.0 / np.sqrt(hd)
+    ref = _t().empty((B, T, nh, hd), dtype=_t().float32, device="cuda")
+    _flash(q, k, v, mask_t, scale, ref)
+    out = _t().full((B, T, nh, hd), np.nan, dtype=_t().float32, device="cuda")
+    kv = mq.view(k)
+    ws_bytes = L.mq_op_flash_attn_workspace_bytes(kv)
+    ws, wo = empty_u8(ws_bytes)
+    K, M = nh * hd, B * T
+    nb = L.mq_workspace_bytes(mq.TYPE_Q8_0, M, K)
+    act, ao = empty_u8(nb)
+    act.fill_(0xAB)
+    mv = mq.view(mask_t) if mask_t is not None else None
+    _call(L.mq_op_flash_attn_q8_0, mq.view(q), kv, mq.view(v), mv, mq.view(out), scale,
+          ctypes.c_void_p(ws.data_ptr() + wo), ws_bytes, ctypes.c_void_p(act.data_ptr() + ao), nb, stream())
+    a, b_ = host(ref), host(out)
+    assert np.array_equal(a.view(np.uint32), b_.view(np.uint32))
+    want, wo2 = empty_u8(nb)
+    mq.check(L.mq_quantize_act_ex(mq.TYPE_Q8_0, ctypes.c_void_p(out.data_ptr()), K, M, K, None, 0,
+                                  ctypes.c_void_p(want.data_ptr() + wo2), nb, mq.PATH_GEMM, stream()))
+    qa, da = live_q8_0_planes(host(want)[wo2:wo2 + nb], M, K)
+    qb, db = live_q8_0_planes(host(act)[ao:ao + nb], M, K)
+    assert np.array_equal(qa, qb)
+    assert np.array_equal(da.view(np.uint32), db.view(np.uint32))
+
+
 def test_flash_attn_pad_mask(attn_form):
     """The rectangular batch of encode_tokens_group_4d: F16 mask [T, T, 1, B], 0 for real keys,
     -inf for padding; padded query rows still attend to the real keys."""
