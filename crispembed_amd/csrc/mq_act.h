@@ -61,4 +61,30 @@ __device__ __forceinline__ float requant_q8_0(float (&v)[16], bool live, int pre
     return f16_bits_to_f32(f32_to_f16_bits(d));
 }
 
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+// hi + lo split of two floats with one explicit rounding (round toward zero) for both
+// halves: the remainder is formed from the very hi value the MFMA will read.  (A plain
+// (_Float16) cast may be emitted as different conversion instructions for the operand and
+// for the remainder; where their roundings disagree the split loses a 2^-11 term.)
+__device__ __forceinline__ void split2(float a, float b, v2h &hi, v2h &lo) {
+    hi = __builtin_bit_cast(v2h, __builtin_amdgcn_cvt_pkrtz(a, b));
+    lo = __builtin_bit_cast(v2h, __builtin_amdgcn_cvt_pkrtz(a - (float)hi[0], b - (float)hi[1]));
+}
+
+__device__ __forceinline__ void split8(const float (&x)[8], v8h &hi, v8h &lo) {
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+        v2h h, l;
+        split2(x[j], x[j + 1], h, l);
+        hi[j] = h[0], hi[j + 1] = h[1], lo[j] = l[0], lo[j + 1] = l[1];
+    }
+}
+
+// fragments per 32-key block: K (NS steps) and V (2 steps x NT column tiles), hi and lo each
+template <int HD>
+constexpr int kv_frags() { return 2 * (HD / 16) + 4 * (HD / 32); }
+
 }  // namespace mq

@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -174,6 +175,21 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
         if (!m->aws.ensure(mq_op_flash_attn_workspace_bytes(&kv)))
             return set_error(MQ_ENOMEM, "attention workspace for %lld rows", (long long)rows);
         const float ascale = 1.0f / std::sqrt((float)hd);
+        // whole 32-key blocks per sequence: K / V straight from the qkv GEMM into the fragments
+        const bool kv_direct = T % 32 == 0 && std::getenv("MQ_BERT_KV_PASS") == nullptr;
+        AttnArgs attn;
+        attn.q = m->qkv.f(), attn.k = m->qkv.f() + H, attn.v = m->qkv.f() + 2 * H;
+        attn.q_st = attn.k_st = attn.v_st = 3 * H;
+        attn.q_sh = attn.k_sh = attn.v_sh = hd;
+        attn.q_sb = attn.k_sb = attn.v_sb = 3 * H * T;
+        attn.out = m->att.f();
+        attn.o_st = H, attn.o_sh = hd, attn.o_sb = H * T;
+        attn.B = B, attn.Tq = T, attn.Tk = T, attn.nq = hp.n_head, attn.nkv = hp.n_head, attn.hd = hd;
+        attn.scale = ascale;
+        attn.ws = m->aws.p;
+        attn.q_ws = m->ws.p;
+        attn.q_var = mq_q8_0_variant();
+        attn.kv_ready = true;
         mq_view xv{};
         xv.data = X;
         xv.type = MQ_TYPE_F32;
@@ -184,11 +200,20 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
         const int G = MQ_PATH_GEMM;
         if ((rc = mq_quantize_act_ex(t, X, H, rows, H, nullptr, MQ_PRE_NONE, m->ws.p, m->ws.bytes, G, s))) return rc;
         for (const Layer &L : m->layers) {  // m->ws holds X quantized at the top of each layer
-            if ((rc = mq_mul_mat_q_ex(t, L.qkv.img.p, L.qkv.n, L.qkv.k, m->ws.p, rows, m->qkv.f(), L.qkv.n,
-                                      L.bqkv.f(), G, s)) ||
-                (rc = mq_op_flash_attn_q8_0(&qv, &kv, &vv, nullptr, &ov, ascale, m->aws.p, m->aws.bytes, m->ws.p,
-                                            m->ws.bytes, s)))
+            if (kv_direct) {
+                // the qkv GEMM writes K and V as the attention's operand fragments; the attention
+                // stores its rows as the o projection's Q8_0 activation
+                if ((rc = hip_rc(launch_gemm_kv(t, L.qkv.img.p, L.qkv.n, L.qkv.k, m->ws.p, rows, m->qkv.f(), L.qkv.n,
+                                                L.bqkv.f(), (int)H, T, hd, hp.n_head, m->aws.p, s),
+                                 "qkv gemm")) ||
+                    (rc = hip_rc(launch_attn(attn, s), "attention")))
+                    return rc;
+            } else if ((rc = mq_mul_mat_q_ex(t, L.qkv.img.p, L.qkv.n, L.qkv.k, m->ws.p, rows, m->qkv.f(), L.qkv.n,
+                                             L.bqkv.f(), G, s)) ||
+                       (rc = mq_op_flash_attn_q8_0(&qv, &kv, &vv, nullptr, &ov, ascale, m->aws.p, m->aws.bytes,
+                                                   m->ws.p, m->ws.bytes, s))) {
                 return rc;
+            }
             if ((rc = mq_mul_mat_q_ex(t, L.o.img.p, L.o.n, L.o.k, m->ws.p, rows, m->y.f(), L.o.n, L.bo.f(), G, s)) ||
                 (rc = mq_op_norm_q8_0(MQ_NORM_LAYER, &xv, &yv, &xv, eps, L.ln1w.f(), L.ln1b.f(), m->ws.p, m->ws.bytes,
                                       s)) ||

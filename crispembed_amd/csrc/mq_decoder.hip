@@ -134,30 +134,6 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(float *qkv, int64_t ld, co
 //              wave.  A workgroup is 8 waves, 2 heads x 128 queries (the two heads of a grouped-
 //              query pair read the same fragments), two waves per SIMD so that one wave's
 //              softmax overlaps the other's matrix work; the longest causal ranges go first.
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef _Float16 v2h __attribute__((ext_vector_type(2)));
-
-// hi + lo split of two floats with one explicit rounding (round toward zero) for both
-// halves: the remainder is formed from the very hi value the MFMA will read.  (A plain
-// (_Float16) cast may be emitted as different conversion instructions for the operand and
-// for the remainder; where their roundings disagree the split loses a 2^-11 term.)
-__device__ __forceinline__ void split2(float a, float b, v2h &hi, v2h &lo) {
-    hi = __builtin_bit_cast(v2h, __builtin_amdgcn_cvt_pkrtz(a, b));
-    lo = __builtin_bit_cast(v2h, __builtin_amdgcn_cvt_pkrtz(a - (float)hi[0], b - (float)hi[1]));
-}
-
-__device__ __forceinline__ void split8(const float (&x)[8], v8h &hi, v8h &lo) {
-#pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-        v2h h, l;
-        split2(x[j], x[j + 1], h, l);
-        hi[j] = h[0], hi[j + 1] = h[1], lo[j] = l[0], lo[j + 1] = l[1];
-    }
-}
-
-// fragments per 32-key block: K (NS steps) and V (2 steps x NT column tiles), hi and lo each
-template <int HD>
-constexpr int kv_frags() { return 2 * (HD / 16) + 4 * (HD / 32); }
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_kv_frag(const AttnArgs a, int nblk) {
@@ -707,7 +683,7 @@ hipError_t launch_rope_table(float2 *cs, int T, int hd, float theta_base, hipStr
 template <int HD>
 static void launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_t s) {
     const dim3 gk((unsigned)nblk, (unsigned)a.nkv, (unsigned)a.B);
-    hipLaunchKernelGGL((k_kv_frag<HD>), gk, dim3(256), 0, s, a, nblk);
+    if (!a.kv_ready) hipLaunchKernelGGL((k_kv_frag<HD>), gk, dim3(256), 0, s, a, nblk);
     // the split-key form when the regular grid (2 heads x 128 queries per workgroup) would
     // leave most CUs idle and there are several key blocks to share out, and for masked
     // head_dim 128 (the 8-wave kernel's mask addressing does not fit its 256 registers and

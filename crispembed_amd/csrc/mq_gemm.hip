@@ -76,6 +76,13 @@ struct GemmArgs {
     int8_t *qo;
     float *qd;
     int q_m_pad, q_kch, q_pre, q_var;
+    // attention K/V as MFMA operand fragments (kvf not NULL, one weight group): output columns
+    // [kv_col0, kv_col0 + kv_nkv kv_hd) are K, the next kv_nkv kv_hd columns V, row b kv_T + key
+    // (kv_T a multiple of 32).  They leave split hi / lo in the attention's fragment layout
+    // (as k_kv_frag writes them: kv_nblk 32-key blocks per (sequence, head)), not as floats;
+    // the columns before kv_col0 are stored as usual.
+    _Float16 *kvf;
+    int kv_col0, kv_T, kv_hd, kv_nkv, kv_nblk;
     int M, N, ldy;
     int m_pad, n_pad;
     int kch;      // 32-byte K chunks per row (kb_pad / 32)
@@ -591,6 +598,56 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
         return;
     }
 
+    // K / V fragments for the attention: K (attention A operand, lane = key) is transposed
+    // through a per-wave LDS tile, V (lane = head dim, register 8 t + j = key 16 t + ...) is
+    // already in its fragment order in the accumulators.
+    constexpr int KST = 36;
+    if (a.kvf) __syncthreads();  // the stage ring becomes the staging area (uniform branch)
+    float *ktile = (float *)smem + wave * (32 * KST);
+    auto kv_store = [&](int i, int j) __attribute__((always_inline)) {
+        const int row0 = m0 + (wm * TM + i) * 32, cb = n0 + (wn * TN + j) * 32;
+        const int b = row0 / a.kv_T, kb = (row0 - b * a.kv_T) >> 5;
+        const int hdk = a.kv_nkv * a.kv_hd, c = cb - a.kv_col0;
+        const bool isv = c >= hdk;
+        const int cc = isv ? c - hdk : c, hk = cc / a.kv_hd, dn = cc - hk * a.kv_hd;
+        const int ns = a.kv_hd >> 4, nt = a.kv_hd >> 5, nfr = 2 * ns + 4 * nt;
+        _Float16 *F = a.kvf + ((int64_t)(b * a.kv_nkv + hk) * a.kv_nblk + kb) * nfr * 512 + lane * 8;
+        if (isv) {
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                float x[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[e] = acc[i][j][8 * t + e];
+                v8h h, l;
+                split8(x, h, l);
+                const int f = t * nt + (dn >> 5);
+                *(v8h *)(F + (2 * ns + 2 * f) * 512) = h;
+                *(v8h *)(F + (2 * ns + 2 * f + 1) * 512) = l;
+            }
+        } else {
+#pragma unroll
+            for (int rr = 0; rr < 16; rr++)
+                ktile[(8 * (rr >> 2) + 4 * lhalf + (rr & 3)) * KST + lrow] = acc[i][j][rr];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int sp = 0; sp < 2; sp++) {
+                const float4 u = *(const float4 *)(ktile + lrow * KST + 16 * sp + 8 * lhalf);
+                const float4 w = *(const float4 *)(ktile + lrow * KST + 16 * sp + 8 * lhalf + 4);
+                const float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+                v8h h, l;
+                split8(x, h, l);
+                const int st = (dn >> 4) + sp;
+                *(v8h *)(F + (2 * st) * 512) = h;
+                *(v8h *)(F + (2 * st + 1) * 512) = l;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    };
+
     // store: lanes 0..31 of a register write 32 consecutive floats of one row.
     // (Staging the tile through LDS for 16-byte row stores was measured slower on
     // MI355X: the extra barrier and LDS pass cost more than the store instructions.)
@@ -598,6 +655,10 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) {
+            if (a.kvf && n0 + (wn * TN + j) * 32 >= a.kv_col0) {  // uniform per wave
+                if (m0 + (wm * TM + i) * 32 < a.M && n0 + (wn * TN + j) * 32 < a.N) kv_store(i, j);
+                continue;
+            }
             const int col = n0 + (wn * TN + j) * 32 + lrow;
             if (col >= a.N) continue;
 #pragma unroll
@@ -729,6 +790,47 @@ hipError_t launch_gemm_group(int type, int ngroups, const void *const *images, c
 hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
                        int64_t ldy, hipStream_t s, const float *bias) {
     return launch_gemm_group(type, 1, &image, &n, k, ws, m, &y, &ldy, &bias, s);
+}
+
+hipError_t launch_gemm_kv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
+                          int64_t ldy, const float *bias, int kv_col0, int T, int hd, int nkv, void *kv_frags,
+                          hipStream_t s) {
+    if (m <= 0 || n <= 0) return hipSuccess;
+    if (T <= 0 || T % 32 || m % T || (hd != 32 && hd != 64 && hd != 128) || kv_col0 % 32 ||
+        (int64_t)kv_col0 + 2 * (int64_t)nkv * hd != n || ((uintptr_t)kv_frags & 15))
+        return hipErrorInvalidValue;
+    const ActPlanes ap = act_planes(type, m, k, true);
+    const WeightPlanes p = weight_planes(type, n, k);
+    const uint8_t *xb = (const uint8_t *)ws, *wb = (const uint8_t *)image;
+    GemmArgs a{};
+    a.xq = (const int8_t *)(xb + ap.xq);
+    a.xd = (const float *)(xb + ap.xd);
+    a.xmin = (const _Float16 *)(xb + ap.xmin);
+    a.wq = (const int8_t *)(wb + p.tq);
+    a.whi = (const int8_t *)(wb + p.thi);
+    a.wd = (const float *)(wb + p.tdw);
+    a.wdmin = (const float *)(wb + p.tdmin);
+    a.wmin = (const _Float16 *)(wb + p.tmin);
+    a.y = y;
+    a.bias = bias;
+    a.kvf = (_Float16 *)kv_frags;
+    a.kv_col0 = kv_col0, a.kv_T = T, a.kv_hd = hd, a.kv_nkv = nkv, a.kv_nblk = T / 32;
+    a.M = (int)m;
+    a.N = (int)n;
+    a.ldy = (int)ldy;
+    a.m_pad = (int)ap.m_pad;
+    a.n_pad = (int)p.n_pad;
+    a.kch = (int)(p.kb_pad / 32);
+    a.nstages = (int)(p.kb_pad / 64);
+    a.nsb = (int)(k / QK_K);
+    a.ngroups = 1;
+    switch (type) {
+        case MQ_TYPE_Q8_0: return launch_fmt<FMT_Q8_0>(a, s);
+        case MQ_TYPE_Q4_K: return launch_fmt<FMT_Q4_K>(a, s);
+        case MQ_TYPE_Q6_K: return launch_fmt<FMT_Q6_K>(a, s);
+        case MQ_TYPE_F16: return launch_fmt<FMT_F16>(a, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gemm_requant(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m,

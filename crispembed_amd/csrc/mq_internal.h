@@ -299,6 +299,13 @@ hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const 
 // MQ_PRE_NONE or MQ_PRE_GELU_ERF.  ws must hold x in the tiled (GEMM) layout.
 hipError_t launch_gemm_requant(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m,
                                const float *bias, int pre, int q8_0_variant, void *out_ws, hipStream_t s);
+// the GEMM of an attention's concatenated q|k|v projection whose K and V columns ([kv_col0,
+// kv_col0 + nkv hd), then nkv hd more; n = kv_col0 + 2 nkv hd) leave as the attention's hi/lo
+// fp16 operand fragments in kv_frags (the layout launch_attn's K/V pass writes, m = B T rows,
+// T a multiple of 32) instead of floats; the columns before kv_col0 go to y as usual
+hipError_t launch_gemm_kv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
+                          int64_t ldy, const float *bias, int kv_col0, int T, int hd, int nkv, void *kv_frags,
+                          hipStream_t s);
 // up to 4 weights of the same type and k on one activation, one launch (bias may be NULL)
 hipError_t launch_gemm_group(int type, int ngroups, const void *const *images, const int64_t *n, int64_t k,
                              const void *ws, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,
@@ -331,6 +338,8 @@ struct AttnArgs {
     // fills qo, qd, q_m_pad and q_kch from it.
     void *q_ws = nullptr;
     int q_var = 0;
+    // the K/V operand fragments are already in ws (written by launch_gemm_kv): no K/V pass
+    bool kv_ready = false;
     int8_t *qo = nullptr;
     float *qd = nullptr;
     int64_t q_m_pad = 0;

@@ -58,3 +58,24 @@ def test_minilm_l6_full_batch(oracle):
     """MiniLM-L6 shape, Q8_0, 32 sequences x 128 tokens (the embeddings/sec workload)."""
     from crispembed_amd import bert
     _check(dict(bert.MINILM_L6), O.Q8_0, 32, 128, "minilm", oracle)
+
+
+@pytest.mark.parametrize("n_head", [8, 4, 2])
+def test_q8_0_fused_path_head_dims(oracle, n_head):
+    """The runner's Q8_0 path with every producer quantizing for its GEMM (norm, attention, FFN-up)
+    and K / V written by the qkv GEMM as attention fragments, at head_dim 32, 64 and 128 (128:
+    the attention's rows quantized after it)."""
+    hp = dict(SMALL)
+    hp.update(n_embd=256, n_head=n_head, n_ff=512, n_max_pos=128)
+    _check(hp, O.Q8_0, 8, 64, f"fused_hd{256 // n_head}", oracle)
+
+
+def test_kv_direct_equals_kv_pass(monkeypatch):
+    """K / V fragments stored by the qkv GEMM are the bytes the attention's K / V pass writes:
+    embeddings and hidden states bit-identical with MQ_BERT_KV_PASS=1 (the separate pass)."""
+    hp = dict(SMALL)
+    hp.update(n_embd=256, n_head=4, n_ff=512, n_max_pos=128)
+    a = _run(hp, O.Q8_0, 8, 64, "kvd")
+    monkeypatch.setenv("MQ_BERT_KV_PASS", "1")
+    b = _run(hp, O.Q8_0, 8, 64, "kvd")
+    assert np.array_equal(a[2], b[2]) and np.array_equal(a[3], b[3])
