@@ -82,6 +82,9 @@ struct BackendCtx {
     const ggml_tensor *ws_x = nullptr;
     int ws_type = -1, ws_path = 0;
     int64_t ws_m = 0, ws_k = 0;
+    // the FLASH_ATTN_EXT node whose K/V fragments a q/k/v GEMM already stored at ws + kv_frag_off
+    const ggml_tensor *kv_ready_for = nullptr;
+    size_t kv_frag_off = 0;
     // HIP graph of the last graph computed twice in a row (its key: graph_key), replayed while
     // the same graph keeps coming back; seen_key is the graph computed eagerly last
     hipGraphExec_t gexec = nullptr;
@@ -624,13 +627,17 @@ int try_fuse_attn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status
     mq_view m{};
     if (node->src[3]) m = view_of(node->src[3]);
     const size_t act = (mq_workspace_bytes(MQ_TYPE_Q8_0, M, K) + 255) & ~(size_t)255;
+    const bool ready = c->kv_ready_for == node;  // K/V fragments stored by the q/k/v GEMM
+    const size_t foff = ready ? c->kv_frag_off : act;
+    c->kv_ready_for = nullptr;
     c->ws_x = nullptr;
-    if (!ensure_ws(c, act + mq_op_flash_attn_workspace_bytes(&k))) {
+    if ((ready && foff < act) || !ensure_ws(c, foff + mq_op_flash_attn_workspace_bytes(&k))) {
         st = GGML_STATUS_ALLOC_FAILED;
         return 1;
     }
-    const int rc = mq_op_flash_attn_q8_0(&q, &k, &v, node->src[3] ? &m : nullptr, &d, op_param_f32(node, 0),
-                                         (char *)c->ws + act, c->ws_bytes - act, c->ws, act, c->stream);
+    const int rc = mq_op_flash_attn_ex(&q, &k, &v, node->src[3] ? &m : nullptr, &d, op_param_f32(node, 0),
+                                       (char *)c->ws + foff, c->ws_bytes - foff, c->ws, act,
+                                       ready ? MQ_ATTN_KV_READY : 0, c->stream);
     if (rc == 0) c->ws_x = x, c->ws_type = MQ_TYPE_Q8_0, c->ws_m = M, c->ws_k = K, c->ws_path = MQ_PATH_GEMM;
     st = op_status(rc, node);
     return 1;
@@ -668,6 +675,48 @@ MulMatMember mul_mat_member(ggml_cgraph *cg, int j, int n) {
 // the same weight type and k (q, k and v of a layer), separated only by view nodes and their
 // own bias ADDs: one activation quantization and one grouped launch.  Returns the nodes
 // consumed from i on; the later members (and their ADDs) are marked in `done`.
+const ggml_tensor *view_root(const ggml_tensor *t) {
+    while (t && t->view_src) t = t->view_src;
+    return t;
+}
+
+// The FLASH_ATTN_EXT that is the next non-view node after a q, k, v group and the only reader of
+// k's and v's results (through reshape / permute views of ggml's [head_dim, T, n_kv_head, B]
+// form over dense rows), or NULL.  Sets T, head_dim and n_kv_head.
+const ggml_tensor *qkv_attention(ggml_cgraph *cg, const MulMatMember *mem, int nm, int n, int64_t M, int &T, int &hd,
+                                 int &nkv) {
+    if (nm != 3) return nullptr;
+    int j = (mem[2].add_idx >= 0 ? mem[2].add_idx : mem[2].idx) + 1;
+    while (j < n && (ggml_is_empty(ggml_graph_node(cg, j)) || is_view_op(ggml_graph_node(cg, j)->op))) j++;
+    if (j >= n) return nullptr;
+    const ggml_tensor *fa = ggml_graph_node(cg, j);
+    if (fa->op != GGML_OP_FLASH_ATTN_EXT) return nullptr;
+    for (int g = 1; g <= 2; g++) {
+        const ggml_tensor *r = mem[g].dst, *t = fa->src[g];
+        const int idx = mem[g].add_idx >= 0 ? mem[g].add_idx : mem[g].idx;
+        if (view_root(t) != r || t->data != r->data || (r->flags & GGML_TENSOR_FLAG_OUTPUT) ||
+            ggml_node_get_use_count(cg, idx) != 1)
+            return nullptr;
+        if (t->ne[0] != 32 && t->ne[0] != 64 && t->ne[0] != 128) return nullptr;
+        if (t->ne[1] % 32 != 0 || t->ne[1] * t->ne[3] != M || t->ne[0] * t->ne[2] != r->ne[0]) return nullptr;
+        if (t->nb[0] != sizeof(float) || t->nb[1] != r->nb[1] || r->nb[1] != (size_t)r->ne[0] * sizeof(float) ||
+            t->nb[2] != (size_t)t->ne[0] * sizeof(float) || t->nb[3] != t->nb[1] * (size_t)t->ne[1])
+            return nullptr;
+    }
+    if (fa->src[1]->ne[0] != fa->src[2]->ne[0] || fa->src[1]->ne[2] != fa->src[2]->ne[2]) return nullptr;
+    // nothing else reads k or v, through any view
+    for (int q = mem[0].idx + 1; q < n; q++) {
+        const ggml_tensor *u = ggml_graph_node(cg, q);
+        if (u == fa || is_view_op(u->op)) continue;
+        for (int si = 0; si < GGML_MAX_SRC; si++) {
+            const ggml_tensor *r = view_root(u->src[si]);
+            if (r && (r == mem[1].dst || r == mem[2].dst) && u != mem[1].dst && u != mem[2].dst) return nullptr;
+        }
+    }
+    T = (int)fa->src[1]->ne[1], hd = (int)fa->src[1]->ne[0], nkv = (int)fa->src[1]->ne[2];
+    return fa;
+}
+
 int try_group_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, std::vector<char> &done, enum ggml_status &st) {
     ggml_tensor *mm = ggml_graph_node(cg, i);
     if (!flat_mul_mat(mm)) return 0;
@@ -702,8 +751,26 @@ int try_group_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, std::vector<
     int64_t n_all = 0;
     for (int g = 0; g < nm; g++) n_all += nn[g];
     const int path = mq_mul_mat_path(mt, n_all, K, M);
-    int rc = quantize_x(c, x, mt, M, K, path);
-    if (rc == 0) rc = mq_mul_mat_q_group(mt, nm, w, nn, K, c->ws, M, y, ldy, b, path, c->stream);
+    int rc = 1;
+    int T = 0, hd = 0, nkv = 0;
+    const ggml_tensor *fa = path == MQ_PATH_GEMM ? qkv_attention(cg, mem, nm, n, M, T, hd, nkv) : nullptr;
+    if (fa) {
+        // k and v go straight into the attention's fragments, after the quantized activations
+        const mq_view kv = view_of(fa->src[1]);
+        const size_t a1 = mq_workspace_bytes(mt, M, K), a2 = mq_workspace_bytes(MQ_TYPE_Q8_0, M, fa->ne[0] * fa->ne[1]);
+        const size_t off = ((a1 > a2 ? a1 : a2) + 255) & ~(size_t)255, fb = mq_op_flash_attn_workspace_bytes(&kv);
+        if (ensure_ws(c, off + fb)) {
+            rc = quantize_x(c, x, mt, M, K, path);
+            if (rc == 0)
+                rc = mq_mul_mat_q_qkv(mt, w, nn, K, c->ws, M, y[0], ldy[0], b, T, hd, nkv, (char *)c->ws + off, fb,
+                                      c->stream);
+            if (rc == 0) c->kv_ready_for = fa, c->kv_frag_off = off;
+        }
+    }
+    if (rc == 1) {
+        rc = quantize_x(c, x, mt, M, K, path);
+        if (rc == 0) rc = mq_mul_mat_q_group(mt, nm, w, nn, K, c->ws, M, y, ldy, b, path, c->stream);
+    }
     if (rc != 0) {
         std::fprintf(stderr, "ggml-mi355: MUL_MAT '%s' (%d grouped) failed: %s\n", mm->name, nm, mq_last_error());
         st = rc == MQ_ENOMEM ? GGML_STATUS_ALLOC_FAILED : GGML_STATUS_FAILED;
@@ -794,10 +861,14 @@ enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node) {
                           d = view_of(node);
             mq_view m{};
             if (node->src[3]) m = view_of(node->src[3]);
+            const bool ready = c->kv_ready_for == node;  // K/V fragments stored by the q/k/v GEMM
+            const size_t foff = ready ? c->kv_frag_off : 0;
+            c->kv_ready_for = nullptr;
             c->ws_x = nullptr;
-            if (!ensure_ws(c, mq_op_flash_attn_workspace_bytes(&k))) return GGML_STATUS_ALLOC_FAILED;
-            return op_status(mq_op_flash_attn(&q, &k, &v, node->src[3] ? &m : nullptr, &d, op_param_f32(node, 0), c->ws,
-                                              c->ws_bytes, c->stream),
+            if (!ensure_ws(c, foff + mq_op_flash_attn_workspace_bytes(&k))) return GGML_STATUS_ALLOC_FAILED;
+            return op_status(mq_op_flash_attn_ex(&q, &k, &v, node->src[3] ? &m : nullptr, &d, op_param_f32(node, 0),
+                                                 (char *)c->ws + foff, c->ws_bytes - foff, nullptr, 0,
+                                                 ready ? MQ_ATTN_KV_READY : 0, c->stream),
                              node);
         }
         default:
@@ -811,6 +882,7 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
     const int n = ggml_graph_n_nodes(cg);
     const bool fuse = std::getenv("MQ_GGML_NO_FUSION") == nullptr;
     c->ws_x = nullptr;  // the inputs may have been rewritten since the last graph
+    c->kv_ready_for = nullptr;
     std::vector<char> done(n, 0);  // nodes already computed as part of an earlier group
     for (int i = 0; i < n; i++) {
         ggml_tensor *node = ggml_graph_node(cg, i);

@@ -312,6 +312,33 @@ int mq_mul_mat_q_requant(int type, const void *w_image, int64_t n, int64_t k, co
     return e == hipSuccess ? MQ_OK : hip_fail(e, "gemm");
 }
 
+int mq_mul_mat_q_qkv(int type, const void *const *w_images, const int64_t *n, int64_t k, const void *workspace,
+                     int64_t m, float *y_q, int64_t ldy_q, const float *const *bias, int T, int head_dim,
+                     int n_kv_head, void *kv_frags, size_t kv_frags_bytes, void *stream) {
+    if (!w_images || !n || !y_q || !kv_frags || !workspace)
+        return fail(MQ_EINVAL, "mq_mul_mat_q_qkv: NULL weights, n, y_q, workspace or kv_frags");
+    for (int g = 0; g < 3; g++) {
+        const int rc = check_weight_shape(type, n[g], k);
+        if (rc) return rc;
+        if (!w_images[g] || !is_aligned(w_images[g], 256))
+            return fail(MQ_EINVAL, "mq_mul_mat_q_qkv: weight image %d missing or not 256-byte aligned", g);
+    }
+    if (head_dim != 32 && head_dim != 64 && head_dim != 128)
+        return fail(MQ_EUNSUPPORTED, "mq_mul_mat_q_qkv: head_dim must be 32, 64 or 128");
+    if (n_kv_head <= 0 || n[1] != (int64_t)n_kv_head * head_dim || n[2] != n[1])
+        return fail(MQ_EINVAL, "mq_mul_mat_q_qkv: k and v must have n_kv_head * head_dim rows");
+    if (T <= 0 || T % 32 != 0 || m <= 0 || m % T != 0 || m > INT32_MAX)
+        return fail(MQ_EINVAL, "mq_mul_mat_q_qkv: m must be whole sequences of T tokens, T a multiple of 32");
+    if (ldy_q < n[0] || !is_aligned(workspace, 256) || ((uintptr_t)kv_frags & 15))
+        return fail(MQ_EINVAL, "mq_mul_mat_q_qkv: bad ldy_q or alignment");
+    const size_t need = attn_workspace_bytes((int)(m / T), T, n_kv_head, head_dim);
+    if (kv_frags_bytes < need)
+        return fail(MQ_EINVAL, "mq_mul_mat_q_qkv: kv_frags of %zu bytes, %zu needed", kv_frags_bytes, need);
+    const hipError_t e = launch_gemm_qkv(type, w_images, n, k, workspace, m, y_q, ldy_q, bias, T, head_dim, n_kv_head,
+                                         kv_frags, (hipStream_t)stream);
+    return e == hipSuccess ? MQ_OK : hip_fail(e, "gemm");
+}
+
 int mq_mul_mat_q_group(int type, int n_groups, const void *const *w_images, const int64_t *n, int64_t k,
                        const void *workspace, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,
                        int path, void *stream) {

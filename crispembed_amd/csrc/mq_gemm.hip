@@ -101,6 +101,7 @@ struct GemmArgs {
         float *y;
         const float *bias;
         int N, n_pad, ldy;
+        int kv_col0;  // as GemmArgs::kv_col0, for this group's columns
     } grp[GEMM_GROUPS - 1];
 };
 
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
         if (g > 0) {
             const GemmArgs::Group &G = a0.grp[g - 1];
             a.wq = G.wq, a.whi = G.whi, a.wd = G.wd, a.wdmin = G.wdmin, a.wmin = G.wmin;
-            a.y = G.y, a.bias = G.bias, a.N = G.N, a.n_pad = G.n_pad, a.ldy = G.ldy;
+            a.y = G.y, a.bias = G.bias, a.N = G.N, a.n_pad = G.n_pad, a.ldy = G.ldy, a.kv_col0 = G.kv_col0;
             tn -= a0.tn_start[g];
         }
     }
@@ -735,9 +736,34 @@ static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
     }
 }
 
+static hipError_t gemm_group_kv(int type, int ngroups, const void *const *images, const int64_t *n, int64_t k,
+                                const void *ws, int64_t m, float *const *y, const int64_t *ldy,
+                                const float *const *bias, const int *kv_col0, _Float16 *kvf, int T, int hd, int nkv,
+                                hipStream_t s);
+
 hipError_t launch_gemm_group(int type, int ngroups, const void *const *images, const int64_t *n, int64_t k,
                              const void *ws, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,
                              hipStream_t s) {
+    return gemm_group_kv(type, ngroups, images, n, k, ws, m, y, ldy, bias, nullptr, nullptr, 0, 0, 0, s);
+}
+
+hipError_t launch_gemm_qkv(int type, const void *const *images, const int64_t *n, int64_t k, const void *ws, int64_t m,
+                           float *yq, int64_t ldyq, const float *const *bias, int T, int hd, int nkv, void *kv_frags,
+                           hipStream_t s) {
+    if (T <= 0 || T % 32 || m % T || (hd != 32 && hd != 64 && hd != 128) || n[1] != (int64_t)nkv * hd ||
+        n[2] != n[1] || n[0] <= 0 || ((uintptr_t)kv_frags & 15))
+        return hipErrorInvalidValue;
+    // group 0 (Q) stores floats; group 1 (K) and group 2 (V) leave as fragments
+    const int col0[3] = {INT_MAX, 0, -(int)n[1]};
+    float *y[3] = {yq, nullptr, nullptr};
+    const int64_t ld[3] = {ldyq, n[1], n[2]};
+    return gemm_group_kv(type, 3, images, n, k, ws, m, y, ld, bias, col0, (_Float16 *)kv_frags, T, hd, nkv, s);
+}
+
+static hipError_t gemm_group_kv(int type, int ngroups, const void *const *images, const int64_t *n, int64_t k,
+                                const void *ws, int64_t m, float *const *y, const int64_t *ldy,
+                                const float *const *bias, const int *kv_col0, _Float16 *kvf, int T, int hd, int nkv,
+                                hipStream_t s) {
     if (ngroups < 1 || ngroups > GEMM_GROUPS) return hipErrorInvalidValue;
     if (m <= 0) return hipSuccess;
     const ActPlanes ap = act_planes(type, m, k, true);
@@ -766,9 +792,10 @@ hipError_t launch_gemm_group(int type, int ngroups, const void *const *images, c
         G.N = (int)n[g];
         G.n_pad = (int)p.n_pad;
         G.ldy = (int)ldy[g];
+        G.kv_col0 = kv_col0 ? kv_col0[g] : INT_MAX;
         if (ng == 0) {
             a.wq = G.wq, a.whi = G.whi, a.wd = G.wd, a.wdmin = G.wdmin, a.wmin = G.wmin;
-            a.y = G.y, a.bias = G.bias, a.N = G.N, a.n_pad = G.n_pad, a.ldy = G.ldy;
+            a.y = G.y, a.bias = G.bias, a.N = G.N, a.n_pad = G.n_pad, a.ldy = G.ldy, a.kv_col0 = G.kv_col0;
             a.kch = (int)(p.kb_pad / 32);
             a.nstages = (int)(p.kb_pad / 64);  // set again per configuration
         } else {
@@ -778,6 +805,11 @@ hipError_t launch_gemm_group(int type, int ngroups, const void *const *images, c
     }
     if (ng == 0) return hipSuccess;
     a.ngroups = ng;
+    if (kvf) {
+        if (ng != ngroups) return hipErrorInvalidValue;  // no empty group among q, k, v
+        a.kvf = kvf;
+        a.kv_T = T, a.kv_hd = hd, a.kv_nkv = nkv, a.kv_nblk = T / 32;
+    }
     switch (type) {
         case MQ_TYPE_Q8_0: return launch_fmt<FMT_Q8_0>(a, s);
         case MQ_TYPE_Q4_K: return launch_fmt<FMT_Q4_K>(a, s);

@@ -306,6 +306,11 @@ hipError_t launch_gemm_requant(int type, const void *image, int64_t n, int64_t k
 hipError_t launch_gemm_kv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
                           int64_t ldy, const float *bias, int kv_col0, int T, int hd, int nkv, void *kv_frags,
                           hipStream_t s);
+// q, k and v projections as one grouped GEMM (images / n / bias of q, k, v): q stores floats to
+// yq, k and v (n[1] = n[2] = nkv hd) leave as the attention's fragments (as launch_gemm_kv)
+hipError_t launch_gemm_qkv(int type, const void *const *images, const int64_t *n, int64_t k, const void *ws, int64_t m,
+                           float *yq, int64_t ldyq, const float *const *bias, int T, int hd, int nkv, void *kv_frags,
+                           hipStream_t s);
 // up to 4 weights of the same type and k on one activation, one launch (bias may be NULL)
 hipError_t launch_gemm_group(int type, int ngroups, const void *const *images, const int64_t *n, int64_t k,
                              const void *ws, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,

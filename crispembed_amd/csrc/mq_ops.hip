@@ -1037,7 +1037,7 @@ extern "C" size_t mq_op_flash_attn_workspace_bytes(const mq_view *k) {
 
 static int flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask, const mq_view *dst,
                       float scale, void *workspace, size_t workspace_bytes, void *act_ws, size_t act_ws_bytes,
-                      void *stream) {
+                      int flags, void *stream) {
     if (const char *e = check_flash(q, k, v, mask, dst)) return fail(e);
     if (!have_data({q, k, v, mask, dst})) return fail("missing data pointer");
     const size_t need = mq_op_flash_attn_workspace_bytes(k);
@@ -1061,6 +1061,7 @@ static int flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, cons
     a.nq = (int)q->ne[2], a.nkv = (int)k->ne[2], a.hd = (int)q->ne[0];
     a.scale = scale;
     a.ws = workspace;
+    a.kv_ready = (flags & MQ_ATTN_KV_READY) != 0;
     if (act_ws) {
         const int64_t K = dst->ne[0] * dst->ne[1], rows = dst->ne[2] * dst->ne[3];
         if (K % 128 != 0 || dst->nb[1] != (size_t)dst->ne[0] * 4 || dst->nb[2] != (size_t)K * 4 ||
@@ -1077,14 +1078,22 @@ static int flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, cons
 extern "C" int mq_op_flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
                                 const mq_view *dst, float scale, void *workspace, size_t workspace_bytes,
                                 void *stream) {
-    return flash_attn(q, k, v, mask, dst, scale, workspace, workspace_bytes, nullptr, 0, stream);
+    return flash_attn(q, k, v, mask, dst, scale, workspace, workspace_bytes, nullptr, 0, 0, stream);
 }
 
 extern "C" int mq_op_flash_attn_q8_0(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
                                      const mq_view *dst, float scale, void *workspace, size_t workspace_bytes,
                                      void *act_workspace, size_t act_workspace_bytes, void *stream) {
     if (!act_workspace) return set_error(MQ_EINVAL, "mq_op_flash_attn_q8_0: no activation workspace");
-    return flash_attn(q, k, v, mask, dst, scale, workspace, workspace_bytes, act_workspace, act_workspace_bytes,
+    return flash_attn(q, k, v, mask, dst, scale, workspace, workspace_bytes, act_workspace, act_workspace_bytes, 0,
+                      stream);
+}
+
+extern "C" int mq_op_flash_attn_ex(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
+                                   const mq_view *dst, float scale, void *workspace, size_t workspace_bytes,
+                                   void *act_workspace, size_t act_workspace_bytes, int flags, void *stream) {
+    if (flags & ~MQ_ATTN_KV_READY) return set_error(MQ_EINVAL, "mq_op_flash_attn_ex: unknown flags");
+    return flash_attn(q, k, v, mask, dst, scale, workspace, workspace_bytes, act_workspace, act_workspace_bytes, flags,
                       stream);
 }
 

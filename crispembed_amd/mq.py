@@ -8,6 +8,7 @@ LIB_PATH = os.path.join(HERE, "libmq.so")
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K = 0, 1, 8, 12, 14, 15
 Q8_0_X86, Q8_0_NEON, Q8_0_REF = 0, 1, 2
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
+ATTN_KV_READY = 1
 PRE_NONE, PRE_GELU_ERF, PRE_SILU_MUL = 0, 1, 2
 TYPE_I32 = 26
 BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV = 0, 1, 2, 3
@@ -63,6 +64,8 @@ _SIGS = {
     "mq_mul_mat_q_ex": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_int, _c_vp]),
     "mq_mul_mat_q_requant": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_int, _c_int, _c_vp,
                                       _c_sz, _c_vp]),
+    "mq_mul_mat_q_qkv": (_c_int, [_c_int, ctypes.POINTER(_c_vp), ctypes.POINTER(_c_i64), _c_i64, _c_vp, _c_i64, _c_vp,
+                                  _c_i64, ctypes.POINTER(_c_vp), _c_int, _c_int, _c_int, _c_vp, _c_sz, _c_vp]),
     "mq_mul_mat_q_group": (_c_int, [_c_int, _c_int, ctypes.POINTER(_c_vp), ctypes.POINTER(_c_i64), _c_i64, _c_vp,
                                     _c_i64, ctypes.POINTER(_c_vp), ctypes.POINTER(_c_i64), ctypes.POINTER(_c_vp),
                                     _c_int, _c_vp]),
@@ -155,6 +158,8 @@ _SIGS.update({
     "mq_op_cpy": (_c_int, [_PV, _PV, _c_vp]),
     "mq_op_flash_attn_workspace_bytes": (_c_sz, [_PV]),
     "mq_op_flash_attn": (_c_int, [_PV, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_sz, _c_vp]),
+    "mq_op_flash_attn_ex": (_c_int, [_PV, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_sz, _c_vp, _c_sz, _c_int,
+                                     _c_vp]),
     "mq_op_flash_attn_q8_0": (_c_int, [_PV, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_sz, _c_vp, _c_sz, _c_vp]),
     "mq_op_supported": (_c_int, [_c_int, _c_int, _PV, _PV, _PV, _PV, _PV]),
     "mq_op_soft_max": (_c_int, [_PV, _PV, _PV, ctypes.c_float, _c_vp]),

@@ -177,6 +177,19 @@ int mq_mul_mat_q_requant(int type, const void *w_image, int64_t n, int64_t k, co
                          const float *bias, int op, int out_type, void *out_workspace, size_t out_workspace_bytes,
                          void *stream);
 
+/* The q, k and v projections of an attention layer (src/crispembed.cpp:1168-1170, each with its
+ * bias ADD) on one activation quantized with path MQ_PATH_GEMM, as one grouped GEMM: q (n[0]
+ * features) is stored to y_q as mq_mul_mat_q_group stores it, while k and v (n[1] = n[2] =
+ * n_kv_head * head_dim features) never become floats -- the GEMM stores them straight into
+ * kv_frags as the attention's K/V operand fragments (the bytes mq_op_flash_attn's own K/V pass
+ * writes into its workspace), ready for mq_op_flash_attn_ex(..., MQ_ATTN_KV_READY) with kv_frags
+ * as its workspace.  m = B * T rows (B sequences of T tokens, T a multiple of 32), head_dim 32,
+ * 64 or 128; kv_frags_bytes >= mq_op_flash_attn_workspace_bytes of the [head_dim, T, n_kv_head,
+ * B] k view. */
+int mq_mul_mat_q_qkv(int type, const void *const *w_images, const int64_t *n, int64_t k, const void *workspace,
+                     int64_t m, float *y_q, int64_t ldy_q, const float *const *bias, int T, int head_dim,
+                     int n_kv_head, void *kv_frags, size_t kv_frags_bytes, void *stream);
+
 /* mq_quantize_act with the graph's elementwise producer folded in: it quantizes
  * op(X + bias) where bias is an fp32 [k] row added to every row of X (NULL: none) and
  * op is one of MQ_PRE_*.  The value quantized is the fp32 tensor the ggml graph

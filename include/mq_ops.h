@@ -125,6 +125,16 @@ int mq_op_flash_attn_q8_0(const mq_view *q, const mq_view *k, const mq_view *v, 
                           const mq_view *dst, float scale, void *workspace, size_t workspace_bytes,
                           void *act_workspace, size_t act_workspace_bytes, void *stream);
 
+/* The attention's K/V operand fragments are already in workspace (written by
+ * mq_mul_mat_q_qkv): the attention skips its K/V pass and reads k and v for their shapes only. */
+#define MQ_ATTN_KV_READY 1
+
+/* mq_op_flash_attn (act_workspace NULL) or mq_op_flash_attn_q8_0 (act_workspace given), with
+ * flags: 0 or MQ_ATTN_KV_READY. */
+int mq_op_flash_attn_ex(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
+                        const mq_view *dst, float scale, void *workspace, size_t workspace_bytes,
+                        void *act_workspace, size_t act_workspace_bytes, int flags, void *stream);
+
 /* ggml_rope_ext: rotates dimension pairs of x [ne0 >= n_dims, n_head, T, B] by the angles of
  * positions pos[i2] (I32 [T]): pair i < n_dims/2 is (2i, 2i+1) for mode 0 and (i, i + n_dims/2)
  * for MQ_ROPE_NEOX; dimensions from n_dims on are copied.  The angle of pair i at position p is

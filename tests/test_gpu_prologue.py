@@ -247,3 +247,53 @@ def test_mul_mat_q_requant_variants(variant):
         del img, ws
     finally:
         L.mq_set_q8_0_variant(old)
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_K])
+@pytest.mark.parametrize("hd,nh,B,T", [(32, 12, 4, 64), (64, 4, 3, 96), (128, 2, 2, 32)])
+def test_qkv_fragments_equal_kv_pass(wtype, hd, nh, B, T):
+    """mq_mul_mat_q_qkv (k and v stored by the GEMM as attention fragments) + mq_op_flash_attn_ex
+    with MQ_ATTN_KV_READY against mq_mul_mat_q_group + mq_op_flash_attn (the K/V pass): q and the
+    attention output bit-identical."""
+    import torch
+    from crispembed_amd import mq
+    L = mq.lib()
+    H = nh * hd
+    k = 512  # whole K-quant superblocks
+    m = B * T
+    rng = np.random.default_rng(hd + T + wtype)
+    imgs, wps = [], []
+    for _ in range(3):
+        w = (rng.standard_normal((H, k)) * 0.05).astype(np.float32)
+        img = weight_image(wtype, np.ascontiguousarray(mq_quantized(wtype, w)), H, k)
+        imgs.append(img)
+        wps.append(img[1])
+    x = dev(rng.standard_normal((m, k)).astype(np.float32))
+    _, ptr, _ = ws = _quant(wtype, x, m, k, 2)
+    biases = [dev(rng.standard_normal(H).astype(np.float32)) for _ in range(3)]
+    VP, I64 = ctypes.c_void_p * 3, ctypes.c_int64 * 3
+    ys = [torch.empty((m, H), dtype=torch.float32, device="cuda") for _ in range(3)]
+    mq.check(L.mq_mul_mat_q_group(wtype, 3, VP(*wps), I64(H, H, H), k, ctypes.c_void_p(ptr), m,
+                                  VP(*[t.data_ptr() for t in ys]), I64(H, H, H), VP(*[b.data_ptr() for b in biases]),
+                                  2, stream()))
+
+    def views(t):  # ggml [hd, T, nh, B] over rows of H floats
+        return t.view(B, T, nh, hd).permute(0, 2, 1, 3)
+    qv, kv, vv = (mq.view(views(t)) for t in ys)
+    fb = L.mq_op_flash_attn_workspace_bytes(kv)
+    f1, o1 = empty_u8(fb)
+    out1 = torch.empty((B, T, nh, hd), dtype=torch.float32, device="cuda")
+    mq.check(L.mq_op_flash_attn(qv, kv, vv, None, mq.view(out1), 1.0 / np.sqrt(hd),
+                                ctypes.c_void_p(f1.data_ptr() + o1), fb, stream()))
+    yq = torch.full((m, H), np.nan, dtype=torch.float32, device="cuda")
+    f2, o2 = empty_u8(fb)
+    mq.check(L.mq_mul_mat_q_qkv(wtype, VP(*wps), I64(H, H, H), k, ctypes.c_void_p(ptr), m,
+                                ctypes.c_void_p(yq.data_ptr()), H, VP(*[b.data_ptr() for b in biases]), T, hd, nh,
+                                ctypes.c_void_p(f2.data_ptr() + o2), fb, stream()))
+    assert np.array_equal(host(yq), host(ys[0]))
+    assert np.array_equal(host(f2)[o2:o2 + fb], host(f1)[o1:o1 + fb])
+    out2 = torch.full((B, T, nh, hd), np.nan, dtype=torch.float32, device="cuda")
+    mq.check(L.mq_op_flash_attn_ex(mq.view(views(yq)), kv, vv, None, mq.view(out2), 1.0 / np.sqrt(hd),
+                                   ctypes.c_void_p(f2.data_ptr() + o2), fb, None, 0, mq.ATTN_KV_READY, stream()))
+    assert np.array_equal(host(out2), host(out1))
+    del imgs, ws
