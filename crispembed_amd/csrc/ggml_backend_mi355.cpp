@@ -14,6 +14,7 @@
 // (ggml_node_get_use_count == 1) and are not graph outputs:
 //   MUL_MAT [-> ADD(bias)], with the MUL_MATs after it on the same activation
 //                                                  one grouped GEMM, biases added by its store
+//   GET_ROWS, GET_ROWS, ADD [, GET_ROWS, ADD]      the embedding sum in one pass
 //   FLASH_ATTN_EXT -> (views) -> MUL_MAT(Q8_0)     the attention also quantizes its result
 //                                                  for the projection (mq_op_flash_attn_q8_0)
 //   [ADD(residual) ->] NORM|RMS_NORM -> MUL(w) [-> ADD(b)]
@@ -446,6 +447,43 @@ bool same_shape(const ggml_tensor *a, const ggml_tensor *b) {
 }
 
 bool flat_mul_mat(const ggml_tensor *mm);
+
+// GET_ROWS(t0, i0), GET_ROWS(t1, i1), ADD [, GET_ROWS(t2, i2), ADD] from node i (the embedding
+// sum), every intermediate read only by the next ADD: one mq_op_get_rows_sum.  Returns the
+// nodes consumed.
+int try_fuse_rows_sum(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status &st) {
+    if (i + 2 >= n) return 0;
+    ggml_tensor *g0 = ggml_graph_node(cg, i), *g1 = ggml_graph_node(cg, i + 1), *a1 = ggml_graph_node(cg, i + 2);
+    auto gather_ok = [](const ggml_tensor *g) {
+        return g->op == GGML_OP_GET_ROWS && g->src[0]->type == GGML_TYPE_F32 && g->src[1]->type == GGML_TYPE_I32;
+    };
+    auto single = [&](int idx) {
+        return !(ggml_graph_node(cg, idx)->flags & GGML_TENSOR_FLAG_OUTPUT) && ggml_node_get_use_count(cg, idx) == 1;
+    };
+    if (!gather_ok(g0) || !gather_ok(g1) || a1->op != GGML_OP_ADD || a1->src[0] != g0 || a1->src[1] != g1 ||
+        !single(i) || !single(i + 1))
+        return 0;
+    ggml_tensor *last = a1, *g2 = nullptr;
+    int used = 3;
+    if (i + 4 < n && single(i + 2)) {
+        ggml_tensor *x2 = ggml_graph_node(cg, i + 3), *a2 = ggml_graph_node(cg, i + 4);
+        if (gather_ok(x2) && a2->op == GGML_OP_ADD && a2->src[0] == a1 && a2->src[1] == x2 && single(i + 3)) {
+            g2 = x2;
+            last = a2;
+            used = 5;
+        }
+    }
+    if (!same_shape(last, g0) || !same_shape(g1, g0) || (g2 && !same_shape(g2, g0))) return 0;
+    const mq_view t0 = view_of(g0->src[0]), t1 = view_of(g1->src[0]), i0 = view_of(g0->src[1]),
+                  i1 = view_of(g1->src[1]), d = view_of(last);
+    mq_view t2{}, i2{};
+    if (g2) t2 = view_of(g2->src[0]), i2 = view_of(g2->src[1]);
+    const mq_view *tabs[3] = {&t0, &t1, &t2}, *ids[3] = {&i0, &i1, &i2};
+    const int rc = mq_op_get_rows_sum(g2 ? 3 : 2, tabs, ids, &d, c->stream);
+    if (rc != 0) return 0;  // a layout this op does not take: the nodes run on their own
+    st = GGML_STATUS_SUCCESS;
+    return used;
+}
 
 // [ADD(x, r) ->] NORM|RMS_NORM -> MUL(w) [-> ADD(b)] starting at node i: returns the number of
 // nodes consumed (0: no match)
@@ -900,6 +938,7 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
                 case GGML_OP_NORM:
                 case GGML_OP_RMS_NORM: used = try_fuse_norm(c, cg, i, n, st); break;
                 case GGML_OP_FLASH_ATTN_EXT: used = try_fuse_attn(c, cg, i, n, st); break;
+                case GGML_OP_GET_ROWS: used = try_fuse_rows_sum(c, cg, i, n, st); break;
                 case GGML_OP_ADD:
                     used = try_fuse_norm(c, cg, i, n, st);
                     if (!used) used = try_fuse_bias_gelu_mul_mat(c, cg, i, n, st);

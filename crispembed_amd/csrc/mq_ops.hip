@@ -373,6 +373,49 @@ __global__ __launch_bounds__(256) void k_get_rows(const DV src, const DV ids, co
     for (int64_t c = lane; c < n; c += 64) dr[c] = ok ? deq_elem<TYPE>(sr, c) : 0.f;
 }
 
+// Sum of 2 or 3 gathered F32 table rows (the embedding ADDs of GET_ROWS results), one wave per
+// output row, added in table order as the ADD nodes add them; an id outside its table adds a
+// zero row, as k_get_rows gathers one.
+struct RowsSumArgs {
+    const float *tab[3];
+    const int32_t *ids[3];
+    int64_t ntab_rows[3], ld[3];
+    int n;
+};
+template <bool V4>
+__global__ __launch_bounds__(256) void k_get_rows_sum(const RowsSumArgs a, float *__restrict__ d, int64_t nrows,
+                                                      int64_t ne0) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+    if (row >= nrows) return;
+    const float *src[3];
+#pragma unroll
+    for (int t = 0; t < 3; t++) {
+        src[t] = nullptr;
+        if (t < a.n) {
+            const int32_t id = a.ids[t][row];
+            src[t] = (id >= 0 && id < a.ntab_rows[t]) ? a.tab[t] + (int64_t)id * a.ld[t] : nullptr;
+        }
+    }
+    float *dr = d + row * ne0;
+    if constexpr (V4) {
+        for (int64_t c = 4 * lane; c < ne0; c += 256) {
+            float4 acc = src[0] ? *(const float4 *)(src[0] + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int t = 1; t < a.n; t++) {
+                const float4 v = src[t] ? *(const float4 *)(src[t] + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+                acc.x = acc.x + v.x, acc.y = acc.y + v.y, acc.z = acc.z + v.z, acc.w = acc.w + v.w;
+            }
+            *(float4 *)(dr + c) = acc;
+        }
+    } else {
+        for (int64_t c = lane; c < ne0; c += 64) {
+            float acc = src[0] ? src[0][c] : 0.f;
+            for (int t = 1; t < a.n; t++) acc = acc + (src[t] ? src[t][c] : 0.f);
+            dr[c] = acc;
+        }
+    }
+}
+
 // Rotary embedding: one thread per (row, pair slot j < ne0/2).  Slots j < n_dims/2 rotate
 // their pair; the others copy elements 2j, 2j + 1 (all at or past n_dims).
 struct RopeParams {
@@ -748,6 +791,38 @@ extern "C" int mq_op_get_rows(const mq_view *src, const mq_view *ids, const mq_v
         default: hipLaunchKernelGGL((k_get_rows<MQ_TYPE_Q6_K>), g, b, 0, s, dv(src), dv(ids), dv(dst), rows); break;
     }
     return hip_rc(hipGetLastError(), "get_rows");
+}
+
+extern "C" int mq_op_get_rows_sum(int n, const mq_view *const *srcs, const mq_view *const *ids, const mq_view *dst,
+                                  void *stream) {
+    if (n < 2 || n > 3 || !srcs || !ids || !dst || !shape_ok(dst)) return fail("get_rows_sum: 2 or 3 tables and a dst");
+    if (dst->type != MQ_TYPE_F32 || dst->nb[0] != 4 || dst->nb[1] != (size_t)dst->ne[0] * 4 || dst->ne[2] != 1 ||
+        dst->ne[3] != 1)
+        return fail("get_rows_sum: dst must be dense F32 rows [ne0, rows]");
+    const int64_t ne0 = dst->ne[0], rows = dst->ne[1];
+    RowsSumArgs a{};
+    a.n = n;
+    bool v4 = ne0 % 4 == 0 && ((uintptr_t)dst->data & 15) == 0;
+    for (int t = 0; t < n; t++) {
+        const mq_view *S = srcs[t], *I = ids[t];
+        if (!S || !I || !shape_ok(S) || !shape_ok(I)) return fail("missing or empty operand");
+        if (S->type != MQ_TYPE_F32 || S->nb[0] != 4 || S->ne[0] != ne0 || S->ne[2] != 1 || S->ne[3] != 1)
+            return fail("get_rows_sum: tables must be F32 [ne0, rows] with contiguous rows");
+        if (I->type != MQ_TYPE_I32 || I->nb[0] != 4 || I->ne[0] != rows || I->ne[1] != 1 || I->ne[2] != 1 ||
+            I->ne[3] != 1)
+            return fail("get_rows_sum: ids must be I32 vectors of dst's row count");
+        if (!S->data || !I->data) return fail("missing data pointer");
+        a.tab[t] = (const float *)S->data;
+        a.ids[t] = (const int32_t *)I->data;
+        a.ntab_rows[t] = S->ne[1];
+        a.ld[t] = (int64_t)(S->nb[1] / 4);
+        v4 = v4 && S->nb[1] % 16 == 0 && ((uintptr_t)S->data & 15) == 0;
+    }
+    if (!dst->data) return fail("missing data pointer");
+    const dim3 g((unsigned)((rows + 3) / 4)), b(256);
+    if (v4) hipLaunchKernelGGL((k_get_rows_sum<true>), g, b, 0, (hipStream_t)stream, a, (float *)dst->data, rows, ne0);
+    else hipLaunchKernelGGL((k_get_rows_sum<false>), g, b, 0, (hipStream_t)stream, a, (float *)dst->data, rows, ne0);
+    return hip_rc(hipGetLastError(), "get_rows_sum");
 }
 
 extern "C" int mq_op_binary(int op, const mq_view *a, const mq_view *b, const mq_view *dst, void *stream) {

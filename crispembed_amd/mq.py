@@ -158,6 +158,7 @@ _SIGS.update({
     "mq_op_cpy": (_c_int, [_PV, _PV, _c_vp]),
     "mq_op_flash_attn_workspace_bytes": (_c_sz, [_PV]),
     "mq_op_flash_attn": (_c_int, [_PV, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_sz, _c_vp]),
+    "mq_op_get_rows_sum": (_c_int, [_c_int, ctypes.POINTER(_PV), ctypes.POINTER(_PV), _PV, _c_vp]),
     "mq_op_flash_attn_ex": (_c_int, [_PV, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_sz, _c_vp, _c_sz, _c_int,
                                      _c_vp]),
     "mq_op_flash_attn_q8_0": (_c_int, [_PV, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_sz, _c_vp, _c_sz, _c_vp]),

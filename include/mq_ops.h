@@ -69,6 +69,14 @@ typedef struct mq_view {
  * row is written as zeros instead of reading out of bounds. */
 int mq_op_get_rows(const mq_view *src, const mq_view *ids, const mq_view *dst, void *stream);
 
+/* dst = get_rows(srcs[0], ids[0]) + get_rows(srcs[1], ids[1]) [+ get_rows(srcs[2], ids[2])],
+ * added in that order: the token + position [+ token-type] embedding sum of
+ * src/crispembed.cpp:1068-1078 (GET_ROWS, GET_ROWS, ADD, GET_ROWS, ADD) in one pass.  n = 2 or 3
+ * F32 tables [ne0, rows_t] with contiguous rows, I32 id vectors of dst's row count, dst dense F32
+ * [ne0, rows].  An id outside its table adds a zero row (as mq_op_get_rows gathers one). */
+int mq_op_get_rows_sum(int n, const mq_view *const *srcs, const mq_view *const *ids, const mq_view *dst,
+                       void *stream);
+
 /* dst = a (op) b, F32, with b broadcast over a (b.ne[i] divides a.ne[i]); dst has a's shape. */
 int mq_op_binary(int op, const mq_view *a, const mq_view *b, const mq_view *dst, void *stream);
 

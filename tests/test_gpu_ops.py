@@ -246,6 +246,32 @@ def test_norm_q8_0_refusals():
     assert rc == -2 and b"multiple of 128" in L.mq_last_error()
 
 
+@pytest.mark.parametrize("ntab,ne0", [(3, 384), (2, 384), (3, 30)])
+def test_get_rows_sum(ntab, ne0):
+    """mq_op_get_rows_sum: the token + position (+ type) embedding sum, bit-identical to the
+    GET_ROWS and ADD nodes in float32 (added in table order), ids outside a table adding zeros."""
+    L = mq.lib()
+    rows = 300
+    rng = _rng(ne0 + ntab)
+    tabs = [rng.standard_normal((n, ne0)).astype(np.float32) for n in (1000, 512, 2)[:ntab]]
+    ids = [rng.integers(0, t.shape[0], rows).astype(np.int32) for t in tabs]
+    ids[0][5] = -3
+    ids[1][7] = 10 ** 6
+    ref = np.zeros((rows, ne0), np.float32)
+    for t, i in zip(tabs, ids):
+        g = np.where(((i >= 0) & (i < t.shape[0]))[:, None], t[np.clip(i, 0, t.shape[0] - 1)], np.float32(0))
+        ref = (ref + g).astype(np.float32) if t is not tabs[0] else g.astype(np.float32)
+    dts = [_cuda(t) for t in tabs]
+    dis = [_cuda(i) for i in ids]
+    out = _t().full((rows, ne0), np.nan, dtype=_t().float32, device="cuda")
+    tv = [mq.view(t) for t in dts]
+    iv = [mq.view(i) for i in dis]
+    PV = ctypes.POINTER(mq.View) * ntab
+    _call(L.mq_op_get_rows_sum, ntab, PV(*[ctypes.pointer(v) for v in tv]), PV(*[ctypes.pointer(v) for v in iv]),
+          mq.view(out), stream())
+    assert np.array_equal(host(out), ref)
+
+
 # ----------------------------------------------------------------------- cpy ----
 def test_cpy_cont_of_permute_and_qkv_slices():
     L = mq.lib()
