@@ -192,8 +192,8 @@ __global__ __launch_bounds__(256) void k_norm(const DV x, const DV r, const DV d
 // of the mat-mul that reads it, in the GEMM layout the tiled activation quantizer writes
 // (1 KB fragments per 32-row tile and 32-value chunk: lane l's 16 bytes are row l % 32,
 // bytes 16 (l / 32) ..; scales [K / 32][m_pad], pad rows of the tile quantized as zeros).
-// Workgroup: RT rows (16: half of a 32-row tile, so a 4096-row input gives every CU a
-// workgroup), NW waves; half a wave takes a row, lane s holding values 4 s + 128 p (p < NV) as
+// Workgroup: RT rows (8: a quarter of a 32-row tile, so a 4096-row input gives every CU two
+// workgroups), NW waves; half a wave takes a row, lane s holding values 4 s + 128 p (p < NV) as
 // float4, so a Q8_0 block is 8 lanes (a 3-step xor max) and the row sums are 5-step half-wave
 // xor sums.  Quants go through LDS and leave as the 16-byte lane units of this workgroup's
 // rows in each fragment (lanes r and r + 32 for its rows r): 256-byte contiguous runs.
@@ -207,7 +207,7 @@ __global__ __launch_bounds__(64 * NW) void k_norm_q8_0(const float *x, const flo
                                                        int variant) {
     constexpr int K = 128 * NV, NCH = K / 32, FST = 1024 + 16;
     constexpr int RPW = RT / NW, NIT = RPW / 2;  // rows per wave, passes of two rows
-    static_assert((RT == 16 || RT == 32) && NIT >= 1 && RPW % 2 == 0, "16 or 32 rows, whole passes");
+    static_assert((RT == 8 || RT == 16 || RT == 32) && NIT >= 1 && RPW % 2 == 0, "8, 16 or 32 rows, whole passes");
     __shared__ __attribute__((aligned(16))) int8_t frag[NCH * FST];
     __shared__ float dsh[NCH][32];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -865,7 +865,7 @@ template <int KIND>
 static void launch_norm_q8_0_kind(int nv, const float *x, const float *r, float *d, float eps, const float *w,
                                   const float *b, int64_t rows, int8_t *xq, float *xd, int64_t m_pad, int variant,
                                   hipStream_t s) {
-    constexpr int NW = 8, RT = 16;
+    constexpr int NW = 4, RT = 8;
     const dim3 grid((unsigned)((rows + 31) / 32 * (32 / RT))), block(64 * NW);
     switch (nv) {
 #define MQ_NQ(NV)                                                                                                      \
