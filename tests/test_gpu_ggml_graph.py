@@ -49,15 +49,17 @@ def _pool(h):
     return p / np.linalg.norm(p)
 
 
-@pytest.mark.parametrize("wtype,hd", [(O.Q8_0, 32), (O.Q8_0, 64), (O.Q4_K, 64), (O.Q6_K, 32), (O.F16, 32)])
-def test_bert_graph_matches_reference(oracle, tmp_path, wtype, hd):
+@pytest.mark.parametrize("wtype,hd,T", [(O.Q8_0, 32, 40), (O.Q8_0, 64, 40), (O.Q4_K, 64, 40), (O.Q6_K, 32, 40),
+                                        (O.F16, 32, 40), (O.Q8_0, 32, 64), (O.Q8_0, 64, 64), (O.Q4_K, 32, 64)])
+def test_bert_graph_matches_reference(oracle, tmp_path, wtype, hd, T):
+    """T = 64 (whole 32-key blocks): the q/k/v GEMM stores k and v as attention fragments."""
     hp = dict(HP, n_head=HP["n_embd"] // hd)
     if wtype in (O.Q4_K, O.Q6_K):
         hp.update(n_embd=256, n_head=256 // hd)
     W = bert.synthetic_weights(hp, wtype, name=f"graph{wtype}_{hd}")
     model = tmp_path / "m.gguf"
     gguf.write_bert_gguf(model, hp, wtype, W)
-    B, T = 3, 40
+    B = 3
     rng = np.random.default_rng(wtype + hd)
     ids = rng.integers(0, hp["n_vocab"], (B, T)).astype(np.int32)
     types = rng.integers(0, 2, (B, T)).astype(np.int32)
@@ -71,14 +73,16 @@ def test_bert_graph_matches_reference(oracle, tmp_path, wtype, hd):
             assert _pool(got[b * T:(b + 1) * T]) @ _pool(ref[b * T:(b + 1) * T]) >= COSINE_MIN
 
 
-def test_bert_graph_padded_batch(oracle, tmp_path):
+@pytest.mark.parametrize("lens", [[37, 5, 20, 1], [64, 5, 33, 1]])
+def test_bert_graph_padded_batch(oracle, tmp_path, lens):
     """encode_tokens_group_4d: items padded to T_max with a -inf key mask; every item's real rows
-    equal the reference encoding of that item alone."""
+    equal the reference encoding of that item alone (T_max 64: k and v as GEMM-stored fragments
+    under the mask)."""
     hp = dict(HP)
     W = bert.synthetic_weights(hp, O.Q8_0, name="graphpad")
     model = tmp_path / "m.gguf"
     gguf.write_bert_gguf(model, hp, O.Q8_0, W)
-    lens = np.array([37, 5, 20, 1], dtype=np.int32)
+    lens = np.array(lens, dtype=np.int32)
     B, T = len(lens), int(lens.max())
     rng = np.random.default_rng(7)
     ids = np.zeros((B, T), np.int32)
