@@ -12,6 +12,8 @@
 // then the output RMS norm of the pooled rows and L2 normalisation.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -150,9 +152,29 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
                      "embedding")))
         return rc;
     if ((rc = hip_rc(launch_rope_table((float2 *)m->rope.p, T, hd, hp.rope_theta, s), "rope table"))) return rc;
+    // K-quant weights with the qkv and gate|up products on the GEMM path: the residual + RMS norm
+    // also leaves its result as their Q8_K activation (launch_add_rmsnorm_q8_K), so Hn is not
+    // quantized again.  hn_q: the workspace holds Hn quantized.
+    const bool norm_q = (t == MQ_TYPE_Q4_K || t == MQ_TYPE_Q6_K) && H % 256 == 0 && H <= 2048 &&
+                        !m->layers.empty() && mq_mul_mat_path(t, m->layers[0].qkv.n, H, rows) == MQ_PATH_GEMM &&
+                        mq_mul_mat_path(t, m->layers[0].gu.n, H, rows) == MQ_PATH_GEMM &&
+                        std::getenv("MQ_DECODER_NORM_PASS") == nullptr;
+    bool hn_q = false;
+    auto mm_hn = [&](const Linear &L, float *y) {  // a product of Hn
+        if (!hn_q) return mm(L, Hn, H, y);
+        return mq_mul_mat_q(t, L.img.p, L.n, L.k, m->ws.p, rows, y, L.n, MQ_PATH_GEMM, s);
+    };
+    auto add_norm = [&](const float *w, const char *what) {  // X += y; Hn = rms_norm(X) * w
+        if (norm_q) {
+            hn_q = true;
+            return hip_rc(launch_add_rmsnorm_q8_K(m->y.f(), X, w, eps, X, Hn, rows, (int)H, m->ws.p, s), what);
+        }
+        return hip_rc(launch_add_rmsnorm(m->y.f(), X, nullptr, nullptr, 0, w, eps, X, Hn, rows, (int)H, s), what);
+    };
     for (size_t il = 0; il < m->layers.size(); il++) {
         const DecLayer &L = m->layers[il];
-        if ((rc = mm(L.qkv, Hn, H, m->qkv.f()))) return rc;
+        if ((rc = mm_hn(L.qkv, m->qkv.f()))) return rc;
+        hn_q = false;
         if ((rc = hip_rc(launch_attn_frag(m->qkv.f(), ldqkv, m->att.f(), qd, B, T, nq, nkv, hd,
                                           1.0f / sqrtf((float)hd), hp.causal, L.has_qn ? L.q_norm.f() : nullptr,
                                           L.has_kn ? L.k_norm.f() : nullptr, eps, (const float2 *)m->rope.p,
@@ -161,10 +183,9 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
             return rc;
         if ((rc = mm(L.o, m->att.f(), qd, m->y.f()))) return rc;
         // X += A Wo^T; Hn = rms_norm(X) * ffn_norm
-        if ((rc = hip_rc(launch_add_rmsnorm(m->y.f(), X, nullptr, nullptr, 0, L.ffn_norm.f(), eps, X, Hn, rows, (int)H, s),
-                         "attention residual")))
-            return rc;
-        if ((rc = mm(L.gu, Hn, H, m->gu.f()))) return rc;
+        if ((rc = add_norm(L.ffn_norm.f(), "attention residual"))) return rc;
+        if ((rc = mm_hn(L.gu, m->gu.f()))) return rc;
+        hn_q = false;
         // down projection of silu(gate) * up, the product formed inside the quantizer
         if ((rc = mq_quantize_act_ex(t, m->gu.f(), 2 * F, rows, F, nullptr, MQ_PRE_SILU_MUL, m->ws.p, m->ws.bytes,
                                      MQ_PATH_AUTO, s)))
@@ -173,9 +194,7 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
             return rc;
         // X += FFN; Hn = rms_norm(X) * (next layer's attn_norm, or the output norm)
         const float *wn = (il + 1 < m->layers.size()) ? m->layers[il + 1].attn_norm.f() : m->out_norm.f();
-        if ((rc = hip_rc(launch_add_rmsnorm(m->y.f(), X, nullptr, nullptr, 0, wn, eps, X, Hn, rows, (int)H, s),
-                         "ffn residual")))
-            return rc;
+        if ((rc = add_norm(wn, "ffn residual"))) return rc;
     }
     // mean pooling averages the output-normed rows (Hn); last-token pooling norms the last row
     if (hp.pooling == 1) return hip_rc(launch_mean_pool_l2(Hn, out, B, T, (int)H, s), "pooling");

@@ -256,6 +256,50 @@ __device__ __forceinline__ float wave_max(float v) {
 // ---------------------------------------------------------------------------
 enum { TQ_Q8_0 = 0, TQ_Q8_K = 1, TQ_F16 = 2 };
 
+// One 256-value Q8_K block of row r of a 32-row tile, lane l of the wave holding values
+// 4l .. 4l + 3 (quantize_row_q8_K).  ggml's max: the FIRST value of largest magnitude -- per
+// lane, the first of its 4 values with the lane's largest |x|; then the lowest lane that holds
+// the wave's largest |x|.  The lane's 4 quants go to dst (its place in the staged fragment),
+// the scale 1 / iscale to *dslot (lane 0), and B_j (the sum of the 32 quants of sub-block j,
+// split as B_j & 63 and 64 (B_j >> 6)) to the min-term fragment msh of the tile.
+__device__ __forceinline__ void q8_K_block_row(const float4 v, int lane, int r, int8_t *dst, float *dslot,
+                                               _Float16 *msh) {
+    const float vals[4] = {v.x, v.y, v.z, v.w};
+    float la = 0.0f, lm = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (fabsf(vals[i]) > la) {
+            la = fabsf(vals[i]);
+            lm = vals[i];
+        }
+    const float amax = wave_max(la);
+    uint32_t packed = 0;
+    int s16 = 0;
+    float dval = 0.0f;
+    if (amax != 0.0f) {
+        const unsigned long long hit = __ballot(la == amax);
+        const float mx = readlane_f(lm, __ffsll((long long)hit) - 1);
+        const float iscale = -127.f / mx;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int qv = nearest_int(iscale * vals[i]);
+            qv = qv < 127 ? qv : 127;
+            packed |= (uint32_t)(qv & 0xff) << (8 * i);
+            s16 += qv;
+        }
+        dval = 1.0f / iscale;
+    }
+    *(uint32_t *)dst = packed;
+    if (lane == 0) *dslot = dval;
+    // B_j lands in lane 8j
+    const int B = sum8(s16);
+    if ((lane & 7) == 0) {
+        const int j = lane >> 3;
+        msh[(r << 3) + j] = (_Float16)(B & 63);
+        msh[((32 + r) << 3) + j] = (_Float16)((B >> 6) * 64);
+    }
+}
+
 template <int FMT, int VARIANT, bool VEC4>
 __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict__ x, int64_t ldx,
                                                         int8_t *__restrict__ xq, float *__restrict__ xd,
@@ -323,43 +367,7 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
             *(uint32_t *)dst = q(v.x) | (q(v.y) << 8) | (q(v.z) << 16) | (q(v.w) << 24);
             if ((sub & 7) == 0) dsh[c][r] = f16_bits_to_f32(f32_to_f16_bits(d));
         } else {
-            // ggml's max: the FIRST value of largest magnitude.  Per lane, the first
-            // of its 4 values with the lane's largest |x|; then the lowest lane that
-            // holds the wave's largest |x|.
-            const float vals[4] = {v.x, v.y, v.z, v.w};
-            float la = 0.0f, lm = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                if (fabsf(vals[i]) > la) {
-                    la = fabsf(vals[i]);
-                    lm = vals[i];
-                }
-            const float amax = wave_max(la);
-            uint32_t packed = 0;
-            int s16 = 0;
-            float dval = 0.0f;
-            if (amax != 0.0f) {
-                const unsigned long long hit = __ballot(la == amax);
-                const float mx = readlane_f(lm, __ffsll((long long)hit) - 1);
-                const float iscale = -127.f / mx;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    int qv = nearest_int(iscale * vals[i]);
-                    qv = qv < 127 ? qv : 127;
-                    packed |= (uint32_t)(qv & 0xff) << (8 * i);
-                    s16 += qv;
-                }
-                dval = 1.0f / iscale;
-            }
-            *(uint32_t *)dst = packed;
-            if (lane == 0) dsh[0][r] = dval;
-            // B_j (sum of the 32 quants of sub-block j) lands in lane 8j
-            const int B = sum8(s16);
-            if ((lane & 7) == 0) {
-                const int j = lane >> 3;
-                msh[(r << 3) + j] = (_Float16)(B & 63);
-                msh[((32 + r) << 3) + j] = (_Float16)((B >> 6) * 64);
-            }
+            q8_K_block_row(v, lane, r, dst, &dsh[0][r], msh);
         }
     }
     __syncthreads();
@@ -376,6 +384,109 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
     if constexpr (FMT == TQ_Q8_K) {
         if (t < 64) ((int4 *)(xmin + ((rt * ncb + cb) << 9)))[t] = ((const int4 *)msh)[t];
     }
+}
+
+// ---------------------------------------------------------------------------
+// Residual ADD + RMS norm whose normed rows also leave as the Q8_K activation of the mat-mul
+// that reads them (the decoder's attn_norm / ffn_norm before the qkv and gate|up products):
+//   x = y + res (written to xout), h = x / sqrt(mean(x^2) + eps) * w (written to hout),
+// and h quantized into the tiled GEMM layout exactly as k_quantize_tiled<TQ_Q8_K> quantizes it.
+// Workgroup: one 32-row tile, 8 waves of 4 rows; a wave holds one row at a time, lane l the
+// values 256 p + 4 l .. + 3 of superblock p, which is the tiled quantizer's lane layout.
+// ---------------------------------------------------------------------------
+template <int NSB>
+__global__ __launch_bounds__(512) void k_add_rmsnorm_q8_K(const float *y, const float *res, const float *__restrict__ w,
+                                                          float eps, float *xout, float *hout, int64_t rows,
+                                                          int8_t *__restrict__ xq, float *__restrict__ xd,
+                                                          _Float16 *__restrict__ xmin, int64_t m_pad) {
+    constexpr int H = 256 * NSB, NCH = H / 32, FST = 1024 + 16;
+    __shared__ __attribute__((aligned(16))) int8_t frag[NCH * FST];
+    __shared__ float dsh[NSB][32];
+    __shared__ __attribute__((aligned(16))) _Float16 msh[NSB][512];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t rt = blockIdx.x;
+    float4 wv[NSB];
+#pragma unroll
+    for (int p = 0; p < NSB; p++) wv[p] = *(const float4 *)(w + 256 * p + 4 * lane);
+    const int cbyte = 4 * (lane & 7);
+#pragma unroll 1
+    for (int it = 0; it < 4; it++) {
+        const int r = wave * 4 + it;
+        const int64_t row = rt * 32 + r;
+        const bool live = row < rows;
+        float4 v[NSB];
+        float ss = 0.f;
+#pragma unroll
+        for (int p = 0; p < NSB; p++) {
+            v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (live) {
+                const int64_t o = row * H + 256 * p + 4 * lane;
+                float4 a = *(const float4 *)(y + o);
+                if (res) {
+                    const float4 c = *(const float4 *)(res + o);
+                    a.x = a.x + c.x, a.y = a.y + c.y, a.z = a.z + c.z, a.w = a.w + c.w;
+                }
+                v[p] = a;
+            }
+            ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
+        }
+        ss += __shfl_xor(ss, 32);
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 8);
+        ss += __shfl_xor(ss, 4);
+        ss += __shfl_xor(ss, 2);
+        ss += __shfl_xor(ss, 1);
+        const float scale = 1.0f / sqrtf(ss / (float)H + eps);
+#pragma unroll
+        for (int p = 0; p < NSB; p++) {
+            float4 h;
+            h.x = v[p].x * scale * wv[p].x, h.y = v[p].y * scale * wv[p].y;
+            h.z = v[p].z * scale * wv[p].z, h.w = v[p].w * scale * wv[p].w;
+            if (live) {
+                const int64_t o = row * H + 256 * p + 4 * lane;
+                if (xout) *(float4 *)(xout + o) = v[p];
+                *(float4 *)(hout + o) = h;
+            } else {
+                h = make_float4(0.f, 0.f, 0.f, 0.f);  // pad rows of the tile quantize to zero
+            }
+            int8_t *dst = frag + (8 * p + (lane >> 3)) * FST + ((r + 32 * (cbyte >> 4)) << 4) + (cbyte & 15);
+            q8_K_block_row(h, lane, r, dst, &dsh[p][r], msh[p]);
+        }
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+    for (int q = t; q < NCH * 64; q += 512) {
+        const int f = q >> 6, L = q & 63;
+        *(int4 *)(xq + ((rt * NCH + f) << 10) + L * 16) = *(const int4 *)(frag + f * FST + L * 16);
+    }
+    for (int q = t; q < NSB * 32; q += 512) xd[(int64_t)(q >> 5) * m_pad + rt * 32 + (q & 31)] = dsh[q >> 5][q & 31];
+    for (int q = t; q < NSB * 64; q += 512)
+        ((int4 *)(xmin + ((rt * NSB + (q >> 6)) << 9)))[q & 63] = ((const int4 *)msh[q >> 6])[q & 63];
+}
+
+hipError_t launch_add_rmsnorm_q8_K(const float *y, const float *res, const float *w, float eps, float *xout,
+                                   float *hout, int64_t rows, int H, void *ws, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (H % 256 != 0 || H > 2048 || ((uintptr_t)ws & 255) || ((uintptr_t)y | (uintptr_t)res | (uintptr_t)w |
+                                                                (uintptr_t)xout | (uintptr_t)hout) & 15)
+        return hipErrorInvalidValue;
+    const ActPlanes ap = act_planes(MQ_TYPE_Q4_K, rows, H, true);
+    uint8_t *b = (uint8_t *)ws;
+    int8_t *xq = (int8_t *)(b + ap.xq);
+    float *xd = (float *)(b + ap.xd);
+    _Float16 *xm = (_Float16 *)(b + ap.xmin);
+    const dim3 g((unsigned)((rows + 31) / 32)), blk(512);
+    switch (H / 256) {
+#define MQ_RQ(N)                                                                                                       \
+    case N:                                                                                                            \
+        hipLaunchKernelGGL((k_add_rmsnorm_q8_K<N>), g, blk, 0, s, y, res, w, eps, xout, hout, rows, xq, xd, xm,         \
+                           ap.m_pad);                                                                                  \
+        break;
+        MQ_RQ(1) MQ_RQ(2) MQ_RQ(3) MQ_RQ(4) MQ_RQ(5) MQ_RQ(6) MQ_RQ(7) MQ_RQ(8)
+#undef MQ_RQ
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

@@ -87,3 +87,31 @@ def test_bidirectional_mean_pooling(oracle):
 
 def test_bidirectional_long(oracle):
     _check(dict(SMALL, n_layer=1, causal=0, pooling=1), O.Q4_K, 2, 150, "dec_mean_long", oracle)
+
+
+def _encode(hp, wtype, B, T, name):
+    import torch
+    from crispembed_amd import decoder, synth
+    W = decoder.synthetic_weights(hp, wtype, name=name)
+    ids = synth.integers(f"{name}/ids_{B}x{T}", (B, T), 0, hp["n_vocab"] - 1)
+    dec = decoder.DecoderEmbedder(hp, wtype, W)
+    ids_d = torch.from_numpy(ids.ravel().copy()).cuda()
+    out = torch.empty((B, hp["n_embd"]), dtype=torch.float32, device="cuda")
+    hid = torch.empty((B * T, hp["n_embd"]), dtype=torch.float32, device="cuda")
+    dec.encode(ids_d.data_ptr(), B, T, out.data_ptr(), stream(), hidden_dev=hid.data_ptr())
+    return host(out), host(hid)
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_K, O.Q6_K])
+def test_norm_q8_K_matches_separate_quantizer(monkeypatch, wtype):
+    """The residual + RMS norm that also leaves its result as the Q8_K activation of the qkv and
+    gate|up products, against the norm followed by the activation quantizer
+    (MQ_DECODER_NORM_PASS=1).  The quantization code is shared; only the norm's sum order
+    differs, so the embeddings agree to a cosine of 0.99999 and the hidden states closely."""
+    hp = dict(SMALL)
+    a_pool, a_hid = _encode(hp, wtype, 2, 64, f"dec_nq_{wtype}")
+    monkeypatch.setenv("MQ_DECODER_NORM_PASS", "1")
+    b_pool, b_hid = _encode(hp, wtype, 2, 64, f"dec_nq_{wtype}")
+    cos = (a_pool * b_pool).sum(-1) / (np.linalg.norm(a_pool, axis=-1) * np.linalg.norm(b_pool, axis=-1))
+    assert cos.min() >= 0.99999
+    assert np.median(np.abs(a_hid - b_hid)) <= 1e-4 * np.abs(b_hid).max()
