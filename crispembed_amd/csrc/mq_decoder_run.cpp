@@ -164,10 +164,11 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
         if (!hn_q) return mm(L, Hn, H, y);
         return mq_mul_mat_q(t, L.img.p, L.n, L.k, m->ws.p, rows, y, L.n, MQ_PATH_GEMM, s);
     };
-    auto add_norm = [&](const float *w, const char *what) {  // X += y; Hn = rms_norm(X) * w
-        if (norm_q) {
+    auto add_norm = [&](const float *w, const char *what, bool last) {  // X += y; Hn = rms_norm(X) * w
+        if (norm_q) {  // inside the stack Hn is read only in its quantized form: not written
             hn_q = true;
-            return hip_rc(launch_add_rmsnorm_q8_K(m->y.f(), X, w, eps, X, Hn, rows, (int)H, m->ws.p, s), what);
+            return hip_rc(launch_add_rmsnorm_q8_K(m->y.f(), X, w, eps, X, last ? Hn : nullptr, rows, (int)H, m->ws.p, s),
+                          what);
         }
         return hip_rc(launch_add_rmsnorm(m->y.f(), X, nullptr, nullptr, 0, w, eps, X, Hn, rows, (int)H, s), what);
     };
@@ -183,7 +184,7 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
             return rc;
         if ((rc = mm(L.o, m->att.f(), qd, m->y.f()))) return rc;
         // X += A Wo^T; Hn = rms_norm(X) * ffn_norm
-        if ((rc = add_norm(L.ffn_norm.f(), "attention residual"))) return rc;
+        if ((rc = add_norm(L.ffn_norm.f(), "attention residual", false))) return rc;
         if ((rc = mm_hn(L.gu, m->gu.f()))) return rc;
         hn_q = false;
         // down projection of silu(gate) * up, the product formed inside the quantizer
@@ -194,7 +195,7 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
             return rc;
         // X += FFN; Hn = rms_norm(X) * (next layer's attn_norm, or the output norm)
         const float *wn = (il + 1 < m->layers.size()) ? m->layers[il + 1].attn_norm.f() : m->out_norm.f();
-        if ((rc = add_norm(wn, "ffn residual"))) return rc;
+        if ((rc = add_norm(wn, "ffn residual", il + 1 == m->layers.size()))) return rc;
     }
     // mean pooling averages the output-normed rows (Hn); last-token pooling norms the last row
     if (hp.pooling == 1) return hip_rc(launch_mean_pool_l2(Hn, out, B, T, (int)H, s), "pooling");

@@ -311,7 +311,7 @@ hipError_t launch_gemm_kv(int type, const void *image, int64_t n, int64_t k, con
 hipError_t launch_gemm_qkv(int type, const void *const *images, const int64_t *n, int64_t k, const void *ws, int64_t m,
                            float *yq, int64_t ldyq, const float *const *bias, int T, int hd, int nkv, void *kv_frags,
                            hipStream_t s);
-// xout = y + res (res may be NULL, xout may be NULL or alias), hout = rms_norm(xout) * w over
+// xout = y + res (res may be NULL, xout may be NULL or alias), hout (NULL: not written) = rms_norm(xout) * w over
 // rows of H floats, and hout quantized to Q8_K in the GEMM activation layout of a K-quant
 // weight (act_planes(MQ_TYPE_Q4_K, rows, H, true)) in ws; H a multiple of 256, at most 2048
 hipError_t launch_add_rmsnorm_q8_K(const float *y, const float *res, const float *w, float eps, float *xout,

@@ -389,7 +389,7 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
 // ---------------------------------------------------------------------------
 // Residual ADD + RMS norm whose normed rows also leave as the Q8_K activation of the mat-mul
 // that reads them (the decoder's attn_norm / ffn_norm before the qkv and gate|up products):
-//   x = y + res (written to xout), h = x / sqrt(mean(x^2) + eps) * w (written to hout),
+//   x = y + res (written to xout), h = x / sqrt(mean(x^2) + eps) * w (written to hout unless NULL),
 // and h quantized into the tiled GEMM layout exactly as k_quantize_tiled<TQ_Q8_K> quantizes it.
 // Workgroup: one 32-row tile, 8 waves of 4 rows; a wave holds one row at a time, lane l the
 // values 256 p + 4 l .. + 3 of superblock p, which is the tiled quantizer's lane layout.
@@ -445,7 +445,7 @@ __global__ __launch_bounds__(512) void k_add_rmsnorm_q8_K(const float *y, const 
             if (live) {
                 const int64_t o = row * H + 256 * p + 4 * lane;
                 if (xout) *(float4 *)(xout + o) = v[p];
-                *(float4 *)(hout + o) = h;
+                if (hout) *(float4 *)(hout + o) = h;
             } else {
                 h = make_float4(0.f, 0.f, 0.f, 0.f);  // pad rows of the tile quantize to zero
             }
