@@ -259,18 +259,30 @@ def bench_decode(torch, L, mq, synth):
             mq.check(L.mq_quantize_act(mq.TYPE_Q4_K, ctypes.c_void_p(xs[kd].data_ptr()), kd, m, kd, ctypes.c_void_p(p),
                                        b, mq.PATH_GEMV, s))
 
+        VP, I64 = ctypes.c_void_p * 3, ctypes.c_int64 * 3
+        dims = {nm: (n, k) for nm, n, k in mats}
+
         def sweep():
+            # q/k/v and gate/up share their input: one quantization and one grouped GEMV each
             for lay in layers:
-                for nm, n, k in mats:
-                    if nm in ("q", "o", "gate", "down"):
-                        quant(k)  # q/k/v and gate/up share their input
-                    mq.check(L.mq_mul_mat_q(mq.TYPE_Q4_K, ctypes.c_void_p(lay[nm][1]), n, k,
-                                            ctypes.c_void_p(wss[k][1]), m, ctypes.c_void_p(ys[nm].data_ptr()), n,
-                                            mq.PATH_GEMV, s))
+                for grp in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
+                    k = dims[grp[0]][1]
+                    quant(k)
+                    if len(grp) == 1:
+                        n = dims[grp[0]][0]
+                        mq.check(L.mq_mul_mat_q(mq.TYPE_Q4_K, ctypes.c_void_p(lay[grp[0]][1]), n, k,
+                                                ctypes.c_void_p(wss[k][1]), m, ctypes.c_void_p(ys[grp[0]].data_ptr()),
+                                                n, mq.PATH_GEMV, s))
+                        continue
+                    g = len(grp)
+                    mq.check(L.mq_mul_mat_q_group(
+                        mq.TYPE_Q4_K, g, VP(*[lay[nm][1] for nm in grp]), I64(*[dims[nm][0] for nm in grp]), k,
+                        ctypes.c_void_p(wss[k][1]), m, VP(*[ys[nm].data_ptr() for nm in grp]),
+                        I64(*[dims[nm][0] for nm in grp]), None, mq.PATH_GEMV, s))
         us = _timed(torch, sweep, 5)
         out[f"layer_sweep_q4_K_m{m}"] = {"sweep_us": round(us, 1), "layer_us": round(us / 28, 2),
                                          "weight_gbs": round(wbytes / (us * 1e-6) / 1e9, 1),
-                                         "kernels_per_layer": 11}
+                                         "kernels_per_layer": 8}
     out["workload"] = ("GEMV m in {1,8}: Qwen3-VL-2B lm_head Q6_K [151936x2048]; 28-layer sweep of Q4_K "
                        "q,k,v,o [2048|1024 x 2048], gate,up [6144x2048], down [2048x6144] (792.7 MB)")
     return out

@@ -355,6 +355,11 @@ int mq_mul_mat_q_group(int type, int n_groups, const void *const *w_images, cons
     if (m == 0) return MQ_OK;
     path = resolve_path(path, m);
     if (path < 0) return path;
+    if (path == MQ_PATH_GEMV && n_groups <= 3) {  // K-quants at m <= 8: one stream launch over all weights
+        const hipError_t e = launch_gemv_group(type, n_groups, w_images, n, k, workspace, m, y, ldy, bias,
+                                               (hipStream_t)stream);
+        return e == hipSuccess ? MQ_OK : hip_fail(e, "gemv");
+    }
     if (path == MQ_PATH_GEMV) {  // weight-streaming: one launch per weight costs nothing extra
         for (int g = 0; g < n_groups; g++) {
             const hipError_t e = launch_gemv(type, w_images[g], n[g], k, workspace, m, y[g], ldy[g], (hipStream_t)stream,

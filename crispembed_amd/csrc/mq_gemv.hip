@@ -15,6 +15,8 @@
 //   F16 uses v_dot2_f32_f16 on fp16 activations.
 #include "mq_internal.h"
 
+#include <climits>
+
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
@@ -268,11 +270,22 @@ __device__ __forceinline__ void q6_compute(const GvLane &L, const Q6W &W, const 
 // activation operands once.  Per tile it issues the weight loads of the NEXT tile before
 // computing this one, writes its 16-row partial sums to LDS and, after one barrier, the
 // workgroup reduces them (double-buffered, so one barrier per tile) and stores the rows.
+// Up to three weights of the same type and K on one activation, their row tiles walked as one
+// tile space: group g owns tiles [ts1 or 0 .. next start), tend tiles in all (ts_g = INT_MAX past
+// the last group).  Selected per tile with scalar selects.
+struct GvGroups {
+    const uint8_t *gv0, *gv1, *gv2;
+    float *y0, *y1, *y2;
+    const float *b0, *b1, *b2;
+    int N0, N1, N2;
+    int64_t ld0, ld1, ld2;
+    int ts1, ts2, tend;
+};
+
 template <int TYPE, int SBW, int PF>
-__global__ __launch_bounds__(512) void k_gemv_kq_stream(const uint8_t *__restrict__ gv, const int8_t *__restrict__ xq,
+__global__ __launch_bounds__(512) void k_gemv_kq_stream(const GvGroups G, const int8_t *__restrict__ xq,
                                                         const float *__restrict__ xd, const void *__restrict__ xaux,
-                                                        float *__restrict__ y, int N, int K, int M, int64_t ldy,
-                                                        const float *__restrict__ bias) {
+                                                        int K, int M) {
     constexpr bool Q4 = TYPE == MQ_TYPE_Q4_K;
     constexpr int BYTES = Q4 ? GV4_BYTES : GV6_BYTES;
     using W = typename std::conditional<Q4, Q4W, Q6W>::type;
@@ -280,7 +293,7 @@ __global__ __launch_bounds__(512) void k_gemv_kq_stream(const uint8_t *__restric
     __shared__ float red[2][8][GV_ROWS][8];
     const GvLane L = gv_lane(M);
     const int nsb = K / QK_K;
-    const int ntiles = (N + GV_ROWS - 1) / GV_ROWS;
+    const int ntiles = G.tend;
     bool live[SBW];
     A act[SBW];
 #pragma unroll
@@ -293,10 +306,12 @@ __global__ __launch_bounds__(512) void k_gemv_kq_stream(const uint8_t *__restric
         }
     }
     auto load = [&](W (&w)[SBW], int t) {
+        const int tl = t >= G.ts2 ? t - G.ts2 : t >= G.ts1 ? t - G.ts1 : t;  // tile within its weight
+        const uint8_t *gv = t >= G.ts2 ? G.gv2 : t >= G.ts1 ? G.gv1 : G.gv0;
 #pragma unroll
         for (int i = 0; i < SBW; i++)
             if (live[i] && t < ntiles) {
-                const uint8_t *T = gv + ((int64_t)t * nsb + L.wave + 8 * i) * BYTES;
+                const uint8_t *T = gv + ((int64_t)tl * nsb + L.wave + 8 * i) * BYTES;
                 if constexpr (Q4) w[i] = q4_load(L, T);
                 else w[i] = q6_load(L, T);
             }
@@ -309,9 +324,13 @@ __global__ __launch_bounds__(512) void k_gemv_kq_stream(const uint8_t *__restric
     for (int it = 0; t < ntiles; it++, t += gridDim.x) {
         // the storing lanes' bias, loaded ahead of the prefetch so that waiting for it at the
         // store does not wait for the next tiles' weights
+        const int g = (t >= G.ts1) + (t >= G.ts2);
+        const int tl = t - (g == 2 ? G.ts2 : g == 1 ? G.ts1 : 0);
+        const float *bias = g == 2 ? G.b2 : g == 1 ? G.b1 : G.b0;
+        const int N = g == 2 ? G.N2 : g == 1 ? G.N1 : G.N0;
         float bz = 0.f;
-        if (bias && threadIdx.x < GV_ROWS * 8 && (int64_t)t * GV_ROWS + (threadIdx.x >> 3) < N)
-            bz = bias[(int64_t)t * GV_ROWS + (threadIdx.x >> 3)];
+        if (bias && threadIdx.x < GV_ROWS * 8 && (int64_t)tl * GV_ROWS + (threadIdx.x >> 3) < N)
+            bz = bias[(int64_t)tl * GV_ROWS + (threadIdx.x >> 3)];
         load(ring[PF], t + PF * (int)gridDim.x);
         W (&cur)[SBW] = ring[0];
         float part[4] = {0.f, 0.f, 0.f, 0.f};
@@ -332,7 +351,9 @@ __global__ __launch_bounds__(512) void k_gemv_kq_stream(const uint8_t *__restric
             float sum = 0.f;
 #pragma unroll
             for (int w = 0; w < 8; w++) sum += red[buf][w][rr][mm];
-            const int64_t row = (int64_t)t * GV_ROWS + rr;
+            const int64_t row = (int64_t)tl * GV_ROWS + rr;
+            float *y = g == 2 ? G.y2 : g == 1 ? G.y1 : G.y0;
+            const int64_t ldy = g == 2 ? G.ld2 : g == 1 ? G.ld1 : G.ld0;
             if (row < N && mm < M) y[(int64_t)mm * ldy + row] = bias ? sum + bz : sum;
         }
 #pragma unroll
@@ -377,9 +398,30 @@ __global__ __launch_bounds__(512) void k_gemv_kq_any(const uint8_t *__restrict__
 }
 
 template <int TYPE>
+static hipError_t launch_kq_stream_groups(const GvGroups &G, const int8_t *xq, const float *xd, const void *xaux,
+                                          int64_t k, int m, hipStream_t s);
+
+template <int TYPE>
 static hipError_t launch_kq_stream(const uint8_t *gv, const int8_t *xq, const float *xd, const void *xaux, float *y,
                                    int64_t n, int64_t k, int m, int64_t ldy, const float *bias, hipStream_t s) {
     const int64_t ntiles = (n + GV_ROWS - 1) / GV_ROWS;
+    const int nsb = (int)(k / QK_K);
+    if ((nsb + 7) / 8 > 3) {  // K > 6144: no operand cache
+        hipLaunchKernelGGL((k_gemv_kq_any<TYPE>), dim3((unsigned)ntiles), dim3(512), 0, s, gv, xq, xd, xaux, y, (int)n,
+                           (int)k, m, ldy, bias);
+        return hipSuccess;
+    }
+    GvGroups G{};
+    G.gv0 = gv, G.y0 = y, G.b0 = bias, G.N0 = (int)n, G.ld0 = ldy;
+    G.ts1 = G.ts2 = INT_MAX;
+    G.tend = (int)ntiles;
+    return launch_kq_stream_groups<TYPE>(G, xq, xd, xaux, k, m, s);
+}
+
+template <int TYPE>
+static hipError_t launch_kq_stream_groups(const GvGroups &G, const int8_t *xq, const float *xd, const void *xaux,
+                                          int64_t k, int m, hipStream_t s) {
+    const int64_t ntiles = G.tend;
     const int nsb = (int)(k / QK_K);
     const int sbw = (nsb + 7) / 8;
     static int ncu = 0;
@@ -399,21 +441,18 @@ static hipError_t launch_kq_stream(const uint8_t *gv, const int8_t *xq, const fl
     const char *pe = getenv("MQ_GEMV_PF");
     const int pf = pe ? atoi(pe) : 2;
     if (pf == 3 && sbw == 1) {
-        hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 3>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy, bias);
+        hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 3>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m);
         return hipSuccess;
     }
     if (pf == 2 && sbw == 1) {
-        hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 2>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy, bias);
+        hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 2>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m);
         return hipSuccess;
     }
     switch (sbw) {
-        case 1: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 1>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy, bias); break;
-        case 2: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 2, 1>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy, bias); break;
-        case 3: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 3, 1>), dim3(grid), block, 0, s, gv, xq, xd, xaux, y, (int)n, (int)k, m, ldy, bias); break;
-        default:
-            hipLaunchKernelGGL((k_gemv_kq_any<TYPE>), dim3((unsigned)ntiles), block, 0, s, gv, xq, xd, xaux, y, (int)n,
-                               (int)k, m, ldy, bias);
-            break;
+        case 1: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 1>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m); break;
+        case 2: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 2, 1>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m); break;
+        case 3: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 3, 1>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m); break;
+        default: return hipErrorInvalidValue;
     }
     return hipSuccess;
 }
@@ -439,6 +478,42 @@ static hipError_t gemv_launch(int type, const uint8_t *wb, const WeightPlanes &p
         default: return hipErrorInvalidValue;
     }
     return hipSuccess;
+}
+
+hipError_t launch_gemv_group(int type, int ng, const void *const *images, const int64_t *n, int64_t k, const void *ws,
+                             int64_t m, float *const *y, const int64_t *ldy, const float *const *bias, hipStream_t s) {
+    const int nsb = (int)(k / QK_K);
+    bool one = (type == MQ_TYPE_Q4_K || type == MQ_TYPE_Q6_K) && ng >= 2 && ng <= 3 && m >= 1 && m <= GEMV_CHUNK &&
+               (nsb + 7) / 8 <= 3;
+    for (int g = 0; one && g < ng; g++) one = n[g] > 0;
+    if (!one) {  // one launch per weight
+        for (int g = 0; g < ng; g++) {
+            const hipError_t e = launch_gemv(type, images[g], n[g], k, ws, m, y[g], ldy[g], s, bias ? bias[g] : nullptr);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    // the K-quant stream kernel over the concatenated row tiles of the weights
+    const ActPlanes ap = act_planes(type, m, k, false);
+    const uint8_t *xb = (const uint8_t *)ws;
+    GvGroups G{};
+    int ts[3] = {0, 0, 0}, t = 0;
+    const uint8_t *gv[3] = {nullptr, nullptr, nullptr};
+    for (int g = 0; g < ng; g++) {
+        gv[g] = (const uint8_t *)images[g] + weight_planes(type, n[g], k).gv;
+        ts[g] = t;
+        t += (int)((n[g] + GV_ROWS - 1) / GV_ROWS);
+    }
+    G.gv0 = gv[0], G.gv1 = gv[1], G.gv2 = gv[2];
+    G.y0 = y[0], G.y1 = y[1], G.y2 = ng > 2 ? y[2] : nullptr;
+    G.b0 = bias ? bias[0] : nullptr, G.b1 = bias ? bias[1] : nullptr, G.b2 = (bias && ng > 2) ? bias[2] : nullptr;
+    G.N0 = (int)n[0], G.N1 = (int)n[1], G.N2 = ng > 2 ? (int)n[2] : 0;
+    G.ld0 = ldy[0], G.ld1 = ldy[1], G.ld2 = ng > 2 ? ldy[2] : 0;
+    G.ts1 = ts[1], G.ts2 = ng > 2 ? ts[2] : INT_MAX, G.tend = t;
+    const int8_t *xq = (const int8_t *)(xb + ap.xq);
+    const float *xd = (const float *)(xb + ap.xd);
+    if (type == MQ_TYPE_Q4_K) return launch_kq_stream_groups<MQ_TYPE_Q4_K>(G, xq, xd, xb + ap.xgm, k, (int)m, s);
+    return launch_kq_stream_groups<MQ_TYPE_Q6_K>(G, xq, xd, xb + ap.xbs, k, (int)m, s);
 }
 
 hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,

@@ -316,6 +316,11 @@ hipError_t launch_gemm_qkv(int type, const void *const *images, const int64_t *n
 // weight (act_planes(MQ_TYPE_Q4_K, rows, H, true)) in ws; H a multiple of 256, at most 2048
 hipError_t launch_add_rmsnorm_q8_K(const float *y, const float *res, const float *w, float eps, float *xout,
                                    float *hout, int64_t rows, int H, void *ws, hipStream_t s);
+// up to 3 weights of the same type and k on one activation on the GEMV path: K-quant weights at
+// m <= 8 in one launch of the stream kernel over their concatenated row tiles (bit-identical to
+// separate launches), otherwise one launch per weight
+hipError_t launch_gemv_group(int type, int ng, const void *const *images, const int64_t *n, int64_t k, const void *ws,
+                             int64_t m, float *const *y, const int64_t *ldy, const float *const *bias, hipStream_t s);
 // up to 4 weights of the same type and k on one activation, one launch (bias may be NULL)
 hipError_t launch_gemm_group(int type, int ngroups, const void *const *images, const int64_t *n, int64_t k,
                              const void *ws, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,
