@@ -190,6 +190,7 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
         attn.q_ws = m->ws.p;
         attn.q_var = mq_q8_0_variant();
         attn.kv_ready = true;
+        attn.q_only = true;  // the o projection reads the attention rows quantized only
         mq_view xv{};
         xv.data = X;
         xv.type = MQ_TYPE_F32;

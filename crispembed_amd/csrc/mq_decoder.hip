@@ -371,13 +371,15 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
         inv[4 * g] = t.x, inv[4 * g + 1] = t.y, inv[4 * g + 2] = t.z, inv[4 * g + 3] = t.w;
     }
     float *ob = a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + l32;
+    if (!QO || !a.q_only) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const int q = q0 + 8 * (r / 4) + 4 * half + (r % 4);
-        if (q >= Tq) continue;
-        float *o = ob + (int64_t)q * a.o_st;
+        for (int r = 0; r < 16; r++) {
+            const int q = q0 + 8 * (r / 4) + 4 * half + (r % 4);
+            if (q >= Tq) continue;
+            float *o = ob + (int64_t)q * a.o_st;
 #pragma unroll
-        for (int n = 0; n < NT; n++) o[32 * n] = oacc[n][r] * inv[r];
+            for (int n = 0; n < NT; n++) o[32 * n] = oacc[n][r] * inv[r];
+        }
     }
     if constexpr (QO) {
         // The same values quantized for the projection that reads them: 32 head dims of one

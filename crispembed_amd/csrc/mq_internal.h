@@ -353,6 +353,9 @@ struct AttnArgs {
     // fills qo, qd, q_m_pad and q_kch from it.
     void *q_ws = nullptr;
     int q_var = 0;
+    // with q_ws: the 8-wave kernel stores only the quantized rows, not the floats in out (the
+    // caller reads the result quantized only; the split-key form still writes out)
+    bool q_only = false;
     // the K/V operand fragments are already in ws (written by launch_gemm_kv): no K/V pass
     bool kv_ready = false;
     int8_t *qo = nullptr;
