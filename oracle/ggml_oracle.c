@@ -9,6 +9,7 @@
 
 #include <math.h>
 #include <pthread.h>
+#include <unistd.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -216,10 +217,17 @@ void or_quantize_row_f16(const float *x, void *vy, int64_t k) {
     for (int64_t i = 0; i < k; i++) y[i] = or_fp32_to_fp16(x[i]);
 }
 
+/* A planted mistake (tests only, set through or_set_mutation): the tests that pin the weight
+ * quantizers show that each of these makes them fail.  0 = none (the published algorithm). */
+static int g_mutation = 0;
+void or_set_mutation(int m) { g_mutation = m; }
+
 /* make_qkx2_quants: asymmetric (scale, min) search for one sub-block with
  * weighted least squares refits over nstep+1 candidate inverse scales. */
 static float make_qkx2_quants(int n, int nmax, const float *x, const float *weights, uint8_t *L, float *the_min,
                               uint8_t *Laux, float rmin, float rdelta, int nstep, int use_mad) {
+    if (g_mutation == OR_MUT_Q4K_NO_SEARCH) nstep = 0;
+    if (g_mutation == OR_MUT_Q4K_RDELTA) rdelta = 0.2f;
     float min = x[0], max = x[0];
     float sum_w = weights[0];
     float sum_x = sum_w * x[0];
@@ -288,6 +296,13 @@ static float make_qkx2_quants(int n, int nmax, const float *x, const float *weig
     return scale;
 }
 
+float or_make_qkx2_quants(int n, int nmax, const float *x, const float *weights, uint8_t *L, float *the_min,
+                          float rmin, float rdelta, int nstep) {
+    uint8_t Laux[256];
+    if (n > 256) return 0.f;
+    return make_qkx2_quants(n, nmax, x, weights, L, the_min, Laux, rmin, rdelta, nstep, 0);
+}
+
 void or_quantize_row_q4_K_ref(const float *x, void *vy, int64_t k) {
     or_block_q4_K *y = (or_block_q4_K *)vy;
     const int64_t nb = k / OR_QK_K;
@@ -320,8 +335,13 @@ void or_quantize_row_q4_K_ref(const float *x, void *vy, int64_t k) {
                 y[i].scales[j + 4] = lm;
             } else {
                 y[i].scales[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
-                y[i].scales[j - 4] |= (uint8_t)((ls >> 4) << 6);
-                y[i].scales[j - 0] |= (uint8_t)((lm >> 4) << 6);
+                if (g_mutation == OR_MUT_Q4K_PACK) {  /* the high bits of scale and min swapped */
+                    y[i].scales[j - 4] |= (uint8_t)((lm >> 4) << 6);
+                    y[i].scales[j - 0] |= (uint8_t)((ls >> 4) << 6);
+                } else {
+                    y[i].scales[j - 4] |= (uint8_t)((ls >> 4) << 6);
+                    y[i].scales[j - 0] |= (uint8_t)((lm >> 4) << 6);
+                }
             }
         }
         y[i].d = or_fp32_to_fp16(max_scale / 63.f);
@@ -375,9 +395,10 @@ static float make_qx_quants(int n, int nmax, const float *x, int8_t *L) {
     }
     float scale = suml2 ? sumlx / suml2 : 0.0f;
     float best = scale * sumlx;
-    for (int is = -9; is <= 9; ++is) {
+    const float step = g_mutation == OR_MUT_Q6K_STEP ? 0.2f : 0.1f;
+    for (int is = -9; is <= 9 && g_mutation != OR_MUT_Q6K_NO_SEARCH; ++is) {
         if (is == 0) continue;
-        iscale = -(nmax + 0.1f * is) / max;
+        iscale = -(nmax + step * is) / max;
         sumlx = suml2 = 0;
         for (int i = 0; i < n; ++i) {
             int l = or_nearest_int(iscale * x[i]);
@@ -398,6 +419,8 @@ static float make_qx_quants(int n, int nmax, const float *x, int8_t *L) {
     }
     return scale;
 }
+
+float or_make_qx_quants(int n, int nmax, const float *x, int8_t *L) { return make_qx_quants(n, nmax, x, L); }
 
 void or_quantize_row_q6_K_ref(const float *x, void *vy, int64_t k) {
     or_block_q6_K *y = (or_block_q6_K *)vy;
@@ -421,7 +444,7 @@ void or_quantize_row_q6_K_ref(const float *x, void *vy, int64_t k) {
             x += OR_QK_K;
             continue;
         }
-        const float iscale = -128.f / max_scale;
+        const float iscale = (g_mutation == OR_MUT_Q6K_ISCALE ? -127.f : -128.f) / max_scale;
         y[i].d = or_fp32_to_fp16(1 / iscale);
         for (int ib = 0; ib < OR_QK_K / 16; ++ib) {
             const int v = or_nearest_int(iscale * scales[ib]);
@@ -724,62 +747,93 @@ void or_mul_mat(int wtype, const void *w, int64_t n, int64_t k, const float *x, 
     free(xq);
 }
 
-void or_mul_mat_exact(int wtype, const void *w, int64_t n, int64_t k, const void *xq, int64_t m, double *y) {
-    const size_t wrs = or_row_size(wtype, k);
-    const size_t xrs = or_row_size(or_vec_dot_type(wtype), k);
-    for (int64_t r = 0; r < m; r++) {
-        const char *xr = (const char *)xq + r * xrs;
-        for (int64_t c = 0; c < n; c++) {
-            const char *wr = (const char *)w + c * wrs;
-            double acc = 0.0;
-            if (wtype == OR_TYPE_Q8_0) {
-                const or_block_q8_0 *a = (const or_block_q8_0 *)wr;
-                const or_block_q8_0 *b = (const or_block_q8_0 *)xr;
-                for (int64_t ib = 0; ib < k / OR_QK8_0; ib++) {
-                    int64_t s = 0;
-                    for (int j = 0; j < OR_QK8_0; j++) s += (int64_t)a[ib].qs[j] * b[ib].qs[j];
-                    acc += (double)or_fp16_to_fp32(a[ib].d) * (double)or_fp16_to_fp32(b[ib].d) * (double)s;
-                }
-            } else if (wtype == OR_TYPE_Q4_K) {
-                const or_block_q4_K *a = (const or_block_q4_K *)wr;
-                const or_block_q8_K *b = (const or_block_q8_K *)xr;
-                for (int64_t ib = 0; ib < k / OR_QK_K; ib++) {
-                    int64_t smain = 0, smin = 0;
-                    for (int j = 0; j < 8; j++) {
-                        uint8_t sc, mn;
-                        or_get_scale_min_k4(j, a[ib].scales, &sc, &mn);
-                        int64_t s = 0, bs = 0;
-                        for (int l = 0; l < 32; l++) {
-                            const int e = 32 * j + l;          /* element index in the superblock */
-                            const int c64 = e / 64, w64 = e % 64;
-                            const uint8_t byte = a[ib].qs[32 * c64 + (w64 % 32)];
-                            const int q = (w64 < 32) ? (byte & 0xF) : (byte >> 4);
-                            s += (int64_t)q * b[ib].qs[e];
-                            bs += b[ib].qs[e];
-                        }
-                        smain += (int64_t)sc * s;
-                        smin += (int64_t)mn * bs;
-                    }
-                    const double dx = (double)b[ib].d;
-                    acc += dx * (double)or_fp16_to_fp32(a[ib].d) * (double)smain -
-                           dx * (double)or_fp16_to_fp32(a[ib].dmin) * (double)smin;
-                }
-            } else if (wtype == OR_TYPE_Q6_K) {
-                const or_block_q6_K *a = (const or_block_q6_K *)wr;
-                const or_block_q8_K *b = (const or_block_q8_K *)xr;
-                for (int64_t ib = 0; ib < k / OR_QK_K; ib++) {
-                    int8_t q6[OR_QK_K];
-                    unpack_q6_K(&a[ib], q6);
-                    int64_t s = 0;
-                    for (int e = 0; e < OR_QK_K; e++) s += (int64_t)a[ib].scales[e / 16] * q6[e] * b[ib].qs[e];
-                    acc += (double)b[ib].d * (double)or_fp16_to_fp32(a[ib].d) * (double)s;
-                }
-            } else if (wtype == OR_TYPE_F16) {
-                const uint16_t *a = (const uint16_t *)wr;
-                const uint16_t *b = (const uint16_t *)xr;
-                for (int64_t e = 0; e < k; e++) acc += (double)or_fp16_to_fp32(a[e]) * (double)or_fp16_to_fp32(b[e]);
-            }
-            y[r * n + c] = acc;
+/* One output of the exact product: integer block sums, the scale products in fp64. */
+static double exact_dot(int wtype, const char *wr, const char *xr, int64_t k) {
+    double acc = 0.0;
+    if (wtype == OR_TYPE_Q8_0) {
+        const or_block_q8_0 *a = (const or_block_q8_0 *)wr;
+        const or_block_q8_0 *b = (const or_block_q8_0 *)xr;
+        for (int64_t ib = 0; ib < k / OR_QK8_0; ib++) {
+            int64_t s = 0;
+            for (int j = 0; j < OR_QK8_0; j++) s += (int64_t)a[ib].qs[j] * b[ib].qs[j];
+            acc += (double)or_fp16_to_fp32(a[ib].d) * (double)or_fp16_to_fp32(b[ib].d) * (double)s;
         }
+    } else if (wtype == OR_TYPE_Q4_K) {
+        const or_block_q4_K *a = (const or_block_q4_K *)wr;
+        const or_block_q8_K *b = (const or_block_q8_K *)xr;
+        for (int64_t ib = 0; ib < k / OR_QK_K; ib++) {
+            int64_t smain = 0, smin = 0;
+            for (int j = 0; j < 8; j++) {
+                uint8_t sc, mn;
+                or_get_scale_min_k4(j, a[ib].scales, &sc, &mn);
+                int64_t s = 0, bs = 0;
+                for (int l = 0; l < 32; l++) {
+                    const int e = 32 * j + l;          /* element index in the superblock */
+                    const int c64 = e / 64, w64 = e % 64;
+                    const uint8_t byte = a[ib].qs[32 * c64 + (w64 % 32)];
+                    const int q = (w64 < 32) ? (byte & 0xF) : (byte >> 4);
+                    s += (int64_t)q * b[ib].qs[e];
+                    bs += b[ib].qs[e];
+                }
+                smain += (int64_t)sc * s;
+                smin += (int64_t)mn * bs;
+            }
+            const double dx = (double)b[ib].d;
+            acc += dx * (double)or_fp16_to_fp32(a[ib].d) * (double)smain -
+                   dx * (double)or_fp16_to_fp32(a[ib].dmin) * (double)smin;
+        }
+    } else if (wtype == OR_TYPE_Q6_K) {
+        const or_block_q6_K *a = (const or_block_q6_K *)wr;
+        const or_block_q8_K *b = (const or_block_q8_K *)xr;
+        for (int64_t ib = 0; ib < k / OR_QK_K; ib++) {
+            int8_t q6[OR_QK_K];
+            unpack_q6_K(&a[ib], q6);
+            int64_t s = 0;
+            for (int e = 0; e < OR_QK_K; e++) s += (int64_t)a[ib].scales[e / 16] * q6[e] * b[ib].qs[e];
+            acc += (double)b[ib].d * (double)or_fp16_to_fp32(a[ib].d) * (double)s;
+        }
+    } else if (wtype == OR_TYPE_F16) {
+        const uint16_t *a = (const uint16_t *)wr;
+        const uint16_t *b = (const uint16_t *)xr;
+        for (int64_t e = 0; e < k; e++) acc += (double)or_fp16_to_fp32(a[e]) * (double)or_fp16_to_fp32(b[e]);
     }
+    return acc;
+}
+
+typedef struct {
+    int wtype;
+    const char *w, *xq;
+    int64_t n, k, m;
+    size_t wrs, xrs;
+    double *y;
+    int64_t n0, n1;
+} exact_job;
+
+static void *exact_worker(void *arg) {
+    const exact_job *j = (const exact_job *)arg;
+    for (int64_t r = 0; r < j->m; r++)
+        for (int64_t c = j->n0; c < j->n1; c++)
+            j->y[r * j->n + c] = exact_dot(j->wtype, j->w + c * j->wrs, j->xq + r * j->xrs, j->k);
+    return NULL;
+}
+
+/* Threads split the output columns only: every output is computed the same way whatever the
+ * thread count, so the result does not depend on it. */
+void or_mul_mat_exact(int wtype, const void *w, int64_t n, int64_t k, const void *xq, int64_t m, double *y) {
+    long nt = sysconf(_SC_NPROCESSORS_ONLN);
+    if (nt < 1) nt = 1;
+    if (nt > 16) nt = 16;
+    if ((int64_t)nt > n) nt = (long)(n > 0 ? n : 1);
+    if (m * n * k < ((int64_t)1 << 22)) nt = 1;
+    pthread_t tid[16];
+    exact_job jobs[16];
+    const size_t wrs = or_row_size(wtype, k), xrs = or_row_size(or_vec_dot_type(wtype), k);
+    for (long t = 0; t < nt; t++) {
+        jobs[t] = (exact_job){wtype, (const char *)w, (const char *)xq, n, k, m, wrs, xrs, y, n * t / nt,
+                              n * (t + 1) / nt};
+        if (nt > 1) pthread_create(&tid[t], NULL, exact_worker, &jobs[t]);
+        else exact_worker(&jobs[t]);
+    }
+    if (nt > 1)
+        for (long t = 0; t < nt; t++) pthread_join(tid[t], NULL);
 }

@@ -86,6 +86,23 @@ void or_quantize_row_q8_K(const float *x, void *y, int64_t k);
 void or_quantize_row_q4_K_ref(const float *x, void *y, int64_t k);
 void or_quantize_row_q6_K_ref(const float *x, void *y, int64_t k);
 void or_quantize_row_f16(const float *x, void *y, int64_t k);
+
+/* The sub-block searches of the K-quant weight quantizers, exposed for the tests that pin them:
+ * make_qkx2_quants (Q4_K: returns the scale, *the_min = -min, levels L in [0, nmax]) and
+ * make_qx_quants with rmse_type 1 (Q6_K: returns the scale, L = level + nmax). */
+float or_make_qkx2_quants(int n, int nmax, const float *x, const float *weights, uint8_t *L, float *the_min,
+                          float rmin, float rdelta, int nstep);
+float or_make_qx_quants(int n, int nmax, const float *x, int8_t *L);
+
+/* Planted mistakes for the tests that show the pins above catch them (0: none). */
+#define OR_MUT_NONE 0
+#define OR_MUT_Q4K_NO_SEARCH 1 /* make_qkx2_quants without its refit search (nstep 0) */
+#define OR_MUT_Q4K_RDELTA 2    /* the search steps by 0.2 instead of 0.1 */
+#define OR_MUT_Q4K_PACK 3      /* the high bits of sub-blocks 4-7's scale and min swapped */
+#define OR_MUT_Q6K_NO_SEARCH 4 /* make_qx_quants without its +-9 search */
+#define OR_MUT_Q6K_STEP 5      /* the search steps by 0.2 instead of 0.1 */
+#define OR_MUT_Q6K_ISCALE 6    /* the 8-bit scales against 127 instead of 128 */
+void or_set_mutation(int m);
 /* ggml_quantize_chunk(type, src, dst, 0, nrows, k, NULL): weight quantization. */
 size_t or_quantize_chunk(int type, const float *src, void *dst, int64_t nrows, int64_t k);
 

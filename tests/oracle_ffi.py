@@ -14,6 +14,8 @@ ORACLE_DIR = os.path.join(ROOT, "oracle")
 ORACLE_SO = os.path.join(ORACLE_DIR, "liboracle.so")
 
 F32, F16, Q8_0, Q4_K, Q6_K, Q8_K = 0, 1, 8, 12, 14, 15
+# planted mistakes of the oracle (ggml_oracle.h OR_MUT_*)
+MUT_NONE, MUT_Q4K_NO_SEARCH, MUT_Q4K_RDELTA, MUT_Q4K_PACK, MUT_Q6K_NO_SEARCH, MUT_Q6K_STEP, MUT_Q6K_ISCALE = range(7)
 Q8_0_X86, Q8_0_NEON, Q8_0_REF = 0, 1, 2
 BLCK = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256}
 TSIZE = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q6_K: 210, Q8_K: 292}
@@ -51,6 +53,9 @@ class Oracle:
             "or_mul_mat_exact": (None, [ci, vp, i64, i64, vp, i64, vp]),
             "or_fast_supported": (ci, [ci]),
             "or_fast_mul_mat": (ci, [ci, vp, i64, i64, vp, i64, i64, vp, i64, ci]),
+            "or_make_qkx2_quants": (ctypes.c_float, [ci, ci, vp, vp, vp, vp, ctypes.c_float, ctypes.c_float, ci]),
+            "or_make_qx_quants": (ctypes.c_float, [ci, ci, vp, vp]),
+            "or_set_mutation": (None, [ci]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -84,6 +89,25 @@ class Oracle:
         out = np.zeros(m * row_size(vt, k), dtype=np.uint8)
         self.L.or_quantize_act_rows(wtype, _ptr(x), k, _ptr(out), m, k, variant)
         return out.reshape(m, row_size(vt, k))
+
+    def make_qkx2_quants(self, x, weights, nmax=15, rmin=-1.0, rdelta=0.1, nstep=20):
+        """-> (scale, the_min, levels uint8) of one sub-block (Q4_K's search)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(weights, dtype=np.float32)
+        L = np.zeros(x.size, np.uint8)
+        mn = ctypes.c_float()
+        s = self.L.or_make_qkx2_quants(x.size, nmax, _ptr(x), _ptr(w), _ptr(L), ctypes.byref(mn), rmin, rdelta, nstep)
+        return np.float32(s), np.float32(mn.value), L
+
+    def make_qx_quants(self, x, nmax=32):
+        """-> (scale, levels int8 = level + nmax) of one sub-block (Q6_K's search)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        L = np.zeros(x.size, np.int8)
+        s = self.L.or_make_qx_quants(x.size, nmax, _ptr(x), _ptr(L))
+        return np.float32(s), L
+
+    def set_mutation(self, m):
+        self.L.or_set_mutation(m)
 
     def dequantize(self, t, w, k, fused=0):
         w = np.ascontiguousarray(w, dtype=np.uint8)
