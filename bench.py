@@ -7,11 +7,13 @@ W[1024 x 4096] on GELU(X)[8192 x 4096].  One step = both mul_mats, each with its
 Q8_K activation quantization, inputs already resident in HBM.
 
 value = whole-step int8 TOPS (2*M*N*K per mul_mat / step time).
-roofline = the dominant kernel (the Q4_K GEMM): algorithmic ops per launch /
-its average launch time from HIP events on the launch stream, against the int8
-dense MFMA peak (5.0 POP/s).
-cpu_baseline = the restated ggml-cpu mul_mat (AVX2 integer dots, threads) on a
-bounded sample of token rows of the same workload, on the host cores.
+roofline = the dominant kernel, the up GEMM (k_gemm<Q4_K>, M 8192 N 4096 K 1024), against
+its binding roofline: the larger of its MFMA floor (ops at the 5.0 POP/s int8 peak) and its
+HBM floor (GGUF weight + quantized X + fp32 Y bytes at 8 TB/s); the launch time is the mean of
+HIP events on the launch stream.  The down GEMM is reported beside it (second_kernel), and
+both also as a fraction of the int8 MFMA peak.
+cpu_baseline = the restated ggml-cpu mul_mat (AVX-512 VNNI or AVX2 integer dots, threads =
+the CPUs this job may use) on a bounded sample of token rows of the same workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras] [--only q8_0|e2e|graph|qwen3|decode]
 """
@@ -123,26 +125,50 @@ def bench_q4k_ffn(args, torch, L, mq, synth):
     torch.cuda.synchronize()
     t_up = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
     t_dn = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
-    gemm_avg_ms = (t_up + t_dn) / 2
-    gemm_ops = (ops_up + ops_dn) / 2
-    achieved = gemm_ops / (gemm_avg_ms * 1e-3) / 1e12
+
+    def gemm_roofline(name, n, k, ops, t_ms, w_bytes):
+        """One GEMM launch against its binding roofline: the larger of its MFMA time (int8 ops at
+        5.0 POP/s) and its HBM time (algorithmic bytes: GGUF weight + quantized X + fp32 Y)."""
+        xq_bytes = M * k + M * (k // 256) * 4  # Q8_K quants + scales
+        nbytes = w_bytes + xq_bytes + M * n * 4
+        t_mfma = ops / (PEAK_INT8_TOPS * 1e12)
+        t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
+        tops = ops / (t_ms * 1e-3) / 1e12
+        gbs = nbytes / (t_ms * 1e-3) / 1e9
+        hbm = t_hbm >= t_mfma
+        return {
+            "kernel": f"k_gemm<Q4_K> {name} (MFMA int8, 2 limbs), M {M} N {n} K {k}",
+            "bound": "hbm" if hbm else "mfma",
+            "achieved": gbs if hbm else tops,
+            "peak": PEAK_HBM_GBS if hbm else PEAK_INT8_TOPS,
+            "unit": "GB/s" if hbm else "TFLOP/s",
+            "frac": (gbs / PEAK_HBM_GBS) if hbm else (tops / PEAK_INT8_TOPS),
+            "us_per_launch": t_ms * 1e3,
+            "algorithmic_ops_per_launch": ops,
+            "algorithmic_bytes_per_launch": nbytes,
+            "int8_tops": tops,
+            "int8_mfma_frac": tops / PEAK_INT8_TOPS,
+            "floor_us": {"mfma": t_mfma * 1e6, "hbm": t_hbm * 1e6},
+        }
+
+    up_rf = gemm_roofline("up", F, H, ops_up, t_up, q_up.size)
+    dn_rf = gemm_roofline("down", H, F, ops_dn, t_dn, q_dn.size)
+    # the dominant kernel of the step is the up GEMM (the longer of the two launches)
+    dom, other = (up_rf, dn_rf) if t_up >= t_dn else (dn_rf, up_rf)
+    roof = dict(dom)
+    roof.update({
+        "peak_source": "MI355X datasheet: HBM3E 8 TB/s; dense int8 MFMA 5.0 POP/s (ops = 2*M*N*K)",
+        "traffic": _measured_traffic("k_gemm<Q4_K>"),
+        "traffic_unit": "HBM bytes per launch, rocprofv3 FETCH_SIZE + WRITE_SIZE (copy-calibrated), mean of the "
+                        "up and down launches",
+        "second_kernel": other,
+    })
     res = {
         "ms_per_step": ms_step,
         "value": (ops_up + ops_dn) / (ms_step * 1e-3) / 1e12,
         "gemm_up_us": t_up * 1e3,
         "gemm_down_us": t_dn * 1e3,
-        "roofline": {
-            "kernel": "k_gemm<Q4_K> (MFMA int8, 2 limbs)",
-            "bound": "mfma",
-            "achieved": achieved,
-            "peak": PEAK_INT8_TOPS,
-            "unit": "TFLOP/s",
-            "peak_source": "MI355X dense int8 MFMA 5.0 POP/s (integer ops counted as 2*M*N*K)",
-            "frac": achieved / PEAK_INT8_TOPS,
-            "traffic": _measured_traffic("k_gemm<Q4_K>"),
-            "traffic_unit": "bytes per launch (HBM, rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
-            "algorithmic_ops_per_launch": gemm_ops,
-        },
+        "roofline": roof,
         "x": (x_up, x_dn, q_up, q_dn),
     }
     return res
@@ -386,7 +412,7 @@ def cpu_baseline_q4k(args, x_up, x_dn, q_up, q_dn):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_ffi as O
     orc = O.Oracle()
-    nthreads = int(os.environ.get("BENCH_CPU_THREADS", min(16, os.cpu_count() or 1)))
+    nthreads, threads_src = cpu_threads()
     fast = orc.fast_supported(O.Q4_K)
     mm = (lambda w, x: orc.fast_mul_mat(O.Q4_K, w, x, nthreads=nthreads)) if fast else \
          (lambda w, x: orc.mul_mat(O.Q4_K, w, x, nthreads=nthreads))
@@ -405,16 +431,45 @@ def cpu_baseline_q4k(args, x_up, x_dn, q_up, q_dn):
         dt += time.perf_counter() - t
         reps += 1
     ops = 2.0 * rows * (F * H + H * F) * reps
-    impl = "AVX2 integer dots" if fast else "scalar C"
+    isa = orc.fast_isa() if fast else "none"
+    impl = {"avx512vnni": "AVX-512 VNNI integer dots", "avx2": "AVX2 integer dots"}.get(isa, "scalar C")
+    model = cpu_model()
     return {
         "value": ops / dt / 1e12,
         "unit": "TOPS",
         "cores": nthreads,
         "kind": "port",
+        "cpu_model": model,
+        "isa": isa,
+        "host_cpus": len(os.sched_getaffinity(0)),
+        "threads_from": threads_src,
         "sample": f"Q4_K up+down mul_mat incl. Q8_K activation quantization on the first {rows} of 8192 "
                   f"token rows, {reps} rep(s), {dt:.1f} s; restated ggml-cpu algorithm ({impl}), "
-                  f"{nthreads} threads",
+                  f"{nthreads} threads ({threads_src}) on {model}",
     }
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: the CPUs this process may run on (what nproc reports), or
+    fewer when OMP_NUM_THREADS grants the job a smaller share of the host (BENCH_CPU_THREADS
+    overrides).  Returns (threads, how they were chosen)."""
+    if os.environ.get("BENCH_CPU_THREADS"):
+        return int(os.environ["BENCH_CPU_THREADS"]), "BENCH_CPU_THREADS"
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and 0 < int(omp) < n:
+        return int(omp), f"the job's CPU share OMP_NUM_THREADS={omp} of nproc={n}"
+    return n, f"nproc={n}"
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
 
 
 def main():

@@ -448,6 +448,19 @@ bool same_shape(const ggml_tensor *a, const ggml_tensor *b) {
 
 bool flat_mul_mat(const ggml_tensor *mm);
 
+// Node idx is the last node of the graph that computes anything (only views follow).  A
+// MUL_MAT there may be observed: with an eval callback (the imatrix collector,
+// src/imatrix.cpp:57-99, installed at src/crispembed.cpp:723) the scheduler computes the graph in
+// pieces that end at each MUL_MAT it observes and then reads that MUL_MAT's src1.  So no fusion
+// may leave the src1 of such a MUL_MAT unwritten.
+bool last_compute_node(ggml_cgraph *cg, int idx, int n) {
+    for (int j = idx + 1; j < n; j++) {
+        const ggml_tensor *t = ggml_graph_node(cg, j);
+        if (!ggml_is_empty(t) && !is_view_op(t->op)) return false;
+    }
+    return true;
+}
+
 // GET_ROWS(t0, i0), GET_ROWS(t1, i1), ADD [, GET_ROWS(t2, i2), ADD] from node i (the embedding
 // sum), every intermediate read only by the next ADD: one mq_op_get_rows_sum.  Returns the
 // nodes consumed.
@@ -561,6 +574,7 @@ int try_fuse_bias_gelu_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, enu
     ggml_tensor *gelu = ggml_graph_node(cg, i + 1), *mm = ggml_graph_node(cg, i + 2);
     if (gelu->op != GGML_OP_UNARY || ggml_get_unary_op(gelu) != GGML_UNARY_OP_GELU_ERF || gelu->src[0] != add) return 0;
     if (mm->op != GGML_OP_MUL_MAT || mm->src[1] != gelu) return 0;
+    if (last_compute_node(cg, i + 2, n)) return 0;  // an observer may read the GELU result
     const ggml_tensor *x = add->src[0], *w = mm->src[0];
     const int64_t K = w->ne[0], N = w->ne[1];
     if (add->type != GGML_TYPE_F32 || x->type != GGML_TYPE_F32 || !is_row_vector(add->src[1], K) || x->ne[0] != K ||
@@ -608,6 +622,7 @@ int try_fuse_ffn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status 
     if (add->op != GGML_OP_ADD || add->src[0] != mm1 || add->type != GGML_TYPE_F32 || !same_shape(add, mm1)) return 0;
     if (gelu->op != GGML_OP_UNARY || ggml_get_unary_op(gelu) != GGML_UNARY_OP_GELU_ERF || gelu->src[0] != add) return 0;
     if (mm2->op != GGML_OP_MUL_MAT || mm2->src[1] != gelu || !flat_mul_mat(mm1) || !flat_mul_mat(mm2)) return 0;
+    if (last_compute_node(cg, i + 3, n)) return 0;  // an observer may read the GELU result
     const ggml_tensor *w1 = mm1->src[0], *x = mm1->src[1], *w2 = mm2->src[0];
     const int64_t K1 = w1->ne[0], N1 = w1->ne[1], N2 = w2->ne[1];
     if (w2->type != GGML_TYPE_Q8_0 || w2->ne[0] != N1 || N1 % 128 != 0 || !is_row_vector(add->src[1], N1)) return 0;

@@ -226,6 +226,11 @@ GGML_API struct ggml_cgraph *ggml_new_graph(struct ggml_context *ctx);
 GGML_API void ggml_build_forward_expand(struct ggml_cgraph *cgraph, struct ggml_tensor *tensor);
 GGML_API int ggml_graph_n_nodes(struct ggml_cgraph *cgraph);
 GGML_API struct ggml_tensor *ggml_graph_node(struct ggml_cgraph *cgraph, int i);
+// Stand-in only (not ggml API): ggml's internal ggml_graph_view(cgraph, i0, i1), which the
+// scheduler uses to compute a graph in pieces, as an allocated object; nodes [i0, i1), use
+// counts of the whole graph.  Free with ggml_compat_graph_view_free.
+GGML_API struct ggml_cgraph *ggml_compat_graph_view(struct ggml_cgraph *cgraph, int i0, int i1);
+GGML_API void ggml_compat_graph_view_free(struct ggml_cgraph *view);
 
 #ifdef __cplusplus
 }

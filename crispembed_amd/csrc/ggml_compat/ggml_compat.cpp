@@ -149,6 +149,9 @@ struct ggml_context {
 struct ggml_cgraph {
     std::vector<ggml_tensor *> nodes;
     std::vector<ggml_tensor *> leafs;
+    // a view of nodes [i0, i1) of another graph (ggml_graph_view): use counts are the whole
+    // graph's, as in ggml, where a view shares its parent's use-count table
+    const ggml_cgraph *parent = nullptr;
 };
 
 extern "C" size_t ggml_tensor_overhead(void) { return sizeof(ggml_tensor) + 16; }
@@ -489,8 +492,18 @@ extern "C" struct ggml_tensor *ggml_graph_get_tensor(const struct ggml_cgraph *g
     return nullptr;
 }
 
+extern "C" struct ggml_cgraph *ggml_compat_graph_view(struct ggml_cgraph *g, int i0, int i1) {
+    ggml_cgraph *v = new ggml_cgraph;
+    v->nodes.assign(g->nodes.begin() + i0, g->nodes.begin() + i1);
+    v->leafs = g->leafs;
+    v->parent = g->parent ? g->parent : g;
+    return v;
+}
+extern "C" void ggml_compat_graph_view_free(struct ggml_cgraph *v) { delete v; }
+
 extern "C" int ggml_node_get_use_count(const struct ggml_cgraph *g, int node_idx) {
     const ggml_tensor *t = g->nodes[node_idx];
+    if (g->parent) g = g->parent;
     int n = 0;
     for (const ggml_tensor *u : g->nodes)
         for (int i = 0; i < GGML_MAX_SRC; i++)

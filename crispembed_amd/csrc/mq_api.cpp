@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 
@@ -75,8 +76,10 @@ struct Workspace {
     void *ptr = nullptr;
     size_t bytes = 0;
 };
+// mq_mul_mat's internal activation buffers (workspace == NULL), one per (device, stream): work
+// queued on one stream never shares its quantized activations with another stream's
 std::mutex g_ws_mu;
-Workspace g_ws[64];  // per HIP device ordinal
+std::map<std::pair<int, void *>, Workspace> g_ws;
 
 bool type_ok(int t) {
     return t == MQ_TYPE_Q8_0 || t == MQ_TYPE_Q4_K || t == MQ_TYPE_Q6_K || t == MQ_TYPE_F16;
@@ -399,10 +402,10 @@ int mq_mul_mat_ex(int type, const void *w_image, int64_t n, int64_t k, const flo
         if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
         if (dev < 0 || dev >= 64) return fail(MQ_EINVAL, "device ordinal %d", dev);
         std::lock_guard<std::mutex> lk(g_ws_mu);
-        Workspace &w = g_ws[dev];
+        Workspace &w = g_ws[{dev, stream}];
         if (w.bytes < need) {
-            // the old buffer may still be read by work queued earlier on any stream
-            e = hipDeviceSynchronize();
+            // the old buffer may still be read by work queued earlier on this stream
+            e = hipStreamSynchronize((hipStream_t)stream);
             if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
             if (w.ptr) (void)hipFree(w.ptr);
             w.ptr = nullptr;

@@ -54,7 +54,16 @@ struct mq_decoder {
     DevBuf tok, out_norm;
     std::vector<DecLayer> layers;
     DevBuf x, h, qkv, att, y, gu, ws, rope, kvf;
+    mq_decoder_observer obs = nullptr;
+    void *obs_user = nullptr;
 };
+
+extern "C" int mq_decoder_set_observer(mq_decoder *m, mq_decoder_observer cb, void *user) {
+    if (!m) return set_error(MQ_EINVAL, "NULL runner");
+    m->obs = cb;
+    m->obs_user = user;
+    return MQ_OK;
+}
 
 extern "C" mq_decoder *mq_decoder_create(const mq_decoder_hparams *hp) {
     if (!hp || hp->n_layer <= 0 || hp->n_embd <= 0 || hp->n_head <= 0 || hp->n_kv_head <= 0 ||
@@ -143,8 +152,19 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
     float *X = hidden ? hidden : m->x.f();
     float *Hn = m->h.f();
     int rc;
-    auto mm = [&](const Linear &L, const float *in, int64_t ldin, float *y) {
-        return mq_mul_mat(t, L.img.p, L.n, L.k, in, ldin, rows, y, L.n, m->ws.p, m->ws.bytes, s);
+    // the observer sees a tensor once the work producing it is done
+    auto observe = [&](const char *name, int il, const float *x, int64_t cols, bool quantized) {
+        if (!m->obs) return MQ_OK;
+        if (hipStreamSynchronize(s) != hipSuccess) return set_error(MQ_EHIP, "stream synchronisation failed");
+        m->obs(name, il, x, rows, cols, quantized ? m->ws.p : nullptr, quantized ? m->ws.bytes : 0, m->obs_user);
+        return MQ_OK;
+    };
+    // a mat-mul of an fp32 input, quantized first (and observed under `name` when set)
+    auto mm = [&](const Linear &L, const float *in, int64_t ldin, float *y, const char *name = nullptr, int il = 0) {
+        const int path = mq_mul_mat_path(t, L.n, L.k, rows);
+        int r = mq_quantize_act(t, in, ldin, rows, L.k, m->ws.p, m->ws.bytes, path, s);
+        if (!r && name) r = observe(name, il, in, L.k, true);
+        return r ? r : mq_mul_mat_q(t, L.img.p, L.n, L.k, m->ws.p, rows, y, L.n, path, s);
     };
     // X = token_embd[ids]; Hn = rms_norm(X) * attn_norm[0]
     if ((rc = hip_rc(launch_add_rmsnorm(nullptr, nullptr, ids, m->tok.f(), hp.n_vocab, m->layers[0].attn_norm.f(), eps, X, Hn, rows,
@@ -160,21 +180,23 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
                         mq_mul_mat_path(t, m->layers[0].gu.n, H, rows) == MQ_PATH_GEMM &&
                         std::getenv("MQ_DECODER_NORM_PASS") == nullptr;
     bool hn_q = false;
-    auto mm_hn = [&](const Linear &L, float *y) {  // a product of Hn
-        if (!hn_q) return mm(L, Hn, H, y);
-        return mq_mul_mat_q(t, L.img.p, L.n, L.k, m->ws.p, rows, y, L.n, MQ_PATH_GEMM, s);
+    auto mm_hn = [&](const Linear &L, float *y, const char *name, int il) {  // a product of Hn
+        if (!hn_q) return mm(L, Hn, H, y, name, il);
+        int r = observe(name, il, Hn, H, true);
+        return r ? r : mq_mul_mat_q(t, L.img.p, L.n, L.k, m->ws.p, rows, y, L.n, MQ_PATH_GEMM, s);
     };
     auto add_norm = [&](const float *w, const char *what, bool last) {  // X += y; Hn = rms_norm(X) * w
-        if (norm_q) {  // inside the stack Hn is read only in its quantized form: not written
+        if (norm_q) {  // inside the stack Hn is read only in its quantized form: not written (unless observed)
             hn_q = true;
-            return hip_rc(launch_add_rmsnorm_q8_K(m->y.f(), X, w, eps, X, last ? Hn : nullptr, rows, (int)H, m->ws.p, s),
+            return hip_rc(launch_add_rmsnorm_q8_K(m->y.f(), X, w, eps, X, (last || m->obs) ? Hn : nullptr, rows, (int)H,
+                                                  m->ws.p, s),
                           what);
         }
         return hip_rc(launch_add_rmsnorm(m->y.f(), X, nullptr, nullptr, 0, w, eps, X, Hn, rows, (int)H, s), what);
     };
     for (size_t il = 0; il < m->layers.size(); il++) {
         const DecLayer &L = m->layers[il];
-        if ((rc = mm_hn(L.qkv, m->qkv.f()))) return rc;
+        if ((rc = mm_hn(L.qkv, m->qkv.f(), "attn_norm", (int)il))) return rc;
         hn_q = false;
         if ((rc = hip_rc(launch_attn_frag(m->qkv.f(), ldqkv, m->att.f(), qd, B, T, nq, nkv, hd,
                                           1.0f / sqrtf((float)hd), hp.causal, L.has_qn ? L.q_norm.f() : nullptr,
@@ -182,20 +204,23 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
                                           m->kvf.p, s),
                          "attention")))
             return rc;
-        if ((rc = mm(L.o, m->att.f(), qd, m->y.f()))) return rc;
+        if ((rc = mm(L.o, m->att.f(), qd, m->y.f(), "attn_out", (int)il))) return rc;
         // X += A Wo^T; Hn = rms_norm(X) * ffn_norm
         if ((rc = add_norm(L.ffn_norm.f(), "attention residual", false))) return rc;
-        if ((rc = mm_hn(L.gu, m->gu.f()))) return rc;
+        if ((rc = mm_hn(L.gu, m->gu.f(), "ffn_norm", (int)il))) return rc;
         hn_q = false;
         // down projection of silu(gate) * up, the product formed inside the quantizer
+        const int dpath = mq_mul_mat_path(t, L.down.n, L.down.k, rows);
         if ((rc = mq_quantize_act_ex(t, m->gu.f(), 2 * F, rows, F, nullptr, MQ_PRE_SILU_MUL, m->ws.p, m->ws.bytes,
-                                     MQ_PATH_AUTO, s)))
+                                     dpath, s)))
             return rc;
-        if ((rc = mq_mul_mat_q(t, L.down.img.p, L.down.n, L.down.k, m->ws.p, rows, m->y.f(), H, MQ_PATH_AUTO, s)))
+        if ((rc = observe("ffn_gate_up", (int)il, m->gu.f(), 2 * F, true))) return rc;
+        if ((rc = mq_mul_mat_q(t, L.down.img.p, L.down.n, L.down.k, m->ws.p, rows, m->y.f(), H, dpath, s)))
             return rc;
         // X += FFN; Hn = rms_norm(X) * (next layer's attn_norm, or the output norm)
         const float *wn = (il + 1 < m->layers.size()) ? m->layers[il + 1].attn_norm.f() : m->out_norm.f();
         if ((rc = add_norm(wn, "ffn residual", il + 1 == m->layers.size()))) return rc;
+        if ((rc = observe("l_out", (int)il, X, H, false))) return rc;
     }
     // mean pooling averages the output-normed rows (Hn); last-token pooling norms the last row
     if (hp.pooling == 1) return hip_rc(launch_mean_pool_l2(Hn, out, B, T, (int)H, s), "pooling");

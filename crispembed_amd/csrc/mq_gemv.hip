@@ -409,7 +409,7 @@ static hipError_t launch_kq_stream(const uint8_t *gv, const int8_t *xq, const fl
     if ((nsb + 7) / 8 > 3) {  // K > 6144: no operand cache
         hipLaunchKernelGGL((k_gemv_kq_any<TYPE>), dim3((unsigned)ntiles), dim3(512), 0, s, gv, xq, xd, xaux, y, (int)n,
                            (int)k, m, ldy, bias);
-        return hipSuccess;
+        return hipGetLastError();
     }
     GvGroups G{};
     G.gv0 = gv, G.y0 = y, G.b0 = bias, G.N0 = (int)n, G.ld0 = ldy;
@@ -442,11 +442,11 @@ static hipError_t launch_kq_stream_groups(const GvGroups &G, const int8_t *xq, c
     const int pf = pe ? atoi(pe) : 2;
     if (pf == 3 && sbw == 1) {
         hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 3>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m);
-        return hipSuccess;
+        return hipGetLastError();
     }
     if (pf == 2 && sbw == 1) {
         hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 2>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m);
-        return hipSuccess;
+        return hipGetLastError();
     }
     switch (sbw) {
         case 1: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 1>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m); break;
@@ -454,7 +454,7 @@ static hipError_t launch_kq_stream_groups(const GvGroups &G, const int8_t *xq, c
         case 3: hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 3, 1>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m); break;
         default: return hipErrorInvalidValue;
     }
-    return hipSuccess;
+    return hipGetLastError();
 }
 
 template <int MM>

@@ -908,6 +908,31 @@ extern "C" int mq_op_norm_q8_0(int kind, const mq_view *x, const mq_view *add, c
     return hip_rc(hipGetLastError(), "norm_q8_0");
 }
 
+extern "C" int mq_op_norm_q8_K(int kind, const mq_view *x, const mq_view *add, const mq_view *sum, const mq_view *dst,
+                               float eps, const float *w, void *workspace, size_t workspace_bytes, void *stream) {
+    if (kind != MQ_NORM_RMS) return fail("norm_q8_K: RMS norm only");
+    if (const char *e = check_norm(kind, x, add, dst ? dst : x)) return fail(e);
+    if (sum && (sum->type != MQ_TYPE_F32 || !shape_ok(sum) || !same_shape(x, sum)))
+        return fail("norm_q8_K: sum must be F32 with x's shape");
+    if (!have_data({x, add, sum, dst}) || !workspace || !w) return fail("missing data pointer");
+    const int64_t K = x->ne[0], rows = x->ne[1] * x->ne[2] * x->ne[3];
+    if (K % 256 != 0 || K > 2048) return fail("norm_q8_K: ne0 must be a multiple of 256, at most 2048");
+    for (const mq_view *t : {x, add, sum, dst})
+        if (t && (t->nb[0] != 4 || t->nb[1] != (size_t)K * 4 || t->nb[2] != t->nb[1] * (size_t)t->ne[1] ||
+                  t->nb[3] != t->nb[2] * (size_t)t->ne[2] || ((uintptr_t)t->data & 15)))
+            return fail("norm_q8_K: x, add, sum and dst must be dense, 16-byte aligned rows");
+    if (((uintptr_t)w & 15) || ((uintptr_t)workspace & 255))
+        return fail("norm_q8_K: w 16-byte, the workspace 256-byte aligned");
+    if (rows > INT32_MAX) return fail("norm_q8_K: too many rows");
+    const ActPlanes ap = act_planes(MQ_TYPE_Q4_K, rows, K, true);
+    if (workspace_bytes < ap.total) return fail("norm_q8_K: workspace too small");
+    const hipError_t e =
+        launch_add_rmsnorm_q8_K((const float *)x->data, add ? (const float *)add->data : nullptr, w, eps,
+                                sum ? (float *)sum->data : nullptr, dst ? (float *)dst->data : nullptr, rows, (int)K,
+                                workspace, (hipStream_t)stream);
+    return hip_rc(e, "norm_q8_K");
+}
+
 extern "C" int mq_op_cpy(const mq_view *src, const mq_view *dst, void *stream) {
     if (const char *e = check_cpy(src, dst)) return fail(e);
     if (!have_data({src, dst})) return fail("missing data pointer");

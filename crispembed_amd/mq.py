@@ -112,6 +112,7 @@ _SIGS = {
     "mq_decoder_set_embeddings": (_c_int, [_c_vp] * 3),
     "mq_decoder_set_layer": (_c_int, [_c_vp, _c_int] + [_c_vp] * 11),
     "mq_decoder_encode": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp]),
+    "mq_decoder_set_observer": (_c_int, [_c_vp, _c_vp, _c_vp]),
     "mq_qk_norm_rope": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, ctypes.c_float, _c_int, _c_int, _c_int, _c_int,
                                  ctypes.c_float, _c_i64, _c_vp]),
     "mq_attention_workspace_bytes": (ctypes.c_size_t, [_c_int, _c_int, _c_int, _c_int]),
@@ -155,6 +156,7 @@ _SIGS.update({
     "mq_op_unary": (_c_int, [_c_int, _PV, _PV, _c_vp]),
     "mq_op_norm": (_c_int, [_c_int, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_vp, _c_vp]),
     "mq_op_norm_q8_0": (_c_int, [_c_int, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_vp, _c_vp, _c_sz, _c_vp]),
+    "mq_op_norm_q8_K": (_c_int, [_c_int, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_vp, _c_sz, _c_vp]),
     "mq_op_cpy": (_c_int, [_PV, _PV, _c_vp]),
     "mq_op_flash_attn_workspace_bytes": (_c_sz, [_PV]),
     "mq_op_flash_attn": (_c_int, [_PV, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_sz, _c_vp]),
@@ -169,6 +171,10 @@ _SIGS.update({
     "mq_op_mul_mat_f32": (_c_int, [_PV, _PV, _PV, _c_vp]),
     "mq_op_rope": (_c_int, [_PV, _PV, _PV, _PV, _c_int, _c_int, _c_int] + [ctypes.c_float] * 6 + [_c_vp]),
 })
+
+
+# mq_decoder_observer (include/mq_decoder.h)
+DECODER_OBSERVER = ctypes.CFUNCTYPE(None, ctypes.c_char_p, _c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_sz, _c_vp)
 
 
 class DecoderHparams(ctypes.Structure):

@@ -122,7 +122,9 @@ int mq_weight_prepare(int type, void *image, int64_t n, int64_t k, int64_t row0,
  * per-block fp16/fp32 scales are applied in fp32.
  * `w_image` is a prepared weight image.  `workspace` receives the quantized
  * activations; size it with mq_workspace_bytes().  workspace == NULL makes the
- * library use (and grow with hipMalloc) an internal per-device buffer. */
+ * library use (and grow with hipMalloc) an internal buffer per (device, stream), so
+ * calls on different streams never share one; calls on one stream from several threads
+ * must be serialised by the caller (as ggml backends are, src/core/gpu_backend_pref.h:180-185). */
 /* The path MQ_PATH_AUTO of mq_mul_mat / mq_mul_mat_ex takes for an n x k weight and m rows:
  * MQ_PATH_GEMV up to mq_gemv_max_m() rows, and up to 32 rows while a 128 x 128 GEMM tile grid
  * would have fewer than 64 workgroups (short inputs on narrow layers); else MQ_PATH_GEMM.

@@ -55,6 +55,28 @@ int mq_decoder_set_layer(mq_decoder *m, int il, const void *wq, const void *wk, 
  * norm).  Enqueued on `stream`. */
 int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T, float *out, float *hidden, void *stream);
 
+/* An observer of the runner's intermediate tensors: the runner's form of the scheduler eval
+ * callback CrispEmbed installs to read every MUL_MAT's input (the imatrix collector,
+ * src/imatrix.cpp:57-99, installed at src/crispembed.cpp:723 and :2483).  With an observer set,
+ * mq_decoder_encode synchronises its stream after each tensor below is final and calls
+ *   cb(name, layer, x, rows, cols, xq, xq_bytes, user)
+ * with x a DEVICE fp32 tensor of rows x cols (dense rows) and xq the quantized activation the
+ * following mat-mul reads (DEVICE, in the layout mq_quantize_act_ex writes for the path
+ * mq_mul_mat_path(wtype, n, cols, rows) of that mat-mul) or NULL:
+ *   "attn_norm"  layer il's normed input, the src1 of the q/k/v mat-muls (xq: its quantization)
+ *   "attn_out"   the attention output rows, the src1 of the o projection (xq: its quantization)
+ *   "ffn_norm"   the normed input of the FFN, the src1 of gate/up (xq: its quantization)
+ *   "ffn_gate_up" the gate and up projections side by side (cols = 2 n_ff); the src1 of the
+ *                down projection is silu(gate) * up, which the quantizer forms (xq: its
+ *                quantization, cols n_ff)
+ *   "l_out"      the residual stream after layer il (xq NULL)
+ * The tensors are only valid during the call.  Observing makes the runner also write the
+ * normed rows it otherwise leaves only in quantized form (the quantized bytes do not change).
+ * cb NULL removes the observer. */
+typedef void (*mq_decoder_observer)(const char *name, int layer, const float *x, int64_t rows, int64_t cols,
+                                    const void *xq, size_t xq_bytes, void *user);
+int mq_decoder_set_observer(mq_decoder *m, mq_decoder_observer cb, void *user);
+
 /* The runner's non-MUL_MAT ops on caller buffers (device pointers, fp32), for callers that
  * build their own graph.  qkv holds B*T rows of ld floats: n_head query heads, then
  * n_kv_head key heads, then n_kv_head value heads, head_dim values each (ld a multiple of 4,

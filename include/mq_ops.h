@@ -102,6 +102,19 @@ int mq_op_norm(int kind, const mq_view *x, const mq_view *add, const mq_view *ds
 int mq_op_norm_q8_0(int kind, const mq_view *x, const mq_view *add, const mq_view *dst, float eps, const float *w,
                     const float *b, void *workspace, size_t workspace_bytes, void *stream);
 
+/* The decoder's form of mq_op_norm_q8_0, for mat-muls on K-quant weights (Q4_K / Q6_K, whose
+ * activations are Q8_K): sum = x + add (add NULL: sum = x; sum NULL: not written; sum may alias
+ * x), dst = rms_norm(sum) * w (dst NULL: not written), and the normed rows quantized to Q8_K
+ * in the GEMM-path activation layout -- the bytes mq_quantize_act_ex(MQ_TYPE_Q4_K, dst, ...,
+ * MQ_PATH_GEMM) writes for them -- into workspace (>= mq_workspace_bytes(MQ_TYPE_Q4_K, rows,
+ * ne0)).  The residual ADD, the rms_norm helper (ggml_rms_norm + ggml_mul,
+ * src/decoder_embed.cpp:680-683,722,789-790) and the from_float quantization of the q/k/v or
+ * gate/up MUL_MAT that reads its result (:724-728,793-795) in one pass.  kind must be
+ * MQ_NORM_RMS; x, add, sum and dst are dense, 16-byte aligned rows of ne0 floats, ne0 a
+ * multiple of 256 and at most 2048; w 16-byte aligned, the workspace 256-byte aligned. */
+int mq_op_norm_q8_K(int kind, const mq_view *x, const mq_view *add, const mq_view *sum, const mq_view *dst, float eps,
+                    const float *w, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Copies src into dst element by element in logical (row-major over ne0..ne3) order; the two
  * views hold the same number of elements and may differ in shape and strides (ggml_cpy,
  * ggml_cont, ggml_dup).  F32 / F16 either side (F32 -> F16 rounds to nearest even). */

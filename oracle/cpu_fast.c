@@ -19,8 +19,14 @@
  *                 sum(q6 * q8) - 32 * bsum_i; acc += d * dx * isum (ggml_vec_dot_q6_K_q8_K).
  * The activation quantizers are the oracle's (bit-exact ggml semantics).
  *
- * The SIMD code is AVX2 + FMA (every x86-64 host of this decade); the library is compiled
- * for that target, never for the build host's own ISA, so it runs on any such CPU.
+ * Two SIMD forms, chosen at run time from the host's CPUID (the library is built here and
+ * runs on another host, so it is never compiled for the build host's own ISA):
+ *   AVX-512 VNNI (+BW/VL): 64-byte vectors, two 32-value blocks (Q8_0) or two sub-blocks
+ *     (K-quants) per instruction; the int8 dots by vpdpbusd (Q8_0) and the scale-weighted
+ *     pair sums of the K-quants by vpmaddubsw + vpdpwssd;
+ *   AVX2 + FMA + F16C: every x86-64 host of this decade.
+ * Both produce the same integer sums; the fp32 accumulation order differs (as ggml's own
+ * AVX2 and AVX-512 builds differ), within the mul_mat bar of the exact product.
  */
 #include <immintrin.h>
 #include <pthread.h>
@@ -123,6 +129,125 @@ FAST_TARGET static float dot_q6_K(int64_t nb, const or_block_q6_K *w, const or_b
     return acc;
 }
 
+/* ---- AVX-512 VNNI forms ---- */
+#define VNNI_TARGET __attribute__((target("avx512f,avx512bw,avx512vl,avx512vnni,avx2,fma,f16c")))
+
+VNNI_TARGET static inline __m512i cat256(__m256i lo, __m256i hi) {
+    return _mm512_inserti64x4(_mm512_castsi256_si512(lo), hi, 1);
+}
+
+VNNI_TARGET static float dot_q8_0_vnni(int64_t nb, const or_block_q8_0 *w, const or_block_q8_0 *x) {
+    __m512 acc = _mm512_setzero_ps();
+    int64_t b = 0;
+    for (; b + 1 < nb; b += 2) {  /* two blocks: int32 lanes 0-7 block b, 8-15 block b + 1 */
+        const __m512i qw = cat256(_mm256_loadu_si256((const __m256i *)w[b].qs),
+                                  _mm256_loadu_si256((const __m256i *)w[b + 1].qs));
+        const __m512i qx = cat256(_mm256_loadu_si256((const __m256i *)x[b].qs),
+                                  _mm256_loadu_si256((const __m256i *)x[b + 1].qs));
+        /* |qw| (unsigned) times qx with qw's sign */
+        const __mmask64 neg = _mm512_movepi8_mask(qw);
+        const __m512i sx = _mm512_mask_sub_epi8(qx, neg, _mm512_setzero_si512(), qx);
+        const __m512i s = _mm512_dpbusd_epi32(_mm512_setzero_si512(), _mm512_abs_epi8(qw), sx);
+        const __m256 d0 = _mm256_set1_ps(_cvtsh_ss(w[b].d) * _cvtsh_ss(x[b].d));
+        const __m256 d1 = _mm256_set1_ps(_cvtsh_ss(w[b + 1].d) * _cvtsh_ss(x[b + 1].d));
+        const __m512 d = _mm512_castpd_ps(
+            _mm512_insertf64x4(_mm512_castpd256_pd512(_mm256_castps_pd(d0)), _mm256_castps_pd(d1), 1));
+        acc = _mm512_fmadd_ps(d, _mm512_cvtepi32_ps(s), acc);
+    }
+    float r = _mm512_reduce_add_ps(acc);
+    if (b < nb) r += dot_q8_0(nb - b, w + b, x + b);
+    return r;
+}
+
+VNNI_TARGET static float dot_q4_K_vnni(int64_t nb, const or_block_q4_K *w, const or_block_q8_K *x) {
+    const __m512i m4 = _mm512_set1_epi8(0x0F);
+    __m512 acc = _mm512_setzero_ps();
+    float accm = 0.0f;
+    for (int64_t b = 0; b < nb; b++) {
+        uint8_t sc[8], mn[8];
+        for (int j = 0; j < 8; j++) or_get_scale_min_k4(j, w[b].scales, &sc[j], &mn[j]);
+        int summ = 0;
+        for (int j = 0; j < 8; j++) summ += mn[j] * (x[b].bsums[2 * j] + x[b].bsums[2 * j + 1]);
+        __m512i sumi = _mm512_setzero_si512();
+        for (int h = 0; h < 2; h++) {
+            /* qs bytes 64h..64h+63: 64-value chunks 2h and 2h+1; low nibbles are sub-blocks 4h and 4h+2,
+             * high nibbles 4h+1 and 4h+3 */
+            const __m512i q4 = _mm512_loadu_si512((const void *)(w[b].qs + 64 * h));
+            const __m512i lo = _mm512_and_si512(q4, m4);
+            const __m512i hi = _mm512_and_si512(_mm512_srli_epi16(q4, 4), m4);
+            const int8_t *xs = x[b].qs + 128 * h;
+            const __m512i xlo = cat256(_mm256_loadu_si256((const __m256i *)xs), _mm256_loadu_si256((const __m256i *)(xs + 64)));
+            const __m512i xhi =
+                cat256(_mm256_loadu_si256((const __m256i *)(xs + 32)), _mm256_loadu_si256((const __m256i *)(xs + 96)));
+            const __m512i slo = cat256(_mm256_set1_epi16(sc[4 * h]), _mm256_set1_epi16(sc[4 * h + 2]));
+            const __m512i shi = cat256(_mm256_set1_epi16(sc[4 * h + 1]), _mm256_set1_epi16(sc[4 * h + 3]));
+            sumi = _mm512_dpwssd_epi32(sumi, _mm512_maddubs_epi16(lo, xlo), slo);
+            sumi = _mm512_dpwssd_epi32(sumi, _mm512_maddubs_epi16(hi, xhi), shi);
+        }
+        const float d = x[b].d * _cvtsh_ss(w[b].d);
+        const float dmin = x[b].d * _cvtsh_ss(w[b].dmin);
+        acc = _mm512_fmadd_ps(_mm512_set1_ps(d), _mm512_cvtepi32_ps(sumi), acc);
+        accm += dmin * (float)summ;
+    }
+    return _mm512_reduce_add_ps(acc) - accm;
+}
+
+VNNI_TARGET static float dot_q6_K_vnni(int64_t nb, const or_block_q6_K *w, const or_block_q8_K *x) {
+    const __m512i m4 = _mm512_set1_epi8(0x0F), m2 = _mm512_set1_epi8(0x03);
+    /* qh shifts: the lower 32 bytes of a pair take bits (0, 4), the upper (2, 6) */
+    const __m512i sh01 = cat256(_mm256_set1_epi16(0), _mm256_set1_epi16(2));
+    const __m512i sh23 = cat256(_mm256_set1_epi16(4), _mm256_set1_epi16(6));
+    /* int16 lane i of a 64-value pair belongs to 16-value sub-block i / 8 of the pair */
+    int16_t ix[32];
+    for (int i = 0; i < 32; i++) ix[i] = (int16_t)(i / 8);
+    const __m512i idx = _mm512_loadu_si512((const void *)ix);
+    float acc = 0.0f;
+    for (int64_t b = 0; b < nb; b++) {
+        const uint8_t *ql = w[b].ql, *qh = w[b].qh;
+        const int8_t *sc = w[b].scales;
+        int corr = 0;
+        for (int i = 0; i < 16; i++) corr += sc[i] * x[b].bsums[i];
+        const __m512i sc16 = _mm512_cvtepi8_epi16(_mm256_castsi128_si256(_mm_loadu_si128((const __m128i *)sc)));
+        __m512i sumi = _mm512_setzero_si512();
+        for (int h = 0; h < 2; h++) {
+            const __m512i l = _mm512_loadu_si512((const void *)(ql + 64 * h));  /* ql halves l0 | l1 */
+            const __m512i hb = _mm512_broadcast_i64x4(_mm256_loadu_si256((const __m256i *)(qh + 32 * h)));
+            /* values 128h + 0..63 and 128h + 64..127 */
+            const __m512i q01 = _mm512_or_si512(_mm512_and_si512(l, m4),
+                                                _mm512_slli_epi16(_mm512_and_si512(_mm512_srlv_epi16(hb, sh01), m2), 4));
+            const __m512i q23 = _mm512_or_si512(_mm512_and_si512(_mm512_srli_epi16(l, 4), m4),
+                                                _mm512_slli_epi16(_mm512_and_si512(_mm512_srlv_epi16(hb, sh23), m2), 4));
+            const __m512i x01 = _mm512_loadu_si512((const void *)(x[b].qs + 128 * h));
+            const __m512i x23 = _mm512_loadu_si512((const void *)(x[b].qs + 128 * h + 64));
+            const __m512i s01 = _mm512_permutexvar_epi16(_mm512_add_epi16(idx, _mm512_set1_epi16((short)(8 * h))), sc16);
+            const __m512i s23 =
+                _mm512_permutexvar_epi16(_mm512_add_epi16(idx, _mm512_set1_epi16((short)(8 * h + 4))), sc16);
+            sumi = _mm512_dpwssd_epi32(sumi, _mm512_maddubs_epi16(q01, x01), s01);
+            sumi = _mm512_dpwssd_epi32(sumi, _mm512_maddubs_epi16(q23, x23), s23);
+        }
+        const float d = _cvtsh_ss(w[b].d) * x[b].d;
+        acc += d * (float)(_mm512_reduce_add_epi32(sumi) - 32 * corr);
+    }
+    return acc;
+}
+
+static int host_vnni(void) {
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+           __builtin_cpu_supports("avx512vl") && __builtin_cpu_supports("avx512vnni");
+}
+
+/* The SIMD form or_fast_mul_mat uses on this host ("avx512vnni", "avx2" or "none"); OR_FAST_ISA=avx2
+ * forces the AVX2 form (for comparing the two). */
+const char *or_fast_isa(void) {
+    __builtin_cpu_init();
+    if (!(__builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma") && __builtin_cpu_supports("f16c")))
+        return "none";
+    const char *f = getenv("OR_FAST_ISA");
+    if (f && strcmp(f, "avx2") == 0) return "avx2";
+    return host_vnni() ? "avx512vnni" : "avx2";
+}
+
 typedef struct {
     int wtype;
     const uint8_t *w, *xq;
@@ -133,6 +258,7 @@ typedef struct {
     float *y;
     int64_t ntn, ntiles;
     int64_t next;  /* work counter (atomic) */
+    int vnni;
 } fast_job;
 
 enum { TILE_M = 16, TILE_N = 16 };
@@ -161,10 +287,18 @@ FAST_TARGET static void *dot_worker(void *arg) {
             for (int64_t ni = n0; ni < n1; ni++) {
                 const void *wr = j->w + ni * j->wrow;
                 float v;
-                switch (j->wtype) {
-                    case OR_TYPE_Q8_0: v = dot_q8_0(j->k / OR_QK8_0, wr, xr); break;
-                    case OR_TYPE_Q4_K: v = dot_q4_K(j->k / OR_QK_K, wr, xr); break;
-                    default: v = dot_q6_K(j->k / OR_QK_K, wr, xr); break;
+                if (j->vnni) {
+                    switch (j->wtype) {
+                        case OR_TYPE_Q8_0: v = dot_q8_0_vnni(j->k / OR_QK8_0, wr, xr); break;
+                        case OR_TYPE_Q4_K: v = dot_q4_K_vnni(j->k / OR_QK_K, wr, xr); break;
+                        default: v = dot_q6_K_vnni(j->k / OR_QK_K, wr, xr); break;
+                    }
+                } else {
+                    switch (j->wtype) {
+                        case OR_TYPE_Q8_0: v = dot_q8_0(j->k / OR_QK8_0, wr, xr); break;
+                        case OR_TYPE_Q4_K: v = dot_q4_K(j->k / OR_QK_K, wr, xr); break;
+                        default: v = dot_q6_K(j->k / OR_QK_K, wr, xr); break;
+                    }
                 }
                 j->y[mi * j->ldy + ni] = v;
             }
@@ -197,6 +331,7 @@ int or_fast_mul_mat(int wtype, const void *w, int64_t n, int64_t k, const float 
     fast_job j;
     memset(&j, 0, sizeof j);
     j.wtype = wtype;
+    j.vnni = strcmp(or_fast_isa(), "avx512vnni") == 0;
     j.w = (const uint8_t *)w;
     j.x = x;
     j.n = n;

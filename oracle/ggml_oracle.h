@@ -127,6 +127,7 @@ void or_mul_mat_exact(int wtype, const void *w, int64_t n, int64_t k, const void
 
 /* ---- CPU baseline (cpu_fast.c): the same mul_mat with AVX2 integer dots and threads ---- */
 int or_fast_supported(int wtype);
+const char *or_fast_isa(void);
 int or_fast_mul_mat(int wtype, const void *w, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m, float *y,
                     int64_t ldy, int nthreads);
 

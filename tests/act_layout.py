@@ -140,3 +140,28 @@ def dequant_image(wtype, img, m, k):
     q, d = decode_image(wtype, img, m, k)
     bs = 32 if wtype == O.Q8_0 else 256
     return (q.reshape(m, -1, bs).astype(np.float64) * d[:, :, None].astype(np.float64)).reshape(m, k)
+
+
+def live_difference(got, want, wtype, m, k):
+    """first_difference restricted to what a GEMM reads for its m live rows: the quants and
+    scales of rows < m (and for Q8_K their min-term operands).  The producers that quantize their
+    own output (norms, attention, the requantizing GEMM) write whole 32-row tiles of live rows;
+    row tiles past them are never read for a stored output and are left as they were."""
+    qg, dg = decode_image(wtype, got, m, k)
+    qw, dw = decode_image(wtype, want, m, k)
+    if not np.array_equal(qg, qw):
+        r, c = np.argwhere(qg != qw)[0]
+        return f"quants: {int((qg != qw).sum())} differ, first at row {r} col {c}"
+    if not np.array_equal(dg.view(np.uint32), dw.view(np.uint32)):
+        r, c = np.argwhere(dg.view(np.uint32) != dw.view(np.uint32))[0]
+        return f"scales: first difference at row {r} block {c}"
+    if wtype != O.Q8_0:
+        p = planes(wtype, m, k)
+        o, n = p["xmin"]
+        fg = np.asarray(got[o:o + n]).view(np.uint16).reshape(p["m_pad"] // 32, k // 256, 64, 8)
+        fw = np.asarray(want[o:o + n]).view(np.uint16).reshape(p["m_pad"] // 32, k // 256, 64, 8)
+        r = np.arange(m)
+        for half in (0, 32):
+            if not np.array_equal(fg[r // 32, :, half + r % 32], fw[r // 32, :, half + r % 32]):
+                return "min-term operands differ"
+    return None

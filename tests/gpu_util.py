@@ -74,3 +74,17 @@ def live_q8_0_planes(raw, m, k):
     off = -(-(m_pad * k) // 256) * 256
     d = raw[off:off + kch * m_pad * 4].view(np.float32).reshape(kch, m_pad)[:, :m]
     return q, d
+
+
+def fetch(ptr, nbytes):
+    """nbytes (a multiple of 4) of device memory at ptr, copied into a new host uint8 array by a
+    device-to-device copy (mq_op_cpy) into torch memory."""
+    t = torch()
+    n = nbytes // 4
+    dst = t.empty(max(n, 1), dtype=t.float32, device="cuda")
+    src = mq.View()
+    src.data, src.type = ptr, mq.TYPE_F32
+    for i, (ne, nb) in enumerate(((n, 4), (1, 4 * n), (1, 4 * n), (1, 4 * n))):
+        src.ne[i], src.nb[i] = ne, nb
+    mq.check(mq.lib().mq_op_cpy(ctypes.byref(src), ctypes.byref(mq.view(dst)), stream()))
+    return host(dst)[:n].view(np.uint8)

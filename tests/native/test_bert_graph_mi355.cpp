@@ -9,6 +9,12 @@
 //                              [--check-replay]
 //   ids / types: B*T int32 (item-major, t fastest); lens: B int32 real lengths (all T: no mask);
 //   out: the encoder_out tensor [H, B*T] as float32.  Prints one JSON line.
+//   --observe: then computes the graph as ggml's scheduler does when an eval callback observes
+//   every MUL_MAT (the imatrix collector, src/imatrix.cpp:57-99): in pieces that end at each
+//   MUL_MAT, reading that MUL_MAT's src1 after its piece, with every graph tensor first filled
+//   with NaN bytes; and once more node by node (MQ_GGML_NO_FUSION=1) as the reference.  Reports
+//   how many observed src1 still hold NaN (unwritten), the largest relative difference of any
+//   src1 and of the imatrix sums (sum of x^2 per column) against the node-by-node run.
 //   --check-replay: after the first (eager) compute, computes the graph for a second id set
 //   (each id + 1; the backend captures it), then for the first set and the second again (the
 //   captured graph replayed, with uploads and readbacks in between), and reports whether the
@@ -46,6 +52,8 @@ static int fail(const char *msg) {
     return 1;
 }
 
+static double fin(double x) { return std::isfinite(x) ? x : 1e30; }  // JSON has no inf / nan
+
 static uint16_t f16_bits(float x) {  // 0 and -inf only (the mask values)
     return std::isinf(x) ? 0xFC00 : 0x0000;
 }
@@ -54,11 +62,12 @@ int main(int argc, char **argv) {
     if (argc < 8) return fail("usage: model.gguf B T ids types lens out [--fused-qkv] [--iters N]");
     const char *path = argv[1];
     const int B = std::atoi(argv[2]), T = std::atoi(argv[3]);
-    bool fused_qkv = false, check_replay = false;
+    bool fused_qkv = false, check_replay = false, observe = false;
     int iters = 0;
     for (int i = 8; i < argc; i++) {
         if (!std::strcmp(argv[i], "--fused-qkv")) fused_qkv = true;
         if (!std::strcmp(argv[i], "--check-replay")) check_replay = true;
+        if (!std::strcmp(argv[i], "--observe")) observe = true;
         if (!std::strcmp(argv[i], "--iters") && i + 1 < argc) iters = std::atoi(argv[++i]);
     }
     const int TB = B * T;
@@ -201,16 +210,20 @@ int main(int argc, char **argv) {
     std::vector<int32_t> pos(TB);
     for (int b = 0; b < B; b++)
         for (int t = 0; t < T; t++) pos[(size_t)b * T + t] = t;
-    ggml_backend_tensor_set(tok_ids, ids_raw.data(), 0, (size_t)TB * 4);
-    ggml_backend_tensor_set(type_ids, types_raw.data(), 0, (size_t)TB * 4);
-    ggml_backend_tensor_set(pos_ids, pos.data(), 0, (size_t)TB * 4);
-    if (pad_mask) {
-        std::vector<uint16_t> m((size_t)B * T * T);
-        for (int b = 0; b < B; b++)
-            for (int q = 0; q < T; q++)
-                for (int k = 0; k < T; k++) m[((size_t)b * T + q) * T + k] = f16_bits(k < lens[b] ? 0.f : -INFINITY);
-        ggml_backend_tensor_set(pad_mask, m.data(), 0, m.size() * 2);
-    }
+    auto set_inputs = [&]() {
+        ggml_backend_tensor_set(tok_ids, ids_raw.data(), 0, (size_t)TB * 4);
+        ggml_backend_tensor_set(type_ids, types_raw.data(), 0, (size_t)TB * 4);
+        ggml_backend_tensor_set(pos_ids, pos.data(), 0, (size_t)TB * 4);
+        if (pad_mask) {
+            std::vector<uint16_t> m((size_t)B * T * T);
+            for (int b = 0; b < B; b++)
+                for (int q = 0; q < T; q++)
+                    for (int k = 0; k < T; k++)
+                        m[((size_t)b * T + q) * T + k] = f16_bits(k < lens[b] ? 0.f : -INFINITY);
+            ggml_backend_tensor_set(pad_mask, m.data(), 0, m.size() * 2);
+        }
+    };
+    set_inputs();
 
     if (ggml_backend_graph_compute(be, gf) != GGML_STATUS_SUCCESS) return fail("graph_compute failed");
     std::vector<float> out((size_t)H * TB);
@@ -240,6 +253,78 @@ int main(int argc, char **argv) {
         std::fclose(f2);
         ggml_backend_tensor_set(tok_ids, ids1, 0, (size_t)TB * 4);
     }
+    // imatrix-style observation of every MUL_MAT's src1 (see --observe above)
+    int observed = 0, src1_nan = -1;
+    double src1_max_rel = -1.0, imatrix_max_rel = -1.0, out_max_rel = -1.0;
+    if (observe) {
+        const int n = ggml_graph_n_nodes(gf);
+        std::vector<int> mms;
+        for (int i = 0; i < n; i++)
+            if (ggml_graph_node(gf, i)->op == GGML_OP_MUL_MAT) mms.push_back(i);
+        auto read_src1 = [&](int i, std::vector<float> &v) {
+            const ggml_tensor *x = ggml_graph_node(gf, i)->src[1];
+            v.resize(ggml_nbytes(x) / sizeof(float));
+            ggml_backend_tensor_get(x, v.data(), 0, ggml_nbytes(x));
+        };
+        std::vector<std::vector<float>> seen(mms.size()), ref(mms.size());
+        ggml_backend_buffer_clear(gbuf, 0xFF);  // 0xFFFFFFFF is a NaN: an unwritten src1 shows
+        set_inputs();
+        int i0 = 0;
+        for (size_t j = 0; j < mms.size(); j++) {
+            ggml_cgraph *v = ggml_compat_graph_view(gf, i0, mms[j] + 1);
+            const enum ggml_status st = ggml_backend_graph_compute(be, v);
+            ggml_compat_graph_view_free(v);
+            if (st != GGML_STATUS_SUCCESS) return fail("graph_compute of an observed piece failed");
+            read_src1(mms[j], seen[j]);
+            i0 = mms[j] + 1;
+        }
+        ggml_cgraph *tail = ggml_compat_graph_view(gf, i0, n);
+        const enum ggml_status st_tail = ggml_backend_graph_compute(be, tail);
+        ggml_compat_graph_view_free(tail);
+        if (st_tail != GGML_STATUS_SUCCESS) return fail("graph_compute of the last piece failed");
+        std::vector<float> obs_out(out.size());
+        ggml_backend_tensor_get(cur, obs_out.data(), 0, obs_out.size() * sizeof(float));
+        // the reference: node by node, every intermediate written
+        ggml_backend_buffer_clear(gbuf, 0xFF);
+        set_inputs();
+        setenv("MQ_GGML_NO_FUSION", "1", 1);
+        const enum ggml_status st_ref = ggml_backend_graph_compute(be, gf);
+        unsetenv("MQ_GGML_NO_FUSION");
+        if (st_ref != GGML_STATUS_SUCCESS) return fail("node-by-node graph_compute failed");
+        for (size_t j = 0; j < mms.size(); j++) read_src1(mms[j], ref[j]);
+        observed = (int)mms.size();
+        src1_nan = 0;
+        src1_max_rel = imatrix_max_rel = 0.0;
+        for (size_t j = 0; j < mms.size(); j++) {
+            const std::vector<float> &a = seen[j], &r = ref[j];
+            const int64_t ne0 = ggml_graph_node(gf, mms[j])->src[1]->ne[0];
+            bool nan = false;
+            double mx = 0.0, d = 0.0;
+            std::vector<double> sa(ne0, 0.0), sr(ne0, 0.0);  // imatrix: sum of x^2 per column
+            for (size_t e = 0; e < a.size(); e++) {
+                nan |= std::isnan(a[e]) || std::isnan(r[e]);
+                mx = std::fmax(mx, std::fabs((double)r[e]));
+                d = std::fmax(d, std::fabs((double)a[e] - (double)r[e]));
+                sa[e % ne0] += (double)a[e] * a[e];
+                sr[e % ne0] += (double)r[e] * r[e];
+            }
+            src1_nan += nan;
+            src1_max_rel = std::fmax(src1_max_rel, nan ? INFINITY : d / (mx > 0 ? mx : 1.0));
+            double smx = 0.0, sd = 0.0;
+            for (int64_t c = 0; c < ne0; c++) {
+                smx = std::fmax(smx, sr[c]);
+                sd = std::fmax(sd, std::fabs(sa[c] - sr[c]));
+            }
+            imatrix_max_rel = std::fmax(imatrix_max_rel, nan ? INFINITY : sd / (smx > 0 ? smx : 1.0));
+        }
+        double omx = 0.0, od = 0.0;
+        for (size_t e = 0; e < out.size(); e++) {
+            omx = std::fmax(omx, std::fabs((double)out[e]));
+            od = std::fmax(od, std::fabs((double)obs_out[e] - (double)out[e]));
+        }
+        out_max_rel = std::isnan(od) ? INFINITY : od / (omx > 0 ? omx : 1.0);
+        set_inputs();
+    }
     double ms = 0.0;
     if (iters > 0) {
         const auto t0 = std::chrono::steady_clock::now();
@@ -248,8 +333,10 @@ int main(int argc, char **argv) {
         ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() / iters;
     }
     std::printf("{\"ok\": true, \"nodes\": %d, \"unsupported\": %d, \"ms_per_graph\": %.4f, \"iters\": %d, "
-                "\"replay_identical\": %d}\n",
-                ggml_graph_n_nodes(gf), unsupported, ms, iters, replay_identical);
+                "\"replay_identical\": %d, \"observed\": %d, \"src1_nan\": %d, \"src1_max_rel\": %.3g, "
+                "\"imatrix_max_rel\": %.3g, \"out_max_rel\": %.3g}\n",
+                ggml_graph_n_nodes(gf), unsupported, ms, iters, replay_identical, observed, src1_nan, fin(src1_max_rel),
+                fin(imatrix_max_rel), fin(out_max_rel));
     ggml_backend_buffer_free(gbuf);
     ggml_backend_buffer_free(wbuf);
     ggml_free(gctx);

@@ -56,6 +56,7 @@ class Oracle:
             "or_make_qkx2_quants": (ctypes.c_float, [ci, ci, vp, vp, vp, vp, ctypes.c_float, ctypes.c_float, ci]),
             "or_make_qx_quants": (ctypes.c_float, [ci, ci, vp, vp]),
             "or_set_mutation": (None, [ci]),
+            "or_fast_isa": (ctypes.c_char_p, []),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -139,6 +140,10 @@ class Oracle:
 
     def fast_supported(self, wtype):
         return bool(self.L.or_fast_supported(wtype))
+
+    def fast_isa(self):
+        """The SIMD form the CPU baseline uses on this host: "avx512vnni", "avx2" or "none"."""
+        return self.L.or_fast_isa().decode()
 
     def fast_mul_mat(self, wtype, w, x, nthreads=8):
         """The CPU baseline (AVX2 integer dots, threads); same semantics as mul_mat."""

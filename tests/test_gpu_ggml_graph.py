@@ -180,3 +180,48 @@ def test_bert_graph_hip_graph_replay(tmp_path):
     a_eager, _ = _run(tmp_path, model, B, T, ids, types, np.full(B, T), ("--check-replay",))
     second_eager = np.fromfile(tmp_path / "out.f32.second", dtype=np.float32)
     assert np.array_equal(a, a_eager) and np.array_equal(second, second_eager)
+
+
+@pytest.mark.parametrize("fused_qkv", [False, True])
+@pytest.mark.parametrize("T", [40, 64])
+def test_imatrix_observer_reads_every_src1(tmp_path, fused_qkv, T):
+    """The MUL_MAT observer contract (src/imatrix.cpp:57-99, installed at src/crispembed.cpp:723):
+    with an eval callback the scheduler computes the graph in pieces that end at each observed
+    MUL_MAT and then reads its src1.  Every graph tensor starts as NaN bytes, so a src1 a fusion
+    left unwritten shows: none may, every src1 must equal the node-by-node run's (to the last
+    bits of the fused norm's lane order) and so must the imatrix sums of x^2, and the pieces
+    together must compute the same encoder output."""
+    W = bert.synthetic_weights(HP, O.Q8_0, name="graphobs")
+    model = tmp_path / "m.gguf"
+    gguf.write_bert_gguf(model, HP, O.Q8_0, W)
+    B = 3
+    ids = np.random.default_rng(12).integers(0, HP["n_vocab"], (B, T)).astype(np.int32)
+    types = np.zeros((B, T), np.int32)
+    extra = ("--observe", "--fused-qkv") if fused_qkv else ("--observe",)
+    _, res = _run(tmp_path, model, B, T, ids, types, np.full(B, T), extra)
+    per_layer = 4 if fused_qkv else 6
+    assert res["observed"] == per_layer * HP["n_layer"]
+    assert res["src1_nan"] == 0
+    assert res["src1_max_rel"] <= 1e-5 and res["imatrix_max_rel"] <= 1e-5, res
+    assert res["out_max_rel"] <= 1e-4, res
+
+
+def test_bert_graph_minilm_full_shape(oracle, tmp_path):
+    """The MiniLM-L6 shape of the end-to-end workload through the ggml graph: 6 layers, H 384,
+    12 heads, FFN 1536, 32 sequences x 128 tokens, Q8_0 (the same batch the embeddings/s
+    figure is measured on), against the CPU encoder on sampled sequences (each sequence is
+    independent: no mask, attention within the item), and every row finite."""
+    hp = dict(bert.MINILM_L6)
+    W = bert.synthetic_weights(hp, O.Q8_0, name="minilm")
+    model = tmp_path / "m.gguf"
+    gguf.write_bert_gguf(model, hp, O.Q8_0, W)
+    B, T = 32, 128
+    ids = np.random.default_rng(32128).integers(1000, 30521, (B, T)).astype(np.int32)
+    types = np.zeros((B, T), np.int32)
+    got, _ = _run(tmp_path, model, B, T, ids, types, np.full(B, T))
+    assert np.isfinite(got).all()
+    for b in (0, 17, 31):
+        _, ref = bert_oracle.encode(oracle, hp, O.Q8_0, W, ids[b:b + 1], types[b:b + 1])
+        rows = got[b * T:(b + 1) * T]
+        assert _cos_rows(rows, ref).min() >= COSINE_MIN, b
+        assert _pool(rows) @ _pool(ref) >= COSINE_MIN, b

@@ -55,15 +55,31 @@ def test_q4_K_min_term_matters(oracle):
     assert rel_err(b, a) > 1e-2
 
 
+@pytest.mark.parametrize("isa", ["host", "avx2"])
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_K, O.Q6_K])
-@pytest.mark.parametrize("m,n,k", [(1, 3, 256), (17, 33, 512), (40, 20, 1536)])
-def test_cpu_baseline_matches_exact_product(oracle, wtype, m, n, k):
-    """The SIMD + threads CPU baseline computes the same mul_mat (block dots in another order)."""
+@pytest.mark.parametrize("m,n,k", [(1, 3, 256), (17, 33, 512), (40, 20, 1536), (5, 9, 2304)])
+def test_cpu_baseline_matches_exact_product(oracle, monkeypatch, isa, wtype, m, n, k):
+    """The SIMD + threads CPU baseline computes the same mul_mat (block dots in another order),
+    in its AVX-512 VNNI form where the host has it and in its AVX2 form."""
     if not oracle.fast_supported(wtype):
         pytest.skip("host without AVX2/FMA/F16C")
+    if isa == "avx2":
+        monkeypatch.setenv("OR_FAST_ISA", "avx2")
+        assert oracle.fast_isa() == "avx2"
     wf, x = _case(wtype, m, n, k, 300 + m + n + k + wtype)
     w = oracle.quantize_chunk(wtype, wf)
     xq = oracle.quantize_act(wtype, x)
     y = oracle.fast_mul_mat(wtype, w, x, nthreads=3)
     assert rel_err(y, mul_mat_exact(wtype, w, xq, k)) < 1e-5
     assert rel_err(y, oracle.mul_mat(wtype, w, x)) < 1e-5
+
+
+@pytest.mark.parametrize("k", [96, 288])
+def test_cpu_baseline_q8_0_odd_block_count(oracle, k):
+    """An odd number of Q8_0 blocks per row: the VNNI form's pairs plus its one-block tail."""
+    if not oracle.fast_supported(O.Q8_0):
+        pytest.skip("host without AVX2/FMA/F16C")
+    wf, x = _case(O.Q8_0, 7, 5, k, k)
+    w = oracle.quantize_chunk(O.Q8_0, wf)
+    y = oracle.fast_mul_mat(O.Q8_0, w, x, nthreads=2)
+    assert rel_err(y, mul_mat_exact(O.Q8_0, w, oracle.quantize_act(O.Q8_0, x), k)) < 1e-5
