@@ -431,3 +431,60 @@ int mq_mul_mat(int type, const void *w_image, int64_t n, int64_t k, const float 
 }
 
 }  // extern "C"
+
+namespace {
+
+// The quantized activations of mq_mul_mat_noalloc: a file-scope device array, so the call needs
+// no allocation.  Each GPU holds its own copy at its own address, found once per device with
+// hipGetSymbolAddress (the array's name is only a host-side stand-in for the device address).
+static __device__ __align__(256) uint8_t scratch[MQ_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+void *g_scratch[64];  // per HIP device ordinal: the device address of `scratch`
+
+int scratch_ptr(void **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) return fail(MQ_EINVAL, "device ordinal %d", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress");
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return MQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mq_mul_mat_noalloc(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m,
+                       float *y, int64_t ldy, int path, void *stream) {
+    int rc = check_weight_shape(type, n, k);
+    if (rc) return rc;
+    if (!w_image || !x || !y) return fail(MQ_EINVAL, "mq_mul_mat_noalloc: NULL pointer");
+    if (m < 0 || m > INT32_MAX || ldx < k || ldy < n) return fail(MQ_EINVAL, "mq_mul_mat_noalloc: bad m/ldx/ldy");
+    if (m == 0) return MQ_OK;
+    if (!is_aligned(w_image, 256)) return fail(MQ_EINVAL, "mq_mul_mat_noalloc: weight image must be 256-byte aligned");
+    if (path == MQ_PATH_AUTO) path = mq_mul_mat_path(type, n, k, m);
+    path = resolve_path(path, m);
+    if (path < 0) return path;
+    const size_t need = act_workspace_bytes(type, m, k);
+    if (need > (size_t)MQ_NOALLOC_SCRATCH_BYTES)
+        return fail(MQ_EINVAL, "mq_mul_mat_noalloc: m=%lld x k=%lld needs %zu bytes of activations, more than the %u-byte "
+                    "scratch array", (long long)m, (long long)k, need, (unsigned)MQ_NOALLOC_SCRATCH_BYTES);
+    void *ws = nullptr;
+    rc = scratch_ptr(&ws);
+    if (rc) return rc;
+    // every byte the kernels read is written first by the quantizer (pad rows and pad K bytes
+    // included), so the previous call's contents need no clearing
+    rc = mq_quantize_act(type, x, ldx, m, k, ws, MQ_NOALLOC_SCRATCH_BYTES, path, stream);
+    if (rc) return rc;
+    return mq_mul_mat_q(type, w_image, n, k, ws, m, y, ldy, path, stream);
+}
+
+}  // extern "C"

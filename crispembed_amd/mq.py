@@ -71,6 +71,8 @@ _SIGS = {
                                     _c_int, _c_vp]),
     "mq_mul_mat_ex": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                                _c_sz, _c_int, _c_vp]),
+    "mq_mul_mat_noalloc": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_int,
+                                    _c_vp]),
     # include/mq_bert.h
     "mq_bert_create": (_c_vp, [_c_vp]),
     "mq_bert_free": (None, [_c_vp]),

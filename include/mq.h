@@ -136,6 +136,19 @@ int mq_mul_mat(int type, const void *w_image, int64_t n, int64_t k, const float 
 int mq_mul_mat_ex(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m,
                   float *y, int64_t ldy, void *workspace, size_t workspace_bytes, int path, void *stream);
 
+/* mq_mul_mat_ex that allocates nothing.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc).  The quantized activations go to a fixed device array
+ * inside libmq.so of MQ_NOALLOC_SCRATCH_BYTES (64 MiB) per GPU, held until the process ends,
+ * instead of a workspace argument or an internal hipMalloc'd buffer; results equal
+ * mq_mul_mat_ex's bit for bit.  Calls whose mq_workspace_bytes(type, m, k) exceeds the array
+ * fail with MQ_EINVAL (e.g. Q8_K activations of 8192 x 4096 need 38.4 MB and fit; 16384 x 4096
+ * do not).  Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two
+ * streams, or two threads) race on it and must be serialised by the caller. */
+#define MQ_NOALLOC_SCRATCH_BYTES (64u << 20)
+int mq_mul_mat_noalloc(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m,
+                       float *y, int64_t ldy, int path, void *stream);
+
 /* The two halves of mq_mul_mat_ex, for callers that reuse one quantized X for
  * several weights (q, k and v share their input in every encoder layer,
  * src/crispembed.cpp:1168-1170) or time the stages separately.
