@@ -98,6 +98,33 @@ int check_weight_shape(int type, int64_t n, int64_t k) {
 
 bool is_aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// The library's own activation workspace for work queued on `stream` of the current device, grown
+// (hipMalloc) to at least `need` bytes.
+int stream_workspace(size_t need, void *stream, void **ws, size_t *bytes) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    Workspace &w = g_ws[{dev, stream}];
+    if (w.bytes < need) {
+        // the old buffer may still be read by work queued earlier on this stream
+        e = hipStreamSynchronize((hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+        if (w.ptr) (void)hipFree(w.ptr);
+        w.ptr = nullptr;
+        w.bytes = 0;
+        e = hipMalloc(&w.ptr, need);
+        if (e != hipSuccess) {
+            w.ptr = nullptr;
+            return fail(MQ_ENOMEM, "hipMalloc(%zu) for the activation workspace failed", need);
+        }
+        w.bytes = need;
+    }
+    *ws = w.ptr;
+    *bytes = w.bytes;
+    return MQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -375,6 +402,47 @@ int mq_mul_mat_q_group(int type, int n_groups, const void *const *w_images, cons
     return e == hipSuccess ? MQ_OK : hip_fail(e, "gemm");
 }
 
+int mq_mul_mat_gemv(int type, int n_groups, const void *const *w_images, const int64_t *n, int64_t k, const float *x,
+                    int64_t ldx, const float *x2, int64_t ldx2, int op, int64_t m, float *const *y, const int64_t *ldy,
+                    const float *const *bias, void *stream) {
+    if (n_groups < 1 || n_groups > 3 || !w_images || !n || !y || !ldy || !x)
+        return fail(MQ_EINVAL, "mq_mul_mat_gemv: 1 to 3 groups with weights, n, y, ldy and x");
+    for (int g = 0; g < n_groups; g++) {
+        const int rc = check_weight_shape(type, n[g], k);
+        if (rc) return rc;
+        if (!w_images[g] || !y[g] || ldy[g] < n[g] || !is_aligned(w_images[g], 256))
+            return fail(MQ_EINVAL, "mq_mul_mat_gemv: group %d: bad weight image, output or ldy", g);
+    }
+    if (op != MQ_PRE_NONE && op != MQ_PRE_SILU_MUL) return fail(MQ_EINVAL, "mq_mul_mat_gemv: op must be MQ_PRE_NONE or MQ_PRE_SILU_MUL");
+    if (op == MQ_PRE_SILU_MUL && (!x2 || ldx2 < k)) return fail(MQ_EINVAL, "mq_mul_mat_gemv: MQ_PRE_SILU_MUL needs x2");
+    if (m < 0 || ldx < k) return fail(MQ_EINVAL, "mq_mul_mat_gemv: bad m or ldx");
+    if (m == 0) return MQ_OK;
+    if (!gemv_fused_ok(type, n_groups, k, m))
+        return fail(MQ_EUNSUPPORTED, "mq_mul_mat_gemv: K-quant weights, m <= %d and k <= 6144 only", GEMV_CHUNK);
+    if (!is_aligned(x, 16) || (ldx & 3) || (x2 && (!is_aligned(x2, 16) || (ldx2 & 3))))
+        return fail(MQ_EINVAL, "mq_mul_mat_gemv: x / x2 must be 16-byte aligned with row strides a multiple of 4");
+    // Every workgroup quantizes the whole activation it reads: that pays (a launch saved) while it
+    // is a few superblock-rows, SiLU rows costing about three plain ones.  Measured on MI355X
+    // (HIP-graph replay, us): q|k|v, m = 8: 5.2 fused / 6.0 two launches; down (k 6144, SiLU):
+    // m = 1 7.4 / 7.7, m = 2 8.8 / 8.0.  Past that the activation is quantized once, into the
+    // stream's internal workspace, and read by the GEMV: the same bytes, the same results.
+    // MQ_GEMV_FUSED: 1 always quantizes inside the GEMV, 0 never (where the layout allows)
+    const int force = env_int("MQ_GEMV_FUSED", -1);
+    const bool side_by_side = op != MQ_PRE_SILU_MUL || (x2 == x + k && ldx2 == ldx);
+    const bool two_step = force == 0 || (force < 0 && m * (k / QK_K) * (op == MQ_PRE_SILU_MUL ? 3 : 1) > 100);
+    if (two_step && side_by_side) {
+        void *ws = nullptr;
+        size_t wsb = 0;
+        int rc = stream_workspace(act_workspace_bytes(type, m, k), stream, &ws, &wsb);
+        if (!rc) rc = mq_quantize_act_ex(type, x, ldx, m, k, nullptr, op, ws, wsb, MQ_PATH_GEMV, stream);
+        if (!rc) rc = mq_mul_mat_q_group(type, n_groups, w_images, n, k, ws, m, y, ldy, bias, MQ_PATH_GEMV, stream);
+        return rc;
+    }
+    const hipError_t e = launch_gemv_group_f32(type, n_groups, w_images, n, k, x, ldx, op == MQ_PRE_SILU_MUL ? x2 : nullptr,
+                                               ldx2, op, m, y, ldy, bias, (hipStream_t)stream);
+    return e == hipSuccess ? MQ_OK : hip_fail(e, "gemv");
+}
+
 int mq_mul_mat_q(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m, float *y,
                  int64_t ldy, int path, void *stream) {
     return mq_mul_mat_q_ex(type, w_image, n, k, workspace, m, y, ldy, nullptr, path, stream);
@@ -397,28 +465,8 @@ int mq_mul_mat_ex(int type, const void *w_image, int64_t n, int64_t k, const flo
         if (workspace_bytes < need)
             return fail(MQ_EINVAL, "mq_mul_mat: workspace %zu bytes < %zu needed", workspace_bytes, need);
     } else {
-        int dev = 0;
-        hipError_t e = hipGetDevice(&dev);
-        if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-        if (dev < 0 || dev >= 64) return fail(MQ_EINVAL, "device ordinal %d", dev);
-        std::lock_guard<std::mutex> lk(g_ws_mu);
-        Workspace &w = g_ws[{dev, stream}];
-        if (w.bytes < need) {
-            // the old buffer may still be read by work queued earlier on this stream
-            e = hipStreamSynchronize((hipStream_t)stream);
-            if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
-            if (w.ptr) (void)hipFree(w.ptr);
-            w.ptr = nullptr;
-            w.bytes = 0;
-            e = hipMalloc(&w.ptr, need);
-            if (e != hipSuccess) {
-                w.ptr = nullptr;
-                return fail(MQ_ENOMEM, "hipMalloc(%zu) for the activation workspace failed", need);
-            }
-            w.bytes = need;
-        }
-        ws = w.ptr;
-        workspace_bytes = w.bytes;
+        rc = stream_workspace(need, stream, &ws, &workspace_bytes);
+        if (rc) return rc;
     }
     rc = mq_quantize_act(type, x, ldx, m, k, ws, workspace_bytes, path, stream);
     if (rc) return rc;

@@ -282,29 +282,125 @@ struct GvGroups {
     int ts1, ts2, tend;
 };
 
-template <int TYPE, int SBW, int PF>
+// fp32 activation rows the GEMV quantizes itself (FQ = true): x (row stride ldx floats), and for
+// MQ_PRE_SILU_MUL the up projection rows x2 (stride ldx2): the value quantized is then
+// silu(x) * x2, as the activation quantizer's prologue forms it.
+struct GvX {
+    const float *x, *x2;
+    int64_t ldx, ldx2;
+    int pre;
+};
+
+// One 256-value superblock sb of rows 0..M-1 of the activation quantized to Q8_K
+// (quantize_row_q8_K: the first value of largest magnitude sets iscale = -127 / max,
+// q = min(127, nearest_int(iscale x)), d = 1 / iscale, the 16-value sums) by one wave: VPL
+// values per lane, 256 / VPL lanes per row, 64 VPL / 256 rows per pass (VPL 4: one row at a
+// time over all 64 lanes; 16: four rows), into this wave's LDS slot laid out as one superblock
+// of the GEMV activation layout: quants qs[row][256], d ds[row], and the Q4_K min-term operand
+// gs[row][16] (B_j & 63, then 64 (B_j >> 6), B_j the sum of the 32 quants of sub-block j).  The
+// arithmetic is the activation quantizer's (no contraction), so the bytes are the ones it writes.
+template <int VPL>
+__device__ __forceinline__ void gv_quantize_sb(const GvX &X, int sb, int M, int lane, int8_t *qs, float *ds,
+                                               _Float16 *gs) {
+#pragma clang fp contract(off)
+    constexpr int LPR = QK_K / VPL, RPP = 64 / LPR;  // lanes per row, rows per pass
+    const int r0 = lane / LPR, p = lane % LPR, gbase = lane - p;
+    for (int rb = 0; rb < M; rb += RPP) {
+        const int m = rb + r0;
+        float v[VPL];
+        if (m < M) {
+            const float *xr = X.x + (int64_t)m * X.ldx + sb * QK_K + VPL * p;
+#pragma unroll
+            for (int u = 0; u < VPL / 4; u++) {
+                const float4 a = *(const float4 *)(xr + 4 * u);
+                v[4 * u] = a.x, v[4 * u + 1] = a.y, v[4 * u + 2] = a.z, v[4 * u + 3] = a.w;
+            }
+            if (X.pre == MQ_PRE_SILU_MUL) {
+                const float *ur = X.x2 + (int64_t)m * X.ldx2 + sb * QK_K + VPL * p;
+#pragma unroll
+                for (int u = 0; u < VPL / 4; u++) {
+                    const float4 b = *(const float4 *)(ur + 4 * u);
+                    const float w4[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[4 * u + e] = (v[4 * u + e] / (1.0f + expf(-v[4 * u + e]))) * w4[e];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < VPL; e++) v[e] = 0.f;
+        }
+        // the lane's first value of largest magnitude, then the row's lowest such lane
+        float la = 0.f, lm = 0.f;
+#pragma unroll
+        for (int e = 0; e < VPL; e++)
+            if (fabsf(v[e]) > la) la = fabsf(v[e]), lm = v[e];
+        float amax = la;
+#pragma unroll
+        for (int off = LPR / 2; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, LPR));
+        const unsigned long long hit = __ballot(la == amax) >> gbase;
+        const unsigned long long row_hits = LPR == 64 ? hit : (hit & ((1ull << LPR) - 1));
+        const float mx = __shfl(lm, gbase + __ffsll((long long)row_hits) - 1);
+        uint32_t w[VPL / 4];
+#pragma unroll
+        for (int u = 0; u < VPL / 4; u++) w[u] = 0;
+        int s = 0;
+        float dval = 0.f;
+        if (amax != 0.0f) {
+            const float iscale = -127.f / mx;
+#pragma unroll
+            for (int e = 0; e < VPL; e++) {
+                const float f = iscale * v[e] + 12582912.f;  // ggml's nearest_int
+                int q = (__float_as_int(f) & 0x007fffff) - 0x00400000;
+                q = q < 127 ? q : 127;
+                w[e >> 2] |= (uint32_t)(q & 0xff) << (8 * (e & 3));
+                s += q;
+            }
+            dval = 1.0f / iscale;
+        }
+        // the sum of the 32 quants of sub-block (VPL p) / 32, complete in its first lane
+#pragma unroll
+        for (int off = 1; off < 32 / VPL; off <<= 1) s += __shfl_xor(s, off, LPR);
+        if (m < M) {
+#pragma unroll
+            for (int u = 0; u < VPL / 4; u++) *(uint32_t *)(qs + m * QK_K + VPL * p + 4 * u) = w[u];
+            if (p == 0) ds[m] = dval;
+            if ((VPL * p) % 32 == 0) {
+                const int j = VPL * p / 32;
+                gs[m * 16 + j] = (_Float16)(s & 63);
+                gs[m * 16 + 8 + j] = (_Float16)((s >> 6) * 64);
+            }
+        }
+    }
+}
+
+// gv_quantize_sb with the lane mapping that keeps the most lanes busy for M rows
+__device__ __forceinline__ void gv_quantize_rows(const GvX &X, int sb, int M, int lane, int8_t *qs, float *ds,
+                                                 _Float16 *gs) {
+    if (M == 1) gv_quantize_sb<4>(X, sb, M, lane, qs, ds, gs);
+    else if (M == 2) gv_quantize_sb<8>(X, sb, M, lane, qs, ds, gs);
+    else gv_quantize_sb<16>(X, sb, M, lane, qs, ds, gs);
+}
+
+template <int TYPE, int SBW, int PF, bool FQ = false>
 __global__ __launch_bounds__(512) void k_gemv_kq_stream(const GvGroups G, const int8_t *__restrict__ xq,
                                                         const float *__restrict__ xd, const void *__restrict__ xaux,
-                                                        int K, int M) {
+                                                        int K, int M, const GvX X = GvX{}) {
     constexpr bool Q4 = TYPE == MQ_TYPE_Q4_K;
     constexpr int BYTES = Q4 ? GV4_BYTES : GV6_BYTES;
     using W = typename std::conditional<Q4, Q4W, Q6W>::type;
     using A = typename std::conditional<Q4, Q4Act, Q6Act>::type;
     __shared__ float red[2][8][GV_ROWS][8];
+    // FQ: each wave's superblocks of the activation, quantized in the prologue
+    __shared__ __attribute__((aligned(16))) int8_t aq[FQ ? 8 * SBW : 1][GEMV_CHUNK * QK_K];
+    __shared__ float ad[FQ ? 8 * SBW : 1][GEMV_CHUNK];
+    __shared__ __attribute__((aligned(16))) _Float16 ag[FQ ? 8 * SBW : 1][GEMV_CHUNK * 16];
     const GvLane L = gv_lane(M);
     const int nsb = K / QK_K;
     const int ntiles = G.tend;
     bool live[SBW];
     A act[SBW];
-#pragma unroll
-    for (int i = 0; i < SBW; i++) {
-        const int sb = L.wave + 8 * i;
-        live[i] = sb < nsb;
-        if (live[i]) {
-            if constexpr (Q4) act[i] = q4_act(L, xq, xd, (const _Float16 *)xaux, K, M, sb);
-            else act[i] = q6_act(L, xq, xd, xaux, K, M, sb);
-        }
-    }
+    W ring[PF + 1][SBW];
+    int t = blockIdx.x;
     auto load = [&](W (&w)[SBW], int t) {
         const int tl = t >= G.ts2 ? t - G.ts2 : t >= G.ts1 ? t - G.ts1 : t;  // tile within its weight
         const uint8_t *gv = t >= G.ts2 ? G.gv2 : t >= G.ts1 ? G.gv1 : G.gv0;
@@ -316,11 +412,41 @@ __global__ __launch_bounds__(512) void k_gemv_kq_stream(const GvGroups G, const 
                 else w[i] = q6_load(L, T);
             }
     };
-    // ring of PF + 1 register sets: the loads of the PF tiles after this one are in flight
-    W ring[PF + 1][SBW];
-    int t = blockIdx.x;
 #pragma unroll
-    for (int f = 0; f < PF; f++) load(ring[f], t + f * (int)gridDim.x);
+    for (int i = 0; i < SBW; i++) live[i] = L.wave + 8 * i < nsb;
+    // ring of PF + 1 register sets: the loads of the PF tiles after this one are in flight
+    if constexpr (FQ) {
+        // the first tiles' weights do not depend on the activation: in flight while it is quantized
+#pragma unroll
+        for (int f = 0; f < PF; f++) load(ring[f], t + f * (int)gridDim.x);
+#pragma unroll
+        for (int i = 0; i < SBW; i++)
+            if (live[i]) {
+                const int slot = L.wave * SBW + i;
+                gv_quantize_rows(X, L.wave + 8 * i, M, L.lane, aq[slot], ad[slot], ag[slot]);
+            }
+        // the wave reads back what its own lanes wrote
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int i = 0; i < SBW; i++)
+            if (live[i]) {  // the slot is one superblock of the activation layout (K = 256)
+                const int slot = L.wave * SBW + i;
+                if constexpr (Q4) act[i] = q4_act(L, aq[slot], ad[slot], ag[slot], QK_K, M, 0);
+                else act[i] = q6_act(L, aq[slot], ad[slot], nullptr, QK_K, M, 0);
+            }
+    } else {
+#pragma unroll
+        for (int i = 0; i < SBW; i++)
+            if (live[i]) {
+                const int sb = L.wave + 8 * i;
+                if constexpr (Q4) act[i] = q4_act(L, xq, xd, (const _Float16 *)xaux, K, M, sb);
+                else act[i] = q6_act(L, xq, xd, xaux, K, M, sb);
+            }
+#pragma unroll
+        for (int f = 0; f < PF; f++) load(ring[f], t + f * (int)gridDim.x);
+    }
     for (int it = 0; t < ntiles; it++, t += gridDim.x) {
         // the storing lanes' bias, loaded ahead of the prefetch so that waiting for it at the
         // store does not wait for the next tiles' weights
@@ -399,7 +525,7 @@ __global__ __launch_bounds__(512) void k_gemv_kq_any(const uint8_t *__restrict__
 
 template <int TYPE>
 static hipError_t launch_kq_stream_groups(const GvGroups &G, const int8_t *xq, const float *xd, const void *xaux,
-                                          int64_t k, int m, hipStream_t s);
+                                          int64_t k, int m, hipStream_t s, const GvX *X = nullptr);
 
 template <int TYPE>
 static hipError_t launch_kq_stream(const uint8_t *gv, const int8_t *xq, const float *xd, const void *xaux, float *y,
@@ -420,7 +546,7 @@ static hipError_t launch_kq_stream(const uint8_t *gv, const int8_t *xq, const fl
 
 template <int TYPE>
 static hipError_t launch_kq_stream_groups(const GvGroups &G, const int8_t *xq, const float *xd, const void *xaux,
-                                          int64_t k, int m, hipStream_t s) {
+                                          int64_t k, int m, hipStream_t s, const GvX *X) {
     const int64_t ntiles = G.tend;
     const int nsb = (int)(k / QK_K);
     const int sbw = (nsb + 7) / 8;
@@ -440,6 +566,22 @@ static hipError_t launch_kq_stream_groups(const GvGroups &G, const int8_t *xq, c
     const dim3 block(512);
     const char *pe = getenv("MQ_GEMV_PF");
     const int pf = pe ? atoi(pe) : 2;
+    if (X) {  // the activation quantized inside the kernel
+        const GvX x = *X;
+        switch (sbw) {
+            case 1:
+                hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 2, true>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m, x);
+                break;
+            case 2:
+                hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 2, 1, true>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m, x);
+                break;
+            case 3:
+                hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 3, 1, true>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m, x);
+                break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     if (pf == 3 && sbw == 1) {
         hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 3>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m);
         return hipGetLastError();
@@ -514,6 +656,37 @@ hipError_t launch_gemv_group(int type, int ng, const void *const *images, const 
     const float *xd = (const float *)(xb + ap.xd);
     if (type == MQ_TYPE_Q4_K) return launch_kq_stream_groups<MQ_TYPE_Q4_K>(G, xq, xd, xb + ap.xgm, k, (int)m, s);
     return launch_kq_stream_groups<MQ_TYPE_Q6_K>(G, xq, xd, xb + ap.xbs, k, (int)m, s);
+}
+
+bool gemv_fused_ok(int type, int ng, int64_t k, int64_t m) {
+    return (type == MQ_TYPE_Q4_K || type == MQ_TYPE_Q6_K) && ng >= 1 && ng <= 3 && m >= 1 && m <= GEMV_CHUNK &&
+           k % QK_K == 0 && (k / QK_K + 7) / 8 <= 3;
+}
+
+hipError_t launch_gemv_group_f32(int type, int ng, const void *const *images, const int64_t *n, int64_t k,
+                                 const float *x, int64_t ldx, const float *x2, int64_t ldx2, int pre, int64_t m,
+                                 float *const *y, const int64_t *ldy, const float *const *bias, hipStream_t s) {
+    if (!gemv_fused_ok(type, ng, k, m) || (pre != MQ_PRE_NONE && pre != MQ_PRE_SILU_MUL) ||
+        (pre == MQ_PRE_SILU_MUL && !x2) || ((uintptr_t)x & 15) || (ldx & 3) || (x2 && (((uintptr_t)x2 & 15) || (ldx2 & 3))))
+        return hipErrorInvalidValue;
+    GvGroups G{};
+    int ts[3] = {0, 0, 0}, t = 0;
+    const uint8_t *gv[3] = {nullptr, nullptr, nullptr};
+    for (int g = 0; g < ng; g++) {
+        if (n[g] <= 0) return hipErrorInvalidValue;
+        gv[g] = (const uint8_t *)images[g] + weight_planes(type, n[g], k).gv;
+        ts[g] = t;
+        t += (int)((n[g] + GV_ROWS - 1) / GV_ROWS);
+    }
+    G.gv0 = gv[0], G.gv1 = gv[1], G.gv2 = gv[2];
+    G.y0 = y[0], G.y1 = ng > 1 ? y[1] : nullptr, G.y2 = ng > 2 ? y[2] : nullptr;
+    G.b0 = bias ? bias[0] : nullptr, G.b1 = (bias && ng > 1) ? bias[1] : nullptr, G.b2 = (bias && ng > 2) ? bias[2] : nullptr;
+    G.N0 = (int)n[0], G.N1 = ng > 1 ? (int)n[1] : 0, G.N2 = ng > 2 ? (int)n[2] : 0;
+    G.ld0 = ldy[0], G.ld1 = ng > 1 ? ldy[1] : 0, G.ld2 = ng > 2 ? ldy[2] : 0;
+    G.ts1 = ng > 1 ? ts[1] : INT_MAX, G.ts2 = ng > 2 ? ts[2] : INT_MAX, G.tend = t;
+    const GvX X{x, x2, ldx, ldx2, pre};
+    if (type == MQ_TYPE_Q4_K) return launch_kq_stream_groups<MQ_TYPE_Q4_K>(G, nullptr, nullptr, nullptr, k, (int)m, s, &X);
+    return launch_kq_stream_groups<MQ_TYPE_Q6_K>(G, nullptr, nullptr, nullptr, k, (int)m, s, &X);
 }
 
 hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,

@@ -321,6 +321,13 @@ hipError_t launch_add_rmsnorm_q8_K(const float *y, const float *res, const float
 // separate launches), otherwise one launch per weight
 hipError_t launch_gemv_group(int type, int ng, const void *const *images, const int64_t *n, int64_t k, const void *ws,
                              int64_t m, float *const *y, const int64_t *ldy, const float *const *bias, hipStream_t s);
+// the K-quant GEMV of up to 3 weights on fp32 activation rows (m <= 8, k <= 6144) that it
+// quantizes itself -- the bytes mq_quantize_act_ex writes, so the results equal the two-step form
+// bit for bit; pre MQ_PRE_NONE, or MQ_PRE_SILU_MUL with x2 the up-projection rows
+bool gemv_fused_ok(int type, int ng, int64_t k, int64_t m);
+hipError_t launch_gemv_group_f32(int type, int ng, const void *const *images, const int64_t *n, int64_t k,
+                                 const float *x, int64_t ldx, const float *x2, int64_t ldx2, int pre, int64_t m,
+                                 float *const *y, const int64_t *ldy, const float *const *bias, hipStream_t s);
 // up to 4 weights of the same type and k on one activation, one launch (bias may be NULL)
 hipError_t launch_gemm_group(int type, int ngroups, const void *const *images, const int64_t *n, int64_t k,
                              const void *ws, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,

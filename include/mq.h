@@ -178,6 +178,24 @@ int mq_mul_mat_q_group(int type, int n_groups, const void *const *w_images, cons
                        const void *workspace, int64_t m, float *const *y, const int64_t *ldy, const float *const *bias,
                        int path, void *stream);
 
+/* The GEMV path with the activation quantization inside the mat-mul kernel, for decode-sized
+ * inputs: m <= 8 fp32 rows, K-quant weights (Q4_K, Q6_K) with k <= 6144, up to 3 weights on one
+ * activation in one launch: Y_g = op(X) W_g^T + bias_g (bias NULL, or bias[g] NULL: none).
+ * Bit for bit what mq_quantize_act_ex(type, X, ..., op, MQ_PATH_GEMV) followed by
+ * mq_mul_mat_q_group(..., MQ_PATH_GEMV) computes, without the separate quantization launch and
+ * without a caller workspace: every workgroup quantizes the activation it reads, while that is a
+ * few superblock-rows (m * k / 256, three times that with SiLU, at most 100); larger ones are
+ * quantized once into the library's internal workspace of this stream (as mq_mul_mat_ex with a
+ * NULL workspace) and read by the same GEMV.  op MQ_PRE_NONE, or
+ * MQ_PRE_SILU_MUL with x2 the up-projection rows (row stride ldx2): the value quantized is then
+ * silu(x) * x2, the SwiGLU input of the down projection.  These are the MUL_MATs of the decode
+ * step, one to eight new tokens: q/k/v (src/qwen2vl_ocr.cpp:2368-2372), o (:2430), gate/up and
+ * down (:2437-2439), the lm_head (:2452).  x and x2 16-byte aligned, ldx and ldx2 multiples of 4;
+ * other shapes return MQ_EUNSUPPORTED (use the two-step form). */
+int mq_mul_mat_gemv(int type, int n_groups, const void *const *w_images, const int64_t *n, int64_t k, const float *x,
+                    int64_t ldx, const float *x2, int64_t ldx2, int op, int64_t m, float *const *y, const int64_t *ldy,
+                    const float *const *bias, void *stream);
+
 /* Two mat-muls in a row without the fp32 tensor between them: computes
  * V = op(X W^T + bias) on the GEMM path (workspace: X quantized with path MQ_PATH_GEMM) and
  * writes V quantized to Q8_0 straight into out_workspace, in the layout that

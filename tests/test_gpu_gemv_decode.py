@@ -163,3 +163,105 @@ def test_qwen3vl_down(oracle, monkeypatch, m):
     wave, one workgroup per CU; and o [2048 x 2048]."""
     _group_check(oracle, monkeypatch, O.Q4_K, [2048], 6144, m, None)
     _group_check(oracle, monkeypatch, O.Q4_K, [2048], 2048, m, 1)
+
+
+def _fused(wtype, imgs, ns, k, x, m, bias=None, x2=None, ldx=None, pre=0):
+    import torch
+    from crispembed_amd import mq
+    g = len(ns)
+    ys = [torch.full((m, n), np.nan, dtype=torch.float32, device="cuda") for n in ns]
+    VP, I64 = ctypes.c_void_p * g, ctypes.c_int64 * g
+    ld = ldx or x.stride(0)
+    mq.check(mq.lib().mq_mul_mat_gemv(wtype, g, VP(*[im[1] for im in imgs]), I64(*ns), k, ctypes.c_void_p(x.data_ptr()),
+                                      ld, ctypes.c_void_p(x2) if x2 else None, ld, pre, m,
+                                      VP(*[t.data_ptr() for t in ys]), I64(*ns),
+                                      VP(*[b.data_ptr() for b in bias]) if bias else None, stream()))
+    return [host(t) for t in ys]
+
+
+@pytest.fixture(params=["fused", "auto"])
+def gemv_form(request, monkeypatch):
+    """mq_mul_mat_gemv with the activation always quantized inside the GEMV (MQ_GEMV_FUSED=1),
+    and with its own choice (large activations quantized once, then the GEMV)."""
+    if request.param == "fused":
+        monkeypatch.setenv("MQ_GEMV_FUSED", "1")
+    else:
+        monkeypatch.delenv("MQ_GEMV_FUSED", raising=False)
+    return request.param
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("ns,k", [([2048, 1024, 1024], 2048), ([2048], 6144), ([300, 77], 4096)])
+def test_fused_gemv_equals_two_step(oracle, gemv_form, wtype, m, ns, k):
+    """mq_mul_mat_gemv (the activation quantized inside the GEMV) against mq_quantize_act +
+    mq_mul_mat_q_group on the GEMV path: bit-identical, and within the bar of the oracle."""
+    import torch
+    from crispembed_amd import mq
+    L = mq.lib()
+    ws_ = [random_blocks(wtype, n, k, 31 * n + k + g) for g, n in enumerate(ns)]
+    imgs = [weight_image(wtype, w, n, k) for w, n in zip(ws_, ns)]
+    x = np.random.default_rng(m * k).standard_normal((m, k)).astype(np.float32)
+    x[0, 5] = 0.0
+    xd = dev(x)
+    bias = [dev(np.random.default_rng(n + 1).standard_normal(n).astype(np.float32)) for n in ns]
+    got = _fused(wtype, imgs, ns, k, xd, m, bias)
+    keep, wsp = _quant(wtype, xd, m, k)
+    g = len(ns)
+    ref = [torch.full((m, n), np.nan, dtype=torch.float32, device="cuda") for n in ns]
+    VP, I64 = ctypes.c_void_p * g, ctypes.c_int64 * g
+    mq.check(L.mq_mul_mat_q_group(wtype, g, VP(*[im[1] for im in imgs]), I64(*ns), k, ctypes.c_void_p(wsp), m,
+                                  VP(*[t.data_ptr() for t in ref]), I64(*ns), VP(*[b.data_ptr() for b in bias]),
+                                  mq.PATH_GEMV, stream()))
+    xq = oracle.quantize_act(wtype, x)
+    for i, n in enumerate(ns):
+        assert np.array_equal(got[i].view(np.uint32), host(ref[i]).view(np.uint32)), i
+        assert rel_err(got[i], oracle.mul_mat_exact(wtype, ws_[i], xq, k) + host(bias[i])) <= TOL
+    del imgs, keep
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_fused_gemv_silu_mul(gemv_form, wtype, m):
+    """The down projection of the decode step on silu(gate) * up formed inside the GEMV, the
+    gate and up rows read from one [gate | up] buffer: bit-identical to the quantizer's
+    MQ_PRE_SILU_MUL prologue followed by the GEMV."""
+    import torch
+    from crispembed_amd import mq
+    L = mq.lib()
+    n, F = 2048, 6144
+    w = random_blocks(wtype, n, F, 7 + m)
+    img = weight_image(wtype, w, n, F)
+    gu = dev((np.random.default_rng(m).standard_normal((m, 2 * F)) * 3).astype(np.float32))
+    got = _fused(wtype, [img], [n], F, gu, m, x2=gu.data_ptr() + F * 4, ldx=2 * F, pre=mq.PRE_SILU_MUL)[0]
+    nb = L.mq_workspace_bytes(wtype, m, F)
+    buf, off = empty_u8(nb)
+    mq.check(L.mq_quantize_act_ex(wtype, ctypes.c_void_p(gu.data_ptr()), 2 * F, m, F, None, mq.PRE_SILU_MUL,
+                                  ctypes.c_void_p(buf.data_ptr() + off), nb, mq.PATH_GEMV, stream()))
+    ref = torch.full((m, n), np.nan, dtype=torch.float32, device="cuda")
+    mq.check(L.mq_mul_mat_q(wtype, ctypes.c_void_p(img[1]), n, F, ctypes.c_void_p(buf.data_ptr() + off), m,
+                            ctypes.c_void_p(ref.data_ptr()), n, mq.PATH_GEMV, stream()))
+    assert np.array_equal(got.view(np.uint32), host(ref).view(np.uint32))
+    del img
+
+
+def test_fused_gemv_lm_head(oracle, gemv_form, lm_head):
+    """The Q6_K lm_head with the activation quantized inside the kernel, m = 1 and 8."""
+    import torch
+    from crispembed_amd import mq
+    w, img, n, k = lm_head
+    for m in (1, 8):
+        x = np.random.default_rng(100 + m).standard_normal((m, k)).astype(np.float32)
+        got = _fused(O.Q6_K, [img], [n], k, dev(x), m)[0]
+        assert rel_err(got, oracle.mul_mat_exact(O.Q6_K, w, oracle.quantize_act(O.Q6_K, x), k)) <= TOL
+
+
+def test_fused_gemv_refusals():
+    from crispembed_amd import mq
+    L = mq.lib()
+    VP, I64 = ctypes.c_void_p * 1, ctypes.c_int64 * 1
+    args = lambda wt, k, m: (wt, 1, VP(256), I64(64), k, ctypes.c_void_p(256), k, None, 0, 0, m, VP(256),  # noqa: E731
+                             I64(64), None, stream())
+    assert L.mq_mul_mat_gemv(*args(mq.TYPE_Q8_0, 512, 1)) == -2  # not a K-quant
+    assert L.mq_mul_mat_gemv(*args(mq.TYPE_Q4_K, 8192, 1)) == -2  # k > 6144
+    assert L.mq_mul_mat_gemv(*args(mq.TYPE_Q4_K, 512, 9)) == -2  # m > 8
