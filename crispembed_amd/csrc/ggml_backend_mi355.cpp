@@ -381,12 +381,34 @@ int quantize_x(BackendCtx *c, const ggml_tensor *x, int mt, int64_t M, int64_t K
     return rc;
 }
 
+// Decode-sized products on K-quant weights take mq_mul_mat_gemv: the GEMV quantizes its own
+// activation, one launch instead of two (unless the activation is already quantized in the
+// workspace, or a graph is being captured: that form may allocate on its first large input).
+bool gemv_fused(const BackendCtx *c, const ggml_tensor *x, int mt, int64_t M, int64_t K, int path) {
+    return path == MQ_PATH_GEMV && (mt == MQ_TYPE_Q4_K || mt == MQ_TYPE_Q6_K) && M <= 8 && K <= 6144 &&
+           !c->capturing && c->ws_x != x && ((uintptr_t)x->data & 15) == 0 && (x->nb[1] / 4) % 4 == 0 &&
+           std::getenv("MQ_GGML_NO_FUSION") == nullptr;
+}
+
 // y = x w^T (+ bias) into dst, for dst rows that continue one another (any row stride)
 enum ggml_status mul_mat_flat(BackendCtx *c, const ggml_tensor *w, const ggml_tensor *x, ggml_tensor *dst,
                               const float *bias, const ggml_tensor *named) {
     const int mt = mq_type_of(w->type);
     const int64_t K = w->ne[0], N = w->ne[1], M = x->ne[1] * x->ne[2] * x->ne[3];
     const int path = mq_mul_mat_path(mt, N, K, M);
+    if (gemv_fused(c, x, mt, M, K, path)) {
+        const void *wi[1] = {w->data};
+        const int64_t nn[1] = {N}, ld[1] = {(int64_t)(dst->nb[1] / 4)};
+        float *yy[1] = {(float *)dst->data};
+        const float *bb[1] = {bias};
+        const int rc = mq_mul_mat_gemv(mt, 1, wi, nn, K, (const float *)x->data, (int64_t)(x->nb[1] / 4), nullptr, 0,
+                                       MQ_PRE_NONE, M, yy, ld, bb, c->stream);
+        if (rc != 0) {
+            std::fprintf(stderr, "ggml-mi355: MUL_MAT '%s' failed: %s\n", named->name, mq_last_error());
+            return rc == MQ_ENOMEM ? GGML_STATUS_ALLOC_FAILED : GGML_STATUS_FAILED;
+        }
+        return GGML_STATUS_SUCCESS;
+    }
     int rc = quantize_x(c, x, mt, M, K, path);
     if (rc == 0)
         rc = mq_mul_mat_q_ex(mt, w->data, N, K, c->ws, M, (float *)dst->data, (int64_t)(dst->nb[1] / 4), bias, path,
@@ -820,6 +842,9 @@ int try_group_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, std::vector<
             if (rc == 0) c->kv_ready_for = fa, c->kv_frag_off = off;
         }
     }
+    if (rc == 1 && nm <= 3 && gemv_fused(c, x, mt, M, K, path))
+        rc = mq_mul_mat_gemv(mt, nm, w, nn, K, (const float *)x->data, (int64_t)(x->nb[1] / 4), nullptr, 0, MQ_PRE_NONE,
+                             M, y, ldy, b, c->stream);
     if (rc == 1) {
         rc = quantize_x(c, x, mt, M, K, path);
         if (rc == 0) rc = mq_mul_mat_q_group(mt, nm, w, nn, K, c->ws, M, y, ldy, b, path, c->stream);
