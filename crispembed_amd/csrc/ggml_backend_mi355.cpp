@@ -291,6 +291,7 @@ ggml_backend_buffer_t buft_alloc(ggml_backend_buffer_type_t buft, size_t size) {
     DeviceGuard g(d->ordinal);
     void *p = nullptr;
     if (hipMalloc(&p, size ? size : 256) != hipSuccess) {
+        (void)hipGetLastError();  // a failed allocation must not surface as the next launch's error
         std::fprintf(stderr, "ggml-mi355: failed to allocate %zu bytes on %s\n", size, d->name.c_str());
         return nullptr;  // the loader reports and fails (src/core/gguf_loader.cpp:408-415)
     }
@@ -361,6 +362,7 @@ bool ensure_ws(BackendCtx *c, size_t need) {
     c->ws = nullptr;
     c->ws_bytes = 0;
     if (hipMalloc(&c->ws, need) != hipSuccess) {
+        (void)hipGetLastError();  // a failed allocation must not surface as the next launch's error
         c->ws = nullptr;
         std::fprintf(stderr, "ggml-mi355: workspace allocation of %zu bytes failed\n", need);
         return false;
@@ -1284,5 +1286,13 @@ ggml_backend_t ggml_backend_mi355_init(int device) {
 bool ggml_backend_is_mi355(ggml_backend_t backend) {
     return backend && backend->guid == backend_guid();
 }
+
+// The two symbols ggml's loader resolves in a backend library built for dynamic loading:
+// ggml_backend_load takes the registry from ggml_backend_init (and checks its api_version),
+// ggml_backend_load_best ranks candidate libraries by ggml_backend_score, 0 meaning "cannot run
+// here".  This library can run wherever a gfx950 device is visible.
+ggml_backend_reg_t ggml_backend_init(void) { return &the_reg(); }
+
+int ggml_backend_score(void) { return devices().empty() ? 0 : 1; }
 
 }  // extern "C"

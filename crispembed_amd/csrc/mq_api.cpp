@@ -115,6 +115,7 @@ int stream_workspace(size_t need, void *stream, void **ws, size_t *bytes) {
         w.bytes = 0;
         e = hipMalloc(&w.ptr, need);
         if (e != hipSuccess) {
+            (void)hipGetLastError();  // a failed allocation must not surface as the next launch's error
             w.ptr = nullptr;
             return fail(MQ_ENOMEM, "hipMalloc(%zu) for the activation workspace failed", need);
         }

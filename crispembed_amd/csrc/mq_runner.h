@@ -26,7 +26,10 @@ struct DevBuf {
         if (p) (void)hipFree(p);
         p = nullptr;
         bytes = 0;
-        if (hipMalloc(&p, n) != hipSuccess) return false;
+        if (hipMalloc(&p, n) != hipSuccess) {
+            (void)hipGetLastError();  // a failed allocation must not surface as the next launch's error
+            return false;
+        }
         bytes = n;
         return true;
     }

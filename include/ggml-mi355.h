@@ -39,6 +39,17 @@ GGML_BACKEND_API ggml_backend_buffer_type_t ggml_backend_mi355_buffer_type(int d
 /* Number of gfx950 devices the backend exposes. */
 GGML_BACKEND_API int ggml_backend_mi355_get_device_count(void);
 
+/* Dynamic-loading entry points of a GGML_BACKEND_DL library (what ggml's
+ * GGML_BACKEND_DL_IMPL / GGML_BACKEND_DL_SCORE_IMPL define in every backend
+ * library): ggml_backend_load(path) calls ggml_backend_init() for the registry
+ * and requires api_version GGML_BACKEND_API_VERSION; ggml_backend_load_best()
+ * ranks candidate libraries by ggml_backend_score() (0: cannot run on this
+ * machine, here: no gfx950 device).  CrispEmbed itself never calls
+ * ggml_backend_load (its backend choice is src/core/gpu_backend_pref.h:70-161),
+ * so these serve ggml builds that discover backends at run time. */
+GGML_BACKEND_API ggml_backend_reg_t ggml_backend_init(void);
+GGML_BACKEND_API int ggml_backend_score(void);
+
 #ifdef __cplusplus
 }
 #endif

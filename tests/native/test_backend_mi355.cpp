@@ -7,6 +7,8 @@
 // summary) with MUL_MAT graphs in place of the 16-element ADD.
 //
 // usage: test-backend-mi355 [backend-name-prefix] [--json]
+#include <dlfcn.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -15,6 +17,7 @@
 #include <string>
 #include <vector>
 
+#include "ggml-backend-impl.h"  // ggml_backend_reg::api_version, as ggml_backend_load checks it
 #include "ggml-backend.h"
 #include "ggml-mi355.h"
 #include "ggml.h"
@@ -68,6 +71,7 @@ struct Result {
     int cases = 0;
     double max_err = 0;
     bool roundtrip = true, partial = true, batched = true, supports = true, computed = true, moe = true;
+    bool sched = true, failures = true;
 };
 
 // One weight of `type` [K in, N out], activations [K, M] (ne2 batches), through the graph.
@@ -325,6 +329,161 @@ static void run_moe_block(ggml_backend_t be, ggml_type type, Result &res) {
     ggml_free(ctx);
 }
 
+// The library's dynamic-loading entry points, looked up the way ggml_backend_load does: dlopen
+// the backend library, dlsym ggml_backend_init (registry, api_version checked) and
+// ggml_backend_score (0: cannot run here).  Returns the score, -1 on a missing or wrong symbol.
+static int check_dl_entry_points() {
+    Dl_info info;
+    if (!dladdr((void *)&ggml_backend_mi355_reg, &info) || !info.dli_fname) return -1;
+    void *h = dlopen(info.dli_fname, RTLD_NOW | RTLD_LOCAL);
+    if (!h) return -1;
+    auto init = (ggml_backend_reg_t (*)(void))dlsym(h, "ggml_backend_init");
+    auto score = (int (*)(void))dlsym(h, "ggml_backend_score");
+    int s = -1;
+    if (init && score) {
+        ggml_backend_reg_t reg = init();
+        if (reg == ggml_backend_mi355_reg() && reg->api_version == GGML_BACKEND_API_VERSION &&
+            std::strcmp(ggml_backend_reg_name(reg), "MI355X") == 0)
+            s = score();
+        // the score says whether the registry has a device
+        if (s >= 0 && (s > 0) != (ggml_backend_reg_dev_count(reg) > 0)) s = -1;
+    }
+    dlclose(h);
+    return s;
+}
+
+// A minimal ggml_backend_sched_graph_compute: the reference's scheduler (src/crispembed.cpp:
+// 700-723, 1471-1483) gives every node the first backend whose supports_op claims it, cuts the
+// graph into splits of consecutive nodes on one backend, copies a split's inputs produced on
+// another backend into it, and fails the call when a split's compute is not SUCCESS.  Graph:
+// Y2 = W2 (tanh(W1 X)); TANH is not claimed, so the splits are MUL_MAT (GPU) | TANH (host) |
+// MUL_MAT (GPU).  The host split reads its input back with tensor_get and leaves its output
+// where the next GPU split reads it (tensor_set), as sched's input copy does.  Checks: three
+// splits, the set_n_threads proc lookup sched makes returns NULL, Y1 against the oracle, Y2
+// against the oracle's product of W2 with the host's tanh of the GPU's Y1 (each at 1e-4).
+static void run_sched_split(ggml_backend_t be, ggml_type type, int64_t M, Result &res) {
+    const int64_t K = 512, N1 = 256, N2 = 96;
+    ggml_init_params ip = {ggml_tensor_overhead() * 8 + ggml_graph_overhead(), nullptr, true};
+    ggml_context *ctx = ggml_init(ip);
+    ggml_tensor *W1 = ggml_new_tensor_2d(ctx, type, K, N1);
+    ggml_tensor *W2 = ggml_new_tensor_2d(ctx, type, N1, N2);
+    ggml_tensor *X = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, K, M);
+    ggml_tensor *Y1 = ggml_mul_mat(ctx, W1, X);
+    ggml_tensor *T = ggml_unary(ctx, Y1, GGML_UNARY_OP_TANH);
+    ggml_tensor *Y2 = ggml_mul_mat(ctx, W2, T);
+    ggml_set_output(Y2);
+    ggml_cgraph *gf = ggml_new_graph(ctx);
+    ggml_build_forward_expand(gf, Y2);
+    ggml_backend_buffer_t buf = ggml_backend_alloc_ctx_tensors(ctx, be);
+    ggml_backend_dev_t dev = ggml_backend_get_device(be);
+    if (!buf || ggml_backend_reg_get_proc_address(ggml_backend_dev_backend_reg(dev), "ggml_backend_set_n_threads")) {
+        res.sched = false;
+        if (buf) ggml_backend_buffer_free(buf);
+        ggml_free(ctx);
+        return;
+    }
+    std::vector<float> w1f = normal((size_t)(N1 * K), 0.05), w2f = normal((size_t)(N2 * N1), 0.05);
+    std::vector<uint8_t> w1(or_row_size((int)type, K) * N1), w2(or_row_size((int)type, N1) * N2);
+    or_quantize_chunk((int)type, w1f.data(), w1.data(), N1, K);
+    or_quantize_chunk((int)type, w2f.data(), w2.data(), N2, N1);
+    std::vector<float> x = normal((size_t)(K * M), 1.0);
+    ggml_backend_tensor_set(W1, w1.data(), 0, w1.size());
+    ggml_backend_tensor_set(W2, w2.data(), 0, w2.size());
+    ggml_backend_tensor_set(X, x.data(), 0, x.size() * 4);
+    const int n = ggml_graph_n_nodes(gf);
+    int splits = 0;
+    std::vector<float> th;
+    for (int i0 = 0; i0 < n;) {
+        const bool on_gpu = ggml_backend_supports_op(be, ggml_graph_node(gf, i0));
+        int i1 = i0 + 1;
+        while (i1 < n && ggml_backend_supports_op(be, ggml_graph_node(gf, i1)) == on_gpu) i1++;
+        splits++;
+        if (on_gpu) {
+            ggml_cgraph *view = ggml_compat_graph_view(gf, i0, i1);
+            const ggml_status st = ggml_backend_graph_compute(be, view);
+            ggml_compat_graph_view_free(view);
+            if (st != GGML_STATUS_SUCCESS) {
+                res.sched = false;
+                break;
+            }
+        } else {
+            for (int i = i0; i < i1; i++) {  // this driver's host backend knows TANH only
+                ggml_tensor *node = ggml_graph_node(gf, i), *src = node->src[0];
+                if (node->op != GGML_OP_UNARY || ggml_get_unary_op(node) != GGML_UNARY_OP_TANH) {
+                    res.sched = false;
+                    break;
+                }
+                std::vector<float> v((size_t)ggml_nelements(src));
+                ggml_backend_tensor_get(src, v.data(), 0, v.size() * 4);
+                for (auto &e : v) e = std::tanh(e);
+                ggml_backend_tensor_set(node, v.data(), 0, v.size() * 4);
+                th = v;
+            }
+        }
+        i0 = i1;
+    }
+    if (res.sched && splits == 3 && th.size() == (size_t)(N1 * M)) {
+        std::vector<float> y1((size_t)(N1 * M)), y1ref(y1.size()), y2((size_t)(N2 * M)), y2ref(y2.size());
+        ggml_backend_tensor_get(Y1, y1.data(), 0, y1.size() * 4);
+        ggml_backend_tensor_get(Y2, y2.data(), 0, y2.size() * 4);
+        or_mul_mat((int)type, w1.data(), N1, K, x.data(), K, M, y1ref.data(), N1, 4, OR_Q8_0_X86);
+        or_mul_mat((int)type, w2.data(), N2, N1, th.data(), N1, M, y2ref.data(), N2, 4, OR_Q8_0_X86);
+        const double e1 = rel_err(y1, y1ref), e2 = rel_err(y2, y2ref);
+        res.max_err = std::fmax(res.max_err, std::fmax(e1, e2));
+        res.cases += 2;
+        if (!(e1 <= 1e-4) || !(e2 <= 1e-4)) {
+            res.sched = false;
+            std::fprintf(stderr, "sched split %s M=%lld: rel err %.3g / %.3g\n", ggml_type_name(type), (long long)M,
+                         e1, e2);
+        }
+    } else {
+        res.sched = false;
+        std::fprintf(stderr, "sched split %s M=%lld: %d splits\n", ggml_type_name(type), (long long)M, splits);
+    }
+    ggml_backend_buffer_free(buf);
+    ggml_free(ctx);
+}
+
+// Failure paths a host relies on: an allocation the device cannot hold returns NULL (the
+// loader then fails cleanly, src/core/gguf_loader.cpp:408-415), a graph with a node the
+// backend does not compute returns a status other than SUCCESS (the caller fails the call,
+// src/crispembed.cpp:1483), and neither leaves the backend unusable: the next allocation and
+// graph still succeed and are checked against the oracle.
+static void run_failures(ggml_backend_t be, Result &res) {
+    ggml_backend_buffer_type_t buft = ggml_backend_get_default_buffer_type(be);
+    if (ggml_backend_buft_alloc_buffer(buft, (size_t)1 << 52) != nullptr) res.failures = false;
+    {
+        ggml_init_params ip = {ggml_tensor_overhead() * 4, nullptr, true};
+        ggml_context *ctx = ggml_init(ip);
+        ggml_new_tensor_2d(ctx, GGML_TYPE_F32, (int64_t)1 << 24, (int64_t)1 << 24);  // 1 PiB
+        if (ggml_backend_alloc_ctx_tensors(ctx, be) != nullptr) res.failures = false;
+        ggml_free(ctx);
+    }
+    {
+        ggml_init_params ip = {ggml_tensor_overhead() * 4 + ggml_graph_overhead(), nullptr, true};
+        ggml_context *ctx = ggml_init(ip);
+        ggml_tensor *x = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 64, 4);
+        ggml_tensor *t = ggml_unary(ctx, x, GGML_UNARY_OP_TANH);
+        ggml_cgraph *gf = ggml_new_graph(ctx);
+        ggml_build_forward_expand(gf, t);
+        ggml_backend_buffer_t buf = ggml_backend_alloc_ctx_tensors(ctx, be);
+        if (!buf) res.failures = false;
+        else {
+            std::vector<float> v(256, 0.5f);
+            ggml_backend_tensor_set(x, v.data(), 0, v.size() * 4);
+            if (ggml_backend_graph_compute(be, gf) == GGML_STATUS_SUCCESS) res.failures = false;
+            ggml_backend_buffer_free(buf);
+        }
+        ggml_free(ctx);
+    }
+    Result after;
+    run_case(be, GGML_TYPE_Q8_0, 384, 40, 77, 1, after);
+    run_case(be, GGML_TYPE_Q4_K, 512, 40, 4, 1, after);
+    if (!(after.computed && after.cases >= 2 && after.max_err <= 1e-4)) res.failures = false;
+    res.cases += after.cases;
+    res.max_err = std::fmax(res.max_err, after.max_err);
+}
+
 int main(int argc, char **argv) {
     const char *requested = "MI355X";
     bool json = false;
@@ -332,12 +491,15 @@ int main(int argc, char **argv) {
         if (std::strcmp(argv[i], "--json") == 0) json = true;
         else requested = argv[i];
     }
+    const int dl_score = check_dl_entry_points();
     ggml_backend_register(ggml_backend_mi355_reg());  // the one-line host hook
     ggml_backend_t be = init_by_name(requested);
     if (!be) {
         std::fprintf(stderr, "test-backend-mi355: no GPU device matching '%s' (%zu devices registered)\n", requested,
                      ggml_backend_dev_count());
-        if (json) std::printf("{\"requested\":\"%s\",\"device_available\":false,\"correct\":false}\n", requested);
+        if (json)
+            std::printf("{\"requested\":\"%s\",\"device_available\":false,\"dl_score\":%d,\"correct\":false}\n",
+                        requested, dl_score);
         return 1;
     }
     ggml_backend_dev_t dev = ggml_backend_get_device(be);
@@ -355,6 +517,11 @@ int main(int argc, char **argv) {
     run_case_id(be, GGML_TYPE_F16, 128, 72, 6, 2, 90, false, res);
     run_moe_block(be, GGML_TYPE_Q8_0, res);
     run_moe_block(be, GGML_TYPE_Q4_K, res);
+    // CPU-fallback splits (GEMM- and GEMV-sized) and the failure paths
+    run_sched_split(be, GGML_TYPE_Q4_K, 40, res);
+    run_sched_split(be, GGML_TYPE_Q4_K, 3, res);
+    run_sched_split(be, GGML_TYPE_Q8_0, 40, res);
+    run_failures(be, res);
     // supports_op must refuse what the kernels do not handle (CPU fallback)
     {
         ggml_init_params ip = {ggml_tensor_overhead() * 16 + ggml_graph_overhead(), nullptr, true};
@@ -382,15 +549,17 @@ int main(int argc, char **argv) {
         ggml_free(ctx);
     }
     const bool correct = res.computed && res.roundtrip && res.partial && res.batched && res.supports && res.moe &&
-                         res.cases > 0 && res.max_err <= 1e-4;
+                         res.sched && res.failures && dl_score > 0 && res.cases > 0 && res.max_err <= 1e-4;
     if (json)
         std::printf("{\"requested\":\"%s\",\"name\":\"%s\",\"description\":\"%s\",\"type\":%d,\"cases\":%d,"
                     "\"max_rel_err\":%.3g,\"roundtrip_ok\":%s,\"partial_write_ok\":%s,\"batched_ok\":%s,"
-                    "\"supports_op_ok\":%s,\"moe_ok\":%s,\"computed\":%s,\"correct\":%s}\n",
+                    "\"supports_op_ok\":%s,\"moe_ok\":%s,\"sched_split_ok\":%s,\"failures_ok\":%s,\"dl_score\":%d,"
+                    "\"computed\":%s,\"correct\":%s}\n",
                     requested, ggml_backend_dev_name(dev), ggml_backend_dev_description(dev),
                     (int)ggml_backend_dev_type(dev), res.cases, res.max_err, res.roundtrip ? "true" : "false",
                     res.partial ? "true" : "false", res.batched ? "true" : "false", res.supports ? "true" : "false",
-                    res.moe ? "true" : "false", res.computed ? "true" : "false", correct ? "true" : "false");
+                    res.moe ? "true" : "false", res.sched ? "true" : "false", res.failures ? "true" : "false", dl_score,
+                    res.computed ? "true" : "false", correct ? "true" : "false");
     else
         std::printf("backend-mi355 name=%s cases=%d max_rel_err=%.3g correct=%d\n", ggml_backend_dev_name(dev),
                     res.cases, res.max_err, correct ? 1 : 0);

@@ -11,7 +11,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 def _declared(header):
     text = open(os.path.join(ROOT, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(mq_\w+|\w*mi355\w*)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(mq_\w+|\w*mi355\w*|ggml_backend_init|ggml_backend_score)\s*\(", text)))
 
 
 def test_libmq_exports_all_declared_symbols():
@@ -104,7 +104,8 @@ def test_ggml_backend_library_exports():
     L = ctypes.CDLL(os.path.join(here, "libggml-mi355.so"))
     names = _declared("ggml-mi355.h")
     assert set(names) >= {"ggml_backend_mi355_reg", "ggml_backend_mi355_init", "ggml_backend_is_mi355",
-                          "ggml_backend_mi355_buffer_type", "ggml_backend_mi355_get_device_count"}
+                          "ggml_backend_mi355_buffer_type", "ggml_backend_mi355_get_device_count",
+                          "ggml_backend_init", "ggml_backend_score"}
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing, missing
 
@@ -122,3 +123,4 @@ def test_backend_driver_without_gpu_reports_no_device():
     assert r.returncode == 1
     out = json.loads(r.stdout.strip().splitlines()[-1])
     assert out["device_available"] is False
+    assert out["dl_score"] == 0  # ggml_backend_init / ggml_backend_score resolve; no gfx950 device here

@@ -1,8 +1,11 @@
 """The ggml backend end to end on the GPU: registry lookup by name, buffer
 allocation, GGUF upload, graph_compute of MUL_MAT nodes (GEMV and GEMM sizes,
 batched activations), MUL_MAT_ID on 3-D expert weights (routing views, broadcast and per-slot
-activations), tensor_get round trips, partial weight writes (one spanning two experts) and the
-supports_op contract, all checked against the CPU oracle by the native driver."""
+activations), tensor_get round trips, partial weight writes (one spanning two experts), the
+supports_op contract, a scheduler-style CPU-fallback split (MUL_MAT | host TANH | MUL_MAT), the
+failure paths (an allocation the device cannot hold, a graph with an unclaimed node) followed by
+working graphs, and the dynamic-loading entry points, all checked against the CPU oracle by the
+native driver."""
 import json
 import os
 import subprocess
@@ -21,6 +24,8 @@ def test_backend_driver_json():
     assert out["name"].startswith("MI355X")
     assert out["cases"] >= 24
     assert out["max_rel_err"] <= 1e-4
-    for k in ("roundtrip_ok", "partial_write_ok", "batched_ok", "supports_op_ok", "moe_ok", "computed", "correct"):
+    assert out["dl_score"] > 0
+    for k in ("roundtrip_ok", "partial_write_ok", "batched_ok", "supports_op_ok", "moe_ok", "sched_split_ok",
+              "failures_ok", "computed", "correct"):
         assert out[k] is True, k
     assert r.returncode == 0
