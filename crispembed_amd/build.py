@@ -102,6 +102,54 @@ def build_test_driver():
     return outs
 
 
+# Host-side AddressSanitizer + UndefinedBehaviorSanitizer build of the same libraries, for the
+# CPU tests (GGUF reader and loaders, host quantizer, C ABI argument checks): every host
+# translation unit instrumented, device code built as usual but never run (the CPU tests launch
+# no kernel).  The shared libraries leave the sanitizer runtime unresolved; the test process
+# preloads clang's (asan_runtime()), which also carries the UBSan handlers.
+ASAN_DIR = os.path.join(HERE, "_asan")
+SAN_FLAGS = ("-O1 -g -Xarch_host -fsanitize=address -Xarch_host -fsanitize=undefined "
+             "-Xarch_host -fno-sanitize-recover=undefined -Xarch_host -fno-omit-frame-pointer").split()
+
+
+def asan_runtime():
+    """clang's shared ASan runtime (the compiler that built the sanitized libraries)."""
+    clang = os.path.join(os.path.dirname(os.path.realpath(HIPCC)), "..", "llvm", "bin", "clang")
+    r = subprocess.run([clang, "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    path = r.stdout.strip()
+    return path if r.returncode == 0 and os.path.isabs(path) and os.path.exists(path) else None
+
+
+def build_sanitized(verbose=True):
+    bdir = os.path.join(ASAN_DIR, "obj")
+    os.makedirs(bdir, exist_ok=True)
+
+    def comp(src, extra):
+        common = [f for f in COMMON if f != "-O3"]
+        obj = os.path.join(bdir, src.replace("/", "_") + ".o")
+        cmd = [HIPCC, *common, *SAN_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+        return obj
+
+    srcs = list(MQ_SOURCES) + list(GGML_SOURCES) + list(COMPAT_SOURCES)
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
+        objs = list(ex.map(lambda a: comp(*a), srcs))
+    n = len(MQ_SOURCES)
+    lib_mq, lib_ggml, lib_compat = (os.path.join(ASAN_DIR, x) for x in ("libmq.so", "libggml-mi355.so",
+                                                                          "libggml-compat.so"))
+    _link(objs[:n], lib_mq)
+    _link(objs[n + len(GGML_SOURCES):], lib_compat)
+    _link(objs[n:n + len(GGML_SOURCES)], lib_ggml, ["-L", ASAN_DIR, "-lmq", "-lggml-compat", "-Wl,-rpath,$ORIGIN"])
+    r = subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "asan"], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"sanitized oracle build failed:\n{r.stdout}\n{r.stderr}")
+    if verbose:
+        print(f"built the host-sanitized libraries in {ASAN_DIR} and oracle/_asan")
+    return ASAN_DIR
+
+
 def build(verbose=True):
     os.makedirs(BUILD, exist_ok=True)
     srcs = list(MQ_SOURCES) + list(GGML_SOURCES)

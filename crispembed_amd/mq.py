@@ -3,7 +3,9 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmq.so")
+# MQ_LIB_DIR selects another build of the same libraries (the host-sanitized one in _asan/)
+LIB_DIR = os.environ.get("MQ_LIB_DIR") or HERE
+LIB_PATH = os.path.join(LIB_DIR, "libmq.so")
 
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K = 0, 1, 8, 12, 14, 15
 Q8_0_X86, Q8_0_NEON, Q8_0_REF = 0, 1, 2

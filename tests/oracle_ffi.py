@@ -11,7 +11,8 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_DIR = os.path.join(ROOT, "oracle")
-ORACLE_SO = os.path.join(ORACLE_DIR, "liboracle.so")
+# MQ_ORACLE_SO: another build of the oracle (the sanitized one, oracle/_asan/liboracle.so)
+ORACLE_SO = os.environ.get("MQ_ORACLE_SO") or os.path.join(ORACLE_DIR, "liboracle.so")
 
 F32, F16, Q8_0, Q4_K, Q6_K, Q8_K = 0, 1, 8, 12, 14, 15
 # planted mistakes of the oracle (ggml_oracle.h OR_MUT_*)
@@ -32,7 +33,7 @@ def _ptr(a):
 
 class Oracle:
     def __init__(self):
-        if not os.path.exists(ORACLE_SO):
+        if not os.path.exists(ORACLE_SO) and not os.environ.get("MQ_ORACLE_SO"):
             subprocess.run(["make", "-C", ORACLE_DIR], check=True, capture_output=True)
         L = ctypes.CDLL(ORACLE_SO)
         i64, vp, ci, sz = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t

@@ -99,7 +99,7 @@ def test_ggml_backend_library_exports():
     import ctypes
     from crispembed_amd import mq
     mq.lib()
-    here = os.path.join(ROOT, "crispembed_amd")
+    here = mq.LIB_DIR
     ctypes.CDLL(os.path.join(here, "libggml-compat.so"), mode=ctypes.RTLD_GLOBAL)
     L = ctypes.CDLL(os.path.join(here, "libggml-mi355.so"))
     names = _declared("ggml-mi355.h")
