@@ -56,16 +56,18 @@ class Dev:
         self.name = name
 
 
-def _measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 byte-counter
-    runs (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE per dispatch, each
-    scaled by what the counter reads for a plain copy of known size)."""
+def _measured_traffic(kernel, launch):
+    """HBM bytes per launch of `kernel` (the `launch` entry: "up" or "down") from the committed
+    rocprofv3 byte-counter runs (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE per dispatch,
+    each scaled by what the counter reads for a plain copy of known size)."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         t = json.load(open(path))
     except (OSError, ValueError):
         return None
-    return t.get("bytes_per_launch") if t.get("kernel") == kernel else None
+    if t.get("kernel") != kernel:
+        return None
+    return t.get("launches", {}).get(launch, {}).get("bytes_per_launch")
 
 
 def quantize_weights(L, wtype, wf):
@@ -153,14 +155,14 @@ def bench_q4k_ffn(args, torch, L, mq, synth):
 
     up_rf = gemm_roofline("up", F, H, ops_up, t_up, q_up.size)
     dn_rf = gemm_roofline("down", H, F, ops_dn, t_dn, q_dn.size)
+    up_rf["traffic"] = _measured_traffic("k_gemm<Q4_K>", "up")
+    dn_rf["traffic"] = _measured_traffic("k_gemm<Q4_K>", "down")
     # the dominant kernel of the step is the up GEMM (the longer of the two launches)
     dom, other = (up_rf, dn_rf) if t_up >= t_dn else (dn_rf, up_rf)
     roof = dict(dom)
     roof.update({
         "peak_source": "MI355X datasheet: HBM3E 8 TB/s; dense int8 MFMA 5.0 POP/s (ops = 2*M*N*K)",
-        "traffic": _measured_traffic("k_gemm<Q4_K>"),
-        "traffic_unit": "HBM bytes per launch, rocprofv3 FETCH_SIZE + WRITE_SIZE (copy-calibrated), mean of the "
-                        "up and down launches",
+        "traffic_unit": "HBM bytes per launch of this kernel, rocprofv3 FETCH_SIZE + WRITE_SIZE (copy-calibrated)",
         "second_kernel": other,
     })
     res = {
