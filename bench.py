@@ -127,6 +127,9 @@ def bench_q4k_ffn(args, torch, L, mq, synth):
     torch.cuda.synchronize()
     t_up = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
     t_dn = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
+    med = lambda v: sorted(v)[len(v) // 2]
+    t_up_med = med([e[0].elapsed_time(e[1]) for e in evs])
+    t_dn_med = med([e[2].elapsed_time(e[3]) for e in evs])
 
     def gemm_roofline(name, n, k, ops, t_ms, w_bytes):
         """One GEMM launch against its binding roofline: the larger of its MFMA time (int8 ops at
@@ -157,12 +160,24 @@ def bench_q4k_ffn(args, torch, L, mq, synth):
     dn_rf = gemm_roofline("down", H, F, ops_dn, t_dn, q_dn.size)
     up_rf["traffic"] = _measured_traffic("k_gemm<Q4_K>", "up")
     dn_rf["traffic"] = _measured_traffic("k_gemm<Q4_K>", "down")
+    up_rf["us_per_launch_median"] = t_up_med * 1e3
+    dn_rf["us_per_launch_median"] = t_dn_med * 1e3
+    # the chip's sustained int8 MFMA rate, measured on it (the datasheet's 5.0 POP/s assumes a
+    # clock the chip does not hold under MFMA load)
+    peak = ctypes.c_double(0.0)
+    mq.check(L.mq_measure_mfma_i8(4000, ctypes.byref(peak), s))
+    for rf in (up_rf, dn_rf):
+        rf["int8_mfma_frac_of_measured_peak"] = rf["int8_tops"] / peak.value
+    measured_peak = {"int8_mfma_tops": peak.value,
+                     "method": "mq_measure_mfma_i8: one wave per SIMD on every CU, 8 independent "
+                               "v_mfma_i32_32x32x32_i8 chains each, no memory traffic, HIP events"}
     # the dominant kernel of the step is the up GEMM (the longer of the two launches)
     dom, other = (up_rf, dn_rf) if t_up >= t_dn else (dn_rf, up_rf)
     roof = dict(dom)
     roof.update({
         "peak_source": "MI355X datasheet: HBM3E 8 TB/s; dense int8 MFMA 5.0 POP/s (ops = 2*M*N*K)",
         "traffic_unit": "HBM bytes per launch of this kernel, rocprofv3 FETCH_SIZE + WRITE_SIZE (copy-calibrated)",
+        "peak_measured": measured_peak,
         "second_kernel": other,
     })
     res = {
@@ -471,20 +486,26 @@ def cpu_baseline_q4k(args, x_up, x_dn, q_up, q_dn):
     mm(q_dn, x_dn[:64])
     per_row = (time.perf_counter() - t) / 64
     rows = int(max(64, min(x_up.shape[0], args.cpu_seconds / max(per_row, 1e-9))))
-    reps, dt = 0, 0.0
-    while reps < 1 or dt < 0.5 * args.cpu_seconds:
+    mm(q_up, x_up[:rows])  # one full-size warm-up
+    mm(q_dn, x_dn[:rows])
+    reps, dt, times = 0, 0.0, []
+    while reps < 10 and (reps < 3 or dt < 0.5 * args.cpu_seconds):
         t = time.perf_counter()
         mm(q_up, x_up[:rows])
         mm(q_dn, x_dn[:rows])
-        dt += time.perf_counter() - t
+        times.append(time.perf_counter() - t)
+        dt += times[-1]
         reps += 1
-    ops = 2.0 * rows * (F * H + H * F) * reps
+    ops_rep = 2.0 * rows * (F * H + H * F)
+    ops = ops_rep * reps
+    t_med = sorted(times)[len(times) // 2]
     isa = orc.fast_isa() if fast else "none"
     impl = {"avx512vnni": "AVX-512 VNNI integer dots", "avx2": "AVX2 integer dots"}.get(isa, "scalar C")
     model = cpu_model()
     return {
-        "value": ops / dt / 1e12,
+        "value": ops_rep / t_med / 1e12,
         "unit": "TOPS",
+        "mean_value": ops / dt / 1e12,
         "cores": nthreads,
         "kind": "port",
         "cpu_model": model,
@@ -492,7 +513,8 @@ def cpu_baseline_q4k(args, x_up, x_dn, q_up, q_dn):
         "host_cpus": len(os.sched_getaffinity(0)),
         "threads_from": threads_src,
         "sample": f"Q4_K up+down mul_mat incl. Q8_K activation quantization on the first {rows} of 8192 "
-                  f"token rows, {reps} rep(s), {dt:.1f} s; restated ggml-cpu algorithm ({impl}), "
+                  f"token rows, median of {reps} rep(s) after a warm-up ({dt:.1f} s); restated ggml-cpu "
+                  f"algorithm ({impl}), "
                   f"{nthreads} threads ({threads_src}) on {model}",
     }
 

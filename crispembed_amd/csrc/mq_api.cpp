@@ -144,6 +144,34 @@ int mq_init(void) {
     return MQ_OK;
 }
 
+int mq_measure_mfma_i8(int iters, double *tops, void *stream) {
+    if (iters <= 0 || !tops) return fail(MQ_EINVAL, "mq_measure_mfma_i8: iters > 0 and tops required");
+    int dev = 0, ncu = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return hip_fail(e, "device query");
+    hipStream_t s = (hipStream_t)stream;
+    int *out = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float ms = 0.f;
+    e = hipMalloc(&out, (size_t)ncu * 256 * sizeof(int));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(MQ_ENOMEM, "hipMalloc for the probe output failed");
+    }
+    if ((e = hipEventCreate(&e0)) == hipSuccess && (e = hipEventCreate(&e1)) == hipSuccess &&
+        (e = mq::launch_mfma_probe(iters, out, ncu, s)) == hipSuccess &&  // warm-up: clocks, code object
+        (e = hipEventRecord(e0, s)) == hipSuccess && (e = mq::launch_mfma_probe(iters, out, ncu, s)) == hipSuccess &&
+        (e = hipEventRecord(e1, s)) == hipSuccess && (e = hipEventSynchronize(e1)) == hipSuccess)
+        e = hipEventElapsedTime(&ms, e0, e1);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipFree(out);
+    if (e != hipSuccess) return hip_fail(e, "MFMA probe");
+    *tops = 2.0 * 32 * 32 * 32 * 8 * (double)iters * 4 * ncu / (ms * 1e-3) / 1e12;
+    return MQ_OK;
+}
+
 int mq_gemv_max_m(void) {
     if (g_gemv_max_m < 0) {
         int v = env_int("MQ_FORCE_GEMV_MAX_M", 8);

@@ -909,4 +909,27 @@ hipError_t launch_gemm_requant(int type, const void *image, int64_t n, int64_t k
     }
 }
 
+// Sustained int8 MFMA rate: each wave keeps 8 independent accumulator chains busy (a chain's
+// next MFMA is 8 issues later, so the matrix pipe never waits on a result); the operands come
+// from the thread index, the sums are written out so nothing is folded away.
+__global__ __launch_bounds__(256) void k_mfma_probe(int iters, int *out) {
+    const int t = threadIdx.x;
+    const v4i a = {t, t * 3 + 1, t * 5 + 2, t * 7 + 3}, b = {t ^ 0x55, t + 9, t * 11, t ^ 0x33};
+    v16i acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[j] = (v16i){};
+    for (int i = 0; i < iters; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[j], 0, 0, 0);
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) sum += acc[j][0] + acc[j][15];
+    out[blockIdx.x * blockDim.x + t] = sum;
+}
+
+hipError_t launch_mfma_probe(int iters, int *out, int ncu, hipStream_t s) {
+    hipLaunchKernelGGL(k_mfma_probe, dim3((unsigned)ncu), dim3(256), 0, s, iters, out);
+    return hipGetLastError();
+}
+
 }  // namespace mq

@@ -290,6 +290,7 @@ hipError_t launch_dequantize(int type, const void *w, float *y, int64_t nrows, i
 hipError_t launch_weight_prepare(int type, void *image, int64_t n, int64_t k, int64_t row0, int64_t row1,
                                  hipStream_t s);
 // bias: NULL, or n floats added to every output row as it is stored
+hipError_t launch_mfma_probe(int iters, int *out, int ncu, hipStream_t s);
 hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
                        int64_t ldy, hipStream_t s, const float *bias = nullptr);
 hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,

@@ -38,6 +38,7 @@ _c_int = ctypes.c_int
 # name -> (restype, argtypes)
 _SIGS = {
     "mq_init": (_c_int, []),
+    "mq_measure_mfma_i8": (_c_int, [_c_int, ctypes.POINTER(ctypes.c_double), ctypes.c_void_p]),
     "mq_last_error": (ctypes.c_char_p, []),
     "mq_gemv_max_m": (_c_int, []),
     "mq_q8_0_variant": (_c_int, []),

@@ -70,6 +70,12 @@ int mq_init(void);
 const char *mq_last_error(void);
 /* Largest m routed to the GEMV path by MQ_PATH_AUTO (default 8; env MQ_FORCE_GEMV_MAX_M). */
 int mq_gemv_max_m(void);
+/* The device's sustained dense int8 MFMA rate, measured: one workgroup per CU, one wave per SIMD,
+ * each wave issuing `iters` x 8 independent v_mfma_i32_32x32x32_i8 (no memory traffic), timed
+ * with HIP events on `stream`; *tops = 2*32*32*32 ops per MFMA / time in TOP/s.  A measurement
+ * aid for comparing kernels with what the chip holds under MFMA load (its clock drops below the
+ * datasheet's); no counterpart in the reference. */
+int mq_measure_mfma_i8(int iters, double *tops, void *stream);
 /* Q8_0 activation rounding variant used by mq_mul_mat (default MQ_Q8_0_X86; env MQ_Q8_0_VARIANT). */
 int mq_q8_0_variant(void);
 int mq_set_q8_0_variant(int variant);
