@@ -113,3 +113,23 @@ def test_full_size_sampled_rows(oracle, wtype, n, k, m, act):
     _check(oracle, wtype, w, x[rows], y[rows], k)
     yv = host(mul_mat(wtype, wp, n, k, dev(x[rows[:8]]), path=mq.PATH_GEMV))
     assert rel_err(yv, y[rows[:8]]) <= TOL
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("m,n,k,pad", [(2048, 4608, 512, 0), (2048, 16384, 768, 64), (4096, 4096, 2048, 0)])
+def test_gemm_many_tiles(oracle, wtype, m, n, k, pad, monkeypatch):
+    """256x128 tiles (MQ_GEMM_CFG=1) on grids of 288-1024 tiles, more than the chip holds at once,
+    with K from 2 to 8 superblocks: oracle on sampled rows (first and last of a tile row among
+    them), columns past n untouched (ldy = n + pad)."""
+    from crispembed_amd import mq
+    import torch
+    monkeypatch.setenv("MQ_GEMM_CFG", "1")
+    w, x = _mk(oracle, wtype, m, n, k, m + n + k + pad)
+    _, wp = weight_image(wtype, w, n, k)
+    ybuf = torch.full((m, n + pad), 7.0, device="cuda")
+    mul_mat(wtype, wp, n, k, dev(x), path=mq.PATH_GEMM, y_dev=ybuf)
+    y = host(ybuf)
+    assert np.all(y[:, n:] == 7.0)
+    rng = np.random.default_rng(k)
+    rows = np.unique(np.concatenate([[0, 255, 256, m - 1], rng.integers(0, m, 36)]))
+    _check(oracle, wtype, w, x[rows], y[rows, :n], k)
