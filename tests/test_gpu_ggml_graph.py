@@ -162,6 +162,29 @@ def test_decoder_graph_matches_reference(oracle, tmp_path, wtype, hd, causal):
     assert _pool(got) @ _pool(ref) >= 0.9999
 
 
+@pytest.mark.parametrize("wtype", [O.Q4_K, O.Q6_K])
+def test_decoder_graph_decode_size(oracle, tmp_path, monkeypatch, wtype):
+    """The decoder graph at decode size (T = 5 tokens: every mat-mul on the self-quantizing GEMV
+    path, q|k|v and gate|up as grouped launches) against the CPU decoder, and against the same
+    graph run node by node (MQ_GGML_NO_FUSION=1: every MUL_MAT on its own, its input quantized by
+    a separate launch)."""
+    import decoder_oracle
+    from crispembed_amd import decoder
+    hp = dict(DEC_HP)
+    W = decoder.synthetic_weights(hp, wtype, name=f"dgraph_decode{wtype}")
+    model = tmp_path / "d.gguf"
+    gguf.write_decoder_gguf(model, hp, wtype, W)
+    ids = np.random.default_rng(wtype + 5).integers(0, hp["n_vocab"], (1, 5)).astype(np.int32)
+    got = _run_dec(tmp_path, model, ids)
+    monkeypatch.setenv("MQ_GGML_NO_FUSION", "1")
+    plain = _run_dec(tmp_path, model, ids)
+    _, x = decoder_oracle.encode(oracle, hp, wtype, W, ids)
+    ref = decoder_oracle.rms_norm(x, W["out_norm"], hp["rms_norm_eps"])
+    assert np.isfinite(got).all()
+    assert _cos_rows(got, ref).min() >= 0.9999
+    assert _cos_rows(got, plain).min() >= 0.99999
+
+
 def test_bert_graph_hip_graph_replay(tmp_path):
     """With MQ_GGML_GRAPH=1 the backend captures a graph computed twice in a row and replays
     it: replays with different inputs uploaded in between (eager copies and readbacks between
