@@ -91,6 +91,7 @@ def test_library_workspace_and_auto_path(oracle):
 
 @pytest.mark.parametrize("wtype,n,k,m,act", [
     (O.Q8_0, 1536, 384, 4096, None),          # MiniLM-L6 FFN-up
+    (O.Q8_0, 384, 1536, 4096, "gelu"),        # MiniLM-L6 FFN-down
     (O.Q4_K, 4096, 1024, 8192, None),         # XLM-R-large FFN-up
     (O.Q4_K, 1024, 4096, 8192, "gelu"),       # XLM-R-large FFN-down on GELU(N(0,1))
 ])
