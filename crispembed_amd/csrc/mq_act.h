@@ -1,5 +1,5 @@
 // mq_act.h -- device helpers shared by the activation quantizers and the GEMM's quantized
-// output: fp16 conversions and ggml's GELU-erf.  The arithmetic is written out without
+// output: fp16 conversions, ggml's GELU-erf and SiLU.  The arithmetic is written out without
 // contraction (the pragma below), so every translation unit that includes it rounds each
 // multiply and add on its own, as the quantizers' ISO C restatement does.
 #pragma once
@@ -20,6 +20,12 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return (float)__b
 __device__ __forceinline__ float gelu_erf_f32(float v) {
 #pragma clang fp contract(off)
     return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+}
+
+// ggml_silu(g) * u (ggml-cpu vec.h ggml_silu_f32, then GGML_OP_MUL) in fp32: g / (1 + exp(-g)), times u
+__device__ __forceinline__ float silu_mul_f32(float g, float u) {
+#pragma clang fp contract(off)
+    return (g / (1.0f + expf(-g))) * u;
 }
 
 // Half of one Q8_0 block of a kernel's quantized output: this lane's 16 values, the other 16

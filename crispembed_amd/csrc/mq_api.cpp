@@ -371,6 +371,23 @@ int mq_mul_mat_q_requant(int type, const void *w_image, int64_t n, int64_t k, co
     return e == hipSuccess ? MQ_OK : hip_fail(e, "gemm");
 }
 
+int mq_mul_mat_q_swiglu(int type, const void *w_image, int64_t n_ff, int64_t k, const void *workspace, int64_t m,
+                        float *y, int64_t ldy, void *stream) {
+    if (n_ff <= 0 || n_ff > INT32_MAX / 2) return fail(MQ_EINVAL, "mq_mul_mat_q_swiglu: bad n_ff");
+    int rc = check_weight_shape(type, 2 * n_ff, k);
+    if (rc) return rc;
+    if (!w_image || !workspace || !y || m < 0 || m > INT32_MAX || ldy < n_ff)
+        return fail(MQ_EINVAL, "mq_mul_mat_q_swiglu: bad arguments");
+    if (!is_aligned(w_image, 256) || !is_aligned(workspace, 256))
+        return fail(MQ_EINVAL, "mq_mul_mat_q_swiglu: weight image and workspace must be 256-byte aligned");
+    if (m == 0) return MQ_OK;
+    if (!gemm_swiglu_fits(m, n_ff))
+        return fail(MQ_EUNSUPPORTED, "mq_mul_mat_q_swiglu: m = %lld, n_ff = %lld runs as mul_mat + quantizer prologue",
+                    (long long)m, (long long)n_ff);
+    const hipError_t e = launch_gemm_swiglu(type, w_image, n_ff, k, workspace, m, y, ldy, (hipStream_t)stream);
+    return e == hipSuccess ? MQ_OK : hip_fail(e, "gemm");
+}
+
 int mq_mul_mat_q_qkv(int type, const void *const *w_images, const int64_t *n, int64_t k, const void *workspace,
                      int64_t m, float *y_q, int64_t ldy_q, const float *const *bias, int T, int head_dim,
                      int n_kv_head, void *kv_frags, size_t kv_frags_bytes, void *stream) {

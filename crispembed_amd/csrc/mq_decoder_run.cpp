@@ -8,7 +8,8 @@
 //          the per-head norms and rotations applied as the attention kernels load q and k
 //   X    = X + A . Wo^T;  Hn = rms_norm(X) * ffn_norm
 //   gu   = Hn . [Wgate; Wup]^T                      one mul_mat, gate and up side by side
-//   X    = X + (silu(gate) * up) . Wdown^T          the product formed by the quantizer
+//   X    = X + (silu(gate) * up) . Wdown^T          the product formed in the gate|up GEMM's
+//                                                   store (large batches) or by the quantizer
 // then the output RMS norm of the pooled rows and L2 normalisation.
 #include <hip/hip_runtime.h>
 
@@ -194,6 +195,11 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
         }
         return hip_rc(launch_add_rmsnorm(m->y.f(), X, nullptr, nullptr, 0, w, eps, X, Hn, rows, (int)H, s), what);
     };
+    // the gate|up GEMM forms silu(gate) * up in its store where the shape allows (not while
+    // observed: the observer reads gate and up); MQ_DECODER_NO_GLU=1 keeps the two-step form
+    const bool glu = !m->obs && !m->layers.empty() && gemm_swiglu_fits(rows, F) &&
+                     mq_mul_mat_path(t, m->layers[0].gu.n, H, rows) == MQ_PATH_GEMM &&
+                     std::getenv("MQ_DECODER_NO_GLU") == nullptr;
     for (size_t il = 0; il < m->layers.size(); il++) {
         const DecLayer &L = m->layers[il];
         if ((rc = mm_hn(L.qkv, m->qkv.f(), "attn_norm", (int)il))) return rc;
@@ -207,14 +213,22 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
         if ((rc = mm(L.o, m->att.f(), qd, m->y.f(), "attn_out", (int)il))) return rc;
         // X += A Wo^T; Hn = rms_norm(X) * ffn_norm
         if ((rc = add_norm(L.ffn_norm.f(), "attention residual", false))) return rc;
-        if ((rc = mm_hn(L.gu, m->gu.f(), "ffn_norm", (int)il))) return rc;
-        hn_q = false;
-        // down projection of silu(gate) * up, the product formed inside the quantizer
         const int dpath = mq_mul_mat_path(t, L.down.n, L.down.k, rows);
-        if ((rc = mq_quantize_act_ex(t, m->gu.f(), 2 * F, rows, F, nullptr, MQ_PRE_SILU_MUL, m->ws.p, m->ws.bytes,
-                                     dpath, s)))
-            return rc;
-        if ((rc = observe("ffn_gate_up", (int)il, m->gu.f(), 2 * F, true))) return rc;
+        if (glu) {
+            // silu(gate) * up formed in the gate|up GEMM's store (F columns), then quantized as is
+            if (!hn_q && (rc = mq_quantize_act(t, Hn, H, rows, H, m->ws.p, m->ws.bytes, MQ_PATH_GEMM, s))) return rc;
+            hn_q = false;
+            if ((rc = mq_mul_mat_q_swiglu(t, L.gu.img.p, F, H, m->ws.p, rows, m->gu.f(), F, s))) return rc;
+            if ((rc = mq_quantize_act(t, m->gu.f(), F, rows, F, m->ws.p, m->ws.bytes, dpath, s))) return rc;
+        } else {
+            if ((rc = mm_hn(L.gu, m->gu.f(), "ffn_norm", (int)il))) return rc;
+            hn_q = false;
+            // down projection of silu(gate) * up, the product formed inside the quantizer
+            if ((rc = mq_quantize_act_ex(t, m->gu.f(), 2 * F, rows, F, nullptr, MQ_PRE_SILU_MUL, m->ws.p,
+                                         m->ws.bytes, dpath, s)))
+                return rc;
+            if ((rc = observe("ffn_gate_up", (int)il, m->gu.f(), 2 * F, true))) return rc;
+        }
         if ((rc = mq_mul_mat_q(t, L.down.img.p, L.down.n, L.down.k, m->ws.p, rows, m->y.f(), H, dpath, s)))
             return rc;
         // X += FFN; Hn = rms_norm(X) * (next layer's attn_norm, or the output norm)

@@ -204,12 +204,32 @@ struct DmaItem {
     int64_t step;
     int lds;
     int pieces;
+    int loff;  // this lane's byte offset from g0, (lane % pieces) 16 unless remapped (used by GLU kernels)
 };
 
-template <class C, int FMT>
-__device__ __forceinline__ DmaItem stage_item(const GemmArgs &a, int f, int m0, int n0) {
+// Weight tile (32 rows) of the workgroup's 32-column block c.  GLU (a gated FFN's gate|up
+// weight, N = 2 n_ff: gate rows, then up rows): block c holds gate tile n0 / 64 + c / 2 for
+// even c, the same up tile for odd c, so a wave's two column tiles (TN = 2) are the gate and up
+// projections of the same 32 features.
+template <bool GLU>
+__device__ __forceinline__ int wtile(const GemmArgs &a, int n0, int c) {
+    if constexpr (GLU) return (c & 1) * (a.N >> 6) + (n0 >> 6) + (c >> 1);
+    else return (n0 >> 5) + c;
+}
+
+// GLU: byte offset of this lane's 16 bytes (4 columns) of a weight scale row of the
+// workgroup's BN columns, from the row's start
+template <bool GLU>
+__device__ __forceinline__ int wrow_off(const GemmArgs &a, int n0, int lane, int pieces) {
+    const int p = lane & (pieces - 1);
+    return (wtile<GLU>(a, n0, p >> 3) * 32 + ((4 * p) & 31)) * 4;
+}
+
+template <class C, int FMT, bool GLU>
+__device__ __forceinline__ DmaItem stage_item(const GemmArgs &a, int f, int m0, int n0, int lane) {
     DmaItem it;
     it.pieces = 64;
+    it.loff = lane * 16;
     if (f < C::XF) {
         const int rt = f / C::KC, kc = f % C::KC;
         it.g0 = a.xq + ((int64_t)((m0 >> 5) + rt) * a.kch + kc) * 1024;
@@ -219,7 +239,7 @@ __device__ __forceinline__ DmaItem stage_item(const GemmArgs &a, int f, int m0, 
         const int f2 = f - C::XF;
         const int pl = f2 / C::WF, f3 = f2 % C::WF;
         const int ct = f3 / C::KC, kc = f3 % C::KC;
-        it.g0 = (pl ? a.whi : a.wq) + ((int64_t)((n0 >> 5) + ct) * a.kch + kc) * 1024;
+        it.g0 = (pl ? a.whi : a.wq) + ((int64_t)wtile<GLU>(a, n0, ct) * a.kch + kc) * 1024;
         it.step = C::KC * 1024;
         it.lds = C::X_BYTES + pl * C::W_BYTES + f3 * 1024;
     } else {
@@ -229,49 +249,59 @@ __device__ __forceinline__ DmaItem stage_item(const GemmArgs &a, int f, int m0, 
             it.step = (int64_t)C::KC * a.m_pad * 4;
             it.lds = C::X_BYTES + C::W_BYTES + f4 * 1024;
             it.pieces = C::BM / 4;
+            it.loff = (lane & (it.pieces - 1)) * 16;
         } else {
-            it.g0 = (const int8_t *)(a.wd + (int64_t)(f4 - C::KC) * a.n_pad + n0);
+            it.g0 = (const int8_t *)(a.wd + (int64_t)(f4 - C::KC) * a.n_pad + (GLU ? 0 : n0));
             it.step = (int64_t)C::KC * a.n_pad * 4;
             it.lds = C::X_BYTES + C::W_BYTES + C::SCX + (f4 - C::KC) * 1024;
             it.pieces = C::BN / 4;
+            if constexpr (GLU) it.loff = wrow_off<GLU>(a, n0, lane, it.pieces);
         }
     }
     return it;
 }
 
 // Superblock epilogue item e for superblock sb (K-quants).
-template <class C, int FMT>
-__device__ __forceinline__ DmaItem epi_item(const GemmArgs &a, int e, int sb, int m0, int n0) {
+template <class C, int FMT, bool GLU>
+__device__ __forceinline__ DmaItem epi_item(const GemmArgs &a, int e, int sb, int m0, int n0, int lane) {
     DmaItem it;
     it.step = 0;
     it.pieces = 64;
+    it.loff = lane * 16;
     if (e == 0) {
         it.g0 = (const int8_t *)(a.xd + (int64_t)sb * a.m_pad + m0);
         it.lds = 0;
         it.pieces = C::BM / 4;
+        it.loff = (lane & (it.pieces - 1)) * 16;
     } else if (e == 1) {
-        it.g0 = (const int8_t *)(a.wd + (int64_t)sb * a.n_pad + n0);
+        it.g0 = (const int8_t *)(a.wd + (int64_t)sb * a.n_pad + (GLU ? 0 : n0));
         it.lds = C::EP_DX;
         it.pieces = C::BN / 4;
+        if constexpr (GLU) it.loff = wrow_off<GLU>(a, n0, lane, it.pieces);
     } else if (e == 2) {
-        it.g0 = (const int8_t *)(a.wdmin + (int64_t)sb * a.n_pad + n0);
+        it.g0 = (const int8_t *)(a.wdmin + (int64_t)sb * a.n_pad + (GLU ? 0 : n0));
         it.lds = C::EP_DX + C::EP_DW;
         it.pieces = C::BN / 4;
+        if constexpr (GLU) it.loff = wrow_off<GLU>(a, n0, lane, it.pieces);
     } else if (e < 3 + C::BM / 32) {
         const int rt = e - 3;
         it.g0 = (const int8_t *)a.xmin + ((int64_t)((m0 >> 5) + rt) * a.nsb + sb) * 1024;
         it.lds = C::EP_DX + C::EP_DW + C::EP_DMIN + rt * 1024;
     } else {
         const int ct = e - 3 - C::BM / 32;
-        it.g0 = (const int8_t *)a.wmin + ((int64_t)((n0 >> 5) + ct) * a.nsb + sb) * 1024;
+        it.g0 = (const int8_t *)a.wmin + ((int64_t)wtile<GLU>(a, n0, ct) * a.nsb + sb) * 1024;
         it.lds = C::EP_DX + C::EP_DW + C::EP_DMIN + C::EP_AMIN + ct * 1024;
     }
     return it;
 }
 
-template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2>
+// GLU: a.N = 2 n_ff columns of a gate|up weight; y receives silu(gate) * up, n_ff columns (the
+// gated FFN's down-projection input, src/decoder_embed.cpp:793-802), and no gate or up value
+// is stored.
+template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2, bool GLU = false>
 __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) {
     using C = Cfg<FMT, WM, WN, TM, TN, KCT>;
+    static_assert(!GLU || TN == 2, "GLU: each wave holds a gate and an up column tile");
     constexpr int KC = C::KC, SPB = C::SPB;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     const int lane = threadIdx.x & 63;
@@ -312,7 +342,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
     // every point, so each wait below is a compile-time constant.
     DmaItem items[C::IPW];
 #pragma unroll
-    for (int i = 0; i < C::IPW; i++) items[i] = stage_item<C, FMT>(a, (wave + C::NW * i) % C::NITEM, m0, n0);
+    for (int i = 0; i < C::IPW; i++) items[i] = stage_item<C, FMT, GLU>(a, (wave + C::NW * i) % C::NITEM, m0, n0, lane);
 
     // Stages past the end are issued too, re-reading the last stage into the
     // slot of a stage that is never computed, so the DMA count per stage stays
@@ -328,14 +358,17 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
                 const int sbc = sb < a.nsb ? sb : a.nsb - 1;
 #pragma unroll
                 for (int i = 0; i < C::EPW; i++) {
-                    const DmaItem it = epi_item<C, FMT>(a, (wave + C::NW * i) % C::NEPI, sbc, m0, n0);
-                    dma16(it.g0 + (lane & (it.pieces - 1)) * 16, ep + it.lds);
+                    const DmaItem it = epi_item<C, FMT, GLU>(a, (wave + C::NW * i) % C::NEPI, sbc, m0, n0, lane);
+                    if constexpr (GLU) dma16(it.g0 + it.loff, ep + it.lds);
+                    else dma16(it.g0 + (lane & (it.pieces - 1)) * 16, ep + it.lds);
                 }
             }
         }
 #pragma unroll
-        for (int i = 0; i < C::IPW; i++)
-            dma16(items[i].g0 + sc * items[i].step + (lane & (items[i].pieces - 1)) * 16, st + items[i].lds);
+        for (int i = 0; i < C::IPW; i++) {
+            if constexpr (GLU) dma16(items[i].g0 + sc * items[i].step + items[i].loff, st + items[i].lds);
+            else dma16(items[i].g0 + sc * items[i].step + (lane & (items[i].pieces - 1)) * 16, st + items[i].lds);
+        }
     };
 
     v16f acc[TM][TN];
@@ -539,7 +572,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
     float bv[TN];
 #pragma unroll
     for (int j = 0; j < TN; j++) {
-        const int col = n0 + (wn * TN + j) * 32 + lrow;
+        const int col = GLU ? wtile<GLU>(a, n0, wn * TN + j) * 32 + lrow : n0 + (wn * TN + j) * 32 + lrow;
         bv[j] = (a.bias && col < a.N) ? a.bias[col] : 0.f;
     }
     // no DMA may still be writing this workgroup's LDS when it exits
@@ -554,6 +587,19 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
             for (int j = 0; j < TN; j++)
 #pragma unroll
                 for (int rr = 0; rr < 16; rr++) acc[i][j][rr] += bv[j];
+    }
+
+    if constexpr (GLU) {
+        // silu(gate) * up of the wave's 32 features (column tile 0: gate, 1: up, same layout)
+        const int col = ((n0 >> 6) + wn) * 32 + lrow;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int rr = 0; rr < 16; rr++) {
+                const int row = m0 + (wm * TM + i) * 32 + 8 * (rr >> 2) + 4 * lhalf + (rr & 3);
+                if (row < a.M) a.y[(int64_t)row * a.ldy + col] = silu_mul_f32(acc[i][0][rr], acc[i][1][rr]);
+            }
+        return;
     }
 
     if (a.qo) {
@@ -670,12 +716,12 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
         }
 }
 
-template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2>
+template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2, bool GLU = false>
 static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
     using C = Cfg<FMT, WM, WN, TM, TN, KCT>;
     static bool attr_set = false;
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm<FMT, WM, WN, TM, TN, MINB, KCT>,
+        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm<FMT, WM, WN, TM, TN, MINB, KCT, GLU>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
         if (e != hipSuccess) return e;
         attr_set = true;
@@ -689,7 +735,7 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
     a.group_m = 8;
     a.nstages = a.kch / KCT;  // kb_pad is a multiple of 128 bytes
     const unsigned grid = (unsigned)(a.tiles_m * a.tiles_n);
-    hipLaunchKernelGGL((k_gemm<FMT, WM, WN, TM, TN, MINB, KCT>), dim3(grid), dim3(C::NT), C::LDS, s, a);
+    hipLaunchKernelGGL((k_gemm<FMT, WM, WN, TM, TN, MINB, KCT, GLU>), dim3(grid), dim3(C::NT), C::LDS, s, a);
     return hipGetLastError();
 }
 
@@ -905,6 +951,55 @@ hipError_t launch_gemm_requant(int type, const void *image, int64_t n, int64_t k
         case MQ_TYPE_Q4_K: return launch_fmt<FMT_Q4_K>(a, s);
         case MQ_TYPE_Q6_K: return launch_fmt<FMT_Q6_K>(a, s);
         case MQ_TYPE_F16: return launch_fmt<FMT_F16>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// The gated FFN's gate|up GEMM with silu(gate) * up formed in its store (k_gemm<..., GLU>).  It
+// runs on the large-grid configurations only (256x128 or 128x128 workgroups, whose waves hold
+// 64-column pairs); shapes the launcher would give 64x64 workgroups are not fused.
+bool gemm_swiglu_fits(int64_t m, int64_t n_ff) {
+    return m > 0 && n_ff > 0 && n_ff % 64 == 0 && tiles(m, 2 * n_ff, 128, 128) >= 512 && 2 * n_ff <= INT32_MAX;
+}
+
+hipError_t launch_gemm_swiglu(int type, const void *image, int64_t n_ff, int64_t k, const void *ws, int64_t m, float *y,
+                              int64_t ldy, hipStream_t s) {
+    if (!gemm_swiglu_fits(m, n_ff) || ldy < n_ff) return hipErrorInvalidValue;
+    const int64_t n = 2 * n_ff;
+    const ActPlanes ap = act_planes(type, m, k, true);
+    const WeightPlanes p = weight_planes(type, n, k);
+    const uint8_t *xb = (const uint8_t *)ws, *wb = (const uint8_t *)image;
+    GemmArgs a{};
+    a.xq = (const int8_t *)(xb + ap.xq);
+    a.xd = (const float *)(xb + ap.xd);
+    a.xmin = (const _Float16 *)(xb + ap.xmin);
+    a.wq = (const int8_t *)(wb + p.tq);
+    a.whi = (const int8_t *)(wb + p.thi);
+    a.wd = (const float *)(wb + p.tdw);
+    a.wdmin = (const float *)(wb + p.tdmin);
+    a.wmin = (const _Float16 *)(wb + p.tmin);
+    a.y = y;
+    a.M = (int)m;
+    a.N = (int)n;
+    a.ldy = (int)ldy;
+    a.m_pad = (int)ap.m_pad;
+    a.n_pad = (int)p.n_pad;
+    a.kch = (int)(p.kb_pad / 32);
+    a.nstages = (int)(p.kb_pad / 64);
+    a.nsb = (int)(k / QK_K);
+    a.ngroups = 1;
+    int cfg = gemm_cfg_env();
+    if (cfg != 1 && cfg != 3) cfg = (tiles(m, n, 256, 128) >= 256) ? 1 : 3;
+    auto go = [&](auto fmt) -> hipError_t {
+        constexpr int F = decltype(fmt)::value;
+        if (cfg == 1) return launch_cfg<F, 4, 2, 2, 2, 1, 2, true>(a, s);
+        return launch_cfg<F, 2, 2, 2, 2, 2, 2, true>(a, s);
+    };
+    switch (type) {
+        case MQ_TYPE_Q8_0: return go(std::integral_constant<int, FMT_Q8_0>{});
+        case MQ_TYPE_Q4_K: return go(std::integral_constant<int, FMT_Q4_K>{});
+        case MQ_TYPE_Q6_K: return go(std::integral_constant<int, FMT_Q6_K>{});
+        case MQ_TYPE_F16: return go(std::integral_constant<int, FMT_F16>{});
         default: return hipErrorInvalidValue;
     }
 }

@@ -300,6 +300,12 @@ hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const 
 // MQ_PRE_NONE or MQ_PRE_GELU_ERF.  ws must hold x in the tiled (GEMM) layout.
 hipError_t launch_gemm_requant(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m,
                                const float *bias, int pre, int q8_0_variant, void *out_ws, hipStream_t s);
+// the GEMM of a gated FFN's gate|up weight (2 n_ff rows: gate, then up) whose store forms
+// silu(gate) * up into y (m x n_ff, row stride ldy); only for shapes gemm_swiglu_fits accepts
+// (n_ff a multiple of 64, grids of the large-tile configurations)
+bool gemm_swiglu_fits(int64_t m, int64_t n_ff);
+hipError_t launch_gemm_swiglu(int type, const void *image, int64_t n_ff, int64_t k, const void *ws, int64_t m, float *y,
+                              int64_t ldy, hipStream_t s);
 // the GEMM of an attention's concatenated q|k|v projection whose K and V columns ([kv_col0,
 // kv_col0 + nkv hd), then nkv hd more; n = kv_col0 + 2 nkv hd) leave as the attention's hi/lo
 // fp16 operand fragments in kv_frags (the layout launch_attn's K/V pass writes, m = B T rows,

@@ -49,7 +49,7 @@ __device__ __forceinline__ float4 pre_load(const float *p, int pre, const float 
     for (int i = 0; i < 4; i++) {
         if (bias) r[i] = r[i] + bias[col + i];
         if (pre == MQ_PRE_GELU_ERF) r[i] = gelu_erf_f32(r[i]);
-        else if (pre == MQ_PRE_SILU_MUL) r[i] = (r[i] / (1.0f + expf(-r[i]))) * u[i];
+        else if (pre == MQ_PRE_SILU_MUL) r[i] = silu_mul_f32(r[i], u[i]);
     }
     return make_float4(r[0], r[1], r[2], r[3]);
 }

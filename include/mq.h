@@ -216,6 +216,18 @@ int mq_mul_mat_q_requant(int type, const void *w_image, int64_t n, int64_t k, co
                          const float *bias, int op, int out_type, void *out_workspace, size_t out_workspace_bytes,
                          void *stream);
 
+/* The gate and up projections of a gated FFN and the product between them, as one GEMM: w_image
+ * holds 2 n_ff rows (the gate weight's n_ff rows, then the up weight's: the gate|up product of
+ * mq_mul_mat_q), the activation is quantized with path MQ_PATH_GEMM, and y (m x n_ff, row stride
+ * ldy) receives silu(gate) * up -- the values mq_quantize_act_ex(..., MQ_PRE_SILU_MUL, ...) forms
+ * from that product, bit for bit -- while gate and up themselves are never written.  This is the
+ * decoder FFN of src/decoder_embed.cpp:793-802 (gate and up MUL_MATs, ggml_silu, ggml_mul) before
+ * its down projection.  Returns MQ_EUNSUPPORTED unless n_ff is a multiple of 64 and the product
+ * has at least 512 tiles of 128 x 128 (smaller shapes run faster as mq_mul_mat_q followed by the
+ * quantizer's MQ_PRE_SILU_MUL prologue). */
+int mq_mul_mat_q_swiglu(int type, const void *w_image, int64_t n_ff, int64_t k, const void *workspace, int64_t m,
+                        float *y, int64_t ldy, void *stream);
+
 /* The q, k and v projections of an attention layer (src/crispembed.cpp:1168-1170, each with its
  * bias ADD) on one activation quantized with path MQ_PATH_GEMM, as one grouped GEMM: q (n[0]
  * features) is stored to y_q as mq_mul_mat_q_group stores it, while k and v (n[1] = n[2] =

@@ -71,7 +71,9 @@ int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T, float *ou
  *                quantization, cols n_ff)
  *   "l_out"      the residual stream after layer il (xq NULL)
  * The tensors are only valid during the call.  Observing makes the runner also write the
- * normed rows it otherwise leaves only in quantized form (the quantized bytes do not change).
+ * normed rows it otherwise leaves only in quantized form, and the gate and up projections that
+ * large batches otherwise never write (silu(gate) * up then formed in the gate|up GEMM's store,
+ * mq_mul_mat_q_swiglu); the quantized bytes do not change.
  * cb NULL removes the observer. */
 typedef void (*mq_decoder_observer)(const char *name, int layer, const float *x, int64_t rows, int64_t cols,
                                     const void *xq, size_t xq_bytes, void *user);

@@ -107,6 +107,23 @@ def test_full_batch_properties(qwen3):
     assert len(qwen3["seen"]) == 5 * qwen3["hp"]["n_layer"]
 
 
+def test_unobserved_batch_bit_identical(qwen3, monkeypatch):
+    """The 16 x 512 batch without the observer: the gate|up GEMM then forms silu(gate) * up in
+    its store (mq_mul_mat_q_swiglu) instead of writing gate and up for the quantizer's prologue,
+    and the normed rows stay in quantized form only.  Every quantized byte is the same, so the
+    pooled embeddings equal the observed run's bit for bit; so do those of the two-step form
+    (MQ_DECODER_NO_GLU=1) without the observer."""
+    import torch
+    hp, dec, ids = qwen3["hp"], qwen3["dec"], qwen3["ids"]
+    ids_d = torch.from_numpy(ids.ravel().copy()).cuda()
+    for no_glu in (False, True):
+        if no_glu:
+            monkeypatch.setenv("MQ_DECODER_NO_GLU", "1")
+        out = torch.empty((B, hp["n_embd"]), dtype=torch.float32, device="cuda")
+        dec.encode(ids_d.data_ptr(), B, T, out.data_ptr(), stream())
+        assert np.array_equal(host(out).view(np.uint32), qwen3["pooled"].view(np.uint32)), no_glu
+
+
 def test_sampled_batch_independent(qwen3):
     """A sequence's embedding in a batch of 2 against the batch of 16 (another GEMM tile grid):
     the same computation up to fp32 rounding, so at the end-to-end bar."""

@@ -297,3 +297,72 @@ def test_qkv_fragments_equal_kv_pass(wtype, hd, nh, B, T):
                                    ctypes.c_void_p(f2.data_ptr() + o2), fb, None, 0, mq.ATTN_KV_READY, stream()))
     assert np.array_equal(host(out2), host(out1))
     del imgs, ws
+
+
+def _silu_mul(g, u):
+    g = g.astype(np.float32)
+    return ((g / (np.float32(1.0) + np.exp(-g))) * u).astype(np.float32)
+
+
+@pytest.mark.parametrize("wtype", TYPES)
+@pytest.mark.parametrize("m,n_ff,k,cfg", [(4096, 1024, 512, ""), (4000, 1536, 256, ""), (2048, 2048, 512, "3")])
+def test_mul_mat_q_swiglu_equals_two_step(oracle, wtype, m, n_ff, k, cfg, monkeypatch):
+    """mq_mul_mat_q_swiglu (silu(gate) * up formed in the gate|up GEMM's store) against the
+    two-step form of the decoder FFN (src/decoder_embed.cpp:793-802): the gate|up product by
+    mq_mul_mat_q_ex, then the quantizer's MQ_PRE_SILU_MUL prologue.  The down projection's
+    quantized activation is byte-identical whichever form made it; the fp32 product equals
+    silu(g) * u of the GEMM's own gate and up to the last bits (device expf), with the columns
+    past n_ff untouched; sampled rows match the oracle's gate and up products at the mul_mat
+    bar.  cfg "3" forces the 128x128 workgroups (the other large-grid configuration)."""
+    import torch
+    from crispembed_amd import mq
+    L = mq.lib()
+    if k % 256 and wtype in (O.Q4_K, O.Q6_K):
+        pytest.skip("K-quant rows are whole superblocks")
+    if cfg:
+        monkeypatch.setenv("MQ_GEMM_CFG", cfg)
+    rng = np.random.default_rng(m + n_ff + k + wtype)
+    wf = (rng.standard_normal((2 * n_ff, k)) * 0.05).astype(np.float32)  # gate rows, then up rows
+    w = oracle.quantize_chunk(wtype, wf)
+    _, wp = img = weight_image(wtype, w, 2 * n_ff, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    keep, ptr, _ = _quant(wtype, dev(x), m, k, 2)
+    # two-step
+    gu = torch.empty((m, 2 * n_ff), dtype=torch.float32, device="cuda")
+    mq.check(L.mq_mul_mat_q_ex(wtype, ctypes.c_void_p(wp), 2 * n_ff, k, ctypes.c_void_p(ptr), m,
+                               ctypes.c_void_p(gu.data_ptr()), 2 * n_ff, None, 2, stream()))
+    _, _, want = _quant(wtype, gu, m, n_ff, 2, None, mq.PRE_SILU_MUL)
+    # fused, into an output with padding columns
+    y = torch.full((m, n_ff + 8), np.nan, dtype=torch.float32, device="cuda")
+    mq.check(L.mq_mul_mat_q_swiglu(wtype, ctypes.c_void_p(wp), n_ff, k, ctypes.c_void_p(ptr), m,
+                                   ctypes.c_void_p(y.data_ptr()), n_ff + 8, stream()))
+    _, _, got = _quant(wtype, y[:, :n_ff], m, n_ff, 2)
+    assert np.array_equal(got, want)
+    yh, guh = host(y), host(gu)
+    assert np.isnan(yh[:, n_ff:]).all()
+    ref = _silu_mul(guh[:, :n_ff], guh[:, n_ff:])
+    np.testing.assert_allclose(yh[:, :n_ff], ref, rtol=2e-6, atol=1e-30)
+    rows = np.unique(np.concatenate([np.arange(0, m, 61), [m - 1]]))
+    xq = oracle.quantize_act(wtype, np.ascontiguousarray(x[rows]))
+    yo = oracle.mul_mat_q(wtype, w, xq, k)
+    assert rel_err(yh[rows, :n_ff], _silu_mul(yo[:, :n_ff], yo[:, n_ff:])) <= TOL
+    del img, keep
+
+
+@pytest.mark.parametrize("m,n_ff", [(1000, 1024), (4096, 1000), (8, 3072)])
+def test_mul_mat_q_swiglu_unsupported_shapes(m, n_ff):
+    """Shapes the fused form does not take (fewer than 512 tiles of 128x128, n_ff not a multiple
+    of 64) are refused with MQ_EUNSUPPORTED before anything is launched."""
+    import torch
+    from crispembed_amd import mq
+    L = mq.lib()
+    k = 256
+    w = np.zeros(L.mq_gguf_bytes(O.Q8_0, 2 * n_ff, k), dtype=np.uint8)
+    _, wp = img = weight_image(O.Q8_0, w, 2 * n_ff, k)
+    keep, ptr, _ = _quant(O.Q8_0, dev(np.ones((m, k), np.float32)), m, k, 2)
+    y = torch.full((m, n_ff), np.nan, dtype=torch.float32, device="cuda")
+    rc = L.mq_mul_mat_q_swiglu(O.Q8_0, ctypes.c_void_p(wp), n_ff, k, ctypes.c_void_p(ptr), m,
+                               ctypes.c_void_p(y.data_ptr()), n_ff, stream())
+    assert rc == -2, rc
+    assert np.isnan(host(y)).all()
+    del img, keep
