@@ -17,6 +17,7 @@
 
 #include "mq_internal.h"
 #include "mq_act.h"
+#include "mq_q8k.h"
 #include "mq_wave.h"
 
 namespace mq {
@@ -196,7 +197,12 @@ __global__ __launch_bounds__(256) void k_kv_frag(const AttnArgs a, int nblk) {
     }
 }
 
-template <int HD, bool MASK, bool QO = false>
+// QO: the output also (or, with q_only, only) stored as the projection's quantized activation:
+// AQ_Q8_0 (Q8_0 blocks of 32 head dims), AQ_Q8_K (head_dim 128: the workgroup's two heads are
+// one 256-value Q8_K superblock of each output row; Tq a multiple of 128)
+enum { AQ_NONE = 0, AQ_Q8_0 = 1, AQ_Q8_K = 2 };
+
+template <int HD, bool MASK, int QO = AQ_NONE>
 __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, float qscale) {
     constexpr int NS = HD / 16, NT = HD / 32, HALF = HD / 2, NFR = kv_frags<HD>();
     constexpr float LOG2E = 1.4426950408889634f;
@@ -209,7 +215,7 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
     // (one long and one short causal range each); the longest ranges are dispatched first
     const int qt = wave < 4 ? wave : 7 - wave;
     const int q0 = ((int)gridDim.z - 1 - (int)blockIdx.z) * 128 + qt * 32;
-    if (h >= a.nq || q0 >= Tq) return;  // no workgroup barrier below
+    if (h >= a.nq || q0 >= Tq) return;  // no workgroup barrier below, except for AQ_Q8_K (never taken there)
     const int hk = h / (a.nq / a.nkv), qi = q0 + l32;
     const int qrow = min(qi, Tq - 1);
     const float2 *cs = a.cs;
@@ -371,7 +377,7 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
         inv[4 * g] = t.x, inv[4 * g + 1] = t.y, inv[4 * g + 2] = t.z, inv[4 * g + 3] = t.w;
     }
     float *ob = a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + l32;
-    if (!QO || !a.q_only) {
+    if (QO == AQ_NONE || !a.q_only) {
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int q = q0 + 8 * (r / 4) + 4 * half + (r % 4);
@@ -381,7 +387,7 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
             for (int n = 0; n < NT; n++) o[32 * n] = oacc[n][r] * inv[r];
         }
     }
-    if constexpr (QO) {
+    if constexpr (QO == AQ_Q8_0) {
         // The same values quantized for the projection that reads them: 32 head dims of one
         // query are one Q8_0 block of output row b * Tq + q, chunk h * NT + n.  The wave's
         // 32 x 32 tile goes through LDS so that lane l holds query l % 32, dims 16 (l / 32) ..,
@@ -414,6 +420,37 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    }
+    if constexpr (QO == AQ_Q8_K) {
+        // Output columns 256 bx .. 256 bx + 255 (heads 2 bx and 2 bx + 1, 128 dims each) are one
+        // Q8_K superblock of every output row.  The two waves of a query tile (head slot hs)
+        // stage their 32 x 128 halves side by side in LDS; after the barrier each quantizes 16 of
+        // the tile's 32 rows over all 256 values, lane l holding values 4l .. 4l + 3 (the tiled
+        // activation quantizer's arithmetic and lane layout), straight into the workspace.  Every
+        // wave of the workgroup reaches the barrier: the host launches this form only for an even
+        // nq and Tq a multiple of 128.
+        static_assert(HD == 128, "a superblock is two heads of 128");
+        constexpr int SST = 260;  // staging row stride in floats
+        __shared__ __attribute__((aligned(16))) float sstg[4][32 * SST];
+        float *tile = sstg[qt];
+        const int hs = wave >> 2;
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                tile[(8 * (r / 4) + 4 * half + (r % 4)) * SST + hs * HD + 32 * n + l32] = oacc[n][r] * inv[r];
+        __syncthreads();
+        const int64_t sb = blockIdx.x;
+        int8_t *qbase = a.qo + ((sb * 8 + (lane >> 3)) << 10) + ((32 * ((lane >> 2) & 1)) << 4) + 4 * (lane & 3);
+#pragma unroll 2
+        for (int i = 0; i < 16; i++) {
+            const int rr = hs * 16 + i;
+            const int64_t row = (int64_t)b * Tq + q0 + rr, rt = row >> 5;
+            const int r32 = (int)(row & 31);
+            const float4 v = *(const float4 *)(tile + rr * SST + 4 * lane);
+            q8_K_block_row(v, lane, r32, qbase + ((rt * a.q_kch) << 10) + (r32 << 4), a.qd + sb * a.q_m_pad + row,
+                           a.qmin + ((rt * a.q_nsb + sb) << 9));
         }
     }
 }
@@ -703,8 +740,13 @@ static void launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_
     const dim3 ga((unsigned)((a.nq + 1) / 2), (unsigned)a.B, (unsigned)((a.Tq + 127) / 128));
     if constexpr (HD <= 64) {
         if (a.qo) {  // quantized output: the unmasked / masked forms with the Q8_0 store
-            if (a.mask) hipLaunchKernelGGL((k_attn_frag<HD, true, true>), ga, dim3(512), 0, s, a, nblk, qscale);
-            else hipLaunchKernelGGL((k_attn_frag<HD, false, true>), ga, dim3(512), 0, s, a, nblk, qscale);
+            if (a.mask) hipLaunchKernelGGL((k_attn_frag<HD, true, AQ_Q8_0>), ga, dim3(512), 0, s, a, nblk, qscale);
+            else hipLaunchKernelGGL((k_attn_frag<HD, false, AQ_Q8_0>), ga, dim3(512), 0, s, a, nblk, qscale);
+            return;
+        }
+    } else {
+        if (a.qo) {  // the Q8_K store (attn_frag_form: no mask, even nq, Tq a multiple of 128)
+            hipLaunchKernelGGL((k_attn_frag<HD, false, AQ_Q8_K>), ga, dim3(512), 0, s, a, nblk, qscale);
             return;
         }
     }
@@ -712,15 +754,19 @@ static void launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_
     else hipLaunchKernelGGL((k_attn_frag<HD, false>), ga, dim3(512), 0, s, a, nblk, qscale);
 }
 
-// true when launch_attn_hd takes the 8-wave fragment kernel, which can also store the output
-// quantized (AttnArgs::qo); otherwise the caller quantizes the fp32 output itself
-static bool attn_frag_form(const AttnArgs &a) {
+// true when launch_attn_hd takes the 8-wave fragment kernel with a store of the output
+// quantized for a weight of type q_type (AttnArgs::qo): Q8_0 at head_dim 32 / 64; Q8_K at
+// head_dim 128 when the workgroup's two heads make whole superblocks of complete query tiles
+// (even nq, Tq a multiple of 128, no mask).  Otherwise the caller quantizes the fp32 output.
+static bool attn_frag_form(const AttnArgs &a, int q_type) {
     const int nblk = (a.Tk + 31) / 32;
     const int64_t wgs = (int64_t)((a.nq + 1) / 2) * a.B * ((a.Tq + 127) / 128);
     bool split = (wgs < 128 && nblk >= 4) || (a.hd == 128 && a.mask);
     if (const char *e = getenv("MQ_ATTN_SPLIT"))
         if (*e) split = atoi(e) != 0;
-    return !split && a.hd <= 64;
+    if (split) return false;
+    if (q_type == MQ_TYPE_Q8_0) return a.hd <= 64;
+    return a.hd == 128 && a.nq % 2 == 0 && a.Tq % 128 == 0 && !a.mask;
 }
 
 hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
@@ -736,14 +782,18 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
     b.qo = nullptr;
     if (a.q_ws) {
         const int64_t rows = (int64_t)a.B * a.Tq, K = (int64_t)a.nq * a.hd;
-        const ActPlanes ap = act_planes(MQ_TYPE_Q8_0, rows, K, true);
+        if (a.q_type != MQ_TYPE_Q8_0 && a.q_type != MQ_TYPE_Q4_K && a.q_type != MQ_TYPE_Q6_K)
+            return hipErrorInvalidValue;
+        const ActPlanes ap = act_planes(a.q_type, rows, K, true);
         if (ap.kb_pad != K || a.o_st != K || a.o_sh != a.hd || a.o_sb != a.Tq * K || ((uintptr_t)a.q_ws & 255))
             return hipErrorInvalidValue;
-        if (attn_frag_form(a)) {
+        if (attn_frag_form(a, a.q_type)) {
             b.qo = (int8_t *)((uint8_t *)a.q_ws + ap.xq);
             b.qd = (float *)((uint8_t *)a.q_ws + ap.xd);
+            b.qmin = a.q_type == MQ_TYPE_Q8_0 ? nullptr : (_Float16 *)((uint8_t *)a.q_ws + ap.xmin);
             b.q_m_pad = ap.m_pad;
             b.q_kch = (int)(K / 32);
+            b.q_nsb = (int)(K / QK_K);
         } else {
             quant_after = true;  // the split-key form stores floats only
         }
@@ -758,7 +808,7 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const int64_t rows = (int64_t)a.B * a.Tq, K = (int64_t)a.nq * a.hd;
-        return launch_quantize_act_planar(MQ_TYPE_Q8_0, a.out, K, a.q_ws, rows, K, a.q_var, true, s);
+        return launch_quantize_act_planar(a.q_type, a.out, K, a.q_ws, rows, K, a.q_var, true, s);
     }
     return hipGetLastError();
 }
@@ -767,7 +817,7 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
 // heads, then nkv value heads, hd floats each) as strided operands.
 hipError_t launch_attn_frag(const float *qkv, int64_t ld, float *out, int64_t ldo, int B, int T, int nq, int nkv,
                             int hd, float scale, int causal, const float *qw, const float *kw, float eps,
-                            const float2 *cs, void *ws, hipStream_t s) {
+                            const float2 *cs, void *ws, hipStream_t s, void *q_ws, int q_type, bool q_only) {
     AttnArgs a;
     a.q = qkv;
     a.k = qkv + (int64_t)nq * hd;
@@ -779,6 +829,7 @@ hipError_t launch_attn_frag(const float *qkv, int64_t ld, float *out, int64_t ld
     a.o_sb = (int64_t)T * ldo, a.o_st = ldo, a.o_sh = hd;
     a.B = B, a.Tq = a.Tk = T, a.nq = nq, a.nkv = nkv, a.hd = hd;
     a.scale = scale, a.causal = causal, a.qw = qw, a.kw = kw, a.eps = eps, a.cs = cs, a.ws = ws;
+    a.q_ws = q_ws, a.q_type = q_type, a.q_only = q_only, a.q_var = mq_q8_0_variant();
     return launch_attn(a, s);
 }
 

@@ -34,7 +34,8 @@ size_t attn_workspace_bytes(int B, int T, int nkv, int hd);
 hipError_t launch_rope_table(float2 *cs, int T, int hd, float theta_base, hipStream_t s);
 hipError_t launch_attn_frag(const float *qkv, int64_t ld, float *out, int64_t ldo, int B, int T, int nq, int nkv,
                             int hd, float scale, int causal, const float *qw, const float *kw, float eps,
-                            const float2 *cs, void *ws, hipStream_t s);
+                            const float2 *cs, void *ws, hipStream_t s, void *q_ws = nullptr,
+                            int q_type = MQ_TYPE_Q8_0, bool q_only = false);
 hipError_t launch_last_rmsnorm_l2(const float *x, const float *w, float eps, float *out, int B, int T, int H,
                                   hipStream_t s);
 hipError_t launch_mean_pool_l2(const float *x, float *out, int B, int T, int H, hipStream_t s);  // mq_encoder.hip
@@ -195,6 +196,12 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
         }
         return hip_rc(launch_add_rmsnorm(m->y.f(), X, nullptr, nullptr, 0, w, eps, X, Hn, rows, (int)H, s), what);
     };
+    // K-quant o projections on the GEMM path read the attention rows as the attention stores
+    // them quantized (Q8_K; launch_attn quantizes its fp32 output itself where its kernel
+    // cannot); MQ_DECODER_ATTN_QPASS=1 keeps the separate quantizer
+    const bool att_q = (t == MQ_TYPE_Q4_K || t == MQ_TYPE_Q6_K) && qd % 256 == 0 && !m->layers.empty() &&
+                       mq_mul_mat_path(t, m->layers[0].o.n, qd, rows) == MQ_PATH_GEMM &&
+                       std::getenv("MQ_DECODER_ATTN_QPASS") == nullptr;
     // the gate|up GEMM forms silu(gate) * up in its store where the shape allows (not while
     // observed: the observer reads gate and up); MQ_DECODER_NO_GLU=1 keeps the two-step form
     const bool glu = !m->obs && !m->layers.empty() && gemm_swiglu_fits(rows, F) &&
@@ -207,10 +214,16 @@ extern "C" int mq_decoder_encode(mq_decoder *m, const int32_t *ids, int B, int T
         if ((rc = hip_rc(launch_attn_frag(m->qkv.f(), ldqkv, m->att.f(), qd, B, T, nq, nkv, hd,
                                           1.0f / sqrtf((float)hd), hp.causal, L.has_qn ? L.q_norm.f() : nullptr,
                                           L.has_kn ? L.k_norm.f() : nullptr, eps, (const float2 *)m->rope.p,
-                                          m->kvf.p, s),
+                                          m->kvf.p, s, att_q ? m->ws.p : nullptr, t, att_q && !m->obs),
                          "attention")))
             return rc;
-        if ((rc = mm(L.o, m->att.f(), qd, m->y.f(), "attn_out", (int)il))) return rc;
+        if (att_q) {  // the attention left its rows quantized in the workspace
+            if ((rc = observe("attn_out", (int)il, m->att.f(), qd, true))) return rc;
+            if ((rc = mq_mul_mat_q(t, L.o.img.p, L.o.n, L.o.k, m->ws.p, rows, m->y.f(), L.o.n, MQ_PATH_GEMM, s)))
+                return rc;
+        } else if ((rc = mm(L.o, m->att.f(), qd, m->y.f(), "attn_out", (int)il))) {
+            return rc;
+        }
         // X += A Wo^T; Hn = rms_norm(X) * ffn_norm
         if ((rc = add_norm(L.ffn_norm.f(), "attention residual", false))) return rc;
         const int dpath = mq_mul_mat_path(t, L.down.n, L.down.k, rows);

@@ -362,11 +362,13 @@ struct AttnArgs {
     const float2 *cs = nullptr;
     void *ws = nullptr;
     // q_ws not NULL: the output rows (B * Tq rows of K = nq * hd values; out must hold them as
-    // dense rows) also quantized to Q8_0 into the GEMM activation workspace q_ws, for the
-    // projection that reads them (rounding variant q_var; K a multiple of 128).  launch_attn
-    // fills qo, qd, q_m_pad and q_kch from it.
+    // dense rows) also quantized into the GEMM activation workspace q_ws of the projection that
+    // reads them, a weight of type q_type: Q8_0 (rounding variant q_var; K a multiple of 128),
+    // or Q8_K for a K-quant weight (K a multiple of 256).  launch_attn fills qo, qd, qmin,
+    // q_m_pad, q_kch and q_nsb from it.
     void *q_ws = nullptr;
     int q_var = 0;
+    int q_type = MQ_TYPE_Q8_0;
     // with q_ws: the 8-wave kernel stores only the quantized rows, not the floats in out (the
     // caller reads the result quantized only; the split-key form still writes out)
     bool q_only = false;
@@ -374,8 +376,9 @@ struct AttnArgs {
     bool kv_ready = false;
     int8_t *qo = nullptr;
     float *qd = nullptr;
+    _Float16 *qmin = nullptr;  // Q8_K: the min-term fragments
     int64_t q_m_pad = 0;
-    int q_kch = 0;
+    int q_kch = 0, q_nsb = 0;
 };
 size_t attn_workspace_bytes(int B, int Tk, int nkv, int hd);
 hipError_t launch_attn(const AttnArgs &a, hipStream_t s);

@@ -1,0 +1,84 @@
+// mq_q8k.h -- ggml's Q8_K row quantization (quantize_row_q8_K) of one 256-value superblock by
+// one wave, shared by the activation quantizers and the producers that store their output as
+// the Q8_K activation of the next mat-mul.  No contraction (the pragma below): the multiplies
+// and divisions round on their own, as the quantizers' ISO C restatement does.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mq_wave.h"
+
+namespace mq {
+
+// ggml's nearest_int: (f + 1.5*2^23) keeps round-half-even(f) in the low mantissa bits.
+__device__ __forceinline__ int nearest_int(float f) {
+#pragma clang fp contract(off)
+    const float v = f + 12582912.f;
+    return (__float_as_int(v) & 0x007fffff) - 0x00400000;
+}
+
+// DPP steps inside each 16-lane row (quad_perm [1,0,3,2] = xor 1, quad_perm [2,3,0,1] = xor 2,
+// row_half_mirror = i <-> 7-i within 8 lanes): after the three, every lane holds the
+// combination over its 8-lane group.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    return fmaxf(v, dpp_f<0x141>(v));
+}
+__device__ __forceinline__ int sum8(int v) {
+    v += dpp_i<0xB1>(v);
+    v += dpp_i<0x4E>(v);
+    return v + dpp_i<0x141>(v);
+}
+
+// One 256-value Q8_K block of row r of a 32-row tile, lane l of the wave holding values
+// 4l .. 4l + 3 (quantize_row_q8_K).  ggml's max: the FIRST value of largest magnitude -- per
+// lane, the first of its 4 values with the lane's largest |x|; then the lowest lane that holds
+// the wave's largest |x|.  The lane's 4 quants go to dst (its place in the fragment: LDS
+// staging or the workspace itself), the scale 1 / iscale to *dslot (lane 0), and B_j (the sum
+// of the 32 quants of sub-block j, split as B_j & 63 and 64 (B_j >> 6)) to the min-term
+// fragment msh of the tile.
+__device__ __forceinline__ void q8_K_block_row(const float4 v, int lane, int r, int8_t *dst, float *dslot,
+                                               _Float16 *msh) {
+#pragma clang fp contract(off)
+    const float vals[4] = {v.x, v.y, v.z, v.w};
+    float la = 0.0f, lm = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (fabsf(vals[i]) > la) {
+            la = fabsf(vals[i]);
+            lm = vals[i];
+        }
+    const float amax = wave_max_f(la);
+    uint32_t packed = 0;
+    int s16 = 0;
+    float dval = 0.0f;
+    if (amax != 0.0f) {
+        const unsigned long long hit = __ballot(la == amax);
+        const float mx = lane_f(lm, __ffsll((long long)hit) - 1);
+        const float iscale = -127.f / mx;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int qv = nearest_int(iscale * vals[i]);
+            qv = qv < 127 ? qv : 127;
+            packed |= (uint32_t)(qv & 0xff) << (8 * i);
+            s16 += qv;
+        }
+        dval = 1.0f / iscale;
+    }
+    *(uint32_t *)dst = packed;
+    if (lane == 0) *dslot = dval;
+    // B_j lands in lane 8j
+    const int B = sum8(s16);
+    if ((lane & 7) == 0) {
+        const int j = lane >> 3;
+        msh[(r << 3) + j] = (_Float16)(B & 63);
+        msh[((32 + r) << 3) + j] = (_Float16)((B >> 6) * 64);
+    }
+}
+
+}  // namespace mq

@@ -15,14 +15,10 @@
 #include "mq_internal.h"
 #include "mq_act.h"
 #include "mq_deq.h"
+#include "mq_q8k.h"
 
 namespace mq {
 
-// ggml's nearest_int: (f + 1.5*2^23) keeps round-half-even(f) in the low mantissa bits.
-__device__ __forceinline__ int nearest_int(float f) {
-    const float v = f + 12582912.f;
-    return (__float_as_int(v) & 0x007fffff) - 0x00400000;
-}
 
 template <bool VEC4>
 __device__ __forceinline__ float4 load4(const float *p) {
@@ -205,38 +201,6 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
 }
 
 
-// Cross-lane steps on the DPP path (no LDS round trip).  Each step combines a
-// lane with a partner inside its 16-lane row: quad_perm [1,0,3,2] (xor 1),
-// quad_perm [2,3,0,1] (xor 2), row_half_mirror (i <-> 7-i within 8 lanes),
-// row_mirror (i <-> 15-i).  After xor1, xor2, half_mirror every lane holds the
-// combination over its 8-lane group; after row_mirror, over its 16-lane row.
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
-}
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
-}
-__device__ __forceinline__ float max8(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));
-    v = fmaxf(v, dpp_f<0x4E>(v));
-    return fmaxf(v, dpp_f<0x141>(v));
-}
-__device__ __forceinline__ int sum8(int v) {
-    v += dpp_i<0xB1>(v);
-    v += dpp_i<0x4E>(v);
-    return v + dpp_i<0x141>(v);
-}
-__device__ __forceinline__ float readlane_f(float v, int l) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
-}
-// max over the whole wave, wave-uniform result
-__device__ __forceinline__ float wave_max(float v) {
-    v = max8(v);
-    v = fmaxf(v, dpp_f<0x140>(v));
-    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
-}
 
 // ---------------------------------------------------------------------------
 // Activations into the tiled GEMM layout (1 KB fragments: lane L of a fragment
@@ -255,50 +219,6 @@ __device__ __forceinline__ float wave_max(float v) {
 //   F16  (TQ_F16) : CB = 128 (64 values per row)
 // ---------------------------------------------------------------------------
 enum { TQ_Q8_0 = 0, TQ_Q8_K = 1, TQ_F16 = 2 };
-
-// One 256-value Q8_K block of row r of a 32-row tile, lane l of the wave holding values
-// 4l .. 4l + 3 (quantize_row_q8_K).  ggml's max: the FIRST value of largest magnitude -- per
-// lane, the first of its 4 values with the lane's largest |x|; then the lowest lane that holds
-// the wave's largest |x|.  The lane's 4 quants go to dst (its place in the staged fragment),
-// the scale 1 / iscale to *dslot (lane 0), and B_j (the sum of the 32 quants of sub-block j,
-// split as B_j & 63 and 64 (B_j >> 6)) to the min-term fragment msh of the tile.
-__device__ __forceinline__ void q8_K_block_row(const float4 v, int lane, int r, int8_t *dst, float *dslot,
-                                               _Float16 *msh) {
-    const float vals[4] = {v.x, v.y, v.z, v.w};
-    float la = 0.0f, lm = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-        if (fabsf(vals[i]) > la) {
-            la = fabsf(vals[i]);
-            lm = vals[i];
-        }
-    const float amax = wave_max(la);
-    uint32_t packed = 0;
-    int s16 = 0;
-    float dval = 0.0f;
-    if (amax != 0.0f) {
-        const unsigned long long hit = __ballot(la == amax);
-        const float mx = readlane_f(lm, __ffsll((long long)hit) - 1);
-        const float iscale = -127.f / mx;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            int qv = nearest_int(iscale * vals[i]);
-            qv = qv < 127 ? qv : 127;
-            packed |= (uint32_t)(qv & 0xff) << (8 * i);
-            s16 += qv;
-        }
-        dval = 1.0f / iscale;
-    }
-    *(uint32_t *)dst = packed;
-    if (lane == 0) *dslot = dval;
-    // B_j lands in lane 8j
-    const int B = sum8(s16);
-    if ((lane & 7) == 0) {
-        const int j = lane >> 3;
-        msh[(r << 3) + j] = (_Float16)(B & 63);
-        msh[((32 + r) << 3) + j] = (_Float16)((B >> 6) * 64);
-    }
-}
 
 template <int FMT, int VARIANT, bool VEC4>
 __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict__ x, int64_t ldx,
