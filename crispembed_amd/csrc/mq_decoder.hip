@@ -197,6 +197,16 @@ __global__ __launch_bounds__(256) void k_kv_frag(const AttnArgs a, int nblk) {
     }
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) const char lds_cchar;
+__device__ __forceinline__ uint32_t lds_addr32(const void *p) { return (uint32_t)(uintptr_t)(lds_cchar *)p; }
+// an LDS read the compiler does not track (the data comes from DMA the explicit waits order)
+__device__ __forceinline__ v8h ds_read_v8h(uint32_t a) {
+    v8h r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+
 // QO: the output also (or, with q_only, only) stored as the projection's quantized activation:
 // AQ_Q8_0 (Q8_0 blocks of 32 head dims), AQ_Q8_K (head_dim 128: the workgroup's two heads are
 // one 256-value Q8_K superblock of each output row; Tq a multiple of 128)
@@ -207,7 +217,10 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
     constexpr int NS = HD / 16, NT = HD / 32, HALF = HD / 2, NFR = kv_frags<HD>();
     constexpr float LOG2E = 1.4426950408889634f;
     __shared__ __attribute__((aligned(16))) float rs[8][32];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
+    extern __shared__ __attribute__((aligned(16))) char lds[];  // unmasked form: key/value ring, then staging
+    // wave-uniform (scalar registers): the wave's head, query tile and ranges
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
     const int h = blockIdx.x * 2 + (wave >> 2);
     const int b = blockIdx.y;
     const int Tq = a.Tq, Tk = a.Tk, causal = a.causal;
@@ -215,15 +228,22 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
     // (one long and one short causal range each); the longest ranges are dispatched first
     const int qt = wave < 4 ? wave : 7 - wave;
     const int q0 = ((int)gridDim.z - 1 - (int)blockIdx.z) * 128 + qt * 32;
-    if (h >= a.nq || q0 >= Tq) return;  // no workgroup barrier below, except for AQ_Q8_K (never taken there)
-    const int hk = h / (a.nq / a.nkv), qi = q0 + l32;
+    // The key/value blocks pass through an LDS ring shared by the workgroup in the unmasked
+    // head_dim 128 form (measured on MI355X: 97 against 110 us per Qwen3-0.6B layer of 16 x 512
+    // tokens; at head_dim 32, MiniLM's 128-token sequences, 10.2 against 9.6 us the other way).
+    // That form has workgroup barriers: a wave without queries (q0 >= Tq, or the missing
+    // second head of an odd nq) stays and computes nothing.  The others have none.
+    constexpr bool RING = !MASK && HD == 128;
+    const bool idle = h >= a.nq || q0 >= Tq;
+    if (!RING && idle) return;
+    const int hq = min(h, a.nq - 1), hk = hq / (a.nq / a.nkv), qi = q0 + l32;
     const int qrow = min(qi, Tq - 1);
     const float2 *cs = a.cs;
 
     // Q^T operand: step st holds Q[qi][16 st + 8 half + j], normed, rotated, times qscale
     v8h qh[NS], ql[NS];
     {
-        const float *qp = a.q + (int64_t)b * a.q_sb + (int64_t)qrow * a.q_st + (int64_t)h * a.q_sh + 8 * half;
+        const float *qp = a.q + (int64_t)b * a.q_sb + (int64_t)qrow * a.q_st + (int64_t)hq * a.q_sh + 8 * half;
         float x[NS][8];
 #pragma unroll
         for (int st = 0; st < NS; st++) {
@@ -272,63 +292,61 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
     for (int n = 0; n < NT; n++) oacc[n] = (v16f){};
     float m_run = -INFINITY, l_run = 0.f;
     const int kend = causal ? min(Tk, q0 + 32) : Tk;
-    const v8h *F = (const v8h *)((const _Float16 *)a.ws + (int64_t)(b * a.nkv + hk) * nblk * NFR * 512) + lane;
-
-    for (int kb = 0; kb * 32 < kend; kb++) {
-        // with a mask: a block that no query of the wave can see (a causal mask's upper
-        // triangle, padding) is skipped whole.  The values are read again after the MFMAs
-        // (cache hits) rather than kept live across them: at 2 waves per SIMD the 16 extra
-        // registers spill.
-        if constexpr (MASK) {
-            bool live = false;
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
-                live |= key < Tk && (float)mrow[key] != -INFINITY;
-            }
-            if (__ballot(live) == 0) continue;
-        }
-        const v8h *Fb = F + (int64_t)kb * NFR * 64;
+    // One key block kb: S^T = K Q^T, the online softmax, O += P V.  load(fr, f0) fills fr with
+    // the block's fragments f0 .. f0 + NFR/2 - 1 (K: hi, lo per 16-deep step; V from 2 NS: hi,
+    // lo per (step, column tile)), complete on return.
+    auto block = [&](int kb, auto &&load) __attribute__((always_inline)) {
         // three accumulators, so consecutive MFMAs never chain on one accumulator
         v16f s_hh = (v16f){}, s_hl = (v16f){}, s_lh = (v16f){};
+        v8h fr[NFR / 2];
+        load(fr, 0);  // K: hi, lo of each 16-deep step
 #pragma unroll
         for (int st = 0; st < NS; st++) {
-            const v8h ah = Fb[(2 * st) * 64], al = Fb[(2 * st + 1) * 64];
+            const v8h ah = fr[2 * st], al = fr[2 * st + 1];
             s_hh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[st], s_hh, 0, 0, 0);
             s_hl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ql[st], s_hl, 0, 0, 0);
             s_lh = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[st], s_lh, 0, 0, 0);
         }
-        v8h bh[2][NT], bl[2][NT];
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int n = 0; n < NT; n++) {
-                bh[t][n] = Fb[(2 * NS + 2 * (t * NT + n)) * 64];
-                bl[t][n] = Fb[(2 * NS + 2 * (t * NT + n) + 1) * 64];
-            }
+        load(fr, 2 * NS);  // V: hi, lo of each (step t, column tile n)
         const v16f sc = s_hh + (s_hl + s_lh);
         float p[16], mblk = -INFINITY;
+        // a block inside every query's range (below the causal diagonal of the wave's first
+        // query, before Tk, no mask) needs no per-key test (a wave-uniform branch)
+        const bool full = !MASK && kb * 32 + 32 <= Tk && (!causal || kb * 32 + 31 <= q0);
+        if (full) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
-            if (key >= Tk || (causal && key > qi)) {
-                p[i] = -INFINITY;
-            } else {
+            for (int i = 0; i < 16; i++) {
                 p[i] = sc[i];
-                if constexpr (MASK) p[i] += LOG2E * (float)mrow[key];
+                mblk = fmaxf(mblk, p[i]);
             }
-            mblk = fmaxf(mblk, p[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
+                if (key >= Tk || (causal && key > qi)) {
+                    p[i] = -INFINITY;
+                } else {
+                    p[i] = sc[i];
+                    if constexpr (MASK) p[i] += LOG2E * (float)mrow[key];
+                }
+                mblk = fmaxf(mblk, p[i]);
+            }
         }
         mblk = fmaxf(mblk, __shfl_xor(mblk, 32));
         const float m_new = fmaxf(m_run, mblk);
         // -inf while every key so far is masked: then alpha and p are 0 (without a mask key
         // 32 kb <= every query of the wave keeps m_new finite)
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = exp2f(m_run - m_use);  // 0 on the first block
+        // 2^x by v_exp_f32 itself: the arguments are <= 0 and results below 2^-126 (flushed by
+        // the instruction, which exp2f's denormal path would keep) are nothing beside the
+        // block's largest probability, 1.  P carries a factor 2^15 (folded into the exponent)
+        // so that its hi / lo fp16 split is exact.
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);  // 0 on the first block
+        const float m_off = m_use - 15.0f;
         float lblk = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            p[i] = exp2f(p[i] - m_use);
+            p[i] = __builtin_amdgcn_exp2f(p[i] - m_off);
             lblk += p[i];
         }
         lblk += __shfl_xor(lblk, 32);
@@ -336,13 +354,21 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
         m_run = m_new;
 
         if (__ballot(alpha != 1.0f)) {
-            // rescale O's rows (queries 8(r/4) + 4 half + r%4) by their query's alpha
+            // rescale O's rows (queries 8(r/4) + 4 half + r%4) by their query's alpha.  The
+            // reads are asm: the compiler would make a plain LDS read wait for the key/value
+            // DMA in flight (it cannot tell rs from the ring)
             rs[wave][l32] = alpha;
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // one wave writes and reads its slot
+            const uint32_t ra = lds_addr32(&rs[wave][4 * half]);
+            v8h t4[4];
+#pragma unroll
+            for (int g = 0; g < 4; g++) t4[g] = ds_read_v8h(ra + 32u * g);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             float al[16];
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                const float4 t = *(const float4 *)&rs[wave][8 * g + 4 * half];
+                asm volatile("" : "+v"(t4[g]));
+                const float4 t = __builtin_bit_cast(float4, t4[g]);
                 al[4 * g] = t.x, al[4 * g + 1] = t.y, al[4 * g + 2] = t.z, al[4 * g + 3] = t.w;
             }
 #pragma unroll
@@ -355,20 +381,85 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
         for (int t = 0; t < 2; t++) {
             float px[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) px[j] = p[8 * t + j] * 32768.0f;
+            for (int j = 0; j < 8; j++) px[j] = p[8 * t + j];
             v8h ph, pl;
             split8(px, ph, pl);
             // term-major order: consecutive MFMAs write different accumulators
 #pragma unroll
-            for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, bh[t][n], oacc[n], 0, 0, 0);
+            for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, fr[2 * (t * NT + n)], oacc[n], 0, 0, 0);
 #pragma unroll
-            for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, bl[t][n], oacc[n], 0, 0, 0);
+            for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, fr[2 * (t * NT + n) + 1], oacc[n], 0, 0, 0);
 #pragma unroll
-            for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl, bh[t][n], oacc[n], 0, 0, 0);
+            for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl, fr[2 * (t * NT + n)], oacc[n], 0, 0, 0);
         }
+    };
+    if constexpr (!RING) {
+        const v8h *F = (const v8h *)((const _Float16 *)a.ws + (int64_t)(b * a.nkv + hk) * nblk * NFR * 512) + lane;
+        for (int kb = 0; kb * 32 < kend; kb++) {
+            if constexpr (MASK) {
+                // a block that no query of the wave can see (a causal mask's upper triangle,
+                // padding) is skipped whole.  The values are read again after the MFMAs (cache
+                // hits) rather than kept live across them: at 2 waves per SIMD the 16 extra
+                // registers spill.
+                bool live = false;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
+                    live |= key < Tk && (float)mrow[key] != -INFINITY;
+                }
+                if (__ballot(live) == 0) continue;
+            }
+            const v8h *Fb = F + (int64_t)kb * NFR * 64;
+            block(kb, [&](v8h(&fr)[NFR / 2], int f0) __attribute__((always_inline)) {
+#pragma unroll
+                for (int i = 0; i < NFR / 2; i++) fr[i] = Fb[(int64_t)(f0 + i) * 64];
+            });
+        }
+    } else {
+        // The workgroup's key blocks pass through a two-slot LDS ring: all 8 waves DMA block
+        // kb + 1 (global_load_lds, 1 KB fragments; both heads' key/value heads, one copy when
+        // they share it) while computing block kb from the other slot, one barrier per block.
+        // Every wave walks the workgroup's whole key range (the longest causal range of its
+        // query tiles) and computes only its own; an idle wave only moves data.
+        const int gq = a.nq / a.nkv;
+        const int hk0 = min(2 * (int)blockIdx.x, a.nq - 1) / gq, hk1 = min(2 * (int)blockIdx.x + 1, a.nq - 1) / gq;
+        const int nfr = hk0 == hk1 ? NFR : 2 * NFR;  // fragments per block in a slot
+        const int qbase = ((int)gridDim.z - 1 - (int)blockIdx.z) * 128;
+        const int nkb = ((causal ? min(Tk, qbase + 128) : Tk) + 31) / 32;
+        const _Float16 *G0 = (const _Float16 *)a.ws + (int64_t)(b * a.nkv + hk0) * nblk * NFR * 512 + lane * 8;
+        const _Float16 *G1 = (const _Float16 *)a.ws + (int64_t)(b * a.nkv + hk1) * nblk * NFR * 512 + lane * 8;
+        const uint32_t ring = lds_addr32(lds);
+        const uint32_t mine = (hk == hk0 ? 0u : (uint32_t)NFR * 1024u) + (uint32_t)lane * 16u;
+        auto issue = [&](int kb) __attribute__((always_inline)) {
+            char *slot = lds + (kb & 1) * (2 * NFR * 1024);
+            for (int f = wave; f < nfr; f += 8) {
+                const _Float16 *src = f < NFR ? G0 + (int64_t)(kb * NFR + f) * 512 : G1 + (int64_t)(kb * NFR + f - NFR) * 512;
+                __builtin_amdgcn_global_load_lds(src, (lds_void *)(slot + f * 1024), 16, 0, 0);
+            }
+        };
+        issue(0);
+        for (int kb = 0; kb < nkb; kb++) {
+            // block kb has landed (this wave's DMAs; the barrier: every wave's), and every wave
+            // is done reading the slot the next DMAs overwrite (block kb - 1)
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (kb + 1 < nkb) issue(kb + 1);
+            if (idle || kb * 32 >= kend) continue;
+            const uint32_t base = ring + (uint32_t)(kb & 1) * (2 * NFR * 1024) + mine;
+            block(kb, [&](v8h(&fr)[NFR / 2], int f0) __attribute__((always_inline)) {
+#pragma unroll
+                for (int i = 0; i < NFR / 2; i++) fr[i] = ds_read_v8h(base + (uint32_t)(f0 + i) * 1024u);
+                // the asm reads complete here; each fragment is tied to the wait
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int i = 0; i < NFR / 2; i++) asm volatile("" : "+v"(fr[i]));
+            });
+        }
+        // the LDS ring is free for the epilogue's staging
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
 
-    rs[wave][l32] = l_run > 0.f ? 1.0f / (l_run * 32768.0f) : 0.f;  // O accumulated 2^15 P V
+    rs[wave][l32] = l_run > 0.f ? 1.0f / l_run : 0.f;  // O and l both carry the factor 2^15
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     float inv[16];
 #pragma unroll
@@ -376,8 +467,8 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
         const float4 t = *(const float4 *)&rs[wave][8 * g + 4 * half];
         inv[4 * g] = t.x, inv[4 * g + 1] = t.y, inv[4 * g + 2] = t.z, inv[4 * g + 3] = t.w;
     }
-    float *ob = a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + l32;
-    if (QO == AQ_NONE || !a.q_only) {
+    float *ob = a.out + (int64_t)b * a.o_sb + (int64_t)hq * a.o_sh + l32;
+    if (!idle && (QO == AQ_NONE || !a.q_only)) {
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int q = q0 + 8 * (r / 4) + 4 * half + (r % 4);
@@ -412,7 +503,7 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
             }
             uint4 pk;
             const float d = requant_q8_0(v, true, MQ_PRE_NONE, a.q_var, pk);
-            if (q < Tq) {
+            if (q < Tq && !idle) {
                 const int64_t chunk = (int64_t)h * NT + n;
                 *(uint4 *)(a.qo + (((row >> 5) * a.q_kch + chunk) << 10) + (((row & 31) + 32 * half) << 4)) = pk;
                 if (half == 0) a.qd[chunk * a.q_m_pad + row] = d;
@@ -431,9 +522,8 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
         // wave of the workgroup reaches the barrier: the host launches this form only for an even
         // nq and Tq a multiple of 128.
         static_assert(HD == 128, "a superblock is two heads of 128");
-        constexpr int SST = 260;  // staging row stride in floats
-        __shared__ __attribute__((aligned(16))) float sstg[4][32 * SST];
-        float *tile = sstg[qt];
+        constexpr int SST = 260;  // staging row stride in floats (the LDS ring's space, free now)
+        float *tile = (float *)lds + qt * (32 * SST);
         const int hs = wave >> 2;
 #pragma unroll
         for (int n = 0; n < NT; n++)
@@ -719,6 +809,22 @@ hipError_t launch_rope_table(float2 *cs, int T, int hd, float theta_base, hipStr
     return hipGetLastError();
 }
 
+// The unmasked 8-wave kernel with its dynamic LDS: at head_dim 128 the two-slot key/value ring
+// (two heads' fragments per slot), or the Q8_K store's staging where that is larger.
+template <int HD, int QO>
+static void launch_attn_8w(dim3 grid, const AttnArgs &a, int nblk, float qscale, hipStream_t s) {
+    constexpr int RING = HD == 128 ? 2 * 2 * kv_frags<HD>() * 1024 : 0, STG = QO == AQ_Q8_K ? 4 * 32 * 260 * 4 : 0;
+    constexpr int BYTES = RING > STG ? RING : STG;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void *)k_attn_frag<HD, false, QO>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                BYTES) != hipSuccess)
+            return;  // the launch below reports the error
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((k_attn_frag<HD, false, QO>), grid, dim3(512), BYTES, s, a, nblk, qscale);
+}
+
 template <int HD>
 static void launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_t s) {
     const dim3 gk((unsigned)nblk, (unsigned)a.nkv, (unsigned)a.B);
@@ -741,17 +847,17 @@ static void launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_
     if constexpr (HD <= 64) {
         if (a.qo) {  // quantized output: the unmasked / masked forms with the Q8_0 store
             if (a.mask) hipLaunchKernelGGL((k_attn_frag<HD, true, AQ_Q8_0>), ga, dim3(512), 0, s, a, nblk, qscale);
-            else hipLaunchKernelGGL((k_attn_frag<HD, false, AQ_Q8_0>), ga, dim3(512), 0, s, a, nblk, qscale);
+            else launch_attn_8w<HD, AQ_Q8_0>(ga, a, nblk, qscale, s);
             return;
         }
     } else {
         if (a.qo) {  // the Q8_K store (attn_frag_form: no mask, even nq, Tq a multiple of 128)
-            hipLaunchKernelGGL((k_attn_frag<HD, false, AQ_Q8_K>), ga, dim3(512), 0, s, a, nblk, qscale);
+            launch_attn_8w<HD, AQ_Q8_K>(ga, a, nblk, qscale, s);
             return;
         }
     }
     if (a.mask) hipLaunchKernelGGL((k_attn_frag<HD, true>), ga, dim3(512), 0, s, a, nblk, qscale);
-    else hipLaunchKernelGGL((k_attn_frag<HD, false>), ga, dim3(512), 0, s, a, nblk, qscale);
+    else launch_attn_8w<HD, AQ_NONE>(ga, a, nblk, qscale, s);
 }
 
 // true when launch_attn_hd takes the 8-wave fragment kernel with a store of the output

@@ -64,12 +64,20 @@ def _attn_ref(x, B, T, nq, nkv, hd, scale, causal):
     return np.einsum("bhij,bhjd->bihd", p, v).reshape(B * T, nq * hd)
 
 
+@pytest.mark.parametrize("form", ["auto", "frag"])
 @pytest.mark.parametrize("causal", [1, 0])
 @pytest.mark.parametrize("hd,nq,nkv", [(64, 4, 2), (128, 2, 1), (128, 16, 8), (64, 3, 3), (128, 6, 2)])
 @pytest.mark.parametrize("B,T", [(1, 1), (2, 37), (2, 200), (1, 300)])
-def test_attention(causal, hd, nq, nkv, B, T):
+def test_attention(causal, hd, nq, nkv, B, T, form, monkeypatch):
+    """The runner's attention against an fp64 reference.  form "frag" forces the 8-wave kernel
+    (its key/value blocks shared through LDS by both heads of a workgroup: an odd nq leaves a
+    workgroup's second head empty, nq / nkv = 3 gives workgroups whose two heads read different
+    key/value heads, and ragged T leaves query tiles empty); "auto" lets small grids take the
+    split-key kernel."""
     from crispembed_amd import mq
     import torch
+    if form == "frag":
+        monkeypatch.setenv("MQ_ATTN_SPLIT", "0")
     x, ld = _qkv(B, T, nq, nkv, hd, 7 * T + hd + nq + causal)
     x *= 2.0  # sharper softmax
     scale = 1.0 / np.sqrt(hd)
