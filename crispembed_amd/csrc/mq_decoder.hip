@@ -148,14 +148,35 @@ __global__ __launch_bounds__(256) void k_kv_frag(const AttnArgs a, int nblk) {
     const float2 *cs = a.cs;
     const bool on = lane < HALF;
     // K rows of the block, normed and rotated (NEOX pair (i, i + HD/2) in one lane), to LDS;
-    // rows past Tk are zero
-    for (int r = wave; r < 32; r += 4) {
-        const int key = kb * 32 + r;
+    // rows past Tk are zero.  The wave's 8 rows are loaded first, all in flight at once.
+    float k0[8], k1[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int key = kb * 32 + wave + 4 * i;
+        const float *x = kp + (int64_t)key * a.k_st;
+        k0[i] = (key < a.Tk && on) ? x[lane] : 0.f;
+        k1[i] = (key < a.Tk && on) ? x[lane + HALF] : 0.f;
+    }
+    // and the V values of this wave's fragments (t, n): 2 NT of them, NT / 2 per wave (head_dim 32:
+    // one, waves 2 and 3 idle)
+    constexpr int VPW = (2 * NT + 3) / 4;
+    float vx[VPW][8];
+#pragma unroll
+    for (int u = 0; u < VPW; u++) {
+        const int f = wave + 4 * u, t = f / NT, n = f % NT;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int key = kb * 32 + 16 * t + 8 * (j / 4) + 4 * half + j % 4;
+            vx[u][j] = (f < 2 * NT && key < a.Tk) ? vp[(int64_t)key * a.v_st + 32 * n + l32] : 0.f;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int r = wave + 4 * i, key = kb * 32 + r;
         float x0 = 0.f, x1 = 0.f;
         if (key < a.Tk) {
-            const float *x = kp + (int64_t)key * a.k_st;
-            x0 = on ? x[lane] : 0.f;
-            x1 = on ? x[lane + HALF] : 0.f;
+            x0 = k0[i];
+            x1 = k1[i];
             if (kw) {
                 const float scale = 1.0f / sqrtf(wave_sum_f(x0 * x0 + x1 * x1) / (float)HD + a.eps);
                 if (on) {
@@ -182,16 +203,12 @@ __global__ __launch_bounds__(256) void k_kv_frag(const AttnArgs a, int nblk) {
         *(v8h *)(F + (2 * st) * 512) = h;
         *(v8h *)(F + (2 * st + 1) * 512) = l;
     }
-    for (int f = wave; f < 2 * NT; f += 4) {
-        const int t = f / NT, n = f % NT;
-        float x[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int key = kb * 32 + 16 * t + 8 * (j / 4) + 4 * half + j % 4;
-            x[j] = key < a.Tk ? vp[(int64_t)key * a.v_st + 32 * n + l32] : 0.f;
-        }
+    for (int u = 0; u < VPW; u++) {
+        const int f = wave + 4 * u;
+        if (f >= 2 * NT) continue;
         v8h h, l;
-        split8(x, h, l);
+        split8(vx[u], h, l);
         *(v8h *)(F + (2 * NS + 2 * f) * 512) = h;
         *(v8h *)(F + (2 * NS + 2 * f + 1) * 512) = l;
     }
