@@ -105,14 +105,15 @@ struct GemmArgs {
     } grp[GEMM_GROUPS - 1];
 };
 
-constexpr int NBUF = 4;   // stage ring in LDS
-constexpr int DIST = 3;   // stages in flight ahead of the newest one being computed
-static_assert(DIST + 1 <= NBUF, "stage ring: DIST stages in flight plus the one being computed");
 
 // WM x WN waves per workgroup, each wave TM x TN MFMA tiles of 32x32; stages of KC 32-byte
-// K chunks (64 bytes by default; 32 halves the ring so two workgroups share a CU).
-template <int FMT, int WM, int WN, int TM, int TN, int KCT = 2>
+// K chunks (64 bytes by default; 32 halves the ring so two workgroups share a CU); a ring of NB
+// stages in LDS with D of them in flight ahead of the one being computed (4 and 3 by default;
+// a shorter ring leaves room for more workgroups per CU).
+template <int FMT, int WM, int WN, int TM, int TN, int KCT = 2, int NBT = 4, int DT = 3>
 struct Cfg {
+    static constexpr int NB = NBT, D = DT;
+    static_assert(D + 1 <= NB, "stage ring: D stages in flight plus the one being computed");
     static constexpr int KC = KCT;              // 32-byte K chunks per stage
     static constexpr int SPB = 256 / (32 * KC);  // stages per 256-value superblock
     static constexpr int NW = WM * WN, NT = 64 * NW, BM = 32 * TM * WM, BN = 32 * TN * WN;
@@ -136,9 +137,13 @@ struct Cfg {
     static constexpr int EP = EP_DX + EP_DW + EP_DMIN + EP_AMIN + EP_BMIN;
     static constexpr int NEPI = (FMT == FMT_Q4_K) ? 3 + BM / 32 + BN / 32 : (limbs ? 2 : 0);
     static constexpr int EPW = (NEPI + NW - 1) / NW;
-    static constexpr int LDS = NBUF * STAGE + 2 * EP;
+    static constexpr int LDS_RING = NB * STAGE + 2 * EP;
+    // the quantized-output and K-fragment epilogues stage a 32 x 36-float tile per wave in the
+    // same memory once the ring is drained
+    static constexpr int LDS_STG = NW * 32 * 36 * 4;
+    static constexpr int LDS = LDS_RING > LDS_STG ? LDS_RING : LDS_STG;
     // DMAs issued per stage by every wave, and the count still in flight when stage
-    // position q (of a superblock) may be computed: those of the DIST-1 later stages.
+    // position q (of a superblock) may be computed: those of the D-1 later stages.
     static constexpr int dmas(int stage_pos) { return IPW + ((limbs && stage_pos % SPB == 0) ? EPW : 0); }
     template <int D>
     static constexpr int waits(int q) {
@@ -298,9 +303,10 @@ __device__ __forceinline__ DmaItem epi_item(const GemmArgs &a, int e, int sb, in
 // GLU: a.N = 2 n_ff columns of a gate|up weight; y receives silu(gate) * up, n_ff columns (the
 // gated FFN's down-projection input, src/decoder_embed.cpp:793-802), and no gate or up value
 // is stored.
-template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2, bool GLU = false>
+template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2, bool GLU = false, int NBT = 4, int DT = 3>
 __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) {
-    using C = Cfg<FMT, WM, WN, TM, TN, KCT>;
+    using C = Cfg<FMT, WM, WN, TM, TN, KCT, NBT, DT>;
+    constexpr int NBUF = C::NB, DIST = C::D;
     static_assert(!GLU || TN == 2, "GLU: each wave holds a gate and an up column tile");
     constexpr int KC = C::KC, SPB = C::SPB;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
@@ -716,12 +722,12 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
         }
 }
 
-template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2, bool GLU = false>
+template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2, bool GLU = false, int NBT = 4, int DT = 3>
 static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
-    using C = Cfg<FMT, WM, WN, TM, TN, KCT>;
+    using C = Cfg<FMT, WM, WN, TM, TN, KCT, NBT, DT>;
     static bool attr_set = false;
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm<FMT, WM, WN, TM, TN, MINB, KCT, GLU>,
+        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm<FMT, WM, WN, TM, TN, MINB, KCT, GLU, NBT, DT>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
         if (e != hipSuccess) return e;
         attr_set = true;
@@ -735,7 +741,7 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
     a.group_m = 8;
     a.nstages = a.kch / KCT;  // kb_pad is a multiple of 128 bytes
     const unsigned grid = (unsigned)(a.tiles_m * a.tiles_n);
-    hipLaunchKernelGGL((k_gemm<FMT, WM, WN, TM, TN, MINB, KCT, GLU>), dim3(grid), dim3(C::NT), C::LDS, s, a);
+    hipLaunchKernelGGL((k_gemm<FMT, WM, WN, TM, TN, MINB, KCT, GLU, NBT, DT>), dim3(grid), dim3(C::NT), C::LDS, s, a);
     return hipGetLastError();
 }
 
@@ -747,6 +753,8 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
 //   6: 4 waves x (64x64)  WG 128x128, 32-byte K stages: 70 KB of LDS, two workgroups per CU
 //      (K-quants)
 //   7: 4 waves x (32x32)  WG 64x64
+//   8: as 7 with a 2-stage ring (one stage in flight): half the LDS, more workgroups per CU
+//   9: as 7 with a 3-stage ring (two in flight; Q8_0 and F16)
 static int gemm_cfg_env() {
     const char *e = getenv("MQ_GEMM_CFG");  // read per launch so a process can compare configurations
     return (e && *e) ? atoi(e) : 0;
@@ -757,16 +765,19 @@ static inline int64_t tiles(int64_t M, int64_t N, int bm, int bn) { return ((M +
 template <int FMT>
 static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
     int cfg = gemm_cfg_env();
-    if (cfg < 1 || cfg > 7 || cfg == 2 || (cfg == 6 && FMT != FMT_Q4_K && FMT != FMT_Q6_K)) {
+    if (cfg < 1 || cfg > 9 || cfg == 2 || (cfg == 6 && FMT != FMT_Q4_K && FMT != FMT_Q6_K) ||
+        (cfg == 9 && FMT != FMT_Q8_0 && FMT != FMT_F16)) {
         // Small grids (under 512 tiles of 128x128): 64x64 workgroups of four 32x32 waves.
         // Every 32-deep K chunk costs a wave VALU work per output of its tile (the block
         // scales), so smaller wave tiles shorten the serial chain each wave walks; with few
         // output tiles that chain, not operand reuse, sets the time (MI355X, Q8_0 4096x384x1536
-        // 32 -> 17 us, Q4_K 512x1024x3072 37 -> 16 us).  Larger grids: 256x128 tiles when that
-        // still gives every CU (256) a workgroup, else 128x128.
+        // 32 -> 17 us, Q4_K 512x1024x3072 37 -> 16 us).  For Q8_0 with a 2-stage ring: half the
+        // LDS, twice the workgroups per CU (17.9 -> 16.2 us at 4096x1536x384; the K-quants and
+        // F16 measured slower with it at 512 rows).  Larger grids: 256x128 tiles when that still
+        // gives every CU (256) a workgroup, else 128x128.
         int64_t n_all = a.N;
         for (int g = 1; g < a.ngroups; g++) n_all += a.grp[g - 1].N;
-        if (tiles(a.M, n_all, 128, 128) < 512) cfg = 7;
+        if (tiles(a.M, n_all, 128, 128) < 512) cfg = FMT == FMT_Q8_0 ? 8 : 7;
         else cfg = (tiles(a.M, n_all, 256, 128) >= 256) ? 1 : 3;
     }
     switch (cfg) {
@@ -778,6 +789,10 @@ static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
             return hipErrorInvalidValue;
 
         case 7: return launch_cfg<FMT, 2, 2, 1, 1, 2>(a, s);
+        case 8: return launch_cfg<FMT, 2, 2, 1, 1, 2, 2, false, 2, 1>(a, s);
+        case 9:
+            if constexpr (FMT == FMT_Q8_0 || FMT == FMT_F16) return launch_cfg<FMT, 2, 2, 1, 1, 2, 2, false, 3, 2>(a, s);
+            return hipErrorInvalidValue;
         default: return launch_cfg<FMT, 1, 1, 2, 2, 2>(a, s);
     }
 }
