@@ -958,6 +958,12 @@ enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node) {
     }
 }
 
+// true when the bytes of tensor a and tensor b overlap
+bool overlaps(const ggml_tensor *a, const ggml_tensor *b) {
+    const char *a0 = (const char *)a->data, *b0 = (const char *)b->data;
+    return a0 && b0 && a0 < b0 + ggml_nbytes(b) && b0 < a0 + ggml_nbytes(a);
+}
+
 enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
     const int n = ggml_graph_n_nodes(cg);
     const bool fuse = std::getenv("MQ_GGML_NO_FUSION") == nullptr;
@@ -969,8 +975,12 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
         if (done[i] || ggml_is_empty(node) || is_view_op(node->op)) continue;
         enum ggml_status st = GGML_STATUS_SUCCESS;
         int used = 0;
-        // a quantized activation stays reusable only from one mat-mul to the next
-        if (node->op != GGML_OP_MUL_MAT || !fuse) c->ws_x = nullptr;
+        // The workspace's quantized activation (ws_x) stays reusable across nodes that neither use
+        // the workspace nor write ws_x's bytes: the q, k and v products of one normed activation,
+        // or its gate and up products, quantize it once although elementwise nodes run between
+        // them.  The nodes that use the workspace drop or replace it themselves.
+        if (!fuse) c->ws_x = nullptr;
+        const ggml_tensor *ws_before = c->ws_x;
         if (fuse) {
             switch (node->op) {
                 case GGML_OP_MUL_MAT:
@@ -993,6 +1003,14 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
             used = 1;
         }
         if (st != GGML_STATUS_SUCCESS) return st;
+        if (c->ws_x && c->ws_x == ws_before)
+            for (int j = i; j < i + used; j++) {
+                const ggml_tensor *t = ggml_graph_node(cg, j);
+                if (!is_view_op(t->op) && overlaps(t, c->ws_x)) {
+                    c->ws_x = nullptr;
+                    break;
+                }
+            }
         i += used - 1;
     }
     c->ws_x = nullptr;
