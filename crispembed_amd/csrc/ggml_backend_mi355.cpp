@@ -681,6 +681,63 @@ int try_fuse_ffn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status 
     return dst == mm2 ? 4 : 5;
 }
 
+// UNARY(SILU)(gate) -> MUL_MAT(w_up, x) -> MUL(silu, up) -> MUL_MAT(w_down, product), the gated FFN
+// of src/decoder_embed.cpp:793-802 with separate gate and up weights: the up projection runs as
+// usual, then the down projection's activation is silu(gate) * up formed by its quantizer
+// (mq_quantize_act_silu_mul), or for a decode-sized K-quant down projection inside its GEMV
+// (mq_mul_mat_gemv, MQ_PRE_SILU_MUL).  Neither the SiLU's nor the product's tensor is written:
+// both have no other reader, and the down projection must not be the graph's last node (an
+// observer reads its src1).
+enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node);
+
+int try_fuse_silu_mul(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status &st) {
+    ggml_tensor *silu = ggml_graph_node(cg, i);
+    if (ggml_get_unary_op(silu) != GGML_UNARY_OP_SILU || i + 3 >= n) return 0;
+    ggml_tensor *up = ggml_graph_node(cg, i + 1), *mul = ggml_graph_node(cg, i + 2), *down = ggml_graph_node(cg, i + 3);
+    if (up->op != GGML_OP_MUL_MAT || mul->op != GGML_OP_MUL || down->op != GGML_OP_MUL_MAT || down->src[1] != mul) return 0;
+    if (!((mul->src[0] == silu && mul->src[1] == up) || (mul->src[0] == up && mul->src[1] == silu))) return 0;
+    if (!feeds_only_next(cg, i) || ggml_node_get_use_count(cg, i + 1) != 1 || (up->flags & GGML_TENSOR_FLAG_OUTPUT) ||
+        !feeds_only_next(cg, i + 2) || last_compute_node(cg, i + 3, n))
+        return 0;
+    const ggml_tensor *gate = silu->src[0];
+    for (const ggml_tensor *t : {gate, (const ggml_tensor *)up, (const ggml_tensor *)silu, (const ggml_tensor *)mul})
+        if (t->type != GGML_TYPE_F32 || !same_shape(t, gate) || t->nb[0] != sizeof(float) || !rows_flat(t)) return 0;
+    if (gate->nb[1] != up->nb[1] || gate->nb[1] % sizeof(float) != 0 || !flat_mul_mat(up) || !flat_mul_mat(down)) return 0;
+    const ggml_tensor *wd = down->src[0];
+    const int mt = mq_type_of(wd->type);
+    const int64_t K = wd->ne[0], N = wd->ne[1], M = mul->ne[1] * mul->ne[2] * mul->ne[3], ld = (int64_t)(gate->nb[1] / 4);
+    if (mul->ne[0] != K || !mq_supports(mt, K)) return 0;
+    const int path = mq_mul_mat_path(mt, N, K, M);
+    const bool gemv = path == MQ_PATH_GEMV && (mt == MQ_TYPE_Q4_K || mt == MQ_TYPE_Q6_K) && M <= 8 && K <= 6144 &&
+                      !c->capturing && ((uintptr_t)gate->data & 15) == 0 && ((uintptr_t)up->data & 15) == 0 && ld % 4 == 0;
+    st = compute_node(c, up);
+    if (st != GGML_STATUS_SUCCESS) return 4;
+    int rc;
+    if (gemv) {
+        const void *wi[1] = {wd->data};
+        const int64_t nn[1] = {N}, ldy[1] = {(int64_t)(down->nb[1] / 4)};
+        float *yy[1] = {(float *)down->data};
+        const float *bb[1] = {nullptr};
+        rc = mq_mul_mat_gemv(mt, 1, wi, nn, K, (const float *)gate->data, ld, (const float *)up->data, ld,
+                             MQ_PRE_SILU_MUL, M, yy, ldy, bb, c->stream);
+    } else {
+        c->ws_x = nullptr;  // the workspace receives the product
+        if (!ensure_ws(c, mq_workspace_bytes(mt, M, K))) {
+            st = GGML_STATUS_ALLOC_FAILED;
+            return 4;
+        }
+        rc = mq_quantize_act_silu_mul(mt, (const float *)gate->data, (const float *)up->data, ld, M, K, c->ws,
+                                      c->ws_bytes, path, c->stream);
+        if (rc == 0) {
+            c->ws_x = mul, c->ws_type = mt, c->ws_m = M, c->ws_k = K, c->ws_path = path;
+            st = mul_mat_flat(c, wd, mul, down, nullptr, down);
+            return 4;
+        }
+    }
+    st = op_status(rc, down);
+    return 4;
+}
+
 // FLASH_ATTN_EXT whose result (after view nodes, as rows of n_head * head_dim) is read by a
 // Q8_0 MUL_MAT on the GEMM path (the output projection): the attention also leaves it quantized
 // for that MUL_MAT (mq_op_flash_attn_q8_0) and the activation cache lets the MUL_MAT skip the
@@ -991,6 +1048,7 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
                 case GGML_OP_RMS_NORM: used = try_fuse_norm(c, cg, i, n, st); break;
                 case GGML_OP_FLASH_ATTN_EXT: used = try_fuse_attn(c, cg, i, n, st); break;
                 case GGML_OP_GET_ROWS: used = try_fuse_rows_sum(c, cg, i, n, st); break;
+                case GGML_OP_UNARY: used = try_fuse_silu_mul(c, cg, i, n, st); break;
                 case GGML_OP_ADD:
                     used = try_fuse_norm(c, cg, i, n, st);
                     if (!used) used = try_fuse_bias_gelu_mul_mat(c, cg, i, n, st);

@@ -332,6 +332,25 @@ int mq_quantize_act_ex(int type, const float *x, int64_t ldx, int64_t m, int64_t
     return e == hipSuccess ? MQ_OK : hip_fail(e, "activation quantization");
 }
 
+int mq_quantize_act_silu_mul(int type, const float *gate, const float *up, int64_t ld, int64_t m, int64_t k,
+                             void *workspace, size_t workspace_bytes, int path, void *stream) {
+    if (!type_ok(type)) return fail(MQ_EUNSUPPORTED, "weight type %d is not Q8_0/Q4_K/Q6_K/F16", type);
+    if (!mq_supports(type, k)) return fail(MQ_EUNSUPPORTED, "k=%lld not supported for type %d", (long long)k, type);
+    if (!gate || !up || !workspace || m < 0 || m > INT32_MAX || ld < k)
+        return fail(MQ_EINVAL, "mq_quantize_act_silu_mul: bad arguments");
+    if (!is_aligned(workspace, 256)) return fail(MQ_EINVAL, "mq_quantize_act_silu_mul: workspace must be 256-byte aligned");
+    if (m == 0) return MQ_OK;
+    path = resolve_path(path, m);
+    if (path < 0) return path;
+    const bool tiled = (path == MQ_PATH_GEMM);
+    const size_t need = tiled ? act_planes(type, m, k, true).total : gemv_ws_bytes(type, m, k);
+    if (workspace_bytes < need)
+        return fail(MQ_EINVAL, "mq_quantize_act_silu_mul: workspace %zu bytes < %zu needed", workspace_bytes, need);
+    const hipError_t e = launch_quantize_act_planar(type, gate, ld, workspace, m, k, mq_q8_0_variant(), tiled,
+                                                    (hipStream_t)stream, MQ_PRE_SILU_MUL, nullptr, up);
+    return e == hipSuccess ? MQ_OK : hip_fail(e, "activation quantization");
+}
+
 int mq_mul_mat_q_ex(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m, float *y,
                     int64_t ldy, const float *bias, int path, void *stream) {
     int rc = check_weight_shape(type, n, k);

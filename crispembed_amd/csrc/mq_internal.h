@@ -277,15 +277,17 @@ inline size_t act_workspace_bytes(int wtype, int64_t m, int64_t k) {
 
 // ---- launchers (defined in the .hip files; return hipError_t) ----
 // Quantize m rows of x (stride ldx floats) into the planar workspace layout.
-// `pre` / `bias`: the elementwise prologue (MQ_PRE_*, bias row or NULL) applied before quantization.
+// `pre` / `bias`: the elementwise prologue (MQ_PRE_*, bias row or NULL) applied before quantization;
+// x2 (MQ_PRE_SILU_MUL, same row stride): the up projection's rows, NULL when they follow the gate
+// projection's k values in each row of x.
 hipError_t launch_quantize_act_planar(int wtype, const float *x, int64_t ldx, void *ws, int64_t m, int64_t k,
                                       int q8_0_variant, bool tiled, hipStream_t s, int pre = MQ_PRE_NONE,
-                                      const float *bias = nullptr);
+                                      const float *bias = nullptr, const float *x2 = nullptr);
 hipError_t launch_quantize_q8_0_gguf(const float *x, int64_t ldx, void *y, int64_t m, int64_t k, int variant,
                                      hipStream_t s);
 hipError_t launch_quantize_q8_K_gguf(const float *x, int64_t ldx, void *y, int64_t m, int64_t k, hipStream_t s);
 hipError_t launch_quantize_f16(const float *x, int64_t ldx, void *y, int64_t m, int64_t k, hipStream_t s,
-                               int pre = MQ_PRE_NONE, const float *bias = nullptr);
+                               int pre = MQ_PRE_NONE, const float *bias = nullptr, int64_t uoff = 0);
 hipError_t launch_dequantize(int type, const void *w, float *y, int64_t nrows, int64_t k, int fused, hipStream_t s);
 hipError_t launch_weight_prepare(int type, void *image, int64_t n, int64_t k, int64_t row0, int64_t row1,
                                  hipStream_t s);

@@ -29,16 +29,17 @@ __device__ __forceinline__ float4 load4(const float *p) {
 // Prologue applied to an activation before it is quantized (the graph's elementwise
 // producers of the MUL_MAT input, fused): v = x + bias[col] (bias may be NULL), then
 //   MQ_PRE_GELU_ERF : v = 0.5 v (1 + erf(v / sqrt 2))            (ggml_gelu_erf)
-//   MQ_PRE_SILU_MUL : v = silu(v) * u, u the value k columns later (ggml_silu, ggml_mul:
-//                     the row holds the gate projection, then the up projection)
+//   MQ_PRE_SILU_MUL : v = silu(v) * u, u the value uoff floats after v (ggml_silu, ggml_mul:
+//                     the gate projection's value and the up projection's; uoff = k when a row
+//                     holds the gate projection, then the up projection)
 // all in fp32.  `pre` and `bias` are uniform: the branches cost nothing without a prologue.
 template <bool VEC4>
-__device__ __forceinline__ float4 pre_load(const float *p, int pre, const float *bias, int64_t col, int64_t k) {
+__device__ __forceinline__ float4 pre_load(const float *p, int pre, const float *bias, int64_t col, int64_t uoff) {
     const float4 v = load4<VEC4>(p);
     if (pre == MQ_PRE_NONE && bias == nullptr) return v;
     float r[4] = {v.x, v.y, v.z, v.w}, u[4] = {1.f, 1.f, 1.f, 1.f};
     if (pre == MQ_PRE_SILU_MUL) {
-        const float4 w = load4<VEC4>(p + k);
+        const float4 w = load4<VEC4>(p + uoff);
         u[0] = w.x, u[1] = w.y, u[2] = w.z, u[3] = w.w;
     }
 #pragma unroll
@@ -64,7 +65,7 @@ template <int VARIANT, int OUT, bool VEC4>
 __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__ x, int64_t ldx,
                                                        int8_t *__restrict__ out, float *__restrict__ xd,
                                                        int64_t m, int64_t k, int64_t m_pad, int64_t kb_pad, int pre,
-                                                       const float *__restrict__ bias) {
+                                                       const float *__restrict__ bias, int64_t uoff) {
     const int64_t nbr = k / QK8_0;
     const int64_t nbx = nbr;
     const int64_t rows = m;
@@ -74,7 +75,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__
     if (blk >= rows * nbx) return;  // 8-lane groups leave together
     const int64_t row = blk / nbx, b = blk - row * nbx;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (row < m && b < nbr) v = pre_load<VEC4>(x + row * ldx + b * QK8_0 + sub * 4, pre, bias, b * QK8_0 + sub * 4, k);
+    if (row < m && b < nbr) v = pre_load<VEC4>(x + row * ldx + b * QK8_0 + sub * 4, pre, bias, b * QK8_0 + sub * 4, uoff);
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
     amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
@@ -115,7 +116,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const float *__restrict__
                                                        int8_t *__restrict__ out, float *__restrict__ xd,
                                                        int16_t *__restrict__ xbs, _Float16 *__restrict__ xmin,
                                                        int64_t m, int64_t k, int64_t m_pad, int pre,
-                                                       const float *__restrict__ bias) {
+                                                       const float *__restrict__ bias, int64_t uoff) {
     const int64_t nbr = k / QK_K;
     const int64_t rows = m;
     const int lane = threadIdx.x & 63;
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const float *__restrict__
     if (blk >= rows * nbr) return;  // whole waves leave together
     const int64_t row = blk / nbr, b = blk - row * nbr;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (row < m) v = pre_load<VEC4>(x + row * ldx + b * QK_K + lane * 4, pre, bias, b * QK_K + lane * 4, k);
+    if (row < m) v = pre_load<VEC4>(x + row * ldx + b * QK_K + lane * 4, pre, bias, b * QK_K + lane * 4, uoff);
     const float vals[4] = {v.x, v.y, v.z, v.w};
     float amax = 0.0f, mx = 0.0f;
     int idx = 0x7fffffff;
@@ -187,12 +188,12 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const float *__restrict__
 template <bool VEC4>
 __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ x, int64_t ldx,
                                                       uint16_t *__restrict__ y, int64_t m, int64_t k, int pre,
-                                                      const float *__restrict__ bias) {
+                                                      const float *__restrict__ bias, int64_t uoff) {
     const int64_t q4 = k / 4;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= m * q4) return;
     const int64_t row = gid / q4, c = gid - row * q4;
-    const float4 v = pre_load<VEC4>(x + row * ldx + c * 4, pre, bias, c * 4, k);
+    const float4 v = pre_load<VEC4>(x + row * ldx + c * 4, pre, bias, c * 4, uoff);
     uint16_t *o = y + row * k + c * 4;
     o[0] = f32_to_f16_bits(v.x);
     o[1] = f32_to_f16_bits(v.y);
@@ -225,7 +226,7 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
                                                         int8_t *__restrict__ xq, float *__restrict__ xd,
                                                         _Float16 *__restrict__ xmin, int64_t m, int64_t k,
                                                         int64_t m_pad, int64_t kb_pad, int pre,
-                                                        const float *__restrict__ bias) {
+                                                        const float *__restrict__ bias, int64_t uoff) {
     constexpr int CB = (FMT == TQ_Q8_K) ? 256 : 128;   // K bytes per workgroup
     constexpr int BPV = (FMT == TQ_F16) ? 2 : 1;       // bytes per value
     constexpr int NCH = CB / 32;                        // fragments per workgroup
@@ -259,7 +260,7 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
         for (int it = 0; it < NIT; it++) {
             const int64_t row = rt * 32 + wave * 8 + it * RPI + rsub;
             vin[it] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (row < m && kv < k) vin[it] = pre_load<VEC4>(x + row * ldx + kv, pre, bias, kv, k);
+            if (row < m && kv < k) vin[it] = pre_load<VEC4>(x + row * ldx + kv, pre, bias, kv, uoff);
         }
     }
 #pragma unroll
@@ -650,16 +651,16 @@ static inline unsigned grid_for(int64_t threads) { return (unsigned)((threads + 
 template <int OUT>
 static hipError_t q8_0_dispatch(const float *x, int64_t ldx, int8_t *out, float *xd, int64_t m, int64_t k, int variant,
                                 int64_t m_pad, int64_t kb_pad, hipStream_t s, int pre = MQ_PRE_NONE,
-                                const float *bias = nullptr) {
+                                const float *bias = nullptr, int64_t uoff = 0) {
     const int64_t rows = m;
     const int64_t nbx = k / QK8_0;
     const int64_t threads = rows * nbx * 8;
     if (threads == 0) return hipSuccess;
-    const bool v4 = aligned16(x, ldx);
+    const bool v4 = aligned16(x, ldx) && uoff % 4 == 0;
     const dim3 g(grid_for(threads)), b(256);
 #define MQ_Q80(VAR)                                                                                             \
-    if (v4) hipLaunchKernelGGL((k_quantize_q8_0<VAR, OUT, true>), g, b, 0, s, x, ldx, out, xd, m, k, m_pad, kb_pad, pre, bias); \
-    else hipLaunchKernelGGL((k_quantize_q8_0<VAR, OUT, false>), g, b, 0, s, x, ldx, out, xd, m, k, m_pad, kb_pad, pre, bias);
+    if (v4) hipLaunchKernelGGL((k_quantize_q8_0<VAR, OUT, true>), g, b, 0, s, x, ldx, out, xd, m, k, m_pad, kb_pad, pre, bias, uoff); \
+    else hipLaunchKernelGGL((k_quantize_q8_0<VAR, OUT, false>), g, b, 0, s, x, ldx, out, xd, m, k, m_pad, kb_pad, pre, bias, uoff);
     switch (variant) {
         case MQ_Q8_0_X86: MQ_Q80(MQ_Q8_0_X86); break;
         case MQ_Q8_0_NEON: MQ_Q80(MQ_Q8_0_NEON); break;
@@ -673,31 +674,31 @@ static hipError_t q8_0_dispatch(const float *x, int64_t ldx, int8_t *out, float 
 template <int OUT>
 static hipError_t q8_K_dispatch(const float *x, int64_t ldx, int8_t *out, float *xd, int16_t *xbs, _Float16 *xmin,
                                 int64_t m, int64_t k, int64_t m_pad, hipStream_t s, int pre = MQ_PRE_NONE,
-                                const float *bias = nullptr) {
+                                const float *bias = nullptr, int64_t uoff = 0) {
     const int64_t rows = m;
     const int64_t threads = rows * (k / QK_K) * 64;
     if (threads == 0) return hipSuccess;
     const dim3 g(grid_for(threads)), b(256);
-    if (aligned16(x, ldx))
-        hipLaunchKernelGGL((k_quantize_q8_K<OUT, true>), g, b, 0, s, x, ldx, out, xd, xbs, xmin, m, k, m_pad, pre, bias);
+    if (aligned16(x, ldx) && uoff % 4 == 0)
+        hipLaunchKernelGGL((k_quantize_q8_K<OUT, true>), g, b, 0, s, x, ldx, out, xd, xbs, xmin, m, k, m_pad, pre, bias, uoff);
     else
-        hipLaunchKernelGGL((k_quantize_q8_K<OUT, false>), g, b, 0, s, x, ldx, out, xd, xbs, xmin, m, k, m_pad, pre, bias);
+        hipLaunchKernelGGL((k_quantize_q8_K<OUT, false>), g, b, 0, s, x, ldx, out, xd, xbs, xmin, m, k, m_pad, pre, bias, uoff);
     return hipGetLastError();
 }
 
 template <int FMT>
 static hipError_t tiled_dispatch(const float *x, int64_t ldx, int8_t *xq, float *xd, _Float16 *xmin, int64_t m,
                                  int64_t k, int variant, int64_t m_pad, int64_t kb_pad, hipStream_t s, int pre,
-                                 const float *bias) {
+                                 const float *bias, int64_t uoff) {
     constexpr int CB = (FMT == TQ_Q8_K) ? 256 : 128;
     if (m_pad % 32 != 0 || kb_pad % CB != 0) return hipErrorInvalidValue;
     const int64_t wgs = (m_pad / 32) * (kb_pad / CB);
     if (wgs == 0) return hipSuccess;
     const dim3 g((unsigned)wgs), b(256);
-    const bool v4 = aligned16(x, ldx);
+    const bool v4 = aligned16(x, ldx) && uoff % 4 == 0;
 #define MQ_TQ(VAR)                                                                                                      \
-    if (v4) hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, true>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad, pre, bias); \
-    else hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, false>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad, pre, bias);
+    if (v4) hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, true>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad, pre, bias, uoff); \
+    else hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, false>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad, pre, bias, uoff);
     if (FMT != TQ_Q8_0) {
         MQ_TQ(MQ_Q8_0_X86);
     } else {
@@ -713,29 +714,33 @@ static hipError_t tiled_dispatch(const float *x, int64_t ldx, int8_t *xq, float 
 }
 
 hipError_t launch_quantize_f16(const float *x, int64_t ldx, void *y, int64_t m, int64_t k, hipStream_t s, int pre,
-                               const float *bias) {
+                               const float *bias, int64_t uoff) {
     const int64_t threads = m * (k / 4);
     if (threads == 0) return hipSuccess;
     const dim3 g(grid_for(threads)), b(256);
-    if (aligned16(x, ldx))
-        hipLaunchKernelGGL((k_quantize_f16<true>), g, b, 0, s, x, ldx, (uint16_t *)y, m, k, pre, bias);
+    if (aligned16(x, ldx) && uoff % 4 == 0)
+        hipLaunchKernelGGL((k_quantize_f16<true>), g, b, 0, s, x, ldx, (uint16_t *)y, m, k, pre, bias, uoff);
     else
-        hipLaunchKernelGGL((k_quantize_f16<false>), g, b, 0, s, x, ldx, (uint16_t *)y, m, k, pre, bias);
+        hipLaunchKernelGGL((k_quantize_f16<false>), g, b, 0, s, x, ldx, (uint16_t *)y, m, k, pre, bias, uoff);
     return hipGetLastError();
 }
 
 hipError_t launch_quantize_act_planar(int wtype, const float *x, int64_t ldx, void *ws, int64_t m, int64_t k,
-                                      int q8_0_variant, bool tiled, hipStream_t s, int pre, const float *bias) {
+                                      int q8_0_variant, bool tiled, hipStream_t s, int pre, const float *bias,
+                                      const float *x2) {
     if (!tiled && m > GEMV_CHUNK) {  // the GEMV's chunked layout
         const size_t cb = gemv_chunk_bytes(wtype, k);
         for (int64_t r0 = 0, c = 0; r0 < m; r0 += GEMV_CHUNK, c++) {
             const hipError_t e = launch_quantize_act_planar(wtype, x + r0 * ldx, ldx, (uint8_t *)ws + c * cb,
                                                             std::min<int64_t>(GEMV_CHUNK, m - r0), k, q8_0_variant,
-                                                            false, s, pre, bias);
+                                                            false, s, pre, bias, x2 ? x2 + r0 * ldx : nullptr);
             if (e != hipSuccess) return e;
         }
         return hipSuccess;
     }
+    // MQ_PRE_SILU_MUL: the up projection's values uoff floats after the gate projection's (the
+    // same row stride): in the same row (k) or in x2
+    const int64_t uoff = x2 ? (int64_t)(x2 - x) : k;
     const ActPlanes a = act_planes(wtype, m, k, tiled);
     uint8_t *base = (uint8_t *)ws;
     int8_t *xq = (int8_t *)(base + a.xq);
@@ -744,19 +749,20 @@ hipError_t launch_quantize_act_planar(int wtype, const float *x, int64_t ldx, vo
         case MQ_TYPE_Q8_0:
             if (tiled)
                 return tiled_dispatch<TQ_Q8_0>(x, ldx, xq, xd, nullptr, m, k, q8_0_variant, a.m_pad, a.kb_pad, s, pre,
-                                               bias);
-            return q8_0_dispatch<OUT_ROWS>(x, ldx, xq, xd, m, k, q8_0_variant, m, k, s, pre, bias);
+                                               bias, uoff);
+            return q8_0_dispatch<OUT_ROWS>(x, ldx, xq, xd, m, k, q8_0_variant, m, k, s, pre, bias, uoff);
         case MQ_TYPE_Q4_K:
         case MQ_TYPE_Q6_K:
             if (tiled)
                 return tiled_dispatch<TQ_Q8_K>(x, ldx, xq, xd, (_Float16 *)(base + a.xmin), m, k, 0, a.m_pad, a.kb_pad, s,
-                                               pre, bias);
+                                               pre, bias, uoff);
             return q8_K_dispatch<OUT_ROWS>(x, ldx, xq, xd, (int16_t *)(base + a.xbs), (_Float16 *)(base + a.xgm), m, k,
-                                           m, s, pre, bias);
+                                           m, s, pre, bias, uoff);
         case MQ_TYPE_F16:
             if (tiled)
-                return tiled_dispatch<TQ_F16>(x, ldx, xq, nullptr, nullptr, m, k, 0, a.m_pad, a.kb_pad, s, pre, bias);
-            return launch_quantize_f16(x, ldx, base + a.xq, m, k, s, pre, bias);
+                return tiled_dispatch<TQ_F16>(x, ldx, xq, nullptr, nullptr, m, k, 0, a.m_pad, a.kb_pad, s, pre, bias,
+                                              uoff);
+            return launch_quantize_f16(x, ldx, base + a.xq, m, k, s, pre, bias, uoff);
         default: return hipErrorInvalidValue;
     }
 }

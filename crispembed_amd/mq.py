@@ -62,6 +62,7 @@ _SIGS = {
                             _c_sz, _c_vp]),
     "mq_quantize_act": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_sz, _c_int, _c_vp]),
     "mq_quantize_act_ex": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_int, _c_vp, _c_sz, _c_int, _c_vp]),
+    "mq_quantize_act_silu_mul": (_c_int, [_c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_sz, _c_int, _c_vp]),
     "mq_mul_mat_q": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_vp]),
     "mq_mul_mat_path": (_c_int, [_c_int, _c_i64, _c_i64, _c_i64]),
     "mq_mul_mat_q_ex": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_int, _c_vp]),

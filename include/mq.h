@@ -253,6 +253,14 @@ int mq_mul_mat_q_qkv(int type, const void *const *w_images, const int64_t *n, in
 int mq_quantize_act_ex(int type, const float *x, int64_t ldx, int64_t m, int64_t k, const float *bias, int op,
                        void *workspace, size_t workspace_bytes, int path, void *stream);
 
+/* MQ_PRE_SILU_MUL of mq_quantize_act_ex with the gate and up projections in two tensors of one
+ * row stride ld (floats): quantizes silu(gate) * up, the ggml_silu and ggml_mul nodes between a
+ * gated FFN's separate gate / up MUL_MATs and its down MUL_MAT (src/decoder_embed.cpp:793-802),
+ * without either node's tensor.  The bytes are those mq_quantize_act_ex(type, x, ...,
+ * MQ_PRE_SILU_MUL, ...) writes for the same values side by side in x. */
+int mq_quantize_act_silu_mul(int type, const float *gate, const float *up, int64_t ld, int64_t m, int64_t k,
+                             void *workspace, size_t workspace_bytes, int path, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -366,3 +366,33 @@ def test_mul_mat_q_swiglu_unsupported_shapes(m, n_ff):
     assert rc == -2, rc
     assert np.isnan(host(y)).all()
     del img, keep
+
+
+@pytest.mark.parametrize("wtype", TYPES)
+@pytest.mark.parametrize("m,k,ld,gap,path", [(5, 1536, 1536, 0, 1), (8, 512, 516, 3, 1), (300, 512, 512, 0, 2),
+                                             (37, 1536, 1540, 1, 2)])
+def test_silu_mul_separate_tensors_bit_exact(wtype, m, k, ld, gap, path):
+    """mq_quantize_act_silu_mul (gate and up in two tensors of one row stride, the backend's
+    fusion of the SILU and MUL nodes into the down MUL_MAT's quantizer) writes the bytes that
+    mq_quantize_act_ex(MQ_PRE_SILU_MUL) writes for the same values side by side; gap (floats
+    between the two tensors) makes their distance unaligned to 16 bytes (the scalar-load form)."""
+    import torch
+    from crispembed_amd import mq
+    L = mq.lib()
+    rng = np.random.default_rng(m + k + ld + gap + wtype)
+    g = (rng.standard_normal((m, k)) * 2.0).astype(np.float32)
+    u = rng.standard_normal((m, k)).astype(np.float32)
+    side = dev(np.concatenate([g, u], axis=1))
+    _, _, want = _quant(wtype, side, m, k, path, None, mq.PRE_SILU_MUL)
+    buf = torch.full((2 * m * ld + gap + 64,), np.nan, dtype=torch.float32, device="cuda")
+    gv = buf[:m * ld].view(m, ld)
+    uv = buf[m * ld + gap:m * ld + gap + m * ld].view(m, ld)
+    gv[:, :k] = torch.from_numpy(g).cuda()
+    uv[:, :k] = torch.from_numpy(u).cuda()
+    nb = L.mq_workspace_bytes(wtype, m, k)
+    ws, off = empty_u8(nb)
+    ws.zero_()
+    mq.check(L.mq_quantize_act_silu_mul(wtype, ctypes.c_void_p(gv.data_ptr()), ctypes.c_void_p(uv.data_ptr()), ld, m,
+                                        k, ctypes.c_void_p(ws.data_ptr() + off), nb, path, stream()))
+    got = host(ws)[off:off + nb]
+    assert np.array_equal(got, want)
