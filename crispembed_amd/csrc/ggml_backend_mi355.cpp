@@ -528,8 +528,12 @@ int try_fuse_norm(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status
     ggml_tensor *first = ggml_graph_node(cg, i);
     const ggml_tensor *res = nullptr;
     int j = i;
+    // the residual sum has other readers (a pre-norm layer's residual stream): it is written too,
+    // which the K-quant form below does
+    bool add_shared = false;
     if (first->op == GGML_OP_ADD) {  // the residual sum feeding the norm
-        if (i + 1 >= n || !feeds_only_next(cg, i)) return 0;
+        if (i + 1 >= n) return 0;
+        add_shared = !feeds_only_next(cg, i);
         const ggml_tensor *nx = ggml_graph_node(cg, i + 1);
         if ((nx->op != GGML_OP_NORM && nx->op != GGML_OP_RMS_NORM) || nx->src[0] != first) return 0;
         if (first->type != GGML_TYPE_F32 || !same_shape(first->src[0], first) || !same_shape(first->src[1], first))
@@ -568,6 +572,24 @@ int try_fuse_norm(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status
         return !t || (t->nb[0] == sizeof(float) && t->nb[1] == (size_t)K * sizeof(float) && rows_flat(t) &&
                       ((uintptr_t)t->data & 15) == 0);
     };
+    // a K-quant MUL_MAT on the GEMM path reading an RMS norm's result (the decoder's attn / ffn
+    // norms before q/k/v and gate/up): mq_op_norm_q8_K leaves it quantized to Q8_K, and writes
+    // the residual sum when that has other readers
+    const int mmt = (mm && mm->op == GGML_OP_MUL_MAT) ? mq_type_of(mm->src[0]->type) : -1;
+    if (mm && (mmt == MQ_TYPE_Q4_K || mmt == MQ_TYPE_Q6_K) && mm->src[1] == last && flat_mul_mat(mm) &&
+        kind == MQ_NORM_RMS && !b && K % 256 == 0 && K <= 2048 && dense(last) && dense(res) &&
+        dense(res ? first->src[0] : nrm->src[0]) && (!add_shared || dense(first)) && ((uintptr_t)w & 15) == 0 &&
+        mq_mul_mat_path(mmt, mm->src[0]->ne[1], K, M) == MQ_PATH_GEMM && ensure_ws(c, mq_workspace_bytes(mmt, M, K))) {
+        mq_view sv{};
+        if (add_shared) sv = view_of(first);
+        c->ws_x = nullptr;
+        const int rc = mq_op_norm_q8_K(kind, &x, res ? &r : nullptr, add_shared ? &sv : nullptr, &d, eps, w, c->ws,
+                                       c->ws_bytes, c->stream);
+        if (rc == 0) c->ws_x = last, c->ws_type = mmt, c->ws_m = M, c->ws_k = K, c->ws_path = MQ_PATH_GEMM;
+        st = op_status(rc, nrm);
+        return used;
+    }
+    if (add_shared) return 0;
     if (mm && mm->op == GGML_OP_MUL_MAT && mm->src[1] == last && mm->src[0]->type == GGML_TYPE_Q8_0 &&
         flat_mul_mat(mm) && K % 128 == 0 && K <= 1024 && dense(last) && dense(res) &&
         dense(res ? first->src[0] : nrm->src[0]) && ((uintptr_t)w & 15) == 0 && ((uintptr_t)b & 15) == 0 &&
