@@ -545,6 +545,24 @@ int try_fuse_norm(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status
     if (j + 1 >= n || !feeds_only_next(cg, j)) return 0;
     ggml_tensor *mul = ggml_graph_node(cg, j + 1);
     if (mul->op != GGML_OP_MUL || mul->src[0] != nrm || !is_row_vector(mul->src[1], nrm->ne[0])) return 0;
+    const int kind0 = nrm->op == GGML_OP_NORM ? MQ_NORM_LAYER : MQ_NORM_RMS;
+    // RMS_NORM -> MUL(w) -> ROPE: the decoder's per-head q / k norm and rotation in one pass
+    if (!res && kind0 == MQ_NORM_RMS && j + 2 < n && feeds_only_next(cg, j + 1)) {
+        ggml_tensor *rp = ggml_graph_node(cg, j + 2);
+        const int32_t *ip = rp->op_params;
+        if (rp->op == GGML_OP_ROPE && rp->src[0] == mul && ip[1] == 128 && ip[2] == MQ_ROPE_NEOX &&
+            mul->ne[0] == 128 && ((uintptr_t)mul->src[1]->data & 3) == 0) {
+            const mq_view x = view_of(nrm->src[0]), p = view_of(rp->src[1]), d = view_of(rp);
+            mq_view f{};
+            if (rp->src[2]) f = view_of(rp->src[2]);
+            const int rc = mq_op_rms_norm_rope(&x, op_param_f32(nrm, 0), (const float *)mul->src[1]->data, &p,
+                                               rp->src[2] ? &f : nullptr, &d, ip[1], ip[2], ip[4], op_param_f32(rp, 5),
+                                               op_param_f32(rp, 6), op_param_f32(rp, 7), op_param_f32(rp, 8),
+                                               op_param_f32(rp, 9), op_param_f32(rp, 10), c->stream);
+            if (rc == 0) return (j - i) + 3;
+            // shapes the fused op does not take run as the separate nodes
+        }
+    }
     ggml_tensor *last = mul;
     const float *b = nullptr;
     if (j + 2 < n && feeds_only_next(cg, j + 1)) {

@@ -460,6 +460,59 @@ __global__ __launch_bounds__(256) void k_rope(const DV x, const DV pos, const fl
     }
 }
 
+// k_rope for rows with every dimension rotated (ne0 = n_dims <= 128): one workgroup per
+// position (i2, i3).  Its n_dims / 2 angles -- the same fp32 chain, freq factors and YaRN mix
+// as k_rope, so the same cos / sin -- are formed once into LDS instead of once per row, then a
+// wave per row (ne1 rows: the heads), lane j < n_dims / 2 rotating pair j.  NORM: the row is
+// first RMS-normed and multiplied by w (ggml_rms_norm, ggml_mul) as k_norm computes it for
+// ne0 = 128 (lane j holds elements j and j + 64, the same sum order), so the result equals
+// mq_op_norm followed by mq_op_rope bit for bit (NEOX, n_dims 128 only).
+template <int MODE, bool NORM>
+__global__ __launch_bounds__(256) void k_rope_rows(const DV x, const DV pos, const float *__restrict__ ff, const DV d,
+                                                   const RopeParams rp, const float *__restrict__ w, float eps) {
+    __shared__ float cs[2][64];
+    const int64_t i2 = blockIdx.x % x.ne[2], i3 = blockIdx.x / x.ne[2];
+    const int hn = rp.n_dims / 2;
+    if ((int)threadIdx.x < hn) {
+        const int j = threadIdx.x;
+        float theta = (float)*(const int32_t *)(pos.p + i2 * pos.nb[0]);
+        for (int k = 0; k < j; k++) theta *= rp.theta_scale;
+        const float extrap = ff ? theta / ff[j] : theta;
+        float th = rp.freq_scale * extrap, mscale = rp.attn_factor;
+        if (rp.ext_factor != 0.0f) {
+            const float y = ((float)j - rp.corr_lo) / fmaxf(0.001f, rp.corr_hi - rp.corr_lo);
+            const float mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * rp.ext_factor;
+            th = th * (1.0f - mix) + extrap * mix;
+            mscale *= 1.0f + 0.1f * logf(1.0f / rp.freq_scale);
+        }
+        cs[0][j] = cosf(th) * mscale;
+        cs[1][j] = sinf(th) * mscale;
+    }
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const bool on = lane < hn;
+    const float c = on ? cs[0][lane] : 0.f, sn = on ? cs[1][lane] : 0.f;
+    const int e0 = MODE == MQ_ROPE_NEOX ? lane : 2 * lane, e1 = MODE == MQ_ROPE_NEOX ? lane + hn : 2 * lane + 1;
+    for (int64_t i1 = wave; i1 < x.ne[1]; i1 += 4) {
+        const float *xr = (const float *)(x.p + off3(x, i1, i2, i3));
+        float *dr = (float *)(d.p + off3(d, i1, i2, i3));
+        float a = on ? xr[e0] : 0.f, b = on ? xr[e1] : 0.f;
+        if constexpr (NORM) {
+            float s = 0.f;
+            s += a * a;
+            s += b * b;
+            const float inv_n = 1.0f / (float)rp.n_dims;
+            const float scale = 1.0f / sqrtf(wave_sum_f(s) * inv_n + eps);
+            a = (a - 0.0f) * scale * w[e0];
+            b = (b - 0.0f) * scale * w[e1];
+        }
+        if (on) {
+            dr[e0] = a * c - b * sn;
+            dr[e1] = a * sn + b * c;
+        }
+    }
+}
+
 // Row moves of the mixture-of-experts mat-mul: one workgroup per row r, float4 copies
 // (rows of k floats, k a multiple of 32 for every weight type), byte offsets per row.
 __global__ __launch_bounds__(256) void k_gather_rows(const char *__restrict__ src, const int64_t *__restrict__ off,
@@ -967,11 +1020,8 @@ static float yarn_corr_dim(int n_dims, int n_ctx_orig, float n_rot, float base) 
     return n_dims * logf((float)n_ctx_orig / (n_rot * 2.0f * 3.14159265358979323846f)) / (2.0f * logf(base));
 }
 
-extern "C" int mq_op_rope(const mq_view *x, const mq_view *pos, const mq_view *freq_factors, const mq_view *dst,
-                          int n_dims, int mode, int n_ctx_orig, float freq_base, float freq_scale, float ext_factor,
-                          float attn_factor, float beta_fast, float beta_slow, void *stream) {
-    if (const char *e = check_rope(mode, x, pos, freq_factors, dst, n_dims)) return fail(e);
-    if (!have_data({x, pos, freq_factors, dst})) return fail("missing data pointer");
+static RopeParams rope_params(int n_dims, int mode, int n_ctx_orig, float freq_base, float freq_scale, float ext_factor,
+                              float attn_factor, float beta_fast, float beta_slow) {
     RopeParams rp;
     rp.n_dims = n_dims, rp.mode = mode;
     rp.theta_scale = powf(freq_base, -2.0f / (float)n_dims);
@@ -980,9 +1030,45 @@ extern "C" int mq_op_rope(const mq_view *x, const mq_view *pos, const mq_view *f
     const float hi = ceilf(yarn_corr_dim(n_dims, n_ctx_orig, beta_slow, freq_base));
     rp.corr_lo = fmaxf(0.0f, lo);
     rp.corr_hi = fminf((float)(n_dims - 1), hi);
+    return rp;
+}
+
+extern "C" int mq_op_rms_norm_rope(const mq_view *x, float eps, const float *w, const mq_view *pos,
+                                   const mq_view *freq_factors, const mq_view *dst, int n_dims, int mode,
+                                   int n_ctx_orig, float freq_base, float freq_scale, float ext_factor,
+                                   float attn_factor, float beta_fast, float beta_slow, void *stream) {
+    if (const char *e = check_rope(mode, x, pos, freq_factors, dst, n_dims)) return fail(e);
+    if (!have_data({x, pos, freq_factors, dst}) || !w) return fail("missing data pointer");
+    if (mode != MQ_ROPE_NEOX || n_dims != 128 || x->ne[0] != 128)
+        return fail("rms_norm_rope: the NEOX rotation of all of ne0 = 128 dimensions only");
+    if (x->ne[2] * x->ne[3] > INT32_MAX) return fail("rms_norm_rope: too many positions");
+    const RopeParams rp = rope_params(n_dims, mode, n_ctx_orig, freq_base, freq_scale, ext_factor, attn_factor,
+                                      beta_fast, beta_slow);
+    const float *ff = freq_factors ? (const float *)freq_factors->data : nullptr;
+    hipLaunchKernelGGL((k_rope_rows<MQ_ROPE_NEOX, true>), dim3((unsigned)(x->ne[2] * x->ne[3])), dim3(256), 0,
+                       (hipStream_t)stream, dv(x), dv(pos), ff, dv(dst), rp, w, eps);
+    return hip_rc(hipGetLastError(), "rms_norm_rope");
+}
+
+extern "C" int mq_op_rope(const mq_view *x, const mq_view *pos, const mq_view *freq_factors, const mq_view *dst,
+                          int n_dims, int mode, int n_ctx_orig, float freq_base, float freq_scale, float ext_factor,
+                          float attn_factor, float beta_fast, float beta_slow, void *stream) {
+    if (const char *e = check_rope(mode, x, pos, freq_factors, dst, n_dims)) return fail(e);
+    if (!have_data({x, pos, freq_factors, dst})) return fail("missing data pointer");
+    const RopeParams rp = rope_params(n_dims, mode, n_ctx_orig, freq_base, freq_scale, ext_factor, attn_factor,
+                                      beta_fast, beta_slow);
     const int64_t units = nel(x) / 2;
     const float *ff = freq_factors ? (const float *)freq_factors->data : nullptr;
     hipStream_t s = (hipStream_t)stream;
+    if (x->ne[0] == n_dims && n_dims <= 128 && x->ne[2] * x->ne[3] <= INT32_MAX) {  // every dimension rotated
+        const dim3 g((unsigned)(x->ne[2] * x->ne[3])), b(256);
+        if (mode == MQ_ROPE_NEOX)
+            hipLaunchKernelGGL((k_rope_rows<MQ_ROPE_NEOX, false>), g, b, 0, s, dv(x), dv(pos), ff, dv(dst), rp, nullptr, 0.f);
+        else
+            hipLaunchKernelGGL((k_rope_rows<MQ_ROPE_NORMAL, false>), g, b, 0, s, dv(x), dv(pos), ff, dv(dst), rp, nullptr,
+                               0.f);
+        return hip_rc(hipGetLastError(), "rope");
+    }
     if (mode == MQ_ROPE_NEOX)
         hipLaunchKernelGGL((k_rope<MQ_ROPE_NEOX>), dim3(grid_units(units)), dim3(256), 0, s, dv(x), dv(pos), ff, dv(dst), rp,
                            units);

@@ -171,6 +171,14 @@ int mq_op_rope(const mq_view *x, const mq_view *pos, const mq_view *freq_factors
                int mode, int n_ctx_orig, float freq_base, float freq_scale, float ext_factor, float attn_factor,
                float beta_fast, float beta_slow, void *stream);
 
+/* mq_op_rope of rms_norm(x) * w: the decoder's per-head q / k norm (ggml_rms_norm over ne0, then
+ * ggml_mul by the F32 row w [ne0]) and rotation (src/decoder_embed.cpp:737-759) in one pass,
+ * equal bit for bit to mq_op_norm(MQ_NORM_RMS, x, NULL, tmp, eps, w, NULL) followed by
+ * mq_op_rope(tmp, ...).  mode MQ_ROPE_NEOX with n_dims = ne0 = 128 only. */
+int mq_op_rms_norm_rope(const mq_view *x, float eps, const float *w, const mq_view *pos, const mq_view *freq_factors,
+                        const mq_view *dst, int n_dims, int mode, int n_ctx_orig, float freq_base, float freq_scale,
+                        float ext_factor, float attn_factor, float beta_fast, float beta_slow, void *stream);
+
 /* ggml_mul_mat_id, the mixture-of-experts mat-mul (src/crispembed.cpp:1365,1371):
  *   experts: n_exp prepared weight images of `type` (n x k each, as mq_weight_prepare builds
  *            them), expert e at expert_images + e * expert_stride bytes;

@@ -614,3 +614,33 @@ def test_repeat_and_mul_mat_f32():
     _call(L.mq_op_mul_mat_f32, mq.view(_cuda(a2)), mq.view(_cuda(b2)), mq.view(y2), stream())
     ref2 = np.einsum("bik,bjk->bji", np.repeat(a2, 3, axis=0).astype(np.float64), b2.astype(np.float64))
     assert np.abs(host(y2) - ref2).max() <= 1e-5
+
+
+@pytest.mark.parametrize("case", ["plain", "yarn", "freq_factors"])
+def test_rms_norm_rope_equals_separate(case):
+    """mq_op_rms_norm_rope (the backend's fusion of a head's RMS_NORM, MUL by the norm weight and
+    ROPE, src/decoder_embed.cpp:737-759) against mq_op_norm then mq_op_rope: bit for bit."""
+    L = mq.lib()
+    B, T, nh, ne0 = 2, 37, 5, 128
+    rng = _rng(77)
+    x = (rng.standard_normal((B, T, nh, ne0)) * 3.0).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(ne0)).astype(np.float32)
+    pos = (np.arange(T, dtype=np.int32) * 3 + 5).astype(np.int32)
+    kw = dict(n_ctx_orig=0, base=1e6, freq_scale=1.0, ext_factor=0.0, attn_factor=1.0, beta_fast=0.0, beta_slow=0.0)
+    ff = None
+    if case == "yarn":
+        kw.update(freq_scale=0.25, ext_factor=1.0, attn_factor=1.0 / (1 + 0.1 * np.log(4.0)), n_ctx_orig=4096,
+                  beta_fast=32.0, beta_slow=1.0)
+    if case == "freq_factors":
+        ff = (1.0 + rng.random(ne0 // 2) * 3).astype(np.float32)
+    dx, dp, dw = _cuda(x), _cuda(pos), _cuda(w)
+    fv = mq.view(_cuda(ff)) if ff is not None else None
+    args = (128, mq.ROPE_NEOX, kw["n_ctx_orig"], kw["base"], kw["freq_scale"], kw["ext_factor"], kw["attn_factor"],
+            kw["beta_fast"], kw["beta_slow"])
+    tmp, want, got = _t().empty_like(dx), _t().empty_like(dx), _t().empty_like(dx)
+    _call(L.mq_op_norm, mq.NORM_RMS, mq.view(dx), None, mq.view(tmp), 1e-6, ctypes.c_void_p(dw.data_ptr()), None,
+          stream())
+    _call(L.mq_op_rope, mq.view(tmp), mq.view(dp), fv, mq.view(want), *args, stream())
+    _call(L.mq_op_rms_norm_rope, mq.view(dx), 1e-6, ctypes.c_void_p(dw.data_ptr()), mq.view(dp), fv, mq.view(got),
+          *args, stream())
+    assert np.array_equal(host(got).view(np.uint32), host(want).view(np.uint32))
