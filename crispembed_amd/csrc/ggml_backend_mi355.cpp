@@ -730,7 +730,8 @@ int try_fuse_ffn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status 
 // observer reads its src1).
 enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node);
 
-int try_fuse_silu_mul(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status &st) {
+int try_fuse_silu_mul(BackendCtx *c, ggml_cgraph *cg, int i, int n, const std::vector<char> &done,
+                      enum ggml_status &st) {
     ggml_tensor *silu = ggml_graph_node(cg, i);
     if (ggml_get_unary_op(silu) != GGML_UNARY_OP_SILU || i + 3 >= n) return 0;
     ggml_tensor *up = ggml_graph_node(cg, i + 1), *mul = ggml_graph_node(cg, i + 2), *down = ggml_graph_node(cg, i + 3);
@@ -750,8 +751,10 @@ int try_fuse_silu_mul(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_st
     const int path = mq_mul_mat_path(mt, N, K, M);
     const bool gemv = path == MQ_PATH_GEMV && (mt == MQ_TYPE_Q4_K || mt == MQ_TYPE_Q6_K) && M <= 8 && K <= 6144 &&
                       !c->capturing && ((uintptr_t)gate->data & 15) == 0 && ((uintptr_t)up->data & 15) == 0 && ld % 4 == 0;
-    st = compute_node(c, up);
-    if (st != GGML_STATUS_SUCCESS) return 4;
+    if (!done[i + 1]) {  // (done: computed already, grouped with the gate projection)
+        st = compute_node(c, up);
+        if (st != GGML_STATUS_SUCCESS) return 4;
+    }
     int rc;
     if (gemv) {
         const void *wi[1] = {wd->data};
@@ -818,6 +821,12 @@ int try_fuse_attn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status
 }
 
 // A MUL_MAT of a group and the bias ADD fused into its store (add_idx < 0: none).
+// true when the bytes of tensor a and tensor b overlap
+bool overlaps(const ggml_tensor *a, const ggml_tensor *b) {
+    const char *a0 = (const char *)a->data, *b0 = (const char *)b->data;
+    return a0 && b0 && a0 < b0 + ggml_nbytes(b) && b0 < a0 + ggml_nbytes(a);
+}
+
 struct MulMatMember {
     ggml_tensor *mm, *dst;
     const float *bias;
@@ -845,9 +854,9 @@ MulMatMember mul_mat_member(ggml_cgraph *cg, int j, int n) {
     return m;
 }
 
-// MUL_MAT [-> ADD(bias)] at node i and the MUL_MATs after it that read the same activation with
-// the same weight type and k (q, k and v of a layer), separated only by view nodes and their
-// own bias ADDs: one activation quantization and one grouped launch.  Returns the nodes
+// MUL_MAT [-> ADD(bias)] at node i and the MUL_MATs after it (within 32 nodes) that read the same
+// activation with the same weight type and k (q, k and v of a layer; a gated FFN's gate and up):
+// one activation quantization and one grouped launch.  Returns the nodes
 // consumed from i on; the later members (and their ADDs) are marked in `done`.
 const ggml_tensor *view_root(const ggml_tensor *t) {
     while (t && t->view_src) t = t->view_src;
@@ -898,13 +907,32 @@ int try_group_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, std::vector<
     MulMatMember mem[4];
     int nm = 0;
     mem[nm++] = mul_mat_member(cg, i, n);
-    for (int j = (mem[0].add_idx >= 0 ? mem[0].add_idx : i) + 1; j < n && nm < 4; j++) {
+    // Later members may also sit behind other nodes (a decoder's q is normed and rotated before
+    // its k product).  Such a member is computed ahead of those nodes, which is safe when none of
+    // them reads or writes the member's output bytes (ggml-alloc may have given them memory the
+    // member's output reuses) or writes the activation's bytes.
+    std::vector<const ggml_tensor *> between;
+    auto clashes = [&](const MulMatMember &m) {
+        for (const ggml_tensor *b : between) {
+            if (overlaps(b, m.mm) || overlaps(b, m.dst) || overlaps(b, x)) return true;
+            for (int k = 0; k < GGML_MAX_SRC; k++)
+                if (b->src[k] && (overlaps(b->src[k], m.mm) || overlaps(b->src[k], m.dst))) return true;
+        }
+        return false;
+    };
+    const int scan_end = std::min(n, i + 32);
+    for (int j = (mem[0].add_idx >= 0 ? mem[0].add_idx : i) + 1; j < scan_end && nm < 4; j++) {
         ggml_tensor *t = ggml_graph_node(cg, j);
         if (is_view_op(t->op) || ggml_is_empty(t)) continue;
         if (t->op != GGML_OP_MUL_MAT || done[j] || t->src[1] != x || t->src[0]->type != w0->type ||
-            t->src[0]->ne[0] != w0->ne[0] || !flat_mul_mat(t))
-            break;
-        mem[nm] = mul_mat_member(cg, j, n);
+            t->src[0]->ne[0] != w0->ne[0] || !flat_mul_mat(t)) {
+            if (t->op == GGML_OP_FLASH_ATTN_EXT || t->op == GGML_OP_MUL_MAT_ID) break;  // workspace users
+            between.push_back(t);
+            continue;
+        }
+        const MulMatMember m = mul_mat_member(cg, j, n);
+        if (!between.empty() && clashes(m)) break;
+        mem[nm] = m;
         if (mem[nm].add_idx >= 0) j = mem[nm].add_idx;
         nm++;
     }
@@ -1055,12 +1083,6 @@ enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node) {
     }
 }
 
-// true when the bytes of tensor a and tensor b overlap
-bool overlaps(const ggml_tensor *a, const ggml_tensor *b) {
-    const char *a0 = (const char *)a->data, *b0 = (const char *)b->data;
-    return a0 && b0 && a0 < b0 + ggml_nbytes(b) && b0 < a0 + ggml_nbytes(a);
-}
-
 enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
     const int n = ggml_graph_n_nodes(cg);
     const bool fuse = std::getenv("MQ_GGML_NO_FUSION") == nullptr;
@@ -1088,7 +1110,7 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
                 case GGML_OP_RMS_NORM: used = try_fuse_norm(c, cg, i, n, st); break;
                 case GGML_OP_FLASH_ATTN_EXT: used = try_fuse_attn(c, cg, i, n, st); break;
                 case GGML_OP_GET_ROWS: used = try_fuse_rows_sum(c, cg, i, n, st); break;
-                case GGML_OP_UNARY: used = try_fuse_silu_mul(c, cg, i, n, st); break;
+                case GGML_OP_UNARY: used = try_fuse_silu_mul(c, cg, i, n, done, st); break;
                 case GGML_OP_ADD:
                     used = try_fuse_norm(c, cg, i, n, st);
                     if (!used) used = try_fuse_bias_gelu_mul_mat(c, cg, i, n, st);
