@@ -15,7 +15,8 @@ both also as a fraction of the int8 MFMA peak.
 cpu_baseline = the restated ggml-cpu mul_mat (AVX-512 VNNI or AVX2 integer dots, threads =
 the CPUs this job may use) on a bounded sample of token rows of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras] [--only q8_0|e2e|graph|qwen3|decode]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
+                      [--only q8_0|e2e|graph|qwen3|qgraph|decode]
 """
 import argparse
 import ctypes
@@ -439,6 +440,47 @@ def bench_minilm_ggml_graph(torch, L, mq):
             "embeddings_per_s": round(B / (ms * 1e-3), 1)}
 
 
+def bench_qwen3_ggml_graph(torch, L, mq):
+    """One 512-token sequence through CrispEmbed's Qwen3 decoder graph (decoder_encode_tokens'
+    single-text path, 815 nodes) on the MI355X ggml backend (tests/native/test_decoder_graph_mi355.cpp,
+    built by build_test_driver), beside the runner (mq_decoder_encode) on the same model at B = 1.
+    Qwen3-Embedding-0.6B shape, Q4_K, the token table cut to 4096 rows (the lookup's size does
+    not change the work); time per graph from the host's clock around ggml_backend_graph_compute."""
+    import subprocess
+    import tempfile
+
+    import numpy as np
+    from crispembed_amd import decoder, gguf, synth
+    exe = os.path.join(ROOT, "crispembed_amd", "bin", "test-decoder-graph-mi355")
+    if not os.path.exists(exe):
+        return {"error": f"{exe} not built"}
+    hp = dict(decoder.QWEN3_EMBED_0_6B, n_vocab=4096)
+    T = 512
+    W = decoder.synthetic_weights(hp, mq.TYPE_Q4_K, name="qwen3_graph")
+    ids = synth.integers(f"qwen3/graph_ids_{T}", (T,), 0, hp["n_vocab"] - 1).astype(np.int32)
+    with tempfile.TemporaryDirectory() as d:
+        gguf.write_decoder_gguf(os.path.join(d, "m.gguf"), hp, mq.TYPE_Q4_K, W)
+        ids.tofile(os.path.join(d, "ids"))
+        r = subprocess.run([exe, os.path.join(d, "m.gguf"), str(T), os.path.join(d, "ids"), os.path.join(d, "out"),
+                            "--iters", "10"], capture_output=True, text=True, timeout=600)
+    try:
+        res = json.loads(r.stdout.strip().splitlines()[-1])
+    except (ValueError, IndexError):
+        return {"error": (r.stderr or r.stdout)[-300:]}
+    if not res.get("ok"):
+        return {"error": res.get("error")}
+    dec = decoder.DecoderEmbedder(hp, mq.TYPE_Q4_K, W)
+    ids_d = torch.from_numpy(ids.copy()).cuda()
+    out = torch.empty((1, hp["n_embd"]), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    runner_ms = _timed(torch, lambda: dec.encode(ids_d.data_ptr(), 1, T, out.data_ptr(), stream.cuda_stream), 10) / 1e3
+    del dec
+    return {"workload": "Qwen3-Embedding-0.6B shape (vocab 4096), Q4_K, one 512-token sequence, CrispEmbed's "
+                        "decoder graph on the MI355X ggml backend",
+            "graph_nodes": res["nodes"], "nodes_not_on_gpu": res["unsupported"],
+            "graph_ms": round(res["ms_per_graph"], 3), "runner_ms": round(runner_ms, 3)}
+
+
 def bench_qwen3_e2e(torch, L, mq):
     """End-to-end Qwen3-Embedding-0.6B-shaped decoder embedder (28 layers, H 1024, 16 query /
     8 key-value heads of 128, SwiGLU FFN 3072, RMSNorm eps 1e-6, NEOX RoPE theta 1e6, causal,
@@ -551,7 +593,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="skip the Q8_0 and GEMV side measurements")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--gemm-cfg", default=None, help="MQ_GEMM_CFG tile configuration (1 or 3)")
-    ap.add_argument("--only", choices=["q8_0", "e2e", "graph", "qwen3", "decode"], default=None,
+    ap.add_argument("--only", choices=["q8_0", "e2e", "graph", "qwen3", "qgraph", "decode"], default=None,
                     help="run one side measurement alone (for per-workload profiles) and print its JSON")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 10 device copies of 256 MiB (reference kernel for rocprof byte counters)")
@@ -580,6 +622,7 @@ def main():
               "e2e": lambda: bench_minilm_e2e(torch, L, mq),
               "graph": lambda: bench_minilm_ggml_graph(torch, L, mq),
               "qwen3": lambda: bench_qwen3_e2e(torch, L, mq),
+              "qgraph": lambda: bench_qwen3_ggml_graph(torch, L, mq),
               "decode": lambda: bench_decode(torch, L, mq, synth)}[args.only]
         print(json.dumps({"only": args.only, "result": fn()}), flush=True)
         return

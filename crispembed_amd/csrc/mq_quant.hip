@@ -312,8 +312,10 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
 // that reads them (the decoder's attn_norm / ffn_norm before the qkv and gate|up products):
 //   x = y + res (written to xout), h = x / sqrt(mean(x^2) + eps) * w (written to hout unless NULL),
 // and h quantized into the tiled GEMM layout exactly as k_quantize_tiled<TQ_Q8_K> quantizes it.
-// Workgroup: one 32-row tile, 8 waves of 4 rows; a wave holds one row at a time, lane l the
-// values 256 p + 4 l .. + 3 of superblock p, which is the tiled quantizer's lane layout.
+// Workgroup: 8 rows of a 32-row tile (four workgroups per tile, so a 512-row input still spreads
+// over 64 CUs), a wave per row with every load in flight before the first use, lane l holding
+// the values 256 p + 4 l .. + 3 of superblock p, which is the tiled quantizer's lane layout; the
+// workgroup writes its rows' 16-byte units of each fragment, scales and min-term halves.
 // ---------------------------------------------------------------------------
 template <int NSB>
 __global__ __launch_bounds__(512) void k_add_rmsnorm_q8_K(const float *y, const float *res, const float *__restrict__ w,
@@ -325,64 +327,65 @@ __global__ __launch_bounds__(512) void k_add_rmsnorm_q8_K(const float *y, const 
     __shared__ float dsh[NSB][32];
     __shared__ __attribute__((aligned(16))) _Float16 msh[NSB][512];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t rt = blockIdx.x;
-    float4 wv[NSB];
+    const int64_t rt = blockIdx.x >> 2;      // 32-row tile
+    const int r0 = (int)(blockIdx.x & 3) * 8;  // this workgroup's 8 rows of it, one per wave
+    const int r = r0 + wave;
+    const int64_t row = rt * 32 + r;
+    const bool live = row < rows;
+    float4 v[NSB];
 #pragma unroll
-    for (int p = 0; p < NSB; p++) wv[p] = *(const float4 *)(w + 256 * p + 4 * lane);
+    for (int p = 0; p < NSB; p++) {  // every load in flight before the first use
+        v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (live) {
+            const int64_t o = row * H + 256 * p + 4 * lane;
+            float4 a = *(const float4 *)(y + o);
+            if (res) {
+                const float4 c = *(const float4 *)(res + o);
+                a.x = a.x + c.x, a.y = a.y + c.y, a.z = a.z + c.z, a.w = a.w + c.w;
+            }
+            v[p] = a;
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < NSB; p++) ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
+    ss += __shfl_xor(ss, 32);
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 8);
+    ss += __shfl_xor(ss, 4);
+    ss += __shfl_xor(ss, 2);
+    ss += __shfl_xor(ss, 1);
+    const float scale = 1.0f / sqrtf(ss / (float)H + eps);
     const int cbyte = 4 * (lane & 7);
-#pragma unroll 1
-    for (int it = 0; it < 4; it++) {
-        const int r = wave * 4 + it;
-        const int64_t row = rt * 32 + r;
-        const bool live = row < rows;
-        float4 v[NSB];
-        float ss = 0.f;
 #pragma unroll
-        for (int p = 0; p < NSB; p++) {
-            v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (live) {
-                const int64_t o = row * H + 256 * p + 4 * lane;
-                float4 a = *(const float4 *)(y + o);
-                if (res) {
-                    const float4 c = *(const float4 *)(res + o);
-                    a.x = a.x + c.x, a.y = a.y + c.y, a.z = a.z + c.z, a.w = a.w + c.w;
-                }
-                v[p] = a;
-            }
-            ss += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
+    for (int p = 0; p < NSB; p++) {
+        const float4 wv = *(const float4 *)(w + 256 * p + 4 * lane);
+        float4 h;
+        h.x = v[p].x * scale * wv.x, h.y = v[p].y * scale * wv.y;
+        h.z = v[p].z * scale * wv.z, h.w = v[p].w * scale * wv.w;
+        if (live) {
+            const int64_t o = row * H + 256 * p + 4 * lane;
+            if (xout) *(float4 *)(xout + o) = v[p];
+            if (hout) *(float4 *)(hout + o) = h;
+        } else {
+            h = make_float4(0.f, 0.f, 0.f, 0.f);  // pad rows of the tile quantize to zero
         }
-        ss += __shfl_xor(ss, 32);
-        ss += __shfl_xor(ss, 16);
-        ss += __shfl_xor(ss, 8);
-        ss += __shfl_xor(ss, 4);
-        ss += __shfl_xor(ss, 2);
-        ss += __shfl_xor(ss, 1);
-        const float scale = 1.0f / sqrtf(ss / (float)H + eps);
-#pragma unroll
-        for (int p = 0; p < NSB; p++) {
-            float4 h;
-            h.x = v[p].x * scale * wv[p].x, h.y = v[p].y * scale * wv[p].y;
-            h.z = v[p].z * scale * wv[p].z, h.w = v[p].w * scale * wv[p].w;
-            if (live) {
-                const int64_t o = row * H + 256 * p + 4 * lane;
-                if (xout) *(float4 *)(xout + o) = v[p];
-                if (hout) *(float4 *)(hout + o) = h;
-            } else {
-                h = make_float4(0.f, 0.f, 0.f, 0.f);  // pad rows of the tile quantize to zero
-            }
-            int8_t *dst = frag + (8 * p + (lane >> 3)) * FST + ((r + 32 * (cbyte >> 4)) << 4) + (cbyte & 15);
-            q8_K_block_row(h, lane, r, dst, &dsh[p][r], msh[p]);
-        }
+        int8_t *dst = frag + (8 * p + (lane >> 3)) * FST + ((r + 32 * (cbyte >> 4)) << 4) + (cbyte & 15);
+        q8_K_block_row(h, lane, r, dst, &dsh[p][r], msh[p]);
     }
     __syncthreads();
+    // this workgroup's lane units of every fragment: rows r0 .. r0 + 7, both 16-byte halves
     const int t = threadIdx.x;
-    for (int q = t; q < NCH * 64; q += 512) {
-        const int f = q >> 6, L = q & 63;
+    for (int q = t; q < NCH * 16; q += 512) {
+        const int f = q >> 4, u = q & 15, L = r0 + (u & 7) + 32 * (u >> 3);
         *(int4 *)(xq + ((rt * NCH + f) << 10) + L * 16) = *(const int4 *)(frag + f * FST + L * 16);
     }
-    for (int q = t; q < NSB * 32; q += 512) xd[(int64_t)(q >> 5) * m_pad + rt * 32 + (q & 31)] = dsh[q >> 5][q & 31];
-    for (int q = t; q < NSB * 64; q += 512)
-        ((int4 *)(xmin + ((rt * NSB + (q >> 6)) << 9)))[q & 63] = ((const int4 *)msh[q >> 6])[q & 63];
+    for (int q = t; q < NSB * 8; q += 512) xd[(int64_t)(q >> 3) * m_pad + rt * 32 + r0 + (q & 7)] = dsh[q >> 3][r0 + (q & 7)];
+    // min-term fragment halves (row, j) and (32 + row, j): two runs of 8 rows x 8 halves = 16 x 8 bytes
+    for (int q = t; q < NSB * 16; q += 512) {
+        const int p = q >> 4, u = q & 15, hr = r0 + (u & 7) + 32 * (u >> 3);
+        *(int4 *)(xmin + ((rt * NSB + p) << 9) + hr * 8) = *(const int4 *)(&msh[p][hr * 8]);
+    }
 }
 
 hipError_t launch_add_rmsnorm_q8_K(const float *y, const float *res, const float *w, float eps, float *xout,
@@ -396,7 +399,7 @@ hipError_t launch_add_rmsnorm_q8_K(const float *y, const float *res, const float
     int8_t *xq = (int8_t *)(b + ap.xq);
     float *xd = (float *)(b + ap.xd);
     _Float16 *xm = (_Float16 *)(b + ap.xmin);
-    const dim3 g((unsigned)((rows + 31) / 32)), blk(512);
+    const dim3 g((unsigned)((rows + 31) / 32 * 4)), blk(512);
     switch (H / 256) {
 #define MQ_RQ(N)                                                                                                       \
     case N:                                                                                                            \

@@ -299,6 +299,7 @@ def main(argv=None):
     s.add_argument("out")
     s.add_argument("--type", default="q8_0", choices=["q8_0", "q4_K", "q6_K", "f16"])
     s.add_argument("--layers", type=int, default=None, help="override the layer count")
+    s.add_argument("--vocab", type=int, default=None, help="override the token table's row count")
     d = sub.add_parser("dump", help="list a GGUF file's metadata and tensors")
     d.add_argument("path")
     args = ap.parse_args(argv)
@@ -318,12 +319,16 @@ def main(argv=None):
         hp = dict(bert.MINILM_L6)
         if args.layers:
             hp["n_layer"] = args.layers
+        if args.vocab:
+            hp["n_vocab"] = args.vocab
         write_bert_gguf(args.out, hp, wtype, bert.synthetic_weights(hp, wtype))
     else:
         from . import decoder
         hp = dict(decoder.QWEN3_EMBED_0_6B)
         if args.layers:
             hp["n_layer"] = args.layers
+        if args.vocab:
+            hp["n_vocab"] = args.vocab
         write_decoder_gguf(args.out, hp, wtype, decoder.synthetic_weights(hp, wtype))
     print(f"wrote {args.out}")
     return 0
