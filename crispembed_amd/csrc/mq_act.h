@@ -69,6 +69,7 @@ __device__ __forceinline__ float requant_q8_0(float (&v)[16], bool live, int pre
 
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 // hi + lo split of two floats with one explicit rounding (round toward zero) for both

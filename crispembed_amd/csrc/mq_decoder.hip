@@ -422,7 +422,7 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
-                    live |= key < Tk && (float)mrow[key] != -INFINITY;
+                    live |= key < Tk && (float)mrow[min(key, Tk - 1)] != -INFINITY;
                 }
                 if (__ballot(live) == 0) continue;
             }
@@ -562,18 +562,24 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
     }
 }
 
-// Split-key form for grids too small to fill the GPU (one sequence, few heads): a workgroup of
-// 4 waves owns one (head, 32-query tile); wave w runs the same online softmax over key blocks
-// w, w + 4, ... and the four partial (max, sum, O) are merged through LDS:
+// Split-key form for grids too small to fill the GPU (one sequence, few heads) and for masked
+// head_dim 128: a workgroup of NW waves owns one (head, 32-query tile); wave w runs the same
+// online softmax over key blocks w, w + NW, ... and the NW partial (max, sum, O) are merged
+// through LDS:
 //   m = max_w m_w,  O = sum_w 2^(m_w - m) O_w,  l = sum_w 2^(m_w - m) l_w,  out = O / l.
-template <int HD, bool MASK>
-__global__ __launch_bounds__(256) void k_attn_split(const AttnArgs a, int nblk, float qscale) {
+// With a mask, each wave first classifies its first 64 key blocks from the mask values of the
+// tile's 32 rows (all loads in flight together): no finite value -> the block is skipped; all
+// values 0 -> it runs unmasked, with no mask reads; else it adds the mask as it goes.  A causal
+// mask thus costs one pass over it, not a dependent load per key block.
+template <int HD, bool MASK, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void k_attn_split(const AttnArgs a, int nblk, float qscale) {
     constexpr int NS = HD / 16, NT = HD / 32, HALF = HD / 2, NFR = kv_frags<HD>();
     constexpr float LOG2E = 1.4426950408889634f;
-    __shared__ __attribute__((aligned(16))) float rs[4][32];
-    __shared__ float mls[4][2][32];
-    __shared__ __attribute__((aligned(16))) float ored[4][NT][16][64];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
+    __shared__ __attribute__((aligned(16))) float rs[NW][32];
+    __shared__ float mls[NW][2][32];
+    __shared__ __attribute__((aligned(16))) float ored[NW][NT][16][64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, l32 = lane & 31,
+              half = lane >> 5;
     const int h = blockIdx.x, b = blockIdx.y;
     const int Tq = a.Tq, Tk = a.Tk, causal = a.causal;
     const int q0 = ((int)gridDim.z - 1 - (int)blockIdx.z) * 32;  // longest causal ranges first
@@ -581,47 +587,66 @@ __global__ __launch_bounds__(256) void k_attn_split(const AttnArgs a, int nblk, 
     const int qrow = min(qi, Tq - 1);
     const float2 *cs = a.cs;
 
-    v8h qh[NS], ql[NS];
+    // the tile's query fragments (hi, lo per 16-dim step), the same for every wave: once in LDS
+    // (in the merge buffer, free until the merge), read back per key block
+    v8h *qf = (v8h *)&ored[0][0][0][0];
+    // wave p < NS / 2 prepares dim steps p and p + NS / 2 (the pair RoPE rotates together);
+    // the RMS norm's sum of squares is reduced across those waves through ssp
     {
+        constexpr int NP = NS / 2;
+        static_assert(NP <= NW, "one dim-step pair per wave");
+        float *ssp = (float *)(qf + 2 * NS * 64);
+        const bool act = wave < NP;
+        const int st0 = act ? wave : 0, st1 = st0 + NP;
         const float *qp = a.q + (int64_t)b * a.q_sb + (int64_t)qrow * a.q_st + (int64_t)h * a.q_sh + 8 * half;
-        float x[NS][8];
+        float x[2][8];
 #pragma unroll
-        for (int st = 0; st < NS; st++) {
+        for (int t = 0; t < 2; t++) {
+            const int st = t ? st1 : st0;
             const float4 u = *(const float4 *)(qp + 16 * st), w = *(const float4 *)(qp + 16 * st + 4);
-            x[st][0] = u.x, x[st][1] = u.y, x[st][2] = u.z, x[st][3] = u.w;
-            x[st][4] = w.x, x[st][5] = w.y, x[st][6] = w.z, x[st][7] = w.w;
+            x[t][0] = u.x, x[t][1] = u.y, x[t][2] = u.z, x[t][3] = u.w;
+            x[t][4] = w.x, x[t][5] = w.y, x[t][6] = w.z, x[t][7] = w.w;
         }
         if (a.qw) {
             float ss = 0.f;
 #pragma unroll
-            for (int st = 0; st < NS; st++)
+            for (int t = 0; t < 2; t++)
 #pragma unroll
-                for (int j = 0; j < 8; j++) ss += x[st][j] * x[st][j];
-            ss += __shfl_xor(ss, 32);
-            const float scale = 1.0f / sqrtf(ss / (float)HD + a.eps);
+                for (int j = 0; j < 8; j++) ss += x[t][j] * x[t][j];
+            ssp[wave * 64 + lane] = act ? ss : 0.f;
+            __syncthreads();
+            float tot = 0.f;
 #pragma unroll
-            for (int st = 0; st < NS; st++)
+            for (int w = 0; w < NP; w++) tot += ssp[w * 64 + lane] + ssp[w * 64 + (lane ^ 32)];
+            const float scale = 1.0f / sqrtf(tot / (float)HD + a.eps);
 #pragma unroll
-                for (int j = 0; j < 8; j++) x[st][j] = x[st][j] * scale * a.qw[16 * st + 8 * half + j];
+            for (int t = 0; t < 2; t++) {
+                const int st = t ? st1 : st0;
+#pragma unroll
+                for (int j = 0; j < 8; j++) x[t][j] = x[t][j] * scale * a.qw[16 * st + 8 * half + j];
+            }
         }
         if (cs) {
 #pragma unroll
-            for (int st = 0; st < NS / 2; st++)
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float2 rot = cs[(int64_t)qrow * HALF + 16 * st + 8 * half + j];
-                    const float x0 = x[st][j], x1 = x[st + NS / 2][j];
-                    x[st][j] = x0 * rot.x - x1 * rot.y;
-                    x[st + NS / 2][j] = x0 * rot.y + x1 * rot.x;
-                }
+            for (int j = 0; j < 8; j++) {
+                const float2 rot = cs[(int64_t)qrow * HALF + 16 * st0 + 8 * half + j];
+                const float x0 = x[0][j], x1 = x[1][j];
+                x[0][j] = x0 * rot.x - x1 * rot.y;
+                x[1][j] = x0 * rot.y + x1 * rot.x;
+            }
         }
+        if (act)
 #pragma unroll
-        for (int st = 0; st < NS; st++) {
+            for (int t = 0; t < 2; t++) {
+                const int st = t ? st1 : st0;
 #pragma unroll
-            for (int j = 0; j < 8; j++) x[st][j] *= qscale;
-            split8(x[st], qh[st], ql[st]);
-        }
+                for (int j = 0; j < 8; j++) x[t][j] *= qscale;
+                v8h qh, ql;
+                split8(x[t], qh, ql);
+                qf[(2 * st) * 64 + lane] = qh, qf[(2 * st + 1) * 64 + lane] = ql;
+            }
     }
+    __syncthreads();
     const _Float16 *mrow = nullptr;
     if constexpr (MASK)
         mrow = (const _Float16 *)a.mask + (int64_t)b * a.m_sb + (int64_t)h * a.m_sh + (int64_t)qrow * a.m_sq;
@@ -632,26 +657,81 @@ __global__ __launch_bounds__(256) void k_attn_split(const AttnArgs a, int nblk, 
     const int kend = causal ? min(Tk, q0 + 32) : Tk;
     const v8h *F = (const v8h *)((const _Float16 *)a.ws + (int64_t)(b * a.nkv + hk) * nblk * NFR * 512) + lane;
 
-    for (int kb = wave; kb * 32 < kend; kb += 4) {
-        float mv[16];
-        if constexpr (MASK) {
-            bool live = false;
+    // bit j: the wave's key block wave + NW j is fully masked (dead) / has an all-zero mask.
+    // Rows 16-byte aligned (m_al): lane l reads 8 keys (16 bytes) of row l / 4 and of row
+    // l / 4 + 16, coalesced; else each lane its own row's 16 keys of the block, 2 bytes at a time.
+    uint64_t dead = 0, zero = 0;
+    if constexpr (MASK) {
+        const int nj = min((kend - 32 * wave + 32 * NW - 1) / (32 * NW), 64);
+        const uint16_t *mbase = a.mask + (int64_t)b * a.m_sb + (int64_t)h * a.m_sh;
+        for (int j0 = 0; j0 < nj; j0 += 4) {
+            bool live[4], nz[4];
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
-                mv[i] = key < Tk ? (float)mrow[key] : -INFINITY;
-                live |= mv[i] != -INFINITY;
+            for (int jj = 0; jj < 4; jj++) {
+                live[jj] = false, nz[jj] = false;
+                const int kb = wave + NW * (j0 + jj);
+                if (a.m_al && kb * 32 + 32 <= Tk) {
+#pragma unroll
+                    for (int r = 0; r < 2; r++) {
+                        const int row = min(q0 + (lane >> 2) + 16 * r, Tq - 1);
+                        const uint4 u = *(const uint4 *)(mbase + (int64_t)row * a.m_sq + kb * 32 + 8 * (lane & 3));
+                        const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            // f16 -inf is 0xFC00; +-0 have no bits outside the sign
+                            live[jj] |= (w4[e] & 0xFFFFu) != 0xFC00u || (w4[e] >> 16) != 0xFC00u;
+                            nz[jj] |= (w4[e] & 0x7FFF7FFFu) != 0u;
+                        }
+                    }
+                    if (j0 + jj >= nj) live[jj] = false, nz[jj] = false;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
+                        const bool in = j0 + jj < nj && key < Tk;
+                        const float m = (float)mrow[min(key, Tk - 1)];
+                        live[jj] |= in && m != -INFINITY;
+                        nz[jj] |= in && m != 0.0f;
+                    }
+                }
             }
-            if (__ballot(live) == 0) continue;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                dead |= (uint64_t)(__ballot(live[jj]) == 0) << (j0 + jj);
+                zero |= (uint64_t)(__ballot(nz[jj]) == 0) << (j0 + jj);
+            }
+        }
+    }
+
+    for (int j = 0, kb = wave; kb * 32 < kend; j++, kb += NW) {
+        bool mixed = MASK;
+        if constexpr (MASK) {
+            if (j < 64) {
+                if ((dead >> j) & 1) continue;
+                mixed = !((zero >> j) & 1);
+            } else {  // past the classified blocks: the same test here
+                bool live = false;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
+                    live |= key < Tk && (float)mrow[min(key, Tk - 1)] != -INFINITY;
+                }
+                if (__ballot(live) == 0) continue;
+            }
         }
         const v8h *Fb = F + (int64_t)kb * NFR * 64;
         v16f s_hh = (v16f){}, s_hl = (v16f){}, s_lh = (v16f){};
+        // an address the compiler cannot see through, so the fragment reads stay in the loop
+        uint32_t qa = lds_addr32(qf) + 16u * lane;
+        asm volatile("" : "+v"(qa));
+        const __attribute__((address_space(3))) v8h *ql3 = (const __attribute__((address_space(3))) v8h *)qa;
 #pragma unroll
         for (int st = 0; st < NS; st++) {
             const v8h ah = Fb[(2 * st) * 64], al = Fb[(2 * st + 1) * 64];
-            s_hh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[st], s_hh, 0, 0, 0);
-            s_hl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ql[st], s_hl, 0, 0, 0);
-            s_lh = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[st], s_lh, 0, 0, 0);
+            const v8h qh = ql3[(2 * st) * 64], ql = ql3[(2 * st + 1) * 64];
+            s_hh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh, s_hh, 0, 0, 0);
+            s_hl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ql, s_hl, 0, 0, 0);
+            s_lh = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh, s_lh, 0, 0, 0);
         }
         v8h bh[2][NT], bl[2][NT];
 #pragma unroll
@@ -662,6 +742,25 @@ __global__ __launch_bounds__(256) void k_attn_split(const AttnArgs a, int nblk, 
                 bl[t][n] = Fb[(2 * NS + 2 * (t * NT + n) + 1) * 64];
             }
         const v16f sc = s_hh + (s_hl + s_lh);
+        v8h mh[2] = {};  // the block's mask values, as stored (f16)
+        if constexpr (MASK)
+            if (mixed) {
+                if (a.m_al && kb * 32 + 32 <= Tk) {
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const uint2 u = *(const uint2 *)(mrow + kb * 32 + 8 * g + 4 * half);
+                        const v4h hv = __builtin_bit_cast(v4h, u);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) mh[g / 2][4 * (g % 2) + e] = hv[e];
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
+                        mh[i / 8][i % 8] = mrow[min(key, Tk - 1)];  // keys past Tk: p = -inf below
+                    }
+                }
+            }
         float p[16], mblk = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
@@ -670,7 +769,8 @@ __global__ __launch_bounds__(256) void k_attn_split(const AttnArgs a, int nblk, 
                 p[i] = -INFINITY;
             } else {
                 p[i] = sc[i];
-                if constexpr (MASK) p[i] += LOG2E * mv[i];
+                if constexpr (MASK)
+                    if (mixed) p[i] += LOG2E * (float)mh[i / 8][i % 8];
             }
             mblk = fmaxf(mblk, p[i]);
         }
@@ -718,24 +818,28 @@ __global__ __launch_bounds__(256) void k_attn_split(const AttnArgs a, int nblk, 
         }
     }
 
-    // merge the four waves' partial results
+    // merge the waves' partial results: wave w reduces columns 32 (w % NT) .. + 31 of rows
+    // r = w / NT, w / NT + NW / NT, ... of the 16 accumulator rows (after every wave's last
+    // query-fragment read)
+    __syncthreads();
     if (half == 0) mls[wave][0][l32] = m_run, mls[wave][1][l32] = l_run;
 #pragma unroll
     for (int n = 0; n < NT; n++)
 #pragma unroll
         for (int r = 0; r < 16; r++) ored[wave][n][r][lane] = oacc[n][r];
     __syncthreads();
-    for (int n = wave; n < NT; n += 4) {
+    constexpr int RS = NW >= NT ? NW / NT : 1;
+    for (int n = wave % NT; n < NT; n += NW >= NT ? NT : NW) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
+        for (int r = NW >= NT ? wave / NT : 0; r < 16; r += RS) {
             const int qq = 8 * (r / 4) + 4 * half + (r % 4), q = q0 + qq;
             float mx = -INFINITY;
 #pragma unroll
-            for (int w = 0; w < 4; w++) mx = fmaxf(mx, mls[w][0][qq]);
+            for (int w = 0; w < NW; w++) mx = fmaxf(mx, mls[w][0][qq]);
             float o = 0.f, l = 0.f;
             if (mx != -INFINITY) {
 #pragma unroll
-                for (int w = 0; w < 4; w++) {
+                for (int w = 0; w < NW; w++) {
                     const float f = exp2f(mls[w][0][qq] - mx);  // 0 for a wave that saw no key
                     o += f * ored[w][n][r][lane];
                     l += f * mls[w][1][qq];
@@ -855,9 +959,19 @@ static void launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_
     if (const char *e = getenv("MQ_ATTN_SPLIT"))
         if (*e) split = atoi(e) != 0;
     if (split) {
+        // 8 waves per workgroup (half the key blocks per wave) while the grid is at most a few
+        // workgroups per CU; MQ_ATTN_SPLIT_WAVES=4/8 forces either (measurements)
         const dim3 g((unsigned)a.nq, (unsigned)a.B, (unsigned)((a.Tq + 31) / 32));
-        if (a.mask) hipLaunchKernelGGL((k_attn_split<HD, true>), g, dim3(256), 0, s, a, nblk, qscale);
-        else hipLaunchKernelGGL((k_attn_split<HD, false>), g, dim3(256), 0, s, a, nblk, qscale);
+        int nw = (int64_t)g.x * g.y * g.z <= 1024 ? 8 : 4;
+        if (const char *e = getenv("MQ_ATTN_SPLIT_WAVES"))
+            if (*e) nw = atoi(e) == 4 ? 4 : 8;
+        if (nw == 8) {
+            if (a.mask) hipLaunchKernelGGL((k_attn_split<HD, true, 8>), g, dim3(512), 0, s, a, nblk, qscale);
+            else hipLaunchKernelGGL((k_attn_split<HD, false, 8>), g, dim3(512), 0, s, a, nblk, qscale);
+        } else {
+            if (a.mask) hipLaunchKernelGGL((k_attn_split<HD, true, 4>), g, dim3(256), 0, s, a, nblk, qscale);
+            else hipLaunchKernelGGL((k_attn_split<HD, false, 4>), g, dim3(256), 0, s, a, nblk, qscale);
+        }
         return;
     }
     const dim3 ga((unsigned)((a.nq + 1) / 2), (unsigned)a.B, (unsigned)((a.Tq + 127) / 128));

@@ -356,6 +356,7 @@ struct AttnArgs {
     int64_t o_sb = 0, o_st = 0, o_sh = 0;
     const uint16_t *mask = nullptr;
     int64_t m_sb = 0, m_sh = 0, m_sq = 0;
+    bool m_al = false;  // mask pointer 16-byte aligned, m_sb / m_sh / m_sq multiples of 8
     int B = 0, Tq = 0, Tk = 0, nq = 0, nkv = 0, hd = 0;
     float scale = 1.0f;
     int causal = 0;

@@ -1242,6 +1242,7 @@ static int flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, cons
         a.m_sq = mask->nb[1] / 2;
         a.m_sh = mask->ne[2] == 1 ? 0 : mask->nb[2] / 2;
         a.m_sb = mask->ne[3] == 1 ? 0 : mask->nb[3] / 2;
+        a.m_al = (uintptr_t)mask->data % 16 == 0 && a.m_sq % 8 == 0 && a.m_sh % 8 == 0 && a.m_sb % 8 == 0;
     }
     a.B = (int)q->ne[3], a.Tq = (int)q->ne[1], a.Tk = (int)k->ne[1];
     a.nq = (int)q->ne[2], a.nkv = (int)k->ne[2], a.hd = (int)q->ne[0];

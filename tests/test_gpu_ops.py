@@ -446,6 +446,41 @@ def test_flash_attn_general_mask_and_empty_rows(attn_form):
     assert np.abs(got - ref).max() / np.abs(ref).max() <= 2e-5
 
 
+@pytest.mark.parametrize("rows", ["aligned", "unaligned"])
+@pytest.mark.parametrize("waves", ["4", "8"])
+@pytest.mark.parametrize("hd,nh,nkv,Tq,Tk", [(128, 4, 2, 300, 300), (128, 2, 1, 40, 16500), (64, 4, 4, 100, 2100)])
+def test_flash_attn_mask_block_classes(monkeypatch, rows, waves, hd, nh, nkv, Tq, Tk):
+    """The split-key kernel's mask block classes: 32 x 32 blocks fully masked (skipped), all zero
+    (run unmasked) and mixed (a causal band, finite values, a partly masked band), at 4 and 8
+    waves per workgroup, with key blocks past the 64 each wave classifies up front (Tk 16500:
+    516 blocks, 129 per wave at 4 waves, 65 at 8); mask rows 16-byte aligned (vector reads) or
+    not (2-byte reads)."""
+    monkeypatch.setenv("MQ_ATTN_SPLIT", "1")
+    monkeypatch.setenv("MQ_ATTN_SPLIT_WAVES", waves)
+    rng = _rng(hd + Tq + Tk)
+    qx = rng.standard_normal((1, Tq, nh, hd)).astype(np.float32)
+    kx, vx = (rng.standard_normal((1, Tk, nkv, hd)).astype(np.float32) for _ in range(2))
+    qpos = np.arange(Tq)[:, None] + (Tk - Tq)
+    mask = np.where(np.arange(Tk)[None, :] > qpos, -np.inf, 0.0)  # causal, query i at key Tk - Tq + i
+    mask[:, 64:100] += rng.standard_normal((Tq, 36)) * 2  # finite values: mixed blocks
+    mask[:, Tk // 2:Tk // 2 + 70] = -np.inf  # fully masked blocks (and two partly masked)
+    mask[::3, Tk - 40:Tk - 20] = -np.inf
+    if Tk > 16384:
+        mask[:, 16400:16420] += rng.standard_normal((Tq, 20))  # finite values past block 512
+    mask = mask.astype(np.float16)[None, None]
+    stride = (Tk + 7) // 8 * 8 + (rows == "unaligned")
+    padded = np.full((1, 1, Tq, stride), np.nan, np.float16)
+    padded[..., :Tk] = mask
+    q, k, v = (_cuda(x).permute(0, 2, 1, 3) for x in (qx, kx, vx))
+    out = _t().empty((1, Tq, nh, hd), dtype=_t().float32, device="cuda")
+    scale = 1.0 / np.sqrt(hd)
+    _flash(q, k, v, _cuda(padded)[..., :Tk], scale, out)
+    ref = _attn64(qx.transpose(0, 2, 1, 3), kx.transpose(0, 2, 1, 3), vx.transpose(0, 2, 1, 3), mask, scale)
+    got = host(out)
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= 2e-5
+
+
 def test_op_rejections_name_the_problem():
     L = mq.lib()
     x = _t().zeros((4, 48), dtype=_t().float32, device="cuda")
