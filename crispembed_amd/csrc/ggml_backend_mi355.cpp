@@ -91,6 +91,18 @@ struct BackendCtx {
     hipGraphExec_t gexec = nullptr;
     uint64_t gkey = 0, seen_key = 0;
     bool capturing = false;
+    // q / k norm and rotation left to the attention: FLASH_ATTN_EXT node qk_fa reads q and k as
+    // qk_q / qk_k (the inputs of their RMS_NORM -> MUL -> ROPE chains) with the norm weights
+    // qk_qw / qk_kw and the rope cache cs
+    const ggml_tensor *qk_fa = nullptr;
+    mq_view qk_q{}, qk_k{};
+    const float *qk_qw = nullptr, *qk_kw = nullptr;
+    float qk_eps = 0.f;
+    // the rope cache (cs_bytes of device memory) of the graph being computed, for the ROPE
+    // parameters, positions and frequency factors cs_key names (empty: none yet)
+    float *cs = nullptr;
+    size_t cs_bytes = 0;
+    std::vector<int64_t> cs_key;
 };
 
 std::vector<DeviceCtx *> &devices();
@@ -325,6 +337,7 @@ void be_free(ggml_backend_t be) {
         (void)hipStreamSynchronize(c->stream);
         if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
         if (c->ws) (void)hipFree(c->ws);
+        if (c->cs) (void)hipFree(c->cs);
         (void)hipStreamDestroy(c->stream);
     }
     delete c;
@@ -520,6 +533,147 @@ int try_fuse_rows_sum(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_st
     if (rc != 0) return 0;  // a layout this op does not take: the nodes run on their own
     st = GGML_STATUS_SUCCESS;
     return used;
+}
+
+bool overlaps(const ggml_tensor *a, const ggml_tensor *b);
+const ggml_tensor *view_root(const ggml_tensor *t);
+
+// RMS_NORM -> MUL(w [hd]) -> ROPE (NEOX over all hd dimensions) at node j, each result read only
+// by the next node: the decoder's per-head q or k norm and rotation.  Returns the ROPE node.
+ggml_tensor *qk_chain(ggml_cgraph *cg, int j, int n) {
+    if (j + 2 >= n) return nullptr;
+    ggml_tensor *nrm = ggml_graph_node(cg, j), *mul = ggml_graph_node(cg, j + 1), *rp = ggml_graph_node(cg, j + 2);
+    if (nrm->op != GGML_OP_RMS_NORM || mul->op != GGML_OP_MUL || rp->op != GGML_OP_ROPE) return nullptr;
+    if (mul->src[0] != nrm || rp->src[0] != mul || !feeds_only_next(cg, j) || !feeds_only_next(cg, j + 1))
+        return nullptr;
+    const int64_t hd = nrm->ne[0];
+    if ((hd != 32 && hd != 64 && hd != 128) || rp->op_params[1] != hd || rp->op_params[2] != MQ_ROPE_NEOX)
+        return nullptr;
+    if (nrm->src[0]->type != GGML_TYPE_F32 || !is_row_vector(mul->src[1], hd) ||
+        ((uintptr_t)mul->src[1]->data & 3) || (rp->flags & GGML_TENSOR_FLAG_OUTPUT))
+        return nullptr;
+    return rp;
+}
+
+// ggml_permute(t, 0, 2, 1, 3) of exactly t (judged by shape and strides)
+bool is_head_permute(const ggml_tensor *p, const ggml_tensor *t) {
+    return p && p->op == GGML_OP_PERMUTE && p->view_src == t && p->view_offs == 0 && p->ne[0] == t->ne[0] &&
+           p->ne[1] == t->ne[2] && p->ne[2] == t->ne[1] && p->ne[3] == t->ne[3] && p->nb[0] == t->nb[0] &&
+           p->nb[1] == t->nb[2] && p->nb[2] == t->nb[1] && p->nb[3] == t->nb[3];
+}
+
+// The q chain (qk_chain) at node i whose rotated q reaches a FLASH_ATTN_EXT only as its q
+// (through the head permute), with k's chain further on feeding the same attention as its k,
+// both with the same positions, ROPE parameters and eps: the six nodes are left to the
+// attention (mq_op_flash_attn_qk_norm_rope reads q and k before the norms), and the rope cache
+// of the positions is computed here (once per graph for the same positions and parameters).
+// Returns the nodes consumed at i (3; k's are marked in done) or 0.
+int try_defer_qk_norm_rope(BackendCtx *c, ggml_cgraph *cg, int i, int n, std::vector<char> &done) {
+    ggml_tensor *rq = qk_chain(cg, i, n);
+    if (!rq || c->qk_fa) return 0;
+    int f = i + 3;
+    while (f < n && ggml_graph_node(cg, f)->op != GGML_OP_FLASH_ATTN_EXT) f++;
+    if (f >= n) return 0;
+    ggml_tensor *fa = ggml_graph_node(cg, f);
+    if (!is_head_permute(fa->src[0], rq)) return 0;
+    ggml_tensor *rk = nullptr;
+    int jk = i + 3;
+    for (; jk < f; jk++)
+        if ((rk = qk_chain(cg, jk, n)) && is_head_permute(fa->src[1], rk)) break;
+    if (jk >= f) return 0;
+    const ggml_tensor *nq = ggml_graph_node(cg, i), *nk = ggml_graph_node(cg, jk);
+    const ggml_tensor *xq = nq->src[0], *xk = nk->src[0];
+    if (std::memcmp(rq->op_params, rk->op_params, 15 * sizeof(int32_t)) != 0 || rq->src[1] != rk->src[1] ||
+        rq->src[2] != rk->src[2] || op_param_f32(nq, 0) != op_param_f32(nk, 0) || fa->src[0]->ne[1] != fa->src[1]->ne[1])
+        return 0;
+    // nothing else reads the rotated q or k; no node that runs before the attention, nor the
+    // attention's result, overwrites the chains' inputs (their buffers are free for reuse once
+    // the RMS_NORM nodes have run, as the graph's allocator sees it)
+    for (int u = i + 3; u < n; u++) {
+        const ggml_tensor *t = ggml_graph_node(cg, u);
+        if (t == fa || is_view_op(t->op)) continue;
+        for (int si = 0; si < GGML_MAX_SRC; si++) {
+            const ggml_tensor *r = view_root(t->src[si]);
+            if (r && (r == rq || r == rk)) return 0;
+        }
+        // (k's chain is skipped; the products that compute q's and k's inputs may still follow)
+        if (u < f && !(u >= jk && u < jk + 3) && !ggml_is_empty(t) &&
+            ((t != view_root(xq) && overlaps(t, xq)) || (t != view_root(xk) && overlaps(t, xk))))
+            return 0;
+    }
+    if (overlaps(fa, xq) || overlaps(fa, xk)) return 0;
+    // q and k as the attention takes them: [hd, T, n_head, B], the head permute of the inputs
+    auto permuted = [](const ggml_tensor *x) {
+        mq_view v = view_of(x);
+        std::swap(v.ne[1], v.ne[2]);
+        std::swap(v.nb[1], v.nb[2]);
+        return v;
+    };
+    const mq_view q = permuted(xq), k = permuted(xk), v = view_of(fa->src[2]), d = view_of(fa);
+    mq_view m{};
+    if (fa->src[3]) m = view_of(fa->src[3]);
+    if (!mq_op_supported(MQ_OP_FLASH_ATTN, 0, &q, &k, &v, fa->src[3] ? &m : nullptr, &d)) return 0;
+    // the rope cache: T positions x hd floats
+    const int64_t T = rq->src[1]->ne[0], hd = nq->ne[0];
+    if (T != q.ne[1]) return 0;
+    std::vector<int64_t> key(rq->op_params, rq->op_params + 15);
+    key.push_back((int64_t)(uintptr_t)rq->src[1]->data);
+    key.push_back((int64_t)(uintptr_t)(rq->src[2] ? rq->src[2]->data : nullptr));
+    key.push_back(T);
+    if (key != c->cs_key) {
+        const size_t need = (size_t)T * hd * sizeof(float);
+        if (need > c->cs_bytes) {
+            if (c->capturing) return 0;  // no allocation under capture: the nodes run on their own
+            hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+            if (c->gexec) {  // the captured graph holds the old table's address
+                (void)hipGraphExecDestroy(c->gexec);
+                c->gexec = nullptr;
+                c->gkey = c->seen_key = 0;
+            }
+            if (c->cs) (void)hipFree(c->cs);
+            c->cs = nullptr, c->cs_bytes = 0;
+            if (hipMalloc((void **)&c->cs, need) != hipSuccess) {
+                (void)hipGetLastError();
+                c->cs = nullptr;
+                return 0;
+            }
+            c->cs_bytes = need;
+        }
+        const mq_view pos = view_of(rq->src[1]);
+        mq_view ff{};
+        if (rq->src[2]) ff = view_of(rq->src[2]);
+        const int32_t *ip = rq->op_params;
+        if (mq_op_rope_cache(&pos, rq->src[2] ? &ff : nullptr, ip[1], ip[4], op_param_f32(rq, 5), op_param_f32(rq, 6),
+                             op_param_f32(rq, 7), op_param_f32(rq, 8), op_param_f32(rq, 9), op_param_f32(rq, 10), c->cs,
+                             c->stream) != 0)
+            return 0;
+        c->cs_key = key;
+    }
+    c->qk_fa = fa;
+    c->qk_q = q, c->qk_k = k;
+    c->qk_qw = (const float *)ggml_graph_node(cg, i + 1)->src[1]->data;
+    c->qk_kw = (const float *)ggml_graph_node(cg, jk + 1)->src[1]->data;
+    c->qk_eps = op_param_f32(nq, 0);
+    done[jk] = done[jk + 1] = done[jk + 2] = 1;
+    return 3;
+}
+
+// The attention of FLASH_ATTN_EXT node fa: mq_op_flash_attn_qk_norm_rope when its q and k chains
+// were left to it, else mq_op_flash_attn_ex on its operands.
+int attn_call(BackendCtx *c, const ggml_tensor *fa, void *ws, size_t ws_bytes, void *act, size_t act_bytes,
+              int flags) {
+    const mq_view v = view_of(fa->src[2]), d = view_of(fa);
+    mq_view m{};
+    if (fa->src[3]) m = view_of(fa->src[3]);
+    if (c->qk_fa == fa) {
+        c->qk_fa = nullptr;
+        return mq_op_flash_attn_qk_norm_rope(&c->qk_q, &c->qk_k, &v, fa->src[3] ? &m : nullptr, &d,
+                                             op_param_f32(fa, 0), c->qk_qw, c->qk_kw, c->qk_eps, c->cs, ws, ws_bytes,
+                                             act, act_bytes, c->stream);
+    }
+    const mq_view q = view_of(fa->src[0]), k = view_of(fa->src[1]);
+    return mq_op_flash_attn_ex(&q, &k, &v, fa->src[3] ? &m : nullptr, &d, op_param_f32(fa, 0), ws, ws_bytes, act,
+                               act_bytes, flags, c->stream);
 }
 
 // [ADD(x, r) ->] NORM|RMS_NORM -> MUL(w) [-> ADD(b)] starting at node i: returns the number of
@@ -800,9 +954,7 @@ int try_fuse_attn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status
         node->nb[2] != (size_t)K * sizeof(float) || node->nb[3] != node->nb[2] * (size_t)node->ne[2])
         return 0;
     if (mq_mul_mat_path(MQ_TYPE_Q8_0, mm->src[0]->ne[1], K, M) != MQ_PATH_GEMM) return 0;
-    const mq_view q = view_of(node->src[0]), k = view_of(node->src[1]), v = view_of(node->src[2]), d = view_of(node);
-    mq_view m{};
-    if (node->src[3]) m = view_of(node->src[3]);
+    const mq_view k = view_of(node->src[1]);
     const size_t act = (mq_workspace_bytes(MQ_TYPE_Q8_0, M, K) + 255) & ~(size_t)255;
     const bool ready = c->kv_ready_for == node;  // K/V fragments stored by the q/k/v GEMM
     const size_t foff = ready ? c->kv_frag_off : act;
@@ -812,9 +964,8 @@ int try_fuse_attn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status
         st = GGML_STATUS_ALLOC_FAILED;
         return 1;
     }
-    const int rc = mq_op_flash_attn_ex(&q, &k, &v, node->src[3] ? &m : nullptr, &d, op_param_f32(node, 0),
-                                       (char *)c->ws + foff, c->ws_bytes - foff, c->ws, act,
-                                       ready ? MQ_ATTN_KV_READY : 0, c->stream);
+    const int rc = attn_call(c, node, (char *)c->ws + foff, c->ws_bytes - foff, c->ws, act,
+                             ready ? MQ_ATTN_KV_READY : 0);
     if (rc == 0) c->ws_x = x, c->ws_type = MQ_TYPE_Q8_0, c->ws_m = M, c->ws_k = K, c->ws_path = MQ_PATH_GEMM;
     st = op_status(rc, node);
     return 1;
@@ -1062,18 +1213,14 @@ enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node) {
                              node);
         }
         case GGML_OP_FLASH_ATTN_EXT: {
-            const mq_view q = view_of(node->src[0]), k = view_of(node->src[1]), v = view_of(node->src[2]),
-                          d = view_of(node);
-            mq_view m{};
-            if (node->src[3]) m = view_of(node->src[3]);
+            const mq_view k = view_of(node->src[1]);
             const bool ready = c->kv_ready_for == node;  // K/V fragments stored by the q/k/v GEMM
             const size_t foff = ready ? c->kv_frag_off : 0;
             c->kv_ready_for = nullptr;
             c->ws_x = nullptr;
             if (!ensure_ws(c, foff + mq_op_flash_attn_workspace_bytes(&k))) return GGML_STATUS_ALLOC_FAILED;
-            return op_status(mq_op_flash_attn_ex(&q, &k, &v, node->src[3] ? &m : nullptr, &d, op_param_f32(node, 0),
-                                                 (char *)c->ws + foff, c->ws_bytes - foff, nullptr, 0,
-                                                 ready ? MQ_ATTN_KV_READY : 0, c->stream),
+            return op_status(attn_call(c, node, (char *)c->ws + foff, c->ws_bytes - foff, nullptr, 0,
+                                       ready ? MQ_ATTN_KV_READY : 0),
                              node);
         }
         default:
@@ -1088,6 +1235,8 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
     const bool fuse = std::getenv("MQ_GGML_NO_FUSION") == nullptr;
     c->ws_x = nullptr;  // the inputs may have been rewritten since the last graph
     c->kv_ready_for = nullptr;
+    c->qk_fa = nullptr;
+    c->cs_key.clear();  // and the positions
     std::vector<char> done(n, 0);  // nodes already computed as part of an earlier group
     for (int i = 0; i < n; i++) {
         ggml_tensor *node = ggml_graph_node(cg, i);
@@ -1107,7 +1256,10 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
                     if (!used) used = try_group_mul_mat(c, cg, i, n, done, st);
                     break;
                 case GGML_OP_NORM:
-                case GGML_OP_RMS_NORM: used = try_fuse_norm(c, cg, i, n, st); break;
+                case GGML_OP_RMS_NORM:
+                    if (!std::getenv("MQ_GGML_NO_QK_ATTN")) used = try_defer_qk_norm_rope(c, cg, i, n, done);
+                    if (!used) used = try_fuse_norm(c, cg, i, n, st);
+                    break;
                 case GGML_OP_FLASH_ATTN_EXT: used = try_fuse_attn(c, cg, i, n, st); break;
                 case GGML_OP_GET_ROWS: used = try_fuse_rows_sum(c, cg, i, n, st); break;
                 case GGML_OP_UNARY: used = try_fuse_silu_mul(c, cg, i, n, done, st); break;

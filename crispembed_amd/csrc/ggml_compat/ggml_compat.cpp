@@ -335,7 +335,9 @@ extern "C" struct ggml_tensor *ggml_permute(struct ggml_context *ctx, struct ggm
         ne[ax[i]] = a->ne[i];
         nb[ax[i]] = a->nb[i];
     }
-    return view_of(ctx, a, ne, nb, 0, GGML_OP_PERMUTE);
+    ggml_tensor *r = view_of(ctx, a, ne, nb, 0, GGML_OP_PERMUTE);
+    std::memcpy(r->op_params, ax, sizeof(ax));  // the axes, as ggml records them
+    return r;
 }
 
 extern "C" struct ggml_tensor *ggml_cont(struct ggml_context *ctx, struct ggml_tensor *a) {

@@ -607,6 +607,10 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_split(const AttnArgs a, int
             x[t][0] = u.x, x[t][1] = u.y, x[t][2] = u.z, x[t][3] = u.w;
             x[t][4] = w.x, x[t][5] = w.y, x[t][6] = w.z, x[t][7] = w.w;
         }
+        float2 rot[8];  // loaded with q, before the norm's reduction
+        if (cs)
+#pragma unroll
+            for (int j = 0; j < 8; j++) rot[j] = cs[(int64_t)qrow * HALF + 16 * st0 + 8 * half + j];
         if (a.qw) {
             float ss = 0.f;
 #pragma unroll
@@ -629,10 +633,9 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_split(const AttnArgs a, int
         if (cs) {
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const float2 rot = cs[(int64_t)qrow * HALF + 16 * st0 + 8 * half + j];
                 const float x0 = x[0][j], x1 = x[1][j];
-                x[0][j] = x0 * rot.x - x1 * rot.y;
-                x[1][j] = x0 * rot.y + x1 * rot.x;
+                x[0][j] = x0 * rot[j].x - x1 * rot[j].y;
+                x[1][j] = x0 * rot[j].y + x1 * rot[j].x;
             }
         }
         if (act)

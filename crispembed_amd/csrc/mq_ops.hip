@@ -467,36 +467,60 @@ __global__ __launch_bounds__(256) void k_rope(const DV x, const DV pos, const fl
 // first RMS-normed and multiplied by w (ggml_rms_norm, ggml_mul) as k_norm computes it for
 // ne0 = 128 (lane j holds elements j and j + 64, the same sum order), so the result equals
 // mq_op_norm followed by mq_op_rope bit for bit (NEOX, n_dims 128 only).
+// (cos, sin) x mscale of rotation pair j at position p, as the rope cache computes them:
+// theta = p * theta_scale^j (j rounded products), / freq_factor[j], YaRN's ramp mix.
+__device__ __forceinline__ float2 rope_cs(const RopeParams &rp, int32_t p, int j, const float *__restrict__ ff) {
+    float theta = (float)p;
+    for (int k = 0; k < j; k++) theta *= rp.theta_scale;
+    const float extrap = ff ? theta / ff[j] : theta;
+    float th = rp.freq_scale * extrap, mscale = rp.attn_factor;
+    if (rp.ext_factor != 0.0f) {
+        const float y = ((float)j - rp.corr_lo) / fmaxf(0.001f, rp.corr_hi - rp.corr_lo);
+        const float mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * rp.ext_factor;
+        th = th * (1.0f - mix) + extrap * mix;
+        mscale *= 1.0f + 0.1f * logf(1.0f / rp.freq_scale);
+    }
+    return make_float2(cosf(th) * mscale, sinf(th) * mscale);
+}
+
+// The table of rope_cs for positions pos[0 .. T-1]: cs[t * n_dims / 2 + j], one wave per position.
+__global__ __launch_bounds__(64) void k_rope_cache(const DV pos, const float *__restrict__ ff, const RopeParams rp,
+                                                   float2 *__restrict__ cs) {
+    const int t = blockIdx.x, j = threadIdx.x, hn = rp.n_dims / 2;
+    if (j < hn) cs[(int64_t)t * hn + j] = rope_cs(rp, *(const int32_t *)(pos.p + t * pos.nb[0]), j, ff);
+}
+
 template <int MODE, bool NORM>
 __global__ __launch_bounds__(256) void k_rope_rows(const DV x, const DV pos, const float *__restrict__ ff, const DV d,
                                                    const RopeParams rp, const float *__restrict__ w, float eps) {
     __shared__ float cs[2][64];
     const int64_t i2 = blockIdx.x % x.ne[2], i3 = blockIdx.x / x.ne[2];
     const int hn = rp.n_dims / 2;
-    if ((int)threadIdx.x < hn) {
-        const int j = threadIdx.x;
-        float theta = (float)*(const int32_t *)(pos.p + i2 * pos.nb[0]);
-        for (int k = 0; k < j; k++) theta *= rp.theta_scale;
-        const float extrap = ff ? theta / ff[j] : theta;
-        float th = rp.freq_scale * extrap, mscale = rp.attn_factor;
-        if (rp.ext_factor != 0.0f) {
-            const float y = ((float)j - rp.corr_lo) / fmaxf(0.001f, rp.corr_hi - rp.corr_lo);
-            const float mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * rp.ext_factor;
-            th = th * (1.0f - mix) + extrap * mix;
-            mscale *= 1.0f + 0.1f * logf(1.0f / rp.freq_scale);
-        }
-        cs[0][j] = cosf(th) * mscale;
-        cs[1][j] = sinf(th) * mscale;
-    }
-    __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const bool on = lane < hn;
-    const float c = on ? cs[0][lane] : 0.f, sn = on ? cs[1][lane] : 0.f;
     const int e0 = MODE == MQ_ROPE_NEOX ? lane : 2 * lane, e1 = MODE == MQ_ROPE_NEOX ? lane + hn : 2 * lane + 1;
-    for (int64_t i1 = wave; i1 < x.ne[1]; i1 += 4) {
-        const float *xr = (const float *)(x.p + off3(x, i1, i2, i3));
+    // the wave's first RU rows are loaded before the angles are computed, so the two overlap
+    constexpr int RU = 4;
+    float a[RU], b[RU];
+#pragma unroll
+    for (int u = 0; u < RU; u++) {
+        const int64_t i1 = wave + 4 * u;
+        a[u] = 0.f, b[u] = 0.f;
+        if (on && i1 < x.ne[1]) {
+            const float *xr = (const float *)(x.p + off3(x, i1, i2, i3));
+            a[u] = xr[e0], b[u] = xr[e1];
+        }
+    }
+    if ((int)threadIdx.x < hn) {
+        const float2 r = rope_cs(rp, *(const int32_t *)(pos.p + i2 * pos.nb[0]), threadIdx.x, ff);
+        cs[0][threadIdx.x] = r.x;
+        cs[1][threadIdx.x] = r.y;
+    }
+    // LDS only: the row loads above stay in flight across the barrier
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const float c = on ? cs[0][lane] : 0.f, sn = on ? cs[1][lane] : 0.f;
+    auto row = [&](int64_t i1, float a, float b) {
         float *dr = (float *)(d.p + off3(d, i1, i2, i3));
-        float a = on ? xr[e0] : 0.f, b = on ? xr[e1] : 0.f;
         if constexpr (NORM) {
             float s = 0.f;
             s += a * a;
@@ -510,6 +534,13 @@ __global__ __launch_bounds__(256) void k_rope_rows(const DV x, const DV pos, con
             dr[e0] = a * c - b * sn;
             dr[e1] = a * sn + b * c;
         }
+    };
+#pragma unroll
+    for (int u = 0; u < RU; u++)
+        if (wave + 4 * u < x.ne[1]) row(wave + 4 * u, a[u], b[u]);
+    for (int64_t i1 = wave + 4 * RU; i1 < x.ne[1]; i1 += 4) {
+        const float *xr = (const float *)(x.p + off3(x, i1, i2, i3));
+        row(i1, on ? xr[e0] : 0.f, on ? xr[e1] : 0.f);
     }
 }
 
@@ -1221,11 +1252,24 @@ extern "C" size_t mq_op_flash_attn_workspace_bytes(const mq_view *k) {
     return attn_workspace_bytes((int)k->ne[3], (int)k->ne[1], (int)k->ne[2], (int)k->ne[0]);
 }
 
+// qk (optional): the per-head RMS norm x weight and NEOX rotation of q and k applied as the
+// attention reads them (q_w / k_w: head_dim floats; cs: (cos, sin) x mscale of position t and
+// pair j at cs[2 (t head_dim / 2 + j)], t over the Tq = Tk positions).
+struct QkNormRope {
+    const float *q_w, *k_w, *cs;
+    float eps;
+};
+
 static int flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask, const mq_view *dst,
                       float scale, void *workspace, size_t workspace_bytes, void *act_ws, size_t act_ws_bytes,
-                      int flags, void *stream) {
+                      int flags, void *stream, const QkNormRope *qk = nullptr) {
     if (const char *e = check_flash(q, k, v, mask, dst)) return fail(e);
     if (!have_data({q, k, v, mask, dst})) return fail("missing data pointer");
+    if (qk) {
+        if (!qk->q_w || !qk->k_w || !qk->cs) return fail("flash_attn_qk_norm_rope: missing data pointer");
+        if (flags & MQ_ATTN_KV_READY) return fail("flash_attn_qk_norm_rope: K/V fragments computed elsewhere");
+        if (q->ne[1] != k->ne[1]) return fail("flash_attn_qk_norm_rope: q and k must share the positions (Tq = Tk)");
+    }
     const size_t need = mq_op_flash_attn_workspace_bytes(k);
     if (!workspace || ((uintptr_t)workspace & 15) != 0 || workspace_bytes < need)
         return set_error(MQ_EINVAL, "mq_op_flash_attn: workspace of %zu bytes (16-byte aligned) needed, %zu given",
@@ -1249,6 +1293,7 @@ static int flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, cons
     a.scale = scale;
     a.ws = workspace;
     a.kv_ready = (flags & MQ_ATTN_KV_READY) != 0;
+    if (qk) a.qw = qk->q_w, a.kw = qk->k_w, a.eps = qk->eps, a.cs = (const float2 *)qk->cs;
     if (act_ws) {
         const int64_t K = dst->ne[0] * dst->ne[1], rows = dst->ne[2] * dst->ne[3];
         if (K % 128 != 0 || dst->nb[1] != (size_t)dst->ne[0] * 4 || dst->nb[2] != (size_t)K * 4 ||
@@ -1282,6 +1327,34 @@ extern "C" int mq_op_flash_attn_ex(const mq_view *q, const mq_view *k, const mq_
     if (flags & ~MQ_ATTN_KV_READY) return set_error(MQ_EINVAL, "mq_op_flash_attn_ex: unknown flags");
     return flash_attn(q, k, v, mask, dst, scale, workspace, workspace_bytes, act_workspace, act_workspace_bytes, flags,
                       stream);
+}
+
+extern "C" int mq_op_flash_attn_qk_norm_rope(const mq_view *q, const mq_view *k, const mq_view *v,
+                                             const mq_view *mask, const mq_view *dst, float scale, const float *q_norm_w,
+                                             const float *k_norm_w, float eps, const float *cs, void *workspace,
+                                             size_t workspace_bytes, void *act_workspace, size_t act_workspace_bytes,
+                                             void *stream) {
+    const QkNormRope qk{q_norm_w, k_norm_w, cs, eps};
+    return flash_attn(q, k, v, mask, dst, scale, workspace, workspace_bytes, act_workspace, act_workspace_bytes, 0,
+                      stream, &qk);
+}
+
+extern "C" int mq_op_rope_cache(const mq_view *pos, const mq_view *freq_factors, int n_dims, int n_ctx_orig,
+                                float freq_base, float freq_scale, float ext_factor, float attn_factor,
+                                float beta_fast, float beta_slow, float *cs, void *stream) {
+    if (!pos || !shape_ok(pos) || pos->type != MQ_TYPE_I32 || pos->ne[1] != 1 || pos->ne[2] != 1 || pos->ne[3] != 1)
+        return fail("rope_cache: pos must be I32 [T]");
+    if (n_dims <= 0 || n_dims % 2 || n_dims > 128) return fail("rope_cache: n_dims must be even, at most 128");
+    const mq_view *ff = freq_factors;
+    if (ff && (!shape_ok(ff) || ff->type != MQ_TYPE_F32 || ff->nb[0] != 4 || ff->ne[0] < n_dims / 2))
+        return fail("rope_cache: freq_factors must be F32 [n_dims/2]");
+    if (!have_data({pos, ff}) || !cs) return fail("missing data pointer");
+    if (pos->ne[0] > INT32_MAX) return fail("rope_cache: too many positions");
+    const RopeParams rp = rope_params(n_dims, MQ_ROPE_NEOX, n_ctx_orig, freq_base, freq_scale, ext_factor,
+                                      attn_factor, beta_fast, beta_slow);
+    hipLaunchKernelGGL(k_rope_cache, dim3((unsigned)pos->ne[0]), dim3(64), 0, (hipStream_t)stream, dv(pos),
+                       ff ? (const float *)ff->data : nullptr, rp, (float2 *)cs);
+    return hip_rc(hipGetLastError(), "rope_cache");
 }
 
 extern "C" int mq_op_supported(int op, int sub, const mq_view *s0, const mq_view *s1, const mq_view *s2,

@@ -221,7 +221,10 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
 // ---------------------------------------------------------------------------
 enum { TQ_Q8_0 = 0, TQ_Q8_K = 1, TQ_F16 = 2 };
 
-template <int FMT, int VARIANT, bool VEC4>
+// RPW rows per wave: 8 (a workgroup per 32-row tile and CB-byte column block) or 2 (four
+// workgroups per tile, rows 8 q .. 8 q + 7 in workgroup q, each writing only its rows' 16-byte
+// units of the fragments, scales and min-term halves: small inputs spread over 4x the CUs).
+template <int FMT, int VARIANT, bool VEC4, int RPW = 8>
 __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict__ x, int64_t ldx,
                                                         int8_t *__restrict__ xq, float *__restrict__ xd,
                                                         _Float16 *__restrict__ xmin, int64_t m, int64_t k,
@@ -239,11 +242,14 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
     __shared__ __attribute__((aligned(16))) _Float16 msh[FMT == TQ_Q8_K ? 512 : 8];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t ncb = kb_pad / CB;
-    const int64_t rt = blockIdx.x / ncb, cb = blockIdx.x - rt * ncb;
+    const int64_t unit = RPW == 8 ? blockIdx.x : blockIdx.x >> 2;
+    const int64_t rt = unit / ncb, cb = unit - rt * ncb;
+    const int rbase = RPW == 8 ? 0 : 8 * (blockIdx.x & 3);  // the workgroup's first row in the tile
     const int sub = lane % LPR, rsub = lane / LPR;
     const int kbyte = sub * 4 * BPV;                    // byte of this lane's 4 values within CB
     const int c = kbyte >> 5, cbyte = kbyte & 31;       // fragment, byte within the 32-byte chunk
-    constexpr int NIT = 8 / RPI;                        // rows per lane
+    static_assert(RPW == 8 || RPW == 2, "8 or 2 rows per wave");
+    constexpr int NIT = RPW / RPI;                      // rows per lane
     const int64_t kv = (cb * CB + kbyte) / BPV;         // first value index of this lane
     float4 vin[NIT];                                    // every load in flight before any math
     if (pre == MQ_PRE_NONE && bias == nullptr) {
@@ -251,21 +257,21 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
         // loop the compiler no longer issues all NIT loads before the first use
 #pragma unroll
         for (int it = 0; it < NIT; it++) {
-            const int64_t row = rt * 32 + wave * 8 + it * RPI + rsub;
+            const int64_t row = rt * 32 + rbase + wave * RPW + it * RPI + rsub;
             vin[it] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (row < m && kv < k) vin[it] = load4<VEC4>(x + row * ldx + kv);
         }
     } else {
 #pragma unroll
         for (int it = 0; it < NIT; it++) {
-            const int64_t row = rt * 32 + wave * 8 + it * RPI + rsub;
+            const int64_t row = rt * 32 + rbase + wave * RPW + it * RPI + rsub;
             vin[it] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (row < m && kv < k) vin[it] = pre_load<VEC4>(x + row * ldx + kv, pre, bias, kv, uoff);
         }
     }
 #pragma unroll
     for (int it = 0; it < NIT; it++) {
-        const int r = wave * 8 + it * RPI + rsub;       // row within the tile
+        const int r = rbase + wave * RPW + it * RPI + rsub;  // row within the tile
         const float4 v = vin[it];
         int8_t *dst = frag + c * FST + ((r + 32 * (cbyte >> 4)) << 4) + (cbyte & 15);
         if constexpr (FMT == TQ_F16) {
@@ -293,17 +299,35 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
     }
     __syncthreads();
     const int t = threadIdx.x;
+    if constexpr (RPW == 8) {
 #pragma unroll
-    for (int p = t; p < NCH * 64; p += 256) {
-        const int f = p >> 6, L = p & 63;
-        const int4 val = *(const int4 *)(frag + f * FST + L * 16);
-        *(int4 *)(xq + ((rt * (kb_pad >> 5) + cb * NCH + f) << 10) + L * 16) = val;
-    }
-    if constexpr (NSC > 0) {
-        if (t < NSC * 32) xd[(cb * NSC + (t >> 5)) * m_pad + rt * 32 + (t & 31)] = dsh[t >> 5][t & 31];
-    }
-    if constexpr (FMT == TQ_Q8_K) {
-        if (t < 64) ((int4 *)(xmin + ((rt * ncb + cb) << 9)))[t] = ((const int4 *)msh)[t];
+        for (int p = t; p < NCH * 64; p += 256) {
+            const int f = p >> 6, L = p & 63;
+            const int4 val = *(const int4 *)(frag + f * FST + L * 16);
+            *(int4 *)(xq + ((rt * (kb_pad >> 5) + cb * NCH + f) << 10) + L * 16) = val;
+        }
+        if constexpr (NSC > 0) {
+            if (t < NSC * 32) xd[(cb * NSC + (t >> 5)) * m_pad + rt * 32 + (t & 31)] = dsh[t >> 5][t & 31];
+        }
+        if constexpr (FMT == TQ_Q8_K) {
+            if (t < 64) ((int4 *)(xmin + ((rt * ncb + cb) << 9)))[t] = ((const int4 *)msh)[t];
+        }
+    } else {
+        // the units of rows rbase .. rbase + 7: lanes rbase + i and 32 + rbase + i of each fragment
+        if (t < NCH * 16) {
+            const int f = t >> 4, L = rbase + (t & 7) + 32 * ((t >> 3) & 1);
+            const int4 val = *(const int4 *)(frag + f * FST + L * 16);
+            *(int4 *)(xq + ((rt * (kb_pad >> 5) + cb * NCH + f) << 10) + L * 16) = val;
+        }
+        if constexpr (NSC > 0) {
+            if (t < NSC * 8) xd[(cb * NSC + (t >> 3)) * m_pad + rt * 32 + rbase + (t & 7)] = dsh[t >> 3][rbase + (t & 7)];
+        }
+        if constexpr (FMT == TQ_Q8_K) {
+            if (t < 16) {
+                const int e = rbase + (t & 7) + 32 * (t >> 3);
+                ((int4 *)(xmin + ((rt * ncb + cb) << 9)))[e] = ((const int4 *)msh)[e];
+            }
+        }
     }
 }
 
@@ -697,11 +721,21 @@ static hipError_t tiled_dispatch(const float *x, int64_t ldx, int8_t *xq, float 
     if (m_pad % 32 != 0 || kb_pad % CB != 0) return hipErrorInvalidValue;
     const int64_t wgs = (m_pad / 32) * (kb_pad / CB);
     if (wgs == 0) return hipSuccess;
-    const dim3 g((unsigned)wgs), b(256);
+    // under 512 tiles: four workgroups per tile (8 rows each; F16 keeps one, its lanes cover
+    // 4 rows per pass)
+    constexpr int RPW_SMALL = FMT == TQ_F16 ? 8 : 2;
+    const bool split = RPW_SMALL == 2 && wgs < 512;
+    const dim3 g((unsigned)(split ? 4 * wgs : wgs)), b(256);
     const bool v4 = aligned16(x, ldx) && uoff % 4 == 0;
-#define MQ_TQ(VAR)                                                                                                      \
-    if (v4) hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, true>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad, pre, bias, uoff); \
-    else hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, false>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad, pre, bias, uoff);
+#define MQ_TQ_R(VAR, RPW)                                                                                                    \
+    if (v4) hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, true, RPW>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad, pre, bias, uoff); \
+    else hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, false, RPW>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad, pre, bias, uoff);
+#define MQ_TQ(VAR)            \
+    if (split) {              \
+        MQ_TQ_R(VAR, RPW_SMALL) \
+    } else {                  \
+        MQ_TQ_R(VAR, 8)       \
+    }
     if (FMT != TQ_Q8_0) {
         MQ_TQ(MQ_Q8_0_X86);
     } else {
@@ -713,6 +747,7 @@ static hipError_t tiled_dispatch(const float *x, int64_t ldx, int8_t *xq, float 
         }
     }
 #undef MQ_TQ
+#undef MQ_TQ_R
     return hipGetLastError();
 }
 

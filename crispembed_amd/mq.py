@@ -180,6 +180,9 @@ _SIGS.update({
     "mq_op_repeat": (_c_int, [_PV, _PV, _c_vp]),
     "mq_op_mul_mat_f32": (_c_int, [_PV, _PV, _PV, _c_vp]),
     "mq_op_rope": (_c_int, [_PV, _PV, _PV, _PV, _c_int, _c_int, _c_int] + [ctypes.c_float] * 6 + [_c_vp]),
+    "mq_op_rope_cache": (_c_int, [_PV, _PV, _c_int, _c_int] + [ctypes.c_float] * 6 + [_c_vp, _c_vp]),
+    "mq_op_flash_attn_qk_norm_rope": (_c_int, [_PV, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_vp, ctypes.c_float,
+                                               _c_vp, _c_vp, _c_sz, _c_vp, _c_sz, _c_vp]),
     "mq_op_rms_norm_rope": (_c_int, [_PV, ctypes.c_float, _c_vp, _PV, _PV, _PV, _c_int, _c_int, _c_int] +
                             [ctypes.c_float] * 6 + [_c_vp]),
 })

@@ -179,6 +179,27 @@ int mq_op_rms_norm_rope(const mq_view *x, float eps, const float *w, const mq_vi
                         const mq_view *dst, int n_dims, int mode, int n_ctx_orig, float freq_base, float freq_scale,
                         float ext_factor, float attn_factor, float beta_fast, float beta_slow, void *stream);
 
+/* The rope cache of mq_op_rope's angles: cs[2 (t n_dims/2 + i)] = cos(theta) attn_factor' and
+ * cs[2 (t n_dims/2 + i) + 1] = sin(theta) attn_factor' for position pos[t] (I32 [T]) and pair
+ * i < n_dims/2, with theta and the YaRN magnitude factor exactly as mq_op_rope computes them
+ * (the angles of the ggml_rope_ext nodes of src/decoder_embed.cpp:758-763).  cs: device memory
+ * of T n_dims floats; n_dims even, at most 128. */
+int mq_op_rope_cache(const mq_view *pos, const mq_view *freq_factors, int n_dims, int n_ctx_orig, float freq_base,
+                     float freq_scale, float ext_factor, float attn_factor, float beta_fast, float beta_slow,
+                     float *cs, void *stream);
+
+/* mq_op_flash_attn_ex (flags 0) whose q and k are taken before the decoder's per-head q / k
+ * norm and rotation (src/decoder_embed.cpp:735-763): the attention reads
+ *   q' = rope(rms_norm(q) * q_norm_w),  k' = rope(rms_norm(k) * k_norm_w)
+ * (RMS norm over head_dim with eps, weights F32 [head_dim], NEOX rotation of all head_dim
+ * dimensions by the angles of cs, the mq_op_rope_cache table with n_dims = head_dim over the
+ * Tq = Tk positions) -- the ROPE(MUL(RMS_NORM)) nodes of q and k and the attention in two
+ * kernels.  Equal to those ops followed by mq_op_flash_attn_ex up to the norm's summation order. */
+int mq_op_flash_attn_qk_norm_rope(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
+                                  const mq_view *dst, float scale, const float *q_norm_w, const float *k_norm_w,
+                                  float eps, const float *cs, void *workspace, size_t workspace_bytes,
+                                  void *act_workspace, size_t act_workspace_bytes, void *stream);
+
 /* ggml_mul_mat_id, the mixture-of-experts mat-mul (src/crispembed.cpp:1365,1371):
  *   experts: n_exp prepared weight images of `type` (n x k each, as mq_weight_prepare builds
  *            them), expert e at expert_images + e * expert_stride bytes;

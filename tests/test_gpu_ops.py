@@ -481,6 +481,88 @@ def test_flash_attn_mask_block_classes(monkeypatch, rows, waves, hd, nh, nkv, Tq
     assert np.abs(got - ref).max() / np.abs(ref).max() <= 2e-5
 
 
+@pytest.mark.parametrize("case", ["plain", "yarn", "freq_factors"])
+def test_rope_cache_matches_rope(case):
+    """mq_op_rope_cache against mq_op_rope: rotating the pair (1, 0) gives (cos, sin) x mscale
+    of the pair's angle, bit for bit."""
+    L = mq.lib()
+    T, n_dims = 45, 128
+    rng = _rng(40)
+    pos = (np.arange(T) * 7 + 3).astype(np.int32)
+    kw = dict(n_ctx_orig=0, base=1e6, freq_scale=1.0, ext_factor=0.0, attn_factor=1.0, beta_fast=0.0, beta_slow=0.0)
+    if case == "yarn":
+        kw.update(n_ctx_orig=4096, freq_scale=0.25, ext_factor=1.0, attn_factor=0.9, beta_fast=32.0, beta_slow=1.0)
+    ff = (1.0 + rng.random(n_dims // 2) * 3).astype(np.float32) if case == "freq_factors" else None
+    fv = mq.view(_cuda(ff)) if ff is not None else None
+    dp = _cuda(pos)
+    args = (kw["n_ctx_orig"], kw["base"], kw["freq_scale"], kw["ext_factor"], kw["attn_factor"], kw["beta_fast"],
+            kw["beta_slow"])
+    cs = _t().empty((T, n_dims), dtype=_t().float32, device="cuda")
+    _call(L.mq_op_rope_cache, mq.view(dp), fv, n_dims, *args, ctypes.c_void_p(cs.data_ptr()), stream())
+    x = np.zeros((1, T, 1, n_dims), np.float32)
+    x[..., :n_dims // 2] = 1.0  # NEOX pairs (i, i + n_dims / 2) = (1, 0)
+    dx = _cuda(x)
+    out = _t().empty_like(dx)
+    _call(L.mq_op_rope, mq.view(dx), mq.view(dp), fv, mq.view(out), n_dims, mq.ROPE_NEOX, *args, stream())
+    r = host(out).reshape(T, n_dims)
+    want = np.stack([r[:, :n_dims // 2], r[:, n_dims // 2:]], -1).reshape(T, n_dims)
+    assert np.array_equal(host(cs).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("hd,nh,nkv,B,T,masked", [(128, 4, 2, 1, 300, True), (128, 8, 4, 2, 64, False),
+                                                  (64, 4, 4, 2, 100, True), (32, 6, 2, 1, 77, False)])
+def test_flash_attn_qk_norm_rope(attn_form, hd, nh, nkv, B, T, masked):
+    """mq_op_flash_attn_qk_norm_rope (q and k normed and rotated as the attention reads them)
+    against mq_op_norm + mq_op_rope of q and k followed by mq_op_flash_attn: equal up to the RMS
+    norm's summation order."""
+    L = mq.lib()
+    rng = _rng(hd + nh + T)
+    qx = rng.standard_normal((B, T, nh, hd)).astype(np.float32) * 3
+    kx, vx = (rng.standard_normal((B, T, nkv, hd)).astype(np.float32) for _ in range(2))
+    qw, kw = (rng.standard_normal(hd).astype(np.float32) for _ in range(2))
+    pos = np.arange(T, dtype=np.int32)
+    eps, base = 1e-6, 1e6
+    dq, dk, dv, dp, dqw, dkw = (_cuda(a) for a in (qx, kx, vx, pos, qw, kw))
+    mask_t = None
+    if masked:
+        mask = np.where(np.arange(T)[None, :] > np.arange(T)[:, None], -np.inf, 0.0).astype(np.float16)
+        mask_t = _cuda(mask[None, None])
+    # the separate ops: norm x w, rope, attention
+    rot = []
+    for x, w in ((dq, dqw), (dk, dkw)):
+        t = _t().empty_like(x)
+        _call(L.mq_op_norm, mq.NORM_RMS, mq.view(x), None, mq.view(t), eps, ctypes.c_void_p(w.data_ptr()), None,
+              stream())
+        _call(L.mq_op_rope, mq.view(t), mq.view(dp), None, mq.view(t), hd, mq.ROPE_NEOX, 0, base, 1.0, 0.0, 1.0, 0.0,
+              0.0, stream())
+        rot.append(t)
+    scale = 1.0 / np.sqrt(hd)
+    want = _t().empty((B, T, nh, hd), dtype=_t().float32, device="cuda")
+    mv = mq.view(mask_t) if mask_t is not None else None
+    _flash(rot[0].permute(0, 2, 1, 3), rot[1].permute(0, 2, 1, 3), dv.permute(0, 2, 1, 3), mask_t, scale, want)
+    # fused
+    cs = _t().empty((T, hd), dtype=_t().float32, device="cuda")
+    _call(L.mq_op_rope_cache, mq.view(dp), None, hd, 0, base, 1.0, 0.0, 1.0, 0.0, 0.0, ctypes.c_void_p(cs.data_ptr()),
+          stream())
+    kv = mq.view(dk.permute(0, 2, 1, 3))
+    ws_bytes = L.mq_op_flash_attn_workspace_bytes(kv)
+    ws = _t().empty(ws_bytes + 256, dtype=_t().uint8, device="cuda")
+    wp = ws.data_ptr() + (-ws.data_ptr()) % 256
+    got = _t().full((B, T, nh, hd), np.nan, dtype=_t().float32, device="cuda")
+    _call(L.mq_op_flash_attn_qk_norm_rope, mq.view(dq.permute(0, 2, 1, 3)), kv, mq.view(dv.permute(0, 2, 1, 3)), mv,
+          mq.view(got), scale, ctypes.c_void_p(dqw.data_ptr()), ctypes.c_void_p(dkw.data_ptr()), eps,
+          ctypes.c_void_p(cs.data_ptr()), ctypes.c_void_p(wp), ws_bytes, None, 0, stream())
+    a, b = host(want), host(got)
+    assert np.isfinite(b).all()
+    assert np.abs(a - b).max() / np.abs(a).max() <= 2e-5
+    # q and k must share positions; K/V fragments from elsewhere are refused
+    short = mq.view(dk[:, :T - 1].permute(0, 2, 1, 3))
+    assert L.mq_op_flash_attn_qk_norm_rope(mq.view(dq.permute(0, 2, 1, 3)), short, short, None, mq.view(got), scale,
+                                           ctypes.c_void_p(dqw.data_ptr()), ctypes.c_void_p(dkw.data_ptr()), eps,
+                                           ctypes.c_void_p(cs.data_ptr()), ctypes.c_void_p(wp), ws_bytes, None, 0,
+                                           stream()) != 0
+
+
 def test_op_rejections_name_the_problem():
     L = mq.lib()
     x = _t().zeros((4, 48), dtype=_t().float32, device="cuda")
