@@ -445,7 +445,8 @@ def bench_qwen3_ggml_graph(torch, L, mq):
     single-text path, 815 nodes) on the MI355X ggml backend (tests/native/test_decoder_graph_mi355.cpp,
     built by build_test_driver), beside the runner (mq_decoder_encode) on the same model at B = 1.
     Qwen3-Embedding-0.6B shape, Q4_K, the token table cut to 4096 rows (the lookup's size does
-    not change the work); time per graph from the host's clock around ggml_backend_graph_compute."""
+    not change the work), one random layer's weights in every layer; time per graph from the
+    host's clock around ggml_backend_graph_compute."""
     import subprocess
     import tempfile
 
@@ -456,7 +457,9 @@ def bench_qwen3_ggml_graph(torch, L, mq):
         return {"error": f"{exe} not built"}
     hp = dict(decoder.QWEN3_EMBED_0_6B, n_vocab=4096)
     T = 512
-    W = decoder.synthetic_weights(hp, mq.TYPE_Q4_K, name="qwen3_graph")
+    # one random layer's weights in all 28 layers (the work does not depend on the values)
+    one = decoder.synthetic_weights(dict(hp, n_layer=1), mq.TYPE_Q4_K, name="qwen3_graph")
+    W = dict(one, layers=one["layers"] * hp["n_layer"])
     ids = synth.integers(f"qwen3/graph_ids_{T}", (T,), 0, hp["n_vocab"] - 1).astype(np.int32)
     with tempfile.TemporaryDirectory() as d:
         gguf.write_decoder_gguf(os.path.join(d, "m.gguf"), hp, mq.TYPE_Q4_K, W)
@@ -635,6 +638,7 @@ def main():
                   "minilm_l6_e2e": bench_minilm_e2e(torch, L, mq),
                   "minilm_l6_ggml_graph": bench_minilm_ggml_graph(torch, L, mq),
                   "qwen3_0_6b_e2e": bench_qwen3_e2e(torch, L, mq),
+                  "qwen3_0_6b_ggml_graph": bench_qwen3_ggml_graph(torch, L, mq),
                   "decode_gemv": bench_decode(torch, L, mq, synth)}
     cpu = None
     if not args.no_cpu:
