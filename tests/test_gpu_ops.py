@@ -555,6 +555,25 @@ def test_flash_attn_qk_norm_rope(attn_form, hd, nh, nkv, B, T, masked):
     a, b = host(want), host(got)
     assert np.isfinite(b).all()
     assert np.abs(a - b).max() / np.abs(a).max() <= 2e-5
+    # with the output projection's Q8_0 activation: dst bit for bit as without it, the rows
+    # bit-identical to the quantizer run on dst (the 8-wave kernel's own store at head_dim <= 64)
+    from gpu_util import empty_u8, live_q8_0_planes
+    K, M = nh * hd, B * T
+    if K % 128 == 0:
+        nb = L.mq_workspace_bytes(mq.TYPE_Q8_0, M, K)
+        act, ao = empty_u8(nb)
+        got2 = _t().full((B, T, nh, hd), np.nan, dtype=_t().float32, device="cuda")
+        _call(L.mq_op_flash_attn_qk_norm_rope, mq.view(dq.permute(0, 2, 1, 3)), kv, mq.view(dv.permute(0, 2, 1, 3)),
+              mv, mq.view(got2), scale, ctypes.c_void_p(dqw.data_ptr()), ctypes.c_void_p(dkw.data_ptr()), eps,
+              ctypes.c_void_p(cs.data_ptr()), ctypes.c_void_p(wp), ws_bytes, ctypes.c_void_p(act.data_ptr() + ao), nb,
+              stream())
+        assert np.array_equal(host(got2).view(np.uint32), b.view(np.uint32))
+        ref_act, ro = empty_u8(nb)
+        mq.check(L.mq_quantize_act_ex(mq.TYPE_Q8_0, ctypes.c_void_p(got2.data_ptr()), K, M, K, None, 0,
+                                      ctypes.c_void_p(ref_act.data_ptr() + ro), nb, mq.PATH_GEMM, stream()))
+        qa, da = live_q8_0_planes(host(ref_act)[ro:ro + nb], M, K)
+        qb, db = live_q8_0_planes(host(act)[ao:ao + nb], M, K)
+        assert np.array_equal(qa, qb) and np.array_equal(da.view(np.uint32), db.view(np.uint32))
     # q and k must share positions; K/V fragments from elsewhere are refused
     short = mq.view(dk[:, :T - 1].permute(0, 2, 1, 3))
     assert L.mq_op_flash_attn_qk_norm_rope(mq.view(dq.permute(0, 2, 1, 3)), short, short, None, mq.view(got), scale,
