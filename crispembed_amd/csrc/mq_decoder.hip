@@ -665,12 +665,13 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_split(const AttnArgs a, int
     // l / 4 + 16, coalesced; else each lane its own row's 16 keys of the block, 2 bytes at a time.
     uint64_t dead = 0, zero = 0;
     if constexpr (MASK) {
+        constexpr int CJ = 2;  // blocks classified per pass
         const int nj = min((kend - 32 * wave + 32 * NW - 1) / (32 * NW), 64);
         const uint16_t *mbase = a.mask + (int64_t)b * a.m_sb + (int64_t)h * a.m_sh;
-        for (int j0 = 0; j0 < nj; j0 += 4) {
-            bool live[4], nz[4];
+        for (int j0 = 0; j0 < nj; j0 += CJ) {
+            bool live[CJ], nz[CJ];
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
+            for (int jj = 0; jj < CJ; jj++) {
                 live[jj] = false, nz[jj] = false;
                 const int kb = wave + NW * (j0 + jj);
                 if (a.m_al && kb * 32 + 32 <= Tk) {
@@ -699,7 +700,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_split(const AttnArgs a, int
                 }
             }
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
+            for (int jj = 0; jj < CJ; jj++) {
                 dead |= (uint64_t)(__ballot(live[jj]) == 0) << (j0 + jj);
                 zero |= (uint64_t)(__ballot(nz[jj]) == 0) << (j0 + jj);
             }
@@ -833,7 +834,9 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_split(const AttnArgs a, int
     __syncthreads();
     constexpr int RS = NW >= NT ? NW / NT : 1;
     for (int n = wave % NT; n < NT; n += NW >= NT ? NT : NW) {
-#pragma unroll
+        // not unrolled: at short sequences each wave runs this code once, and the kernel's
+        // time goes to fetching its instructions
+#pragma unroll 1
         for (int r = NW >= NT ? wave / NT : 0; r < 16; r += RS) {
             const int qq = 8 * (r / 4) + 4 * half + (r % 4), q = q0 + qq;
             float mx = -INFINITY;
