@@ -441,12 +441,14 @@ def bench_minilm_ggml_graph(torch, L, mq):
 
 
 def bench_qwen3_ggml_graph(torch, L, mq):
-    """One 512-token sequence through CrispEmbed's Qwen3 decoder graph (decoder_encode_tokens'
-    single-text path, 815 nodes) on the MI355X ggml backend (tests/native/test_decoder_graph_mi355.cpp,
-    built by build_test_driver), beside the runner (mq_decoder_encode) on the same model at B = 1.
-    Qwen3-Embedding-0.6B shape, Q4_K, the token table cut to 4096 rows (the lookup's size does
-    not change the work), one random layer's weights in every layer; time per graph from the
-    host's clock around ggml_backend_graph_compute."""
+    """CrispEmbed's Qwen3 decoder graphs on the MI355X ggml backend (tests/native/
+    test_decoder_graph_mi355.cpp, built by build_test_driver), Qwen3-Embedding-0.6B shape, Q4_K,
+    vocab 151643, from a CrispEmbed decoder GGUF: (1) decoder_encode_tokens_batch's graph for 16
+    sequences x 512 tokens -- one 8192-token graph with the 8192 x 8192 F16 block-diagonal causal
+    mask (src/decoder_embed.cpp:1322-1641), the drop-in path of the 16 x 512 workload -- and (2) one
+    512-token sequence (decoder_encode_tokens' single-text path, 815 nodes) beside the runner
+    (mq_decoder_encode) on the same model at B = 1.  Time per graph from the host's clock around
+    ggml_backend_graph_compute (which synchronizes), inputs already uploaded."""
     import subprocess
     import tempfile
 
@@ -455,33 +457,49 @@ def bench_qwen3_ggml_graph(torch, L, mq):
     exe = os.path.join(ROOT, "crispembed_amd", "bin", "test-decoder-graph-mi355")
     if not os.path.exists(exe):
         return {"error": f"{exe} not built"}
-    hp = dict(decoder.QWEN3_EMBED_0_6B, n_vocab=4096)
-    T = 512
-    # one random layer's weights in all 28 layers (the work does not depend on the values)
-    one = decoder.synthetic_weights(dict(hp, n_layer=1), mq.TYPE_Q4_K, name="qwen3_graph")
-    W = dict(one, layers=one["layers"] * hp["n_layer"])
-    ids = synth.integers(f"qwen3/graph_ids_{T}", (T,), 0, hp["n_vocab"] - 1).astype(np.int32)
+    hp = dict(decoder.QWEN3_EMBED_0_6B)
+    B, T = 16, 512
+    one = decoder.synthetic_weights(dict(hp, n_layer=1, n_vocab=1), mq.TYPE_Q4_K, name="qwen3_graph")
+    tok = np.random.default_rng(20260101).standard_normal((hp["n_vocab"], hp["n_embd"]), dtype=np.float32)
+    tok *= 0.02
+    W = {"tok": tok, "out_norm": one["out_norm"], "layers": one["layers"] * hp["n_layer"]}
+    ids = synth.integers(f"qwen3/ids_{B}x{T}", (B, T), 0, hp["n_vocab"] - 1).astype(np.int32)
+
+    def drive(d, ids_, extra, iters):
+        ids_.tofile(os.path.join(d, "ids"))
+        r = subprocess.run([exe, os.path.join(d, "m.gguf"), str(T), os.path.join(d, "ids"), os.path.join(d, "out"),
+                            "--iters", str(iters), *extra], capture_output=True, text=True, timeout=600)
+        try:
+            res = json.loads(r.stdout.strip().splitlines()[-1])
+        except (ValueError, IndexError):
+            return {"ok": False, "error": (r.stderr or r.stdout)[-300:]}
+        return res
+
     with tempfile.TemporaryDirectory() as d:
         gguf.write_decoder_gguf(os.path.join(d, "m.gguf"), hp, mq.TYPE_Q4_K, W)
-        ids.tofile(os.path.join(d, "ids"))
-        r = subprocess.run([exe, os.path.join(d, "m.gguf"), str(T), os.path.join(d, "ids"), os.path.join(d, "out"),
-                            "--iters", "10"], capture_output=True, text=True, timeout=600)
-    try:
-        res = json.loads(r.stdout.strip().splitlines()[-1])
-    except (ValueError, IndexError):
-        return {"error": (r.stderr or r.stdout)[-300:]}
-    if not res.get("ok"):
-        return {"error": res.get("error")}
+        batched = drive(d, ids, ("--batch", str(B)), 5)
+        single = drive(d, ids[0], (), 10)
+    for res in (batched, single):
+        if not res.get("ok"):
+            return {"error": res.get("error")}
     dec = decoder.DecoderEmbedder(hp, mq.TYPE_Q4_K, W)
-    ids_d = torch.from_numpy(ids.copy()).cuda()
+    del W, tok
+    ids_d = torch.from_numpy(ids[0].copy()).cuda()
     out = torch.empty((1, hp["n_embd"]), dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
     runner_ms = _timed(torch, lambda: dec.encode(ids_d.data_ptr(), 1, T, out.data_ptr(), stream.cuda_stream), 10) / 1e3
     del dec
-    return {"workload": "Qwen3-Embedding-0.6B shape (vocab 4096), Q4_K, one 512-token sequence, CrispEmbed's "
-                        "decoder graph on the MI355X ggml backend",
-            "graph_nodes": res["nodes"], "nodes_not_on_gpu": res["unsupported"],
-            "graph_ms": round(res["ms_per_graph"], 3), "runner_ms": round(runner_ms, 3)}
+    ms = batched["ms_per_graph"]
+    return {"workload": "Qwen3-Embedding-0.6B shape, Q4_K, vocab 151643, CrispEmbed's decoder graphs on the "
+                        "MI355X ggml backend: 16 seq x 512 tokens as decoder_encode_tokens_batch's one 8192-token "
+                        "graph with its 8192 x 8192 F16 mask, and one 512-token sequence",
+            "departures": "one random layer's Q4_K bytes in all 28 layers (28 separate device copies: the same "
+                          "bytes move as with 28 distinct layers)",
+            "batched_graph_nodes": batched["nodes"], "batched_nodes_not_on_gpu": batched["unsupported"],
+            "batched_T_total": batched["T_total"], "batched_ms": round(ms, 3),
+            "batched_embeddings_per_s": round(B / (ms * 1e-3), 1),
+            "graph_nodes": single["nodes"], "nodes_not_on_gpu": single["unsupported"],
+            "graph_ms": round(single["ms_per_graph"], 3), "runner_ms": round(runner_ms, 3)}
 
 
 def bench_qwen3_e2e(torch, L, mq):

@@ -88,10 +88,13 @@ def build_test_driver():
               "-I", oracle]
     libs = ["-L", HERE, "-lggml-mi355", "-lggml-compat", "-lmq", "-Wl,-rpath," + HERE, "-Wl,-rpath,$ORIGIN/.."]
     outs = []
-    for src, name, extra in (("test_backend_mi355.cpp", "test-backend-mi355",
-                              ["-L", oracle, "-loracle", "-Wl,-rpath," + oracle, "-Wl,-rpath,$ORIGIN/../../oracle"]),
+    with_oracle = ["-L", oracle, "-loracle", "-Wl,-rpath," + oracle, "-Wl,-rpath,$ORIGIN/../../oracle"]
+    rocm = os.path.dirname(os.path.dirname(os.path.realpath(HIPCC)))
+    with_hip = ["-I", os.path.join(rocm, "include"), "-D__HIP_PLATFORM_AMD__", "-L", os.path.join(rocm, "lib"),
+                "-lamdhip64", "-Wl,-rpath," + os.path.join(rocm, "lib")]
+    for src, name, extra in (("test_backend_mi355.cpp", "test-backend-mi355", with_oracle),
                              ("test_bert_graph_mi355.cpp", "test-bert-graph-mi355", []),
-                             ("test_decoder_graph_mi355.cpp", "test-decoder-graph-mi355", [])):
+                             ("test_decoder_graph_mi355.cpp", "test-decoder-graph-mi355", with_oracle + with_hip)):
         out = os.path.join(BIN, name)
         cmd = ["g++", *common, os.path.join(TESTS, "native", src), "-o", out + ".tmp", *libs, *extra]
         r = subprocess.run(cmd, capture_output=True, text=True)

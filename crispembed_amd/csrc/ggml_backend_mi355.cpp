@@ -103,6 +103,17 @@ struct BackendCtx {
     float *cs = nullptr;
     size_t cs_bytes = 0;
     std::vector<int64_t> cs_key;
+    // the block lists (mq_op_mask_blocks, in mb_bytes of device memory) of FLASH_ATTN_EXT mask
+    // mb_mask in the graph being computed: built at the first attention that reads the mask with
+    // the shapes mb_key names, reused by the later ones (a decoder's every layer) until a node
+    // writes the mask's bytes (mb_mask NULL: none)
+    void *mb = nullptr;
+    size_t mb_bytes = 0;
+    const ggml_tensor *mb_mask = nullptr;
+    std::vector<int64_t> mb_key;
+    // ggml_backend_mi355_set_act_observer
+    ggml_backend_mi355_act_observer act_cb = nullptr;
+    void *act_user = nullptr;
 };
 
 std::vector<DeviceCtx *> &devices();
@@ -338,6 +349,7 @@ void be_free(ggml_backend_t be) {
         if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
         if (c->ws) (void)hipFree(c->ws);
         if (c->cs) (void)hipFree(c->cs);
+        if (c->mb) (void)hipFree(c->mb);
         (void)hipStreamDestroy(c->stream);
     }
     delete c;
@@ -396,12 +408,21 @@ int quantize_x(BackendCtx *c, const ggml_tensor *x, int mt, int64_t M, int64_t K
     return rc;
 }
 
+// The activation observer: the quantized activation `act` (mq_quantize_act_ex's layout for
+// type mt, path) that the product at `node` is about to read, after the stream has finished
+// writing it.
+void observe_act(BackendCtx *c, const ggml_tensor *node, int mt, int64_t M, int64_t K, int path, const void *act) {
+    if (!c->act_cb) return;
+    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    c->act_cb(node, mt, path, act, mq_workspace_bytes(mt, M, K), M, K, c->act_user);
+}
+
 // Decode-sized products on K-quant weights take mq_mul_mat_gemv: the GEMV quantizes its own
 // activation, one launch instead of two (unless the activation is already quantized in the
 // workspace, or a graph is being captured: that form may allocate on its first large input).
 bool gemv_fused(const BackendCtx *c, const ggml_tensor *x, int mt, int64_t M, int64_t K, int path) {
     return path == MQ_PATH_GEMV && (mt == MQ_TYPE_Q4_K || mt == MQ_TYPE_Q6_K) && M <= 8 && K <= 6144 &&
-           !c->capturing && c->ws_x != x && ((uintptr_t)x->data & 15) == 0 && (x->nb[1] / 4) % 4 == 0 &&
+           !c->capturing && !c->act_cb && c->ws_x != x && ((uintptr_t)x->data & 15) == 0 && (x->nb[1] / 4) % 4 == 0 &&
            std::getenv("MQ_GGML_NO_FUSION") == nullptr;
 }
 
@@ -425,9 +446,11 @@ enum ggml_status mul_mat_flat(BackendCtx *c, const ggml_tensor *w, const ggml_te
         return GGML_STATUS_SUCCESS;
     }
     int rc = quantize_x(c, x, mt, M, K, path);
-    if (rc == 0)
+    if (rc == 0) {
+        observe_act(c, named, mt, M, K, path, c->ws);
         rc = mq_mul_mat_q_ex(mt, w->data, N, K, c->ws, M, (float *)dst->data, (int64_t)(dst->nb[1] / 4), bias, path,
                              c->stream);
+    }
     if (rc != 0) {
         std::fprintf(stderr, "ggml-mi355: MUL_MAT '%s' failed: %s\n", named->name, mq_last_error());
         return rc == MQ_ENOMEM ? GGML_STATUS_ALLOC_FAILED : GGML_STATUS_FAILED;
@@ -658,22 +681,56 @@ int try_defer_qk_norm_rope(BackendCtx *c, ggml_cgraph *cg, int i, int n, std::ve
     return 3;
 }
 
-// The attention of FLASH_ATTN_EXT node fa: mq_op_flash_attn_qk_norm_rope when its q and k chains
-// were left to it, else mq_op_flash_attn_ex on its operands.
+// The block lists of mask mt (view m) for the attention of q and k: built once per graph and
+// reused while the mask's bytes and the shapes stay (see BackendCtx::mb); NULL where the
+// attention takes none, under capture before a buffer exists, or with MQ_GGML_NO_MASK_BLOCKS=1.
+const void *mask_blocks(BackendCtx *c, const ggml_tensor *mt, const mq_view &q, const mq_view &k, const mq_view &m) {
+    if (std::getenv("MQ_GGML_NO_MASK_BLOCKS")) return nullptr;
+    const size_t need = mq_op_mask_blocks_bytes(&q, &k, &m);
+    if (need == 0) return nullptr;
+    std::vector<int64_t> key = {(int64_t)(uintptr_t)mt->data, q.ne[1], q.ne[2], q.ne[3], k.ne[1]};
+    key.insert(key.end(), mt->ne, mt->ne + 4);
+    key.insert(key.end(), mt->nb, mt->nb + 4);
+    if (c->mb_mask == mt && key == c->mb_key) return c->mb;
+    c->mb_mask = nullptr;
+    if (need > c->mb_bytes) {
+        if (c->capturing) return nullptr;  // no allocation under capture: the attention classifies itself
+        hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        if (c->gexec) {  // the captured graph holds the old lists' address
+            (void)hipGraphExecDestroy(c->gexec);
+            c->gexec = nullptr;
+            c->gkey = c->seen_key = 0;
+        }
+        if (c->mb) (void)hipFree(c->mb);
+        c->mb = nullptr, c->mb_bytes = 0;
+        if (hipMalloc(&c->mb, need) != hipSuccess) {
+            (void)hipGetLastError();
+            c->mb = nullptr;
+            return nullptr;
+        }
+        c->mb_bytes = need;
+    }
+    if (mq_op_mask_blocks(&q, &k, &m, c->mb, c->mb_bytes, c->stream) != 0) return nullptr;
+    c->mb_mask = mt, c->mb_key = key;
+    return c->mb;
+}
+
+// The attention of FLASH_ATTN_EXT node fa: with q and k before their norm and rotation when those
+// chains were left to it (c->qk_fa), else on its operands; with the mask's block lists where the
+// attention takes them.
 int attn_call(BackendCtx *c, const ggml_tensor *fa, void *ws, size_t ws_bytes, void *act, size_t act_bytes,
               int flags) {
     const mq_view v = view_of(fa->src[2]), d = view_of(fa);
     mq_view m{};
     if (fa->src[3]) m = view_of(fa->src[3]);
-    if (c->qk_fa == fa) {
-        c->qk_fa = nullptr;
-        return mq_op_flash_attn_qk_norm_rope(&c->qk_q, &c->qk_k, &v, fa->src[3] ? &m : nullptr, &d,
-                                             op_param_f32(fa, 0), c->qk_qw, c->qk_kw, c->qk_eps, c->cs, ws, ws_bytes,
-                                             act, act_bytes, c->stream);
-    }
-    const mq_view q = view_of(fa->src[0]), k = view_of(fa->src[1]);
-    return mq_op_flash_attn_ex(&q, &k, &v, fa->src[3] ? &m : nullptr, &d, op_param_f32(fa, 0), ws, ws_bytes, act,
-                               act_bytes, flags, c->stream);
+    const bool qk = c->qk_fa == fa;
+    c->qk_fa = nullptr;
+    const mq_view q = qk ? c->qk_q : view_of(fa->src[0]), k = qk ? c->qk_k : view_of(fa->src[1]);
+    const void *blocks = fa->src[3] ? mask_blocks(c, fa->src[3], q, k, m) : nullptr;
+    return mq_op_flash_attn_blocks(&q, &k, &v, fa->src[3] ? &m : nullptr, &d, op_param_f32(fa, 0),
+                                   qk ? c->qk_qw : nullptr, qk ? c->qk_kw : nullptr, qk ? c->qk_eps : 0.f,
+                                   qk ? c->cs : nullptr, blocks, ws, ws_bytes, act, act_bytes, qk ? 0 : flags,
+                                   c->stream);
 }
 
 // [ADD(x, r) ->] NORM|RMS_NORM -> MUL(w) [-> ADD(b)] starting at node i: returns the number of
@@ -821,6 +878,7 @@ int try_fuse_bias_gelu_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, enu
                                 (const float *)add->src[1]->data, MQ_PRE_GELU_ERF, c->ws, c->ws_bytes, path, c->stream);
     if (rc == 0) {
         c->ws_x = gelu, c->ws_type = mt, c->ws_m = M, c->ws_k = K, c->ws_path = path;
+        observe_act(c, mm, mt, M, K, path, c->ws);
         rc = mq_mul_mat_q_ex(mt, w->data, N, K, c->ws, M, (float *)dst->data, (int64_t)(dst->nb[1] / 4), bias2, path,
                              c->stream);
     }
@@ -865,12 +923,16 @@ int try_fuse_ffn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status 
     }
     void *ws2 = (char *)c->ws + off;
     int rc = quantize_x(c, x, mt1, M, K1, MQ_PATH_GEMM);
-    if (rc == 0)
+    if (rc == 0) {
+        observe_act(c, mm1, mt1, M, K1, MQ_PATH_GEMM, c->ws);
         rc = mq_mul_mat_q_requant(mt1, w1->data, N1, K1, c->ws, M, (const float *)add->src[1]->data, MQ_PRE_GELU_ERF,
                                   MQ_TYPE_Q8_0, ws2, c->ws_bytes - off, c->stream);
-    if (rc == 0)
+    }
+    if (rc == 0) {
+        observe_act(c, mm2, MQ_TYPE_Q8_0, M, N1, MQ_PATH_GEMM, ws2);
         rc = mq_mul_mat_q_ex(MQ_TYPE_Q8_0, w2->data, N2, N1, ws2, M, (float *)dst->data, (int64_t)(dst->nb[1] / 4), bias2,
                              MQ_PATH_GEMM, c->stream);
+    }
     st = op_status(rc, mm1);
     return dst == mm2 ? 4 : 5;
 }
@@ -904,7 +966,7 @@ int try_fuse_silu_mul(BackendCtx *c, ggml_cgraph *cg, int i, int n, const std::v
     if (mul->ne[0] != K || !mq_supports(mt, K)) return 0;
     const int path = mq_mul_mat_path(mt, N, K, M);
     const bool gemv = path == MQ_PATH_GEMV && (mt == MQ_TYPE_Q4_K || mt == MQ_TYPE_Q6_K) && M <= 8 && K <= 6144 &&
-                      !c->capturing && ((uintptr_t)gate->data & 15) == 0 && ((uintptr_t)up->data & 15) == 0 && ld % 4 == 0;
+                      !c->capturing && !c->act_cb && ((uintptr_t)gate->data & 15) == 0 && ((uintptr_t)up->data & 15) == 0 && ld % 4 == 0;
     if (!done[i + 1]) {  // (done: computed already, grouped with the gate projection)
         st = compute_node(c, up);
         if (st != GGML_STATUS_SUCCESS) return 4;
@@ -1115,6 +1177,8 @@ int try_group_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, std::vector<
         if (ensure_ws(c, off + fb)) {
             rc = quantize_x(c, x, mt, M, K, path);
             if (rc == 0)
+                for (int g = 0; g < nm; g++) observe_act(c, mem[g].mm, mt, M, K, path, c->ws);
+            if (rc == 0)
                 rc = mq_mul_mat_q_qkv(mt, w, nn, K, c->ws, M, y[0], ldy[0], b, T, hd, nkv, (char *)c->ws + off, fb,
                                       c->stream);
             if (rc == 0) c->kv_ready_for = fa, c->kv_frag_off = off;
@@ -1125,6 +1189,8 @@ int try_group_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, std::vector<
                              M, y, ldy, b, c->stream);
     if (rc == 1) {
         rc = quantize_x(c, x, mt, M, K, path);
+        if (rc == 0)
+            for (int g = 0; g < nm; g++) observe_act(c, mem[g].mm, mt, M, K, path, c->ws);
         if (rc == 0) rc = mq_mul_mat_q_group(mt, nm, w, nn, K, c->ws, M, y, ldy, b, path, c->stream);
     }
     if (rc != 0) {
@@ -1237,10 +1303,15 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
     c->kv_ready_for = nullptr;
     c->qk_fa = nullptr;
     c->cs_key.clear();  // and the positions
+    c->mb_mask = nullptr;  // and the masks
     std::vector<char> done(n, 0);  // nodes already computed as part of an earlier group
     for (int i = 0; i < n; i++) {
         ggml_tensor *node = ggml_graph_node(cg, i);
-        if (done[i] || ggml_is_empty(node) || is_view_op(node->op)) continue;
+        if (done[i] || ggml_is_empty(node) || is_view_op(node->op)) {
+            // a product computed ahead with an earlier group wrote its bytes then
+            if (done[i] && c->mb_mask && !is_view_op(node->op) && overlaps(node, c->mb_mask)) c->mb_mask = nullptr;
+            continue;
+        }
         enum ggml_status st = GGML_STATUS_SUCCESS;
         int used = 0;
         // The workspace's quantized activation (ws_x) stays reusable across nodes that neither use
@@ -1283,6 +1354,14 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
                     break;
                 }
             }
+        if (c->mb_mask)
+            for (int j = i; j < i + used; j++) {
+                const ggml_tensor *t = ggml_graph_node(cg, j);
+                if (!is_view_op(t->op) && overlaps(t, c->mb_mask)) {
+                    c->mb_mask = nullptr;
+                    break;
+                }
+            }
         i += used - 1;
     }
     c->ws_x = nullptr;
@@ -1315,7 +1394,7 @@ uint64_t graph_key(ggml_cgraph *cg) {
         }
     }
     for (const char *k : {"MQ_GGML_NO_FUSION", "MQ_GEMM_CFG", "MQ_ATTN_SPLIT", "MQ_GEMV_WGS", "MQ_GEMV_PF",
-                          "MQ_FORCE_GEMV_MAX_M", "MQ_Q8_0_VARIANT"}) {
+                          "MQ_FORCE_GEMV_MAX_M", "MQ_Q8_0_VARIANT", "MQ_GGML_NO_MASK_BLOCKS", "MQ_ATTN_SPLIT_WAVES"}) {
         const char *v = std::getenv(k);
         if (v) mix(v, std::strlen(v));
         mix("|", 1);
@@ -1584,5 +1663,11 @@ bool ggml_backend_is_mi355(ggml_backend_t backend) {
 ggml_backend_reg_t ggml_backend_init(void) { return &the_reg(); }
 
 int ggml_backend_score(void) { return devices().empty() ? 0 : 1; }
+
+void ggml_backend_mi355_set_act_observer(ggml_backend_t backend, ggml_backend_mi355_act_observer cb, void *user) {
+    if (!ggml_backend_is_mi355(backend)) return;
+    BackendCtx *c = (BackendCtx *)backend->context;
+    c->act_cb = cb, c->act_user = user;
+}
 
 }  // extern "C"

@@ -158,6 +158,7 @@ GGML_API void ggml_set_output(struct ggml_tensor *tensor);
 
 GGML_API size_t ggml_tensor_overhead(void);
 GGML_API size_t ggml_graph_overhead(void);
+GGML_API size_t ggml_graph_overhead_custom(size_t size, bool grads);
 GGML_API struct ggml_context *ggml_init(struct ggml_init_params params);
 GGML_API void ggml_free(struct ggml_context *ctx);
 GGML_API struct ggml_tensor *ggml_new_tensor_1d(struct ggml_context *ctx, enum ggml_type type, int64_t ne0);
@@ -223,6 +224,7 @@ GGML_API struct ggml_tensor *ggml_rope_ext(struct ggml_context *ctx, struct ggml
                                           float freq_scale, float ext_factor, float attn_factor, float beta_fast,
                                           float beta_slow);
 GGML_API struct ggml_cgraph *ggml_new_graph(struct ggml_context *ctx);
+GGML_API struct ggml_cgraph *ggml_new_graph_custom(struct ggml_context *ctx, size_t size, bool grads);
 GGML_API void ggml_build_forward_expand(struct ggml_cgraph *cgraph, struct ggml_tensor *tensor);
 GGML_API int ggml_graph_n_nodes(struct ggml_cgraph *cgraph);
 GGML_API struct ggml_tensor *ggml_graph_node(struct ggml_cgraph *cgraph, int i);

@@ -156,6 +156,8 @@ struct ggml_cgraph {
 
 extern "C" size_t ggml_tensor_overhead(void) { return sizeof(ggml_tensor) + 16; }
 extern "C" size_t ggml_graph_overhead(void) { return 4096; }
+// the node list grows as needed: no size limit to reserve
+extern "C" size_t ggml_graph_overhead_custom(size_t, bool) { return 4096; }
 
 extern "C" struct ggml_context *ggml_init(struct ggml_init_params params) {
     ggml_context *ctx = new ggml_context;
@@ -474,6 +476,8 @@ extern "C" struct ggml_cgraph *ggml_new_graph(struct ggml_context *ctx) {
     ctx->graphs.push_back(g);
     return g;
 }
+
+extern "C" struct ggml_cgraph *ggml_new_graph_custom(struct ggml_context *ctx, size_t, bool) { return ggml_new_graph(ctx); }
 
 static void visit(ggml_cgraph *g, ggml_tensor *t) {
     if (std::find(g->nodes.begin(), g->nodes.end(), t) != g->nodes.end()) return;

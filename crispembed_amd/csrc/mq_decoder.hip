@@ -567,12 +567,16 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
 // online softmax over key blocks w, w + NW, ... and the NW partial (max, sum, O) are merged
 // through LDS:
 //   m = max_w m_w,  O = sum_w 2^(m_w - m) O_w,  l = sum_w 2^(m_w - m) l_w,  out = O / l.
-// With a mask, each wave first classifies its first 64 key blocks from the mask values of the
-// tile's 32 rows (all loads in flight together): no finite value -> the block is skipped; all
-// values 0 -> it runs unmasked, with no mask reads; else it adds the mask as it goes.  A causal
-// mask thus costs one pass over it, not a dependent load per key block.
-template <int HD, bool MASK, int NW>
+// With a mask (MK = 1), each wave first classifies its first 64 key blocks from the mask values
+// of the tile's 32 rows (all loads in flight together): no finite value -> the block is skipped;
+// all values 0 -> it runs unmasked, with no mask reads; else it adds the mask as it goes.  A
+// causal mask thus costs one pass over it, not a dependent load per key block.  With the mask's
+// block lists (MK = 2, launch_mask_blocks: the same classification, made once for all heads and
+// every attention that reads the mask) the waves take the tile's live blocks in turn: a
+// block-diagonal batch mask over thousands of keys then costs the tile's own blocks only.
+template <int HD, int MK, int NW>
 __global__ __launch_bounds__(64 * NW, 2) void k_attn_split(const AttnArgs a, int nblk, float qscale) {
+    constexpr bool MASK = MK != 0;
     constexpr int NS = HD / 16, NT = HD / 32, HALF = HD / 2, NFR = kv_frags<HD>();
     constexpr float LOG2E = 1.4426950408889634f;
     __shared__ __attribute__((aligned(16))) float rs[NW][32];
@@ -664,7 +668,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_split(const AttnArgs a, int
     // Rows 16-byte aligned (m_al): lane l reads 8 keys (16 bytes) of row l / 4 and of row
     // l / 4 + 16, coalesced; else each lane its own row's 16 keys of the block, 2 bytes at a time.
     uint64_t dead = 0, zero = 0;
-    if constexpr (MASK) {
+    if constexpr (MK == 1) {
         constexpr int CJ = 2;  // blocks classified per pass
         const int nj = min((kend - 32 * wave + 32 * NW - 1) / (32 * NW), 64);
         const uint16_t *mbase = a.mask + (int64_t)b * a.m_sb + (int64_t)h * a.m_sh;
@@ -707,22 +711,8 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_split(const AttnArgs a, int
         }
     }
 
-    for (int j = 0, kb = wave; kb * 32 < kend; j++, kb += NW) {
-        bool mixed = MASK;
-        if constexpr (MASK) {
-            if (j < 64) {
-                if ((dead >> j) & 1) continue;
-                mixed = !((zero >> j) & 1);
-            } else {  // past the classified blocks: the same test here
-                bool live = false;
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
-                    live |= key < Tk && (float)mrow[min(key, Tk - 1)] != -INFINITY;
-                }
-                if (__ballot(live) == 0) continue;
-            }
-        }
+    // key block kb (mixed: it adds the mask) into the wave's running (max, sum, O)
+    auto run_block = [&](const int kb, const bool mixed) __attribute__((always_inline)) {
         const v8h *Fb = F + (int64_t)kb * NFR * 64;
         v16f s_hh = (v16f){}, s_hl = (v16f){}, s_lh = (v16f){};
         // an address the compiler cannot see through, so the fragment reads stay in the loop
@@ -819,6 +809,33 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_split(const AttnArgs a, int
             for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, bl[t][n], oacc[n], 0, 0, 0);
 #pragma unroll
             for (int n = 0; n < NT; n++) oacc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl, bh[t][n], oacc[n], 0, 0, 0);
+        }
+    };
+    if constexpr (MK == 2) {
+        const uint32_t *lst = a.blist + ((int64_t)(a.m_sb ? b : 0) * a.bl_nqt + (q0 >> 5)) * a.bl_stride;
+        const int nl = (int)lst[0];
+        for (int j = wave; j < nl; j += NW) {
+            const uint32_t e = lst[1 + j];
+            run_block((int)(e & 0x7FFFFFFFu), (e >> 31) != 0);
+        }
+    } else {
+        for (int j = 0, kb = wave; kb * 32 < kend; j++, kb += NW) {
+            bool mixed = MASK;
+            if constexpr (MASK) {
+                if (j < 64) {
+                    if ((dead >> j) & 1) continue;
+                    mixed = !((zero >> j) & 1);
+                } else {  // past the classified blocks: the same test here
+                    bool live = false;
+#pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        const int key = kb * 32 + 8 * (i / 4) + 4 * half + (i % 4);
+                        live |= key < Tk && (float)mrow[min(key, Tk - 1)] != -INFINITY;
+                    }
+                    if (__ballot(live) == 0) continue;
+                }
+            }
+            run_block(kb, mixed);
         }
     }
 
@@ -952,32 +969,39 @@ static void launch_attn_8w(dim3 grid, const AttnArgs &a, int nblk, float qscale,
     hipLaunchKernelGGL((k_attn_frag<HD, false, QO>), grid, dim3(512), BYTES, s, a, nblk, qscale);
 }
 
+// The split-key form when the regular grid (2 heads x 128 queries per workgroup) would leave
+// most CUs idle and there are several key blocks to share out, and for masked head_dim 128 (the
+// 8-wave kernel's mask addressing does not fit its 256 registers and spills); MQ_ATTN_SPLIT=0/1
+// forces either form (measurements)
+bool attn_split_form(const AttnArgs &a) {
+    const int nblk = (a.Tk + 31) / 32;
+    const int64_t wgs = (int64_t)((a.nq + 1) / 2) * a.B * ((a.Tq + 127) / 128);
+    bool split = (wgs < 128 && nblk >= 4) || (a.hd == 128 && a.mask);
+    if (const char *e = getenv("MQ_ATTN_SPLIT"))
+        if (*e) split = atoi(e) != 0;
+    return split;
+}
+
+template <int HD, int NW>
+static void launch_attn_split(dim3 g, const AttnArgs &a, int nblk, float qscale, hipStream_t s) {
+    if (a.mask && a.blist) hipLaunchKernelGGL((k_attn_split<HD, 2, NW>), g, dim3(64 * NW), 0, s, a, nblk, qscale);
+    else if (a.mask) hipLaunchKernelGGL((k_attn_split<HD, 1, NW>), g, dim3(64 * NW), 0, s, a, nblk, qscale);
+    else hipLaunchKernelGGL((k_attn_split<HD, 0, NW>), g, dim3(64 * NW), 0, s, a, nblk, qscale);
+}
+
 template <int HD>
 static void launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_t s) {
     const dim3 gk((unsigned)nblk, (unsigned)a.nkv, (unsigned)a.B);
     if (!a.kv_ready) hipLaunchKernelGGL((k_kv_frag<HD>), gk, dim3(256), 0, s, a, nblk);
-    // the split-key form when the regular grid (2 heads x 128 queries per workgroup) would
-    // leave most CUs idle and there are several key blocks to share out, and for masked
-    // head_dim 128 (the 8-wave kernel's mask addressing does not fit its 256 registers and
-    // spills); MQ_ATTN_SPLIT=0/1 forces either form (measurements)
-    const int64_t wgs = (int64_t)((a.nq + 1) / 2) * a.B * ((a.Tq + 127) / 128);
-    bool split = (wgs < 128 && nblk >= 4) || (HD == 128 && a.mask);
-    if (const char *e = getenv("MQ_ATTN_SPLIT"))
-        if (*e) split = atoi(e) != 0;
-    if (split) {
+    if (attn_split_form(a)) {
         // 8 waves per workgroup (half the key blocks per wave) while the grid is at most a few
         // workgroups per CU; MQ_ATTN_SPLIT_WAVES=4/8 forces either (measurements)
         const dim3 g((unsigned)a.nq, (unsigned)a.B, (unsigned)((a.Tq + 31) / 32));
         int nw = (int64_t)g.x * g.y * g.z <= 1024 ? 8 : 4;
         if (const char *e = getenv("MQ_ATTN_SPLIT_WAVES"))
             if (*e) nw = atoi(e) == 4 ? 4 : 8;
-        if (nw == 8) {
-            if (a.mask) hipLaunchKernelGGL((k_attn_split<HD, true, 8>), g, dim3(512), 0, s, a, nblk, qscale);
-            else hipLaunchKernelGGL((k_attn_split<HD, false, 8>), g, dim3(512), 0, s, a, nblk, qscale);
-        } else {
-            if (a.mask) hipLaunchKernelGGL((k_attn_split<HD, true, 4>), g, dim3(256), 0, s, a, nblk, qscale);
-            else hipLaunchKernelGGL((k_attn_split<HD, false, 4>), g, dim3(256), 0, s, a, nblk, qscale);
-        }
+        if (nw == 8) launch_attn_split<HD, 8>(g, a, nblk, qscale, s);
+        else launch_attn_split<HD, 4>(g, a, nblk, qscale, s);
         return;
     }
     const dim3 ga((unsigned)((a.nq + 1) / 2), (unsigned)a.B, (unsigned)((a.Tq + 127) / 128));
@@ -1002,14 +1026,75 @@ static void launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_
 // head_dim 128 when the workgroup's two heads make whole superblocks of complete query tiles
 // (even nq, Tq a multiple of 128, no mask).  Otherwise the caller quantizes the fp32 output.
 static bool attn_frag_form(const AttnArgs &a, int q_type) {
-    const int nblk = (a.Tk + 31) / 32;
-    const int64_t wgs = (int64_t)((a.nq + 1) / 2) * a.B * ((a.Tq + 127) / 128);
-    bool split = (wgs < 128 && nblk >= 4) || (a.hd == 128 && a.mask);
-    if (const char *e = getenv("MQ_ATTN_SPLIT"))
-        if (*e) split = atoi(e) != 0;
-    if (split) return false;
+    if (attn_split_form(a)) return false;
     if (q_type == MQ_TYPE_Q8_0) return a.hd <= 64;
     return a.hd == 128 && a.nq % 2 == 0 && a.Tq % 128 == 0 && !a.mask;
+}
+
+// One workgroup per (mask plane, tile of 32 query rows): each wave classifies key blocks wave,
+// wave + 4, ... (lane l: row l / 2 of the tile, keys 16 (l % 2) .. + 15 of the block; f16 -inf is
+// 0xFC00, +-0 have no bits outside the sign) into LDS, then wave 0 writes the live ones in order.
+__global__ __launch_bounds__(256) void k_mask_blocks(const uint16_t *__restrict__ mask, int64_t m_sq, int64_t m_sb,
+                                                     int m_al, int Tq, int Tk, int nkb, uint32_t *__restrict__ out,
+                                                     int stride) {
+    extern __shared__ uint8_t cls[];  // nkb: 0 dead, 1 all zero, 2 mixed
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+    const int qt = blockIdx.x, bm = blockIdx.y;
+    const int row = min(qt * 32 + (lane >> 1), Tq - 1), k0 = 16 * (lane & 1);
+    const uint16_t *mrow = mask + (int64_t)bm * m_sb + (int64_t)row * m_sq;
+    for (int kb = wave; kb < nkb; kb += 4) {
+        bool live = false, nz = false;
+        if (m_al && kb * 32 + 32 <= Tk) {
+            const uint4 *p = (const uint4 *)(mrow + kb * 32 + k0);
+            const uint4 u0 = p[0], u1 = p[1];
+            const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                live |= (w[e] & 0xFFFFu) != 0xFC00u || (w[e] >> 16) != 0xFC00u;
+                nz |= (w[e] & 0x7FFF7FFFu) != 0u;
+            }
+        } else {
+            for (int i = 0; i < 16; i++) {
+                const int key = kb * 32 + k0 + i;
+                if (key < Tk) {
+                    const uint16_t v = mrow[key];
+                    live |= v != 0xFC00u;
+                    nz |= (v & 0x7FFFu) != 0u;
+                }
+            }
+        }
+        const bool any_live = __ballot(live) != 0, any_nz = __ballot(nz) != 0;
+        if (lane == 0) cls[kb] = any_live ? (any_nz ? 2 : 1) : 0;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    uint32_t *lst = out + ((int64_t)bm * gridDim.x + qt) * stride;
+    uint32_t n = 0;
+    for (int base = 0; base < nkb; base += 64) {
+        const int kb = base + lane;
+        const int c = kb < nkb ? cls[kb] : 0;
+        const uint64_t m = __ballot(c != 0);
+        const uint32_t before = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        if (c) lst[1 + n + before] = (uint32_t)kb | (c == 2 ? 0x80000000u : 0u);
+        n += (uint32_t)__popcll(m);
+    }
+    if (lane == 0) lst[0] = n;
+}
+
+// at most 16384 key blocks (LDS of the classification)
+size_t mask_blocks_bytes(int Bm, int Tq, int Tk) {
+    const int64_t nkb = ((int64_t)Tk + 31) / 32, nqt = ((int64_t)Tq + 31) / 32;
+    if (Bm <= 0 || Tq <= 0 || Tk <= 0 || nkb > 16384 || Bm > 65535 || nqt > INT32_MAX) return 0;
+    return (size_t)Bm * nqt * (nkb + 1) * 4;
+}
+
+hipError_t launch_mask_blocks(const uint16_t *mask, int64_t m_sq, int64_t m_sb, bool m_al, int Bm, int Tq, int Tk,
+                              uint32_t *blocks, hipStream_t s) {
+    if (mask_blocks_bytes(Bm, Tq, Tk) == 0) return hipErrorInvalidValue;
+    const int nkb = (Tk + 31) / 32, nqt = (Tq + 31) / 32;
+    hipLaunchKernelGGL(k_mask_blocks, dim3((unsigned)nqt, (unsigned)Bm), dim3(256), (size_t)nkb, s, mask, m_sq, m_sb,
+                       (int)m_al, Tq, Tk, nkb, blocks, nkb + 1);
+    return hipGetLastError();
 }
 
 hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {

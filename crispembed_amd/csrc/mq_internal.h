@@ -357,6 +357,10 @@ struct AttnArgs {
     const uint16_t *mask = nullptr;
     int64_t m_sb = 0, m_sh = 0, m_sq = 0;
     bool m_al = false;  // mask pointer 16-byte aligned, m_sb / m_sh / m_sq multiples of 8
+    // the mask's block lists (launch_mask_blocks; NULL: the attention classifies the mask's
+    // blocks itself): list (mask plane bm, query tile qt) at blist + (bm * bl_nqt + qt) * bl_stride
+    const uint32_t *blist = nullptr;
+    int bl_nqt = 0, bl_stride = 0;
     int B = 0, Tq = 0, Tk = 0, nq = 0, nkv = 0, hd = 0;
     float scale = 1.0f;
     int causal = 0;
@@ -385,5 +389,17 @@ struct AttnArgs {
 };
 size_t attn_workspace_bytes(int B, int Tk, int nkv, int hd);
 hipError_t launch_attn(const AttnArgs &a, hipStream_t s);
+// true when launch_attn takes the split-key kernel for these operands (the form that reads
+// mask block lists); a.mask, a.m_sh and the shape fields are what it looks at
+bool attn_split_form(const AttnArgs &a);
+// Block lists of a mask shared by every head (m_sh = 0) for the split-key attention: for each
+// of Bm mask planes (m_sb apart) and each tile of 32 query rows, one list of 1 + nkb words
+// (nkb = ceil(Tk / 32)): the count n, then the n key blocks of 32 keys in which some row of the
+// tile has a finite mask value, in increasing order, each as kb | 1 << 31 when some value is not
+// zero (the block adds the mask; else it runs unmasked).  Rows past Tq repeat row Tq - 1; keys
+// past Tk are not read.  The same classification the attention makes when it has no list.
+size_t mask_blocks_bytes(int Bm, int Tq, int Tk);
+hipError_t launch_mask_blocks(const uint16_t *mask, int64_t m_sq, int64_t m_sb, bool m_al, int Bm, int Tq, int Tk,
+                              uint32_t *blocks, hipStream_t s);
 
 }  // namespace mq

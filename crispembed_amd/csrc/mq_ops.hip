@@ -1260,9 +1260,56 @@ struct QkNormRope {
     float eps;
 };
 
+// The attention's view of operands q / k / mask (shape fields and the mask's addressing only):
+// what attn_split_form and the mask block lists look at.
+static AttnArgs attn_shape(const mq_view *q, const mq_view *k, const mq_view *mask) {
+    AttnArgs a;
+    a.B = (int)q->ne[3], a.Tq = (int)q->ne[1], a.Tk = (int)k->ne[1];
+    a.nq = (int)q->ne[2], a.nkv = (int)k->ne[2], a.hd = (int)q->ne[0];
+    if (mask) {
+        a.mask = (const uint16_t *)mask->data;
+        a.m_sq = mask->nb[1] / 2;
+        a.m_sh = mask->ne[2] == 1 ? 0 : mask->nb[2] / 2;
+        a.m_sb = mask->ne[3] == 1 ? 0 : mask->nb[3] / 2;
+        a.m_al = (uintptr_t)mask->data % 16 == 0 && a.m_sq % 8 == 0 && a.m_sh % 8 == 0 && a.m_sb % 8 == 0;
+        if (!a.mask) a.mask = (const uint16_t *)(uintptr_t)16;  // before allocation: a mask all the same
+    }
+    return a;
+}
+
+// operands whose attention reads mask block lists: the split-key form with a mask shared by
+// every head
+static bool takes_mask_blocks(const mq_view *q, const mq_view *k, const mq_view *mask) {
+    if (!q || !k || !mask || !shape_ok(q) || !shape_ok(k) || !shape_ok(mask) || mask->type != MQ_TYPE_F16 ||
+        mask->ne[2] != 1 || mask->ne[1] < q->ne[1] || mask->ne[0] < k->ne[1] || q->ne[1] > INT32_MAX ||
+        k->ne[1] > INT32_MAX)
+        return false;
+    const AttnArgs a = attn_shape(q, k, mask);
+    return (a.hd == 32 || a.hd == 64 || a.hd == 128) && attn_split_form(a);
+}
+
+extern "C" size_t mq_op_mask_blocks_bytes(const mq_view *q, const mq_view *k, const mq_view *mask) {
+    if (!takes_mask_blocks(q, k, mask)) return 0;
+    return mask_blocks_bytes(mask->ne[3] == 1 ? 1 : (int)q->ne[3], (int)q->ne[1], (int)k->ne[1]);
+}
+
+extern "C" int mq_op_mask_blocks(const mq_view *q, const mq_view *k, const mq_view *mask, void *blocks,
+                                 size_t blocks_bytes, void *stream) {
+    const size_t need = mq_op_mask_blocks_bytes(q, k, mask);
+    if (need == 0) return fail("mask_blocks: these operands' attention takes no block lists");
+    if (!have_data({q, k, mask}) || !blocks) return fail("missing data pointer");
+    if (((uintptr_t)blocks & 3) || blocks_bytes < need)
+        return set_error(MQ_EINVAL, "mq_op_mask_blocks: %zu bytes (4-byte aligned) needed, %zu given", need,
+                         blocks_bytes);
+    const AttnArgs a = attn_shape(q, k, mask);
+    return hip_rc(launch_mask_blocks(a.mask, a.m_sq, a.m_sb, a.m_al, mask->ne[3] == 1 ? 1 : a.B, a.Tq, a.Tk,
+                                     (uint32_t *)blocks, (hipStream_t)stream),
+                  "mask_blocks");
+}
+
 static int flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask, const mq_view *dst,
                       float scale, void *workspace, size_t workspace_bytes, void *act_ws, size_t act_ws_bytes,
-                      int flags, void *stream, const QkNormRope *qk = nullptr) {
+                      int flags, void *stream, const QkNormRope *qk = nullptr, const void *blocks = nullptr) {
     if (const char *e = check_flash(q, k, v, mask, dst)) return fail(e);
     if (!have_data({q, k, v, mask, dst})) return fail("missing data pointer");
     if (qk) {
@@ -1290,6 +1337,13 @@ static int flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, cons
     }
     a.B = (int)q->ne[3], a.Tq = (int)q->ne[1], a.Tk = (int)k->ne[1];
     a.nq = (int)q->ne[2], a.nkv = (int)k->ne[2], a.hd = (int)q->ne[0];
+    if (blocks) {  // lists from mq_op_mask_blocks of these operands; ignored by the other forms
+        if (!mask || !takes_mask_blocks(q, k, mask)) blocks = nullptr;
+        if ((uintptr_t)blocks & 3) return fail("flash_attn: mask block lists not 4-byte aligned");
+        a.blist = (const uint32_t *)blocks;
+        a.bl_nqt = (a.Tq + 31) / 32;
+        a.bl_stride = (a.Tk + 31) / 32 + 1;
+    }
     a.scale = scale;
     a.ws = workspace;
     a.kv_ready = (flags & MQ_ATTN_KV_READY) != 0;
@@ -1337,6 +1391,21 @@ extern "C" int mq_op_flash_attn_qk_norm_rope(const mq_view *q, const mq_view *k,
     const QkNormRope qk{q_norm_w, k_norm_w, cs, eps};
     return flash_attn(q, k, v, mask, dst, scale, workspace, workspace_bytes, act_workspace, act_workspace_bytes, 0,
                       stream, &qk);
+}
+
+extern "C" int mq_op_flash_attn_blocks(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
+                                       const mq_view *dst, float scale, const float *q_norm_w, const float *k_norm_w,
+                                       float eps, const float *cs, const void *mask_blocks, void *workspace,
+                                       size_t workspace_bytes, void *act_workspace, size_t act_workspace_bytes,
+                                       int flags, void *stream) {
+    if (flags & ~MQ_ATTN_KV_READY) return set_error(MQ_EINVAL, "mq_op_flash_attn_blocks: unknown flags");
+    const bool norm = q_norm_w || k_norm_w || cs;
+    if (norm && !(q_norm_w && k_norm_w && cs))
+        return fail("flash_attn_blocks: q_norm_w, k_norm_w and cs go together");
+    if (mask_blocks && !mask) return fail("flash_attn_blocks: block lists without a mask");
+    const QkNormRope qk{q_norm_w, k_norm_w, cs, eps};
+    return flash_attn(q, k, v, mask, dst, scale, workspace, workspace_bytes, act_workspace, act_workspace_bytes, flags,
+                      stream, norm ? &qk : nullptr, mask_blocks);
 }
 
 extern "C" int mq_op_rope_cache(const mq_view *pos, const mq_view *freq_factors, int n_dims, int n_ctx_orig,

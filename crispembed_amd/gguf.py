@@ -300,6 +300,16 @@ def main(argv=None):
     s.add_argument("--type", default="q8_0", choices=["q8_0", "q4_K", "q6_K", "f16"])
     s.add_argument("--layers", type=int, default=None, help="override the layer count")
     s.add_argument("--vocab", type=int, default=None, help="override the token table's row count")
+    s.add_argument("--one-layer", action="store_true",
+                   help="quantize one random layer and store its bytes in every layer (the same work and bytes "
+                        "for a kernel measurement, without quantizing every layer on the host)")
+    i = sub.add_parser("ids", help="write synthetic token ids (int32, item-major) for the graph drivers")
+    i.add_argument("out")
+    i.add_argument("--batch", type=int, default=1)
+    i.add_argument("--tokens", type=int, required=True)
+    i.add_argument("--low", type=int, default=0)
+    i.add_argument("--high", type=int, required=True, help="largest id (inclusive)")
+    i.add_argument("--name", default="ids", help="the seed's name (the same name gives the same ids)")
     d = sub.add_parser("dump", help="list a GGUF file's metadata and tensors")
     d.add_argument("path")
     args = ap.parse_args(argv)
@@ -313,7 +323,19 @@ def main(argv=None):
                 t, ne, data = g.tensor(n)
                 print(f"  {n}: type {t} ne {ne} {data.nbytes} bytes")
         return 0
+    if args.cmd == "ids":
+        from . import synth
+        ids = synth.integers(args.name, (args.batch * args.tokens,), args.low, args.high).astype(np.int32)
+        ids.tofile(args.out)
+        print(f"wrote {args.out}: {args.batch} x {args.tokens} ids in [{args.low}, {args.high}]")
+        return 0
     wtype = {"q8_0": mq.TYPE_Q8_0, "q4_K": mq.TYPE_Q4_K, "q6_K": mq.TYPE_Q6_K, "f16": mq.TYPE_F16}[args.type]
+
+    def weights(mod, hp):
+        if not args.one_layer:
+            return mod.synthetic_weights(hp, wtype)
+        W = mod.synthetic_weights(dict(hp, n_layer=1), wtype)
+        return dict(W, layers=W["layers"] * hp["n_layer"])
     if args.model == "minilm":
         from . import bert
         hp = dict(bert.MINILM_L6)
@@ -321,7 +343,7 @@ def main(argv=None):
             hp["n_layer"] = args.layers
         if args.vocab:
             hp["n_vocab"] = args.vocab
-        write_bert_gguf(args.out, hp, wtype, bert.synthetic_weights(hp, wtype))
+        write_bert_gguf(args.out, hp, wtype, weights(bert, hp))
     else:
         from . import decoder
         hp = dict(decoder.QWEN3_EMBED_0_6B)
@@ -329,7 +351,7 @@ def main(argv=None):
             hp["n_layer"] = args.layers
         if args.vocab:
             hp["n_vocab"] = args.vocab
-        write_decoder_gguf(args.out, hp, wtype, decoder.synthetic_weights(hp, wtype))
+        write_decoder_gguf(args.out, hp, wtype, weights(decoder, hp))
     print(f"wrote {args.out}")
     return 0
 

@@ -50,6 +50,26 @@ GGML_BACKEND_API int ggml_backend_mi355_get_device_count(void);
 GGML_BACKEND_API ggml_backend_reg_t ggml_backend_init(void);
 GGML_BACKEND_API int ggml_backend_score(void);
 
+/* Observer of the quantized activations the products read.  ggml's eval callback (the imatrix
+ * collector's hook, src/imatrix.cpp:57-99, installed at src/crispembed.cpp:723,2483) sees a
+ * MUL_MAT's F32 src1; on this backend every product first quantizes src1 to the weight's
+ * vec_dot_type as ggml-cpu's from_float does (LEARNINGS.md:4826-4830), and this hook shows those
+ * integer activations, so a caller can check them against ggml's quantization of the src1 it
+ * reads.  No counterpart in ggml (the runner-level sibling is mq_decoder_set_observer).  While
+ * set, before each MUL_MAT on a quantized weight reads its activation, the backend synchronizes
+ * its stream and calls cb with the MUL_MAT node, the weight's mq type (MQ_TYPE_*), the product's
+ * path (MQ_PATH_GEMM / MQ_PATH_GEMV), the device address and size of the quantized activation
+ * in the layout mq_quantize_act_ex writes for that type and path (include/mq.h), and its rows
+ * and K.  The activation is readable during the call only.  Grouped products (q|k|v, gate|up)
+ * report the one activation once per member.  Decode-sized K-quant products quantize in a
+ * separate launch while the observer is set (not inside their GEMV), so that every product is
+ * reported; a product over batches whose strides do not continue the rows is not.  cb NULL:
+ * off. */
+typedef void (*ggml_backend_mi355_act_observer)(const struct ggml_tensor *node, int type, int path, const void *act,
+                                                size_t act_bytes, int64_t rows, int64_t k, void *user);
+GGML_BACKEND_API void ggml_backend_mi355_set_act_observer(ggml_backend_t backend, ggml_backend_mi355_act_observer cb,
+                                                          void *user);
+
 #ifdef __cplusplus
 }
 #endif

@@ -200,6 +200,31 @@ int mq_op_flash_attn_qk_norm_rope(const mq_view *q, const mq_view *k, const mq_v
                                   float eps, const float *cs, void *workspace, size_t workspace_bytes,
                                   void *act_workspace, size_t act_workspace_bytes, void *stream);
 
+/* Block lists of an attention mask, for the batched decoder's T_total x T_total F16 mask
+ * (decoder_encode_tokens_batch, src/decoder_embed.cpp:1406-1443 builds it, :1517 passes it to
+ * every layer's ggml_flash_attn_ext): for each tile of 32 query rows, the 32-key blocks in
+ * which some row of the tile has a finite mask value, and whether the block's values are all
+ * zero.  The attention then runs only those blocks (an all-zero block with no mask reads),
+ * instead of classifying the whole mask in every workgroup of every layer: one pass over the
+ * mask per graph.  mq_op_mask_blocks_bytes is 0 when the attention of these q / k / mask
+ * operands (as mq_op_flash_attn takes them) reads no block lists: no mask, a mask that differs
+ * per head, or an attention form that classifies per block itself; else the bytes of device
+ * memory mq_op_mask_blocks fills (4-byte aligned).  The lists stay valid while the mask's
+ * values and the operands' shapes do. */
+size_t mq_op_mask_blocks_bytes(const mq_view *q, const mq_view *k, const mq_view *mask);
+int mq_op_mask_blocks(const mq_view *q, const mq_view *k, const mq_view *mask, void *blocks, size_t blocks_bytes,
+                      void *stream);
+
+/* The general attention entry point: mq_op_flash_attn_ex with flags, plus the q / k norm and
+ * rotation of mq_op_flash_attn_qk_norm_rope when q_norm_w, k_norm_w and cs are given (all three,
+ * or all NULL), plus mask_blocks: NULL, or mq_op_mask_blocks' lists for these q, k and mask
+ * (ignored when mq_op_mask_blocks_bytes of the operands is 0).  Results equal those entry points'
+ * up to the order in which the waves of a query tile share out its key blocks. */
+int mq_op_flash_attn_blocks(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
+                            const mq_view *dst, float scale, const float *q_norm_w, const float *k_norm_w, float eps,
+                            const float *cs, const void *mask_blocks, void *workspace, size_t workspace_bytes,
+                            void *act_workspace, size_t act_workspace_bytes, int flags, void *stream);
+
 /* ggml_mul_mat_id, the mixture-of-experts mat-mul (src/crispembed.cpp:1365,1371):
  *   experts: n_exp prepared weight images of `type` (n x k each, as mq_weight_prepare builds
  *            them), expert e at expert_images + e * expert_stride bytes;

@@ -481,6 +481,122 @@ def test_flash_attn_mask_block_classes(monkeypatch, rows, waves, hd, nh, nkv, Tq
     assert np.abs(got - ref).max() / np.abs(ref).max() <= 2e-5
 
 
+def _batch_mask(lens, slot, prefix=0):
+    """The T_total x T_total mask decoder_encode_tokens_batch builds (src/decoder_embed.cpp:
+    1406-1443), restated: items of lens[b] tokens in slots of `slot` positions after a shared
+    prefix of `prefix` tokens (lens include the prefix); causal within an item and to the prefix,
+    a padding position sees only itself."""
+    B = len(lens)
+    T = prefix + slot * B
+    m = np.full((T, T), -np.inf, np.float32)
+    for t in range(prefix):
+        m[t, :t + 1] = 0
+    for b, n in enumerate(lens):
+        base, sl = prefix + b * slot, n - prefix
+        for s in range(sl):
+            m[base + s, :prefix] = 0
+            m[base + s, base:base + s + 1] = 0
+        for s in range(sl, slot):
+            m[base + s, base + s] = 0
+    return m.astype(np.float16)
+
+
+def _block_lists(mask, Tq, Tk):
+    """The block lists mq_op_mask_blocks must write for mask [Bm, >= Tq, >= Tk] (f16): per mask
+    plane and tile of 32 query rows (rows past Tq repeat row Tq - 1), the 32-key blocks with a
+    finite value, each flagged when a value is not zero (+-0 are zero; keys past Tk ignored)."""
+    out = []
+    for bm in range(mask.shape[0]):
+        for qt in range((Tq + 31) // 32):
+            rows = np.minimum(qt * 32 + np.arange(32), Tq - 1)
+            blk = mask[bm, rows, :Tk].astype(np.float32)
+            lst = []
+            for kb in range((Tk + 31) // 32):
+                v = blk[:, kb * 32:min(kb * 32 + 32, Tk)]
+                if (v != -np.inf).any():
+                    lst.append((kb, bool((v != 0).any())))
+            out.append(lst)
+    return out
+
+
+@pytest.mark.parametrize("case", ["batch_ragged", "prefix", "planes", "unaligned", "tq_ne_tk"])
+def test_mask_block_lists(case):
+    """mq_op_mask_blocks against the lists restated in numpy (every entry, in order), and
+    mq_op_flash_attn_blocks with those lists against fp64 softmax attention and against the same
+    call without lists: the batched decoder's block-diagonal causal mask with ragged items and
+    padding positions, its prefix-sharing layout, per-batch mask planes, mask rows that are not
+    16-byte aligned (2-byte reads), and Tq != Tk with a finite bias band."""
+    L = mq.lib()
+    rng = _rng(len(case))
+    hd, nh, nkv, B = 128, 4, 2, 1
+    if case == "batch_ragged":
+        mask = _batch_mask([100, 37, 64, 1], 100)[None]
+    elif case == "prefix":
+        mask = _batch_mask([70, 47, 90], 50, prefix=40)[None]
+    elif case == "planes":
+        B = 2
+        mask = np.stack([_batch_mask([60, 5, 33], 60), _batch_mask([17, 60, 60], 60)])
+    elif case == "unaligned":
+        mask = _batch_mask([45, 45, 10], 45)[None]
+    else:
+        Tq, Tk = 70, 333
+        m = np.where(np.arange(Tk)[None, :] > np.arange(Tq)[:, None] + (Tk - Tq), -np.inf, 0.0)
+        m[:, 100:140] += rng.standard_normal((Tq, 40))
+        m[:, 200:290] = -np.inf
+        mask = m.astype(np.float16)[None]
+    Tq, Tk = mask.shape[1], mask.shape[2]
+    stride = (Tk + 7) // 8 * 8 + (case == "unaligned")
+    padded = np.full((mask.shape[0], 1, Tq, stride), np.nan, np.float16)
+    padded[:, 0, :, :Tk] = mask
+    mask_d = _cuda(padded)[..., :Tk]
+    qx = rng.standard_normal((B, Tq, nh, hd)).astype(np.float32)
+    kx, vx = (rng.standard_normal((B, Tk, nkv, hd)).astype(np.float32) for _ in range(2))
+    q, k, v = (_cuda(x).permute(0, 2, 1, 3) for x in (qx, kx, vx))
+    qv, kv, vv, mv = mq.view(q), mq.view(k), mq.view(v), mq.view(mask_d)
+    nbytes = L.mq_op_mask_blocks_bytes(qv, kv, mv)
+    nqt, nkb = (Tq + 31) // 32, (Tk + 31) // 32
+    assert nbytes == mask.shape[0] * nqt * (nkb + 1) * 4
+    blocks = _t().full((nbytes // 4,), 0x7777, dtype=_t().int32, device="cuda")
+    _call(L.mq_op_mask_blocks, qv, kv, mv, ctypes.c_void_p(blocks.data_ptr()), nbytes, stream())
+    got = host(blocks).view(np.uint32).reshape(mask.shape[0] * nqt, nkb + 1)
+    want = _block_lists(mask, Tq, Tk)
+    for i, lst in enumerate(want):
+        n = int(got[i, 0])
+        assert n == len(lst), (i, n, len(lst))
+        assert [(int(e & 0x7FFFFFFF), bool(e >> 31)) for e in got[i, 1:1 + n]] == lst, i
+    ws_bytes = L.mq_op_flash_attn_workspace_bytes(kv)
+    ws = _t().empty(ws_bytes + 256, dtype=_t().uint8, device="cuda")
+    wp = ctypes.c_void_p(ws.data_ptr() + (-ws.data_ptr()) % 256)
+    scale = 1.0 / np.sqrt(hd)
+    ref = _attn64(qx.transpose(0, 2, 1, 3), kx.transpose(0, 2, 1, 3), vx.transpose(0, 2, 1, 3), mask[:, None], scale)
+    outs = []
+    for bl in (ctypes.c_void_p(blocks.data_ptr()), None):
+        out = _t().full((B, Tq, nh, hd), np.nan, dtype=_t().float32, device="cuda")
+        _call(L.mq_op_flash_attn_blocks, qv, kv, vv, mv, mq.view(out), scale, None, None, 0.0, None, bl, wp,
+              ws_bytes, None, 0, 0, stream())
+        outs.append(host(out))
+        assert np.isfinite(outs[-1]).all()
+        assert np.abs(outs[-1] - ref).max() / np.abs(ref).max() <= 2e-5
+    assert np.abs(outs[0] - outs[1]).max() / np.abs(ref).max() <= 1e-6
+
+
+def test_mask_block_lists_not_taken():
+    """Operands whose attention reads no block lists get 0 bytes (and mq_op_mask_blocks refuses
+    them): a mask that differs per head, no mask, and head_dim 64 on a grid the 8-wave kernel
+    fills (it classifies blocks itself)."""
+    L = mq.lib()
+    q = _cuda(np.zeros((1, 4, 64, 128), np.float32))
+    k = _cuda(np.zeros((1, 2, 64, 128), np.float32))
+    per_head = _cuda(np.zeros((1, 4, 64, 64), np.float16))
+    assert L.mq_op_mask_blocks_bytes(mq.view(q), mq.view(k), mq.view(per_head)) == 0
+    assert L.mq_op_mask_blocks_bytes(mq.view(q), mq.view(k), None) == 0
+    assert L.mq_op_mask_blocks(mq.view(q), mq.view(k), mq.view(per_head), None, 0, stream()) < 0
+    q64 = _cuda(np.zeros((32, 12, 128, 64), np.float32))
+    k64 = _cuda(np.zeros((32, 12, 128, 64), np.float32))
+    m64 = _cuda(np.zeros((32, 1, 128, 128), np.float16))
+    assert L.mq_op_mask_blocks_bytes(mq.view(q64), mq.view(k64), mq.view(m64)) == 0
+
+
 @pytest.mark.parametrize("case", ["plain", "yarn", "freq_factors"])
 def test_rope_cache_matches_rope(case):
     """mq_op_rope_cache against mq_op_rope: rotating the pair (1, 0) gives (cos, sin) x mscale
