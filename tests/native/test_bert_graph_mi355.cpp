@@ -15,6 +15,13 @@
 //   with NaN bytes; and once more node by node (MQ_GGML_NO_FUSION=1) as the reference.  Reports
 //   how many observed src1 still hold NaN (unwritten), the largest relative difference of any
 //   src1 and of the imatrix sums (sum of x^2 per column) against the node-by-node run.
+//   --packed [--pack-maxtok N]: the reference's default GPU batching instead (encode_tokens_packed
+//   with its greedy grouping, src/crispembed.cpp:1870-2008, 2192-2216): items are packed end to end,
+//   in groups of at most N tokens (default 384; an item longer than N forms its own group), each
+//   group one graph of T_g = its summed lengths with B = 1, positions restarting per item, and the
+//   block-diagonal F16 mask "seg_mask" [T_g, T_g] (0 within an item, -inf elsewhere); a group of
+//   one item is encode_tokens' graph (no mask).  out then holds the groups' rows one after another
+//   (each item's real tokens only); --iters times all groups' graph_compute calls in sequence.
 //   --check-replay: after the first (eager) compute, computes the graph for a second id set
 //   (each id + 1; the backend captures it), then for the first set and the second again (the
 //   captured graph replayed, with uploads and readbacks in between), and reports whether the
@@ -62,9 +69,11 @@ int main(int argc, char **argv) {
     if (argc < 8) return fail("usage: model.gguf B T ids types lens out [--fused-qkv] [--iters N]");
     const char *path = argv[1];
     const int B = std::atoi(argv[2]), T = std::atoi(argv[3]);
-    bool fused_qkv = false, check_replay = false, observe = false;
-    int iters = 0;
+    bool fused_qkv = false, check_replay = false, observe = false, packed = false;
+    int iters = 0, pack_maxtok = 384;
     for (int i = 8; i < argc; i++) {
+        if (!std::strcmp(argv[i], "--packed")) packed = true;
+        if (!std::strcmp(argv[i], "--pack-maxtok") && i + 1 < argc) pack_maxtok = std::atoi(argv[++i]);
         if (!std::strcmp(argv[i], "--fused-qkv")) fused_qkv = true;
         if (!std::strcmp(argv[i], "--check-replay")) check_replay = true;
         if (!std::strcmp(argv[i], "--observe")) observe = true;
@@ -135,75 +144,167 @@ int main(int argc, char **argv) {
         }
     }
 
-    // the graph (build_encoder_graph's standard post-LN path)
-    ggml_init_params gp = {ggml_tensor_overhead() * (size_t)(n_layer * 64 + 64) + ggml_graph_overhead(), nullptr, true};
-    ggml_context *gctx = ggml_init(gp);
-    ggml_tensor *tok_ids = ggml_new_tensor_1d(gctx, GGML_TYPE_I32, TB);
-    ggml_set_name(tok_ids, "tok_ids");
-    ggml_set_input(tok_ids);
-    ggml_tensor *pos_ids = ggml_new_tensor_1d(gctx, GGML_TYPE_I32, TB);
-    ggml_set_name(pos_ids, "pos_ids");
-    ggml_set_input(pos_ids);
-    ggml_tensor *type_ids = ggml_new_tensor_1d(gctx, GGML_TYPE_I32, TB);
-    ggml_set_name(type_ids, "type_ids");
-    ggml_set_input(type_ids);
-    ggml_tensor *pad_mask = nullptr;
-    if (padded && B > 1) {
-        pad_mask = ggml_new_tensor_4d(gctx, GGML_TYPE_F16, T, T, 1, B);
-        ggml_set_name(pad_mask, "pad_mask");
-        ggml_set_input(pad_mask);
-    }
-    ggml_tensor *cur = ggml_get_rows(gctx, W["token_embd.weight"], tok_ids);
-    cur = ggml_add(gctx, cur, ggml_get_rows(gctx, W["position_embd.weight"], pos_ids));
-    cur = ggml_add(gctx, cur, ggml_get_rows(gctx, W["token_type_embd.weight"], type_ids));
-    cur = ggml_norm(gctx, cur, eps);
-    cur = ggml_mul(gctx, cur, W["embd_ln.weight"]);
-    cur = ggml_add(gctx, cur, W["embd_ln.bias"]);
-    for (int il = 0; il < n_layer; il++) {
-        const std::string p = "enc." + std::to_string(il) + ".";
-        auto w = [&](const char *n) { return W[p + n]; };
-        ggml_tensor *inp = cur, *Q, *K, *V;
-        if (fused_qkv) {
-            ggml_tensor *qkv = ggml_add(gctx, ggml_mul_mat(gctx, qkv_w[il], cur), qkv_b[il]);
-            Q = ggml_cont(gctx, ggml_view_2d(gctx, qkv, H, TB, 3 * H * sizeof(float), 0));
-            K = ggml_cont(gctx, ggml_view_2d(gctx, qkv, H, TB, 3 * H * sizeof(float), H * sizeof(float)));
-            V = ggml_cont(gctx, ggml_view_2d(gctx, qkv, H, TB, 3 * H * sizeof(float), 2 * H * sizeof(float)));
-        } else {
-            Q = ggml_add(gctx, ggml_mul_mat(gctx, w("attn.q.weight"), cur), w("attn.q.bias"));
-            K = ggml_add(gctx, ggml_mul_mat(gctx, w("attn.k.weight"), cur), w("attn.k.bias"));
-            V = ggml_add(gctx, ggml_mul_mat(gctx, w("attn.v.weight"), cur), w("attn.v.bias"));
+    // the graph (build_encoder_graph's standard post-LN path) for Bg items of Tg tokens; mask_kind
+    // 0: none, 1: the per-item padding mask [Tg, Tg, 1, Bg], 2: the packed seg_mask [Tg, Tg]
+    struct EncGraph {
+        ggml_context *ctx;
+        ggml_cgraph *gf;
+        ggml_tensor *tok_ids, *pos_ids, *type_ids, *mask, *out;
+    };
+    auto build_graph = [&](int Bg, int Tg, int mask_kind) {
+        EncGraph e{};
+        const int TBg = Bg * Tg;
+        ggml_init_params gp = {ggml_tensor_overhead() * (size_t)(n_layer * 64 + 64) + ggml_graph_overhead(), nullptr,
+                               true};
+        ggml_context *gctx = e.ctx = ggml_init(gp);
+        e.tok_ids = ggml_new_tensor_1d(gctx, GGML_TYPE_I32, TBg);
+        ggml_set_name(e.tok_ids, "tok_ids");
+        ggml_set_input(e.tok_ids);
+        e.pos_ids = ggml_new_tensor_1d(gctx, GGML_TYPE_I32, TBg);
+        ggml_set_name(e.pos_ids, "pos_ids");
+        ggml_set_input(e.pos_ids);
+        e.type_ids = ggml_new_tensor_1d(gctx, GGML_TYPE_I32, TBg);
+        ggml_set_name(e.type_ids, "type_ids");
+        ggml_set_input(e.type_ids);
+        if (mask_kind == 1) {
+            e.mask = ggml_new_tensor_4d(gctx, GGML_TYPE_F16, Tg, Tg, 1, Bg);
+            ggml_set_name(e.mask, "pad_mask");
+            ggml_set_input(e.mask);
+        } else if (mask_kind == 2) {
+            e.mask = ggml_new_tensor_2d(gctx, GGML_TYPE_F16, Tg, Tg);
+            ggml_set_name(e.mask, "seg_mask");
+            ggml_set_input(e.mask);
         }
-        Q = ggml_permute(gctx, ggml_reshape_4d(gctx, Q, hd, n_head, T, B), 0, 2, 1, 3);
-        K = ggml_permute(gctx, ggml_reshape_4d(gctx, K, hd, n_head, T, B), 0, 2, 1, 3);
-        V = ggml_permute(gctx, ggml_reshape_4d(gctx, V, hd, n_head, T, B), 0, 2, 1, 3);
-        ggml_tensor *attn = ggml_flash_attn_ext(gctx, Q, K, V, pad_mask, 1.0f / std::sqrt((float)hd), 0.0f, 0.0f);
-        attn = ggml_reshape_2d(gctx, attn, H, TB);
-        attn = ggml_add(gctx, ggml_mul_mat(gctx, w("attn.o.weight"), attn), w("attn.o.bias"));
-        cur = ggml_add(gctx, inp, attn);
+        ggml_tensor *cur = ggml_get_rows(gctx, W["token_embd.weight"], e.tok_ids);
+        cur = ggml_add(gctx, cur, ggml_get_rows(gctx, W["position_embd.weight"], e.pos_ids));
+        cur = ggml_add(gctx, cur, ggml_get_rows(gctx, W["token_type_embd.weight"], e.type_ids));
         cur = ggml_norm(gctx, cur, eps);
-        cur = ggml_mul(gctx, cur, w("ln1.weight"));
-        cur = ggml_add(gctx, cur, w("ln1.bias"));
-        ggml_tensor *ffn = ggml_add(gctx, ggml_mul_mat(gctx, w("ffn.fc1.weight"), cur), w("ffn.fc1.bias"));
-        ffn = ggml_gelu_erf(gctx, ffn);
-        ffn = ggml_add(gctx, ggml_mul_mat(gctx, w("ffn.fc2.weight"), ffn), w("ffn.fc2.bias"));
-        cur = ggml_add(gctx, cur, ffn);
-        cur = ggml_norm(gctx, cur, eps);
-        cur = ggml_mul(gctx, cur, w("ln2.weight"));
-        cur = ggml_add(gctx, cur, w("ln2.bias"));
-    }
-    ggml_set_name(cur, "encoder_out");
-    ggml_set_output(cur);
-    ggml_cgraph *gf = ggml_new_graph(gctx);
-    ggml_build_forward_expand(gf, cur);
+        cur = ggml_mul(gctx, cur, W["embd_ln.weight"]);
+        cur = ggml_add(gctx, cur, W["embd_ln.bias"]);
+        for (int il = 0; il < n_layer; il++) {
+            const std::string p = "enc." + std::to_string(il) + ".";
+            auto w = [&](const char *n) { return W[p + n]; };
+            ggml_tensor *inp = cur, *Q, *K, *V;
+            if (fused_qkv) {
+                ggml_tensor *qkv = ggml_add(gctx, ggml_mul_mat(gctx, qkv_w[il], cur), qkv_b[il]);
+                Q = ggml_cont(gctx, ggml_view_2d(gctx, qkv, H, TBg, 3 * H * sizeof(float), 0));
+                K = ggml_cont(gctx, ggml_view_2d(gctx, qkv, H, TBg, 3 * H * sizeof(float), H * sizeof(float)));
+                V = ggml_cont(gctx, ggml_view_2d(gctx, qkv, H, TBg, 3 * H * sizeof(float), 2 * H * sizeof(float)));
+            } else {
+                Q = ggml_add(gctx, ggml_mul_mat(gctx, w("attn.q.weight"), cur), w("attn.q.bias"));
+                K = ggml_add(gctx, ggml_mul_mat(gctx, w("attn.k.weight"), cur), w("attn.k.bias"));
+                V = ggml_add(gctx, ggml_mul_mat(gctx, w("attn.v.weight"), cur), w("attn.v.bias"));
+            }
+            Q = ggml_permute(gctx, ggml_reshape_4d(gctx, Q, hd, n_head, Tg, Bg), 0, 2, 1, 3);
+            K = ggml_permute(gctx, ggml_reshape_4d(gctx, K, hd, n_head, Tg, Bg), 0, 2, 1, 3);
+            V = ggml_permute(gctx, ggml_reshape_4d(gctx, V, hd, n_head, Tg, Bg), 0, 2, 1, 3);
+            ggml_tensor *attn = ggml_flash_attn_ext(gctx, Q, K, V, e.mask, 1.0f / std::sqrt((float)hd), 0.0f, 0.0f);
+            attn = ggml_reshape_2d(gctx, attn, H, TBg);
+            attn = ggml_add(gctx, ggml_mul_mat(gctx, w("attn.o.weight"), attn), w("attn.o.bias"));
+            cur = ggml_add(gctx, inp, attn);
+            cur = ggml_norm(gctx, cur, eps);
+            cur = ggml_mul(gctx, cur, w("ln1.weight"));
+            cur = ggml_add(gctx, cur, w("ln1.bias"));
+            ggml_tensor *ffn = ggml_add(gctx, ggml_mul_mat(gctx, w("ffn.fc1.weight"), cur), w("ffn.fc1.bias"));
+            ffn = ggml_gelu_erf(gctx, ffn);
+            ffn = ggml_add(gctx, ggml_mul_mat(gctx, w("ffn.fc2.weight"), ffn), w("ffn.fc2.bias"));
+            cur = ggml_add(gctx, cur, ffn);
+            cur = ggml_norm(gctx, cur, eps);
+            cur = ggml_mul(gctx, cur, w("ln2.weight"));
+            cur = ggml_add(gctx, cur, w("ln2.bias"));
+        }
+        ggml_set_name(cur, "encoder_out");
+        ggml_set_output(cur);
+        e.gf = ggml_new_graph(gctx);
+        ggml_build_forward_expand(e.gf, cur);
+        e.out = cur;
+        return e;
+    };
+    auto count_unsupported = [&](ggml_cgraph *gf) {  // every node must be claimed by the backend
+        int u = 0;
+        for (int i = 0; i < ggml_graph_n_nodes(gf); i++)
+            if (!ggml_backend_supports_op(be, ggml_graph_node(gf, i))) {
+                std::fprintf(stderr, "unsupported node %d: %s %s\n", i, ggml_op_name(ggml_graph_node(gf, i)->op),
+                             ggml_graph_node(gf, i)->name);
+                u++;
+            }
+        return u;
+    };
 
-    // every node must be claimed by the backend (nothing would fall back to the CPU)
-    int unsupported = 0;
-    for (int i = 0; i < ggml_graph_n_nodes(gf); i++)
-        if (!ggml_backend_supports_op(be, ggml_graph_node(gf, i))) {
-            std::fprintf(stderr, "unsupported node %d: %s %s\n", i, ggml_op_name(ggml_graph_node(gf, i)->op),
-                         ggml_graph_node(gf, i)->name);
-            unsupported++;
+    if (packed) {  // encode_tokens_packed over the greedy groups
+        const int32_t *ids_in = (const int32_t *)ids_raw.data(), *types_in = (const int32_t *)types_raw.data();
+        struct Group {
+            EncGraph e;
+            ggml_backend_buffer_t buf;
+            int i0, i1, T;
+        };
+        std::vector<Group> groups;
+        int unsupported = 0, nodes = 0;
+        for (int i = 0; i < B;) {
+            int j = i, tsum = 0;
+            while (j < B && !(j > i && tsum + lens[j] > pack_maxtok)) tsum += lens[j++];
+            Group gr{build_graph(1, tsum, j - i > 1 ? 2 : 0), nullptr, i, j, tsum};
+            unsupported += count_unsupported(gr.e.gf);
+            nodes += ggml_graph_n_nodes(gr.e.gf);
+            gr.buf = ggml_backend_alloc_ctx_tensors(gr.e.ctx, be);
+            if (!gr.buf) return fail("graph buffer allocation failed");
+            std::vector<int32_t> tok, pos, typ;
+            std::vector<uint16_t> m;
+            if (gr.e.mask) m.assign((size_t)tsum * tsum, 0xFC00);
+            for (int b = i, s0 = 0; b < j; s0 += lens[b], b++)
+                for (int t = 0; t < lens[b]; t++) {
+                    tok.push_back(ids_in[(size_t)b * T + t]), typ.push_back(types_in[(size_t)b * T + t]);
+                    pos.push_back(t);
+                    if (gr.e.mask)
+                        for (int k = 0; k < lens[b]; k++) m[(size_t)(s0 + t) * tsum + s0 + k] = 0x0000;
+                }
+            ggml_backend_tensor_set(gr.e.tok_ids, tok.data(), 0, tok.size() * 4);
+            ggml_backend_tensor_set(gr.e.pos_ids, pos.data(), 0, pos.size() * 4);
+            ggml_backend_tensor_set(gr.e.type_ids, typ.data(), 0, typ.size() * 4);
+            if (gr.e.mask) ggml_backend_tensor_set(gr.e.mask, m.data(), 0, m.size() * 2);
+            groups.push_back(gr);
+            i = j;
         }
+        std::vector<float> out;
+        for (const Group &gr : groups) {
+            if (ggml_backend_graph_compute(be, gr.e.gf) != GGML_STATUS_SUCCESS) return fail("graph_compute failed");
+            const size_t at = out.size();
+            out.resize(at + (size_t)H * gr.T);
+            ggml_backend_tensor_get(gr.e.out, out.data() + at, 0, (size_t)H * gr.T * sizeof(float));
+        }
+        FILE *f = std::fopen(argv[7], "wb");
+        if (!f || std::fwrite(out.data(), sizeof(float), out.size(), f) != out.size()) return fail("cannot write output");
+        std::fclose(f);
+        double ms = 0.0;
+        if (iters > 0) {
+            const auto t0 = std::chrono::steady_clock::now();
+            for (int it = 0; it < iters; it++)
+                for (const Group &gr : groups)
+                    if (ggml_backend_graph_compute(be, gr.e.gf) != GGML_STATUS_SUCCESS) return fail("graph_compute failed");
+            ggml_backend_synchronize(be);
+            ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() / iters;
+        }
+        std::string sizes;
+        for (const Group &gr : groups) sizes += (sizes.empty() ? "" : ", ") + std::to_string(gr.T);
+        std::printf("{\"ok\": true, \"nodes\": %d, \"unsupported\": %d, \"ms_per_graph\": %.4f, \"iters\": %d, "
+                    "\"groups\": %zu, \"group_tokens\": [%s]}\n",
+                    nodes, unsupported, ms, iters, groups.size(), sizes.c_str());
+        for (Group &gr : groups) {
+            ggml_backend_buffer_free(gr.buf);
+            ggml_free(gr.e.ctx);
+        }
+        ggml_backend_buffer_free(wbuf);
+        ggml_free(wctx);
+        ggml_backend_free(be);
+        mq_gguf_close(g);
+        return 0;
+    }
+
+    const EncGraph eg = build_graph(B, T, padded && B > 1 ? 1 : 0);
+    ggml_context *gctx = eg.ctx;
+    ggml_cgraph *gf = eg.gf;
+    ggml_tensor *tok_ids = eg.tok_ids, *pos_ids = eg.pos_ids, *type_ids = eg.type_ids, *pad_mask = eg.mask, *cur = eg.out;
+    const int unsupported = count_unsupported(gf);
     ggml_backend_buffer_t gbuf = ggml_backend_alloc_ctx_tensors(gctx, be);
     if (!gbuf) return fail("graph buffer allocation failed");
 

@@ -36,7 +36,8 @@ def _run(tmp_path, model, B, T, ids, types, lens, extra=(), env=None):
     res = json.loads(r.stdout.strip().splitlines()[-1])
     assert r.returncode == 0 and res["ok"], res
     assert res["unsupported"] == 0
-    return np.fromfile(out, dtype=np.float32).reshape(B * T, -1), res
+    y = np.fromfile(out, dtype=np.float32)
+    return (y if "--packed" in extra else y.reshape(B * T, -1)), res
 
 
 def _cos_rows(a, b):
@@ -97,6 +98,69 @@ def test_bert_graph_padded_batch(oracle, tmp_path, lens):
         cos = _cos_rows(rows, ref)
         assert np.isfinite(rows).all() and cos.min() >= COSINE_MIN, (b, cos.min())
         assert _pool(rows) @ _pool(ref) >= COSINE_MIN
+
+
+@pytest.mark.parametrize("hd,lens,maxtok", [(32, [37, 5, 20, 1, 64, 64, 33], 100), (64, [40, 40, 40, 3], 384),
+                                            (32, [130, 7], 100)])
+def test_bert_graph_packed_batch(oracle, tmp_path, hd, lens, maxtok):
+    """The reference's default GPU batching (encode_tokens_packed, src/crispembed.cpp:1870-2008, with
+    its greedy grouping :2192-2216): items packed end to end into groups of at most maxtok tokens
+    (an item longer than that alone), positions restarting per item, the block-diagonal F16
+    seg_mask; a group of one item runs unmasked.  Every item's rows against the CPU encoder's
+    encoding of that item alone, per row and pooled, at cosine >= 0.99999."""
+    hp = dict(HP, n_head=HP["n_embd"] // hd, n_max_pos=160)
+    W = bert.synthetic_weights(hp, O.Q8_0, name=f"graphpack{hd}")
+    model = tmp_path / "m.gguf"
+    gguf.write_bert_gguf(model, hp, O.Q8_0, W)
+    lens = np.array(lens, dtype=np.int32)
+    B, T = len(lens), int(lens.max())
+    rng = np.random.default_rng(hd + B)
+    ids = rng.integers(0, hp["n_vocab"], (B, T)).astype(np.int32)
+    types = rng.integers(0, 2, (B, T)).astype(np.int32)
+    got, res = _run(tmp_path, model, B, T, ids, types, lens, ("--packed", "--pack-maxtok", str(maxtok)))
+    groups, i = [], 0
+    while i < B:  # the reference's greedy grouping, restated
+        j, tsum = i, 0
+        while j < B and not (j > i and tsum + lens[j] > maxtok):
+            tsum += lens[j]
+            j += 1
+        groups.append(tsum)
+        i = j
+    assert res["groups"] == len(groups) and res["group_tokens"] == groups
+    got = got.reshape(-1, hp["n_embd"])
+    assert got.shape[0] == lens.sum() and np.isfinite(got).all()
+    at = 0
+    for b, n in enumerate(lens):
+        _, ref = bert_oracle.encode(oracle, hp, O.Q8_0, W, ids[b:b + 1, :n], types[b:b + 1, :n])
+        rows = got[at:at + n]
+        at += n
+        cos = _cos_rows(rows, ref)
+        assert cos.min() >= COSINE_MIN, (b, cos.min())
+        assert _pool(rows) @ _pool(ref) >= COSINE_MIN
+
+
+def test_bert_graph_packed_minilm_full_shape(oracle, tmp_path):
+    """The MiniLM-L6 32 x 128 batch through the packed path at the reference's default budget of
+    384 tokens (10 groups of 3 items and one of 2, each a 384- or 256-token graph with its
+    block-diagonal mask): sampled items against the CPU encoder, and every item against the same
+    batch through the unmasked 4-D batch graph."""
+    hp = dict(bert.MINILM_L6)
+    W = bert.synthetic_weights(hp, O.Q8_0, name="minilm")
+    model = tmp_path / "m.gguf"
+    gguf.write_bert_gguf(model, hp, O.Q8_0, W)
+    B, T = 32, 128
+    ids = np.random.default_rng(32128).integers(1000, 30521, (B, T)).astype(np.int32)
+    types = np.zeros((B, T), np.int32)
+    got, res = _run(tmp_path, model, B, T, ids, types, np.full(B, T), ("--packed",))
+    assert res["groups"] == 11 and res["group_tokens"] == [384] * 10 + [256]
+    got = got.reshape(B * T, -1)
+    plain, _ = _run(tmp_path, model, B, T, ids, types, np.full(B, T))
+    assert _cos_rows(got, plain).min() >= COSINE_MIN
+    for b in (0, 2, 3, 31):
+        _, ref = bert_oracle.encode(oracle, hp, O.Q8_0, W, ids[b:b + 1], types[b:b + 1])
+        rows = got[b * T:(b + 1) * T]
+        assert _cos_rows(rows, ref).min() >= COSINE_MIN, b
+        assert _pool(rows) @ _pool(ref) >= COSINE_MIN, b
 
 
 def test_bert_graph_fusion_off_agrees(tmp_path):

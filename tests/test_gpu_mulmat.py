@@ -89,14 +89,30 @@ def test_library_workspace_and_auto_path(oracle):
     _check(oracle, O.Q4_K, w, x, y2, k)
 
 
+def _full_check(oracle, wtype, w, x, y, k):
+    """Every output element against the oracle's threaded integer-dot product (or_fast_mul_mat:
+    the same activation quantization, integer block dots, fp32 scales; pinned against the exact
+    product by tests/test_oracle_mulmat.py), within 1e-4 of max|Y|, and no row off by more than
+    1e-4 of its own largest value."""
+    import os
+    ref = oracle.fast_mul_mat(wtype, w, x, nthreads=min(16, os.cpu_count() or 8))
+    assert y.shape == ref.shape and np.isfinite(y).all()
+    err = np.abs(y.astype(np.float64) - ref)
+    assert err.max() / np.abs(ref).max() <= TOL, err.max() / np.abs(ref).max()
+    row = err.max(1) / np.abs(ref).max(1)
+    assert row.max() <= TOL, (int(row.argmax()), row.max())
+    return err.max() / np.abs(ref).max()
+
+
 @pytest.mark.parametrize("wtype,n,k,m,act", [
     (O.Q8_0, 1536, 384, 4096, None),          # MiniLM-L6 FFN-up
     (O.Q8_0, 384, 1536, 4096, "gelu"),        # MiniLM-L6 FFN-down
     (O.Q4_K, 4096, 1024, 8192, None),         # XLM-R-large FFN-up
     (O.Q4_K, 1024, 4096, 8192, "gelu"),       # XLM-R-large FFN-down on GELU(N(0,1))
 ])
-def test_full_size_sampled_rows(oracle, wtype, n, k, m, act):
-    """Full-size GEMM; oracle on 40 sampled rows; GEMV on 8 of them must agree too."""
+def test_full_size(oracle, wtype, n, k, m, act):
+    """Full-size GEMM: every output element against the oracle's integer-dot product, sampled
+    rows against the fp64 exact product, and the GEMV on 8 of them."""
     from crispembed_amd import mq, synth
     rng = np.random.default_rng(n + k)
     wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
@@ -110,6 +126,7 @@ def test_full_size_sampled_rows(oracle, wtype, n, k, m, act):
     _, wp = weight_image(wtype, w, n, k)
     xd = dev(x)
     y = host(mul_mat(wtype, wp, n, k, xd, path=mq.PATH_GEMM))
+    print("full-output relative error", _full_check(oracle, wtype, w, x, y, k))
     rows = np.unique(np.concatenate([[0, m - 1], rng.integers(0, m, 38)]))
     _check(oracle, wtype, w, x[rows], y[rows], k)
     yv = host(mul_mat(wtype, wp, n, k, dev(x[rows[:8]]), path=mq.PATH_GEMV))
@@ -120,8 +137,9 @@ def test_full_size_sampled_rows(oracle, wtype, n, k, m, act):
 @pytest.mark.parametrize("m,n,k,pad", [(2048, 4608, 512, 0), (2048, 16384, 768, 64), (4096, 4096, 2048, 0)])
 def test_gemm_many_tiles(oracle, wtype, m, n, k, pad, monkeypatch):
     """256x128 tiles (MQ_GEMM_CFG=1) on grids of 288-1024 tiles, more than the chip holds at once,
-    with K from 2 to 8 superblocks: oracle on sampled rows (first and last of a tile row among
-    them), columns past n untouched (ldy = n + pad)."""
+    with K from 2 to 8 superblocks: every output against the oracle's integer-dot product, sampled
+    rows (first and last of a tile row among them) against the exact product, columns past n
+    untouched (ldy = n + pad)."""
     from crispembed_amd import mq
     import torch
     monkeypatch.setenv("MQ_GEMM_CFG", "1")
@@ -131,6 +149,7 @@ def test_gemm_many_tiles(oracle, wtype, m, n, k, pad, monkeypatch):
     mul_mat(wtype, wp, n, k, dev(x), path=mq.PATH_GEMM, y_dev=ybuf)
     y = host(ybuf)
     assert np.all(y[:, n:] == 7.0)
+    _full_check(oracle, wtype, w, x, np.ascontiguousarray(y[:, :n]), k)
     rng = np.random.default_rng(k)
     rows = np.unique(np.concatenate([[0, 255, 256, m - 1], rng.integers(0, m, 36)]))
     _check(oracle, wtype, w, x[rows], y[rows, :n], k)
