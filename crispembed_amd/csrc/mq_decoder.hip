@@ -970,13 +970,15 @@ static void launch_attn_8w(dim3 grid, const AttnArgs &a, int nblk, float qscale,
 }
 
 // The split-key form when the regular grid (2 heads x 128 queries per workgroup) would leave
-// most CUs idle and there are several key blocks to share out, and for masked head_dim 128 (the
-// 8-wave kernel's mask addressing does not fit its 256 registers and spills); MQ_ATTN_SPLIT=0/1
-// forces either form (measurements)
+// most CUs idle and there are several key blocks to share out, for masked head_dim 128 (the
+// 8-wave kernel's mask addressing does not fit its 256 registers and spills), and for a mask
+// shared by every head over 1024 keys or more (a packed batch's block-diagonal mask: the split
+// form runs only the blocks the mask leaves live, the 8-wave kernel tests every key block);
+// MQ_ATTN_SPLIT=0/1 forces either form (measurements)
 bool attn_split_form(const AttnArgs &a) {
     const int nblk = (a.Tk + 31) / 32;
     const int64_t wgs = (int64_t)((a.nq + 1) / 2) * a.B * ((a.Tq + 127) / 128);
-    bool split = (wgs < 128 && nblk >= 4) || (a.hd == 128 && a.mask);
+    bool split = (wgs < 128 && nblk >= 4) || (a.hd == 128 && a.mask) || (a.mask && a.m_sh == 0 && nblk >= 32);
     if (const char *e = getenv("MQ_ATTN_SPLIT"))
         if (*e) split = atoi(e) != 0;
     return split;

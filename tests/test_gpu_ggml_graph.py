@@ -139,11 +139,13 @@ def test_bert_graph_packed_batch(oracle, tmp_path, hd, lens, maxtok):
         assert _pool(rows) @ _pool(ref) >= COSINE_MIN
 
 
-def test_bert_graph_packed_minilm_full_shape(oracle, tmp_path):
+@pytest.mark.parametrize("maxtok", [384, 4096])
+def test_bert_graph_packed_minilm_full_shape(oracle, tmp_path, maxtok):
     """The MiniLM-L6 32 x 128 batch through the packed path at the reference's default budget of
     384 tokens (10 groups of 3 items and one of 2, each a 384- or 256-token graph with its
-    block-diagonal mask): sampled items against the CPU encoder, and every item against the same
-    batch through the unmasked 4-D batch graph."""
+    block-diagonal mask) and at CRISPEMBED_ENCODER_PACK_MAXTOK=4096 (one 4096-token graph, a
+    4096 x 4096 mask): sampled items against the CPU encoder, and every item against the same batch
+    through the unmasked 4-D batch graph."""
     hp = dict(bert.MINILM_L6)
     W = bert.synthetic_weights(hp, O.Q8_0, name="minilm")
     model = tmp_path / "m.gguf"
@@ -151,8 +153,8 @@ def test_bert_graph_packed_minilm_full_shape(oracle, tmp_path):
     B, T = 32, 128
     ids = np.random.default_rng(32128).integers(1000, 30521, (B, T)).astype(np.int32)
     types = np.zeros((B, T), np.int32)
-    got, res = _run(tmp_path, model, B, T, ids, types, np.full(B, T), ("--packed",))
-    assert res["groups"] == 11 and res["group_tokens"] == [384] * 10 + [256]
+    got, res = _run(tmp_path, model, B, T, ids, types, np.full(B, T), ("--packed", "--pack-maxtok", str(maxtok)))
+    assert res["group_tokens"] == ([384] * 10 + [256] if maxtok == 384 else [4096])
     got = got.reshape(B * T, -1)
     plain, _ = _run(tmp_path, model, B, T, ids, types, np.full(B, T))
     assert _cos_rows(got, plain).min() >= COSINE_MIN
