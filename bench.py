@@ -595,6 +595,134 @@ def cpu_baseline_q4k(args, x_up, x_dn, q_up, q_dn):
     }
 
 
+def cpu_baselines_extras(args):
+    """CPU baselines of the side workloads, on the restated ggml-cpu mul_mat (oracle/cpu_fast.c:
+    the activation quantization, AVX-512 VNNI or AVX2 integer block dots, fp32 scales, output
+    tiles over threads) at the same thread count as the headline's, each on a stated sample:
+      q8_0_minilm_ffn_up  the whole W[1536x384] x X[4096x384] product (TOPS);
+      minilm_l6_e2e       the 36 linear layers of one 32 x 128 batch (6 layers of q,k,v,o [384x384],
+                          fc1 [1536x384], fc2 [384x1536] on 4096 rows; the layers differ only in their
+                          values, so one layer is timed and counted six times): the CPU's
+                          embeddings/s can be no higher than 32 / that time (LEARNINGS.md:3397-3402:
+                          the linears are the CPU encoder's time);
+      qwen3_0_6b_e2e      the 196 linear layers of a 16 x 512 batch, timed on one layer over 512 of the
+                          8192 rows and scaled (x 28 layers x 16): the same bound;
+      decode_gemv         the Qwen3-VL-2B layer sweep (28 distinct copies of one layer's 7 Q4_K
+                          matrices, 792.7 MB, more than the host's caches) at m = 1 and 8, per-layer
+                          time and weight GB/s; and the Q6_K lm_head [151936x2048] (4096 quantized rows
+                          tiled) at m = 1."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import numpy as np
+    import oracle_ffi as O
+    from crispembed_amd import synth
+    orc = O.Oracle()
+    nth, src = cpu_threads()
+    isa = orc.fast_isa()
+    model = cpu_model()
+    impl = {"avx512vnni": "AVX-512 VNNI integer dots", "avx2": "AVX2 integer dots"}.get(isa, "scalar C")
+    budget = max(1.0, args.cpu_seconds / 4)
+
+    def mm(wt, w, x):
+        return orc.fast_mul_mat(wt, w, x, nthreads=nth)
+
+    def timed(fn):
+        fn()
+        times, dt = [], 0.0
+        while len(times) < 10 and (len(times) < 3 or dt < budget):
+            t = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t)
+            dt += times[-1]
+        return sorted(times)[len(times) // 2], len(times)
+
+    def base(value, unit, sample):
+        return {"value": value, "unit": unit, "cores": nth, "kind": "port", "cpu_model": model, "isa": isa,
+                "threads_from": src, "sample": f"{sample}; restated ggml-cpu algorithm ({impl}), {nth} threads "
+                                               f"({src}) on {model}, median of the timed reps"}
+
+    def q(wt, name, n, k):
+        return orc.quantize_chunk(wt, synth.normal(name, (n, k), std=0.02))
+
+    out = {}
+    # cfg1
+    w1, x1 = q(O.Q8_0, "cpu/cfg1_w", 1536, 384), synth.normal("cpu/cfg1_x", (4096, 384))
+    t, reps = timed(lambda: mm(O.Q8_0, w1, x1))
+    out["q8_0_minilm_ffn_up"] = base(2.0 * 4096 * 1536 * 384 / t / 1e12, "TOPS",
+                                     f"the full 4096 x 1536 x 384 Q8_0 product incl. Q8_0 activation quantization, "
+                                     f"{reps} reps: {t * 1e3:.2f} ms")
+    # cfg3: one MiniLM layer's six products on 4096 rows
+    H, F, M = 384, 1536, 4096
+    lay = [q(O.Q8_0, f"cpu/cfg3_{i}", n, k) for i, (n, k) in enumerate([(H, H)] * 4 + [(F, H), (H, F)])]
+    xh, xf = synth.normal("cpu/cfg3_xh", (M, H)), synth.gelu_erf(synth.normal("cpu/cfg3_xf", (M, F)))
+    t, reps = timed(lambda: [mm(O.Q8_0, w, xf if w.shape[1] == O.row_size(O.Q8_0, F) else xh) for w in lay])
+    batch = 6 * t
+    out["minilm_l6_e2e"] = base(32 / batch, "embeddings/s (upper bound: linear layers only)",
+                                f"one layer's q, k, v, o, fc1, fc2 Q8_0 products on the batch's 4096 rows "
+                                f"({reps} reps: {t * 1e3:.1f} ms) x 6 layers = {batch * 1e3:.1f} ms per 32-sequence "
+                                f"batch")
+    # cfg4: one Qwen3 layer's products (q|k|v, o, gate|up, down) on 512 of the 8192 rows
+    H, F, QD, Ms = 1024, 3072, 2048, 512
+    lay = [(q(O.Q4_K, "cpu/cfg4_qkv", QD + 2 * 512 * 2, H), H), (q(O.Q4_K, "cpu/cfg4_o", H, QD), QD),
+           (q(O.Q4_K, "cpu/cfg4_gu", 2 * F, H), H), (q(O.Q4_K, "cpu/cfg4_down", H, F), F)]
+    xs = {k: synth.normal(f"cpu/cfg4_x{k}", (Ms, k)) for k in (H, QD, F)}
+    t, reps = timed(lambda: [mm(O.Q4_K, w, xs[k]) for w, k in lay])
+    batch = t * 28 * (8192 / Ms)
+    out["qwen3_0_6b_e2e"] = base(16 / batch, "embeddings/s (upper bound: linear layers only)",
+                                 f"one layer's q|k|v, o, gate|up, down Q4_K products on 512 of the batch's 8192 "
+                                 f"rows ({reps} reps: {t * 1e3:.1f} ms) x 28 layers x 16 = {batch:.2f} s per "
+                                 f"16-sequence batch")
+    # cfg5: layer sweep over 28 distinct copies, m = 1 and 8; lm_head m = 1
+    H, FF = 2048, 6144
+    shapes = [(H, H), (1024, H), (1024, H), (H, H), (FF, H), (FF, H), (H, FF)]
+    one = [q(O.Q4_K, f"cpu/cfg5_{i}", n, k) for i, (n, k) in enumerate(shapes)]
+    layers = [[w.copy() for w in one] for _ in range(28)]
+    wbytes = 28 * sum(w.nbytes for w in one)
+    dec = {}
+    for m in (1, 8):
+        xs = {k: synth.normal(f"cpu/cfg5_x{k}_{m}", (m, k)) for k in (H, FF)}
+        t, reps = timed(lambda: [mm(O.Q4_K, w, xs[k]) for lay_ in layers for w, (n, k) in zip(lay_, shapes)])
+        dec[f"layer_sweep_q4_K_m{m}"] = {"layer_us": round(t / 28 * 1e6, 1), "weight_gbs": round(wbytes / t / 1e9, 1),
+                                         "sweep_ms": round(t * 1e3, 2), "reps": reps}
+    rows = q(O.Q6_K, "cpu/cfg5_lm_head", 4096, H)
+    head = np.tile(rows, (151936 // 4096 + 1, 1))[:151936]
+    x = synth.normal("cpu/cfg5_xhead", (1, H))
+    t, reps = timed(lambda: mm(O.Q6_K, head, x))
+    dec["lm_head_q6_K_m1"] = {"us": round(t * 1e6, 1), "gbs": round(head.nbytes / t / 1e9, 1), "reps": reps}
+    b = base(dec["layer_sweep_q4_K_m1"]["layer_us"], "us per layer (m = 1)",
+             "28 distinct copies of one Qwen3-VL-2B layer's 7 Q4_K matrices (792.7 MB) swept at m = 1 and 8, and "
+             "the Q6_K lm_head [151936 x 2048] (4096 quantized rows tiled) at m = 1, incl. activation quantization")
+    b["detail"] = dec
+    out["decode_gemv"] = b
+    return out
+
+
+def model_floor(kind):
+    """The sum of per-op roofline floors of one batch of the end-to-end workloads (MI355X datasheet
+    peaks: dense int8 5.0 POP/s, dense fp16 2.5 PFLOP/s, HBM 8 TB/s): each linear layer at
+    max(2 M N K / int8 peak, (GGUF weight + quantized activation + fp32 output bytes) / HBM), the
+    attention at max(its algorithmic flops / fp16 peak, q/k/v/out bytes / HBM), and each
+    embedding / norm pass at its fp32 bytes / HBM.  Returns (floor in us, the formula's terms)."""
+    P8, P16, BW = 5.0e15, 2.5e15, 8.0e12
+    if kind == "minilm":
+        B, T, H, F, nh, nl, wb, ab = 32, 128, 384, 1536, 12, 6, 34 / 32, 34 / 32
+        lin = [(3 * H, H), (H, H), (F, H), (H, F)]
+        att_flops = 4.0 * B * nh * T * T * (H // nh)  # full mask
+        norm_bytes = nl * 2 * (12.0 * B * T * H) + 16.0 * B * T * H  # residual + LN per sublayer; embeddings
+    else:
+        B, T, H, F, nh, nl, wb, ab = 16, 512, 1024, 3072, 16, 28, 144 / 256, 292 / 256
+        lin = [(4096, H), (H, 2048), (2 * F, H), (H, F)]
+        att_flops = 2.0 * B * nh * T * T * 128  # causal: half of 4 T^2 hd
+        norm_bytes = nl * 2 * (12.0 * B * T * H)
+    M = B * T
+    t_lin = nl * sum(max(2.0 * M * n * k / P8, (n * k * wb + M * k * ab + 4.0 * M * n) / BW) for n, k in lin)
+    qd = (2048 if kind != "minilm" else H)
+    att_bytes = 4.0 * M * (qd + 2 * (1024 if kind != "minilm" else H) + qd)
+    t_att = nl * max(att_flops / P16, att_bytes / BW)
+    t_norm = norm_bytes / BW
+    return (t_lin + t_att + t_norm) * 1e6, {"linear_us": round(t_lin * 1e6, 1), "attention_us": round(t_att * 1e6, 1),
+                                           "norm_us": round(t_norm * 1e6, 1)}
+
+
 def cpu_threads():
     """Threads for the CPU baseline: the CPUs this process may run on (what nproc reports), or
     fewer when OMP_NUM_THREADS grants the job a smaller share of the host (BENCH_CPU_THREADS
@@ -609,13 +737,20 @@ def cpu_threads():
 
 
 def cpu_model():
+    """The host CPU: /proc/cpuinfo's model name, family / model / stepping, and the CPU count this
+    process may use."""
+    f = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k in ("model name", "cpu family", "model", "stepping") and k not in f:
+                f[k] = v.strip()
     except OSError:
         pass
-    return "unknown CPU"
+    name = f.get("model name", "unknown CPU")
+    return (f"{name} (family {f.get('cpu family', '?')} model {f.get('model', '?')} stepping "
+            f"{f.get('stepping', '?')}, {len(os.sched_getaffinity(0))} CPUs visible)")
 
 
 def main():
@@ -674,6 +809,18 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_q4k(args, x_up, x_dn, q_up, q_dn)
+        if extras is not None:
+            for name, b in cpu_baselines_extras(args).items():
+                if isinstance(extras.get(name), dict):
+                    extras[name]["cpu_baseline"] = b
+    if extras is not None:
+        for name, kind in (("minilm_l6_e2e", "minilm"), ("qwen3_0_6b_e2e", "qwen3")):
+            e = extras.get(name)
+            if isinstance(e, dict) and "batch_ms" in e:
+                floor, terms = model_floor(kind)
+                e["roofline"] = {"bound": "sum of per-op floors", "floor_us": round(floor, 1), "terms": terms,
+                                 "achieved_us": round(e["batch_ms"] * 1e3, 1),
+                                 "frac": round(floor / (e["batch_ms"] * 1e3), 4)}
     out = {
         "metric": METRIC,
         "value": r["value"],

@@ -307,14 +307,76 @@ FAST_TARGET static void *dot_worker(void *arg) {
     return NULL;
 }
 
-static void run_threads(void *(*fn)(void *), fast_job *j, int nthreads) {
+/* A persistent worker pool, as ggml-cpu keeps one (its threadpool spins between ops instead of
+ * creating threads per op): workers wait for a new job generation, spinning for a while and then
+ * sleeping on a condition variable; the caller runs the job too and waits for the workers it
+ * used.  Creating and joining threads per call cost ~20 us a thread, which at decode sizes (one
+ * activation row, a 1-5 MB weight) was most of the call. */
+static struct {
+    pthread_mutex_t mu;
+    pthread_cond_t wake, done;
     pthread_t th[256];
+    int size;                  /* workers created */
+    unsigned gen;              /* job generation (atomic) */
+    int active;                /* workers taking part in the current job */
+    int pending;               /* of those, still running */
+    void *(*fn)(void *);
+    fast_job *job;
+} pool = {.mu = PTHREAD_MUTEX_INITIALIZER, .wake = PTHREAD_COND_INITIALIZER, .done = PTHREAD_COND_INITIALIZER};
+
+static void *pool_worker(void *arg) {
+    const int idx = (int)(intptr_t)arg;
+    unsigned seen = 0;
+    for (;;) {
+        unsigned g = __atomic_load_n(&pool.gen, __ATOMIC_ACQUIRE);
+        for (int spin = 0; g == seen && spin < 200000; spin++) {
+            __builtin_ia32_pause();
+            g = __atomic_load_n(&pool.gen, __ATOMIC_ACQUIRE);
+        }
+        if (g == seen) {
+            pthread_mutex_lock(&pool.mu);
+            while ((g = __atomic_load_n(&pool.gen, __ATOMIC_ACQUIRE)) == seen) pthread_cond_wait(&pool.wake, &pool.mu);
+            pthread_mutex_unlock(&pool.mu);
+        }
+        seen = g;
+        if (idx >= pool.active) continue;
+        pool.fn(pool.job);
+        if (__atomic_sub_fetch(&pool.pending, 1, __ATOMIC_ACQ_REL) == 0) {
+            pthread_mutex_lock(&pool.mu);
+            pthread_cond_signal(&pool.done);
+            pthread_mutex_unlock(&pool.mu);
+        }
+    }
+    return NULL;
+}
+
+static void run_threads(void *(*fn)(void *), fast_job *j, int nthreads) {
     if (nthreads < 1) nthreads = 1;
-    if (nthreads > 256) nthreads = 256;
+    if (nthreads > 257) nthreads = 257;
     j->next = 0;
-    for (int i = 1; i < nthreads; i++) pthread_create(&th[i], NULL, fn, j);
+    const int workers = nthreads - 1;
+    if (workers == 0) {
+        fn(j);
+        return;
+    }
+    pthread_mutex_lock(&pool.mu);
+    while (pool.size < workers) {
+        if (pthread_create(&pool.th[pool.size], NULL, pool_worker, (void *)(intptr_t)pool.size) != 0) break;
+        pthread_detach(pool.th[pool.size]);
+        pool.size++;
+    }
+    pool.fn = fn, pool.job = j;
+    pool.active = workers < pool.size ? workers : pool.size;
+    __atomic_store_n(&pool.pending, pool.active, __ATOMIC_RELEASE);
+    __atomic_add_fetch(&pool.gen, 1, __ATOMIC_RELEASE);
+    pthread_cond_broadcast(&pool.wake);
+    pthread_mutex_unlock(&pool.mu);
     fn(j);
-    for (int i = 1; i < nthreads; i++) pthread_join(th[i], NULL);
+    for (int spin = 0; __atomic_load_n(&pool.pending, __ATOMIC_ACQUIRE) != 0 && spin < 2000000; spin++)
+        __builtin_ia32_pause();
+    pthread_mutex_lock(&pool.mu);
+    while (__atomic_load_n(&pool.pending, __ATOMIC_ACQUIRE) != 0) pthread_cond_wait(&pool.done, &pool.mu);
+    pthread_mutex_unlock(&pool.mu);
 }
 
 int or_fast_supported(int wtype) {

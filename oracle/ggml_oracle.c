@@ -318,7 +318,11 @@ void or_quantize_row_q4_K_ref(const float *x, void *vy, int64_t k) {
             for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
             const float av_x = sqrtf(sum_x2 / 32);
             for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
-            scales[j] = make_qkx2_quants(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, -1.f, 0.1f, 20, 0);
+            if (g_mutation == OR_MUT_Q4K_CALL_UNIT_WEIGHTS)
+                for (int l = 0; l < 32; ++l) weights[l] = 1.f;
+            scales[j] = make_qkx2_quants(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux,
+                                         g_mutation == OR_MUT_Q4K_CALL_RMIN ? -0.5f : -1.f, 0.1f,
+                                         g_mutation == OR_MUT_Q4K_CALL_NSTEP0 ? 0 : 20, 0);
             if (scales[j] > max_scale) max_scale = scales[j];
             if (mins[j] > max_min) max_min = mins[j];
         }

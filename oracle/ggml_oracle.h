@@ -27,9 +27,15 @@
  *   dequantize q8_0/q4_K/q6_K/f16  pinned (independent packer round trips,
  *                                exhaustive scale/min unpacking)
  *   vec_dot_* and mul_mat        pinned (fp64 integer-exact product in numpy)
- *   quantize_row_q4_K_ref, _q6_K_ref  PARITY UNPINNED for exact bytes
- *                                (make_qkx2_quants / make_qx_quants search
- *                                order); only invariants are checked.
+ *   quantize_row_q4_K_ref        pinned: the sub-block search against its definition (its
+ *                                error equals the best candidate's, float64), idempotence on
+ *                                representable superblocks, and the whole row's bytes against a
+ *                                float64 restatement of the published wrapper (weights, search
+ *                                parameters, 6-bit codes, level recomputation): identical
+ *                                superblocks but for fp32 / float64 rounding ties (< 5 %); planted
+ *                                mistakes in the search and at its call site fail them
+ *   quantize_row_q6_K_ref        pinned: the search as an argmax over its candidates,
+ *                                idempotence on representable superblocks, planted mistakes
  */
 #ifndef GGML_ORACLE_H
 #define GGML_ORACLE_H
@@ -102,6 +108,10 @@ float or_make_qx_quants(int n, int nmax, const float *x, int8_t *L);
 #define OR_MUT_Q6K_NO_SEARCH 4 /* make_qx_quants without its +-9 search */
 #define OR_MUT_Q6K_STEP 5      /* the search steps by 0.2 instead of 0.1 */
 #define OR_MUT_Q6K_ISCALE 6    /* the 8-bit scales against 127 instead of 128 */
+/* mistakes at quantize_row_q4_K_ref's call of make_qkx2_quants (the search itself intact) */
+#define OR_MUT_Q4K_CALL_NSTEP0 7       /* nstep 0: no refits */
+#define OR_MUT_Q4K_CALL_UNIT_WEIGHTS 8 /* weights 1 instead of av_x + |x| */
+#define OR_MUT_Q4K_CALL_RMIN 9         /* rmin -0.5 instead of -1 */
 void or_set_mutation(int m);
 /* ggml_quantize_chunk(type, src, dst, 0, nrows, k, NULL): weight quantization. */
 size_t or_quantize_chunk(int type, const float *src, void *dst, int64_t nrows, int64_t k);

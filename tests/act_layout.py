@@ -71,10 +71,16 @@ def decode_q8_K_blocks(blocks, k):
 
 def expected_image(wtype, blocks, m, k):
     """The tiled workspace bytes (length planes()['total']) for the oracle's blocks of m rows
-    (GGUF layout: block_q8_0 rows for Q8_0, block_q8_K rows for Q4_K / Q6_K)."""
+    (GGUF layout: block_q8_0 rows for Q8_0, block_q8_K rows for Q4_K / Q6_K, fp16 rows for F16)."""
     p = planes(wtype, m, k)
     m_pad, kb_pad = p["m_pad"], p["kb_pad"]
     img = np.zeros(p["total"], np.uint8)
+    if wtype == O.F16:  # fp16 activations (ggml's F16 vec_dot_type): the row's fp16 bytes, tiled
+        bfull = np.zeros((m_pad, kb_pad), np.uint8)
+        bfull[:m, :2 * k] = np.ascontiguousarray(blocks).reshape(m, 2 * k)
+        o, n = p["xq"]
+        img[o:o + n][tiled_index(m_pad, kb_pad).ravel()] = bfull.ravel()
+        return img
     qfull = np.zeros((m_pad, kb_pad), np.int8)
     if wtype == O.Q8_0:
         q, d = decode_q8_0_blocks(blocks, k)

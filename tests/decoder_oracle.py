@@ -107,3 +107,74 @@ def layer_from_quants(hp, lay, wdeq, x, acts, B, T):
     gu = (acts["ffn_norm"] @ wdeq["gu"].T).astype(np.float32)
     x2 = (x1 + (acts["ffn_gate_up"] @ wdeq["down"].T).astype(np.float32)).astype(np.float32)
     return {"attn_out": a, "x1": x1, "ffn_norm": h, "ffn_gate_up": gu, "l_out": x2}
+
+
+# ---------------------------------------------------------------- fp32 pipeline ----
+# The same decoder with every step in fp32 as ggml's CPU backend runs it (rms_norm: fp32 squares
+# summed in double, fp32 scale; the rope cache's fp32 angles; fp32 attention scores, softmax and
+# P V; fp32 SiLU; mul_mat on the oracle's integer-dot product with fp32 accumulation) -- another
+# fp32 pipeline with the same requantization points, to measure how far any fp32 pipeline lands
+# from the fp64 one above.
+F32 = np.float32
+
+
+def rms_norm_f32(x, w, eps):
+    x = x.astype(F32)
+    ss = (x * x).astype(np.float64).sum(-1, keepdims=True)
+    scale = (F32(1.0) / np.sqrt((ss / x.shape[-1]).astype(F32) + F32(eps))).astype(F32)
+    return ((x * scale).astype(F32) * w.astype(F32)).astype(F32)
+
+
+def rope_cache_f32(T, d, base):
+    """cos / sin [T, d/2] of ggml's rope cache: theta_i = p * s^i by repeated fp32 products."""
+    half = d // 2
+    s = F32(base) ** F32(-2.0 / d)
+    th = np.zeros((T, half), F32)
+    th[:, 0] = np.arange(T, dtype=F32)
+    for i in range(1, half):
+        th[:, i] = (th[:, i - 1] * s).astype(F32)
+    return np.cos(th).astype(F32), np.sin(th).astype(F32)
+
+
+def attention_f32(hp, lay, q, k, v, B, T, cs):
+    nq, nkv, hd, eps = hp["n_head"], hp["n_kv_head"], hp["head_dim"], hp["rms_norm_eps"]
+    q = rms_norm_f32(q.reshape(B, T, nq, hd), lay["q_norm"], eps)
+    k = rms_norm_f32(k.reshape(B, T, nkv, hd), lay["k_norm"], eps)
+    c, s = cs[0][None, :, None, :], cs[1][None, :, None, :]
+    half = hd // 2
+
+    def rot(x):
+        a, b = x[..., :half], x[..., half:]
+        return np.concatenate([(a * c - b * s).astype(F32), (a * s + b * c).astype(F32)], -1)
+
+    q, k = rot(q).transpose(0, 2, 1, 3), rot(k).transpose(0, 2, 1, 3)
+    v = v.reshape(B, T, nkv, hd).transpose(0, 2, 1, 3).astype(F32)
+    g = nq // nkv
+    kk, vv = np.repeat(k, g, 1), np.repeat(v, g, 1)
+    sc = (np.matmul(q, np.ascontiguousarray(kk.transpose(0, 1, 3, 2))) * F32(1.0 / np.sqrt(hd))).astype(F32)
+    if hp["causal"]:
+        sc = np.where(np.tril(np.ones((T, T), bool)), sc, F32(-np.inf))
+    e = np.exp((sc - sc.max(-1, keepdims=True)).astype(F32)).astype(F32)
+    p = (e / e.sum(-1, keepdims=True, dtype=F32)).astype(F32)
+    return np.matmul(p, vv).astype(F32).transpose(0, 2, 1, 3).reshape(B * T, nq * hd)
+
+
+def encode_f32(orc, hp, wtype, W, ids, nthreads=8):
+    """encode() as an fp32 pipeline (last-token pooling): the pooled, L2-normalised rows."""
+    B, T = ids.shape
+    eps = hp["rms_norm_eps"]
+    cs = rope_cache_f32(T, hp["head_dim"], hp["rope_theta"])
+
+    def mm(x, w):
+        return orc.fast_mul_mat(wtype, w, x, nthreads=nthreads)
+
+    x = W["tok"][ids.ravel()].astype(F32)
+    for lay in W["layers"]:
+        h = rms_norm_f32(x, lay["attn_norm"], eps)
+        a = attention_f32(hp, lay, mm(h, lay["wq"]), mm(h, lay["wk"]), mm(h, lay["wv"]), B, T, cs)
+        x = (x + mm(a, lay["wo"])).astype(F32)
+        h = rms_norm_f32(x, lay["ffn_norm"], eps)
+        g, u = mm(h, lay["wgate"]), mm(h, lay["wup"])
+        x = (x + mm(((g / (F32(1) + np.exp(-g).astype(F32))).astype(F32) * u).astype(F32), lay["wdown"])).astype(F32)
+    pooled = rms_norm_f32(x.reshape(B, T, -1)[:, -1], W["out_norm"], eps).astype(np.float64)
+    return (pooled / np.linalg.norm(pooled, axis=-1, keepdims=True)).astype(F32)

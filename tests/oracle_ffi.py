@@ -17,6 +17,7 @@ ORACLE_SO = os.environ.get("MQ_ORACLE_SO") or os.path.join(ORACLE_DIR, "liboracl
 F32, F16, Q8_0, Q4_K, Q6_K, Q8_K = 0, 1, 8, 12, 14, 15
 # planted mistakes of the oracle (ggml_oracle.h OR_MUT_*)
 MUT_NONE, MUT_Q4K_NO_SEARCH, MUT_Q4K_RDELTA, MUT_Q4K_PACK, MUT_Q6K_NO_SEARCH, MUT_Q6K_STEP, MUT_Q6K_ISCALE = range(7)
+MUT_Q4K_CALL_NSTEP0, MUT_Q4K_CALL_UNIT_WEIGHTS, MUT_Q4K_CALL_RMIN = 7, 8, 9  # at quantize_row_q4_K_ref's call
 Q8_0_X86, Q8_0_NEON, Q8_0_REF = 0, 1, 2
 BLCK = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256}
 TSIZE = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q6_K: 210, Q8_K: 292}

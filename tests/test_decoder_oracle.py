@@ -29,3 +29,22 @@ def test_rms_norm_catches_mean_subtraction():
     """A LayerNorm-style mean subtraction would change a constant row; RMS norm keeps it."""
     x = np.full((1, 8), 2.0, np.float32)
     assert np.allclose(D.rms_norm(x, np.ones(8, np.float32), 0.0), 1.0)
+
+
+def test_fp32_pipeline_is_the_same_decoder(oracle):
+    """decoder_oracle.encode_f32 (the fp32, ggml-CPU-like pipeline that measures how far an fp32
+    run lands from the fp64 one) computes the same model as encode: a 2-layer decoder's pooled
+    embeddings agree at the decoder bar, and its rope cache's angles are pos * base^(-2i/d) to fp32
+    precision."""
+    from crispembed_amd import decoder
+    import oracle_ffi as O
+    hp = dict(n_layer=2, n_embd=256, n_head=4, n_kv_head=2, head_dim=128, n_ff=512, n_vocab=300, rms_norm_eps=1e-6,
+              rope_theta=1e6, causal=1, pooling=2)
+    W = decoder.synthetic_weights(hp, O.Q4_K, name="fp32pipe")
+    ids = np.random.default_rng(3).integers(0, hp["n_vocab"], (2, 40)).astype(np.int32)
+    ref, _ = D.encode(oracle, hp, O.Q4_K, W, ids)
+    got = D.encode_f32(oracle, hp, O.Q4_K, W, ids, nthreads=4)
+    assert ((got.astype(np.float64) * ref).sum(-1) >= 0.9999).all()
+    c, s = D.rope_cache_f32(40, 128, 1e6)
+    ang = np.arange(40)[:, None] * 1e6 ** (-2.0 * np.arange(64) / 128)
+    assert np.abs(c - np.cos(ang)).max() < 1e-4 and np.abs(s - np.sin(ang)).max() < 1e-4

@@ -99,6 +99,25 @@ def test_q8_0_gemm_layout(oracle, q8_0_variant, variant, m, k):
     _assert_image(got, AL.oracle_image(oracle, O.Q8_0, x, variant), O.Q8_0, rows, k)
 
 
+@pytest.mark.parametrize("m,k", [(4096, 384), (300, 1024), (37, 96), (5, 160)])
+def test_f16_gemm_layout(oracle, m, k):
+    """k_quantize_tiled<F16> (the F16 weights' activation, ggml's F16 vec_dot_type: fp32 -> fp16
+    round to nearest even): every byte against the oracle's fp16 rows, with rows of exact fp16
+    rounding ties (1 + (2j + 1) 2^-11, halfway between fp16 neighbours, both directions of the
+    even rule), fp16 subnormals, values that overflow to inf, and -0."""
+    x = _rows(m, k, 3000 + k)
+    ties = np.zeros((4, k), np.float32)
+    j = np.arange(k) % 64
+    ties[0] = 1.0 + (2 * j + 1) * 2.0 ** -11
+    ties[1] = -(1.0 + (2 * j + 1) * 2.0 ** -11)
+    ties[2] = (j + 0.5) * 2.0 ** -24  # subnormal ties
+    ties[3, ::2], ties[3, 1::2] = 70000.0, -0.0
+    x = np.concatenate([x, ties])
+    rows = x.shape[0]
+    got = _gemm_ws(O.F16, dev(x), rows, k)
+    _assert_image(got, AL.oracle_image(oracle, O.F16, x), O.F16, rows, k)
+
+
 @pytest.mark.parametrize("m,k", [(8192, 1024), (8192, 4096), (8192, 3072), (300, 512), (37, 2048)])
 def test_q8_K_gemm_layout(oracle, m, k):
     """k_quantize_tiled<Q8_K>: the cfg2a / cfg2b activations X [8192 x 1024] and [8192 x 4096],

@@ -12,8 +12,12 @@ algorithm fixes rather than from a second copy of it:
   15 (Q4_K; scale and min at 63 somewhere in the superblock) or holds a level -32 at its largest
   magnitude (Q6_K; one sub-block scale at -128) dequantizes to values the quantizer must map
   back to the same bytes;
+* the whole Q4_K row (quantize_row_q4_K_ref's call site included: the weights av_x + |x|, rmin -1,
+  rdelta 0.1, nstep 20, the 6-bit codes and the recomputed levels) against its definition
+  restated in float64 over that search: byte-identical superblocks but for rounding ties;
 * planted mistakes (the oracle's or_set_mutation, CPU only): no search, a wrong search step,
-  swapped packing bits, a wrong scale divisor -- each makes at least one pin above fail.
+  swapped packing bits, a wrong scale divisor, and at the wrapper's call of the search nstep 0,
+  unit weights, rmin -0.5 -- each makes at least one pin above fail.
 """
 import numpy as np
 import pytest
@@ -30,22 +34,25 @@ def _rint(v):
 
 
 # ------------------------------------------------------------------ Q4_K ----
-def qkx2_search(x, w, nmax=15, rmin=-1.0, rdelta=0.1, nstep=20):
+def qkx2_search_full(x, w, nmax=15, rmin=-1.0, rdelta=0.1, nstep=20):
     """make_qkx2_quants as its definition reads, in float64 for the least-squares refits and the
     errors (levels rounded in fp32): start from the levels of the full range [min(x, 0), max],
     then for i = 0..nstep refit (scale, min) by weighted least squares to the levels at inverse
     scale (rmin + rdelta i + nmax) / (max - min) -- min being the best refit's so far -- clamp a
-    positive min to 0, keep the refit whenever its error is lower.  Returns the best error."""
+    positive min to 0, keep the refit whenever its error is lower.  Returns the best error and
+    its (scale, min, levels)."""
     x = x.astype(F32)
     mn, mx = min(F32(x.min()), F32(0)), F32(x.max())
     w64, x64 = w.astype(np.float64), x.astype(np.float64)
     iscale = F32(nmax) / (mx - mn)
     L = np.clip(_rint(iscale * (x - mn)), 0, nmax)
-    best = float((w64 * ((1.0 / float(iscale)) * L + float(mn) - x64) ** 2).sum())
+    best_scale, best_min, best_L = 1.0 / float(iscale), float(mn), L.copy()
+    best = float((w64 * (best_scale * L + float(mn) - x64) ** 2).sum())
     cur_min = float(mn)
     for i in range(nstep + 1):
         iscale = (F32(rmin) + F32(rdelta) * F32(i) + F32(nmax)) / (mx - F32(cur_min))
-        L = np.clip(_rint(F32(iscale) * (x - F32(cur_min))), 0, nmax).astype(np.float64)
+        Li = np.clip(_rint(F32(iscale) * (x - F32(cur_min))), 0, nmax)
+        L = Li.astype(np.float64)
         sw, sl, sl2, sxl, sx = w64.sum(), (w64 * L).sum(), (w64 * L * L).sum(), (w64 * L * x64).sum(), (w64 * x64).sum()
         D = sw * sl2 - sl * sl
         if D <= 0:
@@ -56,7 +63,71 @@ def qkx2_search(x, w, nmax=15, rmin=-1.0, rdelta=0.1, nstep=20):
         err = float((w64 * (scale * L + minv - x64) ** 2).sum())
         if err < best:
             best, cur_min = err, minv
-    return best
+            best_scale, best_min, best_L = scale, minv, Li.copy()
+    return best, best_scale, best_min, best_L
+
+
+def qkx2_search(x, w, **kw):
+    return qkx2_search_full(x, w, **kw)[0]
+
+
+def q4_K_row_from_definition(xs):
+    """quantize_row_q4_K_ref as ggml publishes it, restated in float64 on top of the search
+    above: per 32-value sub-block the weights av_x + |x| (av_x the rms of the sub-block) and
+    make_qkx2_quants(32, 15, ..., rmin -1, rdelta 0.1, nstep 20); the sub-block scales and mins
+    (minus the search's min) as 6-bit codes nearest_int(63 / max * v) clamped to 63, d and dmin =
+    fp16(max / 63); then each level recomputed from the codes, nearest_int((x + dmin m) / (d sc))
+    clamped to [0, 15] (a sub-block whose scale code is 0 keeps the search's levels); nibbles
+    packed low half / high half of each 64 values.  xs [nsb, 256] -> the [nsb, 144] blocks."""
+    nsb = xs.shape[0]
+    out = np.zeros((nsb, 144), np.uint8)
+    for b in range(nsb):
+        x = xs[b].astype(F32)
+        scales, mins, L = np.zeros(8), np.zeros(8), np.zeros(256, np.int64)
+        for j in range(8):
+            xj = x[32 * j:32 * j + 32]
+            s2 = F32(0)
+            for v in xj:  # the definition's fp32 running sum
+                s2 = F32(s2 + v * v)
+            w = (np.sqrt(s2 / F32(32)).astype(F32) + np.abs(xj)).astype(F32)
+            _, scales[j], mn, L[32 * j:32 * j + 32] = qkx2_search_full(xj, w)
+            mins[j] = -mn
+        ms, mm = scales.max(), mins.max()
+        sc = np.minimum(_rint(np.float64(63.0 / ms if ms > 0 else 0.0) * scales), 63)
+        mn_ = np.minimum(_rint(np.float64(63.0 / mm if mm > 0 else 0.0) * mins), 63)
+        d, dmin = np.float16(ms / 63.0), np.float16(mm / 63.0)
+        for j in range(8):
+            d1 = F32(d) * F32(sc[j])
+            if d1 == 0:
+                continue
+            dm = F32(dmin) * F32(mn_[j])
+            L[32 * j:32 * j + 32] = np.clip(_rint((x[32 * j:32 * j + 32] + dm) / d1), 0, 15)
+        out[b, 0:2] = np.frombuffer(d.tobytes(), np.uint8)
+        out[b, 2:4] = np.frombuffer(dmin.tobytes(), np.uint8)
+        out[b, 4:16] = pack_q4_K_scales(sc, mn_)
+        q = L.reshape(4, 2, 32)
+        out[b, 16:] = (q[:, 0] | (q[:, 1] << 4)).reshape(128).astype(np.uint8)
+    return out
+
+
+def q4_wrapper_mismatch(oracle, seed=5, nsb=160):
+    """Fraction of superblocks whose oracle bytes differ from the restatement from the definition
+    (random N(0, 0.02) rows, a quarter of them shifted positive so mins clamp to 0)."""
+    rng = np.random.default_rng(seed)
+    xs = (rng.standard_normal((nsb, 256)) * 0.02).astype(F32)
+    xs[: nsb // 4] += F32(0.015)
+    got = oracle.quantize_chunk(O.Q4_K, xs.reshape(1, -1)).reshape(nsb, 144)
+    return float((got != q4_K_row_from_definition(xs)).any(-1).mean())
+
+
+def test_q4_K_row_bytes_from_the_definition(oracle):
+    """The whole wrapper -- weights, search parameters, 6-bit codes, level recomputation, packing
+    -- against its definition restated with float64 refits: the bytes agree except where fp32 and
+    float64 rounding fall on different sides of a tie (a 6-bit code's .5, or two refits at nearly
+    equal error: then d moves and the superblock's levels with it).  Measured: 3 of 160 superblocks
+    (1.9 %), each such a tie; the planted call-site mistakes (nstep 0, unit weights, rmin -0.5) and
+    the search mistakes change 76-100 % of them, so the bar sits at 5 %."""
+    assert q4_wrapper_mismatch(oracle) <= 0.05
 
 
 def _q4_subblocks(seed, n=400):
@@ -187,6 +258,7 @@ def test_q6_K_idempotent_on_representable_blocks(oracle):
 # ------------------------------------------------------- planted mistakes ----
 PINS = {
     "q4_search": lambda o: q4_search_gap(o) <= 1e-4,
+    "q4_wrapper": lambda o: q4_wrapper_mismatch(o) <= 0.05,
     "q4_roundtrip": lambda o: q4_roundtrip_mismatch(o) == 0,
     "q6_search": lambda o: q6_search_gap(o) <= 1e-6,
     "q6_roundtrip": lambda o: q6_roundtrip_mismatch(o) == 0,
@@ -195,6 +267,8 @@ PINS = {
 
 @pytest.mark.parametrize("mutation,caught_by", [
     (O.MUT_Q4K_NO_SEARCH, "q4_search"), (O.MUT_Q4K_RDELTA, "q4_search"), (O.MUT_Q4K_PACK, "q4_roundtrip"),
+    (O.MUT_Q4K_CALL_NSTEP0, "q4_wrapper"), (O.MUT_Q4K_CALL_UNIT_WEIGHTS, "q4_wrapper"),
+    (O.MUT_Q4K_CALL_RMIN, "q4_wrapper"),
     (O.MUT_Q6K_NO_SEARCH, "q6_search"), (O.MUT_Q6K_STEP, "q6_search"), (O.MUT_Q6K_ISCALE, "q6_roundtrip")])
 def test_planted_mistake_is_caught(oracle, mutation, caught_by):
     oracle.set_mutation(mutation)
