@@ -132,6 +132,20 @@ extern "C" {
 
 const char *mq_last_error(void) { return g_err.c_str(); }
 
+int mq_release_workspace(void *stream) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    auto it = g_ws.find({dev, stream});
+    if (it == g_ws.end()) return MQ_OK;
+    e = hipStreamSynchronize((hipStream_t)stream);  // work queued on the stream may still read it
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    if (it->second.ptr) (void)hipFree(it->second.ptr);
+    g_ws.erase(it);
+    return MQ_OK;
+}
+
 int mq_init(void) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);

@@ -13,6 +13,7 @@
 //               normalised with sqrtf(max(sum x^2, 1e-12)) (src/decoder_embed.cpp:1044-1100)
 // Arithmetic is fp32 throughout; the attention's products run on fp16 MFMAs over split
 // (hi + lo) operands, which keeps fp32 accuracy.
+#include <atomic>
 #include <cstdlib>
 
 #include "mq_internal.h"
@@ -954,19 +955,17 @@ hipError_t launch_rope_table(float2 *cs, int T, int hd, float theta_base, hipStr
 }
 
 // The unmasked 8-wave kernel with its dynamic LDS: at head_dim 128 the two-slot key/value ring
-// (two heads' fragments per slot), or the Q8_K store's staging where that is larger.
+// (two heads' fragments per slot), or the Q8_K store's staging where that is larger (the limit
+// raised once per device).
 template <int HD, int QO>
-static void launch_attn_8w(dim3 grid, const AttnArgs &a, int nblk, float qscale, hipStream_t s) {
+static hipError_t launch_attn_8w(dim3 grid, const AttnArgs &a, int nblk, float qscale, hipStream_t s) {
     constexpr int RING = HD == 128 ? 2 * 2 * kv_frags<HD>() * 1024 : 0, STG = QO == AQ_Q8_K ? 4 * 32 * 260 * 4 : 0;
     constexpr int BYTES = RING > STG ? RING : STG;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute((const void *)k_attn_frag<HD, false, QO>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                BYTES) != hipSuccess)
-            return;  // the launch below reports the error
-        attr_set = true;
-    }
+    static std::atomic<bool> attr_set[MQ_MAX_DEVICES];
+    const hipError_t e = dyn_lds_once((const void *)k_attn_frag<HD, false, QO>, BYTES, attr_set);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((k_attn_frag<HD, false, QO>), grid, dim3(512), BYTES, s, a, nblk, qscale);
+    return hipGetLastError();
 }
 
 // The split-key form when the regular grid (2 heads x 128 queries per workgroup) would leave
@@ -992,7 +991,7 @@ static void launch_attn_split(dim3 g, const AttnArgs &a, int nblk, float qscale,
 }
 
 template <int HD>
-static void launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_t s) {
+static hipError_t launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_t s) {
     const dim3 gk((unsigned)nblk, (unsigned)a.nkv, (unsigned)a.B);
     if (!a.kv_ready) hipLaunchKernelGGL((k_kv_frag<HD>), gk, dim3(256), 0, s, a, nblk);
     if (attn_split_form(a)) {
@@ -1004,23 +1003,22 @@ static void launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipStream_
             if (*e) nw = atoi(e) == 4 ? 4 : 8;
         if (nw == 8) launch_attn_split<HD, 8>(g, a, nblk, qscale, s);
         else launch_attn_split<HD, 4>(g, a, nblk, qscale, s);
-        return;
+        return hipGetLastError();
     }
     const dim3 ga((unsigned)((a.nq + 1) / 2), (unsigned)a.B, (unsigned)((a.Tq + 127) / 128));
     if constexpr (HD <= 64) {
         if (a.qo) {  // quantized output: the unmasked / masked forms with the Q8_0 store
-            if (a.mask) hipLaunchKernelGGL((k_attn_frag<HD, true, AQ_Q8_0>), ga, dim3(512), 0, s, a, nblk, qscale);
-            else launch_attn_8w<HD, AQ_Q8_0>(ga, a, nblk, qscale, s);
-            return;
+            if (!a.mask) return launch_attn_8w<HD, AQ_Q8_0>(ga, a, nblk, qscale, s);
+            hipLaunchKernelGGL((k_attn_frag<HD, true, AQ_Q8_0>), ga, dim3(512), 0, s, a, nblk, qscale);
+            return hipGetLastError();
         }
     } else {
-        if (a.qo) {  // the Q8_K store (attn_frag_form: no mask, even nq, Tq a multiple of 128)
-            launch_attn_8w<HD, AQ_Q8_K>(ga, a, nblk, qscale, s);
-            return;
-        }
+        if (a.qo)  // the Q8_K store (attn_frag_form: no mask, even nq, Tq a multiple of 128)
+            return launch_attn_8w<HD, AQ_Q8_K>(ga, a, nblk, qscale, s);
     }
-    if (a.mask) hipLaunchKernelGGL((k_attn_frag<HD, true>), ga, dim3(512), 0, s, a, nblk, qscale);
-    else launch_attn_8w<HD, AQ_NONE>(ga, a, nblk, qscale, s);
+    if (!a.mask) return launch_attn_8w<HD, AQ_NONE>(ga, a, nblk, qscale, s);
+    hipLaunchKernelGGL((k_attn_frag<HD, true>), ga, dim3(512), 0, s, a, nblk, qscale);
+    return hipGetLastError();
 }
 
 // true when launch_attn_hd takes the 8-wave fragment kernel with a store of the output
@@ -1128,15 +1126,15 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
             quant_after = true;  // the split-key form stores floats only
         }
     }
+    hipError_t e;
     switch (b.hd) {
-        case 128: launch_attn_hd<128>(b, nblk, qscale, s); break;
-        case 64: launch_attn_hd<64>(b, nblk, qscale, s); break;
-        case 32: launch_attn_hd<32>(b, nblk, qscale, s); break;
+        case 128: e = launch_attn_hd<128>(b, nblk, qscale, s); break;
+        case 64: e = launch_attn_hd<64>(b, nblk, qscale, s); break;
+        case 32: e = launch_attn_hd<32>(b, nblk, qscale, s); break;
         default: return hipErrorInvalidValue;
     }
+    if (e != hipSuccess) return e;
     if (quant_after) {
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
         const int64_t rows = (int64_t)a.B * a.Tq, K = (int64_t)a.nq * a.hd;
         return launch_quantize_act_planar(a.q_type, a.out, K, a.q_ws, rows, K, a.q_var, true, s);
     }

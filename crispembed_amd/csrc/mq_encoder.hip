@@ -307,13 +307,9 @@ hipError_t launch_bias_res_ln(const float *y, const float *bias, const float *re
 template <int HD, int KS>
 static hipError_t attention_cfg(const float *qkv, const float *bqkv, float *out, int B, int T, int H, int nh,
                                 hipStream_t s) {
-    static bool attr = false;
-    if (!attr) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_attention<HD, KS>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    static std::atomic<bool> attr_set[MQ_MAX_DEVICES];
+    const hipError_t e = dyn_lds_once((const void *)k_attention<HD, KS>, 160 * 1024, attr_set);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((k_attention<HD, KS>), dim3((unsigned)(B * nh)), dim3(T * KS), attention_lds_bytes(T, HD, KS), s,
                        qkv, bqkv, out, T, H, nh, 1.0f / sqrtf((float)HD));
     return hipGetLastError();

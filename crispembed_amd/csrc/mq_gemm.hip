@@ -725,13 +725,9 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
 template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2, bool GLU = false, int NBT = 4, int DT = 3>
 static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
     using C = Cfg<FMT, WM, WN, TM, TN, KCT, NBT, DT>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm<FMT, WM, WN, TM, TN, MINB, KCT, GLU, NBT, DT>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    static std::atomic<bool> attr_set[MQ_MAX_DEVICES];
+    const hipError_t e = dyn_lds_once((const void *)k_gemm<FMT, WM, WN, TM, TN, MINB, KCT, GLU, NBT, DT>, C::LDS, attr_set);
+    if (e != hipSuccess) return e;
     a.tiles_m = (a.M + C::BM - 1) / C::BM;
     a.tiles_n = (a.N + C::BN - 1) / C::BN;
     for (int g = 1; g < GEMM_GROUPS; g++) {

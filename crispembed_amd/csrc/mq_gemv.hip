@@ -550,12 +550,14 @@ static hipError_t launch_kq_stream_groups(const GvGroups &G, const int8_t *xq, c
     const int64_t ntiles = G.tend;
     const int nsb = (int)(k / QK_K);
     const int sbw = (nsb + 7) / 8;
-    static int ncu = 0;
+    static std::atomic<int> ncu_cache{0};  // the CU count (the same on every MI355X)
+    int ncu = ncu_cache.load(std::memory_order_relaxed);
     if (!ncu) {
         int dev = 0, v = 0;
         if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
             v = 256;
         ncu = v;
+        ncu_cache.store(v, std::memory_order_relaxed);
     }
     // workgroups per CU (at most what fits: two at one cached superblock per wave, one
     // beyond, register-bound); MQ_GEMV_WGS overrides for measurements

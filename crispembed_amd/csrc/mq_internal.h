@@ -7,6 +7,7 @@
 //   block_q8_K {float d; i8 qs[256]; i16 bsums[16]}                   292 B / 256
 #pragma once
 
+#include <atomic>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -14,6 +15,20 @@
 #include "../../include/mq.h"
 
 namespace mq {
+
+// Raises kernel fn's dynamic-LDS limit to `bytes` once per device: flags[dev] is set after a
+// successful hipFuncSetAttribute (threads that race on it both set the same value).
+constexpr int MQ_MAX_DEVICES = 64;
+inline hipError_t dyn_lds_once(const void *fn, int bytes, std::atomic<bool> *flags) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= MQ_MAX_DEVICES) return hipErrorInvalidDevice;
+    if (flags[dev].load(std::memory_order_acquire)) return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess) flags[dev].store(true, std::memory_order_release);
+    return e;
+}
 
 constexpr int QK8_0 = 32;
 constexpr int QK_K = 256;

@@ -58,6 +58,7 @@ _SIGS = {
     "mq_weight_image_bytes": (_c_sz, [_c_int, _c_i64, _c_i64]),
     "mq_weight_prepare": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "mq_workspace_bytes": (_c_sz, [_c_int, _c_i64, _c_i64]),
+    "mq_release_workspace": (_c_int, [_c_vp]),
     "mq_mul_mat": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                             _c_sz, _c_vp]),
     "mq_quantize_act": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_sz, _c_int, _c_vp]),

@@ -130,13 +130,21 @@ int mq_weight_prepare(int type, void *image, int64_t n, int64_t k, int64_t row0,
  * activations; size it with mq_workspace_bytes().  workspace == NULL makes the
  * library use (and grow with hipMalloc) an internal buffer per (device, stream), so
  * calls on different streams never share one; calls on one stream from several threads
- * must be serialised by the caller (as ggml backends are, src/core/gpu_backend_pref.h:180-185). */
+ * must be serialised by the caller (as ggml backends are, src/core/gpu_backend_pref.h:180-185).
+ * Growing that buffer synchronizes the stream and calls hipMalloc, which HIP graph capture does
+ * not allow: under capture pass a workspace, or make an equally large call on the stream before
+ * capturing.  Each stream's buffer lives until mq_release_workspace(stream) or the process ends;
+ * a caller that creates short-lived streams releases it before destroying the stream. */
 /* The path MQ_PATH_AUTO of mq_mul_mat / mq_mul_mat_ex takes for an n x k weight and m rows:
  * MQ_PATH_GEMV up to mq_gemv_max_m() rows, and up to 32 rows while a 128 x 128 GEMM tile grid
  * would have fewer than 64 workgroups (short inputs on narrow layers); else MQ_PATH_GEMM.
  * Callers of the two-step API (mq_quantize_act_ex + mq_mul_mat_q*) pass it to both calls. */
 int mq_mul_mat_path(int type, int64_t n, int64_t k, int64_t m);
 size_t mq_workspace_bytes(int type, int64_t m, int64_t k);
+/* Frees the internal workspace of `stream` on the current device (after synchronizing the
+ * stream), if it has one.  No counterpart in the reference (ggml frees a backend's buffers with
+ * the backend); for callers that create and destroy streams. */
+int mq_release_workspace(void *stream);
 int mq_mul_mat(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m, float *y,
                int64_t ldy, void *workspace, size_t workspace_bytes, void *stream);
 int mq_mul_mat_ex(int type, const void *w_image, int64_t n, int64_t k, const float *x, int64_t ldx, int64_t m,
@@ -192,7 +200,9 @@ int mq_mul_mat_q_group(int type, int n_groups, const void *const *w_images, cons
  * without a caller workspace: every workgroup quantizes the activation it reads, while that is a
  * few superblock-rows (m * k / 256, three times that with SiLU, at most 100); larger ones are
  * quantized once into the library's internal workspace of this stream (as mq_mul_mat_ex with a
- * NULL workspace) and read by the same GEMV.  op MQ_PRE_NONE, or
+ * NULL workspace) and read by the same GEMV -- whose first such call on a stream may synchronize
+ * it and hipMalloc, so under HIP graph capture make one equally large call on the stream before
+ * capturing.  op MQ_PRE_NONE, or
  * MQ_PRE_SILU_MUL with x2 the up-projection rows (row stride ldx2): the value quantized is then
  * silu(x) * x2, the SwiGLU input of the down projection.  These are the MUL_MATs of the decode
  * step, one to eight new tokens: q/k/v (src/qwen2vl_ocr.cpp:2368-2372), o (:2430), gate/up and

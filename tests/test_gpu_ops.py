@@ -346,9 +346,13 @@ def attn_form(request, monkeypatch):
 
 
 @pytest.mark.parametrize("hd,nh,nkv,B,T", [(32, 12, 12, 3, 77), (64, 12, 12, 2, 128), (128, 8, 2, 2, 45),
-                                           (32, 4, 4, 1, 300), (128, 16, 8, 1, 200)])
+                                           (32, 4, 4, 1, 300), (128, 16, 8, 1, 200), (128, 5, 5, 1, 200),
+                                           (128, 3, 1, 2, 64)])
 def test_flash_attn_permuted_views(attn_form, hd, nh, nkv, B, T):
-    """q/k/v as ggml_permute(reshape(x, hd, nh, T, B), 0, 2, 1, 3) of contiguous projections."""
+    """q/k/v as ggml_permute(reshape(x, hd, nh, T, B), 0, 2, 1, 3) of contiguous projections.  Odd
+    head counts at head_dim 128: the 8-wave kernel's key/value ring then has workgroups whose
+    second head does not exist (its waves stay in the loop for the barriers and compute nothing),
+    and grouped heads (3 query heads on one key/value head) straddle workgroups."""
     rng = _rng(hd + T)
     qx = rng.standard_normal((B, T, nh, hd)).astype(np.float32)
     kx = rng.standard_normal((B, T, nkv, hd)).astype(np.float32)
@@ -626,7 +630,8 @@ def test_rope_cache_matches_rope(case):
 
 
 @pytest.mark.parametrize("hd,nh,nkv,B,T,masked", [(128, 4, 2, 1, 300, True), (128, 8, 4, 2, 64, False),
-                                                  (64, 4, 4, 2, 100, True), (32, 6, 2, 1, 77, False)])
+                                                  (64, 4, 4, 2, 100, True), (32, 6, 2, 1, 77, False),
+                                                  (128, 5, 5, 1, 200, False), (128, 3, 1, 2, 64, False)])
 def test_flash_attn_qk_norm_rope(attn_form, hd, nh, nkv, B, T, masked):
     """mq_op_flash_attn_qk_norm_rope (q and k normed and rotated as the attention reads them)
     against mq_op_norm + mq_op_rope of q and k followed by mq_op_flash_attn: equal up to the RMS
