@@ -111,6 +111,14 @@ struct BackendCtx {
     size_t mb_bytes = 0;
     const ggml_tensor *mb_mask = nullptr;
     std::vector<int64_t> mb_key;
+    // the segment structure (mq_op_mask_segments) of mask sg_mask with the shapes sg_key in the
+    // graph being computed: sg_len (0: none, the lists or the mask itself serve), found once
+    // per graph, in sg_buf (sg_bytes of device scratch)
+    void *sg_buf = nullptr;
+    size_t sg_bytes = 0;
+    const ggml_tensor *sg_mask = nullptr;
+    std::vector<int64_t> sg_key;
+    int64_t sg_len = 0;
     // ggml_backend_mi355_set_act_observer
     ggml_backend_mi355_act_observer act_cb = nullptr;
     void *act_user = nullptr;
@@ -350,6 +358,7 @@ void be_free(ggml_backend_t be) {
         if (c->ws) (void)hipFree(c->ws);
         if (c->cs) (void)hipFree(c->cs);
         if (c->mb) (void)hipFree(c->mb);
+        if (c->sg_buf) (void)hipFree(c->sg_buf);
         (void)hipStreamDestroy(c->stream);
     }
     delete c;
@@ -715,22 +724,58 @@ const void *mask_blocks(BackendCtx *c, const ggml_tensor *mt, const mq_view &q, 
     return c->mb;
 }
 
+// The segment length of mask mt (view m) for the attention of q and k when the mask is exactly
+// block-diagonal causal over segments of a multiple of 32 positions (a batched decoder's mask,
+// decoder_encode_tokens_batch): found once per graph (a pass over the mask and a readback, which
+// synchronizes the stream) and reused while the mask's bytes and the shapes stay; 0 otherwise,
+// under capture, for masks the attention would not give block lists (small ones), or with
+// MQ_GGML_NO_MASK_SEGMENTS=1.
+int64_t mask_segments(BackendCtx *c, const ggml_tensor *mt, const mq_view &q, const mq_view &k, const mq_view &m) {
+    if (std::getenv("MQ_GGML_NO_MASK_SEGMENTS") || c->capturing || q.ne[1] < 256) return 0;
+    const size_t need = mq_op_mask_segments_bytes(&q, &k, &m);
+    if (need == 0 || mq_op_mask_blocks_bytes(&q, &k, &m) == 0) return 0;
+    std::vector<int64_t> key = {(int64_t)(uintptr_t)mt->data, q.ne[1], k.ne[1]};
+    key.insert(key.end(), mt->ne, mt->ne + 4);
+    key.insert(key.end(), mt->nb, mt->nb + 4);
+    if (c->sg_mask == mt && key == c->sg_key) return c->sg_len;
+    c->sg_mask = nullptr;
+    if (need > c->sg_bytes) {
+        hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        if (c->sg_buf) (void)hipFree(c->sg_buf);
+        c->sg_buf = nullptr, c->sg_bytes = 0;
+        if (hipMalloc(&c->sg_buf, need) != hipSuccess) {
+            (void)hipGetLastError();
+            c->sg_buf = nullptr;
+            return 0;
+        }
+        c->sg_bytes = need;
+    }
+    int64_t S = 0;
+    if (mq_op_mask_segments(&q, &k, &m, c->sg_buf, c->sg_bytes, &S, c->stream) != 0 || S % 32 != 0) S = 0;
+    c->sg_mask = mt, c->sg_key = key, c->sg_len = S;
+    return S;
+}
+
 // The attention of FLASH_ATTN_EXT node fa: with q and k before their norm and rotation when those
-// chains were left to it (c->qk_fa), else on its operands; with the mask's block lists where the
-// attention takes them.
+// chains were left to it (c->qk_fa), else on its operands; per causal segment when the mask is a
+// batched decoder's, else with the mask's block lists where the attention takes them; with its
+// rows also quantized into act (act_bytes) for a projection on act_type weights when act is given.
 int attn_call(BackendCtx *c, const ggml_tensor *fa, void *ws, size_t ws_bytes, void *act, size_t act_bytes,
-              int flags) {
+              int act_type, int flags) {
     const mq_view v = view_of(fa->src[2]), d = view_of(fa);
     mq_view m{};
     if (fa->src[3]) m = view_of(fa->src[3]);
     const bool qk = c->qk_fa == fa;
     c->qk_fa = nullptr;
     const mq_view q = qk ? c->qk_q : view_of(fa->src[0]), k = qk ? c->qk_k : view_of(fa->src[1]);
-    const void *blocks = fa->src[3] ? mask_blocks(c, fa->src[3], q, k, m) : nullptr;
+    int64_t seg = 0;
+    const void *blocks = nullptr;
+    if (fa->src[3] && !(flags & MQ_ATTN_KV_READY)) seg = mask_segments(c, fa->src[3], q, k, m);
+    if (fa->src[3] && seg == 0) blocks = mask_blocks(c, fa->src[3], q, k, m);
     return mq_op_flash_attn_blocks(&q, &k, &v, fa->src[3] ? &m : nullptr, &d, op_param_f32(fa, 0),
                                    qk ? c->qk_qw : nullptr, qk ? c->qk_kw : nullptr, qk ? c->qk_eps : 0.f,
-                                   qk ? c->cs : nullptr, blocks, ws, ws_bytes, act, act_bytes, qk ? 0 : flags,
-                                   c->stream);
+                                   qk ? c->cs : nullptr, blocks, seg, ws, ws_bytes, act, act_bytes, act_type,
+                                   qk ? 0 : flags, c->stream);
 }
 
 // [ADD(x, r) ->] NORM|RMS_NORM -> MUL(w) [-> ADD(b)] starting at node i: returns the number of
@@ -998,26 +1043,29 @@ int try_fuse_silu_mul(BackendCtx *c, ggml_cgraph *cg, int i, int n, const std::v
 }
 
 // FLASH_ATTN_EXT whose result (after view nodes, as rows of n_head * head_dim) is read by a
-// Q8_0 MUL_MAT on the GEMM path (the output projection): the attention also leaves it quantized
-// for that MUL_MAT (mq_op_flash_attn_q8_0) and the activation cache lets the MUL_MAT skip the
-// quantizer.  The quantized rows sit at the workspace start, the K/V fragments after them.
+// Q8_0, Q4_K or Q6_K MUL_MAT on the GEMM path (the output projection): the attention also leaves
+// it quantized for that MUL_MAT (Q8_0, or Q8_K for the K-quants: by the attention kernel's own
+// store where its form has one, else by the quantizer right after it) and the activation cache
+// lets the MUL_MAT skip the quantizer.  The quantized rows sit at the workspace start, the K/V
+// fragments after them.
 int try_fuse_attn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status &st) {
     ggml_tensor *node = ggml_graph_node(cg, i);
     int nx = i + 1;
     while (nx < n && (ggml_is_empty(ggml_graph_node(cg, nx)) || is_view_op(ggml_graph_node(cg, nx)->op))) nx++;
     if (nx >= n) return 0;
     const ggml_tensor *mm = ggml_graph_node(cg, nx);
-    if (mm->op != GGML_OP_MUL_MAT || mm->src[0]->type != GGML_TYPE_Q8_0 || !flat_mul_mat(mm)) return 0;
+    const int mt = mm->op == GGML_OP_MUL_MAT ? mq_type_of(mm->src[0]->type) : -1;
+    if ((mt != MQ_TYPE_Q8_0 && mt != MQ_TYPE_Q4_K && mt != MQ_TYPE_Q6_K) || !flat_mul_mat(mm)) return 0;
     const ggml_tensor *x = mm->src[1];
     if (x != node && (x->view_src != node || x->view_offs != 0)) return 0;
     const int64_t K = x->ne[0], M = x->ne[1] * x->ne[2] * x->ne[3];
-    if (K != node->ne[0] * node->ne[1] || M != node->ne[2] * node->ne[3] || K % 128 != 0 ||
+    if (K != node->ne[0] * node->ne[1] || M != node->ne[2] * node->ne[3] || K % (mt == MQ_TYPE_Q8_0 ? 128 : 256) != 0 ||
         x->nb[1] != (size_t)K * sizeof(float) || node->nb[1] != (size_t)node->ne[0] * sizeof(float) ||
         node->nb[2] != (size_t)K * sizeof(float) || node->nb[3] != node->nb[2] * (size_t)node->ne[2])
         return 0;
-    if (mq_mul_mat_path(MQ_TYPE_Q8_0, mm->src[0]->ne[1], K, M) != MQ_PATH_GEMM) return 0;
+    if (mq_mul_mat_path(mt, mm->src[0]->ne[1], K, M) != MQ_PATH_GEMM) return 0;
     const mq_view k = view_of(node->src[1]);
-    const size_t act = (mq_workspace_bytes(MQ_TYPE_Q8_0, M, K) + 255) & ~(size_t)255;
+    const size_t act = (mq_workspace_bytes(mt, M, K) + 255) & ~(size_t)255;
     const bool ready = c->kv_ready_for == node;  // K/V fragments stored by the q/k/v GEMM
     const size_t foff = ready ? c->kv_frag_off : act;
     c->kv_ready_for = nullptr;
@@ -1026,9 +1074,9 @@ int try_fuse_attn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status
         st = GGML_STATUS_ALLOC_FAILED;
         return 1;
     }
-    const int rc = attn_call(c, node, (char *)c->ws + foff, c->ws_bytes - foff, c->ws, act,
+    const int rc = attn_call(c, node, (char *)c->ws + foff, c->ws_bytes - foff, c->ws, act, mt,
                              ready ? MQ_ATTN_KV_READY : 0);
-    if (rc == 0) c->ws_x = x, c->ws_type = MQ_TYPE_Q8_0, c->ws_m = M, c->ws_k = K, c->ws_path = MQ_PATH_GEMM;
+    if (rc == 0) c->ws_x = x, c->ws_type = mt, c->ws_m = M, c->ws_k = K, c->ws_path = MQ_PATH_GEMM;
     st = op_status(rc, node);
     return 1;
 }
@@ -1285,7 +1333,7 @@ enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node) {
             c->kv_ready_for = nullptr;
             c->ws_x = nullptr;
             if (!ensure_ws(c, foff + mq_op_flash_attn_workspace_bytes(&k))) return GGML_STATUS_ALLOC_FAILED;
-            return op_status(attn_call(c, node, (char *)c->ws + foff, c->ws_bytes - foff, nullptr, 0,
+            return op_status(attn_call(c, node, (char *)c->ws + foff, c->ws_bytes - foff, nullptr, 0, MQ_TYPE_Q8_0,
                                        ready ? MQ_ATTN_KV_READY : 0),
                              node);
         }
@@ -1303,13 +1351,16 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
     c->kv_ready_for = nullptr;
     c->qk_fa = nullptr;
     c->cs_key.clear();  // and the positions
-    c->mb_mask = nullptr;  // and the masks
+    c->mb_mask = c->sg_mask = nullptr;  // and the masks
     std::vector<char> done(n, 0);  // nodes already computed as part of an earlier group
     for (int i = 0; i < n; i++) {
         ggml_tensor *node = ggml_graph_node(cg, i);
         if (done[i] || ggml_is_empty(node) || is_view_op(node->op)) {
             // a product computed ahead with an earlier group wrote its bytes then
-            if (done[i] && c->mb_mask && !is_view_op(node->op) && overlaps(node, c->mb_mask)) c->mb_mask = nullptr;
+            if (done[i] && !is_view_op(node->op)) {
+                if (c->mb_mask && overlaps(node, c->mb_mask)) c->mb_mask = nullptr;
+                if (c->sg_mask && overlaps(node, c->sg_mask)) c->sg_mask = nullptr;
+            }
             continue;
         }
         enum ggml_status st = GGML_STATUS_SUCCESS;
@@ -1354,14 +1405,12 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
                     break;
                 }
             }
-        if (c->mb_mask)
-            for (int j = i; j < i + used; j++) {
-                const ggml_tensor *t = ggml_graph_node(cg, j);
-                if (!is_view_op(t->op) && overlaps(t, c->mb_mask)) {
-                    c->mb_mask = nullptr;
-                    break;
-                }
-            }
+        for (int j = i; j < i + used && (c->mb_mask || c->sg_mask); j++) {
+            const ggml_tensor *t = ggml_graph_node(cg, j);
+            if (is_view_op(t->op)) continue;
+            if (c->mb_mask && overlaps(t, c->mb_mask)) c->mb_mask = nullptr;
+            if (c->sg_mask && overlaps(t, c->sg_mask)) c->sg_mask = nullptr;
+        }
         i += used - 1;
     }
     c->ws_x = nullptr;
@@ -1394,7 +1443,8 @@ uint64_t graph_key(ggml_cgraph *cg) {
         }
     }
     for (const char *k : {"MQ_GGML_NO_FUSION", "MQ_GEMM_CFG", "MQ_ATTN_SPLIT", "MQ_GEMV_WGS", "MQ_GEMV_PF",
-                          "MQ_FORCE_GEMV_MAX_M", "MQ_Q8_0_VARIANT", "MQ_GGML_NO_MASK_BLOCKS", "MQ_ATTN_SPLIT_WAVES"}) {
+                          "MQ_FORCE_GEMV_MAX_M", "MQ_Q8_0_VARIANT", "MQ_GGML_NO_MASK_BLOCKS", "MQ_ATTN_SPLIT_WAVES",
+                          "MQ_GGML_NO_MASK_SEGMENTS"}) {
         const char *v = std::getenv(k);
         if (v) mix(v, std::strlen(v));
         mix("|", 1);

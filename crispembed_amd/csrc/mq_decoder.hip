@@ -14,6 +14,7 @@
 // Arithmetic is fp32 throughout; the attention's products run on fp16 MFMAs over split
 // (hi + lo) operands, which keeps fp32 accuracy.
 #include <atomic>
+#include <climits>
 #include <cstdlib>
 
 #include "mq_internal.h"
@@ -146,7 +147,7 @@ __global__ __launch_bounds__(256) void k_kv_frag(const AttnArgs a, int nblk) {
     const float *kp = a.k + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
     const float *vp = a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
     const float *kw = a.kw;
-    const float2 *cs = a.cs;
+    const float2 *cs = a.cs ? a.cs + (int64_t)b * a.cs_sb : nullptr;
     const bool on = lane < HALF;
     // K rows of the block, normed and rotated (NEOX pair (i, i + HD/2) in one lane), to LDS;
     // rows past Tk are zero.  The wave's 8 rows are loaded first, all in flight at once.
@@ -256,7 +257,7 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
     if (!RING && idle) return;
     const int hq = min(h, a.nq - 1), hk = hq / (a.nq / a.nkv), qi = q0 + l32;
     const int qrow = min(qi, Tq - 1);
-    const float2 *cs = a.cs;
+    const float2 *cs = a.cs ? a.cs + (int64_t)b * a.cs_sb : nullptr;
 
     // Q^T operand: step st holds Q[qi][16 st + 8 half + j], normed, rotated, times qscale
     v8h qh[NS], ql[NS];
@@ -590,7 +591,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_split(const AttnArgs a, int
     const int q0 = ((int)gridDim.z - 1 - (int)blockIdx.z) * 32;  // longest causal ranges first
     const int hk = h / (a.nq / a.nkv), qi = q0 + l32;
     const int qrow = min(qi, Tq - 1);
-    const float2 *cs = a.cs;
+    const float2 *cs = a.cs ? a.cs + (int64_t)b * a.cs_sb : nullptr;
 
     // the tile's query fragments (hi, lo per 16-dim step), the same for every wave: once in LDS
     // (in the merge buffer, free until the merge), read back per key block
@@ -1079,6 +1080,50 @@ __global__ __launch_bounds__(256) void k_mask_blocks(const uint16_t *__restrict_
         n += (uint32_t)__popcll(m);
     }
     if (lane == 0) lst[0] = n;
+}
+
+// A wave per row: every lane walks its share of the row's keys (16-byte loads when the rows are
+// aligned), counting the finite values and noting the first and last of them and whether any
+// finite value is not +-0; the row is a run of zeros ending on the diagonal when every finite
+// value is zero, the last one is at key r and they are contiguous (count = r - first + 1).
+__global__ __launch_bounds__(256) void k_mask_rows(const uint16_t *__restrict__ mask, int64_t m_sq, int m_al, int T,
+                                                   int32_t *__restrict__ first) {
+    const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= T) return;
+    const uint16_t *row = mask + (int64_t)r * m_sq;
+    int lo = INT_MAX, hi = -1, cnt = 0;
+    bool nz = false;
+    auto see = [&](int key, uint32_t v) {
+        if (v != 0xFC00u) {
+            lo = min(lo, key), hi = max(hi, key), cnt++;
+            nz |= (v & 0x7FFFu) != 0u;
+        }
+    };
+    if (m_al) {
+        const int n8 = T / 8;
+        for (int c = lane; c < n8; c += 64) {
+            const uint4 u = *(const uint4 *)(row + 8 * c);
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) see(8 * c + 2 * e, w[e] & 0xFFFFu), see(8 * c + 2 * e + 1, w[e] >> 16);
+        }
+        for (int key = 8 * n8 + lane; key < T; key += 64) see(key, row[key]);
+    } else {
+        for (int key = lane; key < T; key += 64) see(key, row[key]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        lo = min(lo, __shfl_xor(lo, o)), hi = max(hi, __shfl_xor(hi, o));
+        cnt += __shfl_xor(cnt, o);
+    }
+    const bool any_nz = __ballot(nz) != 0;
+    if (lane == 0) first[r] = (!any_nz && hi == r && cnt == r - lo + 1) ? lo : -1;
+}
+
+hipError_t launch_mask_rows(const uint16_t *mask, int64_t m_sq, bool m_al, int T, int32_t *first, hipStream_t s) {
+    if (T <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_mask_rows, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, mask, m_sq, (int)m_al, T, first);
+    return hipGetLastError();
 }
 
 // at most 16384 key blocks (LDS of the classification)

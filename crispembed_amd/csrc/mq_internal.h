@@ -382,6 +382,7 @@ struct AttnArgs {
     const float *qw = nullptr, *kw = nullptr;
     float eps = 0.f;
     const float2 *cs = nullptr;
+    int64_t cs_sb = 0;  // float2 entries between the angle tables of batch elements (0: shared)
     void *ws = nullptr;
     // q_ws not NULL: the output rows (B * Tq rows of K = nq * hd values; out must hold them as
     // dense rows) also quantized into the GEMM activation workspace q_ws of the projection that
@@ -416,5 +417,9 @@ bool attn_split_form(const AttnArgs &a);
 size_t mask_blocks_bytes(int Bm, int Tq, int Tk);
 hipError_t launch_mask_blocks(const uint16_t *mask, int64_t m_sq, int64_t m_sb, bool m_al, int Bm, int Tq, int Tk,
                               uint32_t *blocks, hipStream_t s);
+// For each of the T rows of a T x T mask (row stride m_sq halves): first[r] = the first key of the
+// run of zeros that ends at key r when the row is exactly that (0 on keys first..r, -inf on every
+// other key), else -1.
+hipError_t launch_mask_rows(const uint16_t *mask, int64_t m_sq, bool m_al, int T, int32_t *first, hipStream_t s);
 
 }  // namespace mq

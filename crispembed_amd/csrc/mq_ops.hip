@@ -1307,9 +1307,51 @@ extern "C" int mq_op_mask_blocks(const mq_view *q, const mq_view *k, const mq_vi
                   "mask_blocks");
 }
 
+extern "C" size_t mq_op_mask_segments_bytes(const mq_view *q, const mq_view *k, const mq_view *mask) {
+    if (!q || !k || !mask || !shape_ok(q) || !shape_ok(k) || !shape_ok(mask) || mask->type != MQ_TYPE_F16 ||
+        mask->ne[2] != 1 || mask->ne[3] != 1 || q->ne[3] != 1 || q->ne[1] != k->ne[1] || mask->ne[1] < q->ne[1] ||
+        mask->ne[0] < k->ne[1] || q->ne[1] > INT32_MAX || mask->nb[0] != 2 || mask->nb[1] % 2)
+        return 0;
+    return (size_t)q->ne[1] * sizeof(int32_t);
+}
+
+extern "C" int mq_op_mask_segments(const mq_view *q, const mq_view *k, const mq_view *mask, void *scratch,
+                                   size_t scratch_bytes, int64_t *seg_len, void *stream) {
+    if (!seg_len) return fail("mask_segments: seg_len required");
+    *seg_len = 0;
+    const size_t need = mq_op_mask_segments_bytes(q, k, mask);
+    if (need == 0) return fail("mask_segments: one F16 mask [>= T, >= T] over q and k of T positions and one batch");
+    if (!have_data({q, k, mask}) || !scratch) return fail("missing data pointer");
+    if (((uintptr_t)scratch & 3) || scratch_bytes < need)
+        return set_error(MQ_EINVAL, "mq_op_mask_segments: %zu bytes (4-byte aligned) of scratch needed", need);
+    const int T = (int)q->ne[1];
+    const int64_t m_sq = mask->nb[1] / 2;
+    const bool m_al = (uintptr_t)mask->data % 16 == 0 && m_sq % 8 == 0;
+    hipStream_t s = (hipStream_t)stream;
+    std::vector<int32_t> first(T);
+    int rc = hip_rc(launch_mask_rows((const uint16_t *)mask->data, m_sq, m_al, T, (int32_t *)scratch, s), "mask_rows");
+    if (rc != 0) return rc;
+    if (hipMemcpyAsync(first.data(), scratch, need, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return set_error(MQ_EHIP, "mq_op_mask_segments: reading the row summary back failed");
+    // segments of S rows: row r's run starts at its segment's first row
+    int64_t S = T;
+    for (int r = 1; r < T; r++)
+        if (first[r] != 0) {
+            S = r;
+            break;
+        }
+    if (T % S != 0) return 0;
+    for (int r = 0; r < T; r++)
+        if (first[r] != (int32_t)(r / S * S)) return 0;
+    *seg_len = S;
+    return 0;
+}
+
 static int flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask, const mq_view *dst,
                       float scale, void *workspace, size_t workspace_bytes, void *act_ws, size_t act_ws_bytes,
-                      int flags, void *stream, const QkNormRope *qk = nullptr, const void *blocks = nullptr) {
+                      int flags, void *stream, const QkNormRope *qk = nullptr, const void *blocks = nullptr,
+                      int64_t causal_seg = 0, int act_type = MQ_TYPE_Q8_0) {
     if (const char *e = check_flash(q, k, v, mask, dst)) return fail(e);
     if (!have_data({q, k, v, mask, dst})) return fail("missing data pointer");
     if (qk) {
@@ -1337,6 +1379,17 @@ static int flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, cons
     }
     a.B = (int)q->ne[3], a.Tq = (int)q->ne[1], a.Tk = (int)k->ne[1];
     a.nq = (int)q->ne[2], a.nkv = (int)k->ne[2], a.hd = (int)q->ne[0];
+    if (causal_seg > 0) {  // the mask is block-diagonal causal (mq_op_mask_segments): per-segment causal attention
+        const int64_t S = causal_seg, T = q->ne[1];
+        if (!mask || k->ne[1] != T || T % S != 0 || S % 32 != 0 || q->ne[3] != 1 || S > INT32_MAX)
+            return fail("flash_attn: causal segments need a mask, Tq = Tk = a multiple of the segment (a multiple "
+                        "of 32) and one batch");
+        a.B = (int)(T / S), a.Tq = a.Tk = (int)S;
+        a.q_sb = S * a.q_st, a.k_sb = S * a.k_st, a.v_sb = S * a.v_st, a.o_sb = S * a.o_st;
+        a.mask = nullptr, a.m_sq = a.m_sh = a.m_sb = 0, a.m_al = false;
+        a.causal = 1;
+        blocks = nullptr;
+    }
     if (blocks) {  // lists from mq_op_mask_blocks of these operands; ignored by the other forms
         if (!mask || !takes_mask_blocks(q, k, mask)) blocks = nullptr;
         if ((uintptr_t)blocks & 3) return fail("flash_attn: mask block lists not 4-byte aligned");
@@ -1348,14 +1401,19 @@ static int flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, cons
     a.ws = workspace;
     a.kv_ready = (flags & MQ_ATTN_KV_READY) != 0;
     if (qk) a.qw = qk->q_w, a.kw = qk->k_w, a.eps = qk->eps, a.cs = (const float2 *)qk->cs;
+    if (qk && causal_seg > 0) a.cs_sb = causal_seg * (q->ne[0] / 2);  // the table holds every row's angles
     if (act_ws) {
         const int64_t K = dst->ne[0] * dst->ne[1], rows = dst->ne[2] * dst->ne[3];
-        if (K % 128 != 0 || dst->nb[1] != (size_t)dst->ne[0] * 4 || dst->nb[2] != (size_t)K * 4 ||
-            dst->nb[3] != dst->nb[2] * (size_t)dst->ne[2])
-            return fail("flash_attn_q8_0: dst must be dense rows of n_head * head_dim floats, a multiple of 128");
-        if (((uintptr_t)act_ws & 255) || act_ws_bytes < act_planes(MQ_TYPE_Q8_0, rows, K, true).total)
-            return set_error(MQ_EINVAL, "mq_op_flash_attn_q8_0: activation workspace (256-byte aligned) too small");
+        if (act_type != MQ_TYPE_Q8_0 && act_type != MQ_TYPE_Q4_K && act_type != MQ_TYPE_Q6_K)
+            return fail("flash_attn: the quantized output is for a Q8_0, Q4_K or Q6_K projection");
+        if (K % (act_type == MQ_TYPE_Q8_0 ? 128 : 256) != 0 || dst->nb[1] != (size_t)dst->ne[0] * 4 ||
+            dst->nb[2] != (size_t)K * 4 || dst->nb[3] != dst->nb[2] * (size_t)dst->ne[2])
+            return fail("flash_attn: a quantized output needs dst as dense rows of n_head * head_dim floats, a "
+                        "multiple of 128 (Q8_0) or 256 (K-quants)");
+        if (((uintptr_t)act_ws & 255) || act_ws_bytes < act_planes(act_type, rows, K, true).total)
+            return set_error(MQ_EINVAL, "mq_op_flash_attn: activation workspace (256-byte aligned) too small");
         a.q_ws = act_ws;
+        a.q_type = act_type;
         a.q_var = mq_q8_0_variant();
     }
     return hip_rc(launch_attn(a, (hipStream_t)stream), "flash_attn");
@@ -1395,17 +1453,19 @@ extern "C" int mq_op_flash_attn_qk_norm_rope(const mq_view *q, const mq_view *k,
 
 extern "C" int mq_op_flash_attn_blocks(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
                                        const mq_view *dst, float scale, const float *q_norm_w, const float *k_norm_w,
-                                       float eps, const float *cs, const void *mask_blocks, void *workspace,
-                                       size_t workspace_bytes, void *act_workspace, size_t act_workspace_bytes,
-                                       int flags, void *stream) {
+                                       float eps, const float *cs, const void *mask_blocks, int64_t causal_segment,
+                                       void *workspace, size_t workspace_bytes, void *act_workspace,
+                                       size_t act_workspace_bytes, int act_type, int flags, void *stream) {
     if (flags & ~MQ_ATTN_KV_READY) return set_error(MQ_EINVAL, "mq_op_flash_attn_blocks: unknown flags");
     const bool norm = q_norm_w || k_norm_w || cs;
     if (norm && !(q_norm_w && k_norm_w && cs))
         return fail("flash_attn_blocks: q_norm_w, k_norm_w and cs go together");
     if (mask_blocks && !mask) return fail("flash_attn_blocks: block lists without a mask");
+    if (causal_segment < 0) return fail("flash_attn_blocks: negative causal segment");
+    if (norm && (flags & MQ_ATTN_KV_READY)) return fail("flash_attn_blocks: K/V fragments computed elsewhere");
     const QkNormRope qk{q_norm_w, k_norm_w, cs, eps};
     return flash_attn(q, k, v, mask, dst, scale, workspace, workspace_bytes, act_workspace, act_workspace_bytes, flags,
-                      stream, norm ? &qk : nullptr, mask_blocks);
+                      stream, norm ? &qk : nullptr, mask_blocks, causal_segment, act_type);
 }
 
 extern "C" int mq_op_rope_cache(const mq_view *pos, const mq_view *freq_factors, int n_dims, int n_ctx_orig,

@@ -215,15 +215,35 @@ size_t mq_op_mask_blocks_bytes(const mq_view *q, const mq_view *k, const mq_view
 int mq_op_mask_blocks(const mq_view *q, const mq_view *k, const mq_view *mask, void *blocks, size_t blocks_bytes,
                       void *stream);
 
+/* The structure of a batched decoder's mask (decoder_encode_tokens_batch without a shared prefix,
+ * every item T_max long: src/decoder_embed.cpp:1429-1437): seg_len = S when the T x T mask of q
+ * and k (T positions, one batch, the mask shared by every head) is exactly block-diagonal causal
+ * over segments of S rows -- 0 on keys from the row's segment start up to the row itself, -inf
+ * on every other key, every value -- else 0.  One pass over the mask and a T x 4-byte readback:
+ * the call synchronizes the stream (not for HIP graph capture).  scratch: device memory of
+ * mq_op_mask_segments_bytes (0: these operands have no such form).  The attention of such a mask
+ * is the per-segment causal attention, with no mask reads (mq_op_flash_attn_blocks'
+ * causal_segment). */
+size_t mq_op_mask_segments_bytes(const mq_view *q, const mq_view *k, const mq_view *mask);
+int mq_op_mask_segments(const mq_view *q, const mq_view *k, const mq_view *mask, void *scratch, size_t scratch_bytes,
+                        int64_t *seg_len, void *stream);
+
 /* The general attention entry point: mq_op_flash_attn_ex with flags, plus the q / k norm and
  * rotation of mq_op_flash_attn_qk_norm_rope when q_norm_w, k_norm_w and cs are given (all three,
  * or all NULL), plus mask_blocks: NULL, or mq_op_mask_blocks' lists for these q, k and mask
- * (ignored when mq_op_mask_blocks_bytes of the operands is 0).  Results equal those entry points'
- * up to the order in which the waves of a query tile share out its key blocks. */
+ * (ignored when mq_op_mask_blocks_bytes of the operands is 0), plus causal_segment: 0, or the
+ * seg_len mq_op_mask_segments found for this mask (a multiple of 32): each segment then runs as a
+ * causal sequence of its own and the mask is not read; plus act_type: the weight type of the
+ * projection that reads the result when act_workspace is given (MQ_TYPE_Q8_0, or MQ_TYPE_Q4_K /
+ * MQ_TYPE_Q6_K for their Q8_K activations: n_head * head_dim a multiple of 256), whose activation
+ * workspace receives the rows quantized as mq_quantize_act_ex(act_type, ..., MQ_PATH_GEMM) writes
+ * them.  Results equal those entry points' up to the order in which the waves of a query tile
+ * share out its key blocks. */
 int mq_op_flash_attn_blocks(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask,
                             const mq_view *dst, float scale, const float *q_norm_w, const float *k_norm_w, float eps,
-                            const float *cs, const void *mask_blocks, void *workspace, size_t workspace_bytes,
-                            void *act_workspace, size_t act_workspace_bytes, int flags, void *stream);
+                            const float *cs, const void *mask_blocks, int64_t causal_segment, void *workspace,
+                            size_t workspace_bytes, void *act_workspace, size_t act_workspace_bytes, int act_type,
+                            int flags, void *stream);
 
 /* ggml_mul_mat_id, the mixture-of-experts mat-mul (src/crispembed.cpp:1365,1371):
  *   experts: n_exp prepared weight images of `type` (n x k each, as mq_weight_prepare builds

@@ -576,12 +576,103 @@ def test_mask_block_lists(case):
     outs = []
     for bl in (ctypes.c_void_p(blocks.data_ptr()), None):
         out = _t().full((B, Tq, nh, hd), np.nan, dtype=_t().float32, device="cuda")
-        _call(L.mq_op_flash_attn_blocks, qv, kv, vv, mv, mq.view(out), scale, None, None, 0.0, None, bl, wp,
-              ws_bytes, None, 0, 0, stream())
+        _call(L.mq_op_flash_attn_blocks, qv, kv, vv, mv, mq.view(out), scale, None, None, 0.0, None, bl, 0, wp,
+              ws_bytes, None, 0, 0, 0, stream())
         outs.append(host(out))
         assert np.isfinite(outs[-1]).all()
         assert np.abs(outs[-1] - ref).max() / np.abs(ref).max() <= 2e-5
     assert np.abs(outs[0] - outs[1]).max() / np.abs(ref).max() <= 1e-6
+
+
+@pytest.mark.parametrize("case,want", [("uniform", 128), ("single", 320), ("unaligned", 64), ("ragged", 0),
+                                       ("prefix", 0), ("finite", 0), ("bidirectional", 0), ("odd", 96)])
+def test_mask_segments(case, want):
+    """mq_op_mask_segments finds the segment length exactly when the mask is block-diagonal causal
+    over uniform segments (the batched decoder's mask with full-length items; one causal sequence;
+    rows not 16-byte aligned), and 0 for every near miss: ragged items (padding rows see only
+    themselves), a shared prefix, one finite nonzero value, bidirectional blocks.  With a segment a
+    multiple of 32 the attention then runs per causal segment: equal to the mask's attention (fp64)
+    and to the block-list form, with the q / k norm and rotation (positions restarting per segment)
+    and with the o projection's Q8_K activation stored as the quantizer would write it."""
+    L = mq.lib()
+    rng = _rng(len(case) + want)
+    if case in ("uniform", "unaligned", "finite"):
+        S = 128 if case != "unaligned" else 64
+        mask = _batch_mask([S] * 4, S)
+        if case == "finite":
+            mask[300, 260] = np.float16(-0.5)
+    elif case == "single":
+        mask = _batch_mask([320], 320)
+    elif case == "odd":
+        mask = _batch_mask([96] * 3, 96)
+    elif case == "ragged":
+        mask = _batch_mask([128, 100, 128, 128], 128)
+    elif case == "prefix":
+        mask = _batch_mask([70, 47, 90], 50, prefix=40)
+    else:
+        mask = np.full((384, 384), -np.inf, np.float16)
+        for b in range(3):
+            mask[128 * b:128 * (b + 1), 128 * b:128 * (b + 1)] = 0
+    T = mask.shape[0]
+    stride = T + 8 + (case == "unaligned")
+    padded = np.full((1, 1, T, stride), np.nan, np.float16)
+    padded[0, 0, :, :T] = mask
+    mask_d = _cuda(padded)[..., :T]
+    hd, nh, nkv = 128, 4, 2
+    qx = rng.standard_normal((1, T, nh, hd)).astype(np.float32)
+    kx, vx = (rng.standard_normal((1, T, nkv, hd)).astype(np.float32) for _ in range(2))
+    q, k, v = (_cuda(x).permute(0, 2, 1, 3) for x in (qx, kx, vx))
+    qv, kv, vv, mv = mq.view(q), mq.view(k), mq.view(v), mq.view(mask_d)
+    nbytes = L.mq_op_mask_segments_bytes(qv, kv, mv)
+    assert nbytes == T * 4
+    scratch = _t().empty(T, dtype=_t().int32, device="cuda")
+    seg = ctypes.c_int64(-1)
+    _call(L.mq_op_mask_segments, qv, kv, mv, ctypes.c_void_p(scratch.data_ptr()), nbytes, ctypes.byref(seg), stream())
+    assert seg.value == want, (case, seg.value)
+    if want == 0 or want % 32:
+        return
+    ws_bytes = L.mq_op_flash_attn_workspace_bytes(kv)
+    ws = _t().empty(ws_bytes + 256, dtype=_t().uint8, device="cuda")
+    wp = ctypes.c_void_p(ws.data_ptr() + (-ws.data_ptr()) % 256)
+    scale = 1.0 / np.sqrt(hd)
+    ref = _attn64(qx.transpose(0, 2, 1, 3), kx.transpose(0, 2, 1, 3), vx.transpose(0, 2, 1, 3), mask[None, None],
+                  scale)
+    nb = L.mq_op_mask_blocks_bytes(qv, kv, mv)
+    blocks = _t().empty(nb // 4, dtype=_t().int32, device="cuda")
+    _call(L.mq_op_mask_blocks, qv, kv, mv, ctypes.c_void_p(blocks.data_ptr()), nb, stream())
+    # q / k norm weights and the angles of positions restarting per segment
+    qw, kw = (_cuda((1.0 + 0.1 * rng.standard_normal(hd)).astype(np.float32)) for _ in range(2))
+    pos = _cuda((np.arange(T) % want).astype(np.int32))
+    cs = _t().empty((T, hd), dtype=_t().float32, device="cuda")
+    _call(L.mq_op_rope_cache, mq.view(pos), None, hd, 0, 1e6, 1.0, 0.0, 1.0, 0.0, 0.0,
+          ctypes.c_void_p(cs.data_ptr()), stream())
+    K, M = nh * hd, T
+    act_bytes = L.mq_workspace_bytes(mq.TYPE_Q4_K, M, K)
+    outs = {}
+    for name, s_, bl, norm in (("seg", want, None, False), ("lists", 0, blocks, False), ("seg_qk", want, None, True),
+                               ("lists_qk", 0, blocks, True)):
+        out = _t().full((1, T, nh, hd), np.nan, dtype=_t().float32, device="cuda")
+        act = _t().full((act_bytes + 256,), 0xAB, dtype=_t().uint8, device="cuda")
+        ap = act.data_ptr() + (-act.data_ptr()) % 256
+        nw = (ctypes.c_void_p(qw.data_ptr()), ctypes.c_void_p(kw.data_ptr()), 1e-6,
+              ctypes.c_void_p(cs.data_ptr())) if norm else (None, None, 0.0, None)
+        _call(L.mq_op_flash_attn_blocks, qv, kv, vv, mv, mq.view(out), scale, *nw,
+              None if bl is None else ctypes.c_void_p(bl.data_ptr()), s_, wp, ws_bytes, ctypes.c_void_p(ap),
+              act_bytes, mq.TYPE_Q4_K, 0, stream())
+        want_act = _t().empty((act_bytes + 256,), dtype=_t().uint8, device="cuda")
+        wq = want_act.data_ptr() + (-want_act.data_ptr()) % 256
+        mq.check(L.mq_quantize_act_ex(mq.TYPE_Q4_K, ctypes.c_void_p(out.data_ptr()), K, M, K, None, 0,
+                                      ctypes.c_void_p(wq), act_bytes, mq.PATH_GEMM, stream()))
+        _t().cuda.synchronize()
+        import act_layout as AL
+        o1, o2 = (ap - act.data_ptr()), (wq - want_act.data_ptr())
+        diff = AL.live_difference(host(act)[o1:o1 + act_bytes], host(want_act)[o2:o2 + act_bytes], mq.TYPE_Q4_K, M, K)
+        assert diff is None, (name, diff)
+        outs[name] = host(out)
+        assert np.isfinite(outs[name]).all()
+    assert np.abs(outs["seg"] - ref).max() / np.abs(ref).max() <= 2e-5
+    for a, b in (("seg", "lists"), ("seg_qk", "lists_qk")):
+        assert np.abs(outs[a] - outs[b]).max() / np.abs(outs[b]).max() <= 1e-6, (a, b)
 
 
 def test_mask_block_lists_not_taken():
