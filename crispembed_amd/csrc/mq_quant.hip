@@ -221,9 +221,10 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
 // ---------------------------------------------------------------------------
 enum { TQ_Q8_0 = 0, TQ_Q8_K = 1, TQ_F16 = 2 };
 
-// RPW rows per wave: 8 (a workgroup per 32-row tile and CB-byte column block) or 2 (four
-// workgroups per tile, rows 8 q .. 8 q + 7 in workgroup q, each writing only its rows' 16-byte
-// units of the fragments, scales and min-term halves: small inputs spread over 4x the CUs).
+// RPW rows per wave: 8 (a workgroup per 32-row tile and CB-byte column block), 2 or 1 (Q8_K:
+// 4 or 8 workgroups per tile, the RW = 4 RPW rows RW q .. RW q + RW - 1 in workgroup q, each
+// writing only its rows' 16-byte units of the fragments, scales and min-term halves: shorter
+// dependency chains per wave and more workgroups to spread).
 template <int FMT, int VARIANT, bool VEC4, int RPW = 8>
 __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict__ x, int64_t ldx,
                                                         int8_t *__restrict__ xq, float *__restrict__ xd,
@@ -241,14 +242,16 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
     __shared__ float dsh[NSC > 0 ? NSC : 1][32];
     __shared__ __attribute__((aligned(16))) _Float16 msh[FMT == TQ_Q8_K ? 512 : 8];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int RW = 4 * RPW, WPT = 32 / RW;          // rows per workgroup, workgroups per tile
     const int64_t ncb = kb_pad / CB;
-    const int64_t unit = RPW == 8 ? blockIdx.x : blockIdx.x >> 2;
+    const int64_t unit = blockIdx.x / WPT;
     const int64_t rt = unit / ncb, cb = unit - rt * ncb;
-    const int rbase = RPW == 8 ? 0 : 8 * (blockIdx.x & 3);  // the workgroup's first row in the tile
+    const int rbase = RW * (int)(blockIdx.x % WPT);     // the workgroup's first row in the tile
     const int sub = lane % LPR, rsub = lane / LPR;
     const int kbyte = sub * 4 * BPV;                    // byte of this lane's 4 values within CB
     const int c = kbyte >> 5, cbyte = kbyte & 31;       // fragment, byte within the 32-byte chunk
-    static_assert(RPW == 8 || RPW == 2, "8 or 2 rows per wave");
+    static_assert(RPW == 8 || RPW == 2 || RPW == 1, "8, 2 or 1 rows per wave");
+    static_assert(RPW % RPI == 0, "whole wave passes");
     constexpr int NIT = RPW / RPI;                      // rows per lane
     const int64_t kv = (cb * CB + kbyte) / BPV;         // first value index of this lane
     float4 vin[NIT];                                    // every load in flight before any math
@@ -269,8 +272,20 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
             if (row < m && kv < k) vin[it] = pre_load<VEC4>(x + row * ldx + kv, pre, bias, kv, uoff);
         }
     }
+    if constexpr (FMT == TQ_Q8_K) {  // one superblock per row, a row per wave pass (RPI = 1)
+        int rr[NIT];
+        int8_t *dd[NIT];
+        float *ds[NIT];
 #pragma unroll
-    for (int it = 0; it < NIT; it++) {
+        for (int it = 0; it < NIT; it++) {
+            rr[it] = rbase + wave * RPW + it * RPI + rsub;
+            dd[it] = frag + c * FST + ((rr[it] + 32 * (cbyte >> 4)) << 4) + (cbyte & 15);
+            ds[it] = &dsh[0][rr[it]];
+        }
+        q8_K_block_rows<NIT>(vin, lane, rr, dd, ds, msh);
+    }
+#pragma unroll
+    for (int it = 0; it < NIT && FMT != TQ_Q8_K; it++) {
         const int r = rbase + wave * RPW + it * RPI + rsub;  // row within the tile
         const float4 v = vin[it];
         int8_t *dst = frag + c * FST + ((r + 32 * (cbyte >> 4)) << 4) + (cbyte & 15);
@@ -293,40 +308,25 @@ __global__ __launch_bounds__(256) void k_quantize_tiled(const float *__restrict_
             };
             *(uint32_t *)dst = q(v.x) | (q(v.y) << 8) | (q(v.z) << 16) | (q(v.w) << 24);
             if ((sub & 7) == 0) dsh[c][r] = f16_bits_to_f32(f32_to_f16_bits(d));
-        } else {
-            q8_K_block_row(v, lane, r, dst, &dsh[0][r], msh);
         }
     }
     __syncthreads();
+    // the 16-byte units of the workgroup's rows rbase .. rbase + RW - 1: lanes rbase + i and
+    // 32 + rbase + i of each fragment (all 64 lanes when RW = 32: whole 1 KB fragments)
     const int t = threadIdx.x;
-    if constexpr (RPW == 8) {
 #pragma unroll
-        for (int p = t; p < NCH * 64; p += 256) {
-            const int f = p >> 6, L = p & 63;
-            const int4 val = *(const int4 *)(frag + f * FST + L * 16);
-            *(int4 *)(xq + ((rt * (kb_pad >> 5) + cb * NCH + f) << 10) + L * 16) = val;
-        }
-        if constexpr (NSC > 0) {
-            if (t < NSC * 32) xd[(cb * NSC + (t >> 5)) * m_pad + rt * 32 + (t & 31)] = dsh[t >> 5][t & 31];
-        }
-        if constexpr (FMT == TQ_Q8_K) {
-            if (t < 64) ((int4 *)(xmin + ((rt * ncb + cb) << 9)))[t] = ((const int4 *)msh)[t];
-        }
-    } else {
-        // the units of rows rbase .. rbase + 7: lanes rbase + i and 32 + rbase + i of each fragment
-        if (t < NCH * 16) {
-            const int f = t >> 4, L = rbase + (t & 7) + 32 * ((t >> 3) & 1);
-            const int4 val = *(const int4 *)(frag + f * FST + L * 16);
-            *(int4 *)(xq + ((rt * (kb_pad >> 5) + cb * NCH + f) << 10) + L * 16) = val;
-        }
-        if constexpr (NSC > 0) {
-            if (t < NSC * 8) xd[(cb * NSC + (t >> 3)) * m_pad + rt * 32 + rbase + (t & 7)] = dsh[t >> 3][rbase + (t & 7)];
-        }
-        if constexpr (FMT == TQ_Q8_K) {
-            if (t < 16) {
-                const int e = rbase + (t & 7) + 32 * (t >> 3);
-                ((int4 *)(xmin + ((rt * ncb + cb) << 9)))[e] = ((const int4 *)msh)[e];
-            }
+    for (int p = t; p < NCH * 2 * RW; p += 256) {
+        const int f = p / (2 * RW), u = p % (2 * RW), L = rbase + u % RW + 32 * (u / RW);
+        const int4 val = *(const int4 *)(frag + f * FST + L * 16);
+        *(int4 *)(xq + ((rt * (kb_pad >> 5) + cb * NCH + f) << 10) + L * 16) = val;
+    }
+    if constexpr (NSC > 0) {
+        if (t < NSC * RW) xd[(cb * NSC + t / RW) * m_pad + rt * 32 + rbase + t % RW] = dsh[t / RW][rbase + t % RW];
+    }
+    if constexpr (FMT == TQ_Q8_K) {
+        if (t < 2 * RW) {
+            const int e = rbase + t % RW + 32 * (t / RW);
+            ((int4 *)(xmin + ((rt * ncb + cb) << 9)))[e] = ((const int4 *)msh)[e];
         }
     }
 }
@@ -721,20 +721,25 @@ static hipError_t tiled_dispatch(const float *x, int64_t ldx, int8_t *xq, float 
     if (m_pad % 32 != 0 || kb_pad % CB != 0) return hipErrorInvalidValue;
     const int64_t wgs = (m_pad / 32) * (kb_pad / CB);
     if (wgs == 0) return hipSuccess;
-    // under 512 tiles: four workgroups per tile (8 rows each; F16 keeps one, its lanes cover
-    // 4 rows per pass)
-    constexpr int RPW_SMALL = FMT == TQ_F16 ? 8 : 2;
-    const bool split = RPW_SMALL == 2 && wgs < 512;
-    const dim3 g((unsigned)(split ? 4 * wgs : wgs)), b(256);
+    // Rows per wave: Q8_K 2 (four workgroups per tile; measured on MI355X inside the Q4_K FFN
+    // step: 8192 x 1024 18.8 -> 14.0 us, 8192 x 4096 43.7 -> 37.3 us against 8); Q8_0 8, or 2
+    // under 512 tiles; F16 8 (its lanes cover 4 rows per pass).  MQ_TQ_RPW=8/2/1 (Q8_K) forces one
+    // (measurements).
+    int rpw = FMT == TQ_Q8_K ? 2 : (FMT == TQ_Q8_0 && wgs < 512 ? 2 : 8);
+    if (const char *e = getenv("MQ_TQ_RPW"))
+        if (*e && FMT == TQ_Q8_K) rpw = atoi(e) == 8 ? 8 : atoi(e) == 1 ? 1 : 2;
+    const dim3 g((unsigned)(wgs * (32 / (4 * rpw)))), b(256);
     const bool v4 = aligned16(x, ldx) && uoff % 4 == 0;
 #define MQ_TQ_R(VAR, RPW)                                                                                                    \
     if (v4) hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, true, RPW>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad, pre, bias, uoff); \
     else hipLaunchKernelGGL((k_quantize_tiled<FMT, VAR, false, RPW>), g, b, 0, s, x, ldx, xq, xd, xmin, m, k, m_pad, kb_pad, pre, bias, uoff);
-#define MQ_TQ(VAR)            \
-    if (split) {              \
-        MQ_TQ_R(VAR, RPW_SMALL) \
-    } else {                  \
-        MQ_TQ_R(VAR, 8)       \
+#define MQ_TQ(VAR)                                   \
+    if (rpw == 8) {                                  \
+        MQ_TQ_R(VAR, 8)                              \
+    } else if (FMT != TQ_F16 && rpw == 2) {          \
+        MQ_TQ_R(VAR, (FMT == TQ_F16 ? 8 : 2))        \
+    } else if (FMT == TQ_Q8_K) {                     \
+        MQ_TQ_R(VAR, (FMT == TQ_Q8_K ? 1 : 8))       \
     }
     if (FMT != TQ_Q8_0) {
         MQ_TQ(MQ_Q8_0_X86);
