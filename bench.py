@@ -131,6 +131,42 @@ def bench_q4k_ffn(args, torch, L, mq, synth):
     med = lambda v: sorted(v)[len(v) // 2]
     t_up_med = med([e[0].elapsed_time(e[1]) for e in evs])
     t_dn_med = med([e[2].elapsed_time(e[3]) for e in evs])
+    # the same two products chained as the encoder FFN runs them: the up GEMM applies GELU-erf and
+    # stores its output as the down GEMM's Q8_K activation (mq_mul_mat_q_requant), so the fp32
+    # intermediate and its quantizer pass disappear
+    chain = {}
+    if L.mq_mul_mat_q_requant_supported(mq.TYPE_Q4_K, mq.TYPE_Q4_K, M, F):
+        def step_chain(evs=None):
+            mq.check(L.mq_quantize_act(up.wtype, ctypes.c_void_p(up.x.data_ptr()), H, M, H,
+                                       ctypes.c_void_p(up.wsp), up.wsb, mq.PATH_GEMM, s))
+            if evs is not None:
+                evs[0].record(stream)
+            mq.check(L.mq_mul_mat_q_requant(mq.TYPE_Q4_K, ctypes.c_void_p(up.wp), F, H, ctypes.c_void_p(up.wsp), M,
+                                            None, mq.PRE_GELU_ERF, mq.TYPE_Q4_K, ctypes.c_void_p(dn.wsp), dn.wsb, s))
+            if evs is not None:
+                evs[1].record(stream)
+            mq.check(L.mq_mul_mat_q(dn.wtype, ctypes.c_void_p(dn.wp), H, F, ctypes.c_void_p(dn.wsp), M,
+                                    ctypes.c_void_p(dn.y.data_ptr()), H, mq.PATH_GEMM, s))
+            if evs is not None:
+                evs[2].record(stream)
+
+        for _ in range(args.warmup):
+            step_chain()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.steps):
+            step_chain()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms_chain = e0.elapsed_time(e1) / args.steps
+        evc = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+        for i in range(args.steps):
+            step_chain(evc[i])
+        torch.cuda.synchronize()
+        chain = {"ms_per_step": ms_chain,
+                 "tops": (ops_up + ops_dn) / (ms_chain * 1e-3) / 1e12,
+                 "gemm_up_requant_us": sum(e[0].elapsed_time(e[1]) for e in evc) / args.steps * 1e3,
+                 "gemm_down_us": sum(e[1].elapsed_time(e[2]) for e in evc) / args.steps * 1e3}
 
     def gemm_roofline(name, n, k, ops, t_ms, w_bytes):
         """One GEMM launch against its binding roofline: the larger of its MFMA time (int8 ops at
@@ -186,6 +222,7 @@ def bench_q4k_ffn(args, torch, L, mq, synth):
         "value": (ops_up + ops_dn) / (ms_step * 1e-3) / 1e12,
         "gemm_up_us": t_up * 1e3,
         "gemm_down_us": t_dn * 1e3,
+        "chain": chain,
         "roofline": roof,
         "x": (x_up, x_dn, q_up, q_dn),
     }
@@ -841,6 +878,7 @@ def main():
             "weights": "fp32 N(0,0.02) -> Q4_K (ggml _ref quantizer)",
             "gemm_up_us": round(r["gemm_up_us"], 2),
             "gemm_down_us": round(r["gemm_down_us"], 2),
+            "ffn_chain": {k: round(v, 3) for k, v in r["chain"].items()},
         },
         "roofline": r["roofline"],
         "cpu_baseline": cpu,

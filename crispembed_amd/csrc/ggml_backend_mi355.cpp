@@ -931,11 +931,12 @@ int try_fuse_bias_gelu_mul_mat(BackendCtx *c, ggml_cgraph *cg, int i, int n, enu
     return dst == mm ? 3 : 4;
 }
 
-// MUL_MAT(w1, x) -> ADD(., bias) -> UNARY(GELU_ERF) -> MUL_MAT(w2, .) [-> ADD(., bias2)] with a
-// Q8_0 w2 and both products on the GEMM path (the encoder FFN): the first GEMM adds the bias,
-// applies GELU-erf and quantizes its own output for the second (mq_mul_mat_q_requant, the same
-// bytes the activation quantizer would write), so the FFN's intermediate is never written.
-// The quantized intermediate sits in the workspace after x's quantized activation.
+// MUL_MAT(w1, x) -> ADD(., bias) -> UNARY(GELU_ERF) -> MUL_MAT(w2, .) [-> ADD(., bias2)] with
+// both products on the GEMM path (the encoder FFN) and a Q8_0 w2, or Q4_K / Q6_K w1 and w2 at
+// the sizes the Q8_K-output GEMM accepts: the first GEMM adds the bias, applies GELU-erf and
+// quantizes its own output for the second (mq_mul_mat_q_requant, the same bytes the activation
+// quantizer would write), so the FFN's intermediate is never written.  The quantized
+// intermediate sits in the workspace after x's quantized activation.
 int try_fuse_ffn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status &st) {
     if (i + 3 >= n || !feeds_only_next(cg, i) || !feeds_only_next(cg, i + 1) || !feeds_only_next(cg, i + 2)) return 0;
     ggml_tensor *mm1 = ggml_graph_node(cg, i), *add = ggml_graph_node(cg, i + 1);
@@ -946,10 +947,11 @@ int try_fuse_ffn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status 
     if (last_compute_node(cg, i + 3, n)) return 0;  // an observer may read the GELU result
     const ggml_tensor *w1 = mm1->src[0], *x = mm1->src[1], *w2 = mm2->src[0];
     const int64_t K1 = w1->ne[0], N1 = w1->ne[1], N2 = w2->ne[1];
-    if (w2->type != GGML_TYPE_Q8_0 || w2->ne[0] != N1 || N1 % 128 != 0 || !is_row_vector(add->src[1], N1)) return 0;
-    const int mt1 = mq_type_of(w1->type);
+    if (w2->ne[0] != N1 || !is_row_vector(add->src[1], N1)) return 0;
+    const int mt1 = mq_type_of(w1->type), mt2 = mq_type_of(w2->type);
     const int64_t M = x->ne[1] * x->ne[2] * x->ne[3];
-    if (mq_mul_mat_path(mt1, N1, K1, M) != MQ_PATH_GEMM || mq_mul_mat_path(MQ_TYPE_Q8_0, N2, N1, M) != MQ_PATH_GEMM)
+    if (!mq_mul_mat_q_requant_supported(mt1, mt2, M, N1)) return 0;
+    if (mq_mul_mat_path(mt1, N1, K1, M) != MQ_PATH_GEMM || mq_mul_mat_path(mt2, N2, N1, M) != MQ_PATH_GEMM)
         return 0;
     ggml_tensor *dst = mm2;
     const float *bias2 = nullptr;
@@ -962,7 +964,7 @@ int try_fuse_ffn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status 
         }
     }
     const size_t off = (mq_workspace_bytes(mt1, M, K1) + 255) & ~(size_t)255;
-    if (!ensure_ws(c, off + mq_workspace_bytes(MQ_TYPE_Q8_0, M, N1))) {
+    if (!ensure_ws(c, off + mq_workspace_bytes(mt2, M, N1))) {
         st = GGML_STATUS_ALLOC_FAILED;
         return dst == mm2 ? 4 : 5;
     }
@@ -971,11 +973,11 @@ int try_fuse_ffn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status 
     if (rc == 0) {
         observe_act(c, mm1, mt1, M, K1, MQ_PATH_GEMM, c->ws);
         rc = mq_mul_mat_q_requant(mt1, w1->data, N1, K1, c->ws, M, (const float *)add->src[1]->data, MQ_PRE_GELU_ERF,
-                                  MQ_TYPE_Q8_0, ws2, c->ws_bytes - off, c->stream);
+                                  mt2, ws2, c->ws_bytes - off, c->stream);
     }
     if (rc == 0) {
-        observe_act(c, mm2, MQ_TYPE_Q8_0, M, N1, MQ_PATH_GEMM, ws2);
-        rc = mq_mul_mat_q_ex(MQ_TYPE_Q8_0, w2->data, N2, N1, ws2, M, (float *)dst->data, (int64_t)(dst->nb[1] / 4), bias2,
+        observe_act(c, mm2, mt2, M, N1, MQ_PATH_GEMM, ws2);
+        rc = mq_mul_mat_q_ex(mt2, w2->data, N2, N1, ws2, M, (float *)dst->data, (int64_t)(dst->nb[1] / 4), bias2,
                              MQ_PATH_GEMM, c->stream);
     }
     st = op_status(rc, mm1);

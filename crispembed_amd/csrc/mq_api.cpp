@@ -386,7 +386,9 @@ int mq_mul_mat_q_requant(int type, const void *w_image, int64_t n, int64_t k, co
                          void *stream) {
     int rc = check_weight_shape(type, n, k);
     if (rc) return rc;
-    if (out_type != MQ_TYPE_Q8_0) return fail(MQ_EUNSUPPORTED, "mq_mul_mat_q_requant: the output type must be Q8_0");
+    const bool q8k = out_type == MQ_TYPE_Q4_K || out_type == MQ_TYPE_Q6_K;
+    if (out_type != MQ_TYPE_Q8_0 && !q8k)
+        return fail(MQ_EUNSUPPORTED, "mq_mul_mat_q_requant: the output type must be Q8_0, Q4_K or Q6_K");
     if (op != MQ_PRE_NONE && op != MQ_PRE_GELU_ERF)
         return fail(MQ_EINVAL, "mq_mul_mat_q_requant: op must be MQ_PRE_NONE or MQ_PRE_GELU_ERF");
     if (n % KSTAGE != 0) return fail(MQ_EINVAL, "mq_mul_mat_q_requant: n must be a multiple of %d", KSTAGE);
@@ -395,13 +397,25 @@ int mq_mul_mat_q_requant(int type, const void *w_image, int64_t n, int64_t k, co
     if (!is_aligned(w_image, 256) || !is_aligned(workspace, 256) || !is_aligned(out_workspace, 256))
         return fail(MQ_EINVAL, "mq_mul_mat_q_requant: weight image and workspaces must be 256-byte aligned");
     if (m == 0) return MQ_OK;
-    const size_t need = act_planes(MQ_TYPE_Q8_0, m, n, true).total;
+    if (q8k && !gemm_requant_q8k_fits(type, m, n))
+        return fail(MQ_EUNSUPPORTED,
+                    "mq_mul_mat_q_requant: Q8_K output needs Q4_K/Q6_K weights, n a multiple of 256 and >= 256 "
+                    "workgroups of 128 x 256 (type %d, m = %lld, n = %lld)",
+                    type, (long long)m, (long long)n);
+    const size_t need = act_planes(out_type, m, n, true).total;
     if (out_workspace_bytes < need)
         return fail(MQ_EINVAL, "mq_mul_mat_q_requant: output workspace of %zu bytes, %zu needed", out_workspace_bytes,
                     need);
-    const hipError_t e = launch_gemm_requant(type, w_image, n, k, workspace, m, bias, op, mq_q8_0_variant(),
+    const hipError_t e = launch_gemm_requant(type, w_image, n, k, workspace, m, bias, op, mq_q8_0_variant(), out_type,
                                              out_workspace, (hipStream_t)stream);
     return e == hipSuccess ? MQ_OK : hip_fail(e, "gemm");
+}
+
+int mq_mul_mat_q_requant_supported(int type, int out_type, int64_t m, int64_t n) {
+    if (!type_ok(type) || m <= 0 || m > INT32_MAX || n <= 0 || n % KSTAGE != 0) return 0;
+    if (out_type == MQ_TYPE_Q8_0) return 1;
+    if (out_type == MQ_TYPE_Q4_K || out_type == MQ_TYPE_Q6_K) return gemm_requant_q8k_fits(type, m, n) ? 1 : 0;
+    return 0;
 }
 
 int mq_mul_mat_q_swiglu(int type, const void *w_image, int64_t n_ff, int64_t k, const void *workspace, int64_t m,

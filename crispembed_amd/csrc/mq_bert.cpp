@@ -126,11 +126,13 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
     const int t = hp.wtype;
     const size_t f4 = sizeof(float);
     const size_t wsb = std::max({mq_workspace_bytes(t, rows, H), mq_workspace_bytes(t, rows, F)});
-    // Q8_0 FFN on the GEMM path: the FFN-up GEMM adds its bias, applies GELU-erf and quantizes its
-    // own output for the FFN-down GEMM (mq_mul_mat_q_requant), into the second workspace
-    const bool ffn_fused = t == MQ_TYPE_Q8_0 && F % 128 == 0 && mq_mul_mat_path(t, F, H, rows) == MQ_PATH_GEMM &&
-                           mq_mul_mat_path(t, H, F, rows) == MQ_PATH_GEMM;
-    const size_t wsb2 = ffn_fused ? mq_workspace_bytes(MQ_TYPE_Q8_0, rows, F) : 0;
+    // FFN on the GEMM path: the FFN-up GEMM adds its bias, applies GELU-erf and quantizes its
+    // own output for the FFN-down GEMM (mq_mul_mat_q_requant: Q8_0, or Q8_K for the K-quants at
+    // the sizes its 128 x 256 tiles fill the GPU), into the second workspace
+    const bool kquant = t == MQ_TYPE_Q4_K || t == MQ_TYPE_Q6_K;
+    const bool ffn_fused = ((t == MQ_TYPE_Q8_0 && F % 128 == 0) || (kquant && gemm_requant_q8k_fits(t, rows, F))) &&
+                           mq_mul_mat_path(t, F, H, rows) == MQ_PATH_GEMM && mq_mul_mat_path(t, H, F, rows) == MQ_PATH_GEMM;
+    const size_t wsb2 = ffn_fused ? mq_workspace_bytes(t, rows, F) : 0;
     if (!m->x.ensure(rows * H * f4) || !m->qkv.ensure(rows * 3 * H * f4) || !m->att.ensure(rows * H * f4) ||
         !m->y.ensure(rows * H * f4) || !m->ff.ensure(rows * F * f4) || !m->ws.ensure(wsb) ||
         (ffn_fused && !m->ws2.ensure(wsb2)))
@@ -153,7 +155,7 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
     // Attention there is the fragment attention of FLASH_ATTN_EXT on strided views of the qkv
     // rows (the q/k/v biases added by the qkv GEMM's store).
     const int hd = (int)(H / hp.n_head);
-    const bool norm_fused = ffn_fused && H % 128 == 0 && H <= 1024 && (hd == 32 || hd == 64 || hd == 128) &&
+    const bool norm_fused = t == MQ_TYPE_Q8_0 && ffn_fused && H % 128 == 0 && H <= 1024 && (hd == 32 || hd == 64 || hd == 128) &&
                             mq_mul_mat_path(t, 3 * H, H, rows) == MQ_PATH_GEMM &&
                             mq_mul_mat_path(t, H, H, rows) == MQ_PATH_GEMM;
     if (norm_fused) {
@@ -240,7 +242,7 @@ extern "C" int mq_bert_encode(mq_bert *m, const int32_t *ids, const int32_t *typ
             if ((rc = mq_quantize_act_ex(t, X, H, rows, H, nullptr, MQ_PRE_NONE, m->ws.p, m->ws.bytes, MQ_PATH_GEMM,
                                          s)) ||
                 (rc = mq_mul_mat_q_requant(t, L.fc1.img.p, L.fc1.n, L.fc1.k, m->ws.p, rows, L.b1.f(), MQ_PRE_GELU_ERF,
-                                           MQ_TYPE_Q8_0, m->ws2.p, m->ws2.bytes, s)) ||
+                                           t, m->ws2.p, m->ws2.bytes, s)) ||
                 (rc = mq_mul_mat_q(t, L.fc2.img.p, L.fc2.n, L.fc2.k, m->ws2.p, rows, m->y.f(), L.fc2.n, MQ_PATH_GEMM,
                                    s)))
                 return rc;

@@ -42,6 +42,7 @@
 // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 #include "mq_internal.h"
 #include "mq_act.h"
+#include "mq_q8k.h"
 
 #include <climits>
 #include <type_traits>
@@ -69,13 +70,16 @@ struct GemmArgs {
     const _Float16 *wmin;   // Q4_K: weight min-term fragments
     float *y;
     const float *bias;  // NULL, or N floats added to every row in the store
-    // quantized output (qo not NULL, one weight group): v = op(acc + bias) is stored as the Q8_0
-    // activation of a following mat-mul in its GEMM layout -- quants tiled [q_m_pad][32 q_kch],
-    // scales [q_kch][q_m_pad] -- instead of as floats in y; q_pre is MQ_PRE_NONE or
-    // MQ_PRE_GELU_ERF, q_var the Q8_0 rounding variant
+    // quantized output (qo not NULL, one weight group): v = op(acc + bias) is stored as the
+    // activation of a following mat-mul in its GEMM layout instead of as floats in y; q_pre is
+    // MQ_PRE_NONE or MQ_PRE_GELU_ERF.  q_fmt 0: Q8_0 (quants tiled [q_m_pad][32 q_kch], scales
+    // [q_kch][q_m_pad], q_var the rounding variant); q_fmt 1: Q8_K (quants tiled, scales
+    // [q_ncb][q_m_pad], min-term fragments qmin [q_m_pad / 32][q_ncb]; needs BN = 256, a
+    // workgroup owning whole 256-value superblocks of its rows)
     int8_t *qo;
     float *qd;
-    int q_m_pad, q_kch, q_pre, q_var;
+    _Float16 *qmin;
+    int q_m_pad, q_kch, q_pre, q_var, q_fmt, q_ncb;
     // attention K/V as MFMA operand fragments (kvf not NULL, one weight group): output columns
     // [kv_col0, kv_col0 + kv_nkv kv_hd) are K, the next kv_nkv kv_hd columns V, row b kv_T + key
     // (kv_T a multiple of 32).  They leave split hi / lo in the attention's fragment layout
@@ -141,7 +145,11 @@ struct Cfg {
     // the quantized-output and K-fragment epilogues stage a 32 x 36-float tile per wave in the
     // same memory once the ring is drained
     static constexpr int LDS_STG = NW * 32 * 36 * 4;
-    static constexpr int LDS = LDS_RING > LDS_STG ? LDS_RING : LDS_STG;
+    // the Q8_K-output epilogue (BN = 256) stages the whole BM x 256 fp32 tile, then the tile's
+    // min-term fragments and row scales
+    static constexpr int LDS_Q8K = BN == 256 ? BM * 1024 + (BM / 32) * 1024 + BM * 4 : 0;
+    static constexpr int LDS_E = LDS_STG > LDS_Q8K ? LDS_STG : LDS_Q8K;
+    static constexpr int LDS = LDS_RING > LDS_E ? LDS_RING : LDS_E;
     // DMAs issued per stage by every wave, and the count still in flight when stage
     // position q (of a superblock) may be computed: those of the D-1 later stages.
     static constexpr int dmas(int stage_pos) { return IPW + ((limbs && stage_pos % SPB == 0) ? EPW : 0); }
@@ -608,6 +616,70 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
         return;
     }
 
+    if (a.qo && a.q_fmt == 1) {
+        // Q8_K output: the workgroup's BN = 256 columns are one superblock of the next product's
+        // K, so every row's Q8_K block is formed here.  The waves stage the BM x 256 tile in LDS
+        // as op(acc + bias) (rows past M as zeros, the activation quantizer's pad rows), then
+        // each wave quantizes RQ rows as k_quantize_tiled<TQ_Q8_K> does (q8_K_rows: the same
+        // bytes), storing its 4 quants per lane and row in place in the fragments; the min-term
+        // fragments and scales leave from LDS at the end.
+        if constexpr (C::BN == 256 && C::BM % C::NW == 0 && 32 % (C::BM / C::NW) == 0 && (C::BM / C::NW) % 8 == 0) {
+            constexpr int RQ = C::BM / C::NW, NTL = C::BM / 32;  // rows per wave, 32-row tiles
+            static_assert(C::LDS_Q8K <= C::LDS, "Q8_K staging fits");
+            float *stg = (float *)smem;                                  // [BM][256]
+            _Float16 *msh = (_Float16 *)(smem + C::BM * 1024);           // [NTL][512]
+            float *dsh = (float *)(smem + C::BM * 1024 + NTL * 1024);    // [BM]
+            const int kb = n0 >> 8;  // the superblock along the next product's K
+            __syncthreads();         // every wave past its last stage: the ring is free
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int rr = 0; rr < 16; rr++) {
+                        const int rl = (wm * TM + i) * 32 + 8 * (rr >> 2) + 4 * lhalf + (rr & 3);
+                        float x = acc[i][j][rr];
+                        if (a.q_pre == MQ_PRE_GELU_ERF) x = gelu_erf_f32(x);
+                        stg[rl * 256 + (wn * TN + j) * 32 + lrow] = m0 + rl < a.M ? x : 0.f;
+                    }
+            __syncthreads();
+            const int rl0 = wave * RQ, tl = rl0 >> 5, rt = (m0 >> 5) + tl;  // the wave's rows: one tile
+            const int c = lane >> 3, cbyte = (4 * lane) & 31;
+            int8_t *qdst = a.qo + (((int64_t)rt * a.q_kch + kb * 8 + c) << 10) + (32 * (cbyte >> 4) << 4) + (cbyte & 15);
+            const bool live = rt * 32 < a.q_m_pad;  // uniform
+#pragma unroll
+            for (int r8 = 0; r8 < RQ; r8 += 8) {
+                float4 v[8];
+                uint32_t q[8];
+                int bs[8];
+                float d[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = *(const float4 *)(stg + (rl0 + r8 + i) * 256 + 4 * lane);
+                q8_K_rows<8>(v, lane, q, bs, d);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int r = (rl0 + r8 + i) & 31;  // row within the tile
+                    if (live) *(uint32_t *)(qdst + (r << 4)) = q[i];
+                    if (lane == 0) dsh[rl0 + r8 + i] = d[i];
+                    if ((lane & 7) == 0) {
+                        const int jj = lane >> 3;
+                        msh[tl * 512 + (r << 3) + jj] = (_Float16)(bs[i] & 63);
+                        msh[tl * 512 + ((32 + r) << 3) + jj] = (_Float16)((bs[i] >> 6) * 64);
+                    }
+                }
+            }
+            __syncthreads();
+            const int t = threadIdx.x;
+            if (t < C::BM && m0 + t < a.q_m_pad) a.qd[(int64_t)kb * a.q_m_pad + m0 + t] = dsh[t];
+            if (t < NTL * 64) {
+                const int tt = t >> 6, rtt = (m0 >> 5) + tt;
+                if (rtt * 32 < a.q_m_pad)
+                    ((int4 *)(a.qmin + (((int64_t)rtt * a.q_ncb + kb) << 9)))[t & 63] = ((const int4 *)(msh + tt * 512))[t & 63];
+            }
+        }
+        return;
+    }
+
     if (a.qo) {
         // Quantized output.  Each wave stages a 32x32 tile in LDS (the stage ring is free once
         // every wave is past its last stage), then lane l takes row l % 32, values
@@ -751,6 +823,7 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
 //   7: 4 waves x (32x32)  WG 64x64
 //   8: as 7 with a 2-stage ring (one stage in flight): half the LDS, more workgroups per CU
 //   9: as 7 with a 3-stage ring (two in flight; Q8_0 and F16)
+//  11: 8 waves x (64x64)  WG 128x256, 32-byte K stages (K-quants; the Q8_K-output GEMM's tiles)
 static int gemm_cfg_env() {
     const char *e = getenv("MQ_GEMM_CFG");  // read per launch so a process can compare configurations
     return (e && *e) ? atoi(e) : 0;
@@ -761,7 +834,7 @@ static inline int64_t tiles(int64_t M, int64_t N, int bm, int bn) { return ((M +
 template <int FMT>
 static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
     int cfg = gemm_cfg_env();
-    if (cfg < 1 || cfg > 9 || cfg == 2 || (cfg == 6 && FMT != FMT_Q4_K && FMT != FMT_Q6_K) ||
+    if (cfg < 1 || cfg > 11 || cfg == 2 || cfg == 10 || (cfg == 11 && FMT != FMT_Q4_K && FMT != FMT_Q6_K) || (cfg == 6 && FMT != FMT_Q4_K && FMT != FMT_Q6_K) ||
         (cfg == 9 && FMT != FMT_Q8_0 && FMT != FMT_F16)) {
         // Small grids (under 512 tiles of 128x128): 64x64 workgroups of four 32x32 waves.
         // Every 32-deep K chunk costs a wave VALU work per output of its tile (the block
@@ -789,6 +862,11 @@ static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
         case 9:
             if constexpr (FMT == FMT_Q8_0 || FMT == FMT_F16) return launch_cfg<FMT, 2, 2, 1, 1, 2, 2, false, 3, 2>(a, s);
             return hipErrorInvalidValue;
+        case 11:
+            if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q6_K) return launch_cfg<FMT, 2, 4, 2, 2, 1, 1, false, 4, 3>(a, s);
+            return hipErrorInvalidValue;
+
+
         default: return launch_cfg<FMT, 1, 1, 2, 2, 2>(a, s);
     }
 }
@@ -922,11 +1000,25 @@ hipError_t launch_gemm_kv(int type, const void *image, int64_t n, int64_t k, con
     }
 }
 
+// Q8_K output: 128 x 256 workgroups (8 waves of 64 x 64, 32-byte K stages in a 4-stage ring),
+// a workgroup per 256-value superblock of the output rows; grids of at least one workgroup per
+// CU.  MI355X, Q4_K 8192 x 4096 x 1024 with GELU-erf: 144 us, against 110 us for the plain
+// 256 x 128 GEMM plus 37.5 us for the quantizer pass over its fp32 output (the epilogue's GELU
+// and quantization do not overlap MFMA work: one workgroup per CU; 64 x 256 tiles, two per CU,
+// measured 164 us).
+bool gemm_requant_q8k_fits(int type, int64_t m, int64_t n) {
+    return (type == MQ_TYPE_Q4_K || type == MQ_TYPE_Q6_K) && m > 0 && n > 0 && n % QK_K == 0 &&
+           tiles(m, n, 128, 256) >= 256 && n <= INT32_MAX;
+}
+
 hipError_t launch_gemm_requant(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m,
-                               const float *bias, int pre, int q8_0_variant, void *out_ws, hipStream_t s) {
+                               const float *bias, int pre, int q8_0_variant, int out_type, void *out_ws, hipStream_t s) {
     if (m <= 0 || n <= 0) return hipSuccess;
+    const bool q8k = out_type == MQ_TYPE_Q4_K || out_type == MQ_TYPE_Q6_K;
+    if (!q8k && out_type != MQ_TYPE_Q8_0) return hipErrorInvalidValue;
+    if (q8k && !gemm_requant_q8k_fits(type, m, n)) return hipErrorInvalidValue;
     if (n % KSTAGE != 0) return hipErrorInvalidValue;  // the output fills the next product's padded K
-    const ActPlanes ap = act_planes(type, m, k, true), op = act_planes(MQ_TYPE_Q8_0, m, n, true);
+    const ActPlanes ap = act_planes(type, m, k, true), op = act_planes(out_type, m, n, true);
     if (op.kb_pad != n || op.m_pad != ap.m_pad) return hipErrorInvalidValue;
     const WeightPlanes p = weight_planes(type, n, k);
     const uint8_t *xb = (const uint8_t *)ws, *wb = (const uint8_t *)image;
@@ -944,10 +1036,13 @@ hipError_t launch_gemm_requant(int type, const void *image, int64_t n, int64_t k
     a.bias = bias;
     a.qo = (int8_t *)(ob + op.xq);
     a.qd = (float *)(ob + op.xd);
+    a.qmin = q8k ? (_Float16 *)(ob + op.xmin) : nullptr;
     a.q_m_pad = (int)op.m_pad;
     a.q_kch = (int)(n / 32);
     a.q_pre = pre;
     a.q_var = q8_0_variant;
+    a.q_fmt = q8k ? 1 : 0;
+    a.q_ncb = (int)(n / QK_K);
     a.M = (int)m;
     a.N = (int)n;
     a.ldy = (int)n;
@@ -957,6 +1052,10 @@ hipError_t launch_gemm_requant(int type, const void *image, int64_t n, int64_t k
     a.nstages = (int)(p.kb_pad / 64);
     a.nsb = (int)(k / QK_K);
     a.ngroups = 1;
+    if (q8k) {
+        if (type == MQ_TYPE_Q4_K) return launch_cfg<FMT_Q4_K, 2, 4, 2, 2, 1, 1, false, 4, 3>(a, s);
+        return launch_cfg<FMT_Q6_K, 2, 4, 2, 2, 1, 1, false, 4, 3>(a, s);
+    }
     switch (type) {
         case MQ_TYPE_Q8_0: return launch_fmt<FMT_Q8_0>(a, s);
         case MQ_TYPE_Q4_K: return launch_fmt<FMT_Q4_K>(a, s);

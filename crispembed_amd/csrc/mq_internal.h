@@ -312,11 +312,14 @@ hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const 
                        int64_t ldy, hipStream_t s, const float *bias = nullptr);
 hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
                        int64_t ldy, hipStream_t s, const float *bias = nullptr);
-// the GEMM with its output v = pre(x w^T + bias) quantized to Q8_0 into out_ws, the GEMM-layout
-// activation workspace of a following mat-mul with k = n (n a multiple of KSTAGE); pre is
-// MQ_PRE_NONE or MQ_PRE_GELU_ERF.  ws must hold x in the tiled (GEMM) layout.
+// the GEMM with its output v = pre(x w^T + bias) quantized into out_ws, the GEMM-layout
+// activation workspace of a following mat-mul with k = n whose weights are out_type: Q8_0
+// (n a multiple of KSTAGE) or Q4_K / Q6_K (Q8_K activations: n a multiple of 256, this product's
+// weights Q4_K or Q6_K, shapes gemm_requant_q8k_fits accepts); pre is MQ_PRE_NONE or
+// MQ_PRE_GELU_ERF.  ws must hold x in the tiled (GEMM) layout.
+bool gemm_requant_q8k_fits(int type, int64_t m, int64_t n);
 hipError_t launch_gemm_requant(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m,
-                               const float *bias, int pre, int q8_0_variant, void *out_ws, hipStream_t s);
+                               const float *bias, int pre, int q8_0_variant, int out_type, void *out_ws, hipStream_t s);
 // the GEMM of a gated FFN's gate|up weight (2 n_ff rows: gate, then up) whose store forms
 // silu(gate) * up into y (m x n_ff, row stride ldy); only for shapes gemm_swiglu_fits accepts
 // (n_ff a multiple of 64, grids of the large-tile configurations)

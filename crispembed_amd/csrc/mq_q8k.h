@@ -81,14 +81,14 @@ __device__ __forceinline__ void q8_K_block_row(const float4 v, int lane, int r, 
     }
 }
 
-// q8_K_block_row for NR rows of a wave at once (row i's values in v[i], lane l holding values
-// 4l .. 4l + 3; its place in the fragment dst[i], its scale slot dslot[i], its tile row r[i]): the
-// same arithmetic, but the NR scales' two divisions (-127 / max and 1 / iscale, wave-uniform
-// values) run once for all rows -- row i's operand in lane i -- instead of once per row, which
-// was a quarter of the row's instructions.  Bit for bit q8_K_block_row's results.
+// q8_K_block_row's arithmetic for NR rows of a wave at once, without the stores (row i's values
+// in v[i], lane l holding values 4l .. 4l + 3): the lane's 4 quants of row i in q[i], B_j (the sum
+// of sub-block j's 32 quants) in lane 8j of bs[i], the scale 1 / iscale in d[i] (wave-uniform).
+// The NR scales' two divisions (-127 / max and 1 / iscale, wave-uniform values) run once for all
+// rows -- row i's operand in lane i -- instead of once per row, which was a quarter of the row's
+// instructions.  Bit for bit q8_K_block_row's results.
 template <int NR>
-__device__ __forceinline__ void q8_K_block_rows(const float4 *v, int lane, const int *r, int8_t *const *dst,
-                                                float *const *dslot, _Float16 *msh) {
+__device__ __forceinline__ void q8_K_rows(const float4 *v, int lane, uint32_t *q, int *bs, float *d) {
 #pragma clang fp contract(off)
     static_assert(NR >= 1 && NR <= 64, "rows per wave");
     float amax[NR], mx[NR];
@@ -127,13 +127,29 @@ __device__ __forceinline__ void q8_K_block_rows(const float4 *v, int lane, const
             }
             dval = lane_f(d_l, i);
         }
-        *(uint32_t *)dst[i] = packed;
-        if (lane == 0) *dslot[i] = dval;
-        const int B = sum8(s16);
+        q[i] = packed;
+        bs[i] = sum8(s16);
+        d[i] = dval;
+    }
+}
+
+// q8_K_rows with q8_K_block_row's stores: row i's place in the fragment dst[i], its scale slot
+// dslot[i], its tile row r[i].
+template <int NR>
+__device__ __forceinline__ void q8_K_block_rows(const float4 *v, int lane, const int *r, int8_t *const *dst,
+                                                float *const *dslot, _Float16 *msh) {
+    uint32_t q[NR];
+    int bs[NR];
+    float d[NR];
+    q8_K_rows<NR>(v, lane, q, bs, d);
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+        *(uint32_t *)dst[i] = q[i];
+        if (lane == 0) *dslot[i] = d[i];
         if ((lane & 7) == 0) {
             const int j = lane >> 3;
-            msh[(r[i] << 3) + j] = (_Float16)(B & 63);
-            msh[((32 + r[i]) << 3) + j] = (_Float16)((B >> 6) * 64);
+            msh[(r[i] << 3) + j] = (_Float16)(bs[i] & 63);
+            msh[((32 + r[i]) << 3) + j] = (_Float16)((bs[i] >> 6) * 64);
         }
     }
 }

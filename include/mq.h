@@ -214,17 +214,24 @@ int mq_mul_mat_gemv(int type, int n_groups, const void *const *w_images, const i
 
 /* Two mat-muls in a row without the fp32 tensor between them: computes
  * V = op(X W^T + bias) on the GEMM path (workspace: X quantized with path MQ_PATH_GEMM) and
- * writes V quantized to Q8_0 straight into out_workspace, in the layout that
- * mq_quantize_act_ex(MQ_TYPE_Q8_0, V, ..., MQ_PATH_GEMM) writes -- the same bytes, bit for
- * bit -- ready for mq_mul_mat_q_ex(MQ_TYPE_Q8_0, W2, n2, n, out_workspace, m, ..., MQ_PATH_GEMM).
- * V itself is never written.  This is the encoder FFN of src/crispembed.cpp:1410-1416 (FFN-up
- * MUL_MAT, bias ADD, ggml_gelu_erf, then the FFN-down MUL_MAT, whose CPU backend quantizes its
- * src1 through the Q8_0 from_float before the block dots).  out_type must be MQ_TYPE_Q8_0, op
- * MQ_PRE_NONE or MQ_PRE_GELU_ERF, n a multiple of 128; out_workspace_bytes >=
- * mq_workspace_bytes(MQ_TYPE_Q8_0, m, n). */
+ * writes V quantized for the next product's weights, of type out_type, straight into
+ * out_workspace, in the layout that mq_quantize_act_ex(out_type, V, ..., MQ_PATH_GEMM) writes --
+ * the same bytes, bit for bit -- ready for mq_mul_mat_q_ex(out_type, W2, n2, n, out_workspace, m,
+ * ..., MQ_PATH_GEMM).  V itself is never written.  This is the encoder FFN of
+ * src/crispembed.cpp:1410-1416 (FFN-up MUL_MAT, bias ADD, ggml_gelu_erf, then the FFN-down
+ * MUL_MAT, whose CPU backend quantizes its src1 through the vec_dot_type's from_float before the
+ * block dots).  out_type MQ_TYPE_Q8_0 (Q8_0 activations): n a multiple of 128.  out_type
+ * MQ_TYPE_Q4_K or MQ_TYPE_Q6_K (Q8_K activations): type Q4_K or Q6_K, n a multiple of 256 and
+ * a product of at least 256 workgroups of 128 x 256 (MQ_EUNSUPPORTED otherwise: use
+ * mq_mul_mat_q_ex and mq_quantize_act_ex).  op MQ_PRE_NONE or MQ_PRE_GELU_ERF;
+ * out_workspace_bytes >= mq_workspace_bytes(out_type, m, n). */
 int mq_mul_mat_q_requant(int type, const void *w_image, int64_t n, int64_t k, const void *workspace, int64_t m,
                          const float *bias, int op, int out_type, void *out_workspace, size_t out_workspace_bytes,
                          void *stream);
+
+/* 1 when mq_mul_mat_q_requant(type, ..., n, k, ..., m, ..., out_type, ...) runs (the shape and type
+ * rules above; k and the workspaces aside), else 0.  No GPU call. */
+int mq_mul_mat_q_requant_supported(int type, int out_type, int64_t m, int64_t n);
 
 /* The gate and up projections of a gated FFN and the product between them, as one GEMM: w_image
  * holds 2 n_ff rows (the gate weight's n_ff rows, then the up weight's: the gate|up product of

@@ -54,6 +54,16 @@ def test_host_only_entry_points_without_gpu():
     assert rq(mq.TYPE_Q8_0, 256, 1536, 384, 256, 4096, None, 2, mq.TYPE_Q8_0, 256, 1 << 30, None) == -1
     assert rq(mq.TYPE_Q8_0, 256, 1536, 384, 256, 4096, None, 1, mq.TYPE_Q8_0, 256, 1024, None) == -1
     assert b"output workspace" in L.mq_last_error()
+    # Q8_K output (a K-quant next product): K-quant weights, n a multiple of 256, >= 256 workgroups
+    # of 128 x 256 -- else unsupported, with the same answer from the query
+    sup = L.mq_mul_mat_q_requant_supported
+    assert sup(mq.TYPE_Q4_K, mq.TYPE_Q4_K, 8192, 4096) == 1 and sup(mq.TYPE_Q6_K, mq.TYPE_Q4_K, 2048, 4096) == 1
+    assert sup(mq.TYPE_Q8_0, mq.TYPE_Q8_0, 4096, 1536) == 1
+    assert sup(mq.TYPE_Q8_0, mq.TYPE_Q4_K, 8192, 4096) == 0  # Q8_0 weights: Q8_0 output only
+    assert sup(mq.TYPE_Q4_K, mq.TYPE_Q4_K, 512, 4096) == 0   # 64 workgroups
+    assert sup(mq.TYPE_Q4_K, mq.TYPE_Q4_K, 8192, 4224) == 0  # not whole superblocks
+    assert rq(mq.TYPE_Q4_K, 256, 4096, 1024, 256, 512, None, 1, mq.TYPE_Q4_K, 256, 1 << 30, None) == -2
+    assert b"Q8_K output" in L.mq_last_error()
 
 
 def test_op_support_checks_without_gpu():

@@ -316,3 +316,63 @@ def test_requant_against_oracle(oracle, wtype, op, m, k, n):
     total = AL.planes(O.Q8_0, m, n)["total"]
     _assert_live(host(ws)[off:off + total], AL.oracle_image(oracle, O.Q8_0, host(v)), O.Q8_0, m, n)
     del img
+
+
+@pytest.mark.parametrize("wtype,out_type,op,m,k,n", [
+    (O.Q4_K, O.Q4_K, 1, 8192, 1024, 4096),  # the XLM-R-large / BGE-M3 FFN-up at 8192 tokens
+    (O.Q4_K, O.Q4_K, 0, 2048, 1024, 4096),
+    (O.Q6_K, O.Q6_K, 1, 2048, 512, 4096),
+    (O.Q4_K, O.Q6_K, 1, 1060, 512, 8192),   # ragged rows: a last 128-row tile past m_pad
+    (O.Q6_K, O.Q4_K, 0, 1060, 256, 8192),
+])
+def test_requant_q8_k_against_oracle(oracle, wtype, out_type, op, m, k, n):
+    """mq_mul_mat_q_requant with a K-quant next product (the FFN-up GEMM storing gelu_erf(y + bias)
+    as the FFN-down GEMM's Q8_K activation from its 128 x 256 workgroups, y never written): the
+    quants, scales and min-term fragments of every live row equal the oracle's quantize_row_q8_K
+    of op(y + bias), y the plain GEMM's fp32 output; and the FFN-down product reads the same
+    result from it as from the separate quantizer's workspace."""
+    import torch
+    mq = _mq()
+    L = mq.lib()
+    assert L.mq_mul_mat_q_requant_supported(wtype, out_type, m, n) == 1
+    rng = np.random.default_rng(m + n + op + 10 * wtype)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    img = weight_image(wtype, oracle.quantize_chunk(wtype, w), n, k)
+    x = dev(rng.standard_normal((m, k)).astype(np.float32))
+    nb1 = L.mq_workspace_bytes(wtype, m, k)
+    ws1, o1 = empty_u8(nb1)
+    p1 = ctypes.c_void_p(ws1.data_ptr() + o1)
+    mq.check(L.mq_quantize_act(wtype, ctypes.c_void_p(x.data_ptr()), k, m, k, p1, nb1, mq.PATH_GEMM, stream()))
+    bias = rng.standard_normal(n).astype(np.float32)
+    bd = dev(bias)
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    mq.check(L.mq_mul_mat_q_ex(wtype, ctypes.c_void_p(img[1]), n, k, p1, m, ctypes.c_void_p(y.data_ptr()), n,
+                               ctypes.c_void_p(bd.data_ptr()), mq.PATH_GEMM, stream()))
+    v = y
+    if op == 1:
+        v = torch.empty_like(y)
+        mq.check(L.mq_op_unary(mq.UNARY_GELU_ERF, mq.view(y), mq.view(v), stream()))
+    nb = L.mq_workspace_bytes(out_type, m, n)
+    ws, off = empty_u8(nb)
+    ws.fill_(0xAB)
+    pw = ctypes.c_void_p(ws.data_ptr() + off)
+    mq.check(L.mq_mul_mat_q_requant(wtype, ctypes.c_void_p(img[1]), n, k, p1, m, ctypes.c_void_p(bd.data_ptr()), op,
+                                    out_type, pw, nb, stream()))
+    total = AL.planes(out_type, m, n)["total"]
+    vh = host(v)
+    del y, v
+    _assert_live(host(ws)[off:off + total], AL.oracle_image(oracle, out_type, vh), out_type, m, n)
+    # the next product (n2 = 256 features) from the fused and from the separate quantizer's workspace
+    n2 = 256
+    w2 = (rng.standard_normal((n2, n)) * 0.02).astype(np.float32)
+    img2 = weight_image(out_type, oracle.quantize_chunk(out_type, w2), n2, n)
+    ws3, o3 = empty_u8(nb)
+    p3 = ctypes.c_void_p(ws3.data_ptr() + o3)
+    vd = dev(vh)
+    mq.check(L.mq_quantize_act(out_type, ctypes.c_void_p(vd.data_ptr()), n, m, n, p3, nb, mq.PATH_GEMM, stream()))
+    z = [torch.full((m, n2), np.nan, dtype=torch.float32, device="cuda") for _ in range(2)]
+    for t, p in zip(z, (pw, p3)):
+        mq.check(L.mq_mul_mat_q_ex(out_type, ctypes.c_void_p(img2[1]), n2, n, p, m, ctypes.c_void_p(t.data_ptr()), n2,
+                                   None, mq.PATH_GEMM, stream()))
+    assert np.array_equal(host(z[0]), host(z[1]))
+    del img, img2
