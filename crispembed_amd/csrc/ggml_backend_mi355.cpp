@@ -1308,14 +1308,25 @@ enum ggml_status compute_node(BackendCtx *c, ggml_tensor *node) {
             return op_status(mq_op_repeat(&x, &d, c->stream), node);
         }
         case GGML_OP_MUL_MAT_ID: {
+            // routed on the device (no stream sync, capturable); MQ_GGML_MOE_HOST=1: the ids read
+            // back to the host and one product per used expert
             const ggml_tensor *as = node->src[0];
             const mq_view b = view_of(node->src[1]), ids = view_of(node->src[2]), d = view_of(node);
-            const int mt = mq_type_of(as->type);
+            const int mt = mq_type_of(as->type), n_exp = (int)as->ne[2];
+            const int64_t rows = ids.ne[0] * ids.ne[1];
             c->ws_x = nullptr;
-            if (!ensure_ws(c, mq_op_mul_mat_id_workspace_bytes(mt, as->ne[1], as->ne[0], ids.ne[0] * ids.ne[1])))
+            const char *he = std::getenv("MQ_GGML_MOE_HOST");
+            if (!(he && std::atoi(he) != 0) && n_exp <= 1024) {  // the device routing's limit
+                if (!ensure_ws(c, mq_op_mul_mat_id_device_workspace_bytes(mt, n_exp, as->ne[1], as->ne[0], rows)))
+                    return GGML_STATUS_ALLOC_FAILED;
+                return op_status(mq_op_mul_mat_id_device(mt, as->data, image_bytes(as), n_exp, as->ne[1], as->ne[0], &b,
+                                                         &ids, &d, c->ws, c->ws_bytes, c->stream),
+                                 node);
+            }
+            if (!ensure_ws(c, mq_op_mul_mat_id_workspace_bytes(mt, as->ne[1], as->ne[0], rows)))
                 return GGML_STATUS_ALLOC_FAILED;
-            return op_status(mq_op_mul_mat_id(mt, as->data, image_bytes(as), (int)as->ne[2], as->ne[1], as->ne[0], &b,
-                                              &ids, &d, c->ws, c->ws_bytes, c->stream),
+            return op_status(mq_op_mul_mat_id(mt, as->data, image_bytes(as), n_exp, as->ne[1], as->ne[0], &b, &ids, &d,
+                                              c->ws, c->ws_bytes, c->stream),
                              node);
         }
         case GGML_OP_ROPE: {
@@ -1446,7 +1457,7 @@ uint64_t graph_key(ggml_cgraph *cg) {
     }
     for (const char *k : {"MQ_GGML_NO_FUSION", "MQ_GEMM_CFG", "MQ_ATTN_SPLIT", "MQ_GEMV_WGS", "MQ_GEMV_PF",
                           "MQ_FORCE_GEMV_MAX_M", "MQ_Q8_0_VARIANT", "MQ_GGML_NO_MASK_BLOCKS", "MQ_ATTN_SPLIT_WAVES",
-                          "MQ_GGML_NO_MASK_SEGMENTS"}) {
+                          "MQ_GGML_NO_MASK_SEGMENTS", "MQ_GGML_MOE_HOST"}) {
         const char *v = std::getenv(k);
         if (v) mix(v, std::strlen(v));
         mix("|", 1);

@@ -87,6 +87,12 @@ struct GemmArgs {
     // the columns before kv_col0 are stored as usual.
     _Float16 *kvf;
     int kv_col0, kv_T, kv_hd, kv_nkv, kv_nblk;
+    // mixture of experts (moe not NULL, one weight group): the rows are sorted by expert in
+    // segments of whole BM-row tiles; moe[0] = the number of live row tiles, moe[1 + tm] = the
+    // expert of row tile tm, whose weight planes lie moe_stride bytes past the previous
+    // expert's (row tiles from moe[0] on are skipped)
+    const int *moe;
+    int64_t moe_stride;
     int M, N, ldy;
     int m_pad, n_pad;
     int kch;      // 32-byte K chunks per row (kb_pad / 32)
@@ -345,6 +351,15 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
             a.y = G.y, a.bias = G.bias, a.N = G.N, a.n_pad = G.n_pad, a.ldy = G.ldy, a.kv_col0 = G.kv_col0;
             tn -= a0.tn_start[g];
         }
+    }
+    if (a0.moe) {
+        if (tm >= a0.moe[0]) return;  // uniform: before any DMA or barrier
+        const int64_t off = (int64_t)a0.moe[1 + tm] * a0.moe_stride;
+        a.wq += off;
+        if (a.whi) a.whi += off;
+        a.wd = (const float *)((const char *)a.wd + off);
+        if (a.wdmin) a.wdmin = (const float *)((const char *)a.wdmin + off);
+        if (a.wmin) a.wmin = (const _Float16 *)((const char *)a.wmin + off);
     }
     const int m0 = tm * C::BM, n0 = tn * C::BN;
     const int nst = a.nstages;
@@ -957,6 +972,53 @@ static hipError_t gemm_group_kv(int type, int ngroups, const void *const *images
 hipError_t launch_gemm(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,
                        int64_t ldy, hipStream_t s, const float *bias) {
     return launch_gemm_group(type, 1, &image, &n, k, ws, m, &y, &ldy, &bias, s);
+}
+
+// The experts' GEMM of a device-routed MUL_MAT_ID: rows sorted by expert in segments of whole
+// moe_tile_rows-row tiles (x quantized in the tiled layout for m_rows rows), the tile table in
+// moe (moe[0] live tiles, moe[1 + t] the expert of tile t), expert e's weight image at
+// images + e * stride.  moe_tile_rows 256: the 256 x 128 workgroups; 64: 64 x 64.
+int gemm_moe_tile_rows(int64_t rows, int64_t n, int n_used_experts) {
+    return (rows >= (int64_t)1024 * n_used_experts && tiles(rows, n, 256, 128) >= 256) ? 256 : 64;
+}
+
+hipError_t launch_gemm_moe(int type, const void *images, size_t stride, int64_t n, int64_t k, const void *ws,
+                           int64_t m_rows, int tile_rows, const int *moe, float *y, hipStream_t s) {
+    if (m_rows <= 0 || n <= 0) return hipSuccess;
+    if (m_rows % tile_rows || (tile_rows != 64 && tile_rows != 256) || stride % 256) return hipErrorInvalidValue;
+    const ActPlanes ap = act_planes(type, m_rows, k, true);
+    const WeightPlanes p = weight_planes(type, n, k);
+    const uint8_t *xb = (const uint8_t *)ws, *wb = (const uint8_t *)images;
+    GemmArgs a{};
+    a.xq = (const int8_t *)(xb + ap.xq);
+    a.xd = (const float *)(xb + ap.xd);
+    a.xmin = (const _Float16 *)(xb + ap.xmin);
+    a.wq = (const int8_t *)(wb + p.tq);
+    a.whi = (const int8_t *)(wb + p.thi);
+    a.wd = (const float *)(wb + p.tdw);
+    a.wdmin = (const float *)(wb + p.tdmin);
+    a.wmin = (const _Float16 *)(wb + p.tmin);
+    a.y = y;
+    a.moe = moe;
+    a.moe_stride = (int64_t)stride;
+    a.M = (int)m_rows;
+    a.N = (int)n;
+    a.ldy = (int)n;
+    a.m_pad = (int)ap.m_pad;
+    a.n_pad = (int)p.n_pad;
+    a.kch = (int)(p.kb_pad / 32);
+    a.nstages = (int)(p.kb_pad / 64);
+    a.nsb = (int)(k / QK_K);
+    a.ngroups = 1;
+    const bool big = tile_rows == 256;
+    switch (type) {
+        case MQ_TYPE_Q8_0:
+            return big ? launch_cfg<FMT_Q8_0, 4, 2, 2, 2, 1>(a, s) : launch_cfg<FMT_Q8_0, 2, 2, 1, 1, 2, 2, false, 2, 1>(a, s);
+        case MQ_TYPE_Q4_K: return big ? launch_cfg<FMT_Q4_K, 4, 2, 2, 2, 1>(a, s) : launch_cfg<FMT_Q4_K, 2, 2, 1, 1, 2>(a, s);
+        case MQ_TYPE_Q6_K: return big ? launch_cfg<FMT_Q6_K, 4, 2, 2, 2, 1>(a, s) : launch_cfg<FMT_Q6_K, 2, 2, 1, 1, 2>(a, s);
+        case MQ_TYPE_F16: return big ? launch_cfg<FMT_F16, 4, 2, 2, 2, 1>(a, s) : launch_cfg<FMT_F16, 2, 2, 1, 1, 2>(a, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gemm_kv(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m, float *y,

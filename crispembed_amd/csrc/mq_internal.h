@@ -318,6 +318,13 @@ hipError_t launch_gemv(int type, const void *image, int64_t n, int64_t k, const 
 // weights Q4_K or Q6_K, shapes gemm_requant_q8k_fits accepts); pre is MQ_PRE_NONE or
 // MQ_PRE_GELU_ERF.  ws must hold x in the tiled (GEMM) layout.
 bool gemm_requant_q8k_fits(int type, int64_t m, int64_t n);
+// the experts' GEMM of a device-routed MUL_MAT_ID: x (m_rows rows, tiled) sorted by expert in
+// segments of whole tile_rows-row tiles; moe[0] = live tiles, moe[1 + t] = expert of tile t;
+// expert e's prepared weight image at images + e * stride; y gets m_rows x n floats.
+// gemm_moe_tile_rows picks tile_rows (64 or 256) for rows sorted rows over n_used_experts.
+int gemm_moe_tile_rows(int64_t rows, int64_t n, int n_used_experts);
+hipError_t launch_gemm_moe(int type, const void *images, size_t stride, int64_t n, int64_t k, const void *ws,
+                           int64_t m_rows, int tile_rows, const int *moe, float *y, hipStream_t s);
 hipError_t launch_gemm_requant(int type, const void *image, int64_t n, int64_t k, const void *ws, int64_t m,
                                const float *bias, int pre, int q8_0_variant, int out_type, void *out_ws, hipStream_t s);
 // the GEMM of a gated FFN's gate|up weight (2 n_ff rows: gate, then up) whose store forms

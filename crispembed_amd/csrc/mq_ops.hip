@@ -562,6 +562,83 @@ __global__ __launch_bounds__(256) void k_scatter_rows(const float *__restrict__ 
     for (int64_t c = threadIdx.x; c < n; c += 256) d[c] = s[c];
 }
 
+// Device-side routing of a mixture-of-experts mat-mul (one workgroup): slot s = (token t, slot i)
+// of ids [n_used, T] goes to expert e = ids[i, t].  The experts' rows are laid out by expert in
+// segments of whole `tile`-row tiles (segment e starts where segment e - 1's tiles end), so
+// that every row tile of the sorted activation belongs to one expert; tiles[0] receives the
+// number of live tiles, tiles[1 + j] the expert of tile j.  src_off / dst_off receive each sorted
+// row's byte offset in b and dst (-1: a pad row); the order of an expert's rows follows the
+// order in which the slots reach the counter (rows are independent).  A slot whose id lies
+// outside [0, n_exp) has no sorted row: its dst row is filled with NaN here.
+constexpr int MOE_MAX_EXPERTS = 1024;
+__global__ __launch_bounds__(1024) void k_moe_route(const char *__restrict__ ids, int64_t ids_nb1, int n_used, int64_t T,
+                                                    int n_exp, int64_t b_ne1, int64_t b_nb1, int64_t b_nb2,
+                                                    int64_t d_nb1, int64_t d_nb2, int tile, int64_t rmax,
+                                                    int64_t *__restrict__ src_off, int64_t *__restrict__ dst_off,
+                                                    int *__restrict__ tiles, char *__restrict__ dst, int64_t n) {
+    __shared__ int cnt[MOE_MAX_EXPERTS], start[MOE_MAX_EXPERTS], fill[MOE_MAX_EXPERTS];
+    const int tid = threadIdx.x;
+    const int64_t R = (int64_t)n_used * T;
+    for (int e = tid; e < n_exp; e += 1024) cnt[e] = 0, fill[e] = 0;
+    for (int64_t r = tid; r < rmax; r += 1024) src_off[r] = -1, dst_off[r] = -1;
+    __syncthreads();
+    for (int64_t sl = tid; sl < R; sl += 1024) {
+        const int64_t t = sl / n_used, i = sl - t * n_used;
+        const int e = *(const int *)(ids + t * ids_nb1 + i * 4);
+        if (e >= 0 && e < n_exp) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int64_t run = 0;
+        for (int e = 0; e < n_exp; e++) {
+            start[e] = (int)run;
+            const int nt = (cnt[e] + tile - 1) / tile;
+            for (int j = 0; j < nt; j++) tiles[1 + run / tile + j] = e;
+            run += (int64_t)nt * tile;
+        }
+        tiles[0] = (int)(run / tile);
+    }
+    __syncthreads();
+    for (int64_t sl = tid; sl < R; sl += 1024) {
+        const int64_t t = sl / n_used, i = sl - t * n_used;
+        const int e = *(const int *)(ids + t * ids_nb1 + i * 4);
+        const int64_t doff = i * d_nb1 + t * d_nb2;
+        if (e >= 0 && e < n_exp) {
+            const int64_t r = start[e] + atomicAdd(&fill[e], 1);
+            src_off[r] = (i % b_ne1) * b_nb1 + t * b_nb2;
+            dst_off[r] = doff;
+        } else {
+            float *d = (float *)(dst + doff);
+            for (int64_t c = 0; c < n; c++) d[c] = __builtin_nanf("");
+        }
+    }
+}
+
+// the sorted rows: row r copied from src + off[r] (zeros for a pad row, off[r] < 0)
+__global__ __launch_bounds__(256) void k_gather_rows_pad(const char *__restrict__ src, const int64_t *__restrict__ off,
+                                                         float *__restrict__ dst, int64_t k) {
+    const int64_t r = blockIdx.x;
+    const int64_t o = off[r];
+    float4 *d = (float4 *)(dst + r * k);
+    if (o < 0) {
+        for (int64_t c = threadIdx.x; c < k / 4; c += 256) d[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        return;
+    }
+    const float4 *sp = (const float4 *)(src + o);
+    for (int64_t c = threadIdx.x; c < k / 4; c += 256) d[c] = sp[c];
+}
+
+// the results back to their slots (pad rows, off[r] < 0, stay)
+__global__ __launch_bounds__(256) void k_scatter_rows_pad(const float *__restrict__ src, const int64_t *__restrict__ off,
+                                                          char *__restrict__ dst, int64_t n) {
+    const int64_t r = blockIdx.x;
+    const int64_t o = off[r];
+    if (o < 0) return;
+    const float *sp = src + r * n;
+    float *d = (float *)(dst + o);
+    for (int64_t c = threadIdx.x; c < n; c += 256) d[c] = sp[c];
+}
+
 // Softmax over ne0, one wave per row (values re-read from memory; rows are short here).
 template <int MT>  // mask element type: 0 none, 1 F16, 2 F32
 __global__ __launch_bounds__(256) void k_soft_max(const DV x, const DV m, const DV d, float scale, int64_t nrows) {
@@ -1203,6 +1280,87 @@ extern "C" int mq_op_mul_mat_id(int type, const void *expert_images, size_t expe
     }
     hipLaunchKernelGGL(k_scatter_rows, dim3((unsigned)R), dim3(256), 0, s, Y, (const int64_t *)(ws + w.dst_off),
                        (char *)dst->data, n);
+    return hip_rc(hipGetLastError(), "mul_mat_id");
+}
+
+// workspace of the device-routed mixture-of-experts mat-mul: the sorted rows (rmax: every
+// expert's segment padded to whole tiles), their results, the two offset lists, the tile table
+// and the activation quantization of the sorted rows (tiled)
+struct MoeDevWs {
+    int tile;
+    int64_t rmax;
+    size_t x, y, src_off, dst_off, tiles, q, total;
+};
+static MoeDevWs moe_dev_ws(int type, int n_exp, int64_t n, int64_t k, int64_t rows) {
+    MoeDevWs w;
+    w.tile = gemm_moe_tile_rows(rows, n, (int)std::min<int64_t>(n_exp, rows));
+    w.rmax = pad_up(rows + std::min<int64_t>(n_exp, rows) * (w.tile - 1), w.tile);
+    size_t o = 0;
+    auto take = [&](size_t b) {
+        const size_t at = o;
+        o = align256(o + b);
+        return at;
+    };
+    w.x = take((size_t)w.rmax * k * 4);
+    w.y = take((size_t)w.rmax * n * 4);
+    w.src_off = take((size_t)w.rmax * 8);
+    w.dst_off = take((size_t)w.rmax * 8);
+    w.tiles = take((size_t)(1 + w.rmax / w.tile) * 4);
+    w.q = take(mq_workspace_bytes(type, w.rmax, k));
+    w.total = o;
+    return w;
+}
+
+extern "C" size_t mq_op_mul_mat_id_device_workspace_bytes(int type, int n_exp, int64_t n, int64_t k, int64_t rows) {
+    if (n <= 0 || k <= 0 || rows <= 0 || n_exp <= 0 || mq_row_size(type, k) == 0) return 0;
+    return moe_dev_ws(type, n_exp, n, k, rows).total;
+}
+
+extern "C" int mq_op_mul_mat_id_device(int type, const void *expert_images, size_t expert_stride, int n_exp, int64_t n,
+                                       int64_t k, const mq_view *b, const mq_view *ids, const mq_view *dst,
+                                       void *workspace, size_t workspace_bytes, void *stream) {
+    if (!expert_images || n_exp <= 0 || !b || !ids || !dst || !b->data || !ids->data || !dst->data || !workspace)
+        return set_error(MQ_EINVAL, "mq_op_mul_mat_id_device: missing operand");
+    if (!mq_supports(type, k) || n <= 0 || n > INT32_MAX || (expert_stride % 256) != 0 ||
+        ((uintptr_t)expert_images & 255) != 0 || n_exp > MOE_MAX_EXPERTS)
+        return set_error(MQ_EUNSUPPORTED, "mq_op_mul_mat_id_device: weight type %d with k %lld, %d experts", type,
+                         (long long)k, n_exp);
+    if (!shape_ok(b) || !shape_ok(ids) || !shape_ok(dst) || b->type != MQ_TYPE_F32 || ids->type != MQ_TYPE_I32 ||
+        dst->type != MQ_TYPE_F32)
+        return set_error(MQ_EINVAL, "mq_op_mul_mat_id_device: types (F32 b and dst, I32 ids)");
+    const int64_t n_used = ids->ne[0], T = ids->ne[1];
+    if (b->ne[0] != k || (b->ne[1] != 1 && b->ne[1] != n_used) || b->ne[2] != T || b->ne[3] != 1 || ids->ne[2] != 1 ||
+        ids->ne[3] != 1 || dst->ne[0] != n || dst->ne[1] != n_used || dst->ne[2] != T || dst->ne[3] != 1)
+        return set_error(MQ_EINVAL,
+                         "mq_op_mul_mat_id_device: shapes (b [k, 1|n_used, T], ids [n_used, T], dst [n, n_used, T])");
+    if (b->nb[0] != 4 || dst->nb[0] != 4 || ids->nb[0] != 4 || b->nb[1] % 16 || b->nb[2] % 16 || dst->nb[1] % 4 ||
+        dst->nb[2] % 4 || ((uintptr_t)b->data & 15) || ids->nb[1] % 4)
+        return set_error(MQ_EINVAL, "mq_op_mul_mat_id_device: rows must be contiguous (b rows 16-byte aligned)");
+    const int64_t R = n_used * T;
+    if (R == 0) return MQ_OK;
+    const MoeDevWs w = moe_dev_ws(type, n_exp, n, k, R);
+    if (w.rmax > INT32_MAX)
+        return set_error(MQ_EUNSUPPORTED, "mq_op_mul_mat_id_device: %lld routed rows", (long long)w.rmax);
+    if (((uintptr_t)workspace & 255) || workspace_bytes < w.total)
+        return set_error(MQ_EINVAL, "mq_op_mul_mat_id_device: workspace of %zu bytes (256-byte aligned) needed, %zu given",
+                         w.total, workspace_bytes);
+    hipStream_t s = (hipStream_t)stream;
+    char *ws = (char *)workspace;
+    int64_t *src_off = (int64_t *)(ws + w.src_off), *dst_off = (int64_t *)(ws + w.dst_off);
+    int *tiles = (int *)(ws + w.tiles);
+    float *X = (float *)(ws + w.x), *Y = (float *)(ws + w.y);
+    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), 0, s, (const char *)ids->data, (int64_t)ids->nb[1], (int)n_used,
+                       T, n_exp, b->ne[1], (int64_t)b->nb[1], (int64_t)b->nb[2], (int64_t)dst->nb[1],
+                       (int64_t)dst->nb[2], w.tile, w.rmax, src_off, dst_off, tiles, (char *)dst->data, n);
+    hipLaunchKernelGGL(k_gather_rows_pad, dim3((unsigned)w.rmax), dim3(256), 0, s, (const char *)b->data, src_off, X, k);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return hip_rc(e, "mul_mat_id routing");
+    int rc = mq_quantize_act_ex(type, X, k, w.rmax, k, nullptr, MQ_PRE_NONE, ws + w.q, workspace_bytes - w.q,
+                                MQ_PATH_GEMM, stream);
+    if (rc != 0) return rc;
+    if ((rc = hip_rc(launch_gemm_moe(type, expert_images, expert_stride, n, k, ws + w.q, w.rmax, w.tile, tiles, Y, s),
+                     "mul_mat_id gemm")))
+        return rc;
+    hipLaunchKernelGGL(k_scatter_rows_pad, dim3((unsigned)w.rmax), dim3(256), 0, s, Y, dst_off, (char *)dst->data, n);
     return hip_rc(hipGetLastError(), "mul_mat_id");
 }
 

@@ -183,6 +183,11 @@ _SIGS.update({
     "mq_op_flash_attn_blocks": (_c_int, [_PV, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_vp, ctypes.c_float,
                                          _c_vp, _c_vp, _c_i64, _c_vp, _c_sz, _c_vp, _c_sz, _c_int, _c_int, _c_vp]),
     "mq_op_supported": (_c_int, [_c_int, _c_int, _PV, _PV, _PV, _PV, _PV]),
+    "mq_op_mul_mat_id_workspace_bytes": (_c_sz, [_c_int, _c_i64, _c_i64, _c_i64]),
+    "mq_op_mul_mat_id": (_c_int, [_c_int, _c_vp, _c_sz, _c_int, _c_i64, _c_i64, _PV, _PV, _PV, _c_vp, _c_sz, _c_vp]),
+    "mq_op_mul_mat_id_device_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_i64, _c_i64, _c_i64]),
+    "mq_op_mul_mat_id_device": (_c_int, [_c_int, _c_vp, _c_sz, _c_int, _c_i64, _c_i64, _PV, _PV, _PV, _c_vp, _c_sz,
+                                         _c_vp]),
     "mq_op_soft_max": (_c_int, [_PV, _PV, _PV, ctypes.c_float, _c_vp]),
     "mq_op_argsort": (_c_int, [_PV, _PV, _c_int, _c_vp]),
     "mq_op_repeat": (_c_int, [_PV, _PV, _c_vp]),

@@ -262,6 +262,20 @@ int mq_op_mul_mat_id(int type, const void *expert_images, size_t expert_stride, 
                      const mq_view *b, const mq_view *ids, const mq_view *dst, void *workspace, size_t workspace_bytes,
                      void *stream);
 
+/* ggml_mul_mat_id (src/crispembed.cpp:1365,1371) with the routing on the device: the same
+ * operands and result as mq_op_mul_mat_id, with no stream synchronization and no host copy, so
+ * it can be enqueued ahead and captured in a HIP graph.  One workgroup counts the slots per
+ * expert and lays the rows out by expert in segments of whole row tiles (64 or 256 rows), one
+ * pass gathers them, one activation quantization and one GEMM launch cover every expert (each
+ * row tile reads its expert's weights from a device table; tiles past the used ones exit), and
+ * one pass scatters the results.  A slot whose id lies outside [0, n_exp) gets a row of NaN.
+ * n_exp <= 1024.  workspace: mq_op_mul_mat_id_device_workspace_bytes(type, n_exp, n, k,
+ * n_used * T) bytes, 256-aligned (the rows padded to whole tiles per expert). */
+size_t mq_op_mul_mat_id_device_workspace_bytes(int type, int n_exp, int64_t n, int64_t k, int64_t rows);
+int mq_op_mul_mat_id_device(int type, const void *expert_images, size_t expert_stride, int n_exp, int64_t n, int64_t k,
+                            const mq_view *b, const mq_view *ids, const mq_view *dst, void *workspace,
+                            size_t workspace_bytes, void *stream);
+
 /* ggml_soft_max_ext without ALiBi (src/crispembed.cpp:1267,1336): dst = softmax over ne0 of
  * x * scale + mask, mask NULL or F16/F32 [ne0, >= ne1, ...] (row i1 of x uses mask row i1; mask
  * planes broadcast over x's by index modulo), -inf entries masked; a row with every entry

@@ -16,9 +16,12 @@ pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def test_backend_driver_json():
+@pytest.mark.parametrize("moe_host", ["0", "1"])
+def test_backend_driver_json(moe_host):
+    """moe_host 0: MUL_MAT_ID routed on the device (the default); 1: the ids read back to the host."""
     exe = os.path.join(ROOT, "crispembed_amd", "bin", "test-backend-mi355")
-    r = subprocess.run([exe, "mi355", "--json"], capture_output=True, text=True, timeout=300)
+    env = dict(os.environ, MQ_GGML_MOE_HOST=moe_host)
+    r = subprocess.run([exe, "mi355", "--json"], capture_output=True, text=True, timeout=300, env=env)
     print(r.stderr[-2000:])
     out = json.loads(r.stdout.strip().splitlines()[-1])
     assert out["name"].startswith("MI355X")
