@@ -566,13 +566,20 @@ static hipError_t launch_kq_stream_groups(const GvGroups &G, const int8_t *xq, c
         if (atoi(e) >= 1 && atoi(e) <= 4) per_cu = atoi(e);
     const unsigned grid = (unsigned)std::min<int64_t>(ntiles, (int64_t)ncu * per_cu);
     const dim3 block(512);
+    // tiles in flight ahead of the one computed (MQ_GEMV_PF: 1, 2 or 3 for measurements).  One:
+    // MI355X, Q6_K lm_head 151936 x 2048 at m = 1 45.9 -> 44.6 us, m = 8 53.3 -> 52.6 us; the
+    // Q4_K layer sweep's separate-quantizer form 41.4 -> 34.8 us per layer (self-quantizing
+    // form unchanged) against two.
     const char *pe = getenv("MQ_GEMV_PF");
-    const int pf = pe ? atoi(pe) : 2;
+    const int pf = pe && *pe ? atoi(pe) : 1;
     if (X) {  // the activation quantized inside the kernel
         const GvX x = *X;
         switch (sbw) {
             case 1:
-                hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 2, true>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m, x);
+                if (pf == 1)
+                    hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 1, true>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m, x);
+                else
+                    hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 1, 2, true>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m, x);
                 break;
             case 2:
                 hipLaunchKernelGGL((k_gemv_kq_stream<TYPE, 2, 1, true>), dim3(grid), block, 0, s, G, xq, xd, xaux, (int)k, m, x);
