@@ -412,6 +412,10 @@ def bench_decode(torch, L, mq, synth):
         del graph
     out["workload"] = ("GEMV m in {1,8}: Qwen3-VL-2B lm_head Q6_K [151936x2048]; 28-layer sweep of Q4_K "
                        "q,k,v,o [2048|1024 x 2048], gate,up [6144x2048], down [2048x6144] (792.7 MB)")
+    out["departures"] = ("lm_head: 4096 distinct quantized rows tiled to 151936, in two device copies walked in "
+                         "turn (510 MB, past the 256 MB last-level cache); layers: one random layer's matrices "
+                         "in 28 device copies; o reads q's output and gate|up the layer input (stand-ins for "
+                         "the attention rows and the normed residual)")
     return out
 
 
@@ -577,6 +581,8 @@ def bench_qwen3_e2e(torch, L, mq):
     qd, kvd = hp["n_head"] * hp["head_dim"], hp["n_kv_head"] * hp["head_dim"]
     lin_ops = 2.0 * M * nl * (H * (qd + 2 * kvd) + qd * H + 3 * H * F)
     return {"workload": "Qwen3-Embedding-0.6B shape, Q4_K linears, 16 seq x 512 tokens, causal, last-token pool + L2",
+            "departures": "one random layer's Q4_K bytes in all 28 layers (28 separate device copies: the same "
+                          "bytes move as with 28 distinct layers)",
             "batch_ms": round(us / 1e3, 3), "embeddings_per_s": round(B / (us * 1e-6), 1),
             "linear_tops": round(lin_ops / (us * 1e-6) / 1e12, 1)}
 
