@@ -38,6 +38,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -122,7 +123,23 @@ struct BackendCtx {
     // ggml_backend_mi355_set_act_observer
     ggml_backend_mi355_act_observer act_cb = nullptr;
     void *act_user = nullptr;
+    // gate|up weight images (the gate weight's rows, then the up weight's, planes built) of the
+    // gated FFNs computed so far, for the gate|up GEMM that forms silu(gate) * up in its store;
+    // each valid while no weight has been written since it was built (gen = weight_gen())
+    struct GluImage {
+        const void *gate, *up;
+        uint64_t gen;
+        void *img;
+    };
+    std::vector<GluImage> glu;
 };
+
+// Bumped by every write into a weight image (set_tensor, memset_tensor, cpy_tensor, clear, and
+// the free of a buffer, whose addresses a later weight may reuse): derived copies of weights
+// built before it are stale.
+std::atomic<uint64_t> g_weight_gen{1};
+uint64_t weight_gen() { return g_weight_gen.load(std::memory_order_acquire); }
+void weights_written() { g_weight_gen.fetch_add(1, std::memory_order_acq_rel); }
 
 std::vector<DeviceCtx *> &devices();
 ggml_backend_reg &the_reg();
@@ -219,6 +236,7 @@ void buf_free(ggml_backend_buffer_t b) {
     DeviceGuard g(c->ordinal);
     (void)hipFree(c->base);
     delete c;
+    weights_written();
 }
 
 void *buf_base(ggml_backend_buffer_t b) { return ((BufferCtx *)b->context)->base; }
@@ -231,6 +249,7 @@ void rebuild_planes(ggml_tensor *t, int64_t e, size_t offset, size_t size) {
     const size_t rs = ggml_row_size(t->type, t->ne[0]);
     const int64_t r0 = (int64_t)(offset / rs), r1 = (int64_t)((offset + size + rs - 1) / rs);
     char *img = (char *)t->data + (size_t)e * image_bytes(t);
+    weights_written();
     if (mq_weight_prepare(mt, img, t->ne[1], t->ne[0], r0, r1, nullptr) != 0) {
         std::fprintf(stderr, "ggml-mi355: weight preparation of '%s' failed: %s\n", t->name, mq_last_error());
         std::abort();
@@ -296,6 +315,7 @@ bool buf_cpy_tensor(ggml_backend_buffer_t b, const ggml_tensor *src, ggml_tensor
             return false;
         hip_check(hipMemcpy(dst->data, src->data, image_bytes(dst) * (size_t)dst->ne[2], hipMemcpyDeviceToDevice),
                   "hipMemcpy D2D");
+        weights_written();
         return true;
     }
     hip_check(hipMemcpy(dst->data, src->data, ggml_nbytes(src), hipMemcpyDeviceToDevice), "hipMemcpy D2D");
@@ -307,6 +327,7 @@ void buf_clear(ggml_backend_buffer_t b, uint8_t value) {
     DeviceGuard g(c->ordinal);
     hip_check(hipMemset(c->base, value, c->size), "hipMemset");
     hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    weights_written();
 }
 
 const ggml_backend_buffer_i kBufferIface = {
@@ -359,6 +380,7 @@ void be_free(ggml_backend_t be) {
         if (c->cs) (void)hipFree(c->cs);
         if (c->mb) (void)hipFree(c->mb);
         if (c->sg_buf) (void)hipFree(c->sg_buf);
+        for (const BackendCtx::GluImage &gi : c->glu) (void)hipFree(gi.img);
         (void)hipStreamDestroy(c->stream);
     }
     delete c;
@@ -984,6 +1006,78 @@ int try_fuse_ffn(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status 
     return dst == mm2 ? 4 : 5;
 }
 
+// The gate|up image of gate weight wg and up weight wu (same type, n_ff x k each): built on first
+// use from their GGUF rows (gate rows, then up rows, then the planes), rebuilt once a weight has
+// been written since.  NULL under capture when it is not built yet (no allocation there).
+void *glu_image(BackendCtx *c, const ggml_tensor *wg, const ggml_tensor *wu) {
+    const uint64_t gen = weight_gen();
+    for (size_t j = 0; j < c->glu.size(); j++) {
+        BackendCtx::GluImage &gi = c->glu[j];
+        if (gi.gate != wg->data || gi.up != wu->data) continue;
+        if (gi.gen == gen) return gi.img;
+        if (c->capturing) return nullptr;
+        hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");  // queued work may read it
+        (void)hipFree(gi.img);
+        c->glu.erase(c->glu.begin() + (long)j);
+        break;
+    }
+    if (c->capturing) return nullptr;
+    const int mt = mq_type_of(wg->type);
+    const int64_t nff = wg->ne[1], k = wg->ne[0];
+    const size_t raw = ggml_row_size(wg->type, k) * (size_t)nff;
+    void *img = nullptr;
+    if (hipMalloc(&img, mq_weight_image_bytes(mt, 2 * nff, k)) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    hip_check(hipMemcpyAsync(img, wg->data, raw, hipMemcpyDeviceToDevice, c->stream), "hipMemcpyAsync D2D");
+    hip_check(hipMemcpyAsync((char *)img + raw, wu->data, raw, hipMemcpyDeviceToDevice, c->stream),
+              "hipMemcpyAsync D2D");
+    if (mq_weight_prepare(mt, img, 2 * nff, k, 0, 2 * nff, c->stream) != 0) {
+        hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        (void)hipFree(img);
+        return nullptr;
+    }
+    c->glu.push_back({wg->data, wu->data, gen, img});
+    return img;
+}
+
+// MUL_MAT(w_gate, x) -> UNARY(SILU) -> MUL_MAT(w_up, x) -> MUL(silu, up), the gated FFN of
+// src/decoder_embed.cpp:793-801 with separate gate and up weights, on the GEMM path at the sizes
+// the gate|up GEMM takes (mq_mul_mat_q_swiglu): one GEMM over the gate|up image forms
+// silu(gate) * up in its store, straight into the MUL's tensor; gate, its SiLU and up are never
+// written (each has no other reader).  The product's values are those of the separate nodes.
+int try_fuse_glu(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status &st) {
+    if (i + 3 >= n) return 0;
+    ggml_tensor *gate = ggml_graph_node(cg, i), *silu = ggml_graph_node(cg, i + 1);
+    ggml_tensor *up = ggml_graph_node(cg, i + 2), *mul = ggml_graph_node(cg, i + 3);
+    if (silu->op != GGML_OP_UNARY || ggml_get_unary_op(silu) != GGML_UNARY_OP_SILU || silu->src[0] != gate) return 0;
+    if (up->op != GGML_OP_MUL_MAT || mul->op != GGML_OP_MUL) return 0;
+    if (!((mul->src[0] == silu && mul->src[1] == up) || (mul->src[0] == up && mul->src[1] == silu))) return 0;
+    // (with an activation observer installed the nodes run as they stand: its callers compare
+    // the products' inputs and outputs node by node)
+    if (!feeds_only_next(cg, i) || !feeds_only_next(cg, i + 1) || ggml_node_get_use_count(cg, i + 2) != 1 ||
+        (up->flags & GGML_TENSOR_FLAG_OUTPUT) || i + 4 >= n || c->act_cb)
+        return 0;
+    const ggml_tensor *wg = gate->src[0], *wu = up->src[0], *x = gate->src[1];
+    if (up->src[1] != x || !flat_mul_mat(gate) || !flat_mul_mat(up) || wg->type != wu->type || wg->ne[0] != wu->ne[0] ||
+        wg->ne[1] != wu->ne[1] || !is_image(wg) || !is_image(wu) || wg->ne[2] != 1 || wu->ne[2] != 1)
+        return 0;
+    const int mt = mq_type_of(wg->type);
+    const int64_t nff = wg->ne[1], K = wg->ne[0], M = x->ne[1] * x->ne[2] * x->ne[3];
+    if ((mt != MQ_TYPE_Q4_K && mt != MQ_TYPE_Q6_K) || !same_shape(mul, gate) || mul->type != GGML_TYPE_F32 ||
+        mul->nb[0] != sizeof(float) || !rows_flat(mul) || mul->nb[1] % sizeof(float) != 0)
+        return 0;
+    if (mq_mul_mat_path(mt, 2 * nff, K, M) != MQ_PATH_GEMM || !mq_mul_mat_q_swiglu_supported(mt, nff, M)) return 0;
+    void *img = glu_image(c, wg, wu);
+    if (!img) return 0;
+    int rc = quantize_x(c, x, mt, M, K, MQ_PATH_GEMM);
+    if (rc == 0)
+        rc = mq_mul_mat_q_swiglu(mt, img, nff, K, c->ws, M, (float *)mul->data, (int64_t)(mul->nb[1] / 4), c->stream);
+    st = op_status(rc, gate);
+    return 4;
+}
+
 // UNARY(SILU)(gate) -> MUL_MAT(w_up, x) -> MUL(silu, up) -> MUL_MAT(w_down, product), the gated FFN
 // of src/decoder_embed.cpp:793-802 with separate gate and up weights: the up projection runs as
 // usual, then the down projection's activation is silu(gate) * up formed by its quantizer
@@ -1387,7 +1481,8 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
         if (fuse) {
             switch (node->op) {
                 case GGML_OP_MUL_MAT:
-                    used = try_fuse_ffn(c, cg, i, n, st);
+                    if (!std::getenv("MQ_GGML_NO_GLU")) used = try_fuse_glu(c, cg, i, n, st);
+                    if (!used) used = try_fuse_ffn(c, cg, i, n, st);
                     if (!used) used = try_group_mul_mat(c, cg, i, n, done, st);
                     break;
                 case GGML_OP_NORM:
@@ -1441,6 +1536,8 @@ uint64_t graph_key(ggml_cgraph *cg) {
     };
     const int n = ggml_graph_n_nodes(cg);
     mix(&n, sizeof n);
+    const uint64_t wgen = weight_gen();  // copies of weights (the gate|up images) follow their writes
+    mix(&wgen, sizeof wgen);
     for (int i = 0; i < n; i++) {
         const ggml_tensor *t = ggml_graph_node(cg, i);
         mix(&t->op, sizeof t->op);
@@ -1457,7 +1554,7 @@ uint64_t graph_key(ggml_cgraph *cg) {
     }
     for (const char *k : {"MQ_GGML_NO_FUSION", "MQ_GEMM_CFG", "MQ_ATTN_SPLIT", "MQ_GEMV_WGS", "MQ_GEMV_PF",
                           "MQ_FORCE_GEMV_MAX_M", "MQ_Q8_0_VARIANT", "MQ_GGML_NO_MASK_BLOCKS", "MQ_ATTN_SPLIT_WAVES",
-                          "MQ_GGML_NO_MASK_SEGMENTS", "MQ_GGML_MOE_HOST"}) {
+                          "MQ_GGML_NO_MASK_SEGMENTS", "MQ_GGML_MOE_HOST", "MQ_GGML_NO_GLU"}) {
         const char *v = std::getenv(k);
         if (v) mix(v, std::strlen(v));
         mix("|", 1);

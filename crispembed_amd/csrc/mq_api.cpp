@@ -418,6 +418,11 @@ int mq_mul_mat_q_requant_supported(int type, int out_type, int64_t m, int64_t n)
     return 0;
 }
 
+int mq_mul_mat_q_swiglu_supported(int type, int64_t n_ff, int64_t m) {
+    if (!type_ok(type) || n_ff <= 0 || n_ff > INT32_MAX / 2 || m <= 0 || m > INT32_MAX) return 0;
+    return gemm_swiglu_fits(m, n_ff) ? 1 : 0;
+}
+
 int mq_mul_mat_q_swiglu(int type, const void *w_image, int64_t n_ff, int64_t k, const void *workspace, int64_t m,
                         float *y, int64_t ldy, void *stream) {
     if (n_ff <= 0 || n_ff > INT32_MAX / 2) return fail(MQ_EINVAL, "mq_mul_mat_q_swiglu: bad n_ff");

@@ -70,6 +70,7 @@ _SIGS = {
     "mq_mul_mat_q_requant": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_int, _c_int, _c_vp,
                                       _c_sz, _c_vp]),
     "mq_mul_mat_q_requant_supported": (_c_int, [_c_int, _c_int, _c_i64, _c_i64]),
+    "mq_mul_mat_q_swiglu_supported": (_c_int, [_c_int, _c_i64, _c_i64]),
     "mq_mul_mat_q_swiglu": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
     "mq_mul_mat_q_qkv": (_c_int, [_c_int, ctypes.POINTER(_c_vp), ctypes.POINTER(_c_i64), _c_i64, _c_vp, _c_i64, _c_vp,
                                   _c_i64, ctypes.POINTER(_c_vp), _c_int, _c_int, _c_int, _c_vp, _c_sz, _c_vp]),

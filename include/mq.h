@@ -245,6 +245,10 @@ int mq_mul_mat_q_requant_supported(int type, int out_type, int64_t m, int64_t n)
 int mq_mul_mat_q_swiglu(int type, const void *w_image, int64_t n_ff, int64_t k, const void *workspace, int64_t m,
                         float *y, int64_t ldy, void *stream);
 
+/* 1 when mq_mul_mat_q_swiglu(type, ..., n_ff, k, ..., m, ...) runs (the type and shape rules
+ * above; k and the buffers aside), else 0.  No GPU call. */
+int mq_mul_mat_q_swiglu_supported(int type, int64_t n_ff, int64_t m);
+
 /* The q, k and v projections of an attention layer (src/crispembed.cpp:1168-1170, each with its
  * bias ADD) on one activation quantized with path MQ_PATH_GEMM, as one grouped GEMM: q (n[0]
  * features) is stored to y_q as mq_mul_mat_q_group stores it, while k and v (n[1] = n[2] =

@@ -113,6 +113,19 @@ def test_batched_graph_full_shape_on_gpu(batched):
     assert (cos[~np.eye(B, dtype=bool)] < 0.9999).all()  # 16 distinct sequences, 16 distinct embeddings
 
 
+def test_glu_fusion_is_the_separate_nodes(batched):
+    """Without an observer the backend forms silu(gate) * up in one gate|up GEMM over a combined
+    weight image (the gate, SiLU, up and MUL nodes as one launch): the 16 x 512 batch's hidden
+    states equal, bit for bit, those of the graph with the nodes computed separately
+    (MQ_GGML_NO_GLU=1)."""
+    model, ids = batched["model"], batched["ids"]
+    d = os.path.dirname(str(model))
+    fused, rf = _run(model, ids, T, ("--iters", "3"), out=os.path.join(d, "glu.f32"))
+    plain, rp = _run(model, ids, T, ("--iters", "3"), env={"MQ_GGML_NO_GLU": "1"}, out=os.path.join(d, "noglu.f32"))
+    print(f"batched graph: {rf['ms_per_graph']:.3f} ms with the gate|up GEMM, {rp['ms_per_graph']:.3f} ms without")
+    assert np.array_equal(fused, plain)
+
+
 def test_quantized_activations_are_the_oracles(batched):
     """(1): every product's quantized activation, every row, against the oracle."""
     res, n_layer = batched["res"], batched["hp"]["n_layer"]
