@@ -132,6 +132,9 @@ struct BackendCtx {
         void *img;
     };
     std::vector<GluImage> glu;
+    // normed rows this graph left unwritten: their only readers are K-quant GEMMs that take the
+    // Q8_K copy the norm left in the workspace (a reader that misses it fails loudly)
+    std::vector<const ggml_tensor *> unwritten;
 };
 
 // Bumped by every write into a weight image (set_tensor, memset_tensor, cpy_tensor, clear, and
@@ -430,7 +433,15 @@ bool ensure_ws(BackendCtx *c, size_t need) {
 // Quantizes activation x (M rows of K floats, row stride in x->nb[1]) for weight type mt into
 // the workspace, unless it is already there.  Returns an mq status.
 int quantize_x(BackendCtx *c, const ggml_tensor *x, int mt, int64_t M, int64_t K, int path) {
-    if (c->ws_x == x && c->ws_type == mt && c->ws_m == M && c->ws_k == K && c->ws_path == path) return 0;
+    // Q4_K and Q6_K read the same tiled Q8_K activation
+    const auto kq = [](int t) { return t == MQ_TYPE_Q4_K || t == MQ_TYPE_Q6_K; };
+    const bool same = c->ws_type == mt || (path == MQ_PATH_GEMM && kq(c->ws_type) && kq(mt));
+    if (c->ws_x == x && same && c->ws_m == M && c->ws_k == K && c->ws_path == path) return 0;
+    if (std::find(c->unwritten.begin(), c->unwritten.end(), x) != c->unwritten.end()) {
+        std::fprintf(stderr, "ggml-mi355: '%s' was left unwritten for the GEMMs that read its quantized copy, "
+                     "which is gone (MQ_GGML_WRITE_NORMS=1 writes it)\n", x->name);
+        return MQ_EINVAL;
+    }
     c->ws_x = nullptr;
     if (!ensure_ws(c, mq_workspace_bytes(mt, M, K))) return MQ_ENOMEM;
     const int rc = mq_quantize_act_ex(mt, (const float *)x->data, (int64_t)(x->nb[1] / 4), M, K, nullptr, MQ_PRE_NONE,
@@ -879,9 +890,29 @@ int try_fuse_norm(BackendCtx *c, ggml_cgraph *cg, int i, int n, enum ggml_status
         mq_view sv{};
         if (add_shared) sv = view_of(first);
         c->ws_x = nullptr;
-        const int rc = mq_op_norm_q8_K(kind, &x, res ? &r : nullptr, add_shared ? &sv : nullptr, &d, eps, w, c->ws,
-                                       c->ws_bytes, c->stream);
+        // The normed rows themselves are left unwritten when every reader (all of the tensor's
+        // uses, counted over the whole graph) is a K-quant MUL_MAT on the GEMM path taking them
+        // as src1 -- they read the Q8_K copy -- and no observer or graph output wants the floats.
+        bool skip_h = !c->act_cb && !(last->flags & GGML_TENSOR_FLAG_OUTPUT) && !std::getenv("MQ_GGML_WRITE_NORMS");
+        if (skip_h) {
+            int uses = 0;
+            for (int jj = i + used; jj < n && skip_h; jj++) {
+                const ggml_tensor *t = ggml_graph_node(cg, jj);
+                bool reads = t->view_src == last;
+                for (int q = 0; q < GGML_MAX_SRC; q++) reads = reads || t->src[q] == last;
+                if (!reads) continue;
+                const int tt = t->op == GGML_OP_MUL_MAT ? mq_type_of(t->src[0]->type) : -1;
+                skip_h = (tt == MQ_TYPE_Q4_K || tt == MQ_TYPE_Q6_K) && t->src[1] == last && t->src[0] != last &&
+                         flat_mul_mat(t) && t->src[0]->ne[0] == K && !last_compute_node(cg, jj, n) &&
+                         mq_mul_mat_path(tt, t->src[0]->ne[1], K, M) == MQ_PATH_GEMM;
+                uses++;
+            }
+            skip_h = skip_h && uses > 0 && uses == ggml_node_get_use_count(cg, i + used - 1);
+        }
+        const int rc = mq_op_norm_q8_K(kind, &x, res ? &r : nullptr, add_shared ? &sv : nullptr, skip_h ? nullptr : &d,
+                                       eps, w, c->ws, c->ws_bytes, c->stream);
         if (rc == 0) c->ws_x = last, c->ws_type = mmt, c->ws_m = M, c->ws_k = K, c->ws_path = MQ_PATH_GEMM;
+        if (rc == 0 && skip_h) c->unwritten.push_back(last);
         st = op_status(rc, nrm);
         return used;
     }
@@ -1459,6 +1490,7 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
     c->qk_fa = nullptr;
     c->cs_key.clear();  // and the positions
     c->mb_mask = c->sg_mask = nullptr;  // and the masks
+    c->unwritten.clear();
     std::vector<char> done(n, 0);  // nodes already computed as part of an earlier group
     for (int i = 0; i < n; i++) {
         ggml_tensor *node = ggml_graph_node(cg, i);
@@ -1554,7 +1586,8 @@ uint64_t graph_key(ggml_cgraph *cg) {
     }
     for (const char *k : {"MQ_GGML_NO_FUSION", "MQ_GEMM_CFG", "MQ_ATTN_SPLIT", "MQ_GEMV_WGS", "MQ_GEMV_PF",
                           "MQ_FORCE_GEMV_MAX_M", "MQ_Q8_0_VARIANT", "MQ_GGML_NO_MASK_BLOCKS", "MQ_ATTN_SPLIT_WAVES",
-                          "MQ_GGML_NO_MASK_SEGMENTS", "MQ_GGML_MOE_HOST", "MQ_GGML_NO_GLU"}) {
+                          "MQ_GGML_NO_MASK_SEGMENTS", "MQ_GGML_MOE_HOST", "MQ_GGML_NO_GLU",
+                          "MQ_GGML_WRITE_NORMS"}) {
         const char *v = std::getenv(k);
         if (v) mix(v, std::strlen(v));
         mix("|", 1);

@@ -115,15 +115,19 @@ def test_batched_graph_full_shape_on_gpu(batched):
 
 def test_glu_fusion_is_the_separate_nodes(batched):
     """Without an observer the backend forms silu(gate) * up in one gate|up GEMM over a combined
-    weight image (the gate, SiLU, up and MUL nodes as one launch): the 16 x 512 batch's hidden
-    states equal, bit for bit, those of the graph with the nodes computed separately
-    (MQ_GGML_NO_GLU=1)."""
+    weight image (the gate, SiLU, up and MUL nodes as one launch) and leaves the attention and FFN
+    norms' float rows unwritten (their readers take the Q8_K copy): the 16 x 512 batch's hidden
+    states equal, bit for bit, those of the graph with the nodes computed separately and every
+    norm written (MQ_GGML_NO_GLU=1, MQ_GGML_WRITE_NORMS=1), and those of each change alone."""
     model, ids = batched["model"], batched["ids"]
     d = os.path.dirname(str(model))
-    fused, rf = _run(model, ids, T, ("--iters", "3"), out=os.path.join(d, "glu.f32"))
-    plain, rp = _run(model, ids, T, ("--iters", "3"), env={"MQ_GGML_NO_GLU": "1"}, out=os.path.join(d, "noglu.f32"))
-    print(f"batched graph: {rf['ms_per_graph']:.3f} ms with the gate|up GEMM, {rp['ms_per_graph']:.3f} ms without")
-    assert np.array_equal(fused, plain)
+    runs = {}
+    for name, env in (("fused", {}), ("no_glu", {"MQ_GGML_NO_GLU": "1"}), ("write_norms", {"MQ_GGML_WRITE_NORMS": "1"}),
+                      ("plain", {"MQ_GGML_NO_GLU": "1", "MQ_GGML_WRITE_NORMS": "1"})):
+        runs[name] = _run(model, ids, T, ("--iters", "3"), env=env, out=os.path.join(d, f"{name}.f32"))
+    print("batched graph ms:", {k: round(v[1]["ms_per_graph"], 3) for k, v in runs.items()})
+    for name in ("no_glu", "write_norms", "plain"):
+        assert np.array_equal(runs["fused"][0], runs[name][0]), name
 
 
 def test_quantized_activations_are_the_oracles(batched):
