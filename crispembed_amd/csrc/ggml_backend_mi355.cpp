@@ -120,6 +120,12 @@ struct BackendCtx {
     const ggml_tensor *sg_mask = nullptr;
     std::vector<int64_t> sg_key;
     int64_t sg_len = 0;
+    // whether mask mz_mask (shapes mz_key) adds nothing to the scores (mq_op_mask_is_zero), found
+    // once per graph; mz_buf: its 4-byte flag on the device
+    void *mz_buf = nullptr;
+    const ggml_tensor *mz_mask = nullptr;
+    std::vector<int64_t> mz_key;
+    bool mz_zero = false;
     // ggml_backend_mi355_set_act_observer
     ggml_backend_mi355_act_observer act_cb = nullptr;
     void *act_user = nullptr;
@@ -383,6 +389,7 @@ void be_free(ggml_backend_t be) {
         if (c->cs) (void)hipFree(c->cs);
         if (c->mb) (void)hipFree(c->mb);
         if (c->sg_buf) (void)hipFree(c->sg_buf);
+        if (c->mz_buf) (void)hipFree(c->mz_buf);
         for (const BackendCtx::GluImage &gi : c->glu) (void)hipFree(gi.img);
         (void)hipStreamDestroy(c->stream);
     }
@@ -789,6 +796,27 @@ int64_t mask_segments(BackendCtx *c, const ggml_tensor *mt, const mq_view &q, co
     return S;
 }
 
+// Whether mask tensor mt adds nothing to the scores of this attention (every value it reads +-0:
+// an equal-length batch's padding mask), found once per graph with one flag read back; false
+// under capture (no synchronization there) and with MQ_GGML_MASK_ALWAYS=1.
+bool mask_zero(BackendCtx *c, const ggml_tensor *mt, const mq_view &q, const mq_view &k, const mq_view &m) {
+    if (c->capturing || std::getenv("MQ_GGML_MASK_ALWAYS")) return false;
+    std::vector<int64_t> key = {(int64_t)(uintptr_t)mt->data, q.ne[1], k.ne[1]};
+    key.insert(key.end(), mt->ne, mt->ne + 4);
+    key.insert(key.end(), mt->nb, mt->nb + 4);
+    if (c->mz_mask == mt && key == c->mz_key) return c->mz_zero;
+    c->mz_mask = nullptr;
+    if (!c->mz_buf && hipMalloc(&c->mz_buf, 256) != hipSuccess) {
+        (void)hipGetLastError();
+        c->mz_buf = nullptr;
+        return false;
+    }
+    int z = 0;
+    if (mq_op_mask_is_zero(&q, &k, &m, c->mz_buf, 256, &z, c->stream) != 0) z = 0;
+    c->mz_mask = mt, c->mz_key = key, c->mz_zero = z != 0;
+    return c->mz_zero;
+}
+
 // The attention of FLASH_ATTN_EXT node fa: with q and k before their norm and rotation when those
 // chains were left to it (c->qk_fa), else on its operands; per causal segment when the mask is a
 // batched decoder's, else with the mask's block lists where the attention takes them; with its
@@ -803,9 +831,11 @@ int attn_call(BackendCtx *c, const ggml_tensor *fa, void *ws, size_t ws_bytes, v
     const mq_view q = qk ? c->qk_q : view_of(fa->src[0]), k = qk ? c->qk_k : view_of(fa->src[1]);
     int64_t seg = 0;
     const void *blocks = nullptr;
-    if (fa->src[3] && !(flags & MQ_ATTN_KV_READY)) seg = mask_segments(c, fa->src[3], q, k, m);
-    if (fa->src[3] && seg == 0) blocks = mask_blocks(c, fa->src[3], q, k, m);
-    return mq_op_flash_attn_blocks(&q, &k, &v, fa->src[3] ? &m : nullptr, &d, op_param_f32(fa, 0),
+    // a mask of zeros adds nothing: the attention runs unmasked (the same scores)
+    const bool masked = fa->src[3] && !mask_zero(c, fa->src[3], q, k, m);
+    if (masked && !(flags & MQ_ATTN_KV_READY)) seg = mask_segments(c, fa->src[3], q, k, m);
+    if (masked && seg == 0) blocks = mask_blocks(c, fa->src[3], q, k, m);
+    return mq_op_flash_attn_blocks(&q, &k, &v, masked ? &m : nullptr, &d, op_param_f32(fa, 0),
                                    qk ? c->qk_qw : nullptr, qk ? c->qk_kw : nullptr, qk ? c->qk_eps : 0.f,
                                    qk ? c->cs : nullptr, blocks, seg, ws, ws_bytes, act, act_bytes, act_type,
                                    qk ? 0 : flags, c->stream);
@@ -1489,7 +1519,7 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
     c->kv_ready_for = nullptr;
     c->qk_fa = nullptr;
     c->cs_key.clear();  // and the positions
-    c->mb_mask = c->sg_mask = nullptr;  // and the masks
+    c->mb_mask = c->sg_mask = c->mz_mask = nullptr;  // and the masks
     c->unwritten.clear();
     std::vector<char> done(n, 0);  // nodes already computed as part of an earlier group
     for (int i = 0; i < n; i++) {
@@ -1499,6 +1529,7 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
             if (done[i] && !is_view_op(node->op)) {
                 if (c->mb_mask && overlaps(node, c->mb_mask)) c->mb_mask = nullptr;
                 if (c->sg_mask && overlaps(node, c->sg_mask)) c->sg_mask = nullptr;
+                if (c->mz_mask && overlaps(node, c->mz_mask)) c->mz_mask = nullptr;
             }
             continue;
         }
@@ -1545,11 +1576,12 @@ enum ggml_status run_nodes(BackendCtx *c, ggml_cgraph *cg) {
                     break;
                 }
             }
-        for (int j = i; j < i + used && (c->mb_mask || c->sg_mask); j++) {
+        for (int j = i; j < i + used && (c->mb_mask || c->sg_mask || c->mz_mask); j++) {
             const ggml_tensor *t = ggml_graph_node(cg, j);
             if (is_view_op(t->op)) continue;
             if (c->mb_mask && overlaps(t, c->mb_mask)) c->mb_mask = nullptr;
             if (c->sg_mask && overlaps(t, c->sg_mask)) c->sg_mask = nullptr;
+            if (c->mz_mask && overlaps(t, c->mz_mask)) c->mz_mask = nullptr;
         }
         i += used - 1;
     }
@@ -1587,7 +1619,7 @@ uint64_t graph_key(ggml_cgraph *cg) {
     for (const char *k : {"MQ_GGML_NO_FUSION", "MQ_GEMM_CFG", "MQ_ATTN_SPLIT", "MQ_GEMV_WGS", "MQ_GEMV_PF",
                           "MQ_FORCE_GEMV_MAX_M", "MQ_Q8_0_VARIANT", "MQ_GGML_NO_MASK_BLOCKS", "MQ_ATTN_SPLIT_WAVES",
                           "MQ_GGML_NO_MASK_SEGMENTS", "MQ_GGML_MOE_HOST", "MQ_GGML_NO_GLU",
-                          "MQ_GGML_WRITE_NORMS"}) {
+                          "MQ_GGML_WRITE_NORMS", "MQ_GGML_MASK_ALWAYS"}) {
         const char *v = std::getenv(k);
         if (v) mix(v, std::strlen(v));
         mix("|", 1);

@@ -431,5 +431,9 @@ hipError_t launch_mask_blocks(const uint16_t *mask, int64_t m_sq, int64_t m_sb, 
 // run of zeros that ends at key r when the row is exactly that (0 on keys first..r, -inf on every
 // other key), else -1.
 hipError_t launch_mask_rows(const uint16_t *mask, int64_t m_sq, bool m_al, int T, int32_t *first, hipStream_t s);
+// *nonzero = 1 when any value of the Tq x Tk region of each (ne2 x ne3) plane of an F16 mask is not
+// +-0 (row stride m_sq, plane strides m_s2, m_s3, in halves); *nonzero is left alone otherwise
+hipError_t launch_mask_nonzero(const uint16_t *mask, int64_t m_sq, int64_t m_s2, int64_t m_s3, int ne2, int ne3, int Tq,
+                               int Tk, int *nonzero, hipStream_t s);
 
 }  // namespace mq

@@ -1506,6 +1506,32 @@ extern "C" int mq_op_mask_segments(const mq_view *q, const mq_view *k, const mq_
     return 0;
 }
 
+extern "C" int mq_op_mask_is_zero(const mq_view *q, const mq_view *k, const mq_view *mask, void *scratch,
+                                  size_t scratch_bytes, int *is_zero, void *stream) {
+    if (!is_zero) return fail("mask_is_zero: is_zero required");
+    *is_zero = 0;
+    if (!q || !k || !mask || !shape_ok(q) || !shape_ok(k) || !shape_ok(mask) || mask->type != MQ_TYPE_F16 ||
+        mask->ne[1] < q->ne[1] || mask->ne[0] < k->ne[1] || q->ne[1] > INT32_MAX || k->ne[1] > INT32_MAX ||
+        mask->nb[0] != 2 || mask->nb[1] % 2 || mask->nb[2] % 2 || mask->nb[3] % 2 || mask->ne[2] * mask->ne[3] > 65535)
+        return fail("mask_is_zero: an F16 mask [>= Tk, >= Tq, ...] over q and k");
+    if (!have_data({q, k, mask}) || !scratch) return fail("missing data pointer");
+    if (((uintptr_t)scratch & 3) || scratch_bytes < sizeof(int))
+        return set_error(MQ_EINVAL, "mq_op_mask_is_zero: 4 bytes (4-byte aligned) of scratch needed");
+    hipStream_t s = (hipStream_t)stream;
+    int nz = 0;
+    if (hipMemsetAsync(scratch, 0, sizeof(int), s) != hipSuccess) return set_error(MQ_EHIP, "mq_op_mask_is_zero: memset");
+    int rc = hip_rc(launch_mask_nonzero((const uint16_t *)mask->data, (int64_t)(mask->nb[1] / 2), (int64_t)(mask->nb[2] / 2),
+                                        (int64_t)(mask->nb[3] / 2), (int)mask->ne[2], (int)mask->ne[3], (int)q->ne[1],
+                                        (int)k->ne[1], (int *)scratch, s),
+                    "mask_nonzero");
+    if (rc != 0) return rc;
+    if (hipMemcpyAsync(&nz, scratch, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return set_error(MQ_EHIP, "mq_op_mask_is_zero: reading the flag back failed");
+    *is_zero = nz == 0;
+    return 0;
+}
+
 static int flash_attn(const mq_view *q, const mq_view *k, const mq_view *v, const mq_view *mask, const mq_view *dst,
                       float scale, void *workspace, size_t workspace_bytes, void *act_ws, size_t act_ws_bytes,
                       int flags, void *stream, const QkNormRope *qk = nullptr, const void *blocks = nullptr,

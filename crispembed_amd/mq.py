@@ -179,6 +179,7 @@ _SIGS.update({
     "mq_op_flash_attn_q8_0": (_c_int, [_PV, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_sz, _c_vp, _c_sz, _c_vp]),
     "mq_op_mask_blocks_bytes": (_c_sz, [_PV, _PV, _PV]),
     "mq_op_mask_blocks": (_c_int, [_PV, _PV, _PV, _c_vp, _c_sz, _c_vp]),
+    "mq_op_mask_is_zero": (_c_int, [_PV, _PV, _PV, _c_vp, _c_sz, ctypes.POINTER(ctypes.c_int), _c_vp]),
     "mq_op_mask_segments_bytes": (_c_sz, [_PV, _PV, _PV]),
     "mq_op_mask_segments": (_c_int, [_PV, _PV, _PV, _c_vp, _c_sz, ctypes.POINTER(_c_i64), _c_vp]),
     "mq_op_flash_attn_blocks": (_c_int, [_PV, _PV, _PV, _PV, _PV, ctypes.c_float, _c_vp, _c_vp, ctypes.c_float,

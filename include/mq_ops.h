@@ -228,6 +228,14 @@ size_t mq_op_mask_segments_bytes(const mq_view *q, const mq_view *k, const mq_vi
 int mq_op_mask_segments(const mq_view *q, const mq_view *k, const mq_view *mask, void *scratch, size_t scratch_bytes,
                         int64_t *seg_len, void *stream);
 
+/* Whether an attention's F16 mask adds nothing: *is_zero = 1 when every value of the Tq x Tk region
+ * (Tq = q->ne[1], Tk = k->ne[1]) of each of the mask's planes is +-0 -- an equal-length batch's
+ * padding mask (src/crispembed.cpp:2052-2135) -- so the attention may run unmasked with the same
+ * scores.  scratch: 4 bytes of device memory.  Synchronizes the stream (one flag read back): not
+ * for capture. */
+int mq_op_mask_is_zero(const mq_view *q, const mq_view *k, const mq_view *mask, void *scratch, size_t scratch_bytes,
+                       int *is_zero, void *stream);
+
 /* The general attention entry point: mq_op_flash_attn_ex with flags, plus the q / k norm and
  * rotation of mq_op_flash_attn_qk_norm_rope when q_norm_w, k_norm_w and cs are given (all three,
  * or all NULL), plus mask_blocks: NULL, or mq_op_mask_blocks' lists for these q, k and mask

@@ -584,6 +584,38 @@ def test_mask_block_lists(case):
     assert np.abs(outs[0] - outs[1]).max() / np.abs(ref).max() <= 1e-6
 
 
+@pytest.mark.parametrize("case,want", [("zeros", 1), ("neg_zero", 1), ("pad_rows", 1), ("last", 0), ("plane1", 0),
+                                       ("half", 0)])
+def test_mask_is_zero(case, want):
+    """mq_op_mask_is_zero: 1 exactly when every value of the Tq x Tk region the attention reads, in
+    every plane, is +-0 (an equal-length batch's padding mask): -0.0 counts as zero, values past
+    the region (the mask's padded query rows) are not read; one -inf in the region's last row and
+    column, a nonzero in the second plane, a 0.5 anywhere make it 0."""
+    L = mq.lib()
+    B, T, Tp = 3, 96, 128  # mask [T keys (+ stride pad), Tp >= T query rows, 1, B]
+    m = np.zeros((B, 1, Tp, T + 8), np.float16)
+    if case == "neg_zero":
+        m[1, 0, 5, 7] = np.float16(-0.0)
+    elif case == "pad_rows":
+        m[:, 0, T:, :] = np.float16(-np.inf)  # query rows past Tq
+        m[:, 0, :, T:] = np.float16(3.0)      # the row stride's unused tail
+    elif case == "last":
+        m[2, 0, T - 1, T - 1] = np.float16(-np.inf)
+    elif case == "plane1":
+        m[1, 0, 40, 3] = np.float16(-np.inf)
+    elif case == "half":
+        m[0, 0, 0, 50] = np.float16(0.5)
+    mask_d = _cuda(m)[..., :T]
+    hd, nh = 64, 2
+    q = _cuda(np.zeros((B, nh, T, hd), np.float32))
+    k = _cuda(np.zeros((B, nh, T, hd), np.float32))
+    scratch = _t().zeros(64, dtype=_t().int32, device="cuda")
+    z = ctypes.c_int(-1)
+    _call(L.mq_op_mask_is_zero, mq.view(q), mq.view(k), mq.view(mask_d), ctypes.c_void_p(scratch.data_ptr()), 256,
+          ctypes.byref(z), stream())
+    assert z.value == want, case
+
+
 @pytest.mark.parametrize("case,want", [("uniform", 128), ("single", 320), ("unaligned", 64), ("ragged", 0),
                                        ("prefix", 0), ("finite", 0), ("bidirectional", 0), ("odd", 96)])
 def test_mask_segments(case, want):
@@ -677,8 +709,8 @@ def test_mask_segments(case, want):
 
 def test_mask_block_lists_not_taken():
     """Operands whose attention reads no block lists get 0 bytes (and mq_op_mask_blocks refuses
-    them): a mask that differs per head, no mask, and head_dim 64 on a grid the 8-wave kernel
-    fills (it classifies blocks itself)."""
+    them): a mask that differs per head and no mask; a mask shared by the heads takes them at
+    every length (here a 4-D padding mask at head_dim 64, on a grid the 8-wave kernel would fill)."""
     L = mq.lib()
     q = _cuda(np.zeros((1, 4, 64, 128), np.float32))
     k = _cuda(np.zeros((1, 2, 64, 128), np.float32))
@@ -689,7 +721,7 @@ def test_mask_block_lists_not_taken():
     q64 = _cuda(np.zeros((32, 12, 128, 64), np.float32))
     k64 = _cuda(np.zeros((32, 12, 128, 64), np.float32))
     m64 = _cuda(np.zeros((32, 1, 128, 128), np.float16))
-    assert L.mq_op_mask_blocks_bytes(mq.view(q64), mq.view(k64), mq.view(m64)) == 0
+    assert L.mq_op_mask_blocks_bytes(mq.view(q64), mq.view(k64), mq.view(m64)) == 32 * 4 * 5 * 4
 
 
 @pytest.mark.parametrize("case", ["plain", "yarn", "freq_factors"])
