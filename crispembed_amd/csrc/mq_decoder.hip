@@ -576,7 +576,9 @@ __global__ __launch_bounds__(512) void k_attn_frag(const AttnArgs a, int nblk, f
 // block lists (MK = 2, launch_mask_blocks: the same classification, made once for all heads and
 // every attention that reads the mask) the waves take the tile's live blocks in turn: a
 // block-diagonal batch mask over thousands of keys then costs the tile's own blocks only.
-template <int HD, int MK, int NW>
+// QO (head_dim 32 / 64): the merged rows also leave as the Q8_0 activation of the projection
+// that reads them (AttnArgs::qo), as the 8-wave kernel's store writes it.
+template <int HD, int MK, int NW, bool QO = false>
 __global__ __launch_bounds__(64 * NW, 2) void k_attn_split(const AttnArgs a, int nblk, float qscale) {
     constexpr bool MASK = MK != 0;
     constexpr int NS = HD / 16, NT = HD / 32, HALF = HD / 2, NFR = kv_frags<HD>();
@@ -870,9 +872,37 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_split(const AttnArgs a, int
                     l += f * mls[w][1][qq];
                 }
             }
+            const float val = l > 0.f ? o / (l * 32768.0f) : 0.f;
             if (q < Tq) {
                 float *ob = a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)q * a.o_st + l32 + 32 * n;
-                *ob = l > 0.f ? o / (l * 32768.0f) : 0.f;
+                *ob = val;
+            }
+            // QO: the merged value also goes to LDS for the quantizer below, into this (n, r)'s
+            // slot of wave 0's partial -- read above by this lane alone (each (n, r) has one wave)
+            if constexpr (QO) ored[0][n][r][lane] = val;
+        }
+    }
+    if constexpr (QO) {
+        // the merged 32 x HD tile quantized as the projection's Q8_0 activation, as the 8-wave
+        // kernel's store writes it: wave n < NT takes dims 32 n .. + 31 (one Q8_0 block of output
+        // row b Tq + q, chunk h NT + n), lane l query l % 32 and its 16 values 16 (l / 32) ..
+        // (row r = 4 (q / 8) + q % 4, lane 32 ((q / 4) % 2) + dim of the merge above)
+        __syncthreads();
+        if (wave < NT) {
+            const int n = wave, qq = l32, q = q0 + qq;
+            const float *src = &ored[0][n][4 * (qq >> 3) + (qq & 3)][32 * ((qq >> 2) & 1) + 16 * half];
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float4 t4 = *(const float4 *)(src + 4 * u);
+                v[4 * u] = t4.x, v[4 * u + 1] = t4.y, v[4 * u + 2] = t4.z, v[4 * u + 3] = t4.w;
+            }
+            uint4 pk;
+            const float d = requant_q8_0(v, true, MQ_PRE_NONE, a.q_var, pk);
+            if (q < Tq) {
+                const int64_t row = (int64_t)b * Tq + q, chunk = (int64_t)h * NT + n;
+                *(uint4 *)(a.qo + (((row >> 5) * a.q_kch + chunk) << 10) + (((row & 31) + 32 * half) << 4)) = pk;
+                if (half == 0) a.qd[chunk * a.q_m_pad + row] = d;
             }
         }
     }
@@ -970,8 +1000,11 @@ static hipError_t launch_attn_8w(dim3 grid, const AttnArgs &a, int nblk, float q
 }
 
 // The split-key form when the regular grid (2 heads x 128 queries per workgroup) would leave
-// most CUs idle and there are several key blocks to share out, for masked head_dim 128 (the
-// 8-wave kernel's mask addressing does not fit its 256 registers and spills), and for a mask
+// most CUs idle, there are several key blocks to share out and the split grid (a head and 32
+// queries per workgroup) fits one round of two workgroups per CU (MI355X, 32 sequences x 128
+// tokens, 6 heads of 64: 96 regular workgroups 15.4 us against 768 split ones 19.4 us), for
+// masked head_dim 128 (the 8-wave kernel's mask addressing does not fit its 256 registers and
+// spills), and for a mask
 // shared by every head over 1024 keys or more (a packed batch's block-diagonal mask: the split
 // form runs only the blocks the mask leaves live, the 8-wave kernel tests every key block);
 // MQ_ATTN_SPLIT=0/1 forces either form (measurements)
@@ -982,17 +1015,26 @@ bool attn_split_form(const AttnArgs &a) {
     // length: its key blocks are classified once per graph (block lists), where the 8-wave kernel
     // reads the mask of every block for every head (MI355X, 32 ragged sequences x 128 tokens,
     // head_dim 32: 38.5 -> 16.6 us; head_dim 64: 42.8 -> 22.7 us)
-    bool split = (wgs < 128 && nblk >= 4) || (a.hd == 128 && a.mask) || (a.mask && a.m_sh == 0);
+    const int64_t split_wgs = (int64_t)a.nq * a.B * ((a.Tq + 31) / 32);
+    bool split = (wgs < 128 && nblk >= 4 && split_wgs <= 512) || (a.hd == 128 && a.mask) || (a.mask && a.m_sh == 0);
     if (const char *e = getenv("MQ_ATTN_SPLIT"))
         if (*e) split = atoi(e) != 0;
     return split;
 }
 
+template <int HD, int NW, bool QO>
+static void launch_attn_split_q(dim3 g, const AttnArgs &a, int nblk, float qscale, hipStream_t s) {
+    if (a.mask && a.blist) hipLaunchKernelGGL((k_attn_split<HD, 2, NW, QO>), g, dim3(64 * NW), 0, s, a, nblk, qscale);
+    else if (a.mask) hipLaunchKernelGGL((k_attn_split<HD, 1, NW, QO>), g, dim3(64 * NW), 0, s, a, nblk, qscale);
+    else hipLaunchKernelGGL((k_attn_split<HD, 0, NW, QO>), g, dim3(64 * NW), 0, s, a, nblk, qscale);
+}
+
 template <int HD, int NW>
 static void launch_attn_split(dim3 g, const AttnArgs &a, int nblk, float qscale, hipStream_t s) {
-    if (a.mask && a.blist) hipLaunchKernelGGL((k_attn_split<HD, 2, NW>), g, dim3(64 * NW), 0, s, a, nblk, qscale);
-    else if (a.mask) hipLaunchKernelGGL((k_attn_split<HD, 1, NW>), g, dim3(64 * NW), 0, s, a, nblk, qscale);
-    else hipLaunchKernelGGL((k_attn_split<HD, 0, NW>), g, dim3(64 * NW), 0, s, a, nblk, qscale);
+    if constexpr (HD <= 64) {
+        if (a.qo) return launch_attn_split_q<HD, NW, true>(g, a, nblk, qscale, s);
+    }
+    launch_attn_split_q<HD, NW, false>(g, a, nblk, qscale, s);
 }
 
 template <int HD>
@@ -1031,8 +1073,8 @@ static hipError_t launch_attn_hd(const AttnArgs &a, int nblk, float qscale, hipS
 // head_dim 128 when the workgroup's two heads make whole superblocks of complete query tiles
 // (even nq, Tq a multiple of 128, no mask).  Otherwise the caller quantizes the fp32 output.
 static bool attn_frag_form(const AttnArgs &a, int q_type) {
+    if (q_type == MQ_TYPE_Q8_0 && a.hd <= 64) return true;  // both forms store Q8_0 rows
     if (attn_split_form(a)) return false;
-    if (q_type == MQ_TYPE_Q8_0) return a.hd <= 64;
     return a.hd == 128 && a.nq % 2 == 0 && a.Tq % 128 == 0 && !a.mask;
 }
 
@@ -1193,7 +1235,7 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
             b.q_kch = (int)(K / 32);
             b.q_nsb = (int)(K / QK_K);
         } else {
-            quant_after = true;  // the split-key form stores floats only
+            quant_after = true;  // the Q8_K store needs the 8-wave form
         }
     }
     hipError_t e;
