@@ -206,6 +206,14 @@ __device__ __forceinline__ float ds_read32(uint32_t a) {
     asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(a));
     return r;
 }
+// the same with a constant byte offset (one address register for many reads)
+template <int OFF>
+__device__ __forceinline__ float ds_read32_o(uint32_t a) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offsets are 16 bits");
+    float r;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+    return r;
+}
 
 // Workgroup barrier that does not wait for outstanding DMAs (a fenced
 // __syncthreads would wait for every one of them, i.e. empty the pipeline).  It
@@ -480,6 +488,43 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
         scale(std::integral_constant<int, NSTEP - 1>{});
     };
 
+    // Q8_0 occupancy form (MINB >= 4: the one-wave-tile workgroup within 80 registers, so six
+    // workgroups share a CU): one block at a time -- its operands, its two MFMAs, the convert +
+    // fma of its 16 outputs per lane -- so only one step's results are live, and the other
+    // waves of the SIMD fill the latency a single wave leaves.  Scale reads at constant offsets
+    // from one address register per operand side.
+    const uint32_t scx_base = lds_addr(smem + (wm * TM * 32 + lrow) * 4);
+    const uint32_t scw_base = lds_addr(smem + (wn * TN * 32 + lrow) * 4);
+    auto compute_q8_0_occ = [&](auto slotc) __attribute__((always_inline)) {
+        constexpr int slot = decltype(slotc)::value;
+        static_assert(TM == 1 && TN == 1, "one 32x32 tile per wave");
+        const int8_t *st = smem + slot * C::STAGE;
+        static_for<0, KC>([&](auto kcc) __attribute__((always_inline)) {
+            constexpr int kc = decltype(kcc)::value;
+            constexpr int sco = slot * C::STAGE + C::X_BYTES + C::W_BYTES + kc * 1024;
+            float dw = ds_read32_o<sco + C::SCX>(scw_base);
+            float dx = ds_read32_o<sco>(scx_base);
+            v4i xa = *(const v4i *)(st + xfrag0 + kc * 1024);
+            const v4i wb = *(const v4i *)(st + wfrag0 + kc * 1024);
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(dw), "+v"(dx));
+            // the MFMAs are pure: tie them after the previous block's fmas (no instruction), or
+            // the compiler hoists every block's MFMAs and keeps all their results live
+            // (scalar operands: a 64-byte vector operand is not valid in the host pass)
+            if constexpr (kc > 0) {
+                const v16f &c = acc[0][0];
+                asm volatile("" : "+v"(xa) : "v"(c[0]), "v"(c[1]), "v"(c[2]), "v"(c[3]), "v"(c[4]), "v"(c[5]), "v"(c[6]),
+                             "v"(c[7]), "v"(c[8]), "v"(c[9]), "v"(c[10]), "v"(c[11]), "v"(c[12]), "v"(c[13]), "v"(c[14]),
+                             "v"(c[15]));
+            }
+            dx = lhalf ? 0.0f : dx;  // the rank-1 MFMA's k = 1 half is zero
+            const v16i tq = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, wb, (v16i){}, 0, 0, 0);
+            const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(dx, dw, (v16f){}, 0, 0, 0);
+#pragma unroll
+            for (int rr = 0; rr < 16; rr++) acc[0][0][rr] += (float)tq[rr] * sc[rr];
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+
     // MFMAs of one stage
     auto compute = [&](const int8_t *st) __attribute__((always_inline)) {
         if constexpr (FMT == FMT_Q8_0) {
@@ -591,7 +636,9 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
                 wait_vmcnt_c<C::template waits<DIST>(q)>();
                 barrier_nofence();  // stage s landed for every wave; stage s-1 fully consumed
                 issue(s + DIST);
-                compute(smem + (q % NBUF) * C::STAGE);  // s0 is a multiple of NBUF: stage s sits in slot q % NBUF
+                // s0 is a multiple of NBUF: stage s sits in slot q % NBUF
+                if constexpr (FMT == FMT_Q8_0 && MINB >= 4) compute_q8_0_occ(std::integral_constant<int, q % NBUF>{});
+                else compute(smem + (q % NBUF) * C::STAGE);
             }
         });
         if constexpr (C::limbs) epilogue(s0 / SPB);
@@ -838,6 +885,7 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
 //   7: 4 waves x (32x32)  WG 64x64
 //   8: as 7 with a 2-stage ring (one stage in flight): half the LDS, more workgroups per CU
 //   9: as 7 with a 3-stage ring (two in flight; Q8_0 and F16)
+//  12: as 8 within 80 registers, six workgroups per CU, one block at a time (Q8_0)
 //  11: 8 waves x (64x64)  WG 128x256, 32-byte K stages (K-quants; the Q8_K-output GEMM's tiles)
 static int gemm_cfg_env() {
     const char *e = getenv("MQ_GEMM_CFG");  // read per launch so a process can compare configurations
@@ -849,19 +897,23 @@ static inline int64_t tiles(int64_t M, int64_t N, int bm, int bn) { return ((M +
 template <int FMT>
 static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
     int cfg = gemm_cfg_env();
-    if (cfg < 1 || cfg > 11 || cfg == 2 || cfg == 10 || (cfg == 11 && FMT != FMT_Q4_K && FMT != FMT_Q6_K) || (cfg == 6 && FMT != FMT_Q4_K && FMT != FMT_Q6_K) ||
-        (cfg == 9 && FMT != FMT_Q8_0 && FMT != FMT_F16)) {
+    if (cfg < 1 || cfg > 12 || cfg == 2 || cfg == 10 || (cfg == 11 && FMT != FMT_Q4_K && FMT != FMT_Q6_K) || (cfg == 6 && FMT != FMT_Q4_K && FMT != FMT_Q6_K) ||
+        (cfg == 9 && FMT != FMT_Q8_0 && FMT != FMT_F16) || (cfg == 12 && FMT != FMT_Q8_0)) {
         // Small grids (under 512 tiles of 128x128): 64x64 workgroups of four 32x32 waves.
         // Every 32-deep K chunk costs a wave VALU work per output of its tile (the block
         // scales), so smaller wave tiles shorten the serial chain each wave walks; with few
         // output tiles that chain, not operand reuse, sets the time (MI355X, Q8_0 4096x384x1536
         // 32 -> 17 us, Q4_K 512x1024x3072 37 -> 16 us).  For Q8_0 with a 2-stage ring: half the
         // LDS, twice the workgroups per CU (17.9 -> 16.2 us at 4096x1536x384; the K-quants and
-        // F16 measured slower with it at 512 rows).  Larger grids: 256x128 tiles when that still
-        // gives every CU (256) a workgroup, else 128x128.
+        // F16 measured slower with it at 512 rows).  Q8_0 grids of 768 or more such workgroups:
+        // the one-block-at-a-time form within 80 registers, all of them resident at once
+        // (4096x1536x384 16.4 -> 15.6 us, 4096x1152x384 15.0 -> 13.6 us; equal at 768).
+        // Larger grids: 256x128 tiles when that still gives every CU (256) a workgroup, else
+        // 128x128.
         int64_t n_all = a.N;
         for (int g = 1; g < a.ngroups; g++) n_all += a.grp[g - 1].N;
-        if (tiles(a.M, n_all, 128, 128) < 512) cfg = FMT == FMT_Q8_0 ? 8 : 7;
+        if (tiles(a.M, n_all, 128, 128) < 512)
+            cfg = FMT == FMT_Q8_0 ? (tiles(a.M, n_all, 64, 64) >= 768 ? 12 : 8) : 7;
         else cfg = (tiles(a.M, n_all, 256, 128) >= 256) ? 1 : 3;
     }
     switch (cfg) {
@@ -879,6 +931,9 @@ static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
             return hipErrorInvalidValue;
         case 11:
             if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q6_K) return launch_cfg<FMT, 2, 4, 2, 2, 1, 1, false, 4, 3>(a, s);
+            return hipErrorInvalidValue;
+        case 12:
+            if constexpr (FMT == FMT_Q8_0) return launch_cfg<FMT, 2, 2, 1, 1, 6, 2, false, 2, 1>(a, s);
             return hipErrorInvalidValue;
 
 

@@ -35,7 +35,7 @@ def _check(oracle, wtype, w, x, y, k):
     return e1
 
 
-@pytest.mark.parametrize("cfg", ["1", "3", "4", "5", "6", "7", "8", "9", "11"])
+@pytest.mark.parametrize("cfg", ["1", "3", "4", "5", "6", "7", "8", "9", "11", "12"])
 @pytest.mark.parametrize("wtype", TYPES)
 @pytest.mark.parametrize("m,n,k", [(37, 70, 512), (128, 128, 256), (300, 260, 768), (129, 257, 1024), (9, 33, 256),
                                    (520, 390, 1536), (200, 140, 384)])
