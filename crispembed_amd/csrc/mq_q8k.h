@@ -17,6 +17,28 @@ __device__ __forceinline__ int nearest_int(float f) {
     return (__float_as_int(v) & 0x007fffff) - 0x00400000;
 }
 
+// The four int8 values a, b, c, d (each in [-128, 127]) as one little-endian word (byte selects).
+__device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
+    const uint32_t ab = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);  // a.b0, b.b0, 0, 0
+    const uint32_t cd = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000c0cu);  // 0, 0, c.b0, d.b0
+    return ab | cd;
+}
+
+// The sum of the four signed bytes of w.
+__device__ __forceinline__ int sum4_i8(uint32_t w) { return __builtin_amdgcn_sdot4((int)w, 0x01010101, 0, false); }
+
+// The lane's largest |x| of its 4 values, and the first value (in order) with that magnitude.
+__device__ __forceinline__ void first_absmax4(const float (&x)[4], float &la, float &lm) {
+    la = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+    lm = fabsf(x[2]) == la ? x[2] : x[3];
+    lm = fabsf(x[1]) == la ? x[1] : lm;
+    lm = fabsf(x[0]) == la ? x[0] : lm;
+}
+
+// nearest_int for the quantizers' |f| <= 127.0001: round half to even, as the magic-number add
+// (f + 1.5*2^23 in the default rounding mode) does for every |f| < 2^22.
+__device__ __forceinline__ int round_even_i(float f) { return (int)rintf(f); }
+
 // DPP steps inside each 16-lane row (quad_perm [1,0,3,2] = xor 1, quad_perm [2,3,0,1] = xor 2,
 // row_half_mirror = i <-> 7-i within 8 lanes): after the three, every lane holds the
 // combination over its 8-lane group.
@@ -46,13 +68,8 @@ __device__ __forceinline__ void q8_K_block_row(const float4 v, int lane, int r, 
                                                _Float16 *msh) {
 #pragma clang fp contract(off)
     const float vals[4] = {v.x, v.y, v.z, v.w};
-    float la = 0.0f, lm = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-        if (fabsf(vals[i]) > la) {
-            la = fabsf(vals[i]);
-            lm = vals[i];
-        }
+    float la, lm;
+    first_absmax4(vals, la, lm);
     const float amax = wave_max_f(la);
     uint32_t packed = 0;
     int s16 = 0;
@@ -61,13 +78,11 @@ __device__ __forceinline__ void q8_K_block_row(const float4 v, int lane, int r, 
         const unsigned long long hit = __ballot(la == amax);
         const float mx = lane_f(lm, __ffsll((long long)hit) - 1);
         const float iscale = -127.f / mx;
+        int qv[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            int qv = nearest_int(iscale * vals[i]);
-            qv = qv < 127 ? qv : 127;
-            packed |= (uint32_t)(qv & 0xff) << (8 * i);
-            s16 += qv;
-        }
+        for (int i = 0; i < 4; i++) qv[i] = min(round_even_i(iscale * vals[i]), 127);
+        packed = pack4_i8(qv[0], qv[1], qv[2], qv[3]);
+        s16 = sum4_i8(packed);
         dval = 1.0f / iscale;
     }
     *(uint32_t *)dst = packed;
@@ -95,13 +110,8 @@ __device__ __forceinline__ void q8_K_rows(const float4 *v, int lane, uint32_t *q
 #pragma unroll
     for (int i = 0; i < NR; i++) {
         const float vals[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-        float la = 0.0f, lm = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            if (fabsf(vals[e]) > la) {
-                la = fabsf(vals[e]);
-                lm = vals[e];
-            }
+        float la, lm;
+        first_absmax4(vals, la, lm);
         amax[i] = wave_max_f(la);
         const unsigned long long hit = __ballot(la == amax[i]);
         mx[i] = amax[i] != 0.0f ? lane_f(lm, __ffsll((long long)hit) - 1) : 1.0f;
@@ -118,13 +128,11 @@ __device__ __forceinline__ void q8_K_rows(const float4 *v, int lane, uint32_t *q
         float dval = 0.0f;
         if (amax[i] != 0.0f) {
             const float iscale = lane_f(is_l, i);
+            int qv[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                int qv = nearest_int(iscale * vals[e]);
-                qv = qv < 127 ? qv : 127;
-                packed |= (uint32_t)(qv & 0xff) << (8 * e);
-                s16 += qv;
-            }
+            for (int e = 0; e < 4; e++) qv[e] = min(round_even_i(iscale * vals[e]), 127);
+            packed = pack4_i8(qv[0], qv[1], qv[2], qv[3]);
+            s16 = sum4_i8(packed);
             dval = lane_f(d_l, i);
         }
         q[i] = packed;
