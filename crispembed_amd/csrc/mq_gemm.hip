@@ -119,23 +119,32 @@ struct GemmArgs {
 // WM x WN waves per workgroup, each wave TM x TN MFMA tiles of 32x32; stages of KC 32-byte
 // K chunks (64 bytes by default; 32 halves the ring so two workgroups share a CU); a ring of NB
 // stages in LDS with D of them in flight ahead of the one being computed (4 and 3 by default;
-// a shorter ring leaves room for more workgroups per CU).
-template <int FMT, int WM, int WN, int TM, int TN, int KCT = 2, int NBT = 4, int DT = 3>
+// a shorter ring leaves room for more workgroups per CU).  KG > 1 (Q8_0, one 32x32 tile per
+// wave): KG groups of WM x WN waves split each stage's KC chunks, group g taking chunks
+// g KC/KG .. (g + 1) KC/KG - 1 of every stage, and their partial sums meet in LDS at the end.
+template <int FMT, int WM, int WN, int TM, int TN, int KCT = 2, int NBT = 4, int DT = 3, int KGT = 1>
 struct Cfg {
     static constexpr int NB = NBT, D = DT;
     static_assert(D + 1 <= NB, "stage ring: D stages in flight plus the one being computed");
     static constexpr int KC = KCT;              // 32-byte K chunks per stage
     static constexpr int SPB = 256 / (32 * KC);  // stages per 256-value superblock
-    static constexpr int NW = WM * WN, NT = 64 * NW, BM = 32 * TM * WM, BN = 32 * TN * WN;
+    static constexpr int KG = KGT, NTW = WM * WN;  // K groups, waves per K group
+    static_assert(KG == 1 || (FMT == FMT_Q8_0 && TM == 1 && TN == 1 && KC % KG == 0), "K groups: Q8_0, one tile per wave");
+    static constexpr int NW = NTW * KG, NT = 64 * NW, BM = 32 * TM * WM, BN = 32 * TN * WN;
     static constexpr bool limbs = (FMT == FMT_Q4_K || FMT == FMT_Q6_K);
     static constexpr int NPL = limbs ? 2 : 1;
     static constexpr int XF = (BM / 32) * KC, WF = (BN / 32) * KC;  // data fragments per stage
     static constexpr int X_BYTES = XF * 1024, W_BYTES = WF * 1024;
-    static constexpr int NSC = (FMT == FMT_Q8_0) ? 2 * KC : 0;     // Q8_0 scale rows per stage
-    // scale rows move as full 64-lane DMAs into 1 KB slots (a row of BM or BN
-    // floats fills the first BM*4 / BN*4 bytes), so no DMA is lane-masked
-    static constexpr int SCX = (FMT == FMT_Q8_0) ? KC * 1024 : 0;
-    static constexpr int SCW = (FMT == FMT_Q8_0) ? KC * 1024 : 0;
+    // Q8_0 scale rows move as full 64-lane DMAs, so no DMA is lane-masked: one row of BM or BN
+    // floats per 1 KB slot (filling its first BM*4 / BN*4 bytes), or with packed scales (the
+    // K-group forms: BM, BN <= 64, KC <= 4) the KC rows of a stage in one slot, 256 bytes each
+    // (lane l fetches a piece of chunk l / 16's row), so a stage's scales are two DMAs
+    static constexpr bool PSC = KG > 1;
+    static_assert(!PSC || (BM <= 64 && BN <= 64 && KC <= 4), "packed scale slots: 4 rows of <= 64 floats");
+    static constexpr int SCROW = PSC ? 256 : 1024;  // bytes from one chunk's scale row to the next
+    static constexpr int NSC = (FMT == FMT_Q8_0) ? (PSC ? 2 : 2 * KC) : 0;  // Q8_0 scale DMAs per stage
+    static constexpr int SCX = (FMT == FMT_Q8_0) ? (PSC ? 1024 : KC * 1024) : 0;
+    static constexpr int SCW = SCX;
     static constexpr int STAGE = X_BYTES + NPL * W_BYTES + SCX + SCW;
     static constexpr int NITEM = XF + NPL * WF + NSC;               // DMA instructions per stage
     static constexpr int IPW = (NITEM + NW - 1) / NW;               // per wave (upper bound)
@@ -154,7 +163,10 @@ struct Cfg {
     // the Q8_K-output epilogue (BN = 256) stages the whole BM x 256 fp32 tile, then the tile's
     // min-term fragments and row scales
     static constexpr int LDS_Q8K = BN == 256 ? BM * 1024 + (BM / 32) * 1024 + BM * 4 : 0;
-    static constexpr int LDS_E = LDS_STG > LDS_Q8K ? LDS_STG : LDS_Q8K;
+    static constexpr int LDS_E0 = LDS_STG > LDS_Q8K ? LDS_STG : LDS_Q8K;
+    // K groups 1 .. KG-1 leave their 32x32 partial sums (4 KB per wave) for group 0
+    static constexpr int LDS_PART = (KG - 1) * NTW * 4096;
+    static constexpr int LDS_E = LDS_E0 > LDS_PART ? LDS_E0 : LDS_PART;
     static constexpr int LDS = LDS_RING > LDS_E ? LDS_RING : LDS_E;
     // DMAs issued per stage by every wave, and the count still in flight when stage
     // position q (of a superblock) may be computed: those of the D-1 later stages.
@@ -271,6 +283,17 @@ __device__ __forceinline__ DmaItem stage_item(const GemmArgs &a, int f, int m0, 
         it.lds = C::X_BYTES + pl * C::W_BYTES + f3 * 1024;
     } else {
         const int f4 = f - C::XF - C::NPL * C::WF;  // Q8_0 scale rows
+        if constexpr (C::PSC) {
+            // chunk (lane / 16) % 4's row: pieces of 16 bytes, lanes past a row's pieces re-read it
+            const int kc = (lane >> 4) & 3, np = (f4 == 0 ? C::BM : C::BN) / 4;
+            const int64_t ld = f4 == 0 ? a.m_pad : a.n_pad;
+            it.g0 = (const int8_t *)(f4 == 0 ? a.xd + m0 : a.wd + n0);
+            it.step = (int64_t)C::KC * ld * 4;
+            it.lds = C::X_BYTES + C::W_BYTES + f4 * C::SCX;
+            it.pieces = 64;
+            it.loff = (int)(kc * ld * 4) + (lane & (np - 1)) * 16;
+            return it;
+        }
         if (f4 < C::KC) {
             it.g0 = (const int8_t *)(a.xd + (int64_t)f4 * a.m_pad + m0);
             it.step = (int64_t)C::KC * a.m_pad * 4;
@@ -325,16 +348,19 @@ __device__ __forceinline__ DmaItem epi_item(const GemmArgs &a, int e, int sb, in
 // GLU: a.N = 2 n_ff columns of a gate|up weight; y receives silu(gate) * up, n_ff columns (the
 // gated FFN's down-projection input, src/decoder_embed.cpp:793-802), and no gate or up value
 // is stored.
-template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2, bool GLU = false, int NBT = 4, int DT = 3>
-__global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) {
-    using C = Cfg<FMT, WM, WN, TM, TN, KCT, NBT, DT>;
+template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2, bool GLU = false, int NBT = 4, int DT = 3,
+          int KG = 1>
+__global__ __launch_bounds__(64 * WM * WN * KG, MINB) void k_gemm(const GemmArgs a0) {
+    using C = Cfg<FMT, WM, WN, TM, TN, KCT, NBT, DT, KG>;
     constexpr int NBUF = C::NB, DIST = C::D;
     static_assert(!GLU || TN == 2, "GLU: each wave holds a gate and an up column tile");
     constexpr int KC = C::KC, SPB = C::SPB;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // uniform: SALU addressing
-    const int wm = wave / WN, wn = wave % WN;
+    const int wt = wave % C::NTW, kg = wave / C::NTW;  // tile wave, K group
+    const int wm = wt / WN, wn = wt % WN;
+    const int kc0 = kg * (C::KC / KG);  // the K group's first chunk of every stage
     const int lrow = lane & 31;
     const int lhalf = lane >> 5;
 
@@ -403,7 +429,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
         }
 #pragma unroll
         for (int i = 0; i < C::IPW; i++) {
-            if constexpr (GLU) dma16(items[i].g0 + sc * items[i].step + items[i].loff, st + items[i].lds);
+            if constexpr (GLU || C::PSC) dma16(items[i].g0 + sc * items[i].step + items[i].loff, st + items[i].lds);
             else dma16(items[i].g0 + sc * items[i].step + (lane & (items[i].pieces - 1)) * 16, st + items[i].lds);
         }
     };
@@ -418,8 +444,8 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
             alo[i][j] = (v16i){};
             if constexpr (C::limbs) ahi[i][j] = (v16i){};
         }
-    const int xfrag0 = wm * TM * KC * 1024 + lane * 16;  // LDS offset of this wave's first X fragment
-    const int wfrag0 = C::X_BYTES + wn * TN * KC * 1024 + lane * 16;
+    const int xfrag0 = (wm * TM * KC + kc0) * 1024 + lane * 16;  // LDS offset of this wave's first X fragment
+    const int wfrag0 = C::X_BYTES + (wn * TN * KC + kc0) * 1024 + lane * 16;
 
     // Q8_0 stage: per block and 32x32 tile, an int8 MFMA (block dot), a rank-1 f32
     // MFMA (scale products) and the convert + fma of the 16 outputs per lane.  The
@@ -444,7 +470,9 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
 #pragma unroll
             for (int j = 0; j < TN; j++) wb[kc][j] = *(const v4i *)(st + wfrag0 + (j * KC + kc) * 1024);
         }
-        static_assert(FMT != FMT_Q8_0 || (KC == 2 && TM <= 2 && TN <= 2), "the wait below names every scale register");
+        // (the occupancy and K-group forms use compute_q8_0_occ instead)
+        static_assert(FMT != FMT_Q8_0 || MINB >= 4 || KG > 1 || (KC == 2 && TM <= 2 && TN <= 2),
+                      "the wait below names every scale register");
         // each register named once: an operand listed twice is copied (v_mov) before the wait,
         // i.e. read before its ds_read has landed, and that stale copy is what gets used
         if constexpr (TM == 2 && TN == 2)
@@ -493,15 +521,15 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
     // fma of its 16 outputs per lane -- so only one step's results are live, and the other
     // waves of the SIMD fill the latency a single wave leaves.  Scale reads at constant offsets
     // from one address register per operand side.
-    const uint32_t scx_base = lds_addr(smem + (wm * TM * 32 + lrow) * 4);
-    const uint32_t scw_base = lds_addr(smem + (wn * TN * 32 + lrow) * 4);
+    const uint32_t scx_base = lds_addr(smem + kc0 * C::SCROW + (wm * TM * 32 + lrow) * 4);
+    const uint32_t scw_base = lds_addr(smem + kc0 * C::SCROW + (wn * TN * 32 + lrow) * 4);
     auto compute_q8_0_occ = [&](auto slotc) __attribute__((always_inline)) {
         constexpr int slot = decltype(slotc)::value;
         static_assert(TM == 1 && TN == 1, "one 32x32 tile per wave");
         const int8_t *st = smem + slot * C::STAGE;
-        static_for<0, KC>([&](auto kcc) __attribute__((always_inline)) {
+        static_for<0, KC / KG>([&](auto kcc) __attribute__((always_inline)) {
             constexpr int kc = decltype(kcc)::value;
-            constexpr int sco = slot * C::STAGE + C::X_BYTES + C::W_BYTES + kc * 1024;
+            constexpr int sco = slot * C::STAGE + C::X_BYTES + C::W_BYTES + kc * C::SCROW;
             float dw = ds_read32_o<sco + C::SCX>(scw_base);
             float dx = ds_read32_o<sco>(scx_base);
             v4i xa = *(const v4i *)(st + xfrag0 + kc * 1024);
@@ -637,11 +665,30 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
                 barrier_nofence();  // stage s landed for every wave; stage s-1 fully consumed
                 issue(s + DIST);
                 // s0 is a multiple of NBUF: stage s sits in slot q % NBUF
-                if constexpr (FMT == FMT_Q8_0 && MINB >= 4) compute_q8_0_occ(std::integral_constant<int, q % NBUF>{});
+                if constexpr (FMT == FMT_Q8_0 && (MINB >= 4 || KG > 1)) compute_q8_0_occ(std::integral_constant<int, q % NBUF>{});
                 else compute(smem + (q % NBUF) * C::STAGE);
             }
         });
         if constexpr (C::limbs) epilogue(s0 / SPB);
+    }
+    if constexpr (KG > 1) {
+        // K groups 1 .. KG-1 hand their partial sums to group 0 through LDS (the ring, once every
+        // wave's DMAs have landed and every wave is past its last stage); group 0 adds them in
+        // group order and stores.  The other groups end here: a later workgroup barrier (the
+        // quantized-output and K/V-fragment stores) waits for the waves still running.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        float *part = (float *)smem;
+        if (kg > 0) {
+#pragma unroll
+            for (int rr = 0; rr < 16; rr++) part[(((kg - 1) * C::NTW + wt) * 16 + rr) * 64 + lane] = acc[0][0][rr];
+        }
+        __syncthreads();
+        if (kg > 0) return;  // uniform per wave
+#pragma unroll
+        for (int g = 1; g < KG; g++)
+#pragma unroll
+            for (int rr = 0; rr < 16; rr++) acc[0][0][rr] += part[(((g - 1) * C::NTW + wt) * 16 + rr) * 64 + lane];
     }
     // the bias of the lane's output columns, loaded before the wait below so that its latency
     // overlaps the last DMAs instead of stalling the stores
@@ -856,11 +903,13 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void k_gemm(const GemmArgs a0) 
         }
 }
 
-template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2, bool GLU = false, int NBT = 4, int DT = 3>
+template <int FMT, int WM, int WN, int TM, int TN, int MINB, int KCT = 2, bool GLU = false, int NBT = 4, int DT = 3,
+          int KG = 1>
 static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
-    using C = Cfg<FMT, WM, WN, TM, TN, KCT, NBT, DT>;
+    using C = Cfg<FMT, WM, WN, TM, TN, KCT, NBT, DT, KG>;
+    if (KG > 1 && ((a.qo && a.q_fmt == 1) || a.moe)) return hipErrorInvalidValue;  // K groups: BN 64, no expert tiles
     static std::atomic<bool> attr_set[MQ_MAX_DEVICES];
-    const hipError_t e = dyn_lds_once((const void *)k_gemm<FMT, WM, WN, TM, TN, MINB, KCT, GLU, NBT, DT>, C::LDS, attr_set);
+    const hipError_t e = dyn_lds_once((const void *)k_gemm<FMT, WM, WN, TM, TN, MINB, KCT, GLU, NBT, DT, KG>, C::LDS, attr_set);
     if (e != hipSuccess) return e;
     a.tiles_m = (a.M + C::BM - 1) / C::BM;
     a.tiles_n = (a.N + C::BN - 1) / C::BN;
@@ -871,7 +920,7 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
     a.group_m = 8;
     a.nstages = a.kch / KCT;  // kb_pad is a multiple of 128 bytes
     const unsigned grid = (unsigned)(a.tiles_m * a.tiles_n);
-    hipLaunchKernelGGL((k_gemm<FMT, WM, WN, TM, TN, MINB, KCT, GLU, NBT, DT>), dim3(grid), dim3(C::NT), C::LDS, s, a);
+    hipLaunchKernelGGL((k_gemm<FMT, WM, WN, TM, TN, MINB, KCT, GLU, NBT, DT, KG>), dim3(grid), dim3(C::NT), C::LDS, s, a);
     return hipGetLastError();
 }
 
@@ -887,6 +936,8 @@ static hipError_t launch_cfg(GemmArgs a, hipStream_t s) {
 //   9: as 7 with a 3-stage ring (two in flight; Q8_0 and F16)
 //  12: as 8 within 80 registers, six workgroups per CU, one block at a time (Q8_0)
 //  11: 8 waves x (64x64)  WG 128x256, 32-byte K stages (K-quants; the Q8_K-output GEMM's tiles)
+//  15: WG 32x64: 2 waves x (32x32) x 4 K groups, 128-byte K stages, 3-stage ring (Q8_0; not
+//      the Q8_K output)
 static int gemm_cfg_env() {
     const char *e = getenv("MQ_GEMM_CFG");  // read per launch so a process can compare configurations
     return (e && *e) ? atoi(e) : 0;
@@ -897,8 +948,10 @@ static inline int64_t tiles(int64_t M, int64_t N, int bm, int bn) { return ((M +
 template <int FMT>
 static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
     int cfg = gemm_cfg_env();
-    if (cfg < 1 || cfg > 12 || cfg == 2 || cfg == 10 || (cfg == 11 && FMT != FMT_Q4_K && FMT != FMT_Q6_K) || (cfg == 6 && FMT != FMT_Q4_K && FMT != FMT_Q6_K) ||
-        (cfg == 9 && FMT != FMT_Q8_0 && FMT != FMT_F16) || (cfg == 12 && FMT != FMT_Q8_0)) {
+    const bool kg_ok = !(a.qo && a.q_fmt == 1) && !a.moe;  // outputs the K-group forms (BN = 64) store
+    if (cfg < 1 || cfg > 15 || cfg == 2 || cfg == 10 || cfg == 13 || cfg == 14 || (cfg == 11 && FMT != FMT_Q4_K && FMT != FMT_Q6_K) || (cfg == 6 && FMT != FMT_Q4_K && FMT != FMT_Q6_K) ||
+        (cfg == 9 && FMT != FMT_Q8_0 && FMT != FMT_F16) || (cfg == 12 && FMT != FMT_Q8_0) ||
+        (cfg == 15 && (FMT != FMT_Q8_0 || !kg_ok))) {
         // Small grids (under 512 tiles of 128x128): 64x64 workgroups of four 32x32 waves.
         // Every 32-deep K chunk costs a wave VALU work per output of its tile (the block
         // scales), so smaller wave tiles shorten the serial chain each wave walks; with few
@@ -908,13 +961,24 @@ static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
         // F16 measured slower with it at 512 rows).  Q8_0 grids of 768 or more such workgroups:
         // the one-block-at-a-time form within 80 registers, all of them resident at once
         // (4096x1536x384 16.4 -> 15.6 us, 4096x1152x384 15.0 -> 13.6 us; equal at 768).
+        // Fewer Q8_0 tiles: 32x64 workgroups whose K chunks are split over four wave groups,
+        // so more waves share each tile's serial chain (4096x384x1536 18.2 -> 15.3 us,
+        // 384x384x1536 13.3 -> 8.1 us, 384x384x384 5.9 -> 4.9 us, 384x1152x384 6.1 -> 5.1 us;
+        // 4096x384x384 7.9 -> 8.1 us), whatever the output (floats, the next product's Q8_0
+        // activation, attention fragments), so every output of one product comes from the same
+        // sums.
         // Larger grids: 256x128 tiles when that still gives every CU (256) a workgroup, else
         // 128x128.
         int64_t n_all = a.N;
         for (int g = 1; g < a.ngroups; g++) n_all += a.grp[g - 1].N;
-        if (tiles(a.M, n_all, 128, 128) < 512)
-            cfg = FMT == FMT_Q8_0 ? (tiles(a.M, n_all, 64, 64) >= 768 ? 12 : 8) : 7;
-        else cfg = (tiles(a.M, n_all, 256, 128) >= 256) ? 1 : 3;
+        if (tiles(a.M, n_all, 128, 128) < 512) {
+            if (FMT != FMT_Q8_0) cfg = 7;
+            else if (tiles(a.M, n_all, 64, 64) >= 768) cfg = 12;
+            else if (!kg_ok) cfg = 8;
+            else cfg = 15;
+        } else {
+            cfg = (tiles(a.M, n_all, 256, 128) >= 256) ? 1 : 3;
+        }
     }
     switch (cfg) {
         case 1: return launch_cfg<FMT, 4, 2, 2, 2, 1>(a, s);
@@ -931,6 +995,9 @@ static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
             return hipErrorInvalidValue;
         case 11:
             if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q6_K) return launch_cfg<FMT, 2, 4, 2, 2, 1, 1, false, 4, 3>(a, s);
+            return hipErrorInvalidValue;
+        case 15:
+            if constexpr (FMT == FMT_Q8_0) return launch_cfg<FMT, 1, 2, 1, 1, 3, 4, false, 3, 2, 4>(a, s);
             return hipErrorInvalidValue;
         case 12:
             if constexpr (FMT == FMT_Q8_0) return launch_cfg<FMT, 2, 2, 1, 1, 6, 2, false, 2, 1>(a, s);
