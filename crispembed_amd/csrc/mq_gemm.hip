@@ -961,12 +961,13 @@ static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
         // F16 measured slower with it at 512 rows).  Q8_0 grids of 768 or more such workgroups:
         // the one-block-at-a-time form within 80 registers, all of them resident at once
         // (4096x1536x384 16.4 -> 15.6 us, 4096x1152x384 15.0 -> 13.6 us; equal at 768).
-        // Fewer Q8_0 tiles: 32x64 workgroups whose K chunks are split over four wave groups,
-        // so more waves share each tile's serial chain (4096x384x1536 18.2 -> 15.3 us,
-        // 384x384x1536 13.3 -> 8.1 us, 384x384x384 5.9 -> 4.9 us, 384x1152x384 6.1 -> 5.1 us;
-        // 4096x384x384 7.9 -> 8.1 us), whatever the output (floats, the next product's Q8_0
-        // activation, attention fragments), so every output of one product comes from the same
-        // sums.
+        // Fewer Q8_0 tiles with K >= 768 or at most 1024 rows: 32x64 workgroups whose K chunks
+        // are split over four wave groups, so more waves share each tile's serial chain
+        // (4096x384x1536 18.2 -> 15.3 us, 384x384x1536 13.3 -> 8.1 us, 384x384x384 5.9 -> 4.9
+        // us, 384x1152x384 6.1 -> 5.1 us; not at 4096x384x384, 7.9 against 8.1 us), whatever the
+        // output (floats, the next product's Q8_0 activation, attention fragments), so the
+        // outputs of one product come from the same sums; below 768 tiles the choice depends on
+        // M and K only, so a grouped launch and its products' separate launches agree there.
         // Larger grids: 256x128 tiles when that still gives every CU (256) a workgroup, else
         // 128x128.
         int64_t n_all = a.N;
@@ -975,7 +976,7 @@ static hipError_t launch_fmt(GemmArgs a, hipStream_t s) {
             if (FMT != FMT_Q8_0) cfg = 7;
             else if (tiles(a.M, n_all, 64, 64) >= 768) cfg = 12;
             else if (!kg_ok) cfg = 8;
-            else cfg = 15;
+            else cfg = (a.kch >= 24 || a.M <= 1024) ? 15 : 8;
         } else {
             cfg = (tiles(a.M, n_all, 256, 128) >= 256) ? 1 : 3;
         }
