@@ -207,7 +207,7 @@ __global__ __launch_bounds__(64 * NW) void k_norm_q8_0(const float *x, const flo
                                                        int variant) {
     constexpr int K = 128 * NV, NCH = K / 32, FST = 1024 + 16;
     constexpr int RPW = RT / NW, NIT = RPW / 2;  // rows per wave, passes of two rows
-    static_assert((RT == 8 || RT == 16 || RT == 32) && NIT >= 1 && RPW % 2 == 0, "8, 16 or 32 rows, whole passes");
+    static_assert((RT == 2 || RT == 8 || RT == 16 || RT == 32) && NIT >= 1 && RPW % 2 == 0, "2, 8, 16 or 32 rows, whole passes");
     __shared__ __attribute__((aligned(16))) int8_t frag[NCH * FST];
     __shared__ float dsh[NCH][32];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1022,11 +1022,10 @@ extern "C" int mq_op_norm(int kind, const mq_view *x, const mq_view *add, const 
     return hip_rc(hipGetLastError(), "norm");
 }
 
-template <int KIND>
-static void launch_norm_q8_0_kind(int nv, const float *x, const float *r, float *d, float eps, const float *w,
-                                  const float *b, int64_t rows, int8_t *xq, float *xd, int64_t m_pad, int variant,
-                                  hipStream_t s) {
-    constexpr int NW = 4, RT = 8;
+template <int KIND, int NW, int RT>
+static void launch_norm_q8_0_rt(int nv, const float *x, const float *r, float *d, float eps, const float *w,
+                                const float *b, int64_t rows, int8_t *xq, float *xd, int64_t m_pad, int variant,
+                                hipStream_t s) {
     const dim3 grid((unsigned)((rows + 31) / 32 * (32 / RT))), block(64 * NW);
     switch (nv) {
 #define MQ_NQ(NV)                                                                                                      \
@@ -1038,6 +1037,19 @@ static void launch_norm_q8_0_kind(int nv, const float *x, const float *r, float 
 #undef MQ_NQ
         default: break;
     }
+}
+
+// 8-row workgroups of 4 waves; at most 1024 rows, 2-row workgroups of one wave, so a 384-row
+// input spreads over 192 CUs instead of 48.  MQ_NORM_RT=2/8 forces either (measurements).
+template <int KIND>
+static void launch_norm_q8_0_kind(int nv, const float *x, const float *r, float *d, float eps, const float *w,
+                                  const float *b, int64_t rows, int8_t *xq, float *xd, int64_t m_pad, int variant,
+                                  hipStream_t s) {
+    int rt = rows <= 1024 ? 2 : 8;
+    if (const char *e = getenv("MQ_NORM_RT"))
+        if (*e) rt = atoi(e) == 2 ? 2 : 8;
+    if (rt == 2) launch_norm_q8_0_rt<KIND, 1, 2>(nv, x, r, d, eps, w, b, rows, xq, xd, m_pad, variant, s);
+    else launch_norm_q8_0_rt<KIND, 4, 8>(nv, x, r, d, eps, w, b, rows, xq, xd, m_pad, variant, s);
 }
 
 extern "C" int mq_op_norm_q8_0(int kind, const mq_view *x, const mq_view *add, const mq_view *dst, float eps,
