@@ -171,7 +171,10 @@ def bench_q4k_ffn(args, torch, L, mq, synth):
     def gemm_roofline(name, n, k, ops, t_ms, w_bytes):
         """One GEMM launch against its binding roofline: the larger of its MFMA time (int8 ops at
         5.0 POP/s) and its HBM time (algorithmic bytes: GGUF weight + quantized X + fp32 Y)."""
-        xq_bytes = M * k + M * (k // 256) * 4  # Q8_K quants + scales
+        # the Q8_K activation as ggml's block_q8_K counts it (292 bytes per 256 values: the scale,
+        # the quants and the 16 sub-block sums), which the GEMM reads as quants, scales and the
+        # min-term fragments of the same sums
+        xq_bytes = M * (k // 256) * 292
         nbytes = w_bytes + xq_bytes + M * n * 4
         t_mfma = ops / (PEAK_INT8_TOPS * 1e12)
         t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
